@@ -1,0 +1,177 @@
+"""Seeded synthetic inputs: GGUF models, quantized weight matrices, prompts.
+
+Weights are N(0, stddev) values quantized with the GGML block quantizers in
+``csrc/tools`` (a restatement of ggml's reference quantizers). Models use the
+qwen2 tensor schema the reference loaders require (model.cpp:861-919,
+metal_model.cpp:851-910): ``token_embd``, ``output_norm``, an explicit
+``output`` and twelve tensors per block.
+
+The Q4_K_M mix is: Q4_K for attention and FFN gate/up, Q6_K for ffn_down and
+the output head, Q8_0 for the embedding. Rows whose length is not a multiple
+of 256 cannot hold a K-quant super-block, so they take the 32-element type of
+the same family, as llama.cpp's Q4_K_M does for such tensors: Q4_K -> Q5_0 and
+Q6_K -> Q8_0 (Qwen2.5-0.5B's hidden size 896 is the case in point).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+import hashlib
+import os
+import pathlib
+
+import numpy as np
+
+from . import _native
+
+F32, F16, Q5_0, Q8_0, Q4_K, Q6_K = 0, 1, 6, 8, 12, 14
+TYPE_NAMES = {F32: "F32", F16: "F16", Q5_0: "Q5_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+BLOCK = {F32: 1, F16: 1, Q5_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}
+
+
+class _Spec(ctypes.Structure):
+    _fields_ = [
+        ("layers", ctypes.c_uint32), ("hidden", ctypes.c_uint32),
+        ("heads", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32),
+        ("ffn", ctypes.c_uint32), ("vocab", ctypes.c_uint32),
+        ("context", ctypes.c_uint32), ("eos_token_id", ctypes.c_uint32),
+        ("rope_theta", ctypes.c_float), ("norm_eps", ctypes.c_float),
+        ("type_embd", ctypes.c_uint32), ("type_attn_qkv", ctypes.c_uint32),
+        ("type_attn_out", ctypes.c_uint32), ("type_ffn_gate_up", ctypes.c_uint32),
+        ("type_ffn_down", ctypes.c_uint32), ("type_output", ctypes.c_uint32),
+        ("seed", ctypes.c_uint64), ("stddev", ctypes.c_float),
+        ("bias_stddev", ctypes.c_float), ("threads", ctypes.c_uint32),
+    ]
+
+
+@dataclasses.dataclass(frozen=True)
+class Qwen2Shape:
+    name: str
+    layers: int
+    hidden: int
+    heads: int
+    kv_heads: int
+    ffn: int
+    vocab: int
+    context: int
+    rope_theta: float = 1e6
+    norm_eps: float = 1e-6
+    eos_token_id: int = 151645
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden // self.heads
+
+
+SHAPES = {
+    # Small shape for golden vectors and fast CPU tests.
+    "tiny": Qwen2Shape("tiny", 2, 256, 4, 2, 512, 1024, 128, eos_token_id=1023),
+    "qwen2.5-0.5b": Qwen2Shape("qwen2.5-0.5b", 24, 896, 14, 2, 4864, 151936, 32768),
+    "qwen2.5-7b": Qwen2Shape("qwen2.5-7b", 28, 3584, 28, 4, 18944, 152064, 32768),
+    "qwen2.5-14b": Qwen2Shape("qwen2.5-14b", 48, 5120, 40, 8, 13824, 152064, 32768),
+}
+
+
+def fallback_type(qtype: int, cols: int) -> int:
+    """The Q4_K_M fallback for rows that are not a multiple of 256."""
+    if cols % BLOCK[qtype] == 0:
+        return qtype
+    if qtype == Q4_K:
+        return Q5_0
+    if qtype == Q6_K:
+        return Q8_0
+    raise ValueError(f"{TYPE_NAMES[qtype]} cannot hold rows of {cols}")
+
+
+def q4_k_m_types(shape: Qwen2Shape) -> dict:
+    h, f = shape.hidden, shape.ffn
+    return dict(
+        type_embd=Q8_0,
+        type_attn_qkv=fallback_type(Q4_K, h),
+        type_attn_out=fallback_type(Q4_K, h),
+        type_ffn_gate_up=fallback_type(Q4_K, h),
+        type_ffn_down=fallback_type(Q6_K, f),
+        type_output=fallback_type(Q6_K, h),
+    )
+
+
+def tiny_all_types() -> dict:
+    """Mix for the tiny golden model: every supported block type appears."""
+    return dict(type_embd=Q8_0, type_attn_qkv=Q4_K, type_attn_out=Q5_0,
+                type_ffn_gate_up=Q4_K, type_ffn_down=Q6_K, type_output=Q6_K)
+
+
+def write_qwen2(path, shape: Qwen2Shape, types: dict | None = None, seed: int = 0,
+                stddev: float = 0.02, bias_stddev: float = 0.02,
+                threads: int | None = None, context: int | None = None) -> pathlib.Path:
+    """Writes a synthetic qwen2 GGUF and returns its path."""
+    types = dict(q4_k_m_types(shape) if types is None else types)
+    if threads is None:
+        threads = min(16, os.cpu_count() or 1)
+    spec = _Spec(shape.layers, shape.hidden, shape.heads, shape.kv_heads, shape.ffn,
+                 shape.vocab, context or shape.context, shape.eos_token_id,
+                 shape.rope_theta, shape.norm_eps,
+                 types["type_embd"], types["type_attn_qkv"], types["type_attn_out"],
+                 types["type_ffn_gate_up"], types["type_ffn_down"], types["type_output"],
+                 seed, stddev, bias_stddev, threads)
+    err = ctypes.create_string_buffer(512)
+    path = pathlib.Path(path)
+    rc = _native.tools().hipllm_tools_write_qwen2(str(path).encode(), ctypes.byref(spec), err, 512)
+    if rc != 0:
+        raise RuntimeError(f"synthetic GGUF writer failed: {err.value.decode()}")
+    return path
+
+
+def normal(n: int, seed: int, stream: int = 0, stddev: float = 1.0, first: int = 0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    _native.tools().hipllm_tools_fill_normal(seed, stream, first, n, stddev, out.ctypes.data)
+    return out
+
+
+def uniform_ids(n: int, bound: int, seed: int, stream: int = 1) -> np.ndarray:
+    out = np.empty(n, dtype=np.int32)
+    _native.tools().hipllm_tools_fill_uniform_int(seed, stream, 0, n, bound, out.ctypes.data)
+    return out
+
+
+def row_bytes(qtype: int, cols: int) -> int:
+    rb = _native.tools().hipllm_tools_row_bytes(qtype, cols)
+    if rb == 0:
+        raise ValueError(f"{TYPE_NAMES.get(qtype, qtype)} cannot hold rows of {cols}")
+    return rb
+
+
+def quantize(w: np.ndarray, qtype: int, threads: int | None = None) -> np.ndarray:
+    """Quantizes a [rows, cols] float32 matrix into [rows, row_bytes] uint8."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    rb = row_bytes(qtype, cols)
+    out = np.empty((rows, rb), dtype=np.uint8)
+    threads = threads or min(16, os.cpu_count() or 1)
+    rc = _native.tools().hipllm_tools_quantize_rows(qtype, w.ctypes.data, rows, cols,
+                                                      out.ctypes.data, threads)
+    if rc != 0:
+        raise RuntimeError("quantization failed")
+    return out
+
+
+def random_quantized(rows: int, cols: int, qtype: int, seed: int, stddev: float = 0.02,
+                     threads: int | None = None) -> np.ndarray:
+    """N(0, stddev) weights quantized to qtype, generated in row slabs."""
+    rb = row_bytes(qtype, cols)
+    out = np.empty((rows, rb), dtype=np.uint8)
+    slab = max(1, (64 << 20) // (cols * 4))
+    for r0 in range(0, rows, slab):
+        r1 = min(rows, r0 + slab)
+        w = normal((r1 - r0) * cols, seed, stream=0x5EED, stddev=stddev, first=r0 * cols)
+        out[r0:r1] = quantize(w.reshape(r1 - r0, cols), qtype, threads)
+    return out
+
+
+def file_sha256(path) -> str:
+    h = hashlib.sha256()
+    with open(path, "rb") as f:
+        for chunk in iter(lambda: f.read(1 << 24), b""):
+            h.update(chunk)
+    return h.hexdigest()
