@@ -1,0 +1,184 @@
+/*
+ * HipLLM C ABI (libhipllm.so): the drop-in boundary of the MI355X backend.
+ *
+ * Two layers:
+ *  1. Kernel launchers. Caller-owned device pointers, a HIP stream passed as
+ *     `void*` (hipStream_t; NULL = default stream), no allocation, return a
+ *     status code. Each names the reference interface it replaces.
+ *  2. A handle API that mirrors the reference backends' class contract
+ *     (MetalLLM, metal_llm.h:20-52; CPULLM, cpu_llm.h:165-194) for bindings
+ *     and harnesses: create / reset / prefill / decode / config /
+ *     memory_stats / destroy.
+ *
+ * Status codes mirror the reference's exception types for the same
+ * conditions: HIPLLM_INVALID_ARGUMENT = std::invalid_argument,
+ * HIPLLM_OUT_OF_RANGE = std::out_of_range, HIPLLM_LENGTH_ERROR =
+ * std::length_error, HIPLLM_RUNTIME_ERROR = std::runtime_error,
+ * HIPLLM_OVERFLOW_ERROR = std::overflow_error. hipllm_last_error() returns the
+ * message of the calling thread's last failure.
+ *
+ * GGML type ids: 0 F32, 1 F16, 6 Q5_0, 8 Q8_0, 12 Q4_K, 14 Q6_K
+ * (metal_model.h:14-29). Quantized weights are passed in their native GGUF
+ * row layout; `row_bytes` is the byte stride between rows.
+ */
+#ifndef HIPLLM_H
+#define HIPLLM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    HIPLLM_OK = 0,
+    HIPLLM_INVALID_ARGUMENT = 1,
+    HIPLLM_OUT_OF_RANGE = 2,
+    HIPLLM_LENGTH_ERROR = 3,
+    HIPLLM_RUNTIME_ERROR = 4,
+    HIPLLM_OVERFLOW_ERROR = 5,
+};
+
+const char* hipllm_last_error(void);
+const char* hipllm_version(void);
+
+/* ---------------------------------------------------------------- kernels */
+
+/* Bit-exact FP32 dequantization of `rows` native rows of `k` values.
+ * Replaces GgufDequantizer::row (model.cpp:543-578). */
+int hipllm_dequant_rows(uint32_t type, const void* w, size_t row_bytes, size_t rows, size_t k, float* out,
+                        void* stream);
+
+/* Per-16 sums of x (k / 16 floats), the activation side-input of the GEMV. */
+int hipllm_prep_sums(const float* x, float* xs16, size_t k, void* stream);
+
+/* Workspace bytes hipllm_gemv needs for an input of k values. */
+size_t hipllm_gemv_workspace_bytes(size_t k);
+
+/* Decode GEMV y[n] = W[n, k] x[k] (+ bias[n]); `workspace` holds
+ * hipllm_gemv_workspace_bytes(k) bytes of device memory.
+ * Replaces metal_gevm_{q5_0,q8_0,q4_k,q6_k,f32} via encode_vector_product
+ * (metal_llm.metal:255-279, 708-781; metal_llm.mm:1891-1999) and CPULLM's
+ * gevmt / gevmtb (cpu_llm.cpp:512-547). */
+int hipllm_gemv(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* bias, float* y,
+                size_t n, size_t k, void* workspace, void* stream);
+
+/* GEMV with caller-supplied per-16 sums and an optional residual:
+ * y = W x (+ bias) (+ residual). rows_per_block 0 picks the default tiling
+ * (2, 4, 8, 16 or 32 are accepted). */
+int hipllm_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* xs16,
+                        const float* bias, const float* residual, float* y, size_t n, size_t k, int rows_per_block,
+                        void* stream);
+
+/* Fused FFN gate/up GEMV + SwiGLU: y = silu(Wg x) * (Wu x); ys16 (nullable,
+ * n % 16 == 0) receives the per-16 sums of y. Replaces the gate/up
+ * encode_vector_product pair + metal_swiglu_f32 (metal_llm.mm:2885-2894;
+ * metal_llm.metal:895-911), cpu_llm.cpp:905-909. */
+int hipllm_gemv_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
+                       const float* xs16, float* y, float* ys16, size_t n, size_t k, void* stream);
+
+/* Row RMSNorm y = x * (1/sqrt(mean(x^2) + eps) * gamma), double sum of
+ * squares; ys16 nullable. Replaces metal_rmsnorm_f32 (metal_llm.metal:785-823)
+ * and Vector::rmsnorm (cpu_llm.cpp:143-166). */
+int hipllm_rmsnorm(const float* x, const float* gamma, float* y, float* ys16, size_t rows, size_t cols, float eps,
+                   void* stream);
+
+/* out[t, :] = dequant(table[ids[t]]); out-of-range ids give zeros.
+ * Replaces metal_embedding_* (metal_llm.metal:1066-1162), embedding()
+ * (cpu_llm.cpp:101-123). */
+int hipllm_embed(uint32_t type, const void* table, size_t row_bytes, const int32_t* ids, size_t rows, size_t vocab,
+                 size_t cols, float* out, void* stream);
+
+/* NeoX RoPE on the Q and K heads of `rows` rows [Q | K | V] at positions
+ * pos0 + r, with a cos/sin table (float2 per position and pair); rotated K
+ * and V are written to the caches at those positions. Replaces
+ * metal_rope_heads_f32 + metal_kv_cache_write_f32 (metal_llm.metal:928-990),
+ * Vector::rope + cache append (cpu_llm.cpp:204-235, 874-886). */
+int hipllm_rope_kv(float* qkv, const float* cos_sin, size_t rot, size_t hq, size_t hkv, size_t d, size_t pos0,
+                   size_t rows, size_t row_stride, float* kcache, float* vcache, void* stream);
+
+/* Scratch floats hipllm_attn_decode needs for up to max_len positions. */
+size_t hipllm_attn_decode_scratch_floats(size_t hq, size_t d, size_t max_len);
+
+/* One-token GQA attention over positions [0, len) of the caches; out16
+ * nullable. Replaces metal_kv_cache_qk_f32 / metal_softmax_f32 /
+ * metal_kv_cache_av_f32 (metal_llm.metal:826-890, 995-1061) and the decode
+ * head loop (cpu_llm.cpp:893-906). */
+int hipllm_attn_decode(const float* q, const float* kcache, const float* vcache, float* out, float* out16,
+                       float* scratch, size_t hq, size_t hkv, size_t d, size_t len, float scale, void* stream);
+
+/* Scratch bytes hipllm_argmax needs for n values. */
+size_t hipllm_argmax_scratch_bytes(size_t n);
+
+/* *out = index of the first maximum of x[0..n) (ties -> lower index).
+ * Replaces metal_argmax_partial/finalize_f32 (metal_llm.metal:1544-1644),
+ * greedy_token (cpu_llm.cpp:34-48). */
+int hipllm_argmax(const float* x, size_t n, uint32_t* out, void* scratch, void* stream);
+
+/* y = silu(g) * u (reference sign-branched sigmoid); y16 nullable.
+ * Replaces metal_swiglu_f32 (metal_llm.metal:895-911). */
+int hipllm_swiglu(const float* g, const float* u, float* y, float* y16, size_t n, void* stream);
+
+/* ------------------------------------------------------------ handle API */
+
+typedef struct HipllmModel HipllmModel;
+
+typedef struct HipllmConfig {
+    uint64_t layer_count;
+    uint64_t embedding_size;
+    uint64_t feed_forward_size;
+    uint64_t attention_head_count;
+    uint64_t kv_head_count;
+    uint64_t head_size;
+    uint64_t rotary_dimension;
+    uint64_t vocabulary_size;
+    uint64_t context_length;
+    uint64_t parameter_count;
+    uint64_t stored_weight_bytes;
+    int32_t eos_token_id;
+    float rope_theta;
+    float norm_epsilon;
+    char architecture[32];
+} HipllmConfig;
+
+typedef struct HipllmMemoryStats {
+    uint64_t weight_bytes;
+    uint64_t kv_cache_bytes;
+    uint64_t recurrent_state_bytes;
+    uint64_t intermediate_bytes;
+    int32_t intermediate_is_estimate;
+} HipllmMemoryStats;
+
+/* Parses a GGUF file with the streaming raw-tensor reader and derives the
+ * model config, without touching a GPU. Replaces MetalRawModel's header
+ * parsing + initialize_config (metal_model.cpp:451-688), as used by the
+ * CLI's architecture probe (chat.cpp:1021-1024). */
+int hipllm_inspect_gguf(const char* gguf_path, HipllmConfig* out);
+
+/* MetalLLM(gguf_path, max_sequence) (metal_llm.h:22-24); device < 0 keeps
+ * the current HIP device. */
+int hipllm_create(const char* gguf_path, size_t max_sequence, int device, HipllmModel** out);
+void hipllm_destroy(HipllmModel* model);
+int hipllm_reset(HipllmModel* model);
+int hipllm_prefill(HipllmModel* model, const int32_t* ids, size_t count, int32_t* next_token);
+int hipllm_decode(HipllmModel* model, int32_t id, int32_t* next_token);
+int hipllm_config(const HipllmModel* model, HipllmConfig* out);
+size_t hipllm_position(const HipllmModel* model);
+size_t hipllm_max_sequence(const HipllmModel* model);
+int hipllm_uses_gpu(const HipllmModel* model);
+int hipllm_memory_stats(const HipllmModel* model, HipllmMemoryStats* out);
+const char* hipllm_device_name(const HipllmModel* model);
+int hipllm_enable_profiling(HipllmModel* model, const char* csv_path);
+int hipllm_disable_profiling(HipllmModel* model);
+/* Logits of the last prefill/decode (vocabulary_size floats, host memory). */
+int hipllm_copy_logits(const HipllmModel* model, float* out, size_t count);
+/* 1 = batched prefill kernels, 0 = token-serial prefill through the decode
+ * path (both produce the same next token within FP32 tolerance). */
+int hipllm_set_batched_prefill(HipllmModel* model, int enabled);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HIPLLM_H */

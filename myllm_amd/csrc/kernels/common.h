@@ -1,0 +1,135 @@
+// Device-side helpers shared by the HipLLM kernels (gfx950 / CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hipllm {
+
+// GGML type ids (GGUF format, metal_model.h:14-29).
+enum : uint32_t {
+    kF32 = 0,
+    kF16 = 1,
+    kQ5_0 = 6,
+    kQ8_0 = 8,
+    kQ4_K = 12,
+    kQ6_K = 14,
+};
+
+// Status codes shared with the C ABI; they mirror the reference's exception
+// types (std::invalid_argument, out_of_range, length_error, runtime_error,
+// overflow_error).
+enum : int {
+    kOk = 0,
+    kInvalidArgument = 1,
+    kOutOfRange = 2,
+    kLengthError = 3,
+    kRuntimeError = 4,
+    kOverflowError = 5,
+};
+
+__host__ __device__ constexpr uint32_t block_elems(uint32_t type) {
+    return type == kQ4_K || type == kQ6_K ? 256u : (type == kQ5_0 || type == kQ8_0) ? 32u : 1u;
+}
+
+__host__ __device__ constexpr uint32_t block_bytes(uint32_t type) {
+    return type == kQ4_K ? 144u : type == kQ6_K ? 210u : type == kQ5_0 ? 22u
+         : type == kQ8_0 ? 34u : type == kF16 ? 2u : 4u;
+}
+
+// Exact binary16 -> binary32, same results as the reference's half_to_float
+// (model.cpp:500-522) including subnormals, infinities and a canonical quiet
+// NaN. Built from integer operations so no rounding mode can interfere.
+__device__ __forceinline__ float half_bits_to_float_exact(uint32_t h) {
+    const uint32_t sign = (h >> 15) & 1u;
+    const uint32_t exponent = (h >> 10) & 0x1fu;
+    const uint32_t mantissa = h & 0x3ffu;
+    uint32_t bits;
+    if (exponent == 0) {
+        if (mantissa == 0) {
+            bits = sign << 31;
+        } else {
+            // value = mantissa * 2^-24; normalise the 10-bit mantissa.
+            const int lead = 31 - __builtin_clz(mantissa);  // 0..9
+            const uint32_t e = static_cast<uint32_t>(lead - 24 + 127);
+            const uint32_t m = (mantissa << (23 - lead)) & 0x7fffffu;
+            bits = (sign << 31) | (e << 23) | m;
+        }
+    } else if (exponent == 31) {
+        bits = mantissa == 0 ? ((sign << 31) | 0x7f800000u) : 0x7fc00000u;
+    } else {
+        bits = (sign << 31) | ((exponent + 112u) << 23) | (mantissa << 13);
+    }
+    return __uint_as_float(bits);
+}
+
+// Hardware conversion (v_cvt_f32_f16); identical to the exact form for every
+// finite or infinite input, used on the GEMV hot path.
+__device__ __forceinline__ float half_lo(uint32_t w) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xffffu)));
+}
+__device__ __forceinline__ float half_hi(uint32_t w) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+}
+
+// Byte-granular little-endian loads from 2-byte-aligned addresses, built from
+// naturally aligned dword loads and v_alignbyte. `p` must be 2-byte aligned and
+// the dwords touched must be in bounds (device weight buffers carry padding).
+__device__ __forceinline__ uint32_t load_u32_a2(const uint8_t* p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+    const uint32_t shift = static_cast<uint32_t>(a & 3u);
+    const uint32_t lo = q[0];
+    const uint32_t hi = q[1];
+    return __builtin_amdgcn_alignbyte(hi, lo, shift);
+}
+
+__device__ __forceinline__ uint2 load_u64_a2(const uint8_t* p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+    const uint32_t shift = static_cast<uint32_t>(a & 3u);
+    const uint32_t w0 = q[0], w1 = q[1], w2 = q[2];
+    return make_uint2(__builtin_amdgcn_alignbyte(w1, w0, shift),
+                      __builtin_amdgcn_alignbyte(w2, w1, shift));
+}
+
+__device__ __forceinline__ uint4 load_u128_a2(const uint8_t* p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+    const uint32_t shift = static_cast<uint32_t>(a & 3u);
+    const uint32_t w0 = q[0], w1 = q[1], w2 = q[2], w3 = q[3], w4 = q[4];
+    return make_uint4(__builtin_amdgcn_alignbyte(w1, w0, shift),
+                      __builtin_amdgcn_alignbyte(w2, w1, shift),
+                      __builtin_amdgcn_alignbyte(w3, w2, shift),
+                      __builtin_amdgcn_alignbyte(w4, w3, shift));
+}
+
+__device__ __forceinline__ uint32_t load_u16_a2(const uint8_t* p) {
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+
+// Unsigned byte k of a dword as float; the backend selects v_cvt_f32_ubyte{0..3}.
+__device__ __forceinline__ float ubyte0(uint32_t w) { return static_cast<float>((w >> 0) & 0xffu); }
+__device__ __forceinline__ float ubyte1(uint32_t w) { return static_cast<float>((w >> 8) & 0xffu); }
+__device__ __forceinline__ float ubyte2(uint32_t w) { return static_cast<float>((w >> 16) & 0xffu); }
+__device__ __forceinline__ float ubyte3(uint32_t w) { return static_cast<float>((w >> 24) & 0xffu); }
+
+__device__ __forceinline__ float warp_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ float warp_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ __forceinline__ double warp_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+}  // namespace hipllm

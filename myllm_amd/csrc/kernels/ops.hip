@@ -1,0 +1,387 @@
+// Decode-path operators around the GEMV: RMSNorm, embedding gather, RoPE +
+// KV-cache write, GQA attention over the device KV cache, argmax.
+//
+// Reference semantics (file:line):
+//   RMSNorm      cpu_llm.cpp:143-166 (double sum of squares; x *= inv * g)
+//   embedding    cpu_llm.cpp:101-123, metal_llm.metal:1066-1162
+//   RoPE (NeoX)  cpu_llm.cpp:204-235; K is cached after rotation (874-886)
+//   attention    cpu_llm.cpp:490-510 (scores * (1/sqrt(D))), 168-186 (softmax),
+//                453-467 (p . V); GQA head map h / (Hq / Hkv) (897-905)
+//   argmax       cpu_llm.cpp:34-48 (first maximum), metal_llm.metal:1544-1644
+#include "formats.h"
+
+namespace hipllm {
+namespace {
+
+// ------------------------------------------------------------ RMSNorm
+// One block per row. y = x * (inv_rms * gamma) with inv_rms from a double
+// sum of squares, as CPULLM. Optionally writes per-16 sums of y (xs16) for
+// the GEMV that consumes y.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
+                                                      float* __restrict__ y, float* __restrict__ ys16, uint32_t cols,
+                                                      float eps) {
+    const uint32_t row = blockIdx.x;
+    const float* xr = x + static_cast<size_t>(row) * cols;
+    float* yr = y + static_cast<size_t>(row) * cols;
+    double ss = 0.0;
+    for (uint32_t i = threadIdx.x; i < cols; i += blockDim.x) {
+        const double v = xr[i];
+        ss += v * v;
+    }
+    ss = warp_sum_d(ss);
+    __shared__ double part[8];
+    __shared__ float inv_s;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) part[wave] = ss;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (uint32_t w = 0; w < (blockDim.x + 63) / 64; ++w) t += part[w];
+        const float ms = static_cast<float>(t / static_cast<double>(cols));
+        inv_s = 1.0f / sqrtf(ms + eps);
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    // 16 consecutive elements per thread-step so the same thread also forms
+    // the per-16 sum.
+    const uint32_t groups = cols / 16;
+    for (uint32_t g = threadIdx.x; g < groups; g += blockDim.x) {
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t c = 16 * g + i;
+            const float v = xr[c] * (inv * gamma[c]);
+            yr[c] = v;
+            s += v;
+        }
+        if (ys16) ys16[static_cast<size_t>(row) * groups + g] = s;
+    }
+    for (uint32_t c = groups * 16 + threadIdx.x; c < cols; c += blockDim.x) yr[c] = xr[c] * (inv * gamma[c]);
+}
+
+// ------------------------------------------------------------ embedding
+
+__global__ void embed_kernel(uint32_t type, const uint8_t* __restrict__ table, size_t row_bytes,
+                             const int32_t* __restrict__ ids, uint32_t vocab, uint32_t cols,
+                             float* __restrict__ out) {
+    const uint32_t t = blockIdx.y;
+    const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= cols) return;
+    const int32_t id = ids[t];
+    float v = 0.0f;
+    if (id >= 0 && static_cast<uint32_t>(id) < vocab) {
+        v = dequant_element(type, table + static_cast<size_t>(id) * row_bytes, c);
+    }
+    out[static_cast<size_t>(t) * cols + c] = v;
+}
+
+// ------------------------------------------------------------ RoPE + KV
+// qkv rows hold [Q (Hq*D) | K (Hkv*D) | V (Hkv*D)] with biases applied. Row r
+// is at absolute position pos0 + r. Rotates Q and K in place with the
+// host-built table (cos, sin per position and pair, computed exactly as
+// CPULLM computes them), stores rotated K and V into the caches at row
+// pos0 + r, and leaves rotated Q in place.
+#pragma clang fp contract(off)
+__global__ void rope_kv_kernel(float* __restrict__ qkv, const float2* __restrict__ table, uint32_t half_rot,
+                               uint32_t hq, uint32_t hkv, uint32_t d, uint32_t pos0, uint32_t row_stride,
+                               float* __restrict__ kcache, float* __restrict__ vcache) {
+    const uint32_t r = blockIdx.x;
+    float* row = qkv + static_cast<size_t>(r) * row_stride;
+    const uint32_t pos = pos0 + r;
+    const uint32_t kvd = hkv * d;
+    const float2* tab = table + static_cast<size_t>(pos) * half_rot;
+    const uint32_t heads = hq + hkv;
+    const uint32_t half = d / 2;
+    for (uint32_t i = threadIdx.x; i < heads * half; i += blockDim.x) {
+        const uint32_t h = i / half;
+        const uint32_t p = i % half;
+        float* base = row + h * d;  // Q heads then K heads are contiguous
+        if (p < half_rot) {
+            const float2 cs = tab[p];
+            const float a = base[p];
+            const float b = base[p + half_rot];
+            const float t1 = a * cs.x;
+            const float t2 = b * cs.y;
+            const float t3 = a * cs.y;
+            const float t4 = b * cs.x;
+            base[p] = t1 - t2;
+            base[p + half_rot] = t3 + t4;
+        }
+    }
+    __syncthreads();
+    float* kc = kcache + static_cast<size_t>(pos) * kvd;
+    float* vc = vcache + static_cast<size_t>(pos) * kvd;
+    for (uint32_t i = threadIdx.x; i < kvd; i += blockDim.x) {
+        kc[i] = row[hq * d + i];
+        vc[i] = row[hq * d + kvd + i];
+    }
+}
+#pragma clang fp contract(fast)
+
+// ------------------------------------------------------------ attention
+// Split-K decode attention (flash-decode). Phase 1: block (head, chunk) scores
+// keys [chunk*C, min(len, chunk*C + C)) against its query, and writes the
+// chunk's running max m, sum of exp l, and unnormalised p.V (D floats).
+// Phase 2: one block per head merges the chunks and writes the head output,
+// plus per-16 sums of the whole output vector for the next GEMV.
+constexpr uint32_t kAttnChunk = 256;
+
+__global__ __launch_bounds__(256) void attn_decode_partial(const float* __restrict__ q, const float* __restrict__ kcache,
+                                                           const float* __restrict__ vcache, float* __restrict__ part,
+                                                           uint32_t hq, uint32_t hkv, uint32_t d, uint32_t len,
+                                                           float scale, uint32_t nchunks) {
+    const uint32_t h = blockIdx.x;
+    const uint32_t chunk = blockIdx.y;
+    const uint32_t g = h / (hq / hkv);
+    const uint32_t kvd = hkv * d;
+    const uint32_t t0 = chunk * kAttnChunk;
+    const uint32_t t1 = min(len, t0 + kAttnChunk);
+    __shared__ float qs[256];
+    __shared__ float ps[kAttnChunk];
+    __shared__ float red[8];
+    for (uint32_t i = threadIdx.x; i < d; i += blockDim.x) qs[i] = q[h * d + i];
+    __syncthreads();
+    const uint32_t t = t0 + threadIdx.x;
+    float s = -INFINITY;
+    if (t < t1) {
+        const float4* k = reinterpret_cast<const float4*>(kcache + static_cast<size_t>(t) * kvd + g * d);
+        float dot = 0.0f;
+        for (uint32_t i = 0; i < d / 4; ++i) {
+            const float4 kv = k[i];
+            dot = fmaf(kv.x, qs[4 * i], dot);
+            dot = fmaf(kv.y, qs[4 * i + 1], dot);
+            dot = fmaf(kv.z, qs[4 * i + 2], dot);
+            dot = fmaf(kv.w, qs[4 * i + 3], dot);
+        }
+        s = dot * scale;
+    }
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float m = warp_max(s);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float p = t < t1 ? expf(s - m) : 0.0f;
+    ps[threadIdx.x] = p;
+    float l = warp_sum(p);
+    __syncthreads();
+    if (lane == 0) red[4 + wave] = l;
+    __syncthreads();
+    l = (red[4] + red[5]) + (red[6] + red[7]);
+    float* out = part + (static_cast<size_t>(h) * nchunks + chunk) * (d + 2);
+    for (uint32_t i = threadIdx.x; i < d; i += blockDim.x) {
+        const float* v = vcache + static_cast<size_t>(t0) * kvd + g * d + i;
+        float acc = 0.0f;
+        for (uint32_t tt = 0; tt < t1 - t0; ++tt) acc = fmaf(ps[tt], v[static_cast<size_t>(tt) * kvd], acc);
+        out[2 + i] = acc;
+    }
+    if (threadIdx.x == 0) {
+        out[0] = m;
+        out[1] = l;
+    }
+}
+
+__global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict__ part, float* __restrict__ out,
+                                                         float* __restrict__ out16, uint32_t d, uint32_t nchunks) {
+    const uint32_t h = blockIdx.x;
+    const float* ph = part + static_cast<size_t>(h) * nchunks * (d + 2);
+    float M = -INFINITY;
+    for (uint32_t c = 0; c < nchunks; ++c) M = fmaxf(M, ph[c * (d + 2)]);
+    float L = 0.0f;
+    for (uint32_t c = 0; c < nchunks; ++c) L += ph[c * (d + 2) + 1] * expf(ph[c * (d + 2)] - M);
+    const float invL = 1.0f / L;
+    __shared__ float vals[256];
+    for (uint32_t i = threadIdx.x; i < d; i += blockDim.x) {
+        float acc = 0.0f;
+        for (uint32_t c = 0; c < nchunks; ++c) acc += ph[c * (d + 2) + 2 + i] * expf(ph[c * (d + 2)] - M);
+        const float v = acc * invL;
+        out[h * d + i] = v;
+        vals[i] = v;
+    }
+    __syncthreads();
+    if (out16) {
+        for (uint32_t gI = threadIdx.x; gI < d / 16; gI += blockDim.x) {
+            float s = 0.0f;
+            for (int i = 0; i < 16; ++i) s += vals[16 * gI + i];
+            out16[h * (d / 16) + gI] = s;
+        }
+    }
+}
+
+// ------------------------------------------------------------ argmax
+// Ties resolve to the lower index; NaN never wins (strict '>').
+__device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+__device__ void block_argmax(float& bv, uint32_t& bi) {
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const uint32_t oi = __shfl_xor(bi, o);
+        if (better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    __shared__ float sv[16];
+    __shared__ uint32_t si[16];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) {
+        sv[wave] = bv;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (uint32_t w = 1; w < blockDim.x / 64; ++w) {
+            if (better(sv[w], si[w], bv, bi)) {
+                bv = sv[w];
+                bi = si[w];
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_partial(const float* __restrict__ x, uint32_t n, uint32_t per_block,
+                                                      float* __restrict__ pv, uint32_t* __restrict__ pi) {
+    const uint32_t b0 = blockIdx.x * per_block;
+    const uint32_t b1 = min(n, b0 + per_block);
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+    for (uint32_t i = b0 + threadIdx.x; i < b1; i += blockDim.x) {
+        const float v = x[i];
+        if (better(v, i, bv, bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+    block_argmax(bv, bi);
+    if (threadIdx.x == 0) {
+        pv[blockIdx.x] = bv;
+        pi[blockIdx.x] = bi;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_final(const float* __restrict__ pv, const uint32_t* __restrict__ pi,
+                                                    uint32_t parts, uint32_t* __restrict__ out) {
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+    for (uint32_t i = threadIdx.x; i < parts; i += blockDim.x) {
+        if (better(pv[i], pi[i], bv, bi)) {
+            bv = pv[i];
+            bi = pi[i];
+        }
+    }
+    block_argmax(bv, bi);
+    if (threadIdx.x == 0) out[0] = bi;
+}
+
+// ------------------------------------------------------------ elementwise
+// y = silu(g) * u with the reference's sign-branched sigmoid
+// (cpu_llm.cpp:188-202); optional per-16 sums of y.
+__global__ void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ y,
+                              float* __restrict__ y16, uint32_t n) {
+    const uint32_t grp = blockIdx.x * blockDim.x + threadIdx.x;
+    if (grp * 16 >= n) return;
+    float s = 0.0f;
+    for (uint32_t i = 16 * grp; i < min(n, 16 * grp + 16); ++i) {
+        const float gate = g[i];
+        const float sig = gate >= 0.0f ? 1.0f / (1.0f + expf(-gate)) : expf(gate) / (1.0f + expf(gate));
+        const float v = gate * sig * u[i];
+        y[i] = v;
+        s += v;
+    }
+    if (y16) y16[grp] = s;
+}
+
+__global__ void add_kernel(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ y, size_t n) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = a[i] + b[i];
+}
+
+}  // namespace
+
+int launch_rmsnorm(const float* x, const float* gamma, float* y, float* ys16, size_t rows, size_t cols, float eps,
+                   hipStream_t stream) {
+    if (!x || !gamma || !y || rows == 0 || cols == 0) return kInvalidArgument;
+    if (ys16 && cols % 16 != 0) return kInvalidArgument;
+    if (!(eps > 0.0f)) return kInvalidArgument;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, stream, x, gamma, y, ys16,
+                       static_cast<uint32_t>(cols), eps);
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+int launch_embed(uint32_t type, const void* table, size_t row_bytes, const int32_t* ids, size_t rows, size_t vocab,
+                 size_t cols, float* out, hipStream_t stream) {
+    if (!table || !ids || !out || rows == 0 || cols == 0 || vocab == 0) return kInvalidArgument;
+    if (cols % block_elems(type) != 0) return kInvalidArgument;
+    const dim3 grid(static_cast<uint32_t>((cols + 255) / 256), static_cast<uint32_t>(rows));
+    hipLaunchKernelGGL(embed_kernel, grid, dim3(256), 0, stream, type, static_cast<const uint8_t*>(table), row_bytes,
+                       ids, static_cast<uint32_t>(vocab), static_cast<uint32_t>(cols), out);
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+int launch_rope_kv(float* qkv, const float* cos_sin, size_t rot, size_t hq, size_t hkv, size_t d, size_t pos0,
+                   size_t rows, size_t row_stride, float* kcache, float* vcache, hipStream_t stream) {
+    if (!qkv || !cos_sin || !kcache || !vcache || rows == 0 || d == 0 || rot == 0 || rot > d || rot % 2) {
+        return kInvalidArgument;
+    }
+    if (hq == 0 || hkv == 0 || hq % hkv != 0 || row_stride < (hq + 2 * hkv) * d) return kInvalidArgument;
+    hipLaunchKernelGGL(rope_kv_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, stream, qkv,
+                       reinterpret_cast<const float2*>(cos_sin), static_cast<uint32_t>(rot / 2),
+                       static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv), static_cast<uint32_t>(d),
+                       static_cast<uint32_t>(pos0), static_cast<uint32_t>(row_stride), kcache, vcache);
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+size_t attn_decode_scratch_floats(size_t hq, size_t d, size_t max_len) {
+    const size_t chunks = (max_len + kAttnChunk - 1) / kAttnChunk;
+    return hq * chunks * (d + 2);
+}
+
+int launch_attn_decode(const float* q, const float* kcache, const float* vcache, float* out, float* out16,
+                       float* scratch, size_t hq, size_t hkv, size_t d, size_t len, float scale, hipStream_t stream) {
+    if (!q || !kcache || !vcache || !out || !scratch || len == 0 || hq == 0 || hkv == 0 || hq % hkv) {
+        return kInvalidArgument;
+    }
+    if (d == 0 || d > 256 || d % 16 != 0) return kInvalidArgument;
+    const uint32_t nchunks = static_cast<uint32_t>((len + kAttnChunk - 1) / kAttnChunk);
+    hipLaunchKernelGGL(attn_decode_partial, dim3(static_cast<uint32_t>(hq), nchunks), dim3(256), 0, stream, q, kcache,
+                       vcache, scratch, static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv),
+                       static_cast<uint32_t>(d), static_cast<uint32_t>(len), scale, nchunks);
+    hipLaunchKernelGGL(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out, out16,
+                       static_cast<uint32_t>(d), nchunks);
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+constexpr uint32_t kArgmaxPerBlock = 2048;
+
+size_t argmax_scratch_bytes(size_t n) {
+    const size_t parts = (n + kArgmaxPerBlock - 1) / kArgmaxPerBlock;
+    return parts * 8;
+}
+
+int launch_argmax(const float* x, size_t n, uint32_t* out, void* scratch, hipStream_t stream) {
+    if (!x || !out || !scratch || n == 0 || n > 0xffffffffull) return kInvalidArgument;
+    const uint32_t parts = static_cast<uint32_t>((n + kArgmaxPerBlock - 1) / kArgmaxPerBlock);
+    float* pv = static_cast<float*>(scratch);
+    uint32_t* pi = reinterpret_cast<uint32_t*>(pv + parts);
+    hipLaunchKernelGGL(argmax_partial, dim3(parts), dim3(256), 0, stream, x, static_cast<uint32_t>(n),
+                       kArgmaxPerBlock, pv, pi);
+    hipLaunchKernelGGL(argmax_final, dim3(1), dim3(256), 0, stream, pv, pi, parts, out);
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+int launch_swiglu(const float* g, const float* u, float* y, float* y16, size_t n, hipStream_t stream) {
+    if (!g || !u || !y || n == 0 || (y16 && n % 16 != 0)) return kInvalidArgument;
+    const uint32_t groups = static_cast<uint32_t>((n + 15) / 16);
+    hipLaunchKernelGGL(swiglu_kernel, dim3((groups + 255) / 256), dim3(256), 0, stream, g, u, y, y16,
+                       static_cast<uint32_t>(n));
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+int launch_add(const float* a, const float* b, float* y, size_t n, hipStream_t stream) {
+    if (!a || !b || !y || n == 0) return kInvalidArgument;
+    hipLaunchKernelGGL(add_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, stream, a, b, y, n);
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+}  // namespace hipllm

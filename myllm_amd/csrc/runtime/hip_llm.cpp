@@ -1,0 +1,614 @@
+// HipLLM implementation: weight upload, device state, and the per-token
+// graph of HIP kernels (see hip_llm.h).
+//
+// Per decode token (MetalLLM::decode, metal_llm.mm:3295-3385; layer graph
+// cpu_llm.cpp:843-914), all on one stream:
+//   embed -> L x [ rmsnorm(+xs16) -> QKV GEMV(+bias) -> RoPE + KV write
+//                  -> attention(+xs16) -> O GEMV(+residual)
+//                  -> rmsnorm(+xs16) -> gate/up GEMV + SwiGLU(+xs16)
+//                  -> down GEMV(+residual) ]
+//   -> rmsnorm(+xs16) -> LM-head GEMV -> argmax -> 4-byte readback.
+#include "hip_llm.h"
+
+#include "../kernels/common.h"
+#include "../kernels/launch.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <stdexcept>
+
+namespace llm {
+namespace {
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+void launch_check(int status, const char* what) {
+    if (status == hipllm::kOk) return;
+    if (status == hipllm::kInvalidArgument) throw std::invalid_argument(std::string(what) + ": invalid kernel arguments");
+    if (status == hipllm::kLengthError) throw std::length_error(std::string(what) + ": shape exceeds kernel limits");
+    throw std::runtime_error(std::string(what) + ": kernel launch failed: " + hipGetErrorString(hipGetLastError()));
+}
+
+std::size_t align_up(std::size_t v, std::size_t a) { return (v + a - 1) / a * a; }
+
+struct DevMatrix {
+    const std::uint8_t* ptr = nullptr;
+    std::uint32_t type = 0;
+    std::size_t rows = 0;
+    std::size_t cols = 0;
+    std::size_t row_bytes = 0;
+};
+
+struct DevLayer {
+    const float* attn_norm = nullptr;
+    DevMatrix q, k, v;          // q/k/v are contiguous when fused_qkv
+    bool fused_qkv = false;
+    const float* qkv_bias = nullptr;  // [bq | bk | bv]
+    DevMatrix o;
+    const float* ffn_norm = nullptr;
+    DevMatrix gate, up, down;
+    bool fused_gate_up = false;
+};
+
+// Device activation buffers (one token row; the serial prefill reuses them).
+struct Activations {
+    float* hidden[2] = {nullptr, nullptr};
+    float* norm = nullptr;
+    float* norm16 = nullptr;
+    float* qkv = nullptr;
+    float* attn = nullptr;
+    float* attn16 = nullptr;
+    float* ffn = nullptr;
+    float* ffn16 = nullptr;
+    float* gate_tmp = nullptr;
+    float* logits = nullptr;
+    float* attn_scratch = nullptr;
+    void* argmax_scratch = nullptr;
+    std::int32_t* ids = nullptr;
+    std::uint32_t* token = nullptr;
+};
+
+}  // namespace
+
+struct HipLLM::Impl {
+    int device = 0;
+    std::string device_name;
+    hipStream_t stream = nullptr;
+    ModelConfig config;
+    std::size_t max_sequence = 0;
+    std::size_t sequence_length = 0;
+    bool batched_prefill = false;
+
+    std::uint8_t* weight_arena = nullptr;
+    std::size_t weight_bytes = 0;  // sum of GGUF tensor payloads
+    DevMatrix embedding, output;
+    const float* output_norm = nullptr;
+    std::vector<DevLayer> layers;
+
+    float* kv_arena = nullptr;
+    std::size_t kv_cache_bytes = 0;
+    std::size_t kv_dim = 0;
+    float* rope_table = nullptr;
+
+    void* act_arena = nullptr;
+    std::size_t act_bytes = 0;
+    Activations act;
+    std::size_t prompt_capacity = 0;
+
+    std::int32_t* host_ids = nullptr;      // pinned
+    std::uint32_t* host_token = nullptr;   // pinned
+
+    std::FILE* profile = nullptr;
+
+    ~Impl() {
+        if (stream) hipStreamSynchronize(stream);
+        if (profile) std::fclose(profile);
+        if (weight_arena) hipFree(weight_arena);
+        if (kv_arena) hipFree(kv_arena);
+        if (rope_table) hipFree(rope_table);
+        if (act_arena) hipFree(act_arena);
+        if (host_ids) hipHostFree(host_ids);
+        if (host_token) hipHostFree(host_token);
+        if (stream) hipStreamDestroy(stream);
+    }
+
+    float* kcache(std::size_t layer) const { return kv_arena + (2 * layer) * max_sequence * kv_dim; }
+    float* vcache(std::size_t layer) const { return kv_arena + (2 * layer + 1) * max_sequence * kv_dim; }
+
+    void load(const std::string& path, std::size_t capacity, int dev);
+    void upload(GgufReader& reader);
+    void allocate_state();
+    void build_rope_table();
+    void ensure_prompt_capacity(std::size_t n);
+
+    void gemv(const DevMatrix& w, const float* x, const float* xs16, const float* bias, const float* residual,
+              float* y, std::size_t rows_override = 0) const;
+    void layer_step(std::size_t li, std::size_t pos, float* hidden, float* next_hidden);
+    void token_step(const std::int32_t* device_id, std::size_t pos, bool head);
+    std::int32_t read_token();
+};
+
+void HipLLM::Impl::load(const std::string& path, std::size_t capacity, int dev) {
+    int count = 0;
+    hip_check(hipGetDeviceCount(&count), "hipGetDeviceCount");
+    if (count <= 0) throw std::runtime_error("no HIP device is available");
+    if (dev < 0) hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev >= count) throw std::invalid_argument("HIP device index is outside the visible devices");
+    device = dev;
+    hip_check(hipSetDevice(device), "hipSetDevice");
+    hipDeviceProp_t prop;
+    hip_check(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    device_name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+    hip_check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
+
+    GgufReader reader(path);
+    ModelConfig cfg = reader.config();
+    if (cfg.architecture != "qwen2") {
+        throw std::runtime_error("HipLLM supports qwen2 GGUF models, got " + cfg.architecture);
+    }
+    if (cfg.layer_count == 0 || cfg.embedding_size == 0 || cfg.feed_forward_size == 0 ||
+        cfg.attention_head_count == 0 || cfg.kv_head_count == 0 || cfg.head_size == 0 ||
+        cfg.vocabulary_size == 0 || cfg.context_length == 0) {
+        throw std::runtime_error("HIP model metadata is incomplete");
+    }
+    if (capacity == 0) capacity = cfg.context_length;
+    if (capacity > cfg.context_length) {
+        throw std::invalid_argument("HIP maximum sequence exceeds the model context length");
+    }
+    if (cfg.embedding_size % 16 != 0 || cfg.feed_forward_size % 16 != 0 || cfg.head_size % 16 != 0 ||
+        cfg.head_size > 256) {
+        throw std::invalid_argument("HIP kernels need hidden, FFN and head sizes that are multiples of 16 "
+                                    "(head size at most 256)");
+    }
+    config = std::move(cfg);
+    max_sequence = capacity;
+    upload(reader);
+    allocate_state();
+    build_rope_table();
+}
+
+void HipLLM::Impl::upload(GgufReader& reader) {
+    const ModelConfig& c = config;
+    const std::size_t H = c.embedding_size, F = c.feed_forward_size, V = c.vocabulary_size;
+    kv_dim = c.kv_head_count * c.head_size;
+
+    // Plan: every tensor is taken (shape-checked, consumed once) up front so
+    // the arena layout is known; Q/K/V weights (and gate/up) are placed back
+    // to back when their formats match, so one GEMV covers them.
+    struct Item {
+        TensorDescriptor t;
+        std::size_t offset = 0;
+    };
+    std::vector<Item> items;
+    std::size_t cursor = 0;
+    auto place = [&](const std::string& name, std::size_t rows, std::size_t cols, bool contiguous) {
+        Item it;
+        it.t = reader.take(name, rows, cols);
+        cursor = contiguous ? cursor : align_up(cursor, 256);
+        it.offset = cursor;
+        cursor += it.t.byte_size;
+        items.push_back(it);
+        return items.size() - 1;
+    };
+    auto require_f32 = [&](std::size_t idx) {
+        if (items[idx].t.type != GgmlType::F32) {
+            throw std::invalid_argument("HIP norm and bias tensors must be F32: " + items[idx].t.name);
+        }
+    };
+    auto supported = [&](std::size_t idx) {
+        const GgmlType t = items[idx].t.type;
+        if (t != GgmlType::F32 && t != GgmlType::F16 && t != GgmlType::Q5_0 && t != GgmlType::Q8_0 &&
+            t != GgmlType::Q4_K && t != GgmlType::Q6_K) {
+            throw std::invalid_argument(std::string("HIP backend does not support ") + ggml_type_name(t) +
+                                        " weights: " + items[idx].t.name);
+        }
+    };
+    const std::size_t i_embd = place("token_embd.weight", V, H, false);
+    const std::size_t i_onorm = place("output_norm.weight", 1, H, false);
+    const std::size_t i_out = place("output.weight", V, H, false);
+    supported(i_embd);
+    supported(i_out);
+    require_f32(i_onorm);
+    struct LayerIdx {
+        std::size_t an, q, k, v, bq, bk, bv, o, fn, g, u, d;
+        bool fused_qkv, fused_gu;
+    };
+    std::vector<LayerIdx> li(c.layer_count);
+    for (std::size_t l = 0; l < c.layer_count; ++l) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        const TensorDescriptor tq = reader.take(p + "attn_q.weight", H, H);
+        LayerIdx& x = li[l];
+        // Peek formats of K/V to decide fusion before placing.
+        x.an = place(p + "attn_norm.weight", 1, H, false);
+        Item iq;
+        iq.t = tq;
+        cursor = align_up(cursor, 256);
+        iq.offset = cursor;
+        cursor += tq.byte_size;
+        items.push_back(iq);
+        x.q = items.size() - 1;
+        x.k = place(p + "attn_k.weight", kv_dim, H, true);
+        x.v = place(p + "attn_v.weight", kv_dim, H, true);
+        x.fused_qkv = items[x.k].t.type == tq.type && items[x.v].t.type == tq.type &&
+                      items[x.k].offset == items[x.q].offset + tq.byte_size &&
+                      items[x.v].offset == items[x.k].offset + items[x.k].t.byte_size;
+        if (!x.fused_qkv) {
+            // Re-align K and V on their own.
+            cursor = items[x.k].offset;
+            cursor = align_up(cursor, 256);
+            items[x.k].offset = cursor;
+            cursor += items[x.k].t.byte_size;
+            cursor = align_up(cursor, 256);
+            items[x.v].offset = cursor;
+            cursor += items[x.v].t.byte_size;
+        }
+        x.bq = place(p + "attn_q.bias", 1, H, false);
+        x.bk = place(p + "attn_k.bias", 1, kv_dim, true);
+        x.bv = place(p + "attn_v.bias", 1, kv_dim, true);
+        x.o = place(p + "attn_output.weight", H, H, false);
+        x.fn = place(p + "ffn_norm.weight", 1, H, false);
+        x.g = place(p + "ffn_gate.weight", F, H, false);
+        x.u = place(p + "ffn_up.weight", F, H, false);
+        x.d = place(p + "ffn_down.weight", H, F, false);
+        x.fused_gu = items[x.g].t.type == items[x.u].t.type;
+        for (std::size_t idx : {x.an, x.bq, x.bk, x.bv, x.fn}) require_f32(idx);
+        for (std::size_t idx : {x.q, x.k, x.v, x.o, x.g, x.u, x.d}) supported(idx);
+    }
+    reader.validate_all_consumed();
+
+    std::size_t total = 0;
+    for (const Item& it : items) total += it.t.byte_size;
+    if (total != c.stored_weight_bytes) {
+        throw std::runtime_error("HIP uploaded weight bytes do not match GGUF tensor bytes");
+    }
+    weight_bytes = total;
+    // Tail padding: realigned dword reads of 2-byte-aligned blocks may touch
+    // up to 16 bytes past a tensor's last byte.
+    const std::size_t arena_bytes = align_up(cursor, 256) + 4096;
+    hip_check(hipMalloc(reinterpret_cast<void**>(&weight_arena), arena_bytes), "hipMalloc(weights)");
+    hip_check(hipMemsetAsync(weight_arena, 0, arena_bytes, stream), "hipMemsetAsync(weights)");
+
+    // Stream tensor bytes through two pinned staging buffers.
+    const std::size_t stage_bytes = 64u << 20;
+    void* stage[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    struct Cleanup {
+        void** s;
+        hipEvent_t* e;
+        ~Cleanup() {
+            for (int i = 0; i < 2; ++i) {
+                if (e[i]) hipEventSynchronize(e[i]), hipEventDestroy(e[i]);
+                if (s[i]) hipHostFree(s[i]);
+            }
+        }
+    } cleanup{stage, done};
+    for (int i = 0; i < 2; ++i) {
+        hip_check(hipHostMalloc(&stage[i], stage_bytes, hipHostMallocDefault), "hipHostMalloc(staging)");
+        hip_check(hipEventCreateWithFlags(&done[i], hipEventDisableTiming), "hipEventCreate");
+    }
+    int slot = 0;
+    bool used[2] = {false, false};
+    for (const Item& it : items) {
+        std::size_t off = 0;
+        while (off < it.t.byte_size) {
+            const std::size_t n = std::min(stage_bytes, it.t.byte_size - off);
+            if (used[slot]) hip_check(hipEventSynchronize(done[slot]), "hipEventSynchronize(staging)");
+            reader.read(it.t, off, stage[slot], n);
+            hip_check(hipMemcpyAsync(weight_arena + it.offset + off, stage[slot], n, hipMemcpyHostToDevice, stream),
+                      "hipMemcpyAsync(weights)");
+            hip_check(hipEventRecord(done[slot], stream), "hipEventRecord");
+            used[slot] = true;
+            slot ^= 1;
+            off += n;
+        }
+    }
+    hip_check(hipStreamSynchronize(stream), "weight upload");
+
+    auto mat = [&](std::size_t idx) {
+        DevMatrix m;
+        m.ptr = weight_arena + items[idx].offset;
+        m.type = static_cast<std::uint32_t>(items[idx].t.type);
+        m.rows = items[idx].t.rows;
+        m.cols = items[idx].t.cols;
+        m.row_bytes = items[idx].t.row_bytes;
+        return m;
+    };
+    auto vec = [&](std::size_t idx) { return reinterpret_cast<const float*>(weight_arena + items[idx].offset); };
+    embedding = mat(i_embd);
+    output = mat(i_out);
+    output_norm = vec(i_onorm);
+    layers.resize(c.layer_count);
+    for (std::size_t l = 0; l < c.layer_count; ++l) {
+        const LayerIdx& x = li[l];
+        DevLayer& L = layers[l];
+        L.attn_norm = vec(x.an);
+        L.q = mat(x.q);
+        L.k = mat(x.k);
+        L.v = mat(x.v);
+        L.fused_qkv = x.fused_qkv;
+        L.qkv_bias = vec(x.bq);
+        L.o = mat(x.o);
+        L.ffn_norm = vec(x.fn);
+        L.gate = mat(x.g);
+        L.up = mat(x.u);
+        L.down = mat(x.d);
+        L.fused_gate_up = x.fused_gu;
+    }
+}
+
+void HipLLM::Impl::allocate_state() {
+    const ModelConfig& c = config;
+    const std::size_t L = c.layer_count;
+    kv_cache_bytes = 2 * L * max_sequence * kv_dim * sizeof(float);
+    hip_check(hipMalloc(reinterpret_cast<void**>(&kv_arena), kv_cache_bytes), "hipMalloc(KV cache)");
+    hip_check(hipHostMalloc(reinterpret_cast<void**>(&host_token), 64, hipHostMallocDefault), "hipHostMalloc(token)");
+    ensure_prompt_capacity(1);
+}
+
+// Activation arena: one token row plus prompt ids. Reallocated only when a
+// longer prompt arrives.
+void HipLLM::Impl::ensure_prompt_capacity(std::size_t n) {
+    if (n <= prompt_capacity && act_arena) return;
+    hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    if (act_arena) hipFree(act_arena);
+    if (host_ids) hipHostFree(host_ids);
+    act_arena = nullptr;
+    host_ids = nullptr;
+    const ModelConfig& c = config;
+    const std::size_t H = c.embedding_size, F = c.feed_forward_size, V = c.vocabulary_size;
+    const std::size_t qkv = H + 2 * kv_dim;
+    std::size_t off = 0;
+    auto reserve = [&](std::size_t bytes) {
+        const std::size_t at = off;
+        off = align_up(off + bytes, 256);
+        return at;
+    };
+    const std::size_t o_h0 = reserve(H * 4), o_h1 = reserve(H * 4), o_norm = reserve(H * 4),
+                      o_norm16 = reserve(H / 16 * 4), o_qkv = reserve(qkv * 4), o_attn = reserve(H * 4),
+                      o_attn16 = reserve(H / 16 * 4), o_ffn = reserve(F * 4), o_ffn16 = reserve(F / 16 * 4),
+                      o_gtmp = reserve(F * 4), o_logits = reserve(V * 4),
+                      o_as = reserve(hipllm::attn_decode_scratch_floats(c.attention_head_count, c.head_size,
+                                                                          max_sequence) * 4),
+                      o_am = reserve(hipllm::argmax_scratch_bytes(V)), o_ids = reserve(n * 4), o_tok = reserve(64);
+    act_bytes = off;
+    hip_check(hipMalloc(&act_arena, act_bytes), "hipMalloc(activations)");
+    auto* base = static_cast<std::uint8_t*>(act_arena);
+    act.hidden[0] = reinterpret_cast<float*>(base + o_h0);
+    act.hidden[1] = reinterpret_cast<float*>(base + o_h1);
+    act.norm = reinterpret_cast<float*>(base + o_norm);
+    act.norm16 = reinterpret_cast<float*>(base + o_norm16);
+    act.qkv = reinterpret_cast<float*>(base + o_qkv);
+    act.attn = reinterpret_cast<float*>(base + o_attn);
+    act.attn16 = reinterpret_cast<float*>(base + o_attn16);
+    act.ffn = reinterpret_cast<float*>(base + o_ffn);
+    act.ffn16 = reinterpret_cast<float*>(base + o_ffn16);
+    act.gate_tmp = reinterpret_cast<float*>(base + o_gtmp);
+    act.logits = reinterpret_cast<float*>(base + o_logits);
+    act.attn_scratch = reinterpret_cast<float*>(base + o_as);
+    act.argmax_scratch = base + o_am;
+    act.ids = reinterpret_cast<std::int32_t*>(base + o_ids);
+    act.token = reinterpret_cast<std::uint32_t*>(base + o_tok);
+    hip_check(hipHostMalloc(reinterpret_cast<void**>(&host_ids), n * 4, hipHostMallocDefault), "hipHostMalloc(ids)");
+    prompt_capacity = n;
+}
+
+// cos/sin for every (position, pair) computed exactly as CPULLM's RoPE
+// (cpu_llm.cpp:218-224): freq = powf(theta, -2 i / R), angle = pos * freq.
+void HipLLM::Impl::build_rope_table() {
+    const std::size_t R = config.rotary_dimension;
+    const std::size_t half = R / 2;
+    std::vector<float> table(max_sequence * half * 2);
+    std::vector<float> freq(half);
+    for (std::size_t p = 0; p < half; ++p) {
+        freq[p] = std::pow(config.rope_theta, -2.0f * static_cast<float>(p) / static_cast<float>(R));
+    }
+    for (std::size_t pos = 0; pos < max_sequence; ++pos) {
+        for (std::size_t p = 0; p < half; ++p) {
+            const float angle = static_cast<float>(pos) * freq[p];
+            table[2 * (pos * half + p)] = std::cos(angle);
+            table[2 * (pos * half + p) + 1] = std::sin(angle);
+        }
+    }
+    hip_check(hipMalloc(reinterpret_cast<void**>(&rope_table), table.size() * sizeof(float)), "hipMalloc(RoPE)");
+    hip_check(hipMemcpy(rope_table, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice),
+              "hipMemcpy(RoPE)");
+}
+
+void HipLLM::Impl::gemv(const DevMatrix& w, const float* x, const float* xs16, const float* bias,
+                        const float* residual, float* y, std::size_t rows_override) const {
+    const std::size_t n = rows_override ? rows_override : w.rows;
+    launch_check(hipllm::launch_gemv_prepped(w.type, w.ptr, w.row_bytes, x, xs16, bias, residual, y, n, w.cols, 0,
+                                             stream),
+                 "GEMV");
+}
+
+void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, float* next_hidden) {
+    const ModelConfig& c = config;
+    const DevLayer& L = layers[li];
+    const std::size_t H = c.embedding_size, F = c.feed_forward_size;
+    const float eps = c.norm_epsilon;
+    launch_check(hipllm::launch_rmsnorm(hidden, L.attn_norm, act.norm, act.norm16, 1, H, eps, stream), "RMSNorm");
+    if (L.fused_qkv) {
+        gemv(L.q, act.norm, act.norm16, L.qkv_bias, nullptr, act.qkv, H + 2 * kv_dim);
+    } else {
+        gemv(L.q, act.norm, act.norm16, L.qkv_bias, nullptr, act.qkv);
+        gemv(L.k, act.norm, act.norm16, L.qkv_bias + H, nullptr, act.qkv + H);
+        gemv(L.v, act.norm, act.norm16, L.qkv_bias + H + kv_dim, nullptr, act.qkv + H + kv_dim);
+    }
+    launch_check(hipllm::launch_rope_kv(act.qkv, rope_table, c.rotary_dimension, c.attention_head_count,
+                                        c.kv_head_count, c.head_size, pos, 1, H + 2 * kv_dim, kcache(li), vcache(li),
+                                        stream),
+                 "RoPE/KV write");
+    const float scale = 1.0f / std::sqrt(static_cast<float>(c.head_size));
+    launch_check(hipllm::launch_attn_decode(act.qkv, kcache(li), vcache(li), act.attn, act.attn16, act.attn_scratch,
+                                            c.attention_head_count, c.kv_head_count, c.head_size, pos + 1, scale,
+                                            stream),
+                 "attention");
+    gemv(L.o, act.attn, act.attn16, nullptr, hidden, next_hidden);
+    launch_check(hipllm::launch_rmsnorm(next_hidden, L.ffn_norm, act.norm, act.norm16, 1, H, eps, stream), "RMSNorm");
+    if (L.fused_gate_up) {
+        launch_check(hipllm::launch_gemv_swiglu(L.gate.type, L.gate.ptr, L.up.ptr, L.gate.row_bytes, act.norm,
+                                                act.norm16, act.ffn, act.ffn16, F, H, stream),
+                     "gate/up GEMV");
+    } else {
+        // Gate and up in different formats: two GEMVs, then SwiGLU.
+        gemv(L.gate, act.norm, act.norm16, nullptr, nullptr, act.gate_tmp);
+        gemv(L.up, act.norm, act.norm16, nullptr, nullptr, act.ffn);
+        launch_check(hipllm::launch_swiglu(act.gate_tmp, act.ffn, act.ffn, act.ffn16, F, stream), "SwiGLU");
+    }
+    // The layer output lands back in `hidden`.
+    gemv(L.down, act.ffn, act.ffn16, nullptr, next_hidden, hidden);
+}
+
+void HipLLM::Impl::token_step(const std::int32_t* device_id, std::size_t pos, bool head) {
+    const ModelConfig& c = config;
+    const std::size_t H = c.embedding_size;
+    float* h = act.hidden[0];
+    float* tmp = act.hidden[1];
+    launch_check(hipllm::launch_embed(embedding.type, embedding.ptr, embedding.row_bytes, device_id, 1,
+                                      c.vocabulary_size, H, h, stream),
+                 "embedding");
+    for (std::size_t l = 0; l < layers.size(); ++l) layer_step(l, pos, h, tmp);
+    if (!head) return;
+    launch_check(hipllm::launch_rmsnorm(h, output_norm, act.norm, act.norm16, 1, H, c.norm_epsilon, stream),
+                 "final RMSNorm");
+    gemv(output, act.norm, act.norm16, nullptr, nullptr, act.logits);
+    launch_check(hipllm::launch_argmax(act.logits, c.vocabulary_size, act.token, act.argmax_scratch, stream),
+                 "argmax");
+}
+
+std::int32_t HipLLM::Impl::read_token() {
+    hip_check(hipMemcpyAsync(host_token, act.token, 4, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync(token)");
+    hip_check(hipStreamSynchronize(stream), "HIP forward");
+    const std::uint32_t t = host_token[0];
+    if (t > static_cast<std::uint32_t>(std::numeric_limits<std::int32_t>::max())) {
+        throw std::overflow_error("HIP token id does not fit in int32_t");
+    }
+    return static_cast<std::int32_t>(t);
+}
+
+HipLLM::HipLLM(const std::string& gguf_path, std::size_t max_sequence, int device)
+    : impl_(std::make_unique<Impl>()) {
+    impl_->load(gguf_path, max_sequence, device);
+}
+
+HipLLM::~HipLLM() = default;
+HipLLM::HipLLM(HipLLM&&) noexcept = default;
+HipLLM& HipLLM::operator=(HipLLM&&) noexcept = default;
+
+void HipLLM::reset() {
+    if (!impl_) throw std::runtime_error("HIP model is not initialized");
+    // KV bytes need no clearing: attention reads only [0, position].
+    impl_->sequence_length = 0;
+}
+
+std::int32_t HipLLM::prefill(const std::vector<std::int32_t>& ids) {
+    if (!impl_) throw std::runtime_error("HIP model is not initialized");
+    Impl& m = *impl_;
+    if (ids.empty()) throw std::invalid_argument("HIP prefill requires at least one token id");
+    if (m.sequence_length != 0) throw std::invalid_argument("HIP prefill requires an empty conversation; call reset first");
+    if (ids.size() > m.max_sequence) throw std::length_error("HIP prefill exceeds the allocated sequence capacity");
+    for (std::int32_t id : ids) {
+        if (id < 0 || static_cast<std::size_t>(id) >= m.config.vocabulary_size) {
+            throw std::out_of_range("HIP prefill token id is outside the vocabulary");
+        }
+    }
+    hip_check(hipSetDevice(m.device), "hipSetDevice");
+    const auto t0 = std::chrono::steady_clock::now();
+    m.ensure_prompt_capacity(ids.size());
+    std::memcpy(m.host_ids, ids.data(), ids.size() * 4);
+    hip_check(hipMemcpyAsync(m.act.ids, m.host_ids, ids.size() * 4, hipMemcpyHostToDevice, m.stream), "hipMemcpy(ids)");
+    for (std::size_t t = 0; t < ids.size(); ++t) m.token_step(m.act.ids + t, t, t + 1 == ids.size());
+    const std::int32_t token = m.read_token();
+    m.sequence_length = ids.size();
+    if (m.profile) {
+        const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        std::fprintf(m.profile, "prefill,%zu,%zu,%.6f\n", ids.size(), ids.size(), ms);
+    }
+    return token;
+}
+
+std::int32_t HipLLM::decode(std::int32_t id) {
+    if (!impl_) throw std::runtime_error("HIP model is not initialized");
+    Impl& m = *impl_;
+    if (m.sequence_length == 0) throw std::invalid_argument("HIP decode requires a completed prefill");
+    if (id < 0 || static_cast<std::size_t>(id) >= m.config.vocabulary_size) {
+        throw std::out_of_range("HIP decode token id is outside the vocabulary");
+    }
+    const std::size_t pos = m.sequence_length;
+    if (pos >= m.max_sequence) throw std::length_error("HIP decode exceeds the allocated sequence capacity");
+    hip_check(hipSetDevice(m.device), "hipSetDevice");
+    const auto t0 = std::chrono::steady_clock::now();
+    m.host_ids[0] = id;
+    hip_check(hipMemcpyAsync(m.act.ids, m.host_ids, 4, hipMemcpyHostToDevice, m.stream), "hipMemcpy(id)");
+    m.token_step(m.act.ids, pos, true);
+    const std::int32_t token = m.read_token();
+    m.sequence_length = pos + 1;
+    if (m.profile) {
+        const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        std::fprintf(m.profile, "decode,1,%zu,%.6f\n", pos + 1, ms);
+    }
+    return token;
+}
+
+void HipLLM::enable_profiling(const std::string& csv_path, bool) {
+    if (!impl_) throw std::runtime_error("HIP model is not initialized");
+    disable_profiling();
+    impl_->profile = std::fopen(csv_path.c_str(), "w");
+    if (!impl_->profile) throw std::runtime_error("cannot open profile CSV: " + csv_path);
+    std::fprintf(impl_->profile, "phase,tokens,sequence,wall_ms\n");
+}
+
+void HipLLM::disable_profiling() {
+    if (impl_ && impl_->profile) {
+        std::fclose(impl_->profile);
+        impl_->profile = nullptr;
+    }
+}
+
+const ModelConfig& HipLLM::config() const {
+    if (!impl_) throw std::runtime_error("HIP model is not initialized");
+    return impl_->config;
+}
+
+std::size_t HipLLM::position() const noexcept { return impl_ ? impl_->sequence_length : 0; }
+std::size_t HipLLM::max_sequence() const noexcept { return impl_ ? impl_->max_sequence : 0; }
+bool HipLLM::uses_gpu() const noexcept { return available(); }
+bool HipLLM::available() const noexcept { return impl_ && impl_->weight_arena && impl_->stream; }
+
+const std::string& HipLLM::device_name() const noexcept {
+    static const std::string empty;
+    return impl_ ? impl_->device_name : empty;
+}
+
+MemoryStats HipLLM::memory_stats() const noexcept {
+    if (!impl_) return {};
+    MemoryStats s;
+    s.weight_bytes = impl_->weight_bytes;
+    s.kv_cache_bytes = impl_->kv_cache_bytes;
+    s.recurrent_state_bytes = 0;
+    s.intermediate_bytes = impl_->act_bytes;
+    s.intermediate_is_estimate = false;
+    return s;
+}
+
+void HipLLM::copy_last_logits(float* dst, std::size_t count) const {
+    if (!impl_) throw std::runtime_error("HIP model is not initialized");
+    if (count != impl_->config.vocabulary_size) throw std::invalid_argument("logits buffer must hold the vocabulary");
+    hip_check(hipStreamSynchronize(impl_->stream), "hipStreamSynchronize");
+    hip_check(hipMemcpy(dst, impl_->act.logits, count * 4, hipMemcpyDeviceToHost), "hipMemcpy(logits)");
+}
+
+void HipLLM::set_batched_prefill(bool enabled) noexcept {
+    if (impl_) impl_->batched_prefill = enabled;
+}
+
+}  // namespace llm

@@ -1,0 +1,306 @@
+"""Python view of libhipllm.so: the HipLLM backend and its kernel launchers.
+
+``HipLLM`` mirrors the reference backend classes (MetalLLM, metal_llm.h:20-52;
+CPULLM, cpu_llm.h:165-194): reset(), prefill(ids) -> int, decode(id) -> int,
+config, position, max_sequence, uses_gpu, memory_stats(), device_name,
+enable_profiling(). Errors map the reference's C++ exception types onto
+Python ones (see ``ERRORS``).
+
+The ``kernels`` namespace exposes each C-ABI launcher over torch device
+tensors (torch only provides device memory and the current stream). There is
+no CPU fallback: without libhipllm.so or a GPU these raise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import types
+
+import numpy as np
+
+from . import _native
+
+OK, INVALID_ARGUMENT, OUT_OF_RANGE, LENGTH_ERROR, RUNTIME_ERROR, OVERFLOW_ERROR = range(6)
+
+
+class LengthError(OverflowError):
+    """std::length_error: sequence capacity exceeded."""
+
+
+class OverflowErrorStd(OverflowError):
+    """std::overflow_error."""
+
+
+ERRORS = {INVALID_ARGUMENT: ValueError, OUT_OF_RANGE: IndexError, LENGTH_ERROR: LengthError,
+          RUNTIME_ERROR: RuntimeError, OVERFLOW_ERROR: OverflowErrorStd}
+
+
+class HipllmConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in (
+        "layer_count", "embedding_size", "feed_forward_size", "attention_head_count",
+        "kv_head_count", "head_size", "rotary_dimension", "vocabulary_size", "context_length",
+        "parameter_count", "stored_weight_bytes")] + [
+        ("eos_token_id", ctypes.c_int32), ("rope_theta", ctypes.c_float),
+        ("norm_epsilon", ctypes.c_float), ("architecture", ctypes.c_char * 32)]
+
+
+class HipllmMemoryStats(ctypes.Structure):
+    _fields_ = [("weight_bytes", ctypes.c_uint64), ("kv_cache_bytes", ctypes.c_uint64),
+                ("recurrent_state_bytes", ctypes.c_uint64), ("intermediate_bytes", ctypes.c_uint64),
+                ("intermediate_is_estimate", ctypes.c_int32)]
+
+
+_P = ctypes.c_void_p
+_S = ctypes.c_size_t
+_U32 = ctypes.c_uint32
+_I32 = ctypes.c_int32
+_F = ctypes.c_float
+_I = ctypes.c_int
+
+SIGNATURES = {
+    "hipllm_last_error": (ctypes.c_char_p, []),
+    "hipllm_version": (ctypes.c_char_p, []),
+    "hipllm_dequant_rows": (_I, [_U32, _P, _S, _S, _S, _P, _P]),
+    "hipllm_prep_sums": (_I, [_P, _P, _S, _P]),
+    "hipllm_gemv_workspace_bytes": (_S, [_S]),
+    "hipllm_gemv": (_I, [_U32, _P, _S, _P, _P, _P, _S, _S, _P, _P]),
+    "hipllm_gemv_prepped": (_I, [_U32, _P, _S, _P, _P, _P, _P, _P, _S, _S, _I, _P]),
+    "hipllm_gemv_swiglu": (_I, [_U32, _P, _P, _S, _P, _P, _P, _P, _S, _S, _P]),
+    "hipllm_rmsnorm": (_I, [_P, _P, _P, _P, _S, _S, _F, _P]),
+    "hipllm_embed": (_I, [_U32, _P, _S, _P, _S, _S, _S, _P, _P]),
+    "hipllm_rope_kv": (_I, [_P, _P, _S, _S, _S, _S, _S, _S, _S, _P, _P, _P]),
+    "hipllm_attn_decode_scratch_floats": (_S, [_S, _S, _S]),
+    "hipllm_attn_decode": (_I, [_P, _P, _P, _P, _P, _P, _S, _S, _S, _S, _F, _P]),
+    "hipllm_argmax_scratch_bytes": (_S, [_S]),
+    "hipllm_argmax": (_I, [_P, _S, _P, _P, _P]),
+    "hipllm_swiglu": (_I, [_P, _P, _P, _P, _S, _P]),
+    "hipllm_create": (_I, [ctypes.c_char_p, _S, _I, ctypes.POINTER(_P)]),
+    "hipllm_destroy": (None, [_P]),
+    "hipllm_reset": (_I, [_P]),
+    "hipllm_prefill": (_I, [_P, _P, _S, ctypes.POINTER(_I32)]),
+    "hipllm_decode": (_I, [_P, _I32, ctypes.POINTER(_I32)]),
+    "hipllm_config": (_I, [_P, ctypes.POINTER(HipllmConfig)]),
+    "hipllm_position": (_S, [_P]),
+    "hipllm_max_sequence": (_S, [_P]),
+    "hipllm_uses_gpu": (_I, [_P]),
+    "hipllm_memory_stats": (_I, [_P, ctypes.POINTER(HipllmMemoryStats)]),
+    "hipllm_device_name": (ctypes.c_char_p, [_P]),
+    "hipllm_enable_profiling": (_I, [_P, ctypes.c_char_p]),
+    "hipllm_disable_profiling": (_I, [_P]),
+    "hipllm_copy_logits": (_I, [_P, _P, _S]),
+    "hipllm_set_batched_prefill": (_I, [_P, _I]),
+    "hipllm_inspect_gguf": (_I, [ctypes.c_char_p, ctypes.POINTER(HipllmConfig)]),
+}
+
+
+def lib() -> ctypes.CDLL:
+    L = _native.hipllm()
+    if not getattr(L, "_hipllm_typed", False):
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        L._hipllm_typed = True
+    return L
+
+
+def header_functions(header_text: str) -> list[str]:
+    """Names of the functions a C header declares (for export checks)."""
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(hipllm_\w+)\s*\(", header_text, re.M)))
+
+
+def check(rc: int) -> None:
+    if rc != OK:
+        msg = lib().hipllm_last_error().decode(errors="replace")
+        raise ERRORS.get(rc, RuntimeError)(msg)
+
+
+def _config_dict(cfg: HipllmConfig) -> dict:
+    d = {n: getattr(cfg, n) for n, _ in HipllmConfig._fields_ if n != "architecture"}
+    d["architecture"] = cfg.architecture.decode()
+    return d
+
+
+def inspect_gguf(path) -> dict:
+    """Parses a GGUF with the streaming reader (no GPU needed)."""
+    cfg = HipllmConfig()
+    check(lib().hipllm_inspect_gguf(str(path).encode(), ctypes.byref(cfg)))
+    return _config_dict(cfg)
+
+
+class HipLLM:
+    """The MI355X qwen2 backend, same contract as the reference's MetalLLM."""
+
+    def __init__(self, gguf_path, max_sequence: int = 0, device: int = -1):
+        self._h = _P()
+        check(lib().hipllm_create(str(gguf_path).encode(), max_sequence, device, ctypes.byref(self._h)))
+        cfg = HipllmConfig()
+        check(lib().hipllm_config(self._h, ctypes.byref(cfg)))
+        self.config = _config_dict(cfg)
+
+    def close(self) -> None:
+        if self._h:
+            lib().hipllm_destroy(self._h)
+            self._h = _P()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def reset(self) -> None:
+        check(lib().hipllm_reset(self._h))
+
+    def prefill(self, ids) -> int:
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        out = _I32()
+        check(lib().hipllm_prefill(self._h, a.ctypes.data if a.size else None, a.size, ctypes.byref(out)))
+        return out.value
+
+    def decode(self, token: int) -> int:
+        out = _I32()
+        check(lib().hipllm_decode(self._h, int(token), ctypes.byref(out)))
+        return out.value
+
+    @property
+    def position(self) -> int:
+        return lib().hipllm_position(self._h)
+
+    @property
+    def max_sequence(self) -> int:
+        return lib().hipllm_max_sequence(self._h)
+
+    @property
+    def uses_gpu(self) -> bool:
+        return bool(lib().hipllm_uses_gpu(self._h))
+
+    @property
+    def device_name(self) -> str:
+        return lib().hipllm_device_name(self._h).decode()
+
+    def memory_stats(self) -> dict:
+        s = HipllmMemoryStats()
+        check(lib().hipllm_memory_stats(self._h, ctypes.byref(s)))
+        return {n: getattr(s, n) for n, _ in HipllmMemoryStats._fields_}
+
+    def enable_profiling(self, csv_path) -> None:
+        check(lib().hipllm_enable_profiling(self._h, str(csv_path).encode()))
+
+    def disable_profiling(self) -> None:
+        check(lib().hipllm_disable_profiling(self._h))
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.config["vocabulary_size"], dtype=np.float32)
+        check(lib().hipllm_copy_logits(self._h, out.ctypes.data, out.size))
+        return out
+
+    def set_batched_prefill(self, enabled: bool) -> None:
+        check(lib().hipllm_set_batched_prefill(self._h, 1 if enabled else 0))
+
+
+def generate(backend, prompt, max_new_tokens: int, stop_token_ids=(), on_step=None):
+    """chat.cpp:831-878 generate(): reset, prefill, then emit/decode."""
+    if len(prompt) == 0:
+        raise ValueError("Generation requires at least one initial token")
+    if max_new_tokens == 0:
+        raise ValueError("Generation requires max_new_tokens > 0")
+    if backend.max_sequence == 0:
+        raise RuntimeError("Backend sequence capacity is zero")
+    if len(prompt) >= backend.max_sequence:
+        raise ValueError("Initial token sequence leaves no room for generated tokens")
+    limit = min(max_new_tokens, backend.max_sequence - len(prompt))
+    backend.reset()
+    nxt = backend.prefill(prompt)
+    if on_step:
+        on_step(backend)
+    out = []
+    for step in range(limit):
+        if nxt in stop_token_ids:
+            break
+        out.append(nxt)
+        if step + 1 >= limit:
+            break
+        nxt = backend.decode(nxt)
+        if on_step:
+            on_step(backend)
+    return out
+
+
+# ------------------------------------------------------------ kernel wrappers
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _k_dequant_rows(qtype, w, row_bytes, rows, k, out, stream=None):
+    check(lib().hipllm_dequant_rows(qtype, _ptr(w), row_bytes, rows, k, _ptr(out), _stream(stream)))
+
+
+def _k_prep_sums(x, xs16, k, stream=None):
+    check(lib().hipllm_prep_sums(_ptr(x), _ptr(xs16), k, _stream(stream)))
+
+
+def _k_gemv(qtype, w, row_bytes, x, bias, y, n, k, workspace, stream=None):
+    check(lib().hipllm_gemv(qtype, _ptr(w), row_bytes, _ptr(x), _ptr(bias), _ptr(y), n, k, _ptr(workspace),
+                            _stream(stream)))
+
+
+def _k_gemv_prepped(qtype, w, row_bytes, x, xs16, bias, residual, y, n, k, rows_per_block=0, stream=None):
+    check(lib().hipllm_gemv_prepped(qtype, _ptr(w), row_bytes, _ptr(x), _ptr(xs16), _ptr(bias), _ptr(residual),
+                                    _ptr(y), n, k, rows_per_block, _stream(stream)))
+
+
+def _k_gemv_swiglu(qtype, wg, wu, row_bytes, x, xs16, y, ys16, n, k, stream=None):
+    check(lib().hipllm_gemv_swiglu(qtype, _ptr(wg), _ptr(wu), row_bytes, _ptr(x), _ptr(xs16), _ptr(y), _ptr(ys16),
+                                   n, k, _stream(stream)))
+
+
+def _k_rmsnorm(x, gamma, y, ys16, rows, cols, eps, stream=None):
+    check(lib().hipllm_rmsnorm(_ptr(x), _ptr(gamma), _ptr(y), _ptr(ys16), rows, cols, eps, _stream(stream)))
+
+
+def _k_embed(qtype, table, row_bytes, ids, rows, vocab, cols, out, stream=None):
+    check(lib().hipllm_embed(qtype, _ptr(table), row_bytes, _ptr(ids), rows, vocab, cols, _ptr(out),
+                             _stream(stream)))
+
+
+def _k_rope_kv(qkv, cos_sin, rot, hq, hkv, d, pos0, rows, row_stride, kcache, vcache, stream=None):
+    check(lib().hipllm_rope_kv(_ptr(qkv), _ptr(cos_sin), rot, hq, hkv, d, pos0, rows, row_stride, _ptr(kcache),
+                               _ptr(vcache), _stream(stream)))
+
+
+def _k_attn_decode(q, kcache, vcache, out, out16, scratch, hq, hkv, d, length, scale, stream=None):
+    check(lib().hipllm_attn_decode(_ptr(q), _ptr(kcache), _ptr(vcache), _ptr(out), _ptr(out16), _ptr(scratch),
+                                   hq, hkv, d, length, scale, _stream(stream)))
+
+
+def _k_argmax(x, n, out, scratch, stream=None):
+    check(lib().hipllm_argmax(_ptr(x), n, _ptr(out), _ptr(scratch), _stream(stream)))
+
+
+def _k_swiglu(g, u, y, y16, n, stream=None):
+    check(lib().hipllm_swiglu(_ptr(g), _ptr(u), _ptr(y), _ptr(y16), n, _stream(stream)))
+
+
+kernels = types.SimpleNamespace(
+    dequant_rows=_k_dequant_rows, prep_sums=_k_prep_sums, gemv=_k_gemv, gemv_prepped=_k_gemv_prepped,
+    gemv_swiglu=_k_gemv_swiglu, rmsnorm=_k_rmsnorm, embed=_k_embed, rope_kv=_k_rope_kv,
+    attn_decode=_k_attn_decode, argmax=_k_argmax, swiglu=_k_swiglu,
+    gemv_workspace_bytes=lambda k: lib().hipllm_gemv_workspace_bytes(k),
+    attn_decode_scratch_floats=lambda hq, d, n: lib().hipllm_attn_decode_scratch_floats(hq, d, n),
+    argmax_scratch_bytes=lambda n: lib().hipllm_argmax_scratch_bytes(n),
+)

@@ -1,0 +1,324 @@
+"""Kernel parity on the GPU, called through the C ABI (libhipllm.so).
+
+Bars (from the project's correctness contract):
+* dequantization, embedding gather, RMSNorm and RoPE: bit-exact against the
+  CPU oracle (the restatement of CPULLM, itself pinned to the reference's
+  golden vectors);
+* GEMV: rel_err = max|y - ref| / max|ref| <= 1e-3, ref = float64 product of
+  the FP32-dequantized weights and the FP32 input;
+* attention, SwiGLU: same rel_err bound against float64;
+* argmax: exact index, ties to the lower index.
+Device weight buffers get 256 bytes of tail padding, as the runtime's arena
+does, because realigned dword loads may read past the last block.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from myllm_amd import synth
+from myllm_amd.hipllm import kernels
+from tests import blocks
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+PAD = 256
+
+
+def dev_bytes(arr: np.ndarray, cuda):
+    flat = np.ascontiguousarray(arr).view(np.uint8).reshape(-1)
+    buf = torch.zeros(flat.size + PAD, dtype=torch.uint8, device=cuda)
+    buf[: flat.size] = torch.from_numpy(flat.copy()).to(cuda)
+    return buf
+
+
+def rel_err(y, ref) -> float:
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return float(np.abs(y - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def random_rows(qtype, rows, cols, seed):
+    if qtype == synth.F32:
+        return synth.normal(rows * cols, seed, stddev=0.02).reshape(rows, cols).view(np.uint8).reshape(rows, -1)
+    if qtype == synth.F16:
+        return synth.normal(rows * cols, seed, stddev=0.02).reshape(rows, cols).astype(np.float16).view(
+            np.uint8).reshape(rows, -1)
+    return synth.random_quantized(rows, cols, qtype, seed)
+
+
+# ------------------------------------------------------------- dequant
+DEQ_SHAPES = [
+    (synth.Q4_K, 7, 512), (synth.Q4_K, 3, 3584), (synth.Q6_K, 5, 4864), (synth.Q6_K, 3, 512),
+    (synth.Q8_0, 9, 96), (synth.Q8_0, 4, 896), (synth.Q5_0, 6, 96), (synth.Q5_0, 3, 896),
+    (synth.F16, 4, 256), (synth.F32, 3, 64),
+]
+
+
+@pytest.mark.parametrize("qtype,rows,cols", DEQ_SHAPES)
+def test_dequant_bit_exact(cuda, qtype, rows, cols):
+    w = random_rows(qtype, rows, cols, seed=rows * 100 + cols)
+    dw = dev_bytes(w, cuda)
+    out = torch.empty(rows * cols, dtype=torch.float32, device=cuda)
+    kernels.dequant_rows(qtype, dw, w.shape[1], rows, cols, out)
+    got = out.cpu().numpy().reshape(rows, cols)
+    ref = oracle.dequant_rows(qtype, w, cols)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("case", range(4))
+def test_dequant_known_answers(cuda, case):
+    qtype, data, cols, expected = blocks.kat_rows()[case]
+    w = np.frombuffer(data, dtype=np.uint8)[None, :]
+    out = torch.empty(cols, dtype=torch.float32, device=cuda)
+    kernels.dequant_rows(qtype, dev_bytes(w, cuda), w.shape[1], 1, cols, out)
+    assert np.array_equal(out.cpu().numpy().astype(np.float64), expected)
+
+
+def test_dequant_special_halves(cuda):
+    # Q8_0 blocks whose scale is a subnormal, infinite or NaN binary16.
+    qs = np.arange(1, 33, dtype=np.int8)
+    data = b"".join(blocks.f16(b) + qs.tobytes() for b in (0x0001, 0x03FF, 0x7C00, 0xFC00, 0x8000, 0x7E00))
+    w = np.frombuffer(data, dtype=np.uint8)[None, :]
+    out = torch.empty(192, dtype=torch.float32, device=cuda)
+    kernels.dequant_rows(synth.Q8_0, dev_bytes(w, cuda), w.shape[1], 1, 192, out)
+    got = out.cpu().numpy()
+    ref = oracle.dequant_rows(synth.Q8_0, w, 192)[0]
+    finite = ~np.isnan(ref)
+    assert np.array_equal(got[finite].view(np.uint32), ref[finite].view(np.uint32))
+    assert np.all(np.isnan(got[~finite]))
+
+
+# ------------------------------------------------------------- GEMV
+def gemv_case(cuda, qtype, n, k, seed, bias=False, residual=False, rows_per_block=0):
+    w = random_rows(qtype, n, k, seed)
+    x = synth.normal(k, seed + 1)
+    dw = dev_bytes(w, cuda)
+    dx = torch.from_numpy(x).to(cuda)
+    xs16 = torch.empty(k // 16, dtype=torch.float32, device=cuda)
+    kernels.prep_sums(dx, xs16, k)
+    b = synth.normal(n, seed + 2) if bias else None
+    r = synth.normal(n, seed + 3) if residual else None
+    y = torch.empty(n, dtype=torch.float32, device=cuda)
+    kernels.gemv_prepped(qtype, dw, w.shape[1], dx, xs16, None if b is None else torch.from_numpy(b).to(cuda),
+                         None if r is None else torch.from_numpy(r).to(cuda), y, n, k, rows_per_block)
+    # Reference: float64 over the FP32 dequantized weights (GPU dequant is
+    # bit-exact to the oracle, checked above).
+    wf = torch.empty(n * k, dtype=torch.float32, device=cuda)
+    kernels.dequant_rows(qtype, dw, w.shape[1], n, k, wf)
+    ref = (wf.view(n, k).double() @ dx.double()).cpu().numpy()
+    if b is not None:
+        ref = ref + b
+    if r is not None:
+        ref = ref + r
+    return y.cpu().numpy(), ref
+
+
+@pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q6_K, synth.Q8_0, synth.Q5_0, synth.F16, synth.F32])
+@pytest.mark.parametrize("n,k", [(1, 256), (37, 512), (130, 1024), (333, 2816)])
+def test_gemv_small(cuda, qtype, n, k):
+    y, ref = gemv_case(cuda, qtype, n, k, seed=n + k)
+    assert rel_err(y, ref) <= 1e-3
+
+
+@pytest.mark.parametrize("qtype", [synth.Q5_0, synth.Q8_0])
+def test_gemv_two_byte_aligned_blocks(cuda, qtype):
+    # 34- and 22-byte blocks: every odd block starts at a 2-byte offset.
+    y, ref = gemv_case(cuda, qtype, 77, 64 * 3, seed=3)
+    assert rel_err(y, ref) <= 1e-3
+
+
+@pytest.mark.parametrize("rows_per_block", [2, 4, 8, 16, 32])
+def test_gemv_tilings_agree(cuda, rows_per_block):
+    y, ref = gemv_case(cuda, synth.Q4_K, 1000, 3584, seed=7, bias=True, residual=True,
+                       rows_per_block=rows_per_block)
+    assert rel_err(y, ref) <= 1e-3
+
+
+@pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q6_K])
+@pytest.mark.parametrize("n,k", [(18944, 3584), (3584, 18944), (4608, 3584)])
+def test_gemv_qwen7b_shapes(cuda, qtype, n, k):
+    y, ref = gemv_case(cuda, qtype, n, k, seed=11)
+    assert rel_err(y, ref) <= 1e-3
+
+
+def test_gemv_qwen05b_q6k_down(cuda):
+    # K = 4864: Q6_K rows of 3990 bytes, so rows alternate 4- and 2-byte alignment.
+    y, ref = gemv_case(cuda, synth.Q6_K, 896, 4864, seed=5, residual=True)
+    assert rel_err(y, ref) <= 1e-3
+
+
+def test_gemv_public_entry_with_workspace(cuda):
+    n, k = 300, 1024
+    w = random_rows(synth.Q4_K, n, k, 21)
+    x = synth.normal(k, 22)
+    dw, dx = dev_bytes(w, cuda), torch.from_numpy(x).to(cuda)
+    ws = torch.empty(kernels.gemv_workspace_bytes(k), dtype=torch.uint8, device=cuda)
+    y = torch.empty(n, dtype=torch.float32, device=cuda)
+    kernels.gemv(synth.Q4_K, dw, w.shape[1], dx, None, y, n, k, ws)
+    ref = oracle.dequant_rows(synth.Q4_K, w, k).astype(np.float64) @ x.astype(np.float64)
+    assert rel_err(y.cpu().numpy(), ref) <= 1e-3
+
+
+@pytest.mark.parametrize("qtype,n,k", [(synth.Q4_K, 4864, 1024), (synth.Q4_K, 2048, 3584),
+                                        (synth.Q5_0, 480, 896)])
+def test_gemv_swiglu(cuda, qtype, n, k):
+    wg, wu = random_rows(qtype, n, k, 31), random_rows(qtype, n, k, 32)
+    x = synth.normal(k, 33)
+    dx = torch.from_numpy(x).to(cuda)
+    xs16 = torch.empty(k // 16, dtype=torch.float32, device=cuda)
+    kernels.prep_sums(dx, xs16, k)
+    y = torch.empty(n, dtype=torch.float32, device=cuda)
+    y16 = torch.empty(n // 16, dtype=torch.float32, device=cuda)
+    kernels.gemv_swiglu(qtype, dev_bytes(wg, cuda), dev_bytes(wu, cuda), wg.shape[1], dx, xs16, y, y16, n, k)
+    g = oracle.dequant_rows(qtype, wg, k).astype(np.float64) @ x
+    u = oracle.dequant_rows(qtype, wu, k).astype(np.float64) @ x
+    ref = g / (1 + np.exp(-g)) * u
+    got = y.cpu().numpy()
+    assert rel_err(got, ref) <= 1e-3
+    assert rel_err(y16.cpu().numpy(), got.astype(np.float64).reshape(-1, 16).sum(axis=1)) <= 1e-5
+
+
+# ------------------------------------------------------------- small ops
+@pytest.mark.parametrize("rows,cols", [(1, 896), (5, 3584), (3, 5120)])
+def test_rmsnorm_bit_exact(cuda, rows, cols):
+    x = synth.normal(rows * cols, 41, stddev=3.0).reshape(rows, cols)
+    g = synth.normal(cols, 42, stddev=0.5) + 1.0
+    y = torch.empty(rows * cols, dtype=torch.float32, device=cuda)
+    y16 = torch.empty(rows * cols // 16, dtype=torch.float32, device=cuda)
+    kernels.rmsnorm(torch.from_numpy(x).to(cuda), torch.from_numpy(g).to(cuda), y, y16, rows, cols, 1e-6)
+    ref = x.copy()
+    for r in range(rows):
+        oracle.lib().oracle_rmsnorm(ref[r].ctypes.data, g.ctypes.data, cols, ctypes.c_float(1e-6))
+    got = y.cpu().numpy().reshape(rows, cols)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    assert rel_err(y16.cpu().numpy(), got.astype(np.float64).reshape(-1, 16).sum(axis=1)) <= 1e-5
+
+
+def _libm():
+    m = ctypes.CDLL("libm.so.6")
+    for f in ("cosf", "sinf"):
+        getattr(m, f).restype = ctypes.c_float
+        getattr(m, f).argtypes = [ctypes.c_float]
+    m.powf.restype = ctypes.c_float
+    m.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+    return m
+
+
+@pytest.mark.parametrize("hq,hkv,d,pos0,rows", [(14, 2, 64, 0, 1), (14, 2, 64, 37, 3), (40, 8, 128, 4000, 2)])
+def test_rope_kv_bit_exact(cuda, hq, hkv, d, pos0, rows):
+    theta = 1e6
+    m = _libm()
+    half = d // 2
+    npos = pos0 + rows
+    # Same float32 expressions as CPULLM's Vector::rope (cpu_llm.cpp:218-224).
+    freq = [m.powf(theta, float(np.float32(-2.0) * np.float32(p) / np.float32(d))) for p in range(half)]
+    table = np.empty((npos, half, 2), dtype=np.float32)
+    for pos in range(pos0, npos):
+        for p in range(half):
+            ang = float(np.float32(pos) * np.float32(freq[p]))
+            table[pos, p] = (m.cosf(ang), m.sinf(ang))
+    stride = (hq + 2 * hkv) * d
+    qkv = synth.normal(rows * stride, 51).reshape(rows, stride)
+    dq = torch.from_numpy(qkv.copy()).to(cuda)
+    kc = torch.zeros(npos * hkv * d, dtype=torch.float32, device=cuda)
+    vc = torch.zeros_like(kc)
+    kernels.rope_kv(dq, torch.from_numpy(table).to(cuda), d, hq, hkv, d, pos0, rows, stride, kc, vc)
+    ref = qkv.copy()
+    for r in range(rows):
+        for h in range(hq + hkv):
+            seg = np.ascontiguousarray(ref[r, h * d:(h + 1) * d])
+            oracle.lib().oracle_rope(seg.ctypes.data, d, pos0 + r, ctypes.c_float(theta), d)
+            ref[r, h * d:(h + 1) * d] = seg
+    got = dq.cpu().numpy().reshape(rows, stride)
+    assert np.array_equal(got[:, : (hq + hkv) * d].view(np.uint32), ref[:, : (hq + hkv) * d].view(np.uint32))
+    kv = hkv * d
+    kcache = kc.cpu().numpy().reshape(npos, kv)
+    vcache = vc.cpu().numpy().reshape(npos, kv)
+    assert np.array_equal(kcache[pos0:], got[:, hq * d: hq * d + kv])
+    assert np.array_equal(vcache[pos0:], qkv[:, hq * d + kv:])
+
+
+@pytest.mark.parametrize("length", [1, 7, 255, 256, 257, 1000])
+@pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (40, 8, 128)])
+def test_attention_decode(cuda, length, hq, hkv, d):
+    kv = hkv * d
+    q = synth.normal(hq * d, 61)
+    k = synth.normal(length * kv, 62).reshape(length, kv)
+    v = synth.normal(length * kv, 63).reshape(length, kv)
+    scale = np.float32(1.0) / np.float32(math.sqrt(d))
+    out = torch.empty(hq * d, dtype=torch.float32, device=cuda)
+    out16 = torch.empty(hq * d // 16, dtype=torch.float32, device=cuda)
+    scratch = torch.empty(kernels.attn_decode_scratch_floats(hq, d, length), dtype=torch.float32, device=cuda)
+    kernels.attn_decode(torch.from_numpy(q).to(cuda), torch.from_numpy(k).to(cuda), torch.from_numpy(v).to(cuda),
+                        out, out16, scratch, hq, hkv, d, length, float(scale))
+    ref = np.empty(hq * d)
+    for h in range(hq):
+        g = h // (hq // hkv)
+        s = k[:, g * d:(g + 1) * d].astype(np.float64) @ q[h * d:(h + 1) * d] * float(scale)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        ref[h * d:(h + 1) * d] = p @ v[:, g * d:(g + 1) * d]
+    got = out.cpu().numpy()
+    assert rel_err(got, ref) <= 1e-5
+    assert rel_err(out16.cpu().numpy(), got.astype(np.float64).reshape(-1, 16).sum(axis=1)) <= 1e-5
+
+
+@pytest.mark.parametrize("n", [1, 100, 2048, 2049, 151936])
+def test_argmax(cuda, n):
+    x = synth.normal(n, 71 + n)
+    for case in range(3):
+        if case == 1 and n > 1:  # tie: the lower index wins
+            i, j = n // 3, n - 1
+            x[i] = x[j] = x.max() + 1
+        if case == 2:
+            x[:] = -np.inf
+            x[n // 2] = 0.0
+        scratch = torch.empty(kernels.argmax_scratch_bytes(n), dtype=torch.uint8, device=cuda)
+        out = torch.empty(1, dtype=torch.int32, device=cuda)
+        kernels.argmax(torch.from_numpy(x).to(cuda), n, out, scratch)
+        assert int(out.item()) == oracle.lib().oracle_argmax(x.ctypes.data, n)
+
+
+def test_embed_bit_exact(cuda):
+    vocab, cols = 300, 896
+    table = random_rows(synth.Q8_0, vocab, cols, 81)
+    ids = np.array([0, 299, 17, 17, -1, 300], dtype=np.int32)
+    out = torch.empty(len(ids) * cols, dtype=torch.float32, device=cuda)
+    kernels.embed(synth.Q8_0, dev_bytes(table, cuda), table.shape[1], torch.from_numpy(ids).to(cuda), len(ids),
+                  vocab, cols, out)
+    got = out.cpu().numpy().reshape(len(ids), cols)
+    ref = oracle.dequant_rows(synth.Q8_0, table, cols)
+    for r, t in enumerate(ids):
+        expect = ref[t] if 0 <= t < vocab else np.zeros(cols, dtype=np.float32)
+        assert np.array_equal(got[r].view(np.uint32), expect.view(np.uint32))
+
+
+def test_swiglu_elementwise(cuda):
+    n = 4864
+    g, u = synth.normal(n, 91, stddev=4.0), synth.normal(n, 92)
+    y = torch.empty(n, dtype=torch.float32, device=cuda)
+    y16 = torch.empty(n // 16, dtype=torch.float32, device=cuda)
+    kernels.swiglu(torch.from_numpy(g).to(cuda), torch.from_numpy(u).to(cuda), y, y16, n)
+    gd = g.astype(np.float64)
+    ref = gd / (1 + np.exp(-gd)) * u
+    assert rel_err(y.cpu().numpy(), ref) <= 1e-6
+
+
+def test_launchers_reject_bad_arguments(cuda):
+    from myllm_amd.hipllm import lib
+    y = torch.empty(16, dtype=torch.float32, device=cuda)
+    w = torch.zeros(1024, dtype=torch.uint8, device=cuda)
+    with pytest.raises(ValueError):
+        kernels.gemv_prepped(synth.Q4_K, w, 144, y, y, None, None, y, 4, 100)  # k not block aligned
+    with pytest.raises(ValueError):
+        kernels.gemv_prepped(99, w, 144, y, y, None, None, y, 4, 256)  # unknown type
+    with pytest.raises(ValueError):
+        kernels.rmsnorm(y, y, y, None, 1, 16, 0.0)  # eps must be positive
+    assert lib().hipllm_version()
