@@ -65,10 +65,11 @@ int hipllm_gemv(uint32_t type, const void* w, size_t row_bytes, const float* x, 
                 size_t n, size_t k, void* workspace, void* stream);
 
 /* GEMV with caller-supplied per-16 sums and an optional residual:
- * y = W x (+ bias) (+ residual). rows_per_block 0 picks the default tiling
- * (2, 4, 8, 16 or 32 are accepted). */
+ * y = W x (+ bias) (+ residual). `tiling` 0 picks the default; otherwise
+ * 10 * R + OPR with R in {1, 2, 4} rows per 8-lane octet and OPR in
+ * {1, 2, 4, 8} octets splitting each row group's super-blocks. */
 int hipllm_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* xs16,
-                        const float* bias, const float* residual, float* y, size_t n, size_t k, int rows_per_block,
+                        const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
                         void* stream);
 
 /* Fused FFN gate/up GEMV + SwiGLU: y = silu(Wg x) * (Wu x); ys16 (nullable,
@@ -77,6 +78,27 @@ int hipllm_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const fl
  * metal_llm.metal:895-911), cpu_llm.cpp:905-909. */
 int hipllm_gemv_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
                        const float* xs16, float* y, float* ys16, size_t n, size_t k, void* stream);
+
+/* xb[m, k] (bf16, row-major, ld = k) = round-to-nearest-even of the FP32
+ * rows x[r * ldx + c]; the activation side-input of hipllm_gemm_mfma. */
+int hipllm_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, void* stream);
+
+/* Prefill matmul Y[m, n] = X[m, k] W[n, k]^T (+ bias[n]) (+ residual[m, n])
+ * with X given as bf16 (hipllm_to_bf16), W in native GGUF rows, bf16 MFMA
+ * with FP32 accumulation; k % 128 == 0. `tile` < 0 picks the default, else
+ * 0..3 = 128x32, 128x64, 256x64, 256x128 (weight rows x X rows per block).
+ * Replaces metal_gemm_{q5_0,q8_0,q4_k,q6_k,f32} via encode_matrix_product
+ * (metal_llm.metal:196-250, 621-704; metal_llm.mm:1782-1889) and CPULLM's
+ * gemmt / gemmtb (cpu_llm.cpp:591-607, 631-653). */
+int hipllm_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* bias,
+                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, void* stream);
+
+/* Workspace bytes hipllm_gemm needs for m rows of k values. */
+size_t hipllm_gemm_workspace_bytes(size_t m, size_t k);
+
+/* hipllm_gemm_mfma on FP32 X rows (ld = ldx), converted into `workspace`. */
+int hipllm_gemm(uint32_t type, const void* w, size_t row_bytes, const float* x, size_t ldx, const float* bias,
+                float* y, size_t m, size_t n, size_t k, void* workspace, void* stream);
 
 /* Row RMSNorm y = x * (1/sqrt(mean(x^2) + eps) * gamma), double sum of
  * squares; ys16 nullable. Replaces metal_rmsnorm_f32 (metal_llm.metal:785-823)

@@ -76,27 +76,24 @@ __device__ __forceinline__ float half_hi(uint32_t w) {
 // naturally aligned dword loads and v_alignbyte. `p` must be 2-byte aligned and
 // the dwords touched must be in bounds (device weight buffers carry padding).
 __device__ __forceinline__ uint32_t load_u32_a2(const uint8_t* p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
-    const uint32_t shift = static_cast<uint32_t>(a & 3u);
+    const uint32_t shift = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3u);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p - shift);
     const uint32_t lo = q[0];
     const uint32_t hi = q[1];
     return __builtin_amdgcn_alignbyte(hi, lo, shift);
 }
 
 __device__ __forceinline__ uint2 load_u64_a2(const uint8_t* p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
-    const uint32_t shift = static_cast<uint32_t>(a & 3u);
+    const uint32_t shift = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3u);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p - shift);
     const uint32_t w0 = q[0], w1 = q[1], w2 = q[2];
     return make_uint2(__builtin_amdgcn_alignbyte(w1, w0, shift),
                       __builtin_amdgcn_alignbyte(w2, w1, shift));
 }
 
 __device__ __forceinline__ uint4 load_u128_a2(const uint8_t* p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
-    const uint32_t shift = static_cast<uint32_t>(a & 3u);
+    const uint32_t shift = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3u);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p - shift);
     const uint32_t w0 = q[0], w1 = q[1], w2 = q[2], w3 = q[3], w4 = q[4];
     return make_uint4(__builtin_amdgcn_alignbyte(w1, w0, shift),
                       __builtin_amdgcn_alignbyte(w2, w1, shift),

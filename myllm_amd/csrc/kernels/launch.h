@@ -13,12 +13,17 @@ int launch_dequant_rows(uint32_t type, const void* w, size_t row_bytes, size_t r
                         hipStream_t stream);
 
 int launch_prep_sums(const float* x, float* xs16, size_t k, hipStream_t stream);
-int gemv_default_rows(uint32_t n, uint32_t units);
+int gemv_default_tiling(uint32_t n, uint32_t units, int mode);
 int launch_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* xs16,
-                        const float* bias, const float* residual, float* y, size_t n, size_t k, int rows_per_block,
+                        const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
                         hipStream_t stream);
 int launch_gemv_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
                        const float* xs16, float* y, float* ys16, size_t n, size_t k, hipStream_t stream);
+
+int gemm_default_tile(uint32_t m, uint32_t n);
+int launch_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, hipStream_t stream);
+int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* bias,
+                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, hipStream_t stream);
 
 int launch_rmsnorm(const float* x, const float* gamma, float* y, float* ys16, size_t rows, size_t cols, float eps,
                    hipStream_t stream);

@@ -1,1 +1,557 @@
+// Prefill matmul Y[M,N] = X[M,K] W[N,K]^T (+ bias[N]) (+ residual[M,N]) on
+// CDNA4 bf16 MFMA with FP32 accumulation, weights in native GGUF block layout.
+//
+// Replaces the reference's one-thread-per-output quantized GEMMs
+// (metal_gemm_{q5_0,q8_0,q4_k,q6_k}_f32, metal_llm.metal:621-704; host
+// encode_matrix_product, metal_llm.mm:1782-1889) and CPULLM's gemmt/gemmtb
+// (cpu_llm.cpp:591-607, 631-653), which re-decode a weight row per output.
+//
+// Design:
+// * X is converted once to bf16 (to_bf16_kernel, round to nearest even).
+// * A block is 4 waves. Block tile = (4 * 32 * NSUB) weight rows x (32 * MSUB)
+//   X rows; every wave owns 32 * NSUB weight rows and all 32 * MSUB X rows.
+// * K advances in steps of 128. Each step, the X tile (bf16) is staged in LDS
+//   (double-buffered, one barrier per step) and every wave dequantizes its own
+//   weight rows straight from HBM into MFMA operand registers, so weights are
+//   read once per X-row tile and never pass through LDS.
+// * v_mfma_f32_32x32x16_bf16: operand lane l holds row (l % 32) and eight
+//   consecutive k. Inside a 128-k step, slice s (0..7) gives lane half
+//   h = l / 32 the k range 64 G + 32 hi + 16 h + 8 p + [0, 8) with G = s >> 2,
+//   hi = (s >> 1) & 1, p = s & 1. X and W use the same map, so each MFMA sums
+//   over a permutation of its 16 k. This map lines up with the GGUF layouts:
+//   Q4_K's low/high nibbles (hi), Q6_K's quarters, Q8_0/Q5_0's 32-blocks.
+// * Dequantized values are computed in FP32 exactly as the reference
+//   dequantizer orders them (model.cpp:581-683) and rounded once to bf16.
 #include "common.h"
+
+namespace hipllm {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+namespace {
+
+constexpr int kStepK = 128;
+constexpr int kLdsRow = kStepK + 8;  // bf16 per LDS row: 272 bytes, spreads rows over banks
+
+__device__ __forceinline__ uint4 g_ld128_a4(const uint8_t* p) {
+    const u32x4a4 v = *reinterpret_cast<const u32x4a4*>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// 16 bytes from a 2-byte-aligned address (reads the enclosing dwords).
+__device__ __forceinline__ uint4 g_ld128_a2(const uint8_t* p) {
+    const uint32_t s = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3u);
+    const uint8_t* base = p - s;
+    const uint4 v = g_ld128_a4(base);
+    const uint32_t e = *reinterpret_cast<const uint32_t*>(base + 16);
+    return make_uint4(__builtin_amdgcn_alignbyte(v.y, v.x, s), __builtin_amdgcn_alignbyte(v.z, v.y, s),
+                      __builtin_amdgcn_alignbyte(v.w, v.z, s), __builtin_amdgcn_alignbyte(e, v.w, s));
+}
+
+__device__ __forceinline__ uint32_t g_ld32_a2(const uint8_t* p) {
+    const uint32_t s = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3u);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p - s);
+    return __builtin_amdgcn_alignbyte(q[1], q[0], s);
+}
+
+__device__ __forceinline__ float f16_bits(uint32_t bits) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits & 0xffffu)));
+}
+
+// Eight values v[i] = a * byte_i - b over the 8 bytes of (w0, w1), rounded to bf16.
+#pragma clang fp contract(off)
+__device__ __forceinline__ bf16x8 affine8(uint32_t w0, uint32_t w1, float a, float b) {
+    bf16x8 r;
+    r[0] = static_cast<__bf16>(a * ubyte0(w0) - b);
+    r[1] = static_cast<__bf16>(a * ubyte1(w0) - b);
+    r[2] = static_cast<__bf16>(a * ubyte2(w0) - b);
+    r[3] = static_cast<__bf16>(a * ubyte3(w0) - b);
+    r[4] = static_cast<__bf16>(a * ubyte0(w1) - b);
+    r[5] = static_cast<__bf16>(a * ubyte1(w1) - b);
+    r[6] = static_cast<__bf16>(a * ubyte2(w1) - b);
+    r[7] = static_cast<__bf16>(a * ubyte3(w1) - b);
+    return r;
+}
+
+// Eight values v[i] = a * (byte_i - 32) (Q6_K) rounded to bf16.
+__device__ __forceinline__ bf16x8 q6_8(uint32_t w0, uint32_t w1, float a) {
+    bf16x8 r;
+    r[0] = static_cast<__bf16>(a * (ubyte0(w0) - 32.0f));
+    r[1] = static_cast<__bf16>(a * (ubyte1(w0) - 32.0f));
+    r[2] = static_cast<__bf16>(a * (ubyte2(w0) - 32.0f));
+    r[3] = static_cast<__bf16>(a * (ubyte3(w0) - 32.0f));
+    r[4] = static_cast<__bf16>(a * (ubyte0(w1) - 32.0f));
+    r[5] = static_cast<__bf16>(a * (ubyte1(w1) - 32.0f));
+    r[6] = static_cast<__bf16>(a * (ubyte2(w1) - 32.0f));
+    r[7] = static_cast<__bf16>(a * (ubyte3(w1) - 32.0f));
+    return r;
+}
+
+// Eight signed bytes times d (Q8_0: v = q * d).
+__device__ __forceinline__ float sbyte(uint32_t w, int i) {
+    return static_cast<float>(static_cast<int8_t>((w >> (8 * i)) & 0xffu));
+}
+__device__ __forceinline__ bf16x8 q8_8(uint32_t w0, uint32_t w1, float d) {
+    bf16x8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = static_cast<__bf16>(sbyte(w0, i) * d);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[4 + i] = static_cast<__bf16>(sbyte(w1, i) * d);
+    return r;
+}
+#pragma clang fp contract(fast)
+
+// Per-type weight fragments. Raw holds the bytes one lane needs for one
+// 128-k step of one weight row; load() issues the global loads, frags()
+// turns them into the eight bf16x8 operands (slice order above).
+template <uint32_t T>
+struct WTile;
+
+// Q4_K (144-byte super-blocks, model.cpp:616-644). A 128-k step is half a
+// super-block: 64-groups j0 = 2 * (step % 2) and j0 + 1. Lane half h reads qs
+// bytes [32 j + 16 h, +16) of each group: low nibbles are sub-block 2j,
+// elements 16 h + [0, 16), high nibbles sub-block 2j + 1.
+template <>
+struct WTile<kQ4_K> {
+    struct Raw {
+        uint4 head;
+        uint4 q[2];
+    };
+    __device__ static __forceinline__ Raw load(const uint8_t* row, uint32_t kb, uint32_t h) {
+        const uint8_t* blk = row + (kb / 256) * 144;
+        const uint32_t j0 = (kb % 256) / 64;
+        Raw r;
+        r.head = g_ld128_a4(blk);
+        r.q[0] = g_ld128_a4(blk + 16 + 32 * j0 + 16 * h);
+        r.q[1] = g_ld128_a4(blk + 16 + 32 * (j0 + 1) + 16 * h);
+        return r;
+    }
+    __device__ static __forceinline__ void frags(const Raw& r, uint32_t kb, uint32_t, bf16x8* f) {
+        const uint32_t j0 = (kb % 256) / 64;
+        const float d = f16_bits(r.head.x);
+        const float dmin = f16_bits(r.head.x >> 16);
+        // get_scale_min_k4 (model.cpp:524-537) for the four sub-blocks 2 j0 .. 2 j0 + 3.
+        uint32_t S, M;
+        if (j0 == 0) {
+            S = r.head.y & 0x3f3f3f3fu;
+            M = r.head.z & 0x3f3f3f3fu;
+        } else {
+            S = (r.head.w & 0x0f0f0f0fu) | ((r.head.y >> 2) & 0x30303030u);
+            M = ((r.head.w >> 4) & 0x0f0f0f0fu) | ((r.head.z >> 2) & 0x30303030u);
+        }
+#pragma unroll
+        for (int G = 0; G < 2; ++G) {
+            const uint4 q = r.q[G];
+            const float d1lo = d * static_cast<float>((S >> (16 * G)) & 0xffu);
+            const float m1lo = dmin * static_cast<float>((M >> (16 * G)) & 0xffu);
+            const float d1hi = d * static_cast<float>((S >> (16 * G + 8)) & 0xffu);
+            const float m1hi = dmin * static_cast<float>((M >> (16 * G + 8)) & 0xffu);
+            f[4 * G + 0] = affine8(q.x & 0x0f0f0f0fu, q.y & 0x0f0f0f0fu, d1lo, m1lo);
+            f[4 * G + 1] = affine8(q.z & 0x0f0f0f0fu, q.w & 0x0f0f0f0fu, d1lo, m1lo);
+            f[4 * G + 2] = affine8((q.x >> 4) & 0x0f0f0f0fu, (q.y >> 4) & 0x0f0f0f0fu, d1hi, m1hi);
+            f[4 * G + 3] = affine8((q.z >> 4) & 0x0f0f0f0fu, (q.w >> 4) & 0x0f0f0f0fu, d1hi, m1hi);
+        }
+    }
+};
+
+// Q6_K (210-byte super-blocks, model.cpp:646-683). A 128-k step is the half
+// n6 = step % 2; slice (G, hi) is quarter 2 G + hi. Lane half h needs
+// l = 16 h + [0, 16): ql bytes 64 n6 + 32 hi + l (low nibble for G = 0, high
+// for G = 1), qh byte 32 n6 + l shifted by 2 * quarter, scale
+// sc[8 n6 + h + 2 * quarter].
+template <>
+struct WTile<kQ6_K> {
+    struct Raw {
+        uint4 ql[2];
+        uint4 qh;
+        uint32_t sc;  // scales 8 n6 + h + {0, 2, 4, 6}
+        uint32_t d;
+    };
+    __device__ static __forceinline__ Raw load(const uint8_t* row, uint32_t kb, uint32_t h) {
+        const uint8_t* blk = row + (kb / 256) * 210;
+        const uint32_t n6 = (kb % 256) / 128;
+        Raw r;
+        r.ql[0] = g_ld128_a2(blk + 64 * n6 + 16 * h);
+        r.ql[1] = g_ld128_a2(blk + 64 * n6 + 32 + 16 * h);
+        r.qh = g_ld128_a2(blk + 128 + 32 * n6 + 16 * h);
+        const uint32_t lo = g_ld32_a2(blk + 192 + 8 * n6);      // scales 8 n6 + 0..3
+        const uint32_t hi = g_ld32_a2(blk + 192 + 8 * n6 + 4);  // scales 8 n6 + 4..7
+        // bytes h, h + 2 of lo and h, h + 2 of hi -> quarters 0, 1, 2, 3
+        const uint32_t sh = 8 * h;
+        r.sc = ((lo >> sh) & 0xffu) | (((lo >> (sh + 16)) & 0xffu) << 8) | (((hi >> sh) & 0xffu) << 16) |
+               (((hi >> (sh + 16)) & 0xffu) << 24);
+        r.d = g_ld32_a2(blk + 208) & 0xffffu;
+        return r;
+    }
+    __device__ static __forceinline__ void frags(const Raw& r, uint32_t, uint32_t, bf16x8* f) {
+        const float d = f16_bits(r.d);
+#pragma unroll
+        for (int G = 0; G < 2; ++G) {
+#pragma unroll
+            for (int hi = 0; hi < 2; ++hi) {
+                const uint32_t quarter = 2 * G + hi;
+                const uint4 l = r.ql[hi];
+                const uint32_t sh = 2 * quarter;
+                const int8_t scb = static_cast<int8_t>((r.sc >> (8 * quarter)) & 0xffu);
+                const float a = d * static_cast<float>(scb);
+                uint32_t L[4] = {l.x, l.y, l.z, l.w};
+                const uint32_t H[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+                uint32_t v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t nib = G == 0 ? (L[i] & 0x0f0f0f0fu) : ((L[i] >> 4) & 0x0f0f0f0fu);
+                    v[i] = nib | (((H[i] >> sh) & 0x03030303u) << 4);
+                }
+                f[4 * G + 2 * hi + 0] = q6_8(v[0], v[1], a);
+                f[4 * G + 2 * hi + 1] = q6_8(v[2], v[3], a);
+            }
+        }
+    }
+};
+
+// Q8_0 (34-byte blocks, model.cpp:603-614): slice (G, hi) is block 4 s' with
+// s' = 2 G + hi of the step; lane half h takes bytes 16 h + [0, 16).
+template <>
+struct WTile<kQ8_0> {
+    struct Raw {
+        uint4 q[4];
+        uint32_t d[4];
+    };
+    __device__ static __forceinline__ Raw load(const uint8_t* row, uint32_t kb, uint32_t h) {
+        const uint8_t* blk = row + (kb / 32) * 34;
+        Raw r;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            r.q[b] = g_ld128_a2(blk + 34 * b + 2 + 16 * h);
+            r.d[b] = g_ld32_a2(blk + 34 * b) & 0xffffu;
+        }
+        return r;
+    }
+    __device__ static __forceinline__ void frags(const Raw& r, uint32_t, uint32_t, bf16x8* f) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const float d = f16_bits(r.d[b]);
+            f[2 * b + 0] = q8_8(r.q[b].x, r.q[b].y, d);
+            f[2 * b + 1] = q8_8(r.q[b].z, r.q[b].w, d);
+        }
+    }
+};
+
+// Q5_0 (22-byte blocks, model.cpp:581-601): slice (G, hi) is block 2 G + hi;
+// lane half h takes elements 16 h + [0, 16): the low (h = 0) or high (h = 1)
+// nibbles of qs[0..16), fifth bits qh >> (16 h + i); v = q d - 16 d.
+template <>
+struct WTile<kQ5_0> {
+    struct Raw {
+        uint4 q[4];
+        uint32_t qh[4];
+        uint32_t d[4];
+    };
+    __device__ static __forceinline__ Raw load(const uint8_t* row, uint32_t kb, uint32_t) {
+        const uint8_t* blk = row + (kb / 32) * 22;
+        Raw r;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            r.d[b] = g_ld32_a2(blk + 22 * b) & 0xffffu;
+            r.qh[b] = g_ld32_a2(blk + 22 * b + 2);
+            r.q[b] = g_ld128_a2(blk + 22 * b + 6);
+        }
+        return r;
+    }
+    __device__ static __forceinline__ void frags(const Raw& r, uint32_t, uint32_t h, bf16x8* f) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const float d = f16_bits(r.d[b]);
+            const float m = 16.0f * d;
+            const uint32_t bits = r.qh[b] >> (16 * h);  // fifth bits of elements 16 h + i
+            const uint32_t Q[4] = {r.q[b].x, r.q[b].y, r.q[b].z, r.q[b].w};
+            uint32_t v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t nib = h == 0 ? (Q[i] & 0x0f0f0f0fu) : ((Q[i] >> 4) & 0x0f0f0f0fu);
+                const uint32_t hb = (bits >> (4 * i)) & 0xfu;
+                v[i] = nib | (((hb * 0x00204081u) & 0x01010101u) << 4);
+            }
+            f[2 * b + 0] = affine8(v[0], v[1], d, m);
+            f[2 * b + 1] = affine8(v[2], v[3], d, m);
+        }
+    }
+};
+
+// F32 weights: slice s covers k = 64 G + 32 hi + 16 h + 8 p + [0, 8).
+template <>
+struct WTile<kF32> {
+    struct Raw {
+        uint4 v[16];
+    };
+    __device__ static __forceinline__ Raw load(const uint8_t* row, uint32_t kb, uint32_t h) {
+        const uint8_t* p = row + 4 * static_cast<size_t>(kb);
+        Raw r;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const uint32_t k0 = 64 * (s >> 2) + 32 * ((s >> 1) & 1) + 16 * h + 8 * (s & 1);
+            r.v[2 * s] = g_ld128_a4(p + 4 * k0);
+            r.v[2 * s + 1] = g_ld128_a4(p + 4 * k0 + 16);
+        }
+        return r;
+    }
+    __device__ static __forceinline__ void frags(const Raw& r, uint32_t, uint32_t, bf16x8* f) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const uint4 a = r.v[2 * s], b = r.v[2 * s + 1];
+            const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) f[s][i] = static_cast<__bf16>(__uint_as_float(w[i]));
+        }
+    }
+};
+
+// F16 weights.
+template <>
+struct WTile<kF16> {
+    struct Raw {
+        uint4 v[8];
+    };
+    __device__ static __forceinline__ Raw load(const uint8_t* row, uint32_t kb, uint32_t h) {
+        const uint8_t* p = row + 2 * static_cast<size_t>(kb);
+        Raw r;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const uint32_t k0 = 64 * (s >> 2) + 32 * ((s >> 1) & 1) + 16 * h + 8 * (s & 1);
+            r.v[s] = g_ld128_a4(p + 2 * k0);
+        }
+        return r;
+    }
+    __device__ static __forceinline__ void frags(const Raw& r, uint32_t, uint32_t, bf16x8* f) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const uint32_t w[4] = {r.v[s].x, r.v[s].y, r.v[s].z, r.v[s].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f[s][2 * i] = static_cast<__bf16>(f16_bits(w[i]));
+                f[s][2 * i + 1] = static_cast<__bf16>(f16_bits(w[i] >> 16));
+            }
+        }
+    }
+};
+
+template <uint32_t T, int NSUB, int MSUB>
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restrict__ w, size_t row_bytes,
+                                                        const __bf16* __restrict__ xb, const float* __restrict__ bias,
+                                                        const float* __restrict__ residual, float* __restrict__ y,
+                                                        uint32_t m, uint32_t n, uint32_t k) {
+    using WT = WTile<T>;
+    constexpr int BM = 32 * MSUB;
+    constexpr int WN = 32 * NSUB;
+    constexpr int BN = 4 * WN;
+    constexpr int kLoads = BM * (kStepK / 8) / 256;  // 16-byte X loads per thread per step
+    __shared__ __attribute__((aligned(16))) __bf16 xs[2][BM * kLdsRow];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wave = tid >> 6, lane = tid & 63;
+    const uint32_t lr = lane & 31, h = lane >> 5;
+    const uint32_t m0 = blockIdx.y * BM;
+    const uint32_t n0 = blockIdx.x * BN + wave * WN;
+
+    const uint8_t* wrow[NSUB];
+#pragma unroll
+    for (int ns = 0; ns < NSUB; ++ns) {
+        const uint32_t r = min(n0 + 32 * ns + lr, n - 1);  // rows past n read row n - 1, never stored
+        wrow[ns] = w + static_cast<size_t>(r) * row_bytes;
+    }
+
+    // X tile loader: thread t moves 16 bytes (8 bf16) of row t / 16 + 16 i,
+    // column chunk t % 16, for i < kLoads.
+    uint4 xr[kLoads];
+    auto load_x = [&](uint32_t kb) {
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+            const uint32_t row = tid / 16 + 16 * i;
+            const uint32_t gm = m0 + row;
+            if (gm < m) {
+                xr[i] = *reinterpret_cast<const uint4*>(xb + static_cast<size_t>(gm) * k + kb + 8 * (tid % 16));
+            } else {
+                xr[i] = make_uint4(0, 0, 0, 0);
+            }
+        }
+    };
+    auto store_x = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+            const uint32_t row = tid / 16 + 16 * i;
+            *reinterpret_cast<uint4*>(&xs[buf][row * kLdsRow + 8 * (tid % 16)]) = xr[i];
+        }
+    };
+
+    f32x16 acc[NSUB][MSUB];
+#pragma unroll
+    for (int ns = 0; ns < NSUB; ++ns)
+#pragma unroll
+        for (int ms = 0; ms < MSUB; ++ms)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[ns][ms][i] = 0.0f;
+
+    const uint32_t steps = k / kStepK;
+    typename WT::Raw raw[NSUB];
+#pragma unroll
+    for (int ns = 0; ns < NSUB; ++ns) raw[ns] = WT::load(wrow[ns], 0, h);
+    load_x(0);
+    store_x(0);
+    __syncthreads();
+
+    for (uint32_t st = 0; st < steps; ++st) {
+        const uint32_t kb = st * kStepK;
+        const int buf = st & 1;
+        bf16x8 bf[NSUB][8];
+#pragma unroll
+        for (int ns = 0; ns < NSUB; ++ns) WT::frags(raw[ns], kb, h, bf[ns]);
+        if (st + 1 < steps) {
+#pragma unroll
+            for (int ns = 0; ns < NSUB; ++ns) raw[ns] = WT::load(wrow[ns], kb + kStepK, h);
+            load_x(kb + kStepK);
+        }
+        const __bf16* xt = xs[buf];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const uint32_t kc = 64 * (s >> 2) + 32 * ((s >> 1) & 1) + 16 * h + 8 * (s & 1);
+#pragma unroll
+            for (int ms = 0; ms < MSUB; ++ms) {
+                const bf16x8 a = *reinterpret_cast<const bf16x8*>(&xt[(32 * ms + lr) * kLdsRow + kc]);
+#pragma unroll
+                for (int ns = 0; ns < NSUB; ++ns) {
+                    acc[ns][ms] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bf[ns][s], acc[ns][ms], 0, 0, 0);
+                }
+            }
+        }
+        if (st + 1 < steps) store_x(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue: acc[ns][ms][4 g + r] = Y[m0 + 32 ms + 8 g + 4 h + r][n0 + 32 ns + lr].
+#pragma unroll
+    for (int ns = 0; ns < NSUB; ++ns) {
+        const uint32_t col = n0 + 32 * ns + lr;
+        if (col >= n) continue;
+        const float b = bias ? bias[col] : 0.0f;
+#pragma unroll
+        for (int ms = 0; ms < MSUB; ++ms) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t row = m0 + 32 * ms + 8 * g + 4 * h + r;
+                    if (row < m) {
+                        const size_t o = static_cast<size_t>(row) * n + col;
+                        float v = acc[ns][ms][4 * g + r] + b;
+                        if (residual) v += residual[o];
+                        y[o] = v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+// xb[r, c] = bf16(x[r * ldx + c]) for r < m, c < k (round to nearest even).
+__global__ void to_bf16_kernel(const float* __restrict__ x, size_t ldx, __bf16* __restrict__ xb, uint32_t m,
+                               uint32_t k) {
+    const uint32_t groups = k / 8;
+    const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= static_cast<size_t>(m) * groups) return;
+    const uint32_t r = static_cast<uint32_t>(idx / groups);
+    const uint32_t c = static_cast<uint32_t>(idx % groups) * 8;
+    const float4 a = *reinterpret_cast<const float4*>(x + r * ldx + c);
+    const float4 b = *reinterpret_cast<const float4*>(x + r * ldx + c + 4);
+    bf16x8 v;
+    v[0] = static_cast<__bf16>(a.x);
+    v[1] = static_cast<__bf16>(a.y);
+    v[2] = static_cast<__bf16>(a.z);
+    v[3] = static_cast<__bf16>(a.w);
+    v[4] = static_cast<__bf16>(b.x);
+    v[5] = static_cast<__bf16>(b.y);
+    v[6] = static_cast<__bf16>(b.z);
+    v[7] = static_cast<__bf16>(b.w);
+    *reinterpret_cast<bf16x8*>(xb + static_cast<size_t>(r) * k + c) = v;
+}
+
+template <uint32_t T, int NSUB, int MSUB>
+void launch_tile(const void* w, size_t row_bytes, const __bf16* xb, const float* bias, const float* residual, float* y,
+                 uint32_t m, uint32_t n, uint32_t k, hipStream_t stream) {
+    constexpr uint32_t BN = 4 * 32 * NSUB, BM = 32 * MSUB;
+    const dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM);
+    hipLaunchKernelGGL((gemm_mfma_kernel<T, NSUB, MSUB>), grid, dim3(256), 0, stream,
+                       static_cast<const uint8_t*>(w), row_bytes, xb, bias, residual, y, m, n, k);
+}
+
+template <uint32_t T>
+int launch_typed(int tile, const void* w, size_t row_bytes, const __bf16* xb, const float* bias,
+                 const float* residual, float* y, uint32_t m, uint32_t n, uint32_t k, hipStream_t stream) {
+    switch (tile) {
+    case 0: launch_tile<T, 1, 1>(w, row_bytes, xb, bias, residual, y, m, n, k, stream); break;
+    case 1: launch_tile<T, 1, 2>(w, row_bytes, xb, bias, residual, y, m, n, k, stream); break;
+    case 2: launch_tile<T, 2, 2>(w, row_bytes, xb, bias, residual, y, m, n, k, stream); break;
+    case 3: launch_tile<T, 2, 4>(w, row_bytes, xb, bias, residual, y, m, n, k, stream); break;
+    default: return kInvalidArgument;
+    }
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+}  // namespace
+
+// Tile choice: 0 = 128 x 32, 1 = 128 x 64, 2 = 256 x 64, 3 = 256 x 128
+// (weight rows x X rows per block). Larger tiles read weights fewer times;
+// smaller ones keep more blocks in flight when m or n is small.
+int gemm_default_tile(uint32_t m, uint32_t n) {
+    const uint64_t target = 512;  // about two blocks per CU
+    const uint32_t bn[4] = {128, 128, 256, 256}, bm[4] = {32, 64, 64, 128};
+    for (int t = 3; t >= 0; --t) {
+        const uint64_t blocks = static_cast<uint64_t>((n + bn[t] - 1) / bn[t]) * ((m + bm[t] - 1) / bm[t]);
+        if (blocks >= target) return t;
+    }
+    return m > 32 ? 1 : 0;
+}
+
+int launch_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, hipStream_t stream) {
+    if (!x || !xb || m == 0 || k == 0 || k % 8 != 0 || ldx < k || ldx % 4 != 0) return kInvalidArgument;
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(xb) % 16 != 0) return kInvalidArgument;
+    if (m > 0xffffffffull || k > 0xffffffffull) return kLengthError;
+    const size_t total = m * (k / 8);
+    const size_t blocks = (total + 255) / 256;
+    if (blocks > 0x7fffffffull) return kLengthError;
+    hipLaunchKernelGGL(to_bf16_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, stream, x, ldx,
+                       static_cast<__bf16*>(xb), static_cast<uint32_t>(m), static_cast<uint32_t>(k));
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* bias,
+                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, hipStream_t stream) {
+    if (!w || !xb || !y || m == 0 || n == 0 || k == 0) return kInvalidArgument;
+    if (k % kStepK != 0) return kInvalidArgument;
+    if (m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull) return kLengthError;
+    if (type != kF32 && type != kF16 && type != kQ5_0 && type != kQ8_0 && type != kQ4_K && type != kQ6_K) {
+        return kInvalidArgument;
+    }
+    if (row_bytes < k / block_elems(type) * block_bytes(type)) return kInvalidArgument;
+    if (reinterpret_cast<uintptr_t>(w) % 2 != 0 || row_bytes % 2 != 0) return kInvalidArgument;
+    if ((type == kQ4_K || type == kF32 || type == kF16) &&
+        (reinterpret_cast<uintptr_t>(w) % 4 != 0 || row_bytes % 4 != 0)) {
+        return kInvalidArgument;
+    }
+    if (reinterpret_cast<uintptr_t>(xb) % 16 != 0) return kInvalidArgument;
+    if (tile < 0) tile = gemm_default_tile(static_cast<uint32_t>(m), static_cast<uint32_t>(n));
+    const uint32_t M = static_cast<uint32_t>(m), N = static_cast<uint32_t>(n), K = static_cast<uint32_t>(k);
+    const auto* x = static_cast<const __bf16*>(xb);
+    switch (type) {
+    case kQ4_K: return launch_typed<kQ4_K>(tile, w, row_bytes, x, bias, residual, y, M, N, K, stream);
+    case kQ6_K: return launch_typed<kQ6_K>(tile, w, row_bytes, x, bias, residual, y, M, N, K, stream);
+    case kQ8_0: return launch_typed<kQ8_0>(tile, w, row_bytes, x, bias, residual, y, M, N, K, stream);
+    case kQ5_0: return launch_typed<kQ5_0>(tile, w, row_bytes, x, bias, residual, y, M, N, K, stream);
+    case kF32: return launch_typed<kF32>(tile, w, row_bytes, x, bias, residual, y, M, N, K, stream);
+    case kF16: return launch_typed<kF16>(tile, w, row_bytes, x, bias, residual, y, M, N, K, stream);
+    default: return kInvalidArgument;
+    }
+}
+
+}  // namespace hipllm

@@ -84,9 +84,9 @@ int hipllm_gemv(uint32_t type, const void* w, size_t row_bytes, const float* x, 
 }
 
 int hipllm_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* xs16,
-                        const float* bias, const float* residual, float* y, size_t n, size_t k, int rows_per_block,
+                        const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
                         void* stream) {
-    return status(hipllm::launch_gemv_prepped(type, w, row_bytes, x, xs16, bias, residual, y, n, k, rows_per_block,
+    return status(hipllm::launch_gemv_prepped(type, w, row_bytes, x, xs16, bias, residual, y, n, k, tiling,
                                               as_stream(stream)),
                   "hipllm_gemv_prepped: invalid arguments or launch failure");
 }
@@ -95,6 +95,30 @@ int hipllm_gemv_swiglu(uint32_t type, const void* wg, const void* wu, size_t row
                        const float* xs16, float* y, float* ys16, size_t n, size_t k, void* stream) {
     return status(hipllm::launch_gemv_swiglu(type, wg, wu, row_bytes, x, xs16, y, ys16, n, k, as_stream(stream)),
                   "hipllm_gemv_swiglu: invalid arguments or launch failure");
+}
+
+int hipllm_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, void* stream) {
+    return status(hipllm::launch_to_bf16(x, ldx, xb, m, k, as_stream(stream)),
+                  "hipllm_to_bf16: invalid arguments (k % 8 == 0, 16-byte aligned buffers) or launch failure");
+}
+
+int hipllm_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* bias,
+                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, void* stream) {
+    return status(hipllm::launch_gemm_mfma(type, w, row_bytes, xb, bias, residual, y, m, n, k, tile,
+                                           as_stream(stream)),
+                  "hipllm_gemm_mfma: invalid arguments (k % 128 == 0, tile 0..3) or launch failure");
+}
+
+size_t hipllm_gemm_workspace_bytes(size_t m, size_t k) { return (m * k * 2 + 255) / 256 * 256; }
+
+int hipllm_gemm(uint32_t type, const void* w, size_t row_bytes, const float* x, size_t ldx, const float* bias,
+                float* y, size_t m, size_t n, size_t k, void* workspace, void* stream) {
+    if (!workspace) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_gemm: workspace is null");
+    const int rc = hipllm::launch_to_bf16(x, ldx, workspace, m, k, as_stream(stream));
+    if (rc != hipllm::kOk) return status(rc, "hipllm_gemm: invalid activation arguments");
+    return status(hipllm::launch_gemm_mfma(type, w, row_bytes, workspace, bias, nullptr, y, m, n, k, -1,
+                                           as_stream(stream)),
+                  "hipllm_gemm: invalid arguments (k % 128 == 0) or launch failure");
 }
 
 int hipllm_rmsnorm(const float* x, const float* gamma, float* y, float* ys16, size_t rows, size_t cols, float eps,

@@ -67,6 +67,10 @@ SIGNATURES = {
     "hipllm_gemv": (_I, [_U32, _P, _S, _P, _P, _P, _S, _S, _P, _P]),
     "hipllm_gemv_prepped": (_I, [_U32, _P, _S, _P, _P, _P, _P, _P, _S, _S, _I, _P]),
     "hipllm_gemv_swiglu": (_I, [_U32, _P, _P, _S, _P, _P, _P, _P, _S, _S, _P]),
+    "hipllm_to_bf16": (_I, [_P, _S, _P, _S, _S, _P]),
+    "hipllm_gemm_mfma": (_I, [_U32, _P, _S, _P, _P, _P, _P, _S, _S, _S, _I, _P]),
+    "hipllm_gemm_workspace_bytes": (_S, [_S, _S]),
+    "hipllm_gemm": (_I, [_U32, _P, _S, _P, _S, _P, _P, _S, _S, _S, _P, _P]),
     "hipllm_rmsnorm": (_I, [_P, _P, _P, _P, _S, _S, _F, _P]),
     "hipllm_embed": (_I, [_U32, _P, _S, _P, _S, _S, _S, _P, _P]),
     "hipllm_rope_kv": (_I, [_P, _P, _S, _S, _S, _S, _S, _S, _S, _P, _P, _P]),
@@ -259,14 +263,28 @@ def _k_gemv(qtype, w, row_bytes, x, bias, y, n, k, workspace, stream=None):
                             _stream(stream)))
 
 
-def _k_gemv_prepped(qtype, w, row_bytes, x, xs16, bias, residual, y, n, k, rows_per_block=0, stream=None):
+def _k_gemv_prepped(qtype, w, row_bytes, x, xs16, bias, residual, y, n, k, tiling=0, stream=None):
     check(lib().hipllm_gemv_prepped(qtype, _ptr(w), row_bytes, _ptr(x), _ptr(xs16), _ptr(bias), _ptr(residual),
-                                    _ptr(y), n, k, rows_per_block, _stream(stream)))
+                                    _ptr(y), n, k, tiling, _stream(stream)))
 
 
 def _k_gemv_swiglu(qtype, wg, wu, row_bytes, x, xs16, y, ys16, n, k, stream=None):
     check(lib().hipllm_gemv_swiglu(qtype, _ptr(wg), _ptr(wu), row_bytes, _ptr(x), _ptr(xs16), _ptr(y), _ptr(ys16),
                                    n, k, _stream(stream)))
+
+
+def _k_to_bf16(x, ldx, xb, m, k, stream=None):
+    check(lib().hipllm_to_bf16(_ptr(x), ldx, _ptr(xb), m, k, _stream(stream)))
+
+
+def _k_gemm_mfma(qtype, w, row_bytes, xb, bias, residual, y, m, n, k, tile=-1, stream=None):
+    check(lib().hipllm_gemm_mfma(qtype, _ptr(w), row_bytes, _ptr(xb), _ptr(bias), _ptr(residual), _ptr(y),
+                                 m, n, k, tile, _stream(stream)))
+
+
+def _k_gemm(qtype, w, row_bytes, x, ldx, bias, y, m, n, k, workspace, stream=None):
+    check(lib().hipllm_gemm(qtype, _ptr(w), row_bytes, _ptr(x), ldx, _ptr(bias), _ptr(y), m, n, k,
+                            _ptr(workspace), _stream(stream)))
 
 
 def _k_rmsnorm(x, gamma, y, ys16, rows, cols, eps, stream=None):
@@ -298,7 +316,8 @@ def _k_swiglu(g, u, y, y16, n, stream=None):
 
 kernels = types.SimpleNamespace(
     dequant_rows=_k_dequant_rows, prep_sums=_k_prep_sums, gemv=_k_gemv, gemv_prepped=_k_gemv_prepped,
-    gemv_swiglu=_k_gemv_swiglu, rmsnorm=_k_rmsnorm, embed=_k_embed, rope_kv=_k_rope_kv,
+    gemv_swiglu=_k_gemv_swiglu, to_bf16=_k_to_bf16, gemm_mfma=_k_gemm_mfma, gemm=_k_gemm,
+    gemm_workspace_bytes=lambda m, k: lib().hipllm_gemm_workspace_bytes(m, k), rmsnorm=_k_rmsnorm, embed=_k_embed, rope_kv=_k_rope_kv,
     attn_decode=_k_attn_decode, argmax=_k_argmax, swiglu=_k_swiglu,
     gemv_workspace_bytes=lambda k: lib().hipllm_gemv_workspace_bytes(k),
     attn_decode_scratch_floats=lambda hq, d, n: lib().hipllm_attn_decode_scratch_floats(hq, d, n),

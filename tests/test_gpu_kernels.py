@@ -96,7 +96,7 @@ def test_dequant_special_halves(cuda):
 
 
 # ------------------------------------------------------------- GEMV
-def gemv_case(cuda, qtype, n, k, seed, bias=False, residual=False, rows_per_block=0):
+def gemv_case(cuda, qtype, n, k, seed, bias=False, residual=False, tiling=0):
     w = random_rows(qtype, n, k, seed)
     x = synth.normal(k, seed + 1)
     dw = dev_bytes(w, cuda)
@@ -107,7 +107,7 @@ def gemv_case(cuda, qtype, n, k, seed, bias=False, residual=False, rows_per_bloc
     r = synth.normal(n, seed + 3) if residual else None
     y = torch.empty(n, dtype=torch.float32, device=cuda)
     kernels.gemv_prepped(qtype, dw, w.shape[1], dx, xs16, None if b is None else torch.from_numpy(b).to(cuda),
-                         None if r is None else torch.from_numpy(r).to(cuda), y, n, k, rows_per_block)
+                         None if r is None else torch.from_numpy(r).to(cuda), y, n, k, tiling)
     # Reference: float64 over the FP32 dequantized weights (GPU dequant is
     # bit-exact to the oracle, checked above).
     wf = torch.empty(n * k, dtype=torch.float32, device=cuda)
@@ -134,11 +134,35 @@ def test_gemv_two_byte_aligned_blocks(cuda, qtype):
     assert rel_err(y, ref) <= 1e-3
 
 
-@pytest.mark.parametrize("rows_per_block", [2, 4, 8, 16, 32])
-def test_gemv_tilings_agree(cuda, rows_per_block):
-    y, ref = gemv_case(cuda, synth.Q4_K, 1000, 3584, seed=7, bias=True, residual=True,
-                       rows_per_block=rows_per_block)
+TILINGS = [11, 12, 14, 18, 21, 22, 24, 28, 41, 42, 44, 48]
+# K-sliced form (Q4_K / Q6_K): 2000 + 100 R + 10 teams + rows per block / 16.
+SLICE_CODES = [2211, 2224, 2412, 2414, 2421, 2443, 2482]
+
+
+@pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q6_K, synth.Q8_0, synth.Q5_0, synth.F16, synth.F32])
+@pytest.mark.parametrize("tiling", TILINGS)
+def test_gemv_tilings_agree(cuda, qtype, tiling):
+    # 1001 rows: no tiling divides it, so every one has a partial last block.
+    y, ref = gemv_case(cuda, qtype, 1001, 2048, seed=7, bias=True, residual=True, tiling=tiling)
     assert rel_err(y, ref) <= 1e-3
+
+
+@pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q6_K])
+@pytest.mark.parametrize("code", SLICE_CODES)
+@pytest.mark.parametrize("k", [2048, 4864, 18944])
+def test_gemv_slice_codes(cuda, qtype, code, k):
+    # k = 2048: 8 super-blocks, half of a wave's slots idle; 4864: 19, two K
+    # slices with a ragged second; 18944: 74, five slices. 1001 rows leave a
+    # partial last block for every rows-per-block choice.
+    if code // 10 % 10 * ((k // 256 + 15) // 16) > 8:
+        pytest.skip("more than 8 waves per block")
+    y, ref = gemv_case(cuda, qtype, 1001, k, seed=code, bias=True, residual=True, tiling=code)
+    assert rel_err(y, ref) <= 1e-3
+
+
+def test_gemv_slice_rejected_for_other_types(cuda):
+    with pytest.raises(ValueError):
+        gemv_case(cuda, synth.Q8_0, 64, 4096, seed=1, tiling=2412)
 
 
 @pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q6_K])
@@ -167,6 +191,7 @@ def test_gemv_public_entry_with_workspace(cuda):
 
 
 @pytest.mark.parametrize("qtype,n,k", [(synth.Q4_K, 4864, 1024), (synth.Q4_K, 2048, 3584),
+                                        (synth.Q4_K, 18944, 3584), (synth.Q6_K, 1040, 5120),
                                         (synth.Q5_0, 480, 896)])
 def test_gemv_swiglu(cuda, qtype, n, k):
     wg, wu = random_rows(qtype, n, k, 31), random_rows(qtype, n, k, 32)

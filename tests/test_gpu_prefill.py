@@ -1,0 +1,104 @@
+"""Prefill matmul parity on the GPU (bf16 MFMA over native GGUF weights).
+
+Two references per case, both float64 over the bit-exact FP32 dequantized
+weights:
+* the contract: against the FP32 operands, max|Y - ref| / max|ref| <= 2e-2;
+* the kernel's own arithmetic: against the same product with X and W first
+  rounded to bf16 (round to nearest even), within 1e-4 -- what is left is
+  FP32 accumulation order, so a wrong operand layout, k map or tile edge
+  fails here even when it would hide inside the 2e-2 bound.
+"""
+
+from __future__ import annotations
+
+import pytest
+
+from myllm_amd import synth
+from myllm_amd.hipllm import kernels
+from tests.test_gpu_kernels import dev_bytes, random_rows, rel_err
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+TYPES = [synth.Q4_K, synth.Q6_K, synth.Q8_0, synth.Q5_0, synth.F16, synth.F32]
+
+
+def gemm_case(cuda, qtype, m, n, k, seed, tile=-1, bias=False, residual=False):
+    w = random_rows(qtype, n, k, seed)
+    dw = dev_bytes(w, cuda)
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    x = torch.randn(m, k, generator=g).to(cuda)
+    xb = torch.empty(m, k, dtype=torch.bfloat16, device=cuda)
+    kernels.to_bf16(x, k, xb, m, k)
+    b = torch.randn(n, generator=g).to(cuda) if bias else None
+    r = torch.randn(m, n, generator=g).to(cuda) if residual else None
+    y = torch.empty(m, n, dtype=torch.float32, device=cuda)
+    kernels.gemm_mfma(qtype, dw, w.shape[1], xb, b, r, y, m, n, k, tile)
+    wf = torch.empty(n, k, dtype=torch.float32, device=cuda)
+    kernels.dequant_rows(qtype, dw, w.shape[1], n, k, wf)
+    ref = x.double() @ wf.double().T
+    ref_b = x.to(torch.bfloat16).double() @ wf.to(torch.bfloat16).double().T
+    for extra in (b, r):
+        if extra is not None:
+            ref = ref + extra.double()
+            ref_b = ref_b + extra.double()
+    assert torch.equal(xb, x.to(torch.bfloat16)), "to_bf16 must round to nearest even like torch"
+    return y.double().cpu().numpy(), ref.cpu().numpy(), ref_b.cpu().numpy()
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("tile", [0, 1, 2, 3])
+def test_gemm_types_and_tiles_ragged(cuda, qtype, tile):
+    # m = 77, n = 333: partial tiles on both axes; k = 512: four 128-steps
+    # (both halves of a K-quant super-block).
+    y, ref, ref_b = gemm_case(cuda, qtype, 77, 333, 512, seed=qtype * 10 + tile, tile=tile, bias=True,
+                              residual=True)
+    assert rel_err(y, ref) <= 2e-2
+    assert rel_err(y, ref_b) <= 1e-4
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_gemm_small_m(cuda, qtype):
+    y, ref, ref_b = gemm_case(cuda, qtype, 1, 260, 1024, seed=3)
+    assert rel_err(y, ref) <= 2e-2
+    assert rel_err(y, ref_b) <= 1e-4
+
+
+@pytest.mark.parametrize("m", [64, 512, 2048])
+def test_gemm_qwen7b_prefill_shape_q4k(cuda, m):
+    # M x K=3584 x N=18944 with Q4_K weights (the prefill matmul microbench).
+    y, ref, ref_b = gemm_case(cuda, synth.Q4_K, m, 18944, 3584, seed=m)
+    assert rel_err(y, ref) <= 2e-2
+    assert rel_err(y, ref_b) <= 1e-4
+
+
+def test_gemm_qwen7b_down_shape_q6k(cuda):
+    y, ref, ref_b = gemm_case(cuda, synth.Q6_K, 512, 3584, 18944, seed=5)
+    assert rel_err(y, ref) <= 2e-2
+    assert rel_err(y, ref_b) <= 1e-4
+
+
+def test_gemm_fp32_entry_with_workspace(cuda):
+    m, n, k = 40, 300, 896
+    w = random_rows(synth.Q5_0, n, k, 9)
+    dw = dev_bytes(w, cuda)
+    x = torch.randn(m, k + 8, device=cuda)  # ldx > k
+    ws = torch.empty(kernels.gemm_workspace_bytes(m, k), dtype=torch.uint8, device=cuda)
+    y = torch.empty(m, n, device=cuda)
+    kernels.gemm(synth.Q5_0, dw, w.shape[1], x, k + 8, None, y, m, n, k, ws)
+    wf = torch.empty(n, k, dtype=torch.float32, device=cuda)
+    kernels.dequant_rows(synth.Q5_0, dw, w.shape[1], n, k, wf)
+    ref = x[:, :k].double() @ wf.double().T
+    assert rel_err(y.double().cpu().numpy(), ref.cpu().numpy()) <= 2e-2
+
+
+def test_gemm_rejects_bad_arguments(cuda):
+    w = torch.zeros(144 * 4 + 256, dtype=torch.uint8, device=cuda)
+    xb = torch.zeros(2, 256, dtype=torch.bfloat16, device=cuda)
+    y = torch.zeros(2, 2, device=cuda)
+    with pytest.raises(ValueError):
+        kernels.gemm_mfma(synth.Q4_K, w, 144, xb, None, None, y, 2, 2, 192)  # k % 128 != 0
+    with pytest.raises(ValueError):
+        kernels.gemm_mfma(synth.Q4_K, w, 144, xb, None, None, y, 2, 2, 256, 7)  # unknown tile
+    with pytest.raises(ValueError):
+        kernels.gemm_mfma(99, w, 144, xb, None, None, y, 2, 2, 256)  # unknown type
