@@ -31,6 +31,7 @@
 // realign with v_alignbyte. Device weight buffers carry 256 bytes of tail
 // padding so those reads stay in bounds.
 #include "common.h"
+#include "launch.h"
 
 namespace hipllm {
 
@@ -818,18 +819,36 @@ int launch_slice(const SliceCfg& cfg, const void* w, const void* w2, size_t row_
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
-// Default slice configuration: R = 4; as many row teams as fit 8 waves per
-// block (at most 4); rows per block so the grid is about two blocks per CU.
-int slice_default(uint32_t n, uint32_t units) {
-    const uint32_t wpr = (units + 15) / 16;
-    uint32_t teams = 1;
-    while (teams * 2 * wpr <= kSliceMaxWaves && teams < 4) teams *= 2;
-    uint32_t rpb = (n / 512 + 15) / 16 * 16;
-    rpb = rpb < 16 ? 16 : rpb > kSliceMaxRows ? kSliceMaxRows : rpb;
-    return 2000 + 400 + 10 * static_cast<int>(teams) + static_cast<int>(rpb / 16);
+bool slice_type(uint32_t type) { return type == kQ4_K || type == kQ6_K; }
+
+// Measured choice on MI355X (tests sweep every code; these won per shape):
+// Q4_K keeps the octet form (R = 4 or 2, OPR = 8) up to tens of thousands of
+// rows and switches to the slice form for LM-head-sized matrices; Q6_K, with
+// more bit work per byte, prefers the slice form once rows hold >= 12
+// super-blocks.
+int gemv_pick_shape(uint32_t type, uint32_t n, uint32_t units, int mode) {
+    if (type == kQ4_K) {
+        if (mode == 0 && n >= 65536 && units >= 12) return 2411;
+        return units >= 32 ? 28 : 48;
+    }
+    if (type == kQ6_K && units >= 12) {
+        if (n >= 65536) return mode == 0 ? 2442 : 2222;
+        if (units >= 32) return 2211;
+        if (n >= 8192) return 2241;
+        return 28;
+    }
+    return gemv_default_tiling(n, units, mode);
 }
 
-bool slice_type(uint32_t type) { return type == kQ4_K || type == kQ6_K; }
+// The fused SwiGLU form writes per-16 sums of its outputs, so its octet
+// tilings need rows per block (32 R / OPR) divisible by 16.
+int gemv_pick(uint32_t type, uint32_t n, uint32_t units, int mode) {
+    const int code = gemv_pick_shape(type, n, units, mode);
+    if (mode == 1 && code < 100 && (32 * (code / 10) / (code % 10)) % 16 != 0) {
+        return gemv_default_tiling(n, units, 1);
+    }
+    return code;
+}
 
 uint32_t unit_elems(uint32_t type) {
     switch (type) {
@@ -899,14 +918,14 @@ int launch_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const fl
     const uint32_t units = static_cast<uint32_t>(k / ue);
     const uint32_t nn = static_cast<uint32_t>(n);
     SliceCfg sc;
-    const int code = tiling ? tiling : (slice_type(type) && units >= 12 ? slice_default(nn, units) : 0);
+    const int code = tiling ? tiling : gemv_pick(type, nn, units, 0);
     if (decode_slice(code, sc)) {
         if (!slice_type(type)) return kInvalidArgument;
         if (type == kQ4_K) return launch_slice<kQ4_K, 0>(sc, w, nullptr, row_bytes, x, xs16, bias, residual, y, nullptr, nn, units, stream);
         return launch_slice<kQ6_K, 0>(sc, w, nullptr, row_bytes, x, xs16, bias, residual, y, nullptr, nn, units, stream);
     }
-    if (tiling != 0 && !valid_tiling(tiling)) return kInvalidArgument;
-    const int t = tiling ? tiling : gemv_default_tiling(nn, units, 0);
+    if (!valid_tiling(code)) return kInvalidArgument;
+    const int t = code;
     switch (type) {
     case kQ4_K: return launch_typed<kQ4_K, 0>(t, w, nullptr, row_bytes, x, xs16, bias, residual, y, nullptr, nn, units, stream);
     case kQ6_K: return launch_typed<kQ6_K, 0>(t, w, nullptr, row_bytes, x, xs16, bias, residual, y, nullptr, nn, units, stream);
@@ -942,11 +961,12 @@ int launch_gemv_swiglu(uint32_t type, const void* wg, const void* wu, size_t row
     const uint32_t units = static_cast<uint32_t>(k / ue);
     const uint32_t nn = static_cast<uint32_t>(n);
     SliceCfg sc;
-    if (slice_type(type) && units >= 12 && decode_slice(slice_default(nn, units), sc)) {
+    const int code = gemv_pick(type, nn, units, 1);
+    if (decode_slice(code, sc)) {
         if (type == kQ4_K) return launch_slice<kQ4_K, 1>(sc, wg, wu, row_bytes, x, xs16, nullptr, nullptr, y, ys16, nn, units, stream);
         return launch_slice<kQ6_K, 1>(sc, wg, wu, row_bytes, x, xs16, nullptr, nullptr, y, ys16, nn, units, stream);
     }
-    const int t = gemv_default_tiling(nn, units, 1);
+    const int t = code;
     switch (type) {
     case kQ4_K: return launch_typed<kQ4_K, 1>(t, wg, wu, row_bytes, x, xs16, nullptr, nullptr, y, ys16, nn, units, stream);
     case kQ6_K: return launch_typed<kQ6_K, 1>(t, wg, wu, row_bytes, x, xs16, nullptr, nullptr, y, ys16, nn, units, stream);

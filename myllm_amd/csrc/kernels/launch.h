@@ -23,7 +23,11 @@ int launch_gemv_swiglu(uint32_t type, const void* wg, const void* wu, size_t row
 int gemm_default_tile(uint32_t m, uint32_t n);
 int launch_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, hipStream_t stream);
 int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* bias,
-                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, hipStream_t stream);
+                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, hipStream_t stream,
+                     size_t ldy = 0);
+int launch_attn_prefill(const float* q, size_t q_stride, const float* kcache, const float* vcache, float* out,
+                        size_t out_stride, size_t rows, size_t hq, size_t hkv, size_t d, size_t pos0, float scale,
+                        hipStream_t stream);
 
 int launch_rmsnorm(const float* x, const float* gamma, float* y, float* ys16, size_t rows, size_t cols, float eps,
                    hipStream_t stream);

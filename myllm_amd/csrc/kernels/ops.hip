@@ -207,6 +207,72 @@ __global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict
     }
 }
 
+// Causal prefill attention (cpu_llm.cpp:609-629 gemmts + causal_mask
+// 316-329 + softmax 168-186 + gemm 549-565; metal_kv_cache_qk/av_f32
+// metal_llm.metal:995-1061): block (row r, head h) attends query row r, at
+// absolute position pos0 + r, to keys [0, pos0 + r] of the caches. Keys are
+// scored 256 at a time (one per thread) with an online softmax; threads
+// d < D accumulate the output dimension d, so V rows are read coalesced.
+__global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restrict__ q, uint32_t q_stride,
+                                                           const float* __restrict__ kcache,
+                                                           const float* __restrict__ vcache, float* __restrict__ out,
+                                                           uint32_t out_stride, uint32_t hq, uint32_t hkv, uint32_t d,
+                                                           uint32_t pos0, float scale) {
+    const uint32_t r = blockIdx.x;
+    const uint32_t h = blockIdx.y;
+    const uint32_t g = h / (hq / hkv);
+    const uint32_t kvd = hkv * d;
+    const uint32_t len = pos0 + r + 1;
+    __shared__ float qs[256];
+    __shared__ float ps[256];
+    __shared__ float red[8];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wave = tid >> 6, lane = tid & 63;
+    for (uint32_t i = tid; i < d; i += blockDim.x) qs[i] = q[static_cast<size_t>(r) * q_stride + h * d + i];
+    __syncthreads();
+    float m_run = -INFINITY, l_run = 0.0f, acc = 0.0f;
+    for (uint32_t t0 = 0; t0 < len; t0 += 256) {
+        const uint32_t t = t0 + tid;
+        float s = -INFINITY;
+        if (t < len) {
+            const float4* k = reinterpret_cast<const float4*>(kcache + static_cast<size_t>(t) * kvd + g * d);
+            float dot = 0.0f;
+            for (uint32_t i = 0; i < d / 4; ++i) {
+                const float4 kv = k[i];
+                dot = fmaf(kv.x, qs[4 * i], dot);
+                dot = fmaf(kv.y, qs[4 * i + 1], dot);
+                dot = fmaf(kv.z, qs[4 * i + 2], dot);
+                dot = fmaf(kv.w, qs[4 * i + 3], dot);
+            }
+            s = dot * scale;
+        }
+        float cm = warp_max(s);
+        if (lane == 0) red[wave] = cm;
+        __syncthreads();
+        cm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        const float m_new = fmaxf(m_run, cm);  // finite: key t0 is always valid
+        const float p = t < len ? expf(s - m_new) : 0.0f;
+        ps[tid] = p;
+        float cs = warp_sum(p);
+        __syncthreads();  // red[0..3] read by all before reuse
+        if (lane == 0) red[4 + wave] = cs;
+        __syncthreads();
+        cs = (red[4] + red[5]) + (red[6] + red[7]);
+        const float corr = expf(m_run - m_new);
+        l_run = l_run * corr + cs;
+        if (tid < d) {
+            const uint32_t cnt = min(256u, len - t0);
+            const float* v = vcache + static_cast<size_t>(t0) * kvd + g * d + tid;
+            float a = 0.0f;
+            for (uint32_t j = 0; j < cnt; ++j) a = fmaf(ps[j], v[static_cast<size_t>(j) * kvd], a);
+            acc = acc * corr + a;
+        }
+        m_run = m_new;
+        __syncthreads();  // ps and red reused by the next chunk
+    }
+    if (tid < d) out[static_cast<size_t>(r) * out_stride + h * d + tid] = acc / l_run;
+}
+
 // ------------------------------------------------------------ argmax
 // Ties resolve to the lower index; NaN never wins (strict '>').
 __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
@@ -349,6 +415,19 @@ int launch_attn_decode(const float* q, const float* kcache, const float* vcache,
                        static_cast<uint32_t>(d), static_cast<uint32_t>(len), scale, nchunks);
     hipLaunchKernelGGL(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out, out16,
                        static_cast<uint32_t>(d), nchunks);
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+int launch_attn_prefill(const float* q, size_t q_stride, const float* kcache, const float* vcache, float* out,
+                        size_t out_stride, size_t rows, size_t hq, size_t hkv, size_t d, size_t pos0, float scale,
+                        hipStream_t stream) {
+    if (!q || !kcache || !vcache || !out || rows == 0 || hq == 0 || hkv == 0 || hq % hkv) return kInvalidArgument;
+    if (d == 0 || d > 256 || d % 4 != 0 || q_stride < hq * d || out_stride < hq * d) return kInvalidArgument;
+    if (rows > 0x7fffffffull || hq > 0xffffull || pos0 + rows > 0xffffffffull) return kLengthError;
+    hipLaunchKernelGGL(attn_prefill_kernel, dim3(static_cast<uint32_t>(rows), static_cast<uint32_t>(hq)), dim3(256),
+                       0, stream, q, static_cast<uint32_t>(q_stride), kcache, vcache, out,
+                       static_cast<uint32_t>(out_stride), static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv),
+                       static_cast<uint32_t>(d), static_cast<uint32_t>(pos0), scale);
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 

@@ -341,7 +341,7 @@ template <uint32_t T, int NSUB, int MSUB>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restrict__ w, size_t row_bytes,
                                                         const __bf16* __restrict__ xb, const float* __restrict__ bias,
                                                         const float* __restrict__ residual, float* __restrict__ y,
-                                                        uint32_t m, uint32_t n, uint32_t k) {
+                                                        uint32_t m, uint32_t n, uint32_t k, uint32_t ldy) {
     using WT = WTile<T>;
     constexpr int BM = 32 * MSUB;
     constexpr int WN = 32 * NSUB;
@@ -443,7 +443,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
                 for (int r = 0; r < 4; ++r) {
                     const uint32_t row = m0 + 32 * ms + 8 * g + 4 * h + r;
                     if (row < m) {
-                        const size_t o = static_cast<size_t>(row) * n + col;
+                        const size_t o = static_cast<size_t>(row) * ldy + col;
                         float v = acc[ns][ms][4 * g + r] + b;
                         if (residual) v += residual[o];
                         y[o] = v;
@@ -478,21 +478,22 @@ __global__ void to_bf16_kernel(const float* __restrict__ x, size_t ldx, __bf16* 
 
 template <uint32_t T, int NSUB, int MSUB>
 void launch_tile(const void* w, size_t row_bytes, const __bf16* xb, const float* bias, const float* residual, float* y,
-                 uint32_t m, uint32_t n, uint32_t k, hipStream_t stream) {
+                 uint32_t m, uint32_t n, uint32_t k, uint32_t ldy, hipStream_t stream) {
     constexpr uint32_t BN = 4 * 32 * NSUB, BM = 32 * MSUB;
     const dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM);
     hipLaunchKernelGGL((gemm_mfma_kernel<T, NSUB, MSUB>), grid, dim3(256), 0, stream,
-                       static_cast<const uint8_t*>(w), row_bytes, xb, bias, residual, y, m, n, k);
+                       static_cast<const uint8_t*>(w), row_bytes, xb, bias, residual, y, m, n, k, ldy);
 }
 
 template <uint32_t T>
 int launch_typed(int tile, const void* w, size_t row_bytes, const __bf16* xb, const float* bias,
-                 const float* residual, float* y, uint32_t m, uint32_t n, uint32_t k, hipStream_t stream) {
+                 const float* residual, float* y, uint32_t m, uint32_t n, uint32_t k, uint32_t ldy,
+                 hipStream_t stream) {
     switch (tile) {
-    case 0: launch_tile<T, 1, 1>(w, row_bytes, xb, bias, residual, y, m, n, k, stream); break;
-    case 1: launch_tile<T, 1, 2>(w, row_bytes, xb, bias, residual, y, m, n, k, stream); break;
-    case 2: launch_tile<T, 2, 2>(w, row_bytes, xb, bias, residual, y, m, n, k, stream); break;
-    case 3: launch_tile<T, 2, 4>(w, row_bytes, xb, bias, residual, y, m, n, k, stream); break;
+    case 0: launch_tile<T, 1, 1>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, stream); break;
+    case 1: launch_tile<T, 1, 2>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, stream); break;
+    case 2: launch_tile<T, 2, 2>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, stream); break;
+    case 3: launch_tile<T, 2, 4>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, stream); break;
     default: return kInvalidArgument;
     }
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
@@ -526,8 +527,10 @@ int launch_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, hip
 }
 
 int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* bias,
-                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, hipStream_t stream) {
-    if (!w || !xb || !y || m == 0 || n == 0 || k == 0) return kInvalidArgument;
+                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, hipStream_t stream,
+                     size_t ldy) {
+    if (ldy == 0) ldy = n;
+    if (!w || !xb || !y || m == 0 || n == 0 || k == 0 || ldy < n || ldy > 0x7fffffffull) return kInvalidArgument;
     if (k % kStepK != 0) return kInvalidArgument;
     if (m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull) return kLengthError;
     if (type != kF32 && type != kF16 && type != kQ5_0 && type != kQ8_0 && type != kQ4_K && type != kQ6_K) {
@@ -544,12 +547,12 @@ int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void*
     const uint32_t M = static_cast<uint32_t>(m), N = static_cast<uint32_t>(n), K = static_cast<uint32_t>(k);
     const auto* x = static_cast<const __bf16*>(xb);
     switch (type) {
-    case kQ4_K: return launch_typed<kQ4_K>(tile, w, row_bytes, x, bias, residual, y, M, N, K, stream);
-    case kQ6_K: return launch_typed<kQ6_K>(tile, w, row_bytes, x, bias, residual, y, M, N, K, stream);
-    case kQ8_0: return launch_typed<kQ8_0>(tile, w, row_bytes, x, bias, residual, y, M, N, K, stream);
-    case kQ5_0: return launch_typed<kQ5_0>(tile, w, row_bytes, x, bias, residual, y, M, N, K, stream);
-    case kF32: return launch_typed<kF32>(tile, w, row_bytes, x, bias, residual, y, M, N, K, stream);
-    case kF16: return launch_typed<kF16>(tile, w, row_bytes, x, bias, residual, y, M, N, K, stream);
+    case kQ4_K: return launch_typed<kQ4_K>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), stream);
+    case kQ6_K: return launch_typed<kQ6_K>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), stream);
+    case kQ8_0: return launch_typed<kQ8_0>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), stream);
+    case kQ5_0: return launch_typed<kQ5_0>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), stream);
+    case kF32: return launch_typed<kF32>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), stream);
+    case kF16: return launch_typed<kF16>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), stream);
     default: return kInvalidArgument;
     }
 }

@@ -257,8 +257,7 @@ int hipllm_copy_logits(const HipllmModel* m, float* out, size_t count) {
 
 int hipllm_set_batched_prefill(HipllmModel* m, int enabled) {
     if (!m) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_set_batched_prefill: null argument");
-    m->model.set_batched_prefill(enabled != 0);
-    return HIPLLM_OK;
+    return guarded([&] { m->model.set_batched_prefill(enabled != 0); });
 }
 
 }  // extern "C"

@@ -76,6 +76,17 @@ struct Activations {
     std::uint32_t* token = nullptr;
 };
 
+// Device buffers of the batched prefill: T prompt rows each.
+struct PrefillActivations {
+    float* hidden[2] = {nullptr, nullptr};  // [T, H]
+    float* norm = nullptr;                  // [T, H]
+    float* qkv = nullptr;                   // [T, H + 2 kv]
+    float* attn = nullptr;                  // [T, H]
+    float* gate = nullptr;                  // [T, F]
+    float* up = nullptr;                    // [T, F]
+    void* xb = nullptr;                     // bf16 [T, max(H, F)]
+};
+
 }  // namespace
 
 struct HipLLM::Impl {
@@ -103,6 +114,11 @@ struct HipLLM::Impl {
     Activations act;
     std::size_t prompt_capacity = 0;
 
+    void* pre_arena = nullptr;
+    std::size_t pre_bytes = 0;
+    std::size_t pre_rows = 0;
+    PrefillActivations pre;
+
     std::int32_t* host_ids = nullptr;      // pinned
     std::uint32_t* host_token = nullptr;   // pinned
 
@@ -115,6 +131,7 @@ struct HipLLM::Impl {
         if (kv_arena) hipFree(kv_arena);
         if (rope_table) hipFree(rope_table);
         if (act_arena) hipFree(act_arena);
+        if (pre_arena) hipFree(pre_arena);
         if (host_ids) hipHostFree(host_ids);
         if (host_token) hipHostFree(host_token);
         if (stream) hipStreamDestroy(stream);
@@ -128,11 +145,18 @@ struct HipLLM::Impl {
     void allocate_state();
     void build_rope_table();
     void ensure_prompt_capacity(std::size_t n);
+    void ensure_prefill_rows(std::size_t n);
+    bool batched_shapes() const;
 
     void gemv(const DevMatrix& w, const float* x, const float* xs16, const float* bias, const float* residual,
               float* y, std::size_t rows_override = 0) const;
     void layer_step(std::size_t li, std::size_t pos, float* hidden, float* next_hidden);
     void token_step(const std::int32_t* device_id, std::size_t pos, bool head);
+    void gemm(const DevMatrix& w, const void* xb, const float* bias, const float* residual, float* y,
+              std::size_t rows, std::size_t ldy, std::size_t n_override = 0) const;
+    void prefill_layer(std::size_t li, std::size_t rows, float* hidden, float* next_hidden);
+    void prefill_batched(std::size_t rows);
+    void head_step(const float* hidden_row);
     std::int32_t read_token();
 };
 
@@ -173,6 +197,7 @@ void HipLLM::Impl::load(const std::string& path, std::size_t capacity, int dev) 
     upload(reader);
     allocate_state();
     build_rope_table();
+    batched_prefill = batched_shapes();
 }
 
 void HipLLM::Impl::upload(GgufReader& reader) {
@@ -477,12 +502,115 @@ void HipLLM::Impl::token_step(const std::int32_t* device_id, std::size_t pos, bo
                                       c.vocabulary_size, H, h, stream),
                  "embedding");
     for (std::size_t l = 0; l < layers.size(); ++l) layer_step(l, pos, h, tmp);
-    if (!head) return;
-    launch_check(hipllm::launch_rmsnorm(h, output_norm, act.norm, act.norm16, 1, H, c.norm_epsilon, stream),
+    if (head) head_step(h);
+}
+
+// Batched prefill buffers, grown to the longest prompt seen.
+void HipLLM::Impl::ensure_prefill_rows(std::size_t n) {
+    if (n <= pre_rows && pre_arena) return;
+    hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    if (pre_arena) hipFree(pre_arena);
+    pre_arena = nullptr;
+    pre_rows = 0;
+    const ModelConfig& c = config;
+    const std::size_t H = c.embedding_size, F = c.feed_forward_size;
+    std::size_t off = 0;
+    auto reserve = [&](std::size_t bytes) {
+        const std::size_t at = off;
+        off = align_up(off + bytes, 256);
+        return at;
+    };
+    const std::size_t o_h0 = reserve(n * H * 4), o_h1 = reserve(n * H * 4), o_norm = reserve(n * H * 4),
+                      o_qkv = reserve(n * (H + 2 * kv_dim) * 4), o_attn = reserve(n * H * 4),
+                      o_gate = reserve(n * F * 4), o_up = reserve(n * F * 4),
+                      o_xb = reserve(n * std::max(H, F) * 2);
+    pre_bytes = off;
+    hip_check(hipMalloc(&pre_arena, pre_bytes), "hipMalloc(prefill activations)");
+    auto* base = static_cast<std::uint8_t*>(pre_arena);
+    pre.hidden[0] = reinterpret_cast<float*>(base + o_h0);
+    pre.hidden[1] = reinterpret_cast<float*>(base + o_h1);
+    pre.norm = reinterpret_cast<float*>(base + o_norm);
+    pre.qkv = reinterpret_cast<float*>(base + o_qkv);
+    pre.attn = reinterpret_cast<float*>(base + o_attn);
+    pre.gate = reinterpret_cast<float*>(base + o_gate);
+    pre.up = reinterpret_cast<float*>(base + o_up);
+    pre.xb = base + o_xb;
+    pre_rows = n;
+}
+
+// The MFMA prefill matmul steps K by 128.
+bool HipLLM::Impl::batched_shapes() const {
+    return config.embedding_size % 128 == 0 && config.feed_forward_size % 128 == 0;
+}
+
+void HipLLM::Impl::gemm(const DevMatrix& w, const void* xb, const float* bias, const float* residual, float* y,
+                        std::size_t rows, std::size_t ldy, std::size_t n_override) const {
+    const std::size_t n = n_override ? n_override : w.rows;
+    launch_check(hipllm::launch_gemm_mfma(w.type, w.ptr, w.row_bytes, xb, bias, residual, y, rows, n, w.cols, -1,
+                                          stream, ldy),
+                 "prefill matmul");
+}
+
+// One decoder layer over `rows` prompt rows (cpu_prefill_layer,
+// cpu_llm.cpp:774-841): every projection is one bf16 MFMA matmul over the
+// native weights; attention is causal over the rows just written to the cache.
+void HipLLM::Impl::prefill_layer(std::size_t li, std::size_t rows, float* hidden, float* next_hidden) {
+    const ModelConfig& c = config;
+    const DevLayer& L = layers[li];
+    const std::size_t H = c.embedding_size, F = c.feed_forward_size;
+    const std::size_t qkv_w = H + 2 * kv_dim;
+    const float eps = c.norm_epsilon;
+    launch_check(hipllm::launch_rmsnorm(hidden, L.attn_norm, pre.norm, nullptr, rows, H, eps, stream), "RMSNorm");
+    launch_check(hipllm::launch_to_bf16(pre.norm, H, pre.xb, rows, H, stream), "bf16 activations");
+    if (L.fused_qkv) {
+        gemm(L.q, pre.xb, L.qkv_bias, nullptr, pre.qkv, rows, qkv_w, qkv_w);
+    } else {
+        gemm(L.q, pre.xb, L.qkv_bias, nullptr, pre.qkv, rows, qkv_w);
+        gemm(L.k, pre.xb, L.qkv_bias + H, nullptr, pre.qkv + H, rows, qkv_w);
+        gemm(L.v, pre.xb, L.qkv_bias + H + kv_dim, nullptr, pre.qkv + H + kv_dim, rows, qkv_w);
+    }
+    launch_check(hipllm::launch_rope_kv(pre.qkv, rope_table, c.rotary_dimension, c.attention_head_count,
+                                        c.kv_head_count, c.head_size, 0, rows, qkv_w, kcache(li), vcache(li), stream),
+                 "RoPE/KV write");
+    const float scale = 1.0f / std::sqrt(static_cast<float>(c.head_size));
+    launch_check(hipllm::launch_attn_prefill(pre.qkv, qkv_w, kcache(li), vcache(li), pre.attn, H, rows,
+                                             c.attention_head_count, c.kv_head_count, c.head_size, 0, scale, stream),
+                 "prefill attention");
+    launch_check(hipllm::launch_to_bf16(pre.attn, H, pre.xb, rows, H, stream), "bf16 activations");
+    gemm(L.o, pre.xb, nullptr, hidden, next_hidden, rows, H);
+    launch_check(hipllm::launch_rmsnorm(next_hidden, L.ffn_norm, pre.norm, nullptr, rows, H, eps, stream), "RMSNorm");
+    launch_check(hipllm::launch_to_bf16(pre.norm, H, pre.xb, rows, H, stream), "bf16 activations");
+    gemm(L.gate, pre.xb, nullptr, nullptr, pre.gate, rows, F);
+    gemm(L.up, pre.xb, nullptr, nullptr, pre.up, rows, F);
+    launch_check(hipllm::launch_swiglu(pre.gate, pre.up, pre.gate, nullptr, rows * F, stream), "SwiGLU");
+    launch_check(hipllm::launch_to_bf16(pre.gate, F, pre.xb, rows, F, stream), "bf16 activations");
+    gemm(L.down, pre.xb, nullptr, next_hidden, hidden, rows, H);
+}
+
+// Final norm, LM head and argmax on one hidden row (decode kernels).
+void HipLLM::Impl::head_step(const float* hidden_row) {
+    const ModelConfig& c = config;
+    launch_check(hipllm::launch_rmsnorm(hidden_row, output_norm, act.norm, act.norm16, 1, c.embedding_size,
+                                        c.norm_epsilon, stream),
                  "final RMSNorm");
     gemv(output, act.norm, act.norm16, nullptr, nullptr, act.logits);
     launch_check(hipllm::launch_argmax(act.logits, c.vocabulary_size, act.token, act.argmax_scratch, stream),
                  "argmax");
+}
+
+// Whole-prompt prefill: embedding of all rows, L batched layers, then the LM
+// head on the last row only (metal_llm.mm:3266-3277; cpu_llm.cpp:1019-1020).
+void HipLLM::Impl::prefill_batched(std::size_t rows) {
+    ensure_prefill_rows(rows);
+    const ModelConfig& c = config;
+    const std::size_t H = c.embedding_size;
+    float* h = pre.hidden[0];
+    float* tmp = pre.hidden[1];
+    launch_check(hipllm::launch_embed(embedding.type, embedding.ptr, embedding.row_bytes, act.ids, rows,
+                                      c.vocabulary_size, H, h, stream),
+                 "embedding");
+    for (std::size_t l = 0; l < layers.size(); ++l) prefill_layer(l, rows, h, tmp);
+    head_step(h + (rows - 1) * H);
 }
 
 std::int32_t HipLLM::Impl::read_token() {
@@ -526,7 +654,11 @@ std::int32_t HipLLM::prefill(const std::vector<std::int32_t>& ids) {
     m.ensure_prompt_capacity(ids.size());
     std::memcpy(m.host_ids, ids.data(), ids.size() * 4);
     hip_check(hipMemcpyAsync(m.act.ids, m.host_ids, ids.size() * 4, hipMemcpyHostToDevice, m.stream), "hipMemcpy(ids)");
-    for (std::size_t t = 0; t < ids.size(); ++t) m.token_step(m.act.ids + t, t, t + 1 == ids.size());
+    if (m.batched_prefill) {
+        m.prefill_batched(ids.size());
+    } else {
+        for (std::size_t t = 0; t < ids.size(); ++t) m.token_step(m.act.ids + t, t, t + 1 == ids.size());
+    }
     const std::int32_t token = m.read_token();
     m.sequence_length = ids.size();
     if (m.profile) {
@@ -607,8 +739,12 @@ void HipLLM::copy_last_logits(float* dst, std::size_t count) const {
     hip_check(hipMemcpy(dst, impl_->act.logits, count * 4, hipMemcpyDeviceToHost), "hipMemcpy(logits)");
 }
 
-void HipLLM::set_batched_prefill(bool enabled) noexcept {
-    if (impl_) impl_->batched_prefill = enabled;
+void HipLLM::set_batched_prefill(bool enabled) {
+    if (!impl_) throw std::runtime_error("HIP model is not initialized");
+    if (enabled && !impl_->batched_shapes()) {
+        throw std::invalid_argument("batched prefill needs hidden and FFN sizes that are multiples of 128");
+    }
+    impl_->batched_prefill = enabled;
 }
 
 }  // namespace llm

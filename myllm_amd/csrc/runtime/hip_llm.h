@@ -76,7 +76,7 @@ public:
     void copy_last_logits(float* destination, std::size_t count) const;
     // Prefill path selection: true = batched (GEMM) prefill, false = the
     // token-serial decode path for every prompt position.
-    void set_batched_prefill(bool enabled) noexcept;
+    void set_batched_prefill(bool enabled);
 
 private:
     struct Impl;

@@ -25,19 +25,25 @@ def run_with_logits(model, prompt, n):
     return toks, np.stack(logits)
 
 
-@pytest.mark.parametrize("batched", [False])
+# Token-serial prefill runs the FP32 decode kernels (bound 1e-3); the batched
+# prefill runs bf16 MFMA matmuls, whose contract bound is 2e-2 on logits.
+LOGIT_BOUND = {False: 1e-3, True: 2e-2}
+
+
+@pytest.mark.parametrize("batched", [False, True])
 def test_tiny_matches_reference(cuda, golden_model, batched):
     path, g = golden_model("tiny")
     with HipLLM(path, int(g["max_sequence"])) as m:
         m.set_batched_prefill(batched)
         toks, logits = run_with_logits(m, g["prompt"], len(g["tokens"]))
-    assert toks == g["tokens"].tolist()
     ref = g["logits"].astype(np.float64)
     err = np.abs(logits - ref).max(axis=1) / np.abs(ref).max(axis=1)
-    assert err.max() <= 1e-3, err
+    print("max rel logit error per step:", err.max())
+    assert toks == g["tokens"].tolist()
+    assert err.max() <= LOGIT_BOUND[batched], err
 
 
-@pytest.mark.parametrize("batched", [False])
+@pytest.mark.parametrize("batched", [False, True])
 def test_qwen05b_greedy_tokens_match_reference(cuda, golden_model, batched):
     path, g = golden_model("qwen2.5-0.5b")
     with HipLLM(path, int(g["max_sequence"])) as m:
@@ -50,7 +56,20 @@ def test_qwen05b_greedy_tokens_match_reference(cuda, golden_model, batched):
     err = np.abs(top - ref).max(axis=1) / np.abs(ref).max(axis=1)
     print("max rel logit error per step:", err.max())
     assert toks == g["tokens"].tolist()
-    assert err.max() <= 1e-3
+    assert err.max() <= LOGIT_BOUND[batched]
+
+
+def test_batched_prefill_is_default_and_switchable(cuda, golden_model):
+    path, g = golden_model("tiny")
+    with HipLLM(path, 64) as m:
+        batched = m.prefill(list(g["prompt"]))
+        lb = m.logits()
+        m.reset()
+        m.set_batched_prefill(False)
+        serial = m.prefill(list(g["prompt"]))
+        ls = m.logits()
+    assert batched == serial == int(g["tokens"][0])
+    assert np.abs(lb - ls).max() / np.abs(ls).max() <= 2e-2
 
 
 def test_contract_errors(cuda, golden_model):
