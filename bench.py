@@ -1,21 +1,31 @@
 #!/usr/bin/env python3
-"""HipLLM benchmark: quantized decode GEMV bandwidth + end-to-end decode.
+"""HipLLM benchmark: quantized decode GEMV bandwidth, prefill matmul, end-to-end.
 
-Headline (``value``): Q4_K decode-GEMV throughput in GB/s of algorithmic
-bytes at Qwen2.5-7B shapes, batch 1. One step = the four weight GEMVs of one
-decoder layer (fused QKV 3584->4608, gate 3584->18944, up 3584->18944, down
-18944->3584), FP32 activations N(0, 1), weights N(0, 0.02) quantized to
+Headline (``value``): Q4_K decode-GEMV throughput in GB/s of algorithmic bytes
+at Qwen2.5-7B shapes, batch 1. One step = the four weight GEMVs of one decoder
+layer (fused QKV 3584->4608, gate 3584->18944, up 3584->18944, down
+18944->3584) with FP32 activations N(0, 1) and N(0, 0.02) weights quantized to
 Q4_K. Steps rotate over enough weight copies (> 2x the 256 MB Infinity Cache)
-that every GEMV streams its weights from HBM. Algorithmic bytes per GEMV =
-N * row_bytes + 4 K + 4 N. Inputs are resident in HBM before timing; the
-timed steps replay a HIP graph of the launches.
+that every GEMV streams its weights from HBM; inputs are resident in HBM
+before timing and the timed steps replay a HIP graph of the launches.
+Algorithmic bytes per GEMV = N * row_bytes + 4 K + 4 N.
 
-Also reported: the same for Q6_K; per-launch kernel durations from HIP events
-(the roofline entry uses the gate/up GEMV, the dominant kernel); end-to-end
-greedy decode and prefill tok/s of synthetic Qwen2.5-0.5B- and 7B-shaped
-Q4_K_M models through the HipLLM backend; and a bounded CPU baseline.
+The same JSON line carries:
+* ``roofline``: the dominant kernel (the 3584->18944 gate GEMV) timed alone
+  with HIP events on its launch stream, against MI355X's 8 TB/s; ``traffic``
+  is read from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary when
+  present (see --profile-kernel);
+* ``gemv``: per-shape results for Q4_K and Q6_K;
+* ``prefill_gemm``: the bf16-MFMA prefill matmul, M in {64, 512, 2048} x
+  K 3584 x N 18944, Q4_K weights, TFLOP/s against the 2.5 PFLOP/s bf16 peak;
+* ``e2e``: greedy prefill and decode tok/s of synthetic Qwen2.5-0.5B-, 7B- and
+  14B-shaped Q4_K_M models through the HipLLM handle API;
+* ``cpu_baseline``: a bounded sample of the same GEMV step on the host (the
+  oracle's CPULLM gevmt, one thread), plus the reference CPULLM's own decode
+  rate on the 0.5B-shaped model when oracle/_ref is built.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-e2e] [--no-cpu]
+                       [--no-14b] [--profile-kernel gate] [--profile-reps N]
 """
 
 from __future__ import annotations
@@ -35,8 +45,10 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "decode tok/s + Q4_K GEMV HBM GB/s (% peak); prefill tok/s; 1 GPU"
 PEAK_HBM_GBPS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0
 SHAPES = [("qkv", 4608, 3584), ("gate", 18944, 3584), ("up", 18944, 3584), ("down", 3584, 18944)]
 MALL_BYTES = 256 << 20
+TRAFFIC_SUMMARY = ROOT / "profiles" / "gemv_q4k_gate_3584x18944_traffic.txt"
 
 
 def log(*a):
@@ -47,25 +59,40 @@ def gemv_bytes(n, k, row_bytes):
     return n * row_bytes + 4 * k + 4 * n
 
 
-def bench_gemv(qtype, steps, warmup, torch, cuda):
+def scratch_dir():
+    return "/dev/shm" if os.path.isdir("/dev/shm") else None
+
+
+class Rotation:
+    """Device copies of one layer's four weight matrices, rotated per step."""
+
+    def __init__(self, qtype, torch, cuda, min_bytes=3 * MALL_BYTES):
+        from myllm_amd import synth
+        self.host = {}
+        for _, n, k in SHAPES:
+            if (n, k) not in self.host:
+                self.host[(n, k)] = synth.random_quantized(n, k, qtype, seed=n * 7 + k)
+        per_step = sum(self.host[(n, k)].nbytes for _, n, k in SHAPES)
+        self.copies = max(4, int(np.ceil(min_bytes / per_step)))
+        self.layers = []
+        for _ in range(self.copies):
+            layer = {}
+            for name, n, k in SHAPES:
+                src = self.host[(n, k)]
+                buf = torch.empty(src.nbytes + 256, dtype=torch.uint8, device=cuda)
+                buf[: src.nbytes].copy_(torch.from_numpy(src.reshape(-1)))
+                layer[name] = buf
+            self.layers.append(layer)
+        self.step_bytes = sum(gemv_bytes(n, k, self.host[(n, k)].shape[1]) for _, n, k in SHAPES)
+
+    def row_bytes(self, n, k):
+        return self.host[(n, k)].shape[1]
+
+
+def gemv_setup(qtype, torch, cuda):
     from myllm_amd import synth
     from myllm_amd.hipllm import kernels
-
-    host = {}
-    for name, n, k in SHAPES:
-        if (n, k) not in host:
-            host[(n, k)] = synth.random_quantized(n, k, qtype, seed=n * 7 + k)
-    per_step = sum(host[(n, k)].nbytes for _, n, k in SHAPES)
-    copies = max(4, int(np.ceil(3 * MALL_BYTES / per_step)))
-    weights = []
-    for c in range(copies):
-        layer = {}
-        for name, n, k in SHAPES:
-            src = host[(n, k)]
-            buf = torch.empty(src.nbytes + 256, dtype=torch.uint8, device=cuda)
-            buf[: src.nbytes].copy_(torch.from_numpy(src.reshape(-1)))
-            layer[name] = (buf, src.shape[1])
-        weights.append(layer)
+    rot = Rotation(qtype, torch, cuda)
     xs = {k: torch.from_numpy(synth.normal(k, seed=k)).to(cuda) for k in (3584, 18944)}
     sums = {}
     for k, x in xs.items():
@@ -73,15 +100,33 @@ def bench_gemv(qtype, steps, warmup, torch, cuda):
         kernels.prep_sums(x, sums[k], k)
     ys = {name: torch.empty(n, dtype=torch.float32, device=cuda) for name, n, _ in SHAPES}
 
-    def launch(c, name, n, k):
-        buf, rb = weights[c][name]
-        kernels.gemv_prepped(qtype, buf, rb, xs[k], sums[k], None, None, ys[name], n, k)
+    def launch(c, name, n, k, stream=None):
+        kernels.gemv_prepped(qtype, rot.layers[c][name], rot.row_bytes(n, k), xs[k], sums[k], None, None,
+                             ys[name], n, k, 0, stream=stream)
 
-    def step(c):
+    return rot, launch
+
+
+def time_kernel(torch, fn, count):
+    """Average duration of fn(i) over `count` launches, HIP events on the
+    current stream (the stream the launchers use)."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(count):
+        fn(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / count
+
+
+def bench_gemv(qtype, steps, warmup, torch, cuda):
+    rot, launch = gemv_setup(qtype, torch, cuda)
+    copies = rot.copies
+
+    def step(c, stream=None):
         for name, n, k in SHAPES:
-            launch(c, name, n, k)
+            launch(c, name, n, k, stream)
 
-    # Warm up eagerly, then capture `copies` steps into one graph.
     for i in range(warmup):
         step(i % copies)
     torch.cuda.synchronize()
@@ -90,7 +135,7 @@ def bench_gemv(qtype, steps, warmup, torch, cuda):
     with torch.cuda.stream(stream):
         with torch.cuda.graph(graph, stream=stream):
             for c in range(copies):
-                step(c)
+                step(c, stream)
     torch.cuda.synchronize()
     graph.replay()
     torch.cuda.synchronize()
@@ -101,30 +146,60 @@ def bench_gemv(qtype, steps, warmup, torch, cuda):
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     timed_steps = replays * copies
-    step_bytes = sum(gemv_bytes(n, k, host[(n, k)].shape[1]) for _, n, k in SHAPES)
-    gbps = step_bytes * timed_steps / elapsed / 1e9
+    gbps = rot.step_bytes * timed_steps / elapsed / 1e9
 
-    # Per-launch kernel durations (HIP events on the launch stream).
-    durations = {name: [] for name, _, _ in SHAPES}
-    events = []
-    for i in range(timed_steps):
-        c = i % copies
-        for name, n, k in SHAPES:
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            launch(c, name, n, k)
-            e1.record()
-            events.append((name, e0, e1))
-    torch.cuda.synchronize()
-    for name, e0, e1 in events:
-        durations[name].append(e0.elapsed_time(e1) * 1e-3)
     kernels_out = {}
     for name, n, k in SHAPES:
-        d = float(np.mean(durations[name]))
-        b = gemv_bytes(n, k, host[(n, k)].shape[1])
-        kernels_out[name] = {"n": n, "k": k, "bytes": b, "avg_us": d * 1e6, "gbps": b / d / 1e9}
+        reps = copies * 8
+        d = time_kernel(torch, lambda i: launch(i % copies, name, n, k), reps)
+        b = gemv_bytes(n, k, rot.row_bytes(n, k))
+        kernels_out[name] = {"n": n, "k": k, "bytes": b, "avg_us": d * 1e6, "gbps": b / d / 1e9, "launches": reps}
+    del graph, rot
+    torch.cuda.empty_cache()
     return {"gbps": gbps, "ms_per_step": elapsed / timed_steps * 1e3, "steps": timed_steps,
-            "copies": copies, "step_bytes": step_bytes, "kernels": kernels_out}
+            "copies": copies, "kernels": kernels_out}
+
+
+def bench_copy(torch, cuda, nbytes):
+    """A plain device copy of nbytes (read + write), rotated past the MALL:
+    the reference point for the HBM counters and for what a trivial
+    streaming kernel reaches at this size."""
+    n = nbytes // 4
+    bufs = [torch.empty(n, dtype=torch.float32, device=cuda) for _ in range(12)]
+    dst = torch.empty(n, dtype=torch.float32, device=cuda)
+    for b in bufs:
+        b.fill_(1.0)
+    d = time_kernel(torch, lambda i: dst.copy_(bufs[i % 12]), 96)
+    return {"bytes_read": n * 4, "bytes_written": n * 4, "avg_us": d * 1e6, "gbps_read_plus_write": 2 * n * 4 / d / 1e9}
+
+
+def bench_prefill_gemm(torch, cuda):
+    from myllm_amd import synth
+    from myllm_amd.hipllm import kernels
+    K, N = 3584, 18944
+    src = synth.random_quantized(N, K, synth.Q4_K, seed=N * 7 + K)
+    copies = 8
+    ws = []
+    for _ in range(copies):
+        w = torch.empty(src.nbytes + 256, dtype=torch.uint8, device=cuda)
+        w[: src.nbytes].copy_(torch.from_numpy(src.reshape(-1)))
+        ws.append(w)
+    out = {}
+    for M in (64, 512, 2048):
+        xb = torch.randn(M, K, device=cuda).to(torch.bfloat16)
+        y = torch.empty(M, N, device=cuda)
+        fn = lambda i: kernels.gemm_mfma(synth.Q4_K, ws[i % copies], src.shape[1], xb, None, None, y, M, N, K)
+        for i in range(3):
+            fn(i)
+        d = time_kernel(torch, fn, 24)
+        flops = 2.0 * M * N * K
+        tf = flops / d / 1e12
+        wbytes = N * src.shape[1] + M * K * 2 + M * N * 4
+        out[str(M)] = {"avg_us": round(d * 1e6, 2), "tflops": round(tf, 1), "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+                       "gbps": round(wbytes / d / 1e9, 1)}
+    del ws
+    torch.cuda.empty_cache()
+    return out
 
 
 def bench_e2e(shape_name, prompt_len, decode_steps, workdir, max_sequence=0):
@@ -136,70 +211,110 @@ def bench_e2e(shape_name, prompt_len, decode_steps, workdir, max_sequence=0):
     path = synth.write_qwen2(pathlib.Path(workdir) / f"{shape_name}.gguf", shape, seed=0)
     gen_s = time.perf_counter() - t0
     prompt = synth.uniform_ids(prompt_len, shape.vocab, seed=0).tolist()
-    t0 = time.perf_counter()
-    model = HipLLM(path, max_sequence or prompt_len + decode_steps + 1)
-    load_s = time.perf_counter() - t0
     try:
-        model.reset()
-        model.prefill(prompt)  # warm-up turn
-        model.decode(1)
-        model.reset()
         t0 = time.perf_counter()
-        nxt = model.prefill(prompt)
-        prefill_s = time.perf_counter() - t0
-        dec = 0.0
-        for _ in range(decode_steps):
+        model = HipLLM(path, max_sequence or prompt_len + decode_steps + 1)
+        load_s = time.perf_counter() - t0
+        try:
+            model.reset()  # warm-up turn (first-launch costs)
+            nxt = model.prefill(prompt)
+            for _ in range(2):
+                nxt = model.decode(nxt)
+            model.reset()
             t0 = time.perf_counter()
-            nxt = model.decode(nxt)
-            dec += time.perf_counter() - t0
-        stats = model.memory_stats()
+            nxt = model.prefill(prompt)
+            prefill_s = time.perf_counter() - t0
+            dec = 0.0
+            for _ in range(decode_steps):
+                t0 = time.perf_counter()
+                nxt = model.decode(nxt)
+                dec += time.perf_counter() - t0
+            stats = model.memory_stats()
+            cfg = model.config
+        finally:
+            model.close()
     finally:
-        model.close()
         os.unlink(path)
     return {"model": shape_name, "prompt_tokens": prompt_len, "decode_steps": decode_steps,
+            "max_sequence": max_sequence or prompt_len + decode_steps + 1,
             "prefill_tok_s": prompt_len / prefill_s, "decode_tok_s": decode_steps / dec,
-            "decode_ms_per_token": dec / decode_steps * 1e3, "weight_bytes": stats["weight_bytes"],
-            "gguf_gen_s": gen_s, "load_s": load_s}
+            "decode_ms_per_token": dec / decode_steps * 1e3,
+            "weight_bytes": stats["weight_bytes"], "kv_cache_bytes": stats["kv_cache_bytes"],
+            "layers": cfg["layer_count"], "gguf_gen_s": gen_s, "load_s": load_s}
 
 
 def cpu_baseline(budget_s: float = 12.0):
-    """CPULLM's FP32 GEMV (gevmt, cpu_llm.cpp:512-526) over the same shapes,
-    one thread, on FP32 weights dequantized from the same Q4_K bytes."""
+    """CPULLM's FP32 GEMV (gevmt, cpu_llm.cpp:512-526), restated in the
+    oracle, over the same four shapes on FP32 weights dequantized from the
+    same Q4_K bytes, one thread."""
     import oracle
     from myllm_amd import synth
 
     mats = {}
-    for name, n, k in SHAPES:
+    for _, n, k in SHAPES:
         if (n, k) not in mats:
             q = synth.random_quantized(n, k, synth.Q4_K, seed=n * 7 + k)
             mats[(n, k)] = (oracle.dequant_rows(synth.Q4_K, q, k), q.shape[1])
     xs = {k: synth.normal(k, seed=k) for k in (3584, 18944)}
-    done_bytes, t0 = 0, time.perf_counter()
-    steps = 0
+    done_bytes, steps = 0, 0
+    t0 = time.perf_counter()
     while time.perf_counter() - t0 < budget_s or steps == 0:
-        for name, n, k in SHAPES:
+        for _, n, k in SHAPES:
             w, rb = mats[(n, k)]
             oracle.gevmt(w, xs[k])
             done_bytes += gemv_bytes(n, k, rb)
         steps += 1
     el = time.perf_counter() - t0
-    out = {"value": done_bytes / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-           "sample": f"{steps} step(s) of the same four GEMVs (QKV, gate, up, down at Qwen2.5-7B shapes) "
-                     f"with the oracle's CPULLM gevmt on FP32-dequantized Q4_K weights, 1 thread of "
-                     f"{os.cpu_count()} host cores, {el:.1f} s"}
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    out = {"value": round(done_bytes / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+           "sample": f"{steps} step(s) of the same four GEMVs (QKV, gate, up, down at Qwen2.5-7B shapes), "
+                     f"the oracle's restatement of CPULLM gevmt on FP32 weights dequantized from the same Q4_K "
+                     f"bytes, 1 thread of {os.cpu_count()} host cores ({cpu_model}), {el:.1f} s",
+           "host_cores": os.cpu_count(), "cpu_model": cpu_model}
     if oracle.REF_BIN.exists():
-        # The reference's own CPULLM on the 0.5B-shaped model: 4-token prompt,
-        # 8 greedy tokens (7 decode steps).
-        with tempfile.TemporaryDirectory(dir="/dev/shm" if os.path.isdir("/dev/shm") else None) as tmp:
-            path = synth.write_qwen2(pathlib.Path(tmp) / "c0.gguf", synth.SHAPES["qwen2.5-0.5b"], seed=0)
-            prompt = synth.uniform_ids(4, synth.SHAPES["qwen2.5-0.5b"].vocab, seed=0)
-            r = oracle.run_reference(path, prompt, 8, max_sequence=64, timeout=600)
-        out["reference_cpullm_qwen05b"] = {
-            "decode_tok_s": r["decode_steps"] / (r["decode_ms"] / 1e3),
-            "prefill_tok_s": r["prompt_tokens"] / (r["prefill_ms"] / 1e3),
-            "sample": "reference CPULLM (oracle/_ref) on the Qwen2.5-0.5B-shaped Q4_K_M model, "
-                      "4-token prompt, 7 decode steps, 1 thread"}
+        with tempfile.TemporaryDirectory(dir=scratch_dir()) as tmp:
+            shape = synth.SHAPES["qwen2.5-0.5b"]
+            path = synth.write_qwen2(pathlib.Path(tmp) / "c0.gguf", shape, seed=0)
+            prompt = synth.uniform_ids(4, shape.vocab, seed=0)
+            r = oracle.run_reference(path, prompt, 8, max_sequence=64, timeout=900)
+        out["reference_cpullm_qwen2.5-0.5b"] = {
+            "decode_tok_s": round(r["decode_steps"] / (r["decode_ms"] / 1e3), 4),
+            "prefill_tok_s": round(r["prompt_tokens"] / (r["prefill_ms"] / 1e3), 4),
+            "sample": "the reference's own CPULLM (oracle/_ref, built from its sources) on the Qwen2.5-0.5B-shaped "
+                      "Q4_K_M model: 4-token prompt, 7 decode steps, 1 thread"}
     return out
+
+
+def read_traffic():
+    """Per-launch HBM bytes of the gate GEMV from the committed rocprofv3
+    summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), or None."""
+    if not TRAFFIC_SUMMARY.exists():
+        return None
+    for line in TRAFFIC_SUMMARY.read_text().splitlines():
+        if line.startswith("hbm_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def profile_kernel(name, reps, torch, cuda):
+    """Runs one GEMV shape `reps` times plus a plain copy of the same byte
+    count, for rocprofv3 counter collection (--pmc FETCH_SIZE / WRITE_SIZE)."""
+    from myllm_amd import synth
+    rot, launch = gemv_setup(synth.Q4_K, torch, cuda)
+    _, n, k = next(s for s in SHAPES if s[0] == name)
+    for i in range(reps):
+        launch(i % rot.copies, name, n, k)
+    torch.cuda.synchronize()
+    copy = bench_copy(torch, cuda, gemv_bytes(n, k, rot.row_bytes(n, k)) // 256 * 256)
+    print(json.dumps({"profiled": name, "launches": reps, "bytes_per_launch": gemv_bytes(n, k, rot.row_bytes(n, k)),
+                      "copy": copy}), flush=True)
 
 
 def main():
@@ -209,11 +324,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-7b", action="store_true")
+    ap.add_argument("--no-14b", action="store_true")
+    ap.add_argument("--profile-kernel", choices=[s[0] for s in SHAPES])
+    ap.add_argument("--profile-reps", type=int, default=200)
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this benchmark runs on exactly one GPU; the multi-GPU layout is "
-                                   "described in DESIGN.md and not built", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this benchmark runs on exactly one GPU: the backend is single-GPU and its "
+                                   "multi-GPU layout is a design, not built", "n_gpus": args.gpus}))
         sys.exit(2)
 
     import torch
@@ -222,6 +339,10 @@ def main():
     cuda = torch.device("cuda:0")
     from myllm_amd import synth
 
+    if args.profile_kernel:
+        profile_kernel(args.profile_kernel, args.profile_reps, torch, cuda)
+        return
+
     log("[bench] Q4_K GEMV")
     q4 = bench_gemv(synth.Q4_K, args.steps, args.warmup, torch, cuda)
     log(f"[bench] Q4_K {q4['gbps']:.1f} GB/s; kernels " +
@@ -229,17 +350,22 @@ def main():
     log("[bench] Q6_K GEMV")
     q6 = bench_gemv(synth.Q6_K, args.steps, args.warmup, torch, cuda)
     log(f"[bench] Q6_K {q6['gbps']:.1f} GB/s")
+    copy = bench_copy(torch, cuda, q4["kernels"]["gate"]["bytes"] // 256 * 256)
+    log(f"[bench] plain copy of the gate GEMV's bytes: {copy['avg_us']:.2f} us")
+    log("[bench] prefill GEMM")
+    gemm = bench_prefill_gemm(torch, cuda)
+    log(f"[bench] prefill GEMM {gemm}")
 
     e2e = {}
     if not args.no_e2e:
-        with tempfile.TemporaryDirectory(dir="/dev/shm" if os.path.isdir("/dev/shm") else None) as tmp:
-            log("[bench] e2e qwen2.5-0.5b")
-            e2e["qwen2.5-0.5b"] = bench_e2e("qwen2.5-0.5b", 16, 32, tmp)
-            log(f"[bench] {e2e['qwen2.5-0.5b']}")
-            if not args.no_7b:
-                log("[bench] e2e qwen2.5-7b")
-                e2e["qwen2.5-7b"] = bench_e2e("qwen2.5-7b", 16, 32, tmp)
-                log(f"[bench] {e2e['qwen2.5-7b']}")
+        with tempfile.TemporaryDirectory(dir=scratch_dir()) as tmp:
+            runs = [("qwen2.5-0.5b", 16, 32, 0), ("qwen2.5-7b", 128, 64, 0)]
+            if not args.no_14b:
+                runs.append(("qwen2.5-14b", 128, 128, 4096))
+            for name, p, d, cap in runs:
+                log(f"[bench] e2e {name}")
+                e2e[name] = bench_e2e(name, p, d, tmp, cap)
+                log(f"[bench] {e2e[name]}")
 
     cpu = None
     if not args.no_cpu:
@@ -248,6 +374,7 @@ def main():
         log(f"[bench] CPU {cpu}")
 
     dom = q4["kernels"]["gate"]
+    traffic = read_traffic()
     out = {
         "metric": METRIC,
         "value": round(q4["gbps"], 2),
@@ -263,18 +390,20 @@ def main():
         "data": "synthetic",
         "config": {"workload": "Q4_K decode GEMV at Qwen2.5-7B shapes, batch 1: one step = fused QKV "
                                "3584->4608 + gate 3584->18944 + up 3584->18944 + down 18944->3584",
-                   "weights": "Q4_K (GGML layout, N(0,0.02))", "activations": "f32 N(0,1)",
-                   "weight_copies_rotated": q4["copies"], "step_bytes": q4["step_bytes"]},
+                   "weights": "Q4_K (GGML block layout, N(0,0.02) quantized)", "activations": "f32 N(0,1)",
+                   "weight_copies_rotated": q4["copies"]},
         "roofline": {"bound": "hbm", "achieved": round(dom["gbps"], 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": round(dom["gbps"] / PEAK_HBM_GBPS, 4), "traffic": None,
-                     "kernel": "gemv_kernel<Q4_K> 3584->18944", "bytes_per_launch": dom["bytes"],
-                     "avg_launch_us": round(dom["avg_us"], 3)},
+                     "frac": round(dom["gbps"] / PEAK_HBM_GBPS, 4), "traffic": traffic,
+                     "kernel": "gemv Q4_K 3584->18944 (gate)", "bytes_per_launch": dom["bytes"],
+                     "avg_launch_us": round(dom["avg_us"], 3), "launches_timed": dom["launches"],
+                     "plain_copy_same_bytes_us": round(copy["avg_us"], 3)},
         "gemv": {"q4_k": {"step_gbps": round(q4["gbps"], 2),
                           "kernels": {k: {"gbps": round(v["gbps"], 1), "avg_us": round(v["avg_us"], 2)}
                                       for k, v in q4["kernels"].items()}},
                  "q6_k": {"step_gbps": round(q6["gbps"], 2),
                           "kernels": {k: {"gbps": round(v["gbps"], 1), "avg_us": round(v["avg_us"], 2)}
                                       for k, v in q6["kernels"].items()}}},
+        "prefill_gemm": {"weights": "Q4_K", "k": 3584, "n": 18944, "by_m": gemm},
         "e2e": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                 for k, v in e2e.items()},
         "cpu_baseline": cpu,
