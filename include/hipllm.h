@@ -142,6 +142,84 @@ int hipllm_argmax(const float* x, size_t n, uint32_t* out, void* scratch, void* 
  * Replaces metal_swiglu_f32 (metal_llm.metal:895-911). */
 int hipllm_swiglu(const float* g, const float* u, float* y, float* y16, size_t n, void* stream);
 
+/* Causal prefill attention: query row r (position pos0 + r, heads at
+ * q + r * q_stride) over cache positions [0, pos0 + r]. Replaces
+ * metal_kv_cache_qk_f32 + softmax + av (metal_llm.metal:826-890, 995-1061)
+ * and CPULLM's prefill head loop (cpu_llm.cpp:609-629, 316-329). */
+int hipllm_attn_prefill(const float* q, size_t q_stride, const float* kcache, const float* vcache, float* out,
+                        size_t out_stride, size_t rows, size_t hq, size_t hkv, size_t d, size_t pos0, float scale,
+                        void* stream);
+
+/* ----------------------------------------------------------- qwen35moe ops */
+
+/* A batch of `vectors` GEMVs in one launch. Vector j: y[j * ldy, n) =
+ * W_j x_j (+ bias) (+ residual[j]); with wu != NULL, y = silu(Wg_j x_j) *
+ * (Wu_j x_j) and ys16 (nullable) gets per-16 sums. With ids, W_j is expert
+ * ids[j] (byte offset ids[j] * expert_stride, ids clamped to experts - 1) and
+ * x_j is row j (x_routed) or row j / routes of x (ld ldx, xs16 ld ldx / 16);
+ * without ids every vector uses W and row j of x.
+ * Replaces metal_expert_gemm_{q4_k,q6_k}_f32 (metal_llm.metal:1476-1521;
+ * moe_llm.mm:2692-2760) and the per-row product of encode_product. */
+int hipllm_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row_bytes, const float* x,
+                        const float* xs16, const float* bias, const float* residual, float* y, float* ys16, size_t n,
+                        size_t k, size_t vectors, const int32_t* ids, size_t experts, size_t routes,
+                        size_t expert_stride, int x_routed, size_t ldx, size_t ldy, void* stream);
+
+/* Per token: softmax over `experts` logits, top-k insertion (strict '>', the
+ * lower id wins ties), renormalised weights. Replaces the router tail of
+ * encode_routes (moe_llm.mm:2642-2690): metal_softmax_f32, metal_topk_f32,
+ * metal_topk_renorm_f32 (metal_llm.metal:826-890, 1424-1474). */
+int hipllm_router_topk(const float* logits, size_t ld, size_t tokens, size_t experts, size_t k, int32_t* ids,
+                       float* weights, void* stream);
+
+/* out = residual + (sum_r w[t, r] down[t k + r] + sigmoid(sgate[t ld]) shared[t]).
+ * Replaces metal_expert_weighted_reduce_f32 + shared-expert gate + residuals
+ * (metal_llm.metal:1525-1542, 1265-1276; moe_llm.mm:2790-2885). */
+int hipllm_moe_combine(const float* residual, const float* down, const float* w, const float* shared,
+                       const float* sgate, size_t ld_sgate, float* out, size_t tokens, size_t h, size_t k,
+                       void* stream);
+
+/* decay = exp(softplus(alpha + dt_bias) a), beta = sigmoid(beta_raw).
+ * Replaces the DeltaNet gate chain of encode_delta_net (moe_llm.mm:2462-2496;
+ * metal_llm.metal:1186-1263). */
+int hipllm_gdn_gates(const float* alpha, const float* beta_raw, size_t ld, const float* dt_bias, const float* a,
+                     float* decay, float* beta, size_t tokens, size_t heads, void* stream);
+
+/* Causal depthwise conv over [history; x] + SiLU, then history <- last k - 1
+ * rows. Replaces metal_depthwise_conv1d_causal_f32, metal_conv_history_commit_f32
+ * and the SiLU after them (metal_llm.metal:1320-1365, 1199-1211). */
+int hipllm_conv1d_silu(const float* x, size_t ldx, float* history, const float* w, float* out, size_t ldo,
+                       size_t tokens, size_t channels, size_t ksize, void* stream);
+
+/* In place x <- x rsqrt(sum(x^2) + eps) per head vector. Replaces
+ * metal_l2norm_heads_f32 (metal_llm.metal:1280-1316). */
+int hipllm_l2norm_heads(float* x, size_t ld, size_t tokens, size_t heads, size_t d, float eps, void* stream);
+
+/* Gated DeltaNet scan over `tokens` rows: per value head h (key head h % key
+ * heads), S *= decay; delta = beta (v - S^T k); S += k delta^T;
+ * o = S^T q / sqrt(d). State [value_heads, d, d] in place; d = 64 or 128.
+ * Replaces metal_gdn_recurrence_f32 (metal_llm.metal:1370-1420). */
+int hipllm_gdn_scan(const float* q, const float* k, size_t ldqk, const float* v, size_t ldv, const float* decay,
+                    const float* beta, float* state, float* out, size_t ldo, size_t tokens, size_t value_heads,
+                    size_t key_heads, size_t d, void* stream);
+
+/* y = rmsnorm(o_head) gamma silu(z) per head; ys16 nullable. Replaces the
+ * state norm + SiLU(z) gate of encode_delta_net (moe_llm.mm:2614-2634). */
+int hipllm_gated_rmsnorm(const float* o, size_t ldo, const float* gamma, const float* z, size_t ldz, float* y,
+                         float* ys16, size_t ldy, size_t tokens, size_t heads, size_t d, float eps, void* stream);
+
+/* Split the per-head interleaved [Q_h | gate_h] projection, RMSNorm Q and K
+ * heads with their gammas, and lay out [Q | K | V] rows for RoPE + cache.
+ * Replaces metal_split_interleaved_q_gate_f32 and the Q/K norms of
+ * encode_full_attention (metal_llm.metal:1167-1184; moe_llm.mm:2258-2310). */
+int hipllm_split_qgate_norm(const float* mixed, size_t ldm, const float* kv, size_t ldkv, const float* q_gamma,
+                            const float* k_gamma, float* qkv, size_t ldqkv, float* gate, size_t ldg, size_t tokens,
+                            size_t hq, size_t hkv, size_t d, float eps, void* stream);
+
+/* y = a sigmoid(g) (y16 nullable per-16 sums). Replaces the attention output
+ * gate of encode_full_attention (moe_llm.mm:2420-2428). */
+int hipllm_gate_mul(const float* a, const float* g, float* y, float* y16, size_t n, void* stream);
+
 /* ------------------------------------------------------------ handle API */
 
 typedef struct HipllmModel HipllmModel;
@@ -162,6 +240,17 @@ typedef struct HipllmConfig {
     float rope_theta;
     float norm_epsilon;
     char architecture[32];
+    /* qwen35moe (zero for qwen2), metal_model.h:37-72 */
+    uint64_t full_attention_interval;
+    uint64_t expert_count;
+    uint64_t expert_used_count;
+    uint64_t expert_feed_forward_size;
+    uint64_t shared_expert_feed_forward_size;
+    uint64_t ssm_conv_kernel;
+    uint64_t ssm_state_size;
+    uint64_t ssm_group_count;
+    uint64_t ssm_time_step_rank;
+    uint64_t ssm_inner_size;
 } HipllmConfig;
 
 typedef struct HipllmMemoryStats {
@@ -178,9 +267,14 @@ typedef struct HipllmMemoryStats {
  * CLI's architecture probe (chat.cpp:1021-1024). */
 int hipllm_inspect_gguf(const char* gguf_path, HipllmConfig* out);
 
-/* MetalLLM(gguf_path, max_sequence) (metal_llm.h:22-24); device < 0 keeps
- * the current HIP device. */
+/* Builds the backend the CLI's --gpu selection picks for the file
+ * (chat.cpp:1019-1035): qwen35moe -> HipMoeLLM (MoeLLM, moe_llm.h:80-115),
+ * otherwise HipLLM (MetalLLM(gguf_path, max_sequence), metal_llm.h:22-24).
+ * device < 0 keeps the current HIP device; expert_cache_count is validated
+ * like MoeLLM's (top-k <= n <= experts) and all experts stay resident. */
 int hipllm_create(const char* gguf_path, size_t max_sequence, int device, HipllmModel** out);
+int hipllm_create_ex(const char* gguf_path, size_t max_sequence, int device, size_t expert_cache_count,
+                     HipllmModel** out);
 void hipllm_destroy(HipllmModel* model);
 int hipllm_reset(HipllmModel* model);
 int hipllm_prefill(HipllmModel* model, const int32_t* ids, size_t count, int32_t* next_token);
@@ -195,9 +289,15 @@ int hipllm_enable_profiling(HipllmModel* model, const char* csv_path);
 int hipllm_disable_profiling(HipllmModel* model);
 /* Logits of the last prefill/decode (vocabulary_size floats, host memory). */
 int hipllm_copy_logits(const HipllmModel* model, float* out, size_t count);
-/* 1 = batched prefill kernels, 0 = token-serial prefill through the decode
- * path (both produce the same next token within FP32 tolerance). */
+/* qwen2 only: 1 = batched (bf16 MFMA) prefill, 0 = token-serial prefill
+ * through the FP32 decode kernels. */
 int hipllm_set_batched_prefill(HipllmModel* model, int enabled);
+/* qwen35moe only: expert ids chosen for the last row of the last forward,
+ * [layer_count, expert_used_count] (MoeLLM keeps them in RouteIds,
+ * moe_llm.mm:2919-2925). */
+int hipllm_copy_routes(const HipllmModel* model, int32_t* out, size_t count);
+/* MoeLLM::expert_cache_count (moe_llm.h:104); 0 for qwen2 models. */
+size_t hipllm_expert_cache_count(const HipllmModel* model);
 
 #ifdef __cplusplus
 }

@@ -37,6 +37,48 @@ typedef struct HipllmQwen2Spec {
     uint32_t threads;
 } HipllmQwen2Spec;
 
+/* Synthetic qwen35moe model (moe_model.cpp:151-234 schema): full-attention
+ * layers where (i + 1) % full_attention_interval == 0, Gated DeltaNet layers
+ * otherwise, routed + shared experts in every layer. */
+typedef struct HipllmQwen35MoeSpec {
+    uint32_t layers;
+    uint32_t hidden;
+    uint32_t heads;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t rotary_dim;
+    uint32_t vocab;
+    uint32_t context;
+    uint32_t eos_token_id;
+    float rope_theta;
+    float norm_eps;
+    uint32_t experts;
+    uint32_t experts_used;
+    uint32_t expert_ffn;
+    uint32_t shared_ffn;
+    uint32_t full_attention_interval;
+    uint32_t conv_kernel;
+    uint32_t state_size;
+    uint32_t group_count;
+    uint32_t time_step_rank;
+    uint32_t type_embd;
+    uint32_t type_output;
+    uint32_t type_attn_qgate;
+    uint32_t type_attn_kv;
+    uint32_t type_attn_out;
+    uint32_t type_ssm_qkv;
+    uint32_t type_ssm_gate;
+    uint32_t type_ssm_out;
+    uint32_t type_expert_gate_up;
+    uint32_t type_expert_down;
+    uint32_t type_shared;
+    uint64_t seed;
+    float stddev;
+    float small_stddev;
+    float conv_stddev;
+    uint32_t threads;
+} HipllmQwen35MoeSpec;
+
 /* Bytes of one row of `cols` elements of GGML type `type`; 0 if unsupported
  * or not block aligned. */
 size_t hipllm_tools_row_bytes(uint32_t type, size_t cols);
@@ -59,6 +101,10 @@ void hipllm_tools_fill_uniform_int(uint64_t seed, uint64_t stream,
  * err (NUL terminated, at most errlen bytes) and returns -1. */
 int hipllm_tools_write_qwen2(const char* path, const HipllmQwen2Spec* spec,
                              char* err, size_t errlen);
+
+/* Writes a qwen35moe GGUF file; same error convention as the qwen2 writer. */
+int hipllm_tools_write_qwen35moe(const char* path, const HipllmQwen35MoeSpec* spec,
+                                 char* err, size_t errlen);
 
 #ifdef __cplusplus
 }

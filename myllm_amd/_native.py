@@ -53,6 +53,9 @@ def tools() -> ctypes.CDLL:
         lib.hipllm_tools_write_qwen2.restype = c.c_int
         lib.hipllm_tools_write_qwen2.argtypes = [
             c.c_char_p, c.c_void_p, c.c_char_p, c.c_size_t]
+        lib.hipllm_tools_write_qwen35moe.restype = c.c_int
+        lib.hipllm_tools_write_qwen35moe.argtypes = [
+            c.c_char_p, c.c_void_p, c.c_char_p, c.c_size_t]
         lib._hipllm_typed = True
     return lib
 

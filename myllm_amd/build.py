@@ -40,8 +40,10 @@ HIP_SOURCES = [
     "kernels/gemv.hip",
     "kernels/ops.hip",
     "kernels/prefill.hip",
+    "kernels/moe.hip",
     "runtime/gguf_reader.cpp",
     "runtime/hip_llm.cpp",
+    "runtime/hip_moe.cpp",
     "runtime/capi.cpp",
 ]
 TOOLS_SOURCES = ["tools/quants.cpp", "tools/synth_gguf.cpp", "tools/tools_capi.cpp"]

@@ -394,6 +394,22 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return g * sig * u;
 }
 
+// Several GEMVs in one launch: blockIdx.y is an output row-vector index j.
+// With ids (expert routing, moe_llm.mm:2692-2760; metal_expert_gemm_q*_f32
+// metal_llm.metal:1476-1521) the weights of vector j are those of expert
+// ids[j] (clamped to experts - 1), at byte offset ids[j] * expert_stride; the
+// input is row j (x_routed) or row j / routes of x. Without ids every vector
+// uses the same weights (a batch of rows through one matrix).
+struct Batch {
+    const int32_t* ids = nullptr;
+    uint32_t experts = 1;
+    uint32_t routes = 1;
+    size_t expert_stride = 0;
+    uint32_t x_routed = 0;
+    uint32_t ldx = 0;  // floats between input rows (multiple of 16)
+    uint32_t ldy = 0;  // floats between output rows
+};
+
 // R rows per octet, OPR octets per row group (K split), 8 / OPR row groups
 // per wave, 4 waves per block: rows per block = 32 R / OPR.
 // MODE 0: y = W x (+ bias) (+ residual).
@@ -404,8 +420,24 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w
                                                    size_t row_bytes, const float* __restrict__ x,
                                                    const float* __restrict__ xs16, const float* __restrict__ bias,
                                                    const float* __restrict__ residual, float* __restrict__ y,
-                                                   float* __restrict__ ys16, uint32_t n, uint32_t units) {
+                                                   float* __restrict__ ys16, uint32_t n, uint32_t units,
+                                                   const Batch batch) {
     using U = Unit<T>;
+    {
+        // Vector j of the batch: shift weights, input, output and residual.
+        const uint32_t j = blockIdx.y;
+        const uint32_t xrow = batch.x_routed ? j : j / batch.routes;
+        if (batch.ids) {
+            const uint32_t e = min(static_cast<uint32_t>(batch.ids[j]), batch.experts - 1);
+            w += static_cast<size_t>(e) * batch.expert_stride;
+            if (MODE == 1) w2 += static_cast<size_t>(e) * batch.expert_stride;
+        }
+        x += static_cast<size_t>(xrow) * batch.ldx;
+        xs16 += static_cast<size_t>(xrow) * (batch.ldx / 16);
+        y += static_cast<size_t>(j) * batch.ldy;
+        if (residual) residual += static_cast<size_t>(j) * batch.ldy;
+        if (ys16) ys16 += static_cast<size_t>(j) * (batch.ldy / 16);
+    }
     constexpr int GPW = 8 / OPR;
     constexpr int RPB = 4 * GPW * R;
     constexpr int NR = MODE == 1 ? 2 * R : R;
@@ -752,17 +784,17 @@ constexpr int kTilings[] = {11, 12, 14, 18, 21, 22, 24, 28, 41, 42, 44, 48};
 template <uint32_t T, int MODE>
 int launch_typed(int tiling, const void* w, const void* w2, size_t row_bytes, const float* x, const float* xs16,
                  const float* bias, const float* residual, float* y, float* ys16, uint32_t n, uint32_t units,
-                 hipStream_t stream) {
+                 hipStream_t stream, const Batch& batch = Batch(), uint32_t vectors = 1) {
     const auto* wp = static_cast<const uint8_t*>(w);
     const auto* wp2 = static_cast<const uint8_t*>(w2);
     const int R = tiling / 10, OPR = tiling % 10;
     const uint32_t rpb = 32u * R / OPR;
-    const dim3 grid((n + rpb - 1) / rpb);
+    const dim3 grid((n + rpb - 1) / rpb, vectors);
     switch (tiling) {
 #define HIPLLM_GEMV_CASE(RR, OO)                                                                           \
     case 10 * RR + OO:                                                                                     \
         hipLaunchKernelGGL((gemv_kernel<T, RR, OO, MODE>), grid, dim3(256), 0, stream, wp, wp2, row_bytes, \
-                           x, xs16, bias, residual, y, ys16, n, units);                                    \
+                           x, xs16, bias, residual, y, ys16, n, units, batch);                             \
         break;
         HIPLLM_GEMV_CASE(1, 1)
         HIPLLM_GEMV_CASE(1, 2)
@@ -974,6 +1006,72 @@ int launch_gemv_swiglu(uint32_t type, const void* wg, const void* wu, size_t row
     case kQ5_0: return launch_typed<kQ5_0, 1>(t, wg, wu, row_bytes, x, xs16, nullptr, nullptr, y, ys16, nn, units, stream);
     case kF32: return launch_typed<kF32, 1>(t, wg, wu, row_bytes, x, xs16, nullptr, nullptr, y, ys16, nn, units, stream);
     case kF16: return launch_typed<kF16, 1>(t, wg, wu, row_bytes, x, xs16, nullptr, nullptr, y, ys16, nn, units, stream);
+    default: return kInvalidArgument;
+    }
+}
+
+}  // namespace hipllm
+
+namespace hipllm {
+
+// A batch of GEMVs through one matrix or through routed experts (see Batch):
+// vector j computes y[j, :n] = W_j x_j (+ bias) (+ residual[j]) or, with
+// wu != nullptr, y[j] = silu(Wg_j x_j) * (Wu_j x_j) with optional ys16[j].
+int launch_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row_bytes, const float* x,
+                        const float* xs16, const float* bias, const float* residual, float* y, float* ys16, size_t n,
+                        size_t k, size_t vectors, const int32_t* ids, size_t experts, size_t routes,
+                        size_t expert_stride, int x_routed, size_t ldx, size_t ldy, hipStream_t stream) {
+    const uint32_t ue = unit_elems(type);
+    if (!w || !x || !xs16 || !y || n == 0 || k == 0 || ue == 0 || k % ue != 0 || vectors == 0) {
+        return kInvalidArgument;
+    }
+    if (row_bytes < k / block_elems(type) * block_bytes(type)) return kInvalidArgument;
+    const bool need16 = type == kQ4_K || type == kF32 || type == kF16;
+    const uintptr_t wa = reinterpret_cast<uintptr_t>(w), ua = reinterpret_cast<uintptr_t>(wu);
+    if (need16 && (row_bytes % 16 != 0 || wa % 16 != 0 || (wu && ua % 16 != 0) || expert_stride % 16 != 0)) {
+        return kInvalidArgument;
+    }
+    if (wa % 2 != 0 || (wu && ua % 2 != 0) || row_bytes % 2 != 0 || expert_stride % 2 != 0) return kInvalidArgument;
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || ldx < k || ldx % 16 != 0 || ldy < n) return kInvalidArgument;
+    if (ids && (experts == 0 || routes == 0 || expert_stride < n * row_bytes)) return kInvalidArgument;
+    if (!ids && (routes == 0)) return kInvalidArgument;
+    if (ys16 && (n % 16 != 0 || ldy % 16 != 0)) return kInvalidArgument;
+    if (n > 0x7fffffffu || k > 0x7fffffffu || vectors > 65535 || ldx > 0xffffffffu || ldy > 0xffffffffu ||
+        experts > 0xffffffffu || routes > 0xffffffffu) {
+        return kLengthError;
+    }
+    Batch b;
+    b.ids = ids;
+    b.experts = ids ? static_cast<uint32_t>(experts) : 1u;
+    b.routes = static_cast<uint32_t>(routes);
+    b.expert_stride = ids ? expert_stride : 0;
+    b.x_routed = x_routed ? 1u : 0u;
+    b.ldx = static_cast<uint32_t>(ldx);
+    b.ldy = static_cast<uint32_t>(ldy);
+    const uint32_t units = static_cast<uint32_t>(k / ue);
+    const uint32_t nn = static_cast<uint32_t>(n);
+    const uint32_t nv = static_cast<uint32_t>(vectors);
+    if (!wu) {
+        int t = gemv_default_tiling(nn, units, 0);
+        switch (type) {
+        case kQ4_K: return launch_typed<kQ4_K, 0>(t, w, nullptr, row_bytes, x, xs16, bias, residual, y, nullptr, nn, units, stream, b, nv);
+        case kQ6_K: return launch_typed<kQ6_K, 0>(t, w, nullptr, row_bytes, x, xs16, bias, residual, y, nullptr, nn, units, stream, b, nv);
+        case kQ8_0: return launch_typed<kQ8_0, 0>(t, w, nullptr, row_bytes, x, xs16, bias, residual, y, nullptr, nn, units, stream, b, nv);
+        case kQ5_0: return launch_typed<kQ5_0, 0>(t, w, nullptr, row_bytes, x, xs16, bias, residual, y, nullptr, nn, units, stream, b, nv);
+        case kF32: return launch_typed<kF32, 0>(t, w, nullptr, row_bytes, x, xs16, bias, residual, y, nullptr, nn, units, stream, b, nv);
+        case kF16: return launch_typed<kF16, 0>(t, w, nullptr, row_bytes, x, xs16, bias, residual, y, nullptr, nn, units, stream, b, nv);
+        default: return kInvalidArgument;
+        }
+    }
+    if (bias || residual) return kInvalidArgument;
+    const int t = gemv_default_tiling(nn, units, 1);
+    switch (type) {
+    case kQ4_K: return launch_typed<kQ4_K, 1>(t, w, wu, row_bytes, x, xs16, nullptr, nullptr, y, ys16, nn, units, stream, b, nv);
+    case kQ6_K: return launch_typed<kQ6_K, 1>(t, w, wu, row_bytes, x, xs16, nullptr, nullptr, y, ys16, nn, units, stream, b, nv);
+    case kQ8_0: return launch_typed<kQ8_0, 1>(t, w, wu, row_bytes, x, xs16, nullptr, nullptr, y, ys16, nn, units, stream, b, nv);
+    case kQ5_0: return launch_typed<kQ5_0, 1>(t, w, wu, row_bytes, x, xs16, nullptr, nullptr, y, ys16, nn, units, stream, b, nv);
+    case kF32: return launch_typed<kF32, 1>(t, w, wu, row_bytes, x, xs16, nullptr, nullptr, y, ys16, nn, units, stream, b, nv);
+    case kF16: return launch_typed<kF16, 1>(t, w, wu, row_bytes, x, xs16, nullptr, nullptr, y, ys16, nn, units, stream, b, nv);
     default: return kInvalidArgument;
     }
 }

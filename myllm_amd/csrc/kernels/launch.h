@@ -20,6 +20,11 @@ int launch_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const fl
 int launch_gemv_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
                        const float* xs16, float* y, float* ys16, size_t n, size_t k, hipStream_t stream);
 
+int launch_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row_bytes, const float* x,
+                        const float* xs16, const float* bias, const float* residual, float* y, float* ys16, size_t n,
+                        size_t k, size_t vectors, const int32_t* ids, size_t experts, size_t routes,
+                        size_t expert_stride, int x_routed, size_t ldx, size_t ldy, hipStream_t stream);
+
 int gemm_default_tile(uint32_t m, uint32_t n);
 int launch_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, hipStream_t stream);
 int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* bias,
@@ -42,5 +47,27 @@ size_t argmax_scratch_bytes(size_t n);
 int launch_argmax(const float* x, size_t n, uint32_t* out, void* scratch, hipStream_t stream);
 int launch_swiglu(const float* g, const float* u, float* y, float* y16, size_t n, hipStream_t stream);
 int launch_add(const float* a, const float* b, float* y, size_t n, hipStream_t stream);
+
+// qwen35moe operators (moe.hip).
+int launch_router_topk(const float* logits, size_t ld, size_t tokens, size_t experts, size_t k, int32_t* ids,
+                       float* weights, hipStream_t stream);
+int launch_moe_combine(const float* residual, const float* down, const float* w, const float* shared,
+                       const float* sgate, size_t ld_sgate, float* out, size_t tokens, size_t h, size_t k,
+                       hipStream_t stream);
+int launch_gdn_gates(const float* alpha, const float* beta_raw, size_t ld, const float* dt_bias, const float* a,
+                     float* decay, float* beta, size_t tokens, size_t heads, hipStream_t stream);
+int launch_conv1d_silu(const float* x, size_t ldx, float* history, const float* w, float* out, size_t ldo,
+                       size_t tokens, size_t channels, size_t ksize, hipStream_t stream);
+int launch_l2norm_heads(float* x, size_t ld, size_t tokens, size_t heads, size_t d, float eps, hipStream_t stream);
+int launch_gdn_scan(const float* q, const float* k, size_t ldqk, const float* v, size_t ldv, const float* decay,
+                    const float* beta, float* state, float* out, size_t ldo, size_t tokens, size_t value_heads,
+                    size_t key_heads, size_t d, hipStream_t stream);
+int launch_gated_rmsnorm(const float* o, size_t ldo, const float* gamma, const float* z, size_t ldz, float* y,
+                         float* ys16, size_t ldy, size_t tokens, size_t heads, size_t d, float eps,
+                         hipStream_t stream);
+int launch_split_qgate_norm(const float* mixed, size_t ldm, const float* kv, size_t ldkv, const float* q_gamma,
+                            const float* k_gamma, float* qkv, size_t ldqkv, float* gate, size_t ldg, size_t tokens,
+                            size_t hq, size_t hkv, size_t d, float eps, hipStream_t stream);
+int launch_gate_mul(const float* a, const float* g, float* y, float* y16, size_t n, hipStream_t stream);
 
 }  // namespace hipllm

@@ -1,0 +1,461 @@
+// qwen35moe operators: router top-k, MoE combine, Gated DeltaNet (gates,
+// causal conv + SiLU + history, L2 head norm, the recurrent state scan, gated
+// RMSNorm) and the gated full-attention pieces (Q/gate split with per-head
+// RMSNorm, sigmoid output gate).
+//
+// Reference semantics (MoeLLM, moe_llm.mm:2238-2843, and its kernels):
+//   router        softmax metal_llm.metal:826-890, top-k insertion 1424-1459
+//                 (strict '>': lower expert id wins ties), renorm 1461-1474
+//   combine       weighted reduce 1525-1542, shared gate 1186-1197 +
+//                 row scale 1265-1276, residuals (moe_llm.mm:2836-2885)
+//   DeltaNet      softplus 1213-1224, exp 1226-1233, conv 1320-1341, history
+//                 1345-1365, SiLU 1199-1211, L2 norm 1280-1316, recurrence
+//                 1370-1420, per-head RMSNorm 785-823 times SiLU(z)
+//   attention     Q/gate split 1167-1184, per-head RMSNorm 785-823, sigmoid
+//                 gate + multiply (moe_llm.mm:2420-2428)
+//
+// Design for CDNA4: the DeltaNet scan keeps each value head's 128 x 128 FP32
+// state in registers for the whole prompt (one block per head and 64-column
+// tile, 256 threads, 32 state values per thread) so the state is read and
+// written once per call however many tokens it scans; norms run one 64-lane
+// wave per head vector; everything else is one pass over its rows.
+#include "common.h"
+
+namespace hipllm {
+namespace {
+
+// Sign-branched sigmoid of the reference (metal_llm.metal:1186-1197).
+__device__ __forceinline__ float sigmoid_ref(float v) {
+    return v >= 0.0f ? 1.0f / (1.0f + expf(-v)) : expf(v) / (1.0f + expf(v));
+}
+
+__device__ __forceinline__ float softplus_ref(float v) {
+    return v > 20.0f ? v : (v < -20.0f ? expf(v) : logf(1.0f + expf(v)));
+}
+
+__device__ __forceinline__ float block_max256(float v, float* red) {
+    v = warp_max(v);
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+    v = warp_sum(v);
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// ------------------------------------------------------------ router
+// One block per token: softmax over the expert logits, top-k insertion by
+// one thread (k <= 8, a single pass over the experts), renormalisation.
+constexpr uint32_t kMaxExperts = 1024;
+
+__global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, uint32_t ld,
+                                                          uint32_t experts, uint32_t k, int32_t* __restrict__ ids,
+                                                          float* __restrict__ weights) {
+    const uint32_t t = blockIdx.x;
+    const float* row = logits + static_cast<size_t>(t) * ld;
+    __shared__ float p[kMaxExperts];
+    __shared__ float red[4];
+    float m = -INFINITY;
+    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) m = fmaxf(m, row[e]);
+    m = block_max256(m, red);
+    float s = 0.0f;
+    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
+        const float v = row[e];
+        const float ex = v == -INFINITY ? 0.0f : expf(v - m);
+        p[e] = ex;
+        s += ex;
+    }
+    s = block_sum256(s, red);
+    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) p[e] = s > 0.0f ? p[e] / s : 0.0f;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float bv[8];
+        int32_t bi[8];
+        for (uint32_t r = 0; r < 8; ++r) {
+            bv[r] = -INFINITY;
+            bi[r] = 0;
+        }
+        for (uint32_t e = 0; e < experts; ++e) {
+            const float c = p[e];
+            uint32_t ins = k;
+            for (uint32_t r = 0; r < k; ++r) {
+                if (c > bv[r]) {
+                    ins = r;
+                    break;
+                }
+            }
+            if (ins < k) {
+                for (uint32_t r = k - 1; r > ins; --r) {
+                    bv[r] = bv[r - 1];
+                    bi[r] = bi[r - 1];
+                }
+                bv[ins] = c;
+                bi[ins] = static_cast<int32_t>(e);
+            }
+        }
+        float sum = 0.0f;
+        for (uint32_t r = 0; r < k; ++r) sum += bv[r];
+        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+        for (uint32_t r = 0; r < k; ++r) {
+            ids[t * k + r] = bi[r];
+            weights[t * k + r] = bv[r] * inv;
+        }
+    }
+}
+
+// ------------------------------------------------------------ MoE combine
+// out[t] = residual[t] + (sum_r w[t, r] * down[t k + r] + sigmoid(sg[t]) * shared[t])
+__global__ void moe_combine_kernel(const float* __restrict__ residual, const float* __restrict__ down,
+                                   const float* __restrict__ w, const float* __restrict__ shared,
+                                   const float* __restrict__ sgate, uint32_t ld_sgate, float* __restrict__ out,
+                                   uint32_t tokens, uint32_t h, uint32_t k) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<size_t>(tokens) * h) return;
+    const uint32_t t = static_cast<uint32_t>(i / h), c = static_cast<uint32_t>(i % h);
+    float acc = 0.0f;
+    for (uint32_t r = 0; r < k; ++r) acc += w[t * k + r] * down[(static_cast<size_t>(t) * k + r) * h + c];
+    float moe = acc;
+    if (shared) moe += shared[i] * sigmoid_ref(sgate[static_cast<size_t>(t) * ld_sgate]);
+    out[i] = residual[i] + moe;
+}
+
+// ------------------------------------------------------------ DeltaNet
+// decay = exp(softplus(alpha + dt_bias) * a), beta = sigmoid(beta_raw).
+__global__ void gdn_gates_kernel(const float* __restrict__ alpha, const float* __restrict__ beta_raw, uint32_t ld,
+                                 const float* __restrict__ dt_bias, const float* __restrict__ a,
+                                 float* __restrict__ decay, float* __restrict__ beta, uint32_t tokens,
+                                 uint32_t heads) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= tokens * heads) return;
+    const uint32_t t = i / heads, h = i % heads;
+    const float sp = softplus_ref(alpha[t * ld + h] + dt_bias[h]);
+    decay[i] = expf(sp * a[h]);
+    beta[i] = sigmoid_ref(beta_raw[t * ld + h]);
+}
+
+// Causal depthwise conv + SiLU over [history (k - 1 rows); x rows], then the
+// history keeps the last k - 1 rows. One thread owns one channel for all
+// tokens, so the history is read before it is overwritten.
+constexpr uint32_t kMaxConv = 9;
+
+__global__ void conv1d_silu_kernel(const float* __restrict__ x, uint32_t ldx, float* __restrict__ history,
+                                   const float* __restrict__ w, float* __restrict__ out, uint32_t ldo,
+                                   uint32_t tokens, uint32_t channels, uint32_t ksize) {
+    const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= channels) return;
+    const uint32_t hr = ksize - 1;
+    float win[kMaxConv];
+    float taps[kMaxConv];
+    for (uint32_t i = 0; i < ksize; ++i) taps[i] = w[static_cast<size_t>(c) * ksize + i];
+    for (uint32_t i = 0; i < hr; ++i) win[i] = history[static_cast<size_t>(i) * channels + c];
+    for (uint32_t t = 0; t < tokens; ++t) {
+        win[hr] = x[static_cast<size_t>(t) * ldx + c];
+        float acc = 0.0f;
+        for (uint32_t i = 0; i < ksize; ++i) acc += win[i] * taps[i];
+        out[static_cast<size_t>(t) * ldo + c] = acc * sigmoid_ref(acc);
+        for (uint32_t i = 0; i < hr; ++i) win[i] = win[i + 1];
+    }
+    for (uint32_t i = 0; i < hr; ++i) history[static_cast<size_t>(i) * channels + c] = win[i];
+}
+
+// x <- x * rsqrt(sum(x^2) + eps) for `heads` vectors of d values per row.
+// One wave per (row, head).
+__global__ __launch_bounds__(64) void l2norm_heads_kernel(float* __restrict__ x, uint32_t ld, uint32_t d,
+                                                         float eps) {
+    const uint32_t t = blockIdx.x, h = blockIdx.y;
+    float* v = x + static_cast<size_t>(t) * ld + static_cast<size_t>(h) * d;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < d; i += 64) ss += v[i] * v[i];
+    ss = warp_sum(ss);
+    const float inv = 1.0f / sqrtf(ss + eps);
+    for (uint32_t i = threadIdx.x; i < d; i += 64) v[i] = v[i] * inv;
+}
+
+// Gated DeltaNet scan. Block (value head h, 64-column tile): thread
+// (col = tid % 64, rg = tid / 64) holds rows [rg NPR, rg NPR + NPR) of
+// columns col of state S_h[Dk][Dv] (row = key dim). Per token, with key head
+// h % key_heads:  S *= decay; pred = S^T k; delta = beta (v - pred);
+// S += k delta^T; o = S^T q / sqrt(Dk).
+template <int NPR>
+__global__ __launch_bounds__(256) void gdn_scan_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                       uint32_t ldqk, const float* __restrict__ v, uint32_t ldv,
+                                                       const float* __restrict__ decay,
+                                                       const float* __restrict__ beta, float* __restrict__ state,
+                                                       float* __restrict__ out, uint32_t ldo, uint32_t tokens,
+                                                       uint32_t value_heads, uint32_t key_heads) {
+    constexpr uint32_t Dk = 4 * NPR;
+    const uint32_t h = blockIdx.x;
+    const uint32_t col = blockIdx.y * 64 + (threadIdx.x & 63);
+    const uint32_t rg = threadIdx.x >> 6;
+    const uint32_t kh = h % key_heads;
+    const uint32_t Dv = Dk;
+    float* S = state + static_cast<size_t>(h) * Dk * Dv;
+    float s[NPR];
+#pragma unroll
+    for (int i = 0; i < NPR; ++i) s[i] = S[static_cast<size_t>(rg * NPR + i) * Dv + col];
+    __shared__ float ks[Dk], qs[Dk];
+    __shared__ float part[4][64];
+    const float qscale = 1.0f / sqrtf(static_cast<float>(Dk));
+    const uint32_t lc = threadIdx.x & 63;
+    for (uint32_t t = 0; t < tokens; ++t) {
+        for (uint32_t i = threadIdx.x; i < Dk; i += 256) {
+            ks[i] = k[static_cast<size_t>(t) * ldqk + kh * Dk + i];
+            qs[i] = q[static_cast<size_t>(t) * ldqk + kh * Dk + i];
+        }
+        const float g = decay[t * value_heads + h];
+        const float b = beta[t * value_heads + h];
+        const float vv = v[static_cast<size_t>(t) * ldv + h * Dv + col];
+        __syncthreads();
+        float pp = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NPR; ++i) {
+            s[i] *= g;
+            pp += s[i] * ks[rg * NPR + i];
+        }
+        part[rg][lc] = pp;
+        __syncthreads();
+        const float pred = (part[0][lc] + part[1][lc]) + (part[2][lc] + part[3][lc]);
+        const float delta = b * (vv - pred);
+        float op = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NPR; ++i) {
+            s[i] += ks[rg * NPR + i] * delta;
+            op += s[i] * qs[rg * NPR + i];
+        }
+        __syncthreads();  // everyone has read part[] (pred) before it is reused
+        part[rg][lc] = op;
+        __syncthreads();
+        if (rg == 0) {
+            const float o = (part[0][lc] + part[1][lc]) + (part[2][lc] + part[3][lc]);
+            out[static_cast<size_t>(t) * ldo + h * Dv + col] = o * qscale;
+        }
+        __syncthreads();  // ks/qs/part reused by the next token
+    }
+#pragma unroll
+    for (int i = 0; i < NPR; ++i) S[static_cast<size_t>(rg * NPR + i) * Dv + col] = s[i];
+}
+
+// y = rmsnorm(o_head) * gamma * silu(z) per (row, value head); FP32 sum of
+// squares like the reference's per-head norm; ys16 (optional) per-16 sums.
+__global__ __launch_bounds__(64) void gated_rmsnorm_kernel(const float* __restrict__ o, uint32_t ldo,
+                                                          const float* __restrict__ gamma,
+                                                          const float* __restrict__ z, uint32_t ldz,
+                                                          float* __restrict__ y, float* __restrict__ ys16,
+                                                          uint32_t ldy, uint32_t d, float eps) {
+    const uint32_t t = blockIdx.x, h = blockIdx.y;
+    const float* ov = o + static_cast<size_t>(t) * ldo + static_cast<size_t>(h) * d;
+    const float* zv = z + static_cast<size_t>(t) * ldz + static_cast<size_t>(h) * d;
+    float* yv = y + static_cast<size_t>(t) * ldy + static_cast<size_t>(h) * d;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < d; i += 64) ss += ov[i] * ov[i];
+    ss = warp_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
+    for (uint32_t i = threadIdx.x; i < d; i += 64) {
+        const float zz = zv[i];
+        yv[i] = ov[i] * inv * gamma[i] * (zz * sigmoid_ref(zz));
+    }
+    if (ys16) {
+        __syncthreads();
+        const uint32_t groups = d / 16;
+        for (uint32_t g = threadIdx.x; g < groups; g += 64) {
+            float acc = 0.0f;
+            for (uint32_t i = 0; i < 16; ++i) acc += yv[16 * g + i];
+            ys16[static_cast<size_t>(t) * (ldy / 16) + static_cast<size_t>(h) * groups + g] = acc;
+        }
+    }
+}
+
+// ------------------------------------------------------------ full attention
+// Block (row t, head h), one wave. h < hq: the interleaved [Q_h | gate_h]
+// pair of `mixed` -> RMSNorm(Q_h) * q_gamma into qkv's Q part, gate_h into
+// `gate`. h >= hq: KV head j = h - hq of `kv` ([K | V] rows) ->
+// RMSNorm(K_j) * k_gamma into qkv's K part and V_j copied into its V part.
+__global__ __launch_bounds__(64) void split_qgate_norm_kernel(const float* __restrict__ mixed, uint32_t ldm,
+                                                             const float* __restrict__ kv, uint32_t ldkv,
+                                                             const float* __restrict__ q_gamma,
+                                                             const float* __restrict__ k_gamma,
+                                                             float* __restrict__ qkv, uint32_t ldqkv,
+                                                             float* __restrict__ gate, uint32_t ldg, uint32_t hq,
+                                                             uint32_t hkv, uint32_t d, float eps) {
+    const uint32_t t = blockIdx.x, h = blockIdx.y;
+    const float* src;
+    const float* gamma;
+    float* dst;
+    if (h < hq) {
+        src = mixed + static_cast<size_t>(t) * ldm + static_cast<size_t>(h) * 2 * d;
+        gamma = q_gamma;
+        dst = qkv + static_cast<size_t>(t) * ldqkv + static_cast<size_t>(h) * d;
+        float* g = gate + static_cast<size_t>(t) * ldg + static_cast<size_t>(h) * d;
+        for (uint32_t i = threadIdx.x; i < d; i += 64) g[i] = src[d + i];
+    } else {
+        const uint32_t j = h - hq;
+        src = kv + static_cast<size_t>(t) * ldkv + static_cast<size_t>(j) * d;
+        gamma = k_gamma;
+        dst = qkv + static_cast<size_t>(t) * ldqkv + static_cast<size_t>(hq + j) * d;
+        const float* vs = kv + static_cast<size_t>(t) * ldkv + static_cast<size_t>(hkv + j) * d;
+        float* vd = qkv + static_cast<size_t>(t) * ldqkv + static_cast<size_t>(hq + hkv + j) * d;
+        for (uint32_t i = threadIdx.x; i < d; i += 64) vd[i] = vs[i];
+    }
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < d; i += 64) ss += src[i] * src[i];
+    ss = warp_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
+    for (uint32_t i = threadIdx.x; i < d; i += 64) dst[i] = src[i] * inv * gamma[i];
+}
+
+// y = a * sigmoid(g) per element, per-16 sums (optional) for the next GEMV.
+__global__ void gate_mul_kernel(const float* __restrict__ a, const float* __restrict__ g, float* __restrict__ y,
+                                float* __restrict__ y16, size_t n16) {
+    const size_t grp = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (grp >= n16) return;
+    float s = 0.0f;
+    for (uint32_t i = 0; i < 16; ++i) {
+        const size_t idx = 16 * grp + i;
+        const float v = a[idx] * sigmoid_ref(g[idx]);
+        y[idx] = v;
+        s += v;
+    }
+    if (y16) y16[grp] = s;
+}
+
+uint32_t blocks_for(size_t n, uint32_t threads) { return static_cast<uint32_t>((n + threads - 1) / threads); }
+
+int launched() { return hipGetLastError() == hipSuccess ? kOk : kRuntimeError; }
+
+}  // namespace
+
+int launch_router_topk(const float* logits, size_t ld, size_t tokens, size_t experts, size_t k, int32_t* ids,
+                       float* weights, hipStream_t stream) {
+    if (!logits || !ids || !weights || tokens == 0 || experts == 0 || k == 0 || k > 8 || k > experts ||
+        ld < experts) {
+        return kInvalidArgument;
+    }
+    if (experts > kMaxExperts || tokens > 0x7fffffffull || ld > 0xffffffffull) return kLengthError;
+    hipLaunchKernelGGL(router_topk_kernel, dim3(static_cast<uint32_t>(tokens)), dim3(256), 0, stream, logits,
+                       static_cast<uint32_t>(ld), static_cast<uint32_t>(experts), static_cast<uint32_t>(k), ids,
+                       weights);
+    return launched();
+}
+
+int launch_moe_combine(const float* residual, const float* down, const float* w, const float* shared,
+                       const float* sgate, size_t ld_sgate, float* out, size_t tokens, size_t h, size_t k,
+                       hipStream_t stream) {
+    if (!residual || !down || !w || !out || tokens == 0 || h == 0 || k == 0 || (shared && (!sgate || !ld_sgate))) {
+        return kInvalidArgument;
+    }
+    if (tokens * h > 0x7fffffffull * 256ull || ld_sgate > 0xffffffffull || h > 0xffffffffull) return kLengthError;
+    hipLaunchKernelGGL(moe_combine_kernel, dim3(blocks_for(tokens * h, 256)), dim3(256), 0, stream, residual, down,
+                       w, shared, sgate, static_cast<uint32_t>(ld_sgate), out, static_cast<uint32_t>(tokens),
+                       static_cast<uint32_t>(h), static_cast<uint32_t>(k));
+    return launched();
+}
+
+int launch_gdn_gates(const float* alpha, const float* beta_raw, size_t ld, const float* dt_bias, const float* a,
+                     float* decay, float* beta, size_t tokens, size_t heads, hipStream_t stream) {
+    if (!alpha || !beta_raw || !dt_bias || !a || !decay || !beta || tokens == 0 || heads == 0 || ld < heads) {
+        return kInvalidArgument;
+    }
+    if (tokens * heads > 0x7fffffffull) return kLengthError;
+    hipLaunchKernelGGL(gdn_gates_kernel, dim3(blocks_for(tokens * heads, 256)), dim3(256), 0, stream, alpha,
+                       beta_raw, static_cast<uint32_t>(ld), dt_bias, a, decay, beta, static_cast<uint32_t>(tokens),
+                       static_cast<uint32_t>(heads));
+    return launched();
+}
+
+int launch_conv1d_silu(const float* x, size_t ldx, float* history, const float* w, float* out, size_t ldo,
+                       size_t tokens, size_t channels, size_t ksize, hipStream_t stream) {
+    if (!x || !history || !w || !out || tokens == 0 || channels == 0 || ksize < 2 || ksize > kMaxConv ||
+        ldx < channels || ldo < channels) {
+        return kInvalidArgument;
+    }
+    if (x == out) return kInvalidArgument;
+    if (channels > 0x7fffffffull || tokens > 0x7fffffffull) return kLengthError;
+    hipLaunchKernelGGL(conv1d_silu_kernel, dim3(blocks_for(channels, 256)), dim3(256), 0, stream, x,
+                       static_cast<uint32_t>(ldx), history, w, out, static_cast<uint32_t>(ldo),
+                       static_cast<uint32_t>(tokens), static_cast<uint32_t>(channels), static_cast<uint32_t>(ksize));
+    return launched();
+}
+
+int launch_l2norm_heads(float* x, size_t ld, size_t tokens, size_t heads, size_t d, float eps, hipStream_t stream) {
+    if (!x || tokens == 0 || heads == 0 || d == 0 || ld < heads * d || !(eps >= 0.0f)) return kInvalidArgument;
+    if (tokens > 0x7fffffffull || heads > 65535) return kLengthError;
+    hipLaunchKernelGGL(l2norm_heads_kernel, dim3(static_cast<uint32_t>(tokens), static_cast<uint32_t>(heads)),
+                       dim3(64), 0, stream, x, static_cast<uint32_t>(ld), static_cast<uint32_t>(d), eps);
+    return launched();
+}
+
+int launch_gdn_scan(const float* q, const float* k, size_t ldqk, const float* v, size_t ldv, const float* decay,
+                    const float* beta, float* state, float* out, size_t ldo, size_t tokens, size_t value_heads,
+                    size_t key_heads, size_t d, hipStream_t stream) {
+    if (!q || !k || !v || !decay || !beta || !state || !out || tokens == 0 || value_heads == 0 || key_heads == 0 ||
+        value_heads % key_heads != 0) {
+        return kInvalidArgument;
+    }
+    if (ldqk < key_heads * d || ldv < value_heads * d || ldo < value_heads * d) return kInvalidArgument;
+    if (tokens > 0x7fffffffull || value_heads > 0x7fffffffull) return kLengthError;
+    const dim3 grid(static_cast<uint32_t>(value_heads), static_cast<uint32_t>(d / 64));
+    const uint32_t T = static_cast<uint32_t>(tokens), Hv = static_cast<uint32_t>(value_heads),
+                   Hk = static_cast<uint32_t>(key_heads);
+    switch (d) {
+    case 64:
+        hipLaunchKernelGGL(gdn_scan_kernel<16>, grid, dim3(256), 0, stream, q, k, static_cast<uint32_t>(ldqk), v,
+                           static_cast<uint32_t>(ldv), decay, beta, state, out, static_cast<uint32_t>(ldo), T, Hv, Hk);
+        break;
+    case 128:
+        hipLaunchKernelGGL(gdn_scan_kernel<32>, grid, dim3(256), 0, stream, q, k, static_cast<uint32_t>(ldqk), v,
+                           static_cast<uint32_t>(ldv), decay, beta, state, out, static_cast<uint32_t>(ldo), T, Hv, Hk);
+        break;
+    default:
+        return kInvalidArgument;  // state size 64 or 128
+    }
+    return launched();
+}
+
+int launch_gated_rmsnorm(const float* o, size_t ldo, const float* gamma, const float* z, size_t ldz, float* y,
+                         float* ys16, size_t ldy, size_t tokens, size_t heads, size_t d, float eps,
+                         hipStream_t stream) {
+    if (!o || !gamma || !z || !y || tokens == 0 || heads == 0 || d == 0 || ldo < heads * d || ldz < heads * d ||
+        ldy < heads * d || !(eps > 0.0f)) {
+        return kInvalidArgument;
+    }
+    if (ys16 && (d % 16 != 0 || ldy % 16 != 0)) return kInvalidArgument;
+    if (tokens > 0x7fffffffull || heads > 65535) return kLengthError;
+    hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3(static_cast<uint32_t>(tokens), static_cast<uint32_t>(heads)),
+                       dim3(64), 0, stream, o, static_cast<uint32_t>(ldo), gamma, z, static_cast<uint32_t>(ldz), y,
+                       ys16, static_cast<uint32_t>(ldy), static_cast<uint32_t>(d), eps);
+    return launched();
+}
+
+int launch_split_qgate_norm(const float* mixed, size_t ldm, const float* kv, size_t ldkv, const float* q_gamma,
+                            const float* k_gamma, float* qkv, size_t ldqkv, float* gate, size_t ldg, size_t tokens,
+                            size_t hq, size_t hkv, size_t d, float eps, hipStream_t stream) {
+    if (!mixed || !kv || !q_gamma || !k_gamma || !qkv || !gate || tokens == 0 || hq == 0 || hkv == 0 || d == 0 ||
+        hq % hkv != 0 || !(eps > 0.0f)) {
+        return kInvalidArgument;
+    }
+    if (ldm < 2 * hq * d || ldkv < 2 * hkv * d || ldqkv < (hq + 2 * hkv) * d || ldg < hq * d) return kInvalidArgument;
+    if (tokens > 0x7fffffffull || hq + hkv > 65535) return kLengthError;
+    hipLaunchKernelGGL(split_qgate_norm_kernel, dim3(static_cast<uint32_t>(tokens), static_cast<uint32_t>(hq + hkv)),
+                       dim3(64), 0, stream, mixed, static_cast<uint32_t>(ldm), kv, static_cast<uint32_t>(ldkv),
+                       q_gamma, k_gamma, qkv, static_cast<uint32_t>(ldqkv), gate, static_cast<uint32_t>(ldg),
+                       static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv), static_cast<uint32_t>(d), eps);
+    return launched();
+}
+
+int launch_gate_mul(const float* a, const float* g, float* y, float* y16, size_t n, hipStream_t stream) {
+    if (!a || !g || !y || n == 0 || n % 16 != 0) return kInvalidArgument;
+    const size_t n16 = n / 16;
+    if (n16 > 0x7fffffffull) return kLengthError;
+    hipLaunchKernelGGL(gate_mul_kernel, dim3(blocks_for(n16, 256)), dim3(256), 0, stream, a, g, y, y16, n16);
+    return launched();
+}
+
+}  // namespace hipllm

@@ -5,16 +5,29 @@
 #include "../kernels/common.h"
 #include "../kernels/launch.h"
 #include "hip_llm.h"
+#include "hip_moe.h"
 
 #include <cstring>
 #include <exception>
+#include <memory>
 #include <new>
 #include <stdexcept>
 #include <string>
 
+// The handle holds the backend the CLI would pick for the file's
+// architecture (chat.cpp:1019-1035): qwen35moe -> HipMoeLLM, qwen2 -> HipLLM.
 struct HipllmModel {
-    llm::HipLLM model;
-    explicit HipllmModel(const char* path, size_t max_sequence, int device) : model(path, max_sequence, device) {}
+    std::unique_ptr<llm::HipLLM> dense;
+    std::unique_ptr<llm::HipMoeLLM> moe;
+
+    template <typename Fn>
+    decltype(auto) visit(Fn&& fn) {
+        return dense ? fn(*dense) : fn(*moe);
+    }
+    template <typename Fn>
+    decltype(auto) visit(Fn&& fn) const {
+        return dense ? fn(static_cast<const llm::HipLLM&>(*dense)) : fn(static_cast<const llm::HipMoeLLM&>(*moe));
+    }
 };
 
 namespace {
@@ -163,29 +176,46 @@ int hipllm_swiglu(const float* g, const float* u, float* y, float* y16, size_t n
                   "hipllm_swiglu: invalid arguments or launch failure");
 }
 
-int hipllm_create(const char* path, size_t max_sequence, int device, HipllmModel** out) {
+int hipllm_create_ex(const char* path, size_t max_sequence, int device, size_t expert_cache_count,
+                     HipllmModel** out) {
     if (!path || !out) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_create: null argument");
     *out = nullptr;
-    return guarded([&] { *out = new HipllmModel(path, max_sequence, device); });
+    return guarded([&] {
+        const std::string arch = llm::GgufReader(path).config().architecture;
+        auto m = std::make_unique<HipllmModel>();
+        if (arch == "qwen35moe") {
+            m->moe = std::make_unique<llm::HipMoeLLM>(path, max_sequence, device, expert_cache_count);
+        } else {
+            m->dense = std::make_unique<llm::HipLLM>(path, max_sequence, device);
+        }
+        *out = m.release();
+    });
+}
+
+int hipllm_create(const char* path, size_t max_sequence, int device, HipllmModel** out) {
+    return hipllm_create_ex(path, max_sequence, device, 8, out);
 }
 
 void hipllm_destroy(HipllmModel* m) { delete m; }
 
 int hipllm_reset(HipllmModel* m) {
     if (!m) return fail(HIPLLM_RUNTIME_ERROR, "HIP model is not initialized");
-    return guarded([&] { m->model.reset(); });
+    return guarded([&] { m->visit([](auto& b) { b.reset(); }); });
 }
 
 int hipllm_prefill(HipllmModel* m, const int32_t* ids, size_t count, int32_t* next) {
     if (!m) return fail(HIPLLM_RUNTIME_ERROR, "HIP model is not initialized");
     if (!next || (!ids && count)) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_prefill: null argument");
-    return guarded([&] { *next = m->model.prefill(std::vector<int32_t>(ids, ids + count)); });
+    return guarded([&] {
+        const std::vector<int32_t> v(ids, ids + count);
+        *next = m->visit([&](auto& b) { return b.prefill(v); });
+    });
 }
 
 int hipllm_decode(HipllmModel* m, int32_t id, int32_t* next) {
     if (!m) return fail(HIPLLM_RUNTIME_ERROR, "HIP model is not initialized");
     if (!next) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_decode: null argument");
-    return guarded([&] { *next = m->model.decode(id); });
+    return guarded([&] { *next = m->visit([&](auto& b) { return b.decode(id); }); });
 }
 
 namespace {
@@ -206,12 +236,22 @@ void fill_config(const llm::ModelConfig& c, HipllmConfig* out) {
         out->rope_theta = c.rope_theta;
         out->norm_epsilon = c.norm_epsilon;
         std::strncpy(out->architecture, c.architecture.c_str(), sizeof(out->architecture) - 1);
+        out->full_attention_interval = c.full_attention_interval;
+        out->expert_count = c.expert_count;
+        out->expert_used_count = c.expert_used_count;
+        out->expert_feed_forward_size = c.expert_feed_forward_size;
+        out->shared_expert_feed_forward_size = c.shared_expert_feed_forward_size;
+        out->ssm_conv_kernel = c.ssm_conv_kernel;
+        out->ssm_state_size = c.ssm_state_size;
+        out->ssm_group_count = c.ssm_group_count;
+        out->ssm_time_step_rank = c.ssm_time_step_rank;
+        out->ssm_inner_size = c.ssm_inner_size;
 }
 }  // namespace
 
 int hipllm_config(const HipllmModel* m, HipllmConfig* out) {
     if (!m || !out) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_config: null argument");
-    return guarded([&] { fill_config(m->model.config(), out); });
+    return guarded([&] { fill_config(m->visit([](const auto& b) -> const llm::ModelConfig& { return b.config(); }), out); });
 }
 
 int hipllm_inspect_gguf(const char* path, HipllmConfig* out) {
@@ -222,13 +262,17 @@ int hipllm_inspect_gguf(const char* path, HipllmConfig* out) {
     });
 }
 
-size_t hipllm_position(const HipllmModel* m) { return m ? m->model.position() : 0; }
-size_t hipllm_max_sequence(const HipllmModel* m) { return m ? m->model.max_sequence() : 0; }
-int hipllm_uses_gpu(const HipllmModel* m) { return m && m->model.uses_gpu() ? 1 : 0; }
+size_t hipllm_position(const HipllmModel* m) {
+    return m ? m->visit([](const auto& b) { return b.position(); }) : 0;
+}
+size_t hipllm_max_sequence(const HipllmModel* m) {
+    return m ? m->visit([](const auto& b) { return b.max_sequence(); }) : 0;
+}
+int hipllm_uses_gpu(const HipllmModel* m) { return m && m->visit([](const auto& b) { return b.uses_gpu(); }) ? 1 : 0; }
 
 int hipllm_memory_stats(const HipllmModel* m, HipllmMemoryStats* out) {
     if (!m || !out) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_memory_stats: null argument");
-    const llm::MemoryStats s = m->model.memory_stats();
+    const llm::MemoryStats s = m->visit([](const auto& b) { return b.memory_stats(); });
     out->weight_bytes = s.weight_bytes;
     out->kv_cache_bytes = s.kv_cache_bytes;
     out->recurrent_state_bytes = s.recurrent_state_bytes;
@@ -237,27 +281,119 @@ int hipllm_memory_stats(const HipllmModel* m, HipllmMemoryStats* out) {
     return HIPLLM_OK;
 }
 
-const char* hipllm_device_name(const HipllmModel* m) { return m ? m->model.device_name().c_str() : ""; }
+const char* hipllm_device_name(const HipllmModel* m) {
+    return m ? m->visit([](const auto& b) -> const std::string& { return b.device_name(); }).c_str() : "";
+}
 
 int hipllm_enable_profiling(HipllmModel* m, const char* csv_path) {
     if (!m || !csv_path) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_enable_profiling: null argument");
-    return guarded([&] { m->model.enable_profiling(csv_path); });
+    return guarded([&] { m->visit([&](auto& b) { b.enable_profiling(csv_path); }); });
 }
 
 int hipllm_disable_profiling(HipllmModel* m) {
     if (!m) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_disable_profiling: null argument");
-    m->model.disable_profiling();
+    m->visit([](auto& b) { b.disable_profiling(); });
     return HIPLLM_OK;
 }
 
 int hipllm_copy_logits(const HipllmModel* m, float* out, size_t count) {
     if (!m || !out) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_copy_logits: null argument");
-    return guarded([&] { m->model.copy_last_logits(out, count); });
+    return guarded([&] { m->visit([&](const auto& b) { b.copy_last_logits(out, count); }); });
 }
 
 int hipllm_set_batched_prefill(HipllmModel* m, int enabled) {
     if (!m) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_set_batched_prefill: null argument");
-    return guarded([&] { m->model.set_batched_prefill(enabled != 0); });
+    if (!m->dense) return fail(HIPLLM_INVALID_ARGUMENT, "batched prefill switch applies to qwen2 models");
+    return guarded([&] { m->dense->set_batched_prefill(enabled != 0); });
+}
+
+int hipllm_copy_routes(const HipllmModel* m, int32_t* out, size_t count) {
+    if (!m || !out) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_copy_routes: null argument");
+    if (!m->moe) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_copy_routes: not a MoE model");
+    return guarded([&] { m->moe->copy_last_routes(out, count); });
+}
+
+size_t hipllm_expert_cache_count(const HipllmModel* m) { return m && m->moe ? m->moe->expert_cache_count() : 0; }
+
+// ---------------------------------------------------------------- MoE kernels
+
+int hipllm_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row_bytes, const float* x,
+                        const float* xs16, const float* bias, const float* residual, float* y, float* ys16, size_t n,
+                        size_t k, size_t vectors, const int32_t* ids, size_t experts, size_t routes,
+                        size_t expert_stride, int x_routed, size_t ldx, size_t ldy, void* stream) {
+    return status(hipllm::launch_gemv_batched(type, w, wu, row_bytes, x, xs16, bias, residual, y, ys16, n, k, vectors,
+                                              ids, experts, routes, expert_stride, x_routed, ldx, ldy,
+                                              as_stream(stream)),
+                  "hipllm_gemv_batched: invalid arguments or launch failure");
+}
+
+int hipllm_router_topk(const float* logits, size_t ld, size_t tokens, size_t experts, size_t k, int32_t* ids,
+                       float* weights, void* stream) {
+    return status(hipllm::launch_router_topk(logits, ld, tokens, experts, k, ids, weights, as_stream(stream)),
+                  "hipllm_router_topk: invalid arguments (k <= 8, experts <= 1024) or launch failure");
+}
+
+int hipllm_moe_combine(const float* residual, const float* down, const float* w, const float* shared,
+                       const float* sgate, size_t ld_sgate, float* out, size_t tokens, size_t h, size_t k,
+                       void* stream) {
+    return status(hipllm::launch_moe_combine(residual, down, w, shared, sgate, ld_sgate, out, tokens, h, k,
+                                             as_stream(stream)),
+                  "hipllm_moe_combine: invalid arguments or launch failure");
+}
+
+int hipllm_gdn_gates(const float* alpha, const float* beta_raw, size_t ld, const float* dt_bias, const float* a,
+                     float* decay, float* beta, size_t tokens, size_t heads, void* stream) {
+    return status(hipllm::launch_gdn_gates(alpha, beta_raw, ld, dt_bias, a, decay, beta, tokens, heads,
+                                           as_stream(stream)),
+                  "hipllm_gdn_gates: invalid arguments or launch failure");
+}
+
+int hipllm_conv1d_silu(const float* x, size_t ldx, float* history, const float* w, float* out, size_t ldo,
+                       size_t tokens, size_t channels, size_t ksize, void* stream) {
+    return status(hipllm::launch_conv1d_silu(x, ldx, history, w, out, ldo, tokens, channels, ksize,
+                                             as_stream(stream)),
+                  "hipllm_conv1d_silu: invalid arguments (2 <= k <= 9, out != x) or launch failure");
+}
+
+int hipllm_l2norm_heads(float* x, size_t ld, size_t tokens, size_t heads, size_t d, float eps, void* stream) {
+    return status(hipllm::launch_l2norm_heads(x, ld, tokens, heads, d, eps, as_stream(stream)),
+                  "hipllm_l2norm_heads: invalid arguments or launch failure");
+}
+
+int hipllm_gdn_scan(const float* q, const float* k, size_t ldqk, const float* v, size_t ldv, const float* decay,
+                    const float* beta, float* state, float* out, size_t ldo, size_t tokens, size_t value_heads,
+                    size_t key_heads, size_t d, void* stream) {
+    return status(hipllm::launch_gdn_scan(q, k, ldqk, v, ldv, decay, beta, state, out, ldo, tokens, value_heads,
+                                          key_heads, d, as_stream(stream)),
+                  "hipllm_gdn_scan: invalid arguments (state size 64 or 128) or launch failure");
+}
+
+int hipllm_gated_rmsnorm(const float* o, size_t ldo, const float* gamma, const float* z, size_t ldz, float* y,
+                         float* ys16, size_t ldy, size_t tokens, size_t heads, size_t d, float eps, void* stream) {
+    return status(hipllm::launch_gated_rmsnorm(o, ldo, gamma, z, ldz, y, ys16, ldy, tokens, heads, d, eps,
+                                               as_stream(stream)),
+                  "hipllm_gated_rmsnorm: invalid arguments or launch failure");
+}
+
+int hipllm_split_qgate_norm(const float* mixed, size_t ldm, const float* kv, size_t ldkv, const float* q_gamma,
+                            const float* k_gamma, float* qkv, size_t ldqkv, float* gate, size_t ldg, size_t tokens,
+                            size_t hq, size_t hkv, size_t d, float eps, void* stream) {
+    return status(hipllm::launch_split_qgate_norm(mixed, ldm, kv, ldkv, q_gamma, k_gamma, qkv, ldqkv, gate, ldg,
+                                                  tokens, hq, hkv, d, eps, as_stream(stream)),
+                  "hipllm_split_qgate_norm: invalid arguments or launch failure");
+}
+
+int hipllm_gate_mul(const float* a, const float* g, float* y, float* y16, size_t n, void* stream) {
+    return status(hipllm::launch_gate_mul(a, g, y, y16, n, as_stream(stream)),
+                  "hipllm_gate_mul: invalid arguments (n % 16 == 0) or launch failure");
+}
+
+int hipllm_attn_prefill(const float* q, size_t q_stride, const float* kcache, const float* vcache, float* out,
+                        size_t out_stride, size_t rows, size_t hq, size_t hkv, size_t d, size_t pos0, float scale,
+                        void* stream) {
+    return status(hipllm::launch_attn_prefill(q, q_stride, kcache, vcache, out, out_stride, rows, hq, hkv, d, pos0,
+                                              scale, as_stream(stream)),
+                  "hipllm_attn_prefill: invalid arguments or launch failure");
 }
 
 }  // extern "C"

@@ -10,8 +10,8 @@
 //   -> rmsnorm(+xs16) -> LM-head GEMV -> argmax -> 4-byte readback.
 #include "hip_llm.h"
 
-#include "../kernels/common.h"
 #include "../kernels/launch.h"
+#include "device_common.h"
 
 #include <hip/hip_runtime.h>
 
@@ -25,27 +25,6 @@
 
 namespace llm {
 namespace {
-
-void hip_check(hipError_t e, const char* what) {
-    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
-}
-
-void launch_check(int status, const char* what) {
-    if (status == hipllm::kOk) return;
-    if (status == hipllm::kInvalidArgument) throw std::invalid_argument(std::string(what) + ": invalid kernel arguments");
-    if (status == hipllm::kLengthError) throw std::length_error(std::string(what) + ": shape exceeds kernel limits");
-    throw std::runtime_error(std::string(what) + ": kernel launch failed: " + hipGetErrorString(hipGetLastError()));
-}
-
-std::size_t align_up(std::size_t v, std::size_t a) { return (v + a - 1) / a * a; }
-
-struct DevMatrix {
-    const std::uint8_t* ptr = nullptr;
-    std::uint32_t type = 0;
-    std::size_t rows = 0;
-    std::size_t cols = 0;
-    std::size_t row_bytes = 0;
-};
 
 struct DevLayer {
     const float* attn_norm = nullptr;
@@ -98,7 +77,7 @@ struct HipLLM::Impl {
     std::size_t sequence_length = 0;
     bool batched_prefill = false;
 
-    std::uint8_t* weight_arena = nullptr;
+    WeightArena weights;
     std::size_t weight_bytes = 0;  // sum of GGUF tensor payloads
     DevMatrix embedding, output;
     const float* output_norm = nullptr;
@@ -127,7 +106,7 @@ struct HipLLM::Impl {
     ~Impl() {
         if (stream) hipStreamSynchronize(stream);
         if (profile) std::fclose(profile);
-        if (weight_arena) hipFree(weight_arena);
+        weights.release();
         if (kv_arena) hipFree(kv_arena);
         if (rope_table) hipFree(rope_table);
         if (act_arena) hipFree(act_arena);
@@ -204,168 +183,81 @@ void HipLLM::Impl::upload(GgufReader& reader) {
     const ModelConfig& c = config;
     const std::size_t H = c.embedding_size, F = c.feed_forward_size, V = c.vocabulary_size;
     kv_dim = c.kv_head_count * c.head_size;
+    WeightArena& A = weights;
 
-    // Plan: every tensor is taken (shape-checked, consumed once) up front so
-    // the arena layout is known; Q/K/V weights (and gate/up) are placed back
-    // to back when their formats match, so one GEMV covers them.
-    struct Item {
-        TensorDescriptor t;
-        std::size_t offset = 0;
-    };
-    std::vector<Item> items;
-    std::size_t cursor = 0;
-    auto place = [&](const std::string& name, std::size_t rows, std::size_t cols, bool contiguous) {
-        Item it;
-        it.t = reader.take(name, rows, cols);
-        cursor = contiguous ? cursor : align_up(cursor, 256);
-        it.offset = cursor;
-        cursor += it.t.byte_size;
-        items.push_back(it);
-        return items.size() - 1;
-    };
+    // Every tensor is taken (shape-checked, consumed once) up front so the
+    // arena layout is known. Q/K/V weights (and their biases) are packed back
+    // to back when their formats match, so one GEMV / matmul covers them.
     auto require_f32 = [&](std::size_t idx) {
-        if (items[idx].t.type != GgmlType::F32) {
-            throw std::invalid_argument("HIP norm and bias tensors must be F32: " + items[idx].t.name);
+        if (A.tensor(idx).type != GgmlType::F32) {
+            throw std::invalid_argument("HIP norm and bias tensors must be F32: " + A.tensor(idx).name);
         }
     };
     auto supported = [&](std::size_t idx) {
-        const GgmlType t = items[idx].t.type;
+        const GgmlType t = A.tensor(idx).type;
         if (t != GgmlType::F32 && t != GgmlType::F16 && t != GgmlType::Q5_0 && t != GgmlType::Q8_0 &&
             t != GgmlType::Q4_K && t != GgmlType::Q6_K) {
             throw std::invalid_argument(std::string("HIP backend does not support ") + ggml_type_name(t) +
-                                        " weights: " + items[idx].t.name);
+                                        " weights: " + A.tensor(idx).name);
         }
     };
-    const std::size_t i_embd = place("token_embd.weight", V, H, false);
-    const std::size_t i_onorm = place("output_norm.weight", 1, H, false);
-    const std::size_t i_out = place("output.weight", V, H, false);
+    const std::size_t i_embd = A.place(reader, "token_embd.weight", V, H);
+    const std::size_t i_onorm = A.place(reader, "output_norm.weight", 1, H);
+    const std::size_t i_out = A.place(reader, "output.weight", V, H);
     supported(i_embd);
     supported(i_out);
     require_f32(i_onorm);
     struct LayerIdx {
         std::size_t an, q, k, v, bq, bk, bv, o, fn, g, u, d;
-        bool fused_qkv, fused_gu;
     };
     std::vector<LayerIdx> li(c.layer_count);
     for (std::size_t l = 0; l < c.layer_count; ++l) {
         const std::string p = "blk." + std::to_string(l) + ".";
-        const TensorDescriptor tq = reader.take(p + "attn_q.weight", H, H);
         LayerIdx& x = li[l];
-        // Peek formats of K/V to decide fusion before placing.
-        x.an = place(p + "attn_norm.weight", 1, H, false);
-        Item iq;
-        iq.t = tq;
-        cursor = align_up(cursor, 256);
-        iq.offset = cursor;
-        cursor += tq.byte_size;
-        items.push_back(iq);
-        x.q = items.size() - 1;
-        x.k = place(p + "attn_k.weight", kv_dim, H, true);
-        x.v = place(p + "attn_v.weight", kv_dim, H, true);
-        x.fused_qkv = items[x.k].t.type == tq.type && items[x.v].t.type == tq.type &&
-                      items[x.k].offset == items[x.q].offset + tq.byte_size &&
-                      items[x.v].offset == items[x.k].offset + items[x.k].t.byte_size;
-        if (!x.fused_qkv) {
-            // Re-align K and V on their own.
-            cursor = items[x.k].offset;
-            cursor = align_up(cursor, 256);
-            items[x.k].offset = cursor;
-            cursor += items[x.k].t.byte_size;
-            cursor = align_up(cursor, 256);
-            items[x.v].offset = cursor;
-            cursor += items[x.v].t.byte_size;
-        }
-        x.bq = place(p + "attn_q.bias", 1, H, false);
-        x.bk = place(p + "attn_k.bias", 1, kv_dim, true);
-        x.bv = place(p + "attn_v.bias", 1, kv_dim, true);
-        x.o = place(p + "attn_output.weight", H, H, false);
-        x.fn = place(p + "ffn_norm.weight", 1, H, false);
-        x.g = place(p + "ffn_gate.weight", F, H, false);
-        x.u = place(p + "ffn_up.weight", F, H, false);
-        x.d = place(p + "ffn_down.weight", H, F, false);
-        x.fused_gu = items[x.g].t.type == items[x.u].t.type;
+        x.an = A.place(reader, p + "attn_norm.weight", 1, H);
+        x.q = A.place(reader, p + "attn_q.weight", H, H);
+        x.k = A.place(reader, p + "attn_k.weight", kv_dim, H, true);
+        x.v = A.place(reader, p + "attn_v.weight", kv_dim, H, true);
+        x.bq = A.place(reader, p + "attn_q.bias", 1, H);
+        x.bk = A.place(reader, p + "attn_k.bias", 1, kv_dim, true);
+        x.bv = A.place(reader, p + "attn_v.bias", 1, kv_dim, true);
+        x.o = A.place(reader, p + "attn_output.weight", H, H);
+        x.fn = A.place(reader, p + "ffn_norm.weight", 1, H);
+        x.g = A.place(reader, p + "ffn_gate.weight", F, H);
+        x.u = A.place(reader, p + "ffn_up.weight", F, H);
+        x.d = A.place(reader, p + "ffn_down.weight", H, F);
         for (std::size_t idx : {x.an, x.bq, x.bk, x.bv, x.fn}) require_f32(idx);
         for (std::size_t idx : {x.q, x.k, x.v, x.o, x.g, x.u, x.d}) supported(idx);
+        if (!A.contiguous(x.bq, x.bk) || !A.contiguous(x.bk, x.bv)) {
+            throw std::runtime_error("HIP Q/K/V biases must pack contiguously");
+        }
     }
     reader.validate_all_consumed();
-
-    std::size_t total = 0;
-    for (const Item& it : items) total += it.t.byte_size;
-    if (total != c.stored_weight_bytes) {
+    if (A.payload_bytes() != c.stored_weight_bytes) {
         throw std::runtime_error("HIP uploaded weight bytes do not match GGUF tensor bytes");
     }
-    weight_bytes = total;
-    // Tail padding: realigned dword reads of 2-byte-aligned blocks may touch
-    // up to 16 bytes past a tensor's last byte.
-    const std::size_t arena_bytes = align_up(cursor, 256) + 4096;
-    hip_check(hipMalloc(reinterpret_cast<void**>(&weight_arena), arena_bytes), "hipMalloc(weights)");
-    hip_check(hipMemsetAsync(weight_arena, 0, arena_bytes, stream), "hipMemsetAsync(weights)");
+    weight_bytes = A.payload_bytes();
+    A.upload(reader, stream);
 
-    // Stream tensor bytes through two pinned staging buffers.
-    const std::size_t stage_bytes = 64u << 20;
-    void* stage[2] = {nullptr, nullptr};
-    hipEvent_t done[2] = {nullptr, nullptr};
-    struct Cleanup {
-        void** s;
-        hipEvent_t* e;
-        ~Cleanup() {
-            for (int i = 0; i < 2; ++i) {
-                if (e[i]) hipEventSynchronize(e[i]), hipEventDestroy(e[i]);
-                if (s[i]) hipHostFree(s[i]);
-            }
-        }
-    } cleanup{stage, done};
-    for (int i = 0; i < 2; ++i) {
-        hip_check(hipHostMalloc(&stage[i], stage_bytes, hipHostMallocDefault), "hipHostMalloc(staging)");
-        hip_check(hipEventCreateWithFlags(&done[i], hipEventDisableTiming), "hipEventCreate");
-    }
-    int slot = 0;
-    bool used[2] = {false, false};
-    for (const Item& it : items) {
-        std::size_t off = 0;
-        while (off < it.t.byte_size) {
-            const std::size_t n = std::min(stage_bytes, it.t.byte_size - off);
-            if (used[slot]) hip_check(hipEventSynchronize(done[slot]), "hipEventSynchronize(staging)");
-            reader.read(it.t, off, stage[slot], n);
-            hip_check(hipMemcpyAsync(weight_arena + it.offset + off, stage[slot], n, hipMemcpyHostToDevice, stream),
-                      "hipMemcpyAsync(weights)");
-            hip_check(hipEventRecord(done[slot], stream), "hipEventRecord");
-            used[slot] = true;
-            slot ^= 1;
-            off += n;
-        }
-    }
-    hip_check(hipStreamSynchronize(stream), "weight upload");
-
-    auto mat = [&](std::size_t idx) {
-        DevMatrix m;
-        m.ptr = weight_arena + items[idx].offset;
-        m.type = static_cast<std::uint32_t>(items[idx].t.type);
-        m.rows = items[idx].t.rows;
-        m.cols = items[idx].t.cols;
-        m.row_bytes = items[idx].t.row_bytes;
-        return m;
-    };
-    auto vec = [&](std::size_t idx) { return reinterpret_cast<const float*>(weight_arena + items[idx].offset); };
-    embedding = mat(i_embd);
-    output = mat(i_out);
-    output_norm = vec(i_onorm);
+    embedding = A.matrix(i_embd);
+    output = A.matrix(i_out);
+    output_norm = A.vec(i_onorm);
     layers.resize(c.layer_count);
     for (std::size_t l = 0; l < c.layer_count; ++l) {
         const LayerIdx& x = li[l];
         DevLayer& L = layers[l];
-        L.attn_norm = vec(x.an);
-        L.q = mat(x.q);
-        L.k = mat(x.k);
-        L.v = mat(x.v);
-        L.fused_qkv = x.fused_qkv;
-        L.qkv_bias = vec(x.bq);
-        L.o = mat(x.o);
-        L.ffn_norm = vec(x.fn);
-        L.gate = mat(x.g);
-        L.up = mat(x.u);
-        L.down = mat(x.d);
-        L.fused_gate_up = x.fused_gu;
+        L.attn_norm = A.vec(x.an);
+        L.q = A.matrix(x.q);
+        L.k = A.matrix(x.k);
+        L.v = A.matrix(x.v);
+        L.fused_qkv = A.contiguous(x.q, x.k) && A.contiguous(x.k, x.v);
+        L.qkv_bias = A.vec(x.bq);
+        L.o = A.matrix(x.o);
+        L.ffn_norm = A.vec(x.fn);
+        L.gate = A.matrix(x.g);
+        L.up = A.matrix(x.u);
+        L.down = A.matrix(x.d);
+        L.fused_gate_up = A.tensor(x.g).type == A.tensor(x.u).type;
     }
 }
 
@@ -714,7 +606,7 @@ const ModelConfig& HipLLM::config() const {
 std::size_t HipLLM::position() const noexcept { return impl_ ? impl_->sequence_length : 0; }
 std::size_t HipLLM::max_sequence() const noexcept { return impl_ ? impl_->max_sequence : 0; }
 bool HipLLM::uses_gpu() const noexcept { return available(); }
-bool HipLLM::available() const noexcept { return impl_ && impl_->weight_arena && impl_->stream; }
+bool HipLLM::available() const noexcept { return impl_ && impl_->weights.base() && impl_->stream; }
 
 const std::string& HipLLM::device_name() const noexcept {
     static const std::string empty;

@@ -1,0 +1,792 @@
+// HipMoeLLM implementation (see hip_moe.h).
+//
+// One forward over T rows (the whole prompt, or one decode token), on one
+// stream (MoeLLM::forward, moe_llm.mm:2887-3039, restated without its 41 host
+// round trips):
+//   embed -> L x [ RMSNorm -> (gated attention | Gated DeltaNet) (+residual)
+//                  -> RMSNorm -> router + top-k -> routed experts (gate/up +
+//                  SwiGLU, down) + shared expert -> combine (+residual) ]
+//   -> RMSNorm(last row) -> LM-head GEMV -> argmax -> 4-byte readback.
+// Projections are FP32-accumulating GEMVs over the native weights: a batched
+// launch covers all T rows (blockIdx.y = row), and the routed experts are the
+// same kernel indexed by the device-resident top-k ids.
+#include "hip_moe.h"
+
+#include "../kernels/launch.h"
+#include "device_common.h"
+
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+#include <stdexcept>
+
+
+namespace llm {
+namespace {
+
+struct MoeLayer {
+    bool full = false;
+    const float* attn_norm = nullptr;
+    const float* post_norm = nullptr;
+    // gated full attention
+    DevMatrix qgate, k, v, o;
+    bool fused_kv = false;
+    const float* q_norm = nullptr;
+    const float* k_norm = nullptr;
+    float* kcache = nullptr;
+    float* vcache = nullptr;
+    // Gated DeltaNet
+    DevMatrix qkv, z, alpha, beta, ssm_out;
+    bool fused_ab = false;
+    const float* conv = nullptr;
+    const float* dt_bias = nullptr;
+    const float* a = nullptr;
+    const float* ssm_norm = nullptr;
+    float* state = nullptr;
+    float* history = nullptr;
+    // experts
+    DevMatrix router, shexp_router;  // F32 [E, H] and [1, H], packed -> one GEMV of E + 1 rows
+    bool fused_router = false;
+    DevMatrix gate_exps, up_exps, down_exps;  // per expert rows; expert_stride between experts
+    DevMatrix sh_gate, sh_up, sh_down;
+};
+
+// Activation rows for up to `rows` tokens.
+struct MoeActivations {
+    float* hidden[2] = {nullptr, nullptr};  // [T, H]
+    float* norm = nullptr;                  // [T, H]
+    float* norm16 = nullptr;                // [T, H / 16]
+    float* wide = nullptr;                  // [T, max(2 Hq D, qkv_w)]  Q+gate mix / DeltaNet QKV
+    float* wide2 = nullptr;                 // [T, max((Hq + 2 Hkv) D, qkv_w)]  attention QKV / conv output
+    float* kv = nullptr;                    // [T, 2 Hkv D]
+    float* feat = nullptr;                  // [T, max(Hq D, inner)]  attention gate / DeltaNet z
+    float* feat2 = nullptr;                 // [T, max(Hq D, inner)]  attention / recurrence output
+    float* gated = nullptr;                 // [T, max(Hq D, inner)]
+    float* gated16 = nullptr;
+    float* ab = nullptr;                    // [T, 2 Hv]
+    float* decay = nullptr;                 // [T, Hv]
+    float* beta = nullptr;                  // [T, Hv]
+    float* rlog = nullptr;                  // [T, E + 1] router logits | shared gate
+    float* rweight = nullptr;               // [T, k]
+    float* act = nullptr;                   // [T k, FF]
+    float* act16 = nullptr;
+    float* down = nullptr;                  // [T k, H]
+    float* sh_act = nullptr;                // [T, FFs]
+    float* sh_act16 = nullptr;
+    float* sh_down = nullptr;               // [T, H]
+    float* logits = nullptr;                // [V]
+    float* attn_scratch = nullptr;
+    void* argmax_scratch = nullptr;
+    std::int32_t* ids = nullptr;            // [T] prompt / decode ids
+    std::uint32_t* token = nullptr;
+};
+
+}  // namespace
+
+struct HipMoeLLM::Impl {
+    int device = 0;
+    std::string device_name;
+    hipStream_t stream = nullptr;
+    ModelConfig config;
+    std::size_t capacity = 0;
+    std::size_t sequence_length = 0;
+    std::size_t expert_cache = 0;
+
+    WeightArena weights;
+    std::size_t weight_bytes = 0;
+    DevMatrix embedding, output;
+    const float* output_norm = nullptr;
+    std::vector<MoeLayer> layers;
+
+    std::size_t H = 0, D = 0, Hq = 0, Hkv = 0, E = 0, K = 0, FF = 0, FFs = 0;
+    std::size_t S = 0, G = 0, Hv = 0, inner = 0, qkv_w = 0, kv_w = 0, q_w = 0;
+
+    void* state_arena = nullptr;
+    std::size_t kv_cache_bytes = 0, recurrent_bytes = 0;
+    float* rope_table = nullptr;
+    std::int32_t* route_ids = nullptr;  // [L, rows, K]
+
+    void* act_arena = nullptr;
+    std::size_t act_bytes = 0;
+    std::size_t act_rows = 0;
+    MoeActivations act;
+    std::int32_t* host_ids = nullptr;
+    std::uint32_t* host_token = nullptr;
+    std::size_t host_ids_cap = 0;
+    std::size_t last_rows = 0;
+    std::FILE* profile = nullptr;
+
+    ~Impl() {
+        if (stream) hipStreamSynchronize(stream);
+        if (profile) std::fclose(profile);
+        weights.release();
+        if (state_arena) hipFree(state_arena);
+        if (rope_table) hipFree(rope_table);
+        if (act_arena) hipFree(act_arena);
+        if (route_ids) hipFree(route_ids);
+        if (host_ids) hipHostFree(host_ids);
+        if (host_token) hipHostFree(host_token);
+        if (stream) hipStreamDestroy(stream);
+    }
+
+    void load(const std::string& path, std::size_t max_sequence, int dev, std::size_t cache_count);
+    void upload(GgufReader& reader);
+    void allocate_state();
+    void build_rope_table();
+    void zero_state();
+    void ensure_rows(std::size_t rows);
+
+    void proj(const DevMatrix& w, const float* x, const float* x16, std::size_t ldx, std::size_t rows, float* y,
+              std::size_t ldy, const float* residual = nullptr, std::size_t n_override = 0) const;
+    void attention_layer(std::size_t li, std::size_t rows, std::size_t pos0, float* hidden, float* next);
+    void deltanet_layer(std::size_t li, std::size_t rows, float* hidden, float* next);
+    void moe_layer(std::size_t li, std::size_t rows, float* hidden, float* next);
+    void forward(std::size_t rows, std::size_t pos0);
+    std::int32_t read_token();
+};
+
+void HipMoeLLM::Impl::load(const std::string& path, std::size_t max_sequence, int dev, std::size_t cache_count) {
+    int count = 0;
+    hip_check(hipGetDeviceCount(&count), "hipGetDeviceCount");
+    if (count <= 0) throw std::runtime_error("no HIP device is available");
+    if (dev < 0) hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev >= count) throw std::invalid_argument("HIP device index is outside the visible devices");
+    device = dev;
+    hip_check(hipSetDevice(device), "hipSetDevice");
+    hipDeviceProp_t prop;
+    hip_check(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    device_name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+    hip_check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
+
+    GgufReader reader(path);
+    const ModelConfig& c = reader.config();
+    if (c.architecture != "qwen35moe") throw std::runtime_error("HipMoeLLM requires qwen35moe, got " + c.architecture);
+    // require_qwen35_config (moe_model.cpp:39-80).
+    if (c.layer_count == 0 || c.full_attention_interval == 0 || c.embedding_size == 0 ||
+        c.attention_head_count == 0 || c.kv_head_count == 0 || c.head_size == 0 || c.rotary_dimension == 0 ||
+        c.expert_count == 0 || c.expert_used_count == 0 || c.expert_used_count > c.expert_count ||
+        c.expert_feed_forward_size == 0 || c.shared_expert_feed_forward_size == 0 || c.ssm_conv_kernel == 0 ||
+        c.ssm_state_size == 0 || c.ssm_group_count == 0 || c.ssm_time_step_rank == 0 || c.ssm_inner_size == 0) {
+        throw std::runtime_error("incomplete qwen35moe GGUF metadata");
+    }
+    if (c.rotary_dimension > c.head_size || c.rotary_dimension % 2 != 0) {
+        throw std::runtime_error("qwen35moe rotary dimension must be even and fit one head");
+    }
+    if (c.expert_used_count > 8) throw std::runtime_error("qwen35moe currently supports at most eight selected experts");
+    if (c.ssm_conv_kernel > 9 || c.ssm_conv_kernel < 2) {
+        throw std::runtime_error("qwen35moe convolution kernel exceeds the history limit");
+    }
+    if (c.ssm_inner_size % c.ssm_time_step_rank != 0 || c.ssm_inner_size / c.ssm_time_step_rank != c.ssm_state_size) {
+        throw std::runtime_error("qwen35moe DeltaNet value-head dimensions are inconsistent");
+    }
+    if (c.ssm_time_step_rank % c.ssm_group_count != 0) {
+        throw std::runtime_error("qwen35moe DeltaNet value heads must group key heads evenly");
+    }
+    // What these kernels cover.
+    if (c.ssm_state_size != 64 && c.ssm_state_size != 128) {
+        throw std::invalid_argument("HIP DeltaNet kernels support state sizes 64 and 128");
+    }
+    if (c.head_size > 256 || c.head_size % 16 != 0 || c.embedding_size % 16 != 0 || c.expert_count > 1024 ||
+        c.expert_feed_forward_size % 16 != 0 || c.shared_expert_feed_forward_size % 16 != 0) {
+        throw std::invalid_argument("HIP MoE kernels need head size <= 256 and widths that are multiples of 16");
+    }
+    capacity = max_sequence == 0 ? std::min<std::size_t>(c.context_length, 1024) : max_sequence;
+    if (capacity == 0 || capacity > c.context_length) {
+        throw std::invalid_argument("MoE sequence capacity is outside the model context length");
+    }
+    if (cache_count < c.expert_used_count || cache_count > c.expert_count) {
+        throw std::invalid_argument("per-layer expert cache count must be between top-k (" +
+                                    std::to_string(c.expert_used_count) + ") and expert count (" +
+                                    std::to_string(c.expert_count) + ")");
+    }
+    expert_cache = cache_count;
+    config = c;
+    H = c.embedding_size;
+    D = c.head_size;
+    Hq = c.attention_head_count;
+    Hkv = c.kv_head_count;
+    E = c.expert_count;
+    K = c.expert_used_count;
+    FF = c.expert_feed_forward_size;
+    FFs = c.shared_expert_feed_forward_size;
+    S = c.ssm_state_size;
+    G = c.ssm_group_count;
+    Hv = c.ssm_time_step_rank;
+    inner = c.ssm_inner_size;
+    qkv_w = 2 * G * S + inner;
+    kv_w = Hkv * D;
+    q_w = Hq * D;
+    for (std::size_t l = c.layer_count; l < c.total_layer_count; ++l) {
+        reader.ignore_prefix("blk." + std::to_string(l) + ".");  // NextN / MTP blocks (moe_model.cpp:84-94)
+    }
+    upload(reader);
+    allocate_state();
+    build_rope_table();
+    zero_state();
+}
+
+void HipMoeLLM::Impl::upload(GgufReader& reader) {
+    const ModelConfig& c = config;
+    WeightArena& A = weights;
+    auto require = [&](std::size_t idx, std::initializer_list<GgmlType> ok, const char* what) {
+        const GgmlType t = A.tensor(idx).type;
+        for (GgmlType g : ok) {
+            if (t == g) return;
+        }
+        throw std::invalid_argument(std::string("HIP MoE backend does not support ") + ggml_type_name(t) + " for " +
+                                    what + ": " + A.tensor(idx).name);
+    };
+    const std::initializer_list<GgmlType> mats = {GgmlType::F32, GgmlType::F16, GgmlType::Q5_0, GgmlType::Q8_0,
+                                                  GgmlType::Q4_K, GgmlType::Q6_K};
+    const std::initializer_list<GgmlType> f32 = {GgmlType::F32};
+    const std::size_t V = c.vocabulary_size;
+    const std::size_t i_embd = A.place(reader, "token_embd.weight", V, H);
+    const std::size_t i_onorm = A.place(reader, "output_norm.weight", 1, H);
+    const std::size_t i_out = A.place(reader, "output.weight", V, H);
+    require(i_embd, mats, "the embedding");
+    require(i_out, mats, "the output head");
+    require(i_onorm, f32, "norms");
+    struct Idx {
+        std::size_t an, pn, qg, k, v, qn, kn, o, qkv, z, al, be, conv, dt, a, sn, so, r, shr, ge, ue, de, sg, su, sd;
+    };
+    std::vector<Idx> idx(c.layer_count);
+    layers.resize(c.layer_count);
+    for (std::size_t l = 0; l < c.layer_count; ++l) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        Idx& x = idx[l];
+        MoeLayer& L = layers[l];
+        L.full = (l + 1) % c.full_attention_interval == 0;  // moe_model.cpp:164-166
+        x.an = A.place(reader, p + "attn_norm.weight", 1, H);
+        x.pn = A.place(reader, p + "post_attention_norm.weight", 1, H);
+        require(x.an, f32, "norms");
+        require(x.pn, f32, "norms");
+        if (L.full) {
+            x.qg = A.place(reader, p + "attn_q.weight", 2 * q_w, H);
+            x.k = A.place(reader, p + "attn_k.weight", kv_w, H);
+            x.v = A.place(reader, p + "attn_v.weight", kv_w, H, true);
+            x.qn = A.place(reader, p + "attn_q_norm.weight", 1, D);
+            x.kn = A.place(reader, p + "attn_k_norm.weight", 1, D);
+            x.o = A.place(reader, p + "attn_output.weight", H, q_w);
+            for (std::size_t i : {x.qg, x.k, x.v, x.o}) require(i, mats, "attention projections");
+            require(x.qn, f32, "norms");
+            require(x.kn, f32, "norms");
+        } else {
+            x.qkv = A.place(reader, p + "attn_qkv.weight", qkv_w, H);
+            x.z = A.place(reader, p + "attn_gate.weight", inner, H);
+            x.al = A.place(reader, p + "ssm_alpha.weight", Hv, H);
+            x.be = A.place(reader, p + "ssm_beta.weight", Hv, H, true);
+            x.conv = A.place(reader, p + "ssm_conv1d.weight", qkv_w, c.ssm_conv_kernel);
+            x.dt = A.place(reader, p + "ssm_dt.bias", 1, Hv);
+            x.a = A.place(reader, p + "ssm_a", 1, Hv);
+            x.sn = A.place(reader, p + "ssm_norm.weight", 1, S);
+            x.so = A.place(reader, p + "ssm_out.weight", H, inner);
+            for (std::size_t i : {x.qkv, x.z, x.al, x.be, x.so}) require(i, mats, "DeltaNet projections");
+            for (std::size_t i : {x.conv, x.dt, x.a, x.sn}) require(i, f32, "DeltaNet vectors");
+        }
+        x.r = A.place(reader, p + "ffn_gate_inp.weight", E, H);
+        x.shr = A.place(reader, p + "ffn_gate_inp_shexp.weight", 1, H, true);
+        x.ge = A.place(reader, p + "ffn_gate_exps.weight", FF * E, H);
+        x.ue = A.place(reader, p + "ffn_up_exps.weight", FF * E, H);
+        x.de = A.place(reader, p + "ffn_down_exps.weight", H * E, FF);
+        x.sg = A.place(reader, p + "ffn_gate_shexp.weight", FFs, H);
+        x.su = A.place(reader, p + "ffn_up_shexp.weight", FFs, H);
+        x.sd = A.place(reader, p + "ffn_down_shexp.weight", H, FFs);
+        require(x.r, mats, "the router");
+        require(x.shr, mats, "the shared-expert gate");
+        for (std::size_t i : {x.ge, x.ue, x.de}) require(i, {GgmlType::Q4_K, GgmlType::Q6_K}, "routed experts");
+        for (std::size_t i : {x.sg, x.su, x.sd}) require(i, mats, "the shared expert");
+        // Exact GGUF dimension vectors of the expert tensors (moe_model.cpp:21-37).
+        const std::vector<std::uint64_t> gd = {H, FF, E}, dd = {FF, H, E};
+        if (A.tensor(x.ge).dimensions != gd || A.tensor(x.ue).dimensions != gd || A.tensor(x.de).dimensions != dd) {
+            throw std::runtime_error("unexpected GGUF dimensions for expert tensors of layer " + std::to_string(l));
+        }
+    }
+    reader.validate_all_consumed();
+    if (A.payload_bytes() != c.stored_weight_bytes) {
+        throw std::runtime_error("HIP uploaded weight bytes do not match GGUF tensor bytes");
+    }
+    weight_bytes = A.payload_bytes();
+    A.upload(reader, stream);
+
+    embedding = A.matrix(i_embd);
+    output = A.matrix(i_out);
+    output_norm = A.vec(i_onorm);
+    for (std::size_t l = 0; l < c.layer_count; ++l) {
+        const Idx& x = idx[l];
+        MoeLayer& L = layers[l];
+        L.attn_norm = A.vec(x.an);
+        L.post_norm = A.vec(x.pn);
+        if (L.full) {
+            L.qgate = A.matrix(x.qg);
+            L.k = A.matrix(x.k);
+            L.v = A.matrix(x.v);
+            L.fused_kv = A.contiguous(x.k, x.v);
+            L.q_norm = A.vec(x.qn);
+            L.k_norm = A.vec(x.kn);
+            L.o = A.matrix(x.o);
+        } else {
+            L.qkv = A.matrix(x.qkv);
+            L.z = A.matrix(x.z);
+            L.alpha = A.matrix(x.al);
+            L.beta = A.matrix(x.be);
+            L.fused_ab = A.contiguous(x.al, x.be);
+            L.conv = A.vec(x.conv);
+            L.dt_bias = A.vec(x.dt);
+            L.a = A.vec(x.a);
+            L.ssm_norm = A.vec(x.sn);
+            L.ssm_out = A.matrix(x.so);
+        }
+        L.router = A.matrix(x.r);
+        L.shexp_router = A.matrix(x.shr);
+        L.fused_router = A.contiguous(x.r, x.shr);
+        L.gate_exps = A.matrix(x.ge, E);
+        L.up_exps = A.matrix(x.ue, E);
+        L.down_exps = A.matrix(x.de, E);
+        L.sh_gate = A.matrix(x.sg);
+        L.sh_up = A.matrix(x.su);
+        L.sh_down = A.matrix(x.sd);
+    }
+}
+
+// KV caches of the full-attention layers, DeltaNet states and conv histories,
+// and the per-layer route ids, in one allocation.
+void HipMoeLLM::Impl::allocate_state() {
+    std::size_t full = 0, dn = 0;
+    for (const MoeLayer& L : layers) (L.full ? full : dn)++;
+    const std::size_t cache_floats = capacity * kv_w;
+    const std::size_t state_floats = Hv * S * S;
+    const std::size_t hist_floats = (config.ssm_conv_kernel - 1) * qkv_w;
+    kv_cache_bytes = full * 2 * cache_floats * 4;
+    recurrent_bytes = dn * (state_floats + hist_floats) * 4;
+    const std::size_t bytes = align_up(kv_cache_bytes, 256) + align_up(recurrent_bytes, 256) + 256;
+    hip_check(hipMalloc(&state_arena, bytes), "hipMalloc(MoE state)");
+    float* p = static_cast<float*>(state_arena);
+    for (MoeLayer& L : layers) {
+        if (!L.full) continue;
+        L.kcache = p;
+        p += cache_floats;
+        L.vcache = p;
+        p += cache_floats;
+    }
+    p = reinterpret_cast<float*>(static_cast<std::uint8_t*>(state_arena) + align_up(kv_cache_bytes, 256));
+    for (MoeLayer& L : layers) {
+        if (L.full) continue;
+        L.state = p;
+        p += state_floats;
+        L.history = p;
+        p += hist_floats;
+    }
+    hip_check(hipHostMalloc(reinterpret_cast<void**>(&host_token), 64, hipHostMallocDefault), "hipHostMalloc(token)");
+    ensure_rows(1);
+}
+
+// cos/sin for every (position, pair) of the rotary width R, with the
+// reference's expression (metal_llm.metal:954-960): freq = pow(theta, -2i/R).
+void HipMoeLLM::Impl::build_rope_table() {
+    const std::size_t R = config.rotary_dimension, half = R / 2;
+    std::vector<float> table(capacity * half * 2);
+    for (std::size_t pos = 0; pos < capacity; ++pos) {
+        for (std::size_t i = 0; i < half; ++i) {
+            const float freq = std::pow(config.rope_theta, -2.0f * static_cast<float>(i) / static_cast<float>(R));
+            const float ang = static_cast<float>(pos) * freq;
+            table[2 * (pos * half + i)] = std::cos(ang);
+            table[2 * (pos * half + i) + 1] = std::sin(ang);
+        }
+    }
+    hip_check(hipMalloc(reinterpret_cast<void**>(&rope_table), table.size() * 4), "hipMalloc(RoPE)");
+    hip_check(hipMemcpy(rope_table, table.data(), table.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(RoPE)");
+}
+
+// reset_state (moe_llm.mm:1531-1548): DeltaNet states and histories start at 0.
+void HipMoeLLM::Impl::zero_state() {
+    const std::size_t off = align_up(kv_cache_bytes, 256);
+    if (recurrent_bytes) {
+        hip_check(hipMemsetAsync(static_cast<std::uint8_t*>(state_arena) + off, 0, recurrent_bytes, stream),
+                  "hipMemsetAsync(DeltaNet state)");
+    }
+    hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+}
+
+void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
+    if (n <= act_rows && act_arena) return;
+    hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    if (act_arena) hipFree(act_arena);
+    if (route_ids) hipFree(route_ids);
+    if (host_ids) hipHostFree(host_ids);
+    act_arena = nullptr;
+    route_ids = nullptr;
+    host_ids = nullptr;
+    act_rows = 0;
+    const std::size_t wide = std::max(2 * q_w, qkv_w), wide2 = std::max(q_w + 2 * kv_w, qkv_w);
+    const std::size_t feat = std::max(q_w, inner);
+    std::size_t off = 0;
+    auto reserve = [&](std::size_t floats) {
+        const std::size_t at = off;
+        off = align_up(off + floats * 4, 256);
+        return at;
+    };
+    const std::size_t o_h0 = reserve(n * H), o_h1 = reserve(n * H), o_norm = reserve(n * H),
+                      o_norm16 = reserve(n * H / 16), o_wide = reserve(n * wide), o_wide2 = reserve(n * wide2),
+                      o_kv = reserve(n * 2 * kv_w), o_feat = reserve(n * feat), o_feat2 = reserve(n * feat),
+                      o_gated = reserve(n * feat), o_gated16 = reserve(n * feat / 16), o_ab = reserve(n * 2 * Hv),
+                      o_decay = reserve(n * Hv), o_beta = reserve(n * Hv), o_rlog = reserve(n * (E + 1)),
+                      o_rw = reserve(n * K), o_act = reserve(n * K * FF), o_act16 = reserve(n * K * FF / 16),
+                      o_down = reserve(n * K * H), o_sha = reserve(n * FFs), o_sha16 = reserve(n * FFs / 16),
+                      o_shd = reserve(n * H), o_logits = reserve(config.vocabulary_size),
+                      o_as = reserve(hipllm::attn_decode_scratch_floats(Hq, D, capacity)),
+                      o_am = reserve(hipllm::argmax_scratch_bytes(config.vocabulary_size) / 4 + 1),
+                      o_ids = reserve(n), o_tok = reserve(16);
+    act_bytes = off;
+    hip_check(hipMalloc(&act_arena, act_bytes), "hipMalloc(MoE activations)");
+    auto* b = static_cast<std::uint8_t*>(act_arena);
+    auto f = [&](std::size_t o) { return reinterpret_cast<float*>(b + o); };
+    act.hidden[0] = f(o_h0);
+    act.hidden[1] = f(o_h1);
+    act.norm = f(o_norm);
+    act.norm16 = f(o_norm16);
+    act.wide = f(o_wide);
+    act.wide2 = f(o_wide2);
+    act.kv = f(o_kv);
+    act.feat = f(o_feat);
+    act.feat2 = f(o_feat2);
+    act.gated = f(o_gated);
+    act.gated16 = f(o_gated16);
+    act.ab = f(o_ab);
+    act.decay = f(o_decay);
+    act.beta = f(o_beta);
+    act.rlog = f(o_rlog);
+    act.rweight = f(o_rw);
+    act.act = f(o_act);
+    act.act16 = f(o_act16);
+    act.down = f(o_down);
+    act.sh_act = f(o_sha);
+    act.sh_act16 = f(o_sha16);
+    act.sh_down = f(o_shd);
+    act.logits = f(o_logits);
+    act.attn_scratch = f(o_as);
+    act.argmax_scratch = b + o_am;
+    act.ids = reinterpret_cast<std::int32_t*>(b + o_ids);
+    act.token = reinterpret_cast<std::uint32_t*>(b + o_tok);
+    hip_check(hipMalloc(reinterpret_cast<void**>(&route_ids), layers.size() * n * K * 4), "hipMalloc(routes)");
+    hip_check(hipHostMalloc(reinterpret_cast<void**>(&host_ids), n * 4, hipHostMallocDefault), "hipHostMalloc(ids)");
+    act_rows = n;
+}
+
+// y[rows, :] = W x[rows, :] (+ residual); one GEMV per row, batched over rows.
+void HipMoeLLM::Impl::proj(const DevMatrix& w, const float* x, const float* x16, std::size_t ldx, std::size_t rows,
+                           float* y, std::size_t ldy, const float* residual, std::size_t n_override) const {
+    const std::size_t n = n_override ? n_override : w.rows;
+    if (rows == 1) {
+        launch_check(hipllm::launch_gemv_prepped(w.type, w.ptr, w.row_bytes, x, x16, nullptr, residual, y, n, w.cols,
+                                                 0, stream),
+                     "GEMV");
+        return;
+    }
+    launch_check(hipllm::launch_gemv_batched(w.type, w.ptr, nullptr, w.row_bytes, x, x16, nullptr, residual, y,
+                                             nullptr, n, w.cols, rows, nullptr, 1, 1, 0, 0, ldx, ldy, stream),
+                 "batched GEMV");
+}
+
+// Gated full attention (moe_llm.mm:2238-2434) over `rows` rows at positions
+// pos0.. ; next = hidden + out_proj(attention * sigmoid(gate)).
+void HipMoeLLM::Impl::attention_layer(std::size_t li, std::size_t rows, std::size_t pos0, float* hidden,
+                                      float* next) {
+    const MoeLayer& L = layers[li];
+    const float eps = config.norm_epsilon;
+    const std::size_t ldqkv = q_w + 2 * kv_w;
+    proj(L.qgate, act.norm, act.norm16, H, rows, act.wide, 2 * q_w);
+    if (L.fused_kv) {
+        proj(L.k, act.norm, act.norm16, H, rows, act.kv, 2 * kv_w, nullptr, 2 * kv_w);
+    } else {
+        proj(L.k, act.norm, act.norm16, H, rows, act.kv, 2 * kv_w);
+        // V rows land after K in each row; batched rows need ldy = 2 kv_w.
+        if (rows == 1) {
+            proj(L.v, act.norm, act.norm16, H, rows, act.kv + kv_w, 2 * kv_w);
+        } else {
+            launch_check(hipllm::launch_gemv_batched(L.v.type, L.v.ptr, nullptr, L.v.row_bytes, act.norm,
+                                                     act.norm16, nullptr, nullptr, act.kv + kv_w, nullptr, kv_w, H,
+                                                     rows, nullptr, 1, 1, 0, 0, H, 2 * kv_w, stream),
+                         "batched GEMV");
+        }
+    }
+    launch_check(hipllm::launch_split_qgate_norm(act.wide, 2 * q_w, act.kv, 2 * kv_w, L.q_norm, L.k_norm, act.wide2,
+                                                 ldqkv, act.feat, q_w, rows, Hq, Hkv, D, eps, stream),
+                 "Q/gate split + head norms");
+    launch_check(hipllm::launch_rope_kv(act.wide2, rope_table, config.rotary_dimension, Hq, Hkv, D, pos0, rows, ldqkv,
+                                        L.kcache, L.vcache, stream),
+                 "RoPE/KV write");
+    const float scale = 1.0f / std::sqrt(static_cast<float>(D));
+    if (rows == 1) {
+        launch_check(hipllm::launch_attn_decode(act.wide2, L.kcache, L.vcache, act.feat2, nullptr, act.attn_scratch,
+                                                Hq, Hkv, D, pos0 + 1, scale, stream),
+                     "attention");
+    } else {
+        launch_check(hipllm::launch_attn_prefill(act.wide2, ldqkv, L.kcache, L.vcache, act.feat2, q_w, rows, Hq, Hkv,
+                                                 D, pos0, scale, stream),
+                     "prefill attention");
+    }
+    launch_check(hipllm::launch_gate_mul(act.feat2, act.feat, act.gated, act.gated16, rows * q_w, stream),
+                 "attention output gate");
+    proj(L.o, act.gated, act.gated16, q_w, rows, next, H, hidden);
+}
+
+// Gated DeltaNet (moe_llm.mm:2436-2640); next = hidden + out_proj(...).
+void HipMoeLLM::Impl::deltanet_layer(std::size_t li, std::size_t rows, float* hidden, float* next) {
+    const MoeLayer& L = layers[li];
+    const float eps = config.norm_epsilon;
+    proj(L.qkv, act.norm, act.norm16, H, rows, act.wide, qkv_w);
+    proj(L.z, act.norm, act.norm16, H, rows, act.feat, inner);
+    if (L.fused_ab) {
+        proj(L.alpha, act.norm, act.norm16, H, rows, act.ab, 2 * Hv, nullptr, 2 * Hv);
+    } else if (rows == 1) {
+        proj(L.alpha, act.norm, act.norm16, H, rows, act.ab, 2 * Hv);
+        proj(L.beta, act.norm, act.norm16, H, rows, act.ab + Hv, 2 * Hv);
+    } else {
+        proj(L.alpha, act.norm, act.norm16, H, rows, act.ab, 2 * Hv);
+        launch_check(hipllm::launch_gemv_batched(L.beta.type, L.beta.ptr, nullptr, L.beta.row_bytes, act.norm,
+                                                 act.norm16, nullptr, nullptr, act.ab + Hv, nullptr, Hv, H, rows,
+                                                 nullptr, 1, 1, 0, 0, H, 2 * Hv, stream),
+                     "batched GEMV");
+    }
+    launch_check(hipllm::launch_gdn_gates(act.ab, act.ab + Hv, 2 * Hv, L.dt_bias, L.a, act.decay, act.beta, rows, Hv,
+                                          stream),
+                 "DeltaNet gates");
+    launch_check(hipllm::launch_conv1d_silu(act.wide, qkv_w, L.history, L.conv, act.wide2, qkv_w, rows, qkv_w,
+                                            config.ssm_conv_kernel, stream),
+                 "DeltaNet conv");
+    // L2-normalise the Q and K heads (2 G vectors of S per row, contiguous).
+    launch_check(hipllm::launch_l2norm_heads(act.wide2, qkv_w, rows, 2 * G, S, eps, stream), "DeltaNet L2 norm");
+    launch_check(hipllm::launch_gdn_scan(act.wide2, act.wide2 + G * S, qkv_w, act.wide2 + 2 * G * S, qkv_w, act.decay,
+                                         act.beta, L.state, act.feat2, inner, rows, Hv, G, S, stream),
+                 "DeltaNet scan");
+    launch_check(hipllm::launch_gated_rmsnorm(act.feat2, inner, L.ssm_norm, act.feat, inner, act.gated, act.gated16,
+                                              inner, rows, Hv, S, eps, stream),
+                 "DeltaNet gated norm");
+    proj(L.ssm_out, act.gated, act.gated16, inner, rows, next, H, hidden);
+}
+
+// MoE FFN (moe_llm.mm:2642-2843): `hidden` is the attention residual; the
+// post-attention norm of it is in act.norm; next = hidden + routed + shared.
+void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden, float* next) {
+    const MoeLayer& L = layers[li];
+    std::int32_t* ids = route_ids + li * act_rows * K;
+    // Router logits and the shared-expert gate in one GEMV when packed.
+    const std::size_t ldr = E + 1;
+    if (L.fused_router) {
+        proj(L.router, act.norm, act.norm16, H, rows, act.rlog, ldr, nullptr, E + 1);
+    } else {
+        if (rows == 1) {
+            proj(L.router, act.norm, act.norm16, H, rows, act.rlog, ldr);
+            proj(L.shexp_router, act.norm, act.norm16, H, rows, act.rlog + E, ldr);
+        } else {
+            launch_check(hipllm::launch_gemv_batched(L.router.type, L.router.ptr, nullptr, L.router.row_bytes,
+                                                     act.norm, act.norm16, nullptr, nullptr, act.rlog, nullptr, E, H,
+                                                     rows, nullptr, 1, 1, 0, 0, H, ldr, stream),
+                         "router GEMV");
+            launch_check(hipllm::launch_gemv_batched(L.shexp_router.type, L.shexp_router.ptr, nullptr,
+                                                     L.shexp_router.row_bytes, act.norm, act.norm16, nullptr, nullptr,
+                                                     act.rlog + E, nullptr, 1, H, rows, nullptr, 1, 1, 0, 0, H, ldr,
+                                                     stream),
+                         "shared gate GEMV");
+        }
+    }
+    launch_check(hipllm::launch_router_topk(act.rlog, ldr, rows, E, K, ids, act.rweight, stream), "router top-k");
+    // Routed experts: gate/up + SwiGLU for every (row, route), then down.
+    launch_check(hipllm::launch_gemv_batched(L.gate_exps.type, L.gate_exps.ptr, L.up_exps.ptr, L.gate_exps.row_bytes,
+                                             act.norm, act.norm16, nullptr, nullptr, act.act, act.act16, FF, H,
+                                             rows * K, ids, E, K, L.gate_exps.expert_stride, 0, H, FF, stream),
+                 "expert gate/up");
+    launch_check(hipllm::launch_gemv_batched(L.down_exps.type, L.down_exps.ptr, nullptr, L.down_exps.row_bytes,
+                                             act.act, act.act16, nullptr, nullptr, act.down, nullptr, H, FF, rows * K,
+                                             ids, E, K, L.down_exps.expert_stride, 1, FF, H, stream),
+                 "expert down");
+    // Shared expert.
+    if (L.sh_gate.type == L.sh_up.type) {
+        launch_check(hipllm::launch_gemv_batched(L.sh_gate.type, L.sh_gate.ptr, L.sh_up.ptr, L.sh_gate.row_bytes,
+                                                 act.norm, act.norm16, nullptr, nullptr, act.sh_act, act.sh_act16, FFs,
+                                                 H, rows, nullptr, 1, 1, 0, 0, H, FFs, stream),
+                     "shared gate/up");
+    } else {
+        proj(L.sh_gate, act.norm, act.norm16, H, rows, act.sh_down, FFs);
+        proj(L.sh_up, act.norm, act.norm16, H, rows, act.sh_act, FFs);
+        launch_check(hipllm::launch_swiglu(act.sh_down, act.sh_act, act.sh_act, act.sh_act16, rows * FFs, stream),
+                     "shared SwiGLU");
+    }
+    proj(L.sh_down, act.sh_act, act.sh_act16, FFs, rows, act.sh_down, H);
+    launch_check(hipllm::launch_moe_combine(hidden, act.down, act.rweight, act.sh_down, act.rlog + E, ldr, next, rows,
+                                            H, K, stream),
+                 "MoE combine");
+}
+
+void HipMoeLLM::Impl::forward(std::size_t rows, std::size_t pos0) {
+    const float eps = config.norm_epsilon;
+    float* h = act.hidden[0];
+    float* tmp = act.hidden[1];
+    launch_check(hipllm::launch_embed(embedding.type, embedding.ptr, embedding.row_bytes, act.ids, rows,
+                                      config.vocabulary_size, H, h, stream),
+                 "embedding");
+    for (std::size_t l = 0; l < layers.size(); ++l) {
+        const MoeLayer& L = layers[l];
+        launch_check(hipllm::launch_rmsnorm(h, L.attn_norm, act.norm, act.norm16, rows, H, eps, stream), "RMSNorm");
+        if (L.full) {
+            attention_layer(l, rows, pos0, h, tmp);
+        } else {
+            deltanet_layer(l, rows, h, tmp);
+        }
+        launch_check(hipllm::launch_rmsnorm(tmp, L.post_norm, act.norm, act.norm16, rows, H, eps, stream), "RMSNorm");
+        moe_layer(l, rows, tmp, h);
+    }
+    const float* last = h + (rows - 1) * H;
+    launch_check(hipllm::launch_rmsnorm(last, output_norm, act.norm, act.norm16, 1, H, eps, stream), "final RMSNorm");
+    launch_check(hipllm::launch_gemv_prepped(output.type, output.ptr, output.row_bytes, act.norm, act.norm16, nullptr,
+                                             nullptr, act.logits, config.vocabulary_size, H, 0, stream),
+                 "LM head");
+    launch_check(hipllm::launch_argmax(act.logits, config.vocabulary_size, act.token, act.argmax_scratch, stream),
+                 "argmax");
+    last_rows = rows;
+}
+
+std::int32_t HipMoeLLM::Impl::read_token() {
+    hip_check(hipMemcpyAsync(host_token, act.token, 4, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync(token)");
+    hip_check(hipStreamSynchronize(stream), "HIP MoE forward");
+    const std::uint32_t t = host_token[0];
+    if (t > static_cast<std::uint32_t>(std::numeric_limits<std::int32_t>::max())) {
+        throw std::overflow_error("generated token does not fit int32_t");
+    }
+    return static_cast<std::int32_t>(t);
+}
+
+HipMoeLLM::HipMoeLLM(const std::string& gguf_path, std::size_t max_sequence, int device,
+                     std::size_t expert_cache_count)
+    : impl_(std::make_unique<Impl>()) {
+    impl_->load(gguf_path, max_sequence, device, expert_cache_count);
+}
+
+HipMoeLLM::~HipMoeLLM() = default;
+HipMoeLLM::HipMoeLLM(HipMoeLLM&&) noexcept = default;
+HipMoeLLM& HipMoeLLM::operator=(HipMoeLLM&&) noexcept = default;
+
+void HipMoeLLM::reset() {
+    if (!impl_) throw std::runtime_error("MoE model is not initialized");
+    hip_check(hipSetDevice(impl_->device), "hipSetDevice");
+    impl_->zero_state();
+    impl_->sequence_length = 0;
+}
+
+std::int32_t HipMoeLLM::prefill(const std::vector<std::int32_t>& ids) {
+    if (!impl_) throw std::runtime_error("MoE model is not initialized");
+    Impl& m = *impl_;
+    if (ids.empty()) throw std::invalid_argument("MoE prefill requires at least one token");
+    if (m.sequence_length != 0) throw std::invalid_argument("MoE prefill requires an empty state; call reset first");
+    if (ids.size() > m.capacity) throw std::length_error("MoE prefill exceeds sequence capacity");
+    for (std::int32_t id : ids) {
+        if (id < 0 || static_cast<std::size_t>(id) >= m.config.vocabulary_size) {
+            throw std::out_of_range("MoE prefill token is outside vocabulary");
+        }
+    }
+    hip_check(hipSetDevice(m.device), "hipSetDevice");
+    const auto t0 = std::chrono::steady_clock::now();
+    m.ensure_rows(ids.size());
+    std::memcpy(m.host_ids, ids.data(), ids.size() * 4);
+    hip_check(hipMemcpyAsync(m.act.ids, m.host_ids, ids.size() * 4, hipMemcpyHostToDevice, m.stream),
+              "hipMemcpy(ids)");
+    m.forward(ids.size(), 0);
+    const std::int32_t token = m.read_token();
+    m.sequence_length = ids.size();
+    if (m.profile) {
+        const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        std::fprintf(m.profile, "prefill,%zu,%zu,%.6f\n", ids.size(), ids.size(), ms);
+    }
+    return token;
+}
+
+std::int32_t HipMoeLLM::decode(std::int32_t id) {
+    if (!impl_) throw std::runtime_error("MoE model is not initialized");
+    Impl& m = *impl_;
+    if (m.sequence_length == 0) throw std::invalid_argument("MoE decode requires a completed prefill");
+    if (m.sequence_length >= m.capacity) throw std::length_error("MoE decode exceeds sequence capacity");
+    if (id < 0 || static_cast<std::size_t>(id) >= m.config.vocabulary_size) {
+        throw std::out_of_range("MoE decode token is outside vocabulary");
+    }
+    hip_check(hipSetDevice(m.device), "hipSetDevice");
+    const auto t0 = std::chrono::steady_clock::now();
+    const std::size_t pos = m.sequence_length;
+    m.host_ids[0] = id;
+    hip_check(hipMemcpyAsync(m.act.ids, m.host_ids, 4, hipMemcpyHostToDevice, m.stream), "hipMemcpy(id)");
+    m.forward(1, pos);
+    const std::int32_t token = m.read_token();
+    m.sequence_length = pos + 1;
+    if (m.profile) {
+        const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        std::fprintf(m.profile, "decode,1,%zu,%.6f\n", pos + 1, ms);
+    }
+    return token;
+}
+
+void HipMoeLLM::enable_profiling(const std::string& csv_path, bool) {
+    if (!impl_) throw std::runtime_error("MoE model is not initialized");
+    disable_profiling();
+    impl_->profile = std::fopen(csv_path.c_str(), "w");
+    if (!impl_->profile) throw std::runtime_error("cannot open profile CSV: " + csv_path);
+    std::fprintf(impl_->profile, "phase,tokens,sequence,wall_ms\n");
+}
+
+void HipMoeLLM::disable_profiling() {
+    if (impl_ && impl_->profile) {
+        std::fclose(impl_->profile);
+        impl_->profile = nullptr;
+    }
+}
+
+const ModelConfig& HipMoeLLM::config() const {
+    if (!impl_) throw std::runtime_error("MoE model is not initialized");
+    return impl_->config;
+}
+
+std::size_t HipMoeLLM::position() const noexcept { return impl_ ? impl_->sequence_length : 0; }
+std::size_t HipMoeLLM::max_sequence() const noexcept { return impl_ ? impl_->capacity : 0; }
+bool HipMoeLLM::uses_gpu() const noexcept { return available(); }
+bool HipMoeLLM::available() const noexcept { return impl_ && impl_->weights.base() && impl_->stream; }
+std::size_t HipMoeLLM::expert_cache_count() const noexcept { return impl_ ? impl_->expert_cache : 0; }
+
+const std::string& HipMoeLLM::device_name() const noexcept {
+    static const std::string empty;
+    return impl_ ? impl_->device_name : empty;
+}
+
+MemoryStats HipMoeLLM::memory_stats() const noexcept {
+    if (!impl_) return {};
+    MemoryStats s;
+    s.weight_bytes = impl_->weight_bytes;
+    s.kv_cache_bytes = impl_->kv_cache_bytes;
+    s.recurrent_state_bytes = impl_->recurrent_bytes;
+    s.intermediate_bytes = impl_->act_bytes;
+    s.intermediate_is_estimate = false;
+    return s;
+}
+
+void HipMoeLLM::copy_last_logits(float* dst, std::size_t count) const {
+    if (!impl_) throw std::runtime_error("MoE model is not initialized");
+    if (count != impl_->config.vocabulary_size) throw std::invalid_argument("logits buffer must hold the vocabulary");
+    hip_check(hipStreamSynchronize(impl_->stream), "hipStreamSynchronize");
+    hip_check(hipMemcpy(dst, impl_->act.logits, count * 4, hipMemcpyDeviceToHost), "hipMemcpy(logits)");
+}
+
+void HipMoeLLM::copy_last_routes(std::int32_t* dst, std::size_t count) const {
+    if (!impl_) throw std::runtime_error("MoE model is not initialized");
+    const Impl& m = *impl_;
+    if (count != m.layers.size() * m.K) throw std::invalid_argument("routes buffer must hold layers x top-k ids");
+    if (m.last_rows == 0) throw std::invalid_argument("no forward has run");
+    hip_check(hipStreamSynchronize(m.stream), "hipStreamSynchronize");
+    for (std::size_t l = 0; l < m.layers.size(); ++l) {
+        hip_check(hipMemcpy(dst + l * m.K, m.route_ids + (l * m.act_rows + m.last_rows - 1) * m.K, m.K * 4,
+                            hipMemcpyDeviceToHost),
+                  "hipMemcpy(routes)");
+    }
+}
+
+}  // namespace llm

@@ -17,6 +17,7 @@
 #include <cstring>
 #include <functional>
 #include <stdexcept>
+#include <cmath>
 #include <string>
 #include <thread>
 #include <vector>
@@ -39,7 +40,17 @@ uint64_t fnv1a(const std::string& s) {
     return h;
 }
 
-enum class Fill { Normal, Ones, Bias };
+// Normal: N(0, stddev); Ones: 1.0; Bias: N(0, bias_stddev) (the second
+// scale); Small: N(0, small_stddev); Conv: N(0, conv_stddev); NegDecay:
+// -(0.25 + 0.5 |N(0, 1)|), a negative DeltaNet A per value head.
+enum class Fill { Normal, Ones, Bias, Small, Conv, NegDecay };
+
+struct Scales {
+    float stddev = 0.02f;
+    float bias = 0.02f;
+    float small = 0.02f;
+    float conv = 0.3f;
+};
 
 struct TensorPlan {
     std::string name;
@@ -109,15 +120,17 @@ private:
 };
 
 void add_tensor(std::vector<TensorPlan>& plan, const std::string& name, size_t rows,
-                size_t cols, uint32_t type, Fill fill, bool vector_shape) {
+                size_t cols, uint32_t type, Fill fill, bool vector_shape, size_t experts = 0) {
     TensorPlan t;
     t.name = name;
-    t.rows = rows;
+    t.rows = experts ? rows * experts : rows;
     t.cols = cols;
     t.type = type;
     t.fill = fill;
-    t.dims = vector_shape ? std::vector<uint64_t>{cols} : std::vector<uint64_t>{cols, rows};
-    t.bytes = row_bytes(type, cols) * rows;
+    t.dims = vector_shape ? std::vector<uint64_t>{cols}
+             : experts   ? std::vector<uint64_t>{cols, rows, experts}
+                         : std::vector<uint64_t>{cols, rows};
+    t.bytes = row_bytes(type, cols) * t.rows;
     if (t.bytes == 0) {
         throw std::runtime_error("tensor " + name + ": type " + std::to_string(type) +
                                  " cannot hold rows of " + std::to_string(cols));
@@ -126,8 +139,7 @@ void add_tensor(std::vector<TensorPlan>& plan, const std::string& name, size_t r
 }
 
 void write_model(const std::string& path, const std::vector<KvEntry>& kvs,
-                 std::vector<TensorPlan>& plan, uint64_t seed, float stddev,
-                 float bias_stddev, unsigned threads) {
+                 std::vector<TensorPlan>& plan, uint64_t seed, const Scales& sc, unsigned threads) {
     uint64_t offset = 0;
     for (TensorPlan& t : plan) {
         offset = (offset + kAlignment - 1) / kAlignment * kAlignment;
@@ -181,10 +193,20 @@ void write_model(const std::string& path, const std::vector<KvEntry>& kvs,
                         std::fill(row.begin(), row.end(), 1.0f);
                         break;
                     case Fill::Normal:
-                        fill_normal(seed, stream, uint64_t(global_row) * t.cols, t.cols, stddev, row.data());
+                        fill_normal(seed, stream, uint64_t(global_row) * t.cols, t.cols, sc.stddev, row.data());
                         break;
                     case Fill::Bias:
-                        fill_normal(seed, stream, uint64_t(global_row) * t.cols, t.cols, bias_stddev, row.data());
+                        fill_normal(seed, stream, uint64_t(global_row) * t.cols, t.cols, sc.bias, row.data());
+                        break;
+                    case Fill::Small:
+                        fill_normal(seed, stream, uint64_t(global_row) * t.cols, t.cols, sc.small, row.data());
+                        break;
+                    case Fill::Conv:
+                        fill_normal(seed, stream, uint64_t(global_row) * t.cols, t.cols, sc.conv, row.data());
+                        break;
+                    case Fill::NegDecay:
+                        fill_normal(seed, stream, uint64_t(global_row) * t.cols, t.cols, 1.0f, row.data());
+                        for (float& v : row) v = -(0.25f + 0.5f * std::fabs(v));
                         break;
                     }
                     if (!quantize_row(t.type, row.data(), t.cols, chunk.data() + r * rb)) {
@@ -265,7 +287,100 @@ void write_qwen2(const std::string& path, const Qwen2Spec& s) {
         add_tensor(plan, p + "ffn_up.weight", s.ffn, s.hidden, s.type_ffn_gate_up, Fill::Normal, false);
         add_tensor(plan, p + "ffn_down.weight", s.hidden, s.ffn, s.type_ffn_down, Fill::Normal, false);
     }
-    write_model(path, kvs, plan, s.seed, s.stddev, s.bias_stddev, s.threads);
+    Scales sc;
+    sc.stddev = s.stddev;
+    sc.bias = s.bias_stddev;
+    write_model(path, kvs, plan, s.seed, sc, s.threads);
+}
+
+void write_qwen35moe(const std::string& path, const Qwen35MoeSpec& s) {
+    if (s.layers == 0 || s.hidden == 0 || s.heads == 0 || s.kv_heads == 0 || s.head_dim == 0 || s.vocab == 0 ||
+        s.context == 0 || s.experts == 0 || s.experts_used == 0 || s.experts_used > s.experts ||
+        s.expert_ffn == 0 || s.shared_ffn == 0 || s.full_attention_interval == 0 || s.conv_kernel == 0 ||
+        s.state_size == 0 || s.group_count == 0 || s.time_step_rank == 0) {
+        throw std::invalid_argument("qwen35moe spec has a zero or inconsistent dimension");
+    }
+    if (s.heads % s.kv_heads != 0 || s.time_step_rank % s.group_count != 0 || s.rotary_dim > s.head_dim ||
+        s.rotary_dim % 2 != 0) {
+        throw std::invalid_argument("qwen35moe head counts do not divide");
+    }
+    const uint32_t inner = s.time_step_rank * s.state_size;
+    const uint32_t qkv_w = 2 * s.group_count * s.state_size + inner;
+    const uint32_t q_w = s.heads * s.head_dim;
+    const uint32_t kv_w = s.kv_heads * s.head_dim;
+    std::vector<KvEntry> kvs;
+    auto kv_u32 = [&](const std::string& k, uint32_t v) { kvs.push_back({k, kKvU32, v, 0, {}}); };
+    auto kv_f32 = [&](const std::string& k, float v) { kvs.push_back({k, kKvF32, 0, v, {}}); };
+    const std::string a = "qwen35moe.";
+    kvs.push_back({"general.architecture", kKvString, 0, 0, "qwen35moe"});
+    kv_u32("general.alignment", kAlignment);
+    kv_u32(a + "block_count", s.layers);
+    kv_u32(a + "nextn_predict_layers", 0);
+    kv_u32(a + "embedding_length", s.hidden);
+    kv_u32(a + "attention.head_count", s.heads);
+    kv_u32(a + "attention.head_count_kv", s.kv_heads);
+    kv_u32(a + "attention.key_length", s.head_dim);
+    kv_u32(a + "attention.value_length", s.head_dim);
+    kv_u32(a + "context_length", s.context);
+    kv_u32(a + "expert_count", s.experts);
+    kv_u32(a + "expert_used_count", s.experts_used);
+    kv_u32(a + "expert_feed_forward_length", s.expert_ffn);
+    kv_u32(a + "expert_shared_feed_forward_length", s.shared_ffn);
+    kv_u32(a + "full_attention_interval", s.full_attention_interval);
+    kv_u32(a + "ssm.conv_kernel", s.conv_kernel);
+    kv_u32(a + "ssm.state_size", s.state_size);
+    kv_u32(a + "ssm.group_count", s.group_count);
+    kv_u32(a + "ssm.time_step_rank", s.time_step_rank);
+    kv_u32(a + "ssm.inner_size", inner);
+    kv_u32(a + "rope.dimension_count", s.rotary_dim);
+    kv_f32(a + "rope.freq_base", s.rope_theta);
+    kv_f32(a + "attention.layer_norm_rms_epsilon", s.norm_eps);
+    kv_u32("tokenizer.ggml.eos_token_id", s.eos_token_id);
+    kv_u32("tokenizer.ggml.tokens_count", s.vocab);
+
+    std::vector<TensorPlan> plan;
+    add_tensor(plan, "token_embd.weight", s.vocab, s.hidden, s.type_embd, Fill::Normal, false);
+    add_tensor(plan, "output_norm.weight", 1, s.hidden, kTypeF32, Fill::Ones, true);
+    add_tensor(plan, "output.weight", s.vocab, s.hidden, s.type_output, Fill::Normal, false);
+    for (uint32_t i = 0; i < s.layers; ++i) {
+        const std::string p = "blk." + std::to_string(i) + ".";
+        add_tensor(plan, p + "attn_norm.weight", 1, s.hidden, kTypeF32, Fill::Ones, true);
+        add_tensor(plan, p + "post_attention_norm.weight", 1, s.hidden, kTypeF32, Fill::Ones, true);
+        if ((i + 1) % s.full_attention_interval == 0) {
+            add_tensor(plan, p + "attn_q.weight", 2 * q_w, s.hidden, s.type_attn_qgate, Fill::Normal, false);
+            add_tensor(plan, p + "attn_k.weight", kv_w, s.hidden, s.type_attn_kv, Fill::Normal, false);
+            add_tensor(plan, p + "attn_v.weight", kv_w, s.hidden, s.type_attn_kv, Fill::Normal, false);
+            add_tensor(plan, p + "attn_q_norm.weight", 1, s.head_dim, kTypeF32, Fill::Ones, true);
+            add_tensor(plan, p + "attn_k_norm.weight", 1, s.head_dim, kTypeF32, Fill::Ones, true);
+            add_tensor(plan, p + "attn_output.weight", s.hidden, q_w, s.type_attn_out, Fill::Normal, false);
+        } else {
+            add_tensor(plan, p + "attn_qkv.weight", qkv_w, s.hidden, s.type_ssm_qkv, Fill::Normal, false);
+            add_tensor(plan, p + "attn_gate.weight", inner, s.hidden, s.type_ssm_gate, Fill::Normal, false);
+            add_tensor(plan, p + "ssm_alpha.weight", s.time_step_rank, s.hidden, kTypeF32, Fill::Small, false);
+            add_tensor(plan, p + "ssm_beta.weight", s.time_step_rank, s.hidden, kTypeF32, Fill::Small, false);
+            add_tensor(plan, p + "ssm_conv1d.weight", qkv_w, s.conv_kernel, kTypeF32, Fill::Conv, false);
+            add_tensor(plan, p + "ssm_dt.bias", 1, s.time_step_rank, kTypeF32, Fill::Small, true);
+            add_tensor(plan, p + "ssm_a", 1, s.time_step_rank, kTypeF32, Fill::NegDecay, true);
+            add_tensor(plan, p + "ssm_norm.weight", 1, s.state_size, kTypeF32, Fill::Ones, true);
+            add_tensor(plan, p + "ssm_out.weight", s.hidden, inner, s.type_ssm_out, Fill::Normal, false);
+        }
+        add_tensor(plan, p + "ffn_gate_inp.weight", s.experts, s.hidden, kTypeF32, Fill::Small, false);
+        add_tensor(plan, p + "ffn_gate_exps.weight", s.expert_ffn, s.hidden, s.type_expert_gate_up, Fill::Normal,
+                   false, s.experts);
+        add_tensor(plan, p + "ffn_up_exps.weight", s.expert_ffn, s.hidden, s.type_expert_gate_up, Fill::Normal,
+                   false, s.experts);
+        add_tensor(plan, p + "ffn_down_exps.weight", s.hidden, s.expert_ffn, s.type_expert_down, Fill::Normal, false,
+                   s.experts);
+        add_tensor(plan, p + "ffn_gate_inp_shexp.weight", 1, s.hidden, kTypeF32, Fill::Small, true);
+        add_tensor(plan, p + "ffn_gate_shexp.weight", s.shared_ffn, s.hidden, s.type_shared, Fill::Normal, false);
+        add_tensor(plan, p + "ffn_up_shexp.weight", s.shared_ffn, s.hidden, s.type_shared, Fill::Normal, false);
+        add_tensor(plan, p + "ffn_down_shexp.weight", s.hidden, s.shared_ffn, s.type_shared, Fill::Normal, false);
+    }
+    Scales sc;
+    sc.stddev = s.stddev;
+    sc.small = s.small_stddev;
+    sc.conv = s.conv_stddev;
+    write_model(path, kvs, plan, s.seed, sc, s.threads);
 }
 
 }  // namespace hipllm_tools

@@ -75,3 +75,18 @@ extern "C" int hipllm_tools_write_qwen2(const char* path, const HipllmQwen2Spec*
         return -1;
     }
 }
+
+extern "C" int hipllm_tools_write_qwen35moe(const char* path, const HipllmQwen35MoeSpec* spec,
+                                            char* err, size_t errlen) {
+    try {
+        if (path == nullptr || spec == nullptr) throw std::invalid_argument("null argument");
+        static_assert(sizeof(HipllmQwen35MoeSpec) == sizeof(hipllm_tools::Qwen35MoeSpec), "spec layout");
+        hipllm_tools::Qwen35MoeSpec s;
+        std::memcpy(&s, spec, sizeof(s));
+        hipllm_tools::write_qwen35moe(path, s);
+        return 0;
+    } catch (const std::exception& e) {
+        copy_error(e.what(), err, errlen);
+        return -1;
+    }
+}

@@ -42,7 +42,11 @@ class HipllmConfig(ctypes.Structure):
         "kv_head_count", "head_size", "rotary_dimension", "vocabulary_size", "context_length",
         "parameter_count", "stored_weight_bytes")] + [
         ("eos_token_id", ctypes.c_int32), ("rope_theta", ctypes.c_float),
-        ("norm_epsilon", ctypes.c_float), ("architecture", ctypes.c_char * 32)]
+        ("norm_epsilon", ctypes.c_float), ("architecture", ctypes.c_char * 32)] + [
+        (n, ctypes.c_uint64) for n in (
+            "full_attention_interval", "expert_count", "expert_used_count", "expert_feed_forward_size",
+            "shared_expert_feed_forward_size", "ssm_conv_kernel", "ssm_state_size", "ssm_group_count",
+            "ssm_time_step_rank", "ssm_inner_size")]
 
 
 class HipllmMemoryStats(ctypes.Structure):
@@ -80,6 +84,21 @@ SIGNATURES = {
     "hipllm_argmax": (_I, [_P, _S, _P, _P, _P]),
     "hipllm_swiglu": (_I, [_P, _P, _P, _P, _S, _P]),
     "hipllm_create": (_I, [ctypes.c_char_p, _S, _I, ctypes.POINTER(_P)]),
+    "hipllm_create_ex": (_I, [ctypes.c_char_p, _S, _I, _S, ctypes.POINTER(_P)]),
+    "hipllm_copy_routes": (_I, [_P, _P, _S]),
+    "hipllm_expert_cache_count": (_S, [_P]),
+    "hipllm_attn_prefill": (_I, [_P, _S, _P, _P, _P, _S, _S, _S, _S, _S, _S, _F, _P]),
+    "hipllm_gemv_batched": (_I, [_U32, _P, _P, _S, _P, _P, _P, _P, _P, _P, _S, _S, _S, _P, _S, _S, _S, _I, _S, _S,
+                                 _P]),
+    "hipllm_router_topk": (_I, [_P, _S, _S, _S, _S, _P, _P, _P]),
+    "hipllm_moe_combine": (_I, [_P, _P, _P, _P, _P, _S, _P, _S, _S, _S, _P]),
+    "hipllm_gdn_gates": (_I, [_P, _P, _S, _P, _P, _P, _P, _S, _S, _P]),
+    "hipllm_conv1d_silu": (_I, [_P, _S, _P, _P, _P, _S, _S, _S, _S, _P]),
+    "hipllm_l2norm_heads": (_I, [_P, _S, _S, _S, _S, _F, _P]),
+    "hipllm_gdn_scan": (_I, [_P, _P, _S, _P, _S, _P, _P, _P, _P, _S, _S, _S, _S, _S, _P]),
+    "hipllm_gated_rmsnorm": (_I, [_P, _S, _P, _P, _S, _P, _P, _S, _S, _S, _S, _F, _P]),
+    "hipllm_split_qgate_norm": (_I, [_P, _S, _P, _S, _P, _P, _P, _S, _P, _S, _S, _S, _S, _S, _F, _P]),
+    "hipllm_gate_mul": (_I, [_P, _P, _P, _P, _S, _P]),
     "hipllm_destroy": (None, [_P]),
     "hipllm_reset": (_I, [_P]),
     "hipllm_prefill": (_I, [_P, _P, _S, ctypes.POINTER(_I32)]),
@@ -136,9 +155,10 @@ def inspect_gguf(path) -> dict:
 class HipLLM:
     """The MI355X qwen2 backend, same contract as the reference's MetalLLM."""
 
-    def __init__(self, gguf_path, max_sequence: int = 0, device: int = -1):
+    def __init__(self, gguf_path, max_sequence: int = 0, device: int = -1, expert_cache_count: int = 8):
         self._h = _P()
-        check(lib().hipllm_create(str(gguf_path).encode(), max_sequence, device, ctypes.byref(self._h)))
+        check(lib().hipllm_create_ex(str(gguf_path).encode(), max_sequence, device, expert_cache_count,
+                                     ctypes.byref(self._h)))
         cfg = HipllmConfig()
         check(lib().hipllm_config(self._h, ctypes.byref(cfg)))
         self.config = _config_dict(cfg)
@@ -208,6 +228,18 @@ class HipLLM:
 
     def set_batched_prefill(self, enabled: bool) -> None:
         check(lib().hipllm_set_batched_prefill(self._h, 1 if enabled else 0))
+
+    def routes(self) -> np.ndarray:
+        """qwen35moe: expert ids of the last row of the last forward, [layers, top-k]."""
+        L = self.config["layer_count"]
+        k = self.config["expert_used_count"]
+        out = np.empty((L, k), dtype=np.int32)
+        check(lib().hipllm_copy_routes(self._h, out.ctypes.data, out.size))
+        return out
+
+    @property
+    def expert_cache_count(self) -> int:
+        return lib().hipllm_expert_cache_count(self._h)
 
 
 def generate(backend, prompt, max_new_tokens: int, stop_token_ids=(), on_step=None):
@@ -287,6 +319,61 @@ def _k_gemm(qtype, w, row_bytes, x, ldx, bias, y, m, n, k, workspace, stream=Non
                             _ptr(workspace), _stream(stream)))
 
 
+def _k_attn_prefill(q, q_stride, kcache, vcache, out, out_stride, rows, hq, hkv, d, pos0, scale, stream=None):
+    check(lib().hipllm_attn_prefill(_ptr(q), q_stride, _ptr(kcache), _ptr(vcache), _ptr(out), out_stride, rows, hq,
+                                    hkv, d, pos0, scale, _stream(stream)))
+
+
+def _k_gemv_batched(qtype, w, wu, row_bytes, x, xs16, bias, residual, y, ys16, n, k, vectors, ids=None,
+                    experts=1, routes=1, expert_stride=0, x_routed=False, ldx=None, ldy=None, stream=None):
+    check(lib().hipllm_gemv_batched(qtype, _ptr(w), _ptr(wu), row_bytes, _ptr(x), _ptr(xs16), _ptr(bias),
+                                    _ptr(residual), _ptr(y), _ptr(ys16), n, k, vectors, _ptr(ids), experts, routes,
+                                    expert_stride, 1 if x_routed else 0, ldx or k, ldy or n, _stream(stream)))
+
+
+def _k_router_topk(logits, ld, tokens, experts, k, ids, weights, stream=None):
+    check(lib().hipllm_router_topk(_ptr(logits), ld, tokens, experts, k, _ptr(ids), _ptr(weights), _stream(stream)))
+
+
+def _k_moe_combine(residual, down, w, shared, sgate, ld_sgate, out, tokens, h, k, stream=None):
+    check(lib().hipllm_moe_combine(_ptr(residual), _ptr(down), _ptr(w), _ptr(shared), _ptr(sgate), ld_sgate,
+                                   _ptr(out), tokens, h, k, _stream(stream)))
+
+
+def _k_gdn_gates(alpha, beta_raw, ld, dt_bias, a, decay, beta, tokens, heads, stream=None):
+    check(lib().hipllm_gdn_gates(_ptr(alpha), _ptr(beta_raw), ld, _ptr(dt_bias), _ptr(a), _ptr(decay), _ptr(beta),
+                                 tokens, heads, _stream(stream)))
+
+
+def _k_conv1d_silu(x, ldx, history, w, out, ldo, tokens, channels, ksize, stream=None):
+    check(lib().hipllm_conv1d_silu(_ptr(x), ldx, _ptr(history), _ptr(w), _ptr(out), ldo, tokens, channels, ksize,
+                                   _stream(stream)))
+
+
+def _k_l2norm_heads(x, ld, tokens, heads, d, eps, stream=None):
+    check(lib().hipllm_l2norm_heads(_ptr(x), ld, tokens, heads, d, eps, _stream(stream)))
+
+
+def _k_gdn_scan(q, k, ldqk, v, ldv, decay, beta, state, out, ldo, tokens, value_heads, key_heads, d, stream=None):
+    check(lib().hipllm_gdn_scan(_ptr(q), _ptr(k), ldqk, _ptr(v), ldv, _ptr(decay), _ptr(beta), _ptr(state),
+                                _ptr(out), ldo, tokens, value_heads, key_heads, d, _stream(stream)))
+
+
+def _k_gated_rmsnorm(o, ldo, gamma, z, ldz, y, ys16, ldy, tokens, heads, d, eps, stream=None):
+    check(lib().hipllm_gated_rmsnorm(_ptr(o), ldo, _ptr(gamma), _ptr(z), ldz, _ptr(y), _ptr(ys16), ldy, tokens,
+                                     heads, d, eps, _stream(stream)))
+
+
+def _k_split_qgate_norm(mixed, ldm, kv, ldkv, q_gamma, k_gamma, qkv, ldqkv, gate, ldg, tokens, hq, hkv, d, eps,
+                        stream=None):
+    check(lib().hipllm_split_qgate_norm(_ptr(mixed), ldm, _ptr(kv), ldkv, _ptr(q_gamma), _ptr(k_gamma), _ptr(qkv),
+                                        ldqkv, _ptr(gate), ldg, tokens, hq, hkv, d, eps, _stream(stream)))
+
+
+def _k_gate_mul(a, g, y, y16, n, stream=None):
+    check(lib().hipllm_gate_mul(_ptr(a), _ptr(g), _ptr(y), _ptr(y16), n, _stream(stream)))
+
+
 def _k_rmsnorm(x, gamma, y, ys16, rows, cols, eps, stream=None):
     check(lib().hipllm_rmsnorm(_ptr(x), _ptr(gamma), _ptr(y), _ptr(ys16), rows, cols, eps, _stream(stream)))
 
@@ -318,7 +405,10 @@ kernels = types.SimpleNamespace(
     dequant_rows=_k_dequant_rows, prep_sums=_k_prep_sums, gemv=_k_gemv, gemv_prepped=_k_gemv_prepped,
     gemv_swiglu=_k_gemv_swiglu, to_bf16=_k_to_bf16, gemm_mfma=_k_gemm_mfma, gemm=_k_gemm,
     gemm_workspace_bytes=lambda m, k: lib().hipllm_gemm_workspace_bytes(m, k), rmsnorm=_k_rmsnorm, embed=_k_embed, rope_kv=_k_rope_kv,
-    attn_decode=_k_attn_decode, argmax=_k_argmax, swiglu=_k_swiglu,
+    attn_decode=_k_attn_decode, argmax=_k_argmax, swiglu=_k_swiglu, attn_prefill=_k_attn_prefill,
+    gemv_batched=_k_gemv_batched, router_topk=_k_router_topk, moe_combine=_k_moe_combine, gdn_gates=_k_gdn_gates,
+    conv1d_silu=_k_conv1d_silu, l2norm_heads=_k_l2norm_heads, gdn_scan=_k_gdn_scan, gated_rmsnorm=_k_gated_rmsnorm,
+    split_qgate_norm=_k_split_qgate_norm, gate_mul=_k_gate_mul,
     gemv_workspace_bytes=lambda k: lib().hipllm_gemv_workspace_bytes(k),
     attn_decode_scratch_floats=lambda hq, d, n: lib().hipllm_attn_decode_scratch_floats(hq, d, n),
     argmax_scratch_bytes=lambda n: lib().hipllm_argmax_scratch_bytes(n),

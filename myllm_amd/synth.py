@@ -73,6 +73,95 @@ SHAPES = {
 }
 
 
+class _MoeSpec(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "layers", "hidden", "heads", "kv_heads", "head_dim", "rotary_dim", "vocab", "context",
+        "eos_token_id")] + [("rope_theta", ctypes.c_float), ("norm_eps", ctypes.c_float)] + [
+        (n, ctypes.c_uint32) for n in (
+        "experts", "experts_used", "expert_ffn", "shared_ffn", "full_attention_interval",
+        "conv_kernel", "state_size", "group_count", "time_step_rank",
+        "type_embd", "type_output", "type_attn_qgate", "type_attn_kv", "type_attn_out",
+        "type_ssm_qkv", "type_ssm_gate", "type_ssm_out", "type_expert_gate_up",
+        "type_expert_down", "type_shared")] + [
+        ("seed", ctypes.c_uint64), ("stddev", ctypes.c_float), ("small_stddev", ctypes.c_float),
+        ("conv_stddev", ctypes.c_float), ("threads", ctypes.c_uint32)]
+
+
+@dataclasses.dataclass(frozen=True)
+class Qwen35MoeShape:
+    """Text-only Qwen3.5/3.6 MoE with Gated DeltaNet layers (qwen35moe)."""
+    name: str
+    layers: int
+    hidden: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    rotary_dim: int
+    vocab: int
+    context: int
+    experts: int
+    experts_used: int
+    expert_ffn: int
+    shared_ffn: int
+    full_attention_interval: int
+    conv_kernel: int
+    state_size: int
+    group_count: int
+    time_step_rank: int
+    rope_theta: float = 1e7
+    norm_eps: float = 1e-6
+    eos_token_id: int = 151645
+
+    @property
+    def inner(self) -> int:
+        return self.time_step_rank * self.state_size
+
+    @property
+    def qkv_width(self) -> int:
+        return 2 * self.group_count * self.state_size + self.inner
+
+
+MOE_SHAPES = {
+    # Small shape for CPU-checkable parity: 2 DeltaNet + 2 gated-attention layers.
+    "moe-tiny": Qwen35MoeShape("moe-tiny", 4, 256, 4, 2, 64, 16, 512, 256, 16, 4, 256, 256, 2, 4, 64, 2, 4,
+                               eos_token_id=511),
+    # Qwen3.5/3.6-35B-A3B widths with the first 4 layers (3 DeltaNet : 1 attention).
+    "qwen3.5-35b-a3b-4l": Qwen35MoeShape("qwen3.5-35b-a3b-4l", 4, 2048, 16, 2, 256, 64, 151936, 4096, 256, 8, 512,
+                                         512, 4, 4, 128, 16, 32),
+    # The full 40-layer Qwen3.5/3.6-35B-A3B text shape.
+    "qwen3.5-35b-a3b": Qwen35MoeShape("qwen3.5-35b-a3b", 40, 2048, 16, 2, 256, 64, 151936, 4096, 256, 8, 512,
+                                      512, 4, 4, 128, 16, 32),
+}
+
+MOE_TYPES = dict(type_embd=Q8_0, type_output=Q6_K, type_attn_qgate=Q4_K, type_attn_kv=Q8_0,
+                 type_attn_out=Q4_K, type_ssm_qkv=Q6_K, type_ssm_gate=Q4_K, type_ssm_out=Q4_K,
+                 type_expert_gate_up=Q4_K, type_expert_down=Q6_K, type_shared=Q8_0)
+
+
+def write_qwen35moe(path, shape: Qwen35MoeShape, seed: int = 0, stddev: float = 0.02,
+                    small_stddev: float = 0.02, conv_stddev: float = 0.3, types: dict | None = None,
+                    threads: int | None = None) -> pathlib.Path:
+    """Writes a synthetic qwen35moe GGUF (Q4_K experts, Q6_K expert down
+    projections) and returns its path."""
+    t = dict(MOE_TYPES, **(types or {}))
+    if threads is None:
+        threads = min(16, os.cpu_count() or 1)
+    spec = _MoeSpec(shape.layers, shape.hidden, shape.heads, shape.kv_heads, shape.head_dim, shape.rotary_dim,
+                    shape.vocab, shape.context, shape.eos_token_id, shape.rope_theta, shape.norm_eps,
+                    shape.experts, shape.experts_used, shape.expert_ffn, shape.shared_ffn,
+                    shape.full_attention_interval, shape.conv_kernel, shape.state_size, shape.group_count,
+                    shape.time_step_rank, t["type_embd"], t["type_output"], t["type_attn_qgate"],
+                    t["type_attn_kv"], t["type_attn_out"], t["type_ssm_qkv"], t["type_ssm_gate"],
+                    t["type_ssm_out"], t["type_expert_gate_up"], t["type_expert_down"], t["type_shared"],
+                    seed, stddev, small_stddev, conv_stddev, threads)
+    err = ctypes.create_string_buffer(512)
+    path = pathlib.Path(path)
+    rc = _native.tools().hipllm_tools_write_qwen35moe(str(path).encode(), ctypes.byref(spec), err, 512)
+    if rc != 0:
+        raise RuntimeError(f"synthetic qwen35moe writer failed: {err.value.decode()}")
+    return path
+
+
 def fallback_type(qtype: int, cols: int) -> int:
     """The Q4_K_M fallback for rows that are not a multiple of 256."""
     if cols % BLOCK[qtype] == 0:

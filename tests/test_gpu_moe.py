@@ -1,0 +1,338 @@
+"""qwen35moe parity on the GPU: every HipMoeLLM kernel against the float64
+host reference (oracle/moe_ref.py, itself pinned by tests/test_moe_ref.py),
+then whole models through the C ABI handle API.
+
+Bars: router ids exact (ties to the lower id) and weights <= 1e-5; FP32
+kernels <= 1e-4 relative to float64 (GEMVs <= 1e-3, the FP32 GEMV bound);
+end to end: identical greedy tokens, identical expert routes at every layer
+and step, logits within max|l - ref| / max|ref| <= 1e-3.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from myllm_amd import synth
+from myllm_amd.hipllm import HipLLM, LengthError, generate, kernels
+from oracle import moe_ref
+from tests.test_gpu_kernels import dev_bytes, random_rows, rel_err
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+def t32(a, cuda):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(cuda)
+
+
+# ------------------------------------------------------------ router
+def test_router_topk_ties_and_weights(cuda):
+    rng = np.random.default_rng(0)
+    T, E, k = 6, 256, 8
+    logits = rng.normal(size=(T, E + 1)).astype(np.float32)
+    logits[1, [3, 9, 200]] = 5.0          # a three-way tie at the top
+    logits[2, :] = 0.5                    # all equal: ids 0..7
+    logits[3, [10, 11]] = logits[3].max() + 1.0
+    ids = torch.empty(T, k, dtype=torch.int32, device=cuda)
+    w = torch.empty(T, k, device=cuda)
+    kernels.router_topk(t32(logits, cuda), E + 1, T, E, k, ids, w)
+    for t in range(T):
+        p = moe_ref.softmax(logits[t, :E].astype(np.float64))
+        ri, rv = moe_ref.topk_insertion(p, k)
+        assert ids[t].cpu().numpy().tolist() == ri.tolist(), t
+        assert rel_err(w[t].cpu().numpy(), moe_ref.renorm(rv)) <= 1e-5
+    assert ids[2].cpu().numpy().tolist() == list(range(8))
+
+
+# ------------------------------------------------------------ batched / expert GEMV
+@pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q6_K])
+def test_expert_gemv_routed(cuda, qtype):
+    E, n, kdim, T, routes = 8, 96, 512, 3, 4
+    w = random_rows(qtype, E * n, kdim, 41)
+    dw = dev_bytes(w, cuda)
+    rb = w.shape[1]
+    wf = torch.empty(E * n, kdim, device=cuda)
+    kernels.dequant_rows(qtype, dw, rb, E * n, kdim, wf)
+    wf = wf.double().cpu().numpy().reshape(E, n, kdim)
+    ids_np = np.array([[5, 0, 7, 2], [1, 1, 3, 6], [7, 4, 0, 5]], dtype=np.int32)
+    # x per token (x_routed = False) and per route (x_routed = True)
+    for routed in (False, True):
+        rows = T * routes if routed else T
+        x = synth.normal(rows * kdim, 42 + routed).reshape(rows, kdim)
+        dx = t32(x, cuda)
+        xs = torch.empty(rows, kdim // 16, device=cuda)
+        for r in range(rows):
+            kernels.prep_sums(dx[r], xs[r], kdim)
+        y = torch.empty(T * routes, n, device=cuda)
+        kernels.gemv_batched(qtype, dw, None, rb, dx, xs, None, None, y, None, n, kdim, T * routes,
+                             ids=torch.from_numpy(ids_np.reshape(-1).copy()).to(cuda), experts=E, routes=routes,
+                             expert_stride=n * rb, x_routed=routed, ldx=kdim, ldy=n)
+        got = y.double().cpu().numpy()
+        for j in range(T * routes):
+            e = ids_np.reshape(-1)[j]
+            xr = x[j] if routed else x[j // routes]
+            assert rel_err(got[j], wf[e] @ xr.astype(np.float64)) <= 1e-3, (routed, j)
+
+
+@pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q8_0, synth.F32])
+def test_batched_rows_and_swiglu(cuda, qtype):
+    T, n, kdim = 5, 128, 512
+    wg, wu = random_rows(qtype, n, kdim, 51), random_rows(qtype, n, kdim, 52)
+    dg, du = dev_bytes(wg, cuda), dev_bytes(wu, cuda)
+    rb = wg.shape[1]
+    x = synth.normal(T * kdim, 53).reshape(T, kdim)
+    dx = t32(x, cuda)
+    xs = torch.empty(T, kdim // 16, device=cuda)
+    for r in range(T):
+        kernels.prep_sums(dx[r], xs[r], kdim)
+    res = synth.normal(T * n, 54).reshape(T, n)
+    y = torch.empty(T, n, device=cuda)
+    kernels.gemv_batched(qtype, dg, None, rb, dx, xs, None, t32(res, cuda), y, None, n, kdim, T)
+    G = torch.empty(n, kdim, device=cuda)
+    U = torch.empty(n, kdim, device=cuda)
+    kernels.dequant_rows(qtype, dg, rb, n, kdim, G)
+    kernels.dequant_rows(qtype, du, rb, n, kdim, U)
+    G, U = G.double().cpu().numpy(), U.double().cpu().numpy()
+    ref = x.astype(np.float64) @ G.T + res
+    assert rel_err(y.cpu().numpy(), ref) <= 1e-3
+    ys16 = torch.empty(T, n // 16, device=cuda)
+    kernels.gemv_batched(qtype, dg, du, rb, dx, xs, None, None, y, ys16, n, kdim, T)
+    g, u = x.astype(np.float64) @ G.T, x.astype(np.float64) @ U.T
+    ref = moe_ref.silu(g) * u
+    got = y.double().cpu().numpy()
+    assert rel_err(got, ref) <= 1e-3
+    assert rel_err(ys16.cpu().numpy(), got.reshape(T, -1, 16).sum(axis=2)) <= 1e-5
+
+
+# ------------------------------------------------------------ DeltaNet pieces
+def test_gdn_gates(cuda):
+    rng = np.random.default_rng(3)
+    T, Hv = 4, 32
+    ab = rng.normal(scale=5.0, size=(T, 2 * Hv)).astype(np.float32)
+    ab[0, :4] = [25.0, -25.0, 20.5, -19.5]  # softplus branches
+    dt = rng.normal(size=Hv).astype(np.float32)
+    a = -np.abs(rng.normal(size=Hv)).astype(np.float32)
+    decay, beta = torch.empty(T, Hv, device=cuda), torch.empty(T, Hv, device=cuda)
+    dab = t32(ab, cuda)
+    kernels.gdn_gates(dab, dab[:, Hv:], 2 * Hv, t32(dt, cuda), t32(a, cuda), decay, beta, T, Hv)
+    ref_d = np.exp(moe_ref.softplus(ab[:, :Hv].astype(np.float64) + dt) * a)
+    ref_b = moe_ref.sigmoid(ab[:, Hv:])
+    assert rel_err(decay.cpu().numpy(), ref_d) <= 1e-5
+    assert rel_err(beta.cpu().numpy(), ref_b) <= 1e-5
+
+
+@pytest.mark.parametrize("ksize", [2, 4])
+def test_conv1d_silu_and_history(cuda, ksize):
+    rng = np.random.default_rng(4)
+    T, C = 7, 300
+    x = rng.normal(size=(T, C)).astype(np.float32)
+    hist = rng.normal(size=(ksize - 1, C)).astype(np.float32)
+    w = rng.normal(size=(C, ksize)).astype(np.float32)
+    dh = t32(hist, cuda)
+    out = torch.empty(T, C, device=cuda)
+    kernels.conv1d_silu(t32(x, cuda), C, dh, t32(w, cuda), out, C, T, C, ksize)
+    h = hist.astype(np.float64)
+    ref = np.empty((T, C))
+    for t in range(T):
+        o, h = moe_ref.conv_step(h, x[t].astype(np.float64), w.astype(np.float64))
+        ref[t] = moe_ref.silu(o)
+    assert rel_err(out.cpu().numpy(), ref) <= 1e-5
+    np.testing.assert_array_equal(dh.cpu().numpy(), h.astype(np.float32))
+
+
+def test_l2norm_heads(cuda):
+    rng = np.random.default_rng(5)
+    T, heads, d, ld = 3, 6, 128, 900
+    x = rng.normal(size=(T, ld)).astype(np.float32)
+    dx = t32(x, cuda)
+    kernels.l2norm_heads(dx, ld, T, heads, d, 1e-6)
+    got = dx.cpu().numpy()
+    ref = moe_ref.l2norm(x[:, :heads * d].reshape(T, heads, d), 1e-6).reshape(T, -1)
+    assert rel_err(got[:, :heads * d], ref) <= 1e-5
+    np.testing.assert_array_equal(got[:, heads * d:], x[:, heads * d:])
+
+
+@pytest.mark.parametrize("d,Hv,G", [(128, 32, 16), (64, 4, 2)])
+def test_gdn_scan_matches_float64_steps(cuda, d, Hv, G):
+    rng = np.random.default_rng(6)
+    T = 9
+    qk = rng.normal(size=(T, 2, G, d))
+    qk = qk / np.linalg.norm(qk, axis=-1, keepdims=True)
+    v = rng.normal(size=(T, Hv, d))
+    decay = rng.uniform(0.3, 1.0, size=(T, Hv))
+    beta = rng.uniform(0.0, 1.0, size=(T, Hv))
+    S0 = rng.normal(scale=0.1, size=(Hv, d, d))
+    ldqk = 2 * G * d + Hv * d
+    buf = np.concatenate([qk.reshape(T, -1), v.reshape(T, -1)], axis=1)
+    dbuf = t32(buf, cuda)
+    state = t32(S0, cuda)
+    out = torch.empty(T, Hv * d, device=cuda)
+    kernels.gdn_scan(dbuf, dbuf[:, G * d:], ldqk, dbuf[:, 2 * G * d:], ldqk, t32(decay, cuda), t32(beta, cuda),
+                     state, out, Hv * d, T, Hv, G, d)
+    S = S0.astype(np.float32).astype(np.float64)
+    ref = np.empty((T, Hv, d))
+    f = lambda a: a.astype(np.float32).astype(np.float64)
+    for t in range(T):
+        S, ref[t] = moe_ref.gdn_step(S, f(qk[t, 0]), f(qk[t, 1]), f(v[t]), f(decay[t]), f(beta[t]), G)
+    assert rel_err(out.cpu().numpy(), ref.reshape(T, -1)) <= 1e-4
+    assert rel_err(state.cpu().numpy(), S) <= 1e-4
+
+
+def test_gated_rmsnorm(cuda):
+    rng = np.random.default_rng(7)
+    T, Hv, d = 3, 8, 128
+    o = rng.normal(size=(T, Hv * d)).astype(np.float32)
+    z = rng.normal(size=(T, Hv * d)).astype(np.float32)
+    g = rng.normal(size=d).astype(np.float32)
+    y = torch.empty(T, Hv * d, device=cuda)
+    y16 = torch.empty(T, Hv * d // 16, device=cuda)
+    kernels.gated_rmsnorm(t32(o, cuda), Hv * d, t32(g, cuda), t32(z, cuda), Hv * d, y, y16, Hv * d, T, Hv, d, 1e-6)
+    ref = (moe_ref.rmsnorm(o.reshape(T, Hv, d), g, 1e-6) * moe_ref.silu(z.reshape(T, Hv, d))).reshape(T, -1)
+    got = y.cpu().numpy()
+    assert rel_err(got, ref) <= 1e-5
+    assert rel_err(y16.cpu().numpy(), got.astype(np.float64).reshape(T, -1, 16).sum(axis=2)) <= 1e-5
+
+
+# ------------------------------------------------------------ attention pieces
+def test_split_qgate_norm_and_gate_mul(cuda):
+    rng = np.random.default_rng(8)
+    T, Hq, Hkv, D = 2, 4, 2, 256
+    mixed = rng.normal(size=(T, Hq * 2 * D)).astype(np.float32)
+    kv = rng.normal(size=(T, 2 * Hkv * D)).astype(np.float32)
+    qg, kg = rng.normal(size=D).astype(np.float32), rng.normal(size=D).astype(np.float32)
+    ldqkv = (Hq + 2 * Hkv) * D
+    qkv = torch.zeros(T, ldqkv, device=cuda)
+    gate = torch.empty(T, Hq * D, device=cuda)
+    kernels.split_qgate_norm(t32(mixed, cuda), Hq * 2 * D, t32(kv, cuda), 2 * Hkv * D, t32(qg, cuda), t32(kg, cuda),
+                             qkv, ldqkv, gate, Hq * D, T, Hq, Hkv, D, 1e-6)
+    m = mixed.reshape(T, Hq, 2 * D).astype(np.float64)
+    ref_q = moe_ref.rmsnorm(m[:, :, :D], qg, 1e-6).reshape(T, -1)
+    ref_k = moe_ref.rmsnorm(kv[:, :Hkv * D].reshape(T, Hkv, D), kg, 1e-6).reshape(T, -1)
+    got = qkv.cpu().numpy()
+    assert rel_err(got[:, :Hq * D], ref_q) <= 1e-5
+    assert rel_err(got[:, Hq * D:(Hq + Hkv) * D], ref_k) <= 1e-5
+    np.testing.assert_array_equal(got[:, (Hq + Hkv) * D:], kv[:, Hkv * D:])
+    np.testing.assert_array_equal(gate.cpu().numpy(), m[:, :, D:].reshape(T, -1).astype(np.float32))
+    a = torch.randn(T, Hq * D, device=cuda)
+    y = torch.empty_like(a)
+    y16 = torch.empty(T * Hq * D // 16, device=cuda)
+    kernels.gate_mul(a, gate, y, y16, T * Hq * D)
+    ref = a.double().cpu().numpy() * moe_ref.sigmoid(gate.double().cpu().numpy())
+    assert rel_err(y.cpu().numpy(), ref) <= 1e-5
+
+
+def test_moe_combine(cuda):
+    rng = np.random.default_rng(9)
+    T, H, k, E = 3, 256, 4, 16
+    res = rng.normal(size=(T, H)).astype(np.float32)
+    down = rng.normal(size=(T * k, H)).astype(np.float32)
+    w = rng.uniform(size=(T, k)).astype(np.float32)
+    sh = rng.normal(size=(T, H)).astype(np.float32)
+    rlog = rng.normal(size=(T, E + 1)).astype(np.float32)
+    out = torch.empty(T, H, device=cuda)
+    drlog = t32(rlog, cuda)
+    kernels.moe_combine(t32(res, cuda), t32(down, cuda), t32(w, cuda), t32(sh, cuda), drlog[:, E:], E + 1, out, T,
+                        H, k)
+    ref = res + np.einsum("tr,trh->th", w.astype(np.float64), down.reshape(T, k, H)) + \
+        sh * moe_ref.sigmoid(rlog[:, E:E + 1])
+    assert rel_err(out.cpu().numpy(), ref) <= 1e-5
+
+
+def test_attn_prefill_continues_a_cache(cuda):
+    rng = np.random.default_rng(10)
+    Hq, Hkv, D, pos0, rows = 4, 2, 256, 5, 3
+    cap = pos0 + rows
+    K = rng.normal(size=(cap, Hkv * D)).astype(np.float32)
+    V = rng.normal(size=(cap, Hkv * D)).astype(np.float32)
+    q = rng.normal(size=(rows, Hq * D)).astype(np.float32)
+    out = torch.empty(rows, Hq * D, device=cuda)
+    scale = 1 / math.sqrt(D)
+    kernels.attn_prefill(t32(q, cuda), Hq * D, t32(K, cuda), t32(V, cuda), out, Hq * D, rows, Hq, Hkv, D, pos0, scale)
+    ref = np.empty((rows, Hq * D))
+    for r in range(rows):
+        L = pos0 + r + 1
+        for h in range(Hq):
+            g = h // (Hq // Hkv)
+            s = K[:L, g * D:(g + 1) * D].astype(np.float64) @ q[r, h * D:(h + 1) * D] * scale
+            ref[r, h * D:(h + 1) * D] = moe_ref.softmax(s) @ V[:L, g * D:(g + 1) * D]
+    assert rel_err(out.cpu().numpy(), ref) <= 1e-4
+
+
+# ------------------------------------------------------------ whole models
+@pytest.fixture(scope="module")
+def moe_tiny(tmp_path_factory):
+    path = tmp_path_factory.mktemp("moe") / "moe-tiny.gguf"
+    return synth.write_qwen35moe(path, synth.MOE_SHAPES["moe-tiny"], seed=3)
+
+
+def run_pair(path, prompt, steps, max_sequence=64):
+    ref = moe_ref.MoeRef(path, max_sequence)
+    got_tok, ref_tok, errs, route_ok = [], [], [], []
+    with HipLLM(path, max_sequence) as m:
+        nxt = m.prefill(prompt)
+        r = ref.prefill(prompt)
+        for step in range(steps + 1):
+            got_tok.append(nxt)
+            ref_tok.append(r)
+            lg = m.logits().astype(np.float64)
+            errs.append(np.abs(lg - ref.logits).max() / np.abs(ref.logits).max())
+            routes = m.routes()
+            route_ok.append(all(routes[l].tolist() == ref.last_routes[l][0].tolist() for l in range(ref.L)))
+            if step == steps:
+                break
+            nxt = m.decode(r)  # both continue from the reference's token
+            r = ref.decode(r)
+    return got_tok, ref_tok, np.array(errs), route_ok
+
+
+def test_moe_tiny_matches_float64_reference(cuda, moe_tiny):
+    prompt = synth.uniform_ids(8, 512, seed=11).tolist()
+    got, ref, errs, routes = run_pair(moe_tiny, prompt, 8)
+    print("max rel logit error per step:", errs.max())
+    assert got == ref
+    assert all(routes)
+    assert errs.max() <= 1e-3
+
+
+def test_moe_contract_and_stats(cuda, moe_tiny):
+    with HipLLM(moe_tiny, 12) as m:
+        assert m.config["architecture"] == "qwen35moe"
+        assert m.uses_gpu and m.expert_cache_count == 8
+        with pytest.raises(ValueError):
+            m.decode(1)
+        with pytest.raises(ValueError):
+            m.prefill([])
+        with pytest.raises(IndexError):
+            m.prefill([1, 2, 512])
+        with pytest.raises(LengthError):
+            m.prefill(list(range(13)))
+        a = generate(m, [3, 4, 5], 5)
+        with pytest.raises(ValueError):
+            m.prefill([1])
+        b = generate(m, [3, 4, 5], 5)  # reset() zeroes the DeltaNet state
+        assert a == b
+        s = m.memory_stats()
+        sh = synth.MOE_SHAPES["moe-tiny"]
+        full = sh.layers // sh.full_attention_interval
+        assert s["kv_cache_bytes"] == full * 2 * 12 * sh.kv_heads * sh.head_dim * 4
+        dn = sh.layers - full
+        assert s["recurrent_state_bytes"] == dn * (sh.time_step_rank * sh.state_size ** 2 +
+                                                   (sh.conv_kernel - 1) * sh.qkv_width) * 4
+    with pytest.raises(ValueError):
+        HipLLM(moe_tiny, 12, expert_cache_count=2)  # below top-k
+
+
+def test_moe_real_widths_match_float64_reference(cuda, tmp_path):
+    # Qwen3.5-35B-A3B widths (2048 hidden, 256 experts top-8, 16 x 256 gated
+    # attention, 32 x 128 DeltaNet), first four layers.
+    shape = synth.MOE_SHAPES["qwen3.5-35b-a3b-4l"]
+    path = synth.write_qwen35moe(tmp_path / "moe4l.gguf", shape, seed=5)
+    prompt = synth.uniform_ids(5, shape.vocab, seed=12).tolist()
+    got, ref, errs, routes = run_pair(path, prompt, 2, max_sequence=32)
+    print("max rel logit error per step:", errs.max())
+    assert got == ref
+    assert all(routes)
+    assert errs.max() <= 1e-3
