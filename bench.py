@@ -19,13 +19,14 @@ The same JSON line carries:
 * ``prefill_gemm``: the bf16-MFMA prefill matmul, M in {64, 512, 2048} x
   K 3584 x N 18944, Q4_K weights, TFLOP/s against the 2.5 PFLOP/s bf16 peak;
 * ``e2e``: greedy prefill and decode tok/s of synthetic Qwen2.5-0.5B-, 7B- and
-  14B-shaped Q4_K_M models through the HipLLM handle API;
+  14B-shaped Q4_K_M models and a Qwen3.5-35B-A3B-shaped qwen35moe model (all
+  256 experts resident) through the HipLLM handle API;
 * ``cpu_baseline``: a bounded sample of the same GEMV step on the host (the
   oracle's CPULLM gevmt, one thread), plus the reference CPULLM's own decode
   rate on the 0.5B-shaped model when oracle/_ref is built.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-e2e] [--no-cpu]
-                       [--no-14b] [--profile-kernel gate] [--profile-reps N]
+                       [--no-14b] [--no-moe] [--profile-kernel gate] [--profile-reps N]
 """
 
 from __future__ import annotations
@@ -243,6 +244,48 @@ def bench_e2e(shape_name, prompt_len, decode_steps, workdir, max_sequence=0):
             "layers": cfg["layer_count"], "gguf_gen_s": gen_s, "load_s": load_s}
 
 
+def bench_e2e_moe(shape_name, prompt_len, decode_steps, workdir):
+    """qwen35moe greedy prefill + decode through the HipLLM handle API (the
+    backend is picked from the file's architecture, as the CLI's --gpu does)."""
+    from myllm_amd import synth
+    from myllm_amd.hipllm import HipLLM
+
+    shape = synth.MOE_SHAPES[shape_name]
+    t0 = time.perf_counter()
+    path = synth.write_qwen35moe(pathlib.Path(workdir) / f"{shape_name}.gguf", shape, seed=0)
+    gen_s = time.perf_counter() - t0
+    prompt = synth.uniform_ids(prompt_len, shape.vocab, seed=0).tolist()
+    cap = prompt_len + decode_steps + 1
+    try:
+        t0 = time.perf_counter()
+        model = HipLLM(path, cap)
+        load_s = time.perf_counter() - t0
+        try:
+            model.reset()
+            nxt = model.prefill(prompt)
+            for _ in range(2):
+                nxt = model.decode(nxt)
+            model.reset()
+            t0 = time.perf_counter()
+            nxt = model.prefill(prompt)
+            prefill_s = time.perf_counter() - t0
+            dec = 0.0
+            for _ in range(decode_steps):
+                t0 = time.perf_counter()
+                nxt = model.decode(nxt)
+                dec += time.perf_counter() - t0
+            stats = model.memory_stats()
+        finally:
+            model.close()
+    finally:
+        os.unlink(path)
+    return {"model": shape_name, "prompt_tokens": prompt_len, "decode_steps": decode_steps, "max_sequence": cap,
+            "prefill_tok_s": prompt_len / prefill_s, "decode_tok_s": decode_steps / dec,
+            "decode_ms_per_token": dec / decode_steps * 1e3, "weight_bytes": stats["weight_bytes"],
+            "recurrent_state_bytes": stats["recurrent_state_bytes"], "kv_cache_bytes": stats["kv_cache_bytes"],
+            "layers": shape.layers, "experts_resident": shape.experts, "gguf_gen_s": gen_s, "load_s": load_s}
+
+
 def cpu_baseline(budget_s: float = 12.0):
     """CPULLM's FP32 GEMV (gevmt, cpu_llm.cpp:512-526), restated in the
     oracle, over the same four shapes on FP32 weights dequantized from the
@@ -325,6 +368,7 @@ def main():
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-14b", action="store_true")
+    ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--profile-kernel", choices=[s[0] for s in SHAPES])
     ap.add_argument("--profile-reps", type=int, default=200)
     args = ap.parse_args()
@@ -366,6 +410,10 @@ def main():
                 log(f"[bench] e2e {name}")
                 e2e[name] = bench_e2e(name, p, d, tmp, cap)
                 log(f"[bench] {e2e[name]}")
+            if not args.no_moe:
+                log("[bench] e2e qwen3.5-35b-a3b (all 256 experts resident)")
+                e2e["qwen3.5-35b-a3b"] = bench_e2e_moe("qwen3.5-35b-a3b", 64, 64, tmp)
+                log(f"[bench] {e2e['qwen3.5-35b-a3b']}")
 
     cpu = None
     if not args.no_cpu:
