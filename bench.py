@@ -370,6 +370,8 @@ def main():
     ap.add_argument("--no-14b", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--profile-kernel", choices=[s[0] for s in SHAPES])
+    ap.add_argument("--e2e-only", choices=["qwen2.5-0.5b", "qwen2.5-7b", "qwen2.5-14b", "qwen3.5-35b-a3b"],
+                    help="run one end-to-end model only (for profiling) and print its result")
     ap.add_argument("--profile-reps", type=int, default=200)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -385,6 +387,16 @@ def main():
 
     if args.profile_kernel:
         profile_kernel(args.profile_kernel, args.profile_reps, torch, cuda)
+        return
+    if args.e2e_only:
+        with tempfile.TemporaryDirectory(dir=scratch_dir()) as tmp:
+            if args.e2e_only == "qwen3.5-35b-a3b":
+                r = bench_e2e_moe(args.e2e_only, 64, 64, tmp)
+            else:
+                p, d, cap = {"qwen2.5-0.5b": (16, 32, 0), "qwen2.5-7b": (128, 64, 0),
+                             "qwen2.5-14b": (128, 128, 4096)}[args.e2e_only]
+                r = bench_e2e(args.e2e_only, p, d, tmp, cap)
+        print(json.dumps(r), flush=True)
         return
 
     log("[bench] Q4_K GEMV")

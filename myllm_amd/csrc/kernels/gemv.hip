@@ -902,7 +902,7 @@ bool valid_tiling(int t) {
 // Default tiling: the largest R and smallest OPR (least activation traffic,
 // fewest cross-octet reductions) that still launches >= 1024 waves, with OPR
 // chosen so units split evenly across the octets of a row group.
-int gemv_default_tiling(uint32_t n, uint32_t units, int mode) {
+int gemv_default_tiling(uint32_t n, uint32_t units, int mode, uint32_t vectors) {
     const uint32_t target_waves = 1024;
     int best = 0;
     double best_score = -1.0;
@@ -911,7 +911,7 @@ int gemv_default_tiling(uint32_t n, uint32_t units, int mode) {
         const uint32_t rpb = 32u * R / OPR;
         if (mode == 1 && rpb % 16 != 0) continue;
         const uint32_t blocks = (n + rpb - 1) / rpb;
-        const uint32_t waves = blocks * 4;
+        const uint32_t waves = blocks * 4 * vectors;
         const uint32_t per = (units + OPR - 1) / OPR;               // units of the busiest octet
         const double balance = static_cast<double>(units) / (per * OPR);
         const double fill = waves >= target_waves ? 1.0 : static_cast<double>(waves) / target_waves;
@@ -1052,7 +1052,7 @@ int launch_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row
     const uint32_t nn = static_cast<uint32_t>(n);
     const uint32_t nv = static_cast<uint32_t>(vectors);
     if (!wu) {
-        int t = gemv_default_tiling(nn, units, 0);
+        int t = gemv_default_tiling(nn, units, 0, nv);
         switch (type) {
         case kQ4_K: return launch_typed<kQ4_K, 0>(t, w, nullptr, row_bytes, x, xs16, bias, residual, y, nullptr, nn, units, stream, b, nv);
         case kQ6_K: return launch_typed<kQ6_K, 0>(t, w, nullptr, row_bytes, x, xs16, bias, residual, y, nullptr, nn, units, stream, b, nv);
@@ -1064,7 +1064,7 @@ int launch_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row
         }
     }
     if (bias || residual) return kInvalidArgument;
-    const int t = gemv_default_tiling(nn, units, 1);
+    const int t = gemv_default_tiling(nn, units, 1, nv);
     switch (type) {
     case kQ4_K: return launch_typed<kQ4_K, 1>(t, w, wu, row_bytes, x, xs16, nullptr, nullptr, y, ys16, nn, units, stream, b, nv);
     case kQ6_K: return launch_typed<kQ6_K, 1>(t, w, wu, row_bytes, x, xs16, nullptr, nullptr, y, ys16, nn, units, stream, b, nv);

@@ -13,7 +13,7 @@ int launch_dequant_rows(uint32_t type, const void* w, size_t row_bytes, size_t r
                         hipStream_t stream);
 
 int launch_prep_sums(const float* x, float* xs16, size_t k, hipStream_t stream);
-int gemv_default_tiling(uint32_t n, uint32_t units, int mode);
+int gemv_default_tiling(uint32_t n, uint32_t units, int mode, uint32_t vectors = 1);
 int launch_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* xs16,
                         const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
                         hipStream_t stream);

@@ -52,8 +52,11 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 }
 
 // ------------------------------------------------------------ router
-// One block per token: softmax over the expert logits, top-k insertion by
-// one thread (k <= 8, a single pass over the experts), renormalisation.
+// One block per token: softmax over the expert logits, then k rounds of a
+// block-wide argmax over the unselected experts (the larger probability, the
+// lower id on ties), then renormalisation. Taking maxima in descending order
+// with lower-id tie-breaks selects exactly what the reference's insertion
+// scan with a strict '>' keeps, in the same rank order.
 constexpr uint32_t kMaxExperts = 1024;
 
 __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, uint32_t ld,
@@ -63,6 +66,10 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
     const float* row = logits + static_cast<size_t>(t) * ld;
     __shared__ float p[kMaxExperts];
     __shared__ float red[4];
+    __shared__ float wv[4];
+    __shared__ uint32_t wi[4];
+    __shared__ float sel_v[8];
+    __shared__ uint32_t sel_i[8];
     float m = -INFINITY;
     for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) m = fmaxf(m, row[e]);
     m = block_max256(m, red);
@@ -76,37 +83,60 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
     s = block_sum256(s, red);
     for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) p[e] = s > 0.0f ? p[e] / s : 0.0f;
     __syncthreads();
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (uint32_t r = 0; r < k; ++r) {
+        float bv = -INFINITY;
+        uint32_t bi = 0xffffffffu;
+        for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
+            const float v = p[e];
+            if (v > bv) {  // e increases per thread, so '>' keeps the lower id on ties
+                bv = v;
+                bi = e;
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o);
+            const uint32_t oi = __shfl_xor(bi, o);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (lane == 0) {
+            wv[wave] = bv;
+            wi[wave] = bi;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float v = wv[0];
+            uint32_t i = wi[0];
+            for (uint32_t w = 1; w < 4; ++w) {
+                if (wv[w] > v || (wv[w] == v && wi[w] < i)) {
+                    v = wv[w];
+                    i = wi[w];
+                }
+            }
+            // No candidate left (all remaining -inf or NaN): rank r keeps
+            // -inf with id 0, as the insertion scan leaves it.
+            if (i >= experts) {
+                v = -INFINITY;
+                i = 0;
+            } else {
+                p[i] = -INFINITY;
+            }
+            sel_v[r] = v;
+            sel_i[r] = i;
+        }
+        __syncthreads();
+    }
     if (threadIdx.x == 0) {
-        float bv[8];
-        int32_t bi[8];
-        for (uint32_t r = 0; r < 8; ++r) {
-            bv[r] = -INFINITY;
-            bi[r] = 0;
-        }
-        for (uint32_t e = 0; e < experts; ++e) {
-            const float c = p[e];
-            uint32_t ins = k;
-            for (uint32_t r = 0; r < k; ++r) {
-                if (c > bv[r]) {
-                    ins = r;
-                    break;
-                }
-            }
-            if (ins < k) {
-                for (uint32_t r = k - 1; r > ins; --r) {
-                    bv[r] = bv[r - 1];
-                    bi[r] = bi[r - 1];
-                }
-                bv[ins] = c;
-                bi[ins] = static_cast<int32_t>(e);
-            }
-        }
         float sum = 0.0f;
-        for (uint32_t r = 0; r < k; ++r) sum += bv[r];
+        for (uint32_t r = 0; r < k; ++r) sum += sel_v[r];
         const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
         for (uint32_t r = 0; r < k; ++r) {
-            ids[t * k + r] = bi[r];
-            weights[t * k + r] = bv[r] * inv;
+            ids[t * k + r] = static_cast<int32_t>(sel_i[r]);
+            weights[t * k + r] = sel_v[r] * inv;
         }
     }
 }
