@@ -120,11 +120,13 @@ __global__ void rope_kv_kernel(float* __restrict__ qkv, const float2* __restrict
 
 // ------------------------------------------------------------ attention
 // Split-K decode attention (flash-decode). Phase 1: block (head, chunk) scores
-// keys [chunk*C, min(len, chunk*C + C)) against its query, and writes the
-// chunk's running max m, sum of exp l, and unnormalised p.V (D floats).
-// Phase 2: one block per head merges the chunks and writes the head output,
-// plus per-16 sums of the whole output vector for the next GEMV.
-constexpr uint32_t kAttnChunk = 256;
+// keys [chunk*C, min(len, chunk*C + C)) against its query (four lanes per
+// key, each a quarter of the head dims), and writes the chunk's running max
+// m, sum of exp l, and unnormalised p.V (D floats; threads split the chunk's
+// keys in 256 / D interleaved parts, reduced in LDS). Phase 2: one block per
+// head merges the chunks and writes the head output, plus per-16 sums of the
+// whole output vector for the next GEMV.
+constexpr uint32_t kAttnChunk = 64;
 
 __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restrict__ q, const float* __restrict__ kcache,
                                                            const float* __restrict__ vcache, float* __restrict__ part,
@@ -135,46 +137,83 @@ __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restri
     const uint32_t g = h / (hq / hkv);
     const uint32_t kvd = hkv * d;
     const uint32_t t0 = chunk * kAttnChunk;
-    const uint32_t t1 = min(len, t0 + kAttnChunk);
-    __shared__ float qs[256];
+    const uint32_t cnt = min(len - t0, kAttnChunk);
+    __shared__ float4 qs4[64];
     __shared__ float ps[kAttnChunk];
     __shared__ float red[8];
-    for (uint32_t i = threadIdx.x; i < d; i += blockDim.x) qs[i] = q[h * d + i];
+    __shared__ float4 accp[256];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t d4 = d / 4;
+    for (uint32_t i = tid; i < d4; i += blockDim.x) qs4[i] = reinterpret_cast<const float4*>(q + h * d)[i];
     __syncthreads();
-    const uint32_t t = t0 + threadIdx.x;
+    // Scores: key j = tid / 4, quarter qq = tid % 4 covers float4 columns qq, qq + 4, ...
+    const uint32_t j = tid >> 2, qq = tid & 3;
     float s = -INFINITY;
-    if (t < t1) {
-        const float4* k = reinterpret_cast<const float4*>(kcache + static_cast<size_t>(t) * kvd + g * d);
+    {
         float dot = 0.0f;
-        for (uint32_t i = 0; i < d / 4; ++i) {
-            const float4 kv = k[i];
-            dot = fmaf(kv.x, qs[4 * i], dot);
-            dot = fmaf(kv.y, qs[4 * i + 1], dot);
-            dot = fmaf(kv.z, qs[4 * i + 2], dot);
-            dot = fmaf(kv.w, qs[4 * i + 3], dot);
+        if (j < cnt) {
+            const float4* k = reinterpret_cast<const float4*>(kcache + static_cast<size_t>(t0 + j) * kvd + g * d);
+            for (uint32_t i = qq; i < d4; i += 4) {
+                const float4 kv = k[i];
+                const float4 qv = qs4[i];
+                dot = fmaf(kv.x, qv.x, dot);
+                dot = fmaf(kv.y, qv.y, dot);
+                dot = fmaf(kv.z, qv.z, dot);
+                dot = fmaf(kv.w, qv.w, dot);
+            }
         }
-        s = dot * scale;
+        dot += __shfl_xor(dot, 1);
+        dot += __shfl_xor(dot, 2);
+        if (j < cnt) s = dot * scale;
     }
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t wave = tid >> 6, lane = tid & 63;
     float m = warp_max(s);
     if (lane == 0) red[wave] = m;
     __syncthreads();
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const float p = t < t1 ? expf(s - m) : 0.0f;
-    ps[threadIdx.x] = p;
-    float l = warp_sum(p);
+    const float p = j < cnt ? expf(s - m) : 0.0f;
+    if (qq == 0) ps[j] = p;
+    float l = warp_sum(qq == 0 ? p : 0.0f);
     __syncthreads();
     if (lane == 0) red[4 + wave] = l;
     __syncthreads();
     l = (red[4] + red[5]) + (red[6] + red[7]);
+    // p.V: float4 column c4 = tid % (d / 4), key subset pp = tid / (d / 4) of
+    // `parts` interleaved subsets, reduced in LDS; threads past parts * d / 4
+    // (when d / 4 does not divide 256) idle.
+    const uint32_t parts = blockDim.x / d4;
     float* out = part + (static_cast<size_t>(h) * nchunks + chunk) * (d + 2);
-    for (uint32_t i = threadIdx.x; i < d; i += blockDim.x) {
-        const float* v = vcache + static_cast<size_t>(t0) * kvd + g * d + i;
-        float acc = 0.0f;
-        for (uint32_t tt = 0; tt < t1 - t0; ++tt) acc = fmaf(ps[tt], v[static_cast<size_t>(tt) * kvd], acc);
-        out[2 + i] = acc;
+    if (tid < parts * d4) {
+        const uint32_t c4 = tid % d4, pp = tid / d4;
+        const float4* v = reinterpret_cast<const float4*>(vcache + static_cast<size_t>(t0) * kvd + g * d) + c4;
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 4
+        for (uint32_t jj = pp; jj < cnt; jj += parts) {
+            const float pj = ps[jj];
+            const float4 vv = v[static_cast<size_t>(jj) * (kvd / 4)];
+            acc.x = fmaf(pj, vv.x, acc.x);
+            acc.y = fmaf(pj, vv.y, acc.y);
+            acc.z = fmaf(pj, vv.z, acc.z);
+            acc.w = fmaf(pj, vv.w, acc.w);
+        }
+        accp[tid] = acc;
     }
-    if (threadIdx.x == 0) {
+    __syncthreads();
+    for (uint32_t c4 = tid; c4 < d4; c4 += blockDim.x) {
+        float4 acc = accp[c4];
+        for (uint32_t pp = 1; pp < parts; ++pp) {
+            const float4 a = accp[pp * d4 + c4];
+            acc.x += a.x;
+            acc.y += a.y;
+            acc.z += a.z;
+            acc.w += a.w;
+        }
+        out[2 + 4 * c4 + 0] = acc.x;
+        out[2 + 4 * c4 + 1] = acc.y;
+        out[2 + 4 * c4 + 2] = acc.z;
+        out[2 + 4 * c4 + 3] = acc.w;
+    }
+    if (tid == 0) {
         out[0] = m;
         out[1] = l;
     }
@@ -409,6 +448,7 @@ int launch_attn_decode(const float* q, const float* kcache, const float* vcache,
         return kInvalidArgument;
     }
     if (d == 0 || d > 256 || d % 16 != 0) return kInvalidArgument;
+    if (len > 0xffffffffull || hq > 0xffffull) return kLengthError;
     const uint32_t nchunks = static_cast<uint32_t>((len + kAttnChunk - 1) / kAttnChunk);
     hipLaunchKernelGGL(attn_decode_partial, dim3(static_cast<uint32_t>(hq), nchunks), dim3(256), 0, stream, q, kcache,
                        vcache, scratch, static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv),
