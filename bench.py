@@ -95,14 +95,14 @@ def gemv_setup(qtype, torch, cuda):
     from myllm_amd.hipllm import kernels
     rot = Rotation(qtype, torch, cuda)
     xs = {k: torch.from_numpy(synth.normal(k, seed=k)).to(cuda) for k in (3584, 18944)}
-    sums = {}
+    xq = {}  # XGroup form of each input (k / 16 groups of 64 bytes)
     for k, x in xs.items():
-        sums[k] = torch.empty(k // 16, dtype=torch.float32, device=cuda)
-        kernels.prep_sums(x, sums[k], k)
+        xq[k] = torch.empty(k, dtype=torch.float32, device=cuda)
+        kernels.prep_x(x, xq[k], k)
     ys = {name: torch.empty(n, dtype=torch.float32, device=cuda) for name, n, _ in SHAPES}
 
     def launch(c, name, n, k, stream=None):
-        kernels.gemv_prepped(qtype, rot.layers[c][name], rot.row_bytes(n, k), xs[k], sums[k], None, None,
+        kernels.gemv_prepped(qtype, rot.layers[c][name], rot.row_bytes(n, k), xs[k], xq[k], None, None,
                              ys[name], n, k, 0, stream=stream)
 
     return rot, launch

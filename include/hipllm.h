@@ -50,8 +50,17 @@ const char* hipllm_version(void);
 int hipllm_dequant_rows(uint32_t type, const void* w, size_t row_bytes, size_t rows, size_t k, float* out,
                         void* stream);
 
-/* Per-16 sums of x (k / 16 floats), the activation side-input of the GEMV. */
-int hipllm_prep_sums(const float* x, float* xs16, size_t k, void* stream);
+/* Activation side-input of the GEMV: for every 16 values of x (k % 16 == 0)
+ * one 64-byte group holding them as 24-bit fixed point in three signed-byte
+ * digits (q = s2 * 65536 + s1 * 256 + s0, x ~= e q, |x - e q| <= e with
+ * e = max|x| / 8355711 over the group), then the FP32 sum of the 16 values
+ * and e: bytes s0[16] s1[16] s2[16], float sum, float e, 8 bytes padding.
+ * xq holds k / 16 groups (4 k bytes, 16-byte aligned). The integer GEMV
+ * multiplies quant bytes with the digits (v_dot4_i32_i8). Producers of GEMV
+ * inputs (hipllm_rmsnorm, hipllm_attn_decode, hipllm_swiglu,
+ * hipllm_gemv_swiglu, hipllm_gated_rmsnorm, hipllm_gate_mul) write this
+ * form directly; hipllm_prep_x makes it from any x. */
+int hipllm_prep_x(const float* x, void* xq, size_t k, void* stream);
 
 /* Workspace bytes hipllm_gemv needs for an input of k values. */
 size_t hipllm_gemv_workspace_bytes(size_t k);
@@ -64,20 +73,23 @@ size_t hipllm_gemv_workspace_bytes(size_t k);
 int hipllm_gemv(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* bias, float* y,
                 size_t n, size_t k, void* workspace, void* stream);
 
-/* GEMV with caller-supplied per-16 sums and an optional residual:
+/* GEMV with a caller-supplied XGroup input (hipllm_prep_x; quantized
+ * weights read xq, F32 / F16 weights read x) and an optional residual:
  * y = W x (+ bias) (+ residual). `tiling` 0 picks the default; otherwise
- * 10 * R + OPR with R in {1, 2, 4} rows per 8-lane octet and OPR in
- * {1, 2, 4, 8} octets splitting each row group's super-blocks. */
-int hipllm_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* xs16,
+ * 100 * R + OPR with R rows per 8-lane octet and OPR octets splitting each
+ * row group's units: 108, 116, 132, 202, 204, 208, 216, 232, 401, 402, 404,
+ * 408, 416, 432, 802, 804, 808, 816, 832. */
+int hipllm_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const float* x, const void* xq,
                         const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
                         void* stream);
 
-/* Fused FFN gate/up GEMV + SwiGLU: y = silu(Wg x) * (Wu x); ys16 (nullable,
- * n % 16 == 0) receives the per-16 sums of y. Replaces the gate/up
+/* Fused FFN gate/up GEMV + SwiGLU: y = silu(Wg x) * (Wu x); yq (nullable,
+ * n % 16 == 0) receives the XGroup form of y. `tiling` 0 picks the default,
+ * else one of 202, 204, 401, 402, 404, 408, 802, 804, 808, 816. Replaces the gate/up
  * encode_vector_product pair + metal_swiglu_f32 (metal_llm.mm:2885-2894;
  * metal_llm.metal:895-911), cpu_llm.cpp:905-909. */
 int hipllm_gemv_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
-                       const float* xs16, float* y, float* ys16, size_t n, size_t k, void* stream);
+                       const void* xq, float* y, void* yq, size_t n, size_t k, int tiling, void* stream);
 
 /* xb[m, k] (bf16, row-major, ld = k) = round-to-nearest-even of the FP32
  * rows x[r * ldx + c]; the activation side-input of hipllm_gemm_mfma. */
@@ -101,9 +113,10 @@ int hipllm_gemm(uint32_t type, const void* w, size_t row_bytes, const float* x, 
                 float* y, size_t m, size_t n, size_t k, void* workspace, void* stream);
 
 /* Row RMSNorm y = x * (1/sqrt(mean(x^2) + eps) * gamma), double sum of
- * squares; ys16 nullable. Replaces metal_rmsnorm_f32 (metal_llm.metal:785-823)
- * and Vector::rmsnorm (cpu_llm.cpp:143-166). */
-int hipllm_rmsnorm(const float* x, const float* gamma, float* y, float* ys16, size_t rows, size_t cols, float eps,
+ * squares; yq (nullable) the XGroup form of y, rows of cols / 16 groups.
+ * Replaces metal_rmsnorm_f32 (metal_llm.metal:785-823) and Vector::rmsnorm
+ * (cpu_llm.cpp:143-166). */
+int hipllm_rmsnorm(const float* x, const float* gamma, float* y, void* yq, size_t rows, size_t cols, float eps,
                    void* stream);
 
 /* out[t, :] = dequant(table[ids[t]]); out-of-range ids give zeros.
@@ -123,11 +136,11 @@ int hipllm_rope_kv(float* qkv, const float* cos_sin, size_t rot, size_t hq, size
 /* Scratch floats hipllm_attn_decode needs for up to max_len positions. */
 size_t hipllm_attn_decode_scratch_floats(size_t hq, size_t d, size_t max_len);
 
-/* One-token GQA attention over positions [0, len) of the caches; out16
- * nullable. Replaces metal_kv_cache_qk_f32 / metal_softmax_f32 /
+/* One-token GQA attention over positions [0, len) of the caches; outq
+ * (nullable) the XGroup form of out. Replaces metal_kv_cache_qk_f32 / metal_softmax_f32 /
  * metal_kv_cache_av_f32 (metal_llm.metal:826-890, 995-1061) and the decode
  * head loop (cpu_llm.cpp:893-906). */
-int hipllm_attn_decode(const float* q, const float* kcache, const float* vcache, float* out, float* out16,
+int hipllm_attn_decode(const float* q, const float* kcache, const float* vcache, float* out, void* outq,
                        float* scratch, size_t hq, size_t hkv, size_t d, size_t len, float scale, void* stream);
 
 /* Scratch bytes hipllm_argmax needs for n values. */
@@ -138,9 +151,9 @@ size_t hipllm_argmax_scratch_bytes(size_t n);
  * greedy_token (cpu_llm.cpp:34-48). */
 int hipllm_argmax(const float* x, size_t n, uint32_t* out, void* scratch, void* stream);
 
-/* y = silu(g) * u (reference sign-branched sigmoid); y16 nullable.
- * Replaces metal_swiglu_f32 (metal_llm.metal:895-911). */
-int hipllm_swiglu(const float* g, const float* u, float* y, float* y16, size_t n, void* stream);
+/* y = silu(g) * u (reference sign-branched sigmoid); yq (nullable) the
+ * XGroup form of y. Replaces metal_swiglu_f32 (metal_llm.metal:895-911). */
+int hipllm_swiglu(const float* g, const float* u, float* y, void* yq, size_t n, void* stream);
 
 /* Causal prefill attention: query row r (position pos0 + r, heads at
  * q + r * q_stride) over cache positions [0, pos0 + r]. Replaces
@@ -154,14 +167,15 @@ int hipllm_attn_prefill(const float* q, size_t q_stride, const float* kcache, co
 
 /* A batch of `vectors` GEMVs in one launch. Vector j: y[j * ldy, n) =
  * W_j x_j (+ bias) (+ residual[j]); with wu != NULL, y = silu(Wg_j x_j) *
- * (Wu_j x_j) and ys16 (nullable) gets per-16 sums. With ids, W_j is expert
- * ids[j] (byte offset ids[j] * expert_stride, ids clamped to experts - 1) and
- * x_j is row j (x_routed) or row j / routes of x (ld ldx, xs16 ld ldx / 16);
+ * (Wu_j x_j) and yq (nullable) gets its XGroup form (ld ldy / 16 groups).
+ * With ids, W_j is expert ids[j] (byte offset ids[j] * expert_stride, ids
+ * clamped to experts - 1) and x_j is row j (x_routed) or row j / routes of x
+ * (ld ldx, xq ld ldx / 16 groups);
  * without ids every vector uses W and row j of x.
  * Replaces metal_expert_gemm_{q4_k,q6_k}_f32 (metal_llm.metal:1476-1521;
  * moe_llm.mm:2692-2760) and the per-row product of encode_product. */
 int hipllm_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row_bytes, const float* x,
-                        const float* xs16, const float* bias, const float* residual, float* y, float* ys16, size_t n,
+                        const void* xq, const float* bias, const float* residual, float* y, void* yq, size_t n,
                         size_t k, size_t vectors, const int32_t* ids, size_t experts, size_t routes,
                         size_t expert_stride, int x_routed, size_t ldx, size_t ldy, void* stream);
 
@@ -203,10 +217,11 @@ int hipllm_gdn_scan(const float* q, const float* k, size_t ldqk, const float* v,
                     const float* beta, float* state, float* out, size_t ldo, size_t tokens, size_t value_heads,
                     size_t key_heads, size_t d, void* stream);
 
-/* y = rmsnorm(o_head) gamma silu(z) per head; ys16 nullable. Replaces the
+/* y = rmsnorm(o_head) gamma silu(z) per head (d <= 256); yq (nullable) the
+ * XGroup form of y. Replaces the
  * state norm + SiLU(z) gate of encode_delta_net (moe_llm.mm:2614-2634). */
 int hipllm_gated_rmsnorm(const float* o, size_t ldo, const float* gamma, const float* z, size_t ldz, float* y,
-                         float* ys16, size_t ldy, size_t tokens, size_t heads, size_t d, float eps, void* stream);
+                         void* yq, size_t ldy, size_t tokens, size_t heads, size_t d, float eps, void* stream);
 
 /* Split the per-head interleaved [Q_h | gate_h] projection, RMSNorm Q and K
  * heads with their gammas, and lay out [Q | K | V] rows for RoPE + cache.
@@ -216,9 +231,9 @@ int hipllm_split_qgate_norm(const float* mixed, size_t ldm, const float* kv, siz
                             const float* k_gamma, float* qkv, size_t ldqkv, float* gate, size_t ldg, size_t tokens,
                             size_t hq, size_t hkv, size_t d, float eps, void* stream);
 
-/* y = a sigmoid(g) (y16 nullable per-16 sums). Replaces the attention output
- * gate of encode_full_attention (moe_llm.mm:2420-2428). */
-int hipllm_gate_mul(const float* a, const float* g, float* y, float* y16, size_t n, void* stream);
+/* y = a sigmoid(g); yq (nullable) the XGroup form of y. Replaces the
+ * attention output gate of encode_full_attention (moe_llm.mm:2420-2428). */
+int hipllm_gate_mul(const float* a, const float* g, float* y, void* yq, size_t n, void* stream);
 
 /* ------------------------------------------------------------ handle API */
 

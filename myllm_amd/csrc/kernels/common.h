@@ -129,4 +129,77 @@ __device__ __forceinline__ double warp_sum_d(double v) {
     return v;
 }
 
+// ---------------------------------------------------------------- XGroup
+// Activation format of the integer GEMV path. Every 16 consecutive values
+// x[16g .. 16g + 15] of a GEMV input are held as 24-bit fixed point
+// q = round(x / e) with |q| <= kXGroupMax, split into balanced base-256
+// digits q = s2 * 65536 + s1 * 256 + s0 (each digit a signed byte, so that
+// v_dot4_i32_i8 multiplies them with weight quants directly), together with
+// the FP32 sum of the 16 values, the scale e = max|x| / kXGroupMax and the
+// digit weights 256 e and 65536 e. The
+// representation error |x - e q| is at most e, 2^-23 of the group's largest
+// magnitude, i.e. the rounding error of FP32 itself at that magnitude; dot
+// products of quants with the digits are exact integers.
+constexpr float kXGroupMax = 8355711.0f;  // 0x7f7f7f: largest q whose digits all fit a signed byte
+
+struct __align__(16) XGroup {
+    uint32_t s0[4], s1[4], s2[4];  // digits, 4 values per dword, value i in byte i % 4 of dword i / 4
+    float sum, e, e256, e65536;    // e256 = 256 e and e65536 = 65536 e (digit weights, exact)
+};
+static_assert(sizeof(XGroup) == 64, "XGroup is 64 bytes");
+
+// Encodes 16 values held by one thread. Groups whose largest magnitude is
+// below 2^-100 are stored as zero (their contribution is below FP32
+// resolution of any realistic output); a non-finite value makes e NaN, so the
+// GEMV outputs that read the group are NaN (FP32 would give inf or NaN).
+__device__ __forceinline__ void xgroup_encode(const float (&v)[16], XGroup* __restrict__ g) {
+    float sum = 0.0f, amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        sum += v[i];
+        amax = fmaxf(amax, fabsf(v[i]));
+    }
+    // fmaxf drops NaN operands, so NaN shows in the sum instead.
+    const bool finite = amax <= 3.4028234663852886e38f && sum == sum;
+    const bool tiny = amax < 7.888609052210118e-31f;  // 2^-100
+    const float e = finite ? (tiny ? 0.0f : amax / kXGroupMax) : __builtin_nanf("");
+    const float inv = (finite && !tiny) ? kXGroupMax / amax : 0.0f;
+    uint32_t w0[4] = {0, 0, 0, 0}, w1[4] = {0, 0, 0, 0}, w2[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        float t = rintf(v[i] * inv);
+        t = fminf(fmaxf(t, -kXGroupMax), kXGroupMax);
+        const int q = static_cast<int>(t);
+        const int d0 = static_cast<int>(static_cast<int8_t>(q & 0xff));
+        const int r = (q - d0) >> 8;
+        const int d1 = static_cast<int>(static_cast<int8_t>(r & 0xff));
+        const int d2 = (r - d1) >> 8;
+        const uint32_t sh = 8u * (i & 3);
+        w0[i >> 2] |= (static_cast<uint32_t>(d0) & 0xffu) << sh;
+        w1[i >> 2] |= (static_cast<uint32_t>(d1) & 0xffu) << sh;
+        w2[i >> 2] |= (static_cast<uint32_t>(d2) & 0xffu) << sh;
+    }
+    uint4* o = reinterpret_cast<uint4*>(g);
+    o[0] = make_uint4(w0[0], w0[1], w0[2], w0[3]);
+    o[1] = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+    o[2] = make_uint4(w2[0], w2[1], w2[2], w2[3]);
+    o[3] = make_uint4(__float_as_uint(sum), __float_as_uint(e), __float_as_uint(e * 256.0f),
+                      __float_as_uint(e * 65536.0f));
+}
+
+// Encodes group g from 16 floats at src (global or LDS, 16-byte aligned).
+__device__ __forceinline__ void xgroup_encode_from(const float* src, XGroup* __restrict__ g) {
+    float v[16];
+    const float4* p = reinterpret_cast<const float4*>(src);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 t = p[i];
+        v[4 * i] = t.x;
+        v[4 * i + 1] = t.y;
+        v[4 * i + 2] = t.z;
+        v[4 * i + 3] = t.w;
+    }
+    xgroup_encode(v, g);
+}
+
 }  // namespace hipllm

@@ -7,21 +7,25 @@
 #include <cstddef>
 #include <cstdint>
 
+#include "common.h"
+
 namespace hipllm {
 
 int launch_dequant_rows(uint32_t type, const void* w, size_t row_bytes, size_t rows, size_t k, float* out,
                         hipStream_t stream);
 
-int launch_prep_sums(const float* x, float* xs16, size_t k, hipStream_t stream);
+// GEMV inputs travel as FP32 values x plus their XGroup form xq (k / 16
+// groups, common.h); quantized weights read xq, F32 / F16 weights read x.
+int launch_prep_x(const float* x, XGroup* xq, size_t k, hipStream_t stream);
 int gemv_default_tiling(uint32_t n, uint32_t units, int mode, uint32_t vectors = 1);
-int launch_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* xs16,
+int launch_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const float* x, const XGroup* xq,
                         const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
                         hipStream_t stream);
 int launch_gemv_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
-                       const float* xs16, float* y, float* ys16, size_t n, size_t k, hipStream_t stream);
+                       const XGroup* xq, float* y, XGroup* yq, size_t n, size_t k, int tiling, hipStream_t stream);
 
 int launch_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row_bytes, const float* x,
-                        const float* xs16, const float* bias, const float* residual, float* y, float* ys16, size_t n,
+                        const XGroup* xq, const float* bias, const float* residual, float* y, XGroup* yq, size_t n,
                         size_t k, size_t vectors, const int32_t* ids, size_t experts, size_t routes,
                         size_t expert_stride, int x_routed, size_t ldx, size_t ldy, hipStream_t stream);
 
@@ -34,18 +38,18 @@ int launch_attn_prefill(const float* q, size_t q_stride, const float* kcache, co
                         size_t out_stride, size_t rows, size_t hq, size_t hkv, size_t d, size_t pos0, float scale,
                         hipStream_t stream);
 
-int launch_rmsnorm(const float* x, const float* gamma, float* y, float* ys16, size_t rows, size_t cols, float eps,
+int launch_rmsnorm(const float* x, const float* gamma, float* y, XGroup* yq, size_t rows, size_t cols, float eps,
                    hipStream_t stream);
 int launch_embed(uint32_t type, const void* table, size_t row_bytes, const int32_t* ids, size_t rows, size_t vocab,
                  size_t cols, float* out, hipStream_t stream);
 int launch_rope_kv(float* qkv, const float* cos_sin, size_t rot, size_t hq, size_t hkv, size_t d, size_t pos0,
                    size_t rows, size_t row_stride, float* kcache, float* vcache, hipStream_t stream);
 size_t attn_decode_scratch_floats(size_t hq, size_t d, size_t max_len);
-int launch_attn_decode(const float* q, const float* kcache, const float* vcache, float* out, float* out16,
+int launch_attn_decode(const float* q, const float* kcache, const float* vcache, float* out, XGroup* outq,
                        float* scratch, size_t hq, size_t hkv, size_t d, size_t len, float scale, hipStream_t stream);
 size_t argmax_scratch_bytes(size_t n);
 int launch_argmax(const float* x, size_t n, uint32_t* out, void* scratch, hipStream_t stream);
-int launch_swiglu(const float* g, const float* u, float* y, float* y16, size_t n, hipStream_t stream);
+int launch_swiglu(const float* g, const float* u, float* y, XGroup* yq, size_t n, hipStream_t stream);
 int launch_add(const float* a, const float* b, float* y, size_t n, hipStream_t stream);
 
 // qwen35moe operators (moe.hip).
@@ -63,11 +67,11 @@ int launch_gdn_scan(const float* q, const float* k, size_t ldqk, const float* v,
                     const float* beta, float* state, float* out, size_t ldo, size_t tokens, size_t value_heads,
                     size_t key_heads, size_t d, hipStream_t stream);
 int launch_gated_rmsnorm(const float* o, size_t ldo, const float* gamma, const float* z, size_t ldz, float* y,
-                         float* ys16, size_t ldy, size_t tokens, size_t heads, size_t d, float eps,
+                         XGroup* yq, size_t ldy, size_t tokens, size_t heads, size_t d, float eps,
                          hipStream_t stream);
 int launch_split_qgate_norm(const float* mixed, size_t ldm, const float* kv, size_t ldkv, const float* q_gamma,
                             const float* k_gamma, float* qkv, size_t ldqkv, float* gate, size_t ldg, size_t tokens,
                             size_t hq, size_t hkv, size_t d, float eps, hipStream_t stream);
-int launch_gate_mul(const float* a, const float* g, float* y, float* y16, size_t n, hipStream_t stream);
+int launch_gate_mul(const float* a, const float* g, float* y, XGroup* yq, size_t n, hipStream_t stream);
 
 }  // namespace hipllm

@@ -274,31 +274,33 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const float* __restrict__
 }
 
 // y = rmsnorm(o_head) * gamma * silu(z) per (row, value head); FP32 sum of
-// squares like the reference's per-head norm; ys16 (optional) per-16 sums.
+// squares like the reference's per-head norm; yq (optional) the XGroup form
+// of y.
 __global__ __launch_bounds__(64) void gated_rmsnorm_kernel(const float* __restrict__ o, uint32_t ldo,
                                                           const float* __restrict__ gamma,
                                                           const float* __restrict__ z, uint32_t ldz,
-                                                          float* __restrict__ y, float* __restrict__ ys16,
+                                                          float* __restrict__ y, XGroup* __restrict__ yq,
                                                           uint32_t ldy, uint32_t d, float eps) {
     const uint32_t t = blockIdx.x, h = blockIdx.y;
     const float* ov = o + static_cast<size_t>(t) * ldo + static_cast<size_t>(h) * d;
     const float* zv = z + static_cast<size_t>(t) * ldz + static_cast<size_t>(h) * d;
     float* yv = y + static_cast<size_t>(t) * ldy + static_cast<size_t>(h) * d;
+    __shared__ __align__(16) float vals[256];
     float ss = 0.0f;
     for (uint32_t i = threadIdx.x; i < d; i += 64) ss += ov[i] * ov[i];
     ss = warp_sum(ss);
     const float inv = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
     for (uint32_t i = threadIdx.x; i < d; i += 64) {
         const float zz = zv[i];
-        yv[i] = ov[i] * inv * gamma[i] * (zz * sigmoid_ref(zz));
+        const float v = ov[i] * inv * gamma[i] * (zz * sigmoid_ref(zz));
+        yv[i] = v;
+        vals[i] = v;
     }
-    if (ys16) {
+    if (yq) {
         __syncthreads();
         const uint32_t groups = d / 16;
         for (uint32_t g = threadIdx.x; g < groups; g += 64) {
-            float acc = 0.0f;
-            for (uint32_t i = 0; i < 16; ++i) acc += yv[16 * g + i];
-            ys16[static_cast<size_t>(t) * (ldy / 16) + static_cast<size_t>(h) * groups + g] = acc;
+            xgroup_encode_from(vals + 16 * g, yq + static_cast<size_t>(t) * (ldy / 16) + static_cast<size_t>(h) * groups + g);
         }
     }
 }
@@ -343,17 +345,17 @@ __global__ __launch_bounds__(64) void split_qgate_norm_kernel(const float* __res
 
 // y = a * sigmoid(g) per element, per-16 sums (optional) for the next GEMV.
 __global__ void gate_mul_kernel(const float* __restrict__ a, const float* __restrict__ g, float* __restrict__ y,
-                                float* __restrict__ y16, size_t n16) {
+                                XGroup* __restrict__ yq, size_t n16) {
     const size_t grp = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (grp >= n16) return;
-    float s = 0.0f;
+    float v[16];
+#pragma unroll
     for (uint32_t i = 0; i < 16; ++i) {
         const size_t idx = 16 * grp + i;
-        const float v = a[idx] * sigmoid_ref(g[idx]);
-        y[idx] = v;
-        s += v;
+        v[i] = a[idx] * sigmoid_ref(g[idx]);
+        y[idx] = v[i];
     }
-    if (y16) y16[grp] = s;
+    if (yq) xgroup_encode(v, yq + grp);
 }
 
 uint32_t blocks_for(size_t n, uint32_t threads) { return static_cast<uint32_t>((n + threads - 1) / threads); }
@@ -450,17 +452,17 @@ int launch_gdn_scan(const float* q, const float* k, size_t ldqk, const float* v,
 }
 
 int launch_gated_rmsnorm(const float* o, size_t ldo, const float* gamma, const float* z, size_t ldz, float* y,
-                         float* ys16, size_t ldy, size_t tokens, size_t heads, size_t d, float eps,
+                         XGroup* yq, size_t ldy, size_t tokens, size_t heads, size_t d, float eps,
                          hipStream_t stream) {
-    if (!o || !gamma || !z || !y || tokens == 0 || heads == 0 || d == 0 || ldo < heads * d || ldz < heads * d ||
-        ldy < heads * d || !(eps > 0.0f)) {
+    if (!o || !gamma || !z || !y || tokens == 0 || heads == 0 || d == 0 || d > 256 || ldo < heads * d ||
+        ldz < heads * d || ldy < heads * d || !(eps > 0.0f)) {
         return kInvalidArgument;
     }
-    if (ys16 && (d % 16 != 0 || ldy % 16 != 0)) return kInvalidArgument;
+    if (yq && (d % 16 != 0 || ldy % 16 != 0 || reinterpret_cast<uintptr_t>(yq) % 16 != 0)) return kInvalidArgument;
     if (tokens > 0x7fffffffull || heads > 65535) return kLengthError;
     hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3(static_cast<uint32_t>(tokens), static_cast<uint32_t>(heads)),
                        dim3(64), 0, stream, o, static_cast<uint32_t>(ldo), gamma, z, static_cast<uint32_t>(ldz), y,
-                       ys16, static_cast<uint32_t>(ldy), static_cast<uint32_t>(d), eps);
+                       yq, static_cast<uint32_t>(ldy), static_cast<uint32_t>(d), eps);
     return launched();
 }
 
@@ -480,11 +482,12 @@ int launch_split_qgate_norm(const float* mixed, size_t ldm, const float* kv, siz
     return launched();
 }
 
-int launch_gate_mul(const float* a, const float* g, float* y, float* y16, size_t n, hipStream_t stream) {
+int launch_gate_mul(const float* a, const float* g, float* y, XGroup* yq, size_t n, hipStream_t stream) {
     if (!a || !g || !y || n == 0 || n % 16 != 0) return kInvalidArgument;
+    if (yq && reinterpret_cast<uintptr_t>(yq) % 16 != 0) return kInvalidArgument;
     const size_t n16 = n / 16;
     if (n16 > 0x7fffffffull) return kLengthError;
-    hipLaunchKernelGGL(gate_mul_kernel, dim3(blocks_for(n16, 256)), dim3(256), 0, stream, a, g, y, y16, n16);
+    hipLaunchKernelGGL(gate_mul_kernel, dim3(blocks_for(n16, 256)), dim3(256), 0, stream, a, g, y, yq, n16);
     return launched();
 }
 

@@ -15,18 +15,30 @@ namespace {
 
 // ------------------------------------------------------------ RMSNorm
 // One block per row. y = x * (inv_rms * gamma) with inv_rms from a double
-// sum of squares, as CPULLM. Optionally writes per-16 sums of y (xs16) for
-// the GEMV that consumes y.
+// sum of squares, as CPULLM. Each thread owns whole 16-groups of the row, so
+// it also writes the XGroup form of y (yq, optional) that the next GEMV
+// consumes. The second pass re-reads x from cache.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
-                                                      float* __restrict__ y, float* __restrict__ ys16, uint32_t cols,
+                                                      float* __restrict__ y, XGroup* __restrict__ yq, uint32_t cols,
                                                       float eps) {
     const uint32_t row = blockIdx.x;
     const float* xr = x + static_cast<size_t>(row) * cols;
     float* yr = y + static_cast<size_t>(row) * cols;
+    const uint32_t groups = cols / 16;
+    const bool vec = (cols % 4 == 0);
     double ss = 0.0;
-    for (uint32_t i = threadIdx.x; i < cols; i += blockDim.x) {
-        const double v = xr[i];
-        ss += v * v;
+    if (vec) {
+        const float4* x4 = reinterpret_cast<const float4*>(xr);
+        for (uint32_t i = threadIdx.x; i < cols / 4; i += blockDim.x) {
+            const float4 v = x4[i];
+            ss += static_cast<double>(v.x) * v.x + static_cast<double>(v.y) * v.y +
+                  static_cast<double>(v.z) * v.z + static_cast<double>(v.w) * v.w;
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < cols; i += blockDim.x) {
+            const double v = xr[i];
+            ss += v * v;
+        }
     }
     ss = warp_sum_d(ss);
     __shared__ double part[8];
@@ -42,21 +54,28 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
     }
     __syncthreads();
     const float inv = inv_s;
-    // 16 consecutive elements per thread-step so the same thread also forms
-    // the per-16 sum.
-    const uint32_t groups = cols / 16;
-    for (uint32_t g = threadIdx.x; g < groups; g += blockDim.x) {
-        float s = 0.0f;
+    if (vec) {
+        for (uint32_t g = threadIdx.x; g < groups; g += blockDim.x) {
+            const float4* x4 = reinterpret_cast<const float4*>(xr + 16 * g);
+            const float4* g4 = reinterpret_cast<const float4*>(gamma + 16 * g);
+            float4* y4 = reinterpret_cast<float4*>(yr + 16 * g);
+            float v[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const uint32_t c = 16 * g + i;
-            const float v = xr[c] * (inv * gamma[c]);
-            yr[c] = v;
-            s += v;
+            for (int i = 0; i < 4; ++i) {
+                const float4 a = x4[i], b = g4[i];
+                const float4 o = make_float4(a.x * (inv * b.x), a.y * (inv * b.y), a.z * (inv * b.z), a.w * (inv * b.w));
+                y4[i] = o;
+                v[4 * i] = o.x;
+                v[4 * i + 1] = o.y;
+                v[4 * i + 2] = o.z;
+                v[4 * i + 3] = o.w;
+            }
+            if (yq) xgroup_encode(v, yq + static_cast<size_t>(row) * groups + g);
         }
-        if (ys16) ys16[static_cast<size_t>(row) * groups + g] = s;
+        for (uint32_t c = groups * 16 + threadIdx.x; c < cols; c += blockDim.x) yr[c] = xr[c] * (inv * gamma[c]);
+    } else {
+        for (uint32_t c = threadIdx.x; c < cols; c += blockDim.x) yr[c] = xr[c] * (inv * gamma[c]);
     }
-    for (uint32_t c = groups * 16 + threadIdx.x; c < cols; c += blockDim.x) yr[c] = xr[c] * (inv * gamma[c]);
 }
 
 // ------------------------------------------------------------ embedding
@@ -124,8 +143,8 @@ __global__ void rope_kv_kernel(float* __restrict__ qkv, const float2* __restrict
 // key, each a quarter of the head dims), and writes the chunk's running max
 // m, sum of exp l, and unnormalised p.V (D floats; threads split the chunk's
 // keys in 256 / D interleaved parts, reduced in LDS). Phase 2: one block per
-// head merges the chunks and writes the head output, plus per-16 sums of the
-// whole output vector for the next GEMV.
+// head merges the chunks and writes the head output, plus its XGroup form for
+// the next GEMV.
 constexpr uint32_t kAttnChunk = 64;
 
 __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restrict__ q, const float* __restrict__ kcache,
@@ -220,7 +239,7 @@ __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restri
 }
 
 __global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict__ part, float* __restrict__ out,
-                                                         float* __restrict__ out16, uint32_t d, uint32_t nchunks) {
+                                                         XGroup* __restrict__ outq, uint32_t d, uint32_t nchunks) {
     const uint32_t h = blockIdx.x;
     const float* ph = part + static_cast<size_t>(h) * nchunks * (d + 2);
     float M = -INFINITY;
@@ -228,7 +247,7 @@ __global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict
     float L = 0.0f;
     for (uint32_t c = 0; c < nchunks; ++c) L += ph[c * (d + 2) + 1] * expf(ph[c * (d + 2)] - M);
     const float invL = 1.0f / L;
-    __shared__ float vals[256];
+    __shared__ __align__(16) float vals[256];
     for (uint32_t i = threadIdx.x; i < d; i += blockDim.x) {
         float acc = 0.0f;
         for (uint32_t c = 0; c < nchunks; ++c) acc += ph[c * (d + 2) + 2 + i] * expf(ph[c * (d + 2)] - M);
@@ -237,11 +256,9 @@ __global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict
         vals[i] = v;
     }
     __syncthreads();
-    if (out16) {
+    if (outq) {
         for (uint32_t gI = threadIdx.x; gI < d / 16; gI += blockDim.x) {
-            float s = 0.0f;
-            for (int i = 0; i < 16; ++i) s += vals[16 * gI + i];
-            out16[h * (d / 16) + gI] = s;
+            xgroup_encode_from(vals + 16 * gI, outq + h * (d / 16) + gI);
         }
     }
 }
@@ -381,20 +398,24 @@ __global__ __launch_bounds__(256) void argmax_final(const float* __restrict__ pv
 
 // ------------------------------------------------------------ elementwise
 // y = silu(g) * u with the reference's sign-branched sigmoid
-// (cpu_llm.cpp:188-202); optional per-16 sums of y.
+// (cpu_llm.cpp:188-202), one thread per 16-group; optional XGroup form of y.
 __global__ void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ y,
-                              float* __restrict__ y16, uint32_t n) {
+                              XGroup* __restrict__ yq, uint32_t n) {
     const uint32_t grp = blockIdx.x * blockDim.x + threadIdx.x;
     if (grp * 16 >= n) return;
-    float s = 0.0f;
-    for (uint32_t i = 16 * grp; i < min(n, 16 * grp + 16); ++i) {
-        const float gate = g[i];
-        const float sig = gate >= 0.0f ? 1.0f / (1.0f + expf(-gate)) : expf(gate) / (1.0f + expf(gate));
-        const float v = gate * sig * u[i];
-        y[i] = v;
-        s += v;
+    float v[16];
+#pragma unroll
+    for (uint32_t k = 0; k < 16; ++k) {
+        const uint32_t i = 16 * grp + k;
+        v[k] = 0.0f;
+        if (i < n) {
+            const float gate = g[i];
+            const float sig = gate >= 0.0f ? 1.0f / (1.0f + expf(-gate)) : expf(gate) / (1.0f + expf(gate));
+            v[k] = gate * sig * u[i];
+            y[i] = v[k];
+        }
     }
-    if (y16) y16[grp] = s;
+    if (yq) xgroup_encode(v, yq + grp);
 }
 
 __global__ void add_kernel(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ y, size_t n) {
@@ -404,12 +425,16 @@ __global__ void add_kernel(const float* __restrict__ a, const float* __restrict_
 
 }  // namespace
 
-int launch_rmsnorm(const float* x, const float* gamma, float* y, float* ys16, size_t rows, size_t cols, float eps,
+int launch_rmsnorm(const float* x, const float* gamma, float* y, XGroup* yq, size_t rows, size_t cols, float eps,
                    hipStream_t stream) {
     if (!x || !gamma || !y || rows == 0 || cols == 0) return kInvalidArgument;
-    if (ys16 && cols % 16 != 0) return kInvalidArgument;
+    if (yq && (cols % 16 != 0 || reinterpret_cast<uintptr_t>(yq) % 16 != 0)) return kInvalidArgument;
+    if (cols % 4 == 0 && (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(y) % 16 != 0 ||
+                          reinterpret_cast<uintptr_t>(gamma) % 16 != 0)) {
+        return kInvalidArgument;
+    }
     if (!(eps > 0.0f)) return kInvalidArgument;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, stream, x, gamma, y, ys16,
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, stream, x, gamma, y, yq,
                        static_cast<uint32_t>(cols), eps);
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
@@ -442,7 +467,7 @@ size_t attn_decode_scratch_floats(size_t hq, size_t d, size_t max_len) {
     return hq * chunks * (d + 2);
 }
 
-int launch_attn_decode(const float* q, const float* kcache, const float* vcache, float* out, float* out16,
+int launch_attn_decode(const float* q, const float* kcache, const float* vcache, float* out, XGroup* outq,
                        float* scratch, size_t hq, size_t hkv, size_t d, size_t len, float scale, hipStream_t stream) {
     if (!q || !kcache || !vcache || !out || !scratch || len == 0 || hq == 0 || hkv == 0 || hq % hkv) {
         return kInvalidArgument;
@@ -453,7 +478,7 @@ int launch_attn_decode(const float* q, const float* kcache, const float* vcache,
     hipLaunchKernelGGL(attn_decode_partial, dim3(static_cast<uint32_t>(hq), nchunks), dim3(256), 0, stream, q, kcache,
                        vcache, scratch, static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv),
                        static_cast<uint32_t>(d), static_cast<uint32_t>(len), scale, nchunks);
-    hipLaunchKernelGGL(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out, out16,
+    hipLaunchKernelGGL(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out, outq,
                        static_cast<uint32_t>(d), nchunks);
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
@@ -489,10 +514,12 @@ int launch_argmax(const float* x, size_t n, uint32_t* out, void* scratch, hipStr
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
-int launch_swiglu(const float* g, const float* u, float* y, float* y16, size_t n, hipStream_t stream) {
-    if (!g || !u || !y || n == 0 || (y16 && n % 16 != 0)) return kInvalidArgument;
+int launch_swiglu(const float* g, const float* u, float* y, XGroup* yq, size_t n, hipStream_t stream) {
+    if (!g || !u || !y || n == 0 || (yq && (n % 16 != 0 || reinterpret_cast<uintptr_t>(yq) % 16 != 0))) {
+        return kInvalidArgument;
+    }
     const uint32_t groups = static_cast<uint32_t>((n + 15) / 16);
-    hipLaunchKernelGGL(swiglu_kernel, dim3((groups + 255) / 256), dim3(256), 0, stream, g, u, y, y16,
+    hipLaunchKernelGGL(swiglu_kernel, dim3((groups + 255) / 256), dim3(256), 0, stream, g, u, y, yq,
                        static_cast<uint32_t>(n));
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }

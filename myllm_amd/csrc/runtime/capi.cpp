@@ -79,34 +79,39 @@ int hipllm_dequant_rows(uint32_t type, const void* w, size_t row_bytes, size_t r
                   "hipllm_dequant_rows: invalid arguments or launch failure");
 }
 
-int hipllm_prep_sums(const float* x, float* xs16, size_t k, void* stream) {
-    return status(hipllm::launch_prep_sums(x, xs16, k, as_stream(stream)), "hipllm_prep_sums failed");
+static hipllm::XGroup* xg(void* p) { return static_cast<hipllm::XGroup*>(p); }
+static const hipllm::XGroup* xgc(const void* p) { return static_cast<const hipllm::XGroup*>(p); }
+
+int hipllm_prep_x(const float* x, void* xq, size_t k, void* stream) {
+    return status(hipllm::launch_prep_x(x, xg(xq), k, as_stream(stream)),
+                  "hipllm_prep_x: invalid arguments (k % 16 == 0, 16-byte aligned buffers) or launch failure");
 }
 
-size_t hipllm_gemv_workspace_bytes(size_t k) { return (k + 15) / 16 * sizeof(float); }
+size_t hipllm_gemv_workspace_bytes(size_t k) { return (k + 15) / 16 * sizeof(hipllm::XGroup); }
 
 int hipllm_gemv(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* bias, float* y,
                 size_t n, size_t k, void* workspace, void* stream) {
     if (!workspace) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_gemv: workspace is null");
-    float* xs16 = static_cast<float*>(workspace);
-    int rc = hipllm::launch_prep_sums(x, xs16, k, as_stream(stream));
+    hipllm::XGroup* xq = xg(workspace);
+    int rc = hipllm::launch_prep_x(x, xq, k, as_stream(stream));
     if (rc != hipllm::kOk) return status(rc, "hipllm_gemv: k must be a positive multiple of 16");
-    return status(hipllm::launch_gemv_prepped(type, w, row_bytes, x, xs16, bias, nullptr, y, n, k, 0,
+    return status(hipllm::launch_gemv_prepped(type, w, row_bytes, x, xq, bias, nullptr, y, n, k, 0,
                                               as_stream(stream)),
                   "hipllm_gemv: invalid arguments or launch failure");
 }
 
-int hipllm_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* xs16,
+int hipllm_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const float* x, const void* xq,
                         const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
                         void* stream) {
-    return status(hipllm::launch_gemv_prepped(type, w, row_bytes, x, xs16, bias, residual, y, n, k, tiling,
+    return status(hipllm::launch_gemv_prepped(type, w, row_bytes, x, xgc(xq), bias, residual, y, n, k, tiling,
                                               as_stream(stream)),
                   "hipllm_gemv_prepped: invalid arguments or launch failure");
 }
 
 int hipllm_gemv_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
-                       const float* xs16, float* y, float* ys16, size_t n, size_t k, void* stream) {
-    return status(hipllm::launch_gemv_swiglu(type, wg, wu, row_bytes, x, xs16, y, ys16, n, k, as_stream(stream)),
+                       const void* xq, float* y, void* yq, size_t n, size_t k, int tiling, void* stream) {
+    return status(hipllm::launch_gemv_swiglu(type, wg, wu, row_bytes, x, xgc(xq), y, xg(yq), n, k, tiling,
+                                             as_stream(stream)),
                   "hipllm_gemv_swiglu: invalid arguments or launch failure");
 }
 
@@ -134,9 +139,9 @@ int hipllm_gemm(uint32_t type, const void* w, size_t row_bytes, const float* x, 
                   "hipllm_gemm: invalid arguments (k % 128 == 0) or launch failure");
 }
 
-int hipllm_rmsnorm(const float* x, const float* gamma, float* y, float* ys16, size_t rows, size_t cols, float eps,
+int hipllm_rmsnorm(const float* x, const float* gamma, float* y, void* yq, size_t rows, size_t cols, float eps,
                    void* stream) {
-    return status(hipllm::launch_rmsnorm(x, gamma, y, ys16, rows, cols, eps, as_stream(stream)),
+    return status(hipllm::launch_rmsnorm(x, gamma, y, xg(yq), rows, cols, eps, as_stream(stream)),
                   "hipllm_rmsnorm: invalid arguments or launch failure");
 }
 
@@ -157,9 +162,9 @@ size_t hipllm_attn_decode_scratch_floats(size_t hq, size_t d, size_t max_len) {
     return hipllm::attn_decode_scratch_floats(hq, d, max_len);
 }
 
-int hipllm_attn_decode(const float* q, const float* kcache, const float* vcache, float* out, float* out16,
+int hipllm_attn_decode(const float* q, const float* kcache, const float* vcache, float* out, void* outq,
                        float* scratch, size_t hq, size_t hkv, size_t d, size_t len, float scale, void* stream) {
-    return status(hipllm::launch_attn_decode(q, kcache, vcache, out, out16, scratch, hq, hkv, d, len, scale,
+    return status(hipllm::launch_attn_decode(q, kcache, vcache, out, xg(outq), scratch, hq, hkv, d, len, scale,
                                              as_stream(stream)),
                   "hipllm_attn_decode: invalid arguments or launch failure");
 }
@@ -171,8 +176,8 @@ int hipllm_argmax(const float* x, size_t n, uint32_t* out, void* scratch, void* 
                   "hipllm_argmax: invalid arguments or launch failure");
 }
 
-int hipllm_swiglu(const float* g, const float* u, float* y, float* y16, size_t n, void* stream) {
-    return status(hipllm::launch_swiglu(g, u, y, y16, n, as_stream(stream)),
+int hipllm_swiglu(const float* g, const float* u, float* y, void* yq, size_t n, void* stream) {
+    return status(hipllm::launch_swiglu(g, u, y, xg(yq), n, as_stream(stream)),
                   "hipllm_swiglu: invalid arguments or launch failure");
 }
 
@@ -318,10 +323,11 @@ size_t hipllm_expert_cache_count(const HipllmModel* m) { return m && m->moe ? m-
 // ---------------------------------------------------------------- MoE kernels
 
 int hipllm_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row_bytes, const float* x,
-                        const float* xs16, const float* bias, const float* residual, float* y, float* ys16, size_t n,
+                        const void* xq, const float* bias, const float* residual, float* y, void* yq, size_t n,
                         size_t k, size_t vectors, const int32_t* ids, size_t experts, size_t routes,
                         size_t expert_stride, int x_routed, size_t ldx, size_t ldy, void* stream) {
-    return status(hipllm::launch_gemv_batched(type, w, wu, row_bytes, x, xs16, bias, residual, y, ys16, n, k, vectors,
+    return status(hipllm::launch_gemv_batched(type, w, wu, row_bytes, x, xgc(xq), bias, residual, y, xg(yq), n, k,
+                                              vectors,
                                               ids, experts, routes, expert_stride, x_routed, ldx, ldy,
                                               as_stream(stream)),
                   "hipllm_gemv_batched: invalid arguments or launch failure");
@@ -369,8 +375,8 @@ int hipllm_gdn_scan(const float* q, const float* k, size_t ldqk, const float* v,
 }
 
 int hipllm_gated_rmsnorm(const float* o, size_t ldo, const float* gamma, const float* z, size_t ldz, float* y,
-                         float* ys16, size_t ldy, size_t tokens, size_t heads, size_t d, float eps, void* stream) {
-    return status(hipllm::launch_gated_rmsnorm(o, ldo, gamma, z, ldz, y, ys16, ldy, tokens, heads, d, eps,
+                         void* yq, size_t ldy, size_t tokens, size_t heads, size_t d, float eps, void* stream) {
+    return status(hipllm::launch_gated_rmsnorm(o, ldo, gamma, z, ldz, y, xg(yq), ldy, tokens, heads, d, eps,
                                                as_stream(stream)),
                   "hipllm_gated_rmsnorm: invalid arguments or launch failure");
 }
@@ -383,8 +389,8 @@ int hipllm_split_qgate_norm(const float* mixed, size_t ldm, const float* kv, siz
                   "hipllm_split_qgate_norm: invalid arguments or launch failure");
 }
 
-int hipllm_gate_mul(const float* a, const float* g, float* y, float* y16, size_t n, void* stream) {
-    return status(hipllm::launch_gate_mul(a, g, y, y16, n, as_stream(stream)),
+int hipllm_gate_mul(const float* a, const float* g, float* y, void* yq, size_t n, void* stream) {
+    return status(hipllm::launch_gate_mul(a, g, y, xg(yq), n, as_stream(stream)),
                   "hipllm_gate_mul: invalid arguments (n % 16 == 0) or launch failure");
 }
 

@@ -3,11 +3,11 @@
 //
 // Per decode token (MetalLLM::decode, metal_llm.mm:3295-3385; layer graph
 // cpu_llm.cpp:843-914), all on one stream:
-//   embed -> L x [ rmsnorm(+xs16) -> QKV GEMV(+bias) -> RoPE + KV write
-//                  -> attention(+xs16) -> O GEMV(+residual)
-//                  -> rmsnorm(+xs16) -> gate/up GEMV + SwiGLU(+xs16)
+//   embed -> L x [ rmsnorm(+xq) -> QKV GEMV(+bias) -> RoPE + KV write
+//                  -> attention(+xq) -> O GEMV(+residual)
+//                  -> rmsnorm(+xq) -> gate/up GEMV + SwiGLU(+xq)
 //                  -> down GEMV(+residual) ]
-//   -> rmsnorm(+xs16) -> LM-head GEMV -> argmax -> 4-byte readback.
+//   -> rmsnorm(+xq) -> LM-head GEMV -> argmax -> 4-byte readback.
 #include "hip_llm.h"
 
 #include "../kernels/launch.h"
@@ -41,12 +41,12 @@ struct DevLayer {
 struct Activations {
     float* hidden[2] = {nullptr, nullptr};
     float* norm = nullptr;
-    float* norm16 = nullptr;
+    hipllm::XGroup* normq = nullptr;
     float* qkv = nullptr;
     float* attn = nullptr;
-    float* attn16 = nullptr;
+    hipllm::XGroup* attnq = nullptr;
     float* ffn = nullptr;
-    float* ffn16 = nullptr;
+    hipllm::XGroup* ffnq = nullptr;
     float* gate_tmp = nullptr;
     float* logits = nullptr;
     float* attn_scratch = nullptr;
@@ -127,7 +127,7 @@ struct HipLLM::Impl {
     void ensure_prefill_rows(std::size_t n);
     bool batched_shapes() const;
 
-    void gemv(const DevMatrix& w, const float* x, const float* xs16, const float* bias, const float* residual,
+    void gemv(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, const float* bias, const float* residual,
               float* y, std::size_t rows_override = 0) const;
     void layer_step(std::size_t li, std::size_t pos, float* hidden, float* next_hidden);
     void token_step(const std::int32_t* device_id, std::size_t pos, bool head);
@@ -288,9 +288,10 @@ void HipLLM::Impl::ensure_prompt_capacity(std::size_t n) {
         off = align_up(off + bytes, 256);
         return at;
     };
+    const std::size_t xg = sizeof(hipllm::XGroup);
     const std::size_t o_h0 = reserve(H * 4), o_h1 = reserve(H * 4), o_norm = reserve(H * 4),
-                      o_norm16 = reserve(H / 16 * 4), o_qkv = reserve(qkv * 4), o_attn = reserve(H * 4),
-                      o_attn16 = reserve(H / 16 * 4), o_ffn = reserve(F * 4), o_ffn16 = reserve(F / 16 * 4),
+                      o_normq = reserve(H / 16 * xg), o_qkv = reserve(qkv * 4), o_attn = reserve(H * 4),
+                      o_attnq = reserve(H / 16 * xg), o_ffn = reserve(F * 4), o_ffnq = reserve(F / 16 * xg),
                       o_gtmp = reserve(F * 4), o_logits = reserve(V * 4),
                       o_as = reserve(hipllm::attn_decode_scratch_floats(c.attention_head_count, c.head_size,
                                                                           max_sequence) * 4),
@@ -301,12 +302,12 @@ void HipLLM::Impl::ensure_prompt_capacity(std::size_t n) {
     act.hidden[0] = reinterpret_cast<float*>(base + o_h0);
     act.hidden[1] = reinterpret_cast<float*>(base + o_h1);
     act.norm = reinterpret_cast<float*>(base + o_norm);
-    act.norm16 = reinterpret_cast<float*>(base + o_norm16);
+    act.normq = reinterpret_cast<hipllm::XGroup*>(base + o_normq);
     act.qkv = reinterpret_cast<float*>(base + o_qkv);
     act.attn = reinterpret_cast<float*>(base + o_attn);
-    act.attn16 = reinterpret_cast<float*>(base + o_attn16);
+    act.attnq = reinterpret_cast<hipllm::XGroup*>(base + o_attnq);
     act.ffn = reinterpret_cast<float*>(base + o_ffn);
-    act.ffn16 = reinterpret_cast<float*>(base + o_ffn16);
+    act.ffnq = reinterpret_cast<hipllm::XGroup*>(base + o_ffnq);
     act.gate_tmp = reinterpret_cast<float*>(base + o_gtmp);
     act.logits = reinterpret_cast<float*>(base + o_logits);
     act.attn_scratch = reinterpret_cast<float*>(base + o_as);
@@ -339,10 +340,10 @@ void HipLLM::Impl::build_rope_table() {
               "hipMemcpy(RoPE)");
 }
 
-void HipLLM::Impl::gemv(const DevMatrix& w, const float* x, const float* xs16, const float* bias,
+void HipLLM::Impl::gemv(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, const float* bias,
                         const float* residual, float* y, std::size_t rows_override) const {
     const std::size_t n = rows_override ? rows_override : w.rows;
-    launch_check(hipllm::launch_gemv_prepped(w.type, w.ptr, w.row_bytes, x, xs16, bias, residual, y, n, w.cols, 0,
+    launch_check(hipllm::launch_gemv_prepped(w.type, w.ptr, w.row_bytes, x, xq, bias, residual, y, n, w.cols, 0,
                                              stream),
                  "GEMV");
 }
@@ -352,37 +353,37 @@ void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, fl
     const DevLayer& L = layers[li];
     const std::size_t H = c.embedding_size, F = c.feed_forward_size;
     const float eps = c.norm_epsilon;
-    launch_check(hipllm::launch_rmsnorm(hidden, L.attn_norm, act.norm, act.norm16, 1, H, eps, stream), "RMSNorm");
+    launch_check(hipllm::launch_rmsnorm(hidden, L.attn_norm, act.norm, act.normq, 1, H, eps, stream), "RMSNorm");
     if (L.fused_qkv) {
-        gemv(L.q, act.norm, act.norm16, L.qkv_bias, nullptr, act.qkv, H + 2 * kv_dim);
+        gemv(L.q, act.norm, act.normq, L.qkv_bias, nullptr, act.qkv, H + 2 * kv_dim);
     } else {
-        gemv(L.q, act.norm, act.norm16, L.qkv_bias, nullptr, act.qkv);
-        gemv(L.k, act.norm, act.norm16, L.qkv_bias + H, nullptr, act.qkv + H);
-        gemv(L.v, act.norm, act.norm16, L.qkv_bias + H + kv_dim, nullptr, act.qkv + H + kv_dim);
+        gemv(L.q, act.norm, act.normq, L.qkv_bias, nullptr, act.qkv);
+        gemv(L.k, act.norm, act.normq, L.qkv_bias + H, nullptr, act.qkv + H);
+        gemv(L.v, act.norm, act.normq, L.qkv_bias + H + kv_dim, nullptr, act.qkv + H + kv_dim);
     }
     launch_check(hipllm::launch_rope_kv(act.qkv, rope_table, c.rotary_dimension, c.attention_head_count,
                                         c.kv_head_count, c.head_size, pos, 1, H + 2 * kv_dim, kcache(li), vcache(li),
                                         stream),
                  "RoPE/KV write");
     const float scale = 1.0f / std::sqrt(static_cast<float>(c.head_size));
-    launch_check(hipllm::launch_attn_decode(act.qkv, kcache(li), vcache(li), act.attn, act.attn16, act.attn_scratch,
+    launch_check(hipllm::launch_attn_decode(act.qkv, kcache(li), vcache(li), act.attn, act.attnq, act.attn_scratch,
                                             c.attention_head_count, c.kv_head_count, c.head_size, pos + 1, scale,
                                             stream),
                  "attention");
-    gemv(L.o, act.attn, act.attn16, nullptr, hidden, next_hidden);
-    launch_check(hipllm::launch_rmsnorm(next_hidden, L.ffn_norm, act.norm, act.norm16, 1, H, eps, stream), "RMSNorm");
+    gemv(L.o, act.attn, act.attnq, nullptr, hidden, next_hidden);
+    launch_check(hipllm::launch_rmsnorm(next_hidden, L.ffn_norm, act.norm, act.normq, 1, H, eps, stream), "RMSNorm");
     if (L.fused_gate_up) {
         launch_check(hipllm::launch_gemv_swiglu(L.gate.type, L.gate.ptr, L.up.ptr, L.gate.row_bytes, act.norm,
-                                                act.norm16, act.ffn, act.ffn16, F, H, stream),
+                                                act.normq, act.ffn, act.ffnq, F, H, 0, stream),
                      "gate/up GEMV");
     } else {
         // Gate and up in different formats: two GEMVs, then SwiGLU.
-        gemv(L.gate, act.norm, act.norm16, nullptr, nullptr, act.gate_tmp);
-        gemv(L.up, act.norm, act.norm16, nullptr, nullptr, act.ffn);
-        launch_check(hipllm::launch_swiglu(act.gate_tmp, act.ffn, act.ffn, act.ffn16, F, stream), "SwiGLU");
+        gemv(L.gate, act.norm, act.normq, nullptr, nullptr, act.gate_tmp);
+        gemv(L.up, act.norm, act.normq, nullptr, nullptr, act.ffn);
+        launch_check(hipllm::launch_swiglu(act.gate_tmp, act.ffn, act.ffn, act.ffnq, F, stream), "SwiGLU");
     }
     // The layer output lands back in `hidden`.
-    gemv(L.down, act.ffn, act.ffn16, nullptr, next_hidden, hidden);
+    gemv(L.down, act.ffn, act.ffnq, nullptr, next_hidden, hidden);
 }
 
 void HipLLM::Impl::token_step(const std::int32_t* device_id, std::size_t pos, bool head) {
@@ -482,10 +483,10 @@ void HipLLM::Impl::prefill_layer(std::size_t li, std::size_t rows, float* hidden
 // Final norm, LM head and argmax on one hidden row (decode kernels).
 void HipLLM::Impl::head_step(const float* hidden_row) {
     const ModelConfig& c = config;
-    launch_check(hipllm::launch_rmsnorm(hidden_row, output_norm, act.norm, act.norm16, 1, c.embedding_size,
+    launch_check(hipllm::launch_rmsnorm(hidden_row, output_norm, act.norm, act.normq, 1, c.embedding_size,
                                         c.norm_epsilon, stream),
                  "final RMSNorm");
-    gemv(output, act.norm, act.norm16, nullptr, nullptr, act.logits);
+    gemv(output, act.norm, act.normq, nullptr, nullptr, act.logits);
     launch_check(hipllm::launch_argmax(act.logits, c.vocabulary_size, act.token, act.argmax_scratch, stream),
                  "argmax");
 }

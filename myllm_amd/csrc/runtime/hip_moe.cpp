@@ -59,24 +59,24 @@ struct MoeLayer {
 struct MoeActivations {
     float* hidden[2] = {nullptr, nullptr};  // [T, H]
     float* norm = nullptr;                  // [T, H]
-    float* norm16 = nullptr;                // [T, H / 16]
+    hipllm::XGroup* normq = nullptr;        // [T, H / 16] XGroup form of norm
     float* wide = nullptr;                  // [T, max(2 Hq D, qkv_w)]  Q+gate mix / DeltaNet QKV
     float* wide2 = nullptr;                 // [T, max((Hq + 2 Hkv) D, qkv_w)]  attention QKV / conv output
     float* kv = nullptr;                    // [T, 2 Hkv D]
     float* feat = nullptr;                  // [T, max(Hq D, inner)]  attention gate / DeltaNet z
     float* feat2 = nullptr;                 // [T, max(Hq D, inner)]  attention / recurrence output
     float* gated = nullptr;                 // [T, max(Hq D, inner)]
-    float* gated16 = nullptr;
+    hipllm::XGroup* gatedq = nullptr;
     float* ab = nullptr;                    // [T, 2 Hv]
     float* decay = nullptr;                 // [T, Hv]
     float* beta = nullptr;                  // [T, Hv]
     float* rlog = nullptr;                  // [T, E + 1] router logits | shared gate
     float* rweight = nullptr;               // [T, k]
     float* act = nullptr;                   // [T k, FF]
-    float* act16 = nullptr;
+    hipllm::XGroup* actq = nullptr;
     float* down = nullptr;                  // [T k, H]
     float* sh_act = nullptr;                // [T, FFs]
-    float* sh_act16 = nullptr;
+    hipllm::XGroup* sh_actq = nullptr;
     float* sh_down = nullptr;               // [T, H]
     float* logits = nullptr;                // [V]
     float* attn_scratch = nullptr;
@@ -140,7 +140,7 @@ struct HipMoeLLM::Impl {
     void zero_state();
     void ensure_rows(std::size_t rows);
 
-    void proj(const DevMatrix& w, const float* x, const float* x16, std::size_t ldx, std::size_t rows, float* y,
+    void proj(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, std::size_t ldx, std::size_t rows, float* y,
               std::size_t ldy, const float* residual = nullptr, std::size_t n_override = 0) const;
     void attention_layer(std::size_t li, std::size_t rows, std::size_t pos0, float* hidden, float* next);
     void deltanet_layer(std::size_t li, std::size_t rows, float* hidden, float* next);
@@ -430,12 +430,12 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
         return at;
     };
     const std::size_t o_h0 = reserve(n * H), o_h1 = reserve(n * H), o_norm = reserve(n * H),
-                      o_norm16 = reserve(n * H / 16), o_wide = reserve(n * wide), o_wide2 = reserve(n * wide2),
+                      o_normq = reserve(n * H), o_wide = reserve(n * wide), o_wide2 = reserve(n * wide2),
                       o_kv = reserve(n * 2 * kv_w), o_feat = reserve(n * feat), o_feat2 = reserve(n * feat),
-                      o_gated = reserve(n * feat), o_gated16 = reserve(n * feat / 16), o_ab = reserve(n * 2 * Hv),
+                      o_gated = reserve(n * feat), o_gatedq = reserve(n * feat), o_ab = reserve(n * 2 * Hv),
                       o_decay = reserve(n * Hv), o_beta = reserve(n * Hv), o_rlog = reserve(n * (E + 1)),
-                      o_rw = reserve(n * K), o_act = reserve(n * K * FF), o_act16 = reserve(n * K * FF / 16),
-                      o_down = reserve(n * K * H), o_sha = reserve(n * FFs), o_sha16 = reserve(n * FFs / 16),
+                      o_rw = reserve(n * K), o_act = reserve(n * K * FF), o_actq = reserve(n * K * FF),
+                      o_down = reserve(n * K * H), o_sha = reserve(n * FFs), o_shaq = reserve(n * FFs),
                       o_shd = reserve(n * H), o_logits = reserve(config.vocabulary_size),
                       o_as = reserve(hipllm::attn_decode_scratch_floats(Hq, D, capacity)),
                       o_am = reserve(hipllm::argmax_scratch_bytes(config.vocabulary_size) / 4 + 1),
@@ -444,27 +444,28 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
     hip_check(hipMalloc(&act_arena, act_bytes), "hipMalloc(MoE activations)");
     auto* b = static_cast<std::uint8_t*>(act_arena);
     auto f = [&](std::size_t o) { return reinterpret_cast<float*>(b + o); };
+    auto g = [&](std::size_t o) { return reinterpret_cast<hipllm::XGroup*>(b + o); };  // 16 floats per group
     act.hidden[0] = f(o_h0);
     act.hidden[1] = f(o_h1);
     act.norm = f(o_norm);
-    act.norm16 = f(o_norm16);
+    act.normq = g(o_normq);
     act.wide = f(o_wide);
     act.wide2 = f(o_wide2);
     act.kv = f(o_kv);
     act.feat = f(o_feat);
     act.feat2 = f(o_feat2);
     act.gated = f(o_gated);
-    act.gated16 = f(o_gated16);
+    act.gatedq = g(o_gatedq);
     act.ab = f(o_ab);
     act.decay = f(o_decay);
     act.beta = f(o_beta);
     act.rlog = f(o_rlog);
     act.rweight = f(o_rw);
     act.act = f(o_act);
-    act.act16 = f(o_act16);
+    act.actq = g(o_actq);
     act.down = f(o_down);
     act.sh_act = f(o_sha);
-    act.sh_act16 = f(o_sha16);
+    act.sh_actq = g(o_shaq);
     act.sh_down = f(o_shd);
     act.logits = f(o_logits);
     act.attn_scratch = f(o_as);
@@ -477,16 +478,16 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
 }
 
 // y[rows, :] = W x[rows, :] (+ residual); one GEMV per row, batched over rows.
-void HipMoeLLM::Impl::proj(const DevMatrix& w, const float* x, const float* x16, std::size_t ldx, std::size_t rows,
+void HipMoeLLM::Impl::proj(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, std::size_t ldx, std::size_t rows,
                            float* y, std::size_t ldy, const float* residual, std::size_t n_override) const {
     const std::size_t n = n_override ? n_override : w.rows;
     if (rows == 1) {
-        launch_check(hipllm::launch_gemv_prepped(w.type, w.ptr, w.row_bytes, x, x16, nullptr, residual, y, n, w.cols,
+        launch_check(hipllm::launch_gemv_prepped(w.type, w.ptr, w.row_bytes, x, xq, nullptr, residual, y, n, w.cols,
                                                  0, stream),
                      "GEMV");
         return;
     }
-    launch_check(hipllm::launch_gemv_batched(w.type, w.ptr, nullptr, w.row_bytes, x, x16, nullptr, residual, y,
+    launch_check(hipllm::launch_gemv_batched(w.type, w.ptr, nullptr, w.row_bytes, x, xq, nullptr, residual, y,
                                              nullptr, n, w.cols, rows, nullptr, 1, 1, 0, 0, ldx, ldy, stream),
                  "batched GEMV");
 }
@@ -498,17 +499,17 @@ void HipMoeLLM::Impl::attention_layer(std::size_t li, std::size_t rows, std::siz
     const MoeLayer& L = layers[li];
     const float eps = config.norm_epsilon;
     const std::size_t ldqkv = q_w + 2 * kv_w;
-    proj(L.qgate, act.norm, act.norm16, H, rows, act.wide, 2 * q_w);
+    proj(L.qgate, act.norm, act.normq, H, rows, act.wide, 2 * q_w);
     if (L.fused_kv) {
-        proj(L.k, act.norm, act.norm16, H, rows, act.kv, 2 * kv_w, nullptr, 2 * kv_w);
+        proj(L.k, act.norm, act.normq, H, rows, act.kv, 2 * kv_w, nullptr, 2 * kv_w);
     } else {
-        proj(L.k, act.norm, act.norm16, H, rows, act.kv, 2 * kv_w);
+        proj(L.k, act.norm, act.normq, H, rows, act.kv, 2 * kv_w);
         // V rows land after K in each row; batched rows need ldy = 2 kv_w.
         if (rows == 1) {
-            proj(L.v, act.norm, act.norm16, H, rows, act.kv + kv_w, 2 * kv_w);
+            proj(L.v, act.norm, act.normq, H, rows, act.kv + kv_w, 2 * kv_w);
         } else {
             launch_check(hipllm::launch_gemv_batched(L.v.type, L.v.ptr, nullptr, L.v.row_bytes, act.norm,
-                                                     act.norm16, nullptr, nullptr, act.kv + kv_w, nullptr, kv_w, H,
+                                                     act.normq, nullptr, nullptr, act.kv + kv_w, nullptr, kv_w, H,
                                                      rows, nullptr, 1, 1, 0, 0, H, 2 * kv_w, stream),
                          "batched GEMV");
         }
@@ -529,26 +530,26 @@ void HipMoeLLM::Impl::attention_layer(std::size_t li, std::size_t rows, std::siz
                                                  D, pos0, scale, stream),
                      "prefill attention");
     }
-    launch_check(hipllm::launch_gate_mul(act.feat2, act.feat, act.gated, act.gated16, rows * q_w, stream),
+    launch_check(hipllm::launch_gate_mul(act.feat2, act.feat, act.gated, act.gatedq, rows * q_w, stream),
                  "attention output gate");
-    proj(L.o, act.gated, act.gated16, q_w, rows, next, H, hidden);
+    proj(L.o, act.gated, act.gatedq, q_w, rows, next, H, hidden);
 }
 
 // Gated DeltaNet (moe_llm.mm:2436-2640); next = hidden + out_proj(...).
 void HipMoeLLM::Impl::deltanet_layer(std::size_t li, std::size_t rows, float* hidden, float* next) {
     const MoeLayer& L = layers[li];
     const float eps = config.norm_epsilon;
-    proj(L.qkv, act.norm, act.norm16, H, rows, act.wide, qkv_w);
-    proj(L.z, act.norm, act.norm16, H, rows, act.feat, inner);
+    proj(L.qkv, act.norm, act.normq, H, rows, act.wide, qkv_w);
+    proj(L.z, act.norm, act.normq, H, rows, act.feat, inner);
     if (L.fused_ab) {
-        proj(L.alpha, act.norm, act.norm16, H, rows, act.ab, 2 * Hv, nullptr, 2 * Hv);
+        proj(L.alpha, act.norm, act.normq, H, rows, act.ab, 2 * Hv, nullptr, 2 * Hv);
     } else if (rows == 1) {
-        proj(L.alpha, act.norm, act.norm16, H, rows, act.ab, 2 * Hv);
-        proj(L.beta, act.norm, act.norm16, H, rows, act.ab + Hv, 2 * Hv);
+        proj(L.alpha, act.norm, act.normq, H, rows, act.ab, 2 * Hv);
+        proj(L.beta, act.norm, act.normq, H, rows, act.ab + Hv, 2 * Hv);
     } else {
-        proj(L.alpha, act.norm, act.norm16, H, rows, act.ab, 2 * Hv);
+        proj(L.alpha, act.norm, act.normq, H, rows, act.ab, 2 * Hv);
         launch_check(hipllm::launch_gemv_batched(L.beta.type, L.beta.ptr, nullptr, L.beta.row_bytes, act.norm,
-                                                 act.norm16, nullptr, nullptr, act.ab + Hv, nullptr, Hv, H, rows,
+                                                 act.normq, nullptr, nullptr, act.ab + Hv, nullptr, Hv, H, rows,
                                                  nullptr, 1, 1, 0, 0, H, 2 * Hv, stream),
                      "batched GEMV");
     }
@@ -563,10 +564,10 @@ void HipMoeLLM::Impl::deltanet_layer(std::size_t li, std::size_t rows, float* hi
     launch_check(hipllm::launch_gdn_scan(act.wide2, act.wide2 + G * S, qkv_w, act.wide2 + 2 * G * S, qkv_w, act.decay,
                                          act.beta, L.state, act.feat2, inner, rows, Hv, G, S, stream),
                  "DeltaNet scan");
-    launch_check(hipllm::launch_gated_rmsnorm(act.feat2, inner, L.ssm_norm, act.feat, inner, act.gated, act.gated16,
+    launch_check(hipllm::launch_gated_rmsnorm(act.feat2, inner, L.ssm_norm, act.feat, inner, act.gated, act.gatedq,
                                               inner, rows, Hv, S, eps, stream),
                  "DeltaNet gated norm");
-    proj(L.ssm_out, act.gated, act.gated16, inner, rows, next, H, hidden);
+    proj(L.ssm_out, act.gated, act.gatedq, inner, rows, next, H, hidden);
 }
 
 // MoE FFN (moe_llm.mm:2642-2843): `hidden` is the attention residual; the
@@ -577,18 +578,18 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
     // Router logits and the shared-expert gate in one GEMV when packed.
     const std::size_t ldr = E + 1;
     if (L.fused_router) {
-        proj(L.router, act.norm, act.norm16, H, rows, act.rlog, ldr, nullptr, E + 1);
+        proj(L.router, act.norm, act.normq, H, rows, act.rlog, ldr, nullptr, E + 1);
     } else {
         if (rows == 1) {
-            proj(L.router, act.norm, act.norm16, H, rows, act.rlog, ldr);
-            proj(L.shexp_router, act.norm, act.norm16, H, rows, act.rlog + E, ldr);
+            proj(L.router, act.norm, act.normq, H, rows, act.rlog, ldr);
+            proj(L.shexp_router, act.norm, act.normq, H, rows, act.rlog + E, ldr);
         } else {
             launch_check(hipllm::launch_gemv_batched(L.router.type, L.router.ptr, nullptr, L.router.row_bytes,
-                                                     act.norm, act.norm16, nullptr, nullptr, act.rlog, nullptr, E, H,
+                                                     act.norm, act.normq, nullptr, nullptr, act.rlog, nullptr, E, H,
                                                      rows, nullptr, 1, 1, 0, 0, H, ldr, stream),
                          "router GEMV");
             launch_check(hipllm::launch_gemv_batched(L.shexp_router.type, L.shexp_router.ptr, nullptr,
-                                                     L.shexp_router.row_bytes, act.norm, act.norm16, nullptr, nullptr,
+                                                     L.shexp_router.row_bytes, act.norm, act.normq, nullptr, nullptr,
                                                      act.rlog + E, nullptr, 1, H, rows, nullptr, 1, 1, 0, 0, H, ldr,
                                                      stream),
                          "shared gate GEMV");
@@ -597,26 +598,26 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
     launch_check(hipllm::launch_router_topk(act.rlog, ldr, rows, E, K, ids, act.rweight, stream), "router top-k");
     // Routed experts: gate/up + SwiGLU for every (row, route), then down.
     launch_check(hipllm::launch_gemv_batched(L.gate_exps.type, L.gate_exps.ptr, L.up_exps.ptr, L.gate_exps.row_bytes,
-                                             act.norm, act.norm16, nullptr, nullptr, act.act, act.act16, FF, H,
+                                             act.norm, act.normq, nullptr, nullptr, act.act, act.actq, FF, H,
                                              rows * K, ids, E, K, L.gate_exps.expert_stride, 0, H, FF, stream),
                  "expert gate/up");
     launch_check(hipllm::launch_gemv_batched(L.down_exps.type, L.down_exps.ptr, nullptr, L.down_exps.row_bytes,
-                                             act.act, act.act16, nullptr, nullptr, act.down, nullptr, H, FF, rows * K,
+                                             act.act, act.actq, nullptr, nullptr, act.down, nullptr, H, FF, rows * K,
                                              ids, E, K, L.down_exps.expert_stride, 1, FF, H, stream),
                  "expert down");
     // Shared expert.
     if (L.sh_gate.type == L.sh_up.type) {
         launch_check(hipllm::launch_gemv_batched(L.sh_gate.type, L.sh_gate.ptr, L.sh_up.ptr, L.sh_gate.row_bytes,
-                                                 act.norm, act.norm16, nullptr, nullptr, act.sh_act, act.sh_act16, FFs,
+                                                 act.norm, act.normq, nullptr, nullptr, act.sh_act, act.sh_actq, FFs,
                                                  H, rows, nullptr, 1, 1, 0, 0, H, FFs, stream),
                      "shared gate/up");
     } else {
-        proj(L.sh_gate, act.norm, act.norm16, H, rows, act.sh_down, FFs);
-        proj(L.sh_up, act.norm, act.norm16, H, rows, act.sh_act, FFs);
-        launch_check(hipllm::launch_swiglu(act.sh_down, act.sh_act, act.sh_act, act.sh_act16, rows * FFs, stream),
+        proj(L.sh_gate, act.norm, act.normq, H, rows, act.sh_down, FFs);
+        proj(L.sh_up, act.norm, act.normq, H, rows, act.sh_act, FFs);
+        launch_check(hipllm::launch_swiglu(act.sh_down, act.sh_act, act.sh_act, act.sh_actq, rows * FFs, stream),
                      "shared SwiGLU");
     }
-    proj(L.sh_down, act.sh_act, act.sh_act16, FFs, rows, act.sh_down, H);
+    proj(L.sh_down, act.sh_act, act.sh_actq, FFs, rows, act.sh_down, H);
     launch_check(hipllm::launch_moe_combine(hidden, act.down, act.rweight, act.sh_down, act.rlog + E, ldr, next, rows,
                                             H, K, stream),
                  "MoE combine");
@@ -631,18 +632,18 @@ void HipMoeLLM::Impl::forward(std::size_t rows, std::size_t pos0) {
                  "embedding");
     for (std::size_t l = 0; l < layers.size(); ++l) {
         const MoeLayer& L = layers[l];
-        launch_check(hipllm::launch_rmsnorm(h, L.attn_norm, act.norm, act.norm16, rows, H, eps, stream), "RMSNorm");
+        launch_check(hipllm::launch_rmsnorm(h, L.attn_norm, act.norm, act.normq, rows, H, eps, stream), "RMSNorm");
         if (L.full) {
             attention_layer(l, rows, pos0, h, tmp);
         } else {
             deltanet_layer(l, rows, h, tmp);
         }
-        launch_check(hipllm::launch_rmsnorm(tmp, L.post_norm, act.norm, act.norm16, rows, H, eps, stream), "RMSNorm");
+        launch_check(hipllm::launch_rmsnorm(tmp, L.post_norm, act.norm, act.normq, rows, H, eps, stream), "RMSNorm");
         moe_layer(l, rows, tmp, h);
     }
     const float* last = h + (rows - 1) * H;
-    launch_check(hipllm::launch_rmsnorm(last, output_norm, act.norm, act.norm16, 1, H, eps, stream), "final RMSNorm");
-    launch_check(hipllm::launch_gemv_prepped(output.type, output.ptr, output.row_bytes, act.norm, act.norm16, nullptr,
+    launch_check(hipllm::launch_rmsnorm(last, output_norm, act.norm, act.normq, 1, H, eps, stream), "final RMSNorm");
+    launch_check(hipllm::launch_gemv_prepped(output.type, output.ptr, output.row_bytes, act.norm, act.normq, nullptr,
                                              nullptr, act.logits, config.vocabulary_size, H, 0, stream),
                  "LM head");
     launch_check(hipllm::launch_argmax(act.logits, config.vocabulary_size, act.token, act.argmax_scratch, stream),

@@ -66,11 +66,11 @@ SIGNATURES = {
     "hipllm_last_error": (ctypes.c_char_p, []),
     "hipllm_version": (ctypes.c_char_p, []),
     "hipllm_dequant_rows": (_I, [_U32, _P, _S, _S, _S, _P, _P]),
-    "hipllm_prep_sums": (_I, [_P, _P, _S, _P]),
+    "hipllm_prep_x": (_I, [_P, _P, _S, _P]),
     "hipllm_gemv_workspace_bytes": (_S, [_S]),
     "hipllm_gemv": (_I, [_U32, _P, _S, _P, _P, _P, _S, _S, _P, _P]),
     "hipllm_gemv_prepped": (_I, [_U32, _P, _S, _P, _P, _P, _P, _P, _S, _S, _I, _P]),
-    "hipllm_gemv_swiglu": (_I, [_U32, _P, _P, _S, _P, _P, _P, _P, _S, _S, _P]),
+    "hipllm_gemv_swiglu": (_I, [_U32, _P, _P, _S, _P, _P, _P, _P, _S, _S, _I, _P]),
     "hipllm_to_bf16": (_I, [_P, _S, _P, _S, _S, _P]),
     "hipllm_gemm_mfma": (_I, [_U32, _P, _S, _P, _P, _P, _P, _S, _S, _S, _I, _P]),
     "hipllm_gemm_workspace_bytes": (_S, [_S, _S]),
@@ -286,8 +286,9 @@ def _k_dequant_rows(qtype, w, row_bytes, rows, k, out, stream=None):
     check(lib().hipllm_dequant_rows(qtype, _ptr(w), row_bytes, rows, k, _ptr(out), _stream(stream)))
 
 
-def _k_prep_sums(x, xs16, k, stream=None):
-    check(lib().hipllm_prep_sums(_ptr(x), _ptr(xs16), k, _stream(stream)))
+def _k_prep_x(x, xq, k, stream=None):
+    """XGroup form of x into xq (k / 16 groups of 64 bytes: allocate k float32s)."""
+    check(lib().hipllm_prep_x(_ptr(x), _ptr(xq), k, _stream(stream)))
 
 
 def _k_gemv(qtype, w, row_bytes, x, bias, y, n, k, workspace, stream=None):
@@ -295,14 +296,14 @@ def _k_gemv(qtype, w, row_bytes, x, bias, y, n, k, workspace, stream=None):
                             _stream(stream)))
 
 
-def _k_gemv_prepped(qtype, w, row_bytes, x, xs16, bias, residual, y, n, k, tiling=0, stream=None):
-    check(lib().hipllm_gemv_prepped(qtype, _ptr(w), row_bytes, _ptr(x), _ptr(xs16), _ptr(bias), _ptr(residual),
+def _k_gemv_prepped(qtype, w, row_bytes, x, xq, bias, residual, y, n, k, tiling=0, stream=None):
+    check(lib().hipllm_gemv_prepped(qtype, _ptr(w), row_bytes, _ptr(x), _ptr(xq), _ptr(bias), _ptr(residual),
                                     _ptr(y), n, k, tiling, _stream(stream)))
 
 
-def _k_gemv_swiglu(qtype, wg, wu, row_bytes, x, xs16, y, ys16, n, k, stream=None):
-    check(lib().hipllm_gemv_swiglu(qtype, _ptr(wg), _ptr(wu), row_bytes, _ptr(x), _ptr(xs16), _ptr(y), _ptr(ys16),
-                                   n, k, _stream(stream)))
+def _k_gemv_swiglu(qtype, wg, wu, row_bytes, x, xq, y, yq, n, k, tiling=0, stream=None):
+    check(lib().hipllm_gemv_swiglu(qtype, _ptr(wg), _ptr(wu), row_bytes, _ptr(x), _ptr(xq), _ptr(y), _ptr(yq),
+                                   n, k, tiling, _stream(stream)))
 
 
 def _k_to_bf16(x, ldx, xb, m, k, stream=None):
@@ -324,10 +325,10 @@ def _k_attn_prefill(q, q_stride, kcache, vcache, out, out_stride, rows, hq, hkv,
                                     hkv, d, pos0, scale, _stream(stream)))
 
 
-def _k_gemv_batched(qtype, w, wu, row_bytes, x, xs16, bias, residual, y, ys16, n, k, vectors, ids=None,
+def _k_gemv_batched(qtype, w, wu, row_bytes, x, xq, bias, residual, y, yq, n, k, vectors, ids=None,
                     experts=1, routes=1, expert_stride=0, x_routed=False, ldx=None, ldy=None, stream=None):
-    check(lib().hipllm_gemv_batched(qtype, _ptr(w), _ptr(wu), row_bytes, _ptr(x), _ptr(xs16), _ptr(bias),
-                                    _ptr(residual), _ptr(y), _ptr(ys16), n, k, vectors, _ptr(ids), experts, routes,
+    check(lib().hipllm_gemv_batched(qtype, _ptr(w), _ptr(wu), row_bytes, _ptr(x), _ptr(xq), _ptr(bias),
+                                    _ptr(residual), _ptr(y), _ptr(yq), n, k, vectors, _ptr(ids), experts, routes,
                                     expert_stride, 1 if x_routed else 0, ldx or k, ldy or n, _stream(stream)))
 
 
@@ -359,8 +360,8 @@ def _k_gdn_scan(q, k, ldqk, v, ldv, decay, beta, state, out, ldo, tokens, value_
                                 _ptr(out), ldo, tokens, value_heads, key_heads, d, _stream(stream)))
 
 
-def _k_gated_rmsnorm(o, ldo, gamma, z, ldz, y, ys16, ldy, tokens, heads, d, eps, stream=None):
-    check(lib().hipllm_gated_rmsnorm(_ptr(o), ldo, _ptr(gamma), _ptr(z), ldz, _ptr(y), _ptr(ys16), ldy, tokens,
+def _k_gated_rmsnorm(o, ldo, gamma, z, ldz, y, yq, ldy, tokens, heads, d, eps, stream=None):
+    check(lib().hipllm_gated_rmsnorm(_ptr(o), ldo, _ptr(gamma), _ptr(z), ldz, _ptr(y), _ptr(yq), ldy, tokens,
                                      heads, d, eps, _stream(stream)))
 
 
@@ -370,12 +371,12 @@ def _k_split_qgate_norm(mixed, ldm, kv, ldkv, q_gamma, k_gamma, qkv, ldqkv, gate
                                         ldqkv, _ptr(gate), ldg, tokens, hq, hkv, d, eps, _stream(stream)))
 
 
-def _k_gate_mul(a, g, y, y16, n, stream=None):
-    check(lib().hipllm_gate_mul(_ptr(a), _ptr(g), _ptr(y), _ptr(y16), n, _stream(stream)))
+def _k_gate_mul(a, g, y, yq, n, stream=None):
+    check(lib().hipllm_gate_mul(_ptr(a), _ptr(g), _ptr(y), _ptr(yq), n, _stream(stream)))
 
 
-def _k_rmsnorm(x, gamma, y, ys16, rows, cols, eps, stream=None):
-    check(lib().hipllm_rmsnorm(_ptr(x), _ptr(gamma), _ptr(y), _ptr(ys16), rows, cols, eps, _stream(stream)))
+def _k_rmsnorm(x, gamma, y, yq, rows, cols, eps, stream=None):
+    check(lib().hipllm_rmsnorm(_ptr(x), _ptr(gamma), _ptr(y), _ptr(yq), rows, cols, eps, _stream(stream)))
 
 
 def _k_embed(qtype, table, row_bytes, ids, rows, vocab, cols, out, stream=None):
@@ -388,8 +389,8 @@ def _k_rope_kv(qkv, cos_sin, rot, hq, hkv, d, pos0, rows, row_stride, kcache, vc
                                _ptr(vcache), _stream(stream)))
 
 
-def _k_attn_decode(q, kcache, vcache, out, out16, scratch, hq, hkv, d, length, scale, stream=None):
-    check(lib().hipllm_attn_decode(_ptr(q), _ptr(kcache), _ptr(vcache), _ptr(out), _ptr(out16), _ptr(scratch),
+def _k_attn_decode(q, kcache, vcache, out, outq, scratch, hq, hkv, d, length, scale, stream=None):
+    check(lib().hipllm_attn_decode(_ptr(q), _ptr(kcache), _ptr(vcache), _ptr(out), _ptr(outq), _ptr(scratch),
                                    hq, hkv, d, length, scale, _stream(stream)))
 
 
@@ -397,12 +398,12 @@ def _k_argmax(x, n, out, scratch, stream=None):
     check(lib().hipllm_argmax(_ptr(x), n, _ptr(out), _ptr(scratch), _stream(stream)))
 
 
-def _k_swiglu(g, u, y, y16, n, stream=None):
-    check(lib().hipllm_swiglu(_ptr(g), _ptr(u), _ptr(y), _ptr(y16), n, _stream(stream)))
+def _k_swiglu(g, u, y, yq, n, stream=None):
+    check(lib().hipllm_swiglu(_ptr(g), _ptr(u), _ptr(y), _ptr(yq), n, _stream(stream)))
 
 
 kernels = types.SimpleNamespace(
-    dequant_rows=_k_dequant_rows, prep_sums=_k_prep_sums, gemv=_k_gemv, gemv_prepped=_k_gemv_prepped,
+    dequant_rows=_k_dequant_rows, prep_x=_k_prep_x, gemv=_k_gemv, gemv_prepped=_k_gemv_prepped,
     gemv_swiglu=_k_gemv_swiglu, to_bf16=_k_to_bf16, gemm_mfma=_k_gemm_mfma, gemm=_k_gemm,
     gemm_workspace_bytes=lambda m, k: lib().hipllm_gemm_workspace_bytes(m, k), rmsnorm=_k_rmsnorm, embed=_k_embed, rope_kv=_k_rope_kv,
     attn_decode=_k_attn_decode, argmax=_k_argmax, swiglu=_k_swiglu, attn_prefill=_k_attn_prefill,

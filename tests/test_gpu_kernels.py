@@ -5,7 +5,9 @@ Bars (from the project's correctness contract):
   CPU oracle (the restatement of CPULLM, itself pinned to the reference's
   golden vectors);
 * GEMV: rel_err = max|y - ref| / max|ref| <= 1e-3, ref = float64 product of
-  the FP32-dequantized weights and the FP32 input;
+  the FP32-dequantized weights and the FP32 input (the GEMV reads the input in
+  its XGroup form, 24-bit fixed point per 16 values, see tests/xgroup.py);
+* producers of GEMV inputs write that form: checked against its definition;
 * attention, SwiGLU: same rel_err bound against float64;
 * argmax: exact index, ties to the lower index.
 Device weight buffers get 256 bytes of tail padding, as the runtime's arena
@@ -23,7 +25,7 @@ import pytest
 import oracle
 from myllm_amd import synth
 from myllm_amd.hipllm import kernels
-from tests import blocks
+from tests import blocks, xgroup
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -101,12 +103,12 @@ def gemv_case(cuda, qtype, n, k, seed, bias=False, residual=False, tiling=0):
     x = synth.normal(k, seed + 1)
     dw = dev_bytes(w, cuda)
     dx = torch.from_numpy(x).to(cuda)
-    xs16 = torch.empty(k // 16, dtype=torch.float32, device=cuda)
-    kernels.prep_sums(dx, xs16, k)
+    xq = xgroup.buffer(torch, k, cuda)
+    kernels.prep_x(dx, xq, k)
     b = synth.normal(n, seed + 2) if bias else None
     r = synth.normal(n, seed + 3) if residual else None
     y = torch.empty(n, dtype=torch.float32, device=cuda)
-    kernels.gemv_prepped(qtype, dw, w.shape[1], dx, xs16, None if b is None else torch.from_numpy(b).to(cuda),
+    kernels.gemv_prepped(qtype, dw, w.shape[1], dx, xq, None if b is None else torch.from_numpy(b).to(cuda),
                          None if r is None else torch.from_numpy(r).to(cuda), y, n, k, tiling)
     # Reference: float64 over the FP32 dequantized weights (GPU dequant is
     # bit-exact to the oracle, checked above).
@@ -128,15 +130,33 @@ def test_gemv_small(cuda, qtype, n, k):
 
 
 @pytest.mark.parametrize("qtype", [synth.Q5_0, synth.Q8_0])
-def test_gemv_two_byte_aligned_blocks(cuda, qtype):
-    # 34- and 22-byte blocks: every odd block starts at a 2-byte offset.
-    y, ref = gemv_case(cuda, qtype, 77, 64 * 3, seed=3)
+@pytest.mark.parametrize("k", [32, 64 * 3, 800, 896])
+def test_gemv_ragged_two_byte_aligned_blocks(cuda, qtype, k):
+    # 34- and 22-byte blocks: every odd block starts at a 2-byte offset. A
+    # unit is 4 blocks: k = 32, 192 and 800 leave a last unit of 1, 2 and 1
+    # blocks (lanes past the row must contribute nothing).
+    y, ref = gemv_case(cuda, qtype, 77, k, seed=3 + k)
     assert rel_err(y, ref) <= 1e-3
 
 
-TILINGS = [11, 12, 14, 18, 21, 22, 24, 28, 41, 42, 44, 48]
-# K-sliced form (Q4_K / Q6_K): 2000 + 100 R + 10 teams + rows per block / 16.
-SLICE_CODES = [2211, 2224, 2412, 2414, 2421, 2443, 2482]
+def test_prep_x_encodes_xgroups(cuda):
+    # Magnitudes spanning many binades, exact zeros, a zero group and a
+    # group with one huge outlier.
+    k = 4096
+    x = synth.normal(k, 5) * np.float32(3.0) ** synth.normal(k, 6, stddev=4.0).astype(np.float32)
+    x[16:32] = 0.0
+    x[40] = 0.0
+    x[64:80] *= np.float32(1e-20)
+    x[96] = np.float32(3e30)
+    xq = xgroup.buffer(torch, k, cuda)
+    kernels.prep_x(torch.from_numpy(x.astype(np.float32)).to(cuda), xq, k)
+    xgroup.check(xq, x)
+    got = xgroup.decode(xq)
+    assert np.all(got["q"][1] == 0) and got["e"][1] == 0.0
+
+
+TILINGS = [108, 116, 132, 202, 204, 208, 216, 232, 401, 402, 404, 408, 416, 432, 802, 804, 808, 816, 832]
+SWIGLU_TILINGS = [202, 204, 401, 402, 404, 408, 802, 804, 808, 816]
 
 
 @pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q6_K, synth.Q8_0, synth.Q5_0, synth.F16, synth.F32])
@@ -147,22 +167,20 @@ def test_gemv_tilings_agree(cuda, qtype, tiling):
     assert rel_err(y, ref) <= 1e-3
 
 
-@pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q6_K])
-@pytest.mark.parametrize("code", SLICE_CODES)
-@pytest.mark.parametrize("k", [2048, 4864, 18944])
-def test_gemv_slice_codes(cuda, qtype, code, k):
-    # k = 2048: 8 super-blocks, half of a wave's slots idle; 4864: 19, two K
-    # slices with a ragged second; 18944: 74, five slices. 1001 rows leave a
-    # partial last block for every rows-per-block choice.
-    if code // 10 % 10 * ((k // 256 + 15) // 16) > 8:
-        pytest.skip("more than 8 waves per block")
-    y, ref = gemv_case(cuda, qtype, 1001, k, seed=code, bias=True, residual=True, tiling=code)
+@pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q6_K, synth.Q8_0])
+@pytest.mark.parametrize("tiling", [116, 216, 232, 416])
+@pytest.mark.parametrize("k", [4864, 18944])
+def test_gemv_wave_split_tilings(cuda, qtype, tiling, k):
+    # OPR 16 / 32: a row group spans 2 / 4 waves whose partials meet in LDS;
+    # 19 and 74 super-blocks split unevenly over the octets.
+    y, ref = gemv_case(cuda, qtype, 1001, k, seed=tiling, bias=True, residual=True, tiling=tiling)
     assert rel_err(y, ref) <= 1e-3
 
 
-def test_gemv_slice_rejected_for_other_types(cuda):
+@pytest.mark.parametrize("tiling", [12, 28, 2412, 103, 1616])
+def test_gemv_rejects_unknown_tilings(cuda, tiling):
     with pytest.raises(ValueError):
-        gemv_case(cuda, synth.Q8_0, 64, 4096, seed=1, tiling=2412)
+        gemv_case(cuda, synth.Q4_K, 64, 1024, seed=1, tiling=tiling)
 
 
 @pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q6_K])
@@ -190,24 +208,35 @@ def test_gemv_public_entry_with_workspace(cuda):
     assert rel_err(y.cpu().numpy(), ref) <= 1e-3
 
 
-@pytest.mark.parametrize("qtype,n,k", [(synth.Q4_K, 4864, 1024), (synth.Q4_K, 2048, 3584),
-                                        (synth.Q4_K, 18944, 3584), (synth.Q6_K, 1040, 5120),
-                                        (synth.Q5_0, 480, 896)])
-def test_gemv_swiglu(cuda, qtype, n, k):
+def swiglu_case(cuda, qtype, n, k, tiling=0):
     wg, wu = random_rows(qtype, n, k, 31), random_rows(qtype, n, k, 32)
     x = synth.normal(k, 33)
     dx = torch.from_numpy(x).to(cuda)
-    xs16 = torch.empty(k // 16, dtype=torch.float32, device=cuda)
-    kernels.prep_sums(dx, xs16, k)
+    xq = xgroup.buffer(torch, k, cuda)
+    kernels.prep_x(dx, xq, k)
     y = torch.empty(n, dtype=torch.float32, device=cuda)
-    y16 = torch.empty(n // 16, dtype=torch.float32, device=cuda)
-    kernels.gemv_swiglu(qtype, dev_bytes(wg, cuda), dev_bytes(wu, cuda), wg.shape[1], dx, xs16, y, y16, n, k)
+    yq = xgroup.buffer(torch, n, cuda)
+    kernels.gemv_swiglu(qtype, dev_bytes(wg, cuda), dev_bytes(wu, cuda), wg.shape[1], dx, xq, y, yq, n, k, tiling)
     g = oracle.dequant_rows(qtype, wg, k).astype(np.float64) @ x
     u = oracle.dequant_rows(qtype, wu, k).astype(np.float64) @ x
     ref = g / (1 + np.exp(-g)) * u
     got = y.cpu().numpy()
     assert rel_err(got, ref) <= 1e-3
-    assert rel_err(y16.cpu().numpy(), got.astype(np.float64).reshape(-1, 16).sum(axis=1)) <= 1e-5
+    xgroup.check(yq, got)
+
+
+@pytest.mark.parametrize("qtype,n,k", [(synth.Q4_K, 4864, 1024), (synth.Q4_K, 2048, 3584),
+                                        (synth.Q4_K, 18944, 3584), (synth.Q6_K, 1040, 5120),
+                                        (synth.Q5_0, 480, 896), (synth.Q8_0, 512, 2048)])
+def test_gemv_swiglu(cuda, qtype, n, k):
+    swiglu_case(cuda, qtype, n, k)
+
+
+@pytest.mark.parametrize("tiling", SWIGLU_TILINGS)
+@pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q6_K])
+def test_gemv_swiglu_tilings(cuda, qtype, tiling):
+    # 1040 rows: a partial last block for every rows-per-block choice.
+    swiglu_case(cuda, qtype, 1040, 2048, tiling)
 
 
 # ------------------------------------------------------------- small ops
@@ -216,14 +245,14 @@ def test_rmsnorm_bit_exact(cuda, rows, cols):
     x = synth.normal(rows * cols, 41, stddev=3.0).reshape(rows, cols)
     g = synth.normal(cols, 42, stddev=0.5) + 1.0
     y = torch.empty(rows * cols, dtype=torch.float32, device=cuda)
-    y16 = torch.empty(rows * cols // 16, dtype=torch.float32, device=cuda)
-    kernels.rmsnorm(torch.from_numpy(x).to(cuda), torch.from_numpy(g).to(cuda), y, y16, rows, cols, 1e-6)
+    yq = xgroup.buffer(torch, cols, cuda, rows)
+    kernels.rmsnorm(torch.from_numpy(x).to(cuda), torch.from_numpy(g).to(cuda), y, yq, rows, cols, 1e-6)
     ref = x.copy()
     for r in range(rows):
         oracle.lib().oracle_rmsnorm(ref[r].ctypes.data, g.ctypes.data, cols, ctypes.c_float(1e-6))
     got = y.cpu().numpy().reshape(rows, cols)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
-    assert rel_err(y16.cpu().numpy(), got.astype(np.float64).reshape(-1, 16).sum(axis=1)) <= 1e-5
+    xgroup.check(yq, got)
 
 
 def _libm():
@@ -279,10 +308,10 @@ def test_attention_decode(cuda, length, hq, hkv, d):
     v = synth.normal(length * kv, 63).reshape(length, kv)
     scale = np.float32(1.0) / np.float32(math.sqrt(d))
     out = torch.empty(hq * d, dtype=torch.float32, device=cuda)
-    out16 = torch.empty(hq * d // 16, dtype=torch.float32, device=cuda)
+    outq = xgroup.buffer(torch, hq * d, cuda)
     scratch = torch.empty(kernels.attn_decode_scratch_floats(hq, d, length), dtype=torch.float32, device=cuda)
     kernels.attn_decode(torch.from_numpy(q).to(cuda), torch.from_numpy(k).to(cuda), torch.from_numpy(v).to(cuda),
-                        out, out16, scratch, hq, hkv, d, length, float(scale))
+                        out, outq, scratch, hq, hkv, d, length, float(scale))
     ref = np.empty(hq * d)
     for h in range(hq):
         g = h // (hq // hkv)
@@ -292,7 +321,7 @@ def test_attention_decode(cuda, length, hq, hkv, d):
         ref[h * d:(h + 1) * d] = p @ v[:, g * d:(g + 1) * d]
     got = out.cpu().numpy()
     assert rel_err(got, ref) <= 1e-5
-    assert rel_err(out16.cpu().numpy(), got.astype(np.float64).reshape(-1, 16).sum(axis=1)) <= 1e-5
+    xgroup.check(outq, got)
 
 
 @pytest.mark.parametrize("n", [1, 100, 2048, 2049, 151936])
@@ -329,11 +358,12 @@ def test_swiglu_elementwise(cuda):
     n = 4864
     g, u = synth.normal(n, 91, stddev=4.0), synth.normal(n, 92)
     y = torch.empty(n, dtype=torch.float32, device=cuda)
-    y16 = torch.empty(n // 16, dtype=torch.float32, device=cuda)
-    kernels.swiglu(torch.from_numpy(g).to(cuda), torch.from_numpy(u).to(cuda), y, y16, n)
+    yq = xgroup.buffer(torch, n, cuda)
+    kernels.swiglu(torch.from_numpy(g).to(cuda), torch.from_numpy(u).to(cuda), y, yq, n)
     gd = g.astype(np.float64)
     ref = gd / (1 + np.exp(-gd)) * u
     assert rel_err(y.cpu().numpy(), ref) <= 1e-6
+    xgroup.check(yq, y.cpu().numpy())
 
 
 def test_launchers_reject_bad_arguments(cuda):

@@ -18,6 +18,7 @@ import pytest
 from myllm_amd import synth
 from myllm_amd.hipllm import HipLLM, LengthError, generate, kernels
 from oracle import moe_ref
+from tests import xgroup
 from tests.test_gpu_kernels import dev_bytes, random_rows, rel_err
 
 torch = pytest.importorskip("torch")
@@ -63,9 +64,9 @@ def test_expert_gemv_routed(cuda, qtype):
         rows = T * routes if routed else T
         x = synth.normal(rows * kdim, 42 + routed).reshape(rows, kdim)
         dx = t32(x, cuda)
-        xs = torch.empty(rows, kdim // 16, device=cuda)
+        xs = torch.empty(rows, kdim, device=cuda)  # XGroup rows, kdim / 16 groups each
         for r in range(rows):
-            kernels.prep_sums(dx[r], xs[r], kdim)
+            kernels.prep_x(dx[r], xs[r], kdim)
         y = torch.empty(T * routes, n, device=cuda)
         kernels.gemv_batched(qtype, dw, None, rb, dx, xs, None, None, y, None, n, kdim, T * routes,
                              ids=torch.from_numpy(ids_np.reshape(-1).copy()).to(cuda), experts=E, routes=routes,
@@ -85,9 +86,9 @@ def test_batched_rows_and_swiglu(cuda, qtype):
     rb = wg.shape[1]
     x = synth.normal(T * kdim, 53).reshape(T, kdim)
     dx = t32(x, cuda)
-    xs = torch.empty(T, kdim // 16, device=cuda)
+    xs = torch.empty(T, kdim, device=cuda)  # XGroup rows
     for r in range(T):
-        kernels.prep_sums(dx[r], xs[r], kdim)
+        kernels.prep_x(dx[r], xs[r], kdim)
     res = synth.normal(T * n, 54).reshape(T, n)
     y = torch.empty(T, n, device=cuda)
     kernels.gemv_batched(qtype, dg, None, rb, dx, xs, None, t32(res, cuda), y, None, n, kdim, T)
@@ -98,13 +99,13 @@ def test_batched_rows_and_swiglu(cuda, qtype):
     G, U = G.double().cpu().numpy(), U.double().cpu().numpy()
     ref = x.astype(np.float64) @ G.T + res
     assert rel_err(y.cpu().numpy(), ref) <= 1e-3
-    ys16 = torch.empty(T, n // 16, device=cuda)
-    kernels.gemv_batched(qtype, dg, du, rb, dx, xs, None, None, y, ys16, n, kdim, T)
+    yq = torch.empty(T, n, device=cuda)
+    kernels.gemv_batched(qtype, dg, du, rb, dx, xs, None, None, y, yq, n, kdim, T)
     g, u = x.astype(np.float64) @ G.T, x.astype(np.float64) @ U.T
     ref = moe_ref.silu(g) * u
     got = y.double().cpu().numpy()
     assert rel_err(got, ref) <= 1e-3
-    assert rel_err(ys16.cpu().numpy(), got.reshape(T, -1, 16).sum(axis=2)) <= 1e-5
+    xgroup.check(yq, y.cpu().numpy())
 
 
 # ------------------------------------------------------------ DeltaNet pieces
@@ -188,12 +189,12 @@ def test_gated_rmsnorm(cuda):
     z = rng.normal(size=(T, Hv * d)).astype(np.float32)
     g = rng.normal(size=d).astype(np.float32)
     y = torch.empty(T, Hv * d, device=cuda)
-    y16 = torch.empty(T, Hv * d // 16, device=cuda)
-    kernels.gated_rmsnorm(t32(o, cuda), Hv * d, t32(g, cuda), t32(z, cuda), Hv * d, y, y16, Hv * d, T, Hv, d, 1e-6)
+    yq = torch.empty(T, Hv * d, device=cuda)
+    kernels.gated_rmsnorm(t32(o, cuda), Hv * d, t32(g, cuda), t32(z, cuda), Hv * d, y, yq, Hv * d, T, Hv, d, 1e-6)
     ref = (moe_ref.rmsnorm(o.reshape(T, Hv, d), g, 1e-6) * moe_ref.silu(z.reshape(T, Hv, d))).reshape(T, -1)
     got = y.cpu().numpy()
     assert rel_err(got, ref) <= 1e-5
-    assert rel_err(y16.cpu().numpy(), got.astype(np.float64).reshape(T, -1, 16).sum(axis=2)) <= 1e-5
+    xgroup.check(yq, got)
 
 
 # ------------------------------------------------------------ attention pieces
@@ -218,10 +219,11 @@ def test_split_qgate_norm_and_gate_mul(cuda):
     np.testing.assert_array_equal(gate.cpu().numpy(), m[:, :, D:].reshape(T, -1).astype(np.float32))
     a = torch.randn(T, Hq * D, device=cuda)
     y = torch.empty_like(a)
-    y16 = torch.empty(T * Hq * D // 16, device=cuda)
-    kernels.gate_mul(a, gate, y, y16, T * Hq * D)
+    yq = torch.empty(T * Hq * D, device=cuda)
+    kernels.gate_mul(a, gate, y, yq, T * Hq * D)
     ref = a.double().cpu().numpy() * moe_ref.sigmoid(gate.double().cpu().numpy())
     assert rel_err(y.cpu().numpy(), ref) <= 1e-5
+    xgroup.check(yq, y.cpu().numpy())
 
 
 def test_moe_combine(cuda):
