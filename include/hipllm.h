@@ -307,6 +307,14 @@ int hipllm_copy_logits(const HipllmModel* model, float* out, size_t count);
 /* qwen2 only: 1 = batched (bf16 MFMA) prefill, 0 = token-serial prefill
  * through the FP32 decode kernels. */
 int hipllm_set_batched_prefill(HipllmModel* model, int enabled);
+
+/* Decode path: 1 (default) = each decode step replays one recorded HIP graph
+ * of the whole step (token and position read from device memory), 0 = its
+ * kernels are launched one by one. Results agree to rounding (attention
+ * splits follow the capacity rather than the length). Replaces the
+ * reference's per-token command-buffer encoding (metal_llm.mm:3295-3385,
+ * moe_llm.mm:3051-3141); no counterpart switch exists there. */
+int hipllm_set_decode_graphs(HipllmModel* model, int enabled);
 /* qwen35moe only: expert ids chosen for the last row of the last forward,
  * [layer_count, expert_used_count] (MoeLLM keeps them in RouteIds,
  * moe_llm.mm:2919-2925). */

@@ -42,11 +42,17 @@ int launch_rmsnorm(const float* x, const float* gamma, float* y, XGroup* yq, siz
                    hipStream_t stream);
 int launch_embed(uint32_t type, const void* table, size_t row_bytes, const int32_t* ids, size_t rows, size_t vocab,
                  size_t cols, float* out, hipStream_t stream);
+// dpos (optional, device): position of row 0 read on the device instead of
+// pos0, so one recorded launch serves every decode step.
 int launch_rope_kv(float* qkv, const float* cos_sin, size_t rot, size_t hq, size_t hkv, size_t d, size_t pos0,
-                   size_t rows, size_t row_stride, float* kcache, float* vcache, hipStream_t stream);
+                   size_t rows, size_t row_stride, float* kcache, float* vcache, hipStream_t stream,
+                   const uint32_t* dpos = nullptr);
 size_t attn_decode_scratch_floats(size_t hq, size_t d, size_t max_len);
+// dpos (optional, device): len = *dpos + 1 read on the device; capacity then
+// bounds it and fixes the launch shape.
 int launch_attn_decode(const float* q, const float* kcache, const float* vcache, float* out, XGroup* outq,
-                       float* scratch, size_t hq, size_t hkv, size_t d, size_t len, float scale, hipStream_t stream);
+                       float* scratch, size_t hq, size_t hkv, size_t d, size_t len, float scale, hipStream_t stream,
+                       const uint32_t* dpos = nullptr, size_t capacity = 0);
 size_t argmax_scratch_bytes(size_t n);
 int launch_argmax(const float* x, size_t n, uint32_t* out, void* scratch, hipStream_t stream);
 int launch_swiglu(const float* g, const float* u, float* y, XGroup* yq, size_t n, hipStream_t stream);

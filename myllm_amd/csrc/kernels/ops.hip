@@ -103,10 +103,11 @@ __global__ void embed_kernel(uint32_t type, const uint8_t* __restrict__ table, s
 #pragma clang fp contract(off)
 __global__ void rope_kv_kernel(float* __restrict__ qkv, const float2* __restrict__ table, uint32_t half_rot,
                                uint32_t hq, uint32_t hkv, uint32_t d, uint32_t pos0, uint32_t row_stride,
-                               float* __restrict__ kcache, float* __restrict__ vcache) {
+                               float* __restrict__ kcache, float* __restrict__ vcache,
+                               const uint32_t* __restrict__ dpos) {
     const uint32_t r = blockIdx.x;
     float* row = qkv + static_cast<size_t>(r) * row_stride;
-    const uint32_t pos = pos0 + r;
+    const uint32_t pos = (dpos ? *dpos : pos0) + r;
     const uint32_t kvd = hkv * d;
     const float2* tab = table + static_cast<size_t>(pos) * half_rot;
     const uint32_t heads = hq + hkv;
@@ -138,103 +139,121 @@ __global__ void rope_kv_kernel(float* __restrict__ qkv, const float2* __restrict
 #pragma clang fp contract(fast)
 
 // ------------------------------------------------------------ attention
-// Split-K decode attention (flash-decode). Phase 1: block (head, chunk) scores
-// keys [chunk*C, min(len, chunk*C + C)) against its query (four lanes per
-// key, each a quarter of the head dims), and writes the chunk's running max
-// m, sum of exp l, and unnormalised p.V (D floats; threads split the chunk's
-// keys in 256 / D interleaved parts, reduced in LDS). Phase 2: one block per
-// head merges the chunks and writes the head output, plus its XGroup form for
-// the next GEMV.
+// Split-K decode attention (flash-decode). Phase 1: block (head, split y)
+// processes the 64-key chunks y, y + S, y + 2S, ... of [0, len) (S splits):
+// per chunk, four lanes per key score it against the query (each a quarter of
+// the head dims), then p.V accumulates in registers (threads split the
+// chunk's keys in 256 / (D / 4) interleaved parts), with an online softmax
+// across the block's chunks. It writes its running max m, sum of exp l and
+// unnormalised p.V (D floats; m = -inf, l = 0 for a split without keys).
+// Phase 2: one block per head merges the S splits and writes the head output,
+// plus its XGroup form for the next GEMV. The length is a value or, for
+// launches recorded once and replayed per token, read from device memory
+// (len = *dpos + 1); S then follows the capacity, not the length.
 constexpr uint32_t kAttnChunk = 64;
+constexpr uint32_t kAttnMaxSplits = 16;
 
 __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restrict__ q, const float* __restrict__ kcache,
                                                            const float* __restrict__ vcache, float* __restrict__ part,
-                                                           uint32_t hq, uint32_t hkv, uint32_t d, uint32_t len,
-                                                           float scale, uint32_t nchunks) {
+                                                           uint32_t hq, uint32_t hkv, uint32_t d, uint32_t len_arg,
+                                                           const uint32_t* __restrict__ dpos, float scale,
+                                                           uint32_t splits) {
     const uint32_t h = blockIdx.x;
-    const uint32_t chunk = blockIdx.y;
+    const uint32_t split = blockIdx.y;
+    const uint32_t len = dpos ? *dpos + 1 : len_arg;
+    const uint32_t nchunks = (len + kAttnChunk - 1) / kAttnChunk;
     const uint32_t g = h / (hq / hkv);
     const uint32_t kvd = hkv * d;
-    const uint32_t t0 = chunk * kAttnChunk;
-    const uint32_t cnt = min(len - t0, kAttnChunk);
     __shared__ float4 qs4[64];
     __shared__ float ps[kAttnChunk];
     __shared__ float red[8];
     __shared__ float4 accp[256];
     const uint32_t tid = threadIdx.x;
     const uint32_t d4 = d / 4;
+    const uint32_t wave = tid >> 6, lane = tid & 63;
     for (uint32_t i = tid; i < d4; i += blockDim.x) qs4[i] = reinterpret_cast<const float4*>(q + h * d)[i];
     __syncthreads();
-    // Scores: key j = tid / 4, quarter qq = tid % 4 covers float4 columns qq, qq + 4, ...
-    const uint32_t j = tid >> 2, qq = tid & 3;
-    float s = -INFINITY;
-    {
-        float dot = 0.0f;
-        if (j < cnt) {
-            const float4* k = reinterpret_cast<const float4*>(kcache + static_cast<size_t>(t0 + j) * kvd + g * d);
-            for (uint32_t i = qq; i < d4; i += 4) {
-                const float4 kv = k[i];
-                const float4 qv = qs4[i];
-                dot = fmaf(kv.x, qv.x, dot);
-                dot = fmaf(kv.y, qv.y, dot);
-                dot = fmaf(kv.z, qv.z, dot);
-                dot = fmaf(kv.w, qv.w, dot);
-            }
-        }
-        dot += __shfl_xor(dot, 1);
-        dot += __shfl_xor(dot, 2);
-        if (j < cnt) s = dot * scale;
-    }
-    const uint32_t wave = tid >> 6, lane = tid & 63;
-    float m = warp_max(s);
-    if (lane == 0) red[wave] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const float p = j < cnt ? expf(s - m) : 0.0f;
-    if (qq == 0) ps[j] = p;
-    float l = warp_sum(qq == 0 ? p : 0.0f);
-    __syncthreads();
-    if (lane == 0) red[4 + wave] = l;
-    __syncthreads();
-    l = (red[4] + red[5]) + (red[6] + red[7]);
-    // p.V: float4 column c4 = tid % (d / 4), key subset pp = tid / (d / 4) of
-    // `parts` interleaved subsets, reduced in LDS; threads past parts * d / 4
-    // (when d / 4 does not divide 256) idle.
+    // p.V ownership: float4 column c4 = tid % (d / 4), key subset pp = tid /
+    // (d / 4) of `parts` (threads past parts * d / 4 idle).
     const uint32_t parts = blockDim.x / d4;
-    float* out = part + (static_cast<size_t>(h) * nchunks + chunk) * (d + 2);
-    if (tid < parts * d4) {
-        const uint32_t c4 = tid % d4, pp = tid / d4;
-        const float4* v = reinterpret_cast<const float4*>(vcache + static_cast<size_t>(t0) * kvd + g * d) + c4;
-        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const bool pv = tid < parts * d4;
+    const uint32_t c4 = tid % d4, pp = tid / d4;
+    float m_run = -INFINITY, l_run = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t chunk = split; chunk < nchunks; chunk += splits) {
+        const uint32_t t0 = chunk * kAttnChunk;
+        const uint32_t cnt = min(len - t0, kAttnChunk);
+        // Scores: key j = tid / 4, quarter qq = tid % 4 covers float4 columns qq, qq + 4, ...
+        const uint32_t j = tid >> 2, qq = tid & 3;
+        float s = -INFINITY;
+        {
+            float dot = 0.0f;
+            if (j < cnt) {
+                const float4* k = reinterpret_cast<const float4*>(kcache + static_cast<size_t>(t0 + j) * kvd + g * d);
+                for (uint32_t i = qq; i < d4; i += 4) {
+                    const float4 kv = k[i];
+                    const float4 qv = qs4[i];
+                    dot = fmaf(kv.x, qv.x, dot);
+                    dot = fmaf(kv.y, qv.y, dot);
+                    dot = fmaf(kv.z, qv.z, dot);
+                    dot = fmaf(kv.w, qv.w, dot);
+                }
+            }
+            dot += __shfl_xor(dot, 1);
+            dot += __shfl_xor(dot, 2);
+            if (j < cnt) s = dot * scale;
+        }
+        float cm = warp_max(s);
+        if (lane == 0) red[wave] = cm;
+        __syncthreads();
+        cm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        const float m_new = fmaxf(m_run, cm);  // finite: every chunk holds a key
+        const float p = j < cnt ? expf(s - m_new) : 0.0f;
+        if (qq == 0) ps[j] = p;
+        float l = warp_sum(qq == 0 ? p : 0.0f);
+        __syncthreads();  // red[0..3] read by all; ps[] complete
+        if (lane == 0) red[4 + wave] = l;
+        __syncthreads();
+        l = (red[4] + red[5]) + (red[6] + red[7]);
+        const float corr = expf(m_run - m_new);  // 0 on the first chunk
+        l_run = l_run * corr + l;
+        m_run = m_new;
+        if (pv) {
+            const float4* v = reinterpret_cast<const float4*>(vcache + static_cast<size_t>(t0) * kvd + g * d) + c4;
+            float4 a = make_float4(acc.x * corr, acc.y * corr, acc.z * corr, acc.w * corr);
 #pragma unroll 4
-        for (uint32_t jj = pp; jj < cnt; jj += parts) {
-            const float pj = ps[jj];
-            const float4 vv = v[static_cast<size_t>(jj) * (kvd / 4)];
-            acc.x = fmaf(pj, vv.x, acc.x);
-            acc.y = fmaf(pj, vv.y, acc.y);
-            acc.z = fmaf(pj, vv.z, acc.z);
-            acc.w = fmaf(pj, vv.w, acc.w);
+            for (uint32_t jj = pp; jj < cnt; jj += parts) {
+                const float pj = ps[jj];
+                const float4 vv = v[static_cast<size_t>(jj) * (kvd / 4)];
+                a.x = fmaf(pj, vv.x, a.x);
+                a.y = fmaf(pj, vv.y, a.y);
+                a.z = fmaf(pj, vv.z, a.z);
+                a.w = fmaf(pj, vv.w, a.w);
+            }
+            acc = a;
         }
-        accp[tid] = acc;
+        __syncthreads();  // ps[] and red[] are rewritten by the next chunk
     }
+    float* out = part + (static_cast<size_t>(h) * splits + split) * (d + 2);
+    if (pv) accp[tid] = acc;
     __syncthreads();
-    for (uint32_t c4 = tid; c4 < d4; c4 += blockDim.x) {
-        float4 acc = accp[c4];
-        for (uint32_t pp = 1; pp < parts; ++pp) {
-            const float4 a = accp[pp * d4 + c4];
-            acc.x += a.x;
-            acc.y += a.y;
-            acc.z += a.z;
-            acc.w += a.w;
+    for (uint32_t cc = tid; cc < d4; cc += blockDim.x) {
+        float4 a = accp[cc];
+        for (uint32_t k = 1; k < parts; ++k) {
+            const float4 b = accp[k * d4 + cc];
+            a.x += b.x;
+            a.y += b.y;
+            a.z += b.z;
+            a.w += b.w;
         }
-        out[2 + 4 * c4 + 0] = acc.x;
-        out[2 + 4 * c4 + 1] = acc.y;
-        out[2 + 4 * c4 + 2] = acc.z;
-        out[2 + 4 * c4 + 3] = acc.w;
+        out[2 + 4 * cc + 0] = a.x;
+        out[2 + 4 * cc + 1] = a.y;
+        out[2 + 4 * cc + 2] = a.z;
+        out[2 + 4 * cc + 3] = a.w;
     }
     if (tid == 0) {
-        out[0] = m;
-        out[1] = l;
+        out[0] = m_run;
+        out[1] = l_run;
     }
 }
 
@@ -242,6 +261,8 @@ __global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict
                                                          XGroup* __restrict__ outq, uint32_t d, uint32_t nchunks) {
     const uint32_t h = blockIdx.x;
     const float* ph = part + static_cast<size_t>(h) * nchunks * (d + 2);
+    // nchunks = the number of splits; a split without keys has m = -inf,
+    // weight exp(-inf - M) = 0 (split 0 always holds key 0, so M is finite).
     float M = -INFINITY;
     for (uint32_t c = 0; c < nchunks; ++c) M = fmaxf(M, ph[c * (d + 2)]);
     float L = 0.0f;
@@ -450,7 +471,8 @@ int launch_embed(uint32_t type, const void* table, size_t row_bytes, const int32
 }
 
 int launch_rope_kv(float* qkv, const float* cos_sin, size_t rot, size_t hq, size_t hkv, size_t d, size_t pos0,
-                   size_t rows, size_t row_stride, float* kcache, float* vcache, hipStream_t stream) {
+                   size_t rows, size_t row_stride, float* kcache, float* vcache, hipStream_t stream,
+                   const uint32_t* dpos) {
     if (!qkv || !cos_sin || !kcache || !vcache || rows == 0 || d == 0 || rot == 0 || rot > d || rot % 2) {
         return kInvalidArgument;
     }
@@ -458,28 +480,39 @@ int launch_rope_kv(float* qkv, const float* cos_sin, size_t rot, size_t hq, size
     hipLaunchKernelGGL(rope_kv_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, stream, qkv,
                        reinterpret_cast<const float2*>(cos_sin), static_cast<uint32_t>(rot / 2),
                        static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv), static_cast<uint32_t>(d),
-                       static_cast<uint32_t>(pos0), static_cast<uint32_t>(row_stride), kcache, vcache);
+                       static_cast<uint32_t>(pos0), static_cast<uint32_t>(row_stride), kcache, vcache, dpos);
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
-size_t attn_decode_scratch_floats(size_t hq, size_t d, size_t max_len) {
+namespace {
+uint32_t attn_splits(size_t max_len) {
     const size_t chunks = (max_len + kAttnChunk - 1) / kAttnChunk;
-    return hq * chunks * (d + 2);
+    return static_cast<uint32_t>(chunks < kAttnMaxSplits ? (chunks ? chunks : 1) : kAttnMaxSplits);
+}
+}  // namespace
+
+size_t attn_decode_scratch_floats(size_t hq, size_t d, size_t max_len) {
+    return hq * attn_splits(max_len) * (d + 2);
 }
 
+// len > 0 keys, or (dpos != nullptr) len = *dpos + 1 read on the device with
+// the split count of capacity keys (scratch sized by
+// attn_decode_scratch_floats(hq, d, capacity); the caller guarantees
+// *dpos < capacity).
 int launch_attn_decode(const float* q, const float* kcache, const float* vcache, float* out, XGroup* outq,
-                       float* scratch, size_t hq, size_t hkv, size_t d, size_t len, float scale, hipStream_t stream) {
-    if (!q || !kcache || !vcache || !out || !scratch || len == 0 || hq == 0 || hkv == 0 || hq % hkv) {
-        return kInvalidArgument;
-    }
+                       float* scratch, size_t hq, size_t hkv, size_t d, size_t len, float scale, hipStream_t stream,
+                       const uint32_t* dpos, size_t capacity) {
+    if (!q || !kcache || !vcache || !out || !scratch || hq == 0 || hkv == 0 || hq % hkv) return kInvalidArgument;
+    if (dpos ? capacity == 0 : len == 0) return kInvalidArgument;
     if (d == 0 || d > 256 || d % 16 != 0) return kInvalidArgument;
-    if (len > 0xffffffffull || hq > 0xffffull) return kLengthError;
-    const uint32_t nchunks = static_cast<uint32_t>((len + kAttnChunk - 1) / kAttnChunk);
-    hipLaunchKernelGGL(attn_decode_partial, dim3(static_cast<uint32_t>(hq), nchunks), dim3(256), 0, stream, q, kcache,
+    if (outq && reinterpret_cast<uintptr_t>(outq) % 16 != 0) return kInvalidArgument;
+    if (len > 0xffffffffull || capacity > 0xffffffffull || hq > 0xffffull) return kLengthError;
+    const uint32_t splits = attn_splits(dpos ? capacity : len);
+    hipLaunchKernelGGL(attn_decode_partial, dim3(static_cast<uint32_t>(hq), splits), dim3(256), 0, stream, q, kcache,
                        vcache, scratch, static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv),
-                       static_cast<uint32_t>(d), static_cast<uint32_t>(len), scale, nchunks);
+                       static_cast<uint32_t>(d), static_cast<uint32_t>(len), dpos, scale, splits);
     hipLaunchKernelGGL(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out, outq,
-                       static_cast<uint32_t>(d), nchunks);
+                       static_cast<uint32_t>(d), splits);
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 

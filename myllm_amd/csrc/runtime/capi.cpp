@@ -306,6 +306,11 @@ int hipllm_copy_logits(const HipllmModel* m, float* out, size_t count) {
     return guarded([&] { m->visit([&](const auto& b) { b.copy_last_logits(out, count); }); });
 }
 
+int hipllm_set_decode_graphs(HipllmModel* m, int enabled) {
+    if (!m) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_set_decode_graphs: null argument");
+    return guarded([&] { m->visit([&](auto& model) { model.set_decode_graphs(enabled != 0); }); });
+}
+
 int hipllm_set_batched_prefill(HipllmModel* m, int enabled) {
     if (!m) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_set_batched_prefill: null argument");
     if (!m->dense) return fail(HIPLLM_INVALID_ARGUMENT, "batched prefill switch applies to qwen2 models");

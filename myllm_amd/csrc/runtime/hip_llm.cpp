@@ -53,6 +53,7 @@ struct Activations {
     void* argmax_scratch = nullptr;
     std::int32_t* ids = nullptr;
     std::uint32_t* token = nullptr;
+    std::uint32_t* step = nullptr;  // decode step inputs: [token id, position]
 };
 
 // Device buffers of the batched prefill: T prompt rows each.
@@ -100,11 +101,20 @@ struct HipLLM::Impl {
 
     std::int32_t* host_ids = nullptr;      // pinned
     std::uint32_t* host_token = nullptr;   // pinned
+    std::uint32_t* host_step = nullptr;    // pinned [token id, position]
+
+    // One decode step recorded as a HIP graph (kernels read the token and
+    // position from act.step) and replayed per token.
+    bool decode_graphs = true;
+    hipGraph_t decode_graph = nullptr;
+    hipGraphExec_t decode_exec = nullptr;
 
     std::FILE* profile = nullptr;
 
     ~Impl() {
         if (stream) hipStreamSynchronize(stream);
+        drop_decode_graph();
+        if (host_step) hipHostFree(host_step);
         if (profile) std::fclose(profile);
         weights.release();
         if (kv_arena) hipFree(kv_arena);
@@ -129,8 +139,10 @@ struct HipLLM::Impl {
 
     void gemv(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, const float* bias, const float* residual,
               float* y, std::size_t rows_override = 0) const;
-    void layer_step(std::size_t li, std::size_t pos, float* hidden, float* next_hidden);
-    void token_step(const std::int32_t* device_id, std::size_t pos, bool head);
+    void layer_step(std::size_t li, std::size_t pos, float* hidden, float* next_hidden, const std::uint32_t* dpos);
+    void token_step(const std::int32_t* device_id, std::size_t pos, bool head, const std::uint32_t* dpos = nullptr);
+    void capture_decode();
+    void drop_decode_graph();
     void gemm(const DevMatrix& w, const void* xb, const float* bias, const float* residual, float* y,
               std::size_t rows, std::size_t ldy, std::size_t n_override = 0) const;
     void prefill_layer(std::size_t li, std::size_t rows, float* hidden, float* next_hidden);
@@ -267,6 +279,7 @@ void HipLLM::Impl::allocate_state() {
     kv_cache_bytes = 2 * L * max_sequence * kv_dim * sizeof(float);
     hip_check(hipMalloc(reinterpret_cast<void**>(&kv_arena), kv_cache_bytes), "hipMalloc(KV cache)");
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&host_token), 64, hipHostMallocDefault), "hipHostMalloc(token)");
+    hip_check(hipHostMalloc(reinterpret_cast<void**>(&host_step), 64, hipHostMallocDefault), "hipHostMalloc(step)");
     ensure_prompt_capacity(1);
 }
 
@@ -275,6 +288,7 @@ void HipLLM::Impl::allocate_state() {
 void HipLLM::Impl::ensure_prompt_capacity(std::size_t n) {
     if (n <= prompt_capacity && act_arena) return;
     hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    drop_decode_graph();  // it points into the arena
     if (act_arena) hipFree(act_arena);
     if (host_ids) hipHostFree(host_ids);
     act_arena = nullptr;
@@ -295,7 +309,8 @@ void HipLLM::Impl::ensure_prompt_capacity(std::size_t n) {
                       o_gtmp = reserve(F * 4), o_logits = reserve(V * 4),
                       o_as = reserve(hipllm::attn_decode_scratch_floats(c.attention_head_count, c.head_size,
                                                                           max_sequence) * 4),
-                      o_am = reserve(hipllm::argmax_scratch_bytes(V)), o_ids = reserve(n * 4), o_tok = reserve(64);
+                      o_am = reserve(hipllm::argmax_scratch_bytes(V)), o_ids = reserve(n * 4), o_tok = reserve(64),
+                      o_step = reserve(16);
     act_bytes = off;
     hip_check(hipMalloc(&act_arena, act_bytes), "hipMalloc(activations)");
     auto* base = static_cast<std::uint8_t*>(act_arena);
@@ -314,6 +329,7 @@ void HipLLM::Impl::ensure_prompt_capacity(std::size_t n) {
     act.argmax_scratch = base + o_am;
     act.ids = reinterpret_cast<std::int32_t*>(base + o_ids);
     act.token = reinterpret_cast<std::uint32_t*>(base + o_tok);
+    act.step = reinterpret_cast<std::uint32_t*>(base + o_step);
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&host_ids), n * 4, hipHostMallocDefault), "hipHostMalloc(ids)");
     prompt_capacity = n;
 }
@@ -348,7 +364,10 @@ void HipLLM::Impl::gemv(const DevMatrix& w, const float* x, const hipllm::XGroup
                  "GEMV");
 }
 
-void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, float* next_hidden) {
+// dpos (device, nullable): the position read on the device (recorded decode
+// step); pos is used otherwise.
+void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, float* next_hidden,
+                              const std::uint32_t* dpos) {
     const ModelConfig& c = config;
     const DevLayer& L = layers[li];
     const std::size_t H = c.embedding_size, F = c.feed_forward_size;
@@ -363,12 +382,12 @@ void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, fl
     }
     launch_check(hipllm::launch_rope_kv(act.qkv, rope_table, c.rotary_dimension, c.attention_head_count,
                                         c.kv_head_count, c.head_size, pos, 1, H + 2 * kv_dim, kcache(li), vcache(li),
-                                        stream),
+                                        stream, dpos),
                  "RoPE/KV write");
     const float scale = 1.0f / std::sqrt(static_cast<float>(c.head_size));
     launch_check(hipllm::launch_attn_decode(act.qkv, kcache(li), vcache(li), act.attn, act.attnq, act.attn_scratch,
                                             c.attention_head_count, c.kv_head_count, c.head_size, pos + 1, scale,
-                                            stream),
+                                            stream, dpos, max_sequence),
                  "attention");
     gemv(L.o, act.attn, act.attnq, nullptr, hidden, next_hidden);
     launch_check(hipllm::launch_rmsnorm(next_hidden, L.ffn_norm, act.norm, act.normq, 1, H, eps, stream), "RMSNorm");
@@ -386,7 +405,8 @@ void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, fl
     gemv(L.down, act.ffn, act.ffnq, nullptr, next_hidden, hidden);
 }
 
-void HipLLM::Impl::token_step(const std::int32_t* device_id, std::size_t pos, bool head) {
+void HipLLM::Impl::token_step(const std::int32_t* device_id, std::size_t pos, bool head,
+                              const std::uint32_t* dpos) {
     const ModelConfig& c = config;
     const std::size_t H = c.embedding_size;
     float* h = act.hidden[0];
@@ -394,8 +414,32 @@ void HipLLM::Impl::token_step(const std::int32_t* device_id, std::size_t pos, bo
     launch_check(hipllm::launch_embed(embedding.type, embedding.ptr, embedding.row_bytes, device_id, 1,
                                       c.vocabulary_size, H, h, stream),
                  "embedding");
-    for (std::size_t l = 0; l < layers.size(); ++l) layer_step(l, pos, h, tmp);
+    for (std::size_t l = 0; l < layers.size(); ++l) layer_step(l, pos, h, tmp, dpos);
     if (head) head_step(h);
+}
+
+// Records one decode step (embedding of act.step[0] at position act.step[1],
+// every layer, LM head, argmax) as a graph. No allocation, copy or memset is
+// recorded: the host writes act.step with an ordinary copy before each replay.
+void HipLLM::Impl::capture_decode() {
+    hip_check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    try {
+        token_step(reinterpret_cast<const std::int32_t*>(act.step), 0, true, act.step + 1);
+    } catch (...) {
+        hipGraph_t g = nullptr;
+        hipStreamEndCapture(stream, &g);
+        if (g) hipGraphDestroy(g);
+        throw;
+    }
+    hip_check(hipStreamEndCapture(stream, &decode_graph), "hipStreamEndCapture");
+    hip_check(hipGraphInstantiate(&decode_exec, decode_graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+}
+
+void HipLLM::Impl::drop_decode_graph() {
+    if (decode_exec) hipGraphExecDestroy(decode_exec);
+    if (decode_graph) hipGraphDestroy(decode_graph);
+    decode_exec = nullptr;
+    decode_graph = nullptr;
 }
 
 // Batched prefill buffers, grown to the longest prompt seen.
@@ -572,9 +616,15 @@ std::int32_t HipLLM::decode(std::int32_t id) {
     if (pos >= m.max_sequence) throw std::length_error("HIP decode exceeds the allocated sequence capacity");
     hip_check(hipSetDevice(m.device), "hipSetDevice");
     const auto t0 = std::chrono::steady_clock::now();
-    m.host_ids[0] = id;
-    hip_check(hipMemcpyAsync(m.act.ids, m.host_ids, 4, hipMemcpyHostToDevice, m.stream), "hipMemcpy(id)");
-    m.token_step(m.act.ids, pos, true);
+    m.host_step[0] = static_cast<std::uint32_t>(id);
+    m.host_step[1] = static_cast<std::uint32_t>(pos);
+    hip_check(hipMemcpyAsync(m.act.step, m.host_step, 8, hipMemcpyHostToDevice, m.stream), "hipMemcpy(step)");
+    if (m.decode_graphs) {
+        if (!m.decode_exec) m.capture_decode();
+        hip_check(hipGraphLaunch(m.decode_exec, m.stream), "hipGraphLaunch(decode)");
+    } else {
+        m.token_step(reinterpret_cast<const std::int32_t*>(m.act.step), pos, true);
+    }
     const std::int32_t token = m.read_token();
     m.sequence_length = pos + 1;
     if (m.profile) {
@@ -630,6 +680,13 @@ void HipLLM::copy_last_logits(float* dst, std::size_t count) const {
     if (count != impl_->config.vocabulary_size) throw std::invalid_argument("logits buffer must hold the vocabulary");
     hip_check(hipStreamSynchronize(impl_->stream), "hipStreamSynchronize");
     hip_check(hipMemcpy(dst, impl_->act.logits, count * 4, hipMemcpyDeviceToHost), "hipMemcpy(logits)");
+}
+
+void HipLLM::set_decode_graphs(bool enabled) {
+    if (!impl_) throw std::runtime_error("HIP model is not initialized");
+    hip_check(hipStreamSynchronize(impl_->stream), "hipStreamSynchronize");
+    impl_->decode_graphs = enabled;
+    if (!enabled) impl_->drop_decode_graph();
 }
 
 void HipLLM::set_batched_prefill(bool enabled) {

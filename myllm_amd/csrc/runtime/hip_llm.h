@@ -77,6 +77,9 @@ public:
     // Prefill path selection: true = batched (GEMM) prefill, false = the
     // token-serial decode path for every prompt position.
     void set_batched_prefill(bool enabled);
+    // Decode path: true (default) = each decode step is one replay of a
+    // recorded HIP graph; false = the step's kernels are launched one by one.
+    void set_decode_graphs(bool enabled);
 
 private:
     struct Impl;

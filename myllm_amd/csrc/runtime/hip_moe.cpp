@@ -83,6 +83,7 @@ struct MoeActivations {
     void* argmax_scratch = nullptr;
     std::int32_t* ids = nullptr;            // [T] prompt / decode ids
     std::uint32_t* token = nullptr;
+    std::uint32_t* step = nullptr;          // decode step inputs: [token id, position]
 };
 
 }  // namespace
@@ -116,12 +117,21 @@ struct HipMoeLLM::Impl {
     MoeActivations act;
     std::int32_t* host_ids = nullptr;
     std::uint32_t* host_token = nullptr;
+    std::uint32_t* host_step = nullptr;  // pinned [token id, position]
     std::size_t host_ids_cap = 0;
     std::size_t last_rows = 0;
     std::FILE* profile = nullptr;
 
+    // One decode step recorded as a HIP graph (kernels read the token and
+    // position from act.step) and replayed per token.
+    bool decode_graphs = true;
+    hipGraph_t decode_graph = nullptr;
+    hipGraphExec_t decode_exec = nullptr;
+
     ~Impl() {
         if (stream) hipStreamSynchronize(stream);
+        drop_decode_graph();
+        if (host_step) hipHostFree(host_step);
         if (profile) std::fclose(profile);
         weights.release();
         if (state_arena) hipFree(state_arena);
@@ -142,10 +152,13 @@ struct HipMoeLLM::Impl {
 
     void proj(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, std::size_t ldx, std::size_t rows, float* y,
               std::size_t ldy, const float* residual = nullptr, std::size_t n_override = 0) const;
-    void attention_layer(std::size_t li, std::size_t rows, std::size_t pos0, float* hidden, float* next);
+    void attention_layer(std::size_t li, std::size_t rows, std::size_t pos0, float* hidden, float* next,
+                         const std::uint32_t* dpos);
     void deltanet_layer(std::size_t li, std::size_t rows, float* hidden, float* next);
     void moe_layer(std::size_t li, std::size_t rows, float* hidden, float* next);
-    void forward(std::size_t rows, std::size_t pos0);
+    void forward(std::size_t rows, std::size_t pos0, const std::int32_t* ids, const std::uint32_t* dpos = nullptr);
+    void capture_decode();
+    void drop_decode_graph();
     std::int32_t read_token();
 };
 
@@ -381,6 +394,7 @@ void HipMoeLLM::Impl::allocate_state() {
         p += hist_floats;
     }
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&host_token), 64, hipHostMallocDefault), "hipHostMalloc(token)");
+    hip_check(hipHostMalloc(reinterpret_cast<void**>(&host_step), 64, hipHostMallocDefault), "hipHostMalloc(step)");
     ensure_rows(1);
 }
 
@@ -414,6 +428,7 @@ void HipMoeLLM::Impl::zero_state() {
 void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
     if (n <= act_rows && act_arena) return;
     hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    drop_decode_graph();  // it points into the arena
     if (act_arena) hipFree(act_arena);
     if (route_ids) hipFree(route_ids);
     if (host_ids) hipHostFree(host_ids);
@@ -439,7 +454,7 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
                       o_shd = reserve(n * H), o_logits = reserve(config.vocabulary_size),
                       o_as = reserve(hipllm::attn_decode_scratch_floats(Hq, D, capacity)),
                       o_am = reserve(hipllm::argmax_scratch_bytes(config.vocabulary_size) / 4 + 1),
-                      o_ids = reserve(n), o_tok = reserve(16);
+                      o_ids = reserve(n), o_tok = reserve(16), o_step = reserve(4);
     act_bytes = off;
     hip_check(hipMalloc(&act_arena, act_bytes), "hipMalloc(MoE activations)");
     auto* b = static_cast<std::uint8_t*>(act_arena);
@@ -472,6 +487,7 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
     act.argmax_scratch = b + o_am;
     act.ids = reinterpret_cast<std::int32_t*>(b + o_ids);
     act.token = reinterpret_cast<std::uint32_t*>(b + o_tok);
+    act.step = reinterpret_cast<std::uint32_t*>(b + o_step);
     hip_check(hipMalloc(reinterpret_cast<void**>(&route_ids), layers.size() * n * K * 4), "hipMalloc(routes)");
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&host_ids), n * 4, hipHostMallocDefault), "hipHostMalloc(ids)");
     act_rows = n;
@@ -494,8 +510,10 @@ void HipMoeLLM::Impl::proj(const DevMatrix& w, const float* x, const hipllm::XGr
 
 // Gated full attention (moe_llm.mm:2238-2434) over `rows` rows at positions
 // pos0.. ; next = hidden + out_proj(attention * sigmoid(gate)).
+// dpos (device, nullable): the decode position read on the device (recorded
+// decode step); pos0 is used otherwise.
 void HipMoeLLM::Impl::attention_layer(std::size_t li, std::size_t rows, std::size_t pos0, float* hidden,
-                                      float* next) {
+                                      float* next, const std::uint32_t* dpos) {
     const MoeLayer& L = layers[li];
     const float eps = config.norm_epsilon;
     const std::size_t ldqkv = q_w + 2 * kv_w;
@@ -518,12 +536,12 @@ void HipMoeLLM::Impl::attention_layer(std::size_t li, std::size_t rows, std::siz
                                                  ldqkv, act.feat, q_w, rows, Hq, Hkv, D, eps, stream),
                  "Q/gate split + head norms");
     launch_check(hipllm::launch_rope_kv(act.wide2, rope_table, config.rotary_dimension, Hq, Hkv, D, pos0, rows, ldqkv,
-                                        L.kcache, L.vcache, stream),
+                                        L.kcache, L.vcache, stream, dpos),
                  "RoPE/KV write");
     const float scale = 1.0f / std::sqrt(static_cast<float>(D));
     if (rows == 1) {
         launch_check(hipllm::launch_attn_decode(act.wide2, L.kcache, L.vcache, act.feat2, nullptr, act.attn_scratch,
-                                                Hq, Hkv, D, pos0 + 1, scale, stream),
+                                                Hq, Hkv, D, pos0 + 1, scale, stream, dpos, capacity),
                      "attention");
     } else {
         launch_check(hipllm::launch_attn_prefill(act.wide2, ldqkv, L.kcache, L.vcache, act.feat2, q_w, rows, Hq, Hkv,
@@ -623,18 +641,19 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
                  "MoE combine");
 }
 
-void HipMoeLLM::Impl::forward(std::size_t rows, std::size_t pos0) {
+void HipMoeLLM::Impl::forward(std::size_t rows, std::size_t pos0, const std::int32_t* ids,
+                              const std::uint32_t* dpos) {
     const float eps = config.norm_epsilon;
     float* h = act.hidden[0];
     float* tmp = act.hidden[1];
-    launch_check(hipllm::launch_embed(embedding.type, embedding.ptr, embedding.row_bytes, act.ids, rows,
+    launch_check(hipllm::launch_embed(embedding.type, embedding.ptr, embedding.row_bytes, ids, rows,
                                       config.vocabulary_size, H, h, stream),
                  "embedding");
     for (std::size_t l = 0; l < layers.size(); ++l) {
         const MoeLayer& L = layers[l];
         launch_check(hipllm::launch_rmsnorm(h, L.attn_norm, act.norm, act.normq, rows, H, eps, stream), "RMSNorm");
         if (L.full) {
-            attention_layer(l, rows, pos0, h, tmp);
+            attention_layer(l, rows, pos0, h, tmp, dpos);
         } else {
             deltanet_layer(l, rows, h, tmp);
         }
@@ -649,6 +668,30 @@ void HipMoeLLM::Impl::forward(std::size_t rows, std::size_t pos0) {
     launch_check(hipllm::launch_argmax(act.logits, config.vocabulary_size, act.token, act.argmax_scratch, stream),
                  "argmax");
     last_rows = rows;
+}
+
+// Records one decode step (token act.step[0] at position act.step[1]) as a
+// graph: no allocation, copy or memset is recorded; the host writes act.step
+// with an ordinary copy before each replay.
+void HipMoeLLM::Impl::capture_decode() {
+    hip_check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    try {
+        forward(1, 0, reinterpret_cast<const std::int32_t*>(act.step), act.step + 1);
+    } catch (...) {
+        hipGraph_t g = nullptr;
+        hipStreamEndCapture(stream, &g);
+        if (g) hipGraphDestroy(g);
+        throw;
+    }
+    hip_check(hipStreamEndCapture(stream, &decode_graph), "hipStreamEndCapture");
+    hip_check(hipGraphInstantiate(&decode_exec, decode_graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+}
+
+void HipMoeLLM::Impl::drop_decode_graph() {
+    if (decode_exec) hipGraphExecDestroy(decode_exec);
+    if (decode_graph) hipGraphDestroy(decode_graph);
+    decode_exec = nullptr;
+    decode_graph = nullptr;
 }
 
 std::int32_t HipMoeLLM::Impl::read_token() {
@@ -695,7 +738,7 @@ std::int32_t HipMoeLLM::prefill(const std::vector<std::int32_t>& ids) {
     std::memcpy(m.host_ids, ids.data(), ids.size() * 4);
     hip_check(hipMemcpyAsync(m.act.ids, m.host_ids, ids.size() * 4, hipMemcpyHostToDevice, m.stream),
               "hipMemcpy(ids)");
-    m.forward(ids.size(), 0);
+    m.forward(ids.size(), 0, m.act.ids);
     const std::int32_t token = m.read_token();
     m.sequence_length = ids.size();
     if (m.profile) {
@@ -716,9 +759,16 @@ std::int32_t HipMoeLLM::decode(std::int32_t id) {
     hip_check(hipSetDevice(m.device), "hipSetDevice");
     const auto t0 = std::chrono::steady_clock::now();
     const std::size_t pos = m.sequence_length;
-    m.host_ids[0] = id;
-    hip_check(hipMemcpyAsync(m.act.ids, m.host_ids, 4, hipMemcpyHostToDevice, m.stream), "hipMemcpy(id)");
-    m.forward(1, pos);
+    m.host_step[0] = static_cast<std::uint32_t>(id);
+    m.host_step[1] = static_cast<std::uint32_t>(pos);
+    hip_check(hipMemcpyAsync(m.act.step, m.host_step, 8, hipMemcpyHostToDevice, m.stream), "hipMemcpy(step)");
+    if (m.decode_graphs) {
+        if (!m.decode_exec) m.capture_decode();
+        hip_check(hipGraphLaunch(m.decode_exec, m.stream), "hipGraphLaunch(decode)");
+        m.last_rows = 1;
+    } else {
+        m.forward(1, pos, reinterpret_cast<const std::int32_t*>(m.act.step));
+    }
     const std::int32_t token = m.read_token();
     m.sequence_length = pos + 1;
     if (m.profile) {
@@ -726,6 +776,13 @@ std::int32_t HipMoeLLM::decode(std::int32_t id) {
         std::fprintf(m.profile, "decode,1,%zu,%.6f\n", pos + 1, ms);
     }
     return token;
+}
+
+void HipMoeLLM::set_decode_graphs(bool enabled) {
+    if (!impl_) throw std::runtime_error("MoE model is not initialized");
+    hip_check(hipStreamSynchronize(impl_->stream), "hipStreamSynchronize");
+    impl_->decode_graphs = enabled;
+    if (!enabled) impl_->drop_decode_graph();
 }
 
 void HipMoeLLM::enable_profiling(const std::string& csv_path, bool) {

@@ -55,6 +55,9 @@ public:
     bool available() const noexcept;
     const std::string& device_name() const noexcept;
     std::size_t expert_cache_count() const noexcept;
+    // Decode path: true (default) = each decode step is one replay of a
+    // recorded HIP graph; false = the step's kernels are launched one by one.
+    void set_decode_graphs(bool enabled);
 
     void copy_last_logits(float* destination, std::size_t count) const;
     // Expert ids chosen for the last token of the last forward, layer-major

@@ -113,6 +113,7 @@ SIGNATURES = {
     "hipllm_disable_profiling": (_I, [_P]),
     "hipllm_copy_logits": (_I, [_P, _P, _S]),
     "hipllm_set_batched_prefill": (_I, [_P, _I]),
+    "hipllm_set_decode_graphs": (_I, [_P, _I]),
     "hipllm_inspect_gguf": (_I, [ctypes.c_char_p, ctypes.POINTER(HipllmConfig)]),
 }
 
@@ -228,6 +229,10 @@ class HipLLM:
 
     def set_batched_prefill(self, enabled: bool) -> None:
         check(lib().hipllm_set_batched_prefill(self._h, 1 if enabled else 0))
+
+    def set_decode_graphs(self, enabled: bool) -> None:
+        """True (default): each decode step replays one recorded HIP graph."""
+        check(lib().hipllm_set_decode_graphs(self._h, 1 if enabled else 0))
 
     def routes(self) -> np.ndarray:
         """qwen35moe: expert ids of the last row of the last forward, [layers, top-k]."""

@@ -120,3 +120,32 @@ def test_reset_reproduces_same_tokens(cuda, golden_model):
         a = generate(m, list(g["prompt"]), 8)
         b = generate(m, list(g["prompt"]), 8)
     assert a == b == g["tokens"][:8].tolist()
+
+
+def _decode_run(path, prompts, steps, graphs, max_sequence=64):
+    """Tokens and logits of prefill + `steps` greedy decodes for each prompt
+    in turn (reset between prompts), with decode graphs on or off."""
+    toks, logits = [], []
+    with HipLLM(path, max_sequence) as m:
+        m.set_decode_graphs(graphs)
+        for prompt in prompts:
+            m.reset()
+            t = m.prefill(prompt)
+            toks.append(t)
+            for _ in range(steps):
+                t = m.decode(t)
+                toks.append(t)
+                logits.append(m.logits())
+    return toks, logits
+
+
+def test_decode_graph_matches_eager_launches(cuda, golden_model):
+    # The second, longer prompt regrows the activation arena, which must
+    # drop and re-record the decode graph.
+    path, g = golden_model("tiny")
+    prompts = [list(g["prompt"])[:4], list(g["prompt"]) * 2]
+    tg, lg = _decode_run(path, prompts, 10, True)
+    te, le = _decode_run(path, prompts, 10, False)
+    assert tg == te
+    for a, b in zip(lg, le):
+        assert np.abs(a - b).max() / np.abs(b).max() <= 1e-5

@@ -338,3 +338,27 @@ def test_moe_real_widths_match_float64_reference(cuda, tmp_path):
     assert got == ref
     assert all(routes)
     assert errs.max() <= 1e-3
+
+
+def test_moe_decode_graph_matches_eager_launches(cuda, moe_tiny):
+    prompts = [synth.uniform_ids(5, 512, seed=21).tolist(), synth.uniform_ids(13, 512, seed=22).tolist()]
+    out = {}
+    for graphs in (True, False):
+        toks, logits, routes = [], [], []
+        with HipLLM(moe_tiny, 40) as m:
+            m.set_decode_graphs(graphs)
+            for prompt in prompts:
+                m.reset()
+                t = m.prefill(prompt)
+                toks.append(t)
+                for _ in range(8):
+                    t = m.decode(t)
+                    toks.append(t)
+                    logits.append(m.logits())
+                    routes.append(m.routes().copy())
+        out[graphs] = (toks, logits, routes)
+    assert out[True][0] == out[False][0]
+    for a, b in zip(out[True][1], out[False][1]):
+        assert np.abs(a - b).max() / np.abs(b).max() <= 1e-5
+    for a, b in zip(out[True][2], out[False][2]):
+        np.testing.assert_array_equal(a, b)
