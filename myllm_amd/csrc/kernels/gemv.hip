@@ -763,8 +763,7 @@ int check_common(uint32_t type, const void* w, const void* w2, size_t row_bytes,
 // SwiGLU form (16-row blocks) measured best at 4 rows x 8 octets for FFN
 // widths and 2 x 4 for expert widths.
 int gemv_pick_shape(uint32_t type, uint32_t n, uint32_t units, int mode) {
-    if (type == kF32 || type == kF16) return gemv_default_tiling(n, units, mode);
-    if (mode == 1) return n >= 8192 ? 408 : 204;
+    if (type == kF32 || type == kF16 || mode == 1 || n < 1024) return gemv_default_tiling(n, units, mode);
     if (n >= 65536) return 802;
     const int R = n >= 16384 ? 4 : 2;
     const int OPR = units >= 12 ? 16 : 8;
@@ -773,26 +772,26 @@ int gemv_pick_shape(uint32_t type, uint32_t n, uint32_t units, int mode) {
 
 }  // namespace
 
-// Default tiling: launches >= 2048 waves where the shape allows, splits
-// units evenly across the octets of a row group, then prefers larger R
-// (activation reuse) and smaller OPR (fewer cross-octet reductions).
+// Default tiling from a simple cost model (used for F32 / F16 weights and
+// batched launches): the busiest lane's sequential units plus the data per
+// resident wave, where fewer than ~1500 waves leave HBM under-fed, and a
+// small charge per excess wave and for cross-wave reductions. The SwiGLU form
+// takes the measured 16-row-block choice.
 int gemv_default_tiling(uint32_t n, uint32_t units, int mode, uint32_t vectors) {
-    const uint32_t target_waves = 2048;
+    if (mode == 1) return n >= 8192 ? 408 : 204;
     int best = 0;
-    double best_score = -1.0;
+    double best_cost = 0.0;
     for (int t : kTilings) {
-        if (!tiling_ok(t, mode)) continue;
         const int R = t / 100, OPR = t % 100;
         const uint32_t rpb = 32u / OPR * R;
-        const uint32_t blocks = (n + rpb - 1) / rpb;
-        const uint32_t waves = blocks * 4 * vectors;
-        const uint32_t per = (units + OPR - 1) / OPR;  // units of the busiest octet
-        const double balance = static_cast<double>(units) / (per * OPR);
-        const double rows_used = static_cast<double>(n) / (blocks * rpb);
-        const double fill = waves >= target_waves ? 1.0 : static_cast<double>(waves) / target_waves;
-        const double score = fill * 4.0 + balance * 2.0 + rows_used + R * 0.05 - OPR * 0.005;
-        if (score > best_score) {
-            best_score = score;
+        const double blocks = static_cast<double>((n + rpb - 1) / rpb);
+        const double waves = blocks * 4.0 * vectors;
+        const double per = static_cast<double>((units + OPR - 1) / OPR);  // units of the busiest octet
+        const double work = static_cast<double>(n) * units * vectors;
+        const double cost = work / (waves < 1536.0 ? waves : 1536.0) + 2.0 * per + 0.5 * waves / 4096.0 +
+                            (OPR > 8 ? 0.5 : 0.0);
+        if (best == 0 || cost < best_cost) {
+            best_cost = cost;
             best = t;
         }
     }

@@ -33,23 +33,6 @@ __device__ __forceinline__ float softplus_ref(float v) {
     return v > 20.0f ? v : (v < -20.0f ? expf(v) : logf(1.0f + expf(v)));
 }
 
-__device__ __forceinline__ float block_max256(float v, float* red) {
-    v = warp_max(v);
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-}
-
-__device__ __forceinline__ float block_sum256(float v, float* red) {
-    v = warp_sum(v);
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    return (red[0] + red[1]) + (red[2] + red[3]);
-}
 
 // ------------------------------------------------------------ router
 // One block per token: softmax over the expert logits, then k rounds of a
@@ -59,85 +42,86 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 // scan with a strict '>' keeps, in the same rank order.
 constexpr uint32_t kMaxExperts = 1024;
 
-__global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, uint32_t ld,
-                                                          uint32_t experts, uint32_t k, int32_t* __restrict__ ids,
-                                                          float* __restrict__ weights) {
-    const uint32_t t = blockIdx.x;
-    const float* row = logits + static_cast<size_t>(t) * ld;
-    __shared__ float p[kMaxExperts];
-    __shared__ float red[4];
-    __shared__ float wv[4];
-    __shared__ uint32_t wi[4];
-    __shared__ float sel_v[8];
-    __shared__ uint32_t sel_i[8];
-    float m = -INFINITY;
-    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) m = fmaxf(m, row[e]);
-    m = block_max256(m, red);
-    float s = 0.0f;
-    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
-        const float v = row[e];
-        const float ex = v == -INFINITY ? 0.0f : expf(v - m);
-        p[e] = ex;
-        s += ex;
+// One 64-lane wave per token, expert e held by lane e % 64 in register
+// e / 64 (kPerLane per lane): softmax with wave reductions, then k rounds of
+// wave argmax (lower id on ties, the reference's strict '>' insertion order),
+// the winner removed from its lane; no LDS and no block barriers.
+constexpr uint32_t kPerLane = kMaxExperts / 64;
+
+__device__ __forceinline__ void wave_argmax(float& v, uint32_t& i) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(v, o);
+        const uint32_t oi = __shfl_xor(i, o);
+        if (ov > v || (ov == v && oi < i)) {
+            v = ov;
+            i = oi;
+        }
     }
-    s = block_sum256(s, red);
-    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) p[e] = s > 0.0f ? p[e] / s : 0.0f;
-    __syncthreads();
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (uint32_t r = 0; r < k; ++r) {
+}
+
+__global__ __launch_bounds__(64) void router_topk_kernel(const float* __restrict__ logits, uint32_t ld,
+                                                         uint32_t experts, uint32_t k, int32_t* __restrict__ ids,
+                                                         float* __restrict__ weights) {
+    const uint32_t t = blockIdx.x;
+    const uint32_t lane = threadIdx.x;
+    const float* row = logits + static_cast<size_t>(t) * ld;
+    float p[kPerLane];
+    float m = -INFINITY;
+#pragma unroll
+    for (uint32_t r = 0; r < kPerLane; ++r) {
+        const uint32_t e = lane + 64 * r;
+        p[r] = e < experts ? row[e] : -INFINITY;
+        m = fmaxf(m, p[r]);
+    }
+    m = warp_max(m);
+    float s = 0.0f;
+#pragma unroll
+    for (uint32_t r = 0; r < kPerLane; ++r) {
+        p[r] = p[r] == -INFINITY ? 0.0f : expf(p[r] - m);
+        s += lane + 64 * r < experts ? p[r] : 0.0f;
+    }
+    s = warp_sum(s);
+#pragma unroll
+    for (uint32_t r = 0; r < kPerLane; ++r) {
+        // Experts past the count, and NaN, are never selected.
+        const float v = s > 0.0f ? p[r] / s : 0.0f;
+        p[r] = (lane + 64 * r < experts && v == v) ? v : -INFINITY;
+    }
+    float my_v = 0.0f;  // lane r keeps the weight of rank r
+    uint32_t my_i = 0;
+    for (uint32_t rank = 0; rank < k; ++rank) {
         float bv = -INFINITY;
         uint32_t bi = 0xffffffffu;
-        for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
-            const float v = p[e];
-            if (v > bv) {  // e increases per thread, so '>' keeps the lower id on ties
-                bv = v;
-                bi = e;
-            }
-        }
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o);
-            const uint32_t oi = __shfl_xor(bi, o);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
+        for (uint32_t r = 0; r < kPerLane; ++r) {
+            if (p[r] > bv) {  // ids increase with r, so '>' keeps the lower id on ties
+                bv = p[r];
+                bi = lane + 64 * r;
             }
         }
-        if (lane == 0) {
-            wv[wave] = bv;
-            wi[wave] = bi;
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            float v = wv[0];
-            uint32_t i = wi[0];
-            for (uint32_t w = 1; w < 4; ++w) {
-                if (wv[w] > v || (wv[w] == v && wi[w] < i)) {
-                    v = wv[w];
-                    i = wi[w];
-                }
+        wave_argmax(bv, bi);
+        if (bi >= experts) {
+            // No candidate left (all remaining -inf): rank keeps -inf with
+            // id 0, as the insertion scan leaves it.
+            bv = -INFINITY;
+            bi = 0;
+        } else if ((bi & 63u) == lane) {
+#pragma unroll
+            for (uint32_t r = 0; r < kPerLane; ++r) {
+                if (r == (bi >> 6)) p[r] = -INFINITY;
             }
-            // No candidate left (all remaining -inf or NaN): rank r keeps
-            // -inf with id 0, as the insertion scan leaves it.
-            if (i >= experts) {
-                v = -INFINITY;
-                i = 0;
-            } else {
-                p[i] = -INFINITY;
-            }
-            sel_v[r] = v;
-            sel_i[r] = i;
         }
-        __syncthreads();
+        if (lane == rank) {
+            my_v = bv;
+            my_i = bi;
+        }
     }
-    if (threadIdx.x == 0) {
-        float sum = 0.0f;
-        for (uint32_t r = 0; r < k; ++r) sum += sel_v[r];
+    const float sum = warp_sum(lane < k ? my_v : 0.0f);
+    if (lane < k) {
         const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-        for (uint32_t r = 0; r < k; ++r) {
-            ids[t * k + r] = static_cast<int32_t>(sel_i[r]);
-            weights[t * k + r] = sel_v[r] * inv;
-        }
+        ids[static_cast<size_t>(t) * k + lane] = static_cast<int32_t>(my_i);
+        weights[static_cast<size_t>(t) * k + lane] = my_v * inv;
     }
 }
 
@@ -371,7 +355,7 @@ int launch_router_topk(const float* logits, size_t ld, size_t tokens, size_t exp
         return kInvalidArgument;
     }
     if (experts > kMaxExperts || tokens > 0x7fffffffull || ld > 0xffffffffull) return kLengthError;
-    hipLaunchKernelGGL(router_topk_kernel, dim3(static_cast<uint32_t>(tokens)), dim3(256), 0, stream, logits,
+    hipLaunchKernelGGL(router_topk_kernel, dim3(static_cast<uint32_t>(tokens)), dim3(64), 0, stream, logits,
                        static_cast<uint32_t>(ld), static_cast<uint32_t>(experts), static_cast<uint32_t>(k), ids,
                        weights);
     return launched();
