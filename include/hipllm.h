@@ -193,6 +193,15 @@ int hipllm_moe_combine(const float* residual, const float* down, const float* w,
                        const float* sgate, size_t ld_sgate, float* out, size_t tokens, size_t h, size_t k,
                        void* stream);
 
+/* hipllm_moe_combine followed by each finished row's RMSNorm (the next
+ * layer's input norm; h % 16 == 0): norm = rmsnorm(out) * gamma and its
+ * XGroup form normq (nullable). Replaces metal_expert_weighted_reduce_f32 +
+ * residual + metal_rmsnorm_f32 (metal_llm.metal:1525-1542, 914-924, 785-823;
+ * moe_llm.mm:2836-2885). */
+int hipllm_moe_combine_norm(const float* residual, const float* down, const float* w, const float* shared,
+                            const float* sgate, size_t ld_sgate, float* out, size_t tokens, size_t h, size_t k,
+                            const float* gamma, float eps, float* norm, void* normq, void* stream);
+
 /* decay = exp(softplus(alpha + dt_bias) a), beta = sigmoid(beta_raw).
  * Replaces the DeltaNet gate chain of encode_delta_net (moe_llm.mm:2462-2496;
  * metal_llm.metal:1186-1263). */

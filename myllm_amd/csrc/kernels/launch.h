@@ -64,6 +64,10 @@ int launch_router_topk(const float* logits, size_t ld, size_t tokens, size_t exp
 int launch_moe_combine(const float* residual, const float* down, const float* w, const float* shared,
                        const float* sgate, size_t ld_sgate, float* out, size_t tokens, size_t h, size_t k,
                        hipStream_t stream);
+// launch_moe_combine, then the RMSNorm of each finished row (h % 16 == 0).
+int launch_moe_combine_norm(const float* residual, const float* down, const float* w, const float* shared,
+                            const float* sgate, size_t ld_sgate, float* out, size_t tokens, size_t h, size_t k,
+                            const float* gamma, float eps, float* norm, XGroup* normq, hipStream_t stream);
 int launch_gdn_gates(const float* alpha, const float* beta_raw, size_t ld, const float* dt_bias, const float* a,
                      float* decay, float* beta, size_t tokens, size_t heads, hipStream_t stream);
 int launch_conv1d_silu(const float* x, size_t ldx, float* history, const float* w, float* out, size_t ldo,

@@ -20,6 +20,7 @@
 // written once per call however many tokens it scans; norms run one 64-lane
 // wave per head vector; everything else is one pass over its rows.
 #include "common.h"
+#include "norm.h"
 
 namespace hipllm {
 namespace {
@@ -139,6 +140,32 @@ __global__ void moe_combine_kernel(const float* __restrict__ residual, const flo
     float moe = acc;
     if (shared) moe += shared[i] * sigmoid_ref(sgate[static_cast<size_t>(t) * ld_sgate]);
     out[i] = residual[i] + moe;
+}
+
+// The same combine, one 1024-thread block per token row (enough loads in
+// flight for the k expert rows), followed by that row's RMSNorm (the next
+// layer's input norm) in the same block.
+__global__ __launch_bounds__(1024) void moe_combine_norm_kernel(const float* __restrict__ residual,
+                                                               const float* __restrict__ down,
+                                                               const float* __restrict__ w,
+                                                               const float* __restrict__ shared,
+                                                               const float* __restrict__ sgate, uint32_t ld_sgate,
+                                                               float* __restrict__ out, uint32_t h, uint32_t k,
+                                                               const float* __restrict__ gamma, float eps,
+                                                               float* __restrict__ norm, XGroup* __restrict__ normq) {
+    const uint32_t t = blockIdx.x;
+    const float sg = shared ? sigmoid_ref(sgate[static_cast<size_t>(t) * ld_sgate]) : 0.0f;
+    for (uint32_t c = threadIdx.x; c < h; c += blockDim.x) {
+        const size_t i = static_cast<size_t>(t) * h + c;
+        float acc = 0.0f;
+        for (uint32_t r = 0; r < k; ++r) acc += w[t * k + r] * down[(static_cast<size_t>(t) * k + r) * h + c];
+        float moe = acc;
+        if (shared) moe += shared[i] * sg;
+        out[i] = residual[i] + moe;
+    }
+    __syncthreads();  // the row is complete (block-visible) before the norm reads it
+    rmsnorm_row(out + static_cast<size_t>(t) * h, gamma, norm + static_cast<size_t>(t) * h,
+                normq ? normq + static_cast<size_t>(t) * (h / 16) : nullptr, h, eps);
 }
 
 // ------------------------------------------------------------ DeltaNet
@@ -371,6 +398,24 @@ int launch_moe_combine(const float* residual, const float* down, const float* w,
     hipLaunchKernelGGL(moe_combine_kernel, dim3(blocks_for(tokens * h, 256)), dim3(256), 0, stream, residual, down,
                        w, shared, sgate, static_cast<uint32_t>(ld_sgate), out, static_cast<uint32_t>(tokens),
                        static_cast<uint32_t>(h), static_cast<uint32_t>(k));
+    return launched();
+}
+
+int launch_moe_combine_norm(const float* residual, const float* down, const float* w, const float* shared,
+                            const float* sgate, size_t ld_sgate, float* out, size_t tokens, size_t h, size_t k,
+                            const float* gamma, float eps, float* norm, XGroup* normq, hipStream_t stream) {
+    if (!residual || !down || !w || !out || !gamma || !norm || tokens == 0 || h == 0 || k == 0 || !(eps > 0.0f) ||
+        (shared && (!sgate || !ld_sgate))) {
+        return kInvalidArgument;
+    }
+    if (h % 16 != 0 || reinterpret_cast<uintptr_t>(out) % 16 != 0 || reinterpret_cast<uintptr_t>(norm) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(gamma) % 16 != 0 || (normq && reinterpret_cast<uintptr_t>(normq) % 16 != 0)) {
+        return kInvalidArgument;
+    }
+    if (tokens > 0x7fffffffull || ld_sgate > 0xffffffffull || h > 0xffffffffull) return kLengthError;
+    hipLaunchKernelGGL(moe_combine_norm_kernel, dim3(static_cast<uint32_t>(tokens)), dim3(1024), 0, stream, residual,
+                       down, w, shared, sgate, static_cast<uint32_t>(ld_sgate), out, static_cast<uint32_t>(h),
+                       static_cast<uint32_t>(k), gamma, eps, norm, normq);
     return launched();
 }
 

@@ -9,73 +9,19 @@
 //                453-467 (p . V); GQA head map h / (Hq / Hkv) (897-905)
 //   argmax       cpu_llm.cpp:34-48 (first maximum), metal_llm.metal:1544-1644
 #include "formats.h"
+#include "norm.h"
 
 namespace hipllm {
 namespace {
 
 // ------------------------------------------------------------ RMSNorm
-// One block per row. y = x * (inv_rms * gamma) with inv_rms from a double
-// sum of squares, as CPULLM. Each thread owns whole 16-groups of the row, so
-// it also writes the XGroup form of y (yq, optional) that the next GEMV
-// consumes. The second pass re-reads x from cache.
+// One block per row (norm.h): y and, optionally, its XGroup form for the GEMV
+// that consumes it.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
                                                       float* __restrict__ y, XGroup* __restrict__ yq, uint32_t cols,
                                                       float eps) {
-    const uint32_t row = blockIdx.x;
-    const float* xr = x + static_cast<size_t>(row) * cols;
-    float* yr = y + static_cast<size_t>(row) * cols;
-    const uint32_t groups = cols / 16;
-    const bool vec = (cols % 4 == 0);
-    double ss = 0.0;
-    if (vec) {
-        const float4* x4 = reinterpret_cast<const float4*>(xr);
-        for (uint32_t i = threadIdx.x; i < cols / 4; i += blockDim.x) {
-            const float4 v = x4[i];
-            ss += static_cast<double>(v.x) * v.x + static_cast<double>(v.y) * v.y +
-                  static_cast<double>(v.z) * v.z + static_cast<double>(v.w) * v.w;
-        }
-    } else {
-        for (uint32_t i = threadIdx.x; i < cols; i += blockDim.x) {
-            const double v = xr[i];
-            ss += v * v;
-        }
-    }
-    ss = warp_sum_d(ss);
-    __shared__ double part[8];
-    __shared__ float inv_s;
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (lane == 0) part[wave] = ss;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        double t = 0.0;
-        for (uint32_t w = 0; w < (blockDim.x + 63) / 64; ++w) t += part[w];
-        const float ms = static_cast<float>(t / static_cast<double>(cols));
-        inv_s = 1.0f / sqrtf(ms + eps);
-    }
-    __syncthreads();
-    const float inv = inv_s;
-    if (vec) {
-        for (uint32_t g = threadIdx.x; g < groups; g += blockDim.x) {
-            const float4* x4 = reinterpret_cast<const float4*>(xr + 16 * g);
-            const float4* g4 = reinterpret_cast<const float4*>(gamma + 16 * g);
-            float4* y4 = reinterpret_cast<float4*>(yr + 16 * g);
-            float v[16];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4 a = x4[i], b = g4[i];
-                const float4 o = make_float4(a.x * (inv * b.x), a.y * (inv * b.y), a.z * (inv * b.z), a.w * (inv * b.w));
-                y4[i] = o;
-                v[4 * i] = o.x;
-                v[4 * i + 1] = o.y;
-                v[4 * i + 2] = o.z;
-                v[4 * i + 3] = o.w;
-            }
-            if (yq) xgroup_encode(v, yq + static_cast<size_t>(row) * groups + g);
-        }
-        for (uint32_t c = groups * 16 + threadIdx.x; c < cols; c += blockDim.x) yr[c] = xr[c] * (inv * gamma[c]);
-    } else {
-        for (uint32_t c = threadIdx.x; c < cols; c += blockDim.x) yr[c] = xr[c] * (inv * gamma[c]);
-    }
+    const size_t row = blockIdx.x;
+    rmsnorm_row(x + row * cols, gamma, y + row * cols, yq ? yq + row * (cols / 16) : nullptr, cols, eps);
 }
 
 // ------------------------------------------------------------ embedding

@@ -148,6 +148,7 @@ struct HipLLM::Impl {
     void prefill_layer(std::size_t li, std::size_t rows, float* hidden, float* next_hidden);
     void prefill_batched(std::size_t rows);
     void head_step(const float* hidden_row);
+    void head_logits();
     std::int32_t read_token();
 };
 
@@ -372,7 +373,7 @@ void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, fl
     const DevLayer& L = layers[li];
     const std::size_t H = c.embedding_size, F = c.feed_forward_size;
     const float eps = c.norm_epsilon;
-    launch_check(hipllm::launch_rmsnorm(hidden, L.attn_norm, act.norm, act.normq, 1, H, eps, stream), "RMSNorm");
+    // act.norm / act.normq hold rmsnorm(hidden) * attn_norm on entry.
     if (L.fused_qkv) {
         gemv(L.q, act.norm, act.normq, L.qkv_bias, nullptr, act.qkv, H + 2 * kv_dim);
     } else {
@@ -401,8 +402,11 @@ void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, fl
         gemv(L.up, act.norm, act.normq, nullptr, nullptr, act.ffn);
         launch_check(hipllm::launch_swiglu(act.gate_tmp, act.ffn, act.ffn, act.ffnq, F, stream), "SwiGLU");
     }
-    // The layer output lands back in `hidden`.
+    // The layer output lands back in `hidden`, followed by its RMSNorm with
+    // the next layer's attention gain (or the output norm after the last).
     gemv(L.down, act.ffn, act.ffnq, nullptr, next_hidden, hidden);
+    const float* next_gamma = li + 1 < layers.size() ? layers[li + 1].attn_norm : output_norm;
+    launch_check(hipllm::launch_rmsnorm(hidden, next_gamma, act.norm, act.normq, 1, H, eps, stream), "RMSNorm");
 }
 
 void HipLLM::Impl::token_step(const std::int32_t* device_id, std::size_t pos, bool head,
@@ -414,8 +418,11 @@ void HipLLM::Impl::token_step(const std::int32_t* device_id, std::size_t pos, bo
     launch_check(hipllm::launch_embed(embedding.type, embedding.ptr, embedding.row_bytes, device_id, 1,
                                       c.vocabulary_size, H, h, stream),
                  "embedding");
+    launch_check(hipllm::launch_rmsnorm(h, layers[0].attn_norm, act.norm, act.normq, 1, H, c.norm_epsilon, stream),
+                 "RMSNorm");
     for (std::size_t l = 0; l < layers.size(); ++l) layer_step(l, pos, h, tmp, dpos);
-    if (head) head_step(h);
+    // The last layer's down GEMV already applied the output norm.
+    if (head) head_logits();
 }
 
 // Records one decode step (embedding of act.step[0] at position act.step[1],
@@ -530,6 +537,12 @@ void HipLLM::Impl::head_step(const float* hidden_row) {
     launch_check(hipllm::launch_rmsnorm(hidden_row, output_norm, act.norm, act.normq, 1, c.embedding_size,
                                         c.norm_epsilon, stream),
                  "final RMSNorm");
+    head_logits();
+}
+
+// LM head and argmax on the normalised row in act.norm / act.normq.
+void HipLLM::Impl::head_logits() {
+    const ModelConfig& c = config;
     gemv(output, act.norm, act.normq, nullptr, nullptr, act.logits);
     launch_check(hipllm::launch_argmax(act.logits, c.vocabulary_size, act.token, act.argmax_scratch, stream),
                  "argmax");

@@ -152,10 +152,12 @@ struct HipMoeLLM::Impl {
 
     void proj(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, std::size_t ldx, std::size_t rows, float* y,
               std::size_t ldy, const float* residual = nullptr, std::size_t n_override = 0) const;
+    void proj_out_norm(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, std::size_t ldx,
+                       std::size_t rows, float* next, const float* hidden, const float* gamma) const;
     void attention_layer(std::size_t li, std::size_t rows, std::size_t pos0, float* hidden, float* next,
                          const std::uint32_t* dpos);
     void deltanet_layer(std::size_t li, std::size_t rows, float* hidden, float* next);
-    void moe_layer(std::size_t li, std::size_t rows, float* hidden, float* next);
+    void moe_layer(std::size_t li, std::size_t rows, float* hidden, float* next, const float* next_gamma);
     void forward(std::size_t rows, std::size_t pos0, const std::int32_t* ids, const std::uint32_t* dpos = nullptr);
     void capture_decode();
     void drop_decode_graph();
@@ -508,6 +510,15 @@ void HipMoeLLM::Impl::proj(const DevMatrix& w, const float* x, const hipllm::XGr
                  "batched GEMV");
 }
 
+// Output projection of a mixer block with the residual, next = hidden + W x,
+// then act.norm = rmsnorm(next) * gamma (the post-mixer norm).
+void HipMoeLLM::Impl::proj_out_norm(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, std::size_t ldx,
+                                    std::size_t rows, float* next, const float* hidden, const float* gamma) const {
+    proj(w, x, xq, ldx, rows, next, H, hidden);
+    launch_check(hipllm::launch_rmsnorm(next, gamma, act.norm, act.normq, rows, H, config.norm_epsilon, stream),
+                 "RMSNorm");
+}
+
 // Gated full attention (moe_llm.mm:2238-2434) over `rows` rows at positions
 // pos0.. ; next = hidden + out_proj(attention * sigmoid(gate)).
 // dpos (device, nullable): the decode position read on the device (recorded
@@ -550,7 +561,7 @@ void HipMoeLLM::Impl::attention_layer(std::size_t li, std::size_t rows, std::siz
     }
     launch_check(hipllm::launch_gate_mul(act.feat2, act.feat, act.gated, act.gatedq, rows * q_w, stream),
                  "attention output gate");
-    proj(L.o, act.gated, act.gatedq, q_w, rows, next, H, hidden);
+    proj_out_norm(L.o, act.gated, act.gatedq, q_w, rows, next, hidden, L.post_norm);
 }
 
 // Gated DeltaNet (moe_llm.mm:2436-2640); next = hidden + out_proj(...).
@@ -585,12 +596,15 @@ void HipMoeLLM::Impl::deltanet_layer(std::size_t li, std::size_t rows, float* hi
     launch_check(hipllm::launch_gated_rmsnorm(act.feat2, inner, L.ssm_norm, act.feat, inner, act.gated, act.gatedq,
                                               inner, rows, Hv, S, eps, stream),
                  "DeltaNet gated norm");
-    proj(L.ssm_out, act.gated, act.gatedq, inner, rows, next, H, hidden);
+    proj_out_norm(L.ssm_out, act.gated, act.gatedq, inner, rows, next, hidden, L.post_norm);
 }
 
 // MoE FFN (moe_llm.mm:2642-2843): `hidden` is the attention residual; the
 // post-attention norm of it is in act.norm; next = hidden + routed + shared.
-void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden, float* next) {
+// next_gamma: the gain of the RMSNorm that follows (next layer's input norm or
+// the output norm), applied to `next` into act.norm in the combine launch.
+void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden, float* next,
+                                const float* next_gamma) {
     const MoeLayer& L = layers[li];
     std::int32_t* ids = route_ids + li * act_rows * K;
     // Router logits and the shared-expert gate in one GEMV when packed.
@@ -636,9 +650,10 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
                      "shared SwiGLU");
     }
     proj(L.sh_down, act.sh_act, act.sh_actq, FFs, rows, act.sh_down, H);
-    launch_check(hipllm::launch_moe_combine(hidden, act.down, act.rweight, act.sh_down, act.rlog + E, ldr, next, rows,
-                                            H, K, stream),
-                 "MoE combine");
+    launch_check(hipllm::launch_moe_combine_norm(hidden, act.down, act.rweight, act.sh_down, act.rlog + E, ldr, next,
+                                                 rows, H, K, next_gamma, config.norm_epsilon, act.norm, act.normq,
+                                                 stream),
+                 "MoE combine + RMSNorm");
 }
 
 void HipMoeLLM::Impl::forward(std::size_t rows, std::size_t pos0, const std::int32_t* ids,
@@ -649,20 +664,23 @@ void HipMoeLLM::Impl::forward(std::size_t rows, std::size_t pos0, const std::int
     launch_check(hipllm::launch_embed(embedding.type, embedding.ptr, embedding.row_bytes, ids, rows,
                                       config.vocabulary_size, H, h, stream),
                  "embedding");
+    // Each norm is fused into the launch that finishes its input row: the
+    // mixer's output projection applies post_norm, the MoE combine applies the
+    // next layer's input norm (the output norm after the last layer).
+    launch_check(hipllm::launch_rmsnorm(h, layers[0].attn_norm, act.norm, act.normq, rows, H, eps, stream),
+                 "RMSNorm");
     for (std::size_t l = 0; l < layers.size(); ++l) {
         const MoeLayer& L = layers[l];
-        launch_check(hipllm::launch_rmsnorm(h, L.attn_norm, act.norm, act.normq, rows, H, eps, stream), "RMSNorm");
         if (L.full) {
             attention_layer(l, rows, pos0, h, tmp, dpos);
         } else {
             deltanet_layer(l, rows, h, tmp);
         }
-        launch_check(hipllm::launch_rmsnorm(tmp, L.post_norm, act.norm, act.normq, rows, H, eps, stream), "RMSNorm");
-        moe_layer(l, rows, tmp, h);
+        moe_layer(l, rows, tmp, h, l + 1 < layers.size() ? layers[l + 1].attn_norm : output_norm);
     }
-    const float* last = h + (rows - 1) * H;
-    launch_check(hipllm::launch_rmsnorm(last, output_norm, act.norm, act.normq, 1, H, eps, stream), "final RMSNorm");
-    launch_check(hipllm::launch_gemv_prepped(output.type, output.ptr, output.row_bytes, act.norm, act.normq, nullptr,
+    const float* last = act.norm + (rows - 1) * H;
+    const hipllm::XGroup* lastq = act.normq + (rows - 1) * (H / 16);
+    launch_check(hipllm::launch_gemv_prepped(output.type, output.ptr, output.row_bytes, last, lastq, nullptr,
                                              nullptr, act.logits, config.vocabulary_size, H, 0, stream),
                  "LM head");
     launch_check(hipllm::launch_argmax(act.logits, config.vocabulary_size, act.token, act.argmax_scratch, stream),

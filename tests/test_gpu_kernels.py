@@ -377,3 +377,4 @@ def test_launchers_reject_bad_arguments(cuda):
     with pytest.raises(ValueError):
         kernels.rmsnorm(y, y, y, None, 1, 16, 0.0)  # eps must be positive
     assert lib().hipllm_version()
+
