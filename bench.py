@@ -108,16 +108,31 @@ def gemv_setup(qtype, torch, cuda):
     return rot, launch
 
 
-def time_kernel(torch, fn, count):
-    """Average duration of fn(i) over `count` launches, HIP events on the
-    current stream (the stream the launchers use)."""
+def time_kernel(torch, fn, count, replays=5):
+    """Average launch duration of fn(i, stream) over `count` launches recorded
+    in one HIP graph and replayed `replays` times, timed with HIP events on the
+    stream the replays run on (torch's current stream), so host launch cost
+    is excluded and back-to-back launches are measured as the decode step runs
+    them."""
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        fn(0, side)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(count):
+                fn(i, side)
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for i in range(count):
-        fn(i)
+    for _ in range(replays):
+        graph.replay()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e-3 / count
+    del graph
+    return e0.elapsed_time(e1) * 1e-3 / (count * replays)
 
 
 def bench_gemv(qtype, steps, warmup, torch, cuda):
@@ -152,7 +167,7 @@ def bench_gemv(qtype, steps, warmup, torch, cuda):
     kernels_out = {}
     for name, n, k in SHAPES:
         reps = copies * 8
-        d = time_kernel(torch, lambda i: launch(i % copies, name, n, k), reps)
+        d = time_kernel(torch, lambda i, st: launch(i % copies, name, n, k, st), reps)
         b = gemv_bytes(n, k, rot.row_bytes(n, k))
         kernels_out[name] = {"n": n, "k": k, "bytes": b, "avg_us": d * 1e6, "gbps": b / d / 1e9, "launches": reps}
     del graph, rot
@@ -170,7 +185,7 @@ def bench_copy(torch, cuda, nbytes):
     dst = torch.empty(n, dtype=torch.float32, device=cuda)
     for b in bufs:
         b.fill_(1.0)
-    d = time_kernel(torch, lambda i: dst.copy_(bufs[i % 12]), 96)
+    d = time_kernel(torch, lambda i, st: dst.copy_(bufs[i % 12]), 96)
     return {"bytes_read": n * 4, "bytes_written": n * 4, "avg_us": d * 1e6, "gbps_read_plus_write": 2 * n * 4 / d / 1e9}
 
 
@@ -189,7 +204,8 @@ def bench_prefill_gemm(torch, cuda):
     for M in (64, 512, 2048):
         xb = torch.randn(M, K, device=cuda).to(torch.bfloat16)
         y = torch.empty(M, N, device=cuda)
-        fn = lambda i: kernels.gemm_mfma(synth.Q4_K, ws[i % copies], src.shape[1], xb, None, None, y, M, N, K)
+        fn = lambda i, st=None: kernels.gemm_mfma(synth.Q4_K, ws[i % copies], src.shape[1], xb, None, None, y, M, N, K,
+                                                  stream=st)
         for i in range(3):
             fn(i)
         d = time_kernel(torch, fn, 24)

@@ -85,7 +85,9 @@ int hipllm_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const fl
 
 /* Fused FFN gate/up GEMV + SwiGLU: y = silu(Wg x) * (Wu x); yq (nullable,
  * n % 16 == 0) receives the XGroup form of y. `tiling` 0 picks the default,
- * else one of 202, 204, 401, 402, 404, 408, 802, 804, 808, 816. Replaces the gate/up
+ * else one of the hipllm_gemv_prepped tilings; with yq only those whose
+ * blocks hold whole 16-groups of y: 202, 204, 401, 402, 404, 408, 802, 804,
+ * 808, 816. Replaces the gate/up
  * encode_vector_product pair + metal_swiglu_f32 (metal_llm.mm:2885-2894;
  * metal_llm.metal:895-911), cpu_llm.cpp:905-909. */
 int hipllm_gemv_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
@@ -192,15 +194,6 @@ int hipllm_router_topk(const float* logits, size_t ld, size_t tokens, size_t exp
 int hipllm_moe_combine(const float* residual, const float* down, const float* w, const float* shared,
                        const float* sgate, size_t ld_sgate, float* out, size_t tokens, size_t h, size_t k,
                        void* stream);
-
-/* hipllm_moe_combine followed by each finished row's RMSNorm (the next
- * layer's input norm; h % 16 == 0): norm = rmsnorm(out) * gamma and its
- * XGroup form normq (nullable). Replaces metal_expert_weighted_reduce_f32 +
- * residual + metal_rmsnorm_f32 (metal_llm.metal:1525-1542, 914-924, 785-823;
- * moe_llm.mm:2836-2885). */
-int hipllm_moe_combine_norm(const float* residual, const float* down, const float* w, const float* shared,
-                            const float* sgate, size_t ld_sgate, float* out, size_t tokens, size_t h, size_t k,
-                            const float* gamma, float eps, float* norm, void* normq, void* stream);
 
 /* decay = exp(softplus(alpha + dt_bias) a), beta = sigmoid(beta_raw).
  * Replaces the DeltaNet gate chain of encode_delta_net (moe_llm.mm:2462-2496;

@@ -111,22 +111,69 @@ __device__ __forceinline__ float ubyte1(uint32_t w) { return static_cast<float>(
 __device__ __forceinline__ float ubyte2(uint32_t w) { return static_cast<float>((w >> 16) & 0xffu); }
 __device__ __forceinline__ float ubyte3(uint32_t w) { return static_cast<float>((w >> 24) & 0xffu); }
 
-__device__ __forceinline__ float warp_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+// ---------------------------------------------------------------- wave reductions
+// Whole-wave reductions for uniform control flow, every lane receiving the
+// result: DPP steps inside each row of 16 lanes (swap neighbours, swap pairs,
+// mirror half-rows, mirror the row), after which every lane of a row holds
+// the row's result, then the four row results read with v_readlane and
+// combined in a fixed order. No LDS traffic and no address registers.
+constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1, 0, 3, 2]
+constexpr int kDppQuadXor2 = 0x4E;   // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+template <int Ctrl>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), Ctrl, 0xf, 0xf, true));
+}
+template <int Ctrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __uint_as_float(dpp_u32<Ctrl>(__float_as_uint(v)));
+}
+template <int Ctrl>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t b = static_cast<uint64_t>(__double_as_longlong(v));
+    const uint64_t lo = dpp_u32<Ctrl>(static_cast<uint32_t>(b));
+    const uint64_t hi = dpp_u32<Ctrl>(static_cast<uint32_t>(b >> 32));
+    return __longlong_as_double(static_cast<long long>(lo | (hi << 32)));
+}
+__device__ __forceinline__ float lane_f32(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ double lane_f64(double v, int lane) {
+    const uint64_t b = static_cast<uint64_t>(__double_as_longlong(v));
+    const uint64_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b), lane));
+    const uint64_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b >> 32), lane));
+    return __longlong_as_double(static_cast<long long>(lo | (hi << 32)));
 }
 
-__device__ __forceinline__ float warp_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+// Sum over the four lanes of each quad (lanes 4i .. 4i + 3), equal in all four.
+__device__ __forceinline__ float quad_sum(float v) {
+    v += dpp_f32<kDppQuadXor1>(v);
+    return v + dpp_f32<kDppQuadXor2>(v);
 }
 
-__device__ __forceinline__ double warp_sum_d(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+__device__ __forceinline__ float wave_sum(float v) {
+    v = quad_sum(v);
+    v += dpp_f32<kDppHalfMirror>(v);
+    v += dpp_f32<kDppMirror>(v);
+    return (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f32<kDppQuadXor1>(v));
+    v = fmaxf(v, dpp_f32<kDppQuadXor2>(v));
+    v = fmaxf(v, dpp_f32<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_f32<kDppMirror>(v));
+    return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+    v += dpp_f64<kDppQuadXor1>(v);
+    v += dpp_f64<kDppQuadXor2>(v);
+    v += dpp_f64<kDppHalfMirror>(v);
+    v += dpp_f64<kDppMirror>(v);
+    return (lane_f64(v, 0) + lane_f64(v, 16)) + (lane_f64(v, 32) + lane_f64(v, 48));
 }
 
 // ---------------------------------------------------------------- XGroup

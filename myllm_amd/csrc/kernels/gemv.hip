@@ -627,8 +627,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w
             }
         }
     }
-    if (MODE == 1 && yq) {
-        // The launcher allows yq only when RPB % 16 == 0: blocks own whole 16-groups.
+    if constexpr (MODE == 1 && RPB % 16 == 0) {
+        // yq needs blocks that own whole 16-groups; the launchers reject it otherwise.
+        if (!yq) return;
         __syncthreads();
         if (tid < static_cast<uint32_t>(RPB / 16) && blk_row0 + 16 * tid < n) {
             xgroup_encode_from(outs + 16 * tid, yq + (blk_row0 / 16 + tid));
@@ -646,10 +647,10 @@ __global__ void prep_x_kernel(const float* __restrict__ x, XGroup* __restrict__ 
 // Tiling code: 100 * R + OPR.
 constexpr int kTilings[] = {108, 116, 132, 202, 204, 208, 216, 232, 401, 402, 404, 408, 416, 432, 802, 804, 808, 816, 832};
 
-// The SwiGLU form writes whole 16-groups of its output per block: rows per
-// block (32 / OPR) R must be a multiple of 16.
-constexpr bool tiling_ok(int t, int mode) {
-    return mode == 0 || (32 / (t % 100)) * (t / 100) % 16 == 0;
+// The XGroup output of the SwiGLU form needs blocks that own whole 16-groups
+// of it: rows per block (32 / OPR) R must be a multiple of 16.
+constexpr bool writes_whole_groups(int t) {
+    return (32 / (t % 100)) * (t / 100) % 16 == 0;
 }
 
 template <uint32_t T, int MODE>
@@ -661,17 +662,13 @@ int launch_typed(int tiling, const void* w, const void* w2, size_t row_bytes, co
     const int R = tiling / 100, OPR = tiling % 100;
     if (R < 1 || OPR < 1 || 32 % OPR != 0) return kInvalidArgument;
     const uint32_t rpb = 32u / OPR * R;
-    if (MODE == 1 && yq && rpb % 16 != 0) return kInvalidArgument;
+    if (MODE == 1 && yq && !writes_whole_groups(tiling)) return kInvalidArgument;
     const dim3 grid((n + rpb - 1) / rpb, vectors);
     switch (tiling) {
 #define HIPLLM_GEMV_CASE(RR, OO)                                                                               \
     case 100 * RR + OO:                                                                                        \
-        if constexpr (tiling_ok(100 * RR + OO, MODE)) {                                                        \
-            hipLaunchKernelGGL((gemv_kernel<T, RR, OO, MODE>), grid, dim3(256), 0, stream, wp, wp2, row_bytes, \
-                               x, xq, bias, residual, y, yq, n, units, kblocks, batch);                        \
-        } else {                                                                                               \
-            return kInvalidArgument;                                                                           \
-        }                                                                                                      \
+        hipLaunchKernelGGL((gemv_kernel<T, RR, OO, MODE>), grid, dim3(256), 0, stream, wp, wp2, row_bytes,     \
+                           x, xq, bias, residual, y, yq, n, units, kblocks, batch);                            \
         break;
         HIPLLM_GEMV_CASE(1, 8)
         HIPLLM_GEMV_CASE(1, 16)
@@ -765,7 +762,8 @@ int check_common(uint32_t type, const void* w, const void* w2, size_t row_bytes,
 int gemv_pick_shape(uint32_t type, uint32_t n, uint32_t units, int mode) {
     if (type == kF32 || type == kF16 || mode == 1 || n < 1024) return gemv_default_tiling(n, units, mode);
     if (n >= 65536) return 802;
-    const int R = n >= 16384 ? 4 : 2;
+    // Long rows (down projections) amortise the row setup over more units: 4 rows per octet.
+    const int R = (n >= 16384 || units >= 32) ? 4 : 2;
     const int OPR = units >= 12 ? 16 : 8;
     return 100 * R + OPR;
 }
@@ -776,9 +774,10 @@ int gemv_pick_shape(uint32_t type, uint32_t n, uint32_t units, int mode) {
 // batched launches): the busiest lane's sequential units plus the data per
 // resident wave, where fewer than ~1500 waves leave HBM under-fed, and a
 // small charge per excess wave and for cross-wave reductions. The SwiGLU form
-// takes the measured 16-row-block choice.
-int gemv_default_tiling(uint32_t n, uint32_t units, int mode, uint32_t vectors) {
-    if (mode == 1) return n >= 8192 ? 408 : 204;
+// takes the measured 16-row-block choice when it writes the XGroup form of
+// its output (blocks must own whole 16-groups), the cost model otherwise.
+int gemv_default_tiling(uint32_t n, uint32_t units, int mode, uint32_t vectors, bool whole_groups) {
+    if (mode == 1 && whole_groups) return n >= 8192 ? 408 : 204;
     int best = 0;
     double best_cost = 0.0;
     for (int t : kTilings) {
@@ -835,7 +834,7 @@ int launch_gemv_swiglu(uint32_t type, const void* wg, const void* wu, size_t row
     const uint32_t units = static_cast<uint32_t>((k + unit_elems(type) - 1) / unit_elems(type));
     const uint32_t nn = static_cast<uint32_t>(n);
     const int code = tiling ? tiling : gemv_pick_shape(type, nn, units, 1);
-    if (!valid_tiling(code) || !tiling_ok(code, 1)) return kInvalidArgument;
+    if (!valid_tiling(code) || (yq && !writes_whole_groups(code))) return kInvalidArgument;
     return launch_any<1>(type, code, wg, wu, row_bytes, x, xq, nullptr, nullptr, y, yq, nn, units,
                          static_cast<uint32_t>(k / 32), stream);
 }
@@ -878,7 +877,7 @@ int launch_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row
         return launch_any<0>(type, t, w, nullptr, row_bytes, x, xq, bias, residual, y, nullptr, nn, units, kb, stream,
                              b, nv);
     }
-    const int t = gemv_default_tiling(nn, units, 1, nv);
+    const int t = gemv_default_tiling(nn, units, 1, nv, yq != nullptr);
     return launch_any<1>(type, t, w, wu, row_bytes, x, xq, nullptr, nullptr, y, yq, nn, units, kb, stream, b, nv);
 }
 

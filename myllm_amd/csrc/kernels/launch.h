@@ -17,7 +17,7 @@ int launch_dequant_rows(uint32_t type, const void* w, size_t row_bytes, size_t r
 // GEMV inputs travel as FP32 values x plus their XGroup form xq (k / 16
 // groups, common.h); quantized weights read xq, F32 / F16 weights read x.
 int launch_prep_x(const float* x, XGroup* xq, size_t k, hipStream_t stream);
-int gemv_default_tiling(uint32_t n, uint32_t units, int mode, uint32_t vectors = 1);
+int gemv_default_tiling(uint32_t n, uint32_t units, int mode, uint32_t vectors = 1, bool whole_groups = true);
 int launch_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const float* x, const XGroup* xq,
                         const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
                         hipStream_t stream);
@@ -64,10 +64,6 @@ int launch_router_topk(const float* logits, size_t ld, size_t tokens, size_t exp
 int launch_moe_combine(const float* residual, const float* down, const float* w, const float* shared,
                        const float* sgate, size_t ld_sgate, float* out, size_t tokens, size_t h, size_t k,
                        hipStream_t stream);
-// launch_moe_combine, then the RMSNorm of each finished row (h % 16 == 0).
-int launch_moe_combine_norm(const float* residual, const float* down, const float* w, const float* shared,
-                            const float* sgate, size_t ld_sgate, float* out, size_t tokens, size_t h, size_t k,
-                            const float* gamma, float eps, float* norm, XGroup* normq, hipStream_t stream);
 int launch_gdn_gates(const float* alpha, const float* beta_raw, size_t ld, const float* dt_bias, const float* a,
                      float* decay, float* beta, size_t tokens, size_t heads, hipStream_t stream);
 int launch_conv1d_silu(const float* x, size_t ldx, float* history, const float* w, float* out, size_t ldo,

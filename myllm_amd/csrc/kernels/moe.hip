@@ -20,7 +20,6 @@
 // written once per call however many tokens it scans; norms run one 64-lane
 // wave per head vector; everything else is one pass over its rows.
 #include "common.h"
-#include "norm.h"
 
 namespace hipllm {
 namespace {
@@ -36,81 +35,96 @@ __device__ __forceinline__ float softplus_ref(float v) {
 
 
 // ------------------------------------------------------------ router
-// One block per token: softmax over the expert logits, then k rounds of a
-// block-wide argmax over the unselected experts (the larger probability, the
-// lower id on ties), then renormalisation. Taking maxima in descending order
-// with lower-id tie-breaks selects exactly what the reference's insertion
-// scan with a strict '>' keeps, in the same rank order.
+// One 64-lane wave per token, expert e held by lane e % 64 in register e / 64
+// (PL registers per lane, PL = 4 covers 256 experts): softmax with wave
+// reductions, then k rounds of a wave-wide maximum over 64-bit keys
+// (probability bits + 1 in the high word, the complemented expert id in the
+// low word, 0 for removed, NaN or absent experts), so one unsigned compare
+// orders by probability and, on equal probabilities, keeps the lower id.
+// Taking maxima in descending order with lower-id tie-breaks selects exactly
+// what the reference's insertion scan with a strict '>' keeps, in the same
+// rank order. The winner's register is cleared in its lane; no LDS, no
+// barriers, DPP and v_readlane only.
 constexpr uint32_t kMaxExperts = 1024;
 
-// One 64-lane wave per token, expert e held by lane e % 64 in register
-// e / 64 (kPerLane per lane): softmax with wave reductions, then k rounds of
-// wave argmax (lower id on ties, the reference's strict '>' insertion order),
-// the winner removed from its lane; no LDS and no block barriers.
-constexpr uint32_t kPerLane = kMaxExperts / 64;
-
-__device__ __forceinline__ void wave_argmax(float& v, uint32_t& i) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(v, o);
-        const uint32_t oi = __shfl_xor(i, o);
-        if (ov > v || (ov == v && oi < i)) {
-            v = ov;
-            i = oi;
-        }
-    }
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t key) {
+    auto step = [&](uint64_t other) { key = other > key ? other : key; };
+    auto mov = [](uint64_t v, auto ctrl) {
+        constexpr int c = decltype(ctrl)::value;
+        return static_cast<uint64_t>(dpp_u32<c>(static_cast<uint32_t>(v))) |
+               (static_cast<uint64_t>(dpp_u32<c>(static_cast<uint32_t>(v >> 32))) << 32);
+    };
+    step(mov(key, std::integral_constant<int, kDppQuadXor1>{}));
+    step(mov(key, std::integral_constant<int, kDppQuadXor2>{}));
+    step(mov(key, std::integral_constant<int, kDppHalfMirror>{}));
+    step(mov(key, std::integral_constant<int, kDppMirror>{}));
+    auto at = [&](int lane) {
+        return static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), lane))) |
+               (static_cast<uint64_t>(static_cast<uint32_t>(
+                    __builtin_amdgcn_readlane(static_cast<int>(key >> 32), lane))) << 32);
+    };
+    const uint64_t a = at(0), b = at(16), c = at(32), d = at(48);
+    const uint64_t ab = a > b ? a : b, cd = c > d ? c : d;
+    return ab > cd ? ab : cd;
 }
 
+template <uint32_t PL>
 __global__ __launch_bounds__(64) void router_topk_kernel(const float* __restrict__ logits, uint32_t ld,
                                                          uint32_t experts, uint32_t k, int32_t* __restrict__ ids,
                                                          float* __restrict__ weights) {
     const uint32_t t = blockIdx.x;
     const uint32_t lane = threadIdx.x;
     const float* row = logits + static_cast<size_t>(t) * ld;
-    float p[kPerLane];
+    float p[PL];
     float m = -INFINITY;
 #pragma unroll
-    for (uint32_t r = 0; r < kPerLane; ++r) {
+    for (uint32_t r = 0; r < PL; ++r) {
         const uint32_t e = lane + 64 * r;
         p[r] = e < experts ? row[e] : -INFINITY;
         m = fmaxf(m, p[r]);
     }
-    m = warp_max(m);
+    m = wave_max(m);
     float s = 0.0f;
 #pragma unroll
-    for (uint32_t r = 0; r < kPerLane; ++r) {
+    for (uint32_t r = 0; r < PL; ++r) {
         p[r] = p[r] == -INFINITY ? 0.0f : expf(p[r] - m);
         s += lane + 64 * r < experts ? p[r] : 0.0f;
     }
-    s = warp_sum(s);
+    s = wave_sum(s);
+    uint32_t key_hi[PL];  // probability bits + 1; 0 = not selectable
 #pragma unroll
-    for (uint32_t r = 0; r < kPerLane; ++r) {
-        // Experts past the count, and NaN, are never selected.
+    for (uint32_t r = 0; r < PL; ++r) {
+        // Probabilities are >= +0, so their bit patterns order like the values.
         const float v = s > 0.0f ? p[r] / s : 0.0f;
-        p[r] = (lane + 64 * r < experts && v == v) ? v : -INFINITY;
+        key_hi[r] = (lane + 64 * r < experts && v == v) ? __float_as_uint(v) + 1u : 0u;
     }
     float my_v = 0.0f;  // lane r keeps the weight of rank r
     uint32_t my_i = 0;
     for (uint32_t rank = 0; rank < k; ++rank) {
-        float bv = -INFINITY;
-        uint32_t bi = 0xffffffffu;
+        uint32_t bh = 0, bi = 0xffffffffu;
 #pragma unroll
-        for (uint32_t r = 0; r < kPerLane; ++r) {
-            if (p[r] > bv) {  // ids increase with r, so '>' keeps the lower id on ties
-                bv = p[r];
+        for (uint32_t r = 0; r < PL; ++r) {
+            if (key_hi[r] > bh) {  // ids increase with r, so '>' keeps the lower id on ties
+                bh = key_hi[r];
                 bi = lane + 64 * r;
             }
         }
-        wave_argmax(bv, bi);
-        if (bi >= experts) {
+        const uint64_t best = wave_max_key((static_cast<uint64_t>(bh) << 32) | static_cast<uint32_t>(~bi));
+        bh = static_cast<uint32_t>(best >> 32);
+        bi = ~static_cast<uint32_t>(best);
+        float bv;
+        if (bh == 0) {
             // No candidate left (all remaining -inf): rank keeps -inf with
             // id 0, as the insertion scan leaves it.
             bv = -INFINITY;
             bi = 0;
-        } else if ((bi & 63u) == lane) {
+        } else {
+            bv = __uint_as_float(bh - 1u);
+            if ((bi & 63u) == lane) {
 #pragma unroll
-            for (uint32_t r = 0; r < kPerLane; ++r) {
-                if (r == (bi >> 6)) p[r] = -INFINITY;
+                for (uint32_t r = 0; r < PL; ++r) {
+                    if (r == (bi >> 6)) key_hi[r] = 0;
+                }
             }
         }
         if (lane == rank) {
@@ -118,7 +132,7 @@ __global__ __launch_bounds__(64) void router_topk_kernel(const float* __restrict
             my_i = bi;
         }
     }
-    const float sum = warp_sum(lane < k ? my_v : 0.0f);
+    const float sum = wave_sum(lane < k ? my_v : 0.0f);
     if (lane < k) {
         const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
         ids[static_cast<size_t>(t) * k + lane] = static_cast<int32_t>(my_i);
@@ -140,32 +154,6 @@ __global__ void moe_combine_kernel(const float* __restrict__ residual, const flo
     float moe = acc;
     if (shared) moe += shared[i] * sigmoid_ref(sgate[static_cast<size_t>(t) * ld_sgate]);
     out[i] = residual[i] + moe;
-}
-
-// The same combine, one 1024-thread block per token row (enough loads in
-// flight for the k expert rows), followed by that row's RMSNorm (the next
-// layer's input norm) in the same block.
-__global__ __launch_bounds__(1024) void moe_combine_norm_kernel(const float* __restrict__ residual,
-                                                               const float* __restrict__ down,
-                                                               const float* __restrict__ w,
-                                                               const float* __restrict__ shared,
-                                                               const float* __restrict__ sgate, uint32_t ld_sgate,
-                                                               float* __restrict__ out, uint32_t h, uint32_t k,
-                                                               const float* __restrict__ gamma, float eps,
-                                                               float* __restrict__ norm, XGroup* __restrict__ normq) {
-    const uint32_t t = blockIdx.x;
-    const float sg = shared ? sigmoid_ref(sgate[static_cast<size_t>(t) * ld_sgate]) : 0.0f;
-    for (uint32_t c = threadIdx.x; c < h; c += blockDim.x) {
-        const size_t i = static_cast<size_t>(t) * h + c;
-        float acc = 0.0f;
-        for (uint32_t r = 0; r < k; ++r) acc += w[t * k + r] * down[(static_cast<size_t>(t) * k + r) * h + c];
-        float moe = acc;
-        if (shared) moe += shared[i] * sg;
-        out[i] = residual[i] + moe;
-    }
-    __syncthreads();  // the row is complete (block-visible) before the norm reads it
-    rmsnorm_row(out + static_cast<size_t>(t) * h, gamma, norm + static_cast<size_t>(t) * h,
-                normq ? normq + static_cast<size_t>(t) * (h / 16) : nullptr, h, eps);
 }
 
 // ------------------------------------------------------------ DeltaNet
@@ -215,7 +203,7 @@ __global__ __launch_bounds__(64) void l2norm_heads_kernel(float* __restrict__ x,
     float* v = x + static_cast<size_t>(t) * ld + static_cast<size_t>(h) * d;
     float ss = 0.0f;
     for (uint32_t i = threadIdx.x; i < d; i += 64) ss += v[i] * v[i];
-    ss = warp_sum(ss);
+    ss = wave_sum(ss);
     const float inv = 1.0f / sqrtf(ss + eps);
     for (uint32_t i = threadIdx.x; i < d; i += 64) v[i] = v[i] * inv;
 }
@@ -299,7 +287,7 @@ __global__ __launch_bounds__(64) void gated_rmsnorm_kernel(const float* __restri
     __shared__ __align__(16) float vals[256];
     float ss = 0.0f;
     for (uint32_t i = threadIdx.x; i < d; i += 64) ss += ov[i] * ov[i];
-    ss = warp_sum(ss);
+    ss = wave_sum(ss);
     const float inv = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
     for (uint32_t i = threadIdx.x; i < d; i += 64) {
         const float zz = zv[i];
@@ -349,7 +337,7 @@ __global__ __launch_bounds__(64) void split_qgate_norm_kernel(const float* __res
     }
     float ss = 0.0f;
     for (uint32_t i = threadIdx.x; i < d; i += 64) ss += src[i] * src[i];
-    ss = warp_sum(ss);
+    ss = wave_sum(ss);
     const float inv = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
     for (uint32_t i = threadIdx.x; i < d; i += 64) dst[i] = src[i] * inv * gamma[i];
 }
@@ -382,7 +370,9 @@ int launch_router_topk(const float* logits, size_t ld, size_t tokens, size_t exp
         return kInvalidArgument;
     }
     if (experts > kMaxExperts || tokens > 0x7fffffffull || ld > 0xffffffffull) return kLengthError;
-    hipLaunchKernelGGL(router_topk_kernel, dim3(static_cast<uint32_t>(tokens)), dim3(64), 0, stream, logits,
+    auto kernel = experts <= 256 ? router_topk_kernel<4> : experts <= 512 ? router_topk_kernel<8>
+                                                                           : router_topk_kernel<kMaxExperts / 64>;
+    hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(tokens)), dim3(64), 0, stream, logits,
                        static_cast<uint32_t>(ld), static_cast<uint32_t>(experts), static_cast<uint32_t>(k), ids,
                        weights);
     return launched();
@@ -398,24 +388,6 @@ int launch_moe_combine(const float* residual, const float* down, const float* w,
     hipLaunchKernelGGL(moe_combine_kernel, dim3(blocks_for(tokens * h, 256)), dim3(256), 0, stream, residual, down,
                        w, shared, sgate, static_cast<uint32_t>(ld_sgate), out, static_cast<uint32_t>(tokens),
                        static_cast<uint32_t>(h), static_cast<uint32_t>(k));
-    return launched();
-}
-
-int launch_moe_combine_norm(const float* residual, const float* down, const float* w, const float* shared,
-                            const float* sgate, size_t ld_sgate, float* out, size_t tokens, size_t h, size_t k,
-                            const float* gamma, float eps, float* norm, XGroup* normq, hipStream_t stream) {
-    if (!residual || !down || !w || !out || !gamma || !norm || tokens == 0 || h == 0 || k == 0 || !(eps > 0.0f) ||
-        (shared && (!sgate || !ld_sgate))) {
-        return kInvalidArgument;
-    }
-    if (h % 16 != 0 || reinterpret_cast<uintptr_t>(out) % 16 != 0 || reinterpret_cast<uintptr_t>(norm) % 16 != 0 ||
-        reinterpret_cast<uintptr_t>(gamma) % 16 != 0 || (normq && reinterpret_cast<uintptr_t>(normq) % 16 != 0)) {
-        return kInvalidArgument;
-    }
-    if (tokens > 0x7fffffffull || ld_sgate > 0xffffffffull || h > 0xffffffffull) return kLengthError;
-    hipLaunchKernelGGL(moe_combine_norm_kernel, dim3(static_cast<uint32_t>(tokens)), dim3(1024), 0, stream, residual,
-                       down, w, shared, sgate, static_cast<uint32_t>(ld_sgate), out, static_cast<uint32_t>(h),
-                       static_cast<uint32_t>(k), gamma, eps, norm, normq);
     return launched();
 }
 

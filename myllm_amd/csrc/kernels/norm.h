@@ -32,7 +32,7 @@ __device__ inline void rmsnorm_row(const float* __restrict__ xr, const float* __
             ss += v * v;
         }
     }
-    ss = warp_sum_d(ss);
+    ss = wave_sum_d(ss);
     __shared__ double part[16];
     __shared__ float inv_s;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;

@@ -145,18 +145,17 @@ __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restri
                     dot = fmaf(kv.w, qv.w, dot);
                 }
             }
-            dot += __shfl_xor(dot, 1);
-            dot += __shfl_xor(dot, 2);
+            dot = quad_sum(dot);
             if (j < cnt) s = dot * scale;
         }
-        float cm = warp_max(s);
+        float cm = wave_max(s);
         if (lane == 0) red[wave] = cm;
         __syncthreads();
         cm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
         const float m_new = fmaxf(m_run, cm);  // finite: every chunk holds a key
         const float p = j < cnt ? expf(s - m_new) : 0.0f;
         if (qq == 0) ps[j] = p;
-        float l = warp_sum(qq == 0 ? p : 0.0f);
+        float l = wave_sum(qq == 0 ? p : 0.0f);
         __syncthreads();  // red[0..3] read by all; ps[] complete
         if (lane == 0) red[4 + wave] = l;
         __syncthreads();
@@ -269,14 +268,14 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
             }
             s = dot * scale;
         }
-        float cm = warp_max(s);
+        float cm = wave_max(s);
         if (lane == 0) red[wave] = cm;
         __syncthreads();
         cm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
         const float m_new = fmaxf(m_run, cm);  // finite: key t0 is always valid
         const float p = t < len ? expf(s - m_new) : 0.0f;
         ps[tid] = p;
-        float cs = warp_sum(p);
+        float cs = wave_sum(p);
         __syncthreads();  // red[0..3] read by all before reuse
         if (lane == 0) red[4 + wave] = cs;
         __syncthreads();

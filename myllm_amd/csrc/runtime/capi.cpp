@@ -352,14 +352,6 @@ int hipllm_moe_combine(const float* residual, const float* down, const float* w,
                   "hipllm_moe_combine: invalid arguments or launch failure");
 }
 
-int hipllm_moe_combine_norm(const float* residual, const float* down, const float* w, const float* shared,
-                            const float* sgate, size_t ld_sgate, float* out, size_t tokens, size_t h, size_t k,
-                            const float* gamma, float eps, float* norm, void* normq, void* stream) {
-    return status(hipllm::launch_moe_combine_norm(residual, down, w, shared, sgate, ld_sgate, out, tokens, h, k, gamma,
-                                                  eps, norm, xg(normq), as_stream(stream)),
-                  "hipllm_moe_combine_norm: invalid arguments or launch failure");
-}
-
 int hipllm_gdn_gates(const float* alpha, const float* beta_raw, size_t ld, const float* dt_bias, const float* a,
                      float* decay, float* beta, size_t tokens, size_t heads, void* stream) {
     return status(hipllm::launch_gdn_gates(alpha, beta_raw, ld, dt_bias, a, decay, beta, tokens, heads,

@@ -629,10 +629,14 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
     }
     launch_check(hipllm::launch_router_topk(act.rlog, ldr, rows, E, K, ids, act.rweight, stream), "router top-k");
     // Routed experts: gate/up + SwiGLU for every (row, route), then down.
+    // The gate/up launches spread rows thinly over many blocks (the expert and
+    // shared widths are small), so the XGroup form of their output comes from
+    // a separate pass rather than their epilogue (which needs 16-row blocks).
     launch_check(hipllm::launch_gemv_batched(L.gate_exps.type, L.gate_exps.ptr, L.up_exps.ptr, L.gate_exps.row_bytes,
-                                             act.norm, act.normq, nullptr, nullptr, act.act, act.actq, FF, H,
+                                             act.norm, act.normq, nullptr, nullptr, act.act, nullptr, FF, H,
                                              rows * K, ids, E, K, L.gate_exps.expert_stride, 0, H, FF, stream),
                  "expert gate/up");
+    launch_check(hipllm::launch_prep_x(act.act, act.actq, rows * K * FF, stream), "expert activations");
     launch_check(hipllm::launch_gemv_batched(L.down_exps.type, L.down_exps.ptr, nullptr, L.down_exps.row_bytes,
                                              act.act, act.actq, nullptr, nullptr, act.down, nullptr, H, FF, rows * K,
                                              ids, E, K, L.down_exps.expert_stride, 1, FF, H, stream),
@@ -640,9 +644,10 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
     // Shared expert.
     if (L.sh_gate.type == L.sh_up.type) {
         launch_check(hipllm::launch_gemv_batched(L.sh_gate.type, L.sh_gate.ptr, L.sh_up.ptr, L.sh_gate.row_bytes,
-                                                 act.norm, act.normq, nullptr, nullptr, act.sh_act, act.sh_actq, FFs,
+                                                 act.norm, act.normq, nullptr, nullptr, act.sh_act, nullptr, FFs,
                                                  H, rows, nullptr, 1, 1, 0, 0, H, FFs, stream),
                      "shared gate/up");
+        launch_check(hipllm::launch_prep_x(act.sh_act, act.sh_actq, rows * FFs, stream), "shared activations");
     } else {
         proj(L.sh_gate, act.norm, act.normq, H, rows, act.sh_down, FFs);
         proj(L.sh_up, act.norm, act.normq, H, rows, act.sh_act, FFs);
@@ -650,10 +655,11 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
                      "shared SwiGLU");
     }
     proj(L.sh_down, act.sh_act, act.sh_actq, FFs, rows, act.sh_down, H);
-    launch_check(hipllm::launch_moe_combine_norm(hidden, act.down, act.rweight, act.sh_down, act.rlog + E, ldr, next,
-                                                 rows, H, K, next_gamma, config.norm_epsilon, act.norm, act.normq,
-                                                 stream),
-                 "MoE combine + RMSNorm");
+    launch_check(hipllm::launch_moe_combine(hidden, act.down, act.rweight, act.sh_down, act.rlog + E, ldr, next, rows,
+                                            H, K, stream),
+                 "MoE combine");
+    launch_check(hipllm::launch_rmsnorm(next, next_gamma, act.norm, act.normq, rows, H, config.norm_epsilon, stream),
+                 "RMSNorm");
 }
 
 void HipMoeLLM::Impl::forward(std::size_t rows, std::size_t pos0, const std::int32_t* ids,

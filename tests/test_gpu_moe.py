@@ -363,24 +363,3 @@ def test_moe_decode_graph_matches_eager_launches(cuda, moe_tiny):
     for a, b in zip(out[True][2], out[False][2]):
         np.testing.assert_array_equal(a, b)
 
-
-def test_moe_combine_norm_matches_combine_then_rmsnorm(cuda):
-    rng = np.random.default_rng(19)
-    T, H, k, E = 3, 2048, 8, 257
-    res = t32(rng.normal(size=(T, H)).astype(np.float32), cuda)
-    down = t32(rng.normal(size=(T * k, H)).astype(np.float32), cuda)
-    w = t32(rng.random(size=(T, k)).astype(np.float32), cuda)
-    shared = t32(rng.normal(size=(T, H)).astype(np.float32), cuda)
-    rlog = t32(rng.normal(size=(T, E)).astype(np.float32), cuda)
-    gamma = t32((rng.normal(size=H) * 0.3 + 1.0).astype(np.float32), cuda)
-    out = torch.empty(T, H, device=cuda)
-    norm = torch.empty(T, H, device=cuda)
-    normq = torch.empty(T, H, device=cuda)
-    kernels.moe_combine_norm(res, down, w, shared, rlog[:, E - 1:], E, out, T, H, k, gamma, 1e-6, norm, normq)
-    out2 = torch.empty(T, H, device=cuda)
-    kernels.moe_combine(res, down, w, shared, rlog[:, E - 1:], E, out2, T, H, k)
-    norm2 = torch.empty(T, H, device=cuda)
-    kernels.rmsnorm(out, gamma, norm2, None, T, H, 1e-6)
-    assert rel_err(out.cpu().numpy(), out2.cpu().numpy()) <= 1e-6
-    assert np.array_equal(norm.cpu().numpy().view(np.uint32), norm2.cpu().numpy().view(np.uint32))
-    xgroup.check(normq, norm.cpu().numpy())
