@@ -101,11 +101,15 @@ int hipllm_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, voi
  * with X given as bf16 (hipllm_to_bf16), W in native GGUF rows, bf16 MFMA
  * with FP32 accumulation; k % 128 == 0. `tile` < 0 picks the default, else
  * 0..3 = 128x32, 128x64, 256x64, 256x128 (weight rows x X rows per block).
+ * `splits` 0 picks the default K split, else 1..1024 blocks along k: with
+ * more than one, y is first set to residual + bias and every split adds its
+ * partial sum with float atomics (y may alias residual).
  * Replaces metal_gemm_{q5_0,q8_0,q4_k,q6_k,f32} via encode_matrix_product
  * (metal_llm.metal:196-250, 621-704; metal_llm.mm:1782-1889) and CPULLM's
  * gemmt / gemmtb (cpu_llm.cpp:591-607, 631-653). */
 int hipllm_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* bias,
-                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, void* stream);
+                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, int splits,
+                     void* stream);
 
 /* Workspace bytes hipllm_gemm needs for m rows of k values. */
 size_t hipllm_gemm_workspace_bytes(size_t m, size_t k);

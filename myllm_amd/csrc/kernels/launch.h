@@ -30,10 +30,11 @@ int launch_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row
                         size_t expert_stride, int x_routed, size_t ldx, size_t ldy, hipStream_t stream);
 
 int gemm_default_tile(uint32_t m, uint32_t n);
+uint32_t gemm_default_splits(uint32_t m, uint32_t n, uint32_t k, int tile);
 int launch_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, hipStream_t stream);
 int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* bias,
-                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, hipStream_t stream,
-                     size_t ldy = 0);
+                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, int splits,
+                     hipStream_t stream, size_t ldy = 0);
 int launch_attn_prefill(const float* q, size_t q_stride, const float* kcache, const float* vcache, float* out,
                         size_t out_stride, size_t rows, size_t hq, size_t hkv, size_t d, size_t pos0, float scale,
                         hipStream_t stream);

@@ -341,7 +341,8 @@ template <uint32_t T, int NSUB, int MSUB>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restrict__ w, size_t row_bytes,
                                                         const __bf16* __restrict__ xb, const float* __restrict__ bias,
                                                         const float* __restrict__ residual, float* __restrict__ y,
-                                                        uint32_t m, uint32_t n, uint32_t k, uint32_t ldy) {
+                                                        uint32_t m, uint32_t n, uint32_t k, uint32_t ldy,
+                                                        uint32_t steps_per_split) {
     using WT = WTile<T>;
     constexpr int BM = 32 * MSUB;
     constexpr int WN = 32 * NSUB;
@@ -393,16 +394,18 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[ns][ms][i] = 0.0f;
 
-    const uint32_t steps = k / kStepK;
+    // K split: block z covers steps [z * steps_per_split, ...) of the k / 128.
+    const uint32_t kb0 = blockIdx.z * steps_per_split * kStepK;
+    const uint32_t steps = min(steps_per_split, k / kStepK - blockIdx.z * steps_per_split);
     typename WT::Raw raw[NSUB];
 #pragma unroll
-    for (int ns = 0; ns < NSUB; ++ns) raw[ns] = WT::load(wrow[ns], 0, h);
-    load_x(0);
+    for (int ns = 0; ns < NSUB; ++ns) raw[ns] = WT::load(wrow[ns], kb0, h);
+    load_x(kb0);
     store_x(0);
     __syncthreads();
 
     for (uint32_t st = 0; st < steps; ++st) {
-        const uint32_t kb = st * kStepK;
+        const uint32_t kb = kb0 + st * kStepK;
         const int buf = st & 1;
         bf16x8 bf[NSUB][8];
 #pragma unroll
@@ -430,11 +433,14 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
     }
 
     // Epilogue: acc[ns][ms][4 g + r] = Y[m0 + 32 ms + 8 g + 4 h + r][n0 + 32 ns + lr].
+    // With a K split, y already holds residual + bias (gemm_init_kernel) and
+    // every split adds its partial sum with a float atomic add in L2.
+    const bool split = gridDim.z > 1;
 #pragma unroll
     for (int ns = 0; ns < NSUB; ++ns) {
         const uint32_t col = n0 + 32 * ns + lr;
         if (col >= n) continue;
-        const float b = bias ? bias[col] : 0.0f;
+        const float b = (bias && !split) ? bias[col] : 0.0f;
 #pragma unroll
         for (int ms = 0; ms < MSUB; ++ms) {
 #pragma unroll
@@ -444,14 +450,29 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
                     const uint32_t row = m0 + 32 * ms + 8 * g + 4 * h + r;
                     if (row < m) {
                         const size_t o = static_cast<size_t>(row) * ldy + col;
-                        float v = acc[ns][ms][4 * g + r] + b;
-                        if (residual) v += residual[o];
-                        y[o] = v;
+                        if (split) {
+                            unsafeAtomicAdd(y + o, acc[ns][ms][4 * g + r]);
+                        } else {
+                            float v = acc[ns][ms][4 * g + r] + b;
+                            if (residual) v += residual[o];
+                            y[o] = v;
+                        }
                     }
                 }
             }
         }
     }
+}
+
+// y[r, c] = residual[r, c] + bias[c] (either may be absent): the starting
+// value a K-split GEMM accumulates into.
+__global__ void gemm_init_kernel(float* __restrict__ y, uint32_t ldy, const float* __restrict__ residual,
+                                 const float* __restrict__ bias, uint32_t m, uint32_t n) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<size_t>(m) * n) return;
+    const uint32_t r = static_cast<uint32_t>(i / n), c = static_cast<uint32_t>(i % n);
+    const size_t o = static_cast<size_t>(r) * ldy + c;
+    y[o] = (residual ? residual[o] : 0.0f) + (bias ? bias[c] : 0.0f);
 }
 
 // xb[r, c] = bf16(x[r * ldx + c]) for r < m, c < k (round to nearest even).
@@ -478,22 +499,30 @@ __global__ void to_bf16_kernel(const float* __restrict__ x, size_t ldx, __bf16* 
 
 template <uint32_t T, int NSUB, int MSUB>
 void launch_tile(const void* w, size_t row_bytes, const __bf16* xb, const float* bias, const float* residual, float* y,
-                 uint32_t m, uint32_t n, uint32_t k, uint32_t ldy, hipStream_t stream) {
+                 uint32_t m, uint32_t n, uint32_t k, uint32_t ldy, uint32_t splits, hipStream_t stream) {
     constexpr uint32_t BN = 4 * 32 * NSUB, BM = 32 * MSUB;
-    const dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM);
+    const uint32_t steps = k / kStepK;
+    const uint32_t per = (steps + splits - 1) / splits;
+    splits = (steps + per - 1) / per;  // every split gets at least one step
+    if (splits > 1) {
+        const size_t total = static_cast<size_t>(m) * n;
+        hipLaunchKernelGGL(gemm_init_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, stream,
+                           y, ldy, residual, bias, m, n);
+    }
+    const dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM, splits);
     hipLaunchKernelGGL((gemm_mfma_kernel<T, NSUB, MSUB>), grid, dim3(256), 0, stream,
-                       static_cast<const uint8_t*>(w), row_bytes, xb, bias, residual, y, m, n, k, ldy);
+                       static_cast<const uint8_t*>(w), row_bytes, xb, bias, residual, y, m, n, k, ldy, per);
 }
 
 template <uint32_t T>
 int launch_typed(int tile, const void* w, size_t row_bytes, const __bf16* xb, const float* bias,
-                 const float* residual, float* y, uint32_t m, uint32_t n, uint32_t k, uint32_t ldy,
+                 const float* residual, float* y, uint32_t m, uint32_t n, uint32_t k, uint32_t ldy, uint32_t splits,
                  hipStream_t stream) {
     switch (tile) {
-    case 0: launch_tile<T, 1, 1>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, stream); break;
-    case 1: launch_tile<T, 1, 2>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, stream); break;
-    case 2: launch_tile<T, 2, 2>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, stream); break;
-    case 3: launch_tile<T, 2, 4>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, stream); break;
+    case 0: launch_tile<T, 1, 1>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, splits, stream); break;
+    case 1: launch_tile<T, 1, 2>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, splits, stream); break;
+    case 2: launch_tile<T, 2, 2>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, splits, stream); break;
+    case 3: launch_tile<T, 2, 4>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, splits, stream); break;
     default: return kInvalidArgument;
     }
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
@@ -502,17 +531,12 @@ int launch_typed(int tile, const void* w, size_t row_bytes, const __bf16* xb, co
 }  // namespace
 
 // Tile choice: 0 = 128 x 32, 1 = 128 x 64, 2 = 256 x 64, 3 = 256 x 128
-// (weight rows x X rows per block). Larger tiles read weights fewer times;
-// smaller ones keep more blocks in flight when m or n is small.
-int gemm_default_tile(uint32_t m, uint32_t n) {
-    const uint64_t target = 512;  // about two blocks per CU
-    const uint32_t bn[4] = {128, 128, 256, 256}, bm[4] = {32, 64, 64, 128};
-    for (int t = 3; t >= 0; --t) {
-        const uint64_t blocks = static_cast<uint64_t>((n + bn[t] - 1) / bn[t]) * ((m + bm[t] - 1) / bm[t]);
-        if (blocks >= target) return t;
-    }
-    return m > 32 ? 1 : 0;
-}
+// (weight rows x X rows per block). Measured on the 7B prefill shapes (M 128
+// to 2048): 128 x 64 (160 VGPRs, three waves per SIMD) is fastest or within
+// a few percent everywhere once small grids are filled with a K split; the
+// larger tiles reuse weights more but run one wave per SIMD. 128 x 32 for a
+// single X tile.
+int gemm_default_tile(uint32_t m, uint32_t) { return m > 32 ? 1 : 0; }
 
 int launch_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, hipStream_t stream) {
     if (!x || !xb || m == 0 || k == 0 || k % 8 != 0 || ldx < k || ldx % 4 != 0) return kInvalidArgument;
@@ -526,9 +550,20 @@ int launch_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, hip
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
+// K splits: enough blocks for about two per CU, each split at least four
+// 128-k steps long.
+uint32_t gemm_default_splits(uint32_t m, uint32_t n, uint32_t k, int tile) {
+    const uint32_t bn[4] = {128, 128, 256, 256}, bm[4] = {32, 64, 64, 128};
+    const uint64_t blocks = static_cast<uint64_t>((n + bn[tile] - 1) / bn[tile]) * ((m + bm[tile] - 1) / bm[tile]);
+    const uint32_t steps = k / kStepK;
+    if (blocks >= 384 || steps < 8) return 1;
+    const uint32_t want = static_cast<uint32_t>((512 + blocks - 1) / blocks);
+    return max(1u, min(want, steps / 4));
+}
+
 int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* bias,
-                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, hipStream_t stream,
-                     size_t ldy) {
+                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, int splits,
+                     hipStream_t stream, size_t ldy) {
     if (ldy == 0) ldy = n;
     if (!w || !xb || !y || m == 0 || n == 0 || k == 0 || ldy < n || ldy > 0x7fffffffull) return kInvalidArgument;
     if (k % kStepK != 0) return kInvalidArgument;
@@ -544,15 +579,18 @@ int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void*
     }
     if (reinterpret_cast<uintptr_t>(xb) % 16 != 0) return kInvalidArgument;
     if (tile < 0) tile = gemm_default_tile(static_cast<uint32_t>(m), static_cast<uint32_t>(n));
+    if (tile > 3) return kInvalidArgument;
     const uint32_t M = static_cast<uint32_t>(m), N = static_cast<uint32_t>(n), K = static_cast<uint32_t>(k);
+    if (splits < 0 || splits > 1024) return kInvalidArgument;
+    const uint32_t S = splits == 0 ? gemm_default_splits(M, N, K, tile) : static_cast<uint32_t>(splits);
     const auto* x = static_cast<const __bf16*>(xb);
     switch (type) {
-    case kQ4_K: return launch_typed<kQ4_K>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), stream);
-    case kQ6_K: return launch_typed<kQ6_K>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), stream);
-    case kQ8_0: return launch_typed<kQ8_0>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), stream);
-    case kQ5_0: return launch_typed<kQ5_0>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), stream);
-    case kF32: return launch_typed<kF32>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), stream);
-    case kF16: return launch_typed<kF16>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), stream);
+    case kQ4_K: return launch_typed<kQ4_K>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
+    case kQ6_K: return launch_typed<kQ6_K>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
+    case kQ8_0: return launch_typed<kQ8_0>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
+    case kQ5_0: return launch_typed<kQ5_0>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
+    case kF32: return launch_typed<kF32>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
+    case kF16: return launch_typed<kF16>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
     default: return kInvalidArgument;
     }
 }

@@ -121,10 +121,11 @@ int hipllm_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, voi
 }
 
 int hipllm_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* bias,
-                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, void* stream) {
-    return status(hipllm::launch_gemm_mfma(type, w, row_bytes, xb, bias, residual, y, m, n, k, tile,
+                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, int splits,
+                     void* stream) {
+    return status(hipllm::launch_gemm_mfma(type, w, row_bytes, xb, bias, residual, y, m, n, k, tile, splits,
                                            as_stream(stream)),
-                  "hipllm_gemm_mfma: invalid arguments (k % 128 == 0, tile 0..3) or launch failure");
+                  "hipllm_gemm_mfma: invalid arguments (k % 128 == 0, tile -1..3, splits 0..1024) or launch failure");
 }
 
 size_t hipllm_gemm_workspace_bytes(size_t m, size_t k) { return (m * k * 2 + 255) / 256 * 256; }
@@ -134,7 +135,7 @@ int hipllm_gemm(uint32_t type, const void* w, size_t row_bytes, const float* x, 
     if (!workspace) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_gemm: workspace is null");
     const int rc = hipllm::launch_to_bf16(x, ldx, workspace, m, k, as_stream(stream));
     if (rc != hipllm::kOk) return status(rc, "hipllm_gemm: invalid activation arguments");
-    return status(hipllm::launch_gemm_mfma(type, w, row_bytes, workspace, bias, nullptr, y, m, n, k, -1,
+    return status(hipllm::launch_gemm_mfma(type, w, row_bytes, workspace, bias, nullptr, y, m, n, k, -1, 0,
                                            as_stream(stream)),
                   "hipllm_gemm: invalid arguments (k % 128 == 0) or launch failure");
 }

@@ -491,7 +491,7 @@ void HipLLM::Impl::gemm(const DevMatrix& w, const void* xb, const float* bias, c
                         std::size_t rows, std::size_t ldy, std::size_t n_override) const {
     const std::size_t n = n_override ? n_override : w.rows;
     launch_check(hipllm::launch_gemm_mfma(w.type, w.ptr, w.row_bytes, xb, bias, residual, y, rows, n, w.cols, -1,
-                                          stream, ldy),
+                                          0, stream, ldy),
                  "prefill matmul");
 }
 

@@ -72,7 +72,7 @@ SIGNATURES = {
     "hipllm_gemv_prepped": (_I, [_U32, _P, _S, _P, _P, _P, _P, _P, _S, _S, _I, _P]),
     "hipllm_gemv_swiglu": (_I, [_U32, _P, _P, _S, _P, _P, _P, _P, _S, _S, _I, _P]),
     "hipllm_to_bf16": (_I, [_P, _S, _P, _S, _S, _P]),
-    "hipllm_gemm_mfma": (_I, [_U32, _P, _S, _P, _P, _P, _P, _S, _S, _S, _I, _P]),
+    "hipllm_gemm_mfma": (_I, [_U32, _P, _S, _P, _P, _P, _P, _S, _S, _S, _I, _I, _P]),
     "hipllm_gemm_workspace_bytes": (_S, [_S, _S]),
     "hipllm_gemm": (_I, [_U32, _P, _S, _P, _S, _P, _P, _S, _S, _S, _P, _P]),
     "hipllm_rmsnorm": (_I, [_P, _P, _P, _P, _S, _S, _F, _P]),
@@ -315,9 +315,9 @@ def _k_to_bf16(x, ldx, xb, m, k, stream=None):
     check(lib().hipllm_to_bf16(_ptr(x), ldx, _ptr(xb), m, k, _stream(stream)))
 
 
-def _k_gemm_mfma(qtype, w, row_bytes, xb, bias, residual, y, m, n, k, tile=-1, stream=None):
+def _k_gemm_mfma(qtype, w, row_bytes, xb, bias, residual, y, m, n, k, tile=-1, stream=None, splits=0):
     check(lib().hipllm_gemm_mfma(qtype, _ptr(w), row_bytes, _ptr(xb), _ptr(bias), _ptr(residual), _ptr(y),
-                                 m, n, k, tile, _stream(stream)))
+                                 m, n, k, tile, splits, _stream(stream)))
 
 
 def _k_gemm(qtype, w, row_bytes, x, ldx, bias, y, m, n, k, workspace, stream=None):

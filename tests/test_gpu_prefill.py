@@ -23,7 +23,7 @@ pytestmark = pytest.mark.gpu
 TYPES = [synth.Q4_K, synth.Q6_K, synth.Q8_0, synth.Q5_0, synth.F16, synth.F32]
 
 
-def gemm_case(cuda, qtype, m, n, k, seed, tile=-1, bias=False, residual=False):
+def gemm_case(cuda, qtype, m, n, k, seed, tile=-1, bias=False, residual=False, splits=0, in_place=False):
     w = random_rows(qtype, n, k, seed)
     dw = dev_bytes(w, cuda)
     g = torch.Generator(device="cpu").manual_seed(seed)
@@ -32,8 +32,8 @@ def gemm_case(cuda, qtype, m, n, k, seed, tile=-1, bias=False, residual=False):
     kernels.to_bf16(x, k, xb, m, k)
     b = torch.randn(n, generator=g).to(cuda) if bias else None
     r = torch.randn(m, n, generator=g).to(cuda) if residual else None
-    y = torch.empty(m, n, dtype=torch.float32, device=cuda)
-    kernels.gemm_mfma(qtype, dw, w.shape[1], xb, b, r, y, m, n, k, tile)
+    y = r.clone() if in_place else torch.empty(m, n, dtype=torch.float32, device=cuda)
+    kernels.gemm_mfma(qtype, dw, w.shape[1], xb, b, y if in_place else r, y, m, n, k, tile, splits=splits)
     wf = torch.empty(n, k, dtype=torch.float32, device=cuda)
     kernels.dequant_rows(qtype, dw, w.shape[1], n, k, wf)
     ref = x.double() @ wf.double().T
@@ -53,6 +53,26 @@ def test_gemm_types_and_tiles_ragged(cuda, qtype, tile):
     # (both halves of a K-quant super-block).
     y, ref, ref_b = gemm_case(cuda, qtype, 77, 333, 512, seed=qtype * 10 + tile, tile=tile, bias=True,
                               residual=True)
+    assert rel_err(y, ref) <= 2e-2
+    assert rel_err(y, ref_b) <= 1e-4
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 7, 10])
+@pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q6_K, synth.Q8_0])
+def test_gemm_k_splits(cuda, qtype, splits):
+    # k = 1280: ten 128-steps, split 1, 2, 3 (4 + 4 + 2), 7 (2 x 5, so 5
+    # splits) and 10 ways; partial tiles, bias and residual on every split.
+    y, ref, ref_b = gemm_case(cuda, qtype, 45, 300, 1280, seed=splits, tile=1, bias=True, residual=True,
+                              splits=splits)
+    assert rel_err(y, ref) <= 2e-2
+    assert rel_err(y, ref_b) <= 1e-4
+
+
+@pytest.mark.parametrize("splits", [1, 4])
+def test_gemm_in_place_residual(cuda, splits):
+    # y aliases residual (the decoder's hidden-state update), with and without a K split.
+    y, ref, ref_b = gemm_case(cuda, synth.Q4_K, 33, 256, 1024, seed=8, tile=0, bias=True, residual=True,
+                              splits=splits, in_place=True)
     assert rel_err(y, ref) <= 2e-2
     assert rel_err(y, ref_b) <= 1e-4
 
@@ -102,3 +122,7 @@ def test_gemm_rejects_bad_arguments(cuda):
         kernels.gemm_mfma(synth.Q4_K, w, 144, xb, None, None, y, 2, 2, 256, 7)  # unknown tile
     with pytest.raises(ValueError):
         kernels.gemm_mfma(99, w, 144, xb, None, None, y, 2, 2, 256)  # unknown type
+    with pytest.raises(ValueError):
+        kernels.gemm_mfma(synth.Q4_K, w, 144, xb, None, None, y, 2, 2, 256, 0, splits=-1)
+    with pytest.raises(ValueError):
+        kernels.gemm_mfma(synth.Q4_K, w, 144, xb, None, None, y, 2, 2, 256, 0, splits=1025)
