@@ -216,6 +216,19 @@ def bench_prefill_gemm(torch, cuda):
                        "gbps": round(wbytes / d / 1e9, 1)}
     del ws
     torch.cuda.empty_cache()
+    # Context, not a comparison of like with like: the same product through
+    # torch.matmul (hipBLASLt) on plain bf16 weights (3.5x the bytes of Q4_K,
+    # no dequant), 4 rotated copies.
+    wb = [torch.randn(K, N, device=cuda).to(torch.bfloat16) for _ in range(4)]  # [K, N], no transposed view
+    for M in (64, 512, 2048):
+        xb = torch.randn(M, K, device=cuda).to(torch.bfloat16)
+        y = torch.empty(M, N, device=cuda, dtype=torch.bfloat16)
+        fn = lambda i, st=None: torch.matmul(xb, wb[i % 4], out=y)
+        d = time_kernel(torch, fn, 16)
+        tf = 2.0 * M * N * K / d / 1e12
+        out[str(M)]["hipblaslt_bf16_weights"] = {"avg_us": round(d * 1e6, 2), "tflops": round(tf, 1)}
+    del wb
+    torch.cuda.empty_cache()
     return out
 
 

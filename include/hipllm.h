@@ -100,7 +100,9 @@ int hipllm_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, voi
 /* Prefill matmul Y[m, n] = X[m, k] W[n, k]^T (+ bias[n]) (+ residual[m, n])
  * with X given as bf16 (hipllm_to_bf16), W in native GGUF rows, bf16 MFMA
  * with FP32 accumulation; k % 128 == 0. `tile` < 0 picks the default, else
- * 0..3 = 128x32, 128x64, 256x64, 256x128 (weight rows x X rows per block).
+ * 0..3 = 128x32, 128x64, 256x64, 256x128 (weight rows x X rows per block),
+ * 4, 5 = 128x128, 128x256 with each weight tile dequantized once into LDS
+ * and shared by all four waves.
  * `splits` 0 picks the default K split, else 1..1024 blocks along k: with
  * more than one, y is first set to residual + bias and every split adds its
  * partial sum with float atomics (y may alias residual).
@@ -229,6 +231,24 @@ int hipllm_gdn_scan(const float* q, const float* k, size_t ldqk, const float* v,
 int hipllm_gated_rmsnorm(const float* o, size_t ldo, const float* gamma, const float* z, size_t ldz, float* y,
                          void* yq, size_t ldy, size_t tokens, size_t heads, size_t d, float eps, void* stream);
 
+/* hipllm_conv1d_silu followed by hipllm_l2norm_heads on the first
+ * norm_channels channels (the Q and K heads), in one pass: one block per
+ * d-channel head segment (d = 64 or 128; channels and norm_channels
+ * multiples of d). Replaces the same Metal kernels as those two. */
+int hipllm_conv_l2norm(const float* x, size_t ldx, float* history, const float* w, float* out, size_t ldo,
+                       size_t tokens, size_t channels, size_t ksize, size_t norm_channels, size_t d, float eps,
+                       void* stream);
+
+/* hipllm_gdn_gates + hipllm_gdn_scan + hipllm_gated_rmsnorm in one launch,
+ * one block per value head: the gates come from the raw alpha / beta rows
+ * (alpha[t * ld_ab + h], beta_raw[t * ld_ab + h]), the head's outputs are
+ * normalised and gated by silu(z) in the block, y and its XGroup form yq
+ * (nullable) are written. Replaces the same Metal kernels as those three. */
+int hipllm_gdn_scan_gated(const float* q, const float* k, size_t ldqk, const float* v, size_t ldv, const float* alpha,
+                          const float* beta_raw, size_t ld_ab, const float* dt_bias, const float* a, float* state,
+                          const float* z, size_t ldz, const float* gamma, float* y, void* yq, size_t ldy,
+                          size_t tokens, size_t value_heads, size_t key_heads, size_t d, float eps, void* stream);
+
 /* Split the per-head interleaved [Q_h | gate_h] projection, RMSNorm Q and K
  * heads with their gammas, and lay out [Q | K | V] rows for RoPE + cache.
  * Replaces metal_split_interleaved_q_gate_f32 and the Q/K norms of
@@ -310,8 +330,10 @@ int hipllm_enable_profiling(HipllmModel* model, const char* csv_path);
 int hipllm_disable_profiling(HipllmModel* model);
 /* Logits of the last prefill/decode (vocabulary_size floats, host memory). */
 int hipllm_copy_logits(const HipllmModel* model, float* out, size_t count);
-/* qwen2 only: 1 = batched (bf16 MFMA) prefill, 0 = token-serial prefill
- * through the FP32 decode kernels. */
+/* qwen2: 1 = batched (bf16 MFMA) prefill, 0 = token-serial prefill through
+ * the FP32 decode kernels. qwen35moe: 1 = prompts of 16 or more rows run the
+ * dense projections as bf16 MFMA matmuls (the router stays FP32), 0 = FP32
+ * GEMVs for every row count. */
 int hipllm_set_batched_prefill(HipllmModel* model, int enabled);
 
 /* Decode path: 1 (default) = each decode step replays one recorded HIP graph

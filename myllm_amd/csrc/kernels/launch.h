@@ -29,7 +29,7 @@ int launch_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row
                         size_t k, size_t vectors, const int32_t* ids, size_t experts, size_t routes,
                         size_t expert_stride, int x_routed, size_t ldx, size_t ldy, hipStream_t stream);
 
-int gemm_default_tile(uint32_t m, uint32_t n);
+int gemm_default_tile(uint32_t m, uint32_t n, uint32_t k);
 uint32_t gemm_default_splits(uint32_t m, uint32_t n, uint32_t k, int tile);
 int launch_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, hipStream_t stream);
 int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* bias,
@@ -73,6 +73,14 @@ int launch_l2norm_heads(float* x, size_t ld, size_t tokens, size_t heads, size_t
 int launch_gdn_scan(const float* q, const float* k, size_t ldqk, const float* v, size_t ldv, const float* decay,
                     const float* beta, float* state, float* out, size_t ldo, size_t tokens, size_t value_heads,
                     size_t key_heads, size_t d, hipStream_t stream);
+int launch_conv_l2norm(const float* x, size_t ldx, float* history, const float* w, float* out, size_t ldo,
+                       size_t tokens, size_t channels, size_t ksize, size_t norm_channels, size_t d, float eps,
+                       hipStream_t stream);
+int launch_gdn_scan_gated(const float* q, const float* k, size_t ldqk, const float* v, size_t ldv, const float* alpha,
+                          const float* beta_raw, size_t ld_ab, const float* dt_bias, const float* a, float* state,
+                          const float* z, size_t ldz, const float* gamma, float* y, XGroup* yq, size_t ldy,
+                          size_t tokens, size_t value_heads, size_t key_heads, size_t d, float eps,
+                          hipStream_t stream);
 int launch_gated_rmsnorm(const float* o, size_t ldo, const float* gamma, const float* z, size_t ldz, float* y,
                          XGroup* yq, size_t ldy, size_t tokens, size_t heads, size_t d, float eps,
                          hipStream_t stream);

@@ -272,6 +272,140 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const float* __restrict__
     for (int i = 0; i < NPR; ++i) S[static_cast<size_t>(rg * NPR + i) * Dv + col] = s[i];
 }
 
+// Fused decode/prefill forms of the DeltaNet pieces above.
+//
+// Causal conv + SiLU + the L2 head norm in one pass: block `seg` owns the D
+// channels of one head segment ([seg D, seg D + D)), one thread per channel,
+// all tokens in order (history read first, written last); segments below
+// norm_channels (the Q and K heads) are L2-normalised per token with a
+// block-wide sum of squares. Same expressions as conv1d_silu_kernel and
+// l2norm_heads_kernel.
+template <uint32_t D>
+__global__ __launch_bounds__(D) void conv_l2norm_kernel(const float* __restrict__ x, uint32_t ldx,
+                                                        float* __restrict__ history, const float* __restrict__ w,
+                                                        float* __restrict__ out, uint32_t ldo, uint32_t tokens,
+                                                        uint32_t channels, uint32_t ksize, uint32_t norm_channels,
+                                                        float eps) {
+    constexpr uint32_t W = D / 64;
+    const uint32_t c = blockIdx.x * D + threadIdx.x;
+    const bool norm = blockIdx.x * D < norm_channels;  // uniform per block
+    const uint32_t hr = ksize - 1;
+    __shared__ float red[W];
+    float win[kMaxConv];
+    float taps[kMaxConv];
+    for (uint32_t i = 0; i < ksize; ++i) taps[i] = w[static_cast<size_t>(c) * ksize + i];
+    for (uint32_t i = 0; i < hr; ++i) win[i] = history[static_cast<size_t>(i) * channels + c];
+    for (uint32_t t = 0; t < tokens; ++t) {
+        win[hr] = x[static_cast<size_t>(t) * ldx + c];
+        float acc = 0.0f;
+        for (uint32_t i = 0; i < ksize; ++i) acc += win[i] * taps[i];
+        float v = acc * sigmoid_ref(acc);
+        if (norm) {
+            const float ss = wave_sum(v * v);
+            if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+            __syncthreads();
+            float tot = 0.0f;
+#pragma unroll
+            for (uint32_t i = 0; i < W; ++i) tot += red[i];
+            v = v * (1.0f / sqrtf(tot + eps));
+            __syncthreads();  // red[] reused by the next token
+        }
+        out[static_cast<size_t>(t) * ldo + c] = v;
+        for (uint32_t i = 0; i < hr; ++i) win[i] = win[i + 1];
+    }
+    for (uint32_t i = 0; i < hr; ++i) history[static_cast<size_t>(i) * channels + c] = win[i];
+}
+
+// Gated DeltaNet scan with its gates and the gated RMSNorm fused. Block =
+// value head h (all D columns), 256 threads: thread (col = tid % D,
+// rg = tid / D) holds rows [rg NPR, rg NPR + NPR) of column col of S_h.
+// Per token: decay = exp(softplus(alpha + dt_bias) a), beta = sigmoid(beta_raw)
+// (gdn_gates_kernel's expressions), the recurrence of gdn_scan_kernel, then
+// y = rmsnorm(o) * gamma * silu(z) over the head (gated_rmsnorm_kernel) and
+// its XGroup form. The state is read and written once per call.
+template <uint32_t D>
+__global__ __launch_bounds__(256) void gdn_scan_gated_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, uint32_t ldqk, const float* __restrict__ v,
+    uint32_t ldv, const float* __restrict__ alpha, const float* __restrict__ beta_raw, uint32_t ld_ab,
+    const float* __restrict__ dt_bias, const float* __restrict__ a, float* __restrict__ state,
+    const float* __restrict__ z, uint32_t ldz, const float* __restrict__ gamma, float* __restrict__ y,
+    XGroup* __restrict__ yq, uint32_t ldy, uint32_t tokens, uint32_t key_heads, float eps) {
+    constexpr uint32_t RG = 256 / D, NPR = D / RG;
+    const uint32_t h = blockIdx.x;
+    const uint32_t col = threadIdx.x % D, rg = threadIdx.x / D;
+    const uint32_t kh = h % key_heads;
+    float* S = state + static_cast<size_t>(h) * D * D;
+    float s[NPR];
+#pragma unroll
+    for (uint32_t i = 0; i < NPR; ++i) s[i] = S[static_cast<size_t>(rg * NPR + i) * D + col];
+    __shared__ float ks[D], qs[D];
+    __shared__ float part[RG][D];
+    __shared__ float red[D / 64];
+    __shared__ __align__(16) float vals[D];
+    const float qscale = 1.0f / sqrtf(static_cast<float>(D));
+    const float dtb = dt_bias[h], ah = a[h], gam = gamma[col];
+    for (uint32_t t = 0; t < tokens; ++t) {
+        for (uint32_t i = threadIdx.x; i < D; i += 256) {
+            ks[i] = k[static_cast<size_t>(t) * ldqk + kh * D + i];
+            qs[i] = q[static_cast<size_t>(t) * ldqk + kh * D + i];
+        }
+        const float g = expf(softplus_ref(alpha[static_cast<size_t>(t) * ld_ab + h] + dtb) * ah);
+        const float b = sigmoid_ref(beta_raw[static_cast<size_t>(t) * ld_ab + h]);
+        const float vv = v[static_cast<size_t>(t) * ldv + h * D + col];
+        __syncthreads();
+        float pp = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < NPR; ++i) {
+            s[i] *= g;
+            pp += s[i] * ks[rg * NPR + i];
+        }
+        part[rg][col] = pp;
+        __syncthreads();
+        float pred = 0.0f;
+#pragma unroll
+        for (uint32_t r = 0; r < RG; ++r) pred += part[r][col];
+        const float delta = b * (vv - pred);
+        float op = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < NPR; ++i) {
+            s[i] += ks[rg * NPR + i] * delta;
+            op += s[i] * qs[rg * NPR + i];
+        }
+        __syncthreads();  // everyone has read part[] (pred) before it is reused
+        part[rg][col] = op;
+        __syncthreads();
+        float o = 0.0f;
+#pragma unroll
+        for (uint32_t r = 0; r < RG; ++r) o += part[r][col];
+        o *= qscale;
+        // Gated RMSNorm over the head's D outputs (threads rg == 0 hold them).
+        if (rg == 0) {
+            const float ss = wave_sum(o * o);
+            if ((col & 63) == 0) red[col >> 6] = ss;
+        }
+        __syncthreads();
+        if (rg == 0) {
+            float tot = 0.0f;
+#pragma unroll
+            for (uint32_t i = 0; i < D / 64; ++i) tot += red[i];
+            const float inv = 1.0f / sqrtf(tot / static_cast<float>(D) + eps);
+            const float zz = z[static_cast<size_t>(t) * ldz + h * D + col];
+            const float yv = o * inv * gam * (zz * sigmoid_ref(zz));
+            y[static_cast<size_t>(t) * ldy + h * D + col] = yv;
+            vals[col] = yv;
+        }
+        __syncthreads();
+        if (yq && threadIdx.x < D / 16) {
+            xgroup_encode_from(vals + 16 * threadIdx.x,
+                               yq + static_cast<size_t>(t) * (ldy / 16) + static_cast<size_t>(h) * (D / 16) +
+                                   threadIdx.x);
+        }
+        __syncthreads();  // ks/qs/part/red/vals reused by the next token
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < NPR; ++i) S[static_cast<size_t>(rg * NPR + i) * D + col] = s[i];
+}
+
 // y = rmsnorm(o_head) * gamma * silu(z) per (row, value head); FP32 sum of
 // squares like the reference's per-head norm; yq (optional) the XGroup form
 // of y.
@@ -464,6 +598,64 @@ int launch_gated_rmsnorm(const float* o, size_t ldo, const float* gamma, const f
     hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3(static_cast<uint32_t>(tokens), static_cast<uint32_t>(heads)),
                        dim3(64), 0, stream, o, static_cast<uint32_t>(ldo), gamma, z, static_cast<uint32_t>(ldz), y,
                        yq, static_cast<uint32_t>(ldy), static_cast<uint32_t>(d), eps);
+    return launched();
+}
+
+int launch_conv_l2norm(const float* x, size_t ldx, float* history, const float* w, float* out, size_t ldo,
+                       size_t tokens, size_t channels, size_t ksize, size_t norm_channels, size_t d, float eps,
+                       hipStream_t stream) {
+    if (!x || !history || !w || !out || tokens == 0 || channels == 0 || ksize < 2 || ksize > kMaxConv ||
+        ldx < channels || ldo < channels || x == out || !(eps >= 0.0f)) {
+        return kInvalidArgument;
+    }
+    if ((d != 64 && d != 128) || channels % d != 0 || norm_channels % d != 0 || norm_channels > channels) {
+        return kInvalidArgument;
+    }
+    if (channels > 0x7fffffffull || tokens > 0x7fffffffull) return kLengthError;
+    const dim3 grid(static_cast<uint32_t>(channels / d));
+    const uint32_t T = static_cast<uint32_t>(tokens), C = static_cast<uint32_t>(channels),
+                   K = static_cast<uint32_t>(ksize), NC = static_cast<uint32_t>(norm_channels);
+    if (d == 64) {
+        hipLaunchKernelGGL(conv_l2norm_kernel<64>, grid, dim3(64), 0, stream, x, static_cast<uint32_t>(ldx), history,
+                           w, out, static_cast<uint32_t>(ldo), T, C, K, NC, eps);
+    } else {
+        hipLaunchKernelGGL(conv_l2norm_kernel<128>, grid, dim3(128), 0, stream, x, static_cast<uint32_t>(ldx), history,
+                           w, out, static_cast<uint32_t>(ldo), T, C, K, NC, eps);
+    }
+    return launched();
+}
+
+int launch_gdn_scan_gated(const float* q, const float* k, size_t ldqk, const float* v, size_t ldv, const float* alpha,
+                          const float* beta_raw, size_t ld_ab, const float* dt_bias, const float* a, float* state,
+                          const float* z, size_t ldz, const float* gamma, float* y, XGroup* yq, size_t ldy,
+                          size_t tokens, size_t value_heads, size_t key_heads, size_t d, float eps,
+                          hipStream_t stream) {
+    if (!q || !k || !v || !alpha || !beta_raw || !dt_bias || !a || !state || !z || !gamma || !y || tokens == 0 ||
+        value_heads == 0 || key_heads == 0 || value_heads % key_heads != 0 || !(eps > 0.0f)) {
+        return kInvalidArgument;
+    }
+    if (ldqk < key_heads * d || ldv < value_heads * d || ldz < value_heads * d || ldy < value_heads * d ||
+        ld_ab < value_heads) {
+        return kInvalidArgument;
+    }
+    if (yq && (ldy % 16 != 0 || reinterpret_cast<uintptr_t>(yq) % 16 != 0)) return kInvalidArgument;
+    if (tokens > 0x7fffffffull || value_heads > 0x7fffffffull) return kLengthError;
+    const dim3 grid(static_cast<uint32_t>(value_heads));
+    const uint32_t T = static_cast<uint32_t>(tokens), Hk = static_cast<uint32_t>(key_heads);
+    switch (d) {
+    case 64:
+        hipLaunchKernelGGL(gdn_scan_gated_kernel<64>, grid, dim3(256), 0, stream, q, k, static_cast<uint32_t>(ldqk), v,
+                           static_cast<uint32_t>(ldv), alpha, beta_raw, static_cast<uint32_t>(ld_ab), dt_bias, a,
+                           state, z, static_cast<uint32_t>(ldz), gamma, y, yq, static_cast<uint32_t>(ldy), T, Hk, eps);
+        break;
+    case 128:
+        hipLaunchKernelGGL(gdn_scan_gated_kernel<128>, grid, dim3(256), 0, stream, q, k, static_cast<uint32_t>(ldqk), v,
+                           static_cast<uint32_t>(ldv), alpha, beta_raw, static_cast<uint32_t>(ld_ab), dt_bias, a,
+                           state, z, static_cast<uint32_t>(ldz), gamma, y, yq, static_cast<uint32_t>(ldy), T, Hk, eps);
+        break;
+    default:
+        return kInvalidArgument;  // state size 64 or 128
+    }
     return launched();
 }
 

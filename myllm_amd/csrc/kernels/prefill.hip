@@ -20,8 +20,9 @@
 //   hi = (s >> 1) & 1, p = s & 1. X and W use the same map, so each MFMA sums
 //   over a permutation of its 16 k. This map lines up with the GGUF layouts:
 //   Q4_K's low/high nibbles (hi), Q6_K's quarters, Q8_0/Q5_0's 32-blocks.
-// * Dequantized values are computed in FP32 exactly as the reference
-//   dequantizer orders them (model.cpp:581-683) and rounded once to bf16.
+// * Dequantized values are computed in FP32 from the reference dequantizer's
+//   scales and offsets (model.cpp:581-683), one fused multiply-add per value,
+//   and rounded once to bf16.
 #include "common.h"
 
 namespace hipllm {
@@ -60,51 +61,53 @@ __device__ __forceinline__ float f16_bits(uint32_t bits) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits & 0xffffu)));
 }
 
-// Eight values v[i] = a * byte_i - b over the 8 bytes of (w0, w1), rounded to bf16.
-#pragma clang fp contract(off)
+// bf16 pairs and fragments built from dwords: v_cvt_pk_bf16_f32 rounds two
+// floats to nearest even in one instruction, and the fragment is four such
+// dwords, so no byte shuffles are needed to assemble it.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+    const f32x2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+// Hides a value's known bits from the optimizer, so that byte k of a masked
+// dword converts with one v_cvt_f32_ubyte{k} instead of a shift, a mask and
+// a byte-0 convert.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm("" : "+v"(v));
+    return v;
+}
+
+// Eight values v[i] = a * byte_i - b over the 8 bytes of (w0, w1), one fused
+// multiply-add each, rounded to bf16. Where b is a power-of-two multiple of a
+// (Q6_K's 32 a, Q8_0's 128 d) the result equals the reference's a * (q - c)
+// exactly; for Q4_K / Q5_0 it differs from the reference's rounded product
+// minus offset by at most one FP32 rounding, far below the bf16 rounding that
+// follows.
 __device__ __forceinline__ bf16x8 affine8(uint32_t w0, uint32_t w1, float a, float b) {
-    bf16x8 r;
-    r[0] = static_cast<__bf16>(a * ubyte0(w0) - b);
-    r[1] = static_cast<__bf16>(a * ubyte1(w0) - b);
-    r[2] = static_cast<__bf16>(a * ubyte2(w0) - b);
-    r[3] = static_cast<__bf16>(a * ubyte3(w0) - b);
-    r[4] = static_cast<__bf16>(a * ubyte0(w1) - b);
-    r[5] = static_cast<__bf16>(a * ubyte1(w1) - b);
-    r[6] = static_cast<__bf16>(a * ubyte2(w1) - b);
-    r[7] = static_cast<__bf16>(a * ubyte3(w1) - b);
-    return r;
+    w0 = opaque(w0);
+    w1 = opaque(w1);
+    const u32x4 u = {pack_bf16(__builtin_fmaf(a, ubyte0(w0), -b), __builtin_fmaf(a, ubyte1(w0), -b)),
+                     pack_bf16(__builtin_fmaf(a, ubyte2(w0), -b), __builtin_fmaf(a, ubyte3(w0), -b)),
+                     pack_bf16(__builtin_fmaf(a, ubyte0(w1), -b), __builtin_fmaf(a, ubyte1(w1), -b)),
+                     pack_bf16(__builtin_fmaf(a, ubyte2(w1), -b), __builtin_fmaf(a, ubyte3(w1), -b))};
+    return __builtin_bit_cast(bf16x8, u);
 }
 
-// Eight values v[i] = a * (byte_i - 32) (Q6_K) rounded to bf16.
+// Eight values v[i] = a * (byte_i - 32) (Q6_K) as a * byte_i - 32 a.
 __device__ __forceinline__ bf16x8 q6_8(uint32_t w0, uint32_t w1, float a) {
-    bf16x8 r;
-    r[0] = static_cast<__bf16>(a * (ubyte0(w0) - 32.0f));
-    r[1] = static_cast<__bf16>(a * (ubyte1(w0) - 32.0f));
-    r[2] = static_cast<__bf16>(a * (ubyte2(w0) - 32.0f));
-    r[3] = static_cast<__bf16>(a * (ubyte3(w0) - 32.0f));
-    r[4] = static_cast<__bf16>(a * (ubyte0(w1) - 32.0f));
-    r[5] = static_cast<__bf16>(a * (ubyte1(w1) - 32.0f));
-    r[6] = static_cast<__bf16>(a * (ubyte2(w1) - 32.0f));
-    r[7] = static_cast<__bf16>(a * (ubyte3(w1) - 32.0f));
-    return r;
+    return affine8(w0, w1, a, 32.0f * a);
 }
 
-// Eight signed bytes times d (Q8_0: v = q * d).
-__device__ __forceinline__ float sbyte(uint32_t w, int i) {
-    return static_cast<float>(static_cast<int8_t>((w >> (8 * i)) & 0xffu));
-}
+// Eight signed bytes times d (Q8_0: v = q * d) as d * (q + 128) - 128 d.
 __device__ __forceinline__ bf16x8 q8_8(uint32_t w0, uint32_t w1, float d) {
-    bf16x8 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = static_cast<__bf16>(sbyte(w0, i) * d);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[4 + i] = static_cast<__bf16>(sbyte(w1, i) * d);
-    return r;
+    return affine8(w0 ^ 0x80808080u, w1 ^ 0x80808080u, d, 128.0f * d);
 }
-#pragma clang fp contract(fast)
-
 // Per-type weight fragments. Raw holds the bytes one lane needs for one
-// 128-k step of one weight row; load() issues the global loads, frags()
+// 128-k step of one weight row; load() issues the global loads, slice<s>()
 // turns them into the eight bf16x8 operands (slice order above).
 template <uint32_t T>
 struct WTile;
@@ -128,31 +131,29 @@ struct WTile<kQ4_K> {
         r.q[1] = g_ld128_a4(blk + 16 + 32 * (j0 + 1) + 16 * h);
         return r;
     }
-    __device__ static __forceinline__ void frags(const Raw& r, uint32_t kb, uint32_t, bf16x8* f) {
+    // Slice s = 4 G + j: G picks the 64-group, j = 0, 1 the low nibbles of
+    // qs dwords (x, y) / (z, w), j = 2, 3 the high nibbles.
+    template <int S>
+    __device__ static __forceinline__ bf16x8 slice(const Raw& r, uint32_t kb, uint32_t) {
+        constexpr int G = S >> 2, J = S & 3;
         const uint32_t j0 = (kb % 256) / 64;
         const float d = f16_bits(r.head.x);
         const float dmin = f16_bits(r.head.x >> 16);
-        // get_scale_min_k4 (model.cpp:524-537) for the four sub-blocks 2 j0 .. 2 j0 + 3.
-        uint32_t S, M;
-        if (j0 == 0) {
-            S = r.head.y & 0x3f3f3f3fu;
-            M = r.head.z & 0x3f3f3f3fu;
-        } else {
-            S = (r.head.w & 0x0f0f0f0fu) | ((r.head.y >> 2) & 0x30303030u);
-            M = ((r.head.w >> 4) & 0x0f0f0f0fu) | ((r.head.z >> 2) & 0x30303030u);
-        }
-#pragma unroll
-        for (int G = 0; G < 2; ++G) {
-            const uint4 q = r.q[G];
-            const float d1lo = d * static_cast<float>((S >> (16 * G)) & 0xffu);
-            const float m1lo = dmin * static_cast<float>((M >> (16 * G)) & 0xffu);
-            const float d1hi = d * static_cast<float>((S >> (16 * G + 8)) & 0xffu);
-            const float m1hi = dmin * static_cast<float>((M >> (16 * G + 8)) & 0xffu);
-            f[4 * G + 0] = affine8(q.x & 0x0f0f0f0fu, q.y & 0x0f0f0f0fu, d1lo, m1lo);
-            f[4 * G + 1] = affine8(q.z & 0x0f0f0f0fu, q.w & 0x0f0f0f0fu, d1lo, m1lo);
-            f[4 * G + 2] = affine8((q.x >> 4) & 0x0f0f0f0fu, (q.y >> 4) & 0x0f0f0f0fu, d1hi, m1hi);
-            f[4 * G + 3] = affine8((q.z >> 4) & 0x0f0f0f0fu, (q.w >> 4) & 0x0f0f0f0fu, d1hi, m1hi);
-        }
+        // get_scale_min_k4 (model.cpp:524-537) for the four sub-blocks 2 j0 .. 2 j0 + 3,
+        // both halves computed and selected with a mask (no branch).
+        const uint32_t S0 = r.head.y & 0x3f3f3f3fu, M0 = r.head.z & 0x3f3f3f3fu;
+        const uint32_t S1 = (r.head.w & 0x0f0f0f0fu) | ((r.head.y >> 2) & 0x30303030u);
+        const uint32_t M1 = ((r.head.w >> 4) & 0x0f0f0f0fu) | ((r.head.z >> 2) & 0x30303030u);
+        const uint32_t hi_half = 0u - static_cast<uint32_t>(j0 != 0);
+        const uint32_t Sc = (S0 & ~hi_half) | (S1 & hi_half);
+        const uint32_t Mn = (M0 & ~hi_half) | (M1 & hi_half);
+        constexpr int sh = 16 * G + (J >= 2 ? 8 : 0);
+        const float d1 = d * static_cast<float>((Sc >> sh) & 0xffu);
+        const float m1 = dmin * static_cast<float>((Mn >> sh) & 0xffu);
+        const uint4 q = r.q[G];
+        const uint32_t a0 = (J & 1) ? q.z : q.x, a1 = (J & 1) ? q.w : q.y;
+        constexpr int ns = J >= 2 ? 4 : 0;
+        return affine8((a0 >> ns) & 0x0f0f0f0fu, (a1 >> ns) & 0x0f0f0f0fu, d1, m1);
     }
 };
 
@@ -185,29 +186,21 @@ struct WTile<kQ6_K> {
         r.d = g_ld32_a2(blk + 208) & 0xffffu;
         return r;
     }
-    __device__ static __forceinline__ void frags(const Raw& r, uint32_t, uint32_t, bf16x8* f) {
+    // Slice s = 4 G + 2 hi + j: quarter 2 G + hi, qs dwords (x, y) or (z, w).
+    template <int S>
+    __device__ static __forceinline__ bf16x8 slice(const Raw& r, uint32_t, uint32_t) {
+        constexpr int G = S >> 2, HI = (S >> 1) & 1, J = S & 1;
+        constexpr int quarter = 2 * G + HI;
         const float d = f16_bits(r.d);
-#pragma unroll
-        for (int G = 0; G < 2; ++G) {
-#pragma unroll
-            for (int hi = 0; hi < 2; ++hi) {
-                const uint32_t quarter = 2 * G + hi;
-                const uint4 l = r.ql[hi];
-                const uint32_t sh = 2 * quarter;
-                const int8_t scb = static_cast<int8_t>((r.sc >> (8 * quarter)) & 0xffu);
-                const float a = d * static_cast<float>(scb);
-                uint32_t L[4] = {l.x, l.y, l.z, l.w};
-                const uint32_t H[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
-                uint32_t v[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t nib = G == 0 ? (L[i] & 0x0f0f0f0fu) : ((L[i] >> 4) & 0x0f0f0f0fu);
-                    v[i] = nib | (((H[i] >> sh) & 0x03030303u) << 4);
-                }
-                f[4 * G + 2 * hi + 0] = q6_8(v[0], v[1], a);
-                f[4 * G + 2 * hi + 1] = q6_8(v[2], v[3], a);
-            }
-        }
+        const int8_t scb = static_cast<int8_t>((r.sc >> (8 * quarter)) & 0xffu);
+        const float a = d * static_cast<float>(scb);
+        const uint4 l = r.ql[HI];
+        const uint32_t L0 = J ? l.z : l.x, L1 = J ? l.w : l.y;
+        const uint32_t H0 = J ? r.qh.z : r.qh.x, H1 = J ? r.qh.w : r.qh.y;
+        constexpr int ns = G == 0 ? 0 : 4;
+        const uint32_t v0 = ((L0 >> ns) & 0x0f0f0f0fu) | (((H0 >> (2 * quarter)) & 0x03030303u) << 4);
+        const uint32_t v1 = ((L1 >> ns) & 0x0f0f0f0fu) | (((H1 >> (2 * quarter)) & 0x03030303u) << 4);
+        return q6_8(v0, v1, a);
     }
 };
 
@@ -229,13 +222,11 @@ struct WTile<kQ8_0> {
         }
         return r;
     }
-    __device__ static __forceinline__ void frags(const Raw& r, uint32_t, uint32_t, bf16x8* f) {
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const float d = f16_bits(r.d[b]);
-            f[2 * b + 0] = q8_8(r.q[b].x, r.q[b].y, d);
-            f[2 * b + 1] = q8_8(r.q[b].z, r.q[b].w, d);
-        }
+    template <int S>
+    __device__ static __forceinline__ bf16x8 slice(const Raw& r, uint32_t, uint32_t) {
+        constexpr int B = S >> 1, J = S & 1;
+        const float d = f16_bits(r.d[B]);
+        return J ? q8_8(r.q[B].z, r.q[B].w, d) : q8_8(r.q[B].x, r.q[B].y, d);
     }
 };
 
@@ -260,23 +251,22 @@ struct WTile<kQ5_0> {
         }
         return r;
     }
-    __device__ static __forceinline__ void frags(const Raw& r, uint32_t, uint32_t h, bf16x8* f) {
+    template <int S>
+    __device__ static __forceinline__ bf16x8 slice(const Raw& r, uint32_t, uint32_t h) {
+        constexpr int B = S >> 1, J = S & 1;
+        const float d = f16_bits(r.d[B]);
+        const float m = 16.0f * d;
+        const uint32_t bits = r.qh[B] >> (16 * h);  // fifth bits of elements 16 h + i
+        const uint32_t Q[4] = {r.q[B].x, r.q[B].y, r.q[B].z, r.q[B].w};
+        uint32_t v[2];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const float d = f16_bits(r.d[b]);
-            const float m = 16.0f * d;
-            const uint32_t bits = r.qh[b] >> (16 * h);  // fifth bits of elements 16 h + i
-            const uint32_t Q[4] = {r.q[b].x, r.q[b].y, r.q[b].z, r.q[b].w};
-            uint32_t v[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t nib = h == 0 ? (Q[i] & 0x0f0f0f0fu) : ((Q[i] >> 4) & 0x0f0f0f0fu);
-                const uint32_t hb = (bits >> (4 * i)) & 0xfu;
-                v[i] = nib | (((hb * 0x00204081u) & 0x01010101u) << 4);
-            }
-            f[2 * b + 0] = affine8(v[0], v[1], d, m);
-            f[2 * b + 1] = affine8(v[2], v[3], d, m);
+        for (int t = 0; t < 2; ++t) {
+            const int i = 2 * J + t;
+            const uint32_t nib = h == 0 ? (Q[i] & 0x0f0f0f0fu) : ((Q[i] >> 4) & 0x0f0f0f0fu);
+            const uint32_t hb = (bits >> (4 * i)) & 0xfu;
+            v[t] = nib | (((hb * 0x00204081u) & 0x01010101u) << 4);
         }
+        return affine8(v[0], v[1], d, m);
     }
 };
 
@@ -297,14 +287,14 @@ struct WTile<kF32> {
         }
         return r;
     }
-    __device__ static __forceinline__ void frags(const Raw& r, uint32_t, uint32_t, bf16x8* f) {
+    template <int S>
+    __device__ static __forceinline__ bf16x8 slice(const Raw& r, uint32_t, uint32_t) {
+        const uint4 a = r.v[2 * S], b = r.v[2 * S + 1];
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        bf16x8 f;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const uint4 a = r.v[2 * s], b = r.v[2 * s + 1];
-            const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-            for (int i = 0; i < 8; ++i) f[s][i] = static_cast<__bf16>(__uint_as_float(w[i]));
-        }
+        for (int i = 0; i < 8; ++i) f[i] = static_cast<__bf16>(__uint_as_float(w[i]));
+        return f;
     }
 };
 
@@ -324,18 +314,50 @@ struct WTile<kF16> {
         }
         return r;
     }
-    __device__ static __forceinline__ void frags(const Raw& r, uint32_t, uint32_t, bf16x8* f) {
+    template <int S>
+    __device__ static __forceinline__ bf16x8 slice(const Raw& r, uint32_t, uint32_t) {
+        const uint32_t w[4] = {r.v[S].x, r.v[S].y, r.v[S].z, r.v[S].w};
+        bf16x8 f;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const uint32_t w[4] = {r.v[s].x, r.v[s].y, r.v[s].z, r.v[s].w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                f[s][2 * i] = static_cast<__bf16>(f16_bits(w[i]));
-                f[s][2 * i + 1] = static_cast<__bf16>(f16_bits(w[i] >> 16));
-            }
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = static_cast<__bf16>(f16_bits(w[i]));
+            f[2 * i + 1] = static_cast<__bf16>(f16_bits(w[i] >> 16));
         }
+        return f;
     }
 };
+
+// All eight slices of one lane's row fragment for one 128-k step.
+template <uint32_t T>
+__device__ __forceinline__ void wtile_frags(const typename WTile<T>::Raw& r, uint32_t kb, uint32_t h, bf16x8* f) {
+    f[0] = WTile<T>::template slice<0>(r, kb, h);
+    f[1] = WTile<T>::template slice<1>(r, kb, h);
+    f[2] = WTile<T>::template slice<2>(r, kb, h);
+    f[3] = WTile<T>::template slice<3>(r, kb, h);
+    f[4] = WTile<T>::template slice<4>(r, kb, h);
+    f[5] = WTile<T>::template slice<5>(r, kb, h);
+    f[6] = WTile<T>::template slice<6>(r, kb, h);
+    f[7] = WTile<T>::template slice<7>(r, kb, h);
+}
+
+// Block -> (weight-row tile, X-row tile), XCD-aware. Workgroups of one
+// dispatch go to the 8 XCDs round-robin (block b to XCD b % 8), each XCD with
+// its own L2. The linear block id is first renumbered so each XCD's blocks are
+// consecutive, then walked in groups of kGroupM X tiles: consecutive blocks on
+// one XCD share a weight tile (read into that XCD's L2 once per group) and the
+// group's X rows stay in the same L2 across weight tiles.
+constexpr uint32_t kXcds = 8, kGroupM = 4;
+__device__ __forceinline__ void block_tile(uint32_t nbs, uint32_t mbs, uint32_t& nb, uint32_t& mb) {
+    const uint32_t total = nbs * mbs, b = blockIdx.x;
+    const uint32_t per = total / kXcds, rem = total % kXcds, x = b % kXcds;
+    const uint32_t id = x * per + min(x, rem) + b / kXcds;
+    const uint32_t span = kGroupM * nbs;
+    const uint32_t first = id / span * kGroupM;
+    const uint32_t gsize = min(mbs - first, kGroupM);
+    const uint32_t in = id % span;
+    mb = first + in % gsize;
+    nb = in / gsize;
+}
 
 template <uint32_t T, int NSUB, int MSUB>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restrict__ w, size_t row_bytes,
@@ -353,8 +375,10 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = tid >> 6, lane = tid & 63;
     const uint32_t lr = lane & 31, h = lane >> 5;
-    const uint32_t m0 = blockIdx.y * BM;
-    const uint32_t n0 = blockIdx.x * BN + wave * WN;
+    uint32_t nb, mb;
+    block_tile((n + BN - 1) / BN, (m + BM - 1) / BM, nb, mb);
+    const uint32_t m0 = mb * BM;
+    const uint32_t n0 = nb * BN + wave * WN;
 
     const uint8_t* wrow[NSUB];
 #pragma unroll
@@ -409,7 +433,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
         const int buf = st & 1;
         bf16x8 bf[NSUB][8];
 #pragma unroll
-        for (int ns = 0; ns < NSUB; ++ns) WT::frags(raw[ns], kb, h, bf[ns]);
+        for (int ns = 0; ns < NSUB; ++ns) wtile_frags<T>(raw[ns], kb, h, bf[ns]);
         if (st + 1 < steps) {
 #pragma unroll
             for (int ns = 0; ns < NSUB; ++ns) raw[ns] = WT::load(wrow[ns], kb + kStepK, h);
@@ -454,6 +478,165 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
                             unsafeAtomicAdd(y + o, acc[ns][ms][4 * g + r]);
                         } else {
                             float v = acc[ns][ms][4 * g + r] + b;
+                            if (residual) v += residual[o];
+                            y[o] = v;
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Shared-dequant form: the block's 128 weight rows are dequantized once per
+// 128-k step into LDS, already in MFMA operand order, and every wave
+// multiplies them into its own 32 * MT X rows, so each weight is converted
+// once per 128 * MT X rows instead of once per 64.
+// * Wave w dequantizes weight rows n0 + 32 w + [0, 32) (the WTile map: lane
+//   (lr, h) gets the eight bf16x8 slices of row lr, half h) and stores slice
+//   s at ws[buf][w][s][lane], 16 bytes per lane: a wave's reads and writes of
+//   one slice are 1 KiB contiguous, free of bank conflicts.
+// * X fragments are loaded from global memory straight into registers with
+//   the same k map; waves own disjoint X rows, so each X element is read once
+//   per block. Rows past m read row m - 1 and their outputs are dropped.
+// * Software pipeline, one barrier per step: while the MFMAs of step st read
+//   LDS buffer st % 2, the wave dequantizes step st + 1 (its bytes loaded one
+//   step earlier) for the other buffer, and loads X of step st + 1 and the
+//   weight bytes of step st + 2. The loop body is one basic block and a
+//   scheduling pattern interleaves the dequant's VALU work with the MFMAs, so
+//   the two run side by side on the SIMD. MT = 1 fits two waves per SIMD
+//   (two blocks per CU); MT = 2 runs one.
+template <uint32_t T, int MT>
+__global__ __launch_bounds__(256, MT == 1 ? 2 : 1) void gemm_lds_kernel(const uint8_t* __restrict__ w, size_t row_bytes,
+                                                          const __bf16* __restrict__ xb,
+                                                          const float* __restrict__ bias,
+                                                          const float* __restrict__ residual, float* __restrict__ y,
+                                                          uint32_t m, uint32_t n, uint32_t k, uint32_t ldy,
+                                                          uint32_t steps_per_split) {
+    using WT = WTile<T>;
+    __shared__ bf16x8 ws[2][4][8][64];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wave = tid >> 6, lane = tid & 63;
+    const uint32_t lr = lane & 31, h = lane >> 5;
+    uint32_t nb, mb;
+    block_tile((n + 127) / 128, (m + 128 * MT - 1) / (128 * MT), nb, mb);
+    const uint32_t n0 = nb * 128;
+    const uint32_t mw = mb * (128 * MT) + wave * (32 * MT);  // this wave's first X row
+
+    const uint8_t* wrow = w + static_cast<size_t>(min(n0 + 32 * wave + lr, n - 1)) * row_bytes;
+    const __bf16* xrow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) xrow[mt] = xb + static_cast<size_t>(min(mw + 32 * mt + lr, m - 1)) * k;
+    auto load_x = [&](uint32_t kb, bf16x8 (&xa)[MT][8]) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const uint32_t kc = 64 * (s >> 2) + 32 * ((s >> 1) & 1) + 16 * h + 8 * (s & 1);
+                xa[mt][s] = *reinterpret_cast<const bf16x8*>(xrow[mt] + kb + kc);
+            }
+        }
+    };
+
+    f32x16 acc[4][MT];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[nt][mt][i] = 0.0f;
+
+    const uint32_t kb0 = blockIdx.z * steps_per_split * kStepK;
+    const uint32_t steps = min(steps_per_split, k / kStepK - blockIdx.z * steps_per_split);
+    const uint32_t klast = kb0 + (steps - 1) * kStepK;  // loads past the split re-read its last step
+    bf16x8 xa[MT][8];
+    load_x(kb0, xa);
+    typename WT::Raw rawn;
+    {
+        const typename WT::Raw raw = WT::load(wrow, kb0, h);
+        rawn = WT::load(wrow, min(kb0 + kStepK, klast), h);
+        bf16x8 f[8];
+        wtile_frags<T>(raw, kb0, h, f);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) ws[0][wave][s][lane] = f[s];
+    }
+    __syncthreads();
+
+    // One pipeline step. cur: this step's X fragments; nxt receives step
+    // st + 1's. rn: step st + 1's weight bytes; r2 receives step st + 2's.
+    auto body = [&](uint32_t st, bf16x8 (&cur)[MT][8], bf16x8 (&nxt)[MT][8], const typename WT::Raw& rn,
+                    typename WT::Raw& r2) {
+        const uint32_t kb = kb0 + st * kStepK;
+        const int buf = st & 1;
+        load_x(min(kb + kStepK, klast), nxt);
+        r2 = WT::load(wrow, min(kb + 2 * kStepK, klast), h);
+        // Slice by slice: the MFMAs of slice s on this step's tile, then
+        // slice s of the next step's tile dequantized and stored, with the
+        // next slice's weight fragments read ahead. A scheduling fence per
+        // slice keeps each slice's VALU work beside its MFMAs.
+        bf16x8 bcur[4], bnxt[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) bcur[nt] = ws[buf][nt][0][lane];
+        auto slice_step = [&](auto sc) {
+            constexpr int S = decltype(sc)::value;
+            if constexpr (S < 7) {
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt) bnxt[nt] = ws[buf][nt][S + 1][lane];
+            }
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    acc[nt][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[mt][S], bcur[nt], acc[nt][mt], 0, 0, 0);
+                }
+            }
+            ws[buf ^ 1][wave][S][lane] = WT::template slice<S>(rn, kb + kStepK, h);  // unused after the last step
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (S < 7) {
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt) bcur[nt] = bnxt[nt];
+            }
+        };
+        slice_step(std::integral_constant<int, 0>{});
+        slice_step(std::integral_constant<int, 1>{});
+        slice_step(std::integral_constant<int, 2>{});
+        slice_step(std::integral_constant<int, 3>{});
+        slice_step(std::integral_constant<int, 4>{});
+        slice_step(std::integral_constant<int, 5>{});
+        slice_step(std::integral_constant<int, 6>{});
+        slice_step(std::integral_constant<int, 7>{});
+        __syncthreads();
+    };
+    // Two steps per iteration with the register sets swapped, so nothing is
+    // copied between steps.
+    bf16x8 xb2[MT][8];
+    typename WT::Raw rawm;
+    for (uint32_t st = 0; st < steps; st += 2) {
+        body(st, xa, xb2, rawn, rawm);
+        if (st + 1 < steps) body(st + 1, xb2, xa, rawm, rawn);
+    }
+
+    // Epilogue: acc[nt][mt][4 g + r] = Y[mw + 32 mt + 8 g + 4 h + r][n0 + 32 nt + lr].
+    const bool split = gridDim.z > 1;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+        const uint32_t col = n0 + 32 * nt + lr;
+        if (col >= n) continue;
+        const float b = (bias && !split) ? bias[col] : 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t row = mw + 32 * mt + 8 * g + 4 * h + r;
+                    if (row < m) {
+                        const size_t o = static_cast<size_t>(row) * ldy + col;
+                        if (split) {
+                            unsafeAtomicAdd(y + o, acc[nt][mt][4 * g + r]);
+                        } else {
+                            float v = acc[nt][mt][4 * g + r] + b;
                             if (residual) v += residual[o];
                             y[o] = v;
                         }
@@ -509,9 +692,26 @@ void launch_tile(const void* w, size_t row_bytes, const __bf16* xb, const float*
         hipLaunchKernelGGL(gemm_init_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, stream,
                            y, ldy, residual, bias, m, n);
     }
-    const dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM, splits);
+    const dim3 grid(((n + BN - 1) / BN) * ((m + BM - 1) / BM), 1, splits);
     hipLaunchKernelGGL((gemm_mfma_kernel<T, NSUB, MSUB>), grid, dim3(256), 0, stream,
                        static_cast<const uint8_t*>(w), row_bytes, xb, bias, residual, y, m, n, k, ldy, per);
+}
+
+template <uint32_t T, int MT>
+void launch_lds(const void* w, size_t row_bytes, const __bf16* xb, const float* bias, const float* residual, float* y,
+                uint32_t m, uint32_t n, uint32_t k, uint32_t ldy, uint32_t splits, hipStream_t stream) {
+    constexpr uint32_t BN = 128, BM = 128 * MT;
+    const uint32_t steps = k / kStepK;
+    const uint32_t per = (steps + splits - 1) / splits;
+    splits = (steps + per - 1) / per;
+    if (splits > 1) {
+        const size_t total = static_cast<size_t>(m) * n;
+        hipLaunchKernelGGL(gemm_init_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, stream,
+                           y, ldy, residual, bias, m, n);
+    }
+    const dim3 grid(((n + BN - 1) / BN) * ((m + BM - 1) / BM), 1, splits);
+    hipLaunchKernelGGL((gemm_lds_kernel<T, MT>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w),
+                       row_bytes, xb, bias, residual, y, m, n, k, ldy, per);
 }
 
 template <uint32_t T>
@@ -519,6 +719,8 @@ int launch_typed(int tile, const void* w, size_t row_bytes, const __bf16* xb, co
                  const float* residual, float* y, uint32_t m, uint32_t n, uint32_t k, uint32_t ldy, uint32_t splits,
                  hipStream_t stream) {
     switch (tile) {
+    case 4: launch_lds<T, 1>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, splits, stream); break;
+    case 5: launch_lds<T, 2>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, splits, stream); break;
     case 0: launch_tile<T, 1, 1>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, splits, stream); break;
     case 1: launch_tile<T, 1, 2>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, splits, stream); break;
     case 2: launch_tile<T, 2, 2>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, splits, stream); break;
@@ -531,12 +733,16 @@ int launch_typed(int tile, const void* w, size_t row_bytes, const __bf16* xb, co
 }  // namespace
 
 // Tile choice: 0 = 128 x 32, 1 = 128 x 64, 2 = 256 x 64, 3 = 256 x 128
-// (weight rows x X rows per block). Measured on the 7B prefill shapes (M 128
-// to 2048): 128 x 64 (160 VGPRs, three waves per SIMD) is fastest or within
-// a few percent everywhere once small grids are filled with a K split; the
-// larger tiles reuse weights more but run one wave per SIMD. 128 x 32 for a
-// single X tile.
-int gemm_default_tile(uint32_t m, uint32_t) { return m > 32 ? 1 : 0; }
+// (weight rows x X rows per block, dequantized in registers), 4 = 128 x 128
+// and 5 = 128 x 256 (dequantized once into LDS). Measured on the 7B prefill
+// shapes (M 128 to 2048): 128 x 64 (three waves per SIMD) is fastest for the
+// short rows (k = 3584); for long rows (the down projection, k = 18944) the
+// shared-dequant 128 x 128 tile with a K split is 10-15% faster. 128 x 32 for
+// a single X tile.
+int gemm_default_tile(uint32_t m, uint32_t, uint32_t k) {
+    if (m <= 32) return 0;
+    return k >= 8192 ? 4 : 1;
+}
 
 int launch_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, hipStream_t stream) {
     if (!x || !xb || m == 0 || k == 0 || k % 8 != 0 || ldx < k || ldx % 4 != 0) return kInvalidArgument;
@@ -550,14 +756,15 @@ int launch_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, hip
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
-// K splits: enough blocks for about two per CU, each split at least four
-// 128-k steps long.
+// K splits: enough blocks for about two per CU (one for the LDS tiles, which
+// hold two blocks per CU at most), each split at least four 128-k steps long.
 uint32_t gemm_default_splits(uint32_t m, uint32_t n, uint32_t k, int tile) {
-    const uint32_t bn[4] = {128, 128, 256, 256}, bm[4] = {32, 64, 64, 128};
+    const uint32_t bn[6] = {128, 128, 256, 256, 128, 128}, bm[6] = {32, 64, 64, 128, 128, 256};
     const uint64_t blocks = static_cast<uint64_t>((n + bn[tile] - 1) / bn[tile]) * ((m + bm[tile] - 1) / bm[tile]);
+    const uint64_t target = tile >= 4 ? 256 : 512;
     const uint32_t steps = k / kStepK;
-    if (blocks >= 384 || steps < 8) return 1;
-    const uint32_t want = static_cast<uint32_t>((512 + blocks - 1) / blocks);
+    if (blocks >= target * 3 / 4 || steps < 8) return 1;
+    const uint32_t want = static_cast<uint32_t>((target + blocks - 1) / blocks);
     return max(1u, min(want, steps / 4));
 }
 
@@ -568,6 +775,7 @@ int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void*
     if (!w || !xb || !y || m == 0 || n == 0 || k == 0 || ldy < n || ldy > 0x7fffffffull) return kInvalidArgument;
     if (k % kStepK != 0) return kInvalidArgument;
     if (m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull) return kLengthError;
+    if (((n + 127) / 128) * ((m + 31) / 32) > 0x7fffffffull) return kLengthError;  // one grid row of tiles
     if (type != kF32 && type != kF16 && type != kQ5_0 && type != kQ8_0 && type != kQ4_K && type != kQ6_K) {
         return kInvalidArgument;
     }
@@ -578,8 +786,8 @@ int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void*
         return kInvalidArgument;
     }
     if (reinterpret_cast<uintptr_t>(xb) % 16 != 0) return kInvalidArgument;
-    if (tile < 0) tile = gemm_default_tile(static_cast<uint32_t>(m), static_cast<uint32_t>(n));
-    if (tile > 3) return kInvalidArgument;
+    if (tile < 0) tile = gemm_default_tile(static_cast<uint32_t>(m), static_cast<uint32_t>(n), static_cast<uint32_t>(k));
+    if (tile > 5) return kInvalidArgument;
     const uint32_t M = static_cast<uint32_t>(m), N = static_cast<uint32_t>(n), K = static_cast<uint32_t>(k);
     if (splits < 0 || splits > 1024) return kInvalidArgument;
     const uint32_t S = splits == 0 ? gemm_default_splits(M, N, K, tile) : static_cast<uint32_t>(splits);

@@ -125,7 +125,7 @@ int hipllm_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void*
                      void* stream) {
     return status(hipllm::launch_gemm_mfma(type, w, row_bytes, xb, bias, residual, y, m, n, k, tile, splits,
                                            as_stream(stream)),
-                  "hipllm_gemm_mfma: invalid arguments (k % 128 == 0, tile -1..3, splits 0..1024) or launch failure");
+                  "hipllm_gemm_mfma: invalid arguments (k % 128 == 0, tile -1..5, splits 0..1024) or launch failure");
 }
 
 size_t hipllm_gemm_workspace_bytes(size_t m, size_t k) { return (m * k * 2 + 255) / 256 * 256; }
@@ -314,8 +314,13 @@ int hipllm_set_decode_graphs(HipllmModel* m, int enabled) {
 
 int hipllm_set_batched_prefill(HipllmModel* m, int enabled) {
     if (!m) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_set_batched_prefill: null argument");
-    if (!m->dense) return fail(HIPLLM_INVALID_ARGUMENT, "batched prefill switch applies to qwen2 models");
-    return guarded([&] { m->dense->set_batched_prefill(enabled != 0); });
+    return guarded([&] {
+        if (m->dense) {
+            m->dense->set_batched_prefill(enabled != 0);
+        } else {
+            m->moe->set_matmul_prefill(enabled != 0);
+        }
+    });
 }
 
 int hipllm_copy_routes(const HipllmModel* m, int32_t* out, size_t count) {
@@ -385,6 +390,24 @@ int hipllm_gated_rmsnorm(const float* o, size_t ldo, const float* gamma, const f
     return status(hipllm::launch_gated_rmsnorm(o, ldo, gamma, z, ldz, y, xg(yq), ldy, tokens, heads, d, eps,
                                                as_stream(stream)),
                   "hipllm_gated_rmsnorm: invalid arguments or launch failure");
+}
+
+int hipllm_conv_l2norm(const float* x, size_t ldx, float* history, const float* w, float* out, size_t ldo,
+                       size_t tokens, size_t channels, size_t ksize, size_t norm_channels, size_t d, float eps,
+                       void* stream) {
+    return status(hipllm::launch_conv_l2norm(x, ldx, history, w, out, ldo, tokens, channels, ksize, norm_channels, d,
+                                             eps, as_stream(stream)),
+                  "hipllm_conv_l2norm: invalid arguments or launch failure");
+}
+
+int hipllm_gdn_scan_gated(const float* q, const float* k, size_t ldqk, const float* v, size_t ldv, const float* alpha,
+                          const float* beta_raw, size_t ld_ab, const float* dt_bias, const float* a, float* state,
+                          const float* z, size_t ldz, const float* gamma, float* y, void* yq, size_t ldy,
+                          size_t tokens, size_t value_heads, size_t key_heads, size_t d, float eps, void* stream) {
+    return status(hipllm::launch_gdn_scan_gated(q, k, ldqk, v, ldv, alpha, beta_raw, ld_ab, dt_bias, a, state, z, ldz,
+                                                gamma, y, xg(yq), ldy, tokens, value_heads, key_heads, d, eps,
+                                                as_stream(stream)),
+                  "hipllm_gdn_scan_gated: invalid arguments (state size 64 or 128) or launch failure");
 }
 
 int hipllm_split_qgate_norm(const float* mixed, size_t ldm, const float* kv, size_t ldkv, const float* q_gamma,

@@ -28,6 +28,16 @@
 namespace llm {
 namespace {
 
+// From this many rows on, the dense projections of a forward run as bf16
+// MFMA matmuls (the weights are read once per 64-row tile instead of once per
+// row).
+constexpr std::size_t kMatmulRows = 16;
+
+// Up to this many rows the DeltaNet runs as two fused launches (conv + L2
+// norm, scan + gates + gated norm); beyond it, as five launches that spread
+// the per-row work over more blocks.
+constexpr std::size_t kFusedDeltaNetRows = 4;
+
 struct MoeLayer {
     bool full = false;
     const float* attn_norm = nullptr;
@@ -68,7 +78,7 @@ struct MoeActivations {
     float* gated = nullptr;                 // [T, max(Hq D, inner)]
     hipllm::XGroup* gatedq = nullptr;
     float* ab = nullptr;                    // [T, 2 Hv]
-    float* decay = nullptr;                 // [T, Hv]
+    float* decay = nullptr;                 // [T, Hv]  (multi-row DeltaNet path)
     float* beta = nullptr;                  // [T, Hv]
     float* rlog = nullptr;                  // [T, E + 1] router logits | shared gate
     float* rweight = nullptr;               // [T, k]
@@ -77,6 +87,8 @@ struct MoeActivations {
     float* down = nullptr;                  // [T k, H]
     float* sh_act = nullptr;                // [T, FFs]
     hipllm::XGroup* sh_actq = nullptr;
+    float* sh_gate = nullptr;               // [T, FFs] shared gate projection (prefill matmul form)
+    void* xb = nullptr;                     // [T, max(H, inner, Hq D, FFs)] bf16 matmul input
     float* sh_down = nullptr;               // [T, H]
     float* logits = nullptr;                // [V]
     float* attn_scratch = nullptr;
@@ -125,6 +137,7 @@ struct HipMoeLLM::Impl {
     // One decode step recorded as a HIP graph (kernels read the token and
     // position from act.step) and replayed per token.
     bool decode_graphs = true;
+    bool matmul_prefill = true;  // multi-row projections as bf16 MFMA matmuls
     hipGraph_t decode_graph = nullptr;
     hipGraphExec_t decode_exec = nullptr;
 
@@ -151,7 +164,9 @@ struct HipMoeLLM::Impl {
     void ensure_rows(std::size_t rows);
 
     void proj(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, std::size_t ldx, std::size_t rows, float* y,
-              std::size_t ldy, const float* residual = nullptr, std::size_t n_override = 0) const;
+              std::size_t ldy, const float* residual = nullptr, std::size_t n_override = 0,
+              const void* xb = nullptr) const;
+    const void* bf16_rows(const float* x, std::size_t ldx, std::size_t k, std::size_t rows) const;
     void proj_out_norm(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, std::size_t ldx,
                        std::size_t rows, float* next, const float* hidden, const float* gamma) const;
     void attention_layer(std::size_t li, std::size_t rows, std::size_t pos0, float* hidden, float* next,
@@ -456,7 +471,8 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
                       o_shd = reserve(n * H), o_logits = reserve(config.vocabulary_size),
                       o_as = reserve(hipllm::attn_decode_scratch_floats(Hq, D, capacity)),
                       o_am = reserve(hipllm::argmax_scratch_bytes(config.vocabulary_size) / 4 + 1),
-                      o_ids = reserve(n), o_tok = reserve(16), o_step = reserve(4);
+                      o_ids = reserve(n), o_tok = reserve(16), o_step = reserve(4),
+                      o_shg = reserve(n * FFs), o_xb = reserve((n * std::max({H, inner, q_w, FFs}) + 1) / 2);
     act_bytes = off;
     hip_check(hipMalloc(&act_arena, act_bytes), "hipMalloc(MoE activations)");
     auto* b = static_cast<std::uint8_t*>(act_arena);
@@ -483,6 +499,8 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
     act.down = f(o_down);
     act.sh_act = f(o_sha);
     act.sh_actq = g(o_shaq);
+    act.sh_gate = f(o_shg);
+    act.xb = b + o_xb;
     act.sh_down = f(o_shd);
     act.logits = f(o_logits);
     act.attn_scratch = f(o_as);
@@ -497,8 +515,16 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
 
 // y[rows, :] = W x[rows, :] (+ residual); one GEMV per row, batched over rows.
 void HipMoeLLM::Impl::proj(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, std::size_t ldx, std::size_t rows,
-                           float* y, std::size_t ldy, const float* residual, std::size_t n_override) const {
+                           float* y, std::size_t ldy, const float* residual, std::size_t n_override,
+                           const void* xb) const {
     const std::size_t n = n_override ? n_override : w.rows;
+    if (xb) {
+        // Prefill rows through the bf16 MFMA matmul (xb: bf16_rows of x).
+        launch_check(hipllm::launch_gemm_mfma(w.type, w.ptr, w.row_bytes, xb, nullptr, residual, y, rows, n, w.cols, -1,
+                                              0, stream, ldy),
+                     "prefill matmul");
+        return;
+    }
     if (rows == 1) {
         launch_check(hipllm::launch_gemv_prepped(w.type, w.ptr, w.row_bytes, x, xq, nullptr, residual, y, n, w.cols,
                                                  0, stream),
@@ -510,11 +536,21 @@ void HipMoeLLM::Impl::proj(const DevMatrix& w, const float* x, const hipllm::XGr
                  "batched GEMV");
 }
 
+// The bf16 copy of `rows` rows of x (k values, ld ldx) that the prefill
+// matmul reads, in act.xb; nullptr when the rows go through the GEMV forms
+// (few rows, or k not a multiple of the matmul's 128-k step). One copy per
+// input: every projection of the same rows shares it until the next call.
+const void* HipMoeLLM::Impl::bf16_rows(const float* x, std::size_t ldx, std::size_t k, std::size_t rows) const {
+    if (!matmul_prefill || rows < kMatmulRows || k % 128 != 0) return nullptr;
+    launch_check(hipllm::launch_to_bf16(x, ldx, act.xb, rows, k, stream), "bf16 activations");
+    return act.xb;
+}
+
 // Output projection of a mixer block with the residual, next = hidden + W x,
 // then act.norm = rmsnorm(next) * gamma (the post-mixer norm).
 void HipMoeLLM::Impl::proj_out_norm(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, std::size_t ldx,
                                     std::size_t rows, float* next, const float* hidden, const float* gamma) const {
-    proj(w, x, xq, ldx, rows, next, H, hidden);
+    proj(w, x, xq, ldx, rows, next, H, hidden, 0, bf16_rows(x, ldx, w.cols, rows));
     launch_check(hipllm::launch_rmsnorm(next, gamma, act.norm, act.normq, rows, H, config.norm_epsilon, stream),
                  "RMSNorm");
 }
@@ -528,20 +564,13 @@ void HipMoeLLM::Impl::attention_layer(std::size_t li, std::size_t rows, std::siz
     const MoeLayer& L = layers[li];
     const float eps = config.norm_epsilon;
     const std::size_t ldqkv = q_w + 2 * kv_w;
-    proj(L.qgate, act.norm, act.normq, H, rows, act.wide, 2 * q_w);
+    const void* xb = bf16_rows(act.norm, H, H, rows);
+    proj(L.qgate, act.norm, act.normq, H, rows, act.wide, 2 * q_w, nullptr, 0, xb);
     if (L.fused_kv) {
-        proj(L.k, act.norm, act.normq, H, rows, act.kv, 2 * kv_w, nullptr, 2 * kv_w);
+        proj(L.k, act.norm, act.normq, H, rows, act.kv, 2 * kv_w, nullptr, 2 * kv_w, xb);
     } else {
-        proj(L.k, act.norm, act.normq, H, rows, act.kv, 2 * kv_w);
-        // V rows land after K in each row; batched rows need ldy = 2 kv_w.
-        if (rows == 1) {
-            proj(L.v, act.norm, act.normq, H, rows, act.kv + kv_w, 2 * kv_w);
-        } else {
-            launch_check(hipllm::launch_gemv_batched(L.v.type, L.v.ptr, nullptr, L.v.row_bytes, act.norm,
-                                                     act.normq, nullptr, nullptr, act.kv + kv_w, nullptr, kv_w, H,
-                                                     rows, nullptr, 1, 1, 0, 0, H, 2 * kv_w, stream),
-                         "batched GEMV");
-        }
+        proj(L.k, act.norm, act.normq, H, rows, act.kv, 2 * kv_w, nullptr, 0, xb);
+        proj(L.v, act.norm, act.normq, H, rows, act.kv + kv_w, 2 * kv_w, nullptr, 0, xb);  // after K in each row
     }
     launch_check(hipllm::launch_split_qgate_norm(act.wide, 2 * q_w, act.kv, 2 * kv_w, L.q_norm, L.k_norm, act.wide2,
                                                  ldqkv, act.feat, q_w, rows, Hq, Hkv, D, eps, stream),
@@ -568,34 +597,45 @@ void HipMoeLLM::Impl::attention_layer(std::size_t li, std::size_t rows, std::siz
 void HipMoeLLM::Impl::deltanet_layer(std::size_t li, std::size_t rows, float* hidden, float* next) {
     const MoeLayer& L = layers[li];
     const float eps = config.norm_epsilon;
-    proj(L.qkv, act.norm, act.normq, H, rows, act.wide, qkv_w);
-    proj(L.z, act.norm, act.normq, H, rows, act.feat, inner);
+    const void* xb = bf16_rows(act.norm, H, H, rows);
+    proj(L.qkv, act.norm, act.normq, H, rows, act.wide, qkv_w, nullptr, 0, xb);
+    proj(L.z, act.norm, act.normq, H, rows, act.feat, inner, nullptr, 0, xb);
     if (L.fused_ab) {
-        proj(L.alpha, act.norm, act.normq, H, rows, act.ab, 2 * Hv, nullptr, 2 * Hv);
-    } else if (rows == 1) {
-        proj(L.alpha, act.norm, act.normq, H, rows, act.ab, 2 * Hv);
-        proj(L.beta, act.norm, act.normq, H, rows, act.ab + Hv, 2 * Hv);
+        proj(L.alpha, act.norm, act.normq, H, rows, act.ab, 2 * Hv, nullptr, 2 * Hv, xb);
     } else {
-        proj(L.alpha, act.norm, act.normq, H, rows, act.ab, 2 * Hv);
-        launch_check(hipllm::launch_gemv_batched(L.beta.type, L.beta.ptr, nullptr, L.beta.row_bytes, act.norm,
-                                                 act.normq, nullptr, nullptr, act.ab + Hv, nullptr, Hv, H, rows,
-                                                 nullptr, 1, 1, 0, 0, H, 2 * Hv, stream),
-                     "batched GEMV");
+        proj(L.alpha, act.norm, act.normq, H, rows, act.ab, 2 * Hv, nullptr, 0, xb);
+        proj(L.beta, act.norm, act.normq, H, rows, act.ab + Hv, 2 * Hv, nullptr, 0, xb);  // after alpha in each row
     }
-    launch_check(hipllm::launch_gdn_gates(act.ab, act.ab + Hv, 2 * Hv, L.dt_bias, L.a, act.decay, act.beta, rows, Hv,
-                                          stream),
-                 "DeltaNet gates");
-    launch_check(hipllm::launch_conv1d_silu(act.wide, qkv_w, L.history, L.conv, act.wide2, qkv_w, rows, qkv_w,
-                                            config.ssm_conv_kernel, stream),
-                 "DeltaNet conv");
-    // L2-normalise the Q and K heads (2 G vectors of S per row, contiguous).
-    launch_check(hipllm::launch_l2norm_heads(act.wide2, qkv_w, rows, 2 * G, S, eps, stream), "DeltaNet L2 norm");
-    launch_check(hipllm::launch_gdn_scan(act.wide2, act.wide2 + G * S, qkv_w, act.wide2 + 2 * G * S, qkv_w, act.decay,
-                                         act.beta, L.state, act.feat2, inner, rows, Hv, G, S, stream),
-                 "DeltaNet scan");
-    launch_check(hipllm::launch_gated_rmsnorm(act.feat2, inner, L.ssm_norm, act.feat, inner, act.gated, act.gatedq,
-                                              inner, rows, Hv, S, eps, stream),
-                 "DeltaNet gated norm");
+    if (rows <= kFusedDeltaNetRows) {
+        // Decode: causal conv + SiLU with the Q and K heads (2 G vectors of
+        // S per row, contiguous) L2-normalised in the same pass, then the
+        // gates, recurrence and gated RMSNorm in one launch (block per value
+        // head).
+        launch_check(hipllm::launch_conv_l2norm(act.wide, qkv_w, L.history, L.conv, act.wide2, qkv_w, rows, qkv_w,
+                                                config.ssm_conv_kernel, 2 * G * S, S, eps, stream),
+                     "DeltaNet conv + L2 norm");
+        launch_check(hipllm::launch_gdn_scan_gated(act.wide2, act.wide2 + G * S, qkv_w, act.wide2 + 2 * G * S, qkv_w,
+                                                   act.ab, act.ab + Hv, 2 * Hv, L.dt_bias, L.a, L.state, act.feat,
+                                                   inner, L.ssm_norm, act.gated, act.gatedq, inner, rows, Hv, G, S,
+                                                   eps, stream),
+                     "DeltaNet scan + gated norm");
+    } else {
+        // Many rows: the per-row steps that parallelise over rows run as
+        // their own launches, and the scan splits each head over two blocks.
+        launch_check(hipllm::launch_gdn_gates(act.ab, act.ab + Hv, 2 * Hv, L.dt_bias, L.a, act.decay, act.beta, rows,
+                                              Hv, stream),
+                     "DeltaNet gates");
+        launch_check(hipllm::launch_conv1d_silu(act.wide, qkv_w, L.history, L.conv, act.wide2, qkv_w, rows, qkv_w,
+                                                config.ssm_conv_kernel, stream),
+                     "DeltaNet conv");
+        launch_check(hipllm::launch_l2norm_heads(act.wide2, qkv_w, rows, 2 * G, S, eps, stream), "DeltaNet L2 norm");
+        launch_check(hipllm::launch_gdn_scan(act.wide2, act.wide2 + G * S, qkv_w, act.wide2 + 2 * G * S, qkv_w,
+                                             act.decay, act.beta, L.state, act.feat2, inner, rows, Hv, G, S, stream),
+                     "DeltaNet scan");
+        launch_check(hipllm::launch_gated_rmsnorm(act.feat2, inner, L.ssm_norm, act.feat, inner, act.gated,
+                                                  act.gatedq, inner, rows, Hv, S, eps, stream),
+                     "DeltaNet gated norm");
+    }
     proj_out_norm(L.ssm_out, act.gated, act.gatedq, inner, rows, next, hidden, L.post_norm);
 }
 
@@ -608,41 +648,37 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
     const MoeLayer& L = layers[li];
     std::int32_t* ids = route_ids + li * act_rows * K;
     // Router logits and the shared-expert gate in one GEMV when packed.
+    // The router logits stay FP32 (GEMV forms) in every path: top-k is
+    // discontinuous, and bf16 rounding of the logits would flip near-tie
+    // routes.
     const std::size_t ldr = E + 1;
     if (L.fused_router) {
         proj(L.router, act.norm, act.normq, H, rows, act.rlog, ldr, nullptr, E + 1);
     } else {
-        if (rows == 1) {
-            proj(L.router, act.norm, act.normq, H, rows, act.rlog, ldr);
-            proj(L.shexp_router, act.norm, act.normq, H, rows, act.rlog + E, ldr);
-        } else {
-            launch_check(hipllm::launch_gemv_batched(L.router.type, L.router.ptr, nullptr, L.router.row_bytes,
-                                                     act.norm, act.normq, nullptr, nullptr, act.rlog, nullptr, E, H,
-                                                     rows, nullptr, 1, 1, 0, 0, H, ldr, stream),
-                         "router GEMV");
-            launch_check(hipllm::launch_gemv_batched(L.shexp_router.type, L.shexp_router.ptr, nullptr,
-                                                     L.shexp_router.row_bytes, act.norm, act.normq, nullptr, nullptr,
-                                                     act.rlog + E, nullptr, 1, H, rows, nullptr, 1, 1, 0, 0, H, ldr,
-                                                     stream),
-                         "shared gate GEMV");
-        }
+        proj(L.router, act.norm, act.normq, H, rows, act.rlog, ldr);
+        proj(L.shexp_router, act.norm, act.normq, H, rows, act.rlog + E, ldr);
     }
+    const void* xb = bf16_rows(act.norm, H, H, rows);
     launch_check(hipllm::launch_router_topk(act.rlog, ldr, rows, E, K, ids, act.rweight, stream), "router top-k");
     // Routed experts: gate/up + SwiGLU for every (row, route), then down.
     // The gate/up launches spread rows thinly over many blocks (the expert and
     // shared widths are small), so the XGroup form of their output comes from
     // a separate pass rather than their epilogue (which needs 16-row blocks).
     launch_check(hipllm::launch_gemv_batched(L.gate_exps.type, L.gate_exps.ptr, L.up_exps.ptr, L.gate_exps.row_bytes,
-                                             act.norm, act.normq, nullptr, nullptr, act.act, nullptr, FF, H,
+                                             act.norm, act.normq, nullptr, nullptr, act.act, act.actq, FF, H,
                                              rows * K, ids, E, K, L.gate_exps.expert_stride, 0, H, FF, stream),
                  "expert gate/up");
-    launch_check(hipllm::launch_prep_x(act.act, act.actq, rows * K * FF, stream), "expert activations");
     launch_check(hipllm::launch_gemv_batched(L.down_exps.type, L.down_exps.ptr, nullptr, L.down_exps.row_bytes,
                                              act.act, act.actq, nullptr, nullptr, act.down, nullptr, H, FF, rows * K,
                                              ids, E, K, L.down_exps.expert_stride, 1, FF, H, stream),
                  "expert down");
     // Shared expert.
-    if (L.sh_gate.type == L.sh_up.type) {
+    if (xb) {
+        proj(L.sh_gate, act.norm, act.normq, H, rows, act.sh_gate, FFs, nullptr, 0, xb);
+        proj(L.sh_up, act.norm, act.normq, H, rows, act.sh_act, FFs, nullptr, 0, xb);
+        launch_check(hipllm::launch_swiglu(act.sh_gate, act.sh_act, act.sh_act, act.sh_actq, rows * FFs, stream),
+                     "shared SwiGLU");
+    } else if (L.sh_gate.type == L.sh_up.type) {
         launch_check(hipllm::launch_gemv_batched(L.sh_gate.type, L.sh_gate.ptr, L.sh_up.ptr, L.sh_gate.row_bytes,
                                                  act.norm, act.normq, nullptr, nullptr, act.sh_act, nullptr, FFs,
                                                  H, rows, nullptr, 1, 1, 0, 0, H, FFs, stream),
@@ -654,7 +690,8 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
         launch_check(hipllm::launch_swiglu(act.sh_down, act.sh_act, act.sh_act, act.sh_actq, rows * FFs, stream),
                      "shared SwiGLU");
     }
-    proj(L.sh_down, act.sh_act, act.sh_actq, FFs, rows, act.sh_down, H);
+    proj(L.sh_down, act.sh_act, act.sh_actq, FFs, rows, act.sh_down, H, nullptr, 0,
+         bf16_rows(act.sh_act, FFs, FFs, rows));
     launch_check(hipllm::launch_moe_combine(hidden, act.down, act.rweight, act.sh_down, act.rlog + E, ldr, next, rows,
                                             H, K, stream),
                  "MoE combine");
@@ -807,6 +844,11 @@ void HipMoeLLM::set_decode_graphs(bool enabled) {
     hip_check(hipStreamSynchronize(impl_->stream), "hipStreamSynchronize");
     impl_->decode_graphs = enabled;
     if (!enabled) impl_->drop_decode_graph();
+}
+
+void HipMoeLLM::set_matmul_prefill(bool enabled) {
+    if (!impl_) throw std::runtime_error("MoE model is not initialized");
+    impl_->matmul_prefill = enabled;
 }
 
 void HipMoeLLM::enable_profiling(const std::string& csv_path, bool) {

@@ -97,6 +97,9 @@ SIGNATURES = {
     "hipllm_l2norm_heads": (_I, [_P, _S, _S, _S, _S, _F, _P]),
     "hipllm_gdn_scan": (_I, [_P, _P, _S, _P, _S, _P, _P, _P, _P, _S, _S, _S, _S, _S, _P]),
     "hipllm_gated_rmsnorm": (_I, [_P, _S, _P, _P, _S, _P, _P, _S, _S, _S, _S, _F, _P]),
+    "hipllm_conv_l2norm": (_I, [_P, _S, _P, _P, _P, _S, _S, _S, _S, _S, _S, _F, _P]),
+    "hipllm_gdn_scan_gated": (_I, [_P, _P, _S, _P, _S, _P, _P, _S, _P, _P, _P, _P, _S, _P, _P, _P, _S, _S, _S, _S,
+                                   _S, _F, _P]),
     "hipllm_split_qgate_norm": (_I, [_P, _S, _P, _S, _P, _P, _P, _S, _P, _S, _S, _S, _S, _S, _F, _P]),
     "hipllm_gate_mul": (_I, [_P, _P, _P, _P, _S, _P]),
     "hipllm_destroy": (None, [_P]),
@@ -370,6 +373,18 @@ def _k_gated_rmsnorm(o, ldo, gamma, z, ldz, y, yq, ldy, tokens, heads, d, eps, s
                                      heads, d, eps, _stream(stream)))
 
 
+def _k_conv_l2norm(x, ldx, history, w, out, ldo, tokens, channels, ksize, norm_channels, d, eps, stream=None):
+    check(lib().hipllm_conv_l2norm(_ptr(x), ldx, _ptr(history), _ptr(w), _ptr(out), ldo, tokens, channels, ksize,
+                                   norm_channels, d, eps, _stream(stream)))
+
+
+def _k_gdn_scan_gated(q, k, ldqk, v, ldv, alpha, beta_raw, ld_ab, dt_bias, a, state, z, ldz, gamma, y, yq, ldy,
+                      tokens, value_heads, key_heads, d, eps, stream=None):
+    check(lib().hipllm_gdn_scan_gated(_ptr(q), _ptr(k), ldqk, _ptr(v), ldv, _ptr(alpha), _ptr(beta_raw), ld_ab,
+                                      _ptr(dt_bias), _ptr(a), _ptr(state), _ptr(z), ldz, _ptr(gamma), _ptr(y), _ptr(yq),
+                                      ldy, tokens, value_heads, key_heads, d, eps, _stream(stream)))
+
+
 def _k_split_qgate_norm(mixed, ldm, kv, ldkv, q_gamma, k_gamma, qkv, ldqkv, gate, ldg, tokens, hq, hkv, d, eps,
                         stream=None):
     check(lib().hipllm_split_qgate_norm(_ptr(mixed), ldm, _ptr(kv), ldkv, _ptr(q_gamma), _ptr(k_gamma), _ptr(qkv),
@@ -414,6 +429,7 @@ kernels = types.SimpleNamespace(
     attn_decode=_k_attn_decode, argmax=_k_argmax, swiglu=_k_swiglu, attn_prefill=_k_attn_prefill,
     gemv_batched=_k_gemv_batched, router_topk=_k_router_topk, moe_combine=_k_moe_combine, gdn_gates=_k_gdn_gates,
     conv1d_silu=_k_conv1d_silu, l2norm_heads=_k_l2norm_heads, gdn_scan=_k_gdn_scan, gated_rmsnorm=_k_gated_rmsnorm,
+    conv_l2norm=_k_conv_l2norm, gdn_scan_gated=_k_gdn_scan_gated,
     split_qgate_norm=_k_split_qgate_norm, gate_mul=_k_gate_mul,
     gemv_workspace_bytes=lambda k: lib().hipllm_gemv_workspace_bytes(k),
     attn_decode_scratch_floats=lambda hq, d, n: lib().hipllm_attn_decode_scratch_floats(hq, d, n),

@@ -197,6 +197,66 @@ def test_gated_rmsnorm(cuda):
     xgroup.check(yq, got)
 
 
+@pytest.mark.parametrize("d", [64, 128])
+def test_conv_l2norm_fused(cuda, d):
+    # conv + SiLU + history over 5 head segments, the first 2 L2-normalised.
+    rng = np.random.default_rng(14)
+    T, C, ksize, nc = 6, 5 * d, 4, 2 * d
+    x = rng.normal(size=(T, C)).astype(np.float32)
+    hist = rng.normal(size=(ksize - 1, C)).astype(np.float32)
+    w = rng.normal(size=(C, ksize)).astype(np.float32)
+    dh = t32(hist, cuda)
+    out = torch.empty(T, C, device=cuda)
+    kernels.conv_l2norm(t32(x, cuda), C, dh, t32(w, cuda), out, C, T, C, ksize, nc, d, 1e-6)
+    h = hist.astype(np.float64)
+    ref = np.empty((T, C))
+    for t in range(T):
+        o, h = moe_ref.conv_step(h, x[t].astype(np.float64), w.astype(np.float64))
+        ref[t] = moe_ref.silu(o)
+    ref[:, :nc] = moe_ref.l2norm(ref[:, :nc].reshape(T, nc // d, d), 1e-6).reshape(T, nc)
+    assert rel_err(out.cpu().numpy(), ref) <= 1e-5
+    np.testing.assert_array_equal(dh.cpu().numpy(), h.astype(np.float32))
+
+
+@pytest.mark.parametrize("d,Hv,G", [(128, 32, 16), (64, 4, 2)])
+def test_gdn_scan_gated_matches_float64_steps(cuda, d, Hv, G):
+    # Gates from raw alpha / beta, the recurrence and the gated RMSNorm in one
+    # launch, against the float64 steps of the three.
+    rng = np.random.default_rng(15)
+    T = 7
+    qk = rng.normal(size=(T, 2, G, d))
+    qk = qk / np.linalg.norm(qk, axis=-1, keepdims=True)
+    v = rng.normal(size=(T, Hv, d))
+    ab = rng.normal(scale=2.0, size=(T, 2 * Hv)).astype(np.float32)
+    dt = rng.normal(size=Hv).astype(np.float32)
+    a = -np.abs(rng.normal(size=Hv)).astype(np.float32)
+    z = rng.normal(size=(T, Hv * d)).astype(np.float32)
+    gamma = rng.normal(size=d).astype(np.float32)
+    S0 = rng.normal(scale=0.1, size=(Hv, d, d))
+    ldqk = 2 * G * d + Hv * d
+    buf = np.concatenate([qk.reshape(T, -1), v.reshape(T, -1)], axis=1)
+    dbuf = t32(buf, cuda)
+    dab = t32(ab, cuda)
+    state = t32(S0, cuda)
+    y = torch.empty(T, Hv * d, device=cuda)
+    yq = torch.empty(T, Hv * d, device=cuda)
+    kernels.gdn_scan_gated(dbuf, dbuf[:, G * d:], ldqk, dbuf[:, 2 * G * d:], ldqk, dab, dab[:, Hv:], 2 * Hv,
+                           t32(dt, cuda), t32(a, cuda), state, t32(z, cuda), Hv * d, t32(gamma, cuda), y, yq, Hv * d,
+                           T, Hv, G, d, 1e-6)
+    f = lambda arr: arr.astype(np.float32).astype(np.float64)
+    decay = np.exp(moe_ref.softplus(ab[:, :Hv].astype(np.float64) + dt) * a)
+    beta = moe_ref.sigmoid(ab[:, Hv:].astype(np.float64))
+    S = f(S0)
+    ref = np.empty((T, Hv, d))
+    for t in range(T):
+        S, o = moe_ref.gdn_step(S, f(qk[t, 0]), f(qk[t, 1]), f(v[t]), decay[t], beta[t], G)
+        ref[t] = moe_ref.rmsnorm(o, gamma, 1e-6) * moe_ref.silu(z[t].reshape(Hv, d))
+    got = y.cpu().numpy()
+    assert rel_err(got, ref.reshape(T, -1)) <= 1e-4
+    assert rel_err(state.cpu().numpy(), S) <= 1e-4
+    xgroup.check(yq, got)
+
+
 # ------------------------------------------------------------ attention pieces
 def test_split_qgate_norm_and_gate_mul(cuda):
     rng = np.random.default_rng(8)
@@ -338,6 +398,50 @@ def test_moe_real_widths_match_float64_reference(cuda, tmp_path):
     assert got == ref
     assert all(routes)
     assert errs.max() <= 1e-3
+
+
+def test_moe_prefill_matmul_path_real_widths(cuda, tmp_path):
+    # A 20-row prompt at 35B-A3B widths takes the bf16 MFMA matmuls for the
+    # dense projections (attention, DeltaNet and shared-expert projections):
+    # logits within the bf16 prefill bar of the float64 graph, at the prompt's
+    # last row and over the decode steps that follow. Every expert is routed
+    # (top-8 of 8), so the graph is continuous in its inputs and bf16
+    # rounding cannot flip a near-tie route (top-k is discontinuous; the
+    # FP32 switch below covers the 256-expert routing).
+    shape = synth.Qwen35MoeShape("moe-allroute-4l", 4, 2048, 16, 2, 256, 64, 4096, 4096, 8, 8, 512, 512, 4, 4, 128,
+                                 16, 32, eos_token_id=4095)
+    path = synth.write_qwen35moe(tmp_path / "moe4l-all.gguf", shape, seed=6)
+    prompt = synth.uniform_ids(20, shape.vocab, seed=13).tolist()
+    ref = moe_ref.MoeRef(path, 32)
+    with HipLLM(path, 32) as m:
+        m.prefill(prompt)
+        r = ref.prefill(prompt)
+        errs = []
+        for step in range(3):
+            lg = m.logits().astype(np.float64)
+            errs.append(np.abs(lg - ref.logits).max() / np.abs(ref.logits).max())
+            m.decode(r)  # both continue from the reference's token
+            r = ref.decode(r)
+    print("max rel logit error per step:", errs)
+    assert max(errs) <= 2e-2
+
+
+def test_moe_fp32_prefill_switch_real_widths(cuda, tmp_path):
+    # The same 20-row prompt on the 256-expert model with the matmul prefill
+    # switched off: FP32 GEMVs for every row, so routes and tokens equal the
+    # float64 graph's.
+    shape = synth.MOE_SHAPES["qwen3.5-35b-a3b-4l"]
+    path = synth.write_qwen35moe(tmp_path / "moe4l.gguf", shape, seed=6)
+    prompt = synth.uniform_ids(20, shape.vocab, seed=13).tolist()
+    ref = moe_ref.MoeRef(path, 32)
+    with HipLLM(path, 32) as m:
+        m.set_batched_prefill(False)
+        got = m.prefill(prompt)
+        assert got == ref.prefill(prompt)
+        lg = m.logits().astype(np.float64)
+        assert np.abs(lg - ref.logits).max() / np.abs(ref.logits).max() <= 1e-3
+        routes = m.routes()
+        assert all(routes[l].tolist() == ref.last_routes[l][0].tolist() for l in range(ref.L))
 
 
 def test_moe_decode_graph_matches_eager_launches(cuda, moe_tiny):

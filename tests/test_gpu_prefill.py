@@ -47,7 +47,7 @@ def gemm_case(cuda, qtype, m, n, k, seed, tile=-1, bias=False, residual=False, s
 
 
 @pytest.mark.parametrize("qtype", TYPES)
-@pytest.mark.parametrize("tile", [0, 1, 2, 3])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5])
 def test_gemm_types_and_tiles_ragged(cuda, qtype, tile):
     # m = 77, n = 333: partial tiles on both axes; k = 512: four 128-steps
     # (both halves of a K-quant super-block).
@@ -62,7 +62,12 @@ def test_gemm_types_and_tiles_ragged(cuda, qtype, tile):
 def test_gemm_k_splits(cuda, qtype, splits):
     # k = 1280: ten 128-steps, split 1, 2, 3 (4 + 4 + 2), 7 (2 x 5, so 5
     # splits) and 10 ways; partial tiles, bias and residual on every split.
-    y, ref, ref_b = gemm_case(cuda, qtype, 45, 300, 1280, seed=splits, tile=1, bias=True, residual=True,
+    for tile in (1, 4):
+        y, ref, ref_b = gemm_case(cuda, qtype, 45, 300, 1280, seed=splits, tile=tile, bias=True, residual=True,
+                                  splits=splits)
+        assert rel_err(y, ref) <= 2e-2
+        assert rel_err(y, ref_b) <= 1e-4
+    y, ref, ref_b = gemm_case(cuda, qtype, 300, 200, 1280, seed=splits, tile=5, bias=True, residual=True,
                               splits=splits)
     assert rel_err(y, ref) <= 2e-2
     assert rel_err(y, ref_b) <= 1e-4
