@@ -141,6 +141,16 @@ int hipllm_embed(uint32_t type, const void* table, size_t row_bytes, const int32
 int hipllm_rope_kv(float* qkv, const float* cos_sin, size_t rot, size_t hq, size_t hkv, size_t d, size_t pos0,
                    size_t rows, size_t row_stride, float* kcache, float* vcache, void* stream);
 
+/* One decode token: hipllm_rope_kv on the raw [Q | K | V] row qkv at
+ * position pos (the row itself is left unrotated) followed by
+ * hipllm_attn_decode over [0, pos], in one launch pair: each attention block
+ * rotates its query head, and the blocks holding the token's own key rotate
+ * and write it (and V) to the caches first. Same bits as the two calls.
+ * Replaces the same Metal and CPULLM steps as those two. */
+int hipllm_attn_decode_rope(const float* qkv, const float* cos_sin, size_t rot, float* kcache, float* vcache,
+                            float* out, void* outq, float* scratch, size_t hq, size_t hkv, size_t d, size_t pos,
+                            float scale, void* stream);
+
 /* Scratch floats hipllm_attn_decode needs for up to max_len positions. */
 size_t hipllm_attn_decode_scratch_floats(size_t hq, size_t d, size_t max_len);
 

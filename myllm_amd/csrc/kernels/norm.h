@@ -3,8 +3,7 @@
 //
 // RMSNorm follows CPULLM's Vector::rmsnorm (cpu_llm.cpp:143-166): double sum
 // of squares, y = x * (inv_rms * gamma), inv_rms = 1 / sqrt(mean + eps) in
-// FP32. Every caller runs the same code with 256 threads, so the standalone
-// kernel and the fused ones produce identical bits.
+// FP32.
 #pragma once
 
 #include "common.h"
@@ -14,9 +13,77 @@ namespace hipllm {
 // Normalises one row with the calling block (blockDim.x <= 1024), writing y
 // and, when yq != nullptr (cols % 16 == 0), its XGroup form. cols % 4 == 0
 // rows use 128-bit accesses (x, gamma and y then 16-byte aligned).
+// Whole 16-groups held in registers: every thread loads its (up to) two
+// groups of x and gamma at once, so the row costs one round trip to memory,
+// the block reduction and the writes.
+__device__ inline void rmsnorm_row_groups(const float* __restrict__ xr, const float* __restrict__ gamma,
+                                          float* __restrict__ yr, XGroup* __restrict__ yq, uint32_t cols,
+                                          float eps) {
+    constexpr int NG = 2;
+    const uint32_t groups = cols / 16;
+    float4 xv[NG][4], gv[NG][4];
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+        const uint32_t g = threadIdx.x + j * blockDim.x;
+        if (g < groups) {
+            const float4* x4 = reinterpret_cast<const float4*>(xr + 16 * g);
+            const float4* g4 = reinterpret_cast<const float4*>(gamma + 16 * g);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                xv[j][i] = x4[i];
+                gv[j][i] = g4[i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xv[j][i] = gv[j][i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = xv[j][i];
+            ss += static_cast<double>(v.x) * v.x + static_cast<double>(v.y) * v.y +
+                  static_cast<double>(v.z) * v.z + static_cast<double>(v.w) * v.w;
+        }
+    }
+    ss = wave_sum_d(ss);
+    __shared__ double part[16];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) part[wave] = ss;
+    __syncthreads();
+    double t = 0.0;
+    for (uint32_t w = 0; w < (blockDim.x + 63) / 64; ++w) t += part[w];
+    const float ms = static_cast<float>(t / static_cast<double>(cols));
+    const float inv = 1.0f / sqrtf(ms + eps);
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+        const uint32_t g = threadIdx.x + j * blockDim.x;
+        if (g >= groups) continue;
+        float4* y4 = reinterpret_cast<float4*>(yr + 16 * g);
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 a = xv[j][i], b = gv[j][i];
+            const float4 o = make_float4(a.x * (inv * b.x), a.y * (inv * b.y), a.z * (inv * b.z), a.w * (inv * b.w));
+            y4[i] = o;
+            v[4 * i] = o.x;
+            v[4 * i + 1] = o.y;
+            v[4 * i + 2] = o.z;
+            v[4 * i + 3] = o.w;
+        }
+        if (yq) xgroup_encode(v, yq + g);
+    }
+}
+
 __device__ inline void rmsnorm_row(const float* __restrict__ xr, const float* __restrict__ gamma,
                                    float* __restrict__ yr, XGroup* __restrict__ yq, uint32_t cols, float eps) {
     const uint32_t groups = cols / 16;
+    if (cols % 16 == 0 && groups <= 2 * blockDim.x) {
+        rmsnorm_row_groups(xr, gamma, yr, yq, cols, eps);
+        return;
+    }
     const bool vec = (cols % 4 == 0);
     double ss = 0.0;
     if (vec) {

@@ -47,6 +47,26 @@ __global__ void embed_kernel(uint32_t type, const uint8_t* __restrict__ table, s
 // CPULLM computes them), stores rotated K and V into the caches at row
 // pos0 + r, and leaves rotated Q in place.
 #pragma clang fp contract(off)
+// Element i of a head rotated with the position's (cos, sin) pairs, the same
+// products and sum as rope_kv_kernel (contraction off): pairs (p, p + half)
+// for p < half, dims past 2 half unchanged.
+__device__ __forceinline__ float rope_elem(const float* __restrict__ x, const float2* __restrict__ tab, uint32_t half,
+                                          uint32_t i) {
+    if (i < half) {
+        const float2 cs = tab[i];
+        const float t1 = x[i] * cs.x;
+        const float t2 = x[i + half] * cs.y;
+        return t1 - t2;
+    }
+    if (i < 2 * half) {
+        const float2 cs = tab[i - half];
+        const float t3 = x[i - half] * cs.y;
+        const float t4 = x[i] * cs.x;
+        return t3 + t4;
+    }
+    return x[i];
+}
+
 __global__ void rope_kv_kernel(float* __restrict__ qkv, const float2* __restrict__ table, uint32_t half_rot,
                                uint32_t hq, uint32_t hkv, uint32_t d, uint32_t pos0, uint32_t row_stride,
                                float* __restrict__ kcache, float* __restrict__ vcache,
@@ -99,11 +119,18 @@ __global__ void rope_kv_kernel(float* __restrict__ qkv, const float2* __restrict
 constexpr uint32_t kAttnChunk = 64;
 constexpr uint32_t kAttnMaxSplits = 16;
 
-__global__ __launch_bounds__(256) void attn_decode_partial(const float* __restrict__ q, const float* __restrict__ kcache,
-                                                           const float* __restrict__ vcache, float* __restrict__ part,
+// With rope != nullptr (the fused decode step), q is this token's raw qkv row
+// ([Q heads | K heads | V heads]): the block rotates its query head into LDS,
+// and the block(s) whose split holds the token's own key (the last chunk)
+// rotate that key head, write it and the value head into the caches at row
+// len - 1, then synchronise before reading them. Every head of a KV group
+// writes the same values there, so the duplicate writes agree.
+__global__ __launch_bounds__(256) void attn_decode_partial(const float* __restrict__ q, float* __restrict__ kcache,
+                                                           float* __restrict__ vcache, float* __restrict__ part,
                                                            uint32_t hq, uint32_t hkv, uint32_t d, uint32_t len_arg,
                                                            const uint32_t* __restrict__ dpos, float scale,
-                                                           uint32_t splits) {
+                                                           uint32_t splits, const float2* __restrict__ rope,
+                                                           uint32_t half_rot) {
     const uint32_t h = blockIdx.x;
     const uint32_t split = blockIdx.y;
     const uint32_t len = dpos ? *dpos + 1 : len_arg;
@@ -117,7 +144,23 @@ __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restri
     const uint32_t tid = threadIdx.x;
     const uint32_t d4 = d / 4;
     const uint32_t wave = tid >> 6, lane = tid & 63;
-    for (uint32_t i = tid; i < d4; i += blockDim.x) qs4[i] = reinterpret_cast<const float4*>(q + h * d)[i];
+    if (rope) {
+        const float2* tab = rope + static_cast<size_t>(len - 1) * half_rot;
+        float* qs = reinterpret_cast<float*>(qs4);
+        for (uint32_t i = tid; i < d; i += blockDim.x) qs[i] = rope_elem(q + h * d, tab, half_rot, i);
+        if ((nchunks - 1) % splits == split) {
+            const float* kn = q + hq * d + g * d;
+            const float* vn = kn + kvd;
+            float* kc = kcache + static_cast<size_t>(len - 1) * kvd + g * d;
+            float* vc = vcache + static_cast<size_t>(len - 1) * kvd + g * d;
+            for (uint32_t i = tid; i < d; i += blockDim.x) {
+                kc[i] = rope_elem(kn, tab, half_rot, i);
+                vc[i] = vn[i];
+            }
+        }
+    } else {
+        for (uint32_t i = tid; i < d4; i += blockDim.x) qs4[i] = reinterpret_cast<const float4*>(q + h * d)[i];
+    }
     __syncthreads();
     // p.V ownership: float4 column c4 = tid % (d / 4), key subset pp = tid /
     // (d / 4) of `parts` (threads past parts * d / 4 idle).
@@ -453,9 +496,33 @@ int launch_attn_decode(const float* q, const float* kcache, const float* vcache,
     if (outq && reinterpret_cast<uintptr_t>(outq) % 16 != 0) return kInvalidArgument;
     if (len > 0xffffffffull || capacity > 0xffffffffull || hq > 0xffffull) return kLengthError;
     const uint32_t splits = attn_splits(dpos ? capacity : len);
-    hipLaunchKernelGGL(attn_decode_partial, dim3(static_cast<uint32_t>(hq), splits), dim3(256), 0, stream, q, kcache,
-                       vcache, scratch, static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv),
-                       static_cast<uint32_t>(d), static_cast<uint32_t>(len), dpos, scale, splits);
+    // Read-only use of the caches (no RoPE table): the kernel writes them only in the fused form.
+    hipLaunchKernelGGL(attn_decode_partial, dim3(static_cast<uint32_t>(hq), splits), dim3(256), 0, stream, q,
+                       const_cast<float*>(kcache), const_cast<float*>(vcache), scratch, static_cast<uint32_t>(hq),
+                       static_cast<uint32_t>(hkv), static_cast<uint32_t>(d), static_cast<uint32_t>(len), dpos, scale,
+                       splits, nullptr, 0u);
+    hipLaunchKernelGGL(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out, outq,
+                       static_cast<uint32_t>(d), splits);
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+// One decode token's RoPE, KV-cache write and attention: qkv is the token's
+// raw [Q | K | V] row, the position is pos (len = pos + 1) or *dpos.
+int launch_attn_decode_rope(const float* qkv, const float* cos_sin, size_t rot, float* kcache, float* vcache,
+                            float* out, XGroup* outq, float* scratch, size_t hq, size_t hkv, size_t d, size_t pos,
+                            float scale, hipStream_t stream, const uint32_t* dpos, size_t capacity) {
+    if (!qkv || !cos_sin || !kcache || !vcache || !out || !scratch || hq == 0 || hkv == 0 || hq % hkv) {
+        return kInvalidArgument;
+    }
+    if (dpos && capacity == 0) return kInvalidArgument;
+    if (d == 0 || d > 256 || d % 16 != 0 || rot == 0 || rot % 2 != 0 || rot > d) return kInvalidArgument;
+    if (outq && reinterpret_cast<uintptr_t>(outq) % 16 != 0) return kInvalidArgument;
+    if (pos >= 0xffffffffull || capacity > 0xffffffffull || hq > 0xffffull) return kLengthError;
+    const uint32_t splits = attn_splits(dpos ? capacity : pos + 1);
+    hipLaunchKernelGGL(attn_decode_partial, dim3(static_cast<uint32_t>(hq), splits), dim3(256), 0, stream, qkv,
+                       kcache, vcache, scratch, static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv),
+                       static_cast<uint32_t>(d), static_cast<uint32_t>(pos + 1), dpos, scale, splits,
+                       reinterpret_cast<const float2*>(cos_sin), static_cast<uint32_t>(rot / 2));
     hipLaunchKernelGGL(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out, outq,
                        static_cast<uint32_t>(d), splits);
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;

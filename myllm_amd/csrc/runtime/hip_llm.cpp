@@ -381,15 +381,13 @@ void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, fl
         gemv(L.k, act.norm, act.normq, L.qkv_bias + H, nullptr, act.qkv + H);
         gemv(L.v, act.norm, act.normq, L.qkv_bias + H + kv_dim, nullptr, act.qkv + H + kv_dim);
     }
-    launch_check(hipllm::launch_rope_kv(act.qkv, rope_table, c.rotary_dimension, c.attention_head_count,
-                                        c.kv_head_count, c.head_size, pos, 1, H + 2 * kv_dim, kcache(li), vcache(li),
-                                        stream, dpos),
-                 "RoPE/KV write");
+    // RoPE of Q and K, the KV-cache write and the attention in one launch
+    // pair (partials, merge).
     const float scale = 1.0f / std::sqrt(static_cast<float>(c.head_size));
-    launch_check(hipllm::launch_attn_decode(act.qkv, kcache(li), vcache(li), act.attn, act.attnq, act.attn_scratch,
-                                            c.attention_head_count, c.kv_head_count, c.head_size, pos + 1, scale,
-                                            stream, dpos, max_sequence),
-                 "attention");
+    launch_check(hipllm::launch_attn_decode_rope(act.qkv, rope_table, c.rotary_dimension, kcache(li), vcache(li),
+                                                 act.attn, act.attnq, act.attn_scratch, c.attention_head_count,
+                                                 c.kv_head_count, c.head_size, pos, scale, stream, dpos, max_sequence),
+                 "RoPE/KV write + attention");
     gemv(L.o, act.attn, act.attnq, nullptr, hidden, next_hidden);
     launch_check(hipllm::launch_rmsnorm(next_hidden, L.ffn_norm, act.norm, act.normq, 1, H, eps, stream), "RMSNorm");
     if (L.fused_gate_up) {

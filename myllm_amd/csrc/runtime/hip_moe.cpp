@@ -575,15 +575,17 @@ void HipMoeLLM::Impl::attention_layer(std::size_t li, std::size_t rows, std::siz
     launch_check(hipllm::launch_split_qgate_norm(act.wide, 2 * q_w, act.kv, 2 * kv_w, L.q_norm, L.k_norm, act.wide2,
                                                  ldqkv, act.feat, q_w, rows, Hq, Hkv, D, eps, stream),
                  "Q/gate split + head norms");
-    launch_check(hipllm::launch_rope_kv(act.wide2, rope_table, config.rotary_dimension, Hq, Hkv, D, pos0, rows, ldqkv,
-                                        L.kcache, L.vcache, stream, dpos),
-                 "RoPE/KV write");
     const float scale = 1.0f / std::sqrt(static_cast<float>(D));
     if (rows == 1) {
-        launch_check(hipllm::launch_attn_decode(act.wide2, L.kcache, L.vcache, act.feat2, nullptr, act.attn_scratch,
-                                                Hq, Hkv, D, pos0 + 1, scale, stream, dpos, capacity),
-                     "attention");
+        // RoPE of Q and K, the KV-cache write and the attention fused.
+        launch_check(hipllm::launch_attn_decode_rope(act.wide2, rope_table, config.rotary_dimension, L.kcache,
+                                                     L.vcache, act.feat2, nullptr, act.attn_scratch, Hq, Hkv, D, pos0,
+                                                     scale, stream, dpos, capacity),
+                     "RoPE/KV write + attention");
     } else {
+        launch_check(hipllm::launch_rope_kv(act.wide2, rope_table, config.rotary_dimension, Hq, Hkv, D, pos0, rows,
+                                            ldqkv, L.kcache, L.vcache, stream, dpos),
+                     "RoPE/KV write");
         launch_check(hipllm::launch_attn_prefill(act.wide2, ldqkv, L.kcache, L.vcache, act.feat2, q_w, rows, Hq, Hkv,
                                                  D, pos0, scale, stream),
                      "prefill attention");

@@ -79,6 +79,7 @@ SIGNATURES = {
     "hipllm_embed": (_I, [_U32, _P, _S, _P, _S, _S, _S, _P, _P]),
     "hipllm_rope_kv": (_I, [_P, _P, _S, _S, _S, _S, _S, _S, _S, _P, _P, _P]),
     "hipllm_attn_decode_scratch_floats": (_S, [_S, _S, _S]),
+    "hipllm_attn_decode_rope": (_I, [_P, _P, _S, _P, _P, _P, _P, _P, _S, _S, _S, _S, _F, _P]),
     "hipllm_attn_decode": (_I, [_P, _P, _P, _P, _P, _P, _S, _S, _S, _S, _F, _P]),
     "hipllm_argmax_scratch_bytes": (_S, [_S]),
     "hipllm_argmax": (_I, [_P, _S, _P, _P, _P]),
@@ -404,6 +405,11 @@ def _k_embed(qtype, table, row_bytes, ids, rows, vocab, cols, out, stream=None):
                              _stream(stream)))
 
 
+def _k_attn_decode_rope(qkv, cos_sin, rot, kcache, vcache, out, outq, scratch, hq, hkv, d, pos, scale, stream=None):
+    check(lib().hipllm_attn_decode_rope(_ptr(qkv), _ptr(cos_sin), rot, _ptr(kcache), _ptr(vcache), _ptr(out),
+                                        _ptr(outq), _ptr(scratch), hq, hkv, d, pos, scale, _stream(stream)))
+
+
 def _k_rope_kv(qkv, cos_sin, rot, hq, hkv, d, pos0, rows, row_stride, kcache, vcache, stream=None):
     check(lib().hipllm_rope_kv(_ptr(qkv), _ptr(cos_sin), rot, hq, hkv, d, pos0, rows, row_stride, _ptr(kcache),
                                _ptr(vcache), _stream(stream)))
@@ -433,5 +439,6 @@ kernels = types.SimpleNamespace(
     split_qgate_norm=_k_split_qgate_norm, gate_mul=_k_gate_mul,
     gemv_workspace_bytes=lambda k: lib().hipllm_gemv_workspace_bytes(k),
     attn_decode_scratch_floats=lambda hq, d, n: lib().hipllm_attn_decode_scratch_floats(hq, d, n),
+    attn_decode_rope=_k_attn_decode_rope,
     argmax_scratch_bytes=lambda n: lib().hipllm_argmax_scratch_bytes(n),
 )

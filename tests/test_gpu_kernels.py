@@ -332,6 +332,45 @@ def test_attention_decode(cuda, length, hq, hkv, d):
     xgroup.check(outq, got)
 
 
+@pytest.mark.parametrize("hq,hkv,d,rot,pos", [(14, 2, 64, 64, 0), (14, 2, 64, 64, 130), (40, 8, 128, 128, 257),
+                                               (16, 2, 256, 64, 70)])
+def test_attention_decode_rope_matches_two_steps(cuda, hq, hkv, d, rot, pos):
+    # The fused decode step (RoPE + cache write inside the attention blocks)
+    # against hipllm_rope_kv followed by hipllm_attn_decode: same bits for
+    # the output, its XGroup form and the cache row; the raw row untouched.
+    rng = np.random.default_rng(pos + d)
+    kv = hkv * d
+    cap = pos + 3
+    stride = (hq + 2 * hkv) * d
+    qkv = rng.normal(size=stride).astype(np.float32)
+    ang = rng.uniform(-3.0, 3.0, size=(cap, rot // 2)).astype(np.float32)
+    table = np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)
+    kc0 = rng.normal(size=(cap, kv)).astype(np.float32)
+    vc0 = rng.normal(size=(cap, kv)).astype(np.float32)
+    dtab = torch.from_numpy(table).to(cuda)
+    scale = float(np.float32(1.0) / np.float32(math.sqrt(d)))
+    outs = []
+    for fused in (False, True):
+        dq = torch.from_numpy(qkv.copy()).to(cuda)
+        kc = torch.from_numpy(kc0.copy()).to(cuda)
+        vc = torch.from_numpy(vc0.copy()).to(cuda)
+        out = torch.empty(hq * d, dtype=torch.float32, device=cuda)
+        outq = xgroup.buffer(torch, hq * d, cuda)
+        scratch = torch.empty(kernels.attn_decode_scratch_floats(hq, d, pos + 1), dtype=torch.float32, device=cuda)
+        if fused:
+            kernels.attn_decode_rope(dq, dtab, rot, kc, vc, out, outq, scratch, hq, hkv, d, pos, scale)
+            assert np.array_equal(dq.cpu().numpy(), qkv)
+        else:
+            kernels.rope_kv(dq, dtab, rot, hq, hkv, d, pos, 1, stride, kc, vc)
+            kernels.attn_decode(dq, kc, vc, out, outq, scratch, hq, hkv, d, pos + 1, scale)
+        outs.append((out.cpu().numpy(), outq.cpu().numpy(), kc.cpu().numpy(), vc.cpu().numpy()))
+    (o1, q1, k1, v1), (o2, q2, k2, v2) = outs
+    assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32))
+    assert np.array_equal(q1.view(np.uint32), q2.view(np.uint32))
+    assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
+    assert not np.array_equal(k2[pos], kc0[pos])
+
+
 @pytest.mark.parametrize("n", [1, 100, 2048, 2049, 151936])
 def test_argmax(cuda, n):
     x = synth.normal(n, 71 + n)
