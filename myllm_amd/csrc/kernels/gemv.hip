@@ -487,6 +487,24 @@ struct Batch {
 // MODE 0: y = W x (+ bias) (+ residual).
 // MODE 1: y = silu(W x) * (W2 x); each octet carries R rows of W and the same
 //         R rows of W2. yq (optional) receives the XGroup form of y.
+// Sum over the OPW octets (8 OPW lanes) of each row group in the wave; the
+// group's first lane holds the result. Octet sums by DPP (neighbour swaps,
+// then the half-row mirror), 16-lane sums by the row mirror, 32- and 64-lane
+// sums from the four row results read with v_readlane.
+template <int OPW>
+__device__ __forceinline__ float octet_group_sum(float v, uint32_t lane) {
+    v += dpp_f32<kDppQuadXor1>(v);
+    v += dpp_f32<kDppQuadXor2>(v);
+    v += dpp_f32<kDppHalfMirror>(v);
+    if constexpr (OPW >= 2) v += dpp_f32<kDppMirror>(v);
+    if constexpr (OPW == 4) {
+        const float lo = lane_f32(v, 0) + lane_f32(v, 16), hi = lane_f32(v, 32) + lane_f32(v, 48);
+        v = lane < 32 ? lo : hi;
+    }
+    if constexpr (OPW == 8) v = (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
+    return v;
+}
+
 template <uint32_t T, int R, int OPR, int MODE>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2,
                                                    size_t row_bytes, const float* __restrict__ x,
@@ -565,17 +583,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w
     }
 
     // Reduce the 8 lanes of the octet, then the octets of the row group in
-    // this wave.
+    // this wave (DPP inside 16-lane rows, v_readlane across rows).
 #pragma unroll
-    for (int i = 0; i < NR; ++i) {
-        float v = acc[i];
-        v += __shfl_xor(v, 1);
-        v += __shfl_xor(v, 2);
-        v += __shfl_xor(v, 4);
-#pragma unroll
-        for (int s = 8; s < 8 * OPW; s <<= 1) v += __shfl_xor(v, s);
-        acc[i] = v;
-    }
+    for (int i = 0; i < NR; ++i) acc[i] = octet_group_sum<OPW>(acc[i], lane);
     __shared__ __align__(16) float outs[RPB];
     const uint32_t blk_row0 = blockIdx.x * RPB;
     if (WPG == 1) {
