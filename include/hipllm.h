@@ -83,6 +83,23 @@ int hipllm_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const fl
                         const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
                         void* stream);
 
+/* hipllm_rmsnorm of the raw row x (gain gamma, k <= 8192, x and gamma
+ * 16-byte aligned) followed by hipllm_gemv_prepped, in one launch: every
+ * block normalises x into LDS (the same bits as hipllm_rmsnorm's XGroup
+ * output) while its first weight loads are in flight. Quantized types only;
+ * `tiling` 0 picks the default, else 208, 216, 408 or 416. Replaces the
+ * reference's RMSNorm + GEVM pair of each decode sub-block (encode_decode_layer,
+ * metal_llm.mm:2758-2904; metal_llm.metal:785-823, 708-781). */
+int hipllm_gemv_norm(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* gamma, float eps,
+                     const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
+                     void* stream);
+
+/* hipllm_rmsnorm followed by hipllm_gemv_swiglu in one launch, as
+ * hipllm_gemv_norm; `tiling` 204 or 408 with yq, else also 208, 216, 416. */
+int hipllm_gemv_swiglu_norm(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
+                            const float* gamma, float eps, float* y, void* yq, size_t n, size_t k, int tiling,
+                            void* stream);
+
 /* Fused FFN gate/up GEMV + SwiGLU: y = silu(Wg x) * (Wu x); yq (nullable,
  * n % 16 == 0) receives the XGroup form of y. `tiling` 0 picks the default,
  * else one of the hipllm_gemv_prepped tilings; with yq only those whose

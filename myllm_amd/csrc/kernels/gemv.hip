@@ -34,6 +34,7 @@
 // padding so those reads stay in bounds.
 #include "common.h"
 #include "launch.h"
+#include "norm.h"
 
 namespace hipllm {
 
@@ -505,13 +506,20 @@ __device__ __forceinline__ float octet_group_sum(float v, uint32_t lane) {
     return v;
 }
 
-template <uint32_t T, int R, int OPR, int MODE>
+// NORM (quantized weights, single vector): x is the raw row and gamma its
+// RMSNorm gain; every block normalises x into LDS (XGroup form, the same
+// bits as the standalone RMSNorm kernel) while its first weight loads are in
+// flight, then multiplies from LDS. Saves the norm's own launch.
+constexpr uint32_t kNormMaxGroups = 512;  // rows of up to 8192 values
+
+template <uint32_t T, int R, int OPR, int MODE, bool NORM = false>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2,
                                                    size_t row_bytes, const float* __restrict__ x,
                                                    const XGroup* __restrict__ xq, const float* __restrict__ bias,
                                                    const float* __restrict__ residual, float* __restrict__ y,
                                                    XGroup* __restrict__ yq, uint32_t n, uint32_t units,
-                                                   uint32_t kblocks, const Batch batch) {
+                                                   uint32_t kblocks, const Batch batch,
+                                                   const float* __restrict__ gamma = nullptr, float eps = 0.0f) {
     using U = Unit<T>;
     {
         // Vector j of the batch: shift weights, input, output and residual.
@@ -576,8 +584,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w
     // latency is covered by the many resident waves (a second register set
     // for prefetching, or staging x in LDS, measured slower: fewer resident
     // waves, extra synchronisation).
-    for (uint32_t u = slot; u < units; u += OPR) {
-        typename U::W wv[NR];
+    typename U::W wv[NR];
+    const bool first = slot < units;
+    if (first) load(slot, wv);
+    if constexpr (NORM) {
+        extern __shared__ __align__(16) uint8_t norm_lds[];  // k / 16 groups, sized at launch
+        XGroup* xs = reinterpret_cast<XGroup*>(norm_lds);
+        rmsnorm_row_to_xgroups(x, gamma, xs, kblocks * 32, eps);
+        __syncthreads();
+        xq = xs;
+    }
+    if (first) consume(slot, wv);
+    for (uint32_t u = slot + OPR; u < units; u += OPR) {
         load(u, wv);
         consume(u, wv);
     }
@@ -704,6 +722,49 @@ int launch_typed(int tiling, const void* w, const void* w2, size_t row_bytes, co
         return kInvalidArgument;
     }
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+// The NORM forms: quantized types, tilings 204 (SwiGLU only), 208, 216, 408, 416.
+template <uint32_t T, int MODE>
+int launch_typed_norm(int tiling, const void* w, const void* w2, size_t row_bytes, const float* x,
+                      const float* gamma, float eps, const float* bias, const float* residual, float* y, XGroup* yq,
+                      uint32_t n, uint32_t units, uint32_t kblocks, hipStream_t stream) {
+    const auto* wp = static_cast<const uint8_t*>(w);
+    const auto* wp2 = static_cast<const uint8_t*>(w2);
+    const uint32_t rpb = 32u / (tiling % 100) * (tiling / 100);
+    if (MODE == 1 && yq && !writes_whole_groups(tiling)) return kInvalidArgument;
+    const dim3 grid((n + rpb - 1) / rpb);
+    const uint32_t lds = kblocks * 32 / 16 * static_cast<uint32_t>(sizeof(XGroup));
+    switch (tiling) {
+#define HIPLLM_GEMV_NORM_CASE(RR, OO)                                                                         \
+    case 100 * RR + OO:                                                                                       \
+        hipLaunchKernelGGL((gemv_kernel<T, RR, OO, MODE, true>), grid, dim3(256), lds, stream, wp, wp2,        \
+                           row_bytes, x, nullptr, bias, residual, y, yq, n, units, kblocks, Batch(), gamma,   \
+                           eps);                                                                              \
+        break;
+        HIPLLM_GEMV_NORM_CASE(2, 4)
+        HIPLLM_GEMV_NORM_CASE(2, 8)
+        HIPLLM_GEMV_NORM_CASE(2, 16)
+        HIPLLM_GEMV_NORM_CASE(4, 8)
+        HIPLLM_GEMV_NORM_CASE(4, 16)
+#undef HIPLLM_GEMV_NORM_CASE
+    default:
+        return kInvalidArgument;
+    }
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+template <int MODE>
+int launch_any_norm(uint32_t type, int tiling, const void* w, const void* w2, size_t row_bytes, const float* x,
+                    const float* gamma, float eps, const float* bias, const float* residual, float* y, XGroup* yq,
+                    uint32_t n, uint32_t units, uint32_t kblocks, hipStream_t stream) {
+    switch (type) {
+    case kQ4_K: return launch_typed_norm<kQ4_K, MODE>(tiling, w, w2, row_bytes, x, gamma, eps, bias, residual, y, yq, n, units, kblocks, stream);
+    case kQ6_K: return launch_typed_norm<kQ6_K, MODE>(tiling, w, w2, row_bytes, x, gamma, eps, bias, residual, y, yq, n, units, kblocks, stream);
+    case kQ8_0: return launch_typed_norm<kQ8_0, MODE>(tiling, w, w2, row_bytes, x, gamma, eps, bias, residual, y, yq, n, units, kblocks, stream);
+    case kQ5_0: return launch_typed_norm<kQ5_0, MODE>(tiling, w, w2, row_bytes, x, gamma, eps, bias, residual, y, yq, n, units, kblocks, stream);
+    default: return kInvalidArgument;
+    }
 }
 
 template <int MODE>
@@ -847,6 +908,55 @@ int launch_gemv_swiglu(uint32_t type, const void* wg, const void* wu, size_t row
     if (!valid_tiling(code) || (yq && !writes_whole_groups(code))) return kInvalidArgument;
     return launch_any<1>(type, code, wg, wu, row_bytes, x, xq, nullptr, nullptr, y, yq, nn, units,
                          static_cast<uint32_t>(k / 32), stream);
+}
+
+// The NORM tiling nearest a plain pick: 2 or 4 rows per octet, 8 or 16
+// octets per row group (204 / 408 for a SwiGLU with XGroup output).
+static int norm_tiling(int t, int mode, bool whole_groups) {
+    if (mode == 1 && whole_groups) return t == 408 ? 408 : 204;
+    const int R = t / 100 >= 4 ? 4 : 2;
+    const int OPR = t % 100 >= 16 ? 16 : 8;
+    return 100 * R + OPR;
+}
+
+static bool norm_ok(uint32_t type, const float* x, const float* gamma, size_t k, float eps) {
+    return (type == kQ4_K || type == kQ6_K || type == kQ8_0 || type == kQ5_0) && x && gamma && k % 16 == 0 &&
+           k / 16 <= kNormMaxGroups && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(gamma) % 16 == 0 && eps > 0.0f;
+}
+
+// y = W rmsnorm(x) (+ bias) (+ residual) with the norm in the GEMV's
+// prologue (quantized weights; k <= 8192).
+int launch_gemv_norm(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* gamma, float eps,
+                     const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
+                     hipStream_t stream) {
+    if (!y) return kInvalidArgument;
+    if (!norm_ok(type, x, gamma, k, eps)) return kInvalidArgument;
+    const int rc = check_common(type, w, nullptr, row_bytes, x, nullptr, n, k);
+    if (rc != kOk && rc != kInvalidArgument) return rc;
+    if (!w || row_bytes < k / block_elems(type) * block_bytes(type)) return kInvalidArgument;
+    const uint32_t units = static_cast<uint32_t>((k + unit_elems(type) - 1) / unit_elems(type));
+    const uint32_t nn = static_cast<uint32_t>(n);
+    const int code = tiling ? tiling : norm_tiling(gemv_pick_shape(type, nn, units, 0), 0, false);
+    return launch_any_norm<0>(type, code, w, nullptr, row_bytes, x, gamma, eps, bias, residual, y, nullptr, nn, units,
+                              static_cast<uint32_t>(k / 32), stream);
+}
+
+// y = silu(Wg rmsnorm(x)) * (Wu rmsnorm(x)), yq (optional) its XGroup form,
+// with the norm in the prologue.
+int launch_gemv_swiglu_norm(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
+                            const float* gamma, float eps, float* y, XGroup* yq, size_t n, size_t k, int tiling,
+                            hipStream_t stream) {
+    if (!wg || !wu || !y) return kInvalidArgument;
+    if (!norm_ok(type, x, gamma, k, eps)) return kInvalidArgument;
+    if (row_bytes < k / block_elems(type) * block_bytes(type)) return kInvalidArgument;
+    if (n == 0 || n > 0x7fffffffull || k == 0 || k % block_elems(type) != 0) return kInvalidArgument;
+    if (yq && (n % 16 != 0 || reinterpret_cast<uintptr_t>(yq) % 16 != 0)) return kInvalidArgument;
+    const uint32_t units = static_cast<uint32_t>((k + unit_elems(type) - 1) / unit_elems(type));
+    const uint32_t nn = static_cast<uint32_t>(n);
+    const int code = tiling ? tiling : norm_tiling(gemv_default_tiling(nn, units, 1, 1, yq != nullptr), 1, yq != nullptr);
+    return launch_any_norm<1>(type, code, wg, wu, row_bytes, x, gamma, eps, nullptr, nullptr, y, yq, nn, units,
+                              static_cast<uint32_t>(k / 32), stream);
 }
 
 // A batch of GEMVs through one matrix or through routed experts (see Batch):

@@ -24,6 +24,12 @@ int launch_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const fl
 int launch_gemv_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
                        const XGroup* xq, float* y, XGroup* yq, size_t n, size_t k, int tiling, hipStream_t stream);
 
+int launch_gemv_norm(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* gamma, float eps,
+                     const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
+                     hipStream_t stream);
+int launch_gemv_swiglu_norm(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
+                            const float* gamma, float eps, float* y, XGroup* yq, size_t n, size_t k, int tiling,
+                            hipStream_t stream);
 int launch_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row_bytes, const float* x,
                         const XGroup* xq, const float* bias, const float* residual, float* y, XGroup* yq, size_t n,
                         size_t k, size_t vectors, const int32_t* ids, size_t experts, size_t routes,

@@ -15,10 +15,12 @@ namespace hipllm {
 // rows use 128-bit accesses (x, gamma and y then 16-byte aligned).
 // Whole 16-groups held in registers: every thread loads its (up to) two
 // groups of x and gamma at once, so the row costs one round trip to memory,
-// the block reduction and the writes.
+// the block reduction and the writes. yr (nullable) receives y, yq
+// (nullable, global or LDS) its XGroup form. Callers with the same block size
+// get identical bits (the GEMVs that normalise their input in a prologue run
+// this with 256 threads, as the standalone kernel does).
 __device__ inline void rmsnorm_row_groups(const float* __restrict__ xr, const float* __restrict__ gamma,
-                                          float* __restrict__ yr, XGroup* __restrict__ yq, uint32_t cols,
-                                          float eps) {
+                                          float* __restrict__ yr, XGroup* yq, uint32_t cols, float eps) {
     constexpr int NG = 2;
     const uint32_t groups = cols / 16;
     float4 xv[NG][4], gv[NG][4];
@@ -61,19 +63,60 @@ __device__ inline void rmsnorm_row_groups(const float* __restrict__ xr, const fl
     for (int j = 0; j < NG; ++j) {
         const uint32_t g = threadIdx.x + j * blockDim.x;
         if (g >= groups) continue;
-        float4* y4 = reinterpret_cast<float4*>(yr + 16 * g);
         float v[16];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float4 a = xv[j][i], b = gv[j][i];
             const float4 o = make_float4(a.x * (inv * b.x), a.y * (inv * b.y), a.z * (inv * b.z), a.w * (inv * b.w));
-            y4[i] = o;
+            if (yr) reinterpret_cast<float4*>(yr + 16 * g)[i] = o;
             v[4 * i] = o.x;
             v[4 * i + 1] = o.y;
             v[4 * i + 2] = o.z;
             v[4 * i + 3] = o.w;
         }
         if (yq) xgroup_encode(v, yq + g);
+    }
+}
+
+// rmsnorm_row_groups' XGroup output with few live registers: x is read
+// twice (sum of squares, then scale and encode), each group transiently, in
+// the same order, so the bits are the same. For kernels that normalise their
+// input in a prologue while other loads are in flight.
+__device__ inline void rmsnorm_row_to_xgroups(const float* __restrict__ xr, const float* __restrict__ gamma,
+                                              XGroup* yq, uint32_t cols, float eps) {
+    const uint32_t groups = cols / 16;
+    double ss = 0.0;
+    for (uint32_t g = threadIdx.x; g < groups; g += blockDim.x) {
+        const float4* x4 = reinterpret_cast<const float4*>(xr + 16 * g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = x4[i];
+            ss += static_cast<double>(v.x) * v.x + static_cast<double>(v.y) * v.y +
+                  static_cast<double>(v.z) * v.z + static_cast<double>(v.w) * v.w;
+        }
+    }
+    ss = wave_sum_d(ss);
+    __shared__ double part[16];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) part[wave] = ss;
+    __syncthreads();
+    double t = 0.0;
+    for (uint32_t w = 0; w < (blockDim.x + 63) / 64; ++w) t += part[w];
+    const float ms = static_cast<float>(t / static_cast<double>(cols));
+    const float inv = 1.0f / sqrtf(ms + eps);
+    for (uint32_t g = threadIdx.x; g < groups; g += blockDim.x) {
+        const float4* x4 = reinterpret_cast<const float4*>(xr + 16 * g);
+        const float4* g4 = reinterpret_cast<const float4*>(gamma + 16 * g);
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 a = x4[i], b = g4[i];
+            v[4 * i] = a.x * (inv * b.x);
+            v[4 * i + 1] = a.y * (inv * b.y);
+            v[4 * i + 2] = a.z * (inv * b.z);
+            v[4 * i + 3] = a.w * (inv * b.w);
+        }
+        xgroup_encode(v, yq + g);
     }
 }
 

@@ -115,6 +115,22 @@ int hipllm_gemv_swiglu(uint32_t type, const void* wg, const void* wu, size_t row
                   "hipllm_gemv_swiglu: invalid arguments or launch failure");
 }
 
+int hipllm_gemv_norm(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* gamma, float eps,
+                     const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
+                     void* stream) {
+    return status(hipllm::launch_gemv_norm(type, w, row_bytes, x, gamma, eps, bias, residual, y, n, k, tiling,
+                                           as_stream(stream)),
+                  "hipllm_gemv_norm: invalid arguments or launch failure");
+}
+
+int hipllm_gemv_swiglu_norm(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
+                            const float* gamma, float eps, float* y, void* yq, size_t n, size_t k, int tiling,
+                            void* stream) {
+    return status(hipllm::launch_gemv_swiglu_norm(type, wg, wu, row_bytes, x, gamma, eps, y, xg(yq), n, k, tiling,
+                                                  as_stream(stream)),
+                  "hipllm_gemv_swiglu_norm: invalid arguments or launch failure");
+}
+
 int hipllm_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, void* stream) {
     return status(hipllm::launch_to_bf16(x, ldx, xb, m, k, as_stream(stream)),
                   "hipllm_to_bf16: invalid arguments (k % 8 == 0, 16-byte aligned buffers) or launch failure");

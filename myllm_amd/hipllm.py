@@ -71,6 +71,8 @@ SIGNATURES = {
     "hipllm_gemv": (_I, [_U32, _P, _S, _P, _P, _P, _S, _S, _P, _P]),
     "hipllm_gemv_prepped": (_I, [_U32, _P, _S, _P, _P, _P, _P, _P, _S, _S, _I, _P]),
     "hipllm_gemv_swiglu": (_I, [_U32, _P, _P, _S, _P, _P, _P, _P, _S, _S, _I, _P]),
+    "hipllm_gemv_norm": (_I, [_U32, _P, _S, _P, _P, _F, _P, _P, _P, _S, _S, _I, _P]),
+    "hipllm_gemv_swiglu_norm": (_I, [_U32, _P, _P, _S, _P, _P, _F, _P, _P, _S, _S, _I, _P]),
     "hipllm_to_bf16": (_I, [_P, _S, _P, _S, _S, _P]),
     "hipllm_gemm_mfma": (_I, [_U32, _P, _S, _P, _P, _P, _P, _S, _S, _S, _I, _I, _P]),
     "hipllm_gemm_workspace_bytes": (_S, [_S, _S]),
@@ -319,6 +321,16 @@ def _k_to_bf16(x, ldx, xb, m, k, stream=None):
     check(lib().hipllm_to_bf16(_ptr(x), ldx, _ptr(xb), m, k, _stream(stream)))
 
 
+def _k_gemv_norm(qtype, w, row_bytes, x, gamma, eps, bias, residual, y, n, k, tiling=0, stream=None):
+    check(lib().hipllm_gemv_norm(qtype, _ptr(w), row_bytes, _ptr(x), _ptr(gamma), eps, _ptr(bias), _ptr(residual),
+                                 _ptr(y), n, k, tiling, _stream(stream)))
+
+
+def _k_gemv_swiglu_norm(qtype, wg, wu, row_bytes, x, gamma, eps, y, yq, n, k, tiling=0, stream=None):
+    check(lib().hipllm_gemv_swiglu_norm(qtype, _ptr(wg), _ptr(wu), row_bytes, _ptr(x), _ptr(gamma), eps, _ptr(y),
+                                        _ptr(yq), n, k, tiling, _stream(stream)))
+
+
 def _k_gemm_mfma(qtype, w, row_bytes, xb, bias, residual, y, m, n, k, tile=-1, stream=None, splits=0):
     check(lib().hipllm_gemm_mfma(qtype, _ptr(w), row_bytes, _ptr(xb), _ptr(bias), _ptr(residual), _ptr(y),
                                  m, n, k, tile, splits, _stream(stream)))
@@ -430,7 +442,7 @@ def _k_swiglu(g, u, y, yq, n, stream=None):
 
 kernels = types.SimpleNamespace(
     dequant_rows=_k_dequant_rows, prep_x=_k_prep_x, gemv=_k_gemv, gemv_prepped=_k_gemv_prepped,
-    gemv_swiglu=_k_gemv_swiglu, to_bf16=_k_to_bf16, gemm_mfma=_k_gemm_mfma, gemm=_k_gemm,
+    gemv_swiglu=_k_gemv_swiglu, gemv_norm=_k_gemv_norm, gemv_swiglu_norm=_k_gemv_swiglu_norm, to_bf16=_k_to_bf16, gemm_mfma=_k_gemm_mfma, gemm=_k_gemm,
     gemm_workspace_bytes=lambda m, k: lib().hipllm_gemm_workspace_bytes(m, k), rmsnorm=_k_rmsnorm, embed=_k_embed, rope_kv=_k_rope_kv,
     attn_decode=_k_attn_decode, argmax=_k_argmax, swiglu=_k_swiglu, attn_prefill=_k_attn_prefill,
     gemv_batched=_k_gemv_batched, router_topk=_k_router_topk, moe_combine=_k_moe_combine, gdn_gates=_k_gdn_gates,

@@ -247,6 +247,70 @@ def test_gemv_swiglu_tilings(cuda, qtype, tiling):
         swiglu_case(cuda, qtype, 1040, 2048, tiling, with_yq=False)
 
 
+# ------------------------------------------------------------- norm prologue
+@pytest.mark.parametrize("tiling", [0, 208, 216, 408, 416])
+@pytest.mark.parametrize("qtype,n,k", [(synth.Q4_K, 4608, 3584), (synth.Q6_K, 1040, 5120), (synth.Q8_0, 1152, 896),
+                                        (synth.Q5_0, 300, 896)])
+def test_gemv_norm_matches_rmsnorm_then_gemv(cuda, qtype, n, k, tiling):
+    # The norm in the GEMV's prologue against hipllm_rmsnorm followed by the
+    # GEMV on its XGroup output (bias and residual included): the same
+    # arithmetic in two separately compiled kernels (FMA contraction may round
+    # differently), so within 1e-6.
+    w = random_rows(qtype, n, k, 81)
+    dw = dev_bytes(w, cuda)
+    x = torch.from_numpy(synth.normal(k, 82, stddev=3.0)).to(cuda)
+    g = torch.from_numpy(synth.normal(k, 83, stddev=0.5) + 1.0).to(cuda)
+    b = torch.from_numpy(synth.normal(n, 84)).to(cuda)
+    r = torch.from_numpy(synth.normal(n, 85)).to(cuda)
+    y1 = torch.empty(n, dtype=torch.float32, device=cuda)
+    y2 = torch.empty(n, dtype=torch.float32, device=cuda)
+    xn = torch.empty(k, dtype=torch.float32, device=cuda)
+    xq = xgroup.buffer(torch, k, cuda)
+    kernels.rmsnorm(x, g, xn, xq, 1, k, 1e-6)
+    kernels.gemv_prepped(qtype, dw, w.shape[1], xn, xq, b, r, y1, n, k, tiling)
+    kernels.gemv_norm(qtype, dw, w.shape[1], x, g, 1e-6, b, r, y2, n, k, tiling)
+    got, ref = y2.cpu().numpy(), y1.cpu().numpy()
+    print("max rel diff", rel_err(got, ref))
+    assert rel_err(got, ref) <= 1e-6
+
+
+@pytest.mark.parametrize("tiling", [204, 408])
+@pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q6_K, synth.Q8_0])
+def test_gemv_swiglu_norm_matches_rmsnorm_then_swiglu(cuda, qtype, tiling):
+    n, k = 1040, 3584 if qtype != synth.Q8_0 else 896
+    wg, wu = random_rows(qtype, n, k, 86), random_rows(qtype, n, k, 87)
+    dg, du = dev_bytes(wg, cuda), dev_bytes(wu, cuda)
+    x = torch.from_numpy(synth.normal(k, 88, stddev=2.0)).to(cuda)
+    g = torch.from_numpy(synth.normal(k, 89, stddev=0.5) + 1.0).to(cuda)
+    xn = torch.empty(k, dtype=torch.float32, device=cuda)
+    xq = xgroup.buffer(torch, k, cuda)
+    kernels.rmsnorm(x, g, xn, xq, 1, k, 1e-6)
+    outs = []
+    for fused in (False, True):
+        y = torch.empty(n, dtype=torch.float32, device=cuda)
+        yq = xgroup.buffer(torch, n, cuda)
+        if fused:
+            kernels.gemv_swiglu_norm(qtype, dg, du, wg.shape[1], x, g, 1e-6, y, yq, n, k, tiling)
+        else:
+            kernels.gemv_swiglu(qtype, dg, du, wg.shape[1], xn, xq, y, yq, n, k, tiling)
+        outs.append((y.cpu().numpy(), yq.cpu().numpy()))
+    print("max rel diff", rel_err(outs[1][0], outs[0][0]))
+    assert rel_err(outs[1][0], outs[0][0]) <= 1e-6
+    xgroup.check(outs[1][1], outs[1][0])
+
+
+def test_gemv_norm_rejects_bad_arguments(cuda):
+    w = torch.zeros(144 * 40, dtype=torch.uint8, device=cuda)
+    x = torch.zeros(9216, device=cuda)
+    y = torch.zeros(4, device=cuda)
+    with pytest.raises(ValueError):  # k beyond the 8192-value LDS prologue
+        kernels.gemv_norm(synth.Q4_K, w, 144 * 36, x, x, 1e-6, None, None, y, 4, 9216)
+    with pytest.raises(ValueError):  # float weights have no norm form
+        kernels.gemv_norm(synth.F32, w, 1024, x, x, 1e-6, None, None, y, 4, 256)
+    with pytest.raises(ValueError):  # unknown norm tiling
+        kernels.gemv_norm(synth.Q4_K, w, 144, x, x, 1e-6, None, None, y, 4, 256, 432)
+
+
 # ------------------------------------------------------------- small ops
 @pytest.mark.parametrize("rows,cols", [(1, 896), (5, 3584), (3, 5120)])
 def test_rmsnorm_bit_exact(cuda, rows, cols):
