@@ -100,6 +100,36 @@ int hipllm_gemv_swiglu_norm(uint32_t type, const void* wg, const void* wu, size_
                             const float* gamma, float eps, float* y, void* yq, size_t n, size_t k, int tiling,
                             void* stream);
 
+/* One GEMV of hipllm_gemv_multi_norm. mode 0: y = W x (+ bias) (+ residual),
+ * quantized or F32 weights; mode 1: y = silu(W x) * (W2 x), quantized weights,
+ * yq (nullable; n % 16 == 0) its XGroup form. reserved must be 0. */
+typedef struct HipllmGemvJob {
+    uint32_t type;
+    uint32_t mode;
+    const void* w;
+    const void* w2;
+    size_t row_bytes;
+    const float* bias;
+    const float* residual;
+    float* y;
+    void* yq;
+    uint32_t n;
+    uint32_t reserved;
+} HipllmGemvJob;
+
+/* Up to 3 GEMVs of one normalised row in one launch: every block normalises x
+ * (k values, k % 32 == 0, k <= 8192; gain gamma) into LDS as
+ * hipllm_rmsnorm does, then runs its job's rows (blocks of job p follow those
+ * of job p - 1; tilings 208, 204 for mode 1, 132 for F32). norm and normq
+ * (nullable, 16-byte aligned) receive the normalised row and its XGroup form.
+ * For one decode row this replaces the RMSNorm and the projections that read
+ * it (the DeltaNet QKV / z / alpha-beta GEVMs, moe_llm.mm:2436-2500; the
+ * gated-attention Q / K / V GEVMs, 2238-2290; the router and shared-expert
+ * gate/up of encode_routes and encode_selected_moe, 2642-2690, 2762-2790),
+ * each a separate dispatch in the reference. */
+int hipllm_gemv_multi_norm(const HipllmGemvJob* jobs, size_t count, const float* x, const float* gamma, float eps,
+                           size_t k, float* norm, void* normq, void* stream);
+
 /* Fused FFN gate/up GEMV + SwiGLU: y = silu(Wg x) * (Wu x); yq (nullable,
  * n % 16 == 0) receives the XGroup form of y. `tiling` 0 picks the default,
  * else one of the hipllm_gemv_prepped tilings; with yq only those whose
@@ -220,6 +250,14 @@ int hipllm_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row
  * metal_topk_renorm_f32 (metal_llm.metal:826-890, 1424-1474). */
 int hipllm_router_topk(const float* logits, size_t ld, size_t tokens, size_t experts, size_t k, int32_t* ids,
                        float* weights, void* stream);
+
+/* hipllm_moe_combine, then norm[t] = rmsnorm(out[t]) * gamma (normq, nullable:
+ * its XGroup form), one block per token. Replaces the FFN residual of
+ * encode_layer_experts and the next encode_rmsnorm (moe_llm.mm:2876-2883,
+ * 2852-2855 of the next layer, 2954 after the last). */
+int hipllm_moe_combine_norm(const float* residual, const float* down, const float* w, const float* shared,
+                            const float* sgate, size_t ld_sgate, float* out, const float* gamma, float* norm,
+                            void* normq, size_t tokens, size_t h, size_t k, float eps, void* stream);
 
 /* out = residual + (sum_r w[t, r] down[t k + r] + sigmoid(sgate[t ld]) shared[t]).
  * Replaces metal_expert_weighted_reduce_f32 + shared-expert gate + residuals

@@ -506,24 +506,27 @@ __device__ __forceinline__ float octet_group_sum(float v, uint32_t lane) {
     return v;
 }
 
-// NORM (quantized weights, single vector): x is the raw row and gamma its
-// RMSNorm gain; every block normalises x into LDS (XGroup form, the same
-// bits as the standalone RMSNorm kernel) while its first weight loads are in
-// flight, then multiplies from LDS. Saves the norm's own launch.
+// NORM (single vector): x is the raw row and gamma its RMSNorm gain; every
+// block normalises x into LDS (the XGroup form for quantized weights, FP32
+// values for F32 weights; the same bits as the standalone RMSNorm kernel)
+// while its first weight loads are in flight, then multiplies from LDS.
+// Saves the norm's own launch.
 constexpr uint32_t kNormMaxGroups = 512;  // rows of up to 8192 values
 
-template <uint32_t T, int R, int OPR, int MODE, bool NORM = false>
-__global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2,
-                                                   size_t row_bytes, const float* __restrict__ x,
-                                                   const XGroup* __restrict__ xq, const float* __restrict__ bias,
-                                                   const float* __restrict__ residual, float* __restrict__ y,
-                                                   XGroup* __restrict__ yq, uint32_t n, uint32_t units,
-                                                   uint32_t kblocks, const Batch batch,
-                                                   const float* __restrict__ gamma = nullptr, float eps = 0.0f) {
+// The work of block (bx, by) of a GEMV launch; the kernels below call it with
+// their block index (or, for a grouped launch, the index within their job).
+template <uint32_t T, int R, int OPR, int MODE, bool NORM>
+__device__ __forceinline__ void gemv_block(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2,
+                                           size_t row_bytes, const float* __restrict__ x,
+                                           const XGroup* __restrict__ xq, const float* __restrict__ bias,
+                                           const float* __restrict__ residual, float* __restrict__ y,
+                                           XGroup* __restrict__ yq, uint32_t n, uint32_t units, uint32_t kblocks,
+                                           const Batch& batch, const float* __restrict__ gamma, float eps,
+                                           uint32_t bx, uint32_t by) {
     using U = Unit<T>;
     {
         // Vector j of the batch: shift weights, input, output and residual.
-        const uint32_t j = blockIdx.y;
+        const uint32_t j = by;
         const uint32_t xrow = batch.x_routed ? j : j / batch.routes;
         if (batch.ids) {
             const uint32_t e = min(static_cast<uint32_t>(batch.ids[j]), batch.experts - 1);
@@ -546,7 +549,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w
     const uint32_t o = tid >> 3, c = tid & 7;
     const uint32_t rg = o / OPR, slot = o % OPR;
     const uint32_t lrow0 = rg * R;  // first row of this octet within the block
-    const uint32_t row0 = blockIdx.x * RPB + lrow0;
+    const uint32_t row0 = bx * RPB + lrow0;
 
     // Byte offsets of this octet's rows (rows past n are computed, never stored).
     uint32_t roff[R];
@@ -588,11 +591,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w
     const bool first = slot < units;
     if (first) load(slot, wv);
     if constexpr (NORM) {
-        extern __shared__ __align__(16) uint8_t norm_lds[];  // k / 16 groups, sized at launch
-        XGroup* xs = reinterpret_cast<XGroup*>(norm_lds);
-        rmsnorm_row_to_xgroups(x, gamma, xs, kblocks * 32, eps);
-        __syncthreads();
-        xq = xs;
+        extern __shared__ __align__(16) uint8_t norm_lds[];  // 4 k bytes, sized at launch
+        if constexpr (T == kF32) {
+            float* xs = reinterpret_cast<float*>(norm_lds);
+            rmsnorm_row(x, gamma, xs, nullptr, kblocks * 32, eps);
+            __syncthreads();
+            x = xs;
+        } else {
+            XGroup* xs = reinterpret_cast<XGroup*>(norm_lds);
+            rmsnorm_row_to_xgroups(x, gamma, xs, kblocks * 32, eps);
+            __syncthreads();
+            xq = xs;
+        }
     }
     if (first) consume(slot, wv);
     for (uint32_t u = slot + OPR; u < units; u += OPR) {
@@ -605,7 +615,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w
 #pragma unroll
     for (int i = 0; i < NR; ++i) acc[i] = octet_group_sum<OPW>(acc[i], lane);
     __shared__ __align__(16) float outs[RPB];
-    const uint32_t blk_row0 = blockIdx.x * RPB;
+    const uint32_t blk_row0 = bx * RPB;
     if (WPG == 1) {
         if (c == 0 && slot == 0) {
 #pragma unroll
@@ -663,6 +673,74 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w
             xgroup_encode_from(outs + 16 * tid, yq + (blk_row0 / 16 + tid));
         }
     }
+}
+
+template <uint32_t T, int R, int OPR, int MODE, bool NORM = false>
+__global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2,
+                                                   size_t row_bytes, const float* __restrict__ x,
+                                                   const XGroup* __restrict__ xq, const float* __restrict__ bias,
+                                                   const float* __restrict__ residual, float* __restrict__ y,
+                                                   XGroup* __restrict__ yq, uint32_t n, uint32_t units,
+                                                   uint32_t kblocks, const Batch batch,
+                                                   const float* __restrict__ gamma = nullptr, float eps = 0.0f) {
+    gemv_block<T, R, OPR, MODE, NORM>(w, w2, row_bytes, x, xq, bias, residual, y, yq, n, units, kblocks, batch,
+                                      gamma, eps, blockIdx.x, blockIdx.y);
+}
+
+struct GemvMulti {
+    GemvJob job[kMultiJobs];
+    uint32_t jobs;
+    uint32_t kblocks;  // k / 32
+    const float* x;
+    const float* gamma;
+    float eps;
+    float* norm;
+    XGroup* normq;
+};
+
+// Grouped launch: up to kMultiJobs GEMVs of one normalised input row (NORM
+// prologue), each job with its own weights, type and form, the blocks of job
+// p following those of job p - 1. One tiling per (type, form): 2 rows x 8
+// octets (MODE 0) and 2 rows x 4 octets (MODE 1, 16-row blocks, so the XGroup
+// output is allowed) for quantized weights, 1 row x 32 octets for F32 (MODE
+// 0). Block 0 of the launch also stores the normalised row and its XGroup
+// form (norm, normq; nullable) for later launches.
+template <int MODE>
+constexpr int multi_tiling(uint32_t type) {
+    return type == kF32 ? 132 : (MODE == 1 ? 204 : 208);
+}
+
+__global__ __launch_bounds__(256) void gemv_multi_kernel(const GemvMulti m) {
+    uint32_t p = 0, bx = blockIdx.x;
+    while (p + 1 < m.jobs && bx >= m.job[p].blocks) {
+        bx -= m.job[p].blocks;
+        ++p;
+    }
+    const uint32_t k = m.kblocks * 32;
+    if (blockIdx.x == 0 && m.norm) {
+        rmsnorm_row(m.x, m.gamma, m.norm, m.normq, k, m.eps);
+        __syncthreads();  // the prologue below reuses the norm's LDS
+    }
+    const GemvJob& j = m.job[p];
+    const auto* w = static_cast<const uint8_t*>(j.w);
+    const auto* w2 = static_cast<const uint8_t*>(j.w2);
+    const uint32_t units = (k + Unit<kQ8_0>::elems - 1) / Unit<kQ8_0>::elems;  // 128-value units
+    const uint32_t units256 = (k + 255) / 256;
+    const Batch b;
+#define HIPLLM_MULTI(TT, MM, RR, OO, UU)                                                                            gemv_block<TT, RR, OO, MM, true>(w, w2, j.row_bytes, m.x, nullptr, j.bias, j.residual, j.y, j.yq, j.n, UU,                                      m.kblocks, b, m.gamma, m.eps, bx, 0)
+    switch (j.type * 2 + j.mode) {
+    case kQ4_K * 2: HIPLLM_MULTI(kQ4_K, 0, 2, 8, units256); break;
+    case kQ4_K * 2 + 1: HIPLLM_MULTI(kQ4_K, 1, 2, 4, units256); break;
+    case kQ6_K * 2: HIPLLM_MULTI(kQ6_K, 0, 2, 8, units256); break;
+    case kQ6_K * 2 + 1: HIPLLM_MULTI(kQ6_K, 1, 2, 4, units256); break;
+    case kQ8_0 * 2: HIPLLM_MULTI(kQ8_0, 0, 2, 8, units); break;
+    case kQ8_0 * 2 + 1: HIPLLM_MULTI(kQ8_0, 1, 2, 4, units); break;
+    case kQ5_0 * 2: HIPLLM_MULTI(kQ5_0, 0, 2, 8, units); break;
+    case kQ5_0 * 2 + 1: HIPLLM_MULTI(kQ5_0, 1, 2, 4, units); break;
+    case kF32 * 2: HIPLLM_MULTI(kF32, 0, 1, 32, units256); break;
+    default: break;  // rejected by the launcher
+    }
+#undef HIPLLM_MULTI
 }
 
 // XGroup form of x, one thread per 16-group.
@@ -957,6 +1035,49 @@ int launch_gemv_swiglu_norm(uint32_t type, const void* wg, const void* wu, size_
     const int code = tiling ? tiling : norm_tiling(gemv_default_tiling(nn, units, 1, 1, yq != nullptr), 1, yq != nullptr);
     return launch_any_norm<1>(type, code, wg, wu, row_bytes, x, gamma, eps, nullptr, nullptr, y, yq, nn, units,
                               static_cast<uint32_t>(k / 32), stream);
+}
+
+int launch_gemv_multi_norm(const GemvJob* jobs, size_t count, const float* x, const float* gamma, float eps, size_t k,
+                           float* norm, XGroup* normq, hipStream_t stream) {
+    if (!jobs || count == 0 || count > kMultiJobs) return kInvalidArgument;
+    if (!x || !gamma || !(eps > 0.0f) || k == 0 || k % 32 != 0 || k / 16 > kNormMaxGroups) return kInvalidArgument;
+    for (const void* p : {static_cast<const void*>(x), static_cast<const void*>(gamma), static_cast<const void*>(norm),
+                          static_cast<const void*>(normq)}) {
+        if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return kInvalidArgument;  // nullptr passes
+    }
+    if (normq && !norm) return kInvalidArgument;
+    GemvMulti m{};
+    uint64_t total = 0;
+    for (size_t i = 0; i < count; ++i) {
+        GemvJob j = jobs[i];
+        const bool quant = j.type == kQ4_K || j.type == kQ6_K || j.type == kQ8_0 || j.type == kQ5_0;
+        if (!j.y || (j.mode != 0 && j.mode != 1) || !(quant || (j.type == kF32 && j.mode == 0))) {
+            return kInvalidArgument;
+        }
+        // The input comes from the prologue: x stands in for the XGroup pointer in the shared checks.
+        const int rc = check_common(j.type, j.w, j.mode ? j.w2 : nullptr, j.row_bytes, x,
+                                    reinterpret_cast<const XGroup*>(x), j.n, k);
+        if (rc != kOk) return rc;
+        if (j.mode == 1 && (!j.w2 || j.bias || j.residual)) return kInvalidArgument;
+        if (j.yq && (j.mode != 1 || j.n % 16 != 0 || reinterpret_cast<uintptr_t>(j.yq) % 16 != 0)) {
+            return kInvalidArgument;
+        }
+        const int t = j.mode ? multi_tiling<1>(j.type) : multi_tiling<0>(j.type);
+        const uint32_t rpb = 32u / (t % 100) * (t / 100);
+        j.blocks = (j.n + rpb - 1) / rpb;
+        total += j.blocks;
+        m.job[i] = j;
+    }
+    if (total > 0x7fffffffull) return kLengthError;
+    m.jobs = static_cast<uint32_t>(count);
+    m.kblocks = static_cast<uint32_t>(k / 32);
+    m.x = x;
+    m.gamma = gamma;
+    m.eps = eps;
+    m.norm = norm;
+    m.normq = normq;
+    hipLaunchKernelGGL(gemv_multi_kernel, dim3(static_cast<uint32_t>(total)), dim3(256), k * 4, stream, m);
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
 // A batch of GEMVs through one matrix or through routed experts (see Batch):

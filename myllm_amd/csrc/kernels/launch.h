@@ -30,6 +30,28 @@ int launch_gemv_norm(uint32_t type, const void* w, size_t row_bytes, const float
 int launch_gemv_swiglu_norm(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
                             const float* gamma, float eps, float* y, XGroup* yq, size_t n, size_t k, int tiling,
                             hipStream_t stream);
+// One GEMV of a grouped launch (launch_gemv_multi_norm). mode 0: y = W x
+// (+ bias) (+ residual); mode 1: y = silu(W x) * (W2 x) and, when yq is set,
+// its XGroup form (n % 16 == 0). Quantized types and F32 (mode 0 only).
+struct GemvJob {
+    uint32_t type = 0;
+    uint32_t mode = 0;
+    const void* w = nullptr;
+    const void* w2 = nullptr;
+    size_t row_bytes = 0;
+    const float* bias = nullptr;
+    const float* residual = nullptr;
+    float* y = nullptr;
+    XGroup* yq = nullptr;
+    uint32_t n = 0;
+    uint32_t blocks = 0;  // set by the launcher
+};
+constexpr size_t kMultiJobs = 3;
+// Up to kMultiJobs GEMVs of rmsnorm(x) * gamma (k values, k / 16 <= 512) in
+// one launch, the norm in every block's prologue; norm / normq (nullable)
+// receive the normalised row and its XGroup form.
+int launch_gemv_multi_norm(const GemvJob* jobs, size_t count, const float* x, const float* gamma, float eps, size_t k,
+                           float* norm, XGroup* normq, hipStream_t stream);
 int launch_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row_bytes, const float* x,
                         const XGroup* xq, const float* bias, const float* residual, float* y, XGroup* yq, size_t n,
                         size_t k, size_t vectors, const int32_t* ids, size_t experts, size_t routes,
@@ -74,6 +96,10 @@ int launch_router_topk(const float* logits, size_t ld, size_t tokens, size_t exp
 int launch_moe_combine(const float* residual, const float* down, const float* w, const float* shared,
                        const float* sgate, size_t ld_sgate, float* out, size_t tokens, size_t h, size_t k,
                        hipStream_t stream);
+// launch_moe_combine, then norm = rmsnorm(out) * gamma (normq: nullable).
+int launch_moe_combine_norm(const float* residual, const float* down, const float* w, const float* shared,
+                            const float* sgate, size_t ld_sgate, float* out, const float* gamma, float* norm,
+                            XGroup* normq, size_t tokens, size_t h, size_t k, float eps, hipStream_t stream);
 int launch_gdn_gates(const float* alpha, const float* beta_raw, size_t ld, const float* dt_bias, const float* a,
                      float* decay, float* beta, size_t tokens, size_t heads, hipStream_t stream);
 int launch_conv1d_silu(const float* x, size_t ldx, float* history, const float* w, float* out, size_t ldo,

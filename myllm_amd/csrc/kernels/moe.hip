@@ -20,6 +20,7 @@
 // written once per call however many tokens it scans; norms run one 64-lane
 // wave per head vector; everything else is one pass over its rows.
 #include "common.h"
+#include "norm.h"
 
 namespace hipllm {
 namespace {
@@ -68,13 +69,11 @@ __device__ __forceinline__ uint64_t wave_max_key(uint64_t key) {
     return ab > cd ? ab : cd;
 }
 
+// Softmax, top-k and renormalisation of one token's logits by one wave
+// (lane = the lane in that wave); writes k ids and weights.
 template <uint32_t PL>
-__global__ __launch_bounds__(64) void router_topk_kernel(const float* __restrict__ logits, uint32_t ld,
-                                                         uint32_t experts, uint32_t k, int32_t* __restrict__ ids,
-                                                         float* __restrict__ weights) {
-    const uint32_t t = blockIdx.x;
-    const uint32_t lane = threadIdx.x;
-    const float* row = logits + static_cast<size_t>(t) * ld;
+__device__ __forceinline__ void topk_row(const float* row, uint32_t experts, uint32_t k, int32_t* __restrict__ ids,
+                                         float* __restrict__ weights, uint32_t lane) {
     float p[PL];
     float m = -INFINITY;
 #pragma unroll
@@ -135,13 +134,33 @@ __global__ __launch_bounds__(64) void router_topk_kernel(const float* __restrict
     const float sum = wave_sum(lane < k ? my_v : 0.0f);
     if (lane < k) {
         const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-        ids[static_cast<size_t>(t) * k + lane] = static_cast<int32_t>(my_i);
-        weights[static_cast<size_t>(t) * k + lane] = my_v * inv;
+        ids[lane] = static_cast<int32_t>(my_i);
+        weights[lane] = my_v * inv;
     }
+}
+
+template <uint32_t PL>
+__global__ __launch_bounds__(64) void router_topk_kernel(const float* __restrict__ logits, uint32_t ld,
+                                                         uint32_t experts, uint32_t k, int32_t* __restrict__ ids,
+                                                         float* __restrict__ weights) {
+    const size_t t = blockIdx.x;
+    topk_row<PL>(logits + t * ld, experts, k, ids + t * k, weights + t * k, threadIdx.x);
 }
 
 // ------------------------------------------------------------ MoE combine
 // out[t] = residual[t] + (sum_r w[t, r] * down[t k + r] + sigmoid(sg[t]) * shared[t])
+__device__ __forceinline__ float moe_combine_value(const float* __restrict__ residual, const float* __restrict__ down,
+                                                   const float* __restrict__ w, const float* __restrict__ shared,
+                                                   const float* __restrict__ sgate, uint32_t ld_sgate, uint32_t t,
+                                                   uint32_t c, uint32_t h, uint32_t k) {
+    const size_t i = static_cast<size_t>(t) * h + c;
+    float acc = 0.0f;
+    for (uint32_t r = 0; r < k; ++r) acc += w[t * k + r] * down[(static_cast<size_t>(t) * k + r) * h + c];
+    float moe = acc;
+    if (shared) moe += shared[i] * sigmoid_ref(sgate[static_cast<size_t>(t) * ld_sgate]);
+    return residual[i] + moe;
+}
+
 __global__ void moe_combine_kernel(const float* __restrict__ residual, const float* __restrict__ down,
                                    const float* __restrict__ w, const float* __restrict__ shared,
                                    const float* __restrict__ sgate, uint32_t ld_sgate, float* __restrict__ out,
@@ -149,11 +168,67 @@ __global__ void moe_combine_kernel(const float* __restrict__ residual, const flo
     const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= static_cast<size_t>(tokens) * h) return;
     const uint32_t t = static_cast<uint32_t>(i / h), c = static_cast<uint32_t>(i % h);
-    float acc = 0.0f;
-    for (uint32_t r = 0; r < k; ++r) acc += w[t * k + r] * down[(static_cast<size_t>(t) * k + r) * h + c];
-    float moe = acc;
-    if (shared) moe += shared[i] * sigmoid_ref(sgate[static_cast<size_t>(t) * ld_sgate]);
-    out[i] = residual[i] + moe;
+    out[i] = moe_combine_value(residual, down, w, shared, sgate, ld_sgate, t, c, h, k);
+}
+
+constexpr uint32_t kCombineMaxK = 8;  // routes held in registers by the vector form
+
+// The combine of one token per block, then the RMSNorm of the finished row
+// (the next layer's input norm, or the output norm) by the same block, with
+// the standalone norm kernel's arithmetic and block size.
+__global__ __launch_bounds__(256) void moe_combine_norm_kernel(
+    const float* __restrict__ residual, const float* __restrict__ down, const float* __restrict__ w,
+    const float* __restrict__ shared, const float* __restrict__ sgate, uint32_t ld_sgate, float* out,
+    const float* __restrict__ gamma, float* __restrict__ norm, XGroup* __restrict__ normq, uint32_t h, uint32_t k,
+    float eps) {
+    const uint32_t t = blockIdx.x;
+    float* row = out + static_cast<size_t>(t) * h;
+    if (h % 4 == 0 && k <= kCombineMaxK) {
+        // float4 columns with every route's load issued before the sums (the
+        // per-column form waits on k loads in turn); the same operations in
+        // the same order per element as moe_combine_value.
+        const uint32_t h4 = h / 4;
+        float wt[kCombineMaxK];
+#pragma unroll
+        for (uint32_t r = 0; r < kCombineMaxK; ++r) wt[r] = r < k ? w[t * k + r] : 0.0f;
+        const float sg = shared ? sigmoid_ref(sgate[static_cast<size_t>(t) * ld_sgate]) : 0.0f;
+        const float4* d4 = reinterpret_cast<const float4*>(down) + static_cast<size_t>(t) * k * h4;
+        const float4* r4 = reinterpret_cast<const float4*>(residual) + static_cast<size_t>(t) * h4;
+        const float4* s4 = reinterpret_cast<const float4*>(shared) + static_cast<size_t>(t) * h4;
+        for (uint32_t c = threadIdx.x; c < h4; c += blockDim.x) {
+            float4 dv[kCombineMaxK];
+#pragma unroll
+            for (uint32_t r = 0; r < kCombineMaxK; ++r) {
+                if (r < k) dv[r] = d4[static_cast<size_t>(r) * h4 + c];
+            }
+            const float4 res = r4[c];
+            const float4 sh = shared ? s4[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (uint32_t r = 0; r < kCombineMaxK; ++r) {
+                if (r < k) {
+                    a[0] += wt[r] * dv[r].x;
+                    a[1] += wt[r] * dv[r].y;
+                    a[2] += wt[r] * dv[r].z;
+                    a[3] += wt[r] * dv[r].w;
+                }
+            }
+            if (shared) {
+                a[0] += sh.x * sg;
+                a[1] += sh.y * sg;
+                a[2] += sh.z * sg;
+                a[3] += sh.w * sg;
+            }
+            reinterpret_cast<float4*>(row)[c] = make_float4(res.x + a[0], res.y + a[1], res.z + a[2], res.w + a[3]);
+        }
+    } else {
+        for (uint32_t c = threadIdx.x; c < h; c += blockDim.x) {
+            row[c] = moe_combine_value(residual, down, w, shared, sgate, ld_sgate, t, c, h, k);
+        }
+    }
+    __syncthreads();
+    rmsnorm_row(row, gamma, norm + static_cast<size_t>(t) * h, normq ? normq + static_cast<size_t>(t) * (h / 16) : nullptr,
+                h, eps);
 }
 
 // ------------------------------------------------------------ DeltaNet
@@ -509,6 +584,29 @@ int launch_router_topk(const float* logits, size_t ld, size_t tokens, size_t exp
     hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(tokens)), dim3(64), 0, stream, logits,
                        static_cast<uint32_t>(ld), static_cast<uint32_t>(experts), static_cast<uint32_t>(k), ids,
                        weights);
+    return launched();
+}
+
+int launch_moe_combine_norm(const float* residual, const float* down, const float* w, const float* shared,
+                            const float* sgate, size_t ld_sgate, float* out, const float* gamma, float* norm,
+                            XGroup* normq, size_t tokens, size_t h, size_t k, float eps, hipStream_t stream) {
+    if (!residual || !down || !w || !out || !gamma || !norm || tokens == 0 || h == 0 || k == 0 ||
+        (shared && (!sgate || !ld_sgate)) || !(eps > 0.0f) ||
+        (normq && (h % 16 != 0 || reinterpret_cast<uintptr_t>(normq) % 16 != 0))) {
+        return kInvalidArgument;
+    }
+    // The norm's vector path reads and writes 16-byte aligned rows.
+    if (h % 4 == 0) {
+        for (const void* p : {static_cast<const void*>(out), static_cast<const void*>(gamma),
+                              static_cast<const void*>(norm), static_cast<const void*>(residual),
+                              static_cast<const void*>(down), static_cast<const void*>(shared)}) {
+            if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return kInvalidArgument;  // nullptr passes
+        }
+    }
+    if (tokens > 0x7fffffffull || ld_sgate > 0xffffffffull || h > 0x7fffffffull / 4) return kLengthError;
+    hipLaunchKernelGGL(moe_combine_norm_kernel, dim3(static_cast<uint32_t>(tokens)), dim3(256), 0, stream, residual,
+                       down, w, shared, sgate, static_cast<uint32_t>(ld_sgate), out, gamma, norm, normq,
+                       static_cast<uint32_t>(h), static_cast<uint32_t>(k), eps);
     return launched();
 }
 

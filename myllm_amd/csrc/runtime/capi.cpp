@@ -131,6 +131,31 @@ int hipllm_gemv_swiglu_norm(uint32_t type, const void* wg, const void* wu, size_
                   "hipllm_gemv_swiglu_norm: invalid arguments or launch failure");
 }
 
+int hipllm_gemv_multi_norm(const HipllmGemvJob* jobs, size_t count, const float* x, const float* gamma, float eps,
+                           size_t k, float* norm, void* normq, void* stream) {
+    hipllm::GemvJob js[hipllm::kMultiJobs];
+    if (!jobs || count == 0 || count > hipllm::kMultiJobs) {
+        return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_gemv_multi_norm: 1 to 3 jobs");
+    }
+    for (size_t i = 0; i < count; ++i) {
+        const HipllmGemvJob& j = jobs[i];
+        if (j.reserved != 0) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_gemv_multi_norm: reserved must be 0");
+        js[i].type = j.type;
+        js[i].mode = j.mode;
+        js[i].w = j.w;
+        js[i].w2 = j.w2;
+        js[i].row_bytes = j.row_bytes;
+        js[i].bias = j.bias;
+        js[i].residual = j.residual;
+        js[i].y = j.y;
+        js[i].yq = xg(j.yq);
+        js[i].n = j.n;
+    }
+    return status(hipllm::launch_gemv_multi_norm(js, count, x, gamma, eps, k, norm, xg(normq), as_stream(stream)),
+                  "hipllm_gemv_multi_norm: invalid arguments (types, k % 32 == 0, k <= 8192, alignment) or launch "
+                  "failure");
+}
+
 int hipllm_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, void* stream) {
     return status(hipllm::launch_to_bf16(x, ldx, xb, m, k, as_stream(stream)),
                   "hipllm_to_bf16: invalid arguments (k % 8 == 0, 16-byte aligned buffers) or launch failure");
@@ -372,6 +397,15 @@ int hipllm_router_topk(const float* logits, size_t ld, size_t tokens, size_t exp
                        float* weights, void* stream) {
     return status(hipllm::launch_router_topk(logits, ld, tokens, experts, k, ids, weights, as_stream(stream)),
                   "hipllm_router_topk: invalid arguments (k <= 8, experts <= 1024) or launch failure");
+}
+
+int hipllm_moe_combine_norm(const float* residual, const float* down, const float* w, const float* shared,
+                            const float* sgate, size_t ld_sgate, float* out, const float* gamma, float* norm,
+                            void* normq, size_t tokens, size_t h, size_t k, float eps, void* stream) {
+    return status(hipllm::launch_moe_combine_norm(residual, down, w, shared, sgate, ld_sgate, out, gamma, norm,
+                                                  static_cast<hipllm::XGroup*>(normq), tokens, h, k, eps,
+                                                  as_stream(stream)),
+                  "hipllm_moe_combine_norm: invalid arguments or launch failure");
 }
 
 int hipllm_moe_combine(const float* residual, const float* down, const float* w, const float* shared,

@@ -38,6 +38,11 @@ constexpr std::size_t kMatmulRows = 16;
 // the per-row work over more blocks.
 constexpr std::size_t kFusedDeltaNetRows = 4;
 
+// A decode step (one row) runs the projections that read the same normalised
+// row as one grouped GEMV launch with the norm in its prologue: DeltaNet
+// QKV + z + alpha/beta, attention Q/gate + K/V, router + shared gate/up.
+constexpr std::size_t kGroupedRows = 1;
+
 struct MoeLayer {
     bool full = false;
     const float* attn_norm = nullptr;
@@ -168,11 +173,16 @@ struct HipMoeLLM::Impl {
               const void* xb = nullptr) const;
     const void* bf16_rows(const float* x, std::size_t ldx, std::size_t k, std::size_t rows) const;
     void proj_out_norm(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, std::size_t ldx,
-                       std::size_t rows, float* next, const float* hidden, const float* gamma) const;
+                       std::size_t rows, float* next, const float* hidden, const float* gamma, bool norm) const;
+    void grouped(const hipllm::GemvJob* jobs, std::size_t count, const float* x, const float* gamma,
+                 bool store_norm, const char* what) const;
+    bool grouped_mixer(const MoeLayer& L, std::size_t rows) const;
+    bool grouped_moe(const MoeLayer& L, std::size_t rows) const;
     void attention_layer(std::size_t li, std::size_t rows, std::size_t pos0, float* hidden, float* next,
                          const std::uint32_t* dpos);
     void deltanet_layer(std::size_t li, std::size_t rows, float* hidden, float* next);
-    void moe_layer(std::size_t li, std::size_t rows, float* hidden, float* next, const float* next_gamma);
+    void moe_layer(std::size_t li, std::size_t rows, float* hidden, float* next, const float* next_gamma,
+                   bool next_norm);
     void forward(std::size_t rows, std::size_t pos0, const std::int32_t* ids, const std::uint32_t* dpos = nullptr);
     void capture_decode();
     void drop_decode_graph();
@@ -547,12 +557,58 @@ const void* HipMoeLLM::Impl::bf16_rows(const float* x, std::size_t ldx, std::siz
 }
 
 // Output projection of a mixer block with the residual, next = hidden + W x,
-// then act.norm = rmsnorm(next) * gamma (the post-mixer norm).
+// then (norm) act.norm = rmsnorm(next) * gamma (the post-mixer norm; the
+// grouped router launch applies it otherwise).
 void HipMoeLLM::Impl::proj_out_norm(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, std::size_t ldx,
-                                    std::size_t rows, float* next, const float* hidden, const float* gamma) const {
+                                    std::size_t rows, float* next, const float* hidden, const float* gamma,
+                                    bool norm) const {
     proj(w, x, xq, ldx, rows, next, H, hidden, 0, bf16_rows(x, ldx, w.cols, rows));
+    if (!norm) return;
     launch_check(hipllm::launch_rmsnorm(next, gamma, act.norm, act.normq, rows, H, config.norm_epsilon, stream),
                  "RMSNorm");
+}
+
+// One grouped GEMV launch over rmsnorm(x) * gamma (one row); store_norm:
+// also write the normalised row and its XGroup form to act.norm / normq.
+void HipMoeLLM::Impl::grouped(const hipllm::GemvJob* jobs, std::size_t count, const float* x, const float* gamma,
+                              bool store_norm, const char* what) const {
+    launch_check(hipllm::launch_gemv_multi_norm(jobs, count, x, gamma, config.norm_epsilon, H,
+                                                store_norm ? act.norm : nullptr, store_norm ? act.normq : nullptr,
+                                                stream),
+                 what);
+}
+
+namespace {
+hipllm::GemvJob job(const DevMatrix& w, float* y, std::size_t n) {
+    hipllm::GemvJob j;
+    j.type = w.type;
+    j.w = w.ptr;
+    j.row_bytes = w.row_bytes;
+    j.y = y;
+    j.n = static_cast<std::uint32_t>(n);
+    return j;
+}
+
+// Weight types the grouped launch multiplies (mode 0; mode 1 quantized only).
+bool groupable(const DevMatrix& w, bool swiglu = false) {
+    const bool quant = w.type == hipllm::kQ4_K || w.type == hipllm::kQ6_K || w.type == hipllm::kQ8_0 ||
+                       w.type == hipllm::kQ5_0;
+    return quant || (!swiglu && w.type == hipllm::kF32);
+}
+}  // namespace
+
+// Whether layer L's input-norm projections run as one grouped launch.
+bool HipMoeLLM::Impl::grouped_mixer(const MoeLayer& L, std::size_t rows) const {
+    if (rows != kGroupedRows || H % 256 != 0 || H > 8192) return false;
+    if (L.full) return groupable(L.qgate) && groupable(L.k) && (L.fused_kv || groupable(L.v));
+    return groupable(L.qkv) && groupable(L.z) && L.fused_ab && groupable(L.alpha);
+}
+
+// Whether layer L's router and shared gate/up run as one grouped launch.
+bool HipMoeLLM::Impl::grouped_moe(const MoeLayer& L, std::size_t rows) const {
+    if (rows != kGroupedRows || H % 256 != 0 || H > 8192 || FFs % 16 != 0) return false;
+    return groupable(L.router) && (L.fused_router || groupable(L.shexp_router)) && groupable(L.sh_gate, true) &&
+           L.sh_gate.type == L.sh_up.type && L.sh_gate.row_bytes == L.sh_up.row_bytes;
 }
 
 // Gated full attention (moe_llm.mm:2238-2434) over `rows` rows at positions
@@ -564,13 +620,26 @@ void HipMoeLLM::Impl::attention_layer(std::size_t li, std::size_t rows, std::siz
     const MoeLayer& L = layers[li];
     const float eps = config.norm_epsilon;
     const std::size_t ldqkv = q_w + 2 * kv_w;
-    const void* xb = bf16_rows(act.norm, H, H, rows);
-    proj(L.qgate, act.norm, act.normq, H, rows, act.wide, 2 * q_w, nullptr, 0, xb);
-    if (L.fused_kv) {
-        proj(L.k, act.norm, act.normq, H, rows, act.kv, 2 * kv_w, nullptr, 2 * kv_w, xb);
+    if (grouped_mixer(L, rows)) {
+        hipllm::GemvJob jobs[3];
+        std::size_t nj = 0;
+        jobs[nj++] = job(L.qgate, act.wide, L.qgate.rows);
+        if (L.fused_kv) {
+            jobs[nj++] = job(L.k, act.kv, 2 * kv_w);
+        } else {
+            jobs[nj++] = job(L.k, act.kv, L.k.rows);
+            jobs[nj++] = job(L.v, act.kv + kv_w, L.v.rows);
+        }
+        grouped(jobs, nj, hidden, L.attn_norm, false, "input norm + Q/gate + K/V");
     } else {
-        proj(L.k, act.norm, act.normq, H, rows, act.kv, 2 * kv_w, nullptr, 0, xb);
-        proj(L.v, act.norm, act.normq, H, rows, act.kv + kv_w, 2 * kv_w, nullptr, 0, xb);  // after K in each row
+        const void* xb = bf16_rows(act.norm, H, H, rows);
+        proj(L.qgate, act.norm, act.normq, H, rows, act.wide, 2 * q_w, nullptr, 0, xb);
+        if (L.fused_kv) {
+            proj(L.k, act.norm, act.normq, H, rows, act.kv, 2 * kv_w, nullptr, 2 * kv_w, xb);
+        } else {
+            proj(L.k, act.norm, act.normq, H, rows, act.kv, 2 * kv_w, nullptr, 0, xb);
+            proj(L.v, act.norm, act.normq, H, rows, act.kv + kv_w, 2 * kv_w, nullptr, 0, xb);  // after K in each row
+        }
     }
     launch_check(hipllm::launch_split_qgate_norm(act.wide, 2 * q_w, act.kv, 2 * kv_w, L.q_norm, L.k_norm, act.wide2,
                                                  ldqkv, act.feat, q_w, rows, Hq, Hkv, D, eps, stream),
@@ -592,21 +661,27 @@ void HipMoeLLM::Impl::attention_layer(std::size_t li, std::size_t rows, std::siz
     }
     launch_check(hipllm::launch_gate_mul(act.feat2, act.feat, act.gated, act.gatedq, rows * q_w, stream),
                  "attention output gate");
-    proj_out_norm(L.o, act.gated, act.gatedq, q_w, rows, next, hidden, L.post_norm);
+    proj_out_norm(L.o, act.gated, act.gatedq, q_w, rows, next, hidden, L.post_norm, !grouped_moe(L, rows));
 }
 
 // Gated DeltaNet (moe_llm.mm:2436-2640); next = hidden + out_proj(...).
 void HipMoeLLM::Impl::deltanet_layer(std::size_t li, std::size_t rows, float* hidden, float* next) {
     const MoeLayer& L = layers[li];
     const float eps = config.norm_epsilon;
-    const void* xb = bf16_rows(act.norm, H, H, rows);
-    proj(L.qkv, act.norm, act.normq, H, rows, act.wide, qkv_w, nullptr, 0, xb);
-    proj(L.z, act.norm, act.normq, H, rows, act.feat, inner, nullptr, 0, xb);
-    if (L.fused_ab) {
-        proj(L.alpha, act.norm, act.normq, H, rows, act.ab, 2 * Hv, nullptr, 2 * Hv, xb);
+    if (grouped_mixer(L, rows)) {
+        const hipllm::GemvJob jobs[3] = {job(L.qkv, act.wide, L.qkv.rows), job(L.z, act.feat, L.z.rows),
+                                         job(L.alpha, act.ab, 2 * Hv)};
+        grouped(jobs, 3, hidden, L.attn_norm, false, "input norm + DeltaNet QKV / z / alpha, beta");
     } else {
-        proj(L.alpha, act.norm, act.normq, H, rows, act.ab, 2 * Hv, nullptr, 0, xb);
-        proj(L.beta, act.norm, act.normq, H, rows, act.ab + Hv, 2 * Hv, nullptr, 0, xb);  // after alpha in each row
+        const void* xb = bf16_rows(act.norm, H, H, rows);
+        proj(L.qkv, act.norm, act.normq, H, rows, act.wide, qkv_w, nullptr, 0, xb);
+        proj(L.z, act.norm, act.normq, H, rows, act.feat, inner, nullptr, 0, xb);
+        if (L.fused_ab) {
+            proj(L.alpha, act.norm, act.normq, H, rows, act.ab, 2 * Hv, nullptr, 2 * Hv, xb);
+        } else {
+            proj(L.alpha, act.norm, act.normq, H, rows, act.ab, 2 * Hv, nullptr, 0, xb);
+            proj(L.beta, act.norm, act.normq, H, rows, act.ab + Hv, 2 * Hv, nullptr, 0, xb);  // after alpha in each row
+        }
     }
     if (rows <= kFusedDeltaNetRows) {
         // Decode: causal conv + SiLU with the Q and K heads (2 G vectors of
@@ -638,15 +713,17 @@ void HipMoeLLM::Impl::deltanet_layer(std::size_t li, std::size_t rows, float* hi
                                                   act.gatedq, inner, rows, Hv, S, eps, stream),
                      "DeltaNet gated norm");
     }
-    proj_out_norm(L.ssm_out, act.gated, act.gatedq, inner, rows, next, hidden, L.post_norm);
+    proj_out_norm(L.ssm_out, act.gated, act.gatedq, inner, rows, next, hidden, L.post_norm, !grouped_moe(L, rows));
 }
 
 // MoE FFN (moe_llm.mm:2642-2843): `hidden` is the attention residual; the
-// post-attention norm of it is in act.norm; next = hidden + routed + shared.
-// next_gamma: the gain of the RMSNorm that follows (next layer's input norm or
-// the output norm), applied to `next` into act.norm in the combine launch.
+// post-attention norm of it is in act.norm (or is made by the grouped router
+// launch); next = hidden + routed + shared. next_gamma: the gain of the
+// RMSNorm that follows (next layer's input norm or the output norm), applied
+// to `next` into act.norm in the combine launch when next_norm (otherwise the
+// next layer's grouped launch normalises in its prologue).
 void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden, float* next,
-                                const float* next_gamma) {
+                                const float* next_gamma, bool next_norm) {
     const MoeLayer& L = layers[li];
     std::int32_t* ids = route_ids + li * act_rows * K;
     // Router logits and the shared-expert gate in one GEMV when packed.
@@ -654,14 +731,33 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
     // discontinuous, and bf16 rounding of the logits would flip near-tie
     // routes.
     const std::size_t ldr = E + 1;
-    if (L.fused_router) {
+    const bool grp = grouped_moe(L, rows);
+    if (grp) {
+        // Post-attention norm (stored for the expert projections), router,
+        // shared-expert gate and shared gate/up + SwiGLU (with its XGroup
+        // form) in one launch.
+        hipllm::GemvJob jobs[3];
+        std::size_t nj = 0;
+        if (L.fused_router) {
+            jobs[nj++] = job(L.router, act.rlog, E + 1);
+        } else {
+            jobs[nj++] = job(L.router, act.rlog, E);
+            jobs[nj++] = job(L.shexp_router, act.rlog + E, 1);
+        }
+        hipllm::GemvJob sh = job(L.sh_gate, act.sh_act, FFs);
+        sh.mode = 1;
+        sh.w2 = L.sh_up.ptr;
+        sh.yq = act.sh_actq;
+        jobs[nj++] = sh;
+        grouped(jobs, nj, hidden, L.post_norm, true, "post-attention norm + router + shared gate/up");
+    } else if (L.fused_router) {
         proj(L.router, act.norm, act.normq, H, rows, act.rlog, ldr, nullptr, E + 1);
     } else {
         proj(L.router, act.norm, act.normq, H, rows, act.rlog, ldr);
         proj(L.shexp_router, act.norm, act.normq, H, rows, act.rlog + E, ldr);
     }
-    const void* xb = bf16_rows(act.norm, H, H, rows);
     launch_check(hipllm::launch_router_topk(act.rlog, ldr, rows, E, K, ids, act.rweight, stream), "router top-k");
+    const void* xb = bf16_rows(act.norm, H, H, rows);
     // Routed experts: gate/up + SwiGLU for every (row, route), then down.
     // The gate/up launches spread rows thinly over many blocks (the expert and
     // shared widths are small), so the XGroup form of their output comes from
@@ -674,19 +770,19 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
                                              act.act, act.actq, nullptr, nullptr, act.down, nullptr, H, FF, rows * K,
                                              ids, E, K, L.down_exps.expert_stride, 1, FF, H, stream),
                  "expert down");
-    // Shared expert.
-    if (xb) {
+    // Shared expert (gate/up already in sh_act / sh_actq after a grouped launch).
+    if (!grp && xb) {
         proj(L.sh_gate, act.norm, act.normq, H, rows, act.sh_gate, FFs, nullptr, 0, xb);
         proj(L.sh_up, act.norm, act.normq, H, rows, act.sh_act, FFs, nullptr, 0, xb);
         launch_check(hipllm::launch_swiglu(act.sh_gate, act.sh_act, act.sh_act, act.sh_actq, rows * FFs, stream),
                      "shared SwiGLU");
-    } else if (L.sh_gate.type == L.sh_up.type) {
+    } else if (!grp && L.sh_gate.type == L.sh_up.type) {
         launch_check(hipllm::launch_gemv_batched(L.sh_gate.type, L.sh_gate.ptr, L.sh_up.ptr, L.sh_gate.row_bytes,
                                                  act.norm, act.normq, nullptr, nullptr, act.sh_act, nullptr, FFs,
                                                  H, rows, nullptr, 1, 1, 0, 0, H, FFs, stream),
                      "shared gate/up");
         launch_check(hipllm::launch_prep_x(act.sh_act, act.sh_actq, rows * FFs, stream), "shared activations");
-    } else {
+    } else if (!grp) {
         proj(L.sh_gate, act.norm, act.normq, H, rows, act.sh_down, FFs);
         proj(L.sh_up, act.norm, act.normq, H, rows, act.sh_act, FFs);
         launch_check(hipllm::launch_swiglu(act.sh_down, act.sh_act, act.sh_act, act.sh_actq, rows * FFs, stream),
@@ -694,11 +790,16 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
     }
     proj(L.sh_down, act.sh_act, act.sh_actq, FFs, rows, act.sh_down, H, nullptr, 0,
          bf16_rows(act.sh_act, FFs, FFs, rows));
-    launch_check(hipllm::launch_moe_combine(hidden, act.down, act.rweight, act.sh_down, act.rlog + E, ldr, next, rows,
-                                            H, K, stream),
-                 "MoE combine");
-    launch_check(hipllm::launch_rmsnorm(next, next_gamma, act.norm, act.normq, rows, H, config.norm_epsilon, stream),
-                 "RMSNorm");
+    if (next_norm) {
+        launch_check(hipllm::launch_moe_combine_norm(hidden, act.down, act.rweight, act.sh_down, act.rlog + E, ldr,
+                                                     next, next_gamma, act.norm, act.normq, rows, H, K,
+                                                     config.norm_epsilon, stream),
+                     "MoE combine + RMSNorm");
+    } else {
+        launch_check(hipllm::launch_moe_combine(hidden, act.down, act.rweight, act.sh_down, act.rlog + E, ldr, next,
+                                                rows, H, K, stream),
+                     "MoE combine");
+    }
 }
 
 void HipMoeLLM::Impl::forward(std::size_t rows, std::size_t pos0, const std::int32_t* ids,
@@ -709,11 +810,14 @@ void HipMoeLLM::Impl::forward(std::size_t rows, std::size_t pos0, const std::int
     launch_check(hipllm::launch_embed(embedding.type, embedding.ptr, embedding.row_bytes, ids, rows,
                                       config.vocabulary_size, H, h, stream),
                  "embedding");
-    // Each norm is fused into the launch that finishes its input row: the
-    // mixer's output projection applies post_norm, the MoE combine applies the
-    // next layer's input norm (the output norm after the last layer).
-    launch_check(hipllm::launch_rmsnorm(h, layers[0].attn_norm, act.norm, act.normq, rows, H, eps, stream),
-                 "RMSNorm");
+    // The MoE combine applies the next layer's input norm (the output norm
+    // after the last layer) unless that layer's grouped launch normalises in
+    // its prologue; the post-mixer norm runs after the output projection, or
+    // inside the grouped router launch.
+    if (!grouped_mixer(layers[0], rows)) {
+        launch_check(hipllm::launch_rmsnorm(h, layers[0].attn_norm, act.norm, act.normq, rows, H, eps, stream),
+                     "RMSNorm");
+    }
     for (std::size_t l = 0; l < layers.size(); ++l) {
         const MoeLayer& L = layers[l];
         if (L.full) {
@@ -721,7 +825,9 @@ void HipMoeLLM::Impl::forward(std::size_t rows, std::size_t pos0, const std::int
         } else {
             deltanet_layer(l, rows, h, tmp);
         }
-        moe_layer(l, rows, tmp, h, l + 1 < layers.size() ? layers[l + 1].attn_norm : output_norm);
+        const bool last = l + 1 == layers.size();
+        moe_layer(l, rows, tmp, h, last ? output_norm : layers[l + 1].attn_norm,
+                  last || !grouped_mixer(layers[l + 1], rows));
     }
     const float* last = act.norm + (rows - 1) * H;
     const hipllm::XGroup* lastq = act.normq + (rows - 1) * (H / 16);

@@ -95,6 +95,8 @@ SIGNATURES = {
                                  _P]),
     "hipllm_router_topk": (_I, [_P, _S, _S, _S, _S, _P, _P, _P]),
     "hipllm_moe_combine": (_I, [_P, _P, _P, _P, _P, _S, _P, _S, _S, _S, _P]),
+    "hipllm_moe_combine_norm": (_I, [_P, _P, _P, _P, _P, _S, _P, _P, _P, _P, _S, _S, _S, _F, _P]),
+    "hipllm_gemv_multi_norm": (_I, [_P, _S, _P, _P, _F, _S, _P, _P, _P]),
     "hipllm_gdn_gates": (_I, [_P, _P, _S, _P, _P, _P, _P, _S, _S, _P]),
     "hipllm_conv1d_silu": (_I, [_P, _S, _P, _P, _P, _S, _S, _S, _S, _P]),
     "hipllm_l2norm_heads": (_I, [_P, _S, _S, _S, _S, _F, _P]),
@@ -362,6 +364,33 @@ def _k_moe_combine(residual, down, w, shared, sgate, ld_sgate, out, tokens, h, k
                                    _ptr(out), tokens, h, k, _stream(stream)))
 
 
+class GemvJob(ctypes.Structure):
+    """HipllmGemvJob (include/hipllm.h)."""
+
+    _fields_ = [("type", ctypes.c_uint32), ("mode", ctypes.c_uint32), ("w", ctypes.c_void_p),
+                ("w2", ctypes.c_void_p), ("row_bytes", ctypes.c_size_t), ("bias", ctypes.c_void_p),
+                ("residual", ctypes.c_void_p), ("y", ctypes.c_void_p), ("yq", ctypes.c_void_p),
+                ("n", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
+def _k_gemv_multi_norm(jobs, x, gamma, eps, k, norm=None, normq=None, stream=None):
+    """jobs: dicts with type, mode (0/1), w, w2, row_bytes, bias, residual, y, yq, n."""
+    arr = (GemvJob * max(1, len(jobs)))()
+    for i, j in enumerate(jobs):
+        arr[i] = GemvJob(j["type"], j.get("mode", 0), _ptr(j["w"]), _ptr(j.get("w2")), j["row_bytes"],
+                         _ptr(j.get("bias")), _ptr(j.get("residual")), _ptr(j["y"]), _ptr(j.get("yq")), j["n"],
+                         j.get("reserved", 0))
+    check(lib().hipllm_gemv_multi_norm(arr, len(jobs), _ptr(x), _ptr(gamma), eps, k, _ptr(norm), _ptr(normq),
+                                       _stream(stream)))
+
+
+def _k_moe_combine_norm(residual, down, w, shared, sgate, ld_sgate, out, gamma, norm, normq, tokens, h, k, eps,
+                        stream=None):
+    check(lib().hipllm_moe_combine_norm(_ptr(residual), _ptr(down), _ptr(w), _ptr(shared), _ptr(sgate), ld_sgate,
+                                        _ptr(out), _ptr(gamma), _ptr(norm), _ptr(normq), tokens, h, k, eps,
+                                        _stream(stream)))
+
+
 def _k_gdn_gates(alpha, beta_raw, ld, dt_bias, a, decay, beta, tokens, heads, stream=None):
     check(lib().hipllm_gdn_gates(_ptr(alpha), _ptr(beta_raw), ld, _ptr(dt_bias), _ptr(a), _ptr(decay), _ptr(beta),
                                  tokens, heads, _stream(stream)))
@@ -445,7 +474,9 @@ kernels = types.SimpleNamespace(
     gemv_swiglu=_k_gemv_swiglu, gemv_norm=_k_gemv_norm, gemv_swiglu_norm=_k_gemv_swiglu_norm, to_bf16=_k_to_bf16, gemm_mfma=_k_gemm_mfma, gemm=_k_gemm,
     gemm_workspace_bytes=lambda m, k: lib().hipllm_gemm_workspace_bytes(m, k), rmsnorm=_k_rmsnorm, embed=_k_embed, rope_kv=_k_rope_kv,
     attn_decode=_k_attn_decode, argmax=_k_argmax, swiglu=_k_swiglu, attn_prefill=_k_attn_prefill,
-    gemv_batched=_k_gemv_batched, router_topk=_k_router_topk, moe_combine=_k_moe_combine, gdn_gates=_k_gdn_gates,
+    gemv_batched=_k_gemv_batched, router_topk=_k_router_topk, moe_combine=_k_moe_combine,
+    moe_combine_norm=_k_moe_combine_norm,
+    gemv_multi_norm=_k_gemv_multi_norm, gdn_gates=_k_gdn_gates,
     conv1d_silu=_k_conv1d_silu, l2norm_heads=_k_l2norm_heads, gdn_scan=_k_gdn_scan, gated_rmsnorm=_k_gated_rmsnorm,
     conv_l2norm=_k_conv_l2norm, gdn_scan_gated=_k_gdn_scan_gated,
     split_qgate_norm=_k_split_qgate_norm, gate_mul=_k_gate_mul,

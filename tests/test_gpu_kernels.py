@@ -299,6 +299,92 @@ def test_gemv_swiglu_norm_matches_rmsnorm_then_swiglu(cuda, qtype, tiling):
     xgroup.check(outs[1][1], outs[1][0])
 
 
+MULTI_CASES = {
+    # DeltaNet decode shape: QKV, z, alpha/beta (F32) of one normalised row
+    "deltanet": (2048, [(synth.Q6_K, 0, 1000), (synth.Q4_K, 0, 520), (synth.F32, 0, 64)]),
+    # attention: Q/gate with bias and residual, packed K/V
+    "attention": (1024, [(synth.Q4_K, 0, 777), (synth.Q8_0, 0, 256)]),
+    # router (E + 1 rows) and shared gate/up + SwiGLU with its XGroup form
+    "router": (2048, [(synth.F32, 0, 257), (synth.Q8_0, 1, 512)]),
+    # SwiGLU of every quantized type, ragged Q5_0 rows (27 blocks)
+    "swiglu": (768, [(synth.Q4_K, 1, 48), (synth.Q6_K, 1, 32), (synth.Q5_0, 0, 100)]),
+    "ragged": (864, [(synth.Q8_0, 1, 64), (synth.Q5_0, 0, 33)]),
+}
+
+
+@pytest.mark.parametrize("case", sorted(MULTI_CASES))
+def test_gemv_multi_norm_matches_rmsnorm_then_gemvs(cuda, case):
+    # Every job of the grouped launch against hipllm_rmsnorm followed by the
+    # single GEMV (tiling 208 / 132) or SwiGLU GEMV (204) on its output:
+    # the same arithmetic in separately compiled kernels, so within 1e-6;
+    # the stored norm and its XGroup form bit for bit.
+    k, specs = MULTI_CASES[case]
+    x = torch.from_numpy(synth.normal(k, 91, stddev=3.0)).to(cuda)
+    g = torch.from_numpy(synth.normal(k, 92, stddev=0.5) + 1.0).to(cuda)
+    xn = torch.empty(k, dtype=torch.float32, device=cuda)
+    xq = xgroup.buffer(torch, k, cuda)
+    kernels.rmsnorm(x, g, xn, xq, 1, k, 1e-6)
+    jobs, refs = [], []
+    for i, (qtype, mode, n) in enumerate(specs):
+        w = random_rows(qtype, n, k, 100 + i)
+        dw = dev_bytes(w, cuda)
+        rb = w.shape[1]
+        y = torch.full((n,), float("nan"), device=cuda)
+        yref = torch.empty(n, device=cuda)
+        j = dict(type=qtype, mode=mode, w=dw, row_bytes=rb, y=y, n=n)
+        if mode == 1:
+            du = dev_bytes(random_rows(qtype, n, k, 200 + i), cuda)
+            j["w2"] = du
+            yq = xgroup.buffer(torch, n, cuda) if n % 16 == 0 else None
+            j["yq"] = yq
+            kernels.gemv_swiglu(qtype, dw, du, rb, xn, xq, yref, None, n, k, 204)
+        else:
+            b = torch.from_numpy(synth.normal(n, 300 + i)).to(cuda) if i == 0 else None
+            r = torch.from_numpy(synth.normal(n, 400 + i)).to(cuda) if i == 0 else None
+            j["bias"], j["residual"] = b, r
+            kernels.gemv_prepped(qtype, dw, rb, xn, xq, b, r, yref, n, k, 132 if qtype == synth.F32 else 208)
+        jobs.append(j)
+        refs.append(yref)
+    norm = torch.empty(k, device=cuda)
+    normq = xgroup.buffer(torch, k, cuda)
+    kernels.gemv_multi_norm(jobs, x, g, 1e-6, k, norm, normq)
+    assert torch.equal(norm.view(torch.int32), xn.view(torch.int32))
+    assert torch.equal(normq.view(torch.int32), xq.view(torch.int32))
+    for j, yref in zip(jobs, refs):
+        got, ref = j["y"].cpu().numpy(), yref.cpu().numpy()
+        print(case, j["type"], j["mode"], "max rel diff", rel_err(got, ref))
+        assert rel_err(got, ref) <= 1e-6
+        if j.get("yq") is not None:
+            xgroup.check(j["yq"], got)
+
+
+def test_gemv_multi_norm_rejects_bad_arguments(cuda):
+    k = 256
+    w = torch.zeros(1024 * 64, dtype=torch.uint8, device=cuda)
+    x = torch.ones(9216, device=cuda)
+    y = torch.zeros(64, device=cuda)
+    ok = dict(type=synth.Q8_0, mode=0, w=w, row_bytes=272, y=y, n=16)
+    kernels.gemv_multi_norm([ok], x, x, 1e-6, k)  # valid
+    torch.cuda.synchronize()
+    bad_jobs = [
+        [ok] * 4,                                                    # at most 3 jobs
+        [dict(ok, type=synth.F16, row_bytes=512)],                   # no F16 form
+        [dict(ok, type=synth.F32, row_bytes=1024, mode=1, w2=w)],    # F32 only in mode 0
+        [dict(ok, mode=1)],                                          # SwiGLU without W2
+        [dict(ok, mode=1, w2=w, yq=y, n=20)],                        # XGroup output needs n % 16 == 0
+        [dict(ok, yq=y)],                                            # XGroup output only in mode 1
+        [dict(ok, reserved=1)],
+        [dict(ok, row_bytes=100)],                                   # rows shorter than k
+    ]
+    for jobs in bad_jobs:
+        with pytest.raises(ValueError):
+            kernels.gemv_multi_norm(jobs, x, x, 1e-6, k)
+    with pytest.raises(ValueError):  # k beyond the 8192-value prologue
+        kernels.gemv_multi_norm([dict(ok, row_bytes=9792)], x, x, 1e-6, 9216)
+    with pytest.raises(ValueError):  # eps must be positive
+        kernels.gemv_multi_norm([ok], x, x, 0.0, k)
+
+
 def test_gemv_norm_rejects_bad_arguments(cuda):
     w = torch.zeros(144 * 40, dtype=torch.uint8, device=cuda)
     x = torch.zeros(9216, device=cuda)

@@ -10,11 +10,13 @@ and step, logits within max|l - ref| / max|ref| <= 1e-3.
 
 from __future__ import annotations
 
+import ctypes
 import math
 
 import numpy as np
 import pytest
 
+import oracle
 from myllm_amd import synth
 from myllm_amd.hipllm import HipLLM, LengthError, generate, kernels
 from oracle import moe_ref
@@ -301,6 +303,51 @@ def test_moe_combine(cuda):
     ref = res + np.einsum("tr,trh->th", w.astype(np.float64), down.reshape(T, k, H)) + \
         sh * moe_ref.sigmoid(rlog[:, E:E + 1])
     assert rel_err(out.cpu().numpy(), ref) <= 1e-5
+
+
+def _oracle_rmsnorm_rows(x: np.ndarray, gamma: np.ndarray, eps: float) -> np.ndarray:
+    ref = np.ascontiguousarray(x, dtype=np.float32).copy()
+    for r in range(ref.shape[0]):
+        oracle.lib().oracle_rmsnorm(ref[r].ctypes.data, gamma.ctypes.data, ref.shape[1], ctypes.c_float(eps))
+    return ref
+
+
+@pytest.mark.parametrize("T,H,k", [(1, 2048, 8), (3, 256, 4), (2, 48, 2), (2, 50, 2), (1, 64, 10)])
+def test_moe_combine_norm(cuda, T, H, k):
+    """Combine + the next RMSNorm in one launch: the row equals the combine
+    launch's, the norm equals the oracle's RMSNorm of that row bit for bit."""
+    rng = np.random.default_rng(19)
+    E = 16
+    res = rng.normal(size=(T, H)).astype(np.float32)
+    down = rng.normal(size=(T * k, H)).astype(np.float32)
+    w = rng.uniform(size=(T, k)).astype(np.float32)
+    sh = rng.normal(size=(T, H)).astype(np.float32)
+    rlog = rng.normal(size=(T, E + 1)).astype(np.float32)
+    gamma = (synth.normal(H, 7, stddev=0.5) + 1.0).astype(np.float32)
+    drlog = t32(rlog, cuda)
+    args = (t32(res, cuda), t32(down, cuda), t32(w, cuda), t32(sh, cuda), drlog[:, E:], E + 1)
+    out_ref = torch.empty(T, H, device=cuda)
+    kernels.moe_combine(*args, out_ref, T, H, k)
+    out = torch.empty(T, H, device=cuda)
+    norm = torch.empty(T, H, device=cuda)
+    normq = xgroup.buffer(torch, H, cuda, T) if H % 16 == 0 else None
+    kernels.moe_combine_norm(*args, out, t32(gamma, cuda), norm, normq, T, H, k, 1e-6)
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), out_ref.cpu().numpy().view(np.uint32))
+    ref = _oracle_rmsnorm_rows(got, gamma, 1e-6)
+    gn = norm.cpu().numpy()
+    assert np.array_equal(gn.view(np.uint32), ref.view(np.uint32))
+    if normq is not None:
+        for t in range(T):
+            xgroup.check(normq[t * H:(t + 1) * H], gn[t])
+
+
+def test_moe_combine_norm_rejects_bad_arguments(cuda):
+    x = torch.zeros(64, device=cuda)
+    with pytest.raises(Exception):  # eps must be positive
+        kernels.moe_combine_norm(x, x, x, None, None, 0, x, x, x, None, 1, 64, 1, 0.0)
+    with pytest.raises(Exception):  # XGroup output needs h % 16 == 0
+        kernels.moe_combine_norm(x, x, x, None, None, 0, x, x, x, x, 1, 40, 1, 1e-6)
 
 
 def test_attn_prefill_continues_a_cache(cuda):
