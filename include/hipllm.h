@@ -86,7 +86,8 @@ int hipllm_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const fl
 /* hipllm_rmsnorm of the raw row x (gain gamma, k <= 8192, x and gamma
  * 16-byte aligned) followed by hipllm_gemv_prepped, in one launch: every
  * block normalises x into LDS (the same bits as hipllm_rmsnorm's XGroup
- * output) while its first weight loads are in flight. Quantized types only;
+ * output) while its first weight loads are in flight. gamma nullptr: no norm,
+ * the prologue makes hipllm_prep_x's XGroup form of x. Quantized types only;
  * `tiling` 0 picks the default, else 208, 216, 408 or 416. Replaces the
  * reference's RMSNorm + GEVM pair of each decode sub-block (encode_decode_layer,
  * metal_llm.mm:2758-2904; metal_llm.metal:785-823, 708-781). */
@@ -120,7 +121,8 @@ typedef struct HipllmGemvJob {
 /* Up to 3 GEMVs of one normalised row in one launch: every block normalises x
  * (k values, k % 32 == 0, k <= 8192; gain gamma) into LDS as
  * hipllm_rmsnorm does, then runs its job's rows (blocks of job p follow those
- * of job p - 1; tilings 208, 204 for mode 1, 132 for F32). norm and normq
+ * of job p - 1; tilings 208, 204 for mode 1 with yq, 108 for mode 1 without,
+ * 132 for F32). norm and normq
  * (nullable, 16-byte aligned) receive the normalised row and its XGroup form.
  * For one decode row this replaces the RMSNorm and the projections that read
  * it (the DeltaNet QKV / z / alpha-beta GEVMs, moe_llm.mm:2436-2500; the

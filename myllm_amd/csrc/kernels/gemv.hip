@@ -594,12 +594,17 @@ __device__ __forceinline__ void gemv_block(const uint8_t* __restrict__ w, const 
         extern __shared__ __align__(16) uint8_t norm_lds[];  // 4 k bytes, sized at launch
         if constexpr (T == kF32) {
             float* xs = reinterpret_cast<float*>(norm_lds);
-            rmsnorm_row(x, gamma, xs, nullptr, kblocks * 32, eps);
+            rmsnorm_row_lean(x, gamma, xs, nullptr, kblocks * 32, eps);
             __syncthreads();
             x = xs;
         } else {
             XGroup* xs = reinterpret_cast<XGroup*>(norm_lds);
-            rmsnorm_row_to_xgroups(x, gamma, xs, kblocks * 32, eps);
+            if (gamma) {
+                rmsnorm_row_lean(x, gamma, nullptr, xs, kblocks * 32, eps);
+            } else {
+                // No gain: the XGroup form of x itself.
+                for (uint32_t g = tid; g < kblocks * 2; g += blockDim.x) xgroup_encode_from(x + 16 * g, xs + g);
+            }
             __syncthreads();
             xq = xs;
         }
@@ -705,12 +710,22 @@ struct GemvMulti {
 // output is allowed) for quantized weights, 1 row x 32 octets for F32 (MODE
 // 0). Block 0 of the launch also stores the normalised row and its XGroup
 // form (norm, normq; nullable) for later launches.
-template <int MODE>
-constexpr int multi_tiling(uint32_t type) {
-    return type == kF32 ? 132 : (MODE == 1 ? 204 : 208);
+// The kernel's registers are the most any compiled-in body needs, and Q6_K
+// needs the most (about 100 VGPRs plain, 150 as SwiGLU, against 75-90 for the
+// other types), so the Q6_K bodies are compiled in only for launches that
+// have such a job (HEAVY: kMultiQ6K, kMultiQ6KSwiGLU). Without the Q6_K
+// SwiGLU body the kernel fits 96 VGPRs (5 waves per SIMD) without scratch.
+// Forms of a job: 0 = MODE 0 (208; F32 132), 1 = SwiGLU with XGroup output
+// (204: 16-row blocks), 2 = SwiGLU without it (108: 4-row blocks, four times
+// the blocks).
+constexpr int multi_tiling(uint32_t type, int form) {
+    return type == kF32 ? 132 : (form == 1 ? 204 : form == 2 ? 108 : 208);
 }
+constexpr uint32_t kMultiQ6K = 1, kMultiQ6KSwiGLU = 2;
 
-__global__ __launch_bounds__(256) void gemv_multi_kernel(const GemvMulti m) {
+template <uint32_t HEAVY>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HEAVY <= kMultiQ6K ? 5 : 1)))
+void gemv_multi_kernel(const GemvMulti m) {
     uint32_t p = 0, bx = blockIdx.x;
     while (p + 1 < m.jobs && bx >= m.job[p].blocks) {
         bx -= m.job[p].blocks;
@@ -718,7 +733,7 @@ __global__ __launch_bounds__(256) void gemv_multi_kernel(const GemvMulti m) {
     }
     const uint32_t k = m.kblocks * 32;
     if (blockIdx.x == 0 && m.norm) {
-        rmsnorm_row(m.x, m.gamma, m.norm, m.normq, k, m.eps);
+        rmsnorm_row_lean(m.x, m.gamma, m.norm, m.normq, k, m.eps);
         __syncthreads();  // the prologue below reuses the norm's LDS
     }
     const GemvJob& j = m.job[p];
@@ -728,16 +743,27 @@ __global__ __launch_bounds__(256) void gemv_multi_kernel(const GemvMulti m) {
     const uint32_t units256 = (k + 255) / 256;
     const Batch b;
 #define HIPLLM_MULTI(TT, MM, RR, OO, UU)                                                                            gemv_block<TT, RR, OO, MM, true>(w, w2, j.row_bytes, m.x, nullptr, j.bias, j.residual, j.y, j.yq, j.n, UU,                                      m.kblocks, b, m.gamma, m.eps, bx, 0)
-    switch (j.type * 2 + j.mode) {
-    case kQ4_K * 2: HIPLLM_MULTI(kQ4_K, 0, 2, 8, units256); break;
-    case kQ4_K * 2 + 1: HIPLLM_MULTI(kQ4_K, 1, 2, 4, units256); break;
-    case kQ6_K * 2: HIPLLM_MULTI(kQ6_K, 0, 2, 8, units256); break;
-    case kQ6_K * 2 + 1: HIPLLM_MULTI(kQ6_K, 1, 2, 4, units256); break;
-    case kQ8_0 * 2: HIPLLM_MULTI(kQ8_0, 0, 2, 8, units); break;
-    case kQ8_0 * 2 + 1: HIPLLM_MULTI(kQ8_0, 1, 2, 4, units); break;
-    case kQ5_0 * 2: HIPLLM_MULTI(kQ5_0, 0, 2, 8, units); break;
-    case kQ5_0 * 2 + 1: HIPLLM_MULTI(kQ5_0, 1, 2, 4, units); break;
-    case kF32 * 2: HIPLLM_MULTI(kF32, 0, 1, 32, units256); break;
+    const uint32_t form = j.mode == 0 ? 0 : (j.yq ? 1 : 2);
+    switch (j.type * 3 + form) {
+    case kQ4_K * 3: HIPLLM_MULTI(kQ4_K, 0, 2, 8, units256); break;
+    case kQ4_K * 3 + 1: HIPLLM_MULTI(kQ4_K, 1, 2, 4, units256); break;
+    case kQ4_K * 3 + 2: HIPLLM_MULTI(kQ4_K, 1, 1, 8, units256); break;
+    case kQ6_K * 3:
+        if constexpr ((HEAVY & kMultiQ6K) != 0) HIPLLM_MULTI(kQ6_K, 0, 2, 8, units256);
+        break;
+    case kQ6_K * 3 + 1:
+        if constexpr ((HEAVY & kMultiQ6KSwiGLU) != 0) HIPLLM_MULTI(kQ6_K, 1, 2, 4, units256);
+        break;
+    case kQ6_K * 3 + 2:
+        if constexpr ((HEAVY & kMultiQ6KSwiGLU) != 0) HIPLLM_MULTI(kQ6_K, 1, 1, 8, units256);
+        break;
+    case kQ8_0 * 3: HIPLLM_MULTI(kQ8_0, 0, 2, 8, units); break;
+    case kQ8_0 * 3 + 1: HIPLLM_MULTI(kQ8_0, 1, 2, 4, units); break;
+    case kQ8_0 * 3 + 2: HIPLLM_MULTI(kQ8_0, 1, 1, 8, units); break;
+    case kQ5_0 * 3: HIPLLM_MULTI(kQ5_0, 0, 2, 8, units); break;
+    case kQ5_0 * 3 + 1: HIPLLM_MULTI(kQ5_0, 1, 2, 4, units); break;
+    case kQ5_0 * 3 + 2: HIPLLM_MULTI(kQ5_0, 1, 1, 8, units); break;
+    case kF32 * 3: HIPLLM_MULTI(kF32, 0, 1, 32, units256); break;
     default: break;  // rejected by the launcher
     }
 #undef HIPLLM_MULTI
@@ -997,14 +1023,16 @@ static int norm_tiling(int t, int mode, bool whole_groups) {
     return 100 * R + OPR;
 }
 
+// gamma nullptr: no norm, the prologue only encodes x (eps unused).
 static bool norm_ok(uint32_t type, const float* x, const float* gamma, size_t k, float eps) {
-    return (type == kQ4_K || type == kQ6_K || type == kQ8_0 || type == kQ5_0) && x && gamma && k % 16 == 0 &&
+    return (type == kQ4_K || type == kQ6_K || type == kQ8_0 || type == kQ5_0) && x && k % 16 == 0 &&
            k / 16 <= kNormMaxGroups && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
-           reinterpret_cast<uintptr_t>(gamma) % 16 == 0 && eps > 0.0f;
+           reinterpret_cast<uintptr_t>(gamma) % 16 == 0 && (!gamma || eps > 0.0f);
 }
 
 // y = W rmsnorm(x) (+ bias) (+ residual) with the norm in the GEMV's
-// prologue (quantized weights; k <= 8192).
+// prologue (quantized weights; k <= 8192); without gamma, y = W x with x's
+// XGroup form made in the prologue.
 int launch_gemv_norm(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* gamma, float eps,
                      const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
                      hipStream_t stream) {
@@ -1048,6 +1076,7 @@ int launch_gemv_multi_norm(const GemvJob* jobs, size_t count, const float* x, co
     if (normq && !norm) return kInvalidArgument;
     GemvMulti m{};
     uint64_t total = 0;
+    uint32_t heavy = 0;
     for (size_t i = 0; i < count; ++i) {
         GemvJob j = jobs[i];
         const bool quant = j.type == kQ4_K || j.type == kQ6_K || j.type == kQ8_0 || j.type == kQ5_0;
@@ -1062,7 +1091,8 @@ int launch_gemv_multi_norm(const GemvJob* jobs, size_t count, const float* x, co
         if (j.yq && (j.mode != 1 || j.n % 16 != 0 || reinterpret_cast<uintptr_t>(j.yq) % 16 != 0)) {
             return kInvalidArgument;
         }
-        const int t = j.mode ? multi_tiling<1>(j.type) : multi_tiling<0>(j.type);
+        if (j.type == kQ6_K) heavy |= j.mode ? kMultiQ6KSwiGLU : kMultiQ6K;
+        const int t = multi_tiling(j.type, j.mode == 0 ? 0 : (j.yq ? 1 : 2));
         const uint32_t rpb = 32u / (t % 100) * (t / 100);
         j.blocks = (j.n + rpb - 1) / rpb;
         total += j.blocks;
@@ -1076,7 +1106,9 @@ int launch_gemv_multi_norm(const GemvJob* jobs, size_t count, const float* x, co
     m.eps = eps;
     m.norm = norm;
     m.normq = normq;
-    hipLaunchKernelGGL(gemv_multi_kernel, dim3(static_cast<uint32_t>(total)), dim3(256), k * 4, stream, m);
+    auto kernel = heavy == 0 ? gemv_multi_kernel<0>
+                  : heavy == kMultiQ6K ? gemv_multi_kernel<kMultiQ6K> : gemv_multi_kernel<kMultiQ6K | kMultiQ6KSwiGLU>;
+    hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(total)), dim3(256), k * 4, stream, m);
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 

@@ -78,12 +78,13 @@ __device__ inline void rmsnorm_row_groups(const float* __restrict__ xr, const fl
     }
 }
 
-// rmsnorm_row_groups' XGroup output with few live registers: x is read
-// twice (sum of squares, then scale and encode), each group transiently, in
-// the same order, so the bits are the same. For kernels that normalise their
+// rmsnorm_row_groups' outputs with few live registers: x is read twice (sum
+// of squares, then scale and encode), each group transiently, in the same
+// order, so the bits are the same. yr (values) and yq (XGroup form) are
+// nullable, global or LDS; cols % 16 == 0. For kernels that normalise their
 // input in a prologue while other loads are in flight.
-__device__ inline void rmsnorm_row_to_xgroups(const float* __restrict__ xr, const float* __restrict__ gamma,
-                                              XGroup* yq, uint32_t cols, float eps) {
+__device__ inline void rmsnorm_row_lean(const float* __restrict__ xr, const float* __restrict__ gamma, float* yr,
+                                        XGroup* yq, uint32_t cols, float eps) {
     const uint32_t groups = cols / 16;
     double ss = 0.0;
     for (uint32_t g = threadIdx.x; g < groups; g += blockDim.x) {
@@ -116,7 +117,12 @@ __device__ inline void rmsnorm_row_to_xgroups(const float* __restrict__ xr, cons
             v[4 * i + 2] = a.z * (inv * b.z);
             v[4 * i + 3] = a.w * (inv * b.w);
         }
-        xgroup_encode(v, yq + g);
+        if (yr) {
+            float4* y4 = reinterpret_cast<float4*>(yr + 16 * g);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) y4[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+        }
+        if (yq) xgroup_encode(v, yq + g);
     }
 }
 

@@ -608,7 +608,8 @@ bool HipMoeLLM::Impl::grouped_mixer(const MoeLayer& L, std::size_t rows) const {
 bool HipMoeLLM::Impl::grouped_moe(const MoeLayer& L, std::size_t rows) const {
     if (rows != kGroupedRows || H % 256 != 0 || H > 8192 || FFs % 16 != 0) return false;
     return groupable(L.router) && (L.fused_router || groupable(L.shexp_router)) && groupable(L.sh_gate, true) &&
-           L.sh_gate.type == L.sh_up.type && L.sh_gate.row_bytes == L.sh_up.row_bytes;
+           L.sh_gate.type == L.sh_up.type && L.sh_gate.row_bytes == L.sh_up.row_bytes &&
+           groupable(L.sh_down, true) && FFs <= 8192;
 }
 
 // Gated full attention (moe_llm.mm:2238-2434) over `rows` rows at positions
@@ -734,8 +735,10 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
     const bool grp = grouped_moe(L, rows);
     if (grp) {
         // Post-attention norm (stored for the expert projections), router,
-        // shared-expert gate and shared gate/up + SwiGLU (with its XGroup
-        // form) in one launch.
+        // shared-expert gate and shared gate/up + SwiGLU in one launch. The
+        // SwiGLU output stays FP32 (4-row blocks, four times as many as the
+        // 16-row blocks its XGroup form would need); the shared down
+        // projection encodes it in its prologue.
         hipllm::GemvJob jobs[3];
         std::size_t nj = 0;
         if (L.fused_router) {
@@ -747,7 +750,6 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
         hipllm::GemvJob sh = job(L.sh_gate, act.sh_act, FFs);
         sh.mode = 1;
         sh.w2 = L.sh_up.ptr;
-        sh.yq = act.sh_actq;
         jobs[nj++] = sh;
         grouped(jobs, nj, hidden, L.post_norm, true, "post-attention norm + router + shared gate/up");
     } else if (L.fused_router) {
@@ -770,7 +772,7 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
                                              act.act, act.actq, nullptr, nullptr, act.down, nullptr, H, FF, rows * K,
                                              ids, E, K, L.down_exps.expert_stride, 1, FF, H, stream),
                  "expert down");
-    // Shared expert (gate/up already in sh_act / sh_actq after a grouped launch).
+    // Shared expert (gate/up already in sh_act after a grouped launch).
     if (!grp && xb) {
         proj(L.sh_gate, act.norm, act.normq, H, rows, act.sh_gate, FFs, nullptr, 0, xb);
         proj(L.sh_up, act.norm, act.normq, H, rows, act.sh_act, FFs, nullptr, 0, xb);
@@ -788,8 +790,14 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
         launch_check(hipllm::launch_swiglu(act.sh_down, act.sh_act, act.sh_act, act.sh_actq, rows * FFs, stream),
                      "shared SwiGLU");
     }
-    proj(L.sh_down, act.sh_act, act.sh_actq, FFs, rows, act.sh_down, H, nullptr, 0,
-         bf16_rows(act.sh_act, FFs, FFs, rows));
+    if (grp) {
+        launch_check(hipllm::launch_gemv_norm(L.sh_down.type, L.sh_down.ptr, L.sh_down.row_bytes, act.sh_act, nullptr,
+                                              0.0f, nullptr, nullptr, act.sh_down, H, FFs, 0, stream),
+                     "shared down");
+    } else {
+        proj(L.sh_down, act.sh_act, act.sh_actq, FFs, rows, act.sh_down, H, nullptr, 0,
+             bf16_rows(act.sh_act, FFs, FFs, rows));
+    }
     if (next_norm) {
         launch_check(hipllm::launch_moe_combine_norm(hidden, act.down, act.rweight, act.sh_down, act.rlog + E, ldr,
                                                      next, next_gamma, act.norm, act.normq, rows, H, K,

@@ -309,13 +309,16 @@ MULTI_CASES = {
     # SwiGLU of every quantized type, ragged Q5_0 rows (27 blocks)
     "swiglu": (768, [(synth.Q4_K, 1, 48), (synth.Q6_K, 1, 32), (synth.Q5_0, 0, 100)]),
     "ragged": (864, [(synth.Q8_0, 1, 64), (synth.Q5_0, 0, 33)]),
+    # mode 2 here: SwiGLU without the XGroup output (4-row blocks), ragged row counts
+    "swiglu_fp32": (1024, [(synth.F32, 0, 257), (synth.Q8_0, 2, 510), (synth.Q6_K, 2, 37)]),
+    "swiglu_fp32_q4": (512, [(synth.Q4_K, 2, 130), (synth.Q5_0, 2, 64)]),
 }
 
 
 @pytest.mark.parametrize("case", sorted(MULTI_CASES))
 def test_gemv_multi_norm_matches_rmsnorm_then_gemvs(cuda, case):
     # Every job of the grouped launch against hipllm_rmsnorm followed by the
-    # single GEMV (tiling 208 / 132) or SwiGLU GEMV (204) on its output:
+    # single GEMV (tiling 208 / 132) or SwiGLU GEMV (204, 108) on its output:
     # the same arithmetic in separately compiled kernels, so within 1e-6;
     # the stored norm and its XGroup form bit for bit.
     k, specs = MULTI_CASES[case]
@@ -331,13 +334,13 @@ def test_gemv_multi_norm_matches_rmsnorm_then_gemvs(cuda, case):
         rb = w.shape[1]
         y = torch.full((n,), float("nan"), device=cuda)
         yref = torch.empty(n, device=cuda)
-        j = dict(type=qtype, mode=mode, w=dw, row_bytes=rb, y=y, n=n)
-        if mode == 1:
+        j = dict(type=qtype, mode=min(mode, 1), w=dw, row_bytes=rb, y=y, n=n)
+        if mode >= 1:
             du = dev_bytes(random_rows(qtype, n, k, 200 + i), cuda)
             j["w2"] = du
-            yq = xgroup.buffer(torch, n, cuda) if n % 16 == 0 else None
+            yq = xgroup.buffer(torch, n, cuda) if n % 16 == 0 and mode == 1 else None
             j["yq"] = yq
-            kernels.gemv_swiglu(qtype, dw, du, rb, xn, xq, yref, None, n, k, 204)
+            kernels.gemv_swiglu(qtype, dw, du, rb, xn, xq, yref, None, n, k, 204 if mode == 1 else 108)
         else:
             b = torch.from_numpy(synth.normal(n, 300 + i)).to(cuda) if i == 0 else None
             r = torch.from_numpy(synth.normal(n, 400 + i)).to(cuda) if i == 0 else None
@@ -383,6 +386,22 @@ def test_gemv_multi_norm_rejects_bad_arguments(cuda):
         kernels.gemv_multi_norm([dict(ok, row_bytes=9792)], x, x, 1e-6, 9216)
     with pytest.raises(ValueError):  # eps must be positive
         kernels.gemv_multi_norm([ok], x, x, 0.0, k)
+
+
+@pytest.mark.parametrize("qtype,n,k", [(synth.Q8_0, 2048, 512), (synth.Q4_K, 300, 768), (synth.Q6_K, 64, 2048)])
+def test_gemv_norm_without_gain_encodes_x(cuda, qtype, n, k):
+    # gamma = None: the prologue only encodes x, against hipllm_prep_x then
+    # the GEMV (separately compiled, so within 1e-6).
+    w = random_rows(qtype, n, k, 93)
+    dw = dev_bytes(w, cuda)
+    x = torch.from_numpy(synth.normal(k, 94, stddev=2.0)).to(cuda)
+    xq = xgroup.buffer(torch, k, cuda)
+    kernels.prep_x(x, xq, k)
+    y1 = torch.empty(n, device=cuda)
+    y2 = torch.empty(n, device=cuda)
+    kernels.gemv_prepped(qtype, dw, w.shape[1], x, xq, None, None, y1, n, k, 208)
+    kernels.gemv_norm(qtype, dw, w.shape[1], x, None, 0.0, None, None, y2, n, k, 208)
+    assert rel_err(y2.cpu().numpy(), y1.cpu().numpy()) <= 1e-6
 
 
 def test_gemv_norm_rejects_bad_arguments(cuda):
