@@ -246,6 +246,31 @@ int hipllm_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row
                         size_t k, size_t vectors, const int32_t* ids, size_t experts, size_t routes,
                         size_t expert_stride, int x_routed, size_t ldx, size_t ldy, void* stream);
 
+/* Routed expert gate/up + SwiGLU with the routing in the same launch: every
+ * block runs hipllm_router_topk's softmax / top-k / renormalisation on its
+ * token's logits (experts <= 256, routes <= 8), then vector t * routes + q
+ * computes y = silu(Wg_e x_t) * (Wu_e x_t) for expert e = ids_out[t, q] (yq:
+ * nullable XGroup form, n % 16 == 0); ids_out and weights_out receive the
+ * routes. Quantized weights, experts at expert_stride bytes. Replaces
+ * metal_softmax_f32 / metal_topk_f32 / metal_topk_renorm_f32 and the expert
+ * gate/up GEMMs with their SwiGLU (metal_llm.metal:826-890, 1424-1521;
+ * moe_llm.mm:2642-2760). */
+int hipllm_gemv_routed_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
+                              const void* xq, size_t ldx, float* y, void* yq, size_t n, size_t k, size_t tokens,
+                              const float* logits, size_t ld_logits, size_t experts, size_t routes,
+                              size_t expert_stride, int32_t* ids_out, float* weights_out, void* stream);
+
+/* The shared expert's down projection with the MoE combine in its epilogue,
+ * one token: y = residual + (sum_q weights[q] down[q n : (q + 1) n] +
+ * sigmoid(sgate[0]) W x), the operations of hipllm_moe_combine. x is raw FP32
+ * (k <= 8192, 16-byte aligned; its XGroup form is made in the prologue);
+ * quantized weights. Replaces the shared-expert down GEVM,
+ * metal_expert_weighted_reduce_f32, the shared gate and the FFN residual
+ * (metal_llm.metal:1525-1542, 1265-1276; moe_llm.mm:2790-2885). */
+int hipllm_gemv_moe_combine(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* residual,
+                            const float* down, const float* weights, const float* sgate, size_t routes, float* y,
+                            size_t n, size_t k, void* stream);
+
 /* Per token: softmax over `experts` logits, top-k insertion (strict '>', the
  * lower id wins ties), renormalised weights. Replaces the router tail of
  * encode_routes (moe_llm.mm:2642-2690): metal_softmax_f32, metal_topk_f32,

@@ -35,6 +35,7 @@
 #include "common.h"
 #include "launch.h"
 #include "norm.h"
+#include "router.h"
 
 namespace hipllm {
 
@@ -473,6 +474,11 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // ids[j] (clamped to experts - 1), at byte offset ids[j] * expert_stride; the
 // input is row j (x_routed) or row j / routes of x. Without ids every vector
 // uses the same weights (a batch of rows through one matrix).
+// ROUTE kernels pick the experts themselves: every block runs the router's
+// softmax / top-k / renormalisation (router.h) on its token's logits with its
+// first wave, takes its route's expert from LDS, and the first block of each
+// token stores the ids and weights (ids_out, weights_out) for the launches
+// that follow.
 struct Batch {
     const int32_t* ids = nullptr;
     uint32_t experts = 1;
@@ -481,7 +487,32 @@ struct Batch {
     uint32_t x_routed = 0;
     uint32_t ldx = 0;  // values between input rows (multiple of 16)
     uint32_t ldy = 0;  // values between output rows
+    const float* logits = nullptr;  // ROUTE: [tokens, ld_logits] router logits
+    uint32_t ld_logits = 0;
+    int32_t* ids_out = nullptr;     // ROUTE: [tokens, routes]
+    float* weights_out = nullptr;   // ROUTE: [tokens, routes]
 };
+constexpr uint32_t kRouteMaxExperts = 256;  // logits held 4 per lane by one wave
+
+// MODE 2 epilogue, the MoE combine of one token on the shared expert's down
+// projection: y[r] = residual[r] + (sum_q weights[q] down[q n + r] +
+// sigmoid(sgate[0]) (W x)[r]), the same operations in the same order as the
+// combine kernel.
+struct MoeCombine {
+    const float* down = nullptr;
+    const float* weights = nullptr;
+    const float* sgate = nullptr;
+    uint32_t routes = 0;
+};
+
+__device__ __forceinline__ float combine_row(const MoeCombine& m, const float* residual, float shared, uint32_t r,
+                                             uint32_t n) {
+    float acc = 0.0f;
+    for (uint32_t q = 0; q < m.routes; ++q) acc += m.weights[q] * m.down[static_cast<size_t>(q) * n + r];
+    float moe = acc;
+    moe += shared * sigmoid_ref(m.sgate[0]);
+    return residual[r] + moe;
+}
 
 // R rows per octet, OPR octets per row group (K split), 32 / OPR row groups
 // per block of 4 waves: rows per block = 32 R / OPR.
@@ -515,20 +546,36 @@ constexpr uint32_t kNormMaxGroups = 512;  // rows of up to 8192 values
 
 // The work of block (bx, by) of a GEMV launch; the kernels below call it with
 // their block index (or, for a grouped launch, the index within their job).
-template <uint32_t T, int R, int OPR, int MODE, bool NORM>
+template <uint32_t T, int R, int OPR, int MODE, bool NORM, bool ROUTE = false>
 __device__ __forceinline__ void gemv_block(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2,
                                            size_t row_bytes, const float* __restrict__ x,
                                            const XGroup* __restrict__ xq, const float* __restrict__ bias,
                                            const float* __restrict__ residual, float* __restrict__ y,
                                            XGroup* __restrict__ yq, uint32_t n, uint32_t units, uint32_t kblocks,
                                            const Batch& batch, const float* __restrict__ gamma, float eps,
-                                           uint32_t bx, uint32_t by) {
+                                           uint32_t bx, uint32_t by, const MoeCombine& cmb = MoeCombine()) {
     using U = Unit<T>;
     {
         // Vector j of the batch: shift weights, input, output and residual.
         const uint32_t j = by;
         const uint32_t xrow = batch.x_routed ? j : j / batch.routes;
-        if (batch.ids) {
+        if constexpr (ROUTE) {
+            __shared__ int32_t route_id[8];
+            __shared__ float route_w[8];
+            const uint32_t t = j / batch.routes, q = j % batch.routes;
+            if (threadIdx.x < 64) {
+                topk_row<kRouteMaxExperts / 64>(batch.logits + static_cast<size_t>(t) * batch.ld_logits,
+                                                 batch.experts, batch.routes, route_id, route_w, threadIdx.x);
+            }
+            __syncthreads();
+            if (bx == 0 && q == 0 && threadIdx.x < batch.routes) {
+                batch.ids_out[t * batch.routes + threadIdx.x] = route_id[threadIdx.x];
+                batch.weights_out[t * batch.routes + threadIdx.x] = route_w[threadIdx.x];
+            }
+            const uint32_t e = min(static_cast<uint32_t>(route_id[q]), batch.experts - 1);
+            w += static_cast<size_t>(e) * batch.expert_stride;
+            if (MODE == 1) w2 += static_cast<size_t>(e) * batch.expert_stride;
+        } else if (batch.ids) {
             const uint32_t e = min(static_cast<uint32_t>(batch.ids[j]), batch.experts - 1);
             w += static_cast<size_t>(e) * batch.expert_stride;
             if (MODE == 1) w2 += static_cast<size_t>(e) * batch.expert_stride;
@@ -626,7 +673,9 @@ __device__ __forceinline__ void gemv_block(const uint8_t* __restrict__ w, const 
 #pragma unroll
             for (int i = 0; i < R; ++i) {
                 const uint32_t r = row0 + i;
-                if (MODE == 0) {
+                if (MODE == 2) {
+                    if (r < n) y[r] = combine_row(cmb, residual, acc[i], r, n);
+                } else if (MODE == 0) {
                     if (r < n) {
                         float s = acc[i];
                         if (bias) s += bias[r];
@@ -657,7 +706,9 @@ __device__ __forceinline__ void gemv_block(const uint8_t* __restrict__ w, const 
                 s += part[g * WPG + k][i];
                 if (MODE == 1) s2 += part[g * WPG + k][R + i];
             }
-            if (MODE == 0) {
+            if (MODE == 2) {
+                if (r < n) y[r] = combine_row(cmb, residual, s, r, n);
+            } else if (MODE == 0) {
                 if (r < n) {
                     if (bias) s += bias[r];
                     if (residual) s += residual[r];
@@ -680,16 +731,17 @@ __device__ __forceinline__ void gemv_block(const uint8_t* __restrict__ w, const 
     }
 }
 
-template <uint32_t T, int R, int OPR, int MODE, bool NORM = false>
+template <uint32_t T, int R, int OPR, int MODE, bool NORM = false, bool ROUTE = false>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2,
                                                    size_t row_bytes, const float* __restrict__ x,
                                                    const XGroup* __restrict__ xq, const float* __restrict__ bias,
                                                    const float* __restrict__ residual, float* __restrict__ y,
                                                    XGroup* __restrict__ yq, uint32_t n, uint32_t units,
                                                    uint32_t kblocks, const Batch batch,
-                                                   const float* __restrict__ gamma = nullptr, float eps = 0.0f) {
-    gemv_block<T, R, OPR, MODE, NORM>(w, w2, row_bytes, x, xq, bias, residual, y, yq, n, units, kblocks, batch,
-                                      gamma, eps, blockIdx.x, blockIdx.y);
+                                                   const float* __restrict__ gamma = nullptr, float eps = 0.0f,
+                                                   const MoeCombine cmb = MoeCombine()) {
+    gemv_block<T, R, OPR, MODE, NORM, ROUTE>(w, w2, row_bytes, x, xq, bias, residual, y, yq, n, units, kblocks,
+                                             batch, gamma, eps, blockIdx.x, blockIdx.y, cmb);
 }
 
 struct GemvMulti {
@@ -832,7 +884,8 @@ int launch_typed(int tiling, const void* w, const void* w2, size_t row_bytes, co
 template <uint32_t T, int MODE>
 int launch_typed_norm(int tiling, const void* w, const void* w2, size_t row_bytes, const float* x,
                       const float* gamma, float eps, const float* bias, const float* residual, float* y, XGroup* yq,
-                      uint32_t n, uint32_t units, uint32_t kblocks, hipStream_t stream) {
+                      uint32_t n, uint32_t units, uint32_t kblocks, hipStream_t stream,
+                      const MoeCombine& cmb = MoeCombine()) {
     const auto* wp = static_cast<const uint8_t*>(w);
     const auto* wp2 = static_cast<const uint8_t*>(w2);
     const uint32_t rpb = 32u / (tiling % 100) * (tiling / 100);
@@ -844,7 +897,7 @@ int launch_typed_norm(int tiling, const void* w, const void* w2, size_t row_byte
     case 100 * RR + OO:                                                                                       \
         hipLaunchKernelGGL((gemv_kernel<T, RR, OO, MODE, true>), grid, dim3(256), lds, stream, wp, wp2,        \
                            row_bytes, x, nullptr, bias, residual, y, yq, n, units, kblocks, Batch(), gamma,   \
-                           eps);                                                                              \
+                           eps, cmb);                                                                         \
         break;
         HIPLLM_GEMV_NORM_CASE(2, 4)
         HIPLLM_GEMV_NORM_CASE(2, 8)
@@ -861,12 +914,13 @@ int launch_typed_norm(int tiling, const void* w, const void* w2, size_t row_byte
 template <int MODE>
 int launch_any_norm(uint32_t type, int tiling, const void* w, const void* w2, size_t row_bytes, const float* x,
                     const float* gamma, float eps, const float* bias, const float* residual, float* y, XGroup* yq,
-                    uint32_t n, uint32_t units, uint32_t kblocks, hipStream_t stream) {
+                    uint32_t n, uint32_t units, uint32_t kblocks, hipStream_t stream,
+                    const MoeCombine& cmb = MoeCombine()) {
     switch (type) {
-    case kQ4_K: return launch_typed_norm<kQ4_K, MODE>(tiling, w, w2, row_bytes, x, gamma, eps, bias, residual, y, yq, n, units, kblocks, stream);
-    case kQ6_K: return launch_typed_norm<kQ6_K, MODE>(tiling, w, w2, row_bytes, x, gamma, eps, bias, residual, y, yq, n, units, kblocks, stream);
-    case kQ8_0: return launch_typed_norm<kQ8_0, MODE>(tiling, w, w2, row_bytes, x, gamma, eps, bias, residual, y, yq, n, units, kblocks, stream);
-    case kQ5_0: return launch_typed_norm<kQ5_0, MODE>(tiling, w, w2, row_bytes, x, gamma, eps, bias, residual, y, yq, n, units, kblocks, stream);
+    case kQ4_K: return launch_typed_norm<kQ4_K, MODE>(tiling, w, w2, row_bytes, x, gamma, eps, bias, residual, y, yq, n, units, kblocks, stream, cmb);
+    case kQ6_K: return launch_typed_norm<kQ6_K, MODE>(tiling, w, w2, row_bytes, x, gamma, eps, bias, residual, y, yq, n, units, kblocks, stream, cmb);
+    case kQ8_0: return launch_typed_norm<kQ8_0, MODE>(tiling, w, w2, row_bytes, x, gamma, eps, bias, residual, y, yq, n, units, kblocks, stream, cmb);
+    case kQ5_0: return launch_typed_norm<kQ5_0, MODE>(tiling, w, w2, row_bytes, x, gamma, eps, bias, residual, y, yq, n, units, kblocks, stream, cmb);
     default: return kInvalidArgument;
     }
 }
@@ -1063,6 +1117,88 @@ int launch_gemv_swiglu_norm(uint32_t type, const void* wg, const void* wu, size_
     const int code = tiling ? tiling : norm_tiling(gemv_default_tiling(nn, units, 1, 1, yq != nullptr), 1, yq != nullptr);
     return launch_any_norm<1>(type, code, wg, wu, row_bytes, x, gamma, eps, nullptr, nullptr, y, yq, nn, units,
                               static_cast<uint32_t>(k / 32), stream);
+}
+
+// y = residual + (sum_q weights[q] down[q] + sigmoid(sgate[0]) W x) for one
+// token, x raw FP32 (its XGroup form made in the prologue).
+int launch_gemv_moe_combine(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* residual,
+                            const float* down, const float* weights, const float* sgate, size_t routes, float* y,
+                            size_t n, size_t k, hipStream_t stream) {
+    if (!y || !residual || !down || !weights || !sgate || routes == 0 || routes > 64) return kInvalidArgument;
+    if (!norm_ok(type, x, nullptr, k, 0.0f)) return kInvalidArgument;
+    if (!w || row_bytes < k / block_elems(type) * block_bytes(type) || k % block_elems(type) != 0) {
+        return kInvalidArgument;
+    }
+    if ((type == kQ4_K && (row_bytes % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0)) ||
+        row_bytes % 2 != 0 || reinterpret_cast<uintptr_t>(w) % 2 != 0) {
+        return kInvalidArgument;
+    }
+    if (n == 0 || n > 0x7fffffffull) return n == 0 ? kInvalidArgument : kLengthError;
+    const uint32_t units = static_cast<uint32_t>((k + unit_elems(type) - 1) / unit_elems(type));
+    const uint32_t nn = static_cast<uint32_t>(n);
+    const int code = norm_tiling(gemv_pick_shape(type, nn, units, 0), 0, false);
+    MoeCombine c;
+    c.down = down;
+    c.weights = weights;
+    c.sgate = sgate;
+    c.routes = static_cast<uint32_t>(routes);
+    return launch_any_norm<2>(type, code, w, nullptr, row_bytes, x, nullptr, 0.0f, nullptr, residual, y, nullptr, nn,
+                              units, static_cast<uint32_t>(k / 32), stream, c);
+}
+
+// Routed expert gate/up + SwiGLU with the routes chosen in every block's
+// prologue (Batch, ROUTE): 16-row blocks, 2 rows x 4 octets, or 4 x 8 from
+// 8192 rows on.
+template <uint32_t T>
+int launch_routed(const void* wg, const void* wu, size_t row_bytes, const float* x, const XGroup* xq, float* y,
+                  XGroup* yq, uint32_t n, uint32_t units, uint32_t kblocks, const Batch& b, uint32_t vectors,
+                  hipStream_t stream) {
+    const auto* wp = static_cast<const uint8_t*>(wg);
+    const auto* up = static_cast<const uint8_t*>(wu);
+    if (n >= 8192) {
+        hipLaunchKernelGGL((gemv_kernel<T, 4, 8, 1, false, true>), dim3((n + 15) / 16, vectors), dim3(256), 0, stream,
+                           wp, up, row_bytes, x, xq, nullptr, nullptr, y, yq, n, units, kblocks, b);
+    } else {
+        hipLaunchKernelGGL((gemv_kernel<T, 2, 4, 1, false, true>), dim3((n + 15) / 16, vectors), dim3(256), 0, stream,
+                           wp, up, row_bytes, x, xq, nullptr, nullptr, y, yq, n, units, kblocks, b);
+    }
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+int launch_gemv_routed_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
+                              const XGroup* xq, size_t ldx, float* y, XGroup* yq, size_t n, size_t k, size_t tokens,
+                              const float* logits, size_t ld_logits, size_t experts, size_t routes,
+                              size_t expert_stride, int32_t* ids_out, float* weights_out, hipStream_t stream) {
+    if (!y || !wu || !logits || !ids_out || !weights_out || tokens == 0) return kInvalidArgument;
+    if (!(type == kQ4_K || type == kQ6_K || type == kQ8_0 || type == kQ5_0)) return kInvalidArgument;
+    const int rc = check_common(type, wg, wu, row_bytes, x, xq, n, k, expert_stride);
+    if (rc != kOk) return rc;
+    if (experts == 0 || routes == 0 || routes > 8 || routes > experts || ld_logits < experts ||
+        expert_stride < n * row_bytes || ldx < k || ldx % 16 != 0) {
+        return kInvalidArgument;
+    }
+    if (yq && (n % 16 != 0 || reinterpret_cast<uintptr_t>(yq) % 16 != 0)) return kInvalidArgument;
+    if (experts > kRouteMaxExperts) return kLengthError;
+    if (tokens * routes > 65535 || ldx > 0xffffffffu || ld_logits > 0xffffffffu) return kLengthError;
+    Batch b;
+    b.experts = static_cast<uint32_t>(experts);
+    b.routes = static_cast<uint32_t>(routes);
+    b.expert_stride = expert_stride;
+    b.ldx = static_cast<uint32_t>(ldx);
+    b.ldy = static_cast<uint32_t>(n);
+    b.logits = logits;
+    b.ld_logits = static_cast<uint32_t>(ld_logits);
+    b.ids_out = ids_out;
+    b.weights_out = weights_out;
+    const uint32_t units = static_cast<uint32_t>((k + unit_elems(type) - 1) / unit_elems(type));
+    const uint32_t nn = static_cast<uint32_t>(n), kb = static_cast<uint32_t>(k / 32);
+    const uint32_t nv = static_cast<uint32_t>(tokens * routes);
+    switch (type) {
+    case kQ4_K: return launch_routed<kQ4_K>(wg, wu, row_bytes, x, xq, y, yq, nn, units, kb, b, nv, stream);
+    case kQ6_K: return launch_routed<kQ6_K>(wg, wu, row_bytes, x, xq, y, yq, nn, units, kb, b, nv, stream);
+    case kQ8_0: return launch_routed<kQ8_0>(wg, wu, row_bytes, x, xq, y, yq, nn, units, kb, b, nv, stream);
+    default: return launch_routed<kQ5_0>(wg, wu, row_bytes, x, xq, y, yq, nn, units, kb, b, nv, stream);
+    }
 }
 
 int launch_gemv_multi_norm(const GemvJob* jobs, size_t count, const float* x, const float* gamma, float eps, size_t k,

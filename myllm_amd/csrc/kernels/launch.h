@@ -52,6 +52,22 @@ constexpr size_t kMultiJobs = 3;
 // receive the normalised row and its XGroup form.
 int launch_gemv_multi_norm(const GemvJob* jobs, size_t count, const float* x, const float* gamma, float eps, size_t k,
                            float* norm, XGroup* normq, hipStream_t stream);
+// y = residual + (sum_q weights[q] down[q n : (q + 1) n] + sigmoid(sgate[0]) W x)
+// for one token: the shared expert's down projection with the MoE combine in
+// its epilogue; x raw FP32 (XGroup form made in the prologue; quantized
+// weights, k <= 8192).
+int launch_gemv_moe_combine(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* residual,
+                            const float* down, const float* weights, const float* sgate, size_t routes, float* y,
+                            size_t n, size_t k, hipStream_t stream);
+// Expert gate/up + SwiGLU for tokens x routes vectors with the routes picked
+// in the prologue from the router logits (softmax, top-k, renormalisation as
+// launch_router_topk; experts <= 256, routes <= 8): vector t * routes + q
+// multiplies row t of x by expert ids_out[t, q]; ids_out / weights_out
+// receive the routes. Quantized weights.
+int launch_gemv_routed_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
+                              const XGroup* xq, size_t ldx, float* y, XGroup* yq, size_t n, size_t k, size_t tokens,
+                              const float* logits, size_t ld_logits, size_t experts, size_t routes,
+                              size_t expert_stride, int32_t* ids_out, float* weights_out, hipStream_t stream);
 int launch_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row_bytes, const float* x,
                         const XGroup* xq, const float* bias, const float* residual, float* y, XGroup* yq, size_t n,
                         size_t k, size_t vectors, const int32_t* ids, size_t experts, size_t routes,

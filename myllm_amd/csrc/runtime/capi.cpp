@@ -393,6 +393,26 @@ int hipllm_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row
                   "hipllm_gemv_batched: invalid arguments or launch failure");
 }
 
+int hipllm_gemv_routed_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
+                              const void* xq, size_t ldx, float* y, void* yq, size_t n, size_t k, size_t tokens,
+                              const float* logits, size_t ld_logits, size_t experts, size_t routes,
+                              size_t expert_stride, int32_t* ids_out, float* weights_out, void* stream) {
+    return status(hipllm::launch_gemv_routed_swiglu(type, wg, wu, row_bytes, x,
+                                                    static_cast<const hipllm::XGroup*>(xq), ldx, y, xg(yq), n, k,
+                                                    tokens, logits, ld_logits, experts, routes, expert_stride,
+                                                    ids_out, weights_out, as_stream(stream)),
+                  "hipllm_gemv_routed_swiglu: invalid arguments (quantized weights, experts <= 256, routes <= 8) or "
+                  "launch failure");
+}
+
+int hipllm_gemv_moe_combine(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* residual,
+                            const float* down, const float* weights, const float* sgate, size_t routes, float* y,
+                            size_t n, size_t k, void* stream) {
+    return status(hipllm::launch_gemv_moe_combine(type, w, row_bytes, x, residual, down, weights, sgate, routes, y, n,
+                                                  k, as_stream(stream)),
+                  "hipllm_gemv_moe_combine: invalid arguments or launch failure");
+}
+
 int hipllm_router_topk(const float* logits, size_t ld, size_t tokens, size_t experts, size_t k, int32_t* ids,
                        float* weights, void* stream) {
     return status(hipllm::launch_router_topk(logits, ld, tokens, experts, k, ids, weights, as_stream(stream)),

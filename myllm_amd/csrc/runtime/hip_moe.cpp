@@ -758,16 +758,29 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
         proj(L.router, act.norm, act.normq, H, rows, act.rlog, ldr);
         proj(L.shexp_router, act.norm, act.normq, H, rows, act.rlog + E, ldr);
     }
-    launch_check(hipllm::launch_router_topk(act.rlog, ldr, rows, E, K, ids, act.rweight, stream), "router top-k");
+    // With the grouped launch, the expert gate/up picks the routes itself
+    // (every block runs the top-k on the token's logits).
+    const bool route_in_gemv = grp && E <= 256 && K <= 8 && groupable(L.gate_exps, true);
+    if (!route_in_gemv) {
+        launch_check(hipllm::launch_router_topk(act.rlog, ldr, rows, E, K, ids, act.rweight, stream),
+                     "router top-k");
+    }
     const void* xb = bf16_rows(act.norm, H, H, rows);
-    // Routed experts: gate/up + SwiGLU for every (row, route), then down.
-    // The gate/up launches spread rows thinly over many blocks (the expert and
-    // shared widths are small), so the XGroup form of their output comes from
-    // a separate pass rather than their epilogue (which needs 16-row blocks).
-    launch_check(hipllm::launch_gemv_batched(L.gate_exps.type, L.gate_exps.ptr, L.up_exps.ptr, L.gate_exps.row_bytes,
-                                             act.norm, act.normq, nullptr, nullptr, act.act, act.actq, FF, H,
-                                             rows * K, ids, E, K, L.gate_exps.expert_stride, 0, H, FF, stream),
-                 "expert gate/up");
+    // Routed experts: gate/up + SwiGLU (and its XGroup form) for every
+    // (row, route), then down.
+    if (route_in_gemv) {
+        launch_check(hipllm::launch_gemv_routed_swiglu(L.gate_exps.type, L.gate_exps.ptr, L.up_exps.ptr,
+                                                       L.gate_exps.row_bytes, act.norm, act.normq, H, act.act,
+                                                       act.actq, FF, H, rows, act.rlog, ldr, E, K,
+                                                       L.gate_exps.expert_stride, ids, act.rweight, stream),
+                     "router top-k + expert gate/up");
+    } else {
+        launch_check(hipllm::launch_gemv_batched(L.gate_exps.type, L.gate_exps.ptr, L.up_exps.ptr,
+                                                 L.gate_exps.row_bytes, act.norm, act.normq, nullptr, nullptr,
+                                                 act.act, act.actq, FF, H, rows * K, ids, E, K,
+                                                 L.gate_exps.expert_stride, 0, H, FF, stream),
+                     "expert gate/up");
+    }
     launch_check(hipllm::launch_gemv_batched(L.down_exps.type, L.down_exps.ptr, nullptr, L.down_exps.row_bytes,
                                              act.act, act.actq, nullptr, nullptr, act.down, nullptr, H, FF, rows * K,
                                              ids, E, K, L.down_exps.expert_stride, 1, FF, H, stream),
@@ -789,6 +802,14 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
         proj(L.sh_up, act.norm, act.normq, H, rows, act.sh_act, FFs);
         launch_check(hipllm::launch_swiglu(act.sh_down, act.sh_act, act.sh_act, act.sh_actq, rows * FFs, stream),
                      "shared SwiGLU");
+    }
+    if (grp && !next_norm) {
+        // The combine in the shared down projection's epilogue.
+        launch_check(hipllm::launch_gemv_moe_combine(L.sh_down.type, L.sh_down.ptr, L.sh_down.row_bytes, act.sh_act,
+                                                     hidden, act.down, act.rweight, act.rlog + E, K, next, H, FFs,
+                                                     stream),
+                     "shared down + MoE combine");
+        return;
     }
     if (grp) {
         launch_check(hipllm::launch_gemv_norm(L.sh_down.type, L.sh_down.ptr, L.sh_down.row_bytes, act.sh_act, nullptr,

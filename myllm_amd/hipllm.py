@@ -97,6 +97,9 @@ SIGNATURES = {
     "hipllm_moe_combine": (_I, [_P, _P, _P, _P, _P, _S, _P, _S, _S, _S, _P]),
     "hipllm_moe_combine_norm": (_I, [_P, _P, _P, _P, _P, _S, _P, _P, _P, _P, _S, _S, _S, _F, _P]),
     "hipllm_gemv_multi_norm": (_I, [_P, _S, _P, _P, _F, _S, _P, _P, _P]),
+    "hipllm_gemv_routed_swiglu": (_I, [_U32, _P, _P, _S, _P, _P, _S, _P, _P, _S, _S, _S, _P, _S, _S, _S, _S, _P, _P,
+                                       _P]),
+    "hipllm_gemv_moe_combine": (_I, [_U32, _P, _S, _P, _P, _P, _P, _P, _S, _P, _S, _S, _P]),
     "hipllm_gdn_gates": (_I, [_P, _P, _S, _P, _P, _P, _P, _S, _S, _P]),
     "hipllm_conv1d_silu": (_I, [_P, _S, _P, _P, _P, _S, _S, _S, _S, _P]),
     "hipllm_l2norm_heads": (_I, [_P, _S, _S, _S, _S, _F, _P]),
@@ -384,6 +387,18 @@ def _k_gemv_multi_norm(jobs, x, gamma, eps, k, norm=None, normq=None, stream=Non
                                        _stream(stream)))
 
 
+def _k_gemv_routed_swiglu(qtype, wg, wu, row_bytes, x, xq, ldx, y, yq, n, k, tokens, logits, ld_logits, experts,
+                          routes, expert_stride, ids_out, weights_out, stream=None):
+    check(lib().hipllm_gemv_routed_swiglu(qtype, _ptr(wg), _ptr(wu), row_bytes, _ptr(x), _ptr(xq), ldx, _ptr(y),
+                                          _ptr(yq), n, k, tokens, _ptr(logits), ld_logits, experts, routes,
+                                          expert_stride, _ptr(ids_out), _ptr(weights_out), _stream(stream)))
+
+
+def _k_gemv_moe_combine(qtype, w, row_bytes, x, residual, down, weights, sgate, routes, y, n, k, stream=None):
+    check(lib().hipllm_gemv_moe_combine(qtype, _ptr(w), row_bytes, _ptr(x), _ptr(residual), _ptr(down),
+                                        _ptr(weights), _ptr(sgate), routes, _ptr(y), n, k, _stream(stream)))
+
+
 def _k_moe_combine_norm(residual, down, w, shared, sgate, ld_sgate, out, gamma, norm, normq, tokens, h, k, eps,
                         stream=None):
     check(lib().hipllm_moe_combine_norm(_ptr(residual), _ptr(down), _ptr(w), _ptr(shared), _ptr(sgate), ld_sgate,
@@ -476,7 +491,8 @@ kernels = types.SimpleNamespace(
     attn_decode=_k_attn_decode, argmax=_k_argmax, swiglu=_k_swiglu, attn_prefill=_k_attn_prefill,
     gemv_batched=_k_gemv_batched, router_topk=_k_router_topk, moe_combine=_k_moe_combine,
     moe_combine_norm=_k_moe_combine_norm,
-    gemv_multi_norm=_k_gemv_multi_norm, gdn_gates=_k_gdn_gates,
+    gemv_multi_norm=_k_gemv_multi_norm, gemv_routed_swiglu=_k_gemv_routed_swiglu,
+    gemv_moe_combine=_k_gemv_moe_combine, gdn_gates=_k_gdn_gates,
     conv1d_silu=_k_conv1d_silu, l2norm_heads=_k_l2norm_heads, gdn_scan=_k_gdn_scan, gated_rmsnorm=_k_gated_rmsnorm,
     conv_l2norm=_k_conv_l2norm, gdn_scan_gated=_k_gdn_scan_gated,
     split_qgate_norm=_k_split_qgate_norm, gate_mul=_k_gate_mul,

@@ -111,6 +111,102 @@ def test_batched_rows_and_swiglu(cuda, qtype):
 
 
 # ------------------------------------------------------------ DeltaNet pieces
+@pytest.mark.parametrize("qtype,E,K,T,n,kdim", [(synth.Q4_K, 256, 8, 1, 64, 512), (synth.Q8_0, 64, 4, 3, 32, 256),
+                                                 (synth.Q6_K, 16, 2, 2, 48, 256)])
+def test_gemv_routed_swiglu_matches_topk_then_batched(cuda, qtype, E, K, T, n, kdim):
+    """Routing in the expert gate/up prologue against router_topk followed by
+    the batched SwiGLU GEMV with those ids: the same ids and weights bit for
+    bit, outputs within 1e-6 (separately compiled), XGroup form of the output."""
+    rng = np.random.default_rng(31)
+    wg = random_rows(qtype, E * n, kdim, 51)
+    wu = random_rows(qtype, E * n, kdim, 52)
+    dg, du = dev_bytes(wg, cuda), dev_bytes(wu, cuda)
+    rb = wg.shape[1]
+    x = synth.normal(T * kdim, 53).reshape(T, kdim)
+    dx = t32(x, cuda)
+    xs = torch.empty(T, kdim, device=cuda)
+    for t in range(T):
+        kernels.prep_x(dx[t], xs[t], kdim)
+    logits = rng.normal(size=(T, E + 1)).astype(np.float32)
+    logits[0, [3, 7]] = logits[0].max() + 1.0  # a tie at the top of token 0
+    dl = t32(logits, cuda)
+    ids_ref = torch.empty(T, K, dtype=torch.int32, device=cuda)
+    w_ref = torch.empty(T, K, device=cuda)
+    kernels.router_topk(dl, E + 1, T, E, K, ids_ref, w_ref)
+    y_ref = torch.empty(T * K, n, device=cuda)
+    yq_ref = xgroup.buffer(torch, n, cuda, T * K)
+    kernels.gemv_batched(qtype, dg, du, rb, dx, xs, None, None, y_ref, yq_ref, n, kdim, T * K, ids=ids_ref.view(-1),
+                         experts=E, routes=K, expert_stride=n * rb, x_routed=False, ldx=kdim, ldy=n)
+    ids = torch.full((T, K), -1, dtype=torch.int32, device=cuda)
+    wts = torch.empty(T, K, device=cuda)
+    y = torch.empty(T * K, n, device=cuda)
+    yq = xgroup.buffer(torch, n, cuda, T * K)
+    kernels.gemv_routed_swiglu(qtype, dg, du, rb, dx, xs, kdim, y, yq, n, kdim, T, dl, E + 1, E, K, n * rb, ids, wts)
+    assert torch.equal(ids, ids_ref)
+    assert torch.equal(wts.view(torch.int32), w_ref.view(torch.int32))
+    got, ref = y.cpu().numpy(), y_ref.cpu().numpy()
+    assert rel_err(got, ref) <= 1e-6
+    for v in range(T * K):
+        xgroup.check(yq[v * n:(v + 1) * n], got[v])
+
+
+def test_gemv_routed_swiglu_rejects_bad_arguments(cuda):
+    w = torch.zeros(272 * 64, dtype=torch.uint8, device=cuda)
+    x = torch.zeros(256, device=cuda)
+    y = torch.zeros(64, device=cuda)
+    ids = torch.zeros(8, dtype=torch.int32, device=cuda)
+    wts = torch.zeros(8, device=cuda)
+    ok = dict(E=4, K=2, n=16, ld=5)
+
+    def call(qtype=synth.Q8_0, **kw):
+        a = {**ok, **kw}
+        kernels.gemv_routed_swiglu(qtype, w, w, 272, x, x, 256, y, None, a["n"], 256, 1, x, a["ld"], a["E"], a["K"],
+                                   a["n"] * 272, ids, wts)
+
+    call()  # valid: equal logits route to experts 0 and 1 with weight 1/2
+    torch.cuda.synchronize()
+    assert ids[:2].cpu().numpy().tolist() == [0, 1]
+    assert wts[:2].cpu().numpy().tolist() == [0.5, 0.5]
+    with pytest.raises(LengthError):  # one wave holds at most 256 logits
+        call(E=257, ld=257)
+    for bad in (dict(K=9, E=16, ld=16), dict(K=5), dict(ld=3)):
+        with pytest.raises(ValueError):
+            call(**bad)
+    with pytest.raises(ValueError):  # quantized weights only
+        call(qtype=synth.F32)
+
+
+@pytest.mark.parametrize("qtype,H,FFs,K", [(synth.Q8_0, 2048, 512, 8), (synth.Q4_K, 512, 768, 4)])
+def test_gemv_moe_combine_matches_down_then_combine(cuda, qtype, H, FFs, K):
+    """The combine in the shared down projection's epilogue against the down
+    GEMV (same tiling, encode prologue) followed by moe_combine: within 1e-6
+    (separately compiled), and against float64 within 1e-4."""
+    rng = np.random.default_rng(33)
+    wd = random_rows(qtype, H, FFs, 61)
+    dw = dev_bytes(wd, cuda)
+    rb = wd.shape[1]
+    act = synth.normal(FFs, 62, stddev=0.5)
+    res = rng.normal(size=H).astype(np.float32)
+    down = rng.normal(size=(K, H)).astype(np.float32)
+    wts = rng.uniform(size=K).astype(np.float32)
+    wts /= wts.sum()
+    sg = np.array([0.3, 0.0], dtype=np.float32)
+    dact, dres, ddown, dwts, dsg = (t32(a, cuda) for a in (act, res, down, wts, sg))
+    sh = torch.empty(H, device=cuda)
+    kernels.gemv_norm(qtype, dw, rb, dact, None, 0.0, None, None, sh, H, FFs)
+    ref = torch.empty(H, device=cuda)
+    kernels.moe_combine(dres, ddown, dwts, sh, dsg, 1, ref, 1, H, K)
+    out = torch.empty(H, device=cuda)
+    kernels.gemv_moe_combine(qtype, dw, rb, dact, dres, ddown, dwts, dsg, K, out, H, FFs)
+    got = out.cpu().numpy()
+    assert rel_err(got, ref.cpu().numpy()) <= 1e-6
+    wf = torch.empty(H, FFs, device=cuda)
+    kernels.dequant_rows(qtype, dw, rb, H, FFs, wf)
+    shared = wf.double().cpu().numpy() @ act.astype(np.float64)
+    exact = res + wts.astype(np.float64) @ down + moe_ref.sigmoid(np.float64(sg[0])) * shared
+    assert rel_err(got, exact) <= 1e-4
+
+
 def test_gdn_gates(cuda):
     rng = np.random.default_rng(3)
     T, Hv = 4, 32
