@@ -414,6 +414,9 @@ def test_gemv_norm_rejects_bad_arguments(cuda):
         kernels.gemv_norm(synth.F32, w, 1024, x, x, 1e-6, None, None, y, 4, 256)
     with pytest.raises(ValueError):  # unknown norm tiling
         kernels.gemv_norm(synth.Q4_K, w, 144, x, x, 1e-6, None, None, y, 4, 256, 432)
+    for code in (100, 7, 1416):  # malformed codes are rejected before any use
+        with pytest.raises(ValueError):
+            kernels.gemv_norm(synth.Q4_K, w, 144, x, x, 1e-6, None, None, y, 4, 256, code)
 
 
 # ------------------------------------------------------------- small ops
