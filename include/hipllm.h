@@ -262,7 +262,7 @@ int hipllm_gemv_routed_swiglu(uint32_t type, const void* wg, const void* wu, siz
 
 /* The shared expert's down projection with the MoE combine in its epilogue,
  * one token: y = residual + (sum_q weights[q] down[q n : (q + 1) n] +
- * sigmoid(sgate[0]) W x), the operations of hipllm_moe_combine. x is raw FP32
+ * sigmoid(sgate[0]) W x), the operations of hipllm_moe_combine (routes <= 8). x is raw FP32
  * (k <= 8192, 16-byte aligned; its XGroup form is made in the prologue);
  * quantized weights. Replaces the shared-expert down GEVM,
  * metal_expert_weighted_reduce_f32, the shared gate and the FFN residual

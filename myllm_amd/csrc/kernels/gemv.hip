@@ -505,10 +505,24 @@ struct MoeCombine {
     uint32_t routes = 0;
 };
 
+constexpr uint32_t kCombineRoutes = 8;  // routes the epilogue loads at once
+
 __device__ __forceinline__ float combine_row(const MoeCombine& m, const float* residual, float shared, uint32_t r,
                                              uint32_t n) {
+    // Every route's value is loaded before the sum (in route order).
+    float dv[kCombineRoutes], wv[kCombineRoutes];
+#pragma unroll
+    for (uint32_t q = 0; q < kCombineRoutes; ++q) {
+        if (q < m.routes) {
+            dv[q] = m.down[static_cast<size_t>(q) * n + r];
+            wv[q] = m.weights[q];
+        }
+    }
     float acc = 0.0f;
-    for (uint32_t q = 0; q < m.routes; ++q) acc += m.weights[q] * m.down[static_cast<size_t>(q) * n + r];
+#pragma unroll
+    for (uint32_t q = 0; q < kCombineRoutes; ++q) {
+        if (q < m.routes) acc += wv[q] * dv[q];
+    }
     float moe = acc;
     moe += shared * sigmoid_ref(m.sgate[0]);
     return residual[r] + moe;
@@ -1130,7 +1144,9 @@ int launch_gemv_swiglu_norm(uint32_t type, const void* wg, const void* wu, size_
 int launch_gemv_moe_combine(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* residual,
                             const float* down, const float* weights, const float* sgate, size_t routes, float* y,
                             size_t n, size_t k, hipStream_t stream) {
-    if (!y || !residual || !down || !weights || !sgate || routes == 0 || routes > 64) return kInvalidArgument;
+    if (!y || !residual || !down || !weights || !sgate || routes == 0 || routes > kCombineRoutes) {
+        return kInvalidArgument;
+    }
     if (!norm_ok(type, x, nullptr, k, 0.0f)) return kInvalidArgument;
     if (!w || row_bytes < k / block_elems(type) * block_bytes(type) || k % block_elems(type) != 0) {
         return kInvalidArgument;

@@ -479,7 +479,7 @@ def test_rope_kv_bit_exact(cuda, hq, hkv, d, pos0, rows):
     assert np.array_equal(vcache[pos0:], qkv[:, hq * d + kv:])
 
 
-@pytest.mark.parametrize("length", [1, 7, 255, 256, 257, 1000])
+@pytest.mark.parametrize("length", [1, 7, 255, 256, 257, 1000, 4096, 5000])
 @pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (40, 8, 128)])
 def test_attention_decode(cuda, length, hq, hkv, d):
     kv = hkv * d

@@ -207,6 +207,17 @@ def test_gemv_moe_combine_matches_down_then_combine(cuda, qtype, H, FFs, K):
     assert rel_err(got, exact) <= 1e-4
 
 
+def test_gemv_moe_combine_rejects_bad_arguments(cuda):
+    w = torch.zeros(34 * 16 * 64, dtype=torch.uint8, device=cuda)
+    x = torch.zeros(9 * 512, device=cuda)
+    with pytest.raises(ValueError):  # the epilogue holds at most 8 routes
+        kernels.gemv_moe_combine(synth.Q8_0, w, 34 * 16, x, x, x, x, x, 9, x, 64, 512)
+    with pytest.raises(ValueError):  # quantized weights only
+        kernels.gemv_moe_combine(synth.F32, w, 2048, x, x, x, x, x, 8, x, 64, 512)
+    with pytest.raises(ValueError):  # the prologue holds at most 8192 inputs
+        kernels.gemv_moe_combine(synth.Q8_0, w, 34 * 16 * 20, x, x, x, x, x, 8, x, 1, 10240)
+
+
 def test_gdn_gates(cuda):
     rng = np.random.default_rng(3)
     T, Hv = 4, 32
