@@ -234,10 +234,12 @@ def test_gdn_gates(cuda):
     assert rel_err(beta.cpu().numpy(), ref_b) <= 1e-5
 
 
-@pytest.mark.parametrize("ksize", [2, 4])
-def test_conv1d_silu_and_history(cuda, ksize):
+@pytest.mark.parametrize("ksize,T", [(2, 7), (4, 7), (4, 2), (4, 1), (4, 64), (9, 70), (4, 33)])
+def test_conv1d_silu_and_history(cuda, ksize, T):
+    # Prompts shorter than the history (T < ksize - 1 shifts old rows), one
+    # chunk, several chunks with a ragged last one.
     rng = np.random.default_rng(4)
-    T, C = 7, 300
+    C = 300
     x = rng.normal(size=(T, C)).astype(np.float32)
     hist = rng.normal(size=(ksize - 1, C)).astype(np.float32)
     w = rng.normal(size=(C, ksize)).astype(np.float32)
