@@ -200,6 +200,15 @@ int hipllm_attn_decode_rope(const float* qkv, const float* cos_sin, size_t rot, 
                             float* out, void* outq, float* scratch, size_t hq, size_t hkv, size_t d, size_t pos,
                             float scale, void* stream);
 
+/* hipllm_attn_decode_rope with the gated attention's output gate in the merge:
+ * out = attention * sigmoid(gate) per element (gate: hq * d values), outq its
+ * XGroup form. Replaces the decode attention and the sigmoid gate + multiply
+ * of encode_full_attention (moe_llm.mm:2238-2434, the gate 2420-2428;
+ * metal_llm.metal:1186-1197). */
+int hipllm_attn_decode_rope_gated(const float* qkv, const float* cos_sin, size_t rot, float* kcache, float* vcache,
+                                  const float* gate, float* out, void* outq, float* scratch, size_t hq, size_t hkv,
+                                  size_t d, size_t pos, float scale, void* stream);
+
 /* Scratch floats hipllm_attn_decode needs for up to max_len positions. */
 size_t hipllm_attn_decode_scratch_floats(size_t hq, size_t d, size_t max_len);
 

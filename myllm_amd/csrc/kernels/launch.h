@@ -98,9 +98,12 @@ size_t attn_decode_scratch_floats(size_t hq, size_t d, size_t max_len);
 int launch_attn_decode(const float* q, const float* kcache, const float* vcache, float* out, XGroup* outq,
                        float* scratch, size_t hq, size_t hkv, size_t d, size_t len, float scale, hipStream_t stream,
                        const uint32_t* dpos = nullptr, size_t capacity = 0);
+// gate (nullable): out = attention * sigmoid(gate) per element (the gated
+// attention's output gate), and outq its XGroup form.
 int launch_attn_decode_rope(const float* qkv, const float* cos_sin, size_t rot, float* kcache, float* vcache,
                             float* out, XGroup* outq, float* scratch, size_t hq, size_t hkv, size_t d, size_t pos,
-                            float scale, hipStream_t stream, const uint32_t* dpos = nullptr, size_t capacity = 0);
+                            float scale, hipStream_t stream, const uint32_t* dpos = nullptr, size_t capacity = 0,
+                            const float* gate = nullptr);
 size_t argmax_scratch_bytes(size_t n);
 int launch_argmax(const float* x, size_t n, uint32_t* out, void* scratch, hipStream_t stream);
 int launch_swiglu(const float* g, const float* u, float* y, XGroup* yq, size_t n, hipStream_t stream);

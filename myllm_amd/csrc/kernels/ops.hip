@@ -10,6 +10,7 @@
 //   argmax       cpu_llm.cpp:34-48 (first maximum), metal_llm.metal:1544-1644
 #include "formats.h"
 #include "norm.h"
+#include "router.h"
 
 namespace hipllm {
 namespace {
@@ -245,8 +246,11 @@ __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restri
     }
 }
 
+// gate (nullable): the head outputs are multiplied by sigmoid(gate) (the
+// gated attention's output gate, as the separate gate kernel computes it).
 __global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict__ part, float* __restrict__ out,
-                                                         XGroup* __restrict__ outq, uint32_t d, uint32_t nchunks) {
+                                                         XGroup* __restrict__ outq, uint32_t d, uint32_t nchunks,
+                                                         const float* __restrict__ gate) {
     const uint32_t h = blockIdx.x;
     const float* ph = part + static_cast<size_t>(h) * nchunks * (d + 2);
     // nchunks = the number of splits; a split without keys has m = -inf,
@@ -260,7 +264,8 @@ __global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict
     for (uint32_t i = threadIdx.x; i < d; i += blockDim.x) {
         float acc = 0.0f;
         for (uint32_t c = 0; c < nchunks; ++c) acc += ph[c * (d + 2) + 2 + i] * expf(ph[c * (d + 2)] - M);
-        const float v = acc * invL;
+        float v = acc * invL;
+        if (gate) v = v * sigmoid_ref(gate[h * d + i]);
         out[h * d + i] = v;
         vals[i] = v;
     }
@@ -502,7 +507,7 @@ int launch_attn_decode(const float* q, const float* kcache, const float* vcache,
                        static_cast<uint32_t>(hkv), static_cast<uint32_t>(d), static_cast<uint32_t>(len), dpos, scale,
                        splits, nullptr, 0u);
     hipLaunchKernelGGL(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out, outq,
-                       static_cast<uint32_t>(d), splits);
+                       static_cast<uint32_t>(d), splits, nullptr);
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
@@ -510,7 +515,8 @@ int launch_attn_decode(const float* q, const float* kcache, const float* vcache,
 // raw [Q | K | V] row, the position is pos (len = pos + 1) or *dpos.
 int launch_attn_decode_rope(const float* qkv, const float* cos_sin, size_t rot, float* kcache, float* vcache,
                             float* out, XGroup* outq, float* scratch, size_t hq, size_t hkv, size_t d, size_t pos,
-                            float scale, hipStream_t stream, const uint32_t* dpos, size_t capacity) {
+                            float scale, hipStream_t stream, const uint32_t* dpos, size_t capacity,
+                            const float* gate) {
     if (!qkv || !cos_sin || !kcache || !vcache || !out || !scratch || hq == 0 || hkv == 0 || hq % hkv) {
         return kInvalidArgument;
     }
@@ -524,7 +530,7 @@ int launch_attn_decode_rope(const float* qkv, const float* cos_sin, size_t rot, 
                        static_cast<uint32_t>(d), static_cast<uint32_t>(pos + 1), dpos, scale, splits,
                        reinterpret_cast<const float2*>(cos_sin), static_cast<uint32_t>(rot / 2));
     hipLaunchKernelGGL(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out, outq,
-                       static_cast<uint32_t>(d), splits);
+                       static_cast<uint32_t>(d), splits, gate);
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 

@@ -208,6 +208,15 @@ int hipllm_attn_decode_rope(const float* qkv, const float* cos_sin, size_t rot, 
                   "hipllm_attn_decode_rope: invalid arguments or launch failure");
 }
 
+int hipllm_attn_decode_rope_gated(const float* qkv, const float* cos_sin, size_t rot, float* kcache, float* vcache,
+                                  const float* gate, float* out, void* outq, float* scratch, size_t hq, size_t hkv,
+                                  size_t d, size_t pos, float scale, void* stream) {
+    if (!gate) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_attn_decode_rope_gated: gate is required");
+    return status(hipllm::launch_attn_decode_rope(qkv, cos_sin, rot, kcache, vcache, out, xg(outq), scratch, hq, hkv,
+                                                  d, pos, scale, as_stream(stream), nullptr, 0, gate),
+                  "hipllm_attn_decode_rope_gated: invalid arguments or launch failure");
+}
+
 size_t hipllm_attn_decode_scratch_floats(size_t hq, size_t d, size_t max_len) {
     return hipllm::attn_decode_scratch_floats(hq, d, max_len);
 }

@@ -647,11 +647,12 @@ void HipMoeLLM::Impl::attention_layer(std::size_t li, std::size_t rows, std::siz
                  "Q/gate split + head norms");
     const float scale = 1.0f / std::sqrt(static_cast<float>(D));
     if (rows == 1) {
-        // RoPE of Q and K, the KV-cache write and the attention fused.
+        // RoPE of Q and K, the KV-cache write, the attention and its output
+        // gate fused.
         launch_check(hipllm::launch_attn_decode_rope(act.wide2, rope_table, config.rotary_dimension, L.kcache,
-                                                     L.vcache, act.feat2, nullptr, act.attn_scratch, Hq, Hkv, D, pos0,
-                                                     scale, stream, dpos, capacity),
-                     "RoPE/KV write + attention");
+                                                     L.vcache, act.gated, act.gatedq, act.attn_scratch, Hq, Hkv, D,
+                                                     pos0, scale, stream, dpos, capacity, act.feat),
+                     "RoPE/KV write + attention + output gate");
     } else {
         launch_check(hipllm::launch_rope_kv(act.wide2, rope_table, config.rotary_dimension, Hq, Hkv, D, pos0, rows,
                                             ldqkv, L.kcache, L.vcache, stream, dpos),
@@ -660,8 +661,10 @@ void HipMoeLLM::Impl::attention_layer(std::size_t li, std::size_t rows, std::siz
                                                  D, pos0, scale, stream),
                      "prefill attention");
     }
-    launch_check(hipllm::launch_gate_mul(act.feat2, act.feat, act.gated, act.gatedq, rows * q_w, stream),
-                 "attention output gate");
+    if (rows != 1) {
+        launch_check(hipllm::launch_gate_mul(act.feat2, act.feat, act.gated, act.gatedq, rows * q_w, stream),
+                     "attention output gate");
+    }
     proj_out_norm(L.o, act.gated, act.gatedq, q_w, rows, next, hidden, L.post_norm, !grouped_moe(L, rows));
 }
 

@@ -97,6 +97,7 @@ SIGNATURES = {
     "hipllm_moe_combine": (_I, [_P, _P, _P, _P, _P, _S, _P, _S, _S, _S, _P]),
     "hipllm_moe_combine_norm": (_I, [_P, _P, _P, _P, _P, _S, _P, _P, _P, _P, _S, _S, _S, _F, _P]),
     "hipllm_gemv_multi_norm": (_I, [_P, _S, _P, _P, _F, _S, _P, _P, _P]),
+    "hipllm_attn_decode_rope_gated": (_I, [_P, _P, _S, _P, _P, _P, _P, _P, _P, _S, _S, _S, _S, _F, _P]),
     "hipllm_gemv_routed_swiglu": (_I, [_U32, _P, _P, _S, _P, _P, _S, _P, _P, _S, _S, _S, _P, _S, _S, _S, _S, _P, _P,
                                        _P]),
     "hipllm_gemv_moe_combine": (_I, [_U32, _P, _S, _P, _P, _P, _P, _P, _S, _P, _S, _S, _P]),
@@ -471,6 +472,13 @@ def _k_rope_kv(qkv, cos_sin, rot, hq, hkv, d, pos0, rows, row_stride, kcache, vc
                                _ptr(vcache), _stream(stream)))
 
 
+def _k_attn_decode_rope_gated(qkv, cos_sin, rot, kcache, vcache, gate, out, outq, scratch, hq, hkv, d, pos, scale,
+                              stream=None):
+    check(lib().hipllm_attn_decode_rope_gated(_ptr(qkv), _ptr(cos_sin), rot, _ptr(kcache), _ptr(vcache), _ptr(gate),
+                                              _ptr(out), _ptr(outq), _ptr(scratch), hq, hkv, d, pos, scale,
+                                              _stream(stream)))
+
+
 def _k_attn_decode(q, kcache, vcache, out, outq, scratch, hq, hkv, d, length, scale, stream=None):
     check(lib().hipllm_attn_decode(_ptr(q), _ptr(kcache), _ptr(vcache), _ptr(out), _ptr(outq), _ptr(scratch),
                                    hq, hkv, d, length, scale, _stream(stream)))
@@ -488,7 +496,8 @@ kernels = types.SimpleNamespace(
     dequant_rows=_k_dequant_rows, prep_x=_k_prep_x, gemv=_k_gemv, gemv_prepped=_k_gemv_prepped,
     gemv_swiglu=_k_gemv_swiglu, gemv_norm=_k_gemv_norm, gemv_swiglu_norm=_k_gemv_swiglu_norm, to_bf16=_k_to_bf16, gemm_mfma=_k_gemm_mfma, gemm=_k_gemm,
     gemm_workspace_bytes=lambda m, k: lib().hipllm_gemm_workspace_bytes(m, k), rmsnorm=_k_rmsnorm, embed=_k_embed, rope_kv=_k_rope_kv,
-    attn_decode=_k_attn_decode, argmax=_k_argmax, swiglu=_k_swiglu, attn_prefill=_k_attn_prefill,
+    attn_decode=_k_attn_decode, attn_decode_rope_gated=_k_attn_decode_rope_gated, argmax=_k_argmax,
+    swiglu=_k_swiglu, attn_prefill=_k_attn_prefill,
     gemv_batched=_k_gemv_batched, router_topk=_k_router_topk, moe_combine=_k_moe_combine,
     moe_combine_norm=_k_moe_combine_norm,
     gemv_multi_norm=_k_gemv_multi_norm, gemv_routed_swiglu=_k_gemv_routed_swiglu,

@@ -543,6 +543,44 @@ def test_attention_decode_rope_matches_two_steps(cuda, hq, hkv, d, rot, pos):
     assert not np.array_equal(k2[pos], kc0[pos])
 
 
+@pytest.mark.parametrize("hq,hkv,d,rot,pos", [(16, 2, 256, 64, 70), (16, 2, 256, 64, 0), (14, 2, 64, 64, 130)])
+def test_attention_decode_rope_gated_matches_gate_kernel(cuda, hq, hkv, d, rot, pos):
+    # The output gate in the merge against the fused step followed by the
+    # gate kernel (gate_mul): same bits for the gated output and its XGroup
+    # form.
+    rng = np.random.default_rng(pos + 3 * d)
+    kv = hkv * d
+    cap = pos + 3
+    stride = (hq + 2 * hkv) * d
+    qkv = rng.normal(size=stride).astype(np.float32)
+    gate = (rng.normal(size=hq * d) * 3.0).astype(np.float32)
+    ang = rng.uniform(-3.0, 3.0, size=(cap, rot // 2)).astype(np.float32)
+    table = np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)
+    kc0 = rng.normal(size=(cap, kv)).astype(np.float32)
+    vc0 = rng.normal(size=(cap, kv)).astype(np.float32)
+    dtab = torch.from_numpy(table).to(cuda)
+    dgate = torch.from_numpy(gate).to(cuda)
+    scale = float(np.float32(1.0) / np.float32(math.sqrt(d)))
+    outs = []
+    for fused in (False, True):
+        dq = torch.from_numpy(qkv.copy()).to(cuda)
+        kc = torch.from_numpy(kc0.copy()).to(cuda)
+        vc = torch.from_numpy(vc0.copy()).to(cuda)
+        out = torch.empty(hq * d, dtype=torch.float32, device=cuda)
+        outq = xgroup.buffer(torch, hq * d, cuda)
+        scratch = torch.empty(kernels.attn_decode_scratch_floats(hq, d, pos + 1), dtype=torch.float32, device=cuda)
+        if fused:
+            kernels.attn_decode_rope_gated(dq, dtab, rot, kc, vc, dgate, out, outq, scratch, hq, hkv, d, pos, scale)
+        else:
+            att = torch.empty(hq * d, dtype=torch.float32, device=cuda)
+            kernels.attn_decode_rope(dq, dtab, rot, kc, vc, att, None, scratch, hq, hkv, d, pos, scale)
+            kernels.gate_mul(att, dgate, out, outq, hq * d)
+        outs.append((out.cpu().numpy(), outq.cpu().numpy()))
+    (o1, q1), (o2, q2) = outs
+    assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32))
+    assert np.array_equal(q1.view(np.uint32), q2.view(np.uint32))
+
+
 @pytest.mark.parametrize("n", [1, 100, 2048, 2049, 151936])
 def test_argmax(cuda, n):
     x = synth.normal(n, 71 + n)
