@@ -126,12 +126,18 @@ constexpr uint32_t kAttnMaxSplits = 16;
 // rotate that key head, write it and the value head into the caches at row
 // len - 1, then synchronise before reading them. Every head of a KV group
 // writes the same values there, so the duplicate writes agree.
+//
+// With one split (short capacities) the block finishes the head itself: out,
+// outq (nullable) and the optional sigmoid gate exactly as the merge computes
+// them for a single split (weight exp(0) = 1), so no merge launch follows.
 __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restrict__ q, float* __restrict__ kcache,
                                                            float* __restrict__ vcache, float* __restrict__ part,
                                                            uint32_t hq, uint32_t hkv, uint32_t d, uint32_t len_arg,
                                                            const uint32_t* __restrict__ dpos, float scale,
                                                            uint32_t splits, const float2* __restrict__ rope,
-                                                           uint32_t half_rot) {
+                                                           uint32_t half_rot, float* __restrict__ fout,
+                                                           XGroup* __restrict__ foutq,
+                                                           const float* __restrict__ gate) {
     const uint32_t h = blockIdx.x;
     const uint32_t split = blockIdx.y;
     const uint32_t len = dpos ? *dpos + 1 : len_arg;
@@ -223,9 +229,39 @@ __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restri
         }
         __syncthreads();  // ps[] and red[] are rewritten by the next chunk
     }
-    float* out = part + (static_cast<size_t>(h) * splits + split) * (d + 2);
     if (pv) accp[tid] = acc;
     __syncthreads();
+    if (splits == 1) {
+        __shared__ __align__(16) float vals[256];
+        const float invL = 1.0f / l_run;
+        for (uint32_t cc = tid; cc < d4; cc += blockDim.x) {
+            float4 a = accp[cc];
+            for (uint32_t k = 1; k < parts; ++k) {
+                const float4 b = accp[k * d4 + cc];
+                a.x += b.x;
+                a.y += b.y;
+                a.z += b.z;
+                a.w += b.w;
+            }
+            const float av[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+                const uint32_t i = 4 * cc + j;
+                float v = av[j] * invL;
+                if (gate) v = v * sigmoid_ref(gate[h * d + i]);
+                fout[h * d + i] = v;
+                vals[i] = v;
+            }
+        }
+        if (foutq) {
+            __syncthreads();
+            for (uint32_t gI = tid; gI < d / 16; gI += blockDim.x) {
+                xgroup_encode_from(vals + 16 * gI, foutq + h * (d / 16) + gI);
+            }
+        }
+        return;
+    }
+    float* out = part + (static_cast<size_t>(h) * splits + split) * (d + 2);
     for (uint32_t cc = tid; cc < d4; cc += blockDim.x) {
         float4 a = accp[cc];
         for (uint32_t k = 1; k < parts; ++k) {
@@ -478,14 +514,21 @@ int launch_rope_kv(float* qkv, const float* cos_sin, size_t rot, size_t hq, size
 }
 
 namespace {
-uint32_t attn_splits(size_t max_len) {
+// Up to two chunks (one for heads of more than 128 dims) one block per head
+// walks them all and writes the output (no merge launch): 28 heads of 128 at
+// one chunk 5.5 us against 7.6 with the merge, at two 7.7 against 8.3, but
+// each further chunk in turn costs about 2.5 us (11.4 against 8.8 at four),
+// and heads of 256 at two chunks measured 10.9 against 9.5. Beyond, one
+// split per chunk up to 16.
+uint32_t attn_splits(size_t max_len, size_t d) {
     const size_t chunks = (max_len + kAttnChunk - 1) / kAttnChunk;
-    return static_cast<uint32_t>(chunks < kAttnMaxSplits ? (chunks ? chunks : 1) : kAttnMaxSplits);
+    if (chunks <= (d > 128 ? 1u : 2u)) return 1;
+    return static_cast<uint32_t>(chunks < kAttnMaxSplits ? chunks : kAttnMaxSplits);
 }
 }  // namespace
 
 size_t attn_decode_scratch_floats(size_t hq, size_t d, size_t max_len) {
-    return hq * attn_splits(max_len) * (d + 2);
+    return hq * attn_splits(max_len, d) * (d + 2);
 }
 
 // len > 0 keys, or (dpos != nullptr) len = *dpos + 1 read on the device with
@@ -500,14 +543,16 @@ int launch_attn_decode(const float* q, const float* kcache, const float* vcache,
     if (d == 0 || d > 256 || d % 16 != 0) return kInvalidArgument;
     if (outq && reinterpret_cast<uintptr_t>(outq) % 16 != 0) return kInvalidArgument;
     if (len > 0xffffffffull || capacity > 0xffffffffull || hq > 0xffffull) return kLengthError;
-    const uint32_t splits = attn_splits(dpos ? capacity : len);
+    const uint32_t splits = attn_splits(dpos ? capacity : len, d);
     // Read-only use of the caches (no RoPE table): the kernel writes them only in the fused form.
     hipLaunchKernelGGL(attn_decode_partial, dim3(static_cast<uint32_t>(hq), splits), dim3(256), 0, stream, q,
                        const_cast<float*>(kcache), const_cast<float*>(vcache), scratch, static_cast<uint32_t>(hq),
                        static_cast<uint32_t>(hkv), static_cast<uint32_t>(d), static_cast<uint32_t>(len), dpos, scale,
-                       splits, nullptr, 0u);
-    hipLaunchKernelGGL(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out, outq,
-                       static_cast<uint32_t>(d), splits, nullptr);
+                       splits, nullptr, 0u, out, outq, nullptr);
+    if (splits > 1) {
+        hipLaunchKernelGGL(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out,
+                           outq, static_cast<uint32_t>(d), splits, nullptr);
+    }
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
@@ -524,13 +569,15 @@ int launch_attn_decode_rope(const float* qkv, const float* cos_sin, size_t rot, 
     if (d == 0 || d > 256 || d % 16 != 0 || rot == 0 || rot % 2 != 0 || rot > d) return kInvalidArgument;
     if (outq && reinterpret_cast<uintptr_t>(outq) % 16 != 0) return kInvalidArgument;
     if (pos >= 0xffffffffull || capacity > 0xffffffffull || hq > 0xffffull) return kLengthError;
-    const uint32_t splits = attn_splits(dpos ? capacity : pos + 1);
+    const uint32_t splits = attn_splits(dpos ? capacity : pos + 1, d);
     hipLaunchKernelGGL(attn_decode_partial, dim3(static_cast<uint32_t>(hq), splits), dim3(256), 0, stream, qkv,
                        kcache, vcache, scratch, static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv),
                        static_cast<uint32_t>(d), static_cast<uint32_t>(pos + 1), dpos, scale, splits,
-                       reinterpret_cast<const float2*>(cos_sin), static_cast<uint32_t>(rot / 2));
-    hipLaunchKernelGGL(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out, outq,
-                       static_cast<uint32_t>(d), splits, gate);
+                       reinterpret_cast<const float2*>(cos_sin), static_cast<uint32_t>(rot / 2), out, outq, gate);
+    if (splits > 1) {
+        hipLaunchKernelGGL(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out,
+                           outq, static_cast<uint32_t>(d), splits, gate);
+    }
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
