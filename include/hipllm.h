@@ -280,6 +280,28 @@ int hipllm_gemv_moe_combine(uint32_t type, const void* w, size_t row_bytes, cons
                             const float* down, const float* weights, const float* sgate, size_t routes, float* y,
                             size_t n, size_t k, void* stream);
 
+/* Routed vectors grouped by expert, for the expert products of several rows:
+ * order = 0..n-1 stably sorted by ids (each clamped to experts - 1); groups =
+ * pairs {first index into order, expert | count << 16} of at most vmax vectors
+ * of one expert; *ngroups = their count, at most
+ * hipllm_route_groups_max(n, experts, vmax). n <= 16384, experts <= 1024. No
+ * counterpart kernel in the reference, which runs one GEMM per route. */
+size_t hipllm_route_groups_max(size_t n, size_t experts, size_t vmax);
+int hipllm_route_groups(const int32_t* ids, size_t n, size_t experts, size_t vmax, int32_t* order, int32_t* groups,
+                        uint32_t* ngroups, void* stream);
+
+/* Routed expert products of several rows as the bf16 MFMA matmul
+ * (hipllm_gemm_mfma's tile 1): one block row per group of
+ * hipllm_route_groups (vmax <= 64), each reading its expert's weight tile
+ * once for all of the group's vectors: y[j, :n] = W_e x_j for every routed
+ * vector j, x_j = row j / routes of xb (bf16, k values per row) or row j when
+ * x_routed; max_groups launch rows (those past *ngroups exit). Replaces the
+ * per-route expert GEMMs of encode_selected_moe for a prompt
+ * (moe_llm.mm:2692-2790; metal_llm.metal:1476-1521). */
+int hipllm_gemm_gather(uint32_t type, const void* w, size_t row_bytes, const void* xb, float* y, size_t n, size_t k,
+                       size_t ldy, const int32_t* order, const int32_t* groups, const uint32_t* ngroups,
+                       size_t max_groups, size_t expert_stride, size_t routes, int x_routed, void* stream);
+
 /* Per token: softmax over `experts` logits, top-k insertion (strict '>', the
  * lower id wins ties), renormalised weights. Replaces the router tail of
  * encode_routes (moe_llm.mm:2642-2690): metal_softmax_f32, metal_topk_f32,

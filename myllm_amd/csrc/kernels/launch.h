@@ -68,6 +68,22 @@ int launch_gemv_routed_swiglu(uint32_t type, const void* wg, const void* wu, siz
                               const XGroup* xq, size_t ldx, float* y, XGroup* yq, size_t n, size_t k, size_t tokens,
                               const float* logits, size_t ld_logits, size_t experts, size_t routes,
                               size_t expert_stride, int32_t* ids_out, float* weights_out, hipStream_t stream);
+// Routed vectors grouped by expert for the several-row expert products:
+// order = 0..n-1 stably sorted by ids (each clamped to experts - 1); groups =
+// pairs {first index into order, expert | count << 16}, at most vmax vectors
+// of one expert each; *ngroups = the group count, at most
+// route_groups_max(n, experts, vmax). n <= 16384, experts <= 1024.
+size_t route_groups_max(size_t n, size_t experts, size_t vmax);
+int launch_route_groups(const int32_t* ids, size_t n, size_t experts, size_t vmax, int32_t* order, int32_t* groups,
+                        uint32_t* ngroups, hipStream_t stream);
+// Expert products of several rows as the bf16 MFMA matmul, one block row per
+// expert group (groups of at most kGatherRows vectors): y[j, :n] = W_e x_j
+// for every routed vector j of the groups, x_j = row j / routes of xb (bf16)
+// or row j when x_routed; max_groups launch rows (those past *ngroups exit).
+constexpr size_t kGatherRows = 64;
+int launch_gemm_gather(uint32_t type, const void* w, size_t row_bytes, const void* xb, float* y, size_t n, size_t k,
+                       size_t ldy, const int32_t* order, const int32_t* groups, const uint32_t* ngroups,
+                       size_t max_groups, size_t expert_stride, size_t routes, int x_routed, hipStream_t stream);
 int launch_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row_bytes, const float* x,
                         const XGroup* xq, const float* bias, const float* residual, float* y, XGroup* yq, size_t n,
                         size_t k, size_t vectors, const int32_t* ids, size_t experts, size_t routes,

@@ -20,6 +20,7 @@
 // written once per call however many tokens it scans; norms run one 64-lane
 // wave per head vector; everything else is one pass over its rows.
 #include "common.h"
+#include "launch.h"
 #include "norm.h"
 #include "router.h"
 
@@ -38,6 +39,59 @@ __global__ __launch_bounds__(64) void router_topk_kernel(const float* __restrict
                                                          float* __restrict__ weights) {
     const size_t t = blockIdx.x;
     topk_row<PL>(logits + t * ld, experts, k, ids + t * k, weights + t * k, threadIdx.x);
+}
+
+// ------------------------------------------------------------ route groups
+// Stable counting sort of n routed vectors by expert in one block, then the
+// expert groups of at most vmax vectors: the ids in LDS; thread e counts
+// expert e's vectors; one thread turns the counts into offsets (vectors and
+// groups); thread e lists its vectors in increasing index and writes its
+// groups. O(experts * n) LDS reads: a few microseconds at prompt sizes.
+constexpr uint32_t kRouteGroupsMax = 16384;
+
+__global__ __launch_bounds__(1024) void route_groups_kernel(const int32_t* __restrict__ ids, uint32_t n,
+                                                            uint32_t experts, uint32_t vmax,
+                                                            int32_t* __restrict__ order,
+                                                            int32_t* __restrict__ groups,
+                                                            uint32_t* __restrict__ ngroups) {
+    __shared__ uint16_t sid[kRouteGroupsMax];
+    __shared__ uint32_t off[kMaxExperts];
+    __shared__ uint32_t goff[kMaxExperts];
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        sid[i] = static_cast<uint16_t>(min(static_cast<uint32_t>(ids[i]), experts - 1));
+    }
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
+        uint32_t c = 0;
+        for (uint32_t i = 0; i < n; ++i) c += sid[i] == e;
+        off[e] = c;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t run = 0, grun = 0;
+        for (uint32_t e = 0; e < experts; ++e) {
+            const uint32_t c = off[e];
+            off[e] = run;
+            goff[e] = grun;
+            run += c;
+            grun += (c + vmax - 1) / vmax;
+        }
+        *ngroups = grun;
+    }
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
+        const uint32_t start = off[e];
+        uint32_t o = start;
+        for (uint32_t i = 0; i < n; ++i) {
+            if (sid[i] == e) order[o++] = static_cast<int32_t>(i);
+        }
+        const uint32_t c = o - start;
+        for (uint32_t q = 0; q * vmax < c; ++q) {
+            const uint32_t gq = goff[e] + q;
+            groups[2 * gq] = static_cast<int32_t>(start + q * vmax);
+            groups[2 * gq + 1] = static_cast<int32_t>(e | (min(vmax, c - q * vmax) << 16));
+        }
+    }
 }
 
 // ------------------------------------------------------------ MoE combine
@@ -504,6 +558,19 @@ int launch_router_topk(const float* logits, size_t ld, size_t tokens, size_t exp
     hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(tokens)), dim3(64), 0, stream, logits,
                        static_cast<uint32_t>(ld), static_cast<uint32_t>(experts), static_cast<uint32_t>(k), ids,
                        weights);
+    return launched();
+}
+
+size_t route_groups_max(size_t n, size_t experts, size_t vmax) {
+    return vmax == 0 ? 0 : (n + vmax - 1) / vmax + (experts < n ? experts : n);
+}
+
+int launch_route_groups(const int32_t* ids, size_t n, size_t experts, size_t vmax, int32_t* order, int32_t* groups,
+                        uint32_t* ngroups, hipStream_t stream) {
+    if (!ids || !order || !groups || !ngroups || n == 0 || experts == 0 || vmax == 0) return kInvalidArgument;
+    if (n > kRouteGroupsMax || experts > kMaxExperts || vmax > 0xffffu) return kLengthError;
+    hipLaunchKernelGGL(route_groups_kernel, dim3(1), dim3(1024), 0, stream, ids, static_cast<uint32_t>(n),
+                       static_cast<uint32_t>(experts), static_cast<uint32_t>(vmax), order, groups, ngroups);
     return launched();
 }
 

@@ -359,12 +359,26 @@ __device__ __forceinline__ void block_tile(uint32_t nbs, uint32_t mbs, uint32_t&
     nb = in / gsize;
 }
 
-template <uint32_t T, int NSUB, int MSUB>
+// Gathered form (routed expert products): block (weight tile x, group y)
+// multiplies the rows of expert group y (launch_route_groups: at most 64
+// routed vectors of one expert) by that expert's weights, gathering each
+// vector's X row (row j / routes of xb, or row j when x_routed) and writing
+// row j of y. Groups past *ngroups exit at once.
+struct Gather {
+    const int32_t* order = nullptr;
+    const int32_t* groups = nullptr;
+    const uint32_t* ngroups = nullptr;
+    size_t expert_stride = 0;
+    uint32_t routes = 1;
+    uint32_t x_routed = 0;
+};
+
+template <uint32_t T, int NSUB, int MSUB, bool GATHER = false>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restrict__ w, size_t row_bytes,
                                                         const __bf16* __restrict__ xb, const float* __restrict__ bias,
                                                         const float* __restrict__ residual, float* __restrict__ y,
                                                         uint32_t m, uint32_t n, uint32_t k, uint32_t ldy,
-                                                        uint32_t steps_per_split) {
+                                                        uint32_t steps_per_split, const Gather gather = Gather()) {
     using WT = WTile<T>;
     constexpr int BM = 32 * MSUB;
     constexpr int WN = 32 * NSUB;
@@ -376,7 +390,20 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
     const uint32_t wave = tid >> 6, lane = tid & 63;
     const uint32_t lr = lane & 31, h = lane >> 5;
     uint32_t nb, mb;
-    block_tile((n + BN - 1) / BN, (m + BM - 1) / BM, nb, mb);
+    uint32_t gfirst = 0;  // GATHER: the group's first index into gather.order
+    if constexpr (GATHER) {
+        if (blockIdx.y >= *gather.ngroups) return;
+        gfirst = static_cast<uint32_t>(gather.groups[2 * blockIdx.y]);
+        const uint32_t packed = static_cast<uint32_t>(gather.groups[2 * blockIdx.y + 1]);
+        w += static_cast<size_t>(packed & 0xffffu) * gather.expert_stride;
+        m = packed >> 16;  // the group's rows
+        nb = blockIdx.x;
+        mb = 0;
+    } else {
+        block_tile((n + BN - 1) / BN, (m + BM - 1) / BM, nb, mb);
+    }
+    // GATHER: local row r is routed vector gather.order[gfirst + r].
+    auto vec = [&](uint32_t r) { return static_cast<uint32_t>(gather.order[gfirst + r]); };
     const uint32_t m0 = mb * BM;
     const uint32_t n0 = nb * BN + wave * WN;
 
@@ -396,7 +423,9 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
             const uint32_t row = tid / 16 + 16 * i;
             const uint32_t gm = m0 + row;
             if (gm < m) {
-                xr[i] = *reinterpret_cast<const uint4*>(xb + static_cast<size_t>(gm) * k + kb + 8 * (tid % 16));
+                size_t src = gm;
+                if constexpr (GATHER) src = gather.x_routed ? vec(gm) : vec(gm) / gather.routes;
+                xr[i] = *reinterpret_cast<const uint4*>(xb + src * k + kb + 8 * (tid % 16));
             } else {
                 xr[i] = make_uint4(0, 0, 0, 0);
             }
@@ -473,7 +502,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
                 for (int r = 0; r < 4; ++r) {
                     const uint32_t row = m0 + 32 * ms + 8 * g + 4 * h + r;
                     if (row < m) {
-                        const size_t o = static_cast<size_t>(row) * ldy + col;
+                        const size_t o = static_cast<size_t>(GATHER ? vec(row) : row) * ldy + col;
                         if (split) {
                             unsafeAtomicAdd(y + o, acc[ns][ms][4 * g + r]);
                         } else {
@@ -697,6 +726,17 @@ void launch_tile(const void* w, size_t row_bytes, const __bf16* xb, const float*
                        static_cast<const uint8_t*>(w), row_bytes, xb, bias, residual, y, m, n, k, ldy, per);
 }
 
+// The gathered expert products: tile 1 (64 rows x 128 weight rows per
+// block, matching groups of at most 64 vectors), no K split.
+template <uint32_t T>
+void launch_gather(const void* w, size_t row_bytes, const __bf16* xb, float* y, uint32_t n, uint32_t k, uint32_t ldy,
+                   uint32_t max_groups, const Gather& g, hipStream_t stream) {
+    constexpr uint32_t BN = 4 * 32;
+    const dim3 grid((n + BN - 1) / BN, max_groups, 1);
+    hipLaunchKernelGGL((gemm_mfma_kernel<T, 1, 2, true>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w),
+                       row_bytes, xb, nullptr, nullptr, y, 0u, n, k, ldy, k / kStepK, g);
+}
+
 template <uint32_t T, int MT>
 void launch_lds(const void* w, size_t row_bytes, const __bf16* xb, const float* bias, const float* residual, float* y,
                 uint32_t m, uint32_t n, uint32_t k, uint32_t ldy, uint32_t splits, hipStream_t stream) {
@@ -801,6 +841,53 @@ int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void*
     case kF16: return launch_typed<kF16>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
     default: return kInvalidArgument;
     }
+}
+
+int launch_gemm_gather(uint32_t type, const void* w, size_t row_bytes, const void* xb, float* y, size_t n, size_t k,
+                       size_t ldy, const int32_t* order, const int32_t* groups, const uint32_t* ngroups,
+                       size_t max_groups, size_t expert_stride, size_t routes, int x_routed, hipStream_t stream) {
+    if (!w || !xb || !y || !order || !groups || !ngroups || n == 0 || k == 0 || max_groups == 0 || routes == 0 ||
+        ldy < n) {
+        return kInvalidArgument;
+    }
+    if (k % kStepK != 0) return kInvalidArgument;
+    if (n > 0x7fffffffull || k > 0x7fffffffull || ldy > 0x7fffffffull || max_groups > 65535 ||
+        routes > 0xffffffffull) {
+        return kLengthError;
+    }
+    if (type != kF32 && type != kF16 && type != kQ5_0 && type != kQ8_0 && type != kQ4_K && type != kQ6_K) {
+        return kInvalidArgument;
+    }
+    if (row_bytes < k / block_elems(type) * block_bytes(type) || expert_stride < n * row_bytes) {
+        return kInvalidArgument;
+    }
+    if (reinterpret_cast<uintptr_t>(w) % 2 != 0 || row_bytes % 2 != 0 || expert_stride % 2 != 0) {
+        return kInvalidArgument;
+    }
+    if ((type == kQ4_K || type == kF32 || type == kF16) &&
+        (reinterpret_cast<uintptr_t>(w) % 4 != 0 || row_bytes % 4 != 0 || expert_stride % 4 != 0)) {
+        return kInvalidArgument;
+    }
+    if (reinterpret_cast<uintptr_t>(xb) % 16 != 0) return kInvalidArgument;
+    Gather g;
+    g.order = order;
+    g.groups = groups;
+    g.ngroups = ngroups;
+    g.expert_stride = expert_stride;
+    g.routes = static_cast<uint32_t>(routes);
+    g.x_routed = x_routed ? 1u : 0u;
+    const auto* x = static_cast<const __bf16*>(xb);
+    const uint32_t N = static_cast<uint32_t>(n), K = static_cast<uint32_t>(k), L = static_cast<uint32_t>(ldy);
+    const uint32_t G = static_cast<uint32_t>(max_groups);
+    switch (type) {
+    case kQ4_K: launch_gather<kQ4_K>(w, row_bytes, x, y, N, K, L, G, g, stream); break;
+    case kQ6_K: launch_gather<kQ6_K>(w, row_bytes, x, y, N, K, L, G, g, stream); break;
+    case kQ8_0: launch_gather<kQ8_0>(w, row_bytes, x, y, N, K, L, G, g, stream); break;
+    case kQ5_0: launch_gather<kQ5_0>(w, row_bytes, x, y, N, K, L, G, g, stream); break;
+    case kF32: launch_gather<kF32>(w, row_bytes, x, y, N, K, L, G, g, stream); break;
+    default: launch_gather<kF16>(w, row_bytes, x, y, N, K, L, G, g, stream); break;
+    }
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
 }  // namespace hipllm

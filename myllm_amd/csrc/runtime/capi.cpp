@@ -422,6 +422,25 @@ int hipllm_gemv_moe_combine(uint32_t type, const void* w, size_t row_bytes, cons
                   "hipllm_gemv_moe_combine: invalid arguments or launch failure");
 }
 
+size_t hipllm_route_groups_max(size_t n, size_t experts, size_t vmax) {
+    return hipllm::route_groups_max(n, experts, vmax);
+}
+
+int hipllm_route_groups(const int32_t* ids, size_t n, size_t experts, size_t vmax, int32_t* order, int32_t* groups,
+                        uint32_t* ngroups, void* stream) {
+    return status(hipllm::launch_route_groups(ids, n, experts, vmax, order, groups, ngroups, as_stream(stream)),
+                  "hipllm_route_groups: invalid arguments (n <= 16384, experts <= 1024) or launch failure");
+}
+
+int hipllm_gemm_gather(uint32_t type, const void* w, size_t row_bytes, const void* xb, float* y, size_t n, size_t k,
+                       size_t ldy, const int32_t* order, const int32_t* groups, const uint32_t* ngroups,
+                       size_t max_groups, size_t expert_stride, size_t routes, int x_routed, void* stream) {
+    return status(hipllm::launch_gemm_gather(type, w, row_bytes, xb, y, n, k, ldy, order, groups, ngroups, max_groups,
+                                             expert_stride, routes, x_routed, as_stream(stream)),
+                  "hipllm_gemm_gather: invalid arguments (k % 128 == 0, max_groups <= 65535, alignment) or launch "
+                  "failure");
+}
+
 int hipllm_router_topk(const float* logits, size_t ld, size_t tokens, size_t experts, size_t k, int32_t* ids,
                        float* weights, void* stream) {
     return status(hipllm::launch_router_topk(logits, ld, tokens, experts, k, ids, weights, as_stream(stream)),

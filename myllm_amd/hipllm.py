@@ -97,6 +97,9 @@ SIGNATURES = {
     "hipllm_moe_combine": (_I, [_P, _P, _P, _P, _P, _S, _P, _S, _S, _S, _P]),
     "hipllm_moe_combine_norm": (_I, [_P, _P, _P, _P, _P, _S, _P, _P, _P, _P, _S, _S, _S, _F, _P]),
     "hipllm_gemv_multi_norm": (_I, [_P, _S, _P, _P, _F, _S, _P, _P, _P]),
+    "hipllm_route_groups_max": (_S, [_S, _S, _S]),
+    "hipllm_route_groups": (_I, [_P, _S, _S, _S, _P, _P, _P, _P]),
+    "hipllm_gemm_gather": (_I, [_U32, _P, _S, _P, _P, _S, _S, _S, _P, _P, _P, _S, _S, _S, _I, _P]),
     "hipllm_attn_decode_rope_gated": (_I, [_P, _P, _S, _P, _P, _P, _P, _P, _P, _S, _S, _S, _S, _F, _P]),
     "hipllm_gemv_routed_swiglu": (_I, [_U32, _P, _P, _S, _P, _P, _S, _P, _P, _S, _S, _S, _P, _S, _S, _S, _S, _P, _P,
                                        _P]),
@@ -359,6 +362,18 @@ def _k_gemv_batched(qtype, w, wu, row_bytes, x, xq, bias, residual, y, yq, n, k,
                                     expert_stride, 1 if x_routed else 0, ldx or k, ldy or n, _stream(stream)))
 
 
+def _k_route_groups(ids, n, experts, vmax, order, groups, ngroups, stream=None):
+    check(lib().hipllm_route_groups(_ptr(ids), n, experts, vmax, _ptr(order), _ptr(groups), _ptr(ngroups),
+                                    _stream(stream)))
+
+
+def _k_gemm_gather(qtype, w, row_bytes, xb, y, n, k, ldy, order, groups, ngroups, max_groups, expert_stride, routes,
+                   x_routed, stream=None):
+    check(lib().hipllm_gemm_gather(qtype, _ptr(w), row_bytes, _ptr(xb), _ptr(y), n, k, ldy, _ptr(order), _ptr(groups),
+                                   _ptr(ngroups), max_groups, expert_stride, routes, 1 if x_routed else 0,
+                                   _stream(stream)))
+
+
 def _k_router_topk(logits, ld, tokens, experts, k, ids, weights, stream=None):
     check(lib().hipllm_router_topk(_ptr(logits), ld, tokens, experts, k, _ptr(ids), _ptr(weights), _stream(stream)))
 
@@ -498,7 +513,8 @@ kernels = types.SimpleNamespace(
     gemm_workspace_bytes=lambda m, k: lib().hipllm_gemm_workspace_bytes(m, k), rmsnorm=_k_rmsnorm, embed=_k_embed, rope_kv=_k_rope_kv,
     attn_decode=_k_attn_decode, attn_decode_rope_gated=_k_attn_decode_rope_gated, argmax=_k_argmax,
     swiglu=_k_swiglu, attn_prefill=_k_attn_prefill,
-    gemv_batched=_k_gemv_batched, router_topk=_k_router_topk, moe_combine=_k_moe_combine,
+    gemv_batched=_k_gemv_batched, route_groups=_k_route_groups, gemm_gather=_k_gemm_gather,
+    route_groups_max=lambda n, e, v: lib().hipllm_route_groups_max(n, e, v), router_topk=_k_router_topk, moe_combine=_k_moe_combine,
     moe_combine_norm=_k_moe_combine_norm,
     gemv_multi_norm=_k_gemv_multi_norm, gemv_routed_swiglu=_k_gemv_routed_swiglu,
     gemv_moe_combine=_k_gemv_moe_combine, gdn_gates=_k_gdn_gates,

@@ -218,6 +218,84 @@ def test_gemv_moe_combine_rejects_bad_arguments(cuda):
         kernels.gemv_moe_combine(synth.Q8_0, w, 34 * 16 * 20, x, x, x, x, x, 8, x, 1, 10240)
 
 
+@pytest.mark.parametrize("n,E,vmax", [(512, 256, 64), (37, 8, 4), (16384, 256, 64), (1, 1, 64), (600, 8, 64)])
+def test_route_groups(cuda, n, E, vmax):
+    """The vectors stably sorted by expert, cut into groups of at most vmax
+    vectors of one expert, in expert order."""
+    rng = np.random.default_rng(n + E)
+    ids = rng.integers(0, E, size=n).astype(np.int32)
+    if n > 4:
+        ids[3] = E + 5   # out of range: the last expert, as the GEMVs clamp it
+    cl = np.minimum(ids, E - 1)
+    mg = kernels.route_groups_max(n, E, vmax)
+    order = torch.full((n,), -1, dtype=torch.int32, device=cuda)
+    groups = torch.full((2 * mg,), -1, dtype=torch.int32, device=cuda)
+    ng = torch.zeros(1, dtype=torch.int32, device=cuda)
+    kernels.route_groups(torch.from_numpy(ids).to(cuda), n, E, vmax, order, groups, ng)
+    np.testing.assert_array_equal(order.cpu().numpy(), np.argsort(cl, kind="stable"))
+    counts = np.bincount(cl, minlength=E)
+    expect, start = [], 0
+    for e in range(E):
+        for q in range(0, counts[e], vmax):
+            expect.append((start + q, e | (min(vmax, counts[e] - q) << 16)))
+        start += counts[e]
+    ngroups = int(ng.item())
+    assert ngroups == len(expect) <= mg
+    np.testing.assert_array_equal(groups.cpu().numpy()[: 2 * ngroups].reshape(-1, 2),
+                                  np.array(expect, dtype=np.int64).reshape(-1, 2))
+
+
+@pytest.mark.parametrize("qtype,T,routed", [(synth.Q4_K, 40, False), (synth.Q6_K, 150, False),
+                                            (synth.Q8_0, 30, True)])
+def test_gemm_gather_matches_bf16_reference(cuda, qtype, T, routed):
+    """Routed expert products as gathered bf16 matmuls against float64
+    products of the bf16-rounded operands (<= 1e-4), with experts holding
+    more than one 64-vector group (T = 150: about 75 vectors each)."""
+    E, K, N, H = 8, 4, 256, 512
+    rng = np.random.default_rng(T)
+    w = random_rows(qtype, E * N, H, 81)
+    dw = dev_bytes(w, cuda)
+    rb = w.shape[1]
+    nv = T * K
+    xrows = nv if routed else T
+    x = torch.from_numpy(synth.normal(xrows * H, 82).reshape(xrows, H)).to(cuda)
+    xb = torch.empty(xrows, H, dtype=torch.bfloat16, device=cuda)
+    kernels.to_bf16(x, H, xb, xrows, H)
+    ids = torch.from_numpy(rng.integers(0, E, size=nv).astype(np.int32)).to(cuda)
+    mg = kernels.route_groups_max(nv, E, 64)
+    order = torch.empty(nv, dtype=torch.int32, device=cuda)
+    groups = torch.empty(2 * mg, dtype=torch.int32, device=cuda)
+    ng = torch.zeros(1, dtype=torch.int32, device=cuda)
+    kernels.route_groups(ids, nv, E, 64, order, groups, ng)
+    y = torch.full((nv, N), float("nan"), device=cuda)
+    kernels.gemm_gather(qtype, dw, rb, xb, y, N, H, N, order, groups, ng, mg, N * rb, K, routed)
+    wf = torch.empty(E * N, H, device=cuda)
+    kernels.dequant_rows(qtype, dw, rb, E * N, H, wf)
+    wb = wf.to(torch.bfloat16).double().reshape(E, N, H)
+    xd = xb.double()
+    idn = ids.cpu().numpy()
+    ref = torch.stack([wb[idn[j]] @ xd[j if routed else j // K] for j in range(nv)])
+    got = y.double()
+    err = ((got - ref).abs().max() / ref.abs().max()).item()
+    print("max rel err", err)
+    assert err <= 1e-4
+
+
+def test_gemm_gather_rejects_bad_arguments(cuda):
+    w = torch.zeros(144 * 64, dtype=torch.uint8, device=cuda)
+    xb = torch.zeros(64, 256, dtype=torch.bfloat16, device=cuda)
+    y = torch.zeros(64, device=cuda)
+    i = torch.zeros(16, dtype=torch.int32, device=cuda)
+    with pytest.raises(ValueError):  # k a multiple of 128
+        kernels.gemm_gather(synth.Q8_0, w, 68, xb, y, 4, 64, 4, i, i, i, 4, 4 * 68, 1, False)
+    with pytest.raises(LengthError):  # one launch row per group
+        kernels.gemm_gather(synth.Q4_K, w, 144, xb, y, 4, 256, 4, i, i, i, 70000, 4 * 144, 1, False)
+    with pytest.raises(ValueError):  # experts closer than their rows
+        kernels.gemm_gather(synth.Q4_K, w, 144, xb, y, 4, 256, 4, i, i, i, 4, 144, 1, False)
+    with pytest.raises(LengthError):
+        kernels.route_groups(i, 16385, 8, 64, i, i, i)
+
+
 def test_gdn_gates(cuda):
     rng = np.random.default_rng(3)
     T, Hv = 4, 32
