@@ -280,6 +280,16 @@ int hipllm_gemv_moe_combine(uint32_t type, const void* w, size_t row_bytes, cons
                             const float* down, const float* weights, const float* sgate, size_t routes, float* y,
                             size_t n, size_t k, void* stream);
 
+/* y[m, n] = x[m, :k] . w[n, :k] in FP32 (row strides in floats): the router
+ * logits of a prompt, reading each weight row once per 32 rows instead of once
+ * per row. K is split over hipllm_matmul_f32_scratch_floats(m, n, k) floats of
+ * scratch (partial sums added in split order, so results are deterministic;
+ * with less scratch it runs unsplit). Replaces the router GEMM of
+ * encode_routes for a prompt (moe_llm.mm:2642-2660). */
+size_t hipllm_matmul_f32_scratch_floats(size_t m, size_t n, size_t k);
+int hipllm_matmul_f32(const float* x, size_t ldx, const float* w, size_t ldw, float* y, size_t ldy, size_t m,
+                      size_t n, size_t k, float* scratch, size_t scratch_floats, void* stream);
+
 /* Routed vectors grouped by expert, for the expert products of several rows:
  * order = 0..n-1 stably sorted by ids (each clamped to experts - 1); groups =
  * pairs {first index into order, expert | count << 16} of at most vmax vectors

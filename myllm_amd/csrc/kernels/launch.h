@@ -68,6 +68,13 @@ int launch_gemv_routed_swiglu(uint32_t type, const void* wg, const void* wu, siz
                               const XGroup* xq, size_t ldx, float* y, XGroup* yq, size_t n, size_t k, size_t tokens,
                               const float* logits, size_t ld_logits, size_t experts, size_t routes,
                               size_t expert_stride, int32_t* ids_out, float* weights_out, hipStream_t stream);
+// y[m, n] = x[m, :k] . w[n, :k] in FP32 (row strides ldx, ldw, ldy floats):
+// the router logits of a prompt, each weight row read once per 32 rows. K
+// split into matmul_f32_scratch_floats(m, n, k) floats of scratch (partial
+// sums, added in split order; with less scratch it runs unsplit).
+size_t matmul_f32_scratch_floats(size_t m, size_t n, size_t k);
+int launch_matmul_f32(const float* x, size_t ldx, const float* w, size_t ldw, float* y, size_t ldy, size_t m, size_t n,
+                      size_t k, float* scratch, size_t scratch_floats, hipStream_t stream);
 // Routed vectors grouped by expert for the several-row expert products:
 // order = 0..n-1 stably sorted by ids (each clamped to experts - 1); groups =
 // pairs {first index into order, expert | count << 16}, at most vmax vectors

@@ -19,6 +19,8 @@
 // tile, 256 threads, 32 state values per thread) so the state is read and
 // written once per call however many tokens it scans; norms run one 64-lane
 // wave per head vector; everything else is one pass over its rows.
+#include <algorithm>
+
 #include "common.h"
 #include "launch.h"
 #include "norm.h"
@@ -39,6 +41,104 @@ __global__ __launch_bounds__(64) void router_topk_kernel(const float* __restrict
                                                          float* __restrict__ weights) {
     const size_t t = blockIdx.x;
     topk_row<PL>(logits + t * ld, experts, k, ids + t * k, weights + t * k, threadIdx.x);
+}
+
+// ------------------------------------------------------------ router over a prompt
+// y[m, n] = x[m, :k] . w[n, :k] in FP32 (the router logits of a prompt; the
+// batched GEMV reads every weight row once per token). Block tile 32 rows x
+// 32 weight rows, 256 threads with 2 x 2 outputs each; k staged through LDS
+// 128 at a time (k-major, so a thread reads its two rows / columns as one
+// float2), the next step's values loaded while this step multiplies. Block z
+// covers k range [z kc, (z + 1) kc) (grid z = the K split; with a split it
+// writes partial sums to part[z], which matmul_reduce_kernel adds in z
+// order). Each output sums its k range in increasing order, one FMA per
+// step: deterministic. A block's time is its FMA chains (about 50 us for
+// k = 2048 unsplit), so the split fills the GPU.
+constexpr uint32_t kMmTile = 32, kMmK = 128;
+
+__global__ __launch_bounds__(256) void matmul_f32_kernel(const float* __restrict__ x, uint32_t ldx,
+                                                         const float* __restrict__ w, uint32_t ldw,
+                                                         float* __restrict__ y, uint32_t ldy, uint32_t m,
+                                                         uint32_t n, uint32_t k, uint32_t kc,
+                                                         float* __restrict__ part) {
+    __shared__ __align__(16) float xs[kMmK][kMmTile + 2];
+    __shared__ __align__(16) float ws[kMmK][kMmTile + 2];
+    constexpr uint32_t kPer = kMmK / 8;  // k values a thread moves per row per step
+    const uint32_t tid = threadIdx.x;
+    const uint32_t m0 = blockIdx.y * kMmTile, n0 = blockIdx.x * kMmTile;
+    const uint32_t tm = (tid / 16) * 2, tn = (tid % 16) * 2;  // this thread's 2 x 2 outputs
+    // Loader: thread t moves k columns kPer (t % 8) .. + kPer of row t / 8.
+    const uint32_t lr = tid / 8, lc = kPer * (tid % 8);
+    const bool xrow = m0 + lr < m, wrow = n0 + lr < n;
+    const float* xp = x + static_cast<size_t>(min(m0 + lr, m - 1)) * ldx;
+    const float* wp = w + static_cast<size_t>(min(n0 + lr, n - 1)) * ldw;
+    const bool vec = (ldx % 4 == 0) && (ldw % 4 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
+                     (reinterpret_cast<uintptr_t>(w) % 16 == 0);
+    auto load = [&](uint32_t k0, float (&xv)[kPer], float (&wv)[kPer]) {
+        const uint32_t kb = k0 + lc;
+        if (vec && kb + kPer <= k) {
+#pragma unroll
+            for (uint32_t i = 0; i < kPer / 4; ++i) {
+                const float4 a = xrow ? *reinterpret_cast<const float4*>(xp + kb + 4 * i) : make_float4(0, 0, 0, 0);
+                const float4 b = wrow ? *reinterpret_cast<const float4*>(wp + kb + 4 * i) : make_float4(0, 0, 0, 0);
+                xv[4 * i] = a.x, xv[4 * i + 1] = a.y, xv[4 * i + 2] = a.z, xv[4 * i + 3] = a.w;
+                wv[4 * i] = b.x, wv[4 * i + 1] = b.y, wv[4 * i + 2] = b.z, wv[4 * i + 3] = b.w;
+            }
+        } else {
+#pragma unroll
+            for (uint32_t i = 0; i < kPer; ++i) {
+                xv[i] = (xrow && kb + i < k) ? xp[kb + i] : 0.0f;
+                wv[i] = (wrow && kb + i < k) ? wp[kb + i] : 0.0f;
+            }
+        }
+    };
+    float acc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+    float xv[kPer], wv[kPer];
+    const uint32_t kbeg = blockIdx.z * kc, kend = min(k, kbeg + kc);
+    load(kbeg, xv, wv);
+    for (uint32_t k0 = kbeg; k0 < kend; k0 += kMmK) {
+        __syncthreads();  // the previous step's reads are done
+#pragma unroll
+        for (uint32_t i = 0; i < kPer; ++i) {
+            xs[lc + i][lr] = xv[i];
+            ws[lc + i][lr] = wv[i];
+        }
+        __syncthreads();
+        if (k0 + kMmK < kend) load(k0 + kMmK, xv, wv);
+        const uint32_t steps = min(kMmK, kend - k0);
+        for (uint32_t kk = 0; kk < steps; ++kk) {
+            const float2 a = *reinterpret_cast<const float2*>(&xs[kk][tm]);
+            const float2 b = *reinterpret_cast<const float2*>(&ws[kk][tn]);
+            acc[0][0] = fmaf(a.x, b.x, acc[0][0]);
+            acc[0][1] = fmaf(a.x, b.y, acc[0][1]);
+            acc[1][0] = fmaf(a.y, b.x, acc[1][0]);
+            acc[1][1] = fmaf(a.y, b.y, acc[1][1]);
+        }
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < 2; ++i) {
+#pragma unroll
+        for (uint32_t j = 0; j < 2; ++j) {
+            if (m0 + tm + i < m && n0 + tn + j < n) {
+                if (part) {
+                    part[(static_cast<size_t>(blockIdx.z) * m + m0 + tm + i) * n + n0 + tn + j] = acc[i][j];
+                } else {
+                    y[static_cast<size_t>(m0 + tm + i) * ldy + n0 + tn + j] = acc[i][j];
+                }
+            }
+        }
+    }
+}
+
+// y[r, c] = sum over z in order of part[z, r, c].
+__global__ void matmul_reduce_kernel(const float* __restrict__ part, float* __restrict__ y, uint32_t ldy, uint32_t m,
+                                     uint32_t n, uint32_t splits) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t total = static_cast<size_t>(m) * n;
+    if (i >= total) return;
+    float acc = part[i];
+    for (uint32_t z = 1; z < splits; ++z) acc += part[z * total + i];
+    y[(i / n) * ldy + i % n] = acc;
 }
 
 // ------------------------------------------------------------ route groups
@@ -558,6 +658,47 @@ int launch_router_topk(const float* logits, size_t ld, size_t tokens, size_t exp
     hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(tokens)), dim3(64), 0, stream, logits,
                        static_cast<uint32_t>(ld), static_cast<uint32_t>(experts), static_cast<uint32_t>(k), ids,
                        weights);
+    return launched();
+}
+
+namespace {
+// K split of the FP32 matmul: enough blocks for the GPU's 256 CUs, at least
+// 128 k per split, at most 16 splits.
+size_t matmul_splits(size_t m, size_t n, size_t k) {
+    const size_t tiles = ((m + kMmTile - 1) / kMmTile) * ((n + kMmTile - 1) / kMmTile);
+    size_t s = tiles >= 256 ? 1 : (256 + tiles - 1) / tiles;
+    s = std::min<size_t>(s, std::min<size_t>(16, (k + kMmK - 1) / kMmK));
+    const size_t kc = ((k + s - 1) / s + kMmK - 1) / kMmK * kMmK;
+    return (k + kc - 1) / kc;
+}
+}  // namespace
+
+size_t matmul_f32_scratch_floats(size_t m, size_t n, size_t k) {
+    const size_t s = matmul_splits(m, n, k);
+    return s > 1 ? s * m * n : 0;
+}
+
+int launch_matmul_f32(const float* x, size_t ldx, const float* w, size_t ldw, float* y, size_t ldy, size_t m, size_t n,
+                      size_t k, float* scratch, size_t scratch_floats, hipStream_t stream) {
+    if (!x || !w || !y || m == 0 || n == 0 || k == 0 || ldx < k || ldw < k || ldy < n) return kInvalidArgument;
+    if (ldx > 0xffffffffull || ldw > 0xffffffffull || ldy > 0xffffffffull || k > 0xffffffffull ||
+        (m + kMmTile - 1) / kMmTile > 65535 || (n + kMmTile - 1) / kMmTile > 0x7fffffffull || m * n > 0xffffffffull) {
+        return kLengthError;
+    }
+    size_t s = matmul_splits(m, n, k);
+    if (s > 1 && (!scratch || scratch_floats < s * m * n)) s = 1;  // no room for the partial sums: unsplit
+    const size_t kc = s > 1 ? ((k + s - 1) / s + kMmK - 1) / kMmK * kMmK : k;
+    const dim3 grid(static_cast<uint32_t>((n + kMmTile - 1) / kMmTile),
+                    static_cast<uint32_t>((m + kMmTile - 1) / kMmTile), static_cast<uint32_t>(s));
+    hipLaunchKernelGGL(matmul_f32_kernel, grid, dim3(256), 0, stream, x, static_cast<uint32_t>(ldx), w,
+                       static_cast<uint32_t>(ldw), y, static_cast<uint32_t>(ldy), static_cast<uint32_t>(m),
+                       static_cast<uint32_t>(n), static_cast<uint32_t>(k), static_cast<uint32_t>(kc),
+                       s > 1 ? scratch : nullptr);
+    if (s > 1) {
+        hipLaunchKernelGGL(matmul_reduce_kernel, dim3(blocks_for(m * n, 256)), dim3(256), 0, stream, scratch, y,
+                           static_cast<uint32_t>(ldy), static_cast<uint32_t>(m), static_cast<uint32_t>(n),
+                           static_cast<uint32_t>(s));
+    }
     return launched();
 }
 

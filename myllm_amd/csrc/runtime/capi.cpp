@@ -422,6 +422,17 @@ int hipllm_gemv_moe_combine(uint32_t type, const void* w, size_t row_bytes, cons
                   "hipllm_gemv_moe_combine: invalid arguments or launch failure");
 }
 
+size_t hipllm_matmul_f32_scratch_floats(size_t m, size_t n, size_t k) {
+    return hipllm::matmul_f32_scratch_floats(m, n, k);
+}
+
+int hipllm_matmul_f32(const float* x, size_t ldx, const float* w, size_t ldw, float* y, size_t ldy, size_t m,
+                      size_t n, size_t k, float* scratch, size_t scratch_floats, void* stream) {
+    return status(hipllm::launch_matmul_f32(x, ldx, w, ldw, y, ldy, m, n, k, scratch, scratch_floats,
+                                            as_stream(stream)),
+                  "hipllm_matmul_f32: invalid arguments or launch failure");
+}
+
 size_t hipllm_route_groups_max(size_t n, size_t experts, size_t vmax) {
     return hipllm::route_groups_max(n, experts, vmax);
 }

@@ -43,6 +43,10 @@ constexpr std::size_t kFusedDeltaNetRows = 4;
 // QKV + z + alpha/beta, attention Q/gate + K/V, router + shared gate/up.
 constexpr std::size_t kGroupedRows = 1;
 
+// From this many rows the router logits run as a tiled FP32 matmul (each
+// weight row read once per 32 rows) instead of a GEMV per row.
+constexpr std::size_t kRouterMatmulRows = 8;
+
 struct MoeLayer {
     bool full = false;
     const float* attn_norm = nullptr;
@@ -106,6 +110,8 @@ struct MoeActivations {
     std::uint32_t* route_ngroups = nullptr;
     float* gate_act = nullptr;              // [T k, FF] expert gate products (prefill matmul path)
     void* act_b = nullptr;                  // [T k, FF] bf16 SwiGLU outputs for the expert down matmul
+    float* mm_scratch = nullptr;            // router matmul partial sums (K split)
+    std::size_t mm_scratch_floats = 0;
 };
 
 }  // namespace
@@ -470,6 +476,12 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
     host_ids = nullptr;
     act_rows = 0;
     const std::size_t wide = std::max(2 * q_w, qkv_w), wide2 = std::max(q_w + 2 * kv_w, qkv_w);
+    // The router matmul's K split needs the most scratch at some row count
+    // below n (fewer rows, more splits): the largest over 1..n.
+    std::size_t mm_floats = 0;
+    for (std::size_t r = kRouterMatmulRows; r <= n; ++r) {
+        mm_floats = std::max(mm_floats, hipllm::matmul_f32_scratch_floats(r, E + 1, H));
+    }
     const std::size_t feat = std::max(q_w, inner);
     std::size_t off = 0;
     auto reserve = [&](std::size_t floats) {
@@ -491,7 +503,8 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
                       o_shg = reserve(n * FFs), o_xb = reserve((n * std::max({H, inner, q_w, FFs}) + 1) / 2),
                       o_ord = reserve(n * K),
                       o_grp = reserve(2 * hipllm::route_groups_max(n * K, E, hipllm::kGatherRows)),
-                      o_ngr = reserve(1), o_gact = reserve(n * K * FF), o_actb = reserve((n * K * FF + 1) / 2);
+                      o_ngr = reserve(1), o_gact = reserve(n * K * FF), o_actb = reserve((n * K * FF + 1) / 2),
+                      o_mms = reserve(mm_floats);
     act_bytes = off;
     hip_check(hipMalloc(&act_arena, act_bytes), "hipMalloc(MoE activations)");
     auto* b = static_cast<std::uint8_t*>(act_arena);
@@ -532,6 +545,8 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
     act.route_ngroups = reinterpret_cast<std::uint32_t*>(b + o_ngr);
     act.gate_act = f(o_gact);
     act.act_b = b + o_actb;
+    act.mm_scratch = f(o_mms);
+    act.mm_scratch_floats = mm_floats;
     hip_check(hipMalloc(reinterpret_cast<void**>(&route_ids), layers.size() * n * K * 4), "hipMalloc(routes)");
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&host_ids), n * 4, hipHostMallocDefault), "hipHostMalloc(ids)");
     act_rows = n;
@@ -780,6 +795,12 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
         sh.w2 = L.sh_up.ptr;
         jobs[nj++] = sh;
         grouped(jobs, nj, hidden, L.post_norm, true, "post-attention norm + router + shared gate/up");
+    } else if (L.fused_router && rows >= kRouterMatmulRows && L.router.type == hipllm::kF32) {
+        // A prompt: the router (and shared-expert gate) rows as an FP32 matmul.
+        launch_check(hipllm::launch_matmul_f32(act.norm, H, reinterpret_cast<const float*>(L.router.ptr),
+                                               L.router.row_bytes / 4, act.rlog, ldr, rows, E + 1, H, act.mm_scratch,
+                                               act.mm_scratch_floats, stream),
+                     "router (matmul)");
     } else if (L.fused_router) {
         proj(L.router, act.norm, act.normq, H, rows, act.rlog, ldr, nullptr, E + 1);
     } else {

@@ -97,6 +97,8 @@ SIGNATURES = {
     "hipllm_moe_combine": (_I, [_P, _P, _P, _P, _P, _S, _P, _S, _S, _S, _P]),
     "hipllm_moe_combine_norm": (_I, [_P, _P, _P, _P, _P, _S, _P, _P, _P, _P, _S, _S, _S, _F, _P]),
     "hipllm_gemv_multi_norm": (_I, [_P, _S, _P, _P, _F, _S, _P, _P, _P]),
+    "hipllm_matmul_f32": (_I, [_P, _S, _P, _S, _P, _S, _S, _S, _S, _P, _S, _P]),
+    "hipllm_matmul_f32_scratch_floats": (_S, [_S, _S, _S]),
     "hipllm_route_groups_max": (_S, [_S, _S, _S]),
     "hipllm_route_groups": (_I, [_P, _S, _S, _S, _P, _P, _P, _P]),
     "hipllm_gemm_gather": (_I, [_U32, _P, _S, _P, _P, _S, _S, _S, _P, _P, _P, _S, _S, _S, _I, _P]),
@@ -362,6 +364,11 @@ def _k_gemv_batched(qtype, w, wu, row_bytes, x, xq, bias, residual, y, yq, n, k,
                                     expert_stride, 1 if x_routed else 0, ldx or k, ldy or n, _stream(stream)))
 
 
+def _k_matmul_f32(x, ldx, w, ldw, y, ldy, m, n, k, scratch=None, stream=None):
+    check(lib().hipllm_matmul_f32(_ptr(x), ldx, _ptr(w), ldw, _ptr(y), ldy, m, n, k, _ptr(scratch),
+                                  0 if scratch is None else scratch.numel(), _stream(stream)))
+
+
 def _k_route_groups(ids, n, experts, vmax, order, groups, ngroups, stream=None):
     check(lib().hipllm_route_groups(_ptr(ids), n, experts, vmax, _ptr(order), _ptr(groups), _ptr(ngroups),
                                     _stream(stream)))
@@ -513,7 +520,8 @@ kernels = types.SimpleNamespace(
     gemm_workspace_bytes=lambda m, k: lib().hipllm_gemm_workspace_bytes(m, k), rmsnorm=_k_rmsnorm, embed=_k_embed, rope_kv=_k_rope_kv,
     attn_decode=_k_attn_decode, attn_decode_rope_gated=_k_attn_decode_rope_gated, argmax=_k_argmax,
     swiglu=_k_swiglu, attn_prefill=_k_attn_prefill,
-    gemv_batched=_k_gemv_batched, route_groups=_k_route_groups, gemm_gather=_k_gemm_gather,
+    gemv_batched=_k_gemv_batched, matmul_f32=_k_matmul_f32,
+    matmul_f32_scratch_floats=lambda m, n, k: lib().hipllm_matmul_f32_scratch_floats(m, n, k), route_groups=_k_route_groups, gemm_gather=_k_gemm_gather,
     route_groups_max=lambda n, e, v: lib().hipllm_route_groups_max(n, e, v), router_topk=_k_router_topk, moe_combine=_k_moe_combine,
     moe_combine_norm=_k_moe_combine_norm,
     gemv_multi_norm=_k_gemv_multi_norm, gemv_routed_swiglu=_k_gemv_routed_swiglu,

@@ -296,6 +296,28 @@ def test_gemm_gather_rejects_bad_arguments(cuda):
         kernels.route_groups(i, 16385, 8, 64, i, i, i)
 
 
+@pytest.mark.parametrize("m,n,k", [(64, 257, 2048), (5, 33, 100), (512, 257, 2048), (1, 1, 1)])
+def test_matmul_f32_matches_float64(cuda, m, n, k):
+    rng = np.random.default_rng(m + n + k)
+    x = rng.normal(size=(m, k)).astype(np.float32)
+    w = (rng.normal(size=(n, k)) / math.sqrt(k)).astype(np.float32)
+    dx, dw = t32(x, cuda), t32(w, cuda)
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    sf = kernels.matmul_f32_scratch_floats(m, n, k)
+    results = []
+    # with the K split (scratch for the partial sums) and without it
+    for scratch in (torch.empty(max(sf, 1), device=cuda), None):
+        y = torch.full((m, n + 3), float("nan"), device=cuda)
+        kernels.matmul_f32(dx, k, dw, k, y, n + 3, m, n, k, scratch)
+        got = y[:, :n].cpu().numpy()
+        assert rel_err(got, ref) <= 1e-5
+        assert np.isnan(y[:, n:].cpu().numpy()).all()  # columns past n untouched
+        y2 = torch.empty(m, n + 3, device=cuda)
+        kernels.matmul_f32(dx, k, dw, k, y2, n + 3, m, n, k, scratch)
+        assert torch.equal(y[:, :n].view(torch.int32), y2[:, :n].view(torch.int32))  # fixed summation order
+        results.append(got)
+
+
 def test_gdn_gates(cuda):
     rng = np.random.default_rng(3)
     T, Hv = 4, 32
