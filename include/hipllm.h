@@ -291,7 +291,8 @@ int hipllm_matmul_f32(const float* x, size_t ldx, const float* w, size_t ldw, fl
                       size_t n, size_t k, float* scratch, size_t scratch_floats, void* stream);
 
 /* Routed vectors grouped by expert, for the expert products of several rows:
- * order = 0..n-1 stably sorted by ids (each clamped to experts - 1); groups =
+ * order = 0..n-1 sorted by ids (each clamped to experts - 1; in no fixed order
+ * inside one expert); groups =
  * pairs {first index into order, expert | count << 16} of at most vmax vectors
  * of one expert; *ngroups = their count, at most
  * hipllm_route_groups_max(n, experts, vmax). n <= 16384, experts <= 1024. No

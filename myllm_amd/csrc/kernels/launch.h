@@ -76,7 +76,8 @@ size_t matmul_f32_scratch_floats(size_t m, size_t n, size_t k);
 int launch_matmul_f32(const float* x, size_t ldx, const float* w, size_t ldw, float* y, size_t ldy, size_t m, size_t n,
                       size_t k, float* scratch, size_t scratch_floats, hipStream_t stream);
 // Routed vectors grouped by expert for the several-row expert products:
-// order = 0..n-1 stably sorted by ids (each clamped to experts - 1); groups =
+// order = 0..n-1 sorted by ids (each clamped to experts - 1; in no fixed
+// order inside one expert); groups =
 // pairs {first index into order, expert | count << 16}, at most vmax vectors
 // of one expert each; *ngroups = the group count, at most
 // route_groups_max(n, experts, vmax). n <= 16384, experts <= 1024.

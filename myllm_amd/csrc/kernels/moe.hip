@@ -142,11 +142,14 @@ __global__ void matmul_reduce_kernel(const float* __restrict__ part, float* __re
 }
 
 // ------------------------------------------------------------ route groups
-// Stable counting sort of n routed vectors by expert in one block, then the
-// expert groups of at most vmax vectors: the ids in LDS; thread e counts
-// expert e's vectors; one thread turns the counts into offsets (vectors and
-// groups); thread e lists its vectors in increasing index and writes its
-// groups. O(experts * n) LDS reads: a few microseconds at prompt sizes.
+// Counting sort of n routed vectors by expert in one block, then the expert
+// groups of at most vmax vectors: per-expert counts with LDS atomics, one
+// thread turns them into offsets (vectors and groups), every vector takes
+// the next slot of its expert (LDS atomic), and thread e writes expert e's
+// groups. The order of the vectors inside one expert follows the atomics;
+// it changes nothing downstream, where every vector's row is computed on its
+// own (its X row against the expert's weights, written to its own y row).
+// O(n + experts); a scan of all ids per expert measured 284 us at 4096 x 256.
 constexpr uint32_t kRouteGroupsMax = 16384;
 
 __global__ __launch_bounds__(1024) void route_groups_kernel(const int32_t* __restrict__ ids, uint32_t n,
@@ -154,24 +157,22 @@ __global__ __launch_bounds__(1024) void route_groups_kernel(const int32_t* __res
                                                             int32_t* __restrict__ order,
                                                             int32_t* __restrict__ groups,
                                                             uint32_t* __restrict__ ngroups) {
-    __shared__ uint16_t sid[kRouteGroupsMax];
+    __shared__ uint32_t cnt[kMaxExperts];
     __shared__ uint32_t off[kMaxExperts];
     __shared__ uint32_t goff[kMaxExperts];
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-        sid[i] = static_cast<uint16_t>(min(static_cast<uint32_t>(ids[i]), experts - 1));
-    }
+    __shared__ uint32_t cur[kMaxExperts];
+    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) cnt[e] = 0;
     __syncthreads();
-    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
-        uint32_t c = 0;
-        for (uint32_t i = 0; i < n; ++i) c += sid[i] == e;
-        off[e] = c;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        atomicAdd(&cnt[min(static_cast<uint32_t>(ids[i]), experts - 1)], 1u);
     }
     __syncthreads();
     if (threadIdx.x == 0) {
         uint32_t run = 0, grun = 0;
         for (uint32_t e = 0; e < experts; ++e) {
-            const uint32_t c = off[e];
+            const uint32_t c = cnt[e];
             off[e] = run;
+            cur[e] = run;
             goff[e] = grun;
             run += c;
             grun += (c + vmax - 1) / vmax;
@@ -179,13 +180,12 @@ __global__ __launch_bounds__(1024) void route_groups_kernel(const int32_t* __res
         *ngroups = grun;
     }
     __syncthreads();
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const uint32_t slot = atomicAdd(&cur[min(static_cast<uint32_t>(ids[i]), experts - 1)], 1u);
+        order[slot] = static_cast<int32_t>(i);
+    }
     for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
-        const uint32_t start = off[e];
-        uint32_t o = start;
-        for (uint32_t i = 0; i < n; ++i) {
-            if (sid[i] == e) order[o++] = static_cast<int32_t>(i);
-        }
-        const uint32_t c = o - start;
+        const uint32_t start = off[e], c = cnt[e];
         for (uint32_t q = 0; q * vmax < c; ++q) {
             const uint32_t gq = goff[e] + q;
             groups[2 * gq] = static_cast<int32_t>(start + q * vmax);
