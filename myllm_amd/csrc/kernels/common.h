@@ -153,10 +153,15 @@ __device__ __forceinline__ float quad_sum(float v) {
     return v + dpp_f32<kDppQuadXor2>(v);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
+// Sum over each row of 16 lanes (lanes 16i .. 16i + 15), equal in all 16.
+__device__ __forceinline__ float row16_sum(float v) {
     v = quad_sum(v);
     v += dpp_f32<kDppHalfMirror>(v);
-    v += dpp_f32<kDppMirror>(v);
+    return v + dpp_f32<kDppMirror>(v);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
     return (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
 }
 

@@ -357,68 +357,81 @@ __global__ __launch_bounds__(64) void l2norm_heads_kernel(float* __restrict__ x,
     for (uint32_t i = threadIdx.x; i < d; i += 64) v[i] = v[i] * inv;
 }
 
-// Gated DeltaNet scan. Block (value head h, 64-column tile): thread
-// (col = tid % 64, rg = tid / 64) holds rows [rg NPR, rg NPR + NPR) of
-// columns col of state S_h[Dk][Dv] (row = key dim). Per token, with key head
-// h % key_heads:  S *= decay; pred = S^T k; delta = beta (v - pred);
-// S += k delta^T; o = S^T q / sqrt(Dk).
-template <int NPR>
-__global__ __launch_bounds__(256) void gdn_scan_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                                       uint32_t ldqk, const float* __restrict__ v, uint32_t ldv,
-                                                       const float* __restrict__ decay,
-                                                       const float* __restrict__ beta, float* __restrict__ state,
-                                                       float* __restrict__ out, uint32_t ldo, uint32_t tokens,
-                                                       uint32_t value_heads, uint32_t key_heads) {
-    constexpr uint32_t Dk = 4 * NPR;
-    const uint32_t h = blockIdx.x;
-    const uint32_t col = blockIdx.y * 64 + (threadIdx.x & 63);
-    const uint32_t rg = threadIdx.x >> 6;
-    const uint32_t kh = h % key_heads;
-    const uint32_t Dv = Dk;
-    float* S = state + static_cast<size_t>(h) * Dk * Dv;
-    float s[NPR];
+// Gated DeltaNet scan. Column j of the state S_h[Dk][Dv] (row = key dim)
+// evolves on its own: per token, with key head h % key_heads,
+// S[:, j] *= decay; pred_j = S[:, j] . k; delta_j = beta (v_j - pred_j);
+// S[:, j] += k delta_j; o_j = S[:, j] . q / sqrt(Dk). So a block is one wave
+// of four columns of one value head: lane 16 c + r holds rows
+// [r NR, r NR + NR) of column c (NR = D / 16), both column sums are 16-lane
+// DPP reductions, and no token needs a block barrier. The next token's
+// inputs are loaded before the current token's recurrence. Blocks are
+// renumbered so that every XCD (which receives every eighth block) runs the
+// columns of whole key heads, whose k and q rows its L2 then holds.
+template <uint32_t D, bool VEC>
+__global__ __launch_bounds__(64) void gdn_scan_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                      uint32_t ldqk, const float* __restrict__ v, uint32_t ldv,
+                                                      const float* __restrict__ decay,
+                                                      const float* __restrict__ beta, float* __restrict__ state,
+                                                      float* __restrict__ out, uint32_t ldo, uint32_t tokens,
+                                                      uint32_t value_heads, uint32_t key_heads) {
+    constexpr uint32_t NR = D / 16, WPH = D / 4;  // rows per lane, blocks per value head
+    const uint32_t nb = gridDim.x;
+    const uint32_t b = nb % 8 == 0 ? (blockIdx.x % 8) * (nb / 8) + blockIdx.x / 8 : blockIdx.x;
+    const uint32_t ratio = value_heads / key_heads;
+    const uint32_t lh = b / WPH;  // value heads of one key head are adjacent in this order
+    const uint32_t kh = lh / ratio, h = (lh % ratio) * key_heads + kh;
+    const uint32_t r = threadIdx.x & 15;
+    const uint32_t col = (b % WPH) * 4 + (threadIdx.x >> 4);
+    float* S = state + static_cast<size_t>(h) * D * D;
+    float s[NR];
 #pragma unroll
-    for (int i = 0; i < NPR; ++i) s[i] = S[static_cast<size_t>(rg * NPR + i) * Dv + col];
-    __shared__ float ks[Dk], qs[Dk];
-    __shared__ float part[4][64];
-    const float qscale = 1.0f / sqrtf(static_cast<float>(Dk));
-    const uint32_t lc = threadIdx.x & 63;
-    for (uint32_t t = 0; t < tokens; ++t) {
-        for (uint32_t i = threadIdx.x; i < Dk; i += 256) {
-            ks[i] = k[static_cast<size_t>(t) * ldqk + kh * Dk + i];
-            qs[i] = q[static_cast<size_t>(t) * ldqk + kh * Dk + i];
+    for (uint32_t i = 0; i < NR; ++i) s[i] = S[static_cast<size_t>(r * NR + i) * D + col];
+    const float qscale = 1.0f / sqrtf(static_cast<float>(D));
+    float kc[NR], qc[NR], vc, gc, bc;
+    auto load = [&](uint32_t t, float (&kk)[NR], float (&qq)[NR], float& vv, float& gg, float& bb) {
+        const size_t off = static_cast<size_t>(t) * ldqk + kh * D + r * NR;
+        if constexpr (VEC) {
+#pragma unroll
+            for (uint32_t i = 0; i < NR; i += 4) {
+                const float4 a = *reinterpret_cast<const float4*>(k + off + i);
+                const float4 c = *reinterpret_cast<const float4*>(q + off + i);
+                kk[i] = a.x, kk[i + 1] = a.y, kk[i + 2] = a.z, kk[i + 3] = a.w;
+                qq[i] = c.x, qq[i + 1] = c.y, qq[i + 2] = c.z, qq[i + 3] = c.w;
+            }
+        } else {
+#pragma unroll
+            for (uint32_t i = 0; i < NR; ++i) kk[i] = k[off + i], qq[i] = q[off + i];
         }
-        const float g = decay[t * value_heads + h];
-        const float b = beta[t * value_heads + h];
-        const float vv = v[static_cast<size_t>(t) * ldv + h * Dv + col];
-        __syncthreads();
+        vv = v[static_cast<size_t>(t) * ldv + h * D + col];
+        gg = decay[static_cast<size_t>(t) * value_heads + h];
+        bb = beta[static_cast<size_t>(t) * value_heads + h];
+    };
+    load(0, kc, qc, vc, gc, bc);
+    for (uint32_t t = 0; t < tokens; ++t) {
+        float kn[NR], qn[NR], vn = 0.0f, gn = 0.0f, bn = 0.0f;
+        if (t + 1 < tokens) load(t + 1, kn, qn, vn, gn, bn);
         float pp = 0.0f;
 #pragma unroll
-        for (int i = 0; i < NPR; ++i) {
-            s[i] *= g;
-            pp += s[i] * ks[rg * NPR + i];
+        for (uint32_t i = 0; i < NR; ++i) {
+            s[i] *= gc;
+            pp += s[i] * kc[i];
         }
-        part[rg][lc] = pp;
-        __syncthreads();
-        const float pred = (part[0][lc] + part[1][lc]) + (part[2][lc] + part[3][lc]);
-        const float delta = b * (vv - pred);
+        const float pred = row16_sum(pp);
+        const float delta = bc * (vc - pred);
         float op = 0.0f;
 #pragma unroll
-        for (int i = 0; i < NPR; ++i) {
-            s[i] += ks[rg * NPR + i] * delta;
-            op += s[i] * qs[rg * NPR + i];
+        for (uint32_t i = 0; i < NR; ++i) {
+            s[i] += kc[i] * delta;
+            op += s[i] * qc[i];
         }
-        __syncthreads();  // everyone has read part[] (pred) before it is reused
-        part[rg][lc] = op;
-        __syncthreads();
-        if (rg == 0) {
-            const float o = (part[0][lc] + part[1][lc]) + (part[2][lc] + part[3][lc]);
-            out[static_cast<size_t>(t) * ldo + h * Dv + col] = o * qscale;
-        }
-        __syncthreads();  // ks/qs/part reused by the next token
+        const float o = row16_sum(op);
+        if (r == 0) out[static_cast<size_t>(t) * ldo + h * D + col] = o * qscale;
+#pragma unroll
+        for (uint32_t i = 0; i < NR; ++i) kc[i] = kn[i], qc[i] = qn[i];
+        vc = vn, gc = gn, bc = bn;
     }
 #pragma unroll
-    for (int i = 0; i < NPR; ++i) S[static_cast<size_t>(rg * NPR + i) * Dv + col] = s[i];
+    for (uint32_t i = 0; i < NR; ++i) S[static_cast<size_t>(r * NR + i) * D + col] = s[i];
 }
 
 // Fused decode/prefill forms of the DeltaNet pieces above.
@@ -796,19 +809,27 @@ int launch_gdn_scan(const float* q, const float* k, size_t ldqk, const float* v,
     }
     if (ldqk < key_heads * d || ldv < value_heads * d || ldo < value_heads * d) return kInvalidArgument;
     if (tokens > 0x7fffffffull || value_heads > 0x7fffffffull) return kLengthError;
-    const dim3 grid(static_cast<uint32_t>(value_heads), static_cast<uint32_t>(d / 64));
+    if (value_heads > 0x7fffffffull / d) return kLengthError;
+    const dim3 grid(static_cast<uint32_t>(value_heads * (d / 4)));
     const uint32_t T = static_cast<uint32_t>(tokens), Hv = static_cast<uint32_t>(value_heads),
                    Hk = static_cast<uint32_t>(key_heads);
-    switch (d) {
-    case 64:
-        hipLaunchKernelGGL(gdn_scan_kernel<16>, grid, dim3(256), 0, stream, q, k, static_cast<uint32_t>(ldqk), v,
-                           static_cast<uint32_t>(ldv), decay, beta, state, out, static_cast<uint32_t>(ldo), T, Hv, Hk);
-        break;
-    case 128:
-        hipLaunchKernelGGL(gdn_scan_kernel<32>, grid, dim3(256), 0, stream, q, k, static_cast<uint32_t>(ldqk), v,
-                           static_cast<uint32_t>(ldv), decay, beta, state, out, static_cast<uint32_t>(ldo), T, Hv, Hk);
-        break;
-    default:
+    // Whole float4 loads of k and q when their rows start on 16 bytes.
+    const bool vec = reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
+                     ldqk % 4 == 0;
+    const uint32_t lq = static_cast<uint32_t>(ldqk), lv = static_cast<uint32_t>(ldv), lo = static_cast<uint32_t>(ldo);
+    if (d == 64 && vec) {
+        hipLaunchKernelGGL((gdn_scan_kernel<64, true>), grid, dim3(64), 0, stream, q, k, lq, v, lv, decay, beta, state,
+                           out, lo, T, Hv, Hk);
+    } else if (d == 64) {
+        hipLaunchKernelGGL((gdn_scan_kernel<64, false>), grid, dim3(64), 0, stream, q, k, lq, v, lv, decay, beta, state,
+                           out, lo, T, Hv, Hk);
+    } else if (d == 128 && vec) {
+        hipLaunchKernelGGL((gdn_scan_kernel<128, true>), grid, dim3(64), 0, stream, q, k, lq, v, lv, decay, beta,
+                           state, out, lo, T, Hv, Hk);
+    } else if (d == 128) {
+        hipLaunchKernelGGL((gdn_scan_kernel<128, false>), grid, dim3(64), 0, stream, q, k, lq, v, lv, decay, beta,
+                           state, out, lo, T, Hv, Hk);
+    } else {
         return kInvalidArgument;  // state size 64 or 128
     }
     return launched();

@@ -742,7 +742,8 @@ void HipMoeLLM::Impl::deltanet_layer(std::size_t li, std::size_t rows, float* hi
                      "DeltaNet scan + gated norm");
     } else {
         // Many rows: the per-row steps that parallelise over rows run as
-        // their own launches, and the scan splits each head over two blocks.
+        // their own launches, and the scan runs one wave per four state
+        // columns (each column's recurrence is independent).
         launch_check(hipllm::launch_gdn_gates(act.ab, act.ab + Hv, 2 * Hv, L.dt_bias, L.a, act.decay, act.beta, rows,
                                               Hv, stream),
                      "DeltaNet gates");

@@ -369,18 +369,19 @@ def test_l2norm_heads(cuda):
     np.testing.assert_array_equal(got[:, heads * d:], x[:, heads * d:])
 
 
-@pytest.mark.parametrize("d,Hv,G", [(128, 32, 16), (64, 4, 2)])
-def test_gdn_scan_matches_float64_steps(cuda, d, Hv, G):
+# pad: extra columns per row, so that odd row strides take the scalar-load form.
+@pytest.mark.parametrize("d,Hv,G,T,pad", [(128, 32, 16, 9, 0), (64, 4, 2, 9, 0), (128, 32, 16, 300, 0),
+                                          (64, 4, 2, 33, 1), (128, 6, 3, 17, 3)])
+def test_gdn_scan_matches_float64_steps(cuda, d, Hv, G, T, pad):
     rng = np.random.default_rng(6)
-    T = 9
     qk = rng.normal(size=(T, 2, G, d))
     qk = qk / np.linalg.norm(qk, axis=-1, keepdims=True)
     v = rng.normal(size=(T, Hv, d))
     decay = rng.uniform(0.3, 1.0, size=(T, Hv))
     beta = rng.uniform(0.0, 1.0, size=(T, Hv))
     S0 = rng.normal(scale=0.1, size=(Hv, d, d))
-    ldqk = 2 * G * d + Hv * d
-    buf = np.concatenate([qk.reshape(T, -1), v.reshape(T, -1)], axis=1)
+    ldqk = 2 * G * d + Hv * d + pad
+    buf = np.concatenate([qk.reshape(T, -1), v.reshape(T, -1), rng.normal(size=(T, pad))], axis=1)
     dbuf = t32(buf, cuda)
     state = t32(S0, cuda)
     out = torch.empty(T, Hv * d, device=cuda)
