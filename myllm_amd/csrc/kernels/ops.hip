@@ -284,22 +284,44 @@ __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restri
 
 // gate (nullable): the head outputs are multiplied by sigmoid(gate) (the
 // gated attention's output gate, as the separate gate kernel computes it).
+// Thread i < d owns output dim i (d <= 256 = blockDim). Every split's m, l
+// and value i are loaded at once (one memory round trip; indices past the
+// last split repeat it and are not used), then combined in split order.
 __global__ __launch_bounds__(256) void attn_decode_merge(const float* __restrict__ part, float* __restrict__ out,
                                                          XGroup* __restrict__ outq, uint32_t d, uint32_t nchunks,
                                                          const float* __restrict__ gate) {
     const uint32_t h = blockIdx.x;
+    const uint32_t i = threadIdx.x;
     const float* ph = part + static_cast<size_t>(h) * nchunks * (d + 2);
-    // nchunks = the number of splits; a split without keys has m = -inf,
-    // weight exp(-inf - M) = 0 (split 0 always holds key 0, so M is finite).
+    // nchunks = the number of splits (<= kAttnMaxSplits); a split without
+    // keys has m = -inf, weight exp(-inf - M) = 0 (split 0 always holds key
+    // 0, so M is finite).
+    const uint32_t ii = min(i, d - 1);
+    float ms[kAttnMaxSplits], ls[kAttnMaxSplits], vs[kAttnMaxSplits];
+#pragma unroll
+    for (uint32_t c = 0; c < kAttnMaxSplits; ++c) {
+        const float* pc = ph + static_cast<size_t>(min(c, nchunks - 1)) * (d + 2);
+        ms[c] = pc[0];
+        ls[c] = pc[1];
+        vs[c] = pc[2 + ii];
+    }
     float M = -INFINITY;
-    for (uint32_t c = 0; c < nchunks; ++c) M = fmaxf(M, ph[c * (d + 2)]);
-    float L = 0.0f;
-    for (uint32_t c = 0; c < nchunks; ++c) L += ph[c * (d + 2) + 1] * expf(ph[c * (d + 2)] - M);
+#pragma unroll
+    for (uint32_t c = 0; c < kAttnMaxSplits; ++c) {
+        if (c < nchunks) M = fmaxf(M, ms[c]);
+    }
+    float L = 0.0f, acc = 0.0f;
+#pragma unroll
+    for (uint32_t c = 0; c < kAttnMaxSplits; ++c) {
+        if (c < nchunks) {
+            const float wgt = expf(ms[c] - M);
+            L += ls[c] * wgt;
+            acc += vs[c] * wgt;
+        }
+    }
     const float invL = 1.0f / L;
     __shared__ __align__(16) float vals[256];
-    for (uint32_t i = threadIdx.x; i < d; i += blockDim.x) {
-        float acc = 0.0f;
-        for (uint32_t c = 0; c < nchunks; ++c) acc += ph[c * (d + 2) + 2 + i] * expf(ph[c * (d + 2)] - M);
+    if (i < d) {
         float v = acc * invL;
         if (gate) v = v * sigmoid_ref(gate[h * d + i]);
         out[h * d + i] = v;
