@@ -363,8 +363,8 @@ __global__ __launch_bounds__(64) void l2norm_heads_kernel(float* __restrict__ x,
 // S[:, j] += k delta_j; o_j = S[:, j] . q / sqrt(Dk). So a block is one wave
 // of four columns of one value head: lane 16 c + r holds rows
 // [r NR, r NR + NR) of column c (NR = D / 16), both column sums are 16-lane
-// DPP reductions, and no token needs a block barrier. The next token's
-// inputs are loaded before the current token's recurrence. Blocks are
+// DPP reductions, and no token needs a block barrier. Each token's inputs
+// are loaded eight tokens ahead of its recurrence. Blocks are
 // renumbered so that every XCD (which receives every eighth block) runs the
 // columns of whole key heads, whose k and q rows its L2 then holds.
 template <uint32_t D, bool VEC>
@@ -387,8 +387,11 @@ __global__ __launch_bounds__(64) void gdn_scan_kernel(const float* __restrict__ 
 #pragma unroll
     for (uint32_t i = 0; i < NR; ++i) s[i] = S[static_cast<size_t>(r * NR + i) * D + col];
     const float qscale = 1.0f / sqrtf(static_cast<float>(D));
-    float kc[NR], qc[NR], vc, gc, bc;
-    auto load = [&](uint32_t t, float (&kk)[NR], float (&qq)[NR], float& vv, float& gg, float& bb) {
+    // Ring of the next PF tokens' inputs in registers: a step takes about a
+    // tenth of a load's latency, so the loads run PF tokens ahead.
+    constexpr uint32_t PF = 8;
+    float kb[PF][NR], qb[PF][NR], vb[PF], gb[PF], bb[PF];
+    auto load = [&](uint32_t t, float (&kk)[NR], float (&qq)[NR], float& vv, float& gg, float& bt) {
         const size_t off = static_cast<size_t>(t) * ldqk + kh * D + r * NR;
         if constexpr (VEC) {
 #pragma unroll
@@ -404,31 +407,36 @@ __global__ __launch_bounds__(64) void gdn_scan_kernel(const float* __restrict__ 
         }
         vv = v[static_cast<size_t>(t) * ldv + h * D + col];
         gg = decay[static_cast<size_t>(t) * value_heads + h];
-        bb = beta[static_cast<size_t>(t) * value_heads + h];
+        bt = beta[static_cast<size_t>(t) * value_heads + h];
     };
-    load(0, kc, qc, vc, gc, bc);
-    for (uint32_t t = 0; t < tokens; ++t) {
-        float kn[NR], qn[NR], vn = 0.0f, gn = 0.0f, bn = 0.0f;
-        if (t + 1 < tokens) load(t + 1, kn, qn, vn, gn, bn);
-        float pp = 0.0f;
 #pragma unroll
-        for (uint32_t i = 0; i < NR; ++i) {
-            s[i] *= gc;
-            pp += s[i] * kc[i];
+    for (uint32_t p = 0; p < PF; ++p) {
+        if (p < tokens) load(p, kb[p], qb[p], vb[p], gb[p], bb[p]);
+    }
+    for (uint32_t t0 = 0; t0 < tokens; t0 += PF) {
+#pragma unroll
+        for (uint32_t p = 0; p < PF; ++p) {
+            const uint32_t t = t0 + p;
+            if (t < tokens) {
+                float pp = 0.0f;
+#pragma unroll
+                for (uint32_t i = 0; i < NR; ++i) {
+                    s[i] *= gb[p];
+                    pp += s[i] * kb[p][i];
+                }
+                const float pred = row16_sum(pp);
+                const float delta = bb[p] * (vb[p] - pred);
+                float op = 0.0f;
+#pragma unroll
+                for (uint32_t i = 0; i < NR; ++i) {
+                    s[i] += kb[p][i] * delta;
+                    op += s[i] * qb[p][i];
+                }
+                const float o = row16_sum(op);
+                if (r == 0) out[static_cast<size_t>(t) * ldo + h * D + col] = o * qscale;
+                if (t + PF < tokens) load(t + PF, kb[p], qb[p], vb[p], gb[p], bb[p]);
+            }
         }
-        const float pred = row16_sum(pp);
-        const float delta = bc * (vc - pred);
-        float op = 0.0f;
-#pragma unroll
-        for (uint32_t i = 0; i < NR; ++i) {
-            s[i] += kc[i] * delta;
-            op += s[i] * qc[i];
-        }
-        const float o = row16_sum(op);
-        if (r == 0) out[static_cast<size_t>(t) * ldo + h * D + col] = o * qscale;
-#pragma unroll
-        for (uint32_t i = 0; i < NR; ++i) kc[i] = kn[i], qc[i] = qn[i];
-        vc = vn, gc = gn, bc = bn;
     }
 #pragma unroll
     for (uint32_t i = 0; i < NR; ++i) S[static_cast<size_t>(r * NR + i) * D + col] = s[i];
