@@ -797,15 +797,18 @@ int launch_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, hip
 }
 
 // K splits: enough blocks for about two per CU (one for the LDS tiles, which
-// hold two blocks per CU at most), each split at least four 128-k steps long.
+// hold two blocks per CU at most), each split at least two 128-k steps long
+// (the X tile is double-buffered over steps). Grids of a few tiles (the
+// qwen35moe projections of short prompts: 1 to 64 tiles of 2048-long rows)
+// take up to eight splits where four 128-k steps per split allowed four.
 uint32_t gemm_default_splits(uint32_t m, uint32_t n, uint32_t k, int tile) {
     const uint32_t bn[6] = {128, 128, 256, 256, 128, 128}, bm[6] = {32, 64, 64, 128, 128, 256};
     const uint64_t blocks = static_cast<uint64_t>((n + bn[tile] - 1) / bn[tile]) * ((m + bm[tile] - 1) / bm[tile]);
     const uint64_t target = tile >= 4 ? 256 : 512;
     const uint32_t steps = k / kStepK;
-    if (blocks >= target * 3 / 4 || steps < 8) return 1;
+    if (blocks >= target * 3 / 4 || steps < 4) return 1;
     const uint32_t want = static_cast<uint32_t>((target + blocks - 1) / blocks);
-    return max(1u, min(want, steps / 4));
+    return max(1u, min(want, steps / 2));
 }
 
 int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* bias,
