@@ -22,8 +22,9 @@ The same JSON line carries:
   14B-shaped Q4_K_M models and a Qwen3.5-35B-A3B-shaped qwen35moe model (all
   256 experts resident) through the HipLLM handle API;
 * ``cpu_baseline``: a bounded sample of the same GEMV step on the host (the
-  oracle's CPULLM gevmt, one thread), plus the reference CPULLM's own decode
-  rate on the 0.5B-shaped model when oracle/_ref is built.
+  oracle's restatement of CPULLM's gevmt, one thread), plus the restated
+  CPULLM's decode rate on the same 7B-shaped model (a bounded sample) and the
+  GPU/CPU decode ratio.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-e2e] [--no-cpu]
                        [--no-14b] [--no-moe] [--profile-kernel gate] [--profile-reps N]
@@ -232,7 +233,9 @@ def bench_prefill_gemm(torch, cuda):
     return out
 
 
-def bench_e2e(shape_name, prompt_len, decode_steps, workdir, max_sequence=0):
+def bench_e2e(shape_name, prompt_len, decode_steps, workdir, max_sequence=0, keep_file=False):
+    """Greedy prefill + decode through the handle API; keep_file leaves the
+    synthetic GGUF in workdir (its path is in the result) for the CPU leg."""
     from myllm_amd import synth
     from myllm_amd.hipllm import HipLLM
 
@@ -264,8 +267,9 @@ def bench_e2e(shape_name, prompt_len, decode_steps, workdir, max_sequence=0):
         finally:
             model.close()
     finally:
-        os.unlink(path)
-    return {"model": shape_name, "prompt_tokens": prompt_len, "decode_steps": decode_steps,
+        if not keep_file:
+            os.unlink(path)
+    return {"model": shape_name, "path": str(path) if keep_file else None, "prompt_tokens": prompt_len, "decode_steps": decode_steps,
             "max_sequence": max_sequence or prompt_len + decode_steps + 1,
             "prefill_tok_s": prompt_len / prefill_s, "decode_tok_s": decode_steps / dec,
             "decode_ms_per_token": dec / decode_steps * 1e3,
@@ -329,10 +333,30 @@ def bench_e2e_moe(shape_name, prompt_len, decode_steps, workdir):
             "prefill_512": {"prompt_tokens": long_len, "prefill_tok_s": long_len / long_s}}
 
 
-def cpu_baseline(budget_s: float = 12.0):
-    """CPULLM's FP32 GEMV (gevmt, cpu_llm.cpp:512-526), restated in the
-    oracle, over the same four shapes on FP32 weights dequantized from the
-    same Q4_K bytes, one thread."""
+def cpu_model_name() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def cpu_baseline(budget_s: float = 12.0, qwen7b_path=None):
+    """The CPU baseline, timed on this host with one thread, as CPULLM runs
+    (it has no threads), from the oracle: the repository's own C++
+    restatement of CPULLM (cpu_llm.cpp, model.cpp), built like the reference
+    (C++17, -O2, no -march, no FP contraction).
+
+    * value: CPULLM's FP32 GEMV (gevmt, cpu_llm.cpp:512-526) over the same
+      four Q4_K GEMV shapes as the headline, on FP32 weights dequantized
+      from the same Q4_K bytes, a budget_s sample, in GB/s of the same
+      algorithmic bytes.
+    * qwen2.5-7b: the restated CPULLM end to end on the same
+      Qwen2.5-7B-shaped Q4_K_M file the GPU decodes (a bounded sample: a
+      4-token prompt and 3 greedy decode steps, generate()'s timing,
+      chat.cpp:851-871)."""
     import oracle
     from myllm_amd import synth
 
@@ -351,30 +375,37 @@ def cpu_baseline(budget_s: float = 12.0):
             done_bytes += gemv_bytes(n, k, rb)
         steps += 1
     el = time.perf_counter() - t0
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    del mats
+    cpu_model = cpu_model_name()
     out = {"value": round(done_bytes / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
            "sample": f"{steps} step(s) of the same four GEMVs (QKV, gate, up, down at Qwen2.5-7B shapes), "
                      f"the oracle's restatement of CPULLM gevmt on FP32 weights dequantized from the same Q4_K "
                      f"bytes, 1 thread of {os.cpu_count()} host cores ({cpu_model}), {el:.1f} s",
            "host_cores": os.cpu_count(), "cpu_model": cpu_model}
-    if oracle.REF_BIN.exists():
-        with tempfile.TemporaryDirectory(dir=scratch_dir()) as tmp:
-            shape = synth.SHAPES["qwen2.5-0.5b"]
-            path = synth.write_qwen2(pathlib.Path(tmp) / "c0.gguf", shape, seed=0)
-            prompt = synth.uniform_ids(4, shape.vocab, seed=0)
-            r = oracle.run_reference(path, prompt, 8, max_sequence=64, timeout=900)
-        out["reference_cpullm_qwen2.5-0.5b"] = {
-            "decode_tok_s": round(r["decode_steps"] / (r["decode_ms"] / 1e3), 4),
-            "prefill_tok_s": round(r["prompt_tokens"] / (r["prefill_ms"] / 1e3), 4),
-            "sample": "the reference's own CPULLM (oracle/_ref, built from its sources) on the Qwen2.5-0.5B-shaped "
-                      "Q4_K_M model: 4-token prompt, 7 decode steps, 1 thread"}
+    if qwen7b_path:
+        shape = synth.SHAPES["qwen2.5-7b"]
+        prompt = synth.uniform_ids(4, shape.vocab, seed=0).tolist()
+        t0 = time.perf_counter()
+        cpu = oracle.CpuOracle(qwen7b_path, 16)
+        load_s = time.perf_counter() - t0
+        try:
+            cpu.reset()
+            t0 = time.perf_counter()
+            nxt = cpu.prefill(prompt)
+            prefill_s = time.perf_counter() - t0
+            dec, steps = 0.0, 3
+            for _ in range(steps):
+                t0 = time.perf_counter()
+                nxt = cpu.decode(nxt)
+                dec += time.perf_counter() - t0
+        finally:
+            cpu.close()
+        out["qwen2.5-7b"] = {
+            "decode_tok_s": round(steps / dec, 4), "prefill_tok_s": round(len(prompt) / prefill_s, 4),
+            "load_s": round(load_s, 1), "cores": 1,
+            "sample": f"the oracle's restated CPULLM on the Qwen2.5-7B-shaped Q4_K_M model the GPU decodes: "
+                      f"{len(prompt)}-token prompt, {steps} greedy decode steps, 1 thread of {os.cpu_count()} "
+                      f"host cores ({cpu_model})"}
     return out
 
 
@@ -456,25 +487,30 @@ def main():
     log(f"[bench] prefill GEMM {gemm}")
 
     e2e = {}
-    if not args.no_e2e:
-        with tempfile.TemporaryDirectory(dir=scratch_dir()) as tmp:
+    cpu = None
+    with tempfile.TemporaryDirectory(dir=scratch_dir()) as tmp:
+        if not args.no_e2e:
             runs = [("qwen2.5-0.5b", 16, 32, 0), ("qwen2.5-7b", 128, 64, 0)]
             if not args.no_14b:
                 runs.append(("qwen2.5-14b", 128, 128, 4096))
             for name, p, d, cap in runs:
                 log(f"[bench] e2e {name}")
-                e2e[name] = bench_e2e(name, p, d, tmp, cap)
+                e2e[name] = bench_e2e(name, p, d, tmp, cap, keep_file=(name == "qwen2.5-7b" and not args.no_cpu))
                 log(f"[bench] {e2e[name]}")
             if not args.no_moe:
                 log("[bench] e2e qwen3.5-35b-a3b (all 256 experts resident)")
                 e2e["qwen3.5-35b-a3b"] = bench_e2e_moe("qwen3.5-35b-a3b", 64, 64, tmp)
                 log(f"[bench] {e2e['qwen3.5-35b-a3b']}")
-
-    cpu = None
-    if not args.no_cpu:
-        log("[bench] CPU baseline")
-        cpu = cpu_baseline()
-        log(f"[bench] CPU {cpu}")
+        if not args.no_cpu:
+            log("[bench] CPU baseline")
+            q7 = e2e.get("qwen2.5-7b", {}).pop("path", None)
+            cpu = cpu_baseline(qwen7b_path=q7)
+            if q7 and "qwen2.5-7b" in cpu:
+                cpu["qwen2.5-7b"]["gpu_over_cpu_decode"] = round(
+                    e2e["qwen2.5-7b"]["decode_tok_s"] / cpu["qwen2.5-7b"]["decode_tok_s"], 1)
+            log(f"[bench] CPU {cpu}")
+    for v in e2e.values():
+        v.pop("path", None)
 
     dom = q4["kernels"]["gate"]
     traffic = read_traffic()

@@ -460,8 +460,22 @@ size_t hipllm_max_sequence(const HipllmModel* model);
 int hipllm_uses_gpu(const HipllmModel* model);
 int hipllm_memory_stats(const HipllmModel* model, HipllmMemoryStats* out);
 const char* hipllm_device_name(const HipllmModel* model);
-int hipllm_enable_profiling(HipllmModel* model, const char* csv_path);
+/* MetalLLM::enable_profiling(csv_path, detailed_kernel_timestamps) /
+ * disable_profiling (metal_llm.h:38-40): the reference's per-forward CSV
+ * (profiler.cpp:619-632) and, with detailed != 0, its command / kernel /
+ * operation sidecars (profiler.cpp:127-174). */
+int hipllm_enable_profiling(HipllmModel* model, const char* csv_path, int detailed);
 int hipllm_disable_profiling(HipllmModel* model);
+/* The tokenizer tables of MetalModelConfig (metal_model.h:68-71), which
+ * run_interactive and make_stop_tokens read (chat.cpp:708-726, 924-931):
+ * entry i of tokenizer.ggml.tokens / tokenizer.ggml.merges (NULL past the
+ * end) and tokenizer.ggml.pre ("" when absent). The strings live as long as
+ * the model. */
+size_t hipllm_vocabulary_count(const HipllmModel* model);
+const char* hipllm_vocabulary_token(const HipllmModel* model, size_t index);
+size_t hipllm_merge_count(const HipllmModel* model);
+const char* hipllm_merge(const HipllmModel* model, size_t index);
+const char* hipllm_tokenizer_pre(const HipllmModel* model);
 /* Logits of the last prefill/decode (vocabulary_size floats, host memory). */
 int hipllm_copy_logits(const HipllmModel* model, float* out, size_t count);
 /* qwen2: 1 = batched (bf16 MFMA) prefill, 0 = token-serial prefill through
@@ -481,8 +495,19 @@ int hipllm_set_decode_graphs(HipllmModel* model, int enabled);
  * [layer_count, expert_used_count] (MoeLLM keeps them in RouteIds,
  * moe_llm.mm:2919-2925). */
 int hipllm_copy_routes(const HipllmModel* model, int32_t* out, size_t count);
+/* qwen35moe only, for parity checks of near-tie routes: with the probe on,
+ * every forward keeps the last row's router logits (and shared-expert gate
+ * logit) of each layer; hipllm_copy_router_logits reads them as
+ * [layer_count, expert_count + 1] floats. Off by default. The reference
+ * keeps them in its router scratch (encode_routes, moe_llm.mm:2642-2690). */
+int hipllm_set_route_probe(HipllmModel* model, int enabled);
+int hipllm_copy_router_logits(const HipllmModel* model, float* out, size_t count);
 /* MoeLLM::expert_cache_count (moe_llm.h:104); 0 for qwen2 models. */
 size_t hipllm_expert_cache_count(const HipllmModel* model);
+/* MoeLLM::expert_cache_stats (moe_llm.h:105, ExpertCacheStats 12-20):
+ * expert lookups since creation (tokens x routes x layers); every expert is
+ * resident, so all are hits. Zero for qwen2 models. */
+int hipllm_expert_cache_stats(const HipllmModel* model, uint64_t* hits, uint64_t* misses);
 
 #ifdef __cplusplus
 }

@@ -815,6 +815,7 @@ int launch_gdn_scan(const float* q, const float* k, size_t ldqk, const float* v,
         value_heads % key_heads != 0) {
         return kInvalidArgument;
     }
+    if (d != 64 && d != 128) return kInvalidArgument;  // state size 64 or 128
     if (ldqk < key_heads * d || ldv < value_heads * d || ldo < value_heads * d) return kInvalidArgument;
     if (tokens > 0x7fffffffull || value_heads > 0x7fffffffull) return kLengthError;
     if (value_heads > 0x7fffffffull / d) return kLengthError;

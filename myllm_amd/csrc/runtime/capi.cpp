@@ -247,10 +247,11 @@ int hipllm_create_ex(const char* path, size_t max_sequence, int device, size_t e
     return guarded([&] {
         const std::string arch = llm::GgufReader(path).config().architecture;
         auto m = std::make_unique<HipllmModel>();
+        const std::string spec = device < 0 ? std::string() : std::to_string(device);
         if (arch == "qwen35moe") {
-            m->moe = std::make_unique<llm::HipMoeLLM>(path, max_sequence, device, expert_cache_count);
+            m->moe = std::make_unique<llm::HipMoeLLM>(path, max_sequence, spec, expert_cache_count);
         } else {
-            m->dense = std::make_unique<llm::HipLLM>(path, max_sequence, device);
+            m->dense = std::make_unique<llm::HipLLM>(path, max_sequence, spec);
         }
         *out = m.release();
     });
@@ -283,7 +284,7 @@ int hipllm_decode(HipllmModel* m, int32_t id, int32_t* next) {
 }
 
 namespace {
-void fill_config(const llm::ModelConfig& c, HipllmConfig* out) {
+void fill_config(const llm::GgufModelConfig& c, HipllmConfig* out) {
         std::memset(out, 0, sizeof(*out));
         out->layer_count = c.layer_count;
         out->embedding_size = c.embedding_size;
@@ -315,7 +316,7 @@ void fill_config(const llm::ModelConfig& c, HipllmConfig* out) {
 
 int hipllm_config(const HipllmModel* m, HipllmConfig* out) {
     if (!m || !out) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_config: null argument");
-    return guarded([&] { fill_config(m->visit([](const auto& b) -> const llm::ModelConfig& { return b.config(); }), out); });
+    return guarded([&] { fill_config(m->visit([](const auto& b) -> const llm::GgufModelConfig& { return b.config(); }), out); });
 }
 
 int hipllm_inspect_gguf(const char* path, HipllmConfig* out) {
@@ -349,10 +350,34 @@ const char* hipllm_device_name(const HipllmModel* m) {
     return m ? m->visit([](const auto& b) -> const std::string& { return b.device_name(); }).c_str() : "";
 }
 
-int hipllm_enable_profiling(HipllmModel* m, const char* csv_path) {
+int hipllm_enable_profiling(HipllmModel* m, const char* csv_path, int detailed) {
     if (!m || !csv_path) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_enable_profiling: null argument");
-    return guarded([&] { m->visit([&](auto& b) { b.enable_profiling(csv_path); }); });
+    return guarded([&] { m->visit([&](auto& b) { b.enable_profiling(csv_path, detailed != 0); }); });
 }
+
+namespace {
+const llm::GgufModelConfig* config_of(const HipllmModel* m) {
+    return &m->visit([](const auto& b) -> const llm::GgufModelConfig& { return b.config(); });
+}
+}  // namespace
+
+size_t hipllm_vocabulary_count(const HipllmModel* m) { return m ? config_of(m)->vocabulary.size() : 0; }
+
+const char* hipllm_vocabulary_token(const HipllmModel* m, size_t index) {
+    if (!m) return nullptr;
+    const auto& v = config_of(m)->vocabulary;
+    return index < v.size() ? v[index].c_str() : nullptr;
+}
+
+size_t hipllm_merge_count(const HipllmModel* m) { return m ? config_of(m)->merges.size() : 0; }
+
+const char* hipllm_merge(const HipllmModel* m, size_t index) {
+    if (!m) return nullptr;
+    const auto& v = config_of(m)->merges;
+    return index < v.size() ? v[index].c_str() : nullptr;
+}
+
+const char* hipllm_tokenizer_pre(const HipllmModel* m) { return m ? config_of(m)->tokenizer_pre.c_str() : ""; }
 
 int hipllm_disable_profiling(HipllmModel* m) {
     if (!m) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_disable_profiling: null argument");
@@ -387,7 +412,27 @@ int hipllm_copy_routes(const HipllmModel* m, int32_t* out, size_t count) {
     return guarded([&] { m->moe->copy_last_routes(out, count); });
 }
 
+int hipllm_set_route_probe(HipllmModel* m, int enabled) {
+    if (!m) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_set_route_probe: null argument");
+    if (!m->moe) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_set_route_probe: not a MoE model");
+    return guarded([&] { m->moe->set_route_probe(enabled != 0); });
+}
+
+int hipllm_copy_router_logits(const HipllmModel* m, float* out, size_t count) {
+    if (!m || !out) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_copy_router_logits: null argument");
+    if (!m->moe) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_copy_router_logits: not a MoE model");
+    return guarded([&] { m->moe->copy_last_router_logits(out, count); });
+}
+
 size_t hipllm_expert_cache_count(const HipllmModel* m) { return m && m->moe ? m->moe->expert_cache_count() : 0; }
+
+int hipllm_expert_cache_stats(const HipllmModel* m, uint64_t* hits, uint64_t* misses) {
+    if (!m || !hits || !misses) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_expert_cache_stats: null argument");
+    const llm::HipExpertCacheStats s = m->moe ? m->moe->expert_cache_stats() : llm::HipExpertCacheStats{};
+    *hits = s.hits;
+    *misses = s.misses;
+    return HIPLLM_OK;
+}
 
 // ---------------------------------------------------------------- MoE kernels
 

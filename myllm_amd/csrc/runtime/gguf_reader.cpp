@@ -222,7 +222,7 @@ struct GgufReader::Impl {
     std::unordered_map<std::string, std::size_t> index;
     std::unordered_set<std::string> consumed;
     std::unordered_set<std::string> ignored;
-    ModelConfig config;
+    GgufModelConfig config;
 
     explicit Impl(const std::string& p) : path(p) {
         fd = ::open(p.c_str(), O_RDONLY);
@@ -391,7 +391,7 @@ struct GgufReader::Impl {
 GgufReader::GgufReader(const std::string& path) : impl_(std::make_unique<Impl>(path)) {}
 GgufReader::~GgufReader() = default;
 
-const ModelConfig& GgufReader::config() const noexcept { return impl_->config; }
+const GgufModelConfig& GgufReader::config() const noexcept { return impl_->config; }
 
 bool GgufReader::has_tensor(const std::string& name) const noexcept {
     return impl_->index.find(name) != impl_->index.end();

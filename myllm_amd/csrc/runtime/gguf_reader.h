@@ -41,7 +41,7 @@ std::size_t ggml_type_size(GgmlType type);
 std::size_t ggml_row_bytes(GgmlType type, std::size_t columns);
 
 // Model hyperparameters, same fields as MetalModelConfig (metal_model.h:37-72).
-struct ModelConfig {
+struct GgufModelConfig {
     std::string architecture;
     std::size_t tensor_count = 0;
     std::size_t parameter_count = 0;
@@ -94,7 +94,7 @@ public:
     GgufReader(const GgufReader&) = delete;
     GgufReader& operator=(const GgufReader&) = delete;
 
-    const ModelConfig& config() const noexcept;
+    const GgufModelConfig& config() const noexcept;
     bool has_tensor(const std::string& name) const noexcept;
 
     // Shape-checked descriptor; marks the tensor consumed (once only).

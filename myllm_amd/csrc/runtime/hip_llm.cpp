@@ -73,7 +73,7 @@ struct HipLLM::Impl {
     int device = 0;
     std::string device_name;
     hipStream_t stream = nullptr;
-    ModelConfig config;
+    GgufModelConfig config;
     std::size_t max_sequence = 0;
     std::size_t sequence_length = 0;
     bool batched_prefill = false;
@@ -174,7 +174,7 @@ void HipLLM::Impl::load(const std::string& path, std::size_t capacity, int dev) 
     hip_check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
 
     GgufReader reader(path);
-    ModelConfig cfg = reader.config();
+    GgufModelConfig cfg = reader.config();
     if (cfg.architecture != "qwen2") {
         throw std::runtime_error("HipLLM supports qwen2 GGUF models, got " + cfg.architecture);
     }
@@ -214,7 +214,7 @@ void HipLLM::Impl::load(const std::string& path, std::size_t capacity, int dev) 
 }
 
 void HipLLM::Impl::upload(GgufReader& reader) {
-    const ModelConfig& c = config;
+    const GgufModelConfig& c = config;
     const std::size_t H = c.embedding_size, F = c.feed_forward_size, V = c.vocabulary_size;
     kv_dim = c.kv_head_count * c.head_size;
     WeightArena& A = weights;
@@ -296,10 +296,17 @@ void HipLLM::Impl::upload(GgufReader& reader) {
 }
 
 void HipLLM::Impl::allocate_state() {
-    const ModelConfig& c = config;
+    const GgufModelConfig& c = config;
     const std::size_t L = c.layer_count;
     kv_cache_bytes = 2 * L * max_sequence * kv_dim * sizeof(float);
     hip_check(hipMalloc(reinterpret_cast<void**>(&kv_arena), kv_cache_bytes), "hipMalloc(KV cache)");
+    // Rows at or past the current length are never part of a result, but a
+    // fresh allocation can hold any bits (NaN/Inf from an earlier owner), so
+    // the cache starts at zero: an in-bounds read of a row past the length
+    // that is then weighted by 0 stays 0. Set once here, outside any graph
+    // capture; reset() keeps the bytes, as the reference does.
+    hip_check(hipMemsetAsync(kv_arena, 0, kv_cache_bytes, stream), "hipMemsetAsync(KV cache)");
+    hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&host_token), 64, hipHostMallocDefault), "hipHostMalloc(token)");
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&host_step), 64, hipHostMallocDefault), "hipHostMalloc(step)");
     ensure_prompt_capacity(1);
@@ -315,7 +322,7 @@ void HipLLM::Impl::ensure_prompt_capacity(std::size_t n) {
     if (host_ids) hipHostFree(host_ids);
     act_arena = nullptr;
     host_ids = nullptr;
-    const ModelConfig& c = config;
+    const GgufModelConfig& c = config;
     const std::size_t H = c.embedding_size, F = c.feed_forward_size, V = c.vocabulary_size;
     const std::size_t qkv = H + 2 * kv_dim;
     std::size_t off = 0;
@@ -390,7 +397,7 @@ void HipLLM::Impl::gemv(const DevMatrix& w, const float* x, const hipllm::XGroup
 // step); pos is used otherwise.
 void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, float* next_hidden,
                               const std::uint32_t* dpos) {
-    const ModelConfig& c = config;
+    const GgufModelConfig& c = config;
     const DevLayer& L = layers[li];
     const std::size_t H = c.embedding_size, F = c.feed_forward_size;
     const float eps = c.norm_epsilon;
@@ -445,7 +452,7 @@ void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, fl
 
 void HipLLM::Impl::token_step(const std::int32_t* device_id, std::size_t pos, bool head,
                               const std::uint32_t* dpos) {
-    const ModelConfig& c = config;
+    const GgufModelConfig& c = config;
     const std::size_t H = c.embedding_size;
     float* h = act.hidden[0];
     float* tmp = act.hidden[1];
@@ -493,7 +500,7 @@ void HipLLM::Impl::ensure_prefill_rows(std::size_t n) {
     if (pre_arena) hipFree(pre_arena);
     pre_arena = nullptr;
     pre_rows = 0;
-    const ModelConfig& c = config;
+    const GgufModelConfig& c = config;
     const std::size_t H = c.embedding_size, F = c.feed_forward_size;
     std::size_t off = 0;
     auto reserve = [&](std::size_t bytes) {
@@ -536,7 +543,7 @@ void HipLLM::Impl::gemm(const DevMatrix& w, const void* xb, const float* bias, c
 // cpu_llm.cpp:774-841): every projection is one bf16 MFMA matmul over the
 // native weights; attention is causal over the rows just written to the cache.
 void HipLLM::Impl::prefill_layer(std::size_t li, std::size_t rows, float* hidden, float* next_hidden) {
-    const ModelConfig& c = config;
+    const GgufModelConfig& c = config;
     const DevLayer& L = layers[li];
     const std::size_t H = c.embedding_size, F = c.feed_forward_size;
     const std::size_t qkv_w = H + 2 * kv_dim;
@@ -570,7 +577,7 @@ void HipLLM::Impl::prefill_layer(std::size_t li, std::size_t rows, float* hidden
 
 // Final norm, LM head and argmax on one hidden row (decode kernels).
 void HipLLM::Impl::head_step(const float* hidden_row) {
-    const ModelConfig& c = config;
+    const GgufModelConfig& c = config;
     launch_check(hipllm::launch_rmsnorm(hidden_row, output_norm, act.norm, act.normq, 1, c.embedding_size,
                                         c.norm_epsilon, stream),
                  "final RMSNorm");
@@ -579,7 +586,7 @@ void HipLLM::Impl::head_step(const float* hidden_row) {
 
 // LM head and argmax on the normalised row in act.norm / act.normq.
 void HipLLM::Impl::head_logits() {
-    const ModelConfig& c = config;
+    const GgufModelConfig& c = config;
     gemv(output, act.norm, act.normq, nullptr, nullptr, act.logits);
     launch_check(hipllm::launch_argmax(act.logits, c.vocabulary_size, act.token, act.argmax_scratch, stream),
                  "argmax");
@@ -589,7 +596,7 @@ void HipLLM::Impl::head_logits() {
 // head on the last row only (metal_llm.mm:3266-3277; cpu_llm.cpp:1019-1020).
 void HipLLM::Impl::prefill_batched(std::size_t rows) {
     ensure_prefill_rows(rows);
-    const ModelConfig& c = config;
+    const GgufModelConfig& c = config;
     const std::size_t H = c.embedding_size;
     float* h = pre.hidden[0];
     float* tmp = pre.hidden[1];
@@ -610,9 +617,19 @@ std::int32_t HipLLM::Impl::read_token() {
     return static_cast<std::int32_t>(t);
 }
 
-HipLLM::HipLLM(const std::string& gguf_path, std::size_t max_sequence, int device)
+int parse_device_spec(const std::string& spec) {
+    if (spec.empty()) return -1;
+    const std::string digits = spec.rfind("hip:", 0) == 0 ? spec.substr(4) : spec;
+    if (digits.empty() || digits.size() > 6 ||
+        digits.find_first_not_of("0123456789") != std::string::npos) {
+        throw std::invalid_argument("HIP device must be \"\", \"N\" or \"hip:N\", got \"" + spec + "\"");
+    }
+    return std::stoi(digits);
+}
+
+HipLLM::HipLLM(const std::string& gguf_path, std::size_t max_sequence, const std::string& device)
     : impl_(std::make_unique<Impl>()) {
-    impl_->load(gguf_path, max_sequence, device);
+    impl_->load(gguf_path, max_sequence, parse_device_spec(device));
 }
 
 HipLLM::~HipLLM() = default;
@@ -699,7 +716,7 @@ void HipLLM::disable_profiling() {
     }
 }
 
-const ModelConfig& HipLLM::config() const {
+const GgufModelConfig& HipLLM::config() const {
     if (!impl_) throw std::runtime_error("HIP model is not initialized");
     return impl_->config;
 }

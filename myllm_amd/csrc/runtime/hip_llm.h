@@ -14,40 +14,24 @@
 // argmax token.
 #pragma once
 
+#include "backend_types.h"
 #include "gguf_reader.h"
 
 #include <cstddef>
 #include <cstdint>
-#include <limits>
 #include <memory>
 #include <string>
 #include <vector>
 
 namespace llm {
 
-// Byte accounting returned by every backend (memory_stats.h:11-37).
-struct MemoryStats {
-    std::uint64_t weight_bytes = 0;
-    std::uint64_t kv_cache_bytes = 0;
-    std::uint64_t recurrent_state_bytes = 0;
-    std::uint64_t intermediate_bytes = 0;
-    bool intermediate_is_estimate = false;
-
-    std::uint64_t total_bytes() const noexcept {
-        const std::uint64_t mx = std::numeric_limits<std::uint64_t>::max();
-        std::uint64_t t = weight_bytes;
-        for (std::uint64_t v : {kv_cache_bytes, recurrent_state_bytes, intermediate_bytes}) {
-            if (v > mx - t) return mx;
-            t += v;
-        }
-        return t;
-    }
-};
-
 class HipLLM {
 public:
-    // device < 0 keeps the calling thread's current HIP device.
-    explicit HipLLM(const std::string& gguf_path, std::size_t max_sequence = 0, int device = -1);
+    // The third parameter is where MetalLLM takes its shader path
+    // (metal_llm.h:22-24), so run_cli's construction compiles unchanged; here
+    // it selects the device: "" (default) keeps the calling thread's current
+    // HIP device, "N" or "hip:N" picks visible device N.
+    explicit HipLLM(const std::string& gguf_path, std::size_t max_sequence = 0, const std::string& device = {});
     ~HipLLM();
 
     HipLLM(const HipLLM&) = delete;
@@ -62,7 +46,7 @@ public:
     void enable_profiling(const std::string& csv_path, bool detailed_kernel_timestamps = false);
     void disable_profiling();
 
-    const ModelConfig& config() const;
+    const GgufModelConfig& config() const;
     std::size_t position() const noexcept;
     std::size_t max_sequence() const noexcept;
     bool uses_gpu() const noexcept;

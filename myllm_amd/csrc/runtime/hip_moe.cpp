@@ -118,9 +118,10 @@ struct MoeActivations {
 
 struct HipMoeLLM::Impl {
     int device = 0;
+    std::uint64_t expert_lookups = 0;  // tokens x routes x MoE layers, all resident
     std::string device_name;
     hipStream_t stream = nullptr;
-    ModelConfig config;
+    GgufModelConfig config;
     std::size_t capacity = 0;
     std::size_t sequence_length = 0;
     std::size_t expert_cache = 0;
@@ -156,6 +157,10 @@ struct HipMoeLLM::Impl {
     bool matmul_prefill = true;  // multi-row projections as bf16 MFMA matmuls
     hipGraph_t decode_graph = nullptr;
     hipGraphExec_t decode_exec = nullptr;
+    // Route probe (parity checks): the last row's router logits and shared
+    // gate of every layer, [L, E + 1], copied after each router when on.
+    float* probe = nullptr;
+    bool probe_on = false;
 
     ~Impl() {
         if (stream) hipStreamSynchronize(stream);
@@ -167,6 +172,7 @@ struct HipMoeLLM::Impl {
         if (rope_table) hipFree(rope_table);
         if (act_arena) hipFree(act_arena);
         if (route_ids) hipFree(route_ids);
+        if (probe) hipFree(probe);
         if (host_ids) hipHostFree(host_ids);
         if (host_token) hipHostFree(host_token);
         if (stream) hipStreamDestroy(stream);
@@ -215,7 +221,7 @@ void HipMoeLLM::Impl::load(const std::string& path, std::size_t max_sequence, in
     hip_check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
 
     GgufReader reader(path);
-    const ModelConfig& c = reader.config();
+    const GgufModelConfig& c = reader.config();
     if (c.architecture != "qwen35moe") throw std::runtime_error("HipMoeLLM requires qwen35moe, got " + c.architecture);
     // require_qwen35_config (moe_model.cpp:39-80).
     if (c.layer_count == 0 || c.full_attention_interval == 0 || c.embedding_size == 0 ||
@@ -282,7 +288,7 @@ void HipMoeLLM::Impl::load(const std::string& path, std::size_t max_sequence, in
 }
 
 void HipMoeLLM::Impl::upload(GgufReader& reader) {
-    const ModelConfig& c = config;
+    const GgufModelConfig& c = config;
     WeightArena& A = weights;
     auto require = [&](std::size_t idx, std::initializer_list<GgmlType> ok, const char* what) {
         const GgmlType t = A.tensor(idx).type;
@@ -416,6 +422,11 @@ void HipMoeLLM::Impl::allocate_state() {
     recurrent_bytes = dn * (state_floats + hist_floats) * 4;
     const std::size_t bytes = align_up(kv_cache_bytes, 256) + align_up(recurrent_bytes, 256) + 256;
     hip_check(hipMalloc(&state_arena, bytes), "hipMalloc(MoE state)");
+    // The KV rows past the current length start at zero (a fresh allocation
+    // can hold NaN/Inf bits); the recurrent part is zeroed on every reset().
+    // Outside any graph capture.
+    hip_check(hipMemsetAsync(state_arena, 0, bytes, stream), "hipMemsetAsync(MoE state)");
+    hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
     float* p = static_cast<float*>(state_arena);
     for (MoeLayer& L : layers) {
         if (!L.full) continue;
@@ -808,6 +819,11 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
         proj(L.router, act.norm, act.normq, H, rows, act.rlog, ldr);
         proj(L.shexp_router, act.norm, act.normq, H, rows, act.rlog + E, ldr);
     }
+    if (probe_on) {
+        hip_check(hipMemcpyAsync(probe + li * ldr, act.rlog + (rows - 1) * ldr, ldr * 4, hipMemcpyDeviceToDevice,
+                                 stream),
+                  "hipMemcpyAsync(route probe)");
+    }
     // With the grouped launch, the expert gate/up picks the routes itself
     // (every block runs the top-k on the token's logits).
     const bool route_in_gemv = grp && E <= 256 && K <= 8 && groupable(L.gate_exps, true);
@@ -975,10 +991,10 @@ std::int32_t HipMoeLLM::Impl::read_token() {
     return static_cast<std::int32_t>(t);
 }
 
-HipMoeLLM::HipMoeLLM(const std::string& gguf_path, std::size_t max_sequence, int device,
+HipMoeLLM::HipMoeLLM(const std::string& gguf_path, std::size_t max_sequence, const std::string& device,
                      std::size_t expert_cache_count)
     : impl_(std::make_unique<Impl>()) {
-    impl_->load(gguf_path, max_sequence, device, expert_cache_count);
+    impl_->load(gguf_path, max_sequence, parse_device_spec(device), expert_cache_count);
 }
 
 HipMoeLLM::~HipMoeLLM() = default;
@@ -1012,6 +1028,7 @@ std::int32_t HipMoeLLM::prefill(const std::vector<std::int32_t>& ids) {
     m.forward(ids.size(), 0, m.act.ids);
     const std::int32_t token = m.read_token();
     m.sequence_length = ids.size();
+    m.expert_lookups += ids.size() * m.config.expert_used_count * m.layers.size();
     if (m.profile) {
         const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         std::fprintf(m.profile, "prefill,%zu,%zu,%.6f\n", ids.size(), ids.size(), ms);
@@ -1042,6 +1059,7 @@ std::int32_t HipMoeLLM::decode(std::int32_t id) {
     }
     const std::int32_t token = m.read_token();
     m.sequence_length = pos + 1;
+    m.expert_lookups += m.config.expert_used_count * m.layers.size();
     if (m.profile) {
         const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         std::fprintf(m.profile, "decode,1,%zu,%.6f\n", pos + 1, ms);
@@ -1061,6 +1079,31 @@ void HipMoeLLM::set_matmul_prefill(bool enabled) {
     impl_->matmul_prefill = enabled;
 }
 
+void HipMoeLLM::set_route_probe(bool enabled) {
+    if (!impl_) throw std::runtime_error("MoE model is not initialized");
+    Impl& m = *impl_;
+    hip_check(hipSetDevice(m.device), "hipSetDevice");
+    hip_check(hipStreamSynchronize(m.stream), "hipStreamSynchronize");
+    if (enabled && !m.probe) {
+        hip_check(hipMalloc(reinterpret_cast<void**>(&m.probe), m.layers.size() * (m.E + 1) * 4),
+                  "hipMalloc(route probe)");
+    }
+    m.drop_decode_graph();  // re-recorded with or without the probe copies
+    m.probe_on = enabled;
+}
+
+void HipMoeLLM::copy_last_router_logits(float* dst, std::size_t count) const {
+    if (!impl_) throw std::runtime_error("MoE model is not initialized");
+    const Impl& m = *impl_;
+    if (!m.probe_on) throw std::invalid_argument("the route probe is off");
+    if (count != m.layers.size() * (m.E + 1)) {
+        throw std::invalid_argument("router logits buffer must hold layers x (experts + 1) floats");
+    }
+    if (m.last_rows == 0) throw std::invalid_argument("no forward has run");
+    hip_check(hipStreamSynchronize(m.stream), "hipStreamSynchronize");
+    hip_check(hipMemcpy(dst, m.probe, count * 4, hipMemcpyDeviceToHost), "hipMemcpy(route probe)");
+}
+
 void HipMoeLLM::enable_profiling(const std::string& csv_path, bool) {
     if (!impl_) throw std::runtime_error("MoE model is not initialized");
     disable_profiling();
@@ -1076,7 +1119,7 @@ void HipMoeLLM::disable_profiling() {
     }
 }
 
-const ModelConfig& HipMoeLLM::config() const {
+const GgufModelConfig& HipMoeLLM::config() const {
     if (!impl_) throw std::runtime_error("MoE model is not initialized");
     return impl_->config;
 }
@@ -1086,6 +1129,12 @@ std::size_t HipMoeLLM::max_sequence() const noexcept { return impl_ ? impl_->cap
 bool HipMoeLLM::uses_gpu() const noexcept { return available(); }
 bool HipMoeLLM::available() const noexcept { return impl_ && impl_->weights.base() && impl_->stream; }
 std::size_t HipMoeLLM::expert_cache_count() const noexcept { return impl_ ? impl_->expert_cache : 0; }
+
+HipExpertCacheStats HipMoeLLM::expert_cache_stats() const noexcept {
+    HipExpertCacheStats s;
+    if (impl_) s.hits = impl_->expert_lookups;
+    return s;
+}
 
 const std::string& HipMoeLLM::device_name() const noexcept {
     static const std::string empty;

@@ -31,7 +31,10 @@ public:
     // (moe_llm.mm:1378-1380). expert_cache_count is accepted for interface
     // parity and validated like the reference (top-k <= n <= experts); all
     // experts are resident regardless.
-    explicit HipMoeLLM(const std::string& gguf_path, std::size_t max_sequence = 0, int device = -1,
+    // device: as HipLLM's (the position of MoeLLM's shader path,
+    // moe_llm.h:82-85), so `HipMoeLLM(path, max_sequence, {}, n)` reads like
+    // run_cli's MoeLLM construction (chat.cpp:1026-1029).
+    explicit HipMoeLLM(const std::string& gguf_path, std::size_t max_sequence = 0, const std::string& device = {},
                        std::size_t expert_cache_count = 8);
     ~HipMoeLLM();
 
@@ -47,7 +50,7 @@ public:
     void enable_profiling(const std::string& csv_path, bool detailed_kernel_timestamps = false);
     void disable_profiling();
 
-    const ModelConfig& config() const;
+    const GgufModelConfig& config() const;
     std::size_t position() const noexcept;
     std::size_t max_sequence() const noexcept;
     bool uses_gpu() const noexcept;
@@ -55,6 +58,9 @@ public:
     bool available() const noexcept;
     const std::string& device_name() const noexcept;
     std::size_t expert_cache_count() const noexcept;
+    // Expert lookups since construction: tokens x routes x MoE layers of
+    // every forward, all hits (every expert is resident).
+    HipExpertCacheStats expert_cache_stats() const noexcept;
     // Decode path: true (default) = each decode step is one replay of a
     // recorded HIP graph; false = the step's kernels are launched one by one.
     void set_decode_graphs(bool enabled);
@@ -66,6 +72,12 @@ public:
     // Expert ids chosen for the last token of the last forward, layer-major
     // [layer_count, expert_used_count] (parity checks).
     void copy_last_routes(std::int32_t* destination, std::size_t count) const;
+    // Route probe: when on, every forward keeps the router logits and the
+    // shared-expert gate logit of its last row for each layer, readable as
+    // [layer_count, expert_count + 1] floats (parity checks of near-tie
+    // routes). Off by default; switching drops the recorded decode graph.
+    void set_route_probe(bool enabled);
+    void copy_last_router_logits(float* destination, std::size_t count) const;
 
 private:
     struct Impl;

@@ -126,7 +126,15 @@ SIGNATURES = {
     "hipllm_uses_gpu": (_I, [_P]),
     "hipllm_memory_stats": (_I, [_P, ctypes.POINTER(HipllmMemoryStats)]),
     "hipllm_device_name": (ctypes.c_char_p, [_P]),
-    "hipllm_enable_profiling": (_I, [_P, ctypes.c_char_p]),
+    "hipllm_enable_profiling": (_I, [_P, ctypes.c_char_p, _I]),
+    "hipllm_set_route_probe": (_I, [_P, _I]),
+    "hipllm_copy_router_logits": (_I, [_P, _P, _S]),
+    "hipllm_vocabulary_count": (_S, [_P]),
+    "hipllm_vocabulary_token": (ctypes.c_char_p, [_P, _S]),
+    "hipllm_merge_count": (_S, [_P]),
+    "hipllm_merge": (ctypes.c_char_p, [_P, _S]),
+    "hipllm_tokenizer_pre": (ctypes.c_char_p, [_P]),
+    "hipllm_expert_cache_stats": (_I, [_P, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
     "hipllm_disable_profiling": (_I, [_P]),
     "hipllm_copy_logits": (_I, [_P, _P, _S]),
     "hipllm_set_batched_prefill": (_I, [_P, _I]),
@@ -233,8 +241,8 @@ class HipLLM:
         check(lib().hipllm_memory_stats(self._h, ctypes.byref(s)))
         return {n: getattr(s, n) for n, _ in HipllmMemoryStats._fields_}
 
-    def enable_profiling(self, csv_path) -> None:
-        check(lib().hipllm_enable_profiling(self._h, str(csv_path).encode()))
+    def enable_profiling(self, csv_path, detailed_kernel_timestamps: bool = False) -> None:
+        check(lib().hipllm_enable_profiling(self._h, str(csv_path).encode(), 1 if detailed_kernel_timestamps else 0))
 
     def disable_profiling(self) -> None:
         check(lib().hipllm_disable_profiling(self._h))
@@ -259,9 +267,40 @@ class HipLLM:
         check(lib().hipllm_copy_routes(self._h, out.ctypes.data, out.size))
         return out
 
+    def set_route_probe(self, enabled: bool) -> None:
+        check(lib().hipllm_set_route_probe(self._h, 1 if enabled else 0))
+
+    def router_logits(self) -> np.ndarray:
+        """qwen35moe with the route probe on: [layers, experts + 1] router
+        logits (last column: shared-expert gate) of the last row of the last
+        forward."""
+        L = self.config["layer_count"]
+        E = self.config["expert_count"]
+        out = np.empty((L, E + 1), dtype=np.float32)
+        check(lib().hipllm_copy_router_logits(self._h, out.ctypes.data, out.size))
+        return out
+
     @property
     def expert_cache_count(self) -> int:
         return lib().hipllm_expert_cache_count(self._h)
+
+    def expert_cache_stats(self) -> dict:
+        hits, misses = ctypes.c_uint64(), ctypes.c_uint64()
+        check(lib().hipllm_expert_cache_stats(self._h, ctypes.byref(hits), ctypes.byref(misses)))
+        return {"hits": hits.value, "misses": misses.value}
+
+    @property
+    def vocabulary(self) -> list:
+        """tokenizer.ggml.tokens as raw UTF-8 bytes per entry."""
+        return [lib().hipllm_vocabulary_token(self._h, i) for i in range(lib().hipllm_vocabulary_count(self._h))]
+
+    @property
+    def merges(self) -> list:
+        return [lib().hipllm_merge(self._h, i) for i in range(lib().hipllm_merge_count(self._h))]
+
+    @property
+    def tokenizer_pre(self) -> str:
+        return lib().hipllm_tokenizer_pre(self._h).decode()
 
 
 def generate(backend, prompt, max_new_tokens: int, stop_token_ids=(), on_step=None):

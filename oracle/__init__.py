@@ -74,6 +74,7 @@ def lib() -> ctypes.CDLL:
         L.oracle_rmsnorm.argtypes = [P, P, c.c_size_t, c.c_float]
         L.oracle_softmax.argtypes = [P, c.c_size_t]
         L.oracle_swiglu.argtypes = [P, P, c.c_size_t]
+        L.oracle_ffn.argtypes = [P, P, P, P, c.c_size_t, c.c_size_t, P]
         L.oracle_rope.argtypes = [P, c.c_size_t, c.c_size_t, c.c_float, c.c_size_t]
         L.oracle_argmax.argtypes = [P, c.c_size_t]
         L.oracle_argmax.restype = c.c_int32
@@ -162,6 +163,17 @@ def gevmt(w: np.ndarray, x: np.ndarray, bias: np.ndarray | None = None) -> np.nd
     lib().oracle_gevmt(w.ctypes.data, x.ctypes.data, None if b is None else b.ctypes.data,
                        w.shape[0], w.shape[1], y.ctypes.data)
     return y
+
+
+def ffn(wg: np.ndarray, wu: np.ndarray, wd: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """The decode-layer FFN in FP32, Wd (silu(Wg x) * (Wu x)) (cpu_llm.cpp:907-913),
+    through the function the oracle's own decode step calls."""
+    wg, wu, wd, x = (np.ascontiguousarray(a, dtype=np.float32) for a in (wg, wu, wd, x))
+    f, h = wg.shape
+    assert wu.shape == (f, h) and wd.shape == (h, f) and x.shape == (h,)
+    out = np.empty(h, dtype=np.float32)
+    lib().oracle_ffn(wg.ctypes.data, wu.ctypes.data, wd.ctypes.data, x.ctypes.data, h, f, out.ctypes.data)
+    return out
 
 
 def generate(model, prompt, max_new_tokens: int, stop_token_ids=(), logits_sink=None):

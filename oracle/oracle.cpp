@@ -575,6 +575,16 @@ void prefill_layer(OracleModel& M, size_t li, std::vector<float>& hidden, size_t
 }
 
 // cpu_decode_layer, cpu_llm.cpp:843-914.
+// The decode FFN of cpu_decode_layer (cpu_llm.cpp:907-913): gate and up
+// products of the normalised row, SwiGLU, down product.
+void ffn_swiglu(const float* wg, const float* wu, const float* wd, const float* x, size_t H, size_t F, float* out) {
+    std::vector<float> G(F), U(F);
+    gevmt(wg, x, nullptr, F, H, G.data());
+    gevmt(wu, x, nullptr, F, H, U.data());
+    swiglu(G.data(), U.data(), F);
+    gevmt(wd, G.data(), nullptr, H, F, out);
+}
+
 void decode_layer(OracleModel& M, size_t li, std::vector<float>& hidden) {
     const OracleConfig& c = M.cfg;
     const Layer& L = M.layers[li];
@@ -621,11 +631,8 @@ void decode_layer(OracleModel& M, size_t li, std::vector<float>& hidden) {
     for (size_t i = 0; i < H; ++i) X[i] = hidden[i] + O[i];
     std::vector<float> Fn = X;
     rmsnorm(Fn.data(), L.ffn_norm.data(), H, c.norm_epsilon);
-    std::vector<float> G(F), U(F), Dn(H);
-    gevmt(L.wg.data(), Fn.data(), nullptr, F, H, G.data());
-    gevmt(L.wu.data(), Fn.data(), nullptr, F, H, U.data());
-    swiglu(G.data(), U.data(), F);
-    gevmt(L.wd.data(), G.data(), nullptr, H, F, Dn.data());
+    std::vector<float> Dn(H);
+    ffn_swiglu(L.wg.data(), L.wu.data(), L.wd.data(), Fn.data(), H, F, Dn.data());
     for (size_t i = 0; i < H; ++i) hidden[i] = X[i] + Dn[i];
 }
 
@@ -766,6 +773,9 @@ void oracle_gevmt(const float* w, const float* x, const float* bias, size_t rows
 void oracle_rmsnorm(float* x, const float* g, size_t n, float eps) { rmsnorm(x, g, n, eps); }
 void oracle_softmax(float* x, size_t n) { softmax(x, n); }
 void oracle_swiglu(float* g, const float* u, size_t n) { swiglu(g, u, n); }
+void oracle_ffn(const float* wg, const float* wu, const float* wd, const float* x, size_t h, size_t f, float* out) {
+    ffn_swiglu(wg, wu, wd, x, h, f, out);
+}
 void oracle_rope(float* x, size_t len, size_t position, float theta, size_t rot) { rope(x, len, position, theta, rot); }
 int32_t oracle_argmax(const float* x, size_t n) { return greedy(x, n); }
 

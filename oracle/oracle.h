@@ -78,6 +78,10 @@ void oracle_gevmt(const float* w, const float* x, const float* bias, size_t rows
 void oracle_rmsnorm(float* x, const float* gamma, size_t n, float eps);
 void oracle_softmax(float* x, size_t n);
 void oracle_swiglu(float* gate, const float* up, size_t n);
+/* The decode-layer FFN (cpu_llm.cpp:907-913) on a normalised row x[h]:
+ * out[h] = Wd (silu(Wg x) * (Wu x)), weights row-major [f, h], [f, h], [h, f];
+ * the same function the oracle's decode step calls. */
+void oracle_ffn(const float* wg, const float* wu, const float* wd, const float* x, size_t h, size_t f, float* out);
 void oracle_rope(float* x, size_t len, size_t position, float theta, size_t rot);
 int32_t oracle_argmax(const float* x, size_t n);
 

@@ -11,8 +11,12 @@ fed the same bytes), and the reference's greedy tokens and logits are stored:
   steps.
 * ``qwen2.5-0.5b_golden.npz``: the Qwen2.5-0.5B-shaped Q4_K_M model; 16-token
   prompt, 32 greedy tokens, and the top-64 (index, logit) pairs of every step.
+* ``qwen2.5-7b_golden.npz``: the Qwen2.5-7B-shaped Q4_K_M model (28 layers,
+  hidden 3584, FFN 18944); 8-token prompt, 16 greedy tokens, top-64 pairs of
+  every step. Bounded so the reference's single-threaded CPULLM finishes in
+  minutes (it holds about 35 GB of FP32 weights and file image).
 
-Usage: python tests/golden/make_golden.py [--only tiny|qwen2.5-0.5b]
+Usage: python tests/golden/make_golden.py [--only tiny|qwen2.5-0.5b|qwen2.5-7b]
 """
 
 from __future__ import annotations
@@ -37,6 +41,8 @@ CASES = {
                  tokens=32, max_sequence=0, full_logits=True),
     "qwen2.5-0.5b": dict(shape="qwen2.5-0.5b", types="q4_k_m", seed=0, prompt_seed=0,
                          prompt_len=16, tokens=32, max_sequence=64, full_logits=False),
+    "qwen2.5-7b": dict(shape="qwen2.5-7b", types="q4_k_m", seed=0, prompt_seed=3,
+                       prompt_len=8, tokens=16, max_sequence=32, full_logits=False),
 }
 
 
@@ -82,5 +88,5 @@ if __name__ == "__main__":
     ap.add_argument("--only", choices=sorted(CASES))
     args = ap.parse_args()
     for name in CASES:
-        if args.only in (None, name):
+        if args.only == name or (args.only is None and name != "qwen2.5-7b"):
             make(name)

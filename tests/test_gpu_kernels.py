@@ -581,6 +581,60 @@ def test_attention_decode_rope_gated_matches_gate_kernel(cuda, hq, hkv, d, rot, 
     assert np.array_equal(q1.view(np.uint32), q2.view(np.uint32))
 
 
+@pytest.mark.parametrize("hq,hkv,d,length", [(14, 2, 64, 1), (14, 2, 64, 37), (14, 2, 64, 130),
+                                              (40, 8, 128, 257), (16, 2, 256, 70)])
+def test_attention_ignores_cache_rows_past_length(cuda, hq, hkv, d, length):
+    # Cache rows at or past the length are not part of the result, whatever
+    # bits they hold: with NaN / Inf there the decode (plain and fused RoPE +
+    # cache write) and prefill attention outputs equal, bit for bit, those
+    # with zeros there. A read of such a row weighted by p = 0 would turn
+    # NaN into NaN and fail this.
+    rng = np.random.default_rng(length + d)
+    kv = hkv * d
+    cap = length + 70  # the last chunk has unused rows, and a whole chunk follows
+    stride = (hq + 2 * hkv) * d
+    k0 = rng.normal(size=(cap, kv)).astype(np.float32)
+    v0 = rng.normal(size=(cap, kv)).astype(np.float32)
+    qkv = rng.normal(size=stride).astype(np.float32)
+    rows_p = min(length, 5)
+    qp = rng.normal(size=(rows_p, hq * d)).astype(np.float32)
+    ang = rng.uniform(-3.0, 3.0, size=(cap, d // 2)).astype(np.float32)
+    dtab = torch.from_numpy(np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)).to(cuda)
+    scale = float(np.float32(1.0) / np.float32(math.sqrt(d)))
+
+    def run(fill):
+        kc0, vc0 = k0.copy(), v0.copy()
+        kc0[length:] = fill
+        vc0[length:] = fill
+        res = []
+        for mode in ("decode", "fused", "prefill"):
+            kc = torch.from_numpy(kc0.copy()).to(cuda)
+            vc = torch.from_numpy(vc0.copy()).to(cuda)
+            scratch = torch.empty(kernels.attn_decode_scratch_floats(hq, d, cap), dtype=torch.float32, device=cuda)
+            if mode == "decode":
+                out = torch.empty(hq * d, dtype=torch.float32, device=cuda)
+                kernels.attn_decode(torch.from_numpy(qkv).to(cuda), kc, vc, out, None, scratch, hq, hkv, d, length,
+                                    scale)
+            elif mode == "fused":
+                out = torch.empty(hq * d, dtype=torch.float32, device=cuda)
+                # The step writes row length - 1 itself; rows past it stay poisoned.
+                kernels.attn_decode_rope(torch.from_numpy(qkv).to(cuda), dtab, d, kc, vc, out, None, scratch, hq, hkv,
+                                         d, length - 1, scale)
+            else:
+                out = torch.empty(rows_p * hq * d, dtype=torch.float32, device=cuda)
+                pos0 = length - rows_p
+                kernels.attn_prefill(torch.from_numpy(qp).to(cuda), hq * d, kc, vc, out, hq * d, rows_p, hq, hkv, d,
+                                     pos0, scale)
+            res.append(out.cpu().numpy())
+        return res
+
+    clean = run(0.0)
+    for fill in (np.nan, np.inf, -np.inf):
+        for a, b in zip(run(fill), clean):
+            assert np.isfinite(b).all()
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), fill
+
+
 @pytest.mark.parametrize("n", [1, 100, 2048, 2049, 151936])
 def test_argmax(cuda, n):
     x = synth.normal(n, 71 + n)

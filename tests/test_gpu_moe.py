@@ -726,3 +726,55 @@ def test_moe_decode_graph_matches_eager_launches(cuda, moe_tiny):
     for a, b in zip(out[True][2], out[False][2]):
         np.testing.assert_array_equal(a, b)
 
+
+
+@pytest.mark.parametrize("prompt_len", [64, 160])
+def test_moe_default_prefill_256_experts_routes_flip_only_at_near_ties(cuda, tmp_path, prompt_len):
+    # The default prompt path at 35B-A3B widths (256 experts, top-8): bf16
+    # MFMA dense projections feeding the FP32 router, the routed experts as
+    # batched GEMVs (64 rows) or, from four routed vectors per expert, as
+    # gathered bf16 matmuls (160 rows). Against the FP32 switch (whose routes
+    # and tokens equal the float64 graph's, test above), layer by layer on
+    # the prompt's last row:
+    # * the router logits agree within the bf16 bar (2e-2 of their largest);
+    # * where the top-8 sets differ, every swapped pair is a near tie that
+    #   the measured logit perturbation eps explains: an expert a kept by the
+    #   FP32 path and dropped by bf16, and b the other way round, have FP32
+    #   logits within 2 eps (a shift of at most eps each way reorders them);
+    #   layers after the first flip see different inputs and are not compared;
+    # * with no flip, the final logits agree within 2e-2 and the first token
+    #   is the same unless the FP32 top-2 margin is inside that error.
+    shape = synth.MOE_SHAPES["qwen3.5-35b-a3b-4l"]
+    path = synth.write_qwen35moe(tmp_path / "moe4l.gguf", shape, seed=6)
+    prompt = synth.uniform_ids(prompt_len, shape.vocab, seed=40 + prompt_len).tolist()
+    res = {}
+    for matmul in (True, False):
+        with HipLLM(path, prompt_len + 4) as m:
+            m.set_batched_prefill(matmul)
+            m.set_route_probe(True)
+            tok = m.prefill(prompt)
+            res[matmul] = (tok, m.logits().astype(np.float64), m.routes(),
+                           m.router_logits()[:, :shape.experts].astype(np.float64))
+    (ta, la, ra, ga), (tb, lb, rb, gb) = res[True], res[False]
+    flipped = False
+    for layer in range(shape.layers):
+        eps = np.abs(ga[layer] - gb[layer]).max()
+        print(f"layer {layer}: router logit max diff {eps:.3e} (max |logit| {np.abs(gb[layer]).max():.3e})")
+        assert eps <= 2e-2 * np.abs(gb[layer]).max()
+        a_set, b_set = set(ra[layer].tolist()), set(rb[layer].tolist())
+        if a_set == b_set:
+            continue
+        for kept in b_set - a_set:
+            for taken in a_set - b_set:
+                gap = gb[layer][kept] - gb[layer][taken]
+                print(f"  flip: fp32 keeps {kept}, bf16 takes {taken}, fp32 logit gap {gap:.3e}")
+                assert gap <= 2 * eps + 1e-6
+        flipped = True
+        break
+    if not flipped:
+        err = np.abs(la - lb).max() / np.abs(lb).max()
+        top2 = np.sort(lb)[-2:]
+        print(f"no route flip; logits rel err {err:.3e}, fp32 top-2 margin {top2[1] - top2[0]:.3e}")
+        assert err <= 2e-2
+        if top2[1] - top2[0] > 2 * np.abs(la - lb).max():
+            assert ta == tb

@@ -82,3 +82,50 @@ def test_reader_rejects_bad_tensor_type(golden_model, tmp_path):
     bad.write_bytes(bytes(data))
     with pytest.raises(RuntimeError, match="unsupported GGUF tensor type"):
         hipllm.inspect_gguf(bad)
+
+
+def tensor_info(data: bytearray, name: str) -> dict:
+    """Byte positions of one tensor-info record of a GGUF file: the name
+    string (u64 length + bytes), n_dims u32, dims u64 x n_dims, type u32,
+    offset u64."""
+    key = name.encode()
+    at = data.index(struct.pack("<Q", len(key)) + key)
+    name_at = at + 8
+    nd_at = name_at + len(key)
+    nd = struct.unpack_from("<I", data, nd_at)[0]
+    dims_at = nd_at + 4
+    dims = list(struct.unpack_from(f"<{nd}Q", data, dims_at))
+    return {"name_at": name_at, "dims_at": dims_at, "dims": dims, "type_at": dims_at + 8 * nd}
+
+
+def edited(path: pathlib.Path, dst: pathlib.Path, edit) -> pathlib.Path:
+    data = bytearray(path.read_bytes())
+    edit(data)
+    dst.write_bytes(bytes(data))
+    return dst
+
+
+def test_reader_rejects_duplicate_tensor(golden_model, tmp_path):
+    # Renaming blk.1's attention norm to blk.0's (same length) leaves two
+    # records of one name (gguf_reader.cpp, tensor index).
+    path, _ = golden_model("tiny")
+
+    def dup(d):
+        t = tensor_info(d, "blk.1.attn_norm.weight")
+        d[t["name_at"]:t["name_at"] + 5] = b"blk.0"
+
+    with pytest.raises(RuntimeError, match="duplicate GGUF tensor: blk.0.attn_norm.weight"):
+        hipllm.inspect_gguf(edited(path, tmp_path / "dup.gguf", dup))
+
+
+def test_reader_rejects_row_not_block_aligned(golden_model, tmp_path):
+    # A Q4_K tensor whose row length (dims[0]) is not a multiple of its
+    # 256-value block (metal_model.cpp:417-448 row-byte rule).
+    path, _ = golden_model("tiny")
+
+    def misalign(d):
+        t = tensor_info(d, "blk.0.attn_q.weight")
+        struct.pack_into("<Q", d, t["dims_at"], t["dims"][0] - 16)
+
+    with pytest.raises(RuntimeError, match="row is not block aligned"):
+        hipllm.inspect_gguf(edited(path, tmp_path / "misaligned.gguf", misalign))
