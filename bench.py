@@ -16,8 +16,9 @@ The same JSON line carries:
   is read from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary when
   present (see --profile-kernel);
 * ``gemv``: per-shape results for Q4_K and Q6_K;
-* ``prefill_gemm``: the bf16-MFMA prefill matmul, M in {64, 512, 2048} x
-  K 3584 x N 18944, Q4_K weights, TFLOP/s against the 2.5 PFLOP/s bf16 peak;
+* ``prefill_gemm``: the fp16-MFMA prefill matmul, M in {64, 512, 2048} x
+  K 3584 x N 18944, Q4_K weights, TFLOP/s against the 2.5 PFLOP/s dense
+  fp16/bf16 MFMA peak;
 * ``e2e``: greedy prefill and decode tok/s of synthetic Qwen2.5-0.5B-, 7B- and
   14B-shaped Q4_K_M models and a Qwen3.5-35B-A3B-shaped qwen35moe model (all
   256 experts resident) through the HipLLM handle API;
@@ -47,7 +48,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "decode tok/s + Q4_K GEMV HBM GB/s (% peak); prefill tok/s; 1 GPU"
 PEAK_HBM_GBPS = 8000.0
-PEAK_BF16_TFLOPS = 2500.0
+PEAK_F16_TFLOPS = 2500.0
 SHAPES = [("qkv", 4608, 3584), ("gate", 18944, 3584), ("up", 18944, 3584), ("down", 3584, 18944)]
 MALL_BYTES = 256 << 20
 TRAFFIC_SUMMARY = ROOT / "profiles" / "gemv_q4k_gate_3584x18944_traffic.txt"
@@ -203,17 +204,20 @@ def bench_prefill_gemm(torch, cuda):
         ws.append(w)
     out = {}
     for M in (64, 512, 2048):
-        xb = torch.randn(M, K, device=cuda).to(torch.bfloat16)
+        x = torch.randn(M, K, device=cuda)
+        xh = torch.empty(M, K, device=cuda, dtype=torch.float16)
+        xs = torch.empty(M, device=cuda)
+        kernels.to_f16(x, K, xh, xs, M, K)
         y = torch.empty(M, N, device=cuda)
-        fn = lambda i, st=None: kernels.gemm_mfma(synth.Q4_K, ws[i % copies], src.shape[1], xb, None, None, y, M, N, K,
-                                                  stream=st)
+        fn = lambda i, st=None: kernels.gemm_mfma(synth.Q4_K, ws[i % copies], src.shape[1], xh, xs, None, None, y, M, N,
+                                                  K, stream=st)
         for i in range(3):
             fn(i)
         d = time_kernel(torch, fn, 24)
         flops = 2.0 * M * N * K
         tf = flops / d / 1e12
         wbytes = N * src.shape[1] + M * K * 2 + M * N * 4
-        out[str(M)] = {"avg_us": round(d * 1e6, 2), "tflops": round(tf, 1), "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+        out[str(M)] = {"avg_us": round(d * 1e6, 2), "tflops": round(tf, 1), "frac_f16_peak": round(tf / PEAK_F16_TFLOPS, 4),
                        "gbps": round(wbytes / d / 1e9, 1)}
     del ws
     torch.cuda.empty_cache()

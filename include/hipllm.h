@@ -142,13 +142,17 @@ int hipllm_gemv_multi_norm(const HipllmGemvJob* jobs, size_t count, const float*
 int hipllm_gemv_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const float* x,
                        const void* xq, float* y, void* yq, size_t n, size_t k, int tiling, void* stream);
 
-/* xb[m, k] (bf16, row-major, ld = k) = round-to-nearest-even of the FP32
- * rows x[r * ldx + c]; the activation side-input of hipllm_gemm_mfma. */
-int hipllm_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, void* stream);
+/* The activation side-input of hipllm_gemm_mfma: per FP32 row
+ * x[r * ldx + c] a power of two xscale[r] = 2^e, e chosen so the row's largest
+ * magnitude over 2^e lies in [2^13, 2^14) (e = 0 for a zero or non-finite
+ * row), and xh[r, c] (fp16, row-major, ld = k) = x / 2^e rounded to nearest
+ * even. k % 8 == 0; x and xh 16-byte aligned. */
+int hipllm_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m, size_t k, void* stream);
 
 /* Prefill matmul Y[m, n] = X[m, k] W[n, k]^T (+ bias[n]) (+ residual[m, n])
- * with X given as bf16 (hipllm_to_bf16), W in native GGUF rows, bf16 MFMA
- * with FP32 accumulation; k % 128 == 0. `tile` < 0 picks the default, else
+ * with X given as scaled fp16 rows (hipllm_to_f16: xh, xscale), W in native
+ * GGUF rows dequantized to fp16 (|w| < 65504), fp16 MFMA with FP32
+ * accumulation; k % 128 == 0. `tile` < 0 picks the default, else
  * 0..3 = 128x32, 128x64, 256x64, 256x128 (weight rows x X rows per block),
  * 4, 5 = 128x128, 128x256 with each weight tile dequantized once into LDS
  * and shared by all four waves.
@@ -158,9 +162,9 @@ int hipllm_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, voi
  * Replaces metal_gemm_{q5_0,q8_0,q4_k,q6_k,f32} via encode_matrix_product
  * (metal_llm.metal:196-250, 621-704; metal_llm.mm:1782-1889) and CPULLM's
  * gemmt / gemmtb (cpu_llm.cpp:591-607, 631-653). */
-int hipllm_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* bias,
-                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, int splits,
-                     void* stream);
+int hipllm_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xh, const float* xscale,
+                     const float* bias, const float* residual, float* y, size_t m, size_t n, size_t k, int tile,
+                     int splits, void* stream);
 
 /* Workspace bytes hipllm_gemm needs for m rows of k values. */
 size_t hipllm_gemm_workspace_bytes(size_t m, size_t k);
@@ -301,17 +305,18 @@ size_t hipllm_route_groups_max(size_t n, size_t experts, size_t vmax);
 int hipllm_route_groups(const int32_t* ids, size_t n, size_t experts, size_t vmax, int32_t* order, int32_t* groups,
                         uint32_t* ngroups, void* stream);
 
-/* Routed expert products of several rows as the bf16 MFMA matmul
+/* Routed expert products of several rows as the fp16 MFMA matmul
  * (hipllm_gemm_mfma's tile 1): one block row per group of
  * hipllm_route_groups (vmax <= 64), each reading its expert's weight tile
  * once for all of the group's vectors: y[j, :n] = W_e x_j for every routed
- * vector j, x_j = row j / routes of xb (bf16, k values per row) or row j when
- * x_routed; max_groups launch rows (those past *ngroups exit). Replaces the
+ * vector j, x_j = row j / routes of xh (hipllm_to_f16 rows and their
+ * xscale, k values per row) or row j when x_routed; max_groups launch rows (those past *ngroups exit). Replaces the
  * per-route expert GEMMs of encode_selected_moe for a prompt
  * (moe_llm.mm:2692-2790; metal_llm.metal:1476-1521). */
-int hipllm_gemm_gather(uint32_t type, const void* w, size_t row_bytes, const void* xb, float* y, size_t n, size_t k,
-                       size_t ldy, const int32_t* order, const int32_t* groups, const uint32_t* ngroups,
-                       size_t max_groups, size_t expert_stride, size_t routes, int x_routed, void* stream);
+int hipllm_gemm_gather(uint32_t type, const void* w, size_t row_bytes, const void* xh, const float* xscale, float* y,
+                       size_t n, size_t k, size_t ldy, const int32_t* order, const int32_t* groups,
+                       const uint32_t* ngroups, size_t max_groups, size_t expert_stride, size_t routes, int x_routed,
+                       void* stream);
 
 /* Per token: softmax over `experts` logits, top-k insertion (strict '>', the
  * lower id wins ties), renormalised weights. Replaces the router tail of
@@ -478,9 +483,9 @@ const char* hipllm_merge(const HipllmModel* model, size_t index);
 const char* hipllm_tokenizer_pre(const HipllmModel* model);
 /* Logits of the last prefill/decode (vocabulary_size floats, host memory). */
 int hipllm_copy_logits(const HipllmModel* model, float* out, size_t count);
-/* qwen2: 1 = batched (bf16 MFMA) prefill, 0 = token-serial prefill through
+/* qwen2: 1 = batched (fp16 MFMA) prefill, 0 = token-serial prefill through
  * the FP32 decode kernels. qwen35moe: 1 = prompts of 16 or more rows run the
- * dense projections as bf16 MFMA matmuls (the router stays FP32), 0 = FP32
+ * dense projections as fp16 MFMA matmuls (the router stays FP32), 0 = FP32
  * GEMVs for every row count. */
 int hipllm_set_batched_prefill(HipllmModel* model, int enabled);
 

@@ -84,14 +84,16 @@ int launch_matmul_f32(const float* x, size_t ldx, const float* w, size_t ldw, fl
 size_t route_groups_max(size_t n, size_t experts, size_t vmax);
 int launch_route_groups(const int32_t* ids, size_t n, size_t experts, size_t vmax, int32_t* order, int32_t* groups,
                         uint32_t* ngroups, hipStream_t stream);
-// Expert products of several rows as the bf16 MFMA matmul, one block row per
+// Expert products of several rows as the fp16 MFMA matmul, one block row per
 // expert group (groups of at most kGatherRows vectors): y[j, :n] = W_e x_j
-// for every routed vector j of the groups, x_j = row j / routes of xb (bf16)
+// for every routed vector j of the groups, x_j = row j / routes of xb (fp16,
+// row scales xscale)
 // or row j when x_routed; max_groups launch rows (those past *ngroups exit).
 constexpr size_t kGatherRows = 64;
-int launch_gemm_gather(uint32_t type, const void* w, size_t row_bytes, const void* xb, float* y, size_t n, size_t k,
-                       size_t ldy, const int32_t* order, const int32_t* groups, const uint32_t* ngroups,
-                       size_t max_groups, size_t expert_stride, size_t routes, int x_routed, hipStream_t stream);
+int launch_gemm_gather(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* xscale, float* y,
+                       size_t n, size_t k, size_t ldy, const int32_t* order, const int32_t* groups,
+                       const uint32_t* ngroups, size_t max_groups, size_t expert_stride, size_t routes, int x_routed,
+                       hipStream_t stream);
 int launch_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row_bytes, const float* x,
                         const XGroup* xq, const float* bias, const float* residual, float* y, XGroup* yq, size_t n,
                         size_t k, size_t vectors, const int32_t* ids, size_t experts, size_t routes,
@@ -99,10 +101,11 @@ int launch_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row
 
 int gemm_default_tile(uint32_t m, uint32_t n, uint32_t k);
 uint32_t gemm_default_splits(uint32_t m, uint32_t n, uint32_t k, int tile);
-int launch_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, hipStream_t stream);
-int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* bias,
-                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, int splits,
-                     hipStream_t stream, size_t ldy = 0);
+// X rows as fp16 MFMA operands with a power-of-two scale per row (xscale[m]).
+int launch_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m, size_t k, hipStream_t stream);
+int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* xscale,
+                     const float* bias, const float* residual, float* y, size_t m, size_t n, size_t k, int tile,
+                     int splits, hipStream_t stream, size_t ldy = 0);
 int launch_attn_prefill(const float* q, size_t q_stride, const float* kcache, const float* vcache, float* out,
                         size_t out_stride, size_t rows, size_t hq, size_t hkv, size_t d, size_t pos0, float scale,
                         hipStream_t stream);

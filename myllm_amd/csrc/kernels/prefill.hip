@@ -1,5 +1,5 @@
 // Prefill matmul Y[M,N] = X[M,K] W[N,K]^T (+ bias[N]) (+ residual[M,N]) on
-// CDNA4 bf16 MFMA with FP32 accumulation, weights in native GGUF block layout.
+// CDNA4 fp16 MFMA with FP32 accumulation, weights in native GGUF block layout.
 //
 // Replaces the reference's one-thread-per-output quantized GEMMs
 // (metal_gemm_{q5_0,q8_0,q4_k,q6_k}_f32, metal_llm.metal:621-704; host
@@ -7,14 +7,20 @@
 // (cpu_llm.cpp:591-607, 631-653), which re-decode a weight row per output.
 //
 // Design:
-// * X is converted once to bf16 (to_bf16_kernel, round to nearest even).
+// * Operands are fp16 (11 significant bits, 8x finer than bf16's 8, at the
+//   same MFMA rate on gfx950). X is converted once per row
+//   (to_f16_kernel): the row is scaled by a power of two that brings its
+//   largest magnitude to [2^13, 2^14), rounded to nearest even, and the
+//   inverse power of two is kept per row (xscale) and applied to the FP32
+//   accumulator in the epilogue, so neither range nor precision depends on
+//   the row's magnitude and the scaling itself is exact.
 // * A block is 4 waves. Block tile = (4 * 32 * NSUB) weight rows x (32 * MSUB)
 //   X rows; every wave owns 32 * NSUB weight rows and all 32 * MSUB X rows.
-// * K advances in steps of 128. Each step, the X tile (bf16) is staged in LDS
+// * K advances in steps of 128. Each step, the X tile (fp16) is staged in LDS
 //   (double-buffered, one barrier per step) and every wave dequantizes its own
 //   weight rows straight from HBM into MFMA operand registers, so weights are
 //   read once per X-row tile and never pass through LDS.
-// * v_mfma_f32_32x32x16_bf16: operand lane l holds row (l % 32) and eight
+// * v_mfma_f32_32x32x16_f16: operand lane l holds row (l % 32) and eight
 //   consecutive k. Inside a 128-k step, slice s (0..7) gives lane half
 //   h = l / 32 the k range 64 G + 32 hi + 16 h + 8 p + [0, 8) with G = s >> 2,
 //   hi = (s >> 1) & 1, p = s & 1. X and W use the same map, so each MFMA sums
@@ -22,19 +28,21 @@
 //   Q4_K's low/high nibbles (hi), Q6_K's quarters, Q8_0/Q5_0's 32-blocks.
 // * Dequantized values are computed in FP32 from the reference dequantizer's
 //   scales and offsets (model.cpp:581-683), one fused multiply-add per value,
-//   and rounded once to bf16.
+//   and rounded once to fp16 (F16 weights are used as stored). Weight values
+//   must lie inside the fp16 range (|w| < 65504), as every GGUF block scale
+//   of a trained or synthetic model does by far.
 #include "common.h"
 
 namespace hipllm {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 hx8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 namespace {
 
 constexpr int kStepK = 128;
-constexpr int kLdsRow = kStepK + 8;  // bf16 per LDS row: 272 bytes, spreads rows over banks
+constexpr int kLdsRow = kStepK + 8;  // fp16 per LDS row: 272 bytes, spreads rows over banks
 
 __device__ __forceinline__ uint4 g_ld128_a4(const uint8_t* p) {
     const u32x4a4 v = *reinterpret_cast<const u32x4a4*>(p);
@@ -61,16 +69,16 @@ __device__ __forceinline__ float f16_bits(uint32_t bits) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits & 0xffffu)));
 }
 
-// bf16 pairs and fragments built from dwords: v_cvt_pk_bf16_f32 rounds two
+// fp16 pairs and fragments built from dwords: v_cvt_pk_f16_f32 rounds two
 // floats to nearest even in one instruction, and the fragment is four such
 // dwords, so no byte shuffles are needed to assemble it.
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 hx2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
     const f32x2 v = {lo, hi};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, hx2));
 }
 
 // Hides a value's known bits from the optimizer, so that byte k of a masked
@@ -82,33 +90,33 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
 }
 
 // Eight values v[i] = a * byte_i - b over the 8 bytes of (w0, w1), one fused
-// multiply-add each, rounded to bf16. Where b is a power-of-two multiple of a
+// multiply-add each, rounded to fp16. Where b is a power-of-two multiple of a
 // (Q6_K's 32 a, Q8_0's 128 d) the result equals the reference's a * (q - c)
 // exactly; for Q4_K / Q5_0 it differs from the reference's rounded product
-// minus offset by at most one FP32 rounding, far below the bf16 rounding that
+// minus offset by at most one FP32 rounding, far below the fp16 rounding that
 // follows.
-__device__ __forceinline__ bf16x8 affine8(uint32_t w0, uint32_t w1, float a, float b) {
+__device__ __forceinline__ hx8 affine8(uint32_t w0, uint32_t w1, float a, float b) {
     w0 = opaque(w0);
     w1 = opaque(w1);
-    const u32x4 u = {pack_bf16(__builtin_fmaf(a, ubyte0(w0), -b), __builtin_fmaf(a, ubyte1(w0), -b)),
-                     pack_bf16(__builtin_fmaf(a, ubyte2(w0), -b), __builtin_fmaf(a, ubyte3(w0), -b)),
-                     pack_bf16(__builtin_fmaf(a, ubyte0(w1), -b), __builtin_fmaf(a, ubyte1(w1), -b)),
-                     pack_bf16(__builtin_fmaf(a, ubyte2(w1), -b), __builtin_fmaf(a, ubyte3(w1), -b))};
-    return __builtin_bit_cast(bf16x8, u);
+    const u32x4 u = {pack_h2(__builtin_fmaf(a, ubyte0(w0), -b), __builtin_fmaf(a, ubyte1(w0), -b)),
+                     pack_h2(__builtin_fmaf(a, ubyte2(w0), -b), __builtin_fmaf(a, ubyte3(w0), -b)),
+                     pack_h2(__builtin_fmaf(a, ubyte0(w1), -b), __builtin_fmaf(a, ubyte1(w1), -b)),
+                     pack_h2(__builtin_fmaf(a, ubyte2(w1), -b), __builtin_fmaf(a, ubyte3(w1), -b))};
+    return __builtin_bit_cast(hx8, u);
 }
 
 // Eight values v[i] = a * (byte_i - 32) (Q6_K) as a * byte_i - 32 a.
-__device__ __forceinline__ bf16x8 q6_8(uint32_t w0, uint32_t w1, float a) {
+__device__ __forceinline__ hx8 q6_8(uint32_t w0, uint32_t w1, float a) {
     return affine8(w0, w1, a, 32.0f * a);
 }
 
 // Eight signed bytes times d (Q8_0: v = q * d) as d * (q + 128) - 128 d.
-__device__ __forceinline__ bf16x8 q8_8(uint32_t w0, uint32_t w1, float d) {
+__device__ __forceinline__ hx8 q8_8(uint32_t w0, uint32_t w1, float d) {
     return affine8(w0 ^ 0x80808080u, w1 ^ 0x80808080u, d, 128.0f * d);
 }
 // Per-type weight fragments. Raw holds the bytes one lane needs for one
 // 128-k step of one weight row; load() issues the global loads, slice<s>()
-// turns them into the eight bf16x8 operands (slice order above).
+// turns them into the eight hx8 operands (slice order above).
 template <uint32_t T>
 struct WTile;
 
@@ -134,7 +142,7 @@ struct WTile<kQ4_K> {
     // Slice s = 4 G + j: G picks the 64-group, j = 0, 1 the low nibbles of
     // qs dwords (x, y) / (z, w), j = 2, 3 the high nibbles.
     template <int S>
-    __device__ static __forceinline__ bf16x8 slice(const Raw& r, uint32_t kb, uint32_t) {
+    __device__ static __forceinline__ hx8 slice(const Raw& r, uint32_t kb, uint32_t) {
         constexpr int G = S >> 2, J = S & 3;
         const uint32_t j0 = (kb % 256) / 64;
         const float d = f16_bits(r.head.x);
@@ -188,7 +196,7 @@ struct WTile<kQ6_K> {
     }
     // Slice s = 4 G + 2 hi + j: quarter 2 G + hi, qs dwords (x, y) or (z, w).
     template <int S>
-    __device__ static __forceinline__ bf16x8 slice(const Raw& r, uint32_t, uint32_t) {
+    __device__ static __forceinline__ hx8 slice(const Raw& r, uint32_t, uint32_t) {
         constexpr int G = S >> 2, HI = (S >> 1) & 1, J = S & 1;
         constexpr int quarter = 2 * G + HI;
         const float d = f16_bits(r.d);
@@ -223,7 +231,7 @@ struct WTile<kQ8_0> {
         return r;
     }
     template <int S>
-    __device__ static __forceinline__ bf16x8 slice(const Raw& r, uint32_t, uint32_t) {
+    __device__ static __forceinline__ hx8 slice(const Raw& r, uint32_t, uint32_t) {
         constexpr int B = S >> 1, J = S & 1;
         const float d = f16_bits(r.d[B]);
         return J ? q8_8(r.q[B].z, r.q[B].w, d) : q8_8(r.q[B].x, r.q[B].y, d);
@@ -252,7 +260,7 @@ struct WTile<kQ5_0> {
         return r;
     }
     template <int S>
-    __device__ static __forceinline__ bf16x8 slice(const Raw& r, uint32_t, uint32_t h) {
+    __device__ static __forceinline__ hx8 slice(const Raw& r, uint32_t, uint32_t h) {
         constexpr int B = S >> 1, J = S & 1;
         const float d = f16_bits(r.d[B]);
         const float m = 16.0f * d;
@@ -288,12 +296,12 @@ struct WTile<kF32> {
         return r;
     }
     template <int S>
-    __device__ static __forceinline__ bf16x8 slice(const Raw& r, uint32_t, uint32_t) {
+    __device__ static __forceinline__ hx8 slice(const Raw& r, uint32_t, uint32_t) {
         const uint4 a = r.v[2 * S], b = r.v[2 * S + 1];
         const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        bf16x8 f;
+        hx8 f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) f[i] = static_cast<__bf16>(__uint_as_float(w[i]));
+        for (int i = 0; i < 8; ++i) f[i] = static_cast<_Float16>(__uint_as_float(w[i]));
         return f;
     }
 };
@@ -314,22 +322,17 @@ struct WTile<kF16> {
         }
         return r;
     }
+    // The stored halves are the operands themselves.
     template <int S>
-    __device__ static __forceinline__ bf16x8 slice(const Raw& r, uint32_t, uint32_t) {
-        const uint32_t w[4] = {r.v[S].x, r.v[S].y, r.v[S].z, r.v[S].w};
-        bf16x8 f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f[2 * i] = static_cast<__bf16>(f16_bits(w[i]));
-            f[2 * i + 1] = static_cast<__bf16>(f16_bits(w[i] >> 16));
-        }
-        return f;
+    __device__ static __forceinline__ hx8 slice(const Raw& r, uint32_t, uint32_t) {
+        const u32x4 u = {r.v[S].x, r.v[S].y, r.v[S].z, r.v[S].w};
+        return __builtin_bit_cast(hx8, u);
     }
 };
 
 // All eight slices of one lane's row fragment for one 128-k step.
 template <uint32_t T>
-__device__ __forceinline__ void wtile_frags(const typename WTile<T>::Raw& r, uint32_t kb, uint32_t h, bf16x8* f) {
+__device__ __forceinline__ void wtile_frags(const typename WTile<T>::Raw& r, uint32_t kb, uint32_t h, hx8* f) {
     f[0] = WTile<T>::template slice<0>(r, kb, h);
     f[1] = WTile<T>::template slice<1>(r, kb, h);
     f[2] = WTile<T>::template slice<2>(r, kb, h);
@@ -375,7 +378,9 @@ struct Gather {
 
 template <uint32_t T, int NSUB, int MSUB, bool GATHER = false>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restrict__ w, size_t row_bytes,
-                                                        const __bf16* __restrict__ xb, const float* __restrict__ bias,
+                                                        const _Float16* __restrict__ xb,
+                                                        const float* __restrict__ xscale,
+                                                        const float* __restrict__ bias,
                                                         const float* __restrict__ residual, float* __restrict__ y,
                                                         uint32_t m, uint32_t n, uint32_t k, uint32_t ldy,
                                                         uint32_t steps_per_split, const Gather gather = Gather()) {
@@ -384,7 +389,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
     constexpr int WN = 32 * NSUB;
     constexpr int BN = 4 * WN;
     constexpr int kLoads = BM * (kStepK / 8) / 256;  // 16-byte X loads per thread per step
-    __shared__ __attribute__((aligned(16))) __bf16 xs[2][BM * kLdsRow];
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][BM * kLdsRow];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = tid >> 6, lane = tid & 63;
@@ -414,7 +419,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
         wrow[ns] = w + static_cast<size_t>(r) * row_bytes;
     }
 
-    // X tile loader: thread t moves 16 bytes (8 bf16) of row t / 16 + 16 i,
+    // X tile loader: thread t moves 16 bytes (8 fp16) of row t / 16 + 16 i,
     // column chunk t % 16, for i < kLoads.
     uint4 xr[kLoads];
     auto load_x = [&](uint32_t kb) {
@@ -460,7 +465,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
     for (uint32_t st = 0; st < steps; ++st) {
         const uint32_t kb = kb0 + st * kStepK;
         const int buf = st & 1;
-        bf16x8 bf[NSUB][8];
+        hx8 bf[NSUB][8];
 #pragma unroll
         for (int ns = 0; ns < NSUB; ++ns) wtile_frags<T>(raw[ns], kb, h, bf[ns]);
         if (st + 1 < steps) {
@@ -468,16 +473,16 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
             for (int ns = 0; ns < NSUB; ++ns) raw[ns] = WT::load(wrow[ns], kb + kStepK, h);
             load_x(kb + kStepK);
         }
-        const __bf16* xt = xs[buf];
+        const _Float16* xt = xs[buf];
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             const uint32_t kc = 64 * (s >> 2) + 32 * ((s >> 1) & 1) + 16 * h + 8 * (s & 1);
 #pragma unroll
             for (int ms = 0; ms < MSUB; ++ms) {
-                const bf16x8 a = *reinterpret_cast<const bf16x8*>(&xt[(32 * ms + lr) * kLdsRow + kc]);
+                const hx8 a = *reinterpret_cast<const hx8*>(&xt[(32 * ms + lr) * kLdsRow + kc]);
 #pragma unroll
                 for (int ns = 0; ns < NSUB; ++ns) {
-                    acc[ns][ms] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bf[ns][s], acc[ns][ms], 0, 0, 0);
+                    acc[ns][ms] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bf[ns][s], acc[ns][ms], 0, 0, 0);
                 }
             }
         }
@@ -485,7 +490,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
         __syncthreads();
     }
 
-    // Epilogue: acc[ns][ms][4 g + r] = Y[m0 + 32 ms + 8 g + 4 h + r][n0 + 32 ns + lr].
+    // Epilogue: acc[ns][ms][4 g + r] = Y[m0 + 32 ms + 8 g + 4 h + r][n0 + 32 ns + lr]
+    // in units of the row's X scale (exact power of two).
     // With a K split, y already holds residual + bias (gemm_init_kernel) and
     // every split adds its partial sum with a float atomic add in L2.
     const bool split = gridDim.z > 1;
@@ -502,11 +508,14 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
                 for (int r = 0; r < 4; ++r) {
                     const uint32_t row = m0 + 32 * ms + 8 * g + 4 * h + r;
                     if (row < m) {
+                        uint32_t src = row;
+                        if constexpr (GATHER) src = gather.x_routed ? vec(row) : vec(row) / gather.routes;
+                        const float a = acc[ns][ms][4 * g + r] * xscale[src];
                         const size_t o = static_cast<size_t>(GATHER ? vec(row) : row) * ldy + col;
                         if (split) {
-                            unsafeAtomicAdd(y + o, acc[ns][ms][4 * g + r]);
+                            unsafeAtomicAdd(y + o, a);
                         } else {
-                            float v = acc[ns][ms][4 * g + r] + b;
+                            float v = a + b;
                             if (residual) v += residual[o];
                             y[o] = v;
                         }
@@ -522,7 +531,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
 // multiplies them into its own 32 * MT X rows, so each weight is converted
 // once per 128 * MT X rows instead of once per 64.
 // * Wave w dequantizes weight rows n0 + 32 w + [0, 32) (the WTile map: lane
-//   (lr, h) gets the eight bf16x8 slices of row lr, half h) and stores slice
+//   (lr, h) gets the eight hx8 slices of row lr, half h) and stores slice
 //   s at ws[buf][w][s][lane], 16 bytes per lane: a wave's reads and writes of
 //   one slice are 1 KiB contiguous, free of bank conflicts.
 // * X fragments are loaded from global memory straight into registers with
@@ -537,13 +546,14 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
 //   (two blocks per CU); MT = 2 runs one.
 template <uint32_t T, int MT>
 __global__ __launch_bounds__(256, MT == 1 ? 2 : 1) void gemm_lds_kernel(const uint8_t* __restrict__ w, size_t row_bytes,
-                                                          const __bf16* __restrict__ xb,
+                                                          const _Float16* __restrict__ xb,
+                                                          const float* __restrict__ xscale,
                                                           const float* __restrict__ bias,
                                                           const float* __restrict__ residual, float* __restrict__ y,
                                                           uint32_t m, uint32_t n, uint32_t k, uint32_t ldy,
                                                           uint32_t steps_per_split) {
     using WT = WTile<T>;
-    __shared__ bf16x8 ws[2][4][8][64];
+    __shared__ hx8 ws[2][4][8][64];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = tid >> 6, lane = tid & 63;
@@ -554,16 +564,16 @@ __global__ __launch_bounds__(256, MT == 1 ? 2 : 1) void gemm_lds_kernel(const ui
     const uint32_t mw = mb * (128 * MT) + wave * (32 * MT);  // this wave's first X row
 
     const uint8_t* wrow = w + static_cast<size_t>(min(n0 + 32 * wave + lr, n - 1)) * row_bytes;
-    const __bf16* xrow[MT];
+    const _Float16* xrow[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) xrow[mt] = xb + static_cast<size_t>(min(mw + 32 * mt + lr, m - 1)) * k;
-    auto load_x = [&](uint32_t kb, bf16x8 (&xa)[MT][8]) {
+    auto load_x = [&](uint32_t kb, hx8 (&xa)[MT][8]) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
                 const uint32_t kc = 64 * (s >> 2) + 32 * ((s >> 1) & 1) + 16 * h + 8 * (s & 1);
-                xa[mt][s] = *reinterpret_cast<const bf16x8*>(xrow[mt] + kb + kc);
+                xa[mt][s] = *reinterpret_cast<const hx8*>(xrow[mt] + kb + kc);
             }
         }
     };
@@ -579,13 +589,13 @@ __global__ __launch_bounds__(256, MT == 1 ? 2 : 1) void gemm_lds_kernel(const ui
     const uint32_t kb0 = blockIdx.z * steps_per_split * kStepK;
     const uint32_t steps = min(steps_per_split, k / kStepK - blockIdx.z * steps_per_split);
     const uint32_t klast = kb0 + (steps - 1) * kStepK;  // loads past the split re-read its last step
-    bf16x8 xa[MT][8];
+    hx8 xa[MT][8];
     load_x(kb0, xa);
     typename WT::Raw rawn;
     {
         const typename WT::Raw raw = WT::load(wrow, kb0, h);
         rawn = WT::load(wrow, min(kb0 + kStepK, klast), h);
-        bf16x8 f[8];
+        hx8 f[8];
         wtile_frags<T>(raw, kb0, h, f);
 #pragma unroll
         for (int s = 0; s < 8; ++s) ws[0][wave][s][lane] = f[s];
@@ -594,7 +604,7 @@ __global__ __launch_bounds__(256, MT == 1 ? 2 : 1) void gemm_lds_kernel(const ui
 
     // One pipeline step. cur: this step's X fragments; nxt receives step
     // st + 1's. rn: step st + 1's weight bytes; r2 receives step st + 2's.
-    auto body = [&](uint32_t st, bf16x8 (&cur)[MT][8], bf16x8 (&nxt)[MT][8], const typename WT::Raw& rn,
+    auto body = [&](uint32_t st, hx8 (&cur)[MT][8], hx8 (&nxt)[MT][8], const typename WT::Raw& rn,
                     typename WT::Raw& r2) {
         const uint32_t kb = kb0 + st * kStepK;
         const int buf = st & 1;
@@ -604,7 +614,7 @@ __global__ __launch_bounds__(256, MT == 1 ? 2 : 1) void gemm_lds_kernel(const ui
         // slice s of the next step's tile dequantized and stored, with the
         // next slice's weight fragments read ahead. A scheduling fence per
         // slice keeps each slice's VALU work beside its MFMAs.
-        bf16x8 bcur[4], bnxt[4];
+        hx8 bcur[4], bnxt[4];
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) bcur[nt] = ws[buf][nt][0][lane];
         auto slice_step = [&](auto sc) {
@@ -617,7 +627,7 @@ __global__ __launch_bounds__(256, MT == 1 ? 2 : 1) void gemm_lds_kernel(const ui
             for (int nt = 0; nt < 4; ++nt) {
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
-                    acc[nt][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[mt][S], bcur[nt], acc[nt][mt], 0, 0, 0);
+                    acc[nt][mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[mt][S], bcur[nt], acc[nt][mt], 0, 0, 0);
                 }
             }
             ws[buf ^ 1][wave][S][lane] = WT::template slice<S>(rn, kb + kStepK, h);  // unused after the last step
@@ -639,7 +649,7 @@ __global__ __launch_bounds__(256, MT == 1 ? 2 : 1) void gemm_lds_kernel(const ui
     };
     // Two steps per iteration with the register sets swapped, so nothing is
     // copied between steps.
-    bf16x8 xb2[MT][8];
+    hx8 xb2[MT][8];
     typename WT::Raw rawm;
     for (uint32_t st = 0; st < steps; st += 2) {
         body(st, xa, xb2, rawn, rawm);
@@ -661,11 +671,12 @@ __global__ __launch_bounds__(256, MT == 1 ? 2 : 1) void gemm_lds_kernel(const ui
                 for (int r = 0; r < 4; ++r) {
                     const uint32_t row = mw + 32 * mt + 8 * g + 4 * h + r;
                     if (row < m) {
+                        const float a = acc[nt][mt][4 * g + r] * xscale[row];
                         const size_t o = static_cast<size_t>(row) * ldy + col;
                         if (split) {
-                            unsafeAtomicAdd(y + o, acc[nt][mt][4 * g + r]);
+                            unsafeAtomicAdd(y + o, a);
                         } else {
-                            float v = acc[nt][mt][4 * g + r] + b;
+                            float v = a + b;
                             if (residual) v += residual[o];
                             y[o] = v;
                         }
@@ -687,31 +698,50 @@ __global__ void gemm_init_kernel(float* __restrict__ y, uint32_t ldy, const floa
     y[o] = (residual ? residual[o] : 0.0f) + (bias ? bias[c] : 0.0f);
 }
 
-// xb[r, c] = bf16(x[r * ldx + c]) for r < m, c < k (round to nearest even).
-__global__ void to_bf16_kernel(const float* __restrict__ x, size_t ldx, __bf16* __restrict__ xb, uint32_t m,
-                               uint32_t k) {
-    const uint32_t groups = k / 8;
-    const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (idx >= static_cast<size_t>(m) * groups) return;
-    const uint32_t r = static_cast<uint32_t>(idx / groups);
-    const uint32_t c = static_cast<uint32_t>(idx % groups) * 8;
-    const float4 a = *reinterpret_cast<const float4*>(x + r * ldx + c);
-    const float4 b = *reinterpret_cast<const float4*>(x + r * ldx + c + 4);
-    bf16x8 v;
-    v[0] = static_cast<__bf16>(a.x);
-    v[1] = static_cast<__bf16>(a.y);
-    v[2] = static_cast<__bf16>(a.z);
-    v[3] = static_cast<__bf16>(a.w);
-    v[4] = static_cast<__bf16>(b.x);
-    v[5] = static_cast<__bf16>(b.y);
-    v[6] = static_cast<__bf16>(b.z);
-    v[7] = static_cast<__bf16>(b.w);
-    *reinterpret_cast<bf16x8*>(xb + static_cast<size_t>(r) * k + c) = v;
+// Row r of x as fp16 operands: xh[r, c] = fp16(x[r, c] * 2^-e) (round to
+// nearest even) and xscale[r] = 2^e, with e chosen so the row's largest
+// magnitude lands in [2^13, 2^14): far from fp16 overflow (65504) and with
+// the row's significant values in the normal range. Both scalings are exact
+// powers of two (e is kept in [-126, 127], so 2^-e stays finite). NaN values
+// are left out of the maximum and stay NaN; a row of zeros, or one holding
+// an Inf, keeps e = 0 (the non-finite values then reach the output as they
+// would in FP32). One 256-thread block per row.
+__global__ __launch_bounds__(256) void to_f16_kernel(const float* __restrict__ x, size_t ldx,
+                                                     _Float16* __restrict__ xh, float* __restrict__ xscale,
+                                                     uint32_t k) {
+    const uint32_t r = blockIdx.x;
+    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(r) * ldx);
+    const uint32_t k4 = k / 4;
+    float mx = 0.0f;
+    for (uint32_t i = threadIdx.x; i < k4; i += 256) {
+        const float4 v = xr[i];
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    __shared__ float red[4];
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e = 0;
+    if (mx > 0.0f && mx <= 3.402823466e38f) {
+        frexpf(mx, &e);  // mx = f 2^e, f in [0.5, 1)
+        e = max(-126, min(127, e - 14));
+    }
+    const float down = ldexpf(1.0f, -e);
+    if (threadIdx.x == 0) xscale[r] = ldexpf(1.0f, e);
+    _Float16* dst = xh + static_cast<size_t>(r) * k;
+    for (uint32_t i = threadIdx.x; i < k / 8; i += 256) {
+        const float4 a = xr[2 * i], b = xr[2 * i + 1];
+        const u32x4 u = {pack_h2(a.x * down, a.y * down), pack_h2(a.z * down, a.w * down),
+                         pack_h2(b.x * down, b.y * down), pack_h2(b.z * down, b.w * down)};
+        *reinterpret_cast<u32x4*>(dst + 8 * i) = u;
+    }
 }
 
 template <uint32_t T, int NSUB, int MSUB>
-void launch_tile(const void* w, size_t row_bytes, const __bf16* xb, const float* bias, const float* residual, float* y,
-                 uint32_t m, uint32_t n, uint32_t k, uint32_t ldy, uint32_t splits, hipStream_t stream) {
+void launch_tile(const void* w, size_t row_bytes, const _Float16* xb, const float* xscale, const float* bias,
+                 const float* residual, float* y, uint32_t m, uint32_t n, uint32_t k, uint32_t ldy, uint32_t splits,
+                 hipStream_t stream) {
     constexpr uint32_t BN = 4 * 32 * NSUB, BM = 32 * MSUB;
     const uint32_t steps = k / kStepK;
     const uint32_t per = (steps + splits - 1) / splits;
@@ -723,23 +753,24 @@ void launch_tile(const void* w, size_t row_bytes, const __bf16* xb, const float*
     }
     const dim3 grid(((n + BN - 1) / BN) * ((m + BM - 1) / BM), 1, splits);
     hipLaunchKernelGGL((gemm_mfma_kernel<T, NSUB, MSUB>), grid, dim3(256), 0, stream,
-                       static_cast<const uint8_t*>(w), row_bytes, xb, bias, residual, y, m, n, k, ldy, per);
+                       static_cast<const uint8_t*>(w), row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, per);
 }
 
 // The gathered expert products: tile 1 (64 rows x 128 weight rows per
 // block, matching groups of at most 64 vectors), no K split.
 template <uint32_t T>
-void launch_gather(const void* w, size_t row_bytes, const __bf16* xb, float* y, uint32_t n, uint32_t k, uint32_t ldy,
-                   uint32_t max_groups, const Gather& g, hipStream_t stream) {
+void launch_gather(const void* w, size_t row_bytes, const _Float16* xb, const float* xscale, float* y, uint32_t n,
+                   uint32_t k, uint32_t ldy, uint32_t max_groups, const Gather& g, hipStream_t stream) {
     constexpr uint32_t BN = 4 * 32;
     const dim3 grid((n + BN - 1) / BN, max_groups, 1);
     hipLaunchKernelGGL((gemm_mfma_kernel<T, 1, 2, true>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w),
-                       row_bytes, xb, nullptr, nullptr, y, 0u, n, k, ldy, k / kStepK, g);
+                       row_bytes, xb, xscale, nullptr, nullptr, y, 0u, n, k, ldy, k / kStepK, g);
 }
 
 template <uint32_t T, int MT>
-void launch_lds(const void* w, size_t row_bytes, const __bf16* xb, const float* bias, const float* residual, float* y,
-                uint32_t m, uint32_t n, uint32_t k, uint32_t ldy, uint32_t splits, hipStream_t stream) {
+void launch_lds(const void* w, size_t row_bytes, const _Float16* xb, const float* xscale, const float* bias,
+                const float* residual, float* y, uint32_t m, uint32_t n, uint32_t k, uint32_t ldy, uint32_t splits,
+                hipStream_t stream) {
     constexpr uint32_t BN = 128, BM = 128 * MT;
     const uint32_t steps = k / kStepK;
     const uint32_t per = (steps + splits - 1) / splits;
@@ -751,20 +782,20 @@ void launch_lds(const void* w, size_t row_bytes, const __bf16* xb, const float* 
     }
     const dim3 grid(((n + BN - 1) / BN) * ((m + BM - 1) / BM), 1, splits);
     hipLaunchKernelGGL((gemm_lds_kernel<T, MT>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w),
-                       row_bytes, xb, bias, residual, y, m, n, k, ldy, per);
+                       row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, per);
 }
 
 template <uint32_t T>
-int launch_typed(int tile, const void* w, size_t row_bytes, const __bf16* xb, const float* bias,
-                 const float* residual, float* y, uint32_t m, uint32_t n, uint32_t k, uint32_t ldy, uint32_t splits,
-                 hipStream_t stream) {
+int launch_typed(int tile, const void* w, size_t row_bytes, const _Float16* xb, const float* xscale,
+                 const float* bias, const float* residual, float* y, uint32_t m, uint32_t n, uint32_t k, uint32_t ldy,
+                 uint32_t splits, hipStream_t stream) {
     switch (tile) {
-    case 4: launch_lds<T, 1>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, splits, stream); break;
-    case 5: launch_lds<T, 2>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, splits, stream); break;
-    case 0: launch_tile<T, 1, 1>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, splits, stream); break;
-    case 1: launch_tile<T, 1, 2>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, splits, stream); break;
-    case 2: launch_tile<T, 2, 2>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, splits, stream); break;
-    case 3: launch_tile<T, 2, 4>(w, row_bytes, xb, bias, residual, y, m, n, k, ldy, splits, stream); break;
+    case 4: launch_lds<T, 1>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, stream); break;
+    case 5: launch_lds<T, 2>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, stream); break;
+    case 0: launch_tile<T, 1, 1>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, stream); break;
+    case 1: launch_tile<T, 1, 2>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, stream); break;
+    case 2: launch_tile<T, 2, 2>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, stream); break;
+    case 3: launch_tile<T, 2, 4>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, stream); break;
     default: return kInvalidArgument;
     }
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
@@ -784,15 +815,12 @@ int gemm_default_tile(uint32_t m, uint32_t, uint32_t k) {
     return k >= 8192 ? 4 : 1;
 }
 
-int launch_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, hipStream_t stream) {
-    if (!x || !xb || m == 0 || k == 0 || k % 8 != 0 || ldx < k || ldx % 4 != 0) return kInvalidArgument;
-    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(xb) % 16 != 0) return kInvalidArgument;
-    if (m > 0xffffffffull || k > 0xffffffffull) return kLengthError;
-    const size_t total = m * (k / 8);
-    const size_t blocks = (total + 255) / 256;
-    if (blocks > 0x7fffffffull) return kLengthError;
-    hipLaunchKernelGGL(to_bf16_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, stream, x, ldx,
-                       static_cast<__bf16*>(xb), static_cast<uint32_t>(m), static_cast<uint32_t>(k));
+int launch_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m, size_t k, hipStream_t stream) {
+    if (!x || !xh || !xscale || m == 0 || k == 0 || k % 8 != 0 || ldx < k || ldx % 4 != 0) return kInvalidArgument;
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(xh) % 16 != 0) return kInvalidArgument;
+    if (m > 0x7fffffffull || k > 0xffffffffull) return kLengthError;
+    hipLaunchKernelGGL(to_f16_kernel, dim3(static_cast<uint32_t>(m)), dim3(256), 0, stream, x, ldx,
+                       static_cast<_Float16*>(xh), xscale, static_cast<uint32_t>(k));
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
@@ -811,11 +839,11 @@ uint32_t gemm_default_splits(uint32_t m, uint32_t n, uint32_t k, int tile) {
     return max(1u, min(want, steps / 2));
 }
 
-int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* bias,
-                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, int splits,
-                     hipStream_t stream, size_t ldy) {
+int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* xscale,
+                     const float* bias, const float* residual, float* y, size_t m, size_t n, size_t k, int tile,
+                     int splits, hipStream_t stream, size_t ldy) {
     if (ldy == 0) ldy = n;
-    if (!w || !xb || !y || m == 0 || n == 0 || k == 0 || ldy < n || ldy > 0x7fffffffull) return kInvalidArgument;
+    if (!w || !xb || !xscale || !y || m == 0 || n == 0 || k == 0 || ldy < n || ldy > 0x7fffffffull) return kInvalidArgument;
     if (k % kStepK != 0) return kInvalidArgument;
     if (m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull) return kLengthError;
     if (((n + 127) / 128) * ((m + 31) / 32) > 0x7fffffffull) return kLengthError;  // one grid row of tiles
@@ -834,22 +862,23 @@ int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void*
     const uint32_t M = static_cast<uint32_t>(m), N = static_cast<uint32_t>(n), K = static_cast<uint32_t>(k);
     if (splits < 0 || splits > 1024) return kInvalidArgument;
     const uint32_t S = splits == 0 ? gemm_default_splits(M, N, K, tile) : static_cast<uint32_t>(splits);
-    const auto* x = static_cast<const __bf16*>(xb);
+    const auto* x = static_cast<const _Float16*>(xb);
     switch (type) {
-    case kQ4_K: return launch_typed<kQ4_K>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
-    case kQ6_K: return launch_typed<kQ6_K>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
-    case kQ8_0: return launch_typed<kQ8_0>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
-    case kQ5_0: return launch_typed<kQ5_0>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
-    case kF32: return launch_typed<kF32>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
-    case kF16: return launch_typed<kF16>(tile, w, row_bytes, x, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
+    case kQ4_K: return launch_typed<kQ4_K>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
+    case kQ6_K: return launch_typed<kQ6_K>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
+    case kQ8_0: return launch_typed<kQ8_0>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
+    case kQ5_0: return launch_typed<kQ5_0>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
+    case kF32: return launch_typed<kF32>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
+    case kF16: return launch_typed<kF16>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
     default: return kInvalidArgument;
     }
 }
 
-int launch_gemm_gather(uint32_t type, const void* w, size_t row_bytes, const void* xb, float* y, size_t n, size_t k,
-                       size_t ldy, const int32_t* order, const int32_t* groups, const uint32_t* ngroups,
-                       size_t max_groups, size_t expert_stride, size_t routes, int x_routed, hipStream_t stream) {
-    if (!w || !xb || !y || !order || !groups || !ngroups || n == 0 || k == 0 || max_groups == 0 || routes == 0 ||
+int launch_gemm_gather(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* xscale, float* y,
+                       size_t n, size_t k, size_t ldy, const int32_t* order, const int32_t* groups,
+                       const uint32_t* ngroups, size_t max_groups, size_t expert_stride, size_t routes, int x_routed,
+                       hipStream_t stream) {
+    if (!w || !xb || !xscale || !y || !order || !groups || !ngroups || n == 0 || k == 0 || max_groups == 0 || routes == 0 ||
         ldy < n) {
         return kInvalidArgument;
     }
@@ -879,16 +908,16 @@ int launch_gemm_gather(uint32_t type, const void* w, size_t row_bytes, const voi
     g.expert_stride = expert_stride;
     g.routes = static_cast<uint32_t>(routes);
     g.x_routed = x_routed ? 1u : 0u;
-    const auto* x = static_cast<const __bf16*>(xb);
+    const auto* x = static_cast<const _Float16*>(xb);
     const uint32_t N = static_cast<uint32_t>(n), K = static_cast<uint32_t>(k), L = static_cast<uint32_t>(ldy);
     const uint32_t G = static_cast<uint32_t>(max_groups);
     switch (type) {
-    case kQ4_K: launch_gather<kQ4_K>(w, row_bytes, x, y, N, K, L, G, g, stream); break;
-    case kQ6_K: launch_gather<kQ6_K>(w, row_bytes, x, y, N, K, L, G, g, stream); break;
-    case kQ8_0: launch_gather<kQ8_0>(w, row_bytes, x, y, N, K, L, G, g, stream); break;
-    case kQ5_0: launch_gather<kQ5_0>(w, row_bytes, x, y, N, K, L, G, g, stream); break;
-    case kF32: launch_gather<kF32>(w, row_bytes, x, y, N, K, L, G, g, stream); break;
-    default: launch_gather<kF16>(w, row_bytes, x, y, N, K, L, G, g, stream); break;
+    case kQ4_K: launch_gather<kQ4_K>(w, row_bytes, x, xscale, y, N, K, L, G, g, stream); break;
+    case kQ6_K: launch_gather<kQ6_K>(w, row_bytes, x, xscale, y, N, K, L, G, g, stream); break;
+    case kQ8_0: launch_gather<kQ8_0>(w, row_bytes, x, xscale, y, N, K, L, G, g, stream); break;
+    case kQ5_0: launch_gather<kQ5_0>(w, row_bytes, x, xscale, y, N, K, L, G, g, stream); break;
+    case kF32: launch_gather<kF32>(w, row_bytes, x, xscale, y, N, K, L, G, g, stream); break;
+    default: launch_gather<kF16>(w, row_bytes, x, xscale, y, N, K, L, G, g, stream); break;
     }
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }

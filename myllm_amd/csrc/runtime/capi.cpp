@@ -156,27 +156,29 @@ int hipllm_gemv_multi_norm(const HipllmGemvJob* jobs, size_t count, const float*
                   "failure");
 }
 
-int hipllm_to_bf16(const float* x, size_t ldx, void* xb, size_t m, size_t k, void* stream) {
-    return status(hipllm::launch_to_bf16(x, ldx, xb, m, k, as_stream(stream)),
-                  "hipllm_to_bf16: invalid arguments (k % 8 == 0, 16-byte aligned buffers) or launch failure");
+int hipllm_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m, size_t k, void* stream) {
+    return status(hipllm::launch_to_f16(x, ldx, xh, xscale, m, k, as_stream(stream)),
+                  "hipllm_to_f16: invalid arguments (k % 8 == 0, 16-byte aligned buffers) or launch failure");
 }
 
-int hipllm_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* bias,
-                     const float* residual, float* y, size_t m, size_t n, size_t k, int tile, int splits,
-                     void* stream) {
-    return status(hipllm::launch_gemm_mfma(type, w, row_bytes, xb, bias, residual, y, m, n, k, tile, splits,
+int hipllm_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xh, const float* xscale,
+                     const float* bias, const float* residual, float* y, size_t m, size_t n, size_t k, int tile,
+                     int splits, void* stream) {
+    return status(hipllm::launch_gemm_mfma(type, w, row_bytes, xh, xscale, bias, residual, y, m, n, k, tile, splits,
                                            as_stream(stream)),
                   "hipllm_gemm_mfma: invalid arguments (k % 128 == 0, tile -1..5, splits 0..1024) or launch failure");
 }
 
-size_t hipllm_gemm_workspace_bytes(size_t m, size_t k) { return (m * k * 2 + 255) / 256 * 256; }
+// Workspace: the fp16 rows (256-byte aligned), then the row scales.
+size_t hipllm_gemm_workspace_bytes(size_t m, size_t k) { return (m * k * 2 + 255) / 256 * 256 + (m * 4 + 255) / 256 * 256; }
 
 int hipllm_gemm(uint32_t type, const void* w, size_t row_bytes, const float* x, size_t ldx, const float* bias,
                 float* y, size_t m, size_t n, size_t k, void* workspace, void* stream) {
     if (!workspace) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_gemm: workspace is null");
-    const int rc = hipllm::launch_to_bf16(x, ldx, workspace, m, k, as_stream(stream));
+    float* xscale = reinterpret_cast<float*>(static_cast<char*>(workspace) + (m * k * 2 + 255) / 256 * 256);
+    const int rc = hipllm::launch_to_f16(x, ldx, workspace, xscale, m, k, as_stream(stream));
     if (rc != hipllm::kOk) return status(rc, "hipllm_gemm: invalid activation arguments");
-    return status(hipllm::launch_gemm_mfma(type, w, row_bytes, workspace, bias, nullptr, y, m, n, k, -1, 0,
+    return status(hipllm::launch_gemm_mfma(type, w, row_bytes, workspace, xscale, bias, nullptr, y, m, n, k, -1, 0,
                                            as_stream(stream)),
                   "hipllm_gemm: invalid arguments (k % 128 == 0) or launch failure");
 }
@@ -488,11 +490,12 @@ int hipllm_route_groups(const int32_t* ids, size_t n, size_t experts, size_t vma
                   "hipllm_route_groups: invalid arguments (n <= 16384, experts <= 1024) or launch failure");
 }
 
-int hipllm_gemm_gather(uint32_t type, const void* w, size_t row_bytes, const void* xb, float* y, size_t n, size_t k,
-                       size_t ldy, const int32_t* order, const int32_t* groups, const uint32_t* ngroups,
-                       size_t max_groups, size_t expert_stride, size_t routes, int x_routed, void* stream) {
-    return status(hipllm::launch_gemm_gather(type, w, row_bytes, xb, y, n, k, ldy, order, groups, ngroups, max_groups,
-                                             expert_stride, routes, x_routed, as_stream(stream)),
+int hipllm_gemm_gather(uint32_t type, const void* w, size_t row_bytes, const void* xh, const float* xscale, float* y,
+                       size_t n, size_t k, size_t ldy, const int32_t* order, const int32_t* groups,
+                       const uint32_t* ngroups, size_t max_groups, size_t expert_stride, size_t routes, int x_routed,
+                       void* stream) {
+    return status(hipllm::launch_gemm_gather(type, w, row_bytes, xh, xscale, y, n, k, ldy, order, groups, ngroups,
+                                             max_groups, expert_stride, routes, x_routed, as_stream(stream)),
                   "hipllm_gemm_gather: invalid arguments (k % 128 == 0, max_groups <= 65535, alignment) or launch "
                   "failure");
 }

@@ -64,7 +64,8 @@ struct PrefillActivations {
     float* attn = nullptr;                  // [T, H]
     float* gate = nullptr;                  // [T, F]
     float* up = nullptr;                    // [T, F]
-    void* xb = nullptr;                     // bf16 [T, max(H, F)]
+    void* xb = nullptr;                     // fp16 [T, max(H, F)] matmul operands
+    float* xscale = nullptr;                // [T] their row scales
 };
 
 }  // namespace
@@ -511,7 +512,7 @@ void HipLLM::Impl::ensure_prefill_rows(std::size_t n) {
     const std::size_t o_h0 = reserve(n * H * 4), o_h1 = reserve(n * H * 4), o_norm = reserve(n * H * 4),
                       o_qkv = reserve(n * (H + 2 * kv_dim) * 4), o_attn = reserve(n * H * 4),
                       o_gate = reserve(n * F * 4), o_up = reserve(n * F * 4),
-                      o_xb = reserve(n * std::max(H, F) * 2);
+                      o_xb = reserve(n * std::max(H, F) * 2), o_xs = reserve(n * 4);
     pre_bytes = off;
     hip_check(hipMalloc(&pre_arena, pre_bytes), "hipMalloc(prefill activations)");
     auto* base = static_cast<std::uint8_t*>(pre_arena);
@@ -523,6 +524,7 @@ void HipLLM::Impl::ensure_prefill_rows(std::size_t n) {
     pre.gate = reinterpret_cast<float*>(base + o_gate);
     pre.up = reinterpret_cast<float*>(base + o_up);
     pre.xb = base + o_xb;
+    pre.xscale = reinterpret_cast<float*>(base + o_xs);
     pre_rows = n;
 }
 
@@ -534,13 +536,13 @@ bool HipLLM::Impl::batched_shapes() const {
 void HipLLM::Impl::gemm(const DevMatrix& w, const void* xb, const float* bias, const float* residual, float* y,
                         std::size_t rows, std::size_t ldy, std::size_t n_override) const {
     const std::size_t n = n_override ? n_override : w.rows;
-    launch_check(hipllm::launch_gemm_mfma(w.type, w.ptr, w.row_bytes, xb, bias, residual, y, rows, n, w.cols, -1,
-                                          0, stream, ldy),
+    launch_check(hipllm::launch_gemm_mfma(w.type, w.ptr, w.row_bytes, xb, pre.xscale, bias, residual, y, rows, n,
+                                          w.cols, -1, 0, stream, ldy),
                  "prefill matmul");
 }
 
 // One decoder layer over `rows` prompt rows (cpu_prefill_layer,
-// cpu_llm.cpp:774-841): every projection is one bf16 MFMA matmul over the
+// cpu_llm.cpp:774-841): every projection is one fp16 MFMA matmul over the
 // native weights; attention is causal over the rows just written to the cache.
 void HipLLM::Impl::prefill_layer(std::size_t li, std::size_t rows, float* hidden, float* next_hidden) {
     const GgufModelConfig& c = config;
@@ -549,7 +551,7 @@ void HipLLM::Impl::prefill_layer(std::size_t li, std::size_t rows, float* hidden
     const std::size_t qkv_w = H + 2 * kv_dim;
     const float eps = c.norm_epsilon;
     launch_check(hipllm::launch_rmsnorm(hidden, L.attn_norm, pre.norm, nullptr, rows, H, eps, stream), "RMSNorm");
-    launch_check(hipllm::launch_to_bf16(pre.norm, H, pre.xb, rows, H, stream), "bf16 activations");
+    launch_check(hipllm::launch_to_f16(pre.norm, H, pre.xb, pre.xscale, rows, H, stream), "fp16 activations");
     if (L.fused_qkv) {
         gemm(L.q, pre.xb, L.qkv_bias, nullptr, pre.qkv, rows, qkv_w, qkv_w);
     } else {
@@ -564,14 +566,14 @@ void HipLLM::Impl::prefill_layer(std::size_t li, std::size_t rows, float* hidden
     launch_check(hipllm::launch_attn_prefill(pre.qkv, qkv_w, kcache(li), vcache(li), pre.attn, H, rows,
                                              c.attention_head_count, c.kv_head_count, c.head_size, 0, scale, stream),
                  "prefill attention");
-    launch_check(hipllm::launch_to_bf16(pre.attn, H, pre.xb, rows, H, stream), "bf16 activations");
+    launch_check(hipllm::launch_to_f16(pre.attn, H, pre.xb, pre.xscale, rows, H, stream), "fp16 activations");
     gemm(L.o, pre.xb, nullptr, hidden, next_hidden, rows, H);
     launch_check(hipllm::launch_rmsnorm(next_hidden, L.ffn_norm, pre.norm, nullptr, rows, H, eps, stream), "RMSNorm");
-    launch_check(hipllm::launch_to_bf16(pre.norm, H, pre.xb, rows, H, stream), "bf16 activations");
+    launch_check(hipllm::launch_to_f16(pre.norm, H, pre.xb, pre.xscale, rows, H, stream), "fp16 activations");
     gemm(L.gate, pre.xb, nullptr, nullptr, pre.gate, rows, F);
     gemm(L.up, pre.xb, nullptr, nullptr, pre.up, rows, F);
     launch_check(hipllm::launch_swiglu(pre.gate, pre.up, pre.gate, nullptr, rows * F, stream), "SwiGLU");
-    launch_check(hipllm::launch_to_bf16(pre.gate, F, pre.xb, rows, F, stream), "bf16 activations");
+    launch_check(hipllm::launch_to_f16(pre.gate, F, pre.xb, pre.xscale, rows, F, stream), "fp16 activations");
     gemm(L.down, pre.xb, nullptr, next_hidden, hidden, rows, H);
 }
 

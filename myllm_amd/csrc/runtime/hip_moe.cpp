@@ -28,7 +28,7 @@
 namespace llm {
 namespace {
 
-// From this many rows on, the dense projections of a forward run as bf16
+// From this many rows on, the dense projections of a forward run as fp16
 // MFMA matmuls (the weights are read once per 64-row tile instead of once per
 // row).
 constexpr std::size_t kMatmulRows = 16;
@@ -97,7 +97,8 @@ struct MoeActivations {
     float* sh_act = nullptr;                // [T, FFs]
     hipllm::XGroup* sh_actq = nullptr;
     float* sh_gate = nullptr;               // [T, FFs] shared gate projection (prefill matmul form)
-    void* xb = nullptr;                     // [T, max(H, inner, Hq D, FFs)] bf16 matmul input
+    void* xb = nullptr;                     // [T, max(H, inner, Hq D, FFs)] fp16 matmul input
+    float* xscale = nullptr;                // [T] its row scales
     float* sh_down = nullptr;               // [T, H]
     float* logits = nullptr;                // [V]
     float* attn_scratch = nullptr;
@@ -109,7 +110,8 @@ struct MoeActivations {
     std::int32_t* route_groups = nullptr;   // [route_groups_max(T k, E, 64)][2] expert groups
     std::uint32_t* route_ngroups = nullptr;
     float* gate_act = nullptr;              // [T k, FF] expert gate products (prefill matmul path)
-    void* act_b = nullptr;                  // [T k, FF] bf16 SwiGLU outputs for the expert down matmul
+    void* act_b = nullptr;                  // [T k, FF] fp16 SwiGLU outputs for the expert down matmul
+    float* act_bscale = nullptr;            // [T k] their row scales
     float* mm_scratch = nullptr;            // router matmul partial sums (K split)
     std::size_t mm_scratch_floats = 0;
 };
@@ -154,7 +156,7 @@ struct HipMoeLLM::Impl {
     // One decode step recorded as a HIP graph (kernels read the token and
     // position from act.step) and replayed per token.
     bool decode_graphs = true;
-    bool matmul_prefill = true;  // multi-row projections as bf16 MFMA matmuls
+    bool matmul_prefill = true;  // multi-row projections as fp16 MFMA matmuls
     hipGraph_t decode_graph = nullptr;
     hipGraphExec_t decode_exec = nullptr;
     // Route probe (parity checks): the last row's router logits and shared
@@ -188,7 +190,7 @@ struct HipMoeLLM::Impl {
     void proj(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, std::size_t ldx, std::size_t rows, float* y,
               std::size_t ldy, const float* residual = nullptr, std::size_t n_override = 0,
               const void* xb = nullptr) const;
-    const void* bf16_rows(const float* x, std::size_t ldx, std::size_t k, std::size_t rows) const;
+    const void* f16_rows(const float* x, std::size_t ldx, std::size_t k, std::size_t rows) const;
     void proj_out_norm(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, std::size_t ldx,
                        std::size_t rows, float* next, const float* hidden, const float* gamma, bool norm) const;
     void grouped(const hipllm::GemvJob* jobs, std::size_t count, const float* x, const float* gamma,
@@ -515,6 +517,7 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
                       o_ord = reserve(n * K),
                       o_grp = reserve(2 * hipllm::route_groups_max(n * K, E, hipllm::kGatherRows)),
                       o_ngr = reserve(1), o_gact = reserve(n * K * FF), o_actb = reserve((n * K * FF + 1) / 2),
+                      o_xs = reserve(n), o_abs = reserve(n * K),
                       o_mms = reserve(mm_floats);
     act_bytes = off;
     hip_check(hipMalloc(&act_arena, act_bytes), "hipMalloc(MoE activations)");
@@ -544,6 +547,7 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
     act.sh_actq = g(o_shaq);
     act.sh_gate = f(o_shg);
     act.xb = b + o_xb;
+    act.xscale = f(o_xs);
     act.sh_down = f(o_shd);
     act.logits = f(o_logits);
     act.attn_scratch = f(o_as);
@@ -556,6 +560,7 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
     act.route_ngroups = reinterpret_cast<std::uint32_t*>(b + o_ngr);
     act.gate_act = f(o_gact);
     act.act_b = b + o_actb;
+    act.act_bscale = f(o_abs);
     act.mm_scratch = f(o_mms);
     act.mm_scratch_floats = mm_floats;
     hip_check(hipMalloc(reinterpret_cast<void**>(&route_ids), layers.size() * n * K * 4), "hipMalloc(routes)");
@@ -569,9 +574,10 @@ void HipMoeLLM::Impl::proj(const DevMatrix& w, const float* x, const hipllm::XGr
                            const void* xb) const {
     const std::size_t n = n_override ? n_override : w.rows;
     if (xb) {
-        // Prefill rows through the bf16 MFMA matmul (xb: bf16_rows of x).
-        launch_check(hipllm::launch_gemm_mfma(w.type, w.ptr, w.row_bytes, xb, nullptr, residual, y, rows, n, w.cols, -1,
-                                              0, stream, ldy),
+        // Prefill rows through the fp16 MFMA matmul (xb: f16_rows of x, row
+        // scales in act.xscale).
+        launch_check(hipllm::launch_gemm_mfma(w.type, w.ptr, w.row_bytes, xb, act.xscale, nullptr, residual, y, rows, n,
+                                              w.cols, -1, 0, stream, ldy),
                      "prefill matmul");
         return;
     }
@@ -586,13 +592,14 @@ void HipMoeLLM::Impl::proj(const DevMatrix& w, const float* x, const hipllm::XGr
                  "batched GEMV");
 }
 
-// The bf16 copy of `rows` rows of x (k values, ld ldx) that the prefill
-// matmul reads, in act.xb; nullptr when the rows go through the GEMV forms
+// The fp16 copy of `rows` rows of x (k values, ld ldx) that the prefill
+// matmul reads, in act.xb (row scales in act.xscale); nullptr when the rows go
+// through the GEMV forms
 // (few rows, or k not a multiple of the matmul's 128-k step). One copy per
 // input: every projection of the same rows shares it until the next call.
-const void* HipMoeLLM::Impl::bf16_rows(const float* x, std::size_t ldx, std::size_t k, std::size_t rows) const {
+const void* HipMoeLLM::Impl::f16_rows(const float* x, std::size_t ldx, std::size_t k, std::size_t rows) const {
     if (!matmul_prefill || rows < kMatmulRows || k % 128 != 0) return nullptr;
-    launch_check(hipllm::launch_to_bf16(x, ldx, act.xb, rows, k, stream), "bf16 activations");
+    launch_check(hipllm::launch_to_f16(x, ldx, act.xb, act.xscale, rows, k, stream), "fp16 activations");
     return act.xb;
 }
 
@@ -602,7 +609,7 @@ const void* HipMoeLLM::Impl::bf16_rows(const float* x, std::size_t ldx, std::siz
 void HipMoeLLM::Impl::proj_out_norm(const DevMatrix& w, const float* x, const hipllm::XGroup* xq, std::size_t ldx,
                                     std::size_t rows, float* next, const float* hidden, const float* gamma,
                                     bool norm) const {
-    proj(w, x, xq, ldx, rows, next, H, hidden, 0, bf16_rows(x, ldx, w.cols, rows));
+    proj(w, x, xq, ldx, rows, next, H, hidden, 0, f16_rows(x, ldx, w.cols, rows));
     if (!norm) return;
     launch_check(hipllm::launch_rmsnorm(next, gamma, act.norm, act.normq, rows, H, config.norm_epsilon, stream),
                  "RMSNorm");
@@ -644,8 +651,8 @@ bool HipMoeLLM::Impl::grouped_mixer(const MoeLayer& L, std::size_t rows) const {
     return groupable(L.qkv) && groupable(L.z) && L.fused_ab && groupable(L.alpha);
 }
 
-// Whether layer L's routed experts run as gathered bf16 matmuls: a prompt
-// whose dense projections already run as matmuls (xb holds its bf16 rows)
+// Whether layer L's routed experts run as gathered fp16 matmuls: a prompt
+// whose dense projections already run as matmuls (xb holds its fp16 rows)
 // and routes at least four vectors per expert on average. Each group block
 // dequantizes a whole weight tile for its vectors, so with fewer the batched
 // GEMV is faster (qwen35moe prefill, 256 experts top-8: 64 tokens 3.06k
@@ -684,7 +691,7 @@ void HipMoeLLM::Impl::attention_layer(std::size_t li, std::size_t rows, std::siz
         }
         grouped(jobs, nj, hidden, L.attn_norm, false, "input norm + Q/gate + K/V");
     } else {
-        const void* xb = bf16_rows(act.norm, H, H, rows);
+        const void* xb = f16_rows(act.norm, H, H, rows);
         proj(L.qgate, act.norm, act.normq, H, rows, act.wide, 2 * q_w, nullptr, 0, xb);
         if (L.fused_kv) {
             proj(L.k, act.norm, act.normq, H, rows, act.kv, 2 * kv_w, nullptr, 2 * kv_w, xb);
@@ -728,7 +735,7 @@ void HipMoeLLM::Impl::deltanet_layer(std::size_t li, std::size_t rows, float* hi
                                          job(L.alpha, act.ab, 2 * Hv)};
         grouped(jobs, 3, hidden, L.attn_norm, false, "input norm + DeltaNet QKV / z / alpha, beta");
     } else {
-        const void* xb = bf16_rows(act.norm, H, H, rows);
+        const void* xb = f16_rows(act.norm, H, H, rows);
         proj(L.qkv, act.norm, act.normq, H, rows, act.wide, qkv_w, nullptr, 0, xb);
         proj(L.z, act.norm, act.normq, H, rows, act.feat, inner, nullptr, 0, xb);
         if (L.fused_ab) {
@@ -784,7 +791,7 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
     std::int32_t* ids = route_ids + li * act_rows * K;
     // Router logits and the shared-expert gate in one GEMV when packed.
     // The router logits stay FP32 (GEMV forms) in every path: top-k is
-    // discontinuous, and bf16 rounding of the logits would flip near-tie
+    // discontinuous, and fp16 rounding of the logits would flip near-tie
     // routes.
     const std::size_t ldr = E + 1;
     const bool grp = grouped_moe(L, rows);
@@ -831,7 +838,7 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
         launch_check(hipllm::launch_router_topk(act.rlog, ldr, rows, E, K, ids, act.rweight, stream),
                      "router top-k");
     }
-    const void* xb = bf16_rows(act.norm, H, H, rows);
+    const void* xb = f16_rows(act.norm, H, H, rows);
     // Routed experts: gate/up + SwiGLU (and its XGroup form) for every
     // (row, route), then down.
     if (route_in_gemv) {
@@ -842,25 +849,26 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
                      "router top-k + expert gate/up");
     } else if (gathered_experts(L, rows, xb)) {
         // A prompt: the routed vectors grouped by expert (up to 64 per group)
-        // and each group multiplied as a bf16 MFMA matmul that reads its
+        // and each group multiplied as an fp16 MFMA matmul that reads its
         // expert's weights once, gate and up, SwiGLU, then down.
         const std::size_t nv = rows * K, mg = hipllm::route_groups_max(nv, E, hipllm::kGatherRows);
         launch_check(hipllm::launch_route_groups(ids, nv, E, hipllm::kGatherRows, act.route_order, act.route_groups,
                                                  act.route_ngroups, stream),
                      "route groups");
-        auto gather = [&](const DevMatrix& w, const void* x, float* y, std::size_t n, std::size_t k, int routed,
-                          const char* what) {
-            launch_check(hipllm::launch_gemm_gather(w.type, w.ptr, w.row_bytes, x, y, n, k, n, act.route_order,
+        auto gather = [&](const DevMatrix& w, const void* x, const float* xs, float* y, std::size_t n, std::size_t k,
+                          int routed, const char* what) {
+            launch_check(hipllm::launch_gemm_gather(w.type, w.ptr, w.row_bytes, x, xs, y, n, k, n, act.route_order,
                                                     act.route_groups, act.route_ngroups, mg, w.expert_stride, K,
                                                     routed, stream),
                          what);
         };
-        gather(L.gate_exps, xb, act.gate_act, FF, H, 0, "expert gate (matmul)");
-        gather(L.up_exps, xb, act.act, FF, H, 0, "expert up (matmul)");
+        gather(L.gate_exps, xb, act.xscale, act.gate_act, FF, H, 0, "expert gate (matmul)");
+        gather(L.up_exps, xb, act.xscale, act.act, FF, H, 0, "expert up (matmul)");
         launch_check(hipllm::launch_swiglu(act.gate_act, act.act, act.act, act.actq, nv * FF, stream),
                      "expert SwiGLU");
-        launch_check(hipllm::launch_to_bf16(act.act, FF, act.act_b, nv, FF, stream), "expert bf16 activations");
-        gather(L.down_exps, act.act_b, act.down, H, FF, 1, "expert down (matmul)");
+        launch_check(hipllm::launch_to_f16(act.act, FF, act.act_b, act.act_bscale, nv, FF, stream),
+                     "expert fp16 activations");
+        gather(L.down_exps, act.act_b, act.act_bscale, act.down, H, FF, 1, "expert down (matmul)");
     } else {
         launch_check(hipllm::launch_gemv_batched(L.gate_exps.type, L.gate_exps.ptr, L.up_exps.ptr,
                                                  L.gate_exps.row_bytes, act.norm, act.normq, nullptr, nullptr,
@@ -906,7 +914,7 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
                      "shared down");
     } else {
         proj(L.sh_down, act.sh_act, act.sh_actq, FFs, rows, act.sh_down, H, nullptr, 0,
-             bf16_rows(act.sh_act, FFs, FFs, rows));
+             f16_rows(act.sh_act, FFs, FFs, rows));
     }
     if (next_norm) {
         launch_check(hipllm::launch_moe_combine_norm(hidden, act.down, act.rweight, act.sh_down, act.rlog + E, ldr,

@@ -65,7 +65,7 @@ public:
     // recorded HIP graph; false = the step's kernels are launched one by one.
     void set_decode_graphs(bool enabled);
     // Prefill of 16 or more rows: true (default) = the dense projections run
-    // as bf16 MFMA matmuls (the router stays FP32); false = FP32 GEMVs only.
+    // as fp16 MFMA matmuls (the router stays FP32); false = FP32 GEMVs only.
     void set_matmul_prefill(bool enabled);
 
     void copy_last_logits(float* destination, std::size_t count) const;

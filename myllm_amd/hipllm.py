@@ -73,8 +73,8 @@ SIGNATURES = {
     "hipllm_gemv_swiglu": (_I, [_U32, _P, _P, _S, _P, _P, _P, _P, _S, _S, _I, _P]),
     "hipllm_gemv_norm": (_I, [_U32, _P, _S, _P, _P, _F, _P, _P, _P, _S, _S, _I, _P]),
     "hipllm_gemv_swiglu_norm": (_I, [_U32, _P, _P, _S, _P, _P, _F, _P, _P, _S, _S, _I, _P]),
-    "hipllm_to_bf16": (_I, [_P, _S, _P, _S, _S, _P]),
-    "hipllm_gemm_mfma": (_I, [_U32, _P, _S, _P, _P, _P, _P, _S, _S, _S, _I, _I, _P]),
+    "hipllm_to_f16": (_I, [_P, _S, _P, _P, _S, _S, _P]),
+    "hipllm_gemm_mfma": (_I, [_U32, _P, _S, _P, _P, _P, _P, _P, _S, _S, _S, _I, _I, _P]),
     "hipllm_gemm_workspace_bytes": (_S, [_S, _S]),
     "hipllm_gemm": (_I, [_U32, _P, _S, _P, _S, _P, _P, _S, _S, _S, _P, _P]),
     "hipllm_rmsnorm": (_I, [_P, _P, _P, _P, _S, _S, _F, _P]),
@@ -101,7 +101,7 @@ SIGNATURES = {
     "hipllm_matmul_f32_scratch_floats": (_S, [_S, _S, _S]),
     "hipllm_route_groups_max": (_S, [_S, _S, _S]),
     "hipllm_route_groups": (_I, [_P, _S, _S, _S, _P, _P, _P, _P]),
-    "hipllm_gemm_gather": (_I, [_U32, _P, _S, _P, _P, _S, _S, _S, _P, _P, _P, _S, _S, _S, _I, _P]),
+    "hipllm_gemm_gather": (_I, [_U32, _P, _S, _P, _P, _P, _S, _S, _S, _P, _P, _P, _S, _S, _S, _I, _P]),
     "hipllm_attn_decode_rope_gated": (_I, [_P, _P, _S, _P, _P, _P, _P, _P, _P, _S, _S, _S, _S, _F, _P]),
     "hipllm_gemv_routed_swiglu": (_I, [_U32, _P, _P, _S, _P, _P, _S, _P, _P, _S, _S, _S, _P, _S, _S, _S, _S, _P, _P,
                                        _P]),
@@ -367,8 +367,8 @@ def _k_gemv_swiglu(qtype, wg, wu, row_bytes, x, xq, y, yq, n, k, tiling=0, strea
                                    n, k, tiling, _stream(stream)))
 
 
-def _k_to_bf16(x, ldx, xb, m, k, stream=None):
-    check(lib().hipllm_to_bf16(_ptr(x), ldx, _ptr(xb), m, k, _stream(stream)))
+def _k_to_f16(x, ldx, xh, xscale, m, k, stream=None):
+    check(lib().hipllm_to_f16(_ptr(x), ldx, _ptr(xh), _ptr(xscale), m, k, _stream(stream)))
 
 
 def _k_gemv_norm(qtype, w, row_bytes, x, gamma, eps, bias, residual, y, n, k, tiling=0, stream=None):
@@ -381,9 +381,9 @@ def _k_gemv_swiglu_norm(qtype, wg, wu, row_bytes, x, gamma, eps, y, yq, n, k, ti
                                         _ptr(yq), n, k, tiling, _stream(stream)))
 
 
-def _k_gemm_mfma(qtype, w, row_bytes, xb, bias, residual, y, m, n, k, tile=-1, stream=None, splits=0):
-    check(lib().hipllm_gemm_mfma(qtype, _ptr(w), row_bytes, _ptr(xb), _ptr(bias), _ptr(residual), _ptr(y),
-                                 m, n, k, tile, splits, _stream(stream)))
+def _k_gemm_mfma(qtype, w, row_bytes, xh, xscale, bias, residual, y, m, n, k, tile=-1, stream=None, splits=0):
+    check(lib().hipllm_gemm_mfma(qtype, _ptr(w), row_bytes, _ptr(xh), _ptr(xscale), _ptr(bias), _ptr(residual),
+                                 _ptr(y), m, n, k, tile, splits, _stream(stream)))
 
 
 def _k_gemm(qtype, w, row_bytes, x, ldx, bias, y, m, n, k, workspace, stream=None):
@@ -413,11 +413,11 @@ def _k_route_groups(ids, n, experts, vmax, order, groups, ngroups, stream=None):
                                     _stream(stream)))
 
 
-def _k_gemm_gather(qtype, w, row_bytes, xb, y, n, k, ldy, order, groups, ngroups, max_groups, expert_stride, routes,
-                   x_routed, stream=None):
-    check(lib().hipllm_gemm_gather(qtype, _ptr(w), row_bytes, _ptr(xb), _ptr(y), n, k, ldy, _ptr(order), _ptr(groups),
-                                   _ptr(ngroups), max_groups, expert_stride, routes, 1 if x_routed else 0,
-                                   _stream(stream)))
+def _k_gemm_gather(qtype, w, row_bytes, xh, xscale, y, n, k, ldy, order, groups, ngroups, max_groups, expert_stride,
+                   routes, x_routed, stream=None):
+    check(lib().hipllm_gemm_gather(qtype, _ptr(w), row_bytes, _ptr(xh), _ptr(xscale), _ptr(y), n, k, ldy, _ptr(order),
+                                   _ptr(groups), _ptr(ngroups), max_groups, expert_stride, routes,
+                                   1 if x_routed else 0, _stream(stream)))
 
 
 def _k_router_topk(logits, ld, tokens, experts, k, ids, weights, stream=None):
@@ -555,7 +555,7 @@ def _k_swiglu(g, u, y, yq, n, stream=None):
 
 kernels = types.SimpleNamespace(
     dequant_rows=_k_dequant_rows, prep_x=_k_prep_x, gemv=_k_gemv, gemv_prepped=_k_gemv_prepped,
-    gemv_swiglu=_k_gemv_swiglu, gemv_norm=_k_gemv_norm, gemv_swiglu_norm=_k_gemv_swiglu_norm, to_bf16=_k_to_bf16, gemm_mfma=_k_gemm_mfma, gemm=_k_gemm,
+    gemv_swiglu=_k_gemv_swiglu, gemv_norm=_k_gemv_norm, gemv_swiglu_norm=_k_gemv_swiglu_norm, to_f16=_k_to_f16, gemm_mfma=_k_gemm_mfma, gemm=_k_gemm,
     gemm_workspace_bytes=lambda m, k: lib().hipllm_gemm_workspace_bytes(m, k), rmsnorm=_k_rmsnorm, embed=_k_embed, rope_kv=_k_rope_kv,
     attn_decode=_k_attn_decode, attn_decode_rope_gated=_k_attn_decode_rope_gated, argmax=_k_argmax,
     swiglu=_k_swiglu, attn_prefill=_k_attn_prefill,

@@ -26,7 +26,7 @@ def run_with_logits(model, prompt, n):
 
 
 # Token-serial prefill runs the FP32 decode kernels (bound 1e-3); the batched
-# prefill runs bf16 MFMA matmuls, whose contract bound is 2e-2 on logits.
+# prefill runs fp16 MFMA matmuls, whose contract bound is 2e-2 on logits.
 LOGIT_BOUND = {False: 1e-3, True: 2e-2}
 
 
@@ -222,7 +222,7 @@ def test_qwen14b_full_size_properties(cuda, tmp_path):
     # 128-token prompt and 128 greedy decode steps. Its CPU reference does
     # not fit a test (about 60 GB of FP32 weights, minutes per token), so the
     # checks are size-independent properties of the GPU paths:
-    # * batched (bf16 MFMA) prefill against token-serial prefill (the FP32
+    # * batched (fp16 MFMA) prefill against token-serial prefill (the FP32
     #   decode kernels): logits within 2e-2, the same first token unless the
     #   serial top-2 margin is inside that error;
     # * 128 decode steps replayed as one recorded graph per token against the

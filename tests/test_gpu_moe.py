@@ -249,10 +249,12 @@ def test_route_groups(cuda, n, E, vmax):
 
 @pytest.mark.parametrize("qtype,T,routed", [(synth.Q4_K, 40, False), (synth.Q6_K, 150, False),
                                             (synth.Q8_0, 30, True)])
-def test_gemm_gather_matches_bf16_reference(cuda, qtype, T, routed):
-    """Routed expert products as gathered bf16 matmuls against float64
-    products of the bf16-rounded operands (<= 1e-4), with experts holding
-    more than one 64-vector group (T = 150: about 75 vectors each)."""
+def test_gemm_gather_matches_f16_operand_reference(cuda, qtype, T, routed):
+    """Routed expert products as gathered fp16 matmuls against float64
+    products of the fp16 operands (the scaled rows of hipllm_to_f16, the
+    fp16-rounded weights; <= 1e-4), with experts holding more than one
+    64-vector group (T = 150: about 75 vectors each) and rows of different
+    magnitudes (the scale of each gathered row follows its source row)."""
     E, K, N, H = 8, 4, 256, 512
     rng = np.random.default_rng(T)
     w = random_rows(qtype, E * N, H, 81)
@@ -260,9 +262,11 @@ def test_gemm_gather_matches_bf16_reference(cuda, qtype, T, routed):
     rb = w.shape[1]
     nv = T * K
     xrows = nv if routed else T
-    x = torch.from_numpy(synth.normal(xrows * H, 82).reshape(xrows, H)).to(cuda)
-    xb = torch.empty(xrows, H, dtype=torch.bfloat16, device=cuda)
-    kernels.to_bf16(x, H, xb, xrows, H)
+    x = synth.normal(xrows * H, 82).reshape(xrows, H) * np.exp2(rng.integers(-10, 11, size=(xrows, 1)))
+    x = torch.from_numpy(x.astype(np.float32)).to(cuda)
+    xb = torch.empty(xrows, H, dtype=torch.float16, device=cuda)
+    xs = torch.empty(xrows, dtype=torch.float32, device=cuda)
+    kernels.to_f16(x, H, xb, xs, xrows, H)
     ids = torch.from_numpy(rng.integers(0, E, size=nv).astype(np.int32)).to(cuda)
     mg = kernels.route_groups_max(nv, E, 64)
     order = torch.empty(nv, dtype=torch.int32, device=cuda)
@@ -270,30 +274,33 @@ def test_gemm_gather_matches_bf16_reference(cuda, qtype, T, routed):
     ng = torch.zeros(1, dtype=torch.int32, device=cuda)
     kernels.route_groups(ids, nv, E, 64, order, groups, ng)
     y = torch.full((nv, N), float("nan"), device=cuda)
-    kernels.gemm_gather(qtype, dw, rb, xb, y, N, H, N, order, groups, ng, mg, N * rb, K, routed)
+    kernels.gemm_gather(qtype, dw, rb, xb, xs, y, N, H, N, order, groups, ng, mg, N * rb, K, routed)
     wf = torch.empty(E * N, H, device=cuda)
     kernels.dequant_rows(qtype, dw, rb, E * N, H, wf)
-    wb = wf.to(torch.bfloat16).double().reshape(E, N, H)
-    xd = xb.double()
+    wb = wf.to(torch.float16).double().reshape(E, N, H)
+    xd = xb.double() * xs.double()[:, None]
     idn = ids.cpu().numpy()
     ref = torch.stack([wb[idn[j]] @ xd[j if routed else j // K] for j in range(nv)])
     got = y.double()
-    err = ((got - ref).abs().max() / ref.abs().max()).item()
+    err = ((got - ref).abs().max(dim=1).values / ref.abs().max(dim=1).values).max().item()
     print("max rel err", err)
     assert err <= 1e-4
 
 
 def test_gemm_gather_rejects_bad_arguments(cuda):
     w = torch.zeros(144 * 64, dtype=torch.uint8, device=cuda)
-    xb = torch.zeros(64, 256, dtype=torch.bfloat16, device=cuda)
+    xb = torch.zeros(64, 256, dtype=torch.float16, device=cuda)
+    xs = torch.ones(64, device=cuda)
     y = torch.zeros(64, device=cuda)
     i = torch.zeros(16, dtype=torch.int32, device=cuda)
     with pytest.raises(ValueError):  # k a multiple of 128
-        kernels.gemm_gather(synth.Q8_0, w, 68, xb, y, 4, 64, 4, i, i, i, 4, 4 * 68, 1, False)
+        kernels.gemm_gather(synth.Q8_0, w, 68, xb, xs, y, 4, 64, 4, i, i, i, 4, 4 * 68, 1, False)
     with pytest.raises(LengthError):  # one launch row per group
-        kernels.gemm_gather(synth.Q4_K, w, 144, xb, y, 4, 256, 4, i, i, i, 70000, 4 * 144, 1, False)
+        kernels.gemm_gather(synth.Q4_K, w, 144, xb, xs, y, 4, 256, 4, i, i, i, 70000, 4 * 144, 1, False)
     with pytest.raises(ValueError):  # experts closer than their rows
-        kernels.gemm_gather(synth.Q4_K, w, 144, xb, y, 4, 256, 4, i, i, i, 4, 144, 1, False)
+        kernels.gemm_gather(synth.Q4_K, w, 144, xb, xs, y, 4, 256, 4, i, i, i, 4, 144, 1, False)
+    with pytest.raises(ValueError):  # no row scales
+        kernels.gemm_gather(synth.Q4_K, w, 144, xb, None, y, 4, 256, 4, i, i, i, 4, 4 * 144, 1, False)
     with pytest.raises(LengthError):
         kernels.route_groups(i, 16385, 8, 64, i, i, i)
 
@@ -660,11 +667,11 @@ def test_moe_real_widths_match_float64_reference(cuda, tmp_path):
 
 
 def test_moe_prefill_matmul_path_real_widths(cuda, tmp_path):
-    # A 20-row prompt at 35B-A3B widths takes the bf16 MFMA matmuls for the
+    # A 20-row prompt at 35B-A3B widths takes the fp16 MFMA matmuls for the
     # dense projections (attention, DeltaNet and shared-expert projections):
-    # logits within the bf16 prefill bar of the float64 graph, at the prompt's
+    # logits within the 2e-2 prefill bar of the float64 graph, at the prompt's
     # last row and over the decode steps that follow. Every expert is routed
-    # (top-8 of 8), so the graph is continuous in its inputs and bf16
+    # (top-8 of 8), so the graph is continuous in its inputs and fp16
     # rounding cannot flip a near-tie route (top-k is discontinuous; the
     # FP32 switch below covers the 256-expert routing).
     shape = synth.Qwen35MoeShape("moe-allroute-4l", 4, 2048, 16, 2, 256, 64, 4096, 4096, 8, 8, 512, 512, 4, 4, 128,
@@ -730,16 +737,16 @@ def test_moe_decode_graph_matches_eager_launches(cuda, moe_tiny):
 
 @pytest.mark.parametrize("prompt_len", [64, 160])
 def test_moe_default_prefill_256_experts_routes_flip_only_at_near_ties(cuda, tmp_path, prompt_len):
-    # The default prompt path at 35B-A3B widths (256 experts, top-8): bf16
+    # The default prompt path at 35B-A3B widths (256 experts, top-8): fp16
     # MFMA dense projections feeding the FP32 router, the routed experts as
     # batched GEMVs (64 rows) or, from four routed vectors per expert, as
-    # gathered bf16 matmuls (160 rows). Against the FP32 switch (whose routes
+    # gathered fp16 matmuls (160 rows). Against the FP32 switch (whose routes
     # and tokens equal the float64 graph's, test above), layer by layer on
     # the prompt's last row:
-    # * the router logits agree within the bf16 bar (2e-2 of their largest);
+    # * the router logits agree within the prefill bar (2e-2 of their largest);
     # * where the top-8 sets differ, every swapped pair is a near tie that
     #   the measured logit perturbation eps explains: an expert a kept by the
-    #   FP32 path and dropped by bf16, and b the other way round, have FP32
+    #   FP32 path and dropped by fp16, and b the other way round, have FP32
     #   logits within 2 eps (a shift of at most eps each way reorders them);
     #   layers after the first flip see different inputs and are not compared;
     # * with no flip, the final logits agree within 2e-2 and the first token
@@ -767,7 +774,7 @@ def test_moe_default_prefill_256_experts_routes_flip_only_at_near_ties(cuda, tmp
         for kept in b_set - a_set:
             for taken in a_set - b_set:
                 gap = gb[layer][kept] - gb[layer][taken]
-                print(f"  flip: fp32 keeps {kept}, bf16 takes {taken}, fp32 logit gap {gap:.3e}")
+                print(f"  flip: fp32 keeps {kept}, fp16 takes {taken}, fp32 logit gap {gap:.3e}")
                 assert gap <= 2 * eps + 1e-6
         flipped = True
         break

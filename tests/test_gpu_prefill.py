@@ -1,17 +1,22 @@
-"""Prefill matmul parity on the GPU (bf16 MFMA over native GGUF weights).
+"""Prefill matmul parity on the GPU (fp16 MFMA over native GGUF weights).
 
 Two references per case, both float64 over the bit-exact FP32 dequantized
 weights:
-* the contract: against the FP32 operands, max|Y - ref| / max|ref| <= 2e-2;
-* the kernel's own arithmetic: against the same product with X and W first
-  rounded to bf16 (round to nearest even), within 1e-4 -- what is left is
-  FP32 accumulation order, so a wrong operand layout, k map or tile edge
-  fails here even when it would hide inside the 2e-2 bound.
+* the contract: against the FP32 operands, max|Y - ref| / max|ref| <= 2e-2
+  (the fp16 operands land near 1e-3);
+* the kernel's own arithmetic: against the same product with X given as its
+  scaled fp16 rows (checked bit for bit against numpy's round-to-nearest-even
+  conversion of the row scaled by the power of two its largest magnitude
+  fixes) and W rounded to fp16, within 1e-4 -- what is left is FP32
+  accumulation order, so a wrong operand layout, k map, scale index or tile
+  edge fails here even when it would hide inside the 2e-2 bound.
 """
 
 from __future__ import annotations
 
 import pytest
+
+import numpy as np
 
 from myllm_amd import synth
 from myllm_amd.hipllm import kernels
@@ -23,27 +28,60 @@ pytestmark = pytest.mark.gpu
 TYPES = [synth.Q4_K, synth.Q6_K, synth.Q8_0, synth.Q5_0, synth.F16, synth.F32]
 
 
+def f16_rows_ref(x: np.ndarray):
+    """The scaled fp16 operand rows: per row 2^e with max|x| / 2^e in
+    [2^13, 2^14) (NaN left out of the maximum; e = 0 for a zero row or one
+    holding an Inf; e clamped to [-126, 127]), xh = fp16(x / 2^e)."""
+    x = np.asarray(x, dtype=np.float32)
+    xh = np.empty(x.shape, dtype=np.float16)
+    scale = np.ones(x.shape[0], dtype=np.float32)
+    for r in range(x.shape[0]):
+        a = np.abs(x[r])
+        mx = np.nanmax(a) if not np.isnan(a).all() else 0.0
+        e = 0
+        if 0 < mx < np.inf:
+            e = min(127, max(-126, int(np.frexp(mx)[1]) - 14))
+        xh[r] = (x[r] * np.float32(2.0 ** -e)).astype(np.float16)
+        scale[r] = np.float32(2.0 ** e)
+    return xh, scale
+
+
+def to_f16(x, cuda):
+    """hipllm_to_f16 of the device rows x, checked against f16_rows_ref."""
+    m, k = x.shape
+    xh = torch.empty(m, k, dtype=torch.float16, device=cuda)
+    xs = torch.empty(m, dtype=torch.float32, device=cuda)
+    kernels.to_f16(x, k, xh, xs, m, k)
+    rh, rs = f16_rows_ref(x.cpu().numpy())
+    assert np.array_equal(xh.cpu().numpy().view(np.uint16), rh.view(np.uint16)), "fp16 rows"
+    assert np.array_equal(xs.cpu().numpy(), rs), "row scales"
+    return xh, xs
+
+
 def gemm_case(cuda, qtype, m, n, k, seed, tile=-1, bias=False, residual=False, splits=0, in_place=False):
     w = random_rows(qtype, n, k, seed)
     dw = dev_bytes(w, cuda)
     g = torch.Generator(device="cpu").manual_seed(seed)
-    x = torch.randn(m, k, generator=g).to(cuda)
-    xb = torch.empty(m, k, dtype=torch.bfloat16, device=cuda)
-    kernels.to_bf16(x, k, xb, m, k)
+    x = torch.randn(m, k, generator=g)
+    # Rows of different magnitudes (the scale follows each row).
+    x = (x * torch.exp2(torch.randint(-12, 13, (m, 1), generator=g).float())).to(cuda)
+    xh, xs = to_f16(x, cuda)
     b = torch.randn(n, generator=g).to(cuda) if bias else None
     r = torch.randn(m, n, generator=g).to(cuda) if residual else None
     y = r.clone() if in_place else torch.empty(m, n, dtype=torch.float32, device=cuda)
-    kernels.gemm_mfma(qtype, dw, w.shape[1], xb, b, y if in_place else r, y, m, n, k, tile, splits=splits)
+    kernels.gemm_mfma(qtype, dw, w.shape[1], xh, xs, b, y if in_place else r, y, m, n, k, tile, splits=splits)
     wf = torch.empty(n, k, dtype=torch.float32, device=cuda)
     kernels.dequant_rows(qtype, dw, w.shape[1], n, k, wf)
     ref = x.double() @ wf.double().T
-    ref_b = x.to(torch.bfloat16).double() @ wf.to(torch.bfloat16).double().T
+    ref_b = (xh.double() * xs.double()[:, None]) @ wf.to(torch.float16).double().T
     for extra in (b, r):
         if extra is not None:
             ref = ref + extra.double()
             ref_b = ref_b + extra.double()
-    assert torch.equal(xb, x.to(torch.bfloat16)), "to_bf16 must round to nearest even like torch"
-    return y.double().cpu().numpy(), ref.cpu().numpy(), ref_b.cpu().numpy()
+    # Relative to each row's own magnitude (rows differ by up to 2^24).
+    ref, ref_b, y = (t.double().cpu().numpy() for t in (ref, ref_b, y))
+    norm = np.abs(ref).max(axis=1, keepdims=True)
+    return y / norm, ref / norm, ref_b / norm
 
 
 @pytest.mark.parametrize("qtype", TYPES)
@@ -117,17 +155,41 @@ def test_gemm_fp32_entry_with_workspace(cuda):
     assert rel_err(y.double().cpu().numpy(), ref.cpu().numpy()) <= 2e-2
 
 
+def test_to_f16_special_rows(cuda):
+    # Zero rows, a row at the FP32 maximum, tiny rows (subnormal fp16 after
+    # scaling only far below the row's largest value), and Inf / NaN rows
+    # (scale 1: the non-finite values pass through).
+    k = 64
+    x = np.zeros((7, k), dtype=np.float32)
+    x[6] = np.linspace(-2e-37, 2e-37, k, dtype=np.float32)  # e clamped at -126
+    x[1] = np.linspace(-3.4e38, 3.4e38, k, dtype=np.float32)
+    x[2] = np.linspace(-1e-30, 1e-30, k, dtype=np.float32)
+    x[2, 0] = 1e-38
+    x[3] = 1.0
+    x[3, 5] = np.inf
+    x[4] = 2.0
+    x[4, 9] = np.nan
+    x[5] = np.linspace(-70000.0, 65504.0 * 4, k, dtype=np.float32)
+    xh, xs = to_f16(torch.from_numpy(x).to(cuda), cuda)
+    assert xs[0].item() == 1.0 and xs[3].item() == 1.0 and xs[4].item() != 1.0
+    assert torch.isnan(xh[4, 9]) and torch.isinf(xh[3, 5]) and xs[6].item() == 2.0 ** -126
+    assert torch.isfinite(xh[1]).all() and torch.isfinite(xh[5]).all()
+
+
 def test_gemm_rejects_bad_arguments(cuda):
     w = torch.zeros(144 * 4 + 256, dtype=torch.uint8, device=cuda)
-    xb = torch.zeros(2, 256, dtype=torch.bfloat16, device=cuda)
+    xh = torch.zeros(2, 256, dtype=torch.float16, device=cuda)
+    xs = torch.ones(2, device=cuda)
     y = torch.zeros(2, 2, device=cuda)
     with pytest.raises(ValueError):
-        kernels.gemm_mfma(synth.Q4_K, w, 144, xb, None, None, y, 2, 2, 192)  # k % 128 != 0
+        kernels.gemm_mfma(synth.Q4_K, w, 144, xh, xs, None, None, y, 2, 2, 192)  # k % 128 != 0
     with pytest.raises(ValueError):
-        kernels.gemm_mfma(synth.Q4_K, w, 144, xb, None, None, y, 2, 2, 256, 7)  # unknown tile
+        kernels.gemm_mfma(synth.Q4_K, w, 144, xh, xs, None, None, y, 2, 2, 256, 7)  # unknown tile
     with pytest.raises(ValueError):
-        kernels.gemm_mfma(99, w, 144, xb, None, None, y, 2, 2, 256)  # unknown type
+        kernels.gemm_mfma(99, w, 144, xh, xs, None, None, y, 2, 2, 256)  # unknown type
     with pytest.raises(ValueError):
-        kernels.gemm_mfma(synth.Q4_K, w, 144, xb, None, None, y, 2, 2, 256, 0, splits=-1)
+        kernels.gemm_mfma(synth.Q4_K, w, 144, xh, xs, None, None, y, 2, 2, 256, 0, splits=-1)
     with pytest.raises(ValueError):
-        kernels.gemm_mfma(synth.Q4_K, w, 144, xb, None, None, y, 2, 2, 256, 0, splits=1025)
+        kernels.gemm_mfma(synth.Q4_K, w, 144, xh, xs, None, None, y, 2, 2, 256, 0, splits=1025)
+    with pytest.raises(ValueError):
+        kernels.gemm_mfma(synth.Q4_K, w, 144, xh, None, None, None, y, 2, 2, 256)  # no row scales
