@@ -705,7 +705,10 @@ __global__ void gemm_init_kernel(float* __restrict__ y, uint32_t ldy, const floa
 // powers of two (e is kept in [-126, 127], so 2^-e stays finite). NaN values
 // are left out of the maximum and stay NaN; a row of zeros, or one holding
 // an Inf, keeps e = 0 (the non-finite values then reach the output as they
-// would in FP32). One 256-thread block per row.
+// would in FP32). Block (r, c) converts values [2048 c, 2048 c + 2048) of
+// row r, after reading the whole row for its maximum (every block of a row
+// computes the same e).
+constexpr uint32_t kF16Chunk = 2048;
 __global__ __launch_bounds__(256) void to_f16_kernel(const float* __restrict__ x, size_t ldx,
                                                      _Float16* __restrict__ xh, float* __restrict__ xscale,
                                                      uint32_t k) {
@@ -728,9 +731,10 @@ __global__ __launch_bounds__(256) void to_f16_kernel(const float* __restrict__ x
         e = max(-126, min(127, e - 14));
     }
     const float down = ldexpf(1.0f, -e);
-    if (threadIdx.x == 0) xscale[r] = ldexpf(1.0f, e);
+    if (threadIdx.x == 0 && blockIdx.y == 0) xscale[r] = ldexpf(1.0f, e);
     _Float16* dst = xh + static_cast<size_t>(r) * k;
-    for (uint32_t i = threadIdx.x; i < k / 8; i += 256) {
+    const uint32_t end = min(k, (blockIdx.y + 1) * kF16Chunk) / 8;
+    for (uint32_t i = blockIdx.y * (kF16Chunk / 8) + threadIdx.x; i < end; i += 256) {
         const float4 a = xr[2 * i], b = xr[2 * i + 1];
         const u32x4 u = {pack_h2(a.x * down, a.y * down), pack_h2(a.z * down, a.w * down),
                          pack_h2(b.x * down, b.y * down), pack_h2(b.z * down, b.w * down)};
@@ -819,7 +823,8 @@ int launch_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m,
     if (!x || !xh || !xscale || m == 0 || k == 0 || k % 8 != 0 || ldx < k || ldx % 4 != 0) return kInvalidArgument;
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(xh) % 16 != 0) return kInvalidArgument;
     if (m > 0x7fffffffull || k > 0xffffffffull) return kLengthError;
-    hipLaunchKernelGGL(to_f16_kernel, dim3(static_cast<uint32_t>(m)), dim3(256), 0, stream, x, ldx,
+    const uint32_t chunks = static_cast<uint32_t>((k + kF16Chunk - 1) / kF16Chunk);
+    hipLaunchKernelGGL(to_f16_kernel, dim3(static_cast<uint32_t>(m), chunks), dim3(256), 0, stream, x, ldx,
                        static_cast<_Float16*>(xh), xscale, static_cast<uint32_t>(k));
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
