@@ -73,6 +73,18 @@ size_t hipllm_gemv_workspace_bytes(size_t k);
 int hipllm_gemv(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* bias, float* y,
                 size_t n, size_t k, void* workspace, void* stream);
 
+/* hipllm_gemv without a workspace and without any allocation, for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * The XGroup form of x goes to a static per-GPU device array of 256 KiB that
+ * lives until the process ends, so k <= 65536 (HIPLLM_LENGTH_ERROR beyond).
+ * Every call on one GPU shares that array: calls that overlap on one GPU
+ * (other streams, other threads) race and must be ordered by the caller. The
+ * stream must belong to the calling thread's current device. Same results
+ * as hipllm_gemv, bit for bit. */
+int hipllm_gemv_noalloc(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* bias, float* y,
+                        size_t n, size_t k, void* stream);
+
 /* GEMV with a caller-supplied XGroup input (hipllm_prep_x; quantized
  * weights read xq, F32 / F16 weights read x) and an optional residual:
  * y = W x (+ bias) (+ residual). `tiling` 0 picks the default; otherwise

@@ -10,6 +10,7 @@
 #include <cstring>
 #include <exception>
 #include <memory>
+#include <mutex>
 #include <new>
 #include <stdexcept>
 #include <string>
@@ -98,6 +99,58 @@ int hipllm_gemv(uint32_t type, const void* w, size_t row_bytes, const float* x, 
     return status(hipllm::launch_gemv_prepped(type, w, row_bytes, x, xq, bias, nullptr, y, n, k, 0,
                                               as_stream(stream)),
                   "hipllm_gemv: invalid arguments or launch failure");
+}
+
+// ------------------------------------------------ GEMV without allocation
+// The XGroup form of x lives in a file-scope device array instead of a
+// caller workspace. Its device address differs per GPU and is not the host
+// name `scratch`, so each device's address comes from hipGetSymbolAddress
+// once (the first call on that device, with it current) and is kept here.
+static constexpr size_t kNoAllocMaxK = 65536;  // 4 bytes of XGroup form per value: 256 KiB per device
+static __device__ __align__(256) unsigned char scratch[kNoAllocMaxK * 4];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The current device's copy of `scratch`, or nullptr with the error set.
+void* device_scratch(int* code, const char** what) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {
+        *code = HIPLLM_RUNTIME_ERROR;
+        *what = "hipllm_gemv_noalloc: no usable current HIP device";
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) {
+            *code = HIPLLM_RUNTIME_ERROR;
+            *what = "hipllm_gemv_noalloc: hipGetSymbolAddress(scratch) failed";
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
+}
+}  // namespace
+
+int hipllm_gemv_noalloc(uint32_t type, const void* w, size_t row_bytes, const float* x, const float* bias, float* y,
+                        size_t n, size_t k, void* stream) {
+    if (k > kNoAllocMaxK) {
+        return fail(HIPLLM_LENGTH_ERROR, "hipllm_gemv_noalloc: k exceeds 65536, the capacity of its static scratch");
+    }
+    int code = HIPLLM_OK;
+    const char* what = "";
+    void* ptr = device_scratch(&code, &what);
+    if (!ptr) return fail(code, what);
+    hipllm::XGroup* xq = static_cast<hipllm::XGroup*>(ptr);
+    const int rc = hipllm::launch_prep_x(x, xq, k, as_stream(stream));
+    if (rc != hipllm::kOk) return status(rc, "hipllm_gemv_noalloc: k must be a positive multiple of 16");
+    return status(hipllm::launch_gemv_prepped(type, w, row_bytes, x, xq, bias, nullptr, y, n, k, 0,
+                                              as_stream(stream)),
+                  "hipllm_gemv_noalloc: invalid arguments or launch failure");
 }
 
 int hipllm_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const float* x, const void* xq,

@@ -69,6 +69,7 @@ SIGNATURES = {
     "hipllm_prep_x": (_I, [_P, _P, _S, _P]),
     "hipllm_gemv_workspace_bytes": (_S, [_S]),
     "hipllm_gemv": (_I, [_U32, _P, _S, _P, _P, _P, _S, _S, _P, _P]),
+    "hipllm_gemv_noalloc": (_I, [_U32, _P, _S, _P, _P, _P, _S, _S, _P]),
     "hipllm_gemv_prepped": (_I, [_U32, _P, _S, _P, _P, _P, _P, _P, _S, _S, _I, _P]),
     "hipllm_gemv_swiglu": (_I, [_U32, _P, _P, _S, _P, _P, _P, _P, _S, _S, _I, _P]),
     "hipllm_gemv_norm": (_I, [_U32, _P, _S, _P, _P, _F, _P, _P, _P, _S, _S, _I, _P]),
@@ -357,6 +358,10 @@ def _k_gemv(qtype, w, row_bytes, x, bias, y, n, k, workspace, stream=None):
                             _stream(stream)))
 
 
+def _k_gemv_noalloc(qtype, w, row_bytes, x, bias, y, n, k, stream=None):
+    check(lib().hipllm_gemv_noalloc(qtype, _ptr(w), row_bytes, _ptr(x), _ptr(bias), _ptr(y), n, k, _stream(stream)))
+
+
 def _k_gemv_prepped(qtype, w, row_bytes, x, xq, bias, residual, y, n, k, tiling=0, stream=None):
     check(lib().hipllm_gemv_prepped(qtype, _ptr(w), row_bytes, _ptr(x), _ptr(xq), _ptr(bias), _ptr(residual),
                                     _ptr(y), n, k, tiling, _stream(stream)))
@@ -554,7 +559,8 @@ def _k_swiglu(g, u, y, yq, n, stream=None):
 
 
 kernels = types.SimpleNamespace(
-    dequant_rows=_k_dequant_rows, prep_x=_k_prep_x, gemv=_k_gemv, gemv_prepped=_k_gemv_prepped,
+    dequant_rows=_k_dequant_rows, prep_x=_k_prep_x, gemv=_k_gemv, gemv_noalloc=_k_gemv_noalloc,
+    gemv_prepped=_k_gemv_prepped,
     gemv_swiglu=_k_gemv_swiglu, gemv_norm=_k_gemv_norm, gemv_swiglu_norm=_k_gemv_swiglu_norm, to_f16=_k_to_f16, gemm_mfma=_k_gemm_mfma, gemm=_k_gemm,
     gemm_workspace_bytes=lambda m, k: lib().hipllm_gemm_workspace_bytes(m, k), rmsnorm=_k_rmsnorm, embed=_k_embed, rope_kv=_k_rope_kv,
     attn_decode=_k_attn_decode, attn_decode_rope_gated=_k_attn_decode_rope_gated, argmax=_k_argmax,
