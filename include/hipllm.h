@@ -376,6 +376,20 @@ int hipllm_gdn_scan(const float* q, const float* k, size_t ldqk, const float* v,
                     const float* beta, float* state, float* out, size_t ldo, size_t tokens, size_t value_heads,
                     size_t key_heads, size_t d, void* stream);
 
+/* hipllm_gdn_scan in the chunk-parallel form: 64-token chunks, each chunk's
+ * delta-rule system (I + A) Delta = R solved through T = (I + A)^-1 for all
+ * chunks at once, then one step per chunk carries the state (16 state
+ * columns per block). Same arguments and results (to FP32 rounding) as
+ * hipllm_gdn_scan; scratch holds hipllm_gdn_chunk_scratch_floats floats.
+ * Replaces the serial scan of the prompt (metal_llm.metal:1370-1420) with the
+ * chunked formulation the reference names as its next step
+ * (QWEN36_35B_A3B_COMPATIBILITY.md:176-181, 476-479). */
+size_t hipllm_gdn_chunk_scratch_floats(size_t tokens, size_t value_heads);
+int hipllm_gdn_scan_chunked(const float* q, const float* k, size_t ldqk, const float* v, size_t ldv,
+                            const float* decay, const float* beta, float* state, float* out, size_t ldo,
+                            size_t tokens, size_t value_heads, size_t key_heads, size_t d, float* scratch,
+                            size_t scratch_floats, void* stream);
+
 /* y = rmsnorm(o_head) gamma silu(z) per head (d <= 256); yq (nullable) the
  * XGroup form of y. Replaces the
  * state norm + SiLU(z) gate of encode_delta_net (moe_llm.mm:2614-2634). */

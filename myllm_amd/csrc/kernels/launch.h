@@ -157,6 +157,13 @@ int launch_gdn_scan(const float* q, const float* k, size_t ldqk, const float* v,
 int launch_conv_l2norm(const float* x, size_t ldx, float* history, const float* w, float* out, size_t ldo,
                        size_t tokens, size_t channels, size_t ksize, size_t norm_channels, size_t d, float eps,
                        hipStream_t stream);
+// The same recurrence as launch_gdn_scan in 64-token chunks (the chunk-
+// parallel form; scratch: gdn_chunk_scratch_floats floats).
+size_t gdn_chunk_scratch_floats(size_t tokens, size_t value_heads);
+int launch_gdn_scan_chunked(const float* q, const float* k, size_t ldqk, const float* v, size_t ldv,
+                            const float* decay, const float* beta, float* state, float* out, size_t ldo,
+                            size_t tokens, size_t value_heads, size_t key_heads, size_t d, float* scratch,
+                            size_t scratch_floats, hipStream_t stream);
 int launch_gdn_scan_gated(const float* q, const float* k, size_t ldqk, const float* v, size_t ldv, const float* alpha,
                           const float* beta_raw, size_t ld_ab, const float* dt_bias, const float* a, float* state,
                           const float* z, size_t ldz, const float* gamma, float* y, XGroup* yq, size_t ldy,

@@ -442,6 +442,247 @@ __global__ __launch_bounds__(64) void gdn_scan_kernel(const float* __restrict__ 
     for (uint32_t i = 0; i < NR; ++i) S[static_cast<size_t>(r * NR + i) * D + col] = s[i];
 }
 
+// Chunked Gated DeltaNet scan for prompts: the recurrence of gdn_scan_kernel
+// over chunks of C = 64 tokens, the chunk-parallel (WY) form of the delta
+// rule. Within a chunk starting from state S0, with G_t the cumulative log
+// decay (G_t = sum of log decay_i, i <= t), the per-token deltas
+// delta_t = beta_t (v_t - k_t . S_{t-1}-decayed) satisfy
+//   (I + A) Delta = R,  A[t][i] = beta_t exp(G_t - G_i) (k_t . k_i) (i < t),
+//                       R[t]    = beta_t (v_t - exp(G_t) S0^T k_t),
+// the outputs are o_t = (exp(G_t) S0^T q_t + sum_{i<=t} exp(G_t - G_i)
+// (q_t . k_i) delta_i) / sqrt(D), and the chunk ends in
+//   S = exp(G_last) S0 + sum_t exp(G_last - G_t) k_t delta_t^T.
+// Every exponent is <= 0. gdn_chunk_prep_kernel builds, for each (value
+// head, chunk) at once, T = (I + A)^-1 and P[t][i] = exp(G_t - G_i)
+// (q_t . k_i) (i <= t); gdn_chunk_scan_kernel then walks the chunks in order
+// for 16 state columns per block (the columns evolve independently), so the
+// serial part is one chunk step per 64 tokens. Rows past the prompt's end are
+// zero keys with beta 0 and decay 1, which leave everything unchanged.
+constexpr uint32_t kChunk = 64;
+constexpr uint32_t kChunkCols = 16;
+
+// G_t (cumulative log decay) and beta_t of one chunk into LDS: the first
+// wave, lane t for token t, an inclusive prefix sum over the wave in a fixed
+// order (both chunk kernels compute the same bits).
+__device__ __forceinline__ void chunk_gates(const float* __restrict__ decay, const float* __restrict__ beta,
+                                            uint32_t value_heads, uint32_t h, uint32_t t0, uint32_t len,
+                                            float* G, float* B) {
+    if (threadIdx.x < kChunk) {
+        const uint32_t t = threadIdx.x;
+        float g = 0.0f, b = 0.0f;
+        if (t < len) {
+            const float dc = decay[static_cast<size_t>(t0 + t) * value_heads + h];
+            g = dc > 0.0f ? logf(dc) : -87.0f;  // decay 0 (underflow) as e^-87
+            b = beta[static_cast<size_t>(t0 + t) * value_heads + h];
+        }
+#pragma unroll
+        for (uint32_t off = 1; off < kChunk; off *= 2) {
+            const float up = __shfl_up(g, off, 64);
+            if (t >= off) g += up;
+        }
+        G[t] = g;
+        B[t] = b;
+    }
+}
+
+// Rows [t0, t0 + 64) of a [tokens, ld] matrix, columns col0 + [0, D), into
+// LDS (rows past len are zero). All of a thread's loads issue before its LDS
+// stores: VEC (16-byte aligned rows) as float4, otherwise as scalars.
+template <uint32_t D, bool VEC>
+__device__ __forceinline__ void chunk_rows(const float* __restrict__ src, uint32_t ld, uint32_t col0, uint32_t t0,
+                                           uint32_t len, float (*dst)[D + 1]) {
+    constexpr uint32_t N4 = kChunk * D / 4 / 256;  // float4 per thread
+    float4 r[N4];
+#pragma unroll
+    for (uint32_t n = 0; n < N4; ++n) {
+        const uint32_t i = threadIdx.x + 256 * n, t = i / (D / 4), d = 4 * (i % (D / 4));
+        const float* p = src + static_cast<size_t>(t0 + t) * ld + col0 + d;
+        if (t >= len) {
+            r[n] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        } else if constexpr (VEC) {
+            r[n] = *reinterpret_cast<const float4*>(p);
+        } else {
+            r[n] = make_float4(p[0], p[1], p[2], p[3]);
+        }
+    }
+#pragma unroll
+    for (uint32_t n = 0; n < N4; ++n) {
+        const uint32_t i = threadIdx.x + 256 * n, t = i / (D / 4), d = 4 * (i % (D / 4));
+        dst[t][d] = r[n].x, dst[t][d + 1] = r[n].y, dst[t][d + 2] = r[n].z, dst[t][d + 3] = r[n].w;
+    }
+}
+
+template <uint32_t D, bool VEC>
+__global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                             uint32_t ldqk, const float* __restrict__ decay,
+                                                             const float* __restrict__ beta,
+                                                             float* __restrict__ tp, uint32_t tokens,
+                                                             uint32_t value_heads, uint32_t key_heads) {
+    const uint32_t h = blockIdx.x, c = blockIdx.y, kh = h % key_heads;
+    const uint32_t t0 = c * kChunk, len = min(kChunk, tokens - t0);
+    __shared__ float Ks[kChunk][D + 1], Qs[kChunk][D + 1];
+    __shared__ float As[kChunk][kChunk + 4];
+    __shared__ float G[kChunk], B[kChunk];
+    chunk_rows<D, VEC>(k, ldqk, kh * D, t0, len, Ks);
+    chunk_rows<D, VEC>(q, ldqk, kh * D, t0, len, Qs);
+    chunk_gates(decay, beta, value_heads, h, t0, len, G, B);
+    __syncthreads();
+    // 4 x 4 (t, i) tile per thread of K K^T and Q K^T.
+    const uint32_t tt = threadIdx.x / 16, ii = threadIdx.x % 16;
+    float kk[4][4] = {}, qk[4][4] = {};
+    for (uint32_t d = 0; d < D; ++d) {
+        float kt[4], qt[4], ki[4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            kt[a] = Ks[4 * tt + a][d];
+            qt[a] = Qs[4 * tt + a][d];
+            ki[a] = Ks[4 * ii + a][d];
+        }
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                kk[a][b] = fmaf(kt[a], ki[b], kk[a][b]);
+                qk[a][b] = fmaf(qt[a], ki[b], qk[a][b]);
+            }
+    }
+    float* T = tp + (static_cast<size_t>(c) * value_heads + h) * 2 * kChunk * kChunk;
+    float* P = T + kChunk * kChunk;
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint32_t t = 4 * tt + a, i = 4 * ii + b;
+            const float dec = i <= t ? expf(G[t] - G[i]) : 0.0f;
+            As[t][i] = i < t ? B[t] * dec * kk[a][b] : 0.0f;
+            P[t * kChunk + i] = dec * qk[a][b];
+        }
+    __syncthreads();
+    // T = (I + A)^-1 by forward substitution, one column per lane of the
+    // first wave (T is unit lower triangular): T[t][j] = [t == j] -
+    // sum_{i < t} A[t][i] T[i][j], every A[t][i] an LDS broadcast; four
+    // partial sums (i mod 4) shorten the dependent chain.
+    if (threadIdx.x < kChunk) {
+        const uint32_t j = threadIdx.x;
+        float col[kChunk];
+#pragma unroll
+        for (uint32_t t = 0; t < kChunk; ++t) {
+            float a4[4] = {t == j ? 1.0f : 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (uint32_t i = 0; i < t; ++i) a4[i % 4] = fmaf(-As[t][i], col[i], a4[i % 4]);
+            const float acc = (a4[0] + a4[1]) + (a4[2] + a4[3]);
+            col[t] = acc;
+            T[t * kChunk + j] = acc;
+        }
+    }
+}
+
+// Block (value head h, column group cg) owns state columns
+// [16 cg, 16 cg + 16) of head h and walks the chunks in order.
+template <uint32_t D, bool VEC>
+__global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                             uint32_t ldqk, const float* __restrict__ v, uint32_t ldv,
+                                                             const float* __restrict__ decay,
+                                                             const float* __restrict__ beta,
+                                                             const float* __restrict__ tp, float* __restrict__ state,
+                                                             float* __restrict__ out, uint32_t ldo, uint32_t tokens,
+                                                             uint32_t value_heads, uint32_t key_heads) {
+    constexpr uint32_t CG = D / kChunkCols;
+    const uint32_t h = blockIdx.x / CG, col0 = (blockIdx.x % CG) * kChunkCols, kh = h % key_heads;
+    const uint32_t tid = threadIdx.x;
+    __shared__ float Ks[kChunk][D + 1], Qs[kChunk][D + 1];
+    __shared__ float Ts[kChunk][kChunk + 1], Ps[kChunk][kChunk + 1];
+    __shared__ float Ss[D][kChunkCols];
+    __shared__ float Rs[kChunk][kChunkCols + 1], Ds[kChunk][kChunkCols + 1];
+    __shared__ float G[kChunk], B[kChunk], E[kChunk];
+    float* S = state + static_cast<size_t>(h) * D * D;
+    for (uint32_t i = tid; i < D * kChunkCols; i += 256) {
+        Ss[i / kChunkCols][i % kChunkCols] = S[static_cast<size_t>(i / kChunkCols) * D + col0 + i % kChunkCols];
+    }
+    const float qscale = 1.0f / sqrtf(static_cast<float>(D));
+    // Chunk-row products: thread (t = tid / 4) computes row t, columns
+    // cq .. cq + 3 of the block's 16. State update: element e = tid,
+    // tid + 256, ... of the D x 16 block (row e / 16, column e % 16).
+    const uint32_t t = tid / 4, cq = (tid % 4) * 4;
+    const uint32_t nchunks = (tokens + kChunk - 1) / kChunk;
+    for (uint32_t c = 0; c < nchunks; ++c) {
+        const uint32_t t0 = c * kChunk, len = min(kChunk, tokens - t0);
+        const float* T = tp + (static_cast<size_t>(c) * value_heads + h) * 2 * kChunk * kChunk;
+        const float* P = T + kChunk * kChunk;
+        __syncthreads();  // the previous chunk's reads of Ks / Qs / Ds are done
+        chunk_rows<D, VEC>(k, ldqk, kh * D, t0, len, Ks);
+        chunk_rows<D, VEC>(q, ldqk, kh * D, t0, len, Qs);
+        {
+            float4 tr[4], pr[4];
+#pragma unroll
+            for (uint32_t n = 0; n < 4; ++n) {
+                tr[n] = reinterpret_cast<const float4*>(T)[tid + 256 * n];
+                pr[n] = reinterpret_cast<const float4*>(P)[tid + 256 * n];
+            }
+#pragma unroll
+            for (uint32_t n = 0; n < 4; ++n) {
+                const uint32_t i = 4 * (tid + 256 * n), r = i / kChunk, c4 = i % kChunk;
+                Ts[r][c4] = tr[n].x, Ts[r][c4 + 1] = tr[n].y, Ts[r][c4 + 2] = tr[n].z, Ts[r][c4 + 3] = tr[n].w;
+                Ps[r][c4] = pr[n].x, Ps[r][c4 + 1] = pr[n].y, Ps[r][c4 + 2] = pr[n].z, Ps[r][c4 + 3] = pr[n].w;
+            }
+        }
+        chunk_gates(decay, beta, value_heads, h, t0, len, G, B);
+        __syncthreads();
+        if (tid < kChunk) E[tid] = expf(G[kChunk - 1] - G[tid]);
+        // X1 = K S0, Y1 = Q S0 for row t, columns cq .. cq + 3.
+        float x1[4] = {}, y1[4] = {};
+        for (uint32_t d = 0; d < D; ++d) {
+            const float kt = Ks[t][d], qt = Qs[t][d];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                x1[j] = fmaf(kt, Ss[d][cq + j], x1[j]);
+                y1[j] = fmaf(qt, Ss[d][cq + j], y1[j]);
+            }
+        }
+        const float eg = expf(G[t]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float vv = t < len ? v[static_cast<size_t>(t0 + t) * ldv + h * D + col0 + cq + j] : 0.0f;
+            Rs[t][cq + j] = B[t] * (vv - eg * x1[j]);
+        }
+        __syncthreads();
+        // Delta = T R (T unit lower triangular).
+        float dl[4] = {};
+        for (uint32_t i = 0; i <= t; ++i) {
+            const float ti = Ts[t][i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dl[j] = fmaf(ti, Rs[i][cq + j], dl[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) Ds[t][cq + j] = dl[j];
+        __syncthreads();
+        // Outputs, then the state update (every read of the old state is done).
+        float o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = eg * y1[j];
+        for (uint32_t i = 0; i <= t; ++i) {
+            const float pi = Ps[t][i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = fmaf(pi, Ds[i][cq + j], o[j]);
+        }
+        if (t < len) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) out[static_cast<size_t>(t0 + t) * ldo + h * D + col0 + cq + j] = o[j] * qscale;
+        }
+        const float keep = expf(G[kChunk - 1]);
+        for (uint32_t e = tid; e < D * kChunkCols; e += 256) {
+            const uint32_t r = e / kChunkCols, j = e % kChunkCols;
+            float acc = 0.0f;
+            for (uint32_t i = 0; i < kChunk; ++i) acc = fmaf(Ks[i][r] * E[i], Ds[i][j], acc);
+            Ss[r][j] = fmaf(keep, Ss[r][j], acc);
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < D * kChunkCols; i += 256) {
+        S[static_cast<size_t>(i / kChunkCols) * D + col0 + i % kChunkCols] = Ss[i / kChunkCols][i % kChunkCols];
+    }
+}
+
 // Fused decode/prefill forms of the DeltaNet pieces above.
 //
 // Causal conv + SiLU + the L2 head norm in one pass: block `seg` owns the D
@@ -841,6 +1082,48 @@ int launch_gdn_scan(const float* q, const float* k, size_t ldqk, const float* v,
     } else {
         return kInvalidArgument;  // state size 64 or 128
     }
+    return launched();
+}
+
+size_t gdn_chunk_scratch_floats(size_t tokens, size_t value_heads) {
+    return (tokens + kChunk - 1) / kChunk * value_heads * 2 * kChunk * kChunk;
+}
+
+int launch_gdn_scan_chunked(const float* q, const float* k, size_t ldqk, const float* v, size_t ldv,
+                            const float* decay, const float* beta, float* state, float* out, size_t ldo,
+                            size_t tokens, size_t value_heads, size_t key_heads, size_t d, float* scratch,
+                            size_t scratch_floats, hipStream_t stream) {
+    if (!q || !k || !v || !decay || !beta || !state || !out || !scratch || tokens == 0 || value_heads == 0 ||
+        key_heads == 0 || value_heads % key_heads != 0) {
+        return kInvalidArgument;
+    }
+    if (d != 64 && d != 128) return kInvalidArgument;  // state size 64 or 128
+    if (ldqk < key_heads * d || ldv < value_heads * d || ldo < value_heads * d) return kInvalidArgument;
+    if (tokens > 0x7fffffffull || value_heads > 65535) return kLengthError;
+    if (scratch_floats < gdn_chunk_scratch_floats(tokens, value_heads)) return kInvalidArgument;
+    const uint32_t T = static_cast<uint32_t>(tokens), Hv = static_cast<uint32_t>(value_heads),
+                   Hk = static_cast<uint32_t>(key_heads), chunks = (T + kChunk - 1) / kChunk;
+    if (chunks > 65535) return kLengthError;
+    const uint32_t lq = static_cast<uint32_t>(ldqk), lv = static_cast<uint32_t>(ldv), lo = static_cast<uint32_t>(ldo);
+    // Whole float4 loads of k and q when their rows start on 16 bytes; the
+    // scratch (T and P of every chunk) is read as float4.
+    if (reinterpret_cast<uintptr_t>(scratch) % 16 != 0) return kInvalidArgument;
+    const bool vec = reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
+                     ldqk % 4 == 0;
+    auto run = [&](auto dc, auto vc) {
+        constexpr uint32_t DD = decltype(dc)::value;
+        constexpr bool V = decltype(vc)::value;
+        hipLaunchKernelGGL((gdn_chunk_prep_kernel<DD, V>), dim3(Hv, chunks), dim3(256), 0, stream, q, k, lq, decay,
+                           beta, scratch, T, Hv, Hk);
+        hipLaunchKernelGGL((gdn_chunk_scan_kernel<DD, V>), dim3(Hv * (DD / kChunkCols)), dim3(256), 0, stream, q, k,
+                           lq, v, lv, decay, beta, scratch, state, out, lo, T, Hv, Hk);
+    };
+    using D128 = std::integral_constant<uint32_t, 128>;
+    using D64 = std::integral_constant<uint32_t, 64>;
+    if (d == 128 && vec) run(D128{}, std::true_type{});
+    else if (d == 128) run(D128{}, std::false_type{});
+    else if (vec) run(D64{}, std::true_type{});
+    else run(D64{}, std::false_type{});
     return launched();
 }
 

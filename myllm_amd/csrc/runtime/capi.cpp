@@ -603,6 +603,21 @@ int hipllm_gdn_scan(const float* q, const float* k, size_t ldqk, const float* v,
                   "hipllm_gdn_scan: invalid arguments (state size 64 or 128) or launch failure");
 }
 
+size_t hipllm_gdn_chunk_scratch_floats(size_t tokens, size_t value_heads) {
+    return hipllm::gdn_chunk_scratch_floats(tokens, value_heads);
+}
+
+int hipllm_gdn_scan_chunked(const float* q, const float* k, size_t ldqk, const float* v, size_t ldv,
+                            const float* decay, const float* beta, float* state, float* out, size_t ldo,
+                            size_t tokens, size_t value_heads, size_t key_heads, size_t d, float* scratch,
+                            size_t scratch_floats, void* stream) {
+    return status(hipllm::launch_gdn_scan_chunked(q, k, ldqk, v, ldv, decay, beta, state, out, ldo, tokens,
+                                                  value_heads, key_heads, d, scratch, scratch_floats,
+                                                  as_stream(stream)),
+                  "hipllm_gdn_scan_chunked: invalid arguments (state size 64 or 128, scratch size) or launch "
+                  "failure");
+}
+
 int hipllm_gated_rmsnorm(const float* o, size_t ldo, const float* gamma, const float* z, size_t ldz, float* y,
                          void* yq, size_t ldy, size_t tokens, size_t heads, size_t d, float eps, void* stream) {
     return status(hipllm::launch_gated_rmsnorm(o, ldo, gamma, z, ldz, y, xg(yq), ldy, tokens, heads, d, eps,

@@ -110,6 +110,8 @@ SIGNATURES = {
     "hipllm_gdn_gates": (_I, [_P, _P, _S, _P, _P, _P, _P, _S, _S, _P]),
     "hipllm_conv1d_silu": (_I, [_P, _S, _P, _P, _P, _S, _S, _S, _S, _P]),
     "hipllm_l2norm_heads": (_I, [_P, _S, _S, _S, _S, _F, _P]),
+    "hipllm_gdn_chunk_scratch_floats": (_S, [_S, _S]),
+    "hipllm_gdn_scan_chunked": (_I, [_P, _P, _S, _P, _S, _P, _P, _P, _P, _S, _S, _S, _S, _S, _P, _S, _P]),
     "hipllm_gdn_scan": (_I, [_P, _P, _S, _P, _S, _P, _P, _P, _P, _S, _S, _S, _S, _S, _P]),
     "hipllm_gated_rmsnorm": (_I, [_P, _S, _P, _P, _S, _P, _P, _S, _S, _S, _S, _F, _P]),
     "hipllm_conv_l2norm": (_I, [_P, _S, _P, _P, _P, _S, _S, _S, _S, _S, _S, _F, _P]),
@@ -492,6 +494,13 @@ def _k_gdn_scan(q, k, ldqk, v, ldv, decay, beta, state, out, ldo, tokens, value_
                                 _ptr(out), ldo, tokens, value_heads, key_heads, d, _stream(stream)))
 
 
+def _k_gdn_scan_chunked(q, k, ldqk, v, ldv, decay, beta, state, out, ldo, tokens, value_heads, key_heads, d, scratch,
+                        stream=None):
+    check(lib().hipllm_gdn_scan_chunked(_ptr(q), _ptr(k), ldqk, _ptr(v), ldv, _ptr(decay), _ptr(beta), _ptr(state),
+                                        _ptr(out), ldo, tokens, value_heads, key_heads, d, _ptr(scratch),
+                                        0 if scratch is None else scratch.numel(), _stream(stream)))
+
+
 def _k_gated_rmsnorm(o, ldo, gamma, z, ldz, y, yq, ldy, tokens, heads, d, eps, stream=None):
     check(lib().hipllm_gated_rmsnorm(_ptr(o), ldo, _ptr(gamma), _ptr(z), ldz, _ptr(y), _ptr(yq), ldy, tokens,
                                      heads, d, eps, _stream(stream)))
@@ -572,6 +581,8 @@ kernels = types.SimpleNamespace(
     gemv_multi_norm=_k_gemv_multi_norm, gemv_routed_swiglu=_k_gemv_routed_swiglu,
     gemv_moe_combine=_k_gemv_moe_combine, gdn_gates=_k_gdn_gates,
     conv1d_silu=_k_conv1d_silu, l2norm_heads=_k_l2norm_heads, gdn_scan=_k_gdn_scan, gated_rmsnorm=_k_gated_rmsnorm,
+    gdn_scan_chunked=_k_gdn_scan_chunked,
+    gdn_chunk_scratch_floats=lambda t, h: lib().hipllm_gdn_chunk_scratch_floats(t, h),
     conv_l2norm=_k_conv_l2norm, gdn_scan_gated=_k_gdn_scan_gated,
     split_qgate_norm=_k_split_qgate_norm, gate_mul=_k_gate_mul,
     gemv_workspace_bytes=lambda k: lib().hipllm_gemv_workspace_bytes(k),
