@@ -44,6 +44,7 @@ HIP_SOURCES = [
     "runtime/gguf_reader.cpp",
     "runtime/hip_llm.cpp",
     "runtime/hip_moe.cpp",
+    "runtime/profile.cpp",
     "runtime/capi.cpp",
 ]
 TOOLS_SOURCES = ["tools/quants.cpp", "tools/synth_gguf.cpp", "tools/tools_capi.cpp"]

@@ -28,6 +28,33 @@ enum : int {
     kOverflowError = 5,
 };
 
+// Host side: the kernels a launcher just started (name, grid, block), kept
+// per host thread for the runtime's profiler, which takes them after each
+// launcher call (a few stores per launch; at most kLaunchNotes are kept).
+struct LaunchNote {
+    const char* kernel;
+    uint32_t grid[3];
+    uint32_t block[3];
+};
+constexpr int kLaunchNotes = 8;
+struct LaunchNotes {
+    LaunchNote note[kLaunchNotes];
+    int count = 0;
+};
+LaunchNotes& launch_notes();
+
+inline void note_launch(const char* kernel, dim3 grid, dim3 block) {
+    LaunchNotes& n = launch_notes();
+    if (n.count >= kLaunchNotes) return;
+    n.note[n.count++] = LaunchNote{kernel, {grid.x, grid.y, grid.z}, {block.x, block.y, block.z}};
+}
+
+#define HIPLLM_LAUNCH(kernel, grid, block, shm, stream, ...)                      \
+    do {                                                                          \
+        ::hipllm::note_launch(#kernel, dim3(grid), dim3(block));                  \
+        hipLaunchKernelGGL(kernel, grid, block, shm, stream, __VA_ARGS__);        \
+    } while (0)
+
 __host__ __device__ constexpr uint32_t block_elems(uint32_t type) {
     return type == kQ4_K || type == kQ6_K ? 256u : (type == kQ5_0 || type == kQ8_0) ? 32u : 1u;
 }

@@ -31,7 +31,7 @@ int launch_dequant_rows(uint32_t type, const void* w, size_t row_bytes, size_t r
     const uint32_t threads = 256;
     const size_t blocks = (total + threads - 1) / threads;
     if (blocks > 0x7fffffffull) return kLengthError;
-    hipLaunchKernelGGL(dequant_rows_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(threads), 0, stream,
+    HIPLLM_LAUNCH(dequant_rows_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(threads), 0, stream,
                        type, static_cast<const uint8_t*>(w), row_bytes, static_cast<uint32_t>(rows),
                        static_cast<uint32_t>(k), out);
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;

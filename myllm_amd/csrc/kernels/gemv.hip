@@ -865,7 +865,7 @@ int launch_typed(int tiling, const void* w, const void* w2, size_t row_bytes, co
     switch (tiling) {
 #define HIPLLM_GEMV_CASE(RR, OO)                                                                               \
     case 100 * RR + OO:                                                                                        \
-        hipLaunchKernelGGL((gemv_kernel<T, RR, OO, MODE>), grid, dim3(256), 0, stream, wp, wp2, row_bytes,     \
+        HIPLLM_LAUNCH((gemv_kernel<T, RR, OO, MODE>), grid, dim3(256), 0, stream, wp, wp2, row_bytes,     \
                            x, xq, bias, residual, y, yq, n, units, kblocks, batch);                            \
         break;
         HIPLLM_GEMV_CASE(1, 8)
@@ -910,7 +910,7 @@ int launch_typed_norm(int tiling, const void* w, const void* w2, size_t row_byte
     switch (tiling) {
 #define HIPLLM_GEMV_NORM_CASE(RR, OO)                                                                         \
     case 100 * RR + OO:                                                                                       \
-        hipLaunchKernelGGL((gemv_kernel<T, RR, OO, MODE, true>), grid, dim3(256), lds, stream, wp, wp2,        \
+        HIPLLM_LAUNCH((gemv_kernel<T, RR, OO, MODE, true>), grid, dim3(256), lds, stream, wp, wp2,        \
                            row_bytes, x, nullptr, bias, residual, y, yq, n, units, kblocks, Batch(), gamma,   \
                            eps, cmb);                                                                         \
         break;
@@ -1053,7 +1053,7 @@ int launch_prep_x(const float* x, XGroup* xq, size_t k, hipStream_t stream) {
     }
     if (k / 16 > 0xffffffffull) return kLengthError;
     const uint32_t groups = static_cast<uint32_t>(k / 16);
-    hipLaunchKernelGGL(prep_x_kernel, dim3((groups + 255) / 256), dim3(256), 0, stream, x, xq, groups);
+    HIPLLM_LAUNCH(prep_x_kernel, dim3((groups + 255) / 256), dim3(256), 0, stream, x, xq, groups);
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
@@ -1178,10 +1178,10 @@ int launch_routed(const void* wg, const void* wu, size_t row_bytes, const float*
     const auto* wp = static_cast<const uint8_t*>(wg);
     const auto* up = static_cast<const uint8_t*>(wu);
     if (n >= 8192) {
-        hipLaunchKernelGGL((gemv_kernel<T, 4, 8, 1, false, true>), dim3((n + 15) / 16, vectors), dim3(256), 0, stream,
+        HIPLLM_LAUNCH((gemv_kernel<T, 4, 8, 1, false, true>), dim3((n + 15) / 16, vectors), dim3(256), 0, stream,
                            wp, up, row_bytes, x, xq, nullptr, nullptr, y, yq, n, units, kblocks, b);
     } else {
-        hipLaunchKernelGGL((gemv_kernel<T, 2, 4, 1, false, true>), dim3((n + 15) / 16, vectors), dim3(256), 0, stream,
+        HIPLLM_LAUNCH((gemv_kernel<T, 2, 4, 1, false, true>), dim3((n + 15) / 16, vectors), dim3(256), 0, stream,
                            wp, up, row_bytes, x, xq, nullptr, nullptr, y, yq, n, units, kblocks, b);
     }
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
@@ -1266,7 +1266,7 @@ int launch_gemv_multi_norm(const GemvJob* jobs, size_t count, const float* x, co
     m.normq = normq;
     auto kernel = heavy == 0 ? gemv_multi_kernel<0>
                   : heavy == kMultiQ6K ? gemv_multi_kernel<kMultiQ6K> : gemv_multi_kernel<kMultiQ6K | kMultiQ6KSwiGLU>;
-    hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(total)), dim3(256), k * 4, stream, m);
+    HIPLLM_LAUNCH(kernel, dim3(static_cast<uint32_t>(total)), dim3(256), k * 4, stream, m);
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 

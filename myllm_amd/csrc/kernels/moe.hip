@@ -917,7 +917,7 @@ int launch_router_topk(const float* logits, size_t ld, size_t tokens, size_t exp
     if (experts > kMaxExperts || tokens > 0x7fffffffull || ld > 0xffffffffull) return kLengthError;
     auto kernel = experts <= 256 ? router_topk_kernel<4> : experts <= 512 ? router_topk_kernel<8>
                                                                            : router_topk_kernel<kMaxExperts / 64>;
-    hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(tokens)), dim3(64), 0, stream, logits,
+    HIPLLM_LAUNCH(kernel, dim3(static_cast<uint32_t>(tokens)), dim3(64), 0, stream, logits,
                        static_cast<uint32_t>(ld), static_cast<uint32_t>(experts), static_cast<uint32_t>(k), ids,
                        weights);
     return launched();
@@ -952,12 +952,12 @@ int launch_matmul_f32(const float* x, size_t ldx, const float* w, size_t ldw, fl
     const size_t kc = s > 1 ? ((k + s - 1) / s + kMmK - 1) / kMmK * kMmK : k;
     const dim3 grid(static_cast<uint32_t>((n + kMmTile - 1) / kMmTile),
                     static_cast<uint32_t>((m + kMmTile - 1) / kMmTile), static_cast<uint32_t>(s));
-    hipLaunchKernelGGL(matmul_f32_kernel, grid, dim3(256), 0, stream, x, static_cast<uint32_t>(ldx), w,
+    HIPLLM_LAUNCH(matmul_f32_kernel, grid, dim3(256), 0, stream, x, static_cast<uint32_t>(ldx), w,
                        static_cast<uint32_t>(ldw), y, static_cast<uint32_t>(ldy), static_cast<uint32_t>(m),
                        static_cast<uint32_t>(n), static_cast<uint32_t>(k), static_cast<uint32_t>(kc),
                        s > 1 ? scratch : nullptr);
     if (s > 1) {
-        hipLaunchKernelGGL(matmul_reduce_kernel, dim3(blocks_for(m * n, 256)), dim3(256), 0, stream, scratch, y,
+        HIPLLM_LAUNCH(matmul_reduce_kernel, dim3(blocks_for(m * n, 256)), dim3(256), 0, stream, scratch, y,
                            static_cast<uint32_t>(ldy), static_cast<uint32_t>(m), static_cast<uint32_t>(n),
                            static_cast<uint32_t>(s));
     }
@@ -972,7 +972,7 @@ int launch_route_groups(const int32_t* ids, size_t n, size_t experts, size_t vma
                         uint32_t* ngroups, hipStream_t stream) {
     if (!ids || !order || !groups || !ngroups || n == 0 || experts == 0 || vmax == 0) return kInvalidArgument;
     if (n > kRouteGroupsMax || experts > kMaxExperts || vmax > 0xffffu) return kLengthError;
-    hipLaunchKernelGGL(route_groups_kernel, dim3(1), dim3(1024), 0, stream, ids, static_cast<uint32_t>(n),
+    HIPLLM_LAUNCH(route_groups_kernel, dim3(1), dim3(1024), 0, stream, ids, static_cast<uint32_t>(n),
                        static_cast<uint32_t>(experts), static_cast<uint32_t>(vmax), order, groups, ngroups);
     return launched();
 }
@@ -994,7 +994,7 @@ int launch_moe_combine_norm(const float* residual, const float* down, const floa
         }
     }
     if (tokens > 0x7fffffffull || ld_sgate > 0xffffffffull || h > 0x7fffffffull / 4) return kLengthError;
-    hipLaunchKernelGGL(moe_combine_norm_kernel, dim3(static_cast<uint32_t>(tokens)), dim3(256), 0, stream, residual,
+    HIPLLM_LAUNCH(moe_combine_norm_kernel, dim3(static_cast<uint32_t>(tokens)), dim3(256), 0, stream, residual,
                        down, w, shared, sgate, static_cast<uint32_t>(ld_sgate), out, gamma, norm, normq,
                        static_cast<uint32_t>(h), static_cast<uint32_t>(k), eps);
     return launched();
@@ -1007,7 +1007,7 @@ int launch_moe_combine(const float* residual, const float* down, const float* w,
         return kInvalidArgument;
     }
     if (tokens * h > 0x7fffffffull * 256ull || ld_sgate > 0xffffffffull || h > 0xffffffffull) return kLengthError;
-    hipLaunchKernelGGL(moe_combine_kernel, dim3(blocks_for(tokens * h, 256)), dim3(256), 0, stream, residual, down,
+    HIPLLM_LAUNCH(moe_combine_kernel, dim3(blocks_for(tokens * h, 256)), dim3(256), 0, stream, residual, down,
                        w, shared, sgate, static_cast<uint32_t>(ld_sgate), out, static_cast<uint32_t>(tokens),
                        static_cast<uint32_t>(h), static_cast<uint32_t>(k));
     return launched();
@@ -1019,7 +1019,7 @@ int launch_gdn_gates(const float* alpha, const float* beta_raw, size_t ld, const
         return kInvalidArgument;
     }
     if (tokens * heads > 0x7fffffffull) return kLengthError;
-    hipLaunchKernelGGL(gdn_gates_kernel, dim3(blocks_for(tokens * heads, 256)), dim3(256), 0, stream, alpha,
+    HIPLLM_LAUNCH(gdn_gates_kernel, dim3(blocks_for(tokens * heads, 256)), dim3(256), 0, stream, alpha,
                        beta_raw, static_cast<uint32_t>(ld), dt_bias, a, decay, beta, static_cast<uint32_t>(tokens),
                        static_cast<uint32_t>(heads));
     return launched();
@@ -1035,7 +1035,7 @@ int launch_conv1d_silu(const float* x, size_t ldx, float* history, const float* 
     if (channels > 0x7fffffffull || (tokens + kConvChunk - 1) / kConvChunk > 65535) return kLengthError;
     const dim3 grid(static_cast<uint32_t>((channels + 63) / 64),
                     static_cast<uint32_t>((tokens + kConvChunk - 1) / kConvChunk));
-    hipLaunchKernelGGL(conv1d_silu_kernel, grid, dim3(256), 0, stream, x, static_cast<uint32_t>(ldx), history, w, out,
+    HIPLLM_LAUNCH(conv1d_silu_kernel, grid, dim3(256), 0, stream, x, static_cast<uint32_t>(ldx), history, w, out,
                        static_cast<uint32_t>(ldo), static_cast<uint32_t>(tokens), static_cast<uint32_t>(channels),
                        static_cast<uint32_t>(ksize));
     return launched();
@@ -1044,7 +1044,7 @@ int launch_conv1d_silu(const float* x, size_t ldx, float* history, const float* 
 int launch_l2norm_heads(float* x, size_t ld, size_t tokens, size_t heads, size_t d, float eps, hipStream_t stream) {
     if (!x || tokens == 0 || heads == 0 || d == 0 || ld < heads * d || !(eps >= 0.0f)) return kInvalidArgument;
     if (tokens > 0x7fffffffull || heads > 65535) return kLengthError;
-    hipLaunchKernelGGL(l2norm_heads_kernel, dim3(static_cast<uint32_t>(tokens), static_cast<uint32_t>(heads)),
+    HIPLLM_LAUNCH(l2norm_heads_kernel, dim3(static_cast<uint32_t>(tokens), static_cast<uint32_t>(heads)),
                        dim3(64), 0, stream, x, static_cast<uint32_t>(ld), static_cast<uint32_t>(d), eps);
     return launched();
 }
@@ -1068,16 +1068,16 @@ int launch_gdn_scan(const float* q, const float* k, size_t ldqk, const float* v,
                      ldqk % 4 == 0;
     const uint32_t lq = static_cast<uint32_t>(ldqk), lv = static_cast<uint32_t>(ldv), lo = static_cast<uint32_t>(ldo);
     if (d == 64 && vec) {
-        hipLaunchKernelGGL((gdn_scan_kernel<64, true>), grid, dim3(64), 0, stream, q, k, lq, v, lv, decay, beta, state,
+        HIPLLM_LAUNCH((gdn_scan_kernel<64, true>), grid, dim3(64), 0, stream, q, k, lq, v, lv, decay, beta, state,
                            out, lo, T, Hv, Hk);
     } else if (d == 64) {
-        hipLaunchKernelGGL((gdn_scan_kernel<64, false>), grid, dim3(64), 0, stream, q, k, lq, v, lv, decay, beta, state,
+        HIPLLM_LAUNCH((gdn_scan_kernel<64, false>), grid, dim3(64), 0, stream, q, k, lq, v, lv, decay, beta, state,
                            out, lo, T, Hv, Hk);
     } else if (d == 128 && vec) {
-        hipLaunchKernelGGL((gdn_scan_kernel<128, true>), grid, dim3(64), 0, stream, q, k, lq, v, lv, decay, beta,
+        HIPLLM_LAUNCH((gdn_scan_kernel<128, true>), grid, dim3(64), 0, stream, q, k, lq, v, lv, decay, beta,
                            state, out, lo, T, Hv, Hk);
     } else if (d == 128) {
-        hipLaunchKernelGGL((gdn_scan_kernel<128, false>), grid, dim3(64), 0, stream, q, k, lq, v, lv, decay, beta,
+        HIPLLM_LAUNCH((gdn_scan_kernel<128, false>), grid, dim3(64), 0, stream, q, k, lq, v, lv, decay, beta,
                            state, out, lo, T, Hv, Hk);
     } else {
         return kInvalidArgument;  // state size 64 or 128
@@ -1113,9 +1113,9 @@ int launch_gdn_scan_chunked(const float* q, const float* k, size_t ldqk, const f
     auto run = [&](auto dc, auto vc) {
         constexpr uint32_t DD = decltype(dc)::value;
         constexpr bool V = decltype(vc)::value;
-        hipLaunchKernelGGL((gdn_chunk_prep_kernel<DD, V>), dim3(Hv, chunks), dim3(256), 0, stream, q, k, lq, decay,
+        HIPLLM_LAUNCH((gdn_chunk_prep_kernel<DD, V>), dim3(Hv, chunks), dim3(256), 0, stream, q, k, lq, decay,
                            beta, scratch, T, Hv, Hk);
-        hipLaunchKernelGGL((gdn_chunk_scan_kernel<DD, V>), dim3(Hv * (DD / kChunkCols)), dim3(256), 0, stream, q, k,
+        HIPLLM_LAUNCH((gdn_chunk_scan_kernel<DD, V>), dim3(Hv * (DD / kChunkCols)), dim3(256), 0, stream, q, k,
                            lq, v, lv, decay, beta, scratch, state, out, lo, T, Hv, Hk);
     };
     using D128 = std::integral_constant<uint32_t, 128>;
@@ -1136,7 +1136,7 @@ int launch_gated_rmsnorm(const float* o, size_t ldo, const float* gamma, const f
     }
     if (yq && (d % 16 != 0 || ldy % 16 != 0 || reinterpret_cast<uintptr_t>(yq) % 16 != 0)) return kInvalidArgument;
     if (tokens > 0x7fffffffull || heads > 65535) return kLengthError;
-    hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3(static_cast<uint32_t>(tokens), static_cast<uint32_t>(heads)),
+    HIPLLM_LAUNCH(gated_rmsnorm_kernel, dim3(static_cast<uint32_t>(tokens), static_cast<uint32_t>(heads)),
                        dim3(64), 0, stream, o, static_cast<uint32_t>(ldo), gamma, z, static_cast<uint32_t>(ldz), y,
                        yq, static_cast<uint32_t>(ldy), static_cast<uint32_t>(d), eps);
     return launched();
@@ -1157,10 +1157,10 @@ int launch_conv_l2norm(const float* x, size_t ldx, float* history, const float* 
     const uint32_t T = static_cast<uint32_t>(tokens), C = static_cast<uint32_t>(channels),
                    K = static_cast<uint32_t>(ksize), NC = static_cast<uint32_t>(norm_channels);
     if (d == 64) {
-        hipLaunchKernelGGL(conv_l2norm_kernel<64>, grid, dim3(64), 0, stream, x, static_cast<uint32_t>(ldx), history,
+        HIPLLM_LAUNCH(conv_l2norm_kernel<64>, grid, dim3(64), 0, stream, x, static_cast<uint32_t>(ldx), history,
                            w, out, static_cast<uint32_t>(ldo), T, C, K, NC, eps);
     } else {
-        hipLaunchKernelGGL(conv_l2norm_kernel<128>, grid, dim3(128), 0, stream, x, static_cast<uint32_t>(ldx), history,
+        HIPLLM_LAUNCH(conv_l2norm_kernel<128>, grid, dim3(128), 0, stream, x, static_cast<uint32_t>(ldx), history,
                            w, out, static_cast<uint32_t>(ldo), T, C, K, NC, eps);
     }
     return launched();
@@ -1185,12 +1185,12 @@ int launch_gdn_scan_gated(const float* q, const float* k, size_t ldqk, const flo
     const uint32_t T = static_cast<uint32_t>(tokens), Hk = static_cast<uint32_t>(key_heads);
     switch (d) {
     case 64:
-        hipLaunchKernelGGL(gdn_scan_gated_kernel<64>, grid, dim3(256), 0, stream, q, k, static_cast<uint32_t>(ldqk), v,
+        HIPLLM_LAUNCH(gdn_scan_gated_kernel<64>, grid, dim3(256), 0, stream, q, k, static_cast<uint32_t>(ldqk), v,
                            static_cast<uint32_t>(ldv), alpha, beta_raw, static_cast<uint32_t>(ld_ab), dt_bias, a,
                            state, z, static_cast<uint32_t>(ldz), gamma, y, yq, static_cast<uint32_t>(ldy), T, Hk, eps);
         break;
     case 128:
-        hipLaunchKernelGGL(gdn_scan_gated_kernel<128>, grid, dim3(256), 0, stream, q, k, static_cast<uint32_t>(ldqk), v,
+        HIPLLM_LAUNCH(gdn_scan_gated_kernel<128>, grid, dim3(256), 0, stream, q, k, static_cast<uint32_t>(ldqk), v,
                            static_cast<uint32_t>(ldv), alpha, beta_raw, static_cast<uint32_t>(ld_ab), dt_bias, a,
                            state, z, static_cast<uint32_t>(ldz), gamma, y, yq, static_cast<uint32_t>(ldy), T, Hk, eps);
         break;
@@ -1209,7 +1209,7 @@ int launch_split_qgate_norm(const float* mixed, size_t ldm, const float* kv, siz
     }
     if (ldm < 2 * hq * d || ldkv < 2 * hkv * d || ldqkv < (hq + 2 * hkv) * d || ldg < hq * d) return kInvalidArgument;
     if (tokens > 0x7fffffffull || hq + hkv > 65535) return kLengthError;
-    hipLaunchKernelGGL(split_qgate_norm_kernel, dim3(static_cast<uint32_t>(tokens), static_cast<uint32_t>(hq + hkv)),
+    HIPLLM_LAUNCH(split_qgate_norm_kernel, dim3(static_cast<uint32_t>(tokens), static_cast<uint32_t>(hq + hkv)),
                        dim3(64), 0, stream, mixed, static_cast<uint32_t>(ldm), kv, static_cast<uint32_t>(ldkv),
                        q_gamma, k_gamma, qkv, static_cast<uint32_t>(ldqkv), gate, static_cast<uint32_t>(ldg),
                        static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv), static_cast<uint32_t>(d), eps);
@@ -1221,7 +1221,7 @@ int launch_gate_mul(const float* a, const float* g, float* y, XGroup* yq, size_t
     if (yq && reinterpret_cast<uintptr_t>(yq) % 16 != 0) return kInvalidArgument;
     const size_t n16 = n / 16;
     if (n16 > 0x7fffffffull) return kLengthError;
-    hipLaunchKernelGGL(gate_mul_kernel, dim3(blocks_for(n16, 256)), dim3(256), 0, stream, a, g, y, yq, n16);
+    HIPLLM_LAUNCH(gate_mul_kernel, dim3(blocks_for(n16, 256)), dim3(256), 0, stream, a, g, y, yq, n16);
     return launched();
 }
 

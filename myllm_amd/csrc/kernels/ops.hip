@@ -506,7 +506,7 @@ int launch_rmsnorm(const float* x, const float* gamma, float* y, XGroup* yq, siz
         return kInvalidArgument;
     }
     if (!(eps > 0.0f)) return kInvalidArgument;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, stream, x, gamma, y, yq,
+    HIPLLM_LAUNCH(rmsnorm_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, stream, x, gamma, y, yq,
                        static_cast<uint32_t>(cols), eps);
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
@@ -516,7 +516,7 @@ int launch_embed(uint32_t type, const void* table, size_t row_bytes, const int32
     if (!table || !ids || !out || rows == 0 || cols == 0 || vocab == 0) return kInvalidArgument;
     if (cols % block_elems(type) != 0) return kInvalidArgument;
     const dim3 grid(static_cast<uint32_t>((cols + 255) / 256), static_cast<uint32_t>(rows));
-    hipLaunchKernelGGL(embed_kernel, grid, dim3(256), 0, stream, type, static_cast<const uint8_t*>(table), row_bytes,
+    HIPLLM_LAUNCH(embed_kernel, grid, dim3(256), 0, stream, type, static_cast<const uint8_t*>(table), row_bytes,
                        ids, static_cast<uint32_t>(vocab), static_cast<uint32_t>(cols), out);
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
@@ -528,7 +528,7 @@ int launch_rope_kv(float* qkv, const float* cos_sin, size_t rot, size_t hq, size
         return kInvalidArgument;
     }
     if (hq == 0 || hkv == 0 || hq % hkv != 0 || row_stride < (hq + 2 * hkv) * d) return kInvalidArgument;
-    hipLaunchKernelGGL(rope_kv_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, stream, qkv,
+    HIPLLM_LAUNCH(rope_kv_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, stream, qkv,
                        reinterpret_cast<const float2*>(cos_sin), static_cast<uint32_t>(rot / 2),
                        static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv), static_cast<uint32_t>(d),
                        static_cast<uint32_t>(pos0), static_cast<uint32_t>(row_stride), kcache, vcache, dpos);
@@ -567,12 +567,12 @@ int launch_attn_decode(const float* q, const float* kcache, const float* vcache,
     if (len > 0xffffffffull || capacity > 0xffffffffull || hq > 0xffffull) return kLengthError;
     const uint32_t splits = attn_splits(dpos ? capacity : len, d);
     // Read-only use of the caches (no RoPE table): the kernel writes them only in the fused form.
-    hipLaunchKernelGGL(attn_decode_partial, dim3(static_cast<uint32_t>(hq), splits), dim3(256), 0, stream, q,
+    HIPLLM_LAUNCH(attn_decode_partial, dim3(static_cast<uint32_t>(hq), splits), dim3(256), 0, stream, q,
                        const_cast<float*>(kcache), const_cast<float*>(vcache), scratch, static_cast<uint32_t>(hq),
                        static_cast<uint32_t>(hkv), static_cast<uint32_t>(d), static_cast<uint32_t>(len), dpos, scale,
                        splits, nullptr, 0u, out, outq, nullptr);
     if (splits > 1) {
-        hipLaunchKernelGGL(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out,
+        HIPLLM_LAUNCH(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out,
                            outq, static_cast<uint32_t>(d), splits, nullptr);
     }
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
@@ -592,12 +592,12 @@ int launch_attn_decode_rope(const float* qkv, const float* cos_sin, size_t rot, 
     if (outq && reinterpret_cast<uintptr_t>(outq) % 16 != 0) return kInvalidArgument;
     if (pos >= 0xffffffffull || capacity > 0xffffffffull || hq > 0xffffull) return kLengthError;
     const uint32_t splits = attn_splits(dpos ? capacity : pos + 1, d);
-    hipLaunchKernelGGL(attn_decode_partial, dim3(static_cast<uint32_t>(hq), splits), dim3(256), 0, stream, qkv,
+    HIPLLM_LAUNCH(attn_decode_partial, dim3(static_cast<uint32_t>(hq), splits), dim3(256), 0, stream, qkv,
                        kcache, vcache, scratch, static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv),
                        static_cast<uint32_t>(d), static_cast<uint32_t>(pos + 1), dpos, scale, splits,
                        reinterpret_cast<const float2*>(cos_sin), static_cast<uint32_t>(rot / 2), out, outq, gate);
     if (splits > 1) {
-        hipLaunchKernelGGL(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out,
+        HIPLLM_LAUNCH(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out,
                            outq, static_cast<uint32_t>(d), splits, gate);
     }
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
@@ -609,7 +609,7 @@ int launch_attn_prefill(const float* q, size_t q_stride, const float* kcache, co
     if (!q || !kcache || !vcache || !out || rows == 0 || hq == 0 || hkv == 0 || hq % hkv) return kInvalidArgument;
     if (d == 0 || d > 256 || d % 4 != 0 || q_stride < hq * d || out_stride < hq * d) return kInvalidArgument;
     if (rows > 0x7fffffffull || hq > 0xffffull || pos0 + rows > 0xffffffffull) return kLengthError;
-    hipLaunchKernelGGL(attn_prefill_kernel, dim3(static_cast<uint32_t>(rows), static_cast<uint32_t>(hq)), dim3(256),
+    HIPLLM_LAUNCH(attn_prefill_kernel, dim3(static_cast<uint32_t>(rows), static_cast<uint32_t>(hq)), dim3(256),
                        0, stream, q, static_cast<uint32_t>(q_stride), kcache, vcache, out,
                        static_cast<uint32_t>(out_stride), static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv),
                        static_cast<uint32_t>(d), static_cast<uint32_t>(pos0), scale);
@@ -628,9 +628,9 @@ int launch_argmax(const float* x, size_t n, uint32_t* out, void* scratch, hipStr
     const uint32_t parts = static_cast<uint32_t>((n + kArgmaxPerBlock - 1) / kArgmaxPerBlock);
     float* pv = static_cast<float*>(scratch);
     uint32_t* pi = reinterpret_cast<uint32_t*>(pv + parts);
-    hipLaunchKernelGGL(argmax_partial, dim3(parts), dim3(256), 0, stream, x, static_cast<uint32_t>(n),
+    HIPLLM_LAUNCH(argmax_partial, dim3(parts), dim3(256), 0, stream, x, static_cast<uint32_t>(n),
                        kArgmaxPerBlock, pv, pi);
-    hipLaunchKernelGGL(argmax_final, dim3(1), dim3(256), 0, stream, pv, pi, parts, out);
+    HIPLLM_LAUNCH(argmax_final, dim3(1), dim3(256), 0, stream, pv, pi, parts, out);
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
@@ -639,14 +639,14 @@ int launch_swiglu(const float* g, const float* u, float* y, XGroup* yq, size_t n
         return kInvalidArgument;
     }
     const uint32_t groups = static_cast<uint32_t>((n + 15) / 16);
-    hipLaunchKernelGGL(swiglu_kernel, dim3((groups + 255) / 256), dim3(256), 0, stream, g, u, y, yq,
+    HIPLLM_LAUNCH(swiglu_kernel, dim3((groups + 255) / 256), dim3(256), 0, stream, g, u, y, yq,
                        static_cast<uint32_t>(n));
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
 int launch_add(const float* a, const float* b, float* y, size_t n, hipStream_t stream) {
     if (!a || !b || !y || n == 0) return kInvalidArgument;
-    hipLaunchKernelGGL(add_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, stream, a, b, y, n);
+    HIPLLM_LAUNCH(add_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, stream, a, b, y, n);
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 

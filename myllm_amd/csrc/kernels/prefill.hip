@@ -752,11 +752,11 @@ void launch_tile(const void* w, size_t row_bytes, const _Float16* xb, const floa
     splits = (steps + per - 1) / per;  // every split gets at least one step
     if (splits > 1) {
         const size_t total = static_cast<size_t>(m) * n;
-        hipLaunchKernelGGL(gemm_init_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, stream,
+        HIPLLM_LAUNCH(gemm_init_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, stream,
                            y, ldy, residual, bias, m, n);
     }
     const dim3 grid(((n + BN - 1) / BN) * ((m + BM - 1) / BM), 1, splits);
-    hipLaunchKernelGGL((gemm_mfma_kernel<T, NSUB, MSUB>), grid, dim3(256), 0, stream,
+    HIPLLM_LAUNCH((gemm_mfma_kernel<T, NSUB, MSUB>), grid, dim3(256), 0, stream,
                        static_cast<const uint8_t*>(w), row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, per);
 }
 
@@ -767,7 +767,7 @@ void launch_gather(const void* w, size_t row_bytes, const _Float16* xb, const fl
                    uint32_t k, uint32_t ldy, uint32_t max_groups, const Gather& g, hipStream_t stream) {
     constexpr uint32_t BN = 4 * 32;
     const dim3 grid((n + BN - 1) / BN, max_groups, 1);
-    hipLaunchKernelGGL((gemm_mfma_kernel<T, 1, 2, true>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w),
+    HIPLLM_LAUNCH((gemm_mfma_kernel<T, 1, 2, true>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w),
                        row_bytes, xb, xscale, nullptr, nullptr, y, 0u, n, k, ldy, k / kStepK, g);
 }
 
@@ -781,11 +781,11 @@ void launch_lds(const void* w, size_t row_bytes, const _Float16* xb, const float
     splits = (steps + per - 1) / per;
     if (splits > 1) {
         const size_t total = static_cast<size_t>(m) * n;
-        hipLaunchKernelGGL(gemm_init_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, stream,
+        HIPLLM_LAUNCH(gemm_init_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, stream,
                            y, ldy, residual, bias, m, n);
     }
     const dim3 grid(((n + BN - 1) / BN) * ((m + BM - 1) / BM), 1, splits);
-    hipLaunchKernelGGL((gemm_lds_kernel<T, MT>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w),
+    HIPLLM_LAUNCH((gemm_lds_kernel<T, MT>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w),
                        row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, per);
 }
 
@@ -824,7 +824,7 @@ int launch_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m,
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(xh) % 16 != 0) return kInvalidArgument;
     if (m > 0x7fffffffull || k > 0xffffffffull) return kLengthError;
     const uint32_t chunks = static_cast<uint32_t>((k + kF16Chunk - 1) / kF16Chunk);
-    hipLaunchKernelGGL(to_f16_kernel, dim3(static_cast<uint32_t>(m), chunks), dim3(256), 0, stream, x, ldx,
+    HIPLLM_LAUNCH(to_f16_kernel, dim3(static_cast<uint32_t>(m), chunks), dim3(256), 0, stream, x, ldx,
                        static_cast<_Float16*>(xh), xscale, static_cast<uint32_t>(k));
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }

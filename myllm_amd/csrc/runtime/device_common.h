@@ -6,6 +6,7 @@
 
 #include "../kernels/common.h"
 #include "gguf_reader.h"
+#include "profile.h"
 
 #include <hip/hip_runtime.h>
 
@@ -23,8 +24,12 @@ inline void hip_check(hipError_t e, const char* what) {
 }
 
 // Kernel launcher status -> the reference's exception type.
+// A profiling session (if any) sees every successful launcher call.
 inline void launch_check(int status, const char* what) {
-    if (status == hipllm::kOk) return;
+    if (status == hipllm::kOk) {
+        if (RunProfiler* p = active_run_profiler()) p->on_launch(what);
+        return;
+    }
     if (status == hipllm::kInvalidArgument) {
         throw std::invalid_argument(std::string(what) + ": invalid kernel arguments");
     }

@@ -118,13 +118,14 @@ struct HipLLM::Impl {
     hipGraph_t decode_graph = nullptr;
     hipGraphExec_t decode_exec = nullptr;
 
-    std::FILE* profile = nullptr;
+    std::unique_ptr<RunProfiler> prof;
+    GraphKernels decode_graph_kernels;
 
     ~Impl() {
         if (stream) hipStreamSynchronize(stream);
         drop_decode_graph();
         if (host_step) hipHostFree(host_step);
-        if (profile) std::fclose(profile);
+        prof.reset();
         weights.release();
         if (kv_arena) hipFree(kv_arena);
         if (rope_table) hipFree(rope_table);
@@ -485,6 +486,7 @@ void HipLLM::Impl::capture_decode() {
     }
     hip_check(hipStreamEndCapture(stream, &decode_graph), "hipStreamEndCapture");
     hip_check(hipGraphInstantiate(&decode_exec, decode_graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+    decode_graph_kernels = graph_kernels(decode_graph);
 }
 
 void HipLLM::Impl::drop_decode_graph() {
@@ -619,6 +621,69 @@ std::int32_t HipLLM::Impl::read_token() {
     return static_cast<std::int32_t>(t);
 }
 
+// Logical traffic of one forward, from shapes, for the operator table: the
+// operator list of the reference backend's estimate (metal_llm.mm:307-433),
+// in FP32 tensor bytes whatever the weights' storage.
+namespace {
+OpTraffic layer_traffic(const GgufModelConfig& c, std::size_t rows, std::size_t keys, bool prompt) {
+    const std::size_t H = c.embedding_size, F = c.feed_forward_size, D = c.head_size;
+    const std::size_t q = c.attention_head_count * D, kv = c.kv_head_count * D;
+    auto proj = [&](std::size_t out, std::size_t in, bool bias) {
+        return prompt ? traffic_matmul(rows, out, in, bias) : traffic_gemv(in, out);
+    };
+    OpTraffic t;
+    t += traffic_elementwise(rows * H, 5, 3, 1);  // RMSNorm
+    t += proj(q, H, true);
+    t += proj(kv, H, true);
+    t += proj(kv, H, true);
+    t += traffic_elementwise(rows * (q + kv), 6, 1, 1);  // RoPE
+    t += traffic_copy(static_cast<std::uint64_t>(rows) * kv * 4 * 2, 1);  // KV write
+    for (std::size_t h = 0; h < c.attention_head_count; ++h) {
+        if (prompt) {
+            OpTraffic qk = traffic_matmul(rows, rows, D);
+            qk.flops += static_cast<std::uint64_t>(rows) * rows;  // scale
+            t += qk;
+            t += traffic_elementwise(rows * rows, 4, 3, 2);  // mask + softmax
+            t += traffic_matmul(rows, D, rows);
+        } else {
+            t += traffic_gemv(D, keys);
+            t += traffic_elementwise(keys, 4, 3, 2);
+            t += traffic_gemv(keys, D);
+        }
+    }
+    t += prompt ? traffic_matmul(rows, H, q) : traffic_gemv(q, H);
+    t += traffic_copy(static_cast<std::uint64_t>(rows) * H * 4, 1);  // residual
+    t += traffic_elementwise(rows * H, 5, 3, 1);
+    t += proj(F, H, false);
+    t += proj(F, H, false);
+    t += traffic_elementwise(rows * F, 8, 2, 1);  // SwiGLU
+    t += prompt ? traffic_matmul(rows, H, F) : traffic_gemv(F, H);
+    t += traffic_copy(static_cast<std::uint64_t>(rows) * H * 4, 1);
+    return t;
+}
+
+OpTraffic head_traffic(const GgufModelConfig& c, std::size_t rows) {
+    OpTraffic t = traffic_elementwise(rows * c.embedding_size, 5, 2, 1);  // final norm
+    t += traffic_gemv(c.embedding_size, c.vocabulary_size);              // LM head, last row
+    t += traffic_elementwise(c.vocabulary_size, 1, 1, 0);                // argmax
+    return t;
+}
+
+OpTraffic prefill_traffic(const GgufModelConfig& c, std::size_t rows) {
+    OpTraffic t = traffic_copy(static_cast<std::uint64_t>(rows) * c.embedding_size * 4, 1);  // embedding
+    for (std::size_t l = 0; l < c.layer_count; ++l) t += layer_traffic(c, rows, rows, true);
+    t += head_traffic(c, rows);
+    return t;
+}
+
+OpTraffic decode_traffic(const GgufModelConfig& c, std::size_t keys) {
+    OpTraffic t = traffic_copy(static_cast<std::uint64_t>(c.embedding_size) * 4, 1);
+    for (std::size_t l = 0; l < c.layer_count; ++l) t += layer_traffic(c, 1, keys, false);
+    t += head_traffic(c, 1);
+    return t;
+}
+}  // namespace
+
 int parse_device_spec(const std::string& spec) {
     if (spec.empty()) return -1;
     const std::string digits = spec.rfind("hip:", 0) == 0 ? spec.substr(4) : spec;
@@ -656,7 +721,7 @@ std::int32_t HipLLM::prefill(const std::vector<std::int32_t>& ids) {
         }
     }
     hip_check(hipSetDevice(m.device), "hipSetDevice");
-    const auto t0 = std::chrono::steady_clock::now();
+    if (m.prof) m.prof->begin("prefill", ids.size(), "prefill.gpu_resident");
     m.ensure_prompt_capacity(ids.size());
     std::memcpy(m.host_ids, ids.data(), ids.size() * 4);
     hip_check(hipMemcpyAsync(m.act.ids, m.host_ids, ids.size() * 4, hipMemcpyHostToDevice, m.stream), "hipMemcpy(ids)");
@@ -665,12 +730,10 @@ std::int32_t HipLLM::prefill(const std::vector<std::int32_t>& ids) {
     } else {
         for (std::size_t t = 0; t < ids.size(); ++t) m.token_step(m.act.ids + t, t, t + 1 == ids.size());
     }
+    if (m.prof) m.prof->mark_gpu_end();
     const std::int32_t token = m.read_token();
     m.sequence_length = ids.size();
-    if (m.profile) {
-        const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-        std::fprintf(m.profile, "prefill,%zu,%zu,%.6f\n", ids.size(), ids.size(), ms);
-    }
+    if (m.prof) m.prof->end(prefill_traffic(m.config, ids.size()));
     return token;
 }
 
@@ -684,38 +747,34 @@ std::int32_t HipLLM::decode(std::int32_t id) {
     const std::size_t pos = m.sequence_length;
     if (pos >= m.max_sequence) throw std::length_error("HIP decode exceeds the allocated sequence capacity");
     hip_check(hipSetDevice(m.device), "hipSetDevice");
-    const auto t0 = std::chrono::steady_clock::now();
+    if (m.prof) m.prof->begin("decode", pos + 1, "decode.gpu_resident");
     m.host_step[0] = static_cast<std::uint32_t>(id);
     m.host_step[1] = static_cast<std::uint32_t>(pos);
     hip_check(hipMemcpyAsync(m.act.step, m.host_step, 8, hipMemcpyHostToDevice, m.stream), "hipMemcpy(step)");
-    if (m.decode_graphs) {
+    // Detailed profiling times every launch, so the step runs eagerly.
+    const bool graph = m.decode_graphs && !(m.prof && m.prof->detailed());
+    if (graph) {
         if (!m.decode_exec) m.capture_decode();
         hip_check(hipGraphLaunch(m.decode_exec, m.stream), "hipGraphLaunch(decode)");
     } else {
         m.token_step(reinterpret_cast<const std::int32_t*>(m.act.step), pos, true);
     }
+    if (m.prof) m.prof->mark_gpu_end();
     const std::int32_t token = m.read_token();
     m.sequence_length = pos + 1;
-    if (m.profile) {
-        const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-        std::fprintf(m.profile, "decode,1,%zu,%.6f\n", pos + 1, ms);
-    }
+    if (m.prof) m.prof->end(decode_traffic(m.config, pos + 1), graph ? &m.decode_graph_kernels : nullptr);
     return token;
 }
 
-void HipLLM::enable_profiling(const std::string& csv_path, bool) {
+void HipLLM::enable_profiling(const std::string& csv_path, bool detailed_kernel_timestamps) {
     if (!impl_) throw std::runtime_error("HIP model is not initialized");
     disable_profiling();
-    impl_->profile = std::fopen(csv_path.c_str(), "w");
-    if (!impl_->profile) throw std::runtime_error("cannot open profile CSV: " + csv_path);
-    std::fprintf(impl_->profile, "phase,tokens,sequence,wall_ms\n");
+    hip_check(hipSetDevice(impl_->device), "hipSetDevice");
+    impl_->prof = std::make_unique<RunProfiler>(csv_path, detailed_kernel_timestamps, impl_->stream);
 }
 
 void HipLLM::disable_profiling() {
-    if (impl_ && impl_->profile) {
-        std::fclose(impl_->profile);
-        impl_->profile = nullptr;
-    }
+    if (impl_) impl_->prof.reset();
 }
 
 const GgufModelConfig& HipLLM::config() const {

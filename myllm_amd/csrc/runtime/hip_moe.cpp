@@ -151,7 +151,8 @@ struct HipMoeLLM::Impl {
     std::uint32_t* host_step = nullptr;  // pinned [token id, position]
     std::size_t host_ids_cap = 0;
     std::size_t last_rows = 0;
-    std::FILE* profile = nullptr;
+    std::unique_ptr<RunProfiler> prof;
+    GraphKernels decode_graph_kernels;
 
     // One decode step recorded as a HIP graph (kernels read the token and
     // position from act.step) and replayed per token.
@@ -168,7 +169,7 @@ struct HipMoeLLM::Impl {
         if (stream) hipStreamSynchronize(stream);
         drop_decode_graph();
         if (host_step) hipHostFree(host_step);
-        if (profile) std::fclose(profile);
+        prof.reset();
         weights.release();
         if (state_arena) hipFree(state_arena);
         if (rope_table) hipFree(rope_table);
@@ -980,6 +981,7 @@ void HipMoeLLM::Impl::capture_decode() {
     }
     hip_check(hipStreamEndCapture(stream, &decode_graph), "hipStreamEndCapture");
     hip_check(hipGraphInstantiate(&decode_exec, decode_graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+    decode_graph_kernels = graph_kernels(decode_graph);
 }
 
 void HipMoeLLM::Impl::drop_decode_graph() {
@@ -1028,19 +1030,18 @@ std::int32_t HipMoeLLM::prefill(const std::vector<std::int32_t>& ids) {
         }
     }
     hip_check(hipSetDevice(m.device), "hipSetDevice");
-    const auto t0 = std::chrono::steady_clock::now();
+    if (m.prof) m.prof->begin("prefill", ids.size(), "prefill.gpu_moe");
     m.ensure_rows(ids.size());
     std::memcpy(m.host_ids, ids.data(), ids.size() * 4);
     hip_check(hipMemcpyAsync(m.act.ids, m.host_ids, ids.size() * 4, hipMemcpyHostToDevice, m.stream),
               "hipMemcpy(ids)");
     m.forward(ids.size(), 0, m.act.ids);
+    if (m.prof) m.prof->mark_gpu_end();
     const std::int32_t token = m.read_token();
     m.sequence_length = ids.size();
     m.expert_lookups += ids.size() * m.config.expert_used_count * m.layers.size();
-    if (m.profile) {
-        const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-        std::fprintf(m.profile, "prefill,%zu,%zu,%.6f\n", ids.size(), ids.size(), ms);
-    }
+    // The reference's MoE scopes carry no traffic estimate (moe_llm.mm:3083-3086).
+    if (m.prof) m.prof->end(OpTraffic{});
     return token;
 }
 
@@ -1053,25 +1054,25 @@ std::int32_t HipMoeLLM::decode(std::int32_t id) {
         throw std::out_of_range("MoE decode token is outside vocabulary");
     }
     hip_check(hipSetDevice(m.device), "hipSetDevice");
-    const auto t0 = std::chrono::steady_clock::now();
     const std::size_t pos = m.sequence_length;
+    if (m.prof) m.prof->begin("decode", pos + 1, "decode.gpu_moe");
     m.host_step[0] = static_cast<std::uint32_t>(id);
     m.host_step[1] = static_cast<std::uint32_t>(pos);
     hip_check(hipMemcpyAsync(m.act.step, m.host_step, 8, hipMemcpyHostToDevice, m.stream), "hipMemcpy(step)");
-    if (m.decode_graphs) {
+    // Detailed profiling times every launch, so the step runs eagerly.
+    const bool graph = m.decode_graphs && !(m.prof && m.prof->detailed());
+    if (graph) {
         if (!m.decode_exec) m.capture_decode();
         hip_check(hipGraphLaunch(m.decode_exec, m.stream), "hipGraphLaunch(decode)");
         m.last_rows = 1;
     } else {
         m.forward(1, pos, reinterpret_cast<const std::int32_t*>(m.act.step));
     }
+    if (m.prof) m.prof->mark_gpu_end();
     const std::int32_t token = m.read_token();
     m.sequence_length = pos + 1;
     m.expert_lookups += m.config.expert_used_count * m.layers.size();
-    if (m.profile) {
-        const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-        std::fprintf(m.profile, "decode,1,%zu,%.6f\n", pos + 1, ms);
-    }
+    if (m.prof) m.prof->end(OpTraffic{}, graph ? &m.decode_graph_kernels : nullptr);
     return token;
 }
 
@@ -1112,19 +1113,15 @@ void HipMoeLLM::copy_last_router_logits(float* dst, std::size_t count) const {
     hip_check(hipMemcpy(dst, m.probe, count * 4, hipMemcpyDeviceToHost), "hipMemcpy(route probe)");
 }
 
-void HipMoeLLM::enable_profiling(const std::string& csv_path, bool) {
+void HipMoeLLM::enable_profiling(const std::string& csv_path, bool detailed_kernel_timestamps) {
     if (!impl_) throw std::runtime_error("MoE model is not initialized");
     disable_profiling();
-    impl_->profile = std::fopen(csv_path.c_str(), "w");
-    if (!impl_->profile) throw std::runtime_error("cannot open profile CSV: " + csv_path);
-    std::fprintf(impl_->profile, "phase,tokens,sequence,wall_ms\n");
+    hip_check(hipSetDevice(impl_->device), "hipSetDevice");
+    impl_->prof = std::make_unique<RunProfiler>(csv_path, detailed_kernel_timestamps, impl_->stream);
 }
 
 void HipMoeLLM::disable_profiling() {
-    if (impl_ && impl_->profile) {
-        std::fclose(impl_->profile);
-        impl_->profile = nullptr;
-    }
+    if (impl_) impl_->prof.reset();
 }
 
 const GgufModelConfig& HipMoeLLM::config() const {
