@@ -193,7 +193,7 @@ def bench_copy(torch, cuda, nbytes):
 
 def bench_prefill_gemm(torch, cuda):
     from myllm_amd import synth
-    from myllm_amd.hipllm import kernels
+    from myllm_amd.hipllm import kernels, lib
     K, N = 3584, 18944
     src = synth.random_quantized(N, K, synth.Q4_K, seed=N * 7 + K)
     copies = 8
@@ -209,8 +209,10 @@ def bench_prefill_gemm(torch, cuda):
         xs = torch.empty(M, device=cuda)
         kernels.to_f16(x, K, xh, xs, M, K)
         y = torch.empty(M, N, device=cuda)
+        split_ws = torch.empty(max(16, lib().hipllm_gemm_mfma_workspace_bytes(M, N, K, -1, 0)), dtype=torch.uint8,
+                               device=cuda)
         fn = lambda i, st=None: kernels.gemm_mfma(synth.Q4_K, ws[i % copies], src.shape[1], xh, xs, None, None, y, M, N,
-                                                  K, stream=st)
+                                                  K, stream=st, workspace=split_ws)
         for i in range(3):
             fn(i)
         d = time_kernel(torch, fn, 24)

@@ -169,14 +169,20 @@ int hipllm_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m,
  * 4, 5 = 128x128, 128x256 with each weight tile dequantized once into LDS
  * and shared by all four waves.
  * `splits` 0 picks the default K split, else 1..1024 blocks along k: with
- * more than one, y is first set to residual + bias and every split adds its
- * partial sum with float atomics (y may alias residual).
+ * more than one, every split writes its partial sums to `workspace` (16-byte
+ * aligned, hipllm_gemm_mfma_workspace_bytes) and a second launch adds them in
+ * split order, then bias and residual, so results are the same on every
+ * run; y may alias residual. Without enough workspace the default split
+ * runs unsplit and an explicit one is rejected.
  * Replaces metal_gemm_{q5_0,q8_0,q4_k,q6_k,f32} via encode_matrix_product
  * (metal_llm.metal:196-250, 621-704; metal_llm.mm:1782-1889) and CPULLM's
  * gemmt / gemmtb (cpu_llm.cpp:591-607, 631-653). */
 int hipllm_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xh, const float* xscale,
                      const float* bias, const float* residual, float* y, size_t m, size_t n, size_t k, int tile,
-                     int splits, void* stream);
+                     int splits, void* workspace, size_t workspace_bytes, void* stream);
+/* Workspace bytes hipllm_gemm_mfma's K split takes for this shape, tile and
+ * splits request (0: it runs unsplit). */
+size_t hipllm_gemm_mfma_workspace_bytes(size_t m, size_t n, size_t k, int tile, int splits);
 
 /* Workspace bytes hipllm_gemm needs for m rows of k values. */
 size_t hipllm_gemm_workspace_bytes(size_t m, size_t k);
@@ -539,6 +545,80 @@ size_t hipllm_expert_cache_count(const HipllmModel* model);
  * expert lookups since creation (tokens x routes x layers); every expert is
  * resident, so all are hits. Zero for qwen2 models. */
 int hipllm_expert_cache_stats(const HipllmModel* model, uint64_t* hits, uint64_t* misses);
+
+/* ------------------------------------------------------------ text front end */
+
+/* Qwen byte-level BPE tokenizer: QwenTokenizer of chat.cpp:349-529 (qwen2 /
+ * qwen35 pre-tokenizer, GPT-2 byte symbols, lowest-rank-first merges,
+ * "<|...|>" special tokens matched longest first). Host code only: no GPU
+ * call is made. Strings are NUL-terminated; a vocabulary or merge string
+ * never holds a NUL byte in GPT-2 byte form. */
+typedef struct HipllmTokenizer HipllmTokenizer;
+int hipllm_tokenizer_create(const char* const* vocabulary, size_t vocabulary_count, const char* const* merges,
+                            size_t merge_count, const char* tokenizer_pre, HipllmTokenizer** out);
+/* From a loaded model's GGUF tables (run_interactive, chat.cpp:924-931). */
+int hipllm_tokenizer_from_model(const HipllmModel* model, HipllmTokenizer** out);
+void hipllm_tokenizer_destroy(HipllmTokenizer* tokenizer);
+/* QwenTokenizer::encode (chat.cpp:379-399) of text[0, length). Writes up to
+ * capacity ids and sets *count to the full number; HIPLLM_LENGTH_ERROR when
+ * capacity is short (call again with *count). HIPLLM_RUNTIME_ERROR when the
+ * vocabulary lacks a byte symbol the text needs (chat.cpp:509-518). */
+int hipllm_tokenize(const HipllmTokenizer* tokenizer, const char* text, size_t length, int32_t* ids,
+                    size_t capacity, size_t* count);
+/* QwenTokenizer::id (chat.cpp:401-404): -1 when absent. */
+int32_t hipllm_token_id(const HipllmTokenizer* tokenizer, const char* token);
+/* QwenTokenizer::is_special (chat.cpp:423). */
+int hipllm_token_is_special(const HipllmTokenizer* tokenizer, int32_t token);
+/* QwenTokenizer::decode_piece (chat.cpp:406-421): the bytes of one token
+ * ("" for special tokens and ids out of range), not NUL-terminated. Sets
+ * *length; HIPLLM_LENGTH_ERROR when capacity is short. */
+int hipllm_decode_piece(const HipllmTokenizer* tokenizer, int32_t token, char* out, size_t capacity,
+                        size_t* length);
+/* Byte ranges [begin, end) of the pre-tokenizer pieces of ordinary text
+ * (pretokenize, chat.cpp:207-298), as 2 * *count values. */
+int hipllm_pretokenize(const HipllmTokenizer* tokenizer, const char* text, size_t length, size_t* ranges,
+                       size_t capacity, size_t* count);
+/* ChatML prompt of one turn (chat_prompt, chat.cpp:655-659), same length
+ * protocol as hipllm_decode_piece. */
+int hipllm_chat_prompt(const char* system, const char* user, char* out, size_t capacity, size_t* length);
+/* make_stop_tokens (chat.cpp:708-726): eos, <|im_end|>, </s>, then every
+ * special token in id order, without repeats. */
+int hipllm_stop_tokens(const HipllmModel* model, const HipllmTokenizer* tokenizer, int32_t* out, size_t capacity,
+                       size_t* count);
+
+/* GenerationStats (chat.h:20-41). */
+typedef struct HipllmGenerationStats {
+    double prefill_ms;
+    double decode_ms;
+    double total_ms;
+    uint64_t prompt_tokens;
+    uint64_t generated_tokens;
+    uint64_t decode_steps;
+    int32_t used_gpu;
+    int32_t stopped;
+    int32_t has_expert_cache_stats;
+    uint64_t expert_cache_hits;
+    uint64_t expert_cache_misses;
+    HipllmMemoryStats memory;
+} HipllmGenerationStats;
+/* chat::run (chat.h:59-75, generate chat.cpp:831-878): reset, prefill, then
+ * greedy emit/decode until a stop token or min(max_new_tokens,
+ * max_sequence - count) tokens. sink (nullable) is called with each emitted
+ * token; tokens (nullable) receives up to capacity of them and *generated
+ * (nullable) their number; stats nullable. The errors of
+ * validate_generation_request (chat.cpp:675-699) are HIPLLM_INVALID_ARGUMENT
+ * / HIPLLM_RUNTIME_ERROR with the same messages. */
+typedef void (*HipllmTokenSink)(int32_t token, void* user);
+int hipllm_run(HipllmModel* model, const int32_t* ids, size_t count, size_t max_new_tokens, const int32_t* stop_ids,
+               size_t stop_count, HipllmTokenSink sink, void* user, int32_t* tokens, size_t capacity,
+               size_t* generated, HipllmGenerationStats* stats);
+/* The "[chat] generation_stats ..." line (print_generation_stats,
+ * chat.cpp:743-785), same length protocol as hipllm_decode_piece. */
+int hipllm_format_generation_stats(const HipllmGenerationStats* stats, char* out, size_t capacity, size_t* length);
+/* The chat command (run_cli, chat.cpp:998-1040) on stdin/stdout/stderr, with
+ * the reference's options; --gpu is required (no CPU backend here). Returns
+ * the exit status. */
+int hipllm_chat_main(int argc, char** argv);
 
 #ifdef __cplusplus
 }

@@ -2,6 +2,8 @@
 
 * ``myllm_amd/lib/libhipllm.so``: HIP kernels for gfx950 + the HipLLM runtime
   + the C ABI (include/hipllm.h), compiled with hipcc.
+* ``myllm_amd/lib/hipllm_chat``: the chat command (a ``main`` over
+  ``hipllm_chat_main``), linked to libhipllm.so with an ``$ORIGIN`` rpath.
 * ``myllm_amd/lib/libhipllm_tools.so``: host-only synthetic-input tools
   (include/hipllm_tools.h), compiled with g++.
 * ``oracle/``: the CPU oracle and, when the reference sources are present,
@@ -45,6 +47,8 @@ HIP_SOURCES = [
     "runtime/hip_llm.cpp",
     "runtime/hip_moe.cpp",
     "runtime/profile.cpp",
+    "runtime/tokenizer.cpp",
+    "runtime/hip_chat.cpp",
     "runtime/capi.cpp",
 ]
 TOOLS_SOURCES = ["tools/quants.cpp", "tools/synth_gguf.cpp", "tools/tools_capi.cpp"]
@@ -74,6 +78,17 @@ def build_hipllm(jobs: int) -> pathlib.Path:
     out = LIB / "libhipllm.so"
     tmp = LIB / "libhipllm.so.tmp"
     _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)])
+    os.replace(tmp, out)
+    build_chat(out)
+    return out
+
+
+def build_chat(libhipllm: pathlib.Path) -> pathlib.Path:
+    """The chat command, linked to libhipllm.so beside it."""
+    out = LIB / "hipllm_chat"
+    tmp = LIB / "hipllm_chat.tmp"
+    _run([HIPCC, "-O2", "-std=c++17", str(CSRC / "runtime" / "chat_main.cpp"), f"-L{libhipllm.parent}", "-lhipllm",
+          "-Wl,-rpath,$ORIGIN", "-o", str(tmp)])
     os.replace(tmp, out)
     return out
 

@@ -103,9 +103,16 @@ int gemm_default_tile(uint32_t m, uint32_t n, uint32_t k);
 uint32_t gemm_default_splits(uint32_t m, uint32_t n, uint32_t k, int tile);
 // X rows as fp16 MFMA operands with a power-of-two scale per row (xscale[m]).
 int launch_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m, size_t k, hipStream_t stream);
+// Bytes of the K-split partial planes launch_gemm_mfma uses for this shape
+// (0 when it runs unsplit).
+size_t gemm_split_bytes(size_t m, size_t n, size_t k, int tile, int splits);
+// With a K split the partial sums go to split_ws (gemm_split_bytes, 16-byte
+// aligned) and are added in split order by a second launch; without enough
+// workspace the default split runs unsplit and an explicit one is rejected.
 int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* xscale,
                      const float* bias, const float* residual, float* y, size_t m, size_t n, size_t k, int tile,
-                     int splits, hipStream_t stream, size_t ldy = 0);
+                     int splits, hipStream_t stream, size_t ldy = 0, void* split_ws = nullptr,
+                     size_t split_ws_bytes = 0);
 int launch_attn_prefill(const float* q, size_t q_stride, const float* kcache, const float* vcache, float* out,
                         size_t out_stride, size_t rows, size_t hq, size_t hkv, size_t d, size_t pos0, float scale,
                         hipStream_t stream);

@@ -492,8 +492,9 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
 
     // Epilogue: acc[ns][ms][4 g + r] = Y[m0 + 32 ms + 8 g + 4 h + r][n0 + 32 ns + lr]
     // in units of the row's X scale (exact power of two).
-    // With a K split, y already holds residual + bias (gemm_init_kernel) and
-    // every split adds its partial sum with a float atomic add in L2.
+    // With a K split, y is the partial-sum buffer: split z stores its plane
+    // z (m rows of ld ldy), and gemm_split_reduce_kernel adds the planes in
+    // split order, so the result does not depend on which split ends first.
     const bool split = gridDim.z > 1;
 #pragma unroll
     for (int ns = 0; ns < NSUB; ++ns) {
@@ -513,7 +514,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint8_t* __restric
                         const float a = acc[ns][ms][4 * g + r] * xscale[src];
                         const size_t o = static_cast<size_t>(GATHER ? vec(row) : row) * ldy + col;
                         if (split) {
-                            unsafeAtomicAdd(y + o, a);
+                            y[static_cast<size_t>(blockIdx.z) * m * ldy + o] = a;
                         } else {
                             float v = a + b;
                             if (residual) v += residual[o];
@@ -656,7 +657,8 @@ __global__ __launch_bounds__(256, MT == 1 ? 2 : 1) void gemm_lds_kernel(const ui
         if (st + 1 < steps) body(st + 1, xb2, xa, rawm, rawn);
     }
 
-    // Epilogue: acc[nt][mt][4 g + r] = Y[mw + 32 mt + 8 g + 4 h + r][n0 + 32 nt + lr].
+    // Epilogue: acc[nt][mt][4 g + r] = Y[mw + 32 mt + 8 g + 4 h + r][n0 + 32 nt + lr];
+    // with a K split, partial planes as in gemm_mfma_kernel.
     const bool split = gridDim.z > 1;
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
@@ -674,7 +676,7 @@ __global__ __launch_bounds__(256, MT == 1 ? 2 : 1) void gemm_lds_kernel(const ui
                         const float a = acc[nt][mt][4 * g + r] * xscale[row];
                         const size_t o = static_cast<size_t>(row) * ldy + col;
                         if (split) {
-                            unsafeAtomicAdd(y + o, a);
+                            y[static_cast<size_t>(blockIdx.z) * m * ldy + o] = a;
                         } else {
                             float v = a + b;
                             if (residual) v += residual[o];
@@ -687,15 +689,24 @@ __global__ __launch_bounds__(256, MT == 1 ? 2 : 1) void gemm_lds_kernel(const ui
     }
 }
 
-// y[r, c] = residual[r, c] + bias[c] (either may be absent): the starting
-// value a K-split GEMM accumulates into.
-__global__ void gemm_init_kernel(float* __restrict__ y, uint32_t ldy, const float* __restrict__ residual,
-                                 const float* __restrict__ bias, uint32_t m, uint32_t n) {
+// y[r, c] = (part[0][r, c] + part[1][r, c] + ... + part[splits - 1][r, c])
+// + bias[c] + residual[r, c] (either may be absent), the partial planes
+// (m x n, dense) added in split order: a K-split product gives the same bits
+// on every run. The additions after the sum follow the unsplit epilogue.
+__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __restrict__ part, uint32_t splits,
+                                                                const float* __restrict__ bias,
+                                                                const float* residual, float* y, uint32_t m,
+                                                                uint32_t n, uint32_t ldy) {
     const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= static_cast<size_t>(m) * n) return;
+    const size_t plane = static_cast<size_t>(m) * n;
+    if (i >= plane) return;
     const uint32_t r = static_cast<uint32_t>(i / n), c = static_cast<uint32_t>(i % n);
+    float a = part[i];
+    for (uint32_t z = 1; z < splits; ++z) a += part[z * plane + i];
+    float v = a + (bias ? bias[c] : 0.0f);
     const size_t o = static_cast<size_t>(r) * ldy + c;
-    y[o] = (residual ? residual[o] : 0.0f) + (bias ? bias[c] : 0.0f);
+    if (residual) v += residual[o];
+    y[o] = v;
 }
 
 // Row r of x as fp16 operands: xh[r, c] = fp16(x[r, c] * 2^-e) (round to
@@ -742,22 +753,29 @@ __global__ __launch_bounds__(256) void to_f16_kernel(const float* __restrict__ x
     }
 }
 
+// A K split of `splits` planes of `per` 128-k steps each writes its partial
+// sums to `part` (splits * m * n floats) and one reduce launch adds them.
+void launch_split_reduce(const float* part, uint32_t splits, const float* bias, const float* residual, float* y,
+                         uint32_t m, uint32_t n, uint32_t ldy, hipStream_t stream) {
+    const size_t total = static_cast<size_t>(m) * n;
+    HIPLLM_LAUNCH(gemm_split_reduce_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, stream,
+                  part, splits, bias, residual, y, m, n, ldy);
+}
+
 template <uint32_t T, int NSUB, int MSUB>
 void launch_tile(const void* w, size_t row_bytes, const _Float16* xb, const float* xscale, const float* bias,
                  const float* residual, float* y, uint32_t m, uint32_t n, uint32_t k, uint32_t ldy, uint32_t splits,
-                 hipStream_t stream) {
+                 uint32_t per, float* part, hipStream_t stream) {
     constexpr uint32_t BN = 4 * 32 * NSUB, BM = 32 * MSUB;
-    const uint32_t steps = k / kStepK;
-    const uint32_t per = (steps + splits - 1) / splits;
-    splits = (steps + per - 1) / per;  // every split gets at least one step
-    if (splits > 1) {
-        const size_t total = static_cast<size_t>(m) * n;
-        HIPLLM_LAUNCH(gemm_init_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, stream,
-                           y, ldy, residual, bias, m, n);
-    }
     const dim3 grid(((n + BN - 1) / BN) * ((m + BM - 1) / BM), 1, splits);
-    HIPLLM_LAUNCH((gemm_mfma_kernel<T, NSUB, MSUB>), grid, dim3(256), 0, stream,
-                       static_cast<const uint8_t*>(w), row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, per);
+    if (splits > 1) {
+        HIPLLM_LAUNCH((gemm_mfma_kernel<T, NSUB, MSUB>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w),
+                      row_bytes, xb, xscale, nullptr, nullptr, part, m, n, k, n, per);
+        launch_split_reduce(part, splits, bias, residual, y, m, n, ldy, stream);
+    } else {
+        HIPLLM_LAUNCH((gemm_mfma_kernel<T, NSUB, MSUB>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w),
+                      row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, per);
+    }
 }
 
 // The gathered expert products: tile 1 (64 rows x 128 weight rows per
@@ -774,32 +792,30 @@ void launch_gather(const void* w, size_t row_bytes, const _Float16* xb, const fl
 template <uint32_t T, int MT>
 void launch_lds(const void* w, size_t row_bytes, const _Float16* xb, const float* xscale, const float* bias,
                 const float* residual, float* y, uint32_t m, uint32_t n, uint32_t k, uint32_t ldy, uint32_t splits,
-                hipStream_t stream) {
+                uint32_t per, float* part, hipStream_t stream) {
     constexpr uint32_t BN = 128, BM = 128 * MT;
-    const uint32_t steps = k / kStepK;
-    const uint32_t per = (steps + splits - 1) / splits;
-    splits = (steps + per - 1) / per;
-    if (splits > 1) {
-        const size_t total = static_cast<size_t>(m) * n;
-        HIPLLM_LAUNCH(gemm_init_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, stream,
-                           y, ldy, residual, bias, m, n);
-    }
     const dim3 grid(((n + BN - 1) / BN) * ((m + BM - 1) / BM), 1, splits);
-    HIPLLM_LAUNCH((gemm_lds_kernel<T, MT>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w),
-                       row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, per);
+    if (splits > 1) {
+        HIPLLM_LAUNCH((gemm_lds_kernel<T, MT>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w), row_bytes,
+                      xb, xscale, nullptr, nullptr, part, m, n, k, n, per);
+        launch_split_reduce(part, splits, bias, residual, y, m, n, ldy, stream);
+    } else {
+        HIPLLM_LAUNCH((gemm_lds_kernel<T, MT>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w), row_bytes,
+                      xb, xscale, bias, residual, y, m, n, k, ldy, per);
+    }
 }
 
 template <uint32_t T>
 int launch_typed(int tile, const void* w, size_t row_bytes, const _Float16* xb, const float* xscale,
                  const float* bias, const float* residual, float* y, uint32_t m, uint32_t n, uint32_t k, uint32_t ldy,
-                 uint32_t splits, hipStream_t stream) {
+                 uint32_t splits, uint32_t per, float* part, hipStream_t stream) {
     switch (tile) {
-    case 4: launch_lds<T, 1>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, stream); break;
-    case 5: launch_lds<T, 2>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, stream); break;
-    case 0: launch_tile<T, 1, 1>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, stream); break;
-    case 1: launch_tile<T, 1, 2>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, stream); break;
-    case 2: launch_tile<T, 2, 2>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, stream); break;
-    case 3: launch_tile<T, 2, 4>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, stream); break;
+    case 4: launch_lds<T, 1>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream); break;
+    case 5: launch_lds<T, 2>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream); break;
+    case 0: launch_tile<T, 1, 1>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream); break;
+    case 1: launch_tile<T, 1, 2>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream); break;
+    case 2: launch_tile<T, 2, 2>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream); break;
+    case 3: launch_tile<T, 2, 4>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream); break;
     default: return kInvalidArgument;
     }
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
@@ -844,9 +860,31 @@ uint32_t gemm_default_splits(uint32_t m, uint32_t n, uint32_t k, int tile) {
     return max(1u, min(want, steps / 2));
 }
 
+namespace {
+// The split count a launch uses: the request (0 = default), rounded so every
+// split gets at least one 128-k step; *per = steps per split.
+uint32_t effective_splits(uint32_t m, uint32_t n, uint32_t k, int tile, int splits, uint32_t* per) {
+    const uint32_t steps = k / kStepK;
+    uint32_t s = splits == 0 ? gemm_default_splits(m, n, k, tile) : static_cast<uint32_t>(splits);
+    s = max(1u, min(s, steps));
+    *per = (steps + s - 1) / s;
+    return (steps + *per - 1) / *per;
+}
+}  // namespace
+
+size_t gemm_split_bytes(size_t m, size_t n, size_t k, int tile, int splits) {
+    if (m == 0 || n == 0 || k < kStepK || m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull) return 0;
+    if (tile < 0) tile = gemm_default_tile(static_cast<uint32_t>(m), static_cast<uint32_t>(n), static_cast<uint32_t>(k));
+    if (tile > 5 || splits < 0 || splits > 1024) return 0;
+    uint32_t per;
+    const uint32_t s = effective_splits(static_cast<uint32_t>(m), static_cast<uint32_t>(n), static_cast<uint32_t>(k),
+                                        tile, splits, &per);
+    return s > 1 ? static_cast<size_t>(s) * m * n * sizeof(float) : 0;
+}
+
 int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* xscale,
                      const float* bias, const float* residual, float* y, size_t m, size_t n, size_t k, int tile,
-                     int splits, hipStream_t stream, size_t ldy) {
+                     int splits, hipStream_t stream, size_t ldy, void* split_ws, size_t split_ws_bytes) {
     if (ldy == 0) ldy = n;
     if (!w || !xb || !xscale || !y || m == 0 || n == 0 || k == 0 || ldy < n || ldy > 0x7fffffffull) return kInvalidArgument;
     if (k % kStepK != 0) return kInvalidArgument;
@@ -866,15 +904,27 @@ int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void*
     if (tile > 5) return kInvalidArgument;
     const uint32_t M = static_cast<uint32_t>(m), N = static_cast<uint32_t>(n), K = static_cast<uint32_t>(k);
     if (splits < 0 || splits > 1024) return kInvalidArgument;
-    const uint32_t S = splits == 0 ? gemm_default_splits(M, N, K, tile) : static_cast<uint32_t>(splits);
+    uint32_t per;
+    uint32_t S = effective_splits(M, N, K, tile, splits, &per);
+    const size_t need = S > 1 ? static_cast<size_t>(S) * m * n * sizeof(float) : 0;
+    if (need > split_ws_bytes || (need && !split_ws)) {
+        // An explicit split needs its partial-sum planes; the default split
+        // falls back to one pass over k.
+        if (splits != 0) return kInvalidArgument;
+        S = 1;
+        per = K / kStepK;
+    }
+    if (S > 1 && reinterpret_cast<uintptr_t>(split_ws) % 16 != 0) return kInvalidArgument;
+    float* part = static_cast<float*>(split_ws);
     const auto* x = static_cast<const _Float16*>(xb);
+    const uint32_t LD = static_cast<uint32_t>(ldy);
     switch (type) {
-    case kQ4_K: return launch_typed<kQ4_K>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
-    case kQ6_K: return launch_typed<kQ6_K>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
-    case kQ8_0: return launch_typed<kQ8_0>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
-    case kQ5_0: return launch_typed<kQ5_0>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
-    case kF32: return launch_typed<kF32>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
-    case kF16: return launch_typed<kF16>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, static_cast<uint32_t>(ldy), S, stream);
+    case kQ4_K: return launch_typed<kQ4_K>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, LD, S, per, part, stream);
+    case kQ6_K: return launch_typed<kQ6_K>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, LD, S, per, part, stream);
+    case kQ8_0: return launch_typed<kQ8_0>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, LD, S, per, part, stream);
+    case kQ5_0: return launch_typed<kQ5_0>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, LD, S, per, part, stream);
+    case kF32: return launch_typed<kF32>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, LD, S, per, part, stream);
+    case kF16: return launch_typed<kF16>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, LD, S, per, part, stream);
     default: return kInvalidArgument;
     }
 }

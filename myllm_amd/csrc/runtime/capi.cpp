@@ -4,11 +4,14 @@
 
 #include "../kernels/common.h"
 #include "../kernels/launch.h"
+#include "hip_chat.h"
 #include "hip_llm.h"
 #include "hip_moe.h"
+#include "tokenizer.h"
 
 #include <cstring>
 #include <exception>
+#include <iostream>
 #include <memory>
 #include <mutex>
 #include <new>
@@ -216,10 +219,15 @@ int hipllm_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m,
 
 int hipllm_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xh, const float* xscale,
                      const float* bias, const float* residual, float* y, size_t m, size_t n, size_t k, int tile,
-                     int splits, void* stream) {
+                     int splits, void* workspace, size_t workspace_bytes, void* stream) {
     return status(hipllm::launch_gemm_mfma(type, w, row_bytes, xh, xscale, bias, residual, y, m, n, k, tile, splits,
-                                           as_stream(stream)),
-                  "hipllm_gemm_mfma: invalid arguments (k % 128 == 0, tile -1..5, splits 0..1024) or launch failure");
+                                           as_stream(stream), 0, workspace, workspace_bytes),
+                  "hipllm_gemm_mfma: invalid arguments (k % 128 == 0, tile -1..5, splits 0..1024, workspace for an "
+                  "explicit split) or launch failure");
+}
+
+size_t hipllm_gemm_mfma_workspace_bytes(size_t m, size_t n, size_t k, int tile, int splits) {
+    return hipllm::gemm_split_bytes(m, n, k, tile, splits);
 }
 
 // Workspace: the fp16 rows (256-byte aligned), then the row scales.
@@ -662,6 +670,205 @@ int hipllm_attn_prefill(const float* q, size_t q_stride, const float* kcache, co
     return status(hipllm::launch_attn_prefill(q, q_stride, kcache, vcache, out, out_stride, rows, hq, hkv, d, pos0,
                                               scale, as_stream(stream)),
                   "hipllm_attn_prefill: invalid arguments or launch failure");
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------ text front end
+
+struct HipllmTokenizer {
+    llm::QwenTokenizer impl;
+};
+
+namespace {
+
+// Copy bytes out under the (capacity, *length) protocol.
+int put_bytes(const std::string& s, char* out, size_t capacity, size_t* length, const char* what) {
+    if (!length) return fail(HIPLLM_INVALID_ARGUMENT, what);
+    *length = s.size();
+    if (capacity < s.size() || (!out && !s.empty())) return fail(HIPLLM_LENGTH_ERROR, what);
+    if (!s.empty()) std::memcpy(out, s.data(), s.size());
+    return HIPLLM_OK;
+}
+
+template <typename T>
+int put_values(const std::vector<T>& v, T* out, size_t capacity, size_t* count, const char* what) {
+    if (!count) return fail(HIPLLM_INVALID_ARGUMENT, what);
+    *count = v.size();
+    if (capacity < v.size() || (!out && !v.empty())) return fail(HIPLLM_LENGTH_ERROR, what);
+    std::copy(v.begin(), v.end(), out);
+    return HIPLLM_OK;
+}
+
+void to_c(const llm::chat::GenerationStats& s, HipllmGenerationStats* o) {
+    std::memset(o, 0, sizeof(*o));
+    o->prefill_ms = s.prefill_ms;
+    o->decode_ms = s.decode_ms;
+    o->total_ms = s.total_ms;
+    o->prompt_tokens = s.prompt_tokens;
+    o->generated_tokens = s.generated_tokens;
+    o->decode_steps = s.decode_steps;
+    o->used_gpu = s.used_gpu ? 1 : 0;
+    o->stopped = s.stopped ? 1 : 0;
+    o->has_expert_cache_stats = s.has_expert_cache_stats ? 1 : 0;
+    o->expert_cache_hits = s.expert_cache_hits;
+    o->expert_cache_misses = s.expert_cache_misses;
+    o->memory.weight_bytes = s.memory.weight_bytes;
+    o->memory.kv_cache_bytes = s.memory.kv_cache_bytes;
+    o->memory.recurrent_state_bytes = s.memory.recurrent_state_bytes;
+    o->memory.intermediate_bytes = s.memory.intermediate_bytes;
+    o->memory.intermediate_is_estimate = s.memory.intermediate_is_estimate ? 1 : 0;
+}
+
+llm::chat::GenerationStats from_c(const HipllmGenerationStats& o) {
+    llm::chat::GenerationStats s;
+    s.prefill_ms = o.prefill_ms;
+    s.decode_ms = o.decode_ms;
+    s.total_ms = o.total_ms;
+    s.prompt_tokens = o.prompt_tokens;
+    s.generated_tokens = o.generated_tokens;
+    s.decode_steps = o.decode_steps;
+    s.used_gpu = o.used_gpu != 0;
+    s.stopped = o.stopped != 0;
+    s.has_expert_cache_stats = o.has_expert_cache_stats != 0;
+    s.expert_cache_hits = o.expert_cache_hits;
+    s.expert_cache_misses = o.expert_cache_misses;
+    s.memory.weight_bytes = o.memory.weight_bytes;
+    s.memory.kv_cache_bytes = o.memory.kv_cache_bytes;
+    s.memory.recurrent_state_bytes = o.memory.recurrent_state_bytes;
+    s.memory.intermediate_bytes = o.memory.intermediate_bytes;
+    s.memory.intermediate_is_estimate = o.memory.intermediate_is_estimate != 0;
+    return s;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hipllm_tokenizer_create(const char* const* vocabulary, size_t vocabulary_count, const char* const* merges,
+                            size_t merge_count, const char* tokenizer_pre, HipllmTokenizer** out) {
+    if (!out || (!vocabulary && vocabulary_count) || (!merges && merge_count)) {
+        return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_tokenizer_create: null argument");
+    }
+    *out = nullptr;
+    return guarded([&] {
+        std::vector<std::string> v, m;
+        v.reserve(vocabulary_count);
+        m.reserve(merge_count);
+        for (size_t i = 0; i < vocabulary_count; ++i) {
+            if (!vocabulary[i]) throw std::invalid_argument("hipllm_tokenizer_create: null vocabulary entry");
+            v.emplace_back(vocabulary[i]);
+        }
+        for (size_t i = 0; i < merge_count; ++i) {
+            if (!merges[i]) throw std::invalid_argument("hipllm_tokenizer_create: null merge entry");
+            m.emplace_back(merges[i]);
+        }
+        *out = new HipllmTokenizer{llm::QwenTokenizer(v, m, tokenizer_pre ? tokenizer_pre : "")};
+    });
+}
+
+int hipllm_tokenizer_from_model(const HipllmModel* model, HipllmTokenizer** out) {
+    if (!model || !out) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_tokenizer_from_model: null argument");
+    *out = nullptr;
+    return guarded([&] {
+        const llm::GgufModelConfig& c = *config_of(model);
+        if (c.vocabulary.empty() || c.merges.empty()) {
+            throw std::runtime_error("model does not contain Qwen tokenizer vocabulary/merges");
+        }
+        *out = new HipllmTokenizer{llm::QwenTokenizer(c.vocabulary, c.merges, c.tokenizer_pre)};
+    });
+}
+
+void hipllm_tokenizer_destroy(HipllmTokenizer* t) { delete t; }
+
+int hipllm_tokenize(const HipllmTokenizer* t, const char* text, size_t length, int32_t* ids, size_t capacity,
+                    size_t* count) {
+    if (!t || (!text && length)) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_tokenize: null argument");
+    int rc = HIPLLM_OK;
+    const int g = guarded([&] {
+        const std::vector<int32_t> v = t->impl.encode(std::string(text ? text : "", length));
+        rc = put_values(v, ids, capacity, count, "hipllm_tokenize: capacity is smaller than the token count");
+    });
+    return g != HIPLLM_OK ? g : rc;
+}
+
+int32_t hipllm_token_id(const HipllmTokenizer* t, const char* token) {
+    return t && token ? t->impl.id(token) : -1;
+}
+
+int hipllm_token_is_special(const HipllmTokenizer* t, int32_t token) { return t && t->impl.is_special(token) ? 1 : 0; }
+
+int hipllm_decode_piece(const HipllmTokenizer* t, int32_t token, char* out, size_t capacity, size_t* length) {
+    if (!t) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_decode_piece: null argument");
+    return put_bytes(t->impl.decode_piece(token), out, capacity, length,
+                     "hipllm_decode_piece: null length or capacity too small");
+}
+
+int hipllm_pretokenize(const HipllmTokenizer* t, const char* text, size_t length, size_t* ranges, size_t capacity,
+                       size_t* count) {
+    if (!t || (!text && length) || !count) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_pretokenize: null argument");
+    int rc = HIPLLM_OK;
+    const int g = guarded([&] {
+        const auto pieces = t->impl.pieces(std::string(text ? text : "", length));
+        std::vector<size_t> flat;
+        flat.reserve(pieces.size() * 2);
+        for (const auto& p : pieces) {
+            flat.push_back(p.first);
+            flat.push_back(p.second);
+        }
+        rc = put_values(flat, ranges, capacity, count, "hipllm_pretokenize: capacity is smaller than 2 * pieces");
+        *count = pieces.size();
+    });
+    return g != HIPLLM_OK ? g : rc;
+}
+
+int hipllm_chat_prompt(const char* system, const char* user, char* out, size_t capacity, size_t* length) {
+    if (!system || !user) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_chat_prompt: null argument");
+    return put_bytes(llm::chat_prompt(system, user), out, capacity, length,
+                     "hipllm_chat_prompt: null length or capacity too small");
+}
+
+int hipllm_stop_tokens(const HipllmModel* model, const HipllmTokenizer* t, int32_t* out, size_t capacity,
+                       size_t* count) {
+    if (!model || !t) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_stop_tokens: null argument");
+    int rc = HIPLLM_OK;
+    const int g = guarded([&] {
+        const int32_t im_end = t->impl.id("<|im_end|>");
+        if (im_end < 0) throw std::runtime_error("model vocabulary has no <|im_end|> token");
+        const auto v = llm::chat::make_stop_tokens(t->impl, *config_of(model), im_end, t->impl.id("</s>"));
+        rc = put_values(v, out, capacity, count, "hipllm_stop_tokens: capacity is smaller than the stop list");
+    });
+    return g != HIPLLM_OK ? g : rc;
+}
+
+int hipllm_run(HipllmModel* model, const int32_t* ids, size_t count, size_t max_new_tokens, const int32_t* stop_ids,
+               size_t stop_count, HipllmTokenSink sink, void* user, int32_t* tokens, size_t capacity,
+               size_t* generated, HipllmGenerationStats* stats) {
+    if (!model) return fail(HIPLLM_RUNTIME_ERROR, "HIP model is not initialized");
+    if ((!ids && count) || (!stop_ids && stop_count)) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_run: null argument");
+    return guarded([&] {
+        std::vector<int32_t> prompt(ids, ids + count);
+        const std::vector<int32_t> stop(stop_ids, stop_ids + stop_count);
+        llm::chat::TokenSink fn;
+        if (sink) fn = [sink, user](int32_t t) { sink(t, user); };
+        const llm::chat::GenerationResult r =
+            model->visit([&](auto& b) { return llm::chat::run(b, std::move(prompt), max_new_tokens, stop, fn); });
+        if (tokens) {
+            std::copy_n(r.generated_tokens.begin(), std::min(capacity, r.generated_tokens.size()), tokens);
+        }
+        if (generated) *generated = r.generated_tokens.size();
+        if (stats) to_c(r.stats, stats);
+    });
+}
+
+int hipllm_format_generation_stats(const HipllmGenerationStats* stats, char* out, size_t capacity, size_t* length) {
+    if (!stats) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_format_generation_stats: null argument");
+    return put_bytes(llm::chat::format_generation_stats(from_c(*stats)), out, capacity, length,
+                     "hipllm_format_generation_stats: null length or capacity too small");
+}
+
+int hipllm_chat_main(int argc, char** argv) {
+    return llm::chat::run_cli(argc, argv, std::cin, std::cout, std::cerr);
 }
 
 }  // extern "C"

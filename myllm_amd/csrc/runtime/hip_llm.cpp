@@ -66,6 +66,8 @@ struct PrefillActivations {
     float* up = nullptr;                    // [T, F]
     void* xb = nullptr;                     // fp16 [T, max(H, F)] matmul operands
     float* xscale = nullptr;                // [T] their row scales
+    void* split = nullptr;                  // K-split partial sums of one matmul
+    std::size_t split_bytes = 0;
 };
 
 }  // namespace
@@ -515,6 +517,14 @@ void HipLLM::Impl::ensure_prefill_rows(std::size_t n) {
                       o_qkv = reserve(n * (H + 2 * kv_dim) * 4), o_attn = reserve(n * H * 4),
                       o_gate = reserve(n * F * 4), o_up = reserve(n * F * 4),
                       o_xb = reserve(n * std::max(H, F) * 2), o_xs = reserve(n * 4);
+    // The largest K-split workspace any layer matmul takes at up to n rows.
+    std::size_t split_bytes = 0;
+    for (std::size_t m = 1; m <= n; ++m) {
+        split_bytes = std::max({split_bytes, hipllm::gemm_split_bytes(m, H + 2 * kv_dim, H, -1, 0),
+                                hipllm::gemm_split_bytes(m, H, H, -1, 0), hipllm::gemm_split_bytes(m, F, H, -1, 0),
+                                hipllm::gemm_split_bytes(m, H, F, -1, 0)});
+    }
+    const std::size_t o_split = reserve(split_bytes);
     pre_bytes = off;
     hip_check(hipMalloc(&pre_arena, pre_bytes), "hipMalloc(prefill activations)");
     auto* base = static_cast<std::uint8_t*>(pre_arena);
@@ -527,6 +537,8 @@ void HipLLM::Impl::ensure_prefill_rows(std::size_t n) {
     pre.up = reinterpret_cast<float*>(base + o_up);
     pre.xb = base + o_xb;
     pre.xscale = reinterpret_cast<float*>(base + o_xs);
+    pre.split = split_bytes ? base + o_split : nullptr;
+    pre.split_bytes = split_bytes;
     pre_rows = n;
 }
 
@@ -539,7 +551,7 @@ void HipLLM::Impl::gemm(const DevMatrix& w, const void* xb, const float* bias, c
                         std::size_t rows, std::size_t ldy, std::size_t n_override) const {
     const std::size_t n = n_override ? n_override : w.rows;
     launch_check(hipllm::launch_gemm_mfma(w.type, w.ptr, w.row_bytes, xb, pre.xscale, bias, residual, y, rows, n,
-                                          w.cols, -1, 0, stream, ldy),
+                                          w.cols, -1, 0, stream, ldy, pre.split, pre.split_bytes),
                  "prefill matmul");
 }
 

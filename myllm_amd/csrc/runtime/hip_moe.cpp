@@ -114,6 +114,8 @@ struct MoeActivations {
     float* act_bscale = nullptr;            // [T k] their row scales
     float* mm_scratch = nullptr;            // router matmul partial sums (K split)
     std::size_t mm_scratch_floats = 0;
+    void* split = nullptr;  // K-split partial sums of one fp16 matmul
+    std::size_t split_bytes = 0;
 };
 
 }  // namespace
@@ -496,6 +498,16 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
     for (std::size_t r = kRouterMatmulRows; r <= n; ++r) {
         mm_floats = std::max(mm_floats, hipllm::matmul_f32_scratch_floats(r, E + 1, H));
     }
+    // Likewise the K-split partial sums of the fp16 projection matmuls.
+    const std::size_t mm_shapes[][2] = {{2 * q_w, H}, {kv_w, H},   {2 * kv_w, H}, {qkv_w, H},
+                                        {inner, H},   {Hv, H},     {2 * Hv, H},   {H, q_w},
+                                        {H, inner},   {FFs, H},    {H, FFs}};
+    std::size_t split_bytes = 0;
+    for (std::size_t r = kMatmulRows; r <= n; ++r) {
+        for (const auto& nk : mm_shapes) {
+            if (nk[1] % 128 == 0) split_bytes = std::max(split_bytes, hipllm::gemm_split_bytes(r, nk[0], nk[1], -1, 0));
+        }
+    }
     const std::size_t feat = std::max(q_w, inner);
     std::size_t off = 0;
     auto reserve = [&](std::size_t floats) {
@@ -519,7 +531,7 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
                       o_grp = reserve(2 * hipllm::route_groups_max(n * K, E, hipllm::kGatherRows)),
                       o_ngr = reserve(1), o_gact = reserve(n * K * FF), o_actb = reserve((n * K * FF + 1) / 2),
                       o_xs = reserve(n), o_abs = reserve(n * K),
-                      o_mms = reserve(mm_floats);
+                      o_mms = reserve(mm_floats), o_split = reserve(split_bytes / 4);
     act_bytes = off;
     hip_check(hipMalloc(&act_arena, act_bytes), "hipMalloc(MoE activations)");
     auto* b = static_cast<std::uint8_t*>(act_arena);
@@ -564,6 +576,8 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
     act.act_bscale = f(o_abs);
     act.mm_scratch = f(o_mms);
     act.mm_scratch_floats = mm_floats;
+    act.split = split_bytes ? b + o_split : nullptr;
+    act.split_bytes = split_bytes;
     hip_check(hipMalloc(reinterpret_cast<void**>(&route_ids), layers.size() * n * K * 4), "hipMalloc(routes)");
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&host_ids), n * 4, hipHostMallocDefault), "hipHostMalloc(ids)");
     act_rows = n;
@@ -578,7 +592,7 @@ void HipMoeLLM::Impl::proj(const DevMatrix& w, const float* x, const hipllm::XGr
         // Prefill rows through the fp16 MFMA matmul (xb: f16_rows of x, row
         // scales in act.xscale).
         launch_check(hipllm::launch_gemm_mfma(w.type, w.ptr, w.row_bytes, xb, act.xscale, nullptr, residual, y, rows, n,
-                                              w.cols, -1, 0, stream, ldy),
+                                              w.cols, -1, 0, stream, ldy, act.split, act.split_bytes),
                      "prefill matmul");
         return;
     }

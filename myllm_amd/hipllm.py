@@ -55,6 +55,18 @@ class HipllmMemoryStats(ctypes.Structure):
                 ("intermediate_is_estimate", ctypes.c_int32)]
 
 
+class HipllmGenerationStats(ctypes.Structure):
+    """GenerationStats (chat.h:20-41)."""
+    _fields_ = [("prefill_ms", ctypes.c_double), ("decode_ms", ctypes.c_double), ("total_ms", ctypes.c_double),
+                ("prompt_tokens", ctypes.c_uint64), ("generated_tokens", ctypes.c_uint64),
+                ("decode_steps", ctypes.c_uint64), ("used_gpu", ctypes.c_int32), ("stopped", ctypes.c_int32),
+                ("has_expert_cache_stats", ctypes.c_int32), ("expert_cache_hits", ctypes.c_uint64),
+                ("expert_cache_misses", ctypes.c_uint64), ("memory", HipllmMemoryStats)]
+
+
+TOKEN_SINK = ctypes.CFUNCTYPE(None, ctypes.c_int32, ctypes.c_void_p)
+
+
 _P = ctypes.c_void_p
 _S = ctypes.c_size_t
 _U32 = ctypes.c_uint32
@@ -75,7 +87,8 @@ SIGNATURES = {
     "hipllm_gemv_norm": (_I, [_U32, _P, _S, _P, _P, _F, _P, _P, _P, _S, _S, _I, _P]),
     "hipllm_gemv_swiglu_norm": (_I, [_U32, _P, _P, _S, _P, _P, _F, _P, _P, _S, _S, _I, _P]),
     "hipllm_to_f16": (_I, [_P, _S, _P, _P, _S, _S, _P]),
-    "hipllm_gemm_mfma": (_I, [_U32, _P, _S, _P, _P, _P, _P, _P, _S, _S, _S, _I, _I, _P]),
+    "hipllm_gemm_mfma": (_I, [_U32, _P, _S, _P, _P, _P, _P, _P, _S, _S, _S, _I, _I, _P, _S, _P]),
+    "hipllm_gemm_mfma_workspace_bytes": (_S, [_S, _S, _S, _I, _I]),
     "hipllm_gemm_workspace_bytes": (_S, [_S, _S]),
     "hipllm_gemm": (_I, [_U32, _P, _S, _P, _S, _P, _P, _S, _S, _S, _P, _P]),
     "hipllm_rmsnorm": (_I, [_P, _P, _P, _P, _S, _S, _F, _P]),
@@ -143,6 +156,21 @@ SIGNATURES = {
     "hipllm_set_batched_prefill": (_I, [_P, _I]),
     "hipllm_set_decode_graphs": (_I, [_P, _I]),
     "hipllm_inspect_gguf": (_I, [ctypes.c_char_p, ctypes.POINTER(HipllmConfig)]),
+    "hipllm_tokenizer_create": (_I, [ctypes.POINTER(ctypes.c_char_p), _S, ctypes.POINTER(ctypes.c_char_p), _S,
+                                     ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "hipllm_tokenizer_from_model": (_I, [_P, ctypes.POINTER(_P)]),
+    "hipllm_tokenizer_destroy": (None, [_P]),
+    "hipllm_tokenize": (_I, [_P, ctypes.c_char_p, _S, _P, _S, ctypes.POINTER(_S)]),
+    "hipllm_token_id": (_I32, [_P, ctypes.c_char_p]),
+    "hipllm_token_is_special": (_I, [_P, _I32]),
+    "hipllm_decode_piece": (_I, [_P, _I32, _P, _S, ctypes.POINTER(_S)]),
+    "hipllm_pretokenize": (_I, [_P, ctypes.c_char_p, _S, _P, _S, ctypes.POINTER(_S)]),
+    "hipllm_chat_prompt": (_I, [ctypes.c_char_p, ctypes.c_char_p, _P, _S, ctypes.POINTER(_S)]),
+    "hipllm_stop_tokens": (_I, [_P, _P, _P, _S, ctypes.POINTER(_S)]),
+    "hipllm_run": (_I, [_P, _P, _S, _S, _P, _S, TOKEN_SINK, _P, _P, _S, ctypes.POINTER(_S),
+                        ctypes.POINTER(HipllmGenerationStats)]),
+    "hipllm_format_generation_stats": (_I, [ctypes.POINTER(HipllmGenerationStats), _P, _S, ctypes.POINTER(_S)]),
+    "hipllm_chat_main": (_I, [_I, ctypes.POINTER(ctypes.c_char_p)]),
 }
 
 
@@ -306,6 +334,144 @@ class HipLLM:
         return lib().hipllm_tokenizer_pre(self._h).decode()
 
 
+def _bytes(text) -> bytes:
+    return text.encode("utf-8") if isinstance(text, str) else bytes(text)
+
+
+def _read_sized(call, what: str) -> bytes:
+    """Two-pass read of a (buffer, capacity, *length) C-ABI call."""
+    n = _S(0)
+    rc = call(None, 0, ctypes.byref(n))
+    if rc not in (OK, LENGTH_ERROR):
+        check(rc)
+    buf = ctypes.create_string_buffer(max(1, n.value))
+    check(call(buf, n.value, ctypes.byref(n)))
+    return buf.raw[:n.value]
+
+
+class QwenTokenizer:
+    """QwenTokenizer (chat.cpp:349-529) in libhipllm.so: encode, id,
+    decode_piece, is_special, plus the pre-tokenizer's piece ranges.
+    Host code only; usable without a GPU."""
+
+    def __init__(self, vocabulary, merges, tokenizer_pre: str = "", *, _handle=None):
+        if _handle is not None:
+            self._h = _handle
+            return
+        voc = [_bytes(v) for v in vocabulary]
+        mer = [_bytes(m) for m in merges]
+        varr = (ctypes.c_char_p * max(1, len(voc)))(*voc)
+        marr = (ctypes.c_char_p * max(1, len(mer)))(*mer)
+        h = _P()
+        check(lib().hipllm_tokenizer_create(varr, len(voc), marr, len(mer), _bytes(tokenizer_pre), ctypes.byref(h)))
+        self._h = h
+
+    @classmethod
+    def from_model(cls, model: "HipLLM") -> "QwenTokenizer":
+        h = _P()
+        check(lib().hipllm_tokenizer_from_model(model._h, ctypes.byref(h)))
+        return cls(None, None, _handle=h)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib().hipllm_tokenizer_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def encode(self, text) -> list:
+        data = _bytes(text)
+        n = _S(0)
+        cap = len(data) + 1
+        while True:
+            out = (ctypes.c_int32 * cap)()
+            rc = lib().hipllm_tokenize(self._h, data, len(data), out, cap, ctypes.byref(n))
+            if rc == LENGTH_ERROR and n.value > cap:
+                cap = n.value
+                continue
+            check(rc)
+            return list(out[:n.value])
+
+    def id(self, token) -> int:
+        return lib().hipllm_token_id(self._h, _bytes(token))
+
+    def is_special(self, token: int) -> bool:
+        return bool(lib().hipllm_token_is_special(self._h, int(token)))
+
+    def decode_piece(self, token: int) -> bytes:
+        return _read_sized(lambda b, c, n: lib().hipllm_decode_piece(self._h, int(token), b, c, n), "decode_piece")
+
+    def decode(self, tokens) -> bytes:
+        return b"".join(self.decode_piece(t) for t in tokens)
+
+    def pieces(self, text) -> list:
+        data = _bytes(text)
+        n = _S(0)
+        cap = 2 * len(data) + 2
+        out = (ctypes.c_size_t * cap)()
+        check(lib().hipllm_pretokenize(self._h, data, len(data), out, cap, ctypes.byref(n)))
+        return [(out[2 * i], out[2 * i + 1]) for i in range(n.value)]
+
+
+def chat_prompt(system, user) -> str:
+    """ChatML wrapping of one turn (chat.cpp:655-659)."""
+    raw = _read_sized(lambda b, c, n: lib().hipllm_chat_prompt(_bytes(system), _bytes(user), b, c, n), "chat_prompt")
+    return raw.decode("utf-8")
+
+
+def stop_tokens(model: "HipLLM", tokenizer: QwenTokenizer) -> list:
+    """make_stop_tokens (chat.cpp:708-726)."""
+    cap = 64
+    while True:
+        out = (ctypes.c_int32 * cap)()
+        n = _S(0)
+        rc = lib().hipllm_stop_tokens(model._h, tokenizer._h, out, cap, ctypes.byref(n))
+        if rc == LENGTH_ERROR and n.value > cap:
+            cap = n.value
+            continue
+        check(rc)
+        return list(out[:n.value])
+
+
+def _stats_dict(s: HipllmGenerationStats) -> dict:
+    d = {k: getattr(s, k) for k, _ in HipllmGenerationStats._fields_ if k != "memory"}
+    d["memory"] = {k: getattr(s.memory, k) for k, _ in HipllmMemoryStats._fields_}
+    for k in ("used_gpu", "stopped", "has_expert_cache_stats"):
+        d[k] = bool(d[k])
+    return d
+
+
+def run(model: "HipLLM", ids, max_new_tokens: int, stop_token_ids=(), token_sink=None):
+    """chat::run (chat.h:59-75) in libhipllm.so: returns (tokens, stats, stats_line)."""
+    ids = np.ascontiguousarray(np.asarray(ids, dtype=np.int32))
+    stop = np.ascontiguousarray(np.asarray(list(stop_token_ids), dtype=np.int32))
+    cap = max(1, int(max_new_tokens))
+    out = (ctypes.c_int32 * cap)()
+    n = _S(0)
+    stats = HipllmGenerationStats()
+    errors = []
+
+    def _sink(token, _user):
+        try:
+            token_sink(int(token))
+        except Exception as e:  # an exception must not cross the C ABI
+            errors.append(e)
+
+    sink = TOKEN_SINK(_sink) if token_sink else TOKEN_SINK()
+    check(lib().hipllm_run(model._h, ids.ctypes.data if ids.size else None, ids.size, int(max_new_tokens),
+                           stop.ctypes.data if stop.size else None, stop.size, sink, None, out, cap,
+                           ctypes.byref(n), ctypes.byref(stats)))
+    if errors:
+        raise errors[0]
+    line = _read_sized(lambda b, c, k: lib().hipllm_format_generation_stats(ctypes.byref(stats), b, c, k),
+                       "format_generation_stats").decode()
+    return list(out[:min(cap, n.value)]), _stats_dict(stats), line
+
+
 def generate(backend, prompt, max_new_tokens: int, stop_token_ids=(), on_step=None):
     """chat.cpp:831-878 generate(): reset, prefill, then emit/decode."""
     if len(prompt) == 0:
@@ -388,9 +554,18 @@ def _k_gemv_swiglu_norm(qtype, wg, wu, row_bytes, x, gamma, eps, y, yq, n, k, ti
                                         _ptr(yq), n, k, tiling, _stream(stream)))
 
 
-def _k_gemm_mfma(qtype, w, row_bytes, xh, xscale, bias, residual, y, m, n, k, tile=-1, stream=None, splits=0):
+def _k_gemm_mfma(qtype, w, row_bytes, xh, xscale, bias, residual, y, m, n, k, tile=-1, stream=None, splits=0,
+                 workspace=None):
+    """workspace: a device buffer for the K split's partial sums; by default
+    one of hipllm_gemm_mfma_workspace_bytes is allocated on y's device."""
+    if workspace is None:
+        need = lib().hipllm_gemm_mfma_workspace_bytes(m, n, k, tile, max(splits, 0))
+        if need:
+            import torch
+            workspace = torch.empty(need, dtype=torch.uint8, device=y.device)
+    nbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     check(lib().hipllm_gemm_mfma(qtype, _ptr(w), row_bytes, _ptr(xh), _ptr(xscale), _ptr(bias), _ptr(residual),
-                                 _ptr(y), m, n, k, tile, splits, _stream(stream)))
+                                 _ptr(y), m, n, k, tile, splits, _ptr(workspace), nbytes, _stream(stream)))
 
 
 def _k_gemm(qtype, w, row_bytes, x, ldx, bias, y, m, n, k, workspace, stream=None):

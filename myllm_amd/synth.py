@@ -264,3 +264,102 @@ def file_sha256(path) -> str:
         for chunk in iter(lambda: f.read(1 << 24), b""):
             h.update(chunk)
     return h.hexdigest()
+
+
+# ------------------------------------------------------------ tokenizer tables
+
+_GGUF_SCALAR_SIZE = {0: 1, 1: 1, 2: 2, 3: 2, 4: 4, 5: 4, 6: 4, 7: 1, 10: 8, 11: 8, 12: 8}
+_GGUF_STRING, _GGUF_ARRAY = 8, 9
+
+
+def _skip_value(buf: bytes, pos: int, vtype: int) -> int:
+    if vtype in _GGUF_SCALAR_SIZE:
+        return pos + _GGUF_SCALAR_SIZE[vtype]
+    if vtype == _GGUF_STRING:
+        (n,) = np.frombuffer(buf, "<u8", 1, pos)
+        return pos + 8 + int(n)
+    if vtype == _GGUF_ARRAY:
+        etype = int(np.frombuffer(buf, "<u4", 1, pos)[0])
+        count = int(np.frombuffer(buf, "<u8", 1, pos + 4)[0])
+        pos += 12
+        if etype in _GGUF_SCALAR_SIZE:
+            return pos + count * _GGUF_SCALAR_SIZE[etype]
+        for _ in range(count):
+            pos = _skip_value(buf, pos, etype)
+        return pos
+    raise ValueError(f"unknown GGUF value type {vtype}")
+
+
+def _gguf_str(s) -> bytes:
+    data = s.encode("utf-8") if isinstance(s, str) else bytes(s)
+    return len(data).to_bytes(8, "little") + data
+
+
+def add_tokenizer(src, dst, tokens, merges, tokenizer_pre: str = "qwen2") -> pathlib.Path:
+    """Copies GGUF ``src`` to ``dst`` with the tokenizer tables the chat front
+    end reads (tokenizer.ggml.tokens / .merges / .pre, as string arrays and a
+    string), replacing any present. The tensor directory and data are copied
+    unchanged; the data start moves to the next ``general.alignment``
+    boundary."""
+    src, dst = pathlib.Path(src), pathlib.Path(dst)
+    with open(src, "rb") as f:
+        head = f.read(1 << 20)
+        while True:
+            try:
+                return _add_tokenizer(src, dst, head, tokens, merges, tokenizer_pre)
+            except (IndexError, ValueError) as e:  # header longer than what was read
+                more = f.read(len(head))
+                if not more:
+                    raise ValueError(f"{src}: malformed GGUF header") from e
+                head += more
+
+
+def _add_tokenizer(src, dst, head, tokens, merges, pre):
+    if head[:4] != b"GGUF":
+        raise ValueError("not a GGUF file")
+    tensor_count = int.from_bytes(head[8:16], "little")
+    kv_count = int.from_bytes(head[16:24], "little")
+    pos, alignment = 24, 32
+    keep = []
+    replaced = {"tokenizer.ggml.tokens", "tokenizer.ggml.merges", "tokenizer.ggml.pre"}
+    for _ in range(kv_count):
+        start = pos
+        klen = int.from_bytes(head[pos:pos + 8], "little")
+        key = head[pos + 8:pos + 8 + klen].decode()
+        pos += 8 + klen
+        vtype = int.from_bytes(head[pos:pos + 4], "little")
+        vpos = pos + 4
+        pos = _skip_value(head, vpos, vtype)
+        if pos > len(head):
+            raise IndexError("short header")
+        if key == "general.alignment":
+            alignment = int.from_bytes(head[vpos:vpos + 4], "little")
+        if key not in replaced:
+            keep.append(head[start:pos])
+    info_start = pos
+    for _ in range(tensor_count):
+        nlen = int.from_bytes(head[pos:pos + 8], "little")
+        pos += 8 + nlen
+        ndim = int.from_bytes(head[pos:pos + 4], "little")
+        pos += 4 + 8 * ndim + 4 + 8
+        if pos > len(head):
+            raise IndexError("short header")
+    infos = head[info_start:pos]
+    data_start = (pos + alignment - 1) // alignment * alignment
+
+    def string_array(key, values):
+        out = _gguf_str(key) + _GGUF_ARRAY.to_bytes(4, "little") + _GGUF_STRING.to_bytes(4, "little")
+        out += len(values).to_bytes(8, "little")
+        return out + b"".join(_gguf_str(v) for v in values)
+
+    extra = [string_array("tokenizer.ggml.tokens", tokens), string_array("tokenizer.ggml.merges", merges),
+             _gguf_str("tokenizer.ggml.pre") + _GGUF_STRING.to_bytes(4, "little") + _gguf_str(pre)]
+    new_head = head[:8] + tensor_count.to_bytes(8, "little") + (len(keep) + len(extra)).to_bytes(8, "little")
+    new_head += b"".join(keep) + b"".join(extra) + infos
+    new_head += b"\0" * ((-len(new_head)) % alignment)
+    with open(src, "rb") as fin, open(dst, "wb") as fout:
+        fout.write(new_head)
+        fin.seek(data_start)
+        while chunk := fin.read(1 << 24):
+            fout.write(chunk)
+    return dst

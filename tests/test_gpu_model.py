@@ -122,6 +122,22 @@ def test_reset_reproduces_same_tokens(cuda, golden_model):
     assert a == b == g["tokens"][:8].tolist()
 
 
+def test_batched_prefill_is_bit_reproducible(cuda, golden_model):
+    """A 64-row prompt on the 0.5B shape splits its prefill matmuls along k;
+    the partial sums are added in a fixed order, so the same prompt gives the
+    same logits bit for bit on every run."""
+    path, g = golden_model("qwen2.5-0.5b")
+    prompt = (list(g["prompt"]) * 4)[:64]
+    runs = []
+    with HipLLM(path, 128) as m:
+        for _ in range(3):
+            m.reset()
+            m.prefill(prompt)
+            runs.append(m.logits().copy())
+    for r in runs[1:]:
+        assert np.array_equal(runs[0].view(np.int32), r.view(np.int32))
+
+
 def _decode_run(path, prompts, steps, graphs, max_sequence=64):
     """Tokens and logits of prefill + `steps` greedy decodes for each prompt
     in turn (reset between prompts), with decode graphs on or off."""

@@ -19,7 +19,7 @@ import pytest
 import numpy as np
 
 from myllm_amd import synth
-from myllm_amd.hipllm import kernels
+from myllm_amd.hipllm import kernels, lib
 from tests.test_gpu_kernels import dev_bytes, random_rows, rel_err
 
 torch = pytest.importorskip("torch")
@@ -109,6 +109,43 @@ def test_gemm_k_splits(cuda, qtype, splits):
                               splits=splits)
     assert rel_err(y, ref) <= 2e-2
     assert rel_err(y, ref_b) <= 1e-4
+
+
+@pytest.mark.parametrize("tile", [1, 4])
+def test_gemm_k_split_is_deterministic(cuda, tile):
+    """The K split's partial sums are added in split order by one reduce
+    launch, not by atomics: repeated runs give the same bits."""
+    first = gemm_case(cuda, synth.Q4_K, 45, 300, 1280, seed=5, tile=tile, bias=True, residual=True, splits=7)[0]
+    for _ in range(4):
+        again = gemm_case(cuda, synth.Q4_K, 45, 300, 1280, seed=5, tile=tile, bias=True, residual=True, splits=7)[0]
+        assert np.array_equal(first, again)
+
+
+def test_gemm_split_workspace_rules(cuda):
+    """An explicit split without room for its partial planes is rejected;
+    the default split without workspace runs unsplit (same bits as splits=1)."""
+    qtype, m, n, k = synth.Q4_K, 40, 256, 1536
+    w = random_rows(qtype, n, k, 9)
+    dw = dev_bytes(w, cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(9)).to(cuda)
+    xh, xs = to_f16(x, cuda)
+    need = lib().hipllm_gemm_mfma_workspace_bytes(m, n, k, -1, 0)
+    assert need == lib().hipllm_gemm_mfma_workspace_bytes(m, n, k, -1, 0) > 0  # this shape splits by default
+    assert lib().hipllm_gemm_mfma_workspace_bytes(m, n, k, -1, 1) == 0
+    y1 = torch.empty(m, n, device=cuda)
+    kernels.gemm_mfma(qtype, dw, w.shape[1], xh, xs, None, None, y1, m, n, k, splits=1)
+    y0 = torch.empty(m, n, device=cuda)
+    kernels.gemm_mfma(qtype, dw, w.shape[1], xh, xs, None, None, y0, m, n, k,
+                      workspace=torch.empty(0, dtype=torch.uint8, device=cuda))
+    assert torch.equal(y0.view(torch.int32), y1.view(torch.int32))
+    need4 = lib().hipllm_gemm_mfma_workspace_bytes(m, n, k, -1, 4)
+    assert need4 == 4 * m * n * 4
+    short = torch.empty(need4 - 16, dtype=torch.uint8, device=cuda)
+    with pytest.raises(ValueError):
+        kernels.gemm_mfma(qtype, dw, w.shape[1], xh, xs, None, None, y0, m, n, k, splits=4, workspace=short)
+    yd = torch.empty(m, n, device=cuda)
+    kernels.gemm_mfma(qtype, dw, w.shape[1], xh, xs, None, None, yd, m, n, k)  # default split, full workspace
+    assert rel_err(yd.cpu().numpy(), y1.cpu().numpy()) <= 1e-6
 
 
 @pytest.mark.parametrize("splits", [1, 4])
