@@ -5,10 +5,13 @@ Headline (``value``): Q4_K decode-GEMV throughput in GB/s of algorithmic bytes
 at Qwen2.5-7B shapes, batch 1. One step = the four weight GEMVs of one decoder
 layer (fused QKV 3584->4608, gate 3584->18944, up 3584->18944, down
 18944->3584) with FP32 activations N(0, 1) and N(0, 0.02) weights quantized to
-Q4_K. Steps rotate over enough weight copies (> 2x the 256 MB Infinity Cache)
-that every GEMV streams its weights from HBM; inputs are resident in HBM
-before timing and the timed steps replay a HIP graph of the launches.
-Algorithmic bytes per GEMV = N * row_bytes + 4 K + 4 N.
+Q4_K, held in the x16 tile-packed form the int8-MFMA GEMV reads (the same
+bytes as the GGUF rows, regrouped into 16-row tiles; the vector GEMV on the
+GGUF rows is timed beside it). Steps rotate over at least 16 weight copies
+(and 3x the 256 MB Infinity Cache) so that every GEMV, also when timed alone,
+streams its weights from HBM; inputs are resident in HBM before timing and
+the timed steps replay a HIP graph of the launches. Algorithmic bytes per
+GEMV = N * row_bytes + 4 K + 4 N.
 
 The same JSON line carries:
 * ``roofline``: the dominant kernel (the 3584->18944 gate GEMV) timed alone
@@ -67,35 +70,48 @@ def scratch_dir():
 
 
 class Rotation:
-    """Device copies of one layer's four weight matrices, rotated per step."""
+    """Device copies of one layer's four weight matrices, rotated per step:
+    at least 16 copies and 3x the 256 MB Infinity Cache, so that a matrix
+    timed alone is also read from HBM every time (its 15 other copies, over
+    570 MB for the gate, pass through the cache between two reads of it).
+    packed: also hold each Q4_K copy in the x16 tile-packed form that the
+    MFMA GEMV reads (same byte count)."""
 
-    def __init__(self, qtype, torch, cuda, min_bytes=3 * MALL_BYTES):
+    def __init__(self, qtype, torch, cuda, min_bytes=3 * MALL_BYTES, packed=False):
         from myllm_amd import synth
+        from myllm_amd.hipllm import kernels
         self.host = {}
         for _, n, k in SHAPES:
             if (n, k) not in self.host:
                 self.host[(n, k)] = synth.random_quantized(n, k, qtype, seed=n * 7 + k)
         per_step = sum(self.host[(n, k)].nbytes for _, n, k in SHAPES)
-        self.copies = max(4, int(np.ceil(min_bytes / per_step)))
-        self.layers = []
+        self.copies = max(16, int(np.ceil(min_bytes / per_step)))
+        self.layers, self.packed = [], []
         for _ in range(self.copies):
-            layer = {}
+            layer, player = {}, {}
             for name, n, k in SHAPES:
                 src = self.host[(n, k)]
                 buf = torch.empty(src.nbytes + 256, dtype=torch.uint8, device=cuda)
                 buf[: src.nbytes].copy_(torch.from_numpy(src.reshape(-1)))
                 layer[name] = buf
+                if packed:
+                    pk = torch.empty(kernels.q4k_x16_bytes(n, k), dtype=torch.uint8, device=cuda)
+                    kernels.q4k_pack_x16(buf, src.shape[1], n, k, pk)
+                    player[name] = pk
             self.layers.append(layer)
+            self.packed.append(player)
         self.step_bytes = sum(gemv_bytes(n, k, self.host[(n, k)].shape[1]) for _, n, k in SHAPES)
 
     def row_bytes(self, n, k):
         return self.host[(n, k)].shape[1]
 
 
-def gemv_setup(qtype, torch, cuda):
+def gemv_setup(qtype, torch, cuda, packed=False):
+    """packed (Q4_K only): launch the MFMA GEMV on the x16-packed copies
+    instead of the vector GEMV on the GGUF rows."""
     from myllm_amd import synth
     from myllm_amd.hipllm import kernels
-    rot = Rotation(qtype, torch, cuda)
+    rot = Rotation(qtype, torch, cuda, packed=packed)
     xs = {k: torch.from_numpy(synth.normal(k, seed=k)).to(cuda) for k in (3584, 18944)}
     xq = {}  # XGroup form of each input (k / 16 groups of 64 bytes)
     for k, x in xs.items():
@@ -104,8 +120,11 @@ def gemv_setup(qtype, torch, cuda):
     ys = {name: torch.empty(n, dtype=torch.float32, device=cuda) for name, n, _ in SHAPES}
 
     def launch(c, name, n, k, stream=None):
-        kernels.gemv_prepped(qtype, rot.layers[c][name], rot.row_bytes(n, k), xs[k], xq[k], None, None,
-                             ys[name], n, k, 0, stream=stream)
+        if packed:
+            kernels.gemv_q4k_x16(rot.packed[c][name], xq[k], None, None, ys[name], n, k, 0, stream=stream)
+        else:
+            kernels.gemv_prepped(qtype, rot.layers[c][name], rot.row_bytes(n, k), xs[k], xq[k], None, None,
+                                 ys[name], n, k, 0, stream=stream)
 
     return rot, launch
 
@@ -137,8 +156,8 @@ def time_kernel(torch, fn, count, replays=5):
     return e0.elapsed_time(e1) * 1e-3 / (count * replays)
 
 
-def bench_gemv(qtype, steps, warmup, torch, cuda):
-    rot, launch = gemv_setup(qtype, torch, cuda)
+def bench_gemv(qtype, steps, warmup, torch, cuda, packed=False):
+    rot, launch = gemv_setup(qtype, torch, cuda, packed=packed)
     copies = rot.copies
 
     def step(c, stream=None):
@@ -430,7 +449,7 @@ def profile_kernel(name, reps, torch, cuda):
     """Runs one GEMV shape `reps` times plus a plain copy of the same byte
     count, for rocprofv3 counter collection (--pmc FETCH_SIZE / WRITE_SIZE)."""
     from myllm_amd import synth
-    rot, launch = gemv_setup(synth.Q4_K, torch, cuda)
+    rot, launch = gemv_setup(synth.Q4_K, torch, cuda, packed=True)
     _, n, k = next(s for s in SHAPES if s[0] == name)
     for i in range(reps):
         launch(i % rot.copies, name, n, k)
@@ -479,10 +498,13 @@ def main():
         print(json.dumps(r), flush=True)
         return
 
-    log("[bench] Q4_K GEMV")
-    q4 = bench_gemv(synth.Q4_K, args.steps, args.warmup, torch, cuda)
+    log("[bench] Q4_K GEMV (x16-packed weights, int8 MFMA)")
+    q4 = bench_gemv(synth.Q4_K, args.steps, args.warmup, torch, cuda, packed=True)
     log(f"[bench] Q4_K {q4['gbps']:.1f} GB/s; kernels " +
         ", ".join(f"{k}={v['gbps']:.0f}GB/s/{v['avg_us']:.1f}us" for k, v in q4["kernels"].items()))
+    log("[bench] Q4_K GEMV (GGUF rows, vector ALU)")
+    q4n = bench_gemv(synth.Q4_K, args.steps, args.warmup, torch, cuda)
+    log(f"[bench] Q4_K GGUF rows {q4n['gbps']:.1f} GB/s")
     log("[bench] Q6_K GEMV")
     q6 = bench_gemv(synth.Q6_K, args.steps, args.warmup, torch, cuda)
     log(f"[bench] Q6_K {q6['gbps']:.1f} GB/s")
@@ -535,16 +557,20 @@ def main():
         "data": "synthetic",
         "config": {"workload": "Q4_K decode GEMV at Qwen2.5-7B shapes, batch 1: one step = fused QKV "
                                "3584->4608 + gate 3584->18944 + up 3584->18944 + down 18944->3584",
-                   "weights": "Q4_K (GGML block layout, N(0,0.02) quantized)", "activations": "f32 N(0,1)",
+                   "weights": "Q4_K (N(0,0.02) quantized), held in the x16 tile-packed form (same bytes as the "
+                              "GGML rows)", "activations": "f32 N(0,1)",
                    "weight_copies_rotated": q4["copies"]},
         "roofline": {"bound": "hbm", "achieved": round(dom["gbps"], 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(dom["gbps"] / PEAK_HBM_GBPS, 4), "traffic": traffic,
-                     "kernel": "gemv Q4_K 3584->18944 (gate)", "bytes_per_launch": dom["bytes"],
+                     "kernel": "gemv Q4_K x16 MFMA 3584->18944 (gate)", "bytes_per_launch": dom["bytes"],
                      "avg_launch_us": round(dom["avg_us"], 3), "launches_timed": dom["launches"],
                      "plain_copy_same_bytes_us": round(copy["avg_us"], 3)},
-        "gemv": {"q4_k": {"step_gbps": round(q4["gbps"], 2),
+        "gemv": {"q4_k": {"step_gbps": round(q4["gbps"], 2), "weights": "x16 tile-packed, int8 MFMA",
                           "kernels": {k: {"gbps": round(v["gbps"], 1), "avg_us": round(v["avg_us"], 2)}
                                       for k, v in q4["kernels"].items()}},
+                 "q4_k_gguf_rows": {"step_gbps": round(q4n["gbps"], 2), "weights": "GGUF rows, vector ALU",
+                                    "kernels": {k: {"gbps": round(v["gbps"], 1), "avg_us": round(v["avg_us"], 2)}
+                                                for k, v in q4n["kernels"].items()}},
                  "q6_k": {"step_gbps": round(q6["gbps"], 2),
                           "kernels": {k: {"gbps": round(v["gbps"], 1), "avg_us": round(v["avg_us"], 2)}
                                       for k, v in q6["kernels"].items()}}},

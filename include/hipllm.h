@@ -95,6 +95,31 @@ int hipllm_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const fl
                         const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
                         void* stream);
 
+/* The x16 tile-packed form of Q4_K weights, a device-side layout of this
+ * backend (no counterpart in GGUF or the reference): rows in tiles of 16 (a
+ * partial last tile zero-padded), tile-units of 2304 contiguous bytes (the
+ * 16 rows' super-block headers, then their quant bytes in the order the
+ * GEMV's lanes read them). hipllm_q4k_x16_bytes: its size for n rows of k
+ * values (k % 256 == 0; 0 otherwise). hipllm_q4k_pack_x16 writes it from
+ * native rows (16-byte aligned buffers, row_bytes % 16 == 0). */
+size_t hipllm_q4k_x16_bytes(size_t n, size_t k);
+int hipllm_q4k_pack_x16(const void* w, size_t row_bytes, size_t n, size_t k, void* packed, void* stream);
+
+/* Decode GEMV y = W x (+ bias) (+ residual) over x16-packed Q4_K weights,
+ * with the integer products of the XGroup digits on the int8 matrix cores
+ * (v_mfma_i32_16x16x64_i8); xq as for hipllm_gemv_prepped. Same arithmetic
+ * as the vector path (exact integer digit sums, FP32 scaling per 16-group),
+ * results equal to it within FP32 rounding of the summation order.
+ * `waves`: 0 picks the launch shape, else 1000 RT + 100 D + W: W waves
+ * per block (4, 8, 16) sharing RT 16-row tiles (1, 2), D units in flight
+ * per wave (1, 2, 4): 1104, 1204, 1404, 1108, 1208, 1116, 1216, 2104, 2204,
+ * 2108, 2208, 2116.
+ * Replaces metal_gevm_q4_k_f32 via encode_vector_product
+ * (metal_llm.metal:708-781; metal_llm.mm:1891-1999) and gevmt for Q4_K rows
+ * (cpu_llm.cpp:512-547). */
+int hipllm_gemv_q4k_x16(const void* packed, const void* xq, const float* bias, const float* residual, float* y,
+                        size_t n, size_t k, int waves, void* stream);
+
 /* hipllm_rmsnorm of the raw row x (gain gamma, k <= 8192, x and gamma
  * 16-byte aligned) followed by hipllm_gemv_prepped, in one launch: every
  * block normalises x into LDS (the same bits as hipllm_rmsnorm's XGroup

@@ -1017,6 +1017,245 @@ int gemv_pick_shape(uint32_t type, uint32_t n, uint32_t units, int mode) {
     return 100 * R + OPR;
 }
 
+// ------------------------------------------------------------ Q4_K on MFMA
+//
+// The decode GEMV of Q4_K weights held in the x16 tile-packed form, with its
+// integer products on the matrix cores (v_mfma_i32_16x16x64_i8).
+//
+// Packed form: rows in tiles of 16 (a partial last tile is zero-padded);
+// tile T, unit (super-block) u takes 2304 contiguous bytes at
+// (T * units + u) * 2304: the 16 rows' 16-byte headers (d, dmin,
+// scales[12]), then for lane l = 16 s + r the quant bytes [16 s, 16 s + 16)
+// of row r (at 256 + 16 l), then its bytes [64 + 16 s, 64 + 16 s + 16) (at
+// 1280 + 16 l). A wave reads each tile-unit as three fully contiguous
+// loads; in the GGUF row order the same wave touches 16 rows 2 KiB apart,
+// which measured 1.5x slower as a pure read on MI355X.
+//
+// Product: a wave owns one 16-row tile (the MFMA's N); lane l holds row
+// r = l % 16 and k-slice s = l / 16 of each 64-value product.
+// * The low nibbles of a lane's first 16 bytes feed MFMA (0, 0), their high
+//   nibbles MFMA (0, 1), the second 16 bytes MFMAs (1, 0), (1, 1). Slice s
+//   of MFMA (p, h) is the activation 16-group 8 p + 4 (s >> 1) + 2 h +
+//   (s & 1) of the unit, in sub-block 4 p + 2 (s >> 1) + h (model.cpp:616-644
+//   places low nibbles of bytes 32 j .. 32 j + 31 at elements 64 j .., the
+//   high nibbles 32 elements later).
+// * A's 16 rows are (group slice g, digit d): row 4 g + d holds digit d of
+//   the XGroup of slice g at k-slice g and zeros elsewhere (d = 3: zero). C
+//   row 4 g + d, column r is then the sum over the group's 16 values of
+//   q * digit d, so lane l receives digits 0..2 of its own slice's group for
+//   its row: t = c0 + 256 c1 + 65536 c2 = sum q * x_int exactly (|t| <=
+//   16 * 15 * 8355711 < 2^31).
+// * Each wave stages the 16 XGroups of its current unit in LDS, beside a
+//   zero region: the 12 lanes with (l % 16) / 4 == l / 16, (l % 16) % 4 < 3
+//   read their A slice from the groups, the others read zeros, with no
+//   branch.
+// * Each lane adds t e d sc - dmin m sum (the group's scale e and FP32 sum,
+//   the row's super-block scales) into one FP32 accumulator; the waves of a
+//   block split the units round-robin and are summed in wave order, the four
+//   lanes of a row by two xor shuffles: deterministic.
+// * The quant bytes, headers and x bytes of kMfmaDepth units are in flight
+//   per wave (a ring refilled as units are consumed).
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+constexpr int kMfmaDepth = 4;
+constexpr uint32_t kTileUnitBytes = 16 * 144;
+constexpr uint32_t kMfmaZeroBytes = 672;  // covers the A reads at offsets 0..655 (+16 bytes)
+
+struct Q4KMfmaUnit {
+    uint4 hd;      // this lane's row header
+    uint4 q0, q1;  // quant bytes 16 s .. and 64 + 16 s ..
+};
+
+__device__ __forceinline__ Q4KMfmaUnit q4k_mfma_load(const uint8_t* tu, uint32_t r, uint32_t lane) {
+    Q4KMfmaUnit v;
+    v.hd = ldw128(tu + 16 * r);
+    v.q0 = ldw128(tu + 256 + 16 * lane);
+    v.q1 = ldw128(tu + 1280 + 16 * lane);
+    return v;
+}
+
+__device__ __forceinline__ i32x4 nibbles(const uint4& q, bool high) {
+    i32x4 b;
+    if (high) {
+        b.x = static_cast<int>((q.x >> 4) & 0x0f0f0f0fu);
+        b.y = static_cast<int>((q.y >> 4) & 0x0f0f0f0fu);
+        b.z = static_cast<int>((q.z >> 4) & 0x0f0f0f0fu);
+        b.w = static_cast<int>((q.w >> 4) & 0x0f0f0f0fu);
+    } else {
+        b.x = static_cast<int>(q.x & 0x0f0f0f0fu);
+        b.y = static_cast<int>(q.y & 0x0f0f0f0fu);
+        b.z = static_cast<int>(q.z & 0x0f0f0f0fu);
+        b.w = static_cast<int>(q.w & 0x0f0f0f0fu);
+    }
+    return b;
+}
+
+// One unit of a lane: four MFMAs, each followed by its group's scaling.
+// a_src: LDS bytes of this lane's A slice for MFMA (0, 0) (the zero region
+// for lanes without A data); se_src: the (sum, e) pair of its slice's group
+// for MFMA (0, 0). MFMA (p, h) is 512 p + 128 h bytes further on for both.
+__device__ __forceinline__ float q4k_mfma_unit(const Q4KMfmaUnit& wu, const uint8_t* a_src, const uint8_t* se_src,
+                                               uint32_t s, float acc) {
+    const uint32_t h0 = wu.hd.x, h1 = wu.hd.y, h2 = wu.hd.z, h3 = wu.hd.w;
+    const float d = half_lo(h0), dmin = half_hi(h0);
+    // 6-bit scale / min bytes of sub-blocks 0..3 (lo) and 4..7 (hi)
+    // (get_scale_min_k4, model.cpp:524-537), shifted to this lane's pair.
+    const uint32_t sh = (s >> 1) * 16;
+    const uint32_t slo = (h1 & 0x3f3f3f3fu) >> sh, mlo = (h2 & 0x3f3f3f3fu) >> sh;
+    const uint32_t shi = ((h3 & 0x0f0f0f0fu) | ((h1 >> 2) & 0x30303030u)) >> sh;
+    const uint32_t mhi = (((h3 >> 4) & 0x0f0f0f0fu) | ((h2 >> 2) & 0x30303030u)) >> sh;
+    i32x4 a[4];
+    float2 se[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t off = 512 * (i >> 1) + 128 * (i & 1);
+        a[i] = *reinterpret_cast<const i32x4*>(a_src + off);
+        se[i] = *reinterpret_cast<const float2*>(se_src + off);
+    }
+    const i32x4 zero = {0, 0, 0, 0};
+    float sum_t = 0.0f, sum_m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int p = i >> 1, h = i & 1;
+        const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], nibbles(p ? wu.q1 : wu.q0, h != 0), zero, 0, 0, 0);
+        const int t = c.x + (c.y << 8) + (c.z << 16);
+        const uint32_t sc = p ? shi : slo, mn = p ? mhi : mlo;
+        const float scale = h ? ubyte1(sc) : ubyte0(sc);
+        const float mins = h ? ubyte1(mn) : ubyte0(mn);
+        sum_t = fmaf(static_cast<float>(t), se[i].y * scale, sum_t);
+        sum_m = fmaf(mins, se[i].x, sum_m);
+    }
+    return fmaf(d, sum_t, fmaf(-dmin, sum_m, acc));
+}
+
+// y = W x (+ bias) (+ residual) for x16-packed Q4_K W. A block of WPB waves
+// owns RT consecutive 16-row tiles; its waves split the units round-robin
+// and each wave multiplies every unit it takes into all RT tiles, so one
+// copy of the unit's activation groups serves 16 RT rows. Per unit a lane
+// loads 16 bytes of x's XGroups (the unit's 16 groups are 1 KiB, one load per
+// lane) with the unit's weights; the wave stores them to its own 1 KiB of
+// LDS and reads its A slices and (sum, e) pairs from there. Each wave also
+// keeps a zero region that the lanes without A data read instead. No block
+// barrier before the products: a wave starts as soon as its first unit has
+// landed. DEPTH units are in flight per wave.
+template <int WPB, int DEPTH, int RT>
+__global__ __launch_bounds__(64 * WPB) void gemv_q4k_x16_kernel(const uint8_t* __restrict__ w,
+                                                                const XGroup* __restrict__ xq,
+                                                                const float* __restrict__ bias,
+                                                                const float* __restrict__ residual,
+                                                                float* __restrict__ y, uint32_t n, uint32_t units) {
+    __shared__ __align__(16) uint8_t xs[WPB][2048];
+    __shared__ float part[WPB][16 * RT];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t r = lane & 15, s = lane >> 4;
+    const uint32_t tiles = (n + 15) / 16;
+    const uint32_t tile0 = blockIdx.x * RT;
+    const size_t tile_bytes = static_cast<size_t>(units) * kTileUnitBytes;
+    const uint8_t* wt[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) wt[t] = w + min(tile0 + t, tiles - 1) * tile_bytes;
+    const uint4* xsrc = reinterpret_cast<const uint4*>(xq);
+    // This wave's units: wave, wave + WPB, ...
+    const uint32_t mine = units > wave ? (units - wave + WPB - 1) / WPB : 0;
+    struct Slot {
+        uint4 x;
+        Q4KMfmaUnit w[RT];
+    };
+    Slot ring[DEPTH];
+    auto fill = [&](Slot& sl, uint32_t u) {
+        sl.x = xsrc[64 * u + lane];
+#pragma unroll
+        for (int t = 0; t < RT; ++t) sl.w[t] = q4k_mfma_load(wt[t] + static_cast<size_t>(u) * kTileUnitBytes, r, lane);
+    };
+#pragma unroll
+    for (int i = 0; i < DEPTH; ++i) {
+        if (static_cast<uint32_t>(i) < mine) fill(ring[i], wave + i * WPB);
+    }
+    uint8_t* lds = xs[wave];
+    if (lane < kMfmaZeroBytes / 16) *reinterpret_cast<uint4*>(lds + 1024 + 16 * lane) = make_uint4(0, 0, 0, 0);
+    const bool a_lane = (r >> 2) == s && (r & 3) < 3;
+    const uint32_t slot = 64 * (4 * (s >> 1) + (s & 1));  // group of slice s in MFMA (0, 0), bytes
+    const uint8_t* a_src = a_lane ? lds + slot + 16 * (r & 3) : lds + 1024;
+    const uint8_t* se_src = lds + slot + 48;
+    float acc[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) acc[t] = 0.0f;
+    for (uint32_t base = 0; base < mine; base += DEPTH) {
+#pragma unroll
+        for (int i = 0; i < DEPTH; ++i) {
+            const uint32_t idx = base + i;
+            if (idx < mine) {
+                *reinterpret_cast<uint4*>(lds + 16 * lane) = ring[i].x;
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int t = 0; t < RT; ++t) acc[t] = q4k_mfma_unit(ring[i].w[t], a_src, se_src, s, acc[t]);
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                if (idx + DEPTH < mine) fill(ring[i], wave + (idx + DEPTH) * WPB);
+            }
+        }
+    }
+    // Rows: lanes r, r + 16, r + 32, r + 48 hold the four group slices.
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+        float v = acc[t];
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        if (lane < 16) part[wave][16 * t + lane] = v;
+    }
+    __syncthreads();
+    if (tid < 16 * RT) {
+        const uint32_t row = tile0 * 16 + tid;
+        if (row < n) {
+            float v = part[0][tid];
+#pragma unroll
+            for (int i = 1; i < WPB; ++i) v += part[i][tid];
+            if (bias) v += bias[row];
+            if (residual) v += residual[row];
+            y[row] = v;
+        }
+    }
+}
+
+// Repacking: one thread per 16-byte chunk of the packed form (144 chunks per
+// tile-unit: 16 headers, 64 first slices, 64 second slices); rows past n
+// give zeros.
+__global__ __launch_bounds__(256) void q4k_pack_x16_kernel(const uint8_t* __restrict__ w, size_t row_bytes,
+                                                           uint8_t* __restrict__ out, uint32_t n, uint32_t units,
+                                                           size_t chunks) {
+    const size_t c = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (c >= chunks) return;
+    const size_t tu = c / 144;
+    const uint32_t j = static_cast<uint32_t>(c % 144);
+    const uint32_t tile = static_cast<uint32_t>(tu / units), u = static_cast<uint32_t>(tu % units);
+    uint32_t r, src;
+    if (j < 16) {
+        r = j;
+        src = 0;
+    } else {
+        const uint32_t l = (j - 16) % 64;
+        r = l & 15;
+        src = 16 + 64 * ((j - 16) / 64) + 16 * (l >> 4);
+    }
+    const uint32_t row = tile * 16 + r;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (row < n) v = ldw128(w + static_cast<size_t>(row) * row_bytes + static_cast<size_t>(u) * 144 + src);
+    *reinterpret_cast<uint4*>(out + c * 16) = v;
+}
+
+// Launch shape code 1000 RT + 100 DEPTH + WPB. Measured on MI355X over
+// 16+ rotated weight copies: tall matrices (>= 1000 tiles, e.g. 3584 ->
+// 18944) run best with 4 waves per block and two units in flight per wave
+// (every wave resident at once); short ones with 8 waves each streaming
+// their units (3584 -> 4608); long rows (>= 32 units, 18944 -> 3584) with 16
+// waves, one unit in flight each. Two tiles per wave measured no faster.
+int q4k_x16_default_waves(uint32_t n, uint32_t units) {
+    const uint32_t tiles = (n + 15) / 16;
+    if (tiles >= 1000) return 1204;
+    if (units >= 32) return 1116;
+    return 1108;
+}
+
 }  // namespace
 
 // Default tiling from a simple cost model (used for F32 / F16 weights and
@@ -1058,6 +1297,63 @@ int launch_prep_x(const float* x, XGroup* xq, size_t k, hipStream_t stream) {
 }
 
 // GEMV over a prepared XGroup input. tiling 0 selects the default.
+size_t q4k_x16_bytes(size_t n, size_t k) {
+    if (n == 0 || k == 0 || k % 256 != 0) return 0;
+    return (n + 15) / 16 * 16 * (k / 256) * 144;
+}
+
+int launch_q4k_pack_x16(const void* w, size_t row_bytes, size_t n, size_t k, void* packed, hipStream_t stream) {
+    if (!w || !packed || n == 0 || k == 0 || k % 256 != 0 || row_bytes < k / 256 * 144) return kInvalidArgument;
+    if (row_bytes % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0 || reinterpret_cast<uintptr_t>(packed) % 16 != 0) {
+        return kInvalidArgument;
+    }
+    if (n > 0x7fffffffull || k > 0x7fffffffull) return kLengthError;
+    const uint32_t units = static_cast<uint32_t>(k / 256);
+    const size_t chunks = (n + 15) / 16 * units * 144;
+    if ((chunks + 255) / 256 > 0x7fffffffull) return kLengthError;
+    HIPLLM_LAUNCH(q4k_pack_x16_kernel, dim3(static_cast<uint32_t>((chunks + 255) / 256)), dim3(256), 0, stream,
+                  static_cast<const uint8_t*>(w), row_bytes, static_cast<uint8_t*>(packed), static_cast<uint32_t>(n),
+                  units, chunks);
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+int launch_gemv_q4k_x16(const void* packed, const XGroup* xq, const float* bias, const float* residual, float* y,
+                        size_t n, size_t k, int waves, hipStream_t stream) {
+    if (!packed || !xq || !y || n == 0 || k == 0 || k % 256 != 0) return kInvalidArgument;
+    if (reinterpret_cast<uintptr_t>(packed) % 16 != 0 || reinterpret_cast<uintptr_t>(xq) % 16 != 0) {
+        return kInvalidArgument;
+    }
+    if (n > 0x7fffffffull) return kLengthError;
+    const uint32_t units = static_cast<uint32_t>(k / 256);
+    const uint32_t nn = static_cast<uint32_t>(n);
+    if (waves == 0) waves = q4k_x16_default_waves(nn, units);
+    const uint32_t tiles = (nn + 15) / 16;
+    const auto* wp = static_cast<const uint8_t*>(packed);
+    switch (waves) {
+#define HIPLLM_X16_CASE(RT, D, W)                                                                                \
+    case 1000 * RT + 100 * D + W:                                                                                \
+        HIPLLM_LAUNCH((gemv_q4k_x16_kernel<W, D, RT>), dim3((tiles + RT - 1) / RT), dim3(64 * W), 0, stream, wp, \
+                      xq, bias, residual, y, nn, units);                                                         \
+        break;
+        HIPLLM_X16_CASE(1, 1, 4)
+        HIPLLM_X16_CASE(1, 2, 4)
+        HIPLLM_X16_CASE(1, 4, 4)
+        HIPLLM_X16_CASE(1, 1, 8)
+        HIPLLM_X16_CASE(1, 2, 8)
+        HIPLLM_X16_CASE(1, 1, 16)
+        HIPLLM_X16_CASE(1, 2, 16)
+        HIPLLM_X16_CASE(2, 1, 4)
+        HIPLLM_X16_CASE(2, 2, 4)
+        HIPLLM_X16_CASE(2, 1, 8)
+        HIPLLM_X16_CASE(2, 2, 8)
+        HIPLLM_X16_CASE(2, 1, 16)
+#undef HIPLLM_X16_CASE
+    default:
+        return kInvalidArgument;
+    }
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
 int launch_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const float* x, const XGroup* xq,
                         const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
                         hipStream_t stream) {

@@ -212,6 +212,21 @@ int hipllm_gemv_multi_norm(const HipllmGemvJob* jobs, size_t count, const float*
                   "failure");
 }
 
+size_t hipllm_q4k_x16_bytes(size_t n, size_t k) { return hipllm::q4k_x16_bytes(n, k); }
+
+int hipllm_q4k_pack_x16(const void* w, size_t row_bytes, size_t n, size_t k, void* packed, void* stream) {
+    return status(hipllm::launch_q4k_pack_x16(w, row_bytes, n, k, packed, as_stream(stream)),
+                  "hipllm_q4k_pack_x16: invalid arguments (k % 256 == 0, 16-byte aligned buffers and rows) or launch "
+                  "failure");
+}
+
+int hipllm_gemv_q4k_x16(const void* packed, const void* xq, const float* bias, const float* residual, float* y,
+                        size_t n, size_t k, int waves, void* stream) {
+    return status(hipllm::launch_gemv_q4k_x16(packed, xgc(xq), bias, residual, y, n, k, waves, as_stream(stream)),
+                  "hipllm_gemv_q4k_x16: invalid arguments (k % 256 == 0, a known launch shape, 16-byte aligned "
+                  "buffers) or launch failure");
+}
+
 int hipllm_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m, size_t k, void* stream) {
     return status(hipllm::launch_to_f16(x, ldx, xh, xscale, m, k, as_stream(stream)),
                   "hipllm_to_f16: invalid arguments (k % 8 == 0, 16-byte aligned buffers) or launch failure");

@@ -1,0 +1,141 @@
+"""The x16 tile-packed Q4_K form and the int8-MFMA decode GEMV over it.
+
+* Packing: the device packer's bytes against a numpy restatement of the
+  layout (tile T, unit u at (T * units + u) * 2304: the 16 rows' headers,
+  then for lane l = 16 s + r the quant bytes [16 s, +16) of row r, then its
+  bytes [64 + 16 s, +16)); rows past n are zero.
+* Product: against float64 over the oracle's bit-exact CPU dequantization of
+  the same GGUF rows (oracle.dequant_rows restates model.cpp:616-644), for
+  ragged row counts, every launch shape, bias and residual, short and long
+  rows; and against the vector GEMV on the GGUF rows, which computes the
+  same exact integer digit sums (only the FP32 summation order differs).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from myllm_amd import synth
+from myllm_amd.hipllm import kernels
+from tests import xgroup
+from tests.test_gpu_kernels import dev_bytes, random_rows, rel_err
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+SHAPES = [1104, 1204, 1404, 1108, 1208, 1116, 1216, 2104, 2204, 2108, 2208, 2116]
+
+
+def pack_ref(w: np.ndarray, n: int, k: int) -> np.ndarray:
+    """numpy restatement of the x16 layout from GGUF rows [n, row_bytes]."""
+    units = k // 256
+    tiles = (n + 15) // 16
+    rows = np.zeros((tiles * 16, units, 144), dtype=np.uint8)
+    rows[:n] = w[:, : units * 144].reshape(n, units, 144)
+    out = np.empty((tiles, units, 2304), dtype=np.uint8)
+    for t in range(tiles):
+        blk = rows[16 * t: 16 * t + 16]  # [16, units, 144]
+        out[t, :, :256] = blk[:, :, :16].transpose(1, 0, 2).reshape(units, 256)
+        for part, base in ((0, 16), (1, 80)):
+            # lane l = 16 s + r: bytes base + 16 s .. of row r
+            sl = np.stack([blk[:, :, base + 16 * s: base + 16 * s + 16] for s in range(4)])  # [4, 16, units, 16]
+            out[t, :, 256 + 1024 * part: 1280 + 1024 * part] = sl.transpose(2, 0, 1, 3).reshape(units, 1024)
+    return out.reshape(-1)
+
+
+def packed_case(cuda, n, k, seed, bias=False, residual=False, waves=0):
+    w = random_rows(synth.Q4_K, n, k, seed)
+    dw = dev_bytes(w, cuda)
+    packed = torch.empty(kernels.q4k_x16_bytes(n, k), dtype=torch.uint8, device=cuda)
+    kernels.q4k_pack_x16(dw, w.shape[1], n, k, packed)
+    x = synth.normal(k, seed + 1)
+    dx = torch.from_numpy(x).to(cuda)
+    xq = xgroup.buffer(torch, k, cuda)
+    kernels.prep_x(dx, xq, k)
+    b = synth.normal(n, seed + 2) if bias else None
+    r = synth.normal(n, seed + 3) if residual else None
+    db = None if b is None else torch.from_numpy(b).to(cuda)
+    dr = None if r is None else torch.from_numpy(r).to(cuda)
+    y = torch.empty(n, dtype=torch.float32, device=cuda)
+    kernels.gemv_q4k_x16(packed, xq, db, dr, y, n, k, waves)
+    yv = torch.empty(n, dtype=torch.float32, device=cuda)
+    kernels.gemv_prepped(synth.Q4_K, dw, w.shape[1], dx, xq, db, dr, yv, n, k, 0)
+    wf = oracle.dequant_rows(synth.Q4_K, w, k).astype(np.float64)
+    ref = wf @ x.astype(np.float64)
+    for extra in (b, r):
+        if extra is not None:
+            ref = ref + extra
+    return y.cpu().numpy(), yv.cpu().numpy(), ref, w, packed
+
+
+@pytest.mark.parametrize("n,k", [(1, 256), (16, 512), (37, 3584), (333, 2816), (1001, 1024)])
+def test_pack_layout(cuda, n, k):
+    w = random_rows(synth.Q4_K, n, k, n + k)
+    packed = torch.empty(kernels.q4k_x16_bytes(n, k), dtype=torch.uint8, device=cuda)
+    assert packed.numel() == (n + 15) // 16 * 16 * (k // 256) * 144
+    kernels.q4k_pack_x16(dev_bytes(w, cuda), w.shape[1], n, k, packed)
+    assert np.array_equal(packed.cpu().numpy(), pack_ref(w, n, k))
+
+
+@pytest.mark.parametrize("n,k", [(1, 256), (16, 256), (37, 512), (333, 2816), (1001, 3584), (130, 18944)])
+def test_gemv_x16_matches_oracle_and_vector_path(cuda, n, k):
+    y, yv, ref, _, _ = packed_case(cuda, n, k, seed=7 * n + k, bias=True, residual=True)
+    assert rel_err(y, ref) <= 1e-5
+    assert rel_err(y, yv) <= 1e-6
+
+
+@pytest.mark.parametrize("waves", SHAPES)
+def test_gemv_x16_launch_shapes(cuda, waves):
+    # 7 units: fewer than some shapes' waves (idle waves), more than others'
+    # (several units per wave, ring refills); 45 rows: a partial tile, and
+    # for two tiles per block a partial tile pair.
+    y, yv, ref, _, _ = packed_case(cuda, 45, 7 * 256, seed=waves, residual=True, waves=waves)
+    assert rel_err(y, ref) <= 1e-5
+    assert rel_err(y, yv) <= 1e-6
+
+
+def test_gemv_x16_deterministic_and_long_rows(cuda):
+    # 159 units (ten per wave at 16 waves per block): every shape reduces in a
+    # fixed order, so repeated launches give the same bits.
+    n, k = 64, 159 * 256
+    y, yv, ref, _, _ = packed_case(cuda, n, k, seed=11, waves=1116)
+    assert rel_err(y, ref) <= 1e-5
+    y2, _, _, _, _ = packed_case(cuda, n, k, seed=11, waves=1116)
+    assert np.array_equal(y.view(np.int32), y2.view(np.int32))
+
+
+def test_gemv_x16_nan_input_propagates(cuda):
+    # A non-finite activation makes its XGroup's e NaN: the rows that read the
+    # group are NaN, as FP32 arithmetic would make them.
+    n, k = 32, 512
+    w = random_rows(synth.Q4_K, n, k, 3)
+    packed = torch.empty(kernels.q4k_x16_bytes(n, k), dtype=torch.uint8, device=cuda)
+    kernels.q4k_pack_x16(dev_bytes(w, cuda), w.shape[1], n, k, packed)
+    x = torch.from_numpy(synth.normal(k, 4)).to(cuda)
+    x[100] = float("nan")
+    xq = xgroup.buffer(torch, k, cuda)
+    kernels.prep_x(x, xq, k)
+    y = torch.empty(n, dtype=torch.float32, device=cuda)
+    kernels.gemv_q4k_x16(packed, xq, None, None, y, n, k, 0)
+    assert torch.isnan(y).all()
+
+
+def test_gemv_x16_rejects_bad_arguments(cuda):
+    n, k = 16, 256
+    packed = torch.zeros(kernels.q4k_x16_bytes(n, k) + 16, dtype=torch.uint8, device=cuda)
+    xq = xgroup.buffer(torch, k, cuda)
+    y = torch.empty(n, dtype=torch.float32, device=cuda)
+    assert kernels.q4k_x16_bytes(n, 300) == 0
+    with pytest.raises(ValueError):
+        kernels.gemv_q4k_x16(packed, xq, None, None, y, n, 300, 0)  # k % 256
+    with pytest.raises(ValueError):
+        kernels.gemv_q4k_x16(packed, xq, None, None, y, n, k, 1103)  # unknown launch shape
+    with pytest.raises(ValueError):
+        kernels.gemv_q4k_x16(packed[8:], xq, None, None, y, n, k, 0)  # misaligned weights
+    w = torch.zeros(n * 144 + 256, dtype=torch.uint8, device=cuda)
+    with pytest.raises(ValueError):
+        kernels.q4k_pack_x16(w, 150, n, k, packed)  # row_bytes % 16
+    with pytest.raises(ValueError):
+        kernels.q4k_pack_x16(w, 144, n, 200, packed)  # k % 256
