@@ -120,6 +120,15 @@ int hipllm_q4k_pack_x16(const void* w, size_t row_bytes, size_t n, size_t k, voi
 int hipllm_gemv_q4k_x16(const void* packed, const void* xq, const float* bias, const float* residual, float* y,
                         size_t n, size_t k, int waves, void* stream);
 
+/* The FFN gate/up pair over x16-packed Q4_K weights in one launch:
+ * y = silu(Wg x) * (Wu x) (the sign-branched SiLU of cpu_llm.cpp:188-202),
+ * and yq (nullable; n % 16 == 0) its XGroup form for the down projection.
+ * Same launch shapes as hipllm_gemv_q4k_x16. Replaces the gate / up GEVMs
+ * and SwiGLU of encode_decode_layer (metal_llm.mm:2850-2890;
+ * metal_llm.metal:708-781) for Q4_K weights. */
+int hipllm_gemv_q4k_x16_swiglu(const void* gate, const void* up, const void* xq, float* y, void* yq, size_t n,
+                               size_t k, int waves, void* stream);
+
 /* hipllm_rmsnorm of the raw row x (gain gamma, k <= 8192, x and gamma
  * 16-byte aligned) followed by hipllm_gemv_prepped, in one launch: every
  * block normalises x into LDS (the same bits as hipllm_rmsnorm's XGroup
@@ -553,6 +562,13 @@ int hipllm_set_batched_prefill(HipllmModel* model, int enabled);
  * reference's per-token command-buffer encoding (metal_llm.mm:3295-3385,
  * moe_llm.mm:3051-3141); no counterpart switch exists there. */
 int hipllm_set_decode_graphs(HipllmModel* model, int enabled);
+/* qwen2 only: 1 (default when the model has such projections) = the decode
+ * GEMVs of Q4_K projections (fused QKV, attention output, FFN gate / up) run
+ * on x16 tile-packed copies made at load time (hipllm_gemv_q4k_x16; the
+ * copies count in memory_stats' weight_bytes), 0 = on the GGUF rows.
+ * HIPLLM_INVALID_ARGUMENT when the model has nothing to pack or is not
+ * qwen2. No counterpart in the reference (a layout of this backend). */
+int hipllm_set_packed_decode(HipllmModel* model, int enabled);
 /* qwen35moe only: expert ids chosen for the last row of the last forward,
  * [layer_count, expert_used_count] (MoeLLM keeps them in RouteIds,
  * moe_llm.mm:2919-2925). */

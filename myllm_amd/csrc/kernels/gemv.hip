@@ -1137,34 +1137,45 @@ __device__ __forceinline__ float q4k_mfma_unit(const Q4KMfmaUnit& wu, const uint
 // keeps a zero region that the lanes without A data read instead. No block
 // barrier before the products: a wave starts as soon as its first unit has
 // landed. DEPTH units are in flight per wave.
-template <int WPB, int DEPTH, int RT>
+// MODE 0: y = W x (+ bias) (+ residual). MODE 1 (the FFN gate/up of one
+// row): w2 is the up matrix in the same form, y = silu(W x) * (W2 x) (the
+// reference's SwiGLU, cpu_llm.cpp:188-202) and yq (nullable) receives the
+// XGroup form of y, one group per 16-row tile (the down projection's input).
+template <int WPB, int DEPTH, int RT, int MODE>
 __global__ __launch_bounds__(64 * WPB) void gemv_q4k_x16_kernel(const uint8_t* __restrict__ w,
+                                                                const uint8_t* __restrict__ w2,
                                                                 const XGroup* __restrict__ xq,
                                                                 const float* __restrict__ bias,
                                                                 const float* __restrict__ residual,
-                                                                float* __restrict__ y, uint32_t n, uint32_t units) {
+                                                                float* __restrict__ y, XGroup* __restrict__ yq,
+                                                                uint32_t n, uint32_t units) {
+    constexpr int NM = MODE == 1 ? 2 : 1;  // matrices
+    constexpr int NA = NM * RT;            // accumulators
     __shared__ __align__(16) uint8_t xs[WPB][2048];
-    __shared__ float part[WPB][16 * RT];
+    __shared__ __align__(16) float part[WPB][16 * NA];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t r = lane & 15, s = lane >> 4;
     const uint32_t tiles = (n + 15) / 16;
     const uint32_t tile0 = blockIdx.x * RT;
     const size_t tile_bytes = static_cast<size_t>(units) * kTileUnitBytes;
-    const uint8_t* wt[RT];
+    const uint8_t* wt[NA];
 #pragma unroll
-    for (int t = 0; t < RT; ++t) wt[t] = w + min(tile0 + t, tiles - 1) * tile_bytes;
+    for (int t = 0; t < RT; ++t) {
+        wt[t] = w + min(tile0 + t, tiles - 1) * tile_bytes;
+        if (MODE == 1) wt[RT + t] = w2 + min(tile0 + t, tiles - 1) * tile_bytes;
+    }
     const uint4* xsrc = reinterpret_cast<const uint4*>(xq);
     // This wave's units: wave, wave + WPB, ...
     const uint32_t mine = units > wave ? (units - wave + WPB - 1) / WPB : 0;
     struct Slot {
         uint4 x;
-        Q4KMfmaUnit w[RT];
+        Q4KMfmaUnit w[NA];
     };
     Slot ring[DEPTH];
     auto fill = [&](Slot& sl, uint32_t u) {
         sl.x = xsrc[64 * u + lane];
 #pragma unroll
-        for (int t = 0; t < RT; ++t) sl.w[t] = q4k_mfma_load(wt[t] + static_cast<size_t>(u) * kTileUnitBytes, r, lane);
+        for (int t = 0; t < NA; ++t) sl.w[t] = q4k_mfma_load(wt[t] + static_cast<size_t>(u) * kTileUnitBytes, r, lane);
     };
 #pragma unroll
     for (int i = 0; i < DEPTH; ++i) {
@@ -1176,9 +1187,9 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q4k_x16_kernel(const uint8_t* _
     const uint32_t slot = 64 * (4 * (s >> 1) + (s & 1));  // group of slice s in MFMA (0, 0), bytes
     const uint8_t* a_src = a_lane ? lds + slot + 16 * (r & 3) : lds + 1024;
     const uint8_t* se_src = lds + slot + 48;
-    float acc[RT];
+    float acc[NA];
 #pragma unroll
-    for (int t = 0; t < RT; ++t) acc[t] = 0.0f;
+    for (int t = 0; t < NA; ++t) acc[t] = 0.0f;
     for (uint32_t base = 0; base < mine; base += DEPTH) {
 #pragma unroll
         for (int i = 0; i < DEPTH; ++i) {
@@ -1188,7 +1199,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q4k_x16_kernel(const uint8_t* _
                 __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
                 __builtin_amdgcn_wave_barrier();
 #pragma unroll
-                for (int t = 0; t < RT; ++t) acc[t] = q4k_mfma_unit(ring[i].w[t], a_src, se_src, s, acc[t]);
+                for (int t = 0; t < NA; ++t) acc[t] = q4k_mfma_unit(ring[i].w[t], a_src, se_src, s, acc[t]);
                 __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
                 __builtin_amdgcn_wave_barrier();
                 if (idx + DEPTH < mine) fill(ring[i], wave + (idx + DEPTH) * WPB);
@@ -1197,7 +1208,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q4k_x16_kernel(const uint8_t* _
     }
     // Rows: lanes r, r + 16, r + 32, r + 48 hold the four group slices.
 #pragma unroll
-    for (int t = 0; t < RT; ++t) {
+    for (int t = 0; t < NA; ++t) {
         float v = acc[t];
         v += __shfl_xor(v, 16);
         v += __shfl_xor(v, 32);
@@ -1206,14 +1217,24 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q4k_x16_kernel(const uint8_t* _
     __syncthreads();
     if (tid < 16 * RT) {
         const uint32_t row = tile0 * 16 + tid;
-        if (row < n) {
-            float v = part[0][tid];
+        float v = part[0][tid];
 #pragma unroll
-            for (int i = 1; i < WPB; ++i) v += part[i][tid];
+        for (int i = 1; i < WPB; ++i) v += part[i][tid];
+        if (MODE == 1) {
+            float u = part[0][16 * RT + tid];
+#pragma unroll
+            for (int i = 1; i < WPB; ++i) u += part[i][16 * RT + tid];
+            v = row < n ? silu_mul(v, u) : 0.0f;
+            part[0][tid] = v;  // the tile's outputs, for the XGroup encoding below
+        } else if (row < n) {
             if (bias) v += bias[row];
             if (residual) v += residual[row];
-            y[row] = v;
         }
+        if (row < n) y[row] = v;
+    }
+    if (MODE == 1 && yq) {
+        __syncthreads();
+        if (tid < static_cast<uint32_t>(RT) && (tile0 + tid) * 16 < n) xgroup_encode_from(&part[0][16 * tid], yq + tile0 + tid);
     }
 }
 
@@ -1317,23 +1338,16 @@ int launch_q4k_pack_x16(const void* w, size_t row_bytes, size_t n, size_t k, voi
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
-int launch_gemv_q4k_x16(const void* packed, const XGroup* xq, const float* bias, const float* residual, float* y,
-                        size_t n, size_t k, int waves, hipStream_t stream) {
-    if (!packed || !xq || !y || n == 0 || k == 0 || k % 256 != 0) return kInvalidArgument;
-    if (reinterpret_cast<uintptr_t>(packed) % 16 != 0 || reinterpret_cast<uintptr_t>(xq) % 16 != 0) {
-        return kInvalidArgument;
-    }
-    if (n > 0x7fffffffull) return kLengthError;
-    const uint32_t units = static_cast<uint32_t>(k / 256);
-    const uint32_t nn = static_cast<uint32_t>(n);
-    if (waves == 0) waves = q4k_x16_default_waves(nn, units);
+namespace {
+template <int MODE>
+int launch_x16(int code, const uint8_t* wp, const uint8_t* wp2, const XGroup* xq, const float* bias,
+               const float* residual, float* y, XGroup* yq, uint32_t nn, uint32_t units, hipStream_t stream) {
     const uint32_t tiles = (nn + 15) / 16;
-    const auto* wp = static_cast<const uint8_t*>(packed);
-    switch (waves) {
-#define HIPLLM_X16_CASE(RT, D, W)                                                                                \
-    case 1000 * RT + 100 * D + W:                                                                                \
-        HIPLLM_LAUNCH((gemv_q4k_x16_kernel<W, D, RT>), dim3((tiles + RT - 1) / RT), dim3(64 * W), 0, stream, wp, \
-                      xq, bias, residual, y, nn, units);                                                         \
+    switch (code) {
+#define HIPLLM_X16_CASE(RT, D, W)                                                                                   \
+    case 1000 * RT + 100 * D + W:                                                                                   \
+        HIPLLM_LAUNCH((gemv_q4k_x16_kernel<W, D, RT, MODE>), dim3((tiles + RT - 1) / RT), dim3(64 * W), 0, stream, wp, \
+                      wp2, xq, bias, residual, y, yq, nn, units);                                                   \
         break;
         HIPLLM_X16_CASE(1, 1, 4)
         HIPLLM_X16_CASE(1, 2, 4)
@@ -1352,6 +1366,36 @@ int launch_gemv_q4k_x16(const void* packed, const XGroup* xq, const float* bias,
         return kInvalidArgument;
     }
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+int check_x16(const void* packed, const XGroup* xq, const float* y, size_t n, size_t k) {
+    if (!packed || !xq || !y || n == 0 || k == 0 || k % 256 != 0) return kInvalidArgument;
+    if (reinterpret_cast<uintptr_t>(packed) % 16 != 0 || reinterpret_cast<uintptr_t>(xq) % 16 != 0) {
+        return kInvalidArgument;
+    }
+    if (n > 0x7fffffffull || k > 0x7fffffffull) return kLengthError;
+    return kOk;
+}
+}  // namespace
+
+int launch_gemv_q4k_x16(const void* packed, const XGroup* xq, const float* bias, const float* residual, float* y,
+                        size_t n, size_t k, int waves, hipStream_t stream) {
+    const int rc = check_x16(packed, xq, y, n, k);
+    if (rc != kOk) return rc;
+    const uint32_t units = static_cast<uint32_t>(k / 256), nn = static_cast<uint32_t>(n);
+    return launch_x16<0>(waves ? waves : q4k_x16_default_waves(nn, units), static_cast<const uint8_t*>(packed),
+                         nullptr, xq, bias, residual, y, nullptr, nn, units, stream);
+}
+
+int launch_gemv_q4k_x16_swiglu(const void* gate, const void* up, const XGroup* xq, float* y, XGroup* yq, size_t n,
+                               size_t k, int waves, hipStream_t stream) {
+    int rc = check_x16(gate, xq, y, n, k);
+    if (rc == kOk) rc = check_x16(up, xq, y, n, k);
+    if (rc != kOk) return rc;
+    if (yq && (n % 16 != 0 || reinterpret_cast<uintptr_t>(yq) % 16 != 0)) return kInvalidArgument;
+    const uint32_t units = static_cast<uint32_t>(k / 256), nn = static_cast<uint32_t>(n);
+    return launch_x16<1>(waves ? waves : q4k_x16_default_waves(nn, units), static_cast<const uint8_t*>(gate),
+                         static_cast<const uint8_t*>(up), xq, nullptr, nullptr, y, yq, nn, units, stream);
 }
 
 int launch_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const float* x, const XGroup* xq,

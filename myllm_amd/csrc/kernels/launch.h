@@ -105,6 +105,8 @@ size_t q4k_x16_bytes(size_t n, size_t k);
 int launch_q4k_pack_x16(const void* w, size_t row_bytes, size_t n, size_t k, void* packed, hipStream_t stream);
 int launch_gemv_q4k_x16(const void* packed, const XGroup* xq, const float* bias, const float* residual, float* y,
                         size_t n, size_t k, int waves, hipStream_t stream);
+int launch_gemv_q4k_x16_swiglu(const void* gate, const void* up, const XGroup* xq, float* y, XGroup* yq, size_t n,
+                               size_t k, int waves, hipStream_t stream);
 
 int gemm_default_tile(uint32_t m, uint32_t n, uint32_t k);
 uint32_t gemm_default_splits(uint32_t m, uint32_t n, uint32_t k, int tile);

@@ -227,6 +227,13 @@ int hipllm_gemv_q4k_x16(const void* packed, const void* xq, const float* bias, c
                   "buffers) or launch failure");
 }
 
+int hipllm_gemv_q4k_x16_swiglu(const void* gate, const void* up, const void* xq, float* y, void* yq, size_t n,
+                               size_t k, int waves, void* stream) {
+    return status(hipllm::launch_gemv_q4k_x16_swiglu(gate, up, xgc(xq), y, xg(yq), n, k, waves, as_stream(stream)),
+                  "hipllm_gemv_q4k_x16_swiglu: invalid arguments (k % 256 == 0, n % 16 == 0 with yq, a known launch "
+                  "shape, 16-byte aligned buffers) or launch failure");
+}
+
 int hipllm_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m, size_t k, void* stream) {
     return status(hipllm::launch_to_f16(x, ldx, xh, xscale, m, k, as_stream(stream)),
                   "hipllm_to_f16: invalid arguments (k % 8 == 0, 16-byte aligned buffers) or launch failure");
@@ -466,6 +473,12 @@ int hipllm_disable_profiling(HipllmModel* m) {
 int hipllm_copy_logits(const HipllmModel* m, float* out, size_t count) {
     if (!m || !out) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_copy_logits: null argument");
     return guarded([&] { m->visit([&](const auto& b) { b.copy_last_logits(out, count); }); });
+}
+
+int hipllm_set_packed_decode(HipllmModel* m, int enabled) {
+    if (!m) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_set_packed_decode: null argument");
+    if (!m->dense) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_set_packed_decode: qwen2 models only");
+    return guarded([&] { m->dense->set_packed_decode(enabled != 0); });
 }
 
 int hipllm_set_decode_graphs(HipllmModel* m, int enabled) {

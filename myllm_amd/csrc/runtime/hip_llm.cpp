@@ -35,6 +35,12 @@ struct DevLayer {
     const float* ffn_norm = nullptr;
     DevMatrix gate, up, down;
     bool fused_gate_up = false;
+    // Q4_K decode weights in the x16 tile-packed form (nullptr: not packed):
+    // the fused QKV rows, the attention output, the FFN gate and up.
+    const void* qkv_x16 = nullptr;
+    const void* o_x16 = nullptr;
+    const void* gate_x16 = nullptr;
+    const void* up_x16 = nullptr;
 };
 
 // Device activation buffers (one token row; the serial prefill reuses them).
@@ -91,6 +97,11 @@ struct HipLLM::Impl {
 
     WeightArena weights;
     std::size_t weight_bytes = 0;  // sum of GGUF tensor payloads
+    // Decode copies of the Q4_K projections in the x16 tile-packed form read
+    // by the int8-MFMA GEMV (the GGUF rows stay for the prefill matmuls).
+    void* x16_arena = nullptr;
+    std::size_t x16_bytes = 0;
+    bool packed_decode = false;
     DevMatrix embedding, output;
     const float* output_norm = nullptr;
     std::vector<DevLayer> layers;
@@ -129,6 +140,7 @@ struct HipLLM::Impl {
         if (host_step) hipHostFree(host_step);
         prof.reset();
         weights.release();
+        if (x16_arena) hipFree(x16_arena);
         if (kv_arena) hipFree(kv_arena);
         if (rope_table) hipFree(rope_table);
         if (act_arena) hipFree(act_arena);
@@ -143,6 +155,8 @@ struct HipLLM::Impl {
 
     void load(const std::string& path, std::size_t capacity, int dev);
     void upload(GgufReader& reader);
+    void pack_decode_weights();
+    void choose_decode_forms();
     void allocate_state();
     void build_rope_table();
     void ensure_prompt_capacity(std::size_t n);
@@ -199,22 +213,67 @@ void HipLLM::Impl::load(const std::string& path, std::size_t capacity, int dev) 
     config = std::move(cfg);
     max_sequence = capacity;
     upload(reader);
+    pack_decode_weights();
     allocate_state();
     build_rope_table();
     batched_prefill = batched_shapes();
-    {
-        auto quantized = [](std::uint32_t t) {
-            return t == hipllm::kQ4_K || t == hipllm::kQ6_K || t == hipllm::kQ8_0 || t == hipllm::kQ5_0;
-        };
-        const std::size_t H = config.embedding_size;
-        fused_norms = H % 16 == 0 && H <= 2048;
-        fused_ffn_norm = fused_norms;
-        for (const DevLayer& L : layers) {
-            fused_norms = fused_norms && L.fused_qkv && quantized(L.q.type);
-            fused_ffn_norm = fused_ffn_norm && L.fused_gate_up && quantized(L.gate.type);
-        }
-        fused_ffn_norm = fused_ffn_norm && fused_norms;
+    choose_decode_forms();
+}
+
+// The decode forms: the x16 MFMA GEMVs read the XGroup form of their input,
+// so with packed weights the norms run as their own launches; otherwise
+// short rows fold the norm into the GEMVs' prologue.
+void HipLLM::Impl::choose_decode_forms() {
+    auto quantized = [](std::uint32_t t) {
+        return t == hipllm::kQ4_K || t == hipllm::kQ6_K || t == hipllm::kQ8_0 || t == hipllm::kQ5_0;
+    };
+    const std::size_t H = config.embedding_size;
+    fused_norms = H % 16 == 0 && H <= 2048 && !packed_decode;
+    fused_ffn_norm = fused_norms;
+    for (const DevLayer& L : layers) {
+        fused_norms = fused_norms && L.fused_qkv && quantized(L.q.type);
+        fused_ffn_norm = fused_ffn_norm && L.fused_gate_up && quantized(L.gate.type);
     }
+    fused_ffn_norm = fused_ffn_norm && fused_norms;
+}
+
+// Q4_K projections whose rows hold whole super-blocks get an x16 copy: the
+// fused QKV rows (when Q, K and V are all Q4_K and contiguous), the
+// attention output, and the FFN gate / up pair (both Q4_K).
+void HipLLM::Impl::pack_decode_weights() {
+    auto q4k = [](const DevMatrix& m) { return m.type == hipllm::kQ4_K && m.cols % 256 == 0 && m.row_bytes % 16 == 0; };
+    const std::size_t H = config.embedding_size;
+    struct Job {
+        const DevMatrix* m;
+        std::size_t rows;
+        const void** dst;
+        std::size_t off;
+    };
+    std::vector<Job> jobs;
+    std::size_t total = 0;
+    auto add = [&](const DevMatrix& m, std::size_t rows, const void** dst) {
+        jobs.push_back({&m, rows, dst, total});
+        total = align_up(total + hipllm::q4k_x16_bytes(rows, m.cols), 256);
+    };
+    for (DevLayer& L : layers) {
+        if (L.fused_qkv && q4k(L.q) && q4k(L.k) && q4k(L.v)) add(L.q, H + 2 * kv_dim, &L.qkv_x16);
+        if (q4k(L.o)) add(L.o, L.o.rows, &L.o_x16);
+        if (L.fused_gate_up && q4k(L.gate) && q4k(L.up)) {
+            add(L.gate, L.gate.rows, &L.gate_x16);
+            add(L.up, L.up.rows, &L.up_x16);
+        }
+    }
+    if (jobs.empty()) return;
+    hip_check(hipMalloc(&x16_arena, total), "hipMalloc(x16 decode weights)");
+    x16_bytes = total;
+    auto* base = static_cast<std::uint8_t*>(x16_arena);
+    for (const Job& j : jobs) {
+        *j.dst = base + j.off;
+        launch_check(hipllm::launch_q4k_pack_x16(j.m->ptr, j.m->row_bytes, j.rows, j.m->cols, base + j.off, stream),
+                     "x16 packing");
+    }
+    hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    packed_decode = true;
 }
 
 void HipLLM::Impl::upload(GgufReader& reader) {
@@ -405,7 +464,12 @@ void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, fl
     const DevLayer& L = layers[li];
     const std::size_t H = c.embedding_size, F = c.feed_forward_size;
     const float eps = c.norm_epsilon;
-    if (fused_norms) {
+    if (packed_decode && L.qkv_x16) {
+        // act.normq holds the XGroup form of rmsnorm(hidden) * attn_norm.
+        launch_check(hipllm::launch_gemv_q4k_x16(L.qkv_x16, act.normq, L.qkv_bias, nullptr, act.qkv, H + 2 * kv_dim, H,
+                                                 0, stream),
+                     "QKV GEMV");
+    } else if (fused_norms) {
         // QKV of rmsnorm(hidden) * attn_norm, the norm in the GEMV's prologue.
         launch_check(hipllm::launch_gemv_norm(L.q.type, L.q.ptr, L.q.row_bytes, hidden, L.attn_norm, eps, L.qkv_bias,
                                               nullptr, act.qkv, H + 2 * kv_dim, H, 0, stream),
@@ -425,7 +489,12 @@ void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, fl
                                                  act.attn, act.attnq, act.attn_scratch, c.attention_head_count,
                                                  c.kv_head_count, c.head_size, pos, scale, stream, dpos, max_sequence),
                  "RoPE/KV write + attention");
-    gemv(L.o, act.attn, act.attnq, nullptr, hidden, next_hidden);
+    if (packed_decode && L.o_x16) {
+        launch_check(hipllm::launch_gemv_q4k_x16(L.o_x16, act.attnq, nullptr, hidden, next_hidden, H, H, 0, stream),
+                     "attention output GEMV");
+    } else {
+        gemv(L.o, act.attn, act.attnq, nullptr, hidden, next_hidden);
+    }
     if (fused_ffn_norm) {
         launch_check(hipllm::launch_gemv_swiglu_norm(L.gate.type, L.gate.ptr, L.up.ptr, L.gate.row_bytes, next_hidden,
                                                      L.ffn_norm, eps, act.ffn, act.ffnq, F, H, 0, stream),
@@ -433,7 +502,11 @@ void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, fl
     } else {
         launch_check(hipllm::launch_rmsnorm(next_hidden, L.ffn_norm, act.norm, act.normq, 1, H, eps, stream),
                      "RMSNorm");
-        if (L.fused_gate_up) {
+        if (packed_decode && L.gate_x16) {
+            launch_check(hipllm::launch_gemv_q4k_x16_swiglu(L.gate_x16, L.up_x16, act.normq, act.ffn, act.ffnq, F, H, 0,
+                                                            stream),
+                         "gate/up GEMV");
+        } else if (L.fused_gate_up) {
             launch_check(hipllm::launch_gemv_swiglu(L.gate.type, L.gate.ptr, L.up.ptr, L.gate.row_bytes, act.norm,
                                                     act.normq, act.ffn, act.ffnq, F, H, 0, stream),
                          "gate/up GEMV");
@@ -807,7 +880,7 @@ const std::string& HipLLM::device_name() const noexcept {
 MemoryStats HipLLM::memory_stats() const noexcept {
     if (!impl_) return {};
     MemoryStats s;
-    s.weight_bytes = impl_->weight_bytes;
+    s.weight_bytes = impl_->weight_bytes + impl_->x16_bytes;
     s.kv_cache_bytes = impl_->kv_cache_bytes;
     s.recurrent_state_bytes = 0;
     s.intermediate_bytes = impl_->act_bytes;
@@ -828,6 +901,17 @@ void HipLLM::set_decode_graphs(bool enabled) {
     impl_->decode_graphs = enabled;
     if (!enabled) impl_->drop_decode_graph();
 }
+
+void HipLLM::set_packed_decode(bool enabled) {
+    if (!impl_) throw std::runtime_error("HIP model is not initialized");
+    if (enabled && !impl_->x16_arena) throw std::invalid_argument("the model has no Q4_K projections to pack");
+    hip_check(hipStreamSynchronize(impl_->stream), "hipStreamSynchronize");
+    impl_->packed_decode = enabled;
+    impl_->choose_decode_forms();
+    impl_->drop_decode_graph();  // recorded with the other forms
+}
+
+bool HipLLM::packed_decode() const noexcept { return impl_ && impl_->packed_decode; }
 
 void HipLLM::set_batched_prefill(bool enabled) {
     if (!impl_) throw std::runtime_error("HIP model is not initialized");

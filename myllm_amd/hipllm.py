@@ -90,6 +90,7 @@ SIGNATURES = {
     "hipllm_q4k_x16_bytes": (_S, [_S, _S]),
     "hipllm_q4k_pack_x16": (_I, [_P, _S, _S, _S, _P, _P]),
     "hipllm_gemv_q4k_x16": (_I, [_P, _P, _P, _P, _P, _S, _S, _I, _P]),
+    "hipllm_gemv_q4k_x16_swiglu": (_I, [_P, _P, _P, _P, _P, _S, _S, _I, _P]),
     "hipllm_gemm_mfma": (_I, [_U32, _P, _S, _P, _P, _P, _P, _P, _S, _S, _S, _I, _I, _P, _S, _P]),
     "hipllm_gemm_mfma_workspace_bytes": (_S, [_S, _S, _S, _I, _I]),
     "hipllm_gemm_workspace_bytes": (_S, [_S, _S]),
@@ -158,6 +159,7 @@ SIGNATURES = {
     "hipllm_copy_logits": (_I, [_P, _P, _S]),
     "hipllm_set_batched_prefill": (_I, [_P, _I]),
     "hipllm_set_decode_graphs": (_I, [_P, _I]),
+    "hipllm_set_packed_decode": (_I, [_P, _I]),
     "hipllm_inspect_gguf": (_I, [ctypes.c_char_p, ctypes.POINTER(HipllmConfig)]),
     "hipllm_tokenizer_create": (_I, [ctypes.POINTER(ctypes.c_char_p), _S, ctypes.POINTER(ctypes.c_char_p), _S,
                                      ctypes.c_char_p, ctypes.POINTER(_P)]),
@@ -288,6 +290,9 @@ class HipLLM:
 
     def set_batched_prefill(self, enabled: bool) -> None:
         check(lib().hipllm_set_batched_prefill(self._h, 1 if enabled else 0))
+
+    def set_packed_decode(self, enabled: bool) -> None:
+        check(lib().hipllm_set_packed_decode(self._h, int(bool(enabled))))
 
     def set_decode_graphs(self, enabled: bool) -> None:
         """True (default): each decode step replays one recorded HIP graph."""
@@ -552,6 +557,11 @@ def _k_gemv_q4k_x16(packed, xq, bias, residual, y, n, k, waves=0, stream=None):
                                     _stream(stream)))
 
 
+def _k_gemv_q4k_x16_swiglu(gate, up, xq, y, yq, n, k, waves=0, stream=None):
+    check(lib().hipllm_gemv_q4k_x16_swiglu(_ptr(gate), _ptr(up), _ptr(xq), _ptr(y), _ptr(yq), n, k, waves,
+                                           _stream(stream)))
+
+
 def _k_to_f16(x, ldx, xh, xscale, m, k, stream=None):
     check(lib().hipllm_to_f16(_ptr(x), ldx, _ptr(xh), _ptr(xscale), m, k, _stream(stream)))
 
@@ -757,6 +767,7 @@ def _k_swiglu(g, u, y, yq, n, stream=None):
 kernels = types.SimpleNamespace(
     dequant_rows=_k_dequant_rows, prep_x=_k_prep_x, gemv=_k_gemv, gemv_noalloc=_k_gemv_noalloc,
     gemv_prepped=_k_gemv_prepped, q4k_pack_x16=_k_q4k_pack_x16, gemv_q4k_x16=_k_gemv_q4k_x16,
+    gemv_q4k_x16_swiglu=_k_gemv_q4k_x16_swiglu,
     q4k_x16_bytes=lambda n, k: lib().hipllm_q4k_x16_bytes(n, k),
     gemv_swiglu=_k_gemv_swiglu, gemv_norm=_k_gemv_norm, gemv_swiglu_norm=_k_gemv_swiglu_norm, to_f16=_k_to_f16, gemm_mfma=_k_gemm_mfma, gemm=_k_gemm,
     gemm_workspace_bytes=lambda m, k: lib().hipllm_gemm_workspace_bytes(m, k), rmsnorm=_k_rmsnorm, embed=_k_embed, rope_kv=_k_rope_kv,

@@ -139,3 +139,44 @@ def test_gemv_x16_rejects_bad_arguments(cuda):
         kernels.q4k_pack_x16(w, 150, n, k, packed)  # row_bytes % 16
     with pytest.raises(ValueError):
         kernels.q4k_pack_x16(w, 144, n, 200, packed)  # k % 256
+
+
+def silu_mul_ref(g, u):
+    """Sign-branched SiLU(g) * u in float64 (cpu_llm.cpp:188-202)."""
+    g = np.asarray(g, dtype=np.float64)
+    sig = np.where(g >= 0, 1.0 / (1.0 + np.exp(-np.abs(g))), np.exp(-np.abs(g)) / (1.0 + np.exp(-np.abs(g))))
+    return g * sig * np.asarray(u, dtype=np.float64)
+
+
+@pytest.mark.parametrize("n,k,waves", [(16, 256, 0), (64, 512, 1108), (1040, 3584, 0), (4864, 1024, 0),
+                                       (320, 2048, 2204), (48, 18944, 1116)])
+def test_gemv_x16_swiglu(cuda, n, k, waves):
+    wg = random_rows(synth.Q4_K, n, k, n + 1)
+    wu = random_rows(synth.Q4_K, n, k, n + 2)
+    pg = torch.empty(kernels.q4k_x16_bytes(n, k), dtype=torch.uint8, device=cuda)
+    pu = torch.empty_like(pg)
+    kernels.q4k_pack_x16(dev_bytes(wg, cuda), wg.shape[1], n, k, pg)
+    kernels.q4k_pack_x16(dev_bytes(wu, cuda), wu.shape[1], n, k, pu)
+    x = synth.normal(k, n + 3)
+    dx = torch.from_numpy(x).to(cuda)
+    xq = xgroup.buffer(torch, k, cuda)
+    kernels.prep_x(dx, xq, k)
+    y = torch.empty(n, dtype=torch.float32, device=cuda)
+    yq = xgroup.buffer(torch, n, cuda)
+    kernels.gemv_q4k_x16_swiglu(pg, pu, xq, y, yq, n, k, waves)
+    g = oracle.dequant_rows(synth.Q4_K, wg, k).astype(np.float64) @ x.astype(np.float64)
+    u = oracle.dequant_rows(synth.Q4_K, wu, k).astype(np.float64) @ x.astype(np.float64)
+    ref = silu_mul_ref(g, u)
+    yv = y.cpu().numpy()
+    assert rel_err(yv, ref) <= 1e-5
+    xgroup.check(yq, yv)
+    # The same pair through the vector path on the GGUF rows.
+    yv2 = torch.empty(n, dtype=torch.float32, device=cuda)
+    kernels.gemv_swiglu(synth.Q4_K, dev_bytes(wg, cuda), dev_bytes(wu, cuda), wg.shape[1], dx, xq, yv2, None, n, k, 0)
+    assert rel_err(yv, yv2.cpu().numpy()) <= 1e-6
+    # Without the XGroup output, and the output rows reject a ragged n.
+    kernels.gemv_q4k_x16_swiglu(pg, pu, xq, y, None, n, k, waves)
+    assert np.array_equal(y.cpu().numpy().view(np.int32), yv.view(np.int32))
+    if n > 16:
+        with pytest.raises(ValueError):
+            kernels.gemv_q4k_x16_swiglu(pg, pu, xq, y, yq, n - 1, k, waves)

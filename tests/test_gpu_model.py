@@ -14,7 +14,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from myllm_amd.hipllm import HipLLM, LengthError, generate
+from myllm_amd.hipllm import kernels, HipLLM, LengthError, generate
 
 pytestmark = pytest.mark.gpu
 
@@ -107,7 +107,12 @@ def test_memory_stats(cuda, golden_model):
     cfg = inspect_gguf(path)
     with HipLLM(path, 64) as m:
         s = m.memory_stats()
-    assert s["weight_bytes"] == cfg["stored_weight_bytes"]
+        m.set_packed_decode(False)
+    # The GGUF payload plus the x16 decode copies of the Q4_K projections
+    # (tiny: fused QKV and the gate / up pair; the attention output is Q5_0).
+    h, f, kv = cfg["embedding_size"], cfg["feed_forward_size"], cfg["kv_head_count"] * cfg["head_size"]
+    x16 = cfg["layer_count"] * (kernels.q4k_x16_bytes(h + 2 * kv, h) + 2 * kernels.q4k_x16_bytes(f, h))
+    assert s["weight_bytes"] == cfg["stored_weight_bytes"] + x16
     kv = cfg["kv_head_count"] * cfg["head_size"]
     assert s["kv_cache_bytes"] == 2 * cfg["layer_count"] * 64 * kv * 4
     assert s["recurrent_state_bytes"] == 0 and s["intermediate_bytes"] > 0
@@ -136,6 +141,29 @@ def test_batched_prefill_is_bit_reproducible(cuda, golden_model):
             runs.append(m.logits().copy())
     for r in runs[1:]:
         assert np.array_equal(runs[0].view(np.int32), r.view(np.int32))
+
+
+def test_packed_decode_matches_gguf_row_decode(cuda, golden_model):
+    """The x16 MFMA GEMVs and the vector GEMVs compute the same exact integer
+    digit sums: decode logits agree to FP32 summation rounding and the greedy
+    tokens are the same, graph or eager."""
+    path, g = golden_model("tiny")
+    prompt = list(g["prompt"])
+    out = {}
+    for packed in (True, False):
+        with HipLLM(path, 64) as m:
+            m.set_packed_decode(packed)
+            m.set_batched_prefill(False)  # serial prefill through the decode GEMVs
+            t = m.prefill(prompt)
+            toks, logits = [t], [m.logits()]
+            for _ in range(12):
+                t = m.decode(t)
+                toks.append(t)
+                logits.append(m.logits())
+            out[packed] = (toks, logits)
+    assert out[True][0] == out[False][0] == g["tokens"][:13].tolist()
+    for a, b in zip(out[True][1], out[False][1]):
+        assert np.abs(a - b).max() / np.abs(b).max() <= 1e-5
 
 
 def _decode_run(path, prompts, steps, graphs, max_sequence=64):
