@@ -110,10 +110,9 @@ int hipllm_q4k_pack_x16(const void* w, size_t row_bytes, size_t n, size_t k, voi
  * (v_mfma_i32_16x16x64_i8); xq as for hipllm_gemv_prepped. Same arithmetic
  * as the vector path (exact integer digit sums, FP32 scaling per 16-group),
  * results equal to it within FP32 rounding of the summation order.
- * `waves`: 0 picks the launch shape, else 1000 RT + 100 D + W: W waves
- * per block (4, 8, 16) sharing RT 16-row tiles (1, 2), D units in flight
- * per wave (1, 2, 4): 1104, 1204, 1404, 1108, 1208, 1116, 1216, 2104, 2204,
- * 2108, 2208, 2116.
+ * `waves`: 0 picks the launch shape, else 1000 RT + 100 + W: W waves
+ * per block (4, 8, 16) sharing RT 16-row tiles (1, 2), one unit in flight
+ * per wave: 1104, 1108, 1116, 2104, 2108, 2116.
  * Replaces metal_gevm_q4_k_f32 via encode_vector_product
  * (metal_llm.metal:708-781; metal_llm.mm:1891-1999) and gevmt for Q4_K rows
  * (cpu_llm.cpp:512-547). */

@@ -52,6 +52,13 @@ __device__ __forceinline__ uint4 ldw128(const uint8_t* p) {  // 16-byte aligned
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Streaming loads of bytes that exactly one lane of one wave reads (the x16
+// form's quant slices, each 16-byte piece read once per launch).
+__device__ __forceinline__ uint4 ldw128_nt(const uint8_t* p) {  // 16-byte aligned
+    const u32x4a16 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4a16*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ uint4 ldw128_a4(const uint8_t* p) {  // 4-byte aligned
     const u32x4a4 v = *reinterpret_cast<const u32x4a4*>(p);
     return make_uint4(v.x, v.y, v.z, v.w);
@@ -1053,10 +1060,9 @@ int gemv_pick_shape(uint32_t type, uint32_t n, uint32_t units, int mode) {
 //   the row's super-block scales) into one FP32 accumulator; the waves of a
 //   block split the units round-robin and are summed in wave order, the four
 //   lanes of a row by two xor shuffles: deterministic.
-// * The quant bytes, headers and x bytes of kMfmaDepth units are in flight
+// * The quant bytes, headers and x bytes of one or two units are in flight
 //   per wave (a ring refilled as units are consumed).
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-constexpr int kMfmaDepth = 4;
 constexpr uint32_t kTileUnitBytes = 16 * 144;
 constexpr uint32_t kMfmaZeroBytes = 672;  // covers the A reads at offsets 0..655 (+16 bytes)
 
@@ -1067,9 +1073,9 @@ struct Q4KMfmaUnit {
 
 __device__ __forceinline__ Q4KMfmaUnit q4k_mfma_load(const uint8_t* tu, uint32_t r, uint32_t lane) {
     Q4KMfmaUnit v;
-    v.hd = ldw128(tu + 16 * r);
-    v.q0 = ldw128(tu + 256 + 16 * lane);
-    v.q1 = ldw128(tu + 1280 + 16 * lane);
+    v.hd = ldw128(tu + 16 * r);  // four lanes per header: cached
+    v.q0 = ldw128_nt(tu + 256 + 16 * lane);
+    v.q1 = ldw128_nt(tu + 1280 + 16 * lane);
     return v;
 }
 
@@ -1136,12 +1142,12 @@ __device__ __forceinline__ float q4k_mfma_unit(const Q4KMfmaUnit& wu, const uint
 // LDS and reads its A slices and (sum, e) pairs from there. Each wave also
 // keeps a zero region that the lanes without A data read instead. No block
 // barrier before the products: a wave starts as soon as its first unit has
-// landed. DEPTH units are in flight per wave.
+// landed.
 // MODE 0: y = W x (+ bias) (+ residual). MODE 1 (the FFN gate/up of one
 // row): w2 is the up matrix in the same form, y = silu(W x) * (W2 x) (the
 // reference's SwiGLU, cpu_llm.cpp:188-202) and yq (nullable) receives the
 // XGroup form of y, one group per 16-row tile (the down projection's input).
-template <int WPB, int DEPTH, int RT, int MODE>
+template <int WPB, int RT, int MODE>
 __global__ __launch_bounds__(64 * WPB) void gemv_q4k_x16_kernel(const uint8_t* __restrict__ w,
                                                                 const uint8_t* __restrict__ w2,
                                                                 const XGroup* __restrict__ xq,
@@ -1165,22 +1171,25 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q4k_x16_kernel(const uint8_t* _
         if (MODE == 1) wt[RT + t] = w2 + min(tile0 + t, tiles - 1) * tile_bytes;
     }
     const uint4* xsrc = reinterpret_cast<const uint4*>(xq);
-    // This wave's units: wave, wave + WPB, ...
-    const uint32_t mine = units > wave ? (units - wave + WPB - 1) / WPB : 0;
+    // This wave's units: wave, wave + WPB, ... (wave-uniform, kept scalar),
+    // counted from a start that rotates with the block: every wave of every
+    // block would otherwise read the same unit's activation groups at the
+    // same moment, from the same few L2 channels.
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t mine = units > wv ? (units - wv + WPB - 1) / WPB : 0;
+    const uint32_t rot = blockIdx.x % units;
     struct Slot {
         uint4 x;
         Q4KMfmaUnit w[NA];
     };
-    Slot ring[DEPTH];
-    auto fill = [&](Slot& sl, uint32_t u) {
+    Slot sl;
+    auto fill = [&](uint32_t idx) {
+        uint32_t u = wv + idx * WPB + rot;
+        if (u >= units) u -= units;
         sl.x = xsrc[64 * u + lane];
 #pragma unroll
         for (int t = 0; t < NA; ++t) sl.w[t] = q4k_mfma_load(wt[t] + static_cast<size_t>(u) * kTileUnitBytes, r, lane);
     };
-#pragma unroll
-    for (int i = 0; i < DEPTH; ++i) {
-        if (static_cast<uint32_t>(i) < mine) fill(ring[i], wave + i * WPB);
-    }
     uint8_t* lds = xs[wave];
     if (lane < kMfmaZeroBytes / 16) *reinterpret_cast<uint4*>(lds + 1024 + 16 * lane) = make_uint4(0, 0, 0, 0);
     const bool a_lane = (r >> 2) == s && (r & 3) < 3;
@@ -1190,21 +1199,19 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q4k_x16_kernel(const uint8_t* _
     float acc[NA];
 #pragma unroll
     for (int t = 0; t < NA; ++t) acc[t] = 0.0f;
-    for (uint32_t base = 0; base < mine; base += DEPTH) {
+    // One unit in flight per wave, refilled as soon as the unit's bytes have
+    // been consumed; the waves of a block, and the blocks of a CU, keep the
+    // memory system busy.
+    if (mine > 0) fill(0);
+    for (uint32_t idx = 0; idx < mine; ++idx) {
+        *reinterpret_cast<uint4*>(lds + 16 * lane) = sl.x;
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int i = 0; i < DEPTH; ++i) {
-            const uint32_t idx = base + i;
-            if (idx < mine) {
-                *reinterpret_cast<uint4*>(lds + 16 * lane) = ring[i].x;
-                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-#pragma unroll
-                for (int t = 0; t < NA; ++t) acc[t] = q4k_mfma_unit(ring[i].w[t], a_src, se_src, s, acc[t]);
-                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                if (idx + DEPTH < mine) fill(ring[i], wave + (idx + DEPTH) * WPB);
-            }
-        }
+        for (int t = 0; t < NA; ++t) acc[t] = q4k_mfma_unit(sl.w[t], a_src, se_src, s, acc[t]);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        if (idx + 1 < mine) fill(idx + 1);
     }
     // Rows: lanes r, r + 16, r + 32, r + 48 hold the four group slices.
 #pragma unroll
@@ -1264,16 +1271,19 @@ __global__ __launch_bounds__(256) void q4k_pack_x16_kernel(const uint8_t* __rest
     *reinterpret_cast<uint4*>(out + c * 16) = v;
 }
 
-// Launch shape code 1000 RT + 100 DEPTH + WPB. Measured on MI355X over
-// 16+ rotated weight copies: tall matrices (>= 1000 tiles, e.g. 3584 ->
-// 18944) run best with 4 waves per block and two units in flight per wave
-// (every wave resident at once); short ones with 8 waves each streaming
-// their units (3584 -> 4608); long rows (>= 32 units, 18944 -> 3584) with 16
-// waves, one unit in flight each. Two tiles per wave measured no faster.
-int q4k_x16_default_waves(uint32_t n, uint32_t units) {
+// Launch shape code 1000 RT + 100 + WPB (one unit in flight per wave).
+// Picked from measurements on MI355X over 16+ rotated weight copies
+// (Qwen2.5-7B and -14B shapes). What decides is how many waves are resident
+// at once and how evenly the blocks fill the 256 CUs: tall matrices of short
+// rows (>= 800 tiles: 3584 -> 18944, 5120 -> 13824) run best with 4 waves per
+// block, all resident in one round, and the SwiGLU pair there with two tiles
+// per block; long rows (>= 32 units) with 16 waves per block while the tiles
+// fit one block per CU (18944 -> 3584), else two tiles per 8-wave block
+// (13824 -> 5120); everything else with 8 waves per block.
+int q4k_x16_default_waves(uint32_t n, uint32_t units, int mode) {
     const uint32_t tiles = (n + 15) / 16;
-    if (tiles >= 1000) return 1204;
-    if (units >= 32) return 1116;
+    if (units >= 32) return tiles <= 256 ? 1116 : 2108;
+    if (tiles >= 800) return mode == 1 ? 2104 : 1104;
     return 1108;
 }
 
@@ -1344,23 +1354,17 @@ int launch_x16(int code, const uint8_t* wp, const uint8_t* wp2, const XGroup* xq
                const float* residual, float* y, XGroup* yq, uint32_t nn, uint32_t units, hipStream_t stream) {
     const uint32_t tiles = (nn + 15) / 16;
     switch (code) {
-#define HIPLLM_X16_CASE(RT, D, W)                                                                                   \
-    case 1000 * RT + 100 * D + W:                                                                                   \
-        HIPLLM_LAUNCH((gemv_q4k_x16_kernel<W, D, RT, MODE>), dim3((tiles + RT - 1) / RT), dim3(64 * W), 0, stream, wp, \
-                      wp2, xq, bias, residual, y, yq, nn, units);                                                   \
+#define HIPLLM_X16_CASE(RT, W)                                                                                      \
+    case 1000 * RT + 100 + W:                                                                                       \
+        HIPLLM_LAUNCH((gemv_q4k_x16_kernel<W, RT, MODE>), dim3((tiles + RT - 1) / RT), dim3(64 * W), 0, stream, wp, wp2, \
+                      xq, bias, residual, y, yq, nn, units);                                                        \
         break;
-        HIPLLM_X16_CASE(1, 1, 4)
-        HIPLLM_X16_CASE(1, 2, 4)
-        HIPLLM_X16_CASE(1, 4, 4)
-        HIPLLM_X16_CASE(1, 1, 8)
-        HIPLLM_X16_CASE(1, 2, 8)
-        HIPLLM_X16_CASE(1, 1, 16)
-        HIPLLM_X16_CASE(1, 2, 16)
-        HIPLLM_X16_CASE(2, 1, 4)
-        HIPLLM_X16_CASE(2, 2, 4)
-        HIPLLM_X16_CASE(2, 1, 8)
-        HIPLLM_X16_CASE(2, 2, 8)
-        HIPLLM_X16_CASE(2, 1, 16)
+        HIPLLM_X16_CASE(1, 4)
+        HIPLLM_X16_CASE(1, 8)
+        HIPLLM_X16_CASE(1, 16)
+        HIPLLM_X16_CASE(2, 4)
+        HIPLLM_X16_CASE(2, 8)
+        HIPLLM_X16_CASE(2, 16)
 #undef HIPLLM_X16_CASE
     default:
         return kInvalidArgument;
@@ -1383,7 +1387,7 @@ int launch_gemv_q4k_x16(const void* packed, const XGroup* xq, const float* bias,
     const int rc = check_x16(packed, xq, y, n, k);
     if (rc != kOk) return rc;
     const uint32_t units = static_cast<uint32_t>(k / 256), nn = static_cast<uint32_t>(n);
-    return launch_x16<0>(waves ? waves : q4k_x16_default_waves(nn, units), static_cast<const uint8_t*>(packed),
+    return launch_x16<0>(waves ? waves : q4k_x16_default_waves(nn, units, 0), static_cast<const uint8_t*>(packed),
                          nullptr, xq, bias, residual, y, nullptr, nn, units, stream);
 }
 
@@ -1394,7 +1398,7 @@ int launch_gemv_q4k_x16_swiglu(const void* gate, const void* up, const XGroup* x
     if (rc != kOk) return rc;
     if (yq && (n % 16 != 0 || reinterpret_cast<uintptr_t>(yq) % 16 != 0)) return kInvalidArgument;
     const uint32_t units = static_cast<uint32_t>(k / 256), nn = static_cast<uint32_t>(n);
-    return launch_x16<1>(waves ? waves : q4k_x16_default_waves(nn, units), static_cast<const uint8_t*>(gate),
+    return launch_x16<1>(waves ? waves : q4k_x16_default_waves(nn, units, 1), static_cast<const uint8_t*>(gate),
                          static_cast<const uint8_t*>(up), xq, nullptr, nullptr, y, yq, nn, units, stream);
 }
 

@@ -25,7 +25,7 @@ from tests.test_gpu_kernels import dev_bytes, random_rows, rel_err
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
-SHAPES = [1104, 1204, 1404, 1108, 1208, 1116, 1216, 2104, 2204, 2108, 2208, 2116]
+SHAPES = [1104, 1108, 1116, 2104, 2108, 2116]
 
 
 def pack_ref(w: np.ndarray, n: int, k: int) -> np.ndarray:
@@ -149,7 +149,7 @@ def silu_mul_ref(g, u):
 
 
 @pytest.mark.parametrize("n,k,waves", [(16, 256, 0), (64, 512, 1108), (1040, 3584, 0), (4864, 1024, 0),
-                                       (320, 2048, 2204), (48, 18944, 1116)])
+                                       (320, 2048, 2104), (48, 18944, 1116)])
 def test_gemv_x16_swiglu(cuda, n, k, waves):
     wg = random_rows(synth.Q4_K, n, k, n + 1)
     wu = random_rows(synth.Q4_K, n, k, n + 2)
