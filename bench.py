@@ -74,8 +74,8 @@ class Rotation:
     at least 16 copies and 3x the 256 MB Infinity Cache, so that a matrix
     timed alone is also read from HBM every time (its 15 other copies, over
     570 MB for the gate, pass through the cache between two reads of it).
-    packed: also hold each Q4_K copy in the x16 tile-packed form that the
-    MFMA GEMV reads (same byte count)."""
+    packed: also hold each Q4_K / Q6_K copy in the x16 tile-packed form that
+    the MFMA GEMV reads (same byte count)."""
 
     def __init__(self, qtype, torch, cuda, min_bytes=3 * MALL_BYTES, packed=False):
         from myllm_amd import synth
@@ -95,8 +95,8 @@ class Rotation:
                 buf[: src.nbytes].copy_(torch.from_numpy(src.reshape(-1)))
                 layer[name] = buf
                 if packed:
-                    pk = torch.empty(kernels.q4k_x16_bytes(n, k), dtype=torch.uint8, device=cuda)
-                    kernels.q4k_pack_x16(buf, src.shape[1], n, k, pk)
+                    pk = torch.empty(kernels.x16_bytes(qtype, n, k), dtype=torch.uint8, device=cuda)
+                    kernels.pack_x16(qtype, buf, src.shape[1], n, k, pk)
                     player[name] = pk
             self.layers.append(layer)
             self.packed.append(player)
@@ -107,7 +107,7 @@ class Rotation:
 
 
 def gemv_setup(qtype, torch, cuda, packed=False):
-    """packed (Q4_K only): launch the MFMA GEMV on the x16-packed copies
+    """packed (Q4_K / Q6_K): launch the MFMA GEMV on the x16-packed copies
     instead of the vector GEMV on the GGUF rows."""
     from myllm_amd import synth
     from myllm_amd.hipllm import kernels
@@ -121,7 +121,7 @@ def gemv_setup(qtype, torch, cuda, packed=False):
 
     def launch(c, name, n, k, stream=None):
         if packed:
-            kernels.gemv_q4k_x16(rot.packed[c][name], xq[k], None, None, ys[name], n, k, 0, stream=stream)
+            kernels.gemv_x16(qtype, rot.packed[c][name], xq[k], None, None, ys[name], n, k, 0, stream=stream)
         else:
             kernels.gemv_prepped(qtype, rot.layers[c][name], rot.row_bytes(n, k), xs[k], xq[k], None, None,
                                  ys[name], n, k, 0, stream=stream)
@@ -505,9 +505,12 @@ def main():
     log("[bench] Q4_K GEMV (GGUF rows, vector ALU)")
     q4n = bench_gemv(synth.Q4_K, args.steps, args.warmup, torch, cuda)
     log(f"[bench] Q4_K GGUF rows {q4n['gbps']:.1f} GB/s")
-    log("[bench] Q6_K GEMV")
-    q6 = bench_gemv(synth.Q6_K, args.steps, args.warmup, torch, cuda)
-    log(f"[bench] Q6_K {q6['gbps']:.1f} GB/s")
+    log("[bench] Q6_K GEMV (x16-packed weights, int8 MFMA)")
+    q6 = bench_gemv(synth.Q6_K, args.steps, args.warmup, torch, cuda, packed=True)
+    log(f"[bench] Q6_K x16 {q6['gbps']:.1f} GB/s")
+    log("[bench] Q6_K GEMV (GGUF rows, vector ALU)")
+    q6n = bench_gemv(synth.Q6_K, args.steps, args.warmup, torch, cuda)
+    log(f"[bench] Q6_K GGUF rows {q6n['gbps']:.1f} GB/s")
     copy = bench_copy(torch, cuda, q4["kernels"]["gate"]["bytes"] // 256 * 256)
     log(f"[bench] plain copy of the gate GEMV's bytes: {copy['avg_us']:.2f} us")
     log("[bench] prefill GEMM")
@@ -571,9 +574,12 @@ def main():
                  "q4_k_gguf_rows": {"step_gbps": round(q4n["gbps"], 2), "weights": "GGUF rows, vector ALU",
                                     "kernels": {k: {"gbps": round(v["gbps"], 1), "avg_us": round(v["avg_us"], 2)}
                                                 for k, v in q4n["kernels"].items()}},
-                 "q6_k": {"step_gbps": round(q6["gbps"], 2),
+                 "q6_k": {"step_gbps": round(q6["gbps"], 2), "weights": "x16 tile-packed, int8 MFMA",
                           "kernels": {k: {"gbps": round(v["gbps"], 1), "avg_us": round(v["avg_us"], 2)}
-                                      for k, v in q6["kernels"].items()}}},
+                                      for k, v in q6["kernels"].items()}},
+                 "q6_k_gguf_rows": {"step_gbps": round(q6n["gbps"], 2), "weights": "GGUF rows, vector ALU",
+                                    "kernels": {k: {"gbps": round(v["gbps"], 1), "avg_us": round(v["avg_us"], 2)}
+                                                for k, v in q6n["kernels"].items()}}},
         "prefill_gemm": {"weights": "Q4_K", "k": 3584, "n": 18944, "by_m": gemm},
         "e2e": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                 for k, v in e2e.items()},

@@ -95,38 +95,41 @@ int hipllm_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const fl
                         const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
                         void* stream);
 
-/* The x16 tile-packed form of Q4_K weights, a device-side layout of this
- * backend (no counterpart in GGUF or the reference): rows in tiles of 16 (a
- * partial last tile zero-padded), tile-units of 2304 contiguous bytes (the
- * 16 rows' super-block headers, then their quant bytes in the order the
- * GEMV's lanes read them). hipllm_q4k_x16_bytes: its size for n rows of k
- * values (k % 256 == 0; 0 otherwise). hipllm_q4k_pack_x16 writes it from
- * native rows (16-byte aligned buffers, row_bytes % 16 == 0). */
-size_t hipllm_q4k_x16_bytes(size_t n, size_t k);
-int hipllm_q4k_pack_x16(const void* w, size_t row_bytes, size_t n, size_t k, void* packed, void* stream);
+/* The x16 tile-packed form of Q4_K and Q6_K weights (type 12 / 14), a
+ * device-side layout of this backend (no counterpart in GGUF or the
+ * reference): rows in tiles of 16 (a partial last tile zero-padded), one
+ * tile-unit of 16 * 144 (Q4_K) or 16 * 210 (Q6_K) contiguous bytes per
+ * 256-value super-block column: the 16 rows' blocks, byte for byte, ordered
+ * the way the GEMV's lanes read them. hipllm_x16_bytes: its size for n rows
+ * of k values (k % 256 == 0; 0 otherwise or for other types).
+ * hipllm_pack_x16 writes it from native rows (packed 16-byte aligned; Q4_K
+ * rows 16-byte, Q6_K rows 2-byte aligned). */
+size_t hipllm_x16_bytes(uint32_t type, size_t n, size_t k);
+int hipllm_pack_x16(uint32_t type, const void* w, size_t row_bytes, size_t n, size_t k, void* packed, void* stream);
 
-/* Decode GEMV y = W x (+ bias) (+ residual) over x16-packed Q4_K weights,
- * with the integer products of the XGroup digits on the int8 matrix cores
- * (v_mfma_i32_16x16x64_i8); xq as for hipllm_gemv_prepped. Same arithmetic
- * as the vector path (exact integer digit sums, FP32 scaling per 16-group),
- * results equal to it within FP32 rounding of the summation order.
+/* Decode GEMV y = W x (+ bias) (+ residual) over x16-packed Q4_K or Q6_K
+ * weights, with the integer products of the XGroup digits on the int8
+ * matrix cores (v_mfma_i32_16x16x64_i8); xq as for hipllm_gemv_prepped.
+ * Same arithmetic as the vector path (exact integer digit sums, FP32 scaling
+ * per 16-group; Q6_K's three digit sums combined in FP32), results equal to
+ * it within FP32 rounding.
  * `waves`: 0 picks the launch shape, else 1000 RT + 100 + W: W waves
  * per block (4, 8, 16) sharing RT 16-row tiles (1, 2), one unit in flight
  * per wave: 1104, 1108, 1116, 2104, 2108, 2116.
- * Replaces metal_gevm_q4_k_f32 via encode_vector_product
- * (metal_llm.metal:708-781; metal_llm.mm:1891-1999) and gevmt for Q4_K rows
- * (cpu_llm.cpp:512-547). */
-int hipllm_gemv_q4k_x16(const void* packed, const void* xq, const float* bias, const float* residual, float* y,
-                        size_t n, size_t k, int waves, void* stream);
+ * Replaces metal_gevm_q4_k_f32 / metal_gevm_q6_k_f32 via
+ * encode_vector_product (metal_llm.metal:708-781; metal_llm.mm:1891-1999)
+ * and gevmt for Q4_K / Q6_K rows (cpu_llm.cpp:512-547). */
+int hipllm_gemv_x16(uint32_t type, const void* packed, const void* xq, const float* bias, const float* residual,
+                    float* y, size_t n, size_t k, int waves, void* stream);
 
-/* The FFN gate/up pair over x16-packed Q4_K weights in one launch:
+/* The FFN gate/up pair over x16-packed weights of one type in one launch:
  * y = silu(Wg x) * (Wu x) (the sign-branched SiLU of cpu_llm.cpp:188-202),
  * and yq (nullable; n % 16 == 0) its XGroup form for the down projection.
- * Same launch shapes as hipllm_gemv_q4k_x16. Replaces the gate / up GEVMs
- * and SwiGLU of encode_decode_layer (metal_llm.mm:2850-2890;
- * metal_llm.metal:708-781) for Q4_K weights. */
-int hipllm_gemv_q4k_x16_swiglu(const void* gate, const void* up, const void* xq, float* y, void* yq, size_t n,
-                               size_t k, int waves, void* stream);
+ * Same launch shapes as hipllm_gemv_x16. Replaces the gate / up GEVMs and
+ * SwiGLU of encode_decode_layer (metal_llm.mm:2850-2890;
+ * metal_llm.metal:708-781). */
+int hipllm_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, const void* xq, float* y, void* yq,
+                           size_t n, size_t k, int waves, void* stream);
 
 /* hipllm_rmsnorm of the raw row x (gain gamma, k <= 8192, x and gamma
  * 16-byte aligned) followed by hipllm_gemv_prepped, in one launch: every
@@ -562,9 +565,10 @@ int hipllm_set_batched_prefill(HipllmModel* model, int enabled);
  * moe_llm.mm:3051-3141); no counterpart switch exists there. */
 int hipllm_set_decode_graphs(HipllmModel* model, int enabled);
 /* qwen2 only: 1 (default when the model has such projections) = the decode
- * GEMVs of Q4_K projections (fused QKV, attention output, FFN gate / up) run
- * on x16 tile-packed copies made at load time (hipllm_gemv_q4k_x16; the
- * copies count in memory_stats' weight_bytes), 0 = on the GGUF rows.
+ * GEMVs of Q4_K and Q6_K projections (fused QKV, attention output, FFN
+ * gate / up and down, LM head) run on x16 tile-packed copies made at load
+ * time (hipllm_gemv_x16; the copies count in memory_stats' weight_bytes),
+ * 0 = on the GGUF rows.
  * HIPLLM_INVALID_ARGUMENT when the model has nothing to pack or is not
  * qwen2. No counterpart in the reference (a layout of this backend). */
 int hipllm_set_packed_decode(HipllmModel* model, int enabled);

@@ -1024,60 +1024,58 @@ int gemv_pick_shape(uint32_t type, uint32_t n, uint32_t units, int mode) {
     return 100 * R + OPR;
 }
 
-// ------------------------------------------------------------ Q4_K on MFMA
+// ------------------------------------------------- Q4_K and Q6_K on MFMA
 //
-// The decode GEMV of Q4_K weights held in the x16 tile-packed form, with its
-// integer products on the matrix cores (v_mfma_i32_16x16x64_i8).
+// The decode GEMV of Q4_K and Q6_K weights held in the x16 tile-packed form,
+// with its integer products on the matrix cores (v_mfma_i32_16x16x64_i8).
 //
 // Packed form: rows in tiles of 16 (a partial last tile is zero-padded);
-// tile T, unit (super-block) u takes 2304 contiguous bytes at
-// (T * units + u) * 2304: the 16 rows' 16-byte headers (d, dmin,
-// scales[12]), then for lane l = 16 s + r the quant bytes [16 s, 16 s + 16)
-// of row r (at 256 + 16 l), then its bytes [64 + 16 s, 64 + 16 s + 16) (at
-// 1280 + 16 l). A wave reads each tile-unit as three fully contiguous
-// loads; in the GGUF row order the same wave touches 16 rows 2 KiB apart,
-// which measured 1.5x slower as a pure read on MI355X.
+// tile T, unit (256-value super-block) u takes 16 * B contiguous bytes at
+// (T * units + u) * 16 B (B = 144 for Q4_K, 210 for Q6_K): the same bytes as
+// the 16 GGUF rows' blocks, ordered so that a wave reads each tile-unit as
+// fully contiguous 1 KiB loads (lane l = 16 s + r: row r, k-slice s). In the
+// GGUF row order the same wave touches 16 rows kilobytes apart, which
+// measured 1.5x slower as a pure read on MI355X.
+// * Q4_K (2304 bytes): the 16 rows' 16-byte headers (d, dmin, scales[12]);
+//   at 256 + 16 l the quant bytes [16 s, 16 s + 16) of row r; at 1280 + 16 l
+//   its bytes [64 + 16 s, 64 + 16 s + 16).
+// * Q6_K (3360 bytes), with ql = bytes 0..127, qh = 128..191 of a row's
+//   block: at 16 l, ql[64 (s >> 1) + 16 (s & 1), +16); at 1024 + 16 l,
+//   ql[64 (s >> 1) + 32 + 16 (s & 1), +16); at 2048 + 16 l,
+//   qh[32 (s >> 1) + 16 (s & 1), +16); at 3072 + 16 r the row's 16 scale
+//   bytes; at 3328 + 2 r its d.
 //
 // Product: a wave owns one 16-row tile (the MFMA's N); lane l holds row
-// r = l % 16 and k-slice s = l / 16 of each 64-value product.
-// * The low nibbles of a lane's first 16 bytes feed MFMA (0, 0), their high
-//   nibbles MFMA (0, 1), the second 16 bytes MFMAs (1, 0), (1, 1). Slice s
-//   of MFMA (p, h) is the activation 16-group 8 p + 4 (s >> 1) + 2 h +
-//   (s & 1) of the unit, in sub-block 4 p + 2 (s >> 1) + h (model.cpp:616-644
-//   places low nibbles of bytes 32 j .. 32 j + 31 at elements 64 j .., the
-//   high nibbles 32 elements later).
+// r = l % 16 and k-slice s = l / 16 of each 64-value product, and each MFMA
+// sums 16 values of one 16-value activation group per slice.
+// * Q4_K: the low nibbles of a lane's first 16 bytes feed MFMA 0, their high
+//   nibbles MFMA 1, the second 16 bytes MFMAs 2, 3. Slice s of MFMA i is the
+//   group 8 (i >> 1) + 4 (s >> 1) + 2 (i & 1) + (s & 1) of the unit, in
+//   sub-block 4 (i >> 1) + 2 (s >> 1) + (i & 1) (model.cpp:616-644 places
+//   low nibbles of bytes 32 j .. 32 j + 31 at elements 64 j .., the high
+//   nibbles 32 elements later).
+// * Q6_K: MFMA i takes quarter i of each 128-value half (model.cpp:646-683:
+//   value l + 32 i of half h is ql[64 h + l + 32 (i & 1)]'s nibble i >> 1
+//   with bits 2 i, 2 i + 1 of qh[32 h + l] above it); slice s of MFMA i is
+//   the group 8 (s >> 1) + 2 i + (s & 1), scaled by scale byte of the same
+//   index. The 6-bit quant q enters the MFMA as it is; the -32 is applied
+//   with the group's FP32 sum.
 // * A's 16 rows are (group slice g, digit d): row 4 g + d holds digit d of
 //   the XGroup of slice g at k-slice g and zeros elsewhere (d = 3: zero). C
 //   row 4 g + d, column r is then the sum over the group's 16 values of
 //   q * digit d, so lane l receives digits 0..2 of its own slice's group for
-//   its row: t = c0 + 256 c1 + 65536 c2 = sum q * x_int exactly (|t| <=
-//   16 * 15 * 8355711 < 2^31).
+//   its row. Q4_K combines them exactly in int32, t = c0 + 256 c1 + 65536 c2
+//   (|t| <= 16 * 15 * 8355711 < 2^31); Q6_K's 6-bit quants would overflow
+//   that, so its three (exact) digit sums are combined in FP32.
 // * Each wave stages the 16 XGroups of its current unit in LDS, beside a
 //   zero region: the 12 lanes with (l % 16) / 4 == l / 16, (l % 16) % 4 < 3
 //   read their A slice from the groups, the others read zeros, with no
 //   branch.
-// * Each lane adds t e d sc - dmin m sum (the group's scale e and FP32 sum,
-//   the row's super-block scales) into one FP32 accumulator; the waves of a
-//   block split the units round-robin and are summed in wave order, the four
-//   lanes of a row by two xor shuffles: deterministic.
-// * The quant bytes, headers and x bytes of one or two units are in flight
-//   per wave (a ring refilled as units are consumed).
+// * Each lane adds its groups' scaled sums into one FP32 accumulator; the
+//   waves of a block split the units round-robin and are summed in wave
+//   order, the four lanes of a row by two xor shuffles: deterministic.
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-constexpr uint32_t kTileUnitBytes = 16 * 144;
 constexpr uint32_t kMfmaZeroBytes = 672;  // covers the A reads at offsets 0..655 (+16 bytes)
-
-struct Q4KMfmaUnit {
-    uint4 hd;      // this lane's row header
-    uint4 q0, q1;  // quant bytes 16 s .. and 64 + 16 s ..
-};
-
-__device__ __forceinline__ Q4KMfmaUnit q4k_mfma_load(const uint8_t* tu, uint32_t r, uint32_t lane) {
-    Q4KMfmaUnit v;
-    v.hd = ldw128(tu + 16 * r);  // four lanes per header: cached
-    v.q0 = ldw128_nt(tu + 256 + 16 * lane);
-    v.q1 = ldw128_nt(tu + 1280 + 16 * lane);
-    return v;
-}
 
 __device__ __forceinline__ i32x4 nibbles(const uint4& q, bool high) {
     i32x4 b;
@@ -1095,66 +1093,148 @@ __device__ __forceinline__ i32x4 nibbles(const uint4& q, bool high) {
     return b;
 }
 
-// One unit of a lane: four MFMAs, each followed by its group's scaling.
-// a_src: LDS bytes of this lane's A slice for MFMA (0, 0) (the zero region
-// for lanes without A data); se_src: the (sum, e) pair of its slice's group
-// for MFMA (0, 0). MFMA (p, h) is 512 p + 128 h bytes further on for both.
-__device__ __forceinline__ float q4k_mfma_unit(const Q4KMfmaUnit& wu, const uint8_t* a_src, const uint8_t* se_src,
-                                               uint32_t s, float acc) {
-    const uint32_t h0 = wu.hd.x, h1 = wu.hd.y, h2 = wu.hd.z, h3 = wu.hd.w;
-    const float d = half_lo(h0), dmin = half_hi(h0);
-    // 6-bit scale / min bytes of sub-blocks 0..3 (lo) and 4..7 (hi)
-    // (get_scale_min_k4, model.cpp:524-537), shifted to this lane's pair.
-    const uint32_t sh = (s >> 1) * 16;
-    const uint32_t slo = (h1 & 0x3f3f3f3fu) >> sh, mlo = (h2 & 0x3f3f3f3fu) >> sh;
-    const uint32_t shi = ((h3 & 0x0f0f0f0fu) | ((h1 >> 2) & 0x30303030u)) >> sh;
-    const uint32_t mhi = (((h3 >> 4) & 0x0f0f0f0fu) | ((h2 >> 2) & 0x30303030u)) >> sh;
-    i32x4 a[4];
-    float2 se[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t off = 512 * (i >> 1) + 128 * (i & 1);
-        a[i] = *reinterpret_cast<const i32x4*>(a_src + off);
-        se[i] = *reinterpret_cast<const float2*>(se_src + off);
-    }
-    const i32x4 zero = {0, 0, 0, 0};
-    float sum_t = 0.0f, sum_m = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int p = i >> 1, h = i & 1;
-        const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], nibbles(p ? wu.q1 : wu.q0, h != 0), zero, 0, 0, 0);
-        const int t = c.x + (c.y << 8) + (c.z << 16);
-        const uint32_t sc = p ? shi : slo, mn = p ? mhi : mlo;
-        const float scale = h ? ubyte1(sc) : ubyte0(sc);
-        const float mins = h ? ubyte1(mn) : ubyte0(mn);
-        sum_t = fmaf(static_cast<float>(t), se[i].y * scale, sum_t);
-        sum_m = fmaf(mins, se[i].x, sum_m);
-    }
-    return fmaf(d, sum_t, fmaf(-dmin, sum_m, acc));
-}
+template <uint32_t QT>
+struct X16;
 
-// y = W x (+ bias) (+ residual) for x16-packed Q4_K W. A block of WPB waves
-// owns RT consecutive 16-row tiles; its waves split the units round-robin
-// and each wave multiplies every unit it takes into all RT tiles, so one
-// copy of the unit's activation groups serves 16 RT rows. Per unit a lane
-// loads 16 bytes of x's XGroups (the unit's 16 groups are 1 KiB, one load per
-// lane) with the unit's weights; the wave stores them to its own 1 KiB of
-// LDS and reads its A slices and (sum, e) pairs from there. Each wave also
-// keeps a zero region that the lanes without A data read instead. No block
-// barrier before the products: a wave starts as soon as its first unit has
-// landed.
+template <>
+struct X16<kQ4_K> {
+    static constexpr uint32_t kBlock = 144;
+    struct Unit {
+        uint4 hd;      // this lane's row header
+        uint4 q0, q1;  // quant bytes 16 s .. and 64 + 16 s ..
+    };
+    __device__ static Unit load(const uint8_t* tu, uint32_t r, uint32_t, uint32_t lane) {
+        Unit v;
+        v.hd = ldw128(tu + 16 * r);  // four lanes per header: cached
+        v.q0 = ldw128_nt(tu + 256 + 16 * lane);
+        v.q1 = ldw128_nt(tu + 1280 + 16 * lane);
+        return v;
+    }
+    // LDS byte offset of slice s's group in MFMA 0 (MFMA i adds group_step(i)).
+    __device__ static uint32_t group_base(uint32_t s) { return 64 * (4 * (s >> 1) + (s & 1)); }
+    static constexpr uint32_t group_step(int i) { return 512 * (i >> 1) + 128 * (i & 1); }
+    // One unit of a lane: four MFMAs, each followed by its group's scaling.
+    // a_src: LDS bytes of this lane's A slice for MFMA 0 (the zero region
+    // for lanes without A data); se_src: the (sum, e) pair of its slice's
+    // group for MFMA 0.
+    __device__ static float unit(const Unit& wu, const uint8_t* a_src, const uint8_t* se_src, uint32_t, uint32_t s,
+                                 float acc) {
+        const uint32_t h0 = wu.hd.x, h1 = wu.hd.y, h2 = wu.hd.z, h3 = wu.hd.w;
+        const float d = half_lo(h0), dmin = half_hi(h0);
+        // 6-bit scale / min bytes of sub-blocks 0..3 (lo) and 4..7 (hi)
+        // (get_scale_min_k4, model.cpp:524-537), shifted to this lane's pair.
+        const uint32_t sh = (s >> 1) * 16;
+        const uint32_t slo = (h1 & 0x3f3f3f3fu) >> sh, mlo = (h2 & 0x3f3f3f3fu) >> sh;
+        const uint32_t shi = ((h3 & 0x0f0f0f0fu) | ((h1 >> 2) & 0x30303030u)) >> sh;
+        const uint32_t mhi = (((h3 >> 4) & 0x0f0f0f0fu) | ((h2 >> 2) & 0x30303030u)) >> sh;
+        i32x4 a[4];
+        float2 se[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            a[i] = *reinterpret_cast<const i32x4*>(a_src + group_step(i));
+            se[i] = *reinterpret_cast<const float2*>(se_src + group_step(i));
+        }
+        const i32x4 zero = {0, 0, 0, 0};
+        float sum_t = 0.0f, sum_m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int p = i >> 1, h = i & 1;
+            const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], nibbles(p ? wu.q1 : wu.q0, h != 0), zero, 0, 0, 0);
+            const int t = c.x + (c.y << 8) + (c.z << 16);
+            const uint32_t sc = p ? shi : slo, mn = p ? mhi : mlo;
+            const float scale = h ? ubyte1(sc) : ubyte0(sc);
+            const float mins = h ? ubyte1(mn) : ubyte0(mn);
+            sum_t = fmaf(static_cast<float>(t), se[i].y * scale, sum_t);
+            sum_m = fmaf(mins, se[i].x, sum_m);
+        }
+        return fmaf(d, sum_t, fmaf(-dmin, sum_m, acc));
+    }
+};
+
+template <>
+struct X16<kQ6_K> {
+    static constexpr uint32_t kBlock = 210;
+    struct Unit {
+        uint4 qa, qb, qh;  // ql[64 h + 16 (s & 1) ..], ql[64 h + 32 + ..], qh[32 h + 16 (s & 1) ..]
+        uint2 sc;          // scale bytes 8 (s >> 1) .. 8 (s >> 1) + 7 of the row
+        uint32_t d;        // the f16 d of rows r & ~1, r | 1
+    };
+    __device__ static Unit load(const uint8_t* tu, uint32_t r, uint32_t s, uint32_t lane) {
+        Unit v;
+        v.qa = ldw128_nt(tu + 16 * lane);
+        v.qb = ldw128_nt(tu + 1024 + 16 * lane);
+        v.qh = ldw128_nt(tu + 2048 + 16 * lane);
+        v.sc = *reinterpret_cast<const uint2*>(tu + 3072 + 16 * r + 8 * (s >> 1));
+        v.d = ldw32(tu + 3328 + 4 * (r >> 1));
+        return v;
+    }
+    __device__ static uint32_t group_base(uint32_t s) { return 64 * (8 * (s >> 1) + (s & 1)); }
+    static constexpr uint32_t group_step(int i) { return 128 * i; }
+    // Bytes of MFMA i's B operand: the low (i < 2) or high nibbles of qa / qb
+    // (i even / odd) with qh's bits 2 i, 2 i + 1 at bits 4, 5.
+    __device__ static uint32_t quant6(uint32_t lo, uint32_t hi, int i) {
+        const uint32_t l = (i >> 1) ? (lo >> 4) & 0x0f0f0f0fu : lo & 0x0f0f0f0fu;
+        const uint32_t h = i == 0 ? hi << 4 : i == 1 ? hi << 2 : i == 2 ? hi : hi >> 2;
+        return (h & 0x30303030u) | l;
+    }
+    __device__ static float unit(const Unit& wu, const uint8_t* a_src, const uint8_t* se_src, uint32_t r, uint32_t s,
+                                 float acc) {
+        const float d = (r & 1) ? half_hi(wu.d) : half_lo(wu.d);
+        i32x4 a[4];
+        float2 se[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            a[i] = *reinterpret_cast<const i32x4*>(a_src + group_step(i));
+            se[i] = *reinterpret_cast<const float2*>(se_src + group_step(i));
+        }
+        const i32x4 zero = {0, 0, 0, 0};
+        const uint32_t sb = 8 * (s & 1);  // this lane's scale byte within each byte pair
+        float sum_t = 0.0f, sum_m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint4& lo = (i & 1) ? wu.qb : wu.qa;
+            i32x4 b;
+            b.x = static_cast<int>(quant6(lo.x, wu.qh.x, i));
+            b.y = static_cast<int>(quant6(lo.y, wu.qh.y, i));
+            b.z = static_cast<int>(quant6(lo.z, wu.qh.z, i));
+            b.w = static_cast<int>(quant6(lo.w, wu.qh.w, i));
+            const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b, zero, 0, 0, 0);
+            const float t = fmaf(65536.0f, static_cast<float>(c.z),
+                                 fmaf(256.0f, static_cast<float>(c.y), static_cast<float>(c.x)));
+            // Scale byte (s & 1) + 2 i of this lane's eight (signed).
+            const uint32_t word = (i >> 1) ? wu.sc.y : wu.sc.x;
+            const float scale = static_cast<float>(static_cast<int8_t>(word >> (sb + 16 * (i & 1))));
+            sum_t = fmaf(t, se[i].y * scale, sum_t);
+            sum_m = fmaf(scale, se[i].x, sum_m);
+        }
+        return fmaf(d, fmaf(-32.0f, sum_m, sum_t), acc);
+    }
+};
+
+// y = W x (+ bias) (+ residual) for x16-packed W of type QT. A block of WPB
+// waves owns RT consecutive 16-row tiles; its waves split the units
+// round-robin and each wave multiplies every unit it takes into all RT
+// tiles, so one copy of the unit's activation groups serves 16 RT rows. Per
+// unit a lane loads 16 bytes of x's XGroups (the unit's 16 groups are 1 KiB,
+// one load per lane) with the unit's weights; the wave stores them to its
+// own 1 KiB of LDS and reads its A slices and (sum, e) pairs from there. Each
+// wave also keeps a zero region that the lanes without A data read instead.
+// No block barrier before the products: a wave starts as soon as its first
+// unit has landed.
 // MODE 0: y = W x (+ bias) (+ residual). MODE 1 (the FFN gate/up of one
 // row): w2 is the up matrix in the same form, y = silu(W x) * (W2 x) (the
 // reference's SwiGLU, cpu_llm.cpp:188-202) and yq (nullable) receives the
 // XGroup form of y, one group per 16-row tile (the down projection's input).
-template <int WPB, int RT, int MODE>
-__global__ __launch_bounds__(64 * WPB) void gemv_q4k_x16_kernel(const uint8_t* __restrict__ w,
-                                                                const uint8_t* __restrict__ w2,
-                                                                const XGroup* __restrict__ xq,
-                                                                const float* __restrict__ bias,
-                                                                const float* __restrict__ residual,
-                                                                float* __restrict__ y, XGroup* __restrict__ yq,
-                                                                uint32_t n, uint32_t units) {
+template <uint32_t QT, int WPB, int RT, int MODE>
+__global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __restrict__ w,
+                                                            const uint8_t* __restrict__ w2,
+                                                            const XGroup* __restrict__ xq,
+                                                            const float* __restrict__ bias,
+                                                            const float* __restrict__ residual,
+                                                            float* __restrict__ y, XGroup* __restrict__ yq,
+                                                            uint32_t n, uint32_t units) {
+    using F = X16<QT>;
+    constexpr uint32_t kTileUnit = 16 * F::kBlock;
     constexpr int NM = MODE == 1 ? 2 : 1;  // matrices
     constexpr int NA = NM * RT;            // accumulators
     __shared__ __align__(16) uint8_t xs[WPB][2048];
@@ -1163,7 +1243,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q4k_x16_kernel(const uint8_t* _
     const uint32_t r = lane & 15, s = lane >> 4;
     const uint32_t tiles = (n + 15) / 16;
     const uint32_t tile0 = blockIdx.x * RT;
-    const size_t tile_bytes = static_cast<size_t>(units) * kTileUnitBytes;
+    const size_t tile_bytes = static_cast<size_t>(units) * kTileUnit;
     const uint8_t* wt[NA];
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
@@ -1180,7 +1260,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q4k_x16_kernel(const uint8_t* _
     const uint32_t rot = blockIdx.x % units;
     struct Slot {
         uint4 x;
-        Q4KMfmaUnit w[NA];
+        typename F::Unit w[NA];
     };
     Slot sl;
     auto fill = [&](uint32_t idx) {
@@ -1188,12 +1268,12 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q4k_x16_kernel(const uint8_t* _
         if (u >= units) u -= units;
         sl.x = xsrc[64 * u + lane];
 #pragma unroll
-        for (int t = 0; t < NA; ++t) sl.w[t] = q4k_mfma_load(wt[t] + static_cast<size_t>(u) * kTileUnitBytes, r, lane);
+        for (int t = 0; t < NA; ++t) sl.w[t] = F::load(wt[t] + static_cast<size_t>(u) * kTileUnit, r, s, lane);
     };
     uint8_t* lds = xs[wave];
     if (lane < kMfmaZeroBytes / 16) *reinterpret_cast<uint4*>(lds + 1024 + 16 * lane) = make_uint4(0, 0, 0, 0);
     const bool a_lane = (r >> 2) == s && (r & 3) < 3;
-    const uint32_t slot = 64 * (4 * (s >> 1) + (s & 1));  // group of slice s in MFMA (0, 0), bytes
+    const uint32_t slot = F::group_base(s);
     const uint8_t* a_src = a_lane ? lds + slot + 16 * (r & 3) : lds + 1024;
     const uint8_t* se_src = lds + slot + 48;
     float acc[NA];
@@ -1201,14 +1281,16 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q4k_x16_kernel(const uint8_t* _
     for (int t = 0; t < NA; ++t) acc[t] = 0.0f;
     // One unit in flight per wave, refilled as soon as the unit's bytes have
     // been consumed; the waves of a block, and the blocks of a CU, keep the
-    // memory system busy.
+    // memory system busy. (With two units in flight the refill of the second
+    // sits under a branch that the last pass skips, and the compiler's waits
+    // then cover every load in flight.)
     if (mine > 0) fill(0);
     for (uint32_t idx = 0; idx < mine; ++idx) {
         *reinterpret_cast<uint4*>(lds + 16 * lane) = sl.x;
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int t = 0; t < NA; ++t) acc[t] = q4k_mfma_unit(sl.w[t], a_src, se_src, s, acc[t]);
+        for (int t = 0; t < NA; ++t) acc[t] = F::unit(sl.w[t], a_src, se_src, r, s, acc[t]);
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
         if (idx + 1 < mine) fill(idx + 1);
@@ -1245,29 +1327,58 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q4k_x16_kernel(const uint8_t* _
     }
 }
 
-// Repacking: one thread per 16-byte chunk of the packed form (144 chunks per
-// tile-unit: 16 headers, 64 first slices, 64 second slices); rows past n
-// give zeros.
-__global__ __launch_bounds__(256) void q4k_pack_x16_kernel(const uint8_t* __restrict__ w, size_t row_bytes,
-                                                           uint8_t* __restrict__ out, uint32_t n, uint32_t units,
-                                                           size_t chunks) {
+// Repacking into the x16 form: one thread per 16-byte chunk of the packed
+// bytes; rows past n give zeros. Q4_K (144 chunks per tile-unit: 16
+// headers, 64 first slices, 64 second slices) reads 16-byte-aligned rows;
+// Q6_K (210 chunks: 64 each of ql / ql / qh slices, 16 scale rows, two
+// chunks of eight d values) reads 2-byte-aligned rows in 16-bit pieces.
+__device__ __forceinline__ uint4 ld128_a2(const uint8_t* p) {
+    const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
+    return make_uint4(q[0] | (static_cast<uint32_t>(q[1]) << 16), q[2] | (static_cast<uint32_t>(q[3]) << 16),
+                      q[4] | (static_cast<uint32_t>(q[5]) << 16), q[6] | (static_cast<uint32_t>(q[7]) << 16));
+}
+
+template <uint32_t QT>
+__global__ __launch_bounds__(256) void pack_x16_kernel(const uint8_t* __restrict__ w, size_t row_bytes,
+                                                       uint8_t* __restrict__ out, uint32_t n, uint32_t units,
+                                                       size_t chunks) {
+    constexpr uint32_t B = X16<QT>::kBlock;
     const size_t c = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (c >= chunks) return;
-    const size_t tu = c / 144;
-    const uint32_t j = static_cast<uint32_t>(c % 144);
+    const size_t tu = c / B;
+    const uint32_t j = static_cast<uint32_t>(c % B);
     const uint32_t tile = static_cast<uint32_t>(tu / units), u = static_cast<uint32_t>(tu % units);
-    uint32_t r, src;
-    if (j < 16) {
-        r = j;
-        src = 0;
-    } else {
-        const uint32_t l = (j - 16) % 64;
-        r = l & 15;
-        src = 16 + 64 * ((j - 16) / 64) + 16 * (l >> 4);
-    }
-    const uint32_t row = tile * 16 + r;
+    const uint8_t* unit0 = w + static_cast<size_t>(u) * B;  // + row * row_bytes
     uint4 v = make_uint4(0, 0, 0, 0);
-    if (row < n) v = ldw128(w + static_cast<size_t>(row) * row_bytes + static_cast<size_t>(u) * 144 + src);
+    if (QT == kQ4_K) {
+        uint32_t r, src;
+        if (j < 16) {
+            r = j;
+            src = 0;
+        } else {
+            const uint32_t l = (j - 16) % 64;
+            r = l & 15;
+            src = 16 + 64 * ((j - 16) / 64) + 16 * (l >> 4);
+        }
+        const uint32_t row = tile * 16 + r;
+        if (row < n) v = ldw128(unit0 + static_cast<size_t>(row) * row_bytes + src);
+    } else if (j < 192) {
+        const uint32_t part = j / 64, l = j % 64, r = l & 15, s = l >> 4;
+        const uint32_t src = part == 2 ? 128 + 32 * (s >> 1) + 16 * (s & 1) : 64 * (s >> 1) + 32 * part + 16 * (s & 1);
+        const uint32_t row = tile * 16 + r;
+        if (row < n) v = ld128_a2(unit0 + static_cast<size_t>(row) * row_bytes + src);
+    } else if (j < 208) {
+        const uint32_t row = tile * 16 + (j - 192);
+        if (row < n) v = ld128_a2(unit0 + static_cast<size_t>(row) * row_bytes + 192);
+    } else {
+        uint32_t hv[8];
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) {
+            const uint32_t row = tile * 16 + 8 * (j - 208) + i;
+            hv[i] = row < n ? *reinterpret_cast<const uint16_t*>(unit0 + static_cast<size_t>(row) * row_bytes + 208) : 0u;
+        }
+        v = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
+    }
     *reinterpret_cast<uint4*>(out + c * 16) = v;
 }
 
@@ -1280,7 +1391,7 @@ __global__ __launch_bounds__(256) void q4k_pack_x16_kernel(const uint8_t* __rest
 // per block; long rows (>= 32 units) with 16 waves per block while the tiles
 // fit one block per CU (18944 -> 3584), else two tiles per 8-wave block
 // (13824 -> 5120); everything else with 8 waves per block.
-int q4k_x16_default_waves(uint32_t n, uint32_t units, int mode) {
+int x16_default_waves(uint32_t n, uint32_t units, int mode) {
     const uint32_t tiles = (n + 15) / 16;
     if (units >= 32) return tiles <= 256 ? 1116 : 2108;
     if (tiles >= 800) return mode == 1 ? 2104 : 1104;
@@ -1327,36 +1438,50 @@ int launch_prep_x(const float* x, XGroup* xq, size_t k, hipStream_t stream) {
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
-// GEMV over a prepared XGroup input. tiling 0 selects the default.
-size_t q4k_x16_bytes(size_t n, size_t k) {
-    if (n == 0 || k == 0 || k % 256 != 0) return 0;
-    return (n + 15) / 16 * 16 * (k / 256) * 144;
+namespace {
+bool x16_type(uint32_t type) { return type == kQ4_K || type == kQ6_K; }
+uint32_t x16_block(uint32_t type) { return type == kQ4_K ? 144u : 210u; }
+}  // namespace
+
+size_t x16_bytes(uint32_t type, size_t n, size_t k) {
+    if (!x16_type(type) || n == 0 || k == 0 || k % 256 != 0) return 0;
+    return (n + 15) / 16 * 16 * (k / 256) * x16_block(type);
 }
 
-int launch_q4k_pack_x16(const void* w, size_t row_bytes, size_t n, size_t k, void* packed, hipStream_t stream) {
-    if (!w || !packed || n == 0 || k == 0 || k % 256 != 0 || row_bytes < k / 256 * 144) return kInvalidArgument;
-    if (row_bytes % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0 || reinterpret_cast<uintptr_t>(packed) % 16 != 0) {
-        return kInvalidArgument;
-    }
+int launch_pack_x16(uint32_t type, const void* w, size_t row_bytes, size_t n, size_t k, void* packed,
+                    hipStream_t stream) {
+    if (!x16_type(type) || !w || !packed || n == 0 || k == 0 || k % 256 != 0) return kInvalidArgument;
+    const uint32_t B = x16_block(type);
+    if (row_bytes < k / 256 * B || reinterpret_cast<uintptr_t>(packed) % 16 != 0) return kInvalidArgument;
+    // Q4_K rows are read in 16-byte pieces, Q6_K rows in 16-bit pieces.
+    const size_t align = type == kQ4_K ? 16 : 2;
+    if (row_bytes % align != 0 || reinterpret_cast<uintptr_t>(w) % align != 0) return kInvalidArgument;
     if (n > 0x7fffffffull || k > 0x7fffffffull) return kLengthError;
     const uint32_t units = static_cast<uint32_t>(k / 256);
-    const size_t chunks = (n + 15) / 16 * units * 144;
+    const size_t chunks = (n + 15) / 16 * units * B;
     if ((chunks + 255) / 256 > 0x7fffffffull) return kLengthError;
-    HIPLLM_LAUNCH(q4k_pack_x16_kernel, dim3(static_cast<uint32_t>((chunks + 255) / 256)), dim3(256), 0, stream,
-                  static_cast<const uint8_t*>(w), row_bytes, static_cast<uint8_t*>(packed), static_cast<uint32_t>(n),
-                  units, chunks);
+    const dim3 grid(static_cast<uint32_t>((chunks + 255) / 256));
+    const auto* wb = static_cast<const uint8_t*>(w);
+    auto* out = static_cast<uint8_t*>(packed);
+    if (type == kQ4_K) {
+        HIPLLM_LAUNCH(pack_x16_kernel<kQ4_K>, grid, dim3(256), 0, stream, wb, row_bytes, out, static_cast<uint32_t>(n),
+                      units, chunks);
+    } else {
+        HIPLLM_LAUNCH(pack_x16_kernel<kQ6_K>, grid, dim3(256), 0, stream, wb, row_bytes, out, static_cast<uint32_t>(n),
+                      units, chunks);
+    }
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
 namespace {
-template <int MODE>
+template <uint32_t QT, int MODE>
 int launch_x16(int code, const uint8_t* wp, const uint8_t* wp2, const XGroup* xq, const float* bias,
                const float* residual, float* y, XGroup* yq, uint32_t nn, uint32_t units, hipStream_t stream) {
     const uint32_t tiles = (nn + 15) / 16;
     switch (code) {
 #define HIPLLM_X16_CASE(RT, W)                                                                                      \
     case 1000 * RT + 100 + W:                                                                                       \
-        HIPLLM_LAUNCH((gemv_q4k_x16_kernel<W, RT, MODE>), dim3((tiles + RT - 1) / RT), dim3(64 * W), 0, stream, wp, wp2, \
+        HIPLLM_LAUNCH((gemv_x16_kernel<QT, W, RT, MODE>), dim3((tiles + RT - 1) / RT), dim3(64 * W), 0, stream, wp, wp2, \
                       xq, bias, residual, y, yq, nn, units);                                                        \
         break;
         HIPLLM_X16_CASE(1, 4)
@@ -1372,8 +1497,8 @@ int launch_x16(int code, const uint8_t* wp, const uint8_t* wp2, const XGroup* xq
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
-int check_x16(const void* packed, const XGroup* xq, const float* y, size_t n, size_t k) {
-    if (!packed || !xq || !y || n == 0 || k == 0 || k % 256 != 0) return kInvalidArgument;
+int check_x16(uint32_t type, const void* packed, const XGroup* xq, const float* y, size_t n, size_t k) {
+    if (!x16_type(type) || !packed || !xq || !y || n == 0 || k == 0 || k % 256 != 0) return kInvalidArgument;
     if (reinterpret_cast<uintptr_t>(packed) % 16 != 0 || reinterpret_cast<uintptr_t>(xq) % 16 != 0) {
         return kInvalidArgument;
     }
@@ -1382,26 +1507,33 @@ int check_x16(const void* packed, const XGroup* xq, const float* y, size_t n, si
 }
 }  // namespace
 
-int launch_gemv_q4k_x16(const void* packed, const XGroup* xq, const float* bias, const float* residual, float* y,
-                        size_t n, size_t k, int waves, hipStream_t stream) {
-    const int rc = check_x16(packed, xq, y, n, k);
+int launch_gemv_x16(uint32_t type, const void* packed, const XGroup* xq, const float* bias, const float* residual,
+                    float* y, size_t n, size_t k, int waves, hipStream_t stream) {
+    const int rc = check_x16(type, packed, xq, y, n, k);
     if (rc != kOk) return rc;
     const uint32_t units = static_cast<uint32_t>(k / 256), nn = static_cast<uint32_t>(n);
-    return launch_x16<0>(waves ? waves : q4k_x16_default_waves(nn, units, 0), static_cast<const uint8_t*>(packed),
-                         nullptr, xq, bias, residual, y, nullptr, nn, units, stream);
+    const int code = waves ? waves : x16_default_waves(nn, units, 0);
+    const auto* wp = static_cast<const uint8_t*>(packed);
+    return type == kQ4_K
+               ? launch_x16<kQ4_K, 0>(code, wp, nullptr, xq, bias, residual, y, nullptr, nn, units, stream)
+               : launch_x16<kQ6_K, 0>(code, wp, nullptr, xq, bias, residual, y, nullptr, nn, units, stream);
 }
 
-int launch_gemv_q4k_x16_swiglu(const void* gate, const void* up, const XGroup* xq, float* y, XGroup* yq, size_t n,
-                               size_t k, int waves, hipStream_t stream) {
-    int rc = check_x16(gate, xq, y, n, k);
-    if (rc == kOk) rc = check_x16(up, xq, y, n, k);
+int launch_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, const XGroup* xq, float* y, XGroup* yq,
+                           size_t n, size_t k, int waves, hipStream_t stream) {
+    int rc = check_x16(type, gate, xq, y, n, k);
+    if (rc == kOk) rc = check_x16(type, up, xq, y, n, k);
     if (rc != kOk) return rc;
     if (yq && (n % 16 != 0 || reinterpret_cast<uintptr_t>(yq) % 16 != 0)) return kInvalidArgument;
     const uint32_t units = static_cast<uint32_t>(k / 256), nn = static_cast<uint32_t>(n);
-    return launch_x16<1>(waves ? waves : q4k_x16_default_waves(nn, units, 1), static_cast<const uint8_t*>(gate),
-                         static_cast<const uint8_t*>(up), xq, nullptr, nullptr, y, yq, nn, units, stream);
+    const int code = waves ? waves : x16_default_waves(nn, units, 1);
+    const auto* g = static_cast<const uint8_t*>(gate);
+    const auto* u = static_cast<const uint8_t*>(up);
+    return type == kQ4_K ? launch_x16<kQ4_K, 1>(code, g, u, xq, nullptr, nullptr, y, yq, nn, units, stream)
+                         : launch_x16<kQ6_K, 1>(code, g, u, xq, nullptr, nullptr, y, yq, nn, units, stream);
 }
 
+// GEMV over a prepared XGroup input. tiling 0 selects the default.
 int launch_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const float* x, const XGroup* xq,
                         const float* bias, const float* residual, float* y, size_t n, size_t k, int tiling,
                         hipStream_t stream) {

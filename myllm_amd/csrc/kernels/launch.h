@@ -99,14 +99,15 @@ int launch_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row
                         size_t k, size_t vectors, const int32_t* ids, size_t experts, size_t routes,
                         size_t expert_stride, int x_routed, size_t ldx, size_t ldy, hipStream_t stream);
 
-// Q4_K rows in 16-row tiles, unit-major (the x16 packed form), and the
-// decode GEMV over it on the int8 MFMA.
-size_t q4k_x16_bytes(size_t n, size_t k);
-int launch_q4k_pack_x16(const void* w, size_t row_bytes, size_t n, size_t k, void* packed, hipStream_t stream);
-int launch_gemv_q4k_x16(const void* packed, const XGroup* xq, const float* bias, const float* residual, float* y,
-                        size_t n, size_t k, int waves, hipStream_t stream);
-int launch_gemv_q4k_x16_swiglu(const void* gate, const void* up, const XGroup* xq, float* y, XGroup* yq, size_t n,
-                               size_t k, int waves, hipStream_t stream);
+// Q4_K / Q6_K rows in 16-row tiles, unit-major (the x16 packed form), and
+// the decode GEMV over it on the int8 MFMA.
+size_t x16_bytes(uint32_t type, size_t n, size_t k);
+int launch_pack_x16(uint32_t type, const void* w, size_t row_bytes, size_t n, size_t k, void* packed,
+                    hipStream_t stream);
+int launch_gemv_x16(uint32_t type, const void* packed, const XGroup* xq, const float* bias, const float* residual,
+                    float* y, size_t n, size_t k, int waves, hipStream_t stream);
+int launch_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, const XGroup* xq, float* y, XGroup* yq,
+                           size_t n, size_t k, int waves, hipStream_t stream);
 
 int gemm_default_tile(uint32_t m, uint32_t n, uint32_t k);
 uint32_t gemm_default_splits(uint32_t m, uint32_t n, uint32_t k, int tile);

@@ -212,26 +212,26 @@ int hipllm_gemv_multi_norm(const HipllmGemvJob* jobs, size_t count, const float*
                   "failure");
 }
 
-size_t hipllm_q4k_x16_bytes(size_t n, size_t k) { return hipllm::q4k_x16_bytes(n, k); }
+size_t hipllm_x16_bytes(uint32_t type, size_t n, size_t k) { return hipllm::x16_bytes(type, n, k); }
 
-int hipllm_q4k_pack_x16(const void* w, size_t row_bytes, size_t n, size_t k, void* packed, void* stream) {
-    return status(hipllm::launch_q4k_pack_x16(w, row_bytes, n, k, packed, as_stream(stream)),
-                  "hipllm_q4k_pack_x16: invalid arguments (k % 256 == 0, 16-byte aligned buffers and rows) or launch "
-                  "failure");
+int hipllm_pack_x16(uint32_t type, const void* w, size_t row_bytes, size_t n, size_t k, void* packed, void* stream) {
+    return status(hipllm::launch_pack_x16(type, w, row_bytes, n, k, packed, as_stream(stream)),
+                  "hipllm_pack_x16: invalid arguments (Q4_K or Q6_K, k % 256 == 0, packed 16-byte aligned, Q4_K rows "
+                  "16-byte and Q6_K rows 2-byte aligned) or launch failure");
 }
 
-int hipllm_gemv_q4k_x16(const void* packed, const void* xq, const float* bias, const float* residual, float* y,
-                        size_t n, size_t k, int waves, void* stream) {
-    return status(hipllm::launch_gemv_q4k_x16(packed, xgc(xq), bias, residual, y, n, k, waves, as_stream(stream)),
-                  "hipllm_gemv_q4k_x16: invalid arguments (k % 256 == 0, a known launch shape, 16-byte aligned "
-                  "buffers) or launch failure");
+int hipllm_gemv_x16(uint32_t type, const void* packed, const void* xq, const float* bias, const float* residual,
+                    float* y, size_t n, size_t k, int waves, void* stream) {
+    return status(hipllm::launch_gemv_x16(type, packed, xgc(xq), bias, residual, y, n, k, waves, as_stream(stream)),
+                  "hipllm_gemv_x16: invalid arguments (Q4_K or Q6_K, k % 256 == 0, a known launch shape, 16-byte "
+                  "aligned buffers) or launch failure");
 }
 
-int hipllm_gemv_q4k_x16_swiglu(const void* gate, const void* up, const void* xq, float* y, void* yq, size_t n,
-                               size_t k, int waves, void* stream) {
-    return status(hipllm::launch_gemv_q4k_x16_swiglu(gate, up, xgc(xq), y, xg(yq), n, k, waves, as_stream(stream)),
-                  "hipllm_gemv_q4k_x16_swiglu: invalid arguments (k % 256 == 0, n % 16 == 0 with yq, a known launch "
-                  "shape, 16-byte aligned buffers) or launch failure");
+int hipllm_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, const void* xq, float* y, void* yq,
+                           size_t n, size_t k, int waves, void* stream) {
+    return status(hipllm::launch_gemv_x16_swiglu(type, gate, up, xgc(xq), y, xg(yq), n, k, waves, as_stream(stream)),
+                  "hipllm_gemv_x16_swiglu: invalid arguments (Q4_K or Q6_K, k % 256 == 0, n % 16 == 0 with yq, a "
+                  "known launch shape, 16-byte aligned buffers) or launch failure");
 }
 
 int hipllm_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m, size_t k, void* stream) {

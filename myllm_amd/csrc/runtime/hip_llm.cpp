@@ -35,12 +35,14 @@ struct DevLayer {
     const float* ffn_norm = nullptr;
     DevMatrix gate, up, down;
     bool fused_gate_up = false;
-    // Q4_K decode weights in the x16 tile-packed form (nullptr: not packed):
-    // the fused QKV rows, the attention output, the FFN gate and up.
+    // Q4_K / Q6_K decode weights in the x16 tile-packed form (nullptr: not
+    // packed): the fused QKV rows, the attention output, the FFN gate, up
+    // and down.
     const void* qkv_x16 = nullptr;
     const void* o_x16 = nullptr;
     const void* gate_x16 = nullptr;
     const void* up_x16 = nullptr;
+    const void* down_x16 = nullptr;
 };
 
 // Device activation buffers (one token row; the serial prefill reuses them).
@@ -97,10 +99,12 @@ struct HipLLM::Impl {
 
     WeightArena weights;
     std::size_t weight_bytes = 0;  // sum of GGUF tensor payloads
-    // Decode copies of the Q4_K projections in the x16 tile-packed form read
-    // by the int8-MFMA GEMV (the GGUF rows stay for the prefill matmuls).
+    // Decode copies of the Q4_K / Q6_K projections in the x16 tile-packed
+    // form read by the int8-MFMA GEMV (the GGUF rows stay for the prefill
+    // matmuls).
     void* x16_arena = nullptr;
     std::size_t x16_bytes = 0;
+    const void* output_x16 = nullptr;  // the LM head's x16 copy
     bool packed_decode = false;
     DevMatrix embedding, output;
     const float* output_norm = nullptr;
@@ -237,11 +241,14 @@ void HipLLM::Impl::choose_decode_forms() {
     fused_ffn_norm = fused_ffn_norm && fused_norms;
 }
 
-// Q4_K projections whose rows hold whole super-blocks get an x16 copy: the
-// fused QKV rows (when Q, K and V are all Q4_K and contiguous), the
-// attention output, and the FFN gate / up pair (both Q4_K).
+// Q4_K and Q6_K projections whose rows hold whole super-blocks get an x16
+// copy: the fused QKV rows, the attention output, the FFN gate / up pair,
+// the FFN down projection and the LM head.
 void HipLLM::Impl::pack_decode_weights() {
-    auto q4k = [](const DevMatrix& m) { return m.type == hipllm::kQ4_K && m.cols % 256 == 0 && m.row_bytes % 16 == 0; };
+    auto packable = [](const DevMatrix& m) {
+        return m.cols % 256 == 0 && ((m.type == hipllm::kQ4_K && m.row_bytes % 16 == 0) ||
+                                     (m.type == hipllm::kQ6_K && m.row_bytes % 2 == 0));
+    };
     const std::size_t H = config.embedding_size;
     struct Job {
         const DevMatrix* m;
@@ -253,23 +260,26 @@ void HipLLM::Impl::pack_decode_weights() {
     std::size_t total = 0;
     auto add = [&](const DevMatrix& m, std::size_t rows, const void** dst) {
         jobs.push_back({&m, rows, dst, total});
-        total = align_up(total + hipllm::q4k_x16_bytes(rows, m.cols), 256);
+        total = align_up(total + hipllm::x16_bytes(m.type, rows, m.cols), 256);
     };
     for (DevLayer& L : layers) {
-        if (L.fused_qkv && q4k(L.q) && q4k(L.k) && q4k(L.v)) add(L.q, H + 2 * kv_dim, &L.qkv_x16);
-        if (q4k(L.o)) add(L.o, L.o.rows, &L.o_x16);
-        if (L.fused_gate_up && q4k(L.gate) && q4k(L.up)) {
+        if (L.fused_qkv && packable(L.q)) add(L.q, H + 2 * kv_dim, &L.qkv_x16);
+        if (packable(L.o)) add(L.o, L.o.rows, &L.o_x16);
+        if (L.fused_gate_up && packable(L.gate)) {
             add(L.gate, L.gate.rows, &L.gate_x16);
             add(L.up, L.up.rows, &L.up_x16);
         }
+        if (packable(L.down)) add(L.down, L.down.rows, &L.down_x16);
     }
+    if (packable(output)) add(output, output.rows, &output_x16);
     if (jobs.empty()) return;
     hip_check(hipMalloc(&x16_arena, total), "hipMalloc(x16 decode weights)");
     x16_bytes = total;
     auto* base = static_cast<std::uint8_t*>(x16_arena);
     for (const Job& j : jobs) {
         *j.dst = base + j.off;
-        launch_check(hipllm::launch_q4k_pack_x16(j.m->ptr, j.m->row_bytes, j.rows, j.m->cols, base + j.off, stream),
+        launch_check(hipllm::launch_pack_x16(j.m->type, j.m->ptr, j.m->row_bytes, j.rows, j.m->cols, base + j.off,
+                                             stream),
                      "x16 packing");
     }
     hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
@@ -466,8 +476,8 @@ void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, fl
     const float eps = c.norm_epsilon;
     if (packed_decode && L.qkv_x16) {
         // act.normq holds the XGroup form of rmsnorm(hidden) * attn_norm.
-        launch_check(hipllm::launch_gemv_q4k_x16(L.qkv_x16, act.normq, L.qkv_bias, nullptr, act.qkv, H + 2 * kv_dim, H,
-                                                 0, stream),
+        launch_check(hipllm::launch_gemv_x16(L.q.type, L.qkv_x16, act.normq, L.qkv_bias, nullptr, act.qkv,
+                                             H + 2 * kv_dim, H, 0, stream),
                      "QKV GEMV");
     } else if (fused_norms) {
         // QKV of rmsnorm(hidden) * attn_norm, the norm in the GEMV's prologue.
@@ -490,7 +500,8 @@ void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, fl
                                                  c.kv_head_count, c.head_size, pos, scale, stream, dpos, max_sequence),
                  "RoPE/KV write + attention");
     if (packed_decode && L.o_x16) {
-        launch_check(hipllm::launch_gemv_q4k_x16(L.o_x16, act.attnq, nullptr, hidden, next_hidden, H, H, 0, stream),
+        launch_check(hipllm::launch_gemv_x16(L.o.type, L.o_x16, act.attnq, nullptr, hidden, next_hidden, H, H, 0,
+                                             stream),
                      "attention output GEMV");
     } else {
         gemv(L.o, act.attn, act.attnq, nullptr, hidden, next_hidden);
@@ -503,8 +514,8 @@ void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, fl
         launch_check(hipllm::launch_rmsnorm(next_hidden, L.ffn_norm, act.norm, act.normq, 1, H, eps, stream),
                      "RMSNorm");
         if (packed_decode && L.gate_x16) {
-            launch_check(hipllm::launch_gemv_q4k_x16_swiglu(L.gate_x16, L.up_x16, act.normq, act.ffn, act.ffnq, F, H, 0,
-                                                            stream),
+            launch_check(hipllm::launch_gemv_x16_swiglu(L.gate.type, L.gate_x16, L.up_x16, act.normq, act.ffn,
+                                                        act.ffnq, F, H, 0, stream),
                          "gate/up GEMV");
         } else if (L.fused_gate_up) {
             launch_check(hipllm::launch_gemv_swiglu(L.gate.type, L.gate.ptr, L.up.ptr, L.gate.row_bytes, act.norm,
@@ -520,7 +531,13 @@ void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, fl
     // The layer output lands back in `hidden`, followed by its RMSNorm with
     // the next layer's attention gain (or the output norm after the last),
     // unless the next layer's QKV GEMV normalises it itself.
-    gemv(L.down, act.ffn, act.ffnq, nullptr, next_hidden, hidden);
+    if (packed_decode && L.down_x16) {
+        launch_check(hipllm::launch_gemv_x16(L.down.type, L.down_x16, act.ffnq, nullptr, next_hidden, hidden, H, F, 0,
+                                             stream),
+                     "down GEMV");
+    } else {
+        gemv(L.down, act.ffn, act.ffnq, nullptr, next_hidden, hidden);
+    }
     if (!fused_norms || li + 1 == layers.size()) {
         const float* next_gamma = li + 1 < layers.size() ? layers[li + 1].attn_norm : output_norm;
         launch_check(hipllm::launch_rmsnorm(hidden, next_gamma, act.norm, act.normq, 1, H, eps, stream), "RMSNorm");
@@ -676,7 +693,13 @@ void HipLLM::Impl::head_step(const float* hidden_row) {
 // LM head and argmax on the normalised row in act.norm / act.normq.
 void HipLLM::Impl::head_logits() {
     const GgufModelConfig& c = config;
-    gemv(output, act.norm, act.normq, nullptr, nullptr, act.logits);
+    if (packed_decode && output_x16) {
+        launch_check(hipllm::launch_gemv_x16(output.type, output_x16, act.normq, nullptr, nullptr, act.logits,
+                                             c.vocabulary_size, c.embedding_size, 0, stream),
+                     "LM head GEMV");
+    } else {
+        gemv(output, act.norm, act.normq, nullptr, nullptr, act.logits);
+    }
     launch_check(hipllm::launch_argmax(act.logits, c.vocabulary_size, act.token, act.argmax_scratch, stream),
                  "argmax");
 }
@@ -904,7 +927,7 @@ void HipLLM::set_decode_graphs(bool enabled) {
 
 void HipLLM::set_packed_decode(bool enabled) {
     if (!impl_) throw std::runtime_error("HIP model is not initialized");
-    if (enabled && !impl_->x16_arena) throw std::invalid_argument("the model has no Q4_K projections to pack");
+    if (enabled && !impl_->x16_arena) throw std::invalid_argument("the model has no Q4_K or Q6_K projections to pack");
     hip_check(hipStreamSynchronize(impl_->stream), "hipStreamSynchronize");
     impl_->packed_decode = enabled;
     impl_->choose_decode_forms();

@@ -64,7 +64,7 @@ public:
     // Decode path: true (default) = each decode step is one replay of a
     // recorded HIP graph; false = the step's kernels are launched one by one.
     void set_decode_graphs(bool enabled);
-    // Decode GEMVs of Q4_K projections on the x16 tile-packed copies (the
+    // Decode GEMVs of Q4_K / Q6_K projections on the x16 tile-packed copies (the
     // int8-MFMA GEMV; on by default when the model has such projections) or
     // on the GGUF rows (the vector GEMV). Results agree to FP32 rounding.
     void set_packed_decode(bool enabled);

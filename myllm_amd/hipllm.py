@@ -87,10 +87,10 @@ SIGNATURES = {
     "hipllm_gemv_norm": (_I, [_U32, _P, _S, _P, _P, _F, _P, _P, _P, _S, _S, _I, _P]),
     "hipllm_gemv_swiglu_norm": (_I, [_U32, _P, _P, _S, _P, _P, _F, _P, _P, _S, _S, _I, _P]),
     "hipllm_to_f16": (_I, [_P, _S, _P, _P, _S, _S, _P]),
-    "hipllm_q4k_x16_bytes": (_S, [_S, _S]),
-    "hipllm_q4k_pack_x16": (_I, [_P, _S, _S, _S, _P, _P]),
-    "hipllm_gemv_q4k_x16": (_I, [_P, _P, _P, _P, _P, _S, _S, _I, _P]),
-    "hipllm_gemv_q4k_x16_swiglu": (_I, [_P, _P, _P, _P, _P, _S, _S, _I, _P]),
+    "hipllm_x16_bytes": (_S, [_U32, _S, _S]),
+    "hipllm_pack_x16": (_I, [_U32, _P, _S, _S, _S, _P, _P]),
+    "hipllm_gemv_x16": (_I, [_U32, _P, _P, _P, _P, _P, _S, _S, _I, _P]),
+    "hipllm_gemv_x16_swiglu": (_I, [_U32, _P, _P, _P, _P, _P, _S, _S, _I, _P]),
     "hipllm_gemm_mfma": (_I, [_U32, _P, _S, _P, _P, _P, _P, _P, _S, _S, _S, _I, _I, _P, _S, _P]),
     "hipllm_gemm_mfma_workspace_bytes": (_S, [_S, _S, _S, _I, _I]),
     "hipllm_gemm_workspace_bytes": (_S, [_S, _S]),
@@ -548,18 +548,18 @@ def _k_gemv_swiglu(qtype, wg, wu, row_bytes, x, xq, y, yq, n, k, tiling=0, strea
                                    n, k, tiling, _stream(stream)))
 
 
-def _k_q4k_pack_x16(w, row_bytes, n, k, packed, stream=None):
-    check(lib().hipllm_q4k_pack_x16(_ptr(w), row_bytes, n, k, _ptr(packed), _stream(stream)))
+def _k_pack_x16(qtype, w, row_bytes, n, k, packed, stream=None):
+    check(lib().hipllm_pack_x16(qtype, _ptr(w), row_bytes, n, k, _ptr(packed), _stream(stream)))
 
 
-def _k_gemv_q4k_x16(packed, xq, bias, residual, y, n, k, waves=0, stream=None):
-    check(lib().hipllm_gemv_q4k_x16(_ptr(packed), _ptr(xq), _ptr(bias), _ptr(residual), _ptr(y), n, k, waves,
-                                    _stream(stream)))
+def _k_gemv_x16(qtype, packed, xq, bias, residual, y, n, k, waves=0, stream=None):
+    check(lib().hipllm_gemv_x16(qtype, _ptr(packed), _ptr(xq), _ptr(bias), _ptr(residual), _ptr(y), n, k, waves,
+                                _stream(stream)))
 
 
-def _k_gemv_q4k_x16_swiglu(gate, up, xq, y, yq, n, k, waves=0, stream=None):
-    check(lib().hipllm_gemv_q4k_x16_swiglu(_ptr(gate), _ptr(up), _ptr(xq), _ptr(y), _ptr(yq), n, k, waves,
-                                           _stream(stream)))
+def _k_gemv_x16_swiglu(qtype, gate, up, xq, y, yq, n, k, waves=0, stream=None):
+    check(lib().hipllm_gemv_x16_swiglu(qtype, _ptr(gate), _ptr(up), _ptr(xq), _ptr(y), _ptr(yq), n, k, waves,
+                                       _stream(stream)))
 
 
 def _k_to_f16(x, ldx, xh, xscale, m, k, stream=None):
@@ -766,9 +766,8 @@ def _k_swiglu(g, u, y, yq, n, stream=None):
 
 kernels = types.SimpleNamespace(
     dequant_rows=_k_dequant_rows, prep_x=_k_prep_x, gemv=_k_gemv, gemv_noalloc=_k_gemv_noalloc,
-    gemv_prepped=_k_gemv_prepped, q4k_pack_x16=_k_q4k_pack_x16, gemv_q4k_x16=_k_gemv_q4k_x16,
-    gemv_q4k_x16_swiglu=_k_gemv_q4k_x16_swiglu,
-    q4k_x16_bytes=lambda n, k: lib().hipllm_q4k_x16_bytes(n, k),
+    gemv_prepped=_k_gemv_prepped, pack_x16=_k_pack_x16, gemv_x16=_k_gemv_x16, gemv_x16_swiglu=_k_gemv_x16_swiglu,
+    x16_bytes=lambda qtype, n, k: lib().hipllm_x16_bytes(qtype, n, k),
     gemv_swiglu=_k_gemv_swiglu, gemv_norm=_k_gemv_norm, gemv_swiglu_norm=_k_gemv_swiglu_norm, to_f16=_k_to_f16, gemm_mfma=_k_gemm_mfma, gemm=_k_gemm,
     gemm_workspace_bytes=lambda m, k: lib().hipllm_gemm_workspace_bytes(m, k), rmsnorm=_k_rmsnorm, embed=_k_embed, rope_kv=_k_rope_kv,
     attn_decode=_k_attn_decode, attn_decode_rope_gated=_k_attn_decode_rope_gated, argmax=_k_argmax,

@@ -1,11 +1,15 @@
-"""The x16 tile-packed Q4_K form and the int8-MFMA decode GEMV over it.
+"""The x16 tile-packed Q4_K / Q6_K forms and the int8-MFMA decode GEMV over
+them.
 
-* Packing: the device packer's bytes against a numpy restatement of the
-  layout (tile T, unit u at (T * units + u) * 2304: the 16 rows' headers,
-  then for lane l = 16 s + r the quant bytes [16 s, +16) of row r, then its
-  bytes [64 + 16 s, +16)); rows past n are zero.
+* Packing: the device packer's bytes against a numpy restatement of each
+  layout (tile T, unit u at (T * units + u) * 16 B; Q4_K: the 16 rows'
+  headers, then for lane l = 16 s + r the quant bytes [16 s, +16) of row r,
+  then its bytes [64 + 16 s, +16); Q6_K: for lane l the ql bytes
+  [64 (s >> 1) + 16 (s & 1), +16), then ql [64 (s >> 1) + 32 + 16 (s & 1),
+  +16), then qh [32 (s >> 1) + 16 (s & 1), +16), then the 16 rows' scale
+  bytes and their d); rows past n are zero.
 * Product: against float64 over the oracle's bit-exact CPU dequantization of
-  the same GGUF rows (oracle.dequant_rows restates model.cpp:616-644), for
+  the same GGUF rows (oracle.dequant_rows restates model.cpp:616-683), for
   ragged row counts, every launch shape, bias and residual, short and long
   rows; and against the vector GEMV on the GGUF rows, which computes the
   same exact integer digit sums (only the FP32 summation order differs).
@@ -26,30 +30,44 @@ torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
 SHAPES = [1104, 1108, 1116, 2104, 2108, 2116]
+TYPES = [synth.Q4_K, synth.Q6_K]
+BLOCK = {synth.Q4_K: 144, synth.Q6_K: 210}
 
 
-def pack_ref(w: np.ndarray, n: int, k: int) -> np.ndarray:
+def pack_ref(qtype: int, w: np.ndarray, n: int, k: int) -> np.ndarray:
     """numpy restatement of the x16 layout from GGUF rows [n, row_bytes]."""
+    B = BLOCK[qtype]
     units = k // 256
     tiles = (n + 15) // 16
-    rows = np.zeros((tiles * 16, units, 144), dtype=np.uint8)
-    rows[:n] = w[:, : units * 144].reshape(n, units, 144)
-    out = np.empty((tiles, units, 2304), dtype=np.uint8)
+    rows = np.zeros((tiles * 16, units, B), dtype=np.uint8)
+    rows[:n] = w[:, : units * B].reshape(n, units, B)
+    out = np.empty((tiles, units, 16 * B), dtype=np.uint8)
     for t in range(tiles):
-        blk = rows[16 * t: 16 * t + 16]  # [16, units, 144]
-        out[t, :, :256] = blk[:, :, :16].transpose(1, 0, 2).reshape(units, 256)
-        for part, base in ((0, 16), (1, 80)):
-            # lane l = 16 s + r: bytes base + 16 s .. of row r
-            sl = np.stack([blk[:, :, base + 16 * s: base + 16 * s + 16] for s in range(4)])  # [4, 16, units, 16]
-            out[t, :, 256 + 1024 * part: 1280 + 1024 * part] = sl.transpose(2, 0, 1, 3).reshape(units, 1024)
+        blk = rows[16 * t: 16 * t + 16]  # [16, units, B]
+
+        def lanes(offset_of_s):
+            # lane l = 16 s + r: 16 bytes at offset_of_s(s) of row r -> [units, 1024]
+            sl = np.stack([blk[:, :, offset_of_s(s): offset_of_s(s) + 16] for s in range(4)])  # [4, 16, units, 16]
+            return sl.transpose(2, 0, 1, 3).reshape(units, 1024)
+
+        if qtype == synth.Q4_K:
+            out[t, :, :256] = blk[:, :, :16].transpose(1, 0, 2).reshape(units, 256)
+            out[t, :, 256:1280] = lanes(lambda s: 16 + 16 * s)
+            out[t, :, 1280:2304] = lanes(lambda s: 80 + 16 * s)
+        else:
+            out[t, :, 0:1024] = lanes(lambda s: 64 * (s >> 1) + 16 * (s & 1))
+            out[t, :, 1024:2048] = lanes(lambda s: 64 * (s >> 1) + 32 + 16 * (s & 1))
+            out[t, :, 2048:3072] = lanes(lambda s: 128 + 32 * (s >> 1) + 16 * (s & 1))
+            out[t, :, 3072:3328] = blk[:, :, 192:208].transpose(1, 0, 2).reshape(units, 256)
+            out[t, :, 3328:3360] = blk[:, :, 208:210].transpose(1, 0, 2).reshape(units, 32)
     return out.reshape(-1)
 
 
-def packed_case(cuda, n, k, seed, bias=False, residual=False, waves=0):
-    w = random_rows(synth.Q4_K, n, k, seed)
+def packed_case(cuda, qtype, n, k, seed, bias=False, residual=False, waves=0):
+    w = random_rows(qtype, n, k, seed)
     dw = dev_bytes(w, cuda)
-    packed = torch.empty(kernels.q4k_x16_bytes(n, k), dtype=torch.uint8, device=cuda)
-    kernels.q4k_pack_x16(dw, w.shape[1], n, k, packed)
+    packed = torch.empty(kernels.x16_bytes(qtype, n, k), dtype=torch.uint8, device=cuda)
+    kernels.pack_x16(qtype, dw, w.shape[1], n, k, packed)
     x = synth.normal(k, seed + 1)
     dx = torch.from_numpy(x).to(cuda)
     xq = xgroup.buffer(torch, k, cuda)
@@ -59,10 +77,10 @@ def packed_case(cuda, n, k, seed, bias=False, residual=False, waves=0):
     db = None if b is None else torch.from_numpy(b).to(cuda)
     dr = None if r is None else torch.from_numpy(r).to(cuda)
     y = torch.empty(n, dtype=torch.float32, device=cuda)
-    kernels.gemv_q4k_x16(packed, xq, db, dr, y, n, k, waves)
+    kernels.gemv_x16(qtype, packed, xq, db, dr, y, n, k, waves)
     yv = torch.empty(n, dtype=torch.float32, device=cuda)
-    kernels.gemv_prepped(synth.Q4_K, dw, w.shape[1], dx, xq, db, dr, yv, n, k, 0)
-    wf = oracle.dequant_rows(synth.Q4_K, w, k).astype(np.float64)
+    kernels.gemv_prepped(qtype, dw, w.shape[1], dx, xq, db, dr, yv, n, k, 0)
+    wf = oracle.dequant_rows(qtype, w, k).astype(np.float64)
     ref = wf @ x.astype(np.float64)
     for extra in (b, r):
         if extra is not None:
@@ -70,75 +88,101 @@ def packed_case(cuda, n, k, seed, bias=False, residual=False, waves=0):
     return y.cpu().numpy(), yv.cpu().numpy(), ref, w, packed
 
 
+@pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("n,k", [(1, 256), (16, 512), (37, 3584), (333, 2816), (1001, 1024)])
-def test_pack_layout(cuda, n, k):
-    w = random_rows(synth.Q4_K, n, k, n + k)
-    packed = torch.empty(kernels.q4k_x16_bytes(n, k), dtype=torch.uint8, device=cuda)
-    assert packed.numel() == (n + 15) // 16 * 16 * (k // 256) * 144
-    kernels.q4k_pack_x16(dev_bytes(w, cuda), w.shape[1], n, k, packed)
-    assert np.array_equal(packed.cpu().numpy(), pack_ref(w, n, k))
+def test_pack_layout(cuda, qtype, n, k):
+    w = random_rows(qtype, n, k, n + k)
+    packed = torch.empty(kernels.x16_bytes(qtype, n, k), dtype=torch.uint8, device=cuda)
+    assert packed.numel() == (n + 15) // 16 * 16 * (k // 256) * BLOCK[qtype]
+    kernels.pack_x16(qtype, dev_bytes(w, cuda), w.shape[1], n, k, packed)
+    assert np.array_equal(packed.cpu().numpy(), pack_ref(qtype, w, n, k))
 
 
+def test_pack_layout_q6k_odd_row_alignment(cuda):
+    """Q6_K rows of an odd unit count start 2-byte aligned (210 = 2 * 105):
+    rows taken from a buffer offset by 2 bytes pack the same."""
+    n, k = 21, 3 * 256
+    w = random_rows(synth.Q6_K, n, k, 5)
+    buf = torch.zeros(w.size + 16, dtype=torch.uint8, device=cuda)
+    buf[2: 2 + w.size] = torch.from_numpy(w.reshape(-1)).to(cuda)
+    packed = torch.empty(kernels.x16_bytes(synth.Q6_K, n, k), dtype=torch.uint8, device=cuda)
+    kernels.pack_x16(synth.Q6_K, buf[2:], w.shape[1], n, k, packed)
+    assert np.array_equal(packed.cpu().numpy(), pack_ref(synth.Q6_K, w, n, k))
+
+
+@pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("n,k", [(1, 256), (16, 256), (37, 512), (333, 2816), (1001, 3584), (130, 18944)])
-def test_gemv_x16_matches_oracle_and_vector_path(cuda, n, k):
-    y, yv, ref, _, _ = packed_case(cuda, n, k, seed=7 * n + k, bias=True, residual=True)
+def test_gemv_x16_matches_oracle_and_vector_path(cuda, qtype, n, k):
+    y, yv, ref, _, _ = packed_case(cuda, qtype, n, k, seed=7 * n + k, bias=True, residual=True)
     assert rel_err(y, ref) <= 1e-5
     assert rel_err(y, yv) <= 1e-6
 
 
+@pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("waves", SHAPES)
-def test_gemv_x16_launch_shapes(cuda, waves):
+def test_gemv_x16_launch_shapes(cuda, qtype, waves):
     # 7 units: fewer than some shapes' waves (idle waves), more than others'
     # (several units per wave, ring refills); 45 rows: a partial tile, and
     # for two tiles per block a partial tile pair.
-    y, yv, ref, _, _ = packed_case(cuda, 45, 7 * 256, seed=waves, residual=True, waves=waves)
+    y, yv, ref, _, _ = packed_case(cuda, qtype, 45, 7 * 256, seed=waves, residual=True, waves=waves)
     assert rel_err(y, ref) <= 1e-5
     assert rel_err(y, yv) <= 1e-6
 
 
-def test_gemv_x16_deterministic_and_long_rows(cuda):
+@pytest.mark.parametrize("qtype", TYPES)
+def test_gemv_x16_deterministic_and_long_rows(cuda, qtype):
     # 159 units (ten per wave at 16 waves per block): every shape reduces in a
     # fixed order, so repeated launches give the same bits.
     n, k = 64, 159 * 256
-    y, yv, ref, _, _ = packed_case(cuda, n, k, seed=11, waves=1116)
+    y, yv, ref, _, _ = packed_case(cuda, qtype, n, k, seed=11, waves=1116)
     assert rel_err(y, ref) <= 1e-5
-    y2, _, _, _, _ = packed_case(cuda, n, k, seed=11, waves=1116)
+    y2, _, _, _, _ = packed_case(cuda, qtype, n, k, seed=11, waves=1116)
     assert np.array_equal(y.view(np.int32), y2.view(np.int32))
 
 
-def test_gemv_x16_nan_input_propagates(cuda):
+@pytest.mark.parametrize("qtype", TYPES)
+def test_gemv_x16_nan_input_propagates(cuda, qtype):
     # A non-finite activation makes its XGroup's e NaN: the rows that read the
     # group are NaN, as FP32 arithmetic would make them.
     n, k = 32, 512
-    w = random_rows(synth.Q4_K, n, k, 3)
-    packed = torch.empty(kernels.q4k_x16_bytes(n, k), dtype=torch.uint8, device=cuda)
-    kernels.q4k_pack_x16(dev_bytes(w, cuda), w.shape[1], n, k, packed)
+    w = random_rows(qtype, n, k, 3)
+    packed = torch.empty(kernels.x16_bytes(qtype, n, k), dtype=torch.uint8, device=cuda)
+    kernels.pack_x16(qtype, dev_bytes(w, cuda), w.shape[1], n, k, packed)
     x = torch.from_numpy(synth.normal(k, 4)).to(cuda)
     x[100] = float("nan")
     xq = xgroup.buffer(torch, k, cuda)
     kernels.prep_x(x, xq, k)
     y = torch.empty(n, dtype=torch.float32, device=cuda)
-    kernels.gemv_q4k_x16(packed, xq, None, None, y, n, k, 0)
+    kernels.gemv_x16(qtype, packed, xq, None, None, y, n, k, 0)
     assert torch.isnan(y).all()
 
 
 def test_gemv_x16_rejects_bad_arguments(cuda):
     n, k = 16, 256
-    packed = torch.zeros(kernels.q4k_x16_bytes(n, k) + 16, dtype=torch.uint8, device=cuda)
+    packed = torch.zeros(kernels.x16_bytes(synth.Q4_K, n, k) + 16, dtype=torch.uint8, device=cuda)
     xq = xgroup.buffer(torch, k, cuda)
     y = torch.empty(n, dtype=torch.float32, device=cuda)
-    assert kernels.q4k_x16_bytes(n, 300) == 0
+    assert kernels.x16_bytes(synth.Q4_K, n, 300) == 0
+    assert kernels.x16_bytes(synth.Q8_0, n, 256) == 0
     with pytest.raises(ValueError):
-        kernels.gemv_q4k_x16(packed, xq, None, None, y, n, 300, 0)  # k % 256
+        kernels.gemv_x16(synth.Q4_K, packed, xq, None, None, y, n, 300, 0)  # k % 256
     with pytest.raises(ValueError):
-        kernels.gemv_q4k_x16(packed, xq, None, None, y, n, k, 1103)  # unknown launch shape
+        kernels.gemv_x16(synth.Q8_0, packed, xq, None, None, y, n, k, 0)  # not a packed type
     with pytest.raises(ValueError):
-        kernels.gemv_q4k_x16(packed[8:], xq, None, None, y, n, k, 0)  # misaligned weights
-    w = torch.zeros(n * 144 + 256, dtype=torch.uint8, device=cuda)
+        kernels.gemv_x16(synth.Q4_K, packed, xq, None, None, y, n, k, 1103)  # unknown launch shape
     with pytest.raises(ValueError):
-        kernels.q4k_pack_x16(w, 150, n, k, packed)  # row_bytes % 16
+        kernels.gemv_x16(synth.Q4_K, packed, xq, None, None, y, n, k, 1204)  # two units in flight: not offered
     with pytest.raises(ValueError):
-        kernels.q4k_pack_x16(w, 144, n, 200, packed)  # k % 256
+        kernels.gemv_x16(synth.Q4_K, packed[8:], xq, None, None, y, n, k, 0)  # misaligned weights
+    w = torch.zeros(n * 210 + 256, dtype=torch.uint8, device=cuda)
+    with pytest.raises(ValueError):
+        kernels.pack_x16(synth.Q4_K, w, 150, n, k, packed)  # Q4_K row_bytes % 16
+    with pytest.raises(ValueError):
+        kernels.pack_x16(synth.Q4_K, w, 144, n, 200, packed)  # k % 256
+    with pytest.raises(ValueError):
+        kernels.pack_x16(synth.Q6_K, w[1:], 210, n, k, packed)  # Q6_K rows must be 2-byte aligned
+    with pytest.raises(ValueError):
+        kernels.pack_x16(synth.Q6_K, w, 209, n, k, packed)  # row shorter than its blocks
 
 
 def silu_mul_ref(g, u):
@@ -148,35 +192,36 @@ def silu_mul_ref(g, u):
     return g * sig * np.asarray(u, dtype=np.float64)
 
 
+@pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("n,k,waves", [(16, 256, 0), (64, 512, 1108), (1040, 3584, 0), (4864, 1024, 0),
-                                       (320, 2048, 2104), (48, 18944, 1116)])
-def test_gemv_x16_swiglu(cuda, n, k, waves):
-    wg = random_rows(synth.Q4_K, n, k, n + 1)
-    wu = random_rows(synth.Q4_K, n, k, n + 2)
-    pg = torch.empty(kernels.q4k_x16_bytes(n, k), dtype=torch.uint8, device=cuda)
+                                       (320, 2048, 2104), (48, 18944, 1116), (13824, 1280, 0)])
+def test_gemv_x16_swiglu(cuda, qtype, n, k, waves):
+    wg = random_rows(qtype, n, k, n + 1)
+    wu = random_rows(qtype, n, k, n + 2)
+    pg = torch.empty(kernels.x16_bytes(qtype, n, k), dtype=torch.uint8, device=cuda)
     pu = torch.empty_like(pg)
-    kernels.q4k_pack_x16(dev_bytes(wg, cuda), wg.shape[1], n, k, pg)
-    kernels.q4k_pack_x16(dev_bytes(wu, cuda), wu.shape[1], n, k, pu)
+    kernels.pack_x16(qtype, dev_bytes(wg, cuda), wg.shape[1], n, k, pg)
+    kernels.pack_x16(qtype, dev_bytes(wu, cuda), wu.shape[1], n, k, pu)
     x = synth.normal(k, n + 3)
     dx = torch.from_numpy(x).to(cuda)
     xq = xgroup.buffer(torch, k, cuda)
     kernels.prep_x(dx, xq, k)
     y = torch.empty(n, dtype=torch.float32, device=cuda)
     yq = xgroup.buffer(torch, n, cuda)
-    kernels.gemv_q4k_x16_swiglu(pg, pu, xq, y, yq, n, k, waves)
-    g = oracle.dequant_rows(synth.Q4_K, wg, k).astype(np.float64) @ x.astype(np.float64)
-    u = oracle.dequant_rows(synth.Q4_K, wu, k).astype(np.float64) @ x.astype(np.float64)
+    kernels.gemv_x16_swiglu(qtype, pg, pu, xq, y, yq, n, k, waves)
+    g = oracle.dequant_rows(qtype, wg, k).astype(np.float64) @ x.astype(np.float64)
+    u = oracle.dequant_rows(qtype, wu, k).astype(np.float64) @ x.astype(np.float64)
     ref = silu_mul_ref(g, u)
     yv = y.cpu().numpy()
     assert rel_err(yv, ref) <= 1e-5
     xgroup.check(yq, yv)
     # The same pair through the vector path on the GGUF rows.
     yv2 = torch.empty(n, dtype=torch.float32, device=cuda)
-    kernels.gemv_swiglu(synth.Q4_K, dev_bytes(wg, cuda), dev_bytes(wu, cuda), wg.shape[1], dx, xq, yv2, None, n, k, 0)
+    kernels.gemv_swiglu(qtype, dev_bytes(wg, cuda), dev_bytes(wu, cuda), wg.shape[1], dx, xq, yv2, None, n, k, 0)
     assert rel_err(yv, yv2.cpu().numpy()) <= 1e-6
     # Without the XGroup output, and the output rows reject a ragged n.
-    kernels.gemv_q4k_x16_swiglu(pg, pu, xq, y, None, n, k, waves)
+    kernels.gemv_x16_swiglu(qtype, pg, pu, xq, y, None, n, k, waves)
     assert np.array_equal(y.cpu().numpy().view(np.int32), yv.view(np.int32))
     if n > 16:
         with pytest.raises(ValueError):
-            kernels.gemv_q4k_x16_swiglu(pg, pu, xq, y, yq, n - 1, k, waves)
+            kernels.gemv_x16_swiglu(qtype, pg, pu, xq, y, yq, n - 1, k, waves)

@@ -14,6 +14,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
+from myllm_amd import synth
 from myllm_amd.hipllm import kernels, HipLLM, LengthError, generate
 
 pytestmark = pytest.mark.gpu
@@ -108,10 +109,18 @@ def test_memory_stats(cuda, golden_model):
     with HipLLM(path, 64) as m:
         s = m.memory_stats()
         m.set_packed_decode(False)
-    # The GGUF payload plus the x16 decode copies of the Q4_K projections
-    # (tiny: fused QKV and the gate / up pair; the attention output is Q5_0).
+    # The GGUF payload plus the x16 decode copies of the Q4_K / Q6_K
+    # projections (tiny: Q4_K fused QKV and gate / up pair, Q6_K down and LM
+    # head; the attention output is Q5_0), each 256-byte aligned.
     h, f, kv = cfg["embedding_size"], cfg["feed_forward_size"], cfg["kv_head_count"] * cfg["head_size"]
-    x16 = cfg["layer_count"] * (kernels.q4k_x16_bytes(h + 2 * kv, h) + 2 * kernels.q4k_x16_bytes(f, h))
+    v = cfg["vocabulary_size"]
+
+    def packed(qtype, n, k):
+        return -(-kernels.x16_bytes(qtype, n, k) // 256) * 256
+
+    per_layer = packed(synth.Q4_K, h + 2 * kv, h) + 2 * packed(synth.Q4_K, f, h) + packed(synth.Q6_K, h, f)
+    x16 = cfg["layer_count"] * per_layer + packed(synth.Q6_K, v, h)
+    assert per_layer > 0
     assert s["weight_bytes"] == cfg["stored_weight_bytes"] + x16
     kv = cfg["kv_head_count"] * cfg["head_size"]
     assert s["kv_cache_bytes"] == 2 * cfg["layer_count"] * 64 * kv * 4
