@@ -119,6 +119,7 @@ __global__ void rope_kv_kernel(float* __restrict__ qkv, const float2* __restrict
 // (len = *dpos + 1); S then follows the capacity, not the length.
 constexpr uint32_t kAttnChunk = 64;
 constexpr uint32_t kAttnMaxSplits = 16;
+constexpr uint32_t kAttnHeadChunks = 4;  // up to 4 split-sized chunks merged inside one block
 
 // With rope != nullptr (the fused decode step), q is this token's raw qkv row
 // ([Q heads | K heads | V heads]): the block rotates its query head into LDS,
@@ -279,6 +280,172 @@ __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restri
     if (tid == 0) {
         out[0] = m_run;
         out[1] = l_run;
+    }
+}
+
+// The split kernel and the merge in one launch for capacities of 2 to NG
+// chunks and heads of D = 64 or 128 dims: one block of NG x 256 threads per
+// head, thread group c (256 threads) doing what split c of a launch with
+// one chunk per split does (scores, softmax and p.V over chunk c), then the
+// groups' (m, l, p.V) merged in the block in group order as the merge
+// kernel merges splits (a group past the last chunk has m = -inf, l = 0,
+// weight 0). Every K and V row a thread uses is loaded at the start, before
+// the RoPE and the block barrier, so the block waits for one memory round
+// trip; the token's own row (len - 1 with rope), which this launch writes
+// into the caches, is taken from the block's own rotated values instead.
+// Same operations in the same order as the two launches: the output bits
+// are equal.
+template <uint32_t NG, uint32_t D>
+__global__ __launch_bounds__(256 * NG) void attn_decode_head(const float* __restrict__ q, float* __restrict__ kcache,
+                                                             float* __restrict__ vcache, uint32_t hq, uint32_t hkv,
+                                                             uint32_t len_arg, const uint32_t* __restrict__ dpos,
+                                                             float scale, const float2* __restrict__ rope,
+                                                             uint32_t half_rot, float* __restrict__ fout,
+                                                             XGroup* __restrict__ foutq,
+                                                             const float* __restrict__ gate) {
+    constexpr uint32_t D4 = D / 4;
+    constexpr uint32_t PARTS = 256 / D4;           // p.V key subsets
+    constexpr uint32_t KR = D4 / 4;                // float4 of a key per scoring lane
+    constexpr uint32_t VR = kAttnChunk / PARTS;    // value rows per p.V lane
+    const uint32_t h = blockIdx.x;
+    const uint32_t len = dpos ? *dpos + 1 : len_arg;
+    const uint32_t nchunks = (len + kAttnChunk - 1) / kAttnChunk;  // <= NG
+    const uint32_t g = h / (hq / hkv);
+    const uint32_t kvd = hkv * D;
+    const uint32_t newrow = rope ? len - 1 : 0xffffffffu;
+    __shared__ float4 qs4[D4], kn4[D4], vn4[D4];
+    __shared__ float ps[NG][kAttnChunk];
+    __shared__ float red[NG][8];
+    __shared__ float ml[NG][2];
+    __shared__ float4 accp[256 * NG];
+    __shared__ __align__(16) float vals[D];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t grp = tid >> 8, lt = tid & 255;
+    const uint32_t wave = lt >> 6, lane = tid & 63;
+    const uint32_t t0 = grp * kAttnChunk;
+    const uint32_t cnt = grp < nchunks ? min(len - t0, kAttnChunk) : 0u;
+    // Scores: key j = lt / 4, quarter qq = lt % 4 covers float4 columns qq, qq + 4, ...
+    const uint32_t j = lt >> 2, qq = lt & 3;
+    // p.V: float4 column c4, keys pp, pp + PARTS, ...
+    const uint32_t c4 = lt % D4, pp = lt / D4;
+    float4 kr[KR], vr[VR];
+    if (j < cnt && t0 + j != newrow) {
+        const float4* k = reinterpret_cast<const float4*>(kcache + static_cast<size_t>(t0 + j) * kvd + g * D);
+#pragma unroll
+        for (uint32_t r = 0; r < KR; ++r) kr[r] = k[qq + 4 * r];
+    }
+    {
+        const float4* v = reinterpret_cast<const float4*>(vcache + static_cast<size_t>(t0) * kvd + g * D) + c4;
+#pragma unroll
+        for (uint32_t r = 0; r < VR; ++r) {
+            const uint32_t jj = pp + r * PARTS;
+            if (jj < cnt && t0 + jj != newrow) vr[r] = v[static_cast<size_t>(jj) * (kvd / 4)];
+        }
+    }
+    if (rope) {
+        const float2* tab = rope + static_cast<size_t>(len - 1) * half_rot;
+        const float* kn = q + hq * D + g * D;
+        const float* vn = kn + kvd;
+        float* kc = kcache + static_cast<size_t>(len - 1) * kvd + g * D;
+        float* vc = vcache + static_cast<size_t>(len - 1) * kvd + g * D;
+        float* qs = reinterpret_cast<float*>(qs4);
+        float* ks = reinterpret_cast<float*>(kn4);
+        float* vs = reinterpret_cast<float*>(vn4);
+        for (uint32_t i = tid; i < D; i += blockDim.x) {
+            qs[i] = rope_elem(q + h * D, tab, half_rot, i);
+            const float kv = rope_elem(kn, tab, half_rot, i);
+            ks[i] = kv;
+            vs[i] = vn[i];
+            kc[i] = kv;
+            vc[i] = vn[i];
+        }
+    } else {
+        for (uint32_t i = tid; i < D4; i += blockDim.x) qs4[i] = reinterpret_cast<const float4*>(q + h * D)[i];
+    }
+    __syncthreads();
+    float s = -INFINITY;
+    {
+        float dot = 0.0f;
+        if (j < cnt) {
+            const bool own = t0 + j == newrow;
+#pragma unroll
+            for (uint32_t r = 0; r < KR; ++r) {
+                const float4 kv = own ? kn4[qq + 4 * r] : kr[r];
+                const float4 qv = qs4[qq + 4 * r];
+                dot = fmaf(kv.x, qv.x, dot);
+                dot = fmaf(kv.y, qv.y, dot);
+                dot = fmaf(kv.z, qv.z, dot);
+                dot = fmaf(kv.w, qv.w, dot);
+            }
+        }
+        dot = quad_sum(dot);
+        if (j < cnt) s = dot * scale;
+    }
+    float cm = wave_max(s);
+    if (lane == 0) red[grp][wave] = cm;
+    __syncthreads();
+    cm = fmaxf(fmaxf(red[grp][0], red[grp][1]), fmaxf(red[grp][2], red[grp][3]));  // -inf without keys
+    const float p = j < cnt ? expf(s - cm) : 0.0f;
+    if (qq == 0) ps[grp][j] = p;
+    float l = wave_sum(qq == 0 ? p : 0.0f);
+    __syncthreads();
+    if (lane == 0) red[grp][4 + wave] = l;
+    __syncthreads();
+    l = (red[grp][4] + red[grp][5]) + (red[grp][6] + red[grp][7]);
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (uint32_t r = 0; r < VR; ++r) {
+        const uint32_t jj = pp + r * PARTS;
+        if (jj < cnt) {
+            const float pj = ps[grp][jj];
+            const float4 vv = t0 + jj == newrow ? vn4[c4] : vr[r];
+            acc.x = fmaf(pj, vv.x, acc.x);
+            acc.y = fmaf(pj, vv.y, acc.y);
+            acc.z = fmaf(pj, vv.z, acc.z);
+            acc.w = fmaf(pj, vv.w, acc.w);
+        }
+    }
+    accp[tid] = acc;
+    if (lt == 0) {
+        ml[grp][0] = cnt ? cm : -INFINITY;
+        ml[grp][1] = cnt ? l : 0.0f;
+    }
+    __syncthreads();
+    // Merge: thread i < D owns output dim i, groups in order.
+    if (tid < D) {
+        const uint32_t cc = tid >> 2, comp = tid & 3;
+        float M = -INFINITY;
+#pragma unroll
+        for (uint32_t c = 0; c < NG; ++c) {
+            if (c < nchunks) M = fmaxf(M, ml[c][0]);
+        }
+        float L = 0.0f, a = 0.0f;
+#pragma unroll
+        for (uint32_t c = 0; c < NG; ++c) {
+            if (c < nchunks) {
+                float4 v = accp[c * 256 + cc];
+#pragma unroll
+                for (uint32_t k = 1; k < PARTS; ++k) {
+                    const float4 b = accp[c * 256 + k * D4 + cc];
+                    v.x += b.x;
+                    v.y += b.y;
+                    v.z += b.z;
+                    v.w += b.w;
+                }
+                const float vi = comp == 0 ? v.x : comp == 1 ? v.y : comp == 2 ? v.z : v.w;
+                const float wgt = expf(ml[c][0] - M);
+                L += ml[c][1] * wgt;
+                a += vi * wgt;
+            }
+        }
+        float v = a * (1.0f / L);
+        if (gate) v = v * sigmoid_ref(gate[h * D + tid]);
+        fout[h * D + tid] = v;
+        vals[tid] = v;
+    }
+    if (foutq) {
+        __syncthreads();
+        for (uint32_t gI = tid; gI < D / 16; gI += blockDim.x) xgroup_encode_from(vals + 16 * gI, foutq + h * (D / 16) + gI);
     }
 }
 
@@ -541,7 +708,10 @@ namespace {
 // one chunk 5.5 us against 7.6 with the merge, at two 7.7 against 8.3, but
 // each further chunk in turn costs about 2.5 us (11.4 against 8.8 at four),
 // and heads of 256 at two chunks measured 10.9 against 9.5. Beyond, one
-// split per chunk up to 16.
+// split per chunk up to 16; the launchers run 2 to 4 splits of 64- or
+// 128-dim heads as one block per head with the chunks side by side and all
+// K / V loads issued first (28 heads of 128 at four chunks: 9.8 + 4.6 us as
+// two launches, one launch about 5 us less).
 uint32_t attn_splits(size_t max_len, size_t d) {
     const size_t chunks = (max_len + kAttnChunk - 1) / kAttnChunk;
     if (chunks <= (d > 128 ? 1u : 2u)) return 1;
@@ -566,7 +736,20 @@ int launch_attn_decode(const float* q, const float* kcache, const float* vcache,
     if (outq && reinterpret_cast<uintptr_t>(outq) % 16 != 0) return kInvalidArgument;
     if (len > 0xffffffffull || capacity > 0xffffffffull || hq > 0xffffull) return kLengthError;
     const uint32_t splits = attn_splits(dpos ? capacity : len, d);
-    // Read-only use of the caches (no RoPE table): the kernel writes them only in the fused form.
+    // Read-only use of the caches (no RoPE table): the kernels write them only in the fused form.
+    if (splits >= 2 && splits <= kAttnHeadChunks && (d == 64 || d == 128)) {
+#define HIPLLM_ATTN_HEAD(D)                                                                                       \
+    HIPLLM_LAUNCH((attn_decode_head<kAttnHeadChunks, D>), dim3(static_cast<uint32_t>(hq)), dim3(256 * kAttnHeadChunks), \
+                  0, stream, q, const_cast<float*>(kcache), const_cast<float*>(vcache), static_cast<uint32_t>(hq),    \
+                  static_cast<uint32_t>(hkv), static_cast<uint32_t>(len), dpos, scale, nullptr, 0u, out, outq, nullptr)
+        if (d == 64) {
+            HIPLLM_ATTN_HEAD(64);
+        } else {
+            HIPLLM_ATTN_HEAD(128);
+        }
+#undef HIPLLM_ATTN_HEAD
+        return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+    }
     HIPLLM_LAUNCH(attn_decode_partial, dim3(static_cast<uint32_t>(hq), splits), dim3(256), 0, stream, q,
                        const_cast<float*>(kcache), const_cast<float*>(vcache), scratch, static_cast<uint32_t>(hq),
                        static_cast<uint32_t>(hkv), static_cast<uint32_t>(d), static_cast<uint32_t>(len), dpos, scale,
@@ -592,6 +775,20 @@ int launch_attn_decode_rope(const float* qkv, const float* cos_sin, size_t rot, 
     if (outq && reinterpret_cast<uintptr_t>(outq) % 16 != 0) return kInvalidArgument;
     if (pos >= 0xffffffffull || capacity > 0xffffffffull || hq > 0xffffull) return kLengthError;
     const uint32_t splits = attn_splits(dpos ? capacity : pos + 1, d);
+    if (splits >= 2 && splits <= kAttnHeadChunks && (d == 64 || d == 128)) {
+#define HIPLLM_ATTN_HEAD(D)                                                                                       \
+    HIPLLM_LAUNCH((attn_decode_head<kAttnHeadChunks, D>), dim3(static_cast<uint32_t>(hq)), dim3(256 * kAttnHeadChunks), \
+                  0, stream, qkv, kcache, vcache, static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv),             \
+                  static_cast<uint32_t>(pos + 1), dpos, scale, reinterpret_cast<const float2*>(cos_sin),              \
+                  static_cast<uint32_t>(rot / 2), out, outq, gate)
+        if (d == 64) {
+            HIPLLM_ATTN_HEAD(64);
+        } else {
+            HIPLLM_ATTN_HEAD(128);
+        }
+#undef HIPLLM_ATTN_HEAD
+        return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+    }
     HIPLLM_LAUNCH(attn_decode_partial, dim3(static_cast<uint32_t>(hq), splits), dim3(256), 0, stream, qkv,
                        kcache, vcache, scratch, static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv),
                        static_cast<uint32_t>(d), static_cast<uint32_t>(pos + 1), dpos, scale, splits,

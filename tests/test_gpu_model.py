@@ -60,6 +60,23 @@ def test_qwen05b_greedy_tokens_match_reference(cuda, golden_model, batched):
     assert err.max() <= LOGIT_BOUND[batched]
 
 
+def test_attention_head_kernel_matches_split_kernel(cuda, golden_model):
+    """Decode attention at a capacity of 2 to 4 chunks of 64 keys runs one
+    block per head that merges its chunks in LDS; at larger capacities one
+    block per chunk and a merge launch. Both compute each chunk and the
+    merge the same way, so a decode crossing from 2 into 3 and 4 chunks gives
+    the same tokens and logit bits at capacity 256 as at capacity 1024."""
+    path, g = golden_model("qwen2.5-0.5b")
+    prompt = (list(g["prompt"]) * 40)[:100]
+    runs = []
+    for cap in (256, 1024):
+        with HipLLM(path, cap) as m:
+            toks, logits = run_with_logits(m, prompt, 120)
+        runs.append((toks, logits))
+    assert runs[0][0] == runs[1][0]
+    assert np.array_equal(runs[0][1].view(np.int32), runs[1][1].view(np.int32))
+
+
 def test_batched_prefill_is_default_and_switchable(cuda, golden_model):
     path, g = golden_model("tiny")
     with HipLLM(path, 64) as m:
