@@ -107,6 +107,26 @@ int hipllm_gemv_prepped(uint32_t type, const void* w, size_t row_bytes, const fl
 size_t hipllm_x16_bytes(uint32_t type, size_t n, size_t k);
 int hipllm_pack_x16(uint32_t type, const void* w, size_t row_bytes, size_t n, size_t k, void* packed, void* stream);
 
+/* An RMSNorm (cpu_llm.cpp:143-166) fused into an x16 GEMV; every field is
+ * nullable and a null `norm` argument means none.
+ * - Before the product (sumsq_in, eps; k <= 8192): xq holds the XGroup form
+ *   of x * gamma for the raw row x, sumsq_in its k / 16 per-16-value sums of
+ *   squares in double; the products are scaled by 1 / sqrt(mean + eps), so
+ *   y = W (x * inv_rms * gamma) (+ bias) (+ residual), up to FP32 rounding.
+ * - After the product (gamma_out, yq_out, sumsq_out; hipllm_gemv_x16 only,
+ *   n % 16 == 0): y as usual, plus the XGroup form of y * gamma_out and the
+ *   n / 16 double sums of squares of y: the input of a launch with a norm
+ *   before its product.
+ * Replaces the RMSNorm dispatches around the decode GEVMs
+ * (metal_llm.mm:2776-2790, 2838-2848; metal_llm.metal:785-823). */
+typedef struct HipllmX16Norm {
+    const double* sumsq_in;
+    float eps;
+    const float* gamma_out;
+    void* yq_out;
+    double* sumsq_out;
+} HipllmX16Norm;
+
 /* Decode GEMV y = W x (+ bias) (+ residual) over x16-packed Q4_K or Q6_K
  * weights, with the integer products of the XGroup digits on the int8
  * matrix cores (v_mfma_i32_16x16x64_i8); xq as for hipllm_gemv_prepped.
@@ -120,16 +140,16 @@ int hipllm_pack_x16(uint32_t type, const void* w, size_t row_bytes, size_t n, si
  * encode_vector_product (metal_llm.metal:708-781; metal_llm.mm:1891-1999)
  * and gevmt for Q4_K / Q6_K rows (cpu_llm.cpp:512-547). */
 int hipllm_gemv_x16(uint32_t type, const void* packed, const void* xq, const float* bias, const float* residual,
-                    float* y, size_t n, size_t k, int waves, void* stream);
+                    float* y, size_t n, size_t k, int waves, const HipllmX16Norm* norm, void* stream);
 
 /* The FFN gate/up pair over x16-packed weights of one type in one launch:
  * y = silu(Wg x) * (Wu x) (the sign-branched SiLU of cpu_llm.cpp:188-202),
  * and yq (nullable; n % 16 == 0) its XGroup form for the down projection.
- * Same launch shapes as hipllm_gemv_x16. Replaces the gate / up GEVMs and
- * SwiGLU of encode_decode_layer (metal_llm.mm:2850-2890;
- * metal_llm.metal:708-781). */
+ * Same launch shapes as hipllm_gemv_x16; `norm` as there (a norm before
+ * the products only). Replaces the gate / up GEVMs and SwiGLU of
+ * encode_decode_layer (metal_llm.mm:2850-2890; metal_llm.metal:708-781). */
 int hipllm_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, const void* xq, float* y, void* yq,
-                           size_t n, size_t k, int waves, void* stream);
+                           size_t n, size_t k, int waves, const HipllmX16Norm* norm, void* stream);
 
 /* hipllm_rmsnorm of the raw row x (gain gamma, k <= 8192, x and gamma
  * 16-byte aligned) followed by hipllm_gemv_prepped, in one launch: every
@@ -572,6 +592,15 @@ int hipllm_set_decode_graphs(HipllmModel* model, int enabled);
  * HIPLLM_INVALID_ARGUMENT when the model has nothing to pack or is not
  * qwen2. No counterpart in the reference (a layout of this backend). */
 int hipllm_set_packed_decode(HipllmModel* model, int enabled);
+/* qwen2 only: 1 (default) = decode RMSNorms folded into the neighbouring
+ * GEMVs where the model's forms allow (the GEMV prologue for rows of up to
+ * 2048 values on GGUF rows; with x16 copies of every projection, the norm
+ * data written by the attention output / FFN down GEMVs and applied by QKV,
+ * gate / up and the LM head, HipllmX16Norm), 0 = every norm is its own
+ * launch (hipllm_rmsnorm). Results agree to FP32 rounding. Replaces the
+ * RMSNorm dispatches of encode_decode_layer (metal_llm.mm:2776-2848); no
+ * counterpart switch exists there. */
+int hipllm_set_fused_norms(HipllmModel* model, int enabled);
 /* qwen35moe only: expert ids chosen for the last row of the last forward,
  * [layer_count, expert_used_count] (MoeLLM keeps them in RouteIds,
  * moe_llm.mm:2919-2925). */

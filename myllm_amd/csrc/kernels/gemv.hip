@@ -1225,14 +1225,23 @@ struct X16<kQ6_K> {
 // row): w2 is the up matrix in the same form, y = silu(W x) * (W2 x) (the
 // reference's SwiGLU, cpu_llm.cpp:188-202) and yq (nullable) receives the
 // XGroup form of y, one group per 16-row tile (the down projection's input).
-template <uint32_t QT, int WPB, int RT, int MODE>
+// NORM 1 (an RMSNorm before the product): xq holds the XGroup form of
+// x * gamma for the raw row x, nrm.sumsq_in its per-16-value sums of squares
+// (k / 16 doubles, as a NORM 2 launch writes them); the block reduces them in
+// a fixed order (wave 0, lanes strided, then the wave sum) to inv = 1 /
+// sqrt(mean + eps) and scales the products by it: W (x * inv * gamma). NORM 2
+// (MODE 0; an RMSNorm after y, n % 16 == 0): each 16-row tile of y also
+// writes the XGroup form of y * nrm.gamma_out and the double sum of squares
+// of its 16 values (in row order), the input of a NORM 1 launch.
+template <uint32_t QT, int WPB, int RT, int MODE, int NORM>
 __global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __restrict__ w,
                                                             const uint8_t* __restrict__ w2,
                                                             const XGroup* __restrict__ xq,
                                                             const float* __restrict__ bias,
                                                             const float* __restrict__ residual,
                                                             float* __restrict__ y, XGroup* __restrict__ yq,
-                                                            uint32_t n, uint32_t units) {
+                                                            uint32_t n, uint32_t units, X16Norm nrm) {
+    static_assert(NORM != 2 || MODE == 0, "the output norm data comes from plain GEMVs");
     using F = X16<QT>;
     constexpr uint32_t kTileUnit = 16 * F::kBlock;
     constexpr int NM = MODE == 1 ? 2 : 1;  // matrices
@@ -1285,6 +1294,25 @@ __global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __res
     // sits under a branch that the last pass skips, and the compiler's waits
     // then cover every load in flight.)
     if (mine > 0) fill(0);
+    __shared__ float inv_s;
+    if (NORM == 1 && wave == 0) {
+        // Up to 512 partials (k <= 8192), all loads issued before the sum.
+        const uint32_t tiles_in = 16 * units;
+        double v[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t i = lane + 64 * t;
+            v[t] = i < tiles_in ? nrm.sumsq_in[i] : 0.0;
+        }
+        double ss = v[0];
+#pragma unroll
+        for (int t = 1; t < 8; ++t) ss += v[t];
+        ss = wave_sum_d(ss);
+        if (lane == 0) {
+            const float ms = static_cast<float>(ss / static_cast<double>(256 * units));
+            inv_s = 1.0f / sqrtf(ms + nrm.eps);
+        }
+    }
     for (uint32_t idx = 0; idx < mine; ++idx) {
         *reinterpret_cast<uint4*>(lds + 16 * lane) = sl.x;
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -1309,10 +1337,12 @@ __global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __res
         float v = part[0][tid];
 #pragma unroll
         for (int i = 1; i < WPB; ++i) v += part[i][tid];
+        if (NORM == 1) v *= inv_s;
         if (MODE == 1) {
             float u = part[0][16 * RT + tid];
 #pragma unroll
             for (int i = 1; i < WPB; ++i) u += part[i][16 * RT + tid];
+            if (NORM == 1) u *= inv_s;
             v = row < n ? silu_mul(v, u) : 0.0f;
             part[0][tid] = v;  // the tile's outputs, for the XGroup encoding below
         } else if (row < n) {
@@ -1320,10 +1350,28 @@ __global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __res
             if (residual) v += residual[row];
         }
         if (row < n) y[row] = v;
+        if (NORM == 2) {
+            // Each thread rewrites only its own slots, after reading them.
+            part[0][tid] = row < n ? v * nrm.gamma_out[row] : 0.0f;
+            part[1][tid] = row < n ? v : 0.0f;
+        }
     }
     if (MODE == 1 && yq) {
         __syncthreads();
         if (tid < static_cast<uint32_t>(RT) && (tile0 + tid) * 16 < n) xgroup_encode_from(&part[0][16 * tid], yq + tile0 + tid);
+    }
+    if (NORM == 2) {
+        __syncthreads();
+        if (tid < static_cast<uint32_t>(RT) && (tile0 + tid) * 16 < n) {
+            xgroup_encode_from(&part[0][16 * tid], nrm.yq_out + tile0 + tid);
+            double ss = 0.0;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const double t = part[1][16 * tid + i];
+                ss += t * t;
+            }
+            nrm.sumsq_out[tile0 + tid] = ss;
+        }
     }
 }
 
@@ -1474,15 +1522,16 @@ int launch_pack_x16(uint32_t type, const void* w, size_t row_bytes, size_t n, si
 }
 
 namespace {
-template <uint32_t QT, int MODE>
+template <uint32_t QT, int MODE, int NORM>
 int launch_x16(int code, const uint8_t* wp, const uint8_t* wp2, const XGroup* xq, const float* bias,
-               const float* residual, float* y, XGroup* yq, uint32_t nn, uint32_t units, hipStream_t stream) {
+               const float* residual, float* y, XGroup* yq, uint32_t nn, uint32_t units, const X16Norm& nrm,
+               hipStream_t stream) {
     const uint32_t tiles = (nn + 15) / 16;
     switch (code) {
 #define HIPLLM_X16_CASE(RT, W)                                                                                      \
     case 1000 * RT + 100 + W:                                                                                       \
-        HIPLLM_LAUNCH((gemv_x16_kernel<QT, W, RT, MODE>), dim3((tiles + RT - 1) / RT), dim3(64 * W), 0, stream, wp, wp2, \
-                      xq, bias, residual, y, yq, nn, units);                                                        \
+        HIPLLM_LAUNCH((gemv_x16_kernel<QT, W, RT, MODE, NORM>), dim3((tiles + RT - 1) / RT), dim3(64 * W), 0, stream, \
+                      wp, wp2, xq, bias, residual, y, yq, nn, units, nrm);                                           \
         break;
         HIPLLM_X16_CASE(1, 4)
         HIPLLM_X16_CASE(1, 8)
@@ -1507,30 +1556,63 @@ int check_x16(uint32_t type, const void* packed, const XGroup* xq, const float* 
 }
 }  // namespace
 
+namespace {
+// norm: nullptr or neither input nor output form -> 0; sumsq_in -> 1 (k <= 8192);
+// gamma_out -> 2 (plain GEMV, n % 16 == 0, yq_out 16-byte aligned, sumsq_out);
+// -1 when the combination is not offered.
+int x16_norm_kind(const X16Norm* norm, int mode, size_t n, size_t k) {
+    if (!norm || (!norm->sumsq_in && !norm->gamma_out)) return 0;
+    if (norm->sumsq_in && norm->gamma_out) return -1;
+    if (norm->sumsq_in) return k <= 8192 ? 1 : -1;
+    if (mode != 0 || n % 16 != 0 || !norm->yq_out || !norm->sumsq_out) return -1;
+    if (reinterpret_cast<uintptr_t>(norm->yq_out) % 16 != 0) return -1;
+    return 2;
+}
+
+template <uint32_t QT, int MODE>
+int launch_x16_norm(int kind, int code, const uint8_t* wp, const uint8_t* wp2, const XGroup* xq, const float* bias,
+                    const float* residual, float* y, XGroup* yq, uint32_t nn, uint32_t units, const X16Norm* norm,
+                    hipStream_t stream) {
+    const X16Norm nrm = norm ? *norm : X16Norm{};
+    if (kind == 1) return launch_x16<QT, MODE, 1>(code, wp, wp2, xq, bias, residual, y, yq, nn, units, nrm, stream);
+    if constexpr (MODE == 0) {
+        if (kind == 2) return launch_x16<QT, 0, 2>(code, wp, wp2, xq, bias, residual, y, yq, nn, units, nrm, stream);
+    }
+    return launch_x16<QT, MODE, 0>(code, wp, wp2, xq, bias, residual, y, yq, nn, units, nrm, stream);
+}
+}  // namespace
+
 int launch_gemv_x16(uint32_t type, const void* packed, const XGroup* xq, const float* bias, const float* residual,
-                    float* y, size_t n, size_t k, int waves, hipStream_t stream) {
+                    float* y, size_t n, size_t k, int waves, hipStream_t stream, const X16Norm* norm) {
     const int rc = check_x16(type, packed, xq, y, n, k);
     if (rc != kOk) return rc;
+    const int kind = x16_norm_kind(norm, 0, n, k);
+    if (kind < 0) return kInvalidArgument;
     const uint32_t units = static_cast<uint32_t>(k / 256), nn = static_cast<uint32_t>(n);
     const int code = waves ? waves : x16_default_waves(nn, units, 0);
     const auto* wp = static_cast<const uint8_t*>(packed);
     return type == kQ4_K
-               ? launch_x16<kQ4_K, 0>(code, wp, nullptr, xq, bias, residual, y, nullptr, nn, units, stream)
-               : launch_x16<kQ6_K, 0>(code, wp, nullptr, xq, bias, residual, y, nullptr, nn, units, stream);
+               ? launch_x16_norm<kQ4_K, 0>(kind, code, wp, nullptr, xq, bias, residual, y, nullptr, nn, units, norm,
+                                           stream)
+               : launch_x16_norm<kQ6_K, 0>(kind, code, wp, nullptr, xq, bias, residual, y, nullptr, nn, units, norm,
+                                           stream);
 }
 
 int launch_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, const XGroup* xq, float* y, XGroup* yq,
-                           size_t n, size_t k, int waves, hipStream_t stream) {
+                           size_t n, size_t k, int waves, hipStream_t stream, const X16Norm* norm) {
     int rc = check_x16(type, gate, xq, y, n, k);
     if (rc == kOk) rc = check_x16(type, up, xq, y, n, k);
     if (rc != kOk) return rc;
     if (yq && (n % 16 != 0 || reinterpret_cast<uintptr_t>(yq) % 16 != 0)) return kInvalidArgument;
+    const int kind = x16_norm_kind(norm, 1, n, k);
+    if (kind < 0) return kInvalidArgument;
     const uint32_t units = static_cast<uint32_t>(k / 256), nn = static_cast<uint32_t>(n);
     const int code = waves ? waves : x16_default_waves(nn, units, 1);
     const auto* g = static_cast<const uint8_t*>(gate);
     const auto* u = static_cast<const uint8_t*>(up);
-    return type == kQ4_K ? launch_x16<kQ4_K, 1>(code, g, u, xq, nullptr, nullptr, y, yq, nn, units, stream)
-                         : launch_x16<kQ6_K, 1>(code, g, u, xq, nullptr, nullptr, y, yq, nn, units, stream);
+    return type == kQ4_K
+               ? launch_x16_norm<kQ4_K, 1>(kind, code, g, u, xq, nullptr, nullptr, y, yq, nn, units, norm, stream)
+               : launch_x16_norm<kQ6_K, 1>(kind, code, g, u, xq, nullptr, nullptr, y, yq, nn, units, norm, stream);
 }
 
 // GEMV over a prepared XGroup input. tiling 0 selects the default.

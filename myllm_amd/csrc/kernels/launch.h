@@ -104,10 +104,20 @@ int launch_gemv_batched(uint32_t type, const void* w, const void* wu, size_t row
 size_t x16_bytes(uint32_t type, size_t n, size_t k);
 int launch_pack_x16(uint32_t type, const void* w, size_t row_bytes, size_t n, size_t k, void* packed,
                     hipStream_t stream);
+// An RMSNorm fused into an x16 GEMV (all fields nullable): sumsq_in / eps for
+// a norm before the product (xq then holds x * gamma), gamma_out / yq_out /
+// sumsq_out for the data of a norm after y (plain GEMV only).
+struct X16Norm {
+    const double* sumsq_in;
+    float eps;
+    const float* gamma_out;
+    XGroup* yq_out;
+    double* sumsq_out;
+};
 int launch_gemv_x16(uint32_t type, const void* packed, const XGroup* xq, const float* bias, const float* residual,
-                    float* y, size_t n, size_t k, int waves, hipStream_t stream);
+                    float* y, size_t n, size_t k, int waves, hipStream_t stream, const X16Norm* norm = nullptr);
 int launch_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, const XGroup* xq, float* y, XGroup* yq,
-                           size_t n, size_t k, int waves, hipStream_t stream);
+                           size_t n, size_t k, int waves, hipStream_t stream, const X16Norm* norm = nullptr);
 
 int gemm_default_tile(uint32_t m, uint32_t n, uint32_t k);
 uint32_t gemm_default_splits(uint32_t m, uint32_t n, uint32_t k, int tile);

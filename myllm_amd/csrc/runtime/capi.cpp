@@ -220,18 +220,30 @@ int hipllm_pack_x16(uint32_t type, const void* w, size_t row_bytes, size_t n, si
                   "16-byte and Q6_K rows 2-byte aligned) or launch failure");
 }
 
+namespace {
+hipllm::X16Norm x16_norm(const HipllmX16Norm* n) {
+    return hipllm::X16Norm{n->sumsq_in, n->eps, n->gamma_out, static_cast<hipllm::XGroup*>(n->yq_out), n->sumsq_out};
+}
+}  // namespace
+
 int hipllm_gemv_x16(uint32_t type, const void* packed, const void* xq, const float* bias, const float* residual,
-                    float* y, size_t n, size_t k, int waves, void* stream) {
-    return status(hipllm::launch_gemv_x16(type, packed, xgc(xq), bias, residual, y, n, k, waves, as_stream(stream)),
+                    float* y, size_t n, size_t k, int waves, const HipllmX16Norm* norm, void* stream) {
+    const hipllm::X16Norm nrm = norm ? x16_norm(norm) : hipllm::X16Norm{};
+    return status(hipllm::launch_gemv_x16(type, packed, xgc(xq), bias, residual, y, n, k, waves, as_stream(stream),
+                                          norm ? &nrm : nullptr),
                   "hipllm_gemv_x16: invalid arguments (Q4_K or Q6_K, k % 256 == 0, a known launch shape, 16-byte "
-                  "aligned buffers) or launch failure");
+                  "aligned buffers, a norm before (k <= 8192) or after (n % 16 == 0) the product, not both) or launch "
+                  "failure");
 }
 
 int hipllm_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, const void* xq, float* y, void* yq,
-                           size_t n, size_t k, int waves, void* stream) {
-    return status(hipllm::launch_gemv_x16_swiglu(type, gate, up, xgc(xq), y, xg(yq), n, k, waves, as_stream(stream)),
+                           size_t n, size_t k, int waves, const HipllmX16Norm* norm, void* stream) {
+    const hipllm::X16Norm nrm = norm ? x16_norm(norm) : hipllm::X16Norm{};
+    return status(hipllm::launch_gemv_x16_swiglu(type, gate, up, xgc(xq), y, xg(yq), n, k, waves, as_stream(stream),
+                                                 norm ? &nrm : nullptr),
                   "hipllm_gemv_x16_swiglu: invalid arguments (Q4_K or Q6_K, k % 256 == 0, n % 16 == 0 with yq, a "
-                  "known launch shape, 16-byte aligned buffers) or launch failure");
+                  "known launch shape, 16-byte aligned buffers, only a norm before the products, k <= 8192) or "
+                  "launch failure");
 }
 
 int hipllm_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m, size_t k, void* stream) {
@@ -473,6 +485,12 @@ int hipllm_disable_profiling(HipllmModel* m) {
 int hipllm_copy_logits(const HipllmModel* m, float* out, size_t count) {
     if (!m || !out) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_copy_logits: null argument");
     return guarded([&] { m->visit([&](const auto& b) { b.copy_last_logits(out, count); }); });
+}
+
+int hipllm_set_fused_norms(HipllmModel* m, int enabled) {
+    if (!m) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_set_fused_norms: null argument");
+    if (!m->dense) return fail(HIPLLM_INVALID_ARGUMENT, "hipllm_set_fused_norms: qwen2 models only");
+    return guarded([&] { m->dense->set_fused_norms(enabled != 0); });
 }
 
 int hipllm_set_packed_decode(HipllmModel* m, int enabled) {

@@ -62,6 +62,7 @@ struct Activations {
     std::int32_t* ids = nullptr;
     std::uint32_t* token = nullptr;
     std::uint32_t* step = nullptr;  // decode step inputs: [token id, position]
+    double* sumsq = nullptr;        // per-16-value sums of squares of the row to normalise next
 };
 
 // Device buffers of the batched prefill: T prompt rows each.
@@ -96,6 +97,11 @@ struct HipLLM::Impl {
     // -7% with both GEMVs fused, 7B 0% and 14B -5% with the QKV one alone).
     bool fused_norms = false;
     bool fused_ffn_norm = false;
+    // The RMSNorms between x16 GEMVs ride in them: the attention output and
+    // FFN down GEMVs write the next norm's input data, QKV, gate / up and the
+    // LM head apply it.
+    bool norm_epilogues = false;
+    bool norm_fusion = true;  // switch for both fused forms
 
     WeightArena weights;
     std::size_t weight_bytes = 0;  // sum of GGUF tensor payloads
@@ -178,7 +184,7 @@ struct HipLLM::Impl {
     void prefill_layer(std::size_t li, std::size_t rows, float* hidden, float* next_hidden);
     void prefill_batched(std::size_t rows);
     void head_step(const float* hidden_row);
-    void head_logits();
+    void head_logits(bool norm_in = false);
     std::int32_t read_token();
 };
 
@@ -232,8 +238,12 @@ void HipLLM::Impl::choose_decode_forms() {
         return t == hipllm::kQ4_K || t == hipllm::kQ6_K || t == hipllm::kQ8_0 || t == hipllm::kQ5_0;
     };
     const std::size_t H = config.embedding_size;
-    fused_norms = H % 16 == 0 && H <= 2048 && !packed_decode;
+    fused_norms = norm_fusion && H % 16 == 0 && H <= 2048 && !packed_decode;
     fused_ffn_norm = fused_norms;
+    norm_epilogues = norm_fusion && packed_decode && H % 16 == 0 && H <= 8192 && output_x16 != nullptr;
+    for (const DevLayer& L : layers) {
+        norm_epilogues = norm_epilogues && L.qkv_x16 && L.o_x16 && L.gate_x16 && L.down_x16;
+    }
     for (const DevLayer& L : layers) {
         fused_norms = fused_norms && L.fused_qkv && quantized(L.q.type);
         fused_ffn_norm = fused_ffn_norm && L.fused_gate_up && quantized(L.gate.type);
@@ -412,7 +422,7 @@ void HipLLM::Impl::ensure_prompt_capacity(std::size_t n) {
                       o_as = reserve(hipllm::attn_decode_scratch_floats(c.attention_head_count, c.head_size,
                                                                           max_sequence) * 4),
                       o_am = reserve(hipllm::argmax_scratch_bytes(V)), o_ids = reserve(n * 4), o_tok = reserve(64),
-                      o_step = reserve(16);
+                      o_step = reserve(16), o_ssq = reserve((H + 15) / 16 * sizeof(double));
     act_bytes = off;
     hip_check(hipMalloc(&act_arena, act_bytes), "hipMalloc(activations)");
     auto* base = static_cast<std::uint8_t*>(act_arena);
@@ -432,6 +442,7 @@ void HipLLM::Impl::ensure_prompt_capacity(std::size_t n) {
     act.ids = reinterpret_cast<std::int32_t*>(base + o_ids);
     act.token = reinterpret_cast<std::uint32_t*>(base + o_tok);
     act.step = reinterpret_cast<std::uint32_t*>(base + o_step);
+    act.sumsq = reinterpret_cast<double*>(base + o_ssq);
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&host_ids), n * 4, hipHostMallocDefault), "hipHostMalloc(ids)");
     prompt_capacity = n;
 }
@@ -474,10 +485,25 @@ void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, fl
     const DevLayer& L = layers[li];
     const std::size_t H = c.embedding_size, F = c.feed_forward_size;
     const float eps = c.norm_epsilon;
+    // Norm data that the x16 GEMVs pass along (norm_epilogues): the sums of
+    // squares of the row, its XGroup form times the gain in act.normq.
+    hipllm::X16Norm norm_in{};
+    norm_in.sumsq_in = act.sumsq;
+    norm_in.eps = eps;
+    auto norm_out = [&](const float* gamma) {
+        hipllm::X16Norm o{};
+        o.gamma_out = gamma;
+        o.yq_out = act.normq;
+        o.sumsq_out = act.sumsq;
+        return o;
+    };
     if (packed_decode && L.qkv_x16) {
-        // act.normq holds the XGroup form of rmsnorm(hidden) * attn_norm.
+        // act.normq holds the XGroup form of rmsnorm(hidden) * attn_norm, or
+        // (norm_epilogues past layer 0) of hidden * attn_norm with the sums
+        // of squares of hidden.
+        const bool in = norm_epilogues && li > 0;
         launch_check(hipllm::launch_gemv_x16(L.q.type, L.qkv_x16, act.normq, L.qkv_bias, nullptr, act.qkv,
-                                             H + 2 * kv_dim, H, 0, stream),
+                                             H + 2 * kv_dim, H, 0, stream, in ? &norm_in : nullptr),
                      "QKV GEMV");
     } else if (fused_norms) {
         // QKV of rmsnorm(hidden) * attn_norm, the norm in the GEMV's prologue.
@@ -492,21 +518,26 @@ void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, fl
         gemv(L.k, act.norm, act.normq, L.qkv_bias + H, nullptr, act.qkv + H);
         gemv(L.v, act.norm, act.normq, L.qkv_bias + H + kv_dim, nullptr, act.qkv + H + kv_dim);
     }
-    // RoPE of Q and K, the KV-cache write and the attention in one launch
-    // pair (partials, merge).
+    // RoPE of Q and K, the KV-cache write and the attention: one launch for
+    // short capacities, else a launch pair (partials, merge).
     const float scale = 1.0f / std::sqrt(static_cast<float>(c.head_size));
     launch_check(hipllm::launch_attn_decode_rope(act.qkv, rope_table, c.rotary_dimension, kcache(li), vcache(li),
                                                  act.attn, act.attnq, act.attn_scratch, c.attention_head_count,
                                                  c.kv_head_count, c.head_size, pos, scale, stream, dpos, max_sequence),
                  "RoPE/KV write + attention");
     if (packed_decode && L.o_x16) {
+        const hipllm::X16Norm out = norm_out(L.ffn_norm);
         launch_check(hipllm::launch_gemv_x16(L.o.type, L.o_x16, act.attnq, nullptr, hidden, next_hidden, H, H, 0,
-                                             stream),
+                                             stream, norm_epilogues ? &out : nullptr),
                      "attention output GEMV");
     } else {
         gemv(L.o, act.attn, act.attnq, nullptr, hidden, next_hidden);
     }
-    if (fused_ffn_norm) {
+    if (norm_epilogues) {
+        launch_check(hipllm::launch_gemv_x16_swiglu(L.gate.type, L.gate_x16, L.up_x16, act.normq, act.ffn, act.ffnq, F,
+                                                    H, 0, stream, &norm_in),
+                     "gate/up GEMV");
+    } else if (fused_ffn_norm) {
         launch_check(hipllm::launch_gemv_swiglu_norm(L.gate.type, L.gate.ptr, L.up.ptr, L.gate.row_bytes, next_hidden,
                                                      L.ffn_norm, eps, act.ffn, act.ffnq, F, H, 0, stream),
                      "gate/up GEMV");
@@ -530,16 +561,18 @@ void HipLLM::Impl::layer_step(std::size_t li, std::size_t pos, float* hidden, fl
     }
     // The layer output lands back in `hidden`, followed by its RMSNorm with
     // the next layer's attention gain (or the output norm after the last),
-    // unless the next layer's QKV GEMV normalises it itself.
+    // unless the next layer's QKV GEMV normalises it itself (its prologue, or
+    // the norm data of this GEMV's epilogue).
+    const float* next_gamma = li + 1 < layers.size() ? layers[li + 1].attn_norm : output_norm;
     if (packed_decode && L.down_x16) {
+        const hipllm::X16Norm out = norm_out(next_gamma);
         launch_check(hipllm::launch_gemv_x16(L.down.type, L.down_x16, act.ffnq, nullptr, next_hidden, hidden, H, F, 0,
-                                             stream),
+                                             stream, norm_epilogues ? &out : nullptr),
                      "down GEMV");
     } else {
         gemv(L.down, act.ffn, act.ffnq, nullptr, next_hidden, hidden);
     }
-    if (!fused_norms || li + 1 == layers.size()) {
-        const float* next_gamma = li + 1 < layers.size() ? layers[li + 1].attn_norm : output_norm;
+    if (!norm_epilogues && (!fused_norms || li + 1 == layers.size())) {
         launch_check(hipllm::launch_rmsnorm(hidden, next_gamma, act.norm, act.normq, 1, H, eps, stream), "RMSNorm");
     }
 }
@@ -559,8 +592,9 @@ void HipLLM::Impl::token_step(const std::int32_t* device_id, std::size_t pos, bo
                      "RMSNorm");
     }
     for (std::size_t l = 0; l < layers.size(); ++l) layer_step(l, pos, h, tmp, dpos);
-    // The last layer's down GEMV already applied the output norm.
-    if (head) head_logits();
+    // The last layer already produced the output norm's input (normalised,
+    // or with the norm data for the LM head GEMV).
+    if (head) head_logits(norm_epilogues);
 }
 
 // Records one decode step (embedding of act.step[0] at position act.step[1],
@@ -690,12 +724,17 @@ void HipLLM::Impl::head_step(const float* hidden_row) {
     head_logits();
 }
 
-// LM head and argmax on the normalised row in act.norm / act.normq.
-void HipLLM::Impl::head_logits() {
+// LM head and argmax on the normalised row in act.norm / act.normq, or
+// (norm_in) on act.normq = XGroup(hidden * output_norm) with the sums of
+// squares of hidden in act.sumsq.
+void HipLLM::Impl::head_logits(bool norm_in) {
     const GgufModelConfig& c = config;
     if (packed_decode && output_x16) {
+        hipllm::X16Norm in{};
+        in.sumsq_in = act.sumsq;
+        in.eps = c.norm_epsilon;
         launch_check(hipllm::launch_gemv_x16(output.type, output_x16, act.normq, nullptr, nullptr, act.logits,
-                                             c.vocabulary_size, c.embedding_size, 0, stream),
+                                             c.vocabulary_size, c.embedding_size, 0, stream, norm_in ? &in : nullptr),
                      "LM head GEMV");
     } else {
         gemv(output, act.norm, act.normq, nullptr, nullptr, act.logits);
@@ -935,6 +974,16 @@ void HipLLM::set_packed_decode(bool enabled) {
 }
 
 bool HipLLM::packed_decode() const noexcept { return impl_ && impl_->packed_decode; }
+
+void HipLLM::set_fused_norms(bool enabled) {
+    if (!impl_) throw std::runtime_error("HIP model is not initialized");
+    hip_check(hipStreamSynchronize(impl_->stream), "hipStreamSynchronize");
+    impl_->norm_fusion = enabled;
+    impl_->choose_decode_forms();
+    impl_->drop_decode_graph();  // recorded with the other forms
+}
+
+bool HipLLM::fused_norms() const noexcept { return impl_ && (impl_->fused_norms || impl_->norm_epilogues); }
 
 void HipLLM::set_batched_prefill(bool enabled) {
     if (!impl_) throw std::runtime_error("HIP model is not initialized");

@@ -69,6 +69,13 @@ public:
     // on the GGUF rows (the vector GEMV). Results agree to FP32 rounding.
     void set_packed_decode(bool enabled);
     bool packed_decode() const noexcept;
+    // Decode RMSNorms folded into the neighbouring GEMVs where the model's
+    // forms allow (true, default): the GEMV prologue for rows of up to 2048
+    // values on GGUF rows, or the x16 GEMVs' norm data (producer epilogue,
+    // consumer scaling); false = every norm is its own launch. Results agree
+    // to FP32 rounding.
+    void set_fused_norms(bool enabled);
+    bool fused_norms() const noexcept;
 
 private:
     struct Impl;

@@ -89,8 +89,8 @@ SIGNATURES = {
     "hipllm_to_f16": (_I, [_P, _S, _P, _P, _S, _S, _P]),
     "hipllm_x16_bytes": (_S, [_U32, _S, _S]),
     "hipllm_pack_x16": (_I, [_U32, _P, _S, _S, _S, _P, _P]),
-    "hipllm_gemv_x16": (_I, [_U32, _P, _P, _P, _P, _P, _S, _S, _I, _P]),
-    "hipllm_gemv_x16_swiglu": (_I, [_U32, _P, _P, _P, _P, _P, _S, _S, _I, _P]),
+    "hipllm_gemv_x16": (_I, [_U32, _P, _P, _P, _P, _P, _S, _S, _I, _P, _P]),
+    "hipllm_gemv_x16_swiglu": (_I, [_U32, _P, _P, _P, _P, _P, _S, _S, _I, _P, _P]),
     "hipllm_gemm_mfma": (_I, [_U32, _P, _S, _P, _P, _P, _P, _P, _S, _S, _S, _I, _I, _P, _S, _P]),
     "hipllm_gemm_mfma_workspace_bytes": (_S, [_S, _S, _S, _I, _I]),
     "hipllm_gemm_workspace_bytes": (_S, [_S, _S]),
@@ -160,6 +160,7 @@ SIGNATURES = {
     "hipllm_set_batched_prefill": (_I, [_P, _I]),
     "hipllm_set_decode_graphs": (_I, [_P, _I]),
     "hipllm_set_packed_decode": (_I, [_P, _I]),
+    "hipllm_set_fused_norms": (_I, [_P, _I]),
     "hipllm_inspect_gguf": (_I, [ctypes.c_char_p, ctypes.POINTER(HipllmConfig)]),
     "hipllm_tokenizer_create": (_I, [ctypes.POINTER(ctypes.c_char_p), _S, ctypes.POINTER(ctypes.c_char_p), _S,
                                      ctypes.c_char_p, ctypes.POINTER(_P)]),
@@ -293,6 +294,9 @@ class HipLLM:
 
     def set_packed_decode(self, enabled: bool) -> None:
         check(lib().hipllm_set_packed_decode(self._h, int(bool(enabled))))
+
+    def set_fused_norms(self, enabled: bool) -> None:
+        check(lib().hipllm_set_fused_norms(self._h, int(bool(enabled))))
 
     def set_decode_graphs(self, enabled: bool) -> None:
         """True (default): each decode step replays one recorded HIP graph."""
@@ -552,14 +556,33 @@ def _k_pack_x16(qtype, w, row_bytes, n, k, packed, stream=None):
     check(lib().hipllm_pack_x16(qtype, _ptr(w), row_bytes, n, k, _ptr(packed), _stream(stream)))
 
 
-def _k_gemv_x16(qtype, packed, xq, bias, residual, y, n, k, waves=0, stream=None):
+class HipllmX16Norm(ctypes.Structure):
+    """An RMSNorm fused into an x16 GEMV (include/hipllm.h)."""
+    _fields_ = [("sumsq_in", ctypes.c_void_p), ("eps", ctypes.c_float), ("gamma_out", ctypes.c_void_p),
+                ("yq_out", ctypes.c_void_p), ("sumsq_out", ctypes.c_void_p)]
+
+
+def _x16_norm(norm):
+    """norm: None or a dict with sumsq_in / eps, or gamma_out / yq_out / sumsq_out (tensors)."""
+    if norm is None:
+        return None
+    def addr(name):
+        t = norm.get(name)
+        return None if t is None else t.data_ptr()
+
+    n = HipllmX16Norm(addr("sumsq_in"), float(norm.get("eps", 0.0)), addr("gamma_out"), addr("yq_out"),
+                      addr("sumsq_out"))
+    return ctypes.byref(n)
+
+
+def _k_gemv_x16(qtype, packed, xq, bias, residual, y, n, k, waves=0, stream=None, norm=None):
     check(lib().hipllm_gemv_x16(qtype, _ptr(packed), _ptr(xq), _ptr(bias), _ptr(residual), _ptr(y), n, k, waves,
-                                _stream(stream)))
+                                _x16_norm(norm), _stream(stream)))
 
 
-def _k_gemv_x16_swiglu(qtype, gate, up, xq, y, yq, n, k, waves=0, stream=None):
+def _k_gemv_x16_swiglu(qtype, gate, up, xq, y, yq, n, k, waves=0, stream=None, norm=None):
     check(lib().hipllm_gemv_x16_swiglu(qtype, _ptr(gate), _ptr(up), _ptr(xq), _ptr(y), _ptr(yq), n, k, waves,
-                                       _stream(stream)))
+                                       _x16_norm(norm), _stream(stream)))
 
 
 def _k_to_f16(x, ldx, xh, xscale, m, k, stream=None):

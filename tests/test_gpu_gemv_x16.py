@@ -225,3 +225,126 @@ def test_gemv_x16_swiglu(cuda, qtype, n, k, waves):
     if n > 16:
         with pytest.raises(ValueError):
             kernels.gemv_x16_swiglu(qtype, pg, pu, xq, y, yq, n - 1, k, waves)
+
+
+def rms_inv(x: np.ndarray, eps: float) -> np.float32:
+    """1 / sqrt(mean(x^2) + eps) as the reference's RMSNorm forms it (double
+    sum of squares, FP32 mean, eps and root; cpu_llm.cpp:143-166)."""
+    ss = float(np.sum(x.astype(np.float64) ** 2))
+    ms = np.float32(ss / x.size)
+    return np.float32(1.0) / np.sqrt(ms + np.float32(eps), dtype=np.float32)
+
+
+def tile_sumsq(v: np.ndarray) -> np.ndarray:
+    """Per-16-value double sums of squares, each summed in value order."""
+    out = np.zeros(v.size // 16)
+    for t in range(out.size):
+        acc = 0.0
+        for x in v[16 * t: 16 * t + 16].astype(np.float64):
+            acc += x * x
+        out[t] = acc
+    return out
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("n,k,waves", [(48, 256, 0), (4608, 3584, 0), (300, 5120, 2108), (1001, 2048, 1104)])
+def test_gemv_x16_norm_before_product(cuda, qtype, n, k, waves):
+    """W rmsnorm(x) from the XGroup form of x * gamma and the per-16 sums of
+    squares of x, against float64 over the oracle's weights and the
+    reference's normalised row."""
+    w = random_rows(qtype, n, k, n + k)
+    packed = torch.empty(kernels.x16_bytes(qtype, n, k), dtype=torch.uint8, device=cuda)
+    kernels.pack_x16(qtype, dev_bytes(w, cuda), w.shape[1], n, k, packed)
+    x = (3.0 * synth.normal(k, n)).astype(np.float32)
+    gamma = (1.0 + 0.3 * synth.normal(k, n + 1)).astype(np.float32)
+    eps = 1e-6
+    xq = xgroup.buffer(torch, k, cuda)
+    kernels.prep_x(torch.from_numpy(x * gamma).to(cuda), xq, k)
+    ssq = torch.from_numpy(tile_sumsq(x)).to(cuda)
+    b = synth.normal(n, n + 2)
+    y = torch.empty(n, dtype=torch.float32, device=cuda)
+    kernels.gemv_x16(qtype, packed, xq, torch.from_numpy(b).to(cuda), None, y, n, k, waves,
+                     norm={"sumsq_in": ssq, "eps": eps})
+    xn = x * (rms_inv(x, eps) * gamma)  # the reference's normalised row (FP32)
+    ref = oracle.dequant_rows(qtype, w, k).astype(np.float64) @ xn.astype(np.float64) + b
+    assert rel_err(y.cpu().numpy(), ref) <= 1e-5
+    # The SwiGLU pair with the same norm.
+    wu = random_rows(qtype, n, k, n + k + 1)
+    pu = torch.empty_like(packed)
+    kernels.pack_x16(qtype, dev_bytes(wu, cuda), wu.shape[1], n, k, pu)
+    if n % 16 == 0:
+        ys = torch.empty(n, dtype=torch.float32, device=cuda)
+        yq = xgroup.buffer(torch, n, cuda)
+        kernels.gemv_x16_swiglu(qtype, packed, pu, xq, ys, yq, n, k, 0, norm={"sumsq_in": ssq, "eps": eps})
+        g = oracle.dequant_rows(qtype, w, k).astype(np.float64) @ xn.astype(np.float64)
+        u = oracle.dequant_rows(qtype, wu, k).astype(np.float64) @ xn.astype(np.float64)
+        assert rel_err(ys.cpu().numpy(), silu_mul_ref(g, u)) <= 1e-5
+        xgroup.check(yq, ys.cpu().numpy())
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("n,k,waves", [(3584, 18944, 0), (3584, 3584, 0), (64, 512, 2104), (5120, 13824, 0)])
+def test_gemv_x16_norm_after_product(cuda, qtype, n, k, waves):
+    """y is the plain GEMV's, bit for bit; the norm data is the XGroup form of
+    y * gamma and the per-16 double sums of squares of y in row order; a
+    consumer applying it equals the consumer of the standalone RMSNorm."""
+    w = random_rows(qtype, n, k, n + 3 * k)
+    packed = torch.empty(kernels.x16_bytes(qtype, n, k), dtype=torch.uint8, device=cuda)
+    kernels.pack_x16(qtype, dev_bytes(w, cuda), w.shape[1], n, k, packed)
+    x = synth.normal(k, 5)
+    xq = xgroup.buffer(torch, k, cuda)
+    kernels.prep_x(torch.from_numpy(x).to(cuda), xq, k)
+    res = torch.from_numpy(synth.normal(n, 6)).to(cuda)
+    gamma = torch.from_numpy((1.0 + 0.3 * synth.normal(n, 7)).astype(np.float32)).to(cuda)
+    y0 = torch.empty(n, dtype=torch.float32, device=cuda)
+    kernels.gemv_x16(qtype, packed, xq, None, res, y0, n, k, waves)
+    y = torch.empty(n, dtype=torch.float32, device=cuda)
+    yq = xgroup.buffer(torch, n, cuda)
+    ssq = torch.empty(n // 16, dtype=torch.float64, device=cuda)
+    kernels.gemv_x16(qtype, packed, xq, None, res, y, n, k, waves,
+                     norm={"gamma_out": gamma, "yq_out": yq, "sumsq_out": ssq})
+    yv = y.cpu().numpy()
+    assert np.array_equal(yv.view(np.int32), y0.cpu().numpy().view(np.int32))
+    xgroup.check(yq, yv * gamma.cpu().numpy())
+    assert np.array_equal(ssq.cpu().numpy(), tile_sumsq(yv))
+    if n <= 8192 and n % 256 == 0:
+        # Consumer: n rows of the next matrix read the norm data ...
+        m = 256
+        w2 = random_rows(synth.Q4_K, m, n, 9)
+        p2 = torch.empty(kernels.x16_bytes(synth.Q4_K, m, n), dtype=torch.uint8, device=cuda)
+        kernels.pack_x16(synth.Q4_K, dev_bytes(w2, cuda), w2.shape[1], m, n, p2)
+        z = torch.empty(m, dtype=torch.float32, device=cuda)
+        kernels.gemv_x16(synth.Q4_K, p2, yq, None, None, z, m, n, 0, norm={"sumsq_in": ssq, "eps": 1e-6})
+        # ... against the standalone RMSNorm's XGroup output.
+        nq = xgroup.buffer(torch, n, cuda)
+        nf = torch.empty(n, dtype=torch.float32, device=cuda)
+        kernels.rmsnorm(y, gamma, nf, nq, 1, n, 1e-6)
+        z0 = torch.empty(m, dtype=torch.float32, device=cuda)
+        kernels.gemv_x16(synth.Q4_K, p2, nq, None, None, z0, m, n, 0)
+        assert rel_err(z.cpu().numpy(), z0.cpu().numpy()) <= 2e-6
+
+
+def test_gemv_x16_norm_rejects_bad_combinations(cuda):
+    n, k = 32, 256
+    packed = torch.zeros(kernels.x16_bytes(synth.Q4_K, n, k), dtype=torch.uint8, device=cuda)
+    xq = xgroup.buffer(torch, k, cuda)
+    y = torch.empty(n, dtype=torch.float32, device=cuda)
+    ssq = torch.zeros(64, dtype=torch.float64, device=cuda)
+    gamma = torch.ones(n, dtype=torch.float32, device=cuda)
+    yq = xgroup.buffer(torch, n, cuda)
+    with pytest.raises(ValueError):  # both forms at once
+        kernels.gemv_x16(synth.Q4_K, packed, xq, None, None, y, n, k, 0,
+                         norm={"sumsq_in": ssq, "gamma_out": gamma, "yq_out": yq, "sumsq_out": ssq})
+    with pytest.raises(ValueError):  # output form without its buffers
+        kernels.gemv_x16(synth.Q4_K, packed, xq, None, None, y, n, k, 0, norm={"gamma_out": gamma})
+    with pytest.raises(ValueError):  # output form with a ragged tile
+        kernels.gemv_x16(synth.Q4_K, packed, xq, None, None, y, n - 1, k, 0,
+                         norm={"gamma_out": gamma, "yq_out": yq, "sumsq_out": ssq})
+    with pytest.raises(ValueError):  # the SwiGLU pair takes no output form
+        kernels.gemv_x16_swiglu(synth.Q4_K, packed, packed, xq, y, None, n, k, 0,
+                                norm={"gamma_out": gamma, "yq_out": yq, "sumsq_out": ssq})
+    big = 9216
+    pb = torch.zeros(kernels.x16_bytes(synth.Q4_K, 16, big), dtype=torch.uint8, device=cuda)
+    xb = xgroup.buffer(torch, big, cuda)
+    with pytest.raises(ValueError):  # input form beyond 8192 values
+        kernels.gemv_x16(synth.Q4_K, pb, xb, None, None, y, 16, big, 0, norm={"sumsq_in": ssq})

@@ -77,6 +77,23 @@ def test_attention_head_kernel_matches_split_kernel(cuda, golden_model):
     assert np.array_equal(runs[0][1].view(np.int32), runs[1][1].view(np.int32))
 
 
+def test_fused_norms_match_separate_norms(cuda, golden_model):
+    """With x16 copies of every projection the decode RMSNorms ride in the
+    GEMVs (norm data from the attention output and FFN down epilogues, the
+    scaling in QKV, gate / up and the LM head): same greedy tokens as the
+    reference's CPULLM and as separate norm launches, logits within FP32
+    rounding of them."""
+    path, g = golden_model("qwen2.5-7b")
+    runs = {}
+    for fused in (True, False):
+        with HipLLM(path, int(g["max_sequence"])) as m:
+            m.set_fused_norms(fused)
+            runs[fused] = run_with_logits(m, g["prompt"], len(g["tokens"]))
+    assert runs[True][0] == runs[False][0] == g["tokens"].tolist()
+    a, b = runs[True][1].astype(np.float64), runs[False][1].astype(np.float64)
+    assert (np.abs(a - b).max(axis=1) / np.abs(b).max(axis=1)).max() <= 1e-4
+
+
 def test_batched_prefill_is_default_and_switchable(cuda, golden_model):
     path, g = golden_model("tiny")
     with HipLLM(path, 64) as m:
