@@ -49,7 +49,15 @@ struct DevMatrix {
     std::size_t cols = 0;
     std::size_t row_bytes = 0;
     std::size_t expert_stride = 0;
+    const void* x16 = nullptr;  // x16 tile-packed copy for decode GEMVs, when made
 };
+
+// Q4_K / Q6_K matrices whose rows hold whole 256-value super-blocks (and the
+// row alignment the packer reads) can get an x16 tile-packed copy.
+inline bool x16_packable(const DevMatrix& m) {
+    return m.cols % 256 == 0 && ((m.type == hipllm::kQ4_K && m.row_bytes % 16 == 0) ||
+                                 (m.type == hipllm::kQ6_K && m.row_bytes % 2 == 0));
+}
 
 // Plans the device weight arena (every tensor 256-byte aligned, or packed
 // right after its predecessor when requested so matching matrices can be

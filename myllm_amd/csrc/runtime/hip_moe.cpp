@@ -132,6 +132,10 @@ struct HipMoeLLM::Impl {
 
     WeightArena weights;
     std::size_t weight_bytes = 0;
+    // Decode copies of Q4_K / Q6_K projections in the x16 tile-packed form
+    // (the GGUF rows stay for the prefill matmuls).
+    void* x16_arena = nullptr;
+    std::size_t x16_bytes = 0;
     DevMatrix embedding, output;
     const float* output_norm = nullptr;
     std::vector<MoeLayer> layers;
@@ -173,6 +177,7 @@ struct HipMoeLLM::Impl {
         if (host_step) hipHostFree(host_step);
         prof.reset();
         weights.release();
+        if (x16_arena) hipFree(x16_arena);
         if (state_arena) hipFree(state_arena);
         if (rope_table) hipFree(rope_table);
         if (act_arena) hipFree(act_arena);
@@ -185,6 +190,7 @@ struct HipMoeLLM::Impl {
 
     void load(const std::string& path, std::size_t max_sequence, int dev, std::size_t cache_count);
     void upload(GgufReader& reader);
+    void pack_decode_weights();
     void allocate_state();
     void build_rope_table();
     void zero_state();
@@ -287,9 +293,35 @@ void HipMoeLLM::Impl::load(const std::string& path, std::size_t max_sequence, in
         reader.ignore_prefix("blk." + std::to_string(l) + ".");  // NextN / MTP blocks (moe_model.cpp:84-94)
     }
     upload(reader);
+    pack_decode_weights();
     allocate_state();
     build_rope_table();
     zero_state();
+}
+
+// x16 copies of the one-row decode GEMVs that read an XGroup input and run
+// alone: the attention / DeltaNet output projections and the LM head.
+void HipMoeLLM::Impl::pack_decode_weights() {
+    std::vector<DevMatrix*> mats = {&output};
+    for (MoeLayer& L : layers) mats.push_back(L.full ? &L.o : &L.ssm_out);
+    std::vector<std::size_t> offs;
+    std::size_t total = 0;
+    for (DevMatrix* m : mats) {
+        offs.push_back(total);
+        if (x16_packable(*m)) total = align_up(total + hipllm::x16_bytes(m->type, m->rows, m->cols), 256);
+    }
+    if (total == 0) return;
+    hip_check(hipMalloc(&x16_arena, total), "hipMalloc(x16 decode weights)");
+    x16_bytes = total;
+    auto* base = static_cast<std::uint8_t*>(x16_arena);
+    for (std::size_t i = 0; i < mats.size(); ++i) {
+        DevMatrix& m = *mats[i];
+        if (!x16_packable(m)) continue;
+        launch_check(hipllm::launch_pack_x16(m.type, m.ptr, m.row_bytes, m.rows, m.cols, base + offs[i], stream),
+                     "x16 packing");
+        m.x16 = base + offs[i];
+    }
+    hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
 }
 
 void HipMoeLLM::Impl::upload(GgufReader& reader) {
@@ -597,6 +629,11 @@ void HipMoeLLM::Impl::proj(const DevMatrix& w, const float* x, const hipllm::XGr
         return;
     }
     if (rows == 1) {
+        if (w.x16 && xq && n == w.rows) {
+            launch_check(hipllm::launch_gemv_x16(w.type, w.x16, xq, nullptr, residual, y, n, w.cols, 0, stream),
+                         "GEMV");
+            return;
+        }
         launch_check(hipllm::launch_gemv_prepped(w.type, w.ptr, w.row_bytes, x, xq, nullptr, residual, y, n, w.cols,
                                                  0, stream),
                      "GEMV");
@@ -972,9 +1009,15 @@ void HipMoeLLM::Impl::forward(std::size_t rows, std::size_t pos0, const std::int
     }
     const float* last = act.norm + (rows - 1) * H;
     const hipllm::XGroup* lastq = act.normq + (rows - 1) * (H / 16);
-    launch_check(hipllm::launch_gemv_prepped(output.type, output.ptr, output.row_bytes, last, lastq, nullptr,
-                                             nullptr, act.logits, config.vocabulary_size, H, 0, stream),
-                 "LM head");
+    if (output.x16) {
+        launch_check(hipllm::launch_gemv_x16(output.type, output.x16, lastq, nullptr, nullptr, act.logits,
+                                             config.vocabulary_size, H, 0, stream),
+                     "LM head");
+    } else {
+        launch_check(hipllm::launch_gemv_prepped(output.type, output.ptr, output.row_bytes, last, lastq, nullptr,
+                                                 nullptr, act.logits, config.vocabulary_size, H, 0, stream),
+                     "LM head");
+    }
     launch_check(hipllm::launch_argmax(act.logits, config.vocabulary_size, act.token, act.argmax_scratch, stream),
                  "argmax");
     last_rows = rows;
@@ -1163,7 +1206,7 @@ const std::string& HipMoeLLM::device_name() const noexcept {
 MemoryStats HipMoeLLM::memory_stats() const noexcept {
     if (!impl_) return {};
     MemoryStats s;
-    s.weight_bytes = impl_->weight_bytes;
+    s.weight_bytes = impl_->weight_bytes + impl_->x16_bytes;
     s.kv_cache_bytes = impl_->kv_cache_bytes;
     s.recurrent_state_bytes = impl_->recurrent_bytes;
     s.intermediate_bytes = impl_->act_bytes;
