@@ -151,6 +151,24 @@ int hipllm_gemv_x16(uint32_t type, const void* packed, const void* xq, const flo
 int hipllm_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, const void* xq, float* y, void* yq,
                            size_t n, size_t k, int waves, const HipllmX16Norm* norm, void* stream);
 
+/* One token's routed expert vectors over the x16 copy of a whole expert
+ * block ([experts * n, k] rows packed as one matrix, n rows per expert,
+ * n % 16 == 0): route j (j < routes <= 8) multiplies expert ids[j] (clamped
+ * to experts - 1) or, when logits != nullptr, the route the kernel picks
+ * itself (softmax / top-k / renormalisation of the token's router logits as
+ * hipllm_router_topk computes them, experts <= 256; ids and weights stored
+ * to ids_out / weights_out) by row j of xq (x_routed) or row 0 (rows ldx
+ * values apart), into row j of y (ldy apart). packed2 != nullptr: the gate /
+ * up pair, y = silu(Wg x) * (Wu x) and yq (nullable, ldy % 16 == 0) its
+ * XGroup form. Launch shapes as hipllm_gemv_x16 (1104, 1108, 2104, 2108).
+ * Replaces metal_expert_gemm_q4_k_f32 / metal_expert_gemm_q6_k_f32 and
+ * metal_topk_f32 / metal_topk_renorm_f32 of encode_selected_moe
+ * (metal_llm.metal:1424-1521; moe_llm.mm:2642-2790). */
+int hipllm_gemv_x16_routed(uint32_t type, const void* packed, const void* packed2, const void* xq, size_t ldx,
+                           int x_routed, float* y, void* yq, size_t ldy, size_t n, size_t k, size_t experts,
+                           size_t routes, const int32_t* ids, const float* logits, int32_t* ids_out,
+                           float* weights_out, int waves, void* stream);
+
 /* hipllm_rmsnorm of the raw row x (gain gamma, k <= 8192, x and gamma
  * 16-byte aligned) followed by hipllm_gemv_prepped, in one launch: every
  * block normalises x into LDS (the same bits as hipllm_rmsnorm's XGroup

@@ -1233,15 +1233,64 @@ struct X16<kQ6_K> {
 // (MODE 0; an RMSNorm after y, n % 16 == 0): each 16-row tile of y also
 // writes the XGroup form of y * nrm.gamma_out and the double sum of squares
 // of its 16 values (in row order), the input of a NORM 1 launch.
-template <uint32_t QT, int WPB, int RT, int MODE, int NORM>
+//
+// RTE (one token's routed expert vectors, grid.y = route j): the weights of
+// route j are expert e's rows, e * expert_bytes into the packed copy of the
+// whole [experts * n, k] block (n, the rows of one expert, a multiple of
+// 16); its input is row j of x (x_routed) or row 0, its output row j of y
+// and yq (ldy values apart). RTE 1 reads e = ids[j] (clamped to experts -
+// 1); RTE 2 picks the routes itself: the first wave runs the router's
+// softmax / top-k / renormalisation (router.h) on the token's logits, and
+// block (0, 0) stores the ids and weights for the launches that follow.
+struct X16Route {
+    const int32_t* ids;
+    const float* logits;
+    int32_t* ids_out;
+    float* weights_out;
+    uint32_t experts;
+    uint32_t routes;
+    size_t expert_bytes;
+    uint32_t x_routed;
+    uint32_t ldx;
+    uint32_t ldy;
+};
+
+template <uint32_t QT, int WPB, int RT, int MODE, int NORM, int RTE = 0>
 __global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __restrict__ w,
                                                             const uint8_t* __restrict__ w2,
                                                             const XGroup* __restrict__ xq,
                                                             const float* __restrict__ bias,
                                                             const float* __restrict__ residual,
                                                             float* __restrict__ y, XGroup* __restrict__ yq,
-                                                            uint32_t n, uint32_t units, X16Norm nrm) {
+                                                            uint32_t n, uint32_t units, X16Norm nrm,
+                                                            X16Route route = X16Route{}) {
     static_assert(NORM != 2 || MODE == 0, "the output norm data comes from plain GEMVs");
+    static_assert(RTE == 0 || NORM == 0, "routed vectors take no norm");
+    if constexpr (RTE != 0) {
+        const uint32_t j = blockIdx.y;
+        uint32_t e;
+        if constexpr (RTE == 2) {
+            __shared__ int32_t route_id[8];
+            __shared__ float route_w[8];
+            if (threadIdx.x < 64) {
+                topk_row<kRouteMaxExperts / 64>(route.logits, route.experts, route.routes, route_id, route_w,
+                                                threadIdx.x);
+            }
+            __syncthreads();
+            if (blockIdx.x == 0 && j == 0 && threadIdx.x < route.routes) {
+                route.ids_out[threadIdx.x] = route_id[threadIdx.x];
+                route.weights_out[threadIdx.x] = route_w[threadIdx.x];
+            }
+            e = min(static_cast<uint32_t>(route_id[j]), route.experts - 1);
+        } else {
+            e = min(static_cast<uint32_t>(route.ids[j]), route.experts - 1);
+        }
+        w += static_cast<size_t>(e) * route.expert_bytes;
+        if (MODE == 1) w2 += static_cast<size_t>(e) * route.expert_bytes;
+        xq += static_cast<size_t>(route.x_routed ? j : 0) * (route.ldx / 16);
+        y += static_cast<size_t>(j) * route.ldy;
+        if (yq) yq += static_cast<size_t>(j) * (route.ldy / 16);
+    }
     using F = X16<QT>;
     constexpr uint32_t kTileUnit = 16 * F::kBlock;
     constexpr int NM = MODE == 1 ? 2 : 1;  // matrices
@@ -1613,6 +1662,76 @@ int launch_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, cons
     return type == kQ4_K
                ? launch_x16_norm<kQ4_K, 1>(kind, code, g, u, xq, nullptr, nullptr, y, yq, nn, units, norm, stream)
                : launch_x16_norm<kQ6_K, 1>(kind, code, g, u, xq, nullptr, nullptr, y, yq, nn, units, norm, stream);
+}
+
+namespace {
+template <uint32_t QT, int MODE, int RTE>
+int launch_x16_routed_code(int code, const uint8_t* wp, const uint8_t* wp2, const XGroup* xq, float* y, XGroup* yq,
+                           uint32_t nn, uint32_t units, const X16Route& route, hipStream_t stream) {
+    const uint32_t tiles = (nn + 15) / 16;
+    const X16Norm none{};
+    switch (code) {
+#define HIPLLM_X16R_CASE(RT, W)                                                                                     \
+    case 1000 * RT + 100 + W:                                                                                       \
+        HIPLLM_LAUNCH((gemv_x16_kernel<QT, W, RT, MODE, 0, RTE>), dim3((tiles + RT - 1) / RT, route.routes),        \
+                      dim3(64 * W), 0, stream, wp, wp2, xq, nullptr, nullptr, y, yq, nn, units, none, route);       \
+        break;
+        HIPLLM_X16R_CASE(1, 4)
+        HIPLLM_X16R_CASE(1, 8)
+        HIPLLM_X16R_CASE(2, 4)
+        HIPLLM_X16R_CASE(2, 8)
+#undef HIPLLM_X16R_CASE
+    default:
+        return kInvalidArgument;
+    }
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+template <uint32_t QT>
+int launch_x16_routed_type(int code, const uint8_t* wp, const uint8_t* wp2, const XGroup* xq, float* y, XGroup* yq,
+                           uint32_t nn, uint32_t units, const X16Route& route, hipStream_t stream) {
+    if (wp2) {
+        return route.logits ? launch_x16_routed_code<QT, 1, 2>(code, wp, wp2, xq, y, yq, nn, units, route, stream)
+                            : launch_x16_routed_code<QT, 1, 1>(code, wp, wp2, xq, y, yq, nn, units, route, stream);
+    }
+    return route.logits ? launch_x16_routed_code<QT, 0, 2>(code, wp, wp2, xq, y, yq, nn, units, route, stream)
+                        : launch_x16_routed_code<QT, 0, 1>(code, wp, wp2, xq, y, yq, nn, units, route, stream);
+}
+}  // namespace
+
+// Measured on MI355X (Qwen3.5-35B-A3B expert shapes): 8 waves per block for
+// the gate / up pair (512 rows of 2048), two tiles per 4-wave block for the
+// down projection (2048 rows of 512: two units per row).
+int launch_gemv_x16_routed(uint32_t type, const void* packed, const void* packed2, const XGroup* xq, size_t ldx,
+                           int x_routed, float* y, XGroup* yq, size_t ldy, size_t n, size_t k, size_t experts,
+                           size_t routes, const int32_t* ids, const float* logits, int32_t* ids_out,
+                           float* weights_out, int waves, hipStream_t stream) {
+    int rc = check_x16(type, packed, xq, y, n, k);
+    if (rc == kOk && packed2) rc = check_x16(type, packed2, xq, y, n, k);
+    if (rc != kOk) return rc;
+    if (n % 16 != 0 || experts == 0 || routes == 0 || routes > 8 || ldx % 16 != 0 || ldx < k || ldy < n) {
+        return kInvalidArgument;
+    }
+    if (yq && (!packed2 || ldy % 16 != 0 || reinterpret_cast<uintptr_t>(yq) % 16 != 0)) return kInvalidArgument;
+    if (logits ? (experts > kRouteMaxExperts || !ids_out || !weights_out) : !ids) return kInvalidArgument;
+    if (experts > 0xffffffffull || ldx > 0xffffffffull || ldy > 0xffffffffull) return kLengthError;
+    const uint32_t units = static_cast<uint32_t>(k / 256), nn = static_cast<uint32_t>(n);
+    X16Route route{};
+    route.ids = ids;
+    route.logits = logits;
+    route.ids_out = ids_out;
+    route.weights_out = weights_out;
+    route.experts = static_cast<uint32_t>(experts);
+    route.routes = static_cast<uint32_t>(routes);
+    route.expert_bytes = x16_bytes(type, n, k);
+    route.x_routed = x_routed ? 1u : 0u;
+    route.ldx = static_cast<uint32_t>(ldx);
+    route.ldy = static_cast<uint32_t>(ldy);
+    const int code = waves ? waves : (units <= 4 ? 2104 : 1108);
+    const auto* wp = static_cast<const uint8_t*>(packed);
+    const auto* wp2 = static_cast<const uint8_t*>(packed2);
+    return type == kQ4_K ? launch_x16_routed_type<kQ4_K>(code, wp, wp2, xq, y, yq, nn, units, route, stream)
+                         : launch_x16_routed_type<kQ6_K>(code, wp, wp2, xq, y, yq, nn, units, route, stream);
 }
 
 // GEMV over a prepared XGroup input. tiling 0 selects the default.

@@ -118,6 +118,16 @@ int launch_gemv_x16(uint32_t type, const void* packed, const XGroup* xq, const f
                     float* y, size_t n, size_t k, int waves, hipStream_t stream, const X16Norm* norm = nullptr);
 int launch_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, const XGroup* xq, float* y, XGroup* yq,
                            size_t n, size_t k, int waves, hipStream_t stream, const X16Norm* norm = nullptr);
+// One token's routed expert vectors over the x16 copy of a whole expert block
+// ([experts * n, k], n rows per expert, n % 16 == 0): route j multiplies
+// expert ids[j] (or, with logits, the router's top-k picked in the kernel,
+// ids / weights stored to ids_out / weights_out) by row j of x (x_routed) or
+// row 0, into row j of y (ldy apart). packed2 != nullptr: the gate / up
+// SwiGLU pair (yq nullable: its XGroup form).
+int launch_gemv_x16_routed(uint32_t type, const void* packed, const void* packed2, const XGroup* xq, size_t ldx,
+                           int x_routed, float* y, XGroup* yq, size_t ldy, size_t n, size_t k, size_t experts,
+                           size_t routes, const int32_t* ids, const float* logits, int32_t* ids_out,
+                           float* weights_out, int waves, hipStream_t stream);
 
 int gemm_default_tile(uint32_t m, uint32_t n, uint32_t k);
 uint32_t gemm_default_splits(uint32_t m, uint32_t n, uint32_t k, int tile);

@@ -246,6 +246,18 @@ int hipllm_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, cons
                   "launch failure");
 }
 
+int hipllm_gemv_x16_routed(uint32_t type, const void* packed, const void* packed2, const void* xq, size_t ldx,
+                           int x_routed, float* y, void* yq, size_t ldy, size_t n, size_t k, size_t experts,
+                           size_t routes, const int32_t* ids, const float* logits, int32_t* ids_out,
+                           float* weights_out, int waves, void* stream) {
+    return status(hipllm::launch_gemv_x16_routed(type, packed, packed2, xgc(xq), ldx, x_routed, y, xg(yq), ldy, n, k,
+                                                 experts, routes, ids, logits, ids_out, weights_out, waves,
+                                                 as_stream(stream)),
+                  "hipllm_gemv_x16_routed: invalid arguments (Q4_K or Q6_K, k % 256 == 0, n % 16 == 0, routes <= 8, "
+                  "experts <= 256 with logits, ids or logits, a known launch shape, 16-byte aligned buffers) or "
+                  "launch failure");
+}
+
 int hipllm_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m, size_t k, void* stream) {
     return status(hipllm::launch_to_f16(x, ldx, xh, xscale, m, k, as_stream(stream)),
                   "hipllm_to_f16: invalid arguments (k % 8 == 0, 16-byte aligned buffers) or launch failure");

@@ -299,25 +299,43 @@ void HipMoeLLM::Impl::load(const std::string& path, std::size_t max_sequence, in
     zero_state();
 }
 
-// x16 copies of the one-row decode GEMVs that read an XGroup input and run
-// alone: the attention / DeltaNet output projections and the LM head.
+// x16 copies of the one-row decode GEMVs that read an XGroup input: the
+// attention / DeltaNet output projections, the LM head, and every layer's
+// routed expert blocks (gate, up, down; all experts of a projection packed
+// as one matrix of experts x rows rows, so expert e's tiles start at e times
+// its rows / 16).
 void HipMoeLLM::Impl::pack_decode_weights() {
-    std::vector<DevMatrix*> mats = {&output};
-    for (MoeLayer& L : layers) mats.push_back(L.full ? &L.o : &L.ssm_out);
+    struct Job {
+        DevMatrix* m;
+        std::size_t rows;  // rows packed: the matrix's, or every expert's
+    };
+    std::vector<Job> jobs = {{&output, output.rows}};
+    auto expert_block = [&](DevMatrix& m) {
+        return x16_packable(m) && m.rows % 16 == 0 && m.expert_stride == m.rows * m.row_bytes;
+    };
+    for (MoeLayer& L : layers) {
+        jobs.push_back({L.full ? &L.o : &L.ssm_out, (L.full ? L.o : L.ssm_out).rows});
+        if (expert_block(L.gate_exps) && expert_block(L.up_exps) && L.gate_exps.type == L.up_exps.type &&
+            expert_block(L.down_exps)) {
+            jobs.push_back({&L.gate_exps, E * L.gate_exps.rows});
+            jobs.push_back({&L.up_exps, E * L.up_exps.rows});
+            jobs.push_back({&L.down_exps, E * L.down_exps.rows});
+        }
+    }
     std::vector<std::size_t> offs;
     std::size_t total = 0;
-    for (DevMatrix* m : mats) {
+    for (const Job& j : jobs) {
         offs.push_back(total);
-        if (x16_packable(*m)) total = align_up(total + hipllm::x16_bytes(m->type, m->rows, m->cols), 256);
+        if (x16_packable(*j.m)) total = align_up(total + hipllm::x16_bytes(j.m->type, j.rows, j.m->cols), 256);
     }
     if (total == 0) return;
     hip_check(hipMalloc(&x16_arena, total), "hipMalloc(x16 decode weights)");
     x16_bytes = total;
     auto* base = static_cast<std::uint8_t*>(x16_arena);
-    for (std::size_t i = 0; i < mats.size(); ++i) {
-        DevMatrix& m = *mats[i];
+    for (std::size_t i = 0; i < jobs.size(); ++i) {
+        DevMatrix& m = *jobs[i].m;
         if (!x16_packable(m)) continue;
-        launch_check(hipllm::launch_pack_x16(m.type, m.ptr, m.row_bytes, m.rows, m.cols, base + offs[i], stream),
+        launch_check(hipllm::launch_pack_x16(m.type, m.ptr, m.row_bytes, jobs[i].rows, m.cols, base + offs[i], stream),
                      "x16 packing");
         m.x16 = base + offs[i];
     }
@@ -893,7 +911,17 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
     const void* xb = f16_rows(act.norm, H, H, rows);
     // Routed experts: gate/up + SwiGLU (and its XGroup form) for every
     // (row, route), then down.
-    if (route_in_gemv) {
+    const bool x16_experts = rows == 1 && E <= 256 && K <= 8 && L.gate_exps.x16 && L.up_exps.x16 && L.down_exps.x16;
+    if (x16_experts) {
+        // One token: the expert gate / up pair on the x16 copies, with the
+        // top-k in the kernel when the grouped launch left it to the experts
+        // (ids and weights stored for down and the combine).
+        launch_check(hipllm::launch_gemv_x16_routed(L.gate_exps.type, L.gate_exps.x16, L.up_exps.x16, act.normq, H, 0,
+                                                    act.act, act.actq, FF, FF, H, E, K, route_in_gemv ? nullptr : ids,
+                                                    route_in_gemv ? act.rlog : nullptr, route_in_gemv ? ids : nullptr,
+                                                    route_in_gemv ? act.rweight : nullptr, 0, stream),
+                     "router top-k + expert gate/up");
+    } else if (route_in_gemv) {
         launch_check(hipllm::launch_gemv_routed_swiglu(L.gate_exps.type, L.gate_exps.ptr, L.up_exps.ptr,
                                                        L.gate_exps.row_bytes, act.norm, act.normq, H, act.act,
                                                        act.actq, FF, H, rows, act.rlog, ldr, E, K,
@@ -928,7 +956,12 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
                                                  L.gate_exps.expert_stride, 0, H, FF, stream),
                      "expert gate/up");
     }
-    if (!gathered_experts(L, rows, xb)) {
+    if (x16_experts) {
+        launch_check(hipllm::launch_gemv_x16_routed(L.down_exps.type, L.down_exps.x16, nullptr, act.actq, FF, 1,
+                                                    act.down, nullptr, H, H, FF, E, K, ids, nullptr, nullptr, nullptr,
+                                                    0, stream),
+                     "expert down");
+    } else if (!gathered_experts(L, rows, xb)) {
         launch_check(hipllm::launch_gemv_batched(L.down_exps.type, L.down_exps.ptr, nullptr, L.down_exps.row_bytes,
                                                  act.act, act.actq, nullptr, nullptr, act.down, nullptr, H, FF,
                                                  rows * K, ids, E, K, L.down_exps.expert_stride, 1, FF, H, stream),

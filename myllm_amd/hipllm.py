@@ -91,6 +91,7 @@ SIGNATURES = {
     "hipllm_pack_x16": (_I, [_U32, _P, _S, _S, _S, _P, _P]),
     "hipllm_gemv_x16": (_I, [_U32, _P, _P, _P, _P, _P, _S, _S, _I, _P, _P]),
     "hipllm_gemv_x16_swiglu": (_I, [_U32, _P, _P, _P, _P, _P, _S, _S, _I, _P, _P]),
+    "hipllm_gemv_x16_routed": (_I, [_U32, _P, _P, _P, _S, _I, _P, _P, _S, _S, _S, _S, _S, _P, _P, _P, _P, _I, _P]),
     "hipllm_gemm_mfma": (_I, [_U32, _P, _S, _P, _P, _P, _P, _P, _S, _S, _S, _I, _I, _P, _S, _P]),
     "hipllm_gemm_mfma_workspace_bytes": (_S, [_S, _S, _S, _I, _I]),
     "hipllm_gemm_workspace_bytes": (_S, [_S, _S]),
@@ -585,6 +586,13 @@ def _k_gemv_x16_swiglu(qtype, gate, up, xq, y, yq, n, k, waves=0, stream=None, n
                                        _x16_norm(norm), _stream(stream)))
 
 
+def _k_gemv_x16_routed(qtype, packed, packed2, xq, ldx, x_routed, y, yq, ldy, n, k, experts, routes, ids=None,
+                       logits=None, ids_out=None, weights_out=None, waves=0, stream=None):
+    check(lib().hipllm_gemv_x16_routed(qtype, _ptr(packed), _ptr(packed2), _ptr(xq), ldx, int(bool(x_routed)),
+                                       _ptr(y), _ptr(yq), ldy, n, k, experts, routes, _ptr(ids), _ptr(logits),
+                                       _ptr(ids_out), _ptr(weights_out), waves, _stream(stream)))
+
+
 def _k_to_f16(x, ldx, xh, xscale, m, k, stream=None):
     check(lib().hipllm_to_f16(_ptr(x), ldx, _ptr(xh), _ptr(xscale), m, k, _stream(stream)))
 
@@ -790,6 +798,7 @@ def _k_swiglu(g, u, y, yq, n, stream=None):
 kernels = types.SimpleNamespace(
     dequant_rows=_k_dequant_rows, prep_x=_k_prep_x, gemv=_k_gemv, gemv_noalloc=_k_gemv_noalloc,
     gemv_prepped=_k_gemv_prepped, pack_x16=_k_pack_x16, gemv_x16=_k_gemv_x16, gemv_x16_swiglu=_k_gemv_x16_swiglu,
+    gemv_x16_routed=_k_gemv_x16_routed,
     x16_bytes=lambda qtype, n, k: lib().hipllm_x16_bytes(qtype, n, k),
     gemv_swiglu=_k_gemv_swiglu, gemv_norm=_k_gemv_norm, gemv_swiglu_norm=_k_gemv_swiglu_norm, to_f16=_k_to_f16, gemm_mfma=_k_gemm_mfma, gemm=_k_gemm,
     gemm_workspace_bytes=lambda m, k: lib().hipllm_gemm_workspace_bytes(m, k), rmsnorm=_k_rmsnorm, embed=_k_embed, rope_kv=_k_rope_kv,

@@ -150,6 +150,63 @@ def test_gemv_routed_swiglu_matches_topk_then_batched(cuda, qtype, E, K, T, n, k
         xgroup.check(yq[v * n:(v + 1) * n], got[v])
 
 
+@pytest.mark.parametrize("qtype,E,K,n,kdim,waves", [(synth.Q4_K, 256, 8, 64, 512, 0), (synth.Q6_K, 16, 2, 48, 768, 1104),
+                                                    (synth.Q4_K, 32, 4, 512, 2048, 2108)])
+def test_gemv_x16_routed_matches_vector_routes(cuda, qtype, E, K, n, kdim, waves):
+    """The x16 routed expert GEMVs of one token against the vector ones on
+    the GGUF rows: gate / up with the top-k in the kernel (ids and weights bit
+    for bit, outputs within 1e-6, XGroup form of the output), then down by
+    those ids from the routed SwiGLU outputs (within 1e-6)."""
+    rng = np.random.default_rng(E + n)
+    wg = random_rows(qtype, E * n, kdim, 61)
+    wu = random_rows(qtype, E * n, kdim, 62)
+    wd = random_rows(qtype, E * kdim, n, 63) if n % 256 == 0 else None
+    dg, du = dev_bytes(wg, cuda), dev_bytes(wu, cuda)
+    rb = wg.shape[1]
+
+    def pack(w, rows, cols):
+        p = torch.empty(kernels.x16_bytes(qtype, rows, cols), dtype=torch.uint8, device=cuda)
+        kernels.pack_x16(qtype, dev_bytes(w, cuda), w.shape[1], rows, cols, p)
+        return p
+
+    pg, pu = pack(wg, E * n, kdim), pack(wu, E * n, kdim)
+    x = synth.normal(kdim, 64)
+    dx = t32(x, cuda)
+    xq = xgroup.buffer(torch, kdim, cuda)
+    kernels.prep_x(dx, xq, kdim)
+    logits = rng.normal(size=E).astype(np.float32)
+    logits[[1, 5]] = logits.max() + 1.0  # a tie at the top
+    dl = t32(logits, cuda)
+    ids_ref = torch.empty(K, dtype=torch.int32, device=cuda)
+    w_ref = torch.empty(K, device=cuda)
+    y_ref = torch.empty(K, n, device=cuda)
+    yq_ref = xgroup.buffer(torch, n, cuda, K)
+    kernels.gemv_routed_swiglu(qtype, dg, du, rb, dx, xq, kdim, y_ref, yq_ref, n, kdim, 1, dl, E, E, K, n * rb,
+                               ids_ref, w_ref)
+    ids = torch.full((K,), -1, dtype=torch.int32, device=cuda)
+    wts = torch.empty(K, device=cuda)
+    y = torch.empty(K, n, device=cuda)
+    yq = xgroup.buffer(torch, n, cuda, K)
+    kernels.gemv_x16_routed(qtype, pg, pu, xq, kdim, False, y, yq, n, n, kdim, E, K, logits=dl, ids_out=ids,
+                            weights_out=wts, waves=waves)
+    assert torch.equal(ids, ids_ref)
+    assert torch.equal(wts.view(torch.int32), w_ref.view(torch.int32))
+    got = y.cpu().numpy()
+    assert rel_err(got, y_ref.cpu().numpy()) <= 1e-6
+    for v in range(K):
+        xgroup.check(yq[v * n:(v + 1) * n], got[v])
+    if wd is None:
+        return
+    pd = pack(wd, E * kdim, n)
+    dd = dev_bytes(wd, cuda)
+    d_ref = torch.empty(K, kdim, device=cuda)
+    kernels.gemv_batched(qtype, dd, None, wd.shape[1], y, yq, None, None, d_ref, None, kdim, n, K, ids=ids,
+                         experts=E, routes=K, expert_stride=kdim * wd.shape[1], x_routed=True, ldx=n, ldy=kdim)
+    d = torch.empty(K, kdim, device=cuda)
+    kernels.gemv_x16_routed(qtype, pd, None, yq, n, True, d, None, kdim, kdim, n, E, K, ids=ids)
+    assert rel_err(d.cpu().numpy(), d_ref.cpu().numpy()) <= 1e-6
+
+
 def test_gemv_routed_swiglu_rejects_bad_arguments(cuda):
     w = torch.zeros(272 * 64, dtype=torch.uint8, device=cuda)
     x = torch.zeros(256, device=cuda)
