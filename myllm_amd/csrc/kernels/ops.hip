@@ -284,15 +284,16 @@ __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restri
 }
 
 // The split kernel and the merge in one launch for capacities of 2 to NG
-// chunks and heads of D = 64 or 128 dims: one block of NG x 256 threads per
+// chunks and heads of D = 64, 128 or 256 dims: one block of NG x 256 threads per
 // head, thread group c (256 threads) doing what split c of a launch with
 // one chunk per split does (scores, softmax and p.V over chunk c), then the
 // groups' (m, l, p.V) merged in the block in group order as the merge
 // kernel merges splits (a group past the last chunk has m = -inf, l = 0,
-// weight 0). Every K and V row a thread uses is loaded at the start, before
-// the RoPE and the block barrier, so the block waits for one memory round
-// trip; the token's own row (len - 1 with rope), which this launch writes
-// into the caches, is taken from the block's own rotated values instead.
+// weight 0). For D <= 128 every K and V row a thread uses is loaded at the
+// start, before the RoPE and the block barrier, so the block waits for one
+// memory round trip (D = 256: K after the barrier, then V); the token's own
+// row (len - 1 with rope), which this launch writes into the caches, is
+// taken from the block's own rotated values instead.
 // Same operations in the same order as the two launches: the output bits
 // are equal.
 template <uint32_t NG, uint32_t D>
@@ -307,6 +308,10 @@ __global__ __launch_bounds__(256 * NG) void attn_decode_head(const float* __rest
     constexpr uint32_t PARTS = 256 / D4;           // p.V key subsets
     constexpr uint32_t KR = D4 / 4;                // float4 of a key per scoring lane
     constexpr uint32_t VR = kAttnChunk / PARTS;    // value rows per p.V lane
+    // 256-dim heads load their rows where they are used: a lane's K (64
+    // floats) and V rows held from the start would exceed the registers of a
+    // 1024-thread block.
+    constexpr bool kPre = D <= 128;
     const uint32_t h = blockIdx.x;
     const uint32_t len = dpos ? *dpos + 1 : len_arg;
     const uint32_t nchunks = (len + kAttnChunk - 1) / kAttnChunk;  // <= NG
@@ -328,18 +333,20 @@ __global__ __launch_bounds__(256 * NG) void attn_decode_head(const float* __rest
     const uint32_t j = lt >> 2, qq = lt & 3;
     // p.V: float4 column c4, keys pp, pp + PARTS, ...
     const uint32_t c4 = lt % D4, pp = lt / D4;
-    float4 kr[KR], vr[VR];
-    if (j < cnt && t0 + j != newrow) {
-        const float4* k = reinterpret_cast<const float4*>(kcache + static_cast<size_t>(t0 + j) * kvd + g * D);
+    float4 kr[kPre ? KR : 1], vr[kPre ? VR : 1];
+    const float4* krow = reinterpret_cast<const float4*>(kcache + static_cast<size_t>(t0 + j) * kvd + g * D);
+    if constexpr (kPre) {
+        if (j < cnt && t0 + j != newrow) {
 #pragma unroll
-        for (uint32_t r = 0; r < KR; ++r) kr[r] = k[qq + 4 * r];
+            for (uint32_t r = 0; r < KR; ++r) kr[r] = krow[qq + 4 * r];
+        }
     }
-    {
-        const float4* v = reinterpret_cast<const float4*>(vcache + static_cast<size_t>(t0) * kvd + g * D) + c4;
+    const float4* vrow = reinterpret_cast<const float4*>(vcache + static_cast<size_t>(t0) * kvd + g * D) + c4;
+    if constexpr (kPre) {
 #pragma unroll
         for (uint32_t r = 0; r < VR; ++r) {
             const uint32_t jj = pp + r * PARTS;
-            if (jj < cnt && t0 + jj != newrow) vr[r] = v[static_cast<size_t>(jj) * (kvd / 4)];
+            if (jj < cnt && t0 + jj != newrow) vr[r] = vrow[static_cast<size_t>(jj) * (kvd / 4)];
         }
     }
     if (rope) {
@@ -370,7 +377,12 @@ __global__ __launch_bounds__(256 * NG) void attn_decode_head(const float* __rest
             const bool own = t0 + j == newrow;
 #pragma unroll
             for (uint32_t r = 0; r < KR; ++r) {
-                const float4 kv = own ? kn4[qq + 4 * r] : kr[r];
+                float4 kv;
+                if constexpr (kPre) {
+                    kv = own ? kn4[qq + 4 * r] : kr[r];
+                } else {
+                    kv = own ? kn4[qq + 4 * r] : krow[qq + 4 * r];
+                }
                 const float4 qv = qs4[qq + 4 * r];
                 dot = fmaf(kv.x, qv.x, dot);
                 dot = fmaf(kv.y, qv.y, dot);
@@ -398,7 +410,12 @@ __global__ __launch_bounds__(256 * NG) void attn_decode_head(const float* __rest
         const uint32_t jj = pp + r * PARTS;
         if (jj < cnt) {
             const float pj = ps[grp][jj];
-            const float4 vv = t0 + jj == newrow ? vn4[c4] : vr[r];
+            float4 vv;
+            if constexpr (kPre) {
+                vv = t0 + jj == newrow ? vn4[c4] : vr[r];
+            } else {
+                vv = t0 + jj == newrow ? vn4[c4] : vrow[static_cast<size_t>(jj) * (kvd / 4)];
+            }
             acc.x = fmaf(pj, vv.x, acc.x);
             acc.y = fmaf(pj, vv.y, acc.y);
             acc.z = fmaf(pj, vv.z, acc.z);
@@ -708,10 +725,10 @@ namespace {
 // one chunk 5.5 us against 7.6 with the merge, at two 7.7 against 8.3, but
 // each further chunk in turn costs about 2.5 us (11.4 against 8.8 at four),
 // and heads of 256 at two chunks measured 10.9 against 9.5. Beyond, one
-// split per chunk up to 16; the launchers run 2 to 4 splits of 64- or
-// 128-dim heads as one block per head with the chunks side by side and all
-// K / V loads issued first (28 heads of 128 at four chunks: 9.8 + 4.6 us as
-// two launches, one launch about 5 us less).
+// split per chunk up to 16; the launchers run 2 to 4 splits of 64-, 128-
+// or 256-dim heads as one block per head with the chunks side by side and
+// the K (and V) loads issued first (28 heads of 128 at four chunks: 9.8 +
+// 4.6 us as two launches, one launch about 5 us less).
 uint32_t attn_splits(size_t max_len, size_t d) {
     const size_t chunks = (max_len + kAttnChunk - 1) / kAttnChunk;
     if (chunks <= (d > 128 ? 1u : 2u)) return 1;
@@ -737,15 +754,17 @@ int launch_attn_decode(const float* q, const float* kcache, const float* vcache,
     if (len > 0xffffffffull || capacity > 0xffffffffull || hq > 0xffffull) return kLengthError;
     const uint32_t splits = attn_splits(dpos ? capacity : len, d);
     // Read-only use of the caches (no RoPE table): the kernels write them only in the fused form.
-    if (splits >= 2 && splits <= kAttnHeadChunks && (d == 64 || d == 128)) {
+    if (splits >= 2 && splits <= kAttnHeadChunks && (d == 64 || d == 128 || d == 256)) {
 #define HIPLLM_ATTN_HEAD(D)                                                                                       \
     HIPLLM_LAUNCH((attn_decode_head<kAttnHeadChunks, D>), dim3(static_cast<uint32_t>(hq)), dim3(256 * kAttnHeadChunks), \
                   0, stream, q, const_cast<float*>(kcache), const_cast<float*>(vcache), static_cast<uint32_t>(hq),    \
                   static_cast<uint32_t>(hkv), static_cast<uint32_t>(len), dpos, scale, nullptr, 0u, out, outq, nullptr)
         if (d == 64) {
             HIPLLM_ATTN_HEAD(64);
-        } else {
+        } else if (d == 128) {
             HIPLLM_ATTN_HEAD(128);
+        } else {
+            HIPLLM_ATTN_HEAD(256);
         }
 #undef HIPLLM_ATTN_HEAD
         return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
@@ -775,7 +794,7 @@ int launch_attn_decode_rope(const float* qkv, const float* cos_sin, size_t rot, 
     if (outq && reinterpret_cast<uintptr_t>(outq) % 16 != 0) return kInvalidArgument;
     if (pos >= 0xffffffffull || capacity > 0xffffffffull || hq > 0xffffull) return kLengthError;
     const uint32_t splits = attn_splits(dpos ? capacity : pos + 1, d);
-    if (splits >= 2 && splits <= kAttnHeadChunks && (d == 64 || d == 128)) {
+    if (splits >= 2 && splits <= kAttnHeadChunks && (d == 64 || d == 128 || d == 256)) {
 #define HIPLLM_ATTN_HEAD(D)                                                                                       \
     HIPLLM_LAUNCH((attn_decode_head<kAttnHeadChunks, D>), dim3(static_cast<uint32_t>(hq)), dim3(256 * kAttnHeadChunks), \
                   0, stream, qkv, kcache, vcache, static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv),             \
@@ -783,8 +802,10 @@ int launch_attn_decode_rope(const float* qkv, const float* cos_sin, size_t rot, 
                   static_cast<uint32_t>(rot / 2), out, outq, gate)
         if (d == 64) {
             HIPLLM_ATTN_HEAD(64);
-        } else {
+        } else if (d == 128) {
             HIPLLM_ATTN_HEAD(128);
+        } else {
+            HIPLLM_ATTN_HEAD(256);
         }
 #undef HIPLLM_ATTN_HEAD
         return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
