@@ -131,14 +131,24 @@ constexpr uint32_t kAttnHeadChunks = 4;  // up to 4 split-sized chunks merged in
 // With one split (short capacities) the block finishes the head itself: out,
 // outq (nullable) and the optional sigmoid gate exactly as the merge computes
 // them for a single split (weight exp(0) = 1), so no merge launch follows.
+//
+// DT (64 or 128; 0 = any d, given at run time): the block's first chunk has
+// its K and V rows loaded at the start, before the RoPE and the barrier, so
+// a split with one chunk waits for one memory round trip; its token's own
+// row, written by this launch, comes from the block's rotated values.
+template <uint32_t DT>
 __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restrict__ q, float* __restrict__ kcache,
                                                            float* __restrict__ vcache, float* __restrict__ part,
-                                                           uint32_t hq, uint32_t hkv, uint32_t d, uint32_t len_arg,
+                                                           uint32_t hq, uint32_t hkv, uint32_t d_arg, uint32_t len_arg,
                                                            const uint32_t* __restrict__ dpos, float scale,
                                                            uint32_t splits, const float2* __restrict__ rope,
                                                            uint32_t half_rot, float* __restrict__ fout,
                                                            XGroup* __restrict__ foutq,
                                                            const float* __restrict__ gate) {
+    constexpr bool kPre = DT != 0;
+    constexpr uint32_t KR = kPre ? DT / 16 : 1;          // float4 of a key per scoring lane
+    constexpr uint32_t VR = kPre ? kAttnChunk * DT / 1024 : 1;  // value rows per p.V lane
+    const uint32_t d = kPre ? DT : d_arg;
     const uint32_t h = blockIdx.x;
     const uint32_t split = blockIdx.y;
     const uint32_t len = dpos ? *dpos + 1 : len_arg;
@@ -146,12 +156,39 @@ __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restri
     const uint32_t g = h / (hq / hkv);
     const uint32_t kvd = hkv * d;
     __shared__ float4 qs4[64];
+    __shared__ float4 kn4[kPre ? DT / 4 : 1], vn4[kPre ? DT / 4 : 1];
     __shared__ float ps[kAttnChunk];
     __shared__ float red[8];
     __shared__ float4 accp[256];
     const uint32_t tid = threadIdx.x;
     const uint32_t d4 = d / 4;
     const uint32_t wave = tid >> 6, lane = tid & 63;
+    // p.V ownership: float4 column c4 = tid % (d / 4), key subset pp = tid /
+    // (d / 4) of `parts` (threads past parts * d / 4 idle).
+    const uint32_t parts = blockDim.x / d4;
+    const bool pv = tid < parts * d4;
+    const uint32_t c4 = tid % d4, pp = tid / d4;
+    // Scores: key j = tid / 4, quarter qq = tid % 4 covers float4 columns qq, qq + 4, ...
+    const uint32_t j = tid >> 2, qq = tid & 3;
+    const uint32_t newrow = rope ? len - 1 : 0xffffffffu;
+    float4 kr[KR], vr[VR];
+    if constexpr (kPre) {
+        if (split < nchunks) {
+            const uint32_t t0 = split * kAttnChunk;
+            const uint32_t cnt = min(len - t0, kAttnChunk);
+            if (j < cnt && t0 + j != newrow) {
+                const float4* k = reinterpret_cast<const float4*>(kcache + static_cast<size_t>(t0 + j) * kvd + g * d);
+#pragma unroll
+                for (uint32_t r = 0; r < KR; ++r) kr[r] = k[qq + 4 * r];
+            }
+            const float4* v = reinterpret_cast<const float4*>(vcache + static_cast<size_t>(t0) * kvd + g * d) + c4;
+#pragma unroll
+            for (uint32_t r = 0; r < VR; ++r) {
+                const uint32_t jj = pp + r * (256 / (DT / 4));
+                if (jj < cnt && t0 + jj != newrow) vr[r] = v[static_cast<size_t>(jj) * (kvd / 4)];
+            }
+        }
+    }
     if (rope) {
         const float2* tab = rope + static_cast<size_t>(len - 1) * half_rot;
         float* qs = reinterpret_cast<float*>(qs4);
@@ -162,38 +199,50 @@ __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restri
             float* kc = kcache + static_cast<size_t>(len - 1) * kvd + g * d;
             float* vc = vcache + static_cast<size_t>(len - 1) * kvd + g * d;
             for (uint32_t i = tid; i < d; i += blockDim.x) {
-                kc[i] = rope_elem(kn, tab, half_rot, i);
+                const float kv = rope_elem(kn, tab, half_rot, i);
+                kc[i] = kv;
                 vc[i] = vn[i];
+                if constexpr (kPre) {
+                    reinterpret_cast<float*>(kn4)[i] = kv;
+                    reinterpret_cast<float*>(vn4)[i] = vn[i];
+                }
             }
         }
     } else {
         for (uint32_t i = tid; i < d4; i += blockDim.x) qs4[i] = reinterpret_cast<const float4*>(q + h * d)[i];
     }
     __syncthreads();
-    // p.V ownership: float4 column c4 = tid % (d / 4), key subset pp = tid /
-    // (d / 4) of `parts` (threads past parts * d / 4 idle).
-    const uint32_t parts = blockDim.x / d4;
-    const bool pv = tid < parts * d4;
-    const uint32_t c4 = tid % d4, pp = tid / d4;
     float m_run = -INFINITY, l_run = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (uint32_t chunk = split; chunk < nchunks; chunk += splits) {
         const uint32_t t0 = chunk * kAttnChunk;
         const uint32_t cnt = min(len - t0, kAttnChunk);
-        // Scores: key j = tid / 4, quarter qq = tid % 4 covers float4 columns qq, qq + 4, ...
-        const uint32_t j = tid >> 2, qq = tid & 3;
+        const bool first = kPre && chunk == split;  // rows held in registers
         float s = -INFINITY;
         {
             float dot = 0.0f;
             if (j < cnt) {
                 const float4* k = reinterpret_cast<const float4*>(kcache + static_cast<size_t>(t0 + j) * kvd + g * d);
-                for (uint32_t i = qq; i < d4; i += 4) {
-                    const float4 kv = k[i];
-                    const float4 qv = qs4[i];
-                    dot = fmaf(kv.x, qv.x, dot);
-                    dot = fmaf(kv.y, qv.y, dot);
-                    dot = fmaf(kv.z, qv.z, dot);
-                    dot = fmaf(kv.w, qv.w, dot);
+                const bool own = t0 + j == newrow;
+                if (first) {
+#pragma unroll
+                    for (uint32_t r = 0; r < KR; ++r) {
+                        const float4 kv = own ? kn4[qq + 4 * r] : kr[r];
+                        const float4 qv = qs4[qq + 4 * r];
+                        dot = fmaf(kv.x, qv.x, dot);
+                        dot = fmaf(kv.y, qv.y, dot);
+                        dot = fmaf(kv.z, qv.z, dot);
+                        dot = fmaf(kv.w, qv.w, dot);
+                    }
+                } else {
+                    for (uint32_t i = qq; i < d4; i += 4) {
+                        const float4 kv = k[i];
+                        const float4 qv = qs4[i];
+                        dot = fmaf(kv.x, qv.x, dot);
+                        dot = fmaf(kv.y, qv.y, dot);
+                        dot = fmaf(kv.z, qv.z, dot);
+                        dot = fmaf(kv.w, qv.w, dot);
+                    }
                 }
             }
             dot = quad_sum(dot);
@@ -217,14 +266,29 @@ __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restri
         if (pv) {
             const float4* v = reinterpret_cast<const float4*>(vcache + static_cast<size_t>(t0) * kvd + g * d) + c4;
             float4 a = make_float4(acc.x * corr, acc.y * corr, acc.z * corr, acc.w * corr);
+            if (first) {
+#pragma unroll
+                for (uint32_t r = 0; r < VR; ++r) {
+                    const uint32_t jj = pp + r * parts;
+                    if (jj < cnt) {
+                        const float pj = ps[jj];
+                        const float4 vv = t0 + jj == newrow ? vn4[c4] : vr[r];
+                        a.x = fmaf(pj, vv.x, a.x);
+                        a.y = fmaf(pj, vv.y, a.y);
+                        a.z = fmaf(pj, vv.z, a.z);
+                        a.w = fmaf(pj, vv.w, a.w);
+                    }
+                }
+            } else {
 #pragma unroll 4
-            for (uint32_t jj = pp; jj < cnt; jj += parts) {
-                const float pj = ps[jj];
-                const float4 vv = v[static_cast<size_t>(jj) * (kvd / 4)];
-                a.x = fmaf(pj, vv.x, a.x);
-                a.y = fmaf(pj, vv.y, a.y);
-                a.z = fmaf(pj, vv.z, a.z);
-                a.w = fmaf(pj, vv.w, a.w);
+                for (uint32_t jj = pp; jj < cnt; jj += parts) {
+                    const float pj = ps[jj];
+                    const float4 vv = v[static_cast<size_t>(jj) * (kvd / 4)];
+                    a.x = fmaf(pj, vv.x, a.x);
+                    a.y = fmaf(pj, vv.y, a.y);
+                    a.z = fmaf(pj, vv.z, a.z);
+                    a.w = fmaf(pj, vv.w, a.w);
+                }
             }
             acc = a;
         }
@@ -769,10 +833,19 @@ int launch_attn_decode(const float* q, const float* kcache, const float* vcache,
 #undef HIPLLM_ATTN_HEAD
         return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
     }
-    HIPLLM_LAUNCH(attn_decode_partial, dim3(static_cast<uint32_t>(hq), splits), dim3(256), 0, stream, q,
-                       const_cast<float*>(kcache), const_cast<float*>(vcache), scratch, static_cast<uint32_t>(hq),
-                       static_cast<uint32_t>(hkv), static_cast<uint32_t>(d), static_cast<uint32_t>(len), dpos, scale,
-                       splits, nullptr, 0u, out, outq, nullptr);
+#define HIPLLM_ATTN_PARTIAL(DT)                                                                                   \
+    HIPLLM_LAUNCH((attn_decode_partial<DT>), dim3(static_cast<uint32_t>(hq), splits), dim3(256), 0, stream, q,       \
+                  const_cast<float*>(kcache), const_cast<float*>(vcache), scratch, static_cast<uint32_t>(hq),        \
+                  static_cast<uint32_t>(hkv), static_cast<uint32_t>(d), static_cast<uint32_t>(len), dpos, scale,      \
+                  splits, nullptr, 0u, out, outq, nullptr)
+    if (d == 64) {
+        HIPLLM_ATTN_PARTIAL(64);
+    } else if (d == 128) {
+        HIPLLM_ATTN_PARTIAL(128);
+    } else {
+        HIPLLM_ATTN_PARTIAL(0);
+    }
+#undef HIPLLM_ATTN_PARTIAL
     if (splits > 1) {
         HIPLLM_LAUNCH(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out,
                            outq, static_cast<uint32_t>(d), splits, nullptr);
@@ -810,10 +883,19 @@ int launch_attn_decode_rope(const float* qkv, const float* cos_sin, size_t rot, 
 #undef HIPLLM_ATTN_HEAD
         return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
     }
-    HIPLLM_LAUNCH(attn_decode_partial, dim3(static_cast<uint32_t>(hq), splits), dim3(256), 0, stream, qkv,
-                       kcache, vcache, scratch, static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv),
-                       static_cast<uint32_t>(d), static_cast<uint32_t>(pos + 1), dpos, scale, splits,
-                       reinterpret_cast<const float2*>(cos_sin), static_cast<uint32_t>(rot / 2), out, outq, gate);
+#define HIPLLM_ATTN_PARTIAL(DT)                                                                                   \
+    HIPLLM_LAUNCH((attn_decode_partial<DT>), dim3(static_cast<uint32_t>(hq), splits), dim3(256), 0, stream, qkv,     \
+                  kcache, vcache, scratch, static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv),                    \
+                  static_cast<uint32_t>(d), static_cast<uint32_t>(pos + 1), dpos, scale, splits,                     \
+                  reinterpret_cast<const float2*>(cos_sin), static_cast<uint32_t>(rot / 2), out, outq, gate)
+    if (d == 64) {
+        HIPLLM_ATTN_PARTIAL(64);
+    } else if (d == 128) {
+        HIPLLM_ATTN_PARTIAL(128);
+    } else {
+        HIPLLM_ATTN_PARTIAL(0);
+    }
+#undef HIPLLM_ATTN_PARTIAL
     if (splits > 1) {
         HIPLLM_LAUNCH(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out,
                            outq, static_cast<uint32_t>(d), splits, gate);
