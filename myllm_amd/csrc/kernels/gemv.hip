@@ -1343,6 +1343,17 @@ __global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __res
     // sits under a branch that the last pass skips, and the compiler's waits
     // then cover every load in flight.)
     if (mine > 0) fill(0);
+    // The epilogue's per-row operands, loaded now rather than after the
+    // block reduction (same values, same sums).
+    float pre_b = 0.0f, pre_r = 0.0f, pre_g = 0.0f;
+    if (MODE == 0 && tid < 16 * RT) {
+        const uint32_t row = tile0 * 16 + tid;
+        if (row < n) {
+            if (bias) pre_b = bias[row];
+            if (residual) pre_r = residual[row];
+            if (NORM == 2) pre_g = nrm.gamma_out[row];
+        }
+    }
     __shared__ float inv_s;
     if (NORM == 1 && wave == 0) {
         // Up to 512 partials (k <= 8192), all loads issued before the sum.
@@ -1395,13 +1406,13 @@ __global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __res
             v = row < n ? silu_mul(v, u) : 0.0f;
             part[0][tid] = v;  // the tile's outputs, for the XGroup encoding below
         } else if (row < n) {
-            if (bias) v += bias[row];
-            if (residual) v += residual[row];
+            if (bias) v += pre_b;
+            if (residual) v += pre_r;
         }
         if (row < n) y[row] = v;
         if (NORM == 2) {
             // Each thread rewrites only its own slots, after reading them.
-            part[0][tid] = row < n ? v * nrm.gamma_out[row] : 0.0f;
+            part[0][tid] = row < n ? v * pre_g : 0.0f;
             part[1][tid] = row < n ? v : 0.0f;
         }
     }
