@@ -142,6 +142,18 @@ typedef struct HipllmX16Norm {
 int hipllm_gemv_x16(uint32_t type, const void* packed, const void* xq, const float* bias, const float* residual,
                     float* y, size_t n, size_t k, int waves, const HipllmX16Norm* norm, void* stream);
 
+/* Two GEMVs of one RMSNorm-ed row over x16-packed weights (Q4_K or Q6_K
+ * each) in one launch: y_a = W_a n and y_b = W_b n with n = rmsnorm(x) *
+ * gamma (double sum of squares, every block normalising x itself; k <= 8192).
+ * With conv_w, y_a is the input of a causal conv over its channels: y_a[c] =
+ * silu(sum_j history[j][c] w[c][j] + (W_a n)[c] w[c][ksize - 1]) and the
+ * (ksize - 1) x n_a history shifts by one row (ksize 2..4). Replaces the
+ * decode-step QKV / z GEVMs and the conv of encode_linear_attention
+ * (moe_llm.mm:2436-2520; metal_llm.metal:708-781, 1320-1365). */
+int hipllm_gemv_x16_pair(uint32_t type_a, const void* packed_a, size_t n_a, float* y_a, uint32_t type_b,
+                         const void* packed_b, size_t n_b, float* y_b, size_t k, const float* x, const float* gamma,
+                         float eps, const float* conv_w, float* history, size_t ksize, void* stream);
+
 /* The FFN gate/up pair over x16-packed weights of one type in one launch:
  * y = silu(Wg x) * (Wu x) (the sign-branched SiLU of cpu_llm.cpp:188-202),
  * and yq (nullable; n % 16 == 0) its XGroup form for the down projection.
@@ -493,6 +505,20 @@ int hipllm_gdn_scan_gated(const float* q, const float* k, size_t ldqk, const flo
                           const float* beta_raw, size_t ld_ab, const float* dt_bias, const float* a, float* state,
                           const float* z, size_t ldz, const float* gamma, float* y, void* yq, size_t ldy,
                           size_t tokens, size_t value_heads, size_t key_heads, size_t d, float eps, void* stream);
+
+/* One decode token of a Gated DeltaNet layer after its projections (see
+ * hipllm_gemv_x16_pair), one block per value head: qkv is the token's
+ * convolved [Q (key_heads d) | K (key_heads d) | V (value_heads d)] row and
+ * z its gate row; alpha and beta come from the F32 projection ab_w
+ * ([alpha rows | beta rows], 2 value_heads x hidden, hidden <= 4096) of
+ * rmsnorm(x) * x_gamma; then the Q / K head L2 norms and the step of
+ * hipllm_gdn_scan_gated (gates, recurrence, gated RMSNorm; y and its XGroup
+ * form yq, nullable). Replaces the decode-step use of the alpha / beta
+ * GEVMs, L2 norms and recurrence of encode_linear_attention
+ * (moe_llm.mm:2436-2640; metal_llm.metal:1320-1420). */
+int hipllm_gdn_decode(const float* qkv, const float* x, const float* x_gamma, const float* ab_w, size_t hidden,
+                      const float* dt_bias, const float* a, float* state, const float* z, const float* gamma, float* y,
+                      void* yq, size_t value_heads, size_t key_heads, size_t d, float eps, void* stream);
 
 /* Split the per-head interleaved [Q_h | gate_h] projection, RMSNorm Q and K
  * heads with their gammas, and lay out [Q | K | V] rows for RoPE + cache.

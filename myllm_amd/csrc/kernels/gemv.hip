@@ -1255,19 +1255,34 @@ struct X16Route {
     uint32_t ldy;
 };
 
-template <uint32_t QT, int WPB, int RT, int MODE, int NORM, int RTE = 0>
-__global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __restrict__ w,
-                                                            const uint8_t* __restrict__ w2,
-                                                            const XGroup* __restrict__ xq,
-                                                            const float* __restrict__ bias,
-                                                            const float* __restrict__ residual,
-                                                            float* __restrict__ y, XGroup* __restrict__ yq,
-                                                            uint32_t n, uint32_t units, X16Norm nrm,
-                                                            X16Route route = X16Route{}) {
+// CONV (MODE 0 with NORM 3; cv.w nullable): y is the projection of a
+// causal conv's input channels (row = channel): each row's value x is
+// convolved with its ksize (<= 4) taps over the channel's history rows and
+// x, y = conv * sigmoid(conv) (the conv + SiLU of conv1d_silu_kernel), and
+// the channel's history shifts by one row with x appended. The tile's taps
+// and history are loaded at kernel start.
+struct X16Conv {
+    const float* w;      // [channels, ksize]
+    float* history;      // [ksize - 1, channels]
+    uint32_t channels;   // the history's row length (>= n)
+    uint32_t ksize;
+};
+constexpr uint32_t kX16ConvMax = 4;
+
+// The work of block (bx, by); the kernels below call it with their block
+// index (or, for a paired launch, the index within the job).
+template <uint32_t QT, int WPB, int RT, int MODE, int NORM, int RTE, bool CONV>
+__device__ __forceinline__ void x16_body(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2,
+                                         const XGroup* __restrict__ xq, const float* __restrict__ bias,
+                                         const float* __restrict__ residual, float* __restrict__ y,
+                                         XGroup* __restrict__ yq, uint32_t n, uint32_t units, const X16Norm nrm,
+                                         const X16Route route, const X16Conv cv, uint32_t bx, uint32_t by) {
     static_assert(NORM != 2 || MODE == 0, "the output norm data comes from plain GEMVs");
     static_assert(RTE == 0 || NORM == 0, "routed vectors take no norm");
+    static_assert(NORM != 3 || (MODE == 0 && RT == 1), "the in-block norm serves plain one-tile GEMVs");
+    static_assert(!CONV || NORM == 3, "the conv epilogue comes with the in-block norm");
     if constexpr (RTE != 0) {
-        const uint32_t j = blockIdx.y;
+        const uint32_t j = by;
         uint32_t e;
         if constexpr (RTE == 2) {
             __shared__ int32_t route_id[8];
@@ -1277,7 +1292,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __res
                                                 threadIdx.x);
             }
             __syncthreads();
-            if (blockIdx.x == 0 && j == 0 && threadIdx.x < route.routes) {
+            if (bx == 0 && j == 0 && threadIdx.x < route.routes) {
                 route.ids_out[threadIdx.x] = route_id[threadIdx.x];
                 route.weights_out[threadIdx.x] = route_w[threadIdx.x];
             }
@@ -1300,7 +1315,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __res
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t r = lane & 15, s = lane >> 4;
     const uint32_t tiles = (n + 15) / 16;
-    const uint32_t tile0 = blockIdx.x * RT;
+    const uint32_t tile0 = bx * RT;
     const size_t tile_bytes = static_cast<size_t>(units) * kTileUnit;
     const uint8_t* wt[NA];
 #pragma unroll
@@ -1315,7 +1330,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __res
     // same moment, from the same few L2 channels.
     const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
     const uint32_t mine = units > wv ? (units - wv + WPB - 1) / WPB : 0;
-    const uint32_t rot = blockIdx.x % units;
+    const uint32_t rot = bx % units;
     struct Slot {
         uint4 x;
         typename F::Unit w[NA];
@@ -1324,7 +1339,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __res
     auto fill = [&](uint32_t idx) {
         uint32_t u = wv + idx * WPB + rot;
         if (u >= units) u -= units;
-        sl.x = xsrc[64 * u + lane];
+        if constexpr (NORM != 3) sl.x = xsrc[64 * u + lane];
 #pragma unroll
         for (int t = 0; t < NA; ++t) sl.w[t] = F::load(wt[t] + static_cast<size_t>(u) * kTileUnit, r, s, lane);
     };
@@ -1346,12 +1361,22 @@ __global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __res
     // The epilogue's per-row operands, loaded now rather than after the
     // block reduction (same values, same sums).
     float pre_b = 0.0f, pre_r = 0.0f, pre_g = 0.0f;
+    float ctap[kX16ConvMax], chist[kX16ConvMax - 1];
     if (MODE == 0 && tid < 16 * RT) {
         const uint32_t row = tile0 * 16 + tid;
         if (row < n) {
             if (bias) pre_b = bias[row];
             if (residual) pre_r = residual[row];
             if (NORM == 2) pre_g = nrm.gamma_out[row];
+            if (CONV && cv.w) {
+#pragma unroll
+                for (uint32_t j = 0; j < kX16ConvMax; ++j) {
+                    ctap[j] = j < cv.ksize ? cv.w[static_cast<size_t>(row) * cv.ksize + j] : 0.0f;
+                    if (j + 1 < kX16ConvMax) {
+                        chist[j] = j + 1 < cv.ksize ? cv.history[static_cast<size_t>(j) * cv.channels + row] : 0.0f;
+                    }
+                }
+            }
         }
     }
     __shared__ float inv_s;
@@ -1373,7 +1398,26 @@ __global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __res
             inv_s = 1.0f / sqrtf(ms + nrm.eps);
         }
     }
-    for (uint32_t idx = 0; idx < mine; ++idx) {
+    // NORM 3: the block normalises the raw input row into LDS (the XGroup
+    // form of x * inv * gamma, the same bits as the standalone RMSNorm) while
+    // its first weight loads are in flight; the waves read their A slices
+    // and (sum, e) pairs straight from there.
+    extern __shared__ __align__(16) uint8_t x16_norm_lds[];  // 4 k bytes, sized at launch
+    if constexpr (NORM == 3) {
+        rmsnorm_row_lean(nrm.x_in, nrm.gamma_in, nullptr, reinterpret_cast<XGroup*>(x16_norm_lds), 256 * units,
+                         nrm.eps);
+        __syncthreads();
+        for (uint32_t idx = 0; idx < mine; ++idx) {
+            uint32_t u = wv + idx * WPB + rot;
+            if (u >= units) u -= units;
+            const uint8_t* xu = x16_norm_lds + 1024 * u;
+            const uint8_t* a_u = a_lane ? xu + slot + 16 * (r & 3) : lds + 1024;
+#pragma unroll
+            for (int t = 0; t < NA; ++t) acc[t] = F::unit(sl.w[t], a_u, xu + slot + 48, r, s, acc[t]);
+            if (idx + 1 < mine) fill(idx + 1);
+        }
+    }
+    for (uint32_t idx = 0; NORM != 3 && idx < mine; ++idx) {
         *reinterpret_cast<uint4*>(lds + 16 * lane) = sl.x;
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -1408,6 +1452,21 @@ __global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __res
         } else if (row < n) {
             if (bias) v += pre_b;
             if (residual) v += pre_r;
+            if (CONV && cv.w) {
+                // conv1d_silu_kernel's sum: the history rows in order, then x.
+                const uint32_t hr = cv.ksize - 1;
+                float cacc = 0.0f;
+#pragma unroll
+                for (uint32_t j = 0; j < kX16ConvMax; ++j) {
+                    const float win = j < hr ? chist[j] : v;
+                    if (j < cv.ksize) cacc += win * ctap[j];
+                    if (j < hr) {
+                        const float next = j + 1 < hr ? chist[j + 1 < kX16ConvMax - 1 ? j + 1 : 0] : v;
+                        cv.history[static_cast<size_t>(j) * cv.channels + row] = next;
+                    }
+                }
+                v = cacc * sigmoid_ref(cacc);
+            }
         }
         if (row < n) y[row] = v;
         if (NORM == 2) {
@@ -1432,6 +1491,41 @@ __global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __res
             }
             nrm.sumsq_out[tile0 + tid] = ss;
         }
+    }
+}
+
+template <uint32_t QT, int WPB, int RT, int MODE, int NORM, int RTE = 0>
+__global__ __launch_bounds__(64 * WPB) void gemv_x16_kernel(const uint8_t* __restrict__ w,
+                                                            const uint8_t* __restrict__ w2,
+                                                            const XGroup* __restrict__ xq,
+                                                            const float* __restrict__ bias,
+                                                            const float* __restrict__ residual,
+                                                            float* __restrict__ y, XGroup* __restrict__ yq,
+                                                            uint32_t n, uint32_t units, X16Norm nrm,
+                                                            X16Route route = X16Route{}) {
+    x16_body<QT, WPB, RT, MODE, NORM, RTE, false>(w, w2, xq, bias, residual, y, yq, n, units, nrm, route, X16Conv{},
+                                                  blockIdx.x, blockIdx.y);
+}
+
+// Two plain GEMVs of one normalised row in one launch (NORM 3: every block
+// normalises the raw row itself): blocks [0, blocks_a) compute job A's 16-row
+// tiles (with the conv epilogue when cv.w is set), the rest job B's. QA and
+// QB are the jobs' x16 types.
+struct X16Job {
+    const uint8_t* w;
+    float* y;
+    uint32_t n;
+};
+
+template <uint32_t QA, uint32_t QB, int WPB>
+__global__ __launch_bounds__(64 * WPB) void gemv_x16_pair_kernel(const X16Job a, const X16Job b, uint32_t blocks_a,
+                                                                 uint32_t units, X16Norm nrm, X16Conv cv) {
+    if (blockIdx.x < blocks_a) {
+        x16_body<QA, WPB, 1, 0, 3, 0, true>(a.w, nullptr, nullptr, nullptr, nullptr, a.y, nullptr, a.n, units, nrm,
+                                            X16Route{}, cv, blockIdx.x, 0);
+    } else {
+        x16_body<QB, WPB, 1, 0, 3, 0, false>(b.w, nullptr, nullptr, nullptr, nullptr, b.y, nullptr, b.n, units, nrm,
+                                             X16Route{}, X16Conv{}, blockIdx.x - blocks_a, 0);
     }
 }
 
@@ -1673,6 +1767,51 @@ int launch_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, cons
     return type == kQ4_K
                ? launch_x16_norm<kQ4_K, 1>(kind, code, g, u, xq, nullptr, nullptr, y, yq, nn, units, norm, stream)
                : launch_x16_norm<kQ6_K, 1>(kind, code, g, u, xq, nullptr, nullptr, y, yq, nn, units, norm, stream);
+}
+
+namespace {
+template <uint32_t QA, uint32_t QB>
+int launch_x16_pair_types(int wpb, const X16Job& a, const X16Job& b, uint32_t blocks, uint32_t blocks_a,
+                          uint32_t units, const X16Norm& nrm, const X16Conv& cv, hipStream_t stream) {
+    const size_t lds = static_cast<size_t>(units) * 1024;
+    if (wpb == 4) {
+        HIPLLM_LAUNCH((gemv_x16_pair_kernel<QA, QB, 4>), dim3(blocks), dim3(256), lds, stream, a, b, blocks_a, units,
+                      nrm, cv);
+    } else {
+        HIPLLM_LAUNCH((gemv_x16_pair_kernel<QA, QB, 8>), dim3(blocks), dim3(512), lds, stream, a, b, blocks_a, units,
+                      nrm, cv);
+    }
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+}  // namespace
+
+// Measured shape: one tile per block, 8 waves from 8 units up (one or two
+// units per wave), 4 below.
+int launch_gemv_x16_pair(uint32_t type_a, const void* packed_a, size_t n_a, float* y_a, uint32_t type_b,
+                         const void* packed_b, size_t n_b, float* y_b, size_t k, const float* x, const float* gamma,
+                         float eps, const float* conv_w, float* history, size_t ksize, hipStream_t stream) {
+    int rc = check_x16(type_a, packed_a, reinterpret_cast<const XGroup*>(x), y_a, n_a, k);
+    if (rc == kOk) rc = check_x16(type_b, packed_b, reinterpret_cast<const XGroup*>(x), y_b, n_b, k);
+    if (rc != kOk) return rc;
+    if (!gamma || reinterpret_cast<uintptr_t>(gamma) % 16 != 0 || !(eps > 0.0f) || k > 8192) return kInvalidArgument;
+    if (conv_w && (!history || ksize < 2 || ksize > kX16ConvMax)) return kInvalidArgument;
+    const uint32_t units = static_cast<uint32_t>(k / 256);
+    const uint32_t blocks_a = static_cast<uint32_t>((n_a + 15) / 16), blocks_b = static_cast<uint32_t>((n_b + 15) / 16);
+    const X16Job a{static_cast<const uint8_t*>(packed_a), y_a, static_cast<uint32_t>(n_a)};
+    const X16Job b{static_cast<const uint8_t*>(packed_b), y_b, static_cast<uint32_t>(n_b)};
+    X16Norm nrm{};
+    nrm.eps = eps;
+    nrm.x_in = x;
+    nrm.gamma_in = gamma;
+    const X16Conv cv{conv_w, history, static_cast<uint32_t>(n_a), static_cast<uint32_t>(ksize)};
+    const int wpb = units >= 8 ? 8 : 4;
+    const uint32_t blocks = blocks_a + blocks_b;
+    if (type_a == kQ4_K) {
+        return type_b == kQ4_K ? launch_x16_pair_types<kQ4_K, kQ4_K>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream)
+                               : launch_x16_pair_types<kQ4_K, kQ6_K>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream);
+    }
+    return type_b == kQ4_K ? launch_x16_pair_types<kQ6_K, kQ4_K>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream)
+                           : launch_x16_pair_types<kQ6_K, kQ6_K>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream);
 }
 
 namespace {

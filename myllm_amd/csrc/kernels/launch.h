@@ -113,11 +113,20 @@ struct X16Norm {
     const float* gamma_out;
     XGroup* yq_out;
     double* sumsq_out;
+    const float* x_in;      // the raw row normalised in every block (paired launch)
+    const float* gamma_in;
 };
 int launch_gemv_x16(uint32_t type, const void* packed, const XGroup* xq, const float* bias, const float* residual,
                     float* y, size_t n, size_t k, int waves, hipStream_t stream, const X16Norm* norm = nullptr);
 int launch_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, const XGroup* xq, float* y, XGroup* yq,
                            size_t n, size_t k, int waves, hipStream_t stream, const X16Norm* norm = nullptr);
+// y_a = conv(W_a rmsnorm(x) * gamma) (conv + SiLU over history when conv_w
+// is set, channel = row) and y_b = W_b rmsnorm(x) * gamma in one launch, each
+// block normalising the raw row x itself (k <= 8192, x and gamma 16-byte
+// aligned, ksize <= 4).
+int launch_gemv_x16_pair(uint32_t type_a, const void* packed_a, size_t n_a, float* y_a, uint32_t type_b,
+                         const void* packed_b, size_t n_b, float* y_b, size_t k, const float* x, const float* gamma,
+                         float eps, const float* conv_w, float* history, size_t ksize, hipStream_t stream);
 // One token's routed expert vectors over the x16 copy of a whole expert block
 // ([experts * n, k], n rows per expert, n % 16 == 0): route j multiplies
 // expert ids[j] (or, with logits, the router's top-k picked in the kernel,
@@ -206,6 +215,14 @@ int launch_gdn_scan_gated(const float* q, const float* k, size_t ldqk, const flo
                           const float* z, size_t ldz, const float* gamma, float* y, XGroup* yq, size_t ldy,
                           size_t tokens, size_t value_heads, size_t key_heads, size_t d, float eps,
                           hipStream_t stream);
+// One decode token after the projections (launch_gemv_x16_pair made the
+// convolved [Q | K | V] row qkv and the gate row z): alpha / beta from the
+// F32 projection ab_w ([2 value_heads, hidden], hidden <= 4096) of
+// rmsnorm(x) * x_gamma, the Q / K L2 norms, then launch_gdn_scan_gated's
+// step; one block per value head.
+int launch_gdn_decode(const float* qkv, const float* x, const float* x_gamma, const float* ab_w, size_t hidden,
+                      const float* dt_bias, const float* a, float* state, const float* z, const float* gamma, float* y,
+                      XGroup* yq, size_t value_heads, size_t key_heads, size_t d, float eps, hipStream_t stream);
 int launch_gated_rmsnorm(const float* o, size_t ldo, const float* gamma, const float* z, size_t ldz, float* y,
                          XGroup* yq, size_t ldy, size_t tokens, size_t heads, size_t d, float eps,
                          hipStream_t stream);

@@ -817,6 +817,150 @@ __global__ __launch_bounds__(256) void gdn_scan_gated_kernel(
     for (uint32_t i = 0; i < NPR; ++i) S[static_cast<size_t>(rg * NPR + i) * D + col] = s[i];
 }
 
+// One decode token of a Gated DeltaNet layer after its projections, block h
+// = value head h (256 threads). qkv is the token's convolved [Q (G D) | K
+// (G D) | V (Hv D)] row (the conv + SiLU ran in the projection's epilogue),
+// z the gate row. The block also makes its own two gate inputs: with x the
+// layer's raw input row and x_gamma its RMSNorm gain, alpha_h and beta_h are
+// the dots of rows h and Hv + h of the F32 projection ab_w ([2 Hv, hidden])
+// with rmsnorm(x) * x_gamma (double sum of squares as in the RMSNorm
+// kernel). Then the L2 norms of Q and K head kh = h % G (wave sums in order,
+// as conv_l2norm_kernel), and gdn_scan_gated_kernel's gates, recurrence and
+// gated RMSNorm. All loads are issued at the start: state, the head's Q, K,
+// V and z values, x, its gain and the two projection rows.
+constexpr uint32_t kGdnDecodeMaxHidden = 4096;
+
+template <uint32_t D>
+__global__ __launch_bounds__(256) void gdn_decode_kernel(
+    const float* __restrict__ qkv, const float* __restrict__ x, const float* __restrict__ x_gamma,
+    const float* __restrict__ ab_w, uint32_t hidden, const float* __restrict__ dt_bias, const float* __restrict__ a,
+    float* __restrict__ state, const float* __restrict__ z, const float* __restrict__ gamma, float* __restrict__ y,
+    XGroup* __restrict__ yq, uint32_t value_heads, uint32_t key_heads, float eps) {
+    constexpr uint32_t RG = 256 / D, NPR = D / RG;
+    constexpr uint32_t NX = kGdnDecodeMaxHidden / 256;
+    const uint32_t h = blockIdx.x, tid = threadIdx.x;
+    const uint32_t col = tid % D, rg = tid / D, wave = tid >> 6, lane = tid & 63;
+    const uint32_t G = key_heads, kh = h % G;
+    float* S = state + static_cast<size_t>(h) * D * D;
+    float s[NPR];
+#pragma unroll
+    for (uint32_t i = 0; i < NPR; ++i) s[i] = S[static_cast<size_t>(rg * NPR + i) * D + col];
+    const float qk = tid < 2 * D ? qkv[(tid < D ? kh : G + kh) * D + tid % D] : 0.0f;
+    const float vv = qkv[(2 * G + h) * D + col];
+    const float zz = z[static_cast<size_t>(h) * D + col];
+    const float dtb = dt_bias[h], ah = a[h], gam = gamma[col];
+    const float* wa = ab_w + static_cast<size_t>(h) * hidden;
+    const float* wb = ab_w + static_cast<size_t>(value_heads + h) * hidden;
+    float xv[NX], gv[NX], av[NX], bv[NX];
+#pragma unroll
+    for (uint32_t i = 0; i < NX; ++i) {
+        const uint32_t e = tid + 256 * i;
+        const bool ok = e < hidden;
+        xv[i] = ok ? x[e] : 0.0f;
+        gv[i] = ok ? x_gamma[e] : 0.0f;
+        av[i] = ok ? wa[e] : 0.0f;
+        bv[i] = ok ? wb[e] : 0.0f;
+    }
+    __shared__ double red_d[4];
+    __shared__ float red_f[3][4];
+    // Input RMSNorm and the two gate dots.
+    double ss = 0.0;
+#pragma unroll
+    for (uint32_t i = 0; i < NX; ++i) ss += static_cast<double>(xv[i]) * xv[i];
+    ss = wave_sum_d(ss);
+    // Q / K head sums of squares (waves [0, D / 64) hold Q, the next D / 64 K).
+    const float qss = wave_sum(qk * qk);
+    if (lane == 0) {
+        red_d[wave] = ss;
+        red_f[0][wave] = qss;
+    }
+    __syncthreads();
+    const double tot = (red_d[0] + red_d[1]) + (red_d[2] + red_d[3]);
+    const float inv = 1.0f / sqrtf(static_cast<float>(tot / static_cast<double>(hidden)) + eps);
+    float da = 0.0f, db = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < NX; ++i) {
+        const float xn = xv[i] * (inv * gv[i]);
+        da = fmaf(av[i], xn, da);
+        db = fmaf(bv[i], xn, db);
+    }
+    da = wave_sum(da);
+    db = wave_sum(db);
+    if (lane == 0) {
+        red_f[1][wave] = da;
+        red_f[2][wave] = db;
+    }
+    __shared__ float ks[D], qs[D];
+    if (tid < 2 * D) {
+        const uint32_t seg = tid / D;
+        float t = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < D / 64; ++j) t += red_f[0][seg * (D / 64) + j];
+        const float v = qk * (1.0f / sqrtf(t + eps));
+        if (seg == 0) {
+            qs[tid] = v;
+        } else {
+            ks[tid - D] = v;
+        }
+    }
+    __syncthreads();
+    const float alpha = (red_f[1][0] + red_f[1][1]) + (red_f[1][2] + red_f[1][3]);
+    const float beta_raw = (red_f[2][0] + red_f[2][1]) + (red_f[2][2] + red_f[2][3]);
+
+    // gdn_scan_gated_kernel's token step.
+    __shared__ float part[RG][D];
+    __shared__ float red[D / 64];
+    __shared__ __align__(16) float vals[D];
+    const float qscale = 1.0f / sqrtf(static_cast<float>(D));
+    const float g = expf(softplus_ref(alpha + dtb) * ah);
+    const float b = sigmoid_ref(beta_raw);
+    float pp = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < NPR; ++i) {
+        s[i] *= g;
+        pp += s[i] * ks[rg * NPR + i];
+    }
+    part[rg][col] = pp;
+    __syncthreads();
+    float pred = 0.0f;
+#pragma unroll
+    for (uint32_t q = 0; q < RG; ++q) pred += part[q][col];
+    const float delta = b * (vv - pred);
+    float op = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < NPR; ++i) {
+        s[i] += ks[rg * NPR + i] * delta;
+        op += s[i] * qs[rg * NPR + i];
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < NPR; ++i) S[static_cast<size_t>(rg * NPR + i) * D + col] = s[i];
+    __syncthreads();  // everyone has read part[] (pred) before it is reused
+    part[rg][col] = op;
+    __syncthreads();
+    float o = 0.0f;
+#pragma unroll
+    for (uint32_t q = 0; q < RG; ++q) o += part[q][col];
+    o *= qscale;
+    if (rg == 0) {
+        const float oss = wave_sum(o * o);
+        if ((col & 63) == 0) red[col >> 6] = oss;
+    }
+    __syncthreads();
+    if (rg == 0) {
+        float t = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < D / 64; ++i) t += red[i];
+        const float on = 1.0f / sqrtf(t / static_cast<float>(D) + eps);
+        const float yv = o * on * gam * (zz * sigmoid_ref(zz));
+        y[static_cast<size_t>(h) * D + col] = yv;
+        vals[col] = yv;
+    }
+    if (yq) {
+        __syncthreads();
+        if (tid < D / 16) xgroup_encode_from(vals + 16 * tid, yq + static_cast<size_t>(h) * (D / 16) + tid);
+    }
+}
+
 // y = rmsnorm(o_head) * gamma * silu(z) per (row, value head); FP32 sum of
 // squares like the reference's per-head norm; yq (optional) the XGroup form
 // of y.
@@ -1193,6 +1337,34 @@ int launch_gdn_scan_gated(const float* q, const float* k, size_t ldqk, const flo
         HIPLLM_LAUNCH(gdn_scan_gated_kernel<128>, grid, dim3(256), 0, stream, q, k, static_cast<uint32_t>(ldqk), v,
                            static_cast<uint32_t>(ldv), alpha, beta_raw, static_cast<uint32_t>(ld_ab), dt_bias, a,
                            state, z, static_cast<uint32_t>(ldz), gamma, y, yq, static_cast<uint32_t>(ldy), T, Hk, eps);
+        break;
+    default:
+        return kInvalidArgument;  // state size 64 or 128
+    }
+    return launched();
+}
+
+int launch_gdn_decode(const float* qkv, const float* x, const float* x_gamma, const float* ab_w, size_t hidden,
+                      const float* dt_bias, const float* a, float* state, const float* z, const float* gamma, float* y,
+                      XGroup* yq, size_t value_heads, size_t key_heads, size_t d, float eps, hipStream_t stream) {
+    if (!qkv || !x || !x_gamma || !ab_w || !dt_bias || !a || !state || !z || !gamma || !y || key_heads == 0 ||
+        value_heads == 0 || value_heads % key_heads != 0 || hidden == 0 || hidden > kGdnDecodeMaxHidden ||
+        !(eps > 0.0f)) {
+        return kInvalidArgument;
+    }
+    if (yq && reinterpret_cast<uintptr_t>(yq) % 16 != 0) return kInvalidArgument;
+    if (value_heads > 65535) return kLengthError;
+    const dim3 grid(static_cast<uint32_t>(value_heads));
+    const uint32_t Hv = static_cast<uint32_t>(value_heads), Hk = static_cast<uint32_t>(key_heads),
+                   Hd = static_cast<uint32_t>(hidden);
+    switch (d) {
+    case 64:
+        HIPLLM_LAUNCH(gdn_decode_kernel<64>, grid, dim3(256), 0, stream, qkv, x, x_gamma, ab_w, Hd, dt_bias, a, state,
+                      z, gamma, y, yq, Hv, Hk, eps);
+        break;
+    case 128:
+        HIPLLM_LAUNCH(gdn_decode_kernel<128>, grid, dim3(256), 0, stream, qkv, x, x_gamma, ab_w, Hd, dt_bias, a,
+                      state, z, gamma, y, yq, Hv, Hk, eps);
         break;
     default:
         return kInvalidArgument;  // state size 64 or 128

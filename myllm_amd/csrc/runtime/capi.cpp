@@ -246,6 +246,15 @@ int hipllm_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, cons
                   "launch failure");
 }
 
+int hipllm_gemv_x16_pair(uint32_t type_a, const void* packed_a, size_t n_a, float* y_a, uint32_t type_b,
+                         const void* packed_b, size_t n_b, float* y_b, size_t k, const float* x, const float* gamma,
+                         float eps, const float* conv_w, float* history, size_t ksize, void* stream) {
+    return status(hipllm::launch_gemv_x16_pair(type_a, packed_a, n_a, y_a, type_b, packed_b, n_b, y_b, k, x, gamma,
+                                                eps, conv_w, history, ksize, as_stream(stream)),
+                  "hipllm_gemv_x16_pair: invalid arguments (Q4_K or Q6_K, k % 256 == 0, k <= 8192, 16-byte aligned "
+                  "buffers, eps > 0, ksize 2..4 with a history) or launch failure");
+}
+
 int hipllm_gemv_x16_routed(uint32_t type, const void* packed, const void* packed2, const void* xq, size_t ldx,
                            int x_routed, float* y, void* yq, size_t ldy, size_t n, size_t k, size_t experts,
                            size_t routes, const int32_t* ids, const float* logits, int32_t* ids_out,
@@ -707,6 +716,14 @@ int hipllm_gdn_scan_gated(const float* q, const float* k, size_t ldqk, const flo
                                                 gamma, y, xg(yq), ldy, tokens, value_heads, key_heads, d, eps,
                                                 as_stream(stream)),
                   "hipllm_gdn_scan_gated: invalid arguments (state size 64 or 128) or launch failure");
+}
+
+int hipllm_gdn_decode(const float* qkv, const float* x, const float* x_gamma, const float* ab_w, size_t hidden,
+                      const float* dt_bias, const float* a, float* state, const float* z, const float* gamma, float* y,
+                      void* yq, size_t value_heads, size_t key_heads, size_t d, float eps, void* stream) {
+    return status(hipllm::launch_gdn_decode(qkv, x, x_gamma, ab_w, hidden, dt_bias, a, state, z, gamma, y, xg(yq),
+                                            value_heads, key_heads, d, eps, as_stream(stream)),
+                  "hipllm_gdn_decode: invalid arguments (state size 64 or 128, hidden <= 4096) or launch failure");
 }
 
 int hipllm_split_qgate_norm(const float* mixed, size_t ldm, const float* kv, size_t ldkv, const float* q_gamma,

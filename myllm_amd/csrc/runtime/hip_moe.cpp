@@ -205,6 +205,7 @@ struct HipMoeLLM::Impl {
     void grouped(const hipllm::GemvJob* jobs, std::size_t count, const float* x, const float* gamma,
                  bool store_norm, const char* what) const;
     bool grouped_mixer(const MoeLayer& L, std::size_t rows) const;
+    bool x16_deltanet(const MoeLayer& L, std::size_t rows) const;
     bool gathered_experts(const MoeLayer& L, std::size_t rows, const void* xb) const;
     bool grouped_moe(const MoeLayer& L, std::size_t rows) const;
     void attention_layer(std::size_t li, std::size_t rows, std::size_t pos0, float* hidden, float* next,
@@ -315,6 +316,10 @@ void HipMoeLLM::Impl::pack_decode_weights() {
     };
     for (MoeLayer& L : layers) {
         jobs.push_back({L.full ? &L.o : &L.ssm_out, (L.full ? L.o : L.ssm_out).rows});
+        if (!L.full && x16_packable(L.qkv) && x16_packable(L.z)) {
+            jobs.push_back({&L.qkv, L.qkv.rows});
+            jobs.push_back({&L.z, L.z.rows});
+        }
         if (expert_block(L.gate_exps) && expert_block(L.up_exps) && L.gate_exps.type == L.up_exps.type &&
             expert_block(L.down_exps)) {
             jobs.push_back({&L.gate_exps, E * L.gate_exps.rows});
@@ -721,6 +726,16 @@ bool HipMoeLLM::Impl::grouped_mixer(const MoeLayer& L, std::size_t rows) const {
     return groupable(L.qkv) && groupable(L.z) && L.fused_ab && groupable(L.alpha);
 }
 
+// Whether DeltaNet layer L's decode step runs on the x16 copies: QKV (with
+// the conv in its epilogue) and z as one paired launch that normalises the
+// input in every block, then one launch per value head for alpha / beta,
+// the L2 norms, the recurrence and the gated norm.
+bool HipMoeLLM::Impl::x16_deltanet(const MoeLayer& L, std::size_t rows) const {
+    return !L.full && rows == 1 && grouped_mixer(L, rows) && L.qkv.x16 && L.z.x16 &&
+           L.alpha.type == hipllm::kF32 && L.fused_ab && H <= 4096 && (S == 64 || S == 128) &&
+           config.ssm_conv_kernel >= 2 && config.ssm_conv_kernel <= 4;
+}
+
 // Whether layer L's routed experts run as gathered fp16 matmuls: a prompt
 // whose dense projections already run as matmuls (xb holds its fp16 rows)
 // and routes at least four vectors per expert on average. Each group block
@@ -800,6 +815,20 @@ void HipMoeLLM::Impl::attention_layer(std::size_t li, std::size_t rows, std::siz
 void HipMoeLLM::Impl::deltanet_layer(std::size_t li, std::size_t rows, float* hidden, float* next) {
     const MoeLayer& L = layers[li];
     const float eps = config.norm_epsilon;
+    if (x16_deltanet(L, rows)) {
+        launch_check(hipllm::launch_gemv_x16_pair(L.qkv.type, L.qkv.x16, qkv_w, act.wide, L.z.type, L.z.x16, inner,
+                                                  act.feat, H, hidden, L.attn_norm, eps, L.conv, L.history,
+                                                  config.ssm_conv_kernel, stream),
+                     "input norm + DeltaNet QKV (+ conv) / z");
+        launch_check(hipllm::launch_gdn_decode(act.wide, hidden, L.attn_norm,
+                                               reinterpret_cast<const float*>(L.alpha.ptr), H, L.dt_bias, L.a,
+                                               L.state, act.feat, L.ssm_norm, act.gated, act.gatedq, Hv, G, S, eps,
+                                               stream),
+                     "DeltaNet alpha / beta + L2 norms + scan + gated norm");
+        proj_out_norm(L.ssm_out, act.gated, act.gatedq, inner, rows, next, hidden, L.post_norm,
+                      !grouped_moe(L, rows));
+        return;
+    }
     if (grouped_mixer(L, rows)) {
         const hipllm::GemvJob jobs[3] = {job(L.qkv, act.wide, L.qkv.rows), job(L.z, act.feat, L.z.rows),
                                          job(L.alpha, act.ab, 2 * Hv)};

@@ -135,6 +135,8 @@ SIGNATURES = {
     "hipllm_conv_l2norm": (_I, [_P, _S, _P, _P, _P, _S, _S, _S, _S, _S, _S, _F, _P]),
     "hipllm_gdn_scan_gated": (_I, [_P, _P, _S, _P, _S, _P, _P, _S, _P, _P, _P, _P, _S, _P, _P, _P, _S, _S, _S, _S,
                                    _S, _F, _P]),
+    "hipllm_gdn_decode": (_I, [_P, _P, _P, _P, _S, _P, _P, _P, _P, _P, _P, _P, _S, _S, _S, _F, _P]),
+    "hipllm_gemv_x16_pair": (_I, [_U32, _P, _S, _P, _U32, _P, _S, _P, _S, _P, _P, _F, _P, _P, _S, _P]),
     "hipllm_split_qgate_norm": (_I, [_P, _S, _P, _S, _P, _P, _P, _S, _P, _S, _S, _S, _S, _S, _F, _P]),
     "hipllm_gate_mul": (_I, [_P, _P, _P, _P, _S, _P]),
     "hipllm_destroy": (None, [_P]),
@@ -746,6 +748,19 @@ def _k_gdn_scan_gated(q, k, ldqk, v, ldv, alpha, beta_raw, ld_ab, dt_bias, a, st
                                       ldy, tokens, value_heads, key_heads, d, eps, _stream(stream)))
 
 
+def _k_gdn_decode(qkv, x, x_gamma, ab_w, hidden, dt_bias, a, state, z, gamma, y, yq, value_heads, key_heads, d,
+                  eps, stream=None):
+    check(lib().hipllm_gdn_decode(_ptr(qkv), _ptr(x), _ptr(x_gamma), _ptr(ab_w), hidden, _ptr(dt_bias), _ptr(a),
+                                  _ptr(state), _ptr(z), _ptr(gamma), _ptr(y), _ptr(yq), value_heads, key_heads, d, eps,
+                                  _stream(stream)))
+
+
+def _k_gemv_x16_pair(type_a, packed_a, n_a, y_a, type_b, packed_b, n_b, y_b, k, x, gamma, eps, conv_w=None,
+                     history=None, ksize=0, stream=None):
+    check(lib().hipllm_gemv_x16_pair(type_a, _ptr(packed_a), n_a, _ptr(y_a), type_b, _ptr(packed_b), n_b, _ptr(y_b), k,
+                                     _ptr(x), _ptr(gamma), eps, _ptr(conv_w), _ptr(history), ksize, _stream(stream)))
+
+
 def _k_split_qgate_norm(mixed, ldm, kv, ldkv, q_gamma, k_gamma, qkv, ldqkv, gate, ldg, tokens, hq, hkv, d, eps,
                         stream=None):
     check(lib().hipllm_split_qgate_norm(_ptr(mixed), ldm, _ptr(kv), ldkv, _ptr(q_gamma), _ptr(k_gamma), _ptr(qkv),
@@ -813,7 +828,8 @@ kernels = types.SimpleNamespace(
     conv1d_silu=_k_conv1d_silu, l2norm_heads=_k_l2norm_heads, gdn_scan=_k_gdn_scan, gated_rmsnorm=_k_gated_rmsnorm,
     gdn_scan_chunked=_k_gdn_scan_chunked,
     gdn_chunk_scratch_floats=lambda t, h: lib().hipllm_gdn_chunk_scratch_floats(t, h),
-    conv_l2norm=_k_conv_l2norm, gdn_scan_gated=_k_gdn_scan_gated,
+    conv_l2norm=_k_conv_l2norm, gdn_scan_gated=_k_gdn_scan_gated, gdn_decode=_k_gdn_decode,
+    gemv_x16_pair=_k_gemv_x16_pair,
     split_qgate_norm=_k_split_qgate_norm, gate_mul=_k_gate_mul,
     gemv_workspace_bytes=lambda k: lib().hipllm_gemv_workspace_bytes(k),
     attn_decode_scratch_floats=lambda hq, d, n: lib().hipllm_attn_decode_scratch_floats(hq, d, n),

@@ -348,3 +348,62 @@ def test_gemv_x16_norm_rejects_bad_combinations(cuda):
     xb = xgroup.buffer(torch, big, cuda)
     with pytest.raises(ValueError):  # input form beyond 8192 values
         kernels.gemv_x16(synth.Q4_K, pb, xb, None, None, y, 16, big, 0, norm={"sumsq_in": ssq})
+
+
+@pytest.mark.parametrize("ta,tb,na,nb,k,ksize", [(synth.Q6_K, synth.Q4_K, 96, 64, 2048, 4),
+                                                (synth.Q4_K, synth.Q6_K, 40, 37, 512, 3),
+                                                (synth.Q4_K, synth.Q4_K, 64, 48, 768, 0)])
+def test_pair_norm_conv_matches_float64(cuda, ta, tb, na, nb, k, ksize):
+    """Two GEMVs of one row in one launch, each block normalising the raw row
+    itself, job A with the causal conv + SiLU epilogue (history shifted by one
+    row), against float64 over the oracle's dequantization; two calls in a
+    row, so the second reads the history the first wrote."""
+    wa, wb = random_rows(ta, na, k, 61), random_rows(tb, nb, k, 62)
+    pa = torch.empty(kernels.x16_bytes(ta, na, k), dtype=torch.uint8, device=cuda)
+    pb = torch.empty(kernels.x16_bytes(tb, nb, k), dtype=torch.uint8, device=cuda)
+    kernels.pack_x16(ta, dev_bytes(wa, cuda), wa.shape[1], na, k, pa)
+    kernels.pack_x16(tb, dev_bytes(wb, cuda), wb.shape[1], nb, k, pb)
+    fa = oracle.dequant_rows(ta, wa, k).astype(np.float64)
+    fb = oracle.dequant_rows(tb, wb, k).astype(np.float64)
+    rng = np.random.default_rng(63)
+    gamma = rng.normal(size=k).astype(np.float32)
+    conv = rng.normal(scale=0.5, size=(na, max(ksize, 1))).astype(np.float32)
+    hist = rng.normal(size=(max(ksize - 1, 1), na)).astype(np.float32)
+    dconv = torch.from_numpy(conv).to(cuda) if ksize else None
+    dhist = torch.from_numpy(hist.copy()).to(cuda) if ksize else None
+    for call in range(2):
+        x = rng.normal(size=k).astype(np.float32)
+        ya = torch.empty(na, device=cuda)
+        yb = torch.empty(nb, device=cuda)
+        kernels.gemv_x16_pair(ta, pa, na, ya, tb, pb, nb, yb, k, torch.from_numpy(x).to(cuda),
+                              torch.from_numpy(gamma).to(cuda), 1e-6, dconv, dhist, ksize)
+        xs = x.astype(np.float64)
+        n = xs / np.sqrt(np.mean(xs * xs) + 1e-6) * gamma
+        pre = fa @ n
+        assert rel_err(yb.cpu().numpy(), fb @ n) <= 1e-3, call
+        if not ksize:
+            assert rel_err(ya.cpu().numpy(), pre) <= 1e-3, call
+            continue
+        win = np.concatenate([hist.astype(np.float64), pre[None, :]])  # [ksize, na]
+        o = np.einsum("jc,cj->c", win, conv.astype(np.float64))
+        assert rel_err(ya.cpu().numpy(), o / (1.0 + np.exp(-o))) <= 1e-3, call
+        got_hist = dhist.cpu().numpy()
+        np.testing.assert_array_equal(got_hist[:-1], hist[1:])
+        assert rel_err(got_hist[-1], pre) <= 1e-3, call
+        hist = got_hist.copy()
+
+
+def test_pair_rejects_bad_arguments(cuda):
+    w = torch.zeros(kernels.x16_bytes(synth.Q4_K, 16, 512), dtype=torch.uint8, device=cuda)
+    v = torch.zeros(512, device=cuda)
+    ok = (synth.Q4_K, w, 16, v, synth.Q4_K, w, 16, v, 512, v, v, 1e-6)
+    kernels.gemv_x16_pair(*ok)
+    for i, bad in ((0, synth.Q8_0), (8, 320), (11, 0.0)):
+        args = list(ok)
+        args[i] = bad
+        with pytest.raises(ValueError):
+            kernels.gemv_x16_pair(*args)
+    with pytest.raises(ValueError):  # conv without a history
+        kernels.gemv_x16_pair(*ok, conv_w=v, history=None, ksize=4)
+    with pytest.raises(ValueError):  # ksize beyond the epilogue's four taps
+        kernels.gemv_x16_pair(*ok, conv_w=v, history=v, ksize=5)

@@ -588,6 +588,51 @@ def test_gdn_scan_gated_matches_float64_steps(cuda, d, Hv, G):
     xgroup.check(yq, got)
 
 
+@pytest.mark.parametrize("d,Hv,G,H", [(128, 32, 16, 2048), (64, 4, 2, 512), (64, 6, 3, 768)])
+def test_gdn_decode_matches_float64_step(cuda, d, Hv, G, H):
+    # One decode token after the projections: alpha / beta from the F32
+    # projection of rmsnorm(x) * gamma, the Q / K L2 norms, gates, recurrence
+    # and gated norm, against the float64 steps; three tokens in a row
+    # (the state carries over).
+    rng = np.random.default_rng(17)
+    ab_w = rng.normal(scale=0.05, size=(2 * Hv, H)).astype(np.float32)
+    xg = rng.normal(size=H).astype(np.float32)
+    dt = rng.normal(size=Hv).astype(np.float32)
+    a = -np.abs(rng.normal(size=Hv)).astype(np.float32)
+    gamma = rng.normal(size=d).astype(np.float32)
+    S0 = rng.normal(scale=0.1, size=(Hv, d, d)).astype(np.float32)
+    state = t32(S0, cuda)
+    S = S0.astype(np.float64)
+    f = lambda arr: arr.astype(np.float32).astype(np.float64)
+    for step in range(3):
+        qkv = rng.normal(size=(2 * G + Hv) * d).astype(np.float32)
+        x = rng.normal(size=H).astype(np.float32)
+        z = rng.normal(size=Hv * d).astype(np.float32)
+        y = torch.empty(Hv * d, device=cuda)
+        yq = torch.empty(Hv * d, device=cuda)
+        kernels.gdn_decode(t32(qkv, cuda), t32(x, cuda), t32(xg, cuda), t32(ab_w, cuda), H, t32(dt, cuda),
+                           t32(a, cuda), state, t32(z, cuda), t32(gamma, cuda), y, yq, Hv, G, d, 1e-6)
+        n = moe_ref.rmsnorm(x.astype(np.float64), xg, 1e-6)
+        ab = ab_w.astype(np.float64) @ n
+        decay = np.exp(moe_ref.softplus(ab[:Hv] + dt) * a)
+        beta = moe_ref.sigmoid(ab[Hv:])
+        qk = moe_ref.l2norm(qkv[:2 * G * d].astype(np.float64).reshape(2, G, d), 1e-6)
+        S, o = moe_ref.gdn_step(S, qk[0], qk[1], f(qkv[2 * G * d:]).reshape(Hv, d), decay, beta, G)
+        ref = moe_ref.rmsnorm(o, gamma, 1e-6) * moe_ref.silu(z.reshape(Hv, d))
+        got = y.cpu().numpy()
+        assert rel_err(got, ref.reshape(-1)) <= 1e-4, step
+        assert rel_err(state.cpu().numpy(), S) <= 1e-4, step
+        xgroup.check(yq, got)
+
+
+def test_gdn_decode_rejects_bad_shapes(cuda):
+    z = torch.zeros(8192, device=cuda)
+    args = lambda Hv, G, d, H: (z, z, z, z, H, z, z, z, z, z, z, None, Hv, G, d, 1e-6)
+    for bad in ((10, 4, 64, 512), (4, 4, 96, 512), (4, 4, 64, 0), (4, 4, 64, 4352)):
+        with pytest.raises(ValueError):
+            kernels.gdn_decode(*args(*bad))
+
+
 # ------------------------------------------------------------ attention pieces
 def test_split_qgate_norm_and_gate_mul(cuda):
     rng = np.random.default_rng(8)
