@@ -181,6 +181,20 @@ int hipllm_gemv_x16_routed(uint32_t type, const void* packed, const void* packed
                            size_t routes, const int32_t* ids, const float* logits, int32_t* ids_out,
                            float* weights_out, int waves, void* stream);
 
+/* One token's routed expert down projections, the shared expert's down
+ * projection and the MoE combine in one launch, all on x16 copies: route j
+ * (j < routes <= 8) multiplies expert ids[j]'s rows of the packed [experts *
+ * n, k_r] down block (Q4_K or Q6_K) by XGroup row j of xq (ldx values
+ * apart), the shared expert's packed [n, k_s] down matrix (Q4_K, Q6_K or
+ * Q8_0, k_s <= 2048) multiplies the FP32 row sx, and y = residual + (sum_j
+ * weights[j] down_j + sigmoid(sgate[0]) shared) (n % 16 == 0). Replaces the
+ * expert down GEMMs, shared-expert down GEVM and the weighted sum of
+ * encode_selected_moe (moe_llm.mm:2790-2843; metal_llm.metal:1424-1521). */
+int hipllm_gemv_x16_moe_down(uint32_t type_r, const void* down_packed, const int32_t* ids, size_t experts,
+                             const void* xq, size_t ldx, size_t k_r, uint32_t type_s, const void* shared_packed,
+                             const float* sx, size_t k_s, const float* weights, const float* sgate,
+                             const float* residual, float* y, size_t n, size_t routes, void* stream);
+
 /* hipllm_rmsnorm of the raw row x (gain gamma, k <= 8192, x and gamma
  * 16-byte aligned) followed by hipllm_gemv_prepped, in one launch: every
  * block normalises x into LDS (the same bits as hipllm_rmsnorm's XGroup

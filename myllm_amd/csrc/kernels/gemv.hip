@@ -1075,7 +1075,7 @@ int gemv_pick_shape(uint32_t type, uint32_t n, uint32_t units, int mode) {
 //   waves of a block split the units round-robin and are summed in wave
 //   order, the four lanes of a row by two xor shuffles: deterministic.
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-constexpr uint32_t kMfmaZeroBytes = 672;  // covers the A reads at offsets 0..655 (+16 bytes)
+constexpr uint32_t kMfmaZeroBytes = 784;  // covers the A reads at offsets 0..768 (+16 bytes; Q8_0's last MFMA)
 
 __device__ __forceinline__ i32x4 nibbles(const uint4& q, bool high) {
     i32x4 b;
@@ -1208,6 +1208,59 @@ struct X16<kQ6_K> {
             sum_m = fmaf(scale, se[i].x, sum_m);
         }
         return fmaf(d, fmaf(-32.0f, sum_m, sum_t), acc);
+    }
+};
+
+// Q8_0 (34-byte blocks of 32 values: f16 d, 32 int8 quants): a tile-unit
+// holds for MFMA i and lane l = 16 s + r the 16 quants of row r at values
+// [64 i + 16 s, +16) of the unit (block 2 i + (s >> 1), bytes 16 (s & 1)
+// on), 1 KiB per MFMA, then per row its eight d values ordered so that a
+// lane reads the four of its blocks 2 i + (s >> 1) as one 8-byte word. The
+// quants are the MFMA's B operand as they are (signed bytes); MFMA i's A
+// slices are groups 4 i .. 4 i + 3 of the unit, so each lane's result is one
+// group's three exact digit sums for its row, combined in FP32 (their
+// magnitude can exceed int32) and scaled by the group's e and the block's d.
+template <>
+struct X16<kQ8_0> {
+    static constexpr uint32_t kBlock = 272;  // 8 blocks of 34 bytes per row and unit
+    struct Unit {
+        uint4 q[4];  // MFMA i's quant slice
+        uint2 d;     // this lane's four block scales (f16), MFMA 0..3
+    };
+    __device__ static Unit load(const uint8_t* tu, uint32_t r, uint32_t s, uint32_t lane) {
+        Unit v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v.q[i] = ldw128_nt(tu + 1024 * i + 16 * lane);
+        v.d = *reinterpret_cast<const uint2*>(tu + 4096 + 16 * r + 8 * (s >> 1));
+        return v;
+    }
+    __device__ static uint32_t group_base(uint32_t s) { return 64 * s; }
+    static constexpr uint32_t group_step(int i) { return 256 * i; }
+    __device__ static float unit(const Unit& wu, const uint8_t* a_src, const uint8_t* se_src, uint32_t, uint32_t,
+                                 float acc) {
+        i32x4 a[4];
+        float2 se[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            a[i] = *reinterpret_cast<const i32x4*>(a_src + group_step(i));
+            se[i] = *reinterpret_cast<const float2*>(se_src + group_step(i));
+        }
+        const i32x4 zero = {0, 0, 0, 0};
+        const float dv[4] = {half_lo(wu.d.x), half_hi(wu.d.x), half_lo(wu.d.y), half_hi(wu.d.y)};
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            i32x4 b;
+            b.x = static_cast<int>(wu.q[i].x);
+            b.y = static_cast<int>(wu.q[i].y);
+            b.z = static_cast<int>(wu.q[i].z);
+            b.w = static_cast<int>(wu.q[i].w);
+            const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b, zero, 0, 0, 0);
+            const float t = fmaf(65536.0f, static_cast<float>(c.z),
+                                 fmaf(256.0f, static_cast<float>(c.y), static_cast<float>(c.x)));
+            sum = fmaf(t, se[i].y * dv[i], sum);
+        }
+        return acc + sum;
     }
 };
 
@@ -1564,6 +1617,25 @@ __global__ __launch_bounds__(256) void pack_x16_kernel(const uint8_t* __restrict
         }
         const uint32_t row = tile * 16 + r;
         if (row < n) v = ldw128(unit0 + static_cast<size_t>(row) * row_bytes + src);
+    } else if (QT == kQ8_0) {
+        if (j < 256) {
+            // MFMA i = j / 64, lane 16 s + r: block 2 i + (s >> 1), quant bytes 16 (s & 1) on.
+            const uint32_t i = j / 64, l = j % 64, r = l & 15, s = l >> 4;
+            const uint32_t row = tile * 16 + r;
+            const uint32_t src = 34 * (2 * i + (s >> 1)) + 2 + 16 * (s & 1);
+            if (row < n) v = ld128_a2(unit0 + static_cast<size_t>(row) * row_bytes + src);
+        } else {
+            // Row j - 256's d values, half 4 p + i = block 2 i + p.
+            const uint32_t row = tile * 16 + (j - 256);
+            uint32_t hv[8];
+#pragma unroll
+            for (uint32_t h = 0; h < 8; ++h) {
+                const uint32_t blk = 2 * (h & 3) + (h >> 2);
+                hv[h] = row < n ? *reinterpret_cast<const uint16_t*>(unit0 + static_cast<size_t>(row) * row_bytes + 34 * blk)
+                                : 0u;
+            }
+            v = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
+        }
     } else if (j < 192) {
         const uint32_t part = j / 64, l = j % 64, r = l & 15, s = l >> 4;
         const uint32_t src = part == 2 ? 128 + 32 * (s >> 1) + 16 * (s & 1) : 64 * (s >> 1) + 32 * part + 16 * (s & 1);
@@ -1641,8 +1713,8 @@ int launch_prep_x(const float* x, XGroup* xq, size_t k, hipStream_t stream) {
 }
 
 namespace {
-bool x16_type(uint32_t type) { return type == kQ4_K || type == kQ6_K; }
-uint32_t x16_block(uint32_t type) { return type == kQ4_K ? 144u : 210u; }
+bool x16_type(uint32_t type) { return type == kQ4_K || type == kQ6_K || type == kQ8_0; }
+uint32_t x16_block(uint32_t type) { return type == kQ4_K ? 144u : type == kQ6_K ? 210u : 272u; }
 }  // namespace
 
 size_t x16_bytes(uint32_t type, size_t n, size_t k) {
@@ -1655,7 +1727,7 @@ int launch_pack_x16(uint32_t type, const void* w, size_t row_bytes, size_t n, si
     if (!x16_type(type) || !w || !packed || n == 0 || k == 0 || k % 256 != 0) return kInvalidArgument;
     const uint32_t B = x16_block(type);
     if (row_bytes < k / 256 * B || reinterpret_cast<uintptr_t>(packed) % 16 != 0) return kInvalidArgument;
-    // Q4_K rows are read in 16-byte pieces, Q6_K rows in 16-bit pieces.
+    // Q4_K rows are read in 16-byte pieces, Q6_K and Q8_0 rows in 16-bit pieces.
     const size_t align = type == kQ4_K ? 16 : 2;
     if (row_bytes % align != 0 || reinterpret_cast<uintptr_t>(w) % align != 0) return kInvalidArgument;
     if (n > 0x7fffffffull || k > 0x7fffffffull) return kLengthError;
@@ -1667,6 +1739,9 @@ int launch_pack_x16(uint32_t type, const void* w, size_t row_bytes, size_t n, si
     auto* out = static_cast<uint8_t*>(packed);
     if (type == kQ4_K) {
         HIPLLM_LAUNCH(pack_x16_kernel<kQ4_K>, grid, dim3(256), 0, stream, wb, row_bytes, out, static_cast<uint32_t>(n),
+                      units, chunks);
+    } else if (type == kQ8_0) {
+        HIPLLM_LAUNCH(pack_x16_kernel<kQ8_0>, grid, dim3(256), 0, stream, wb, row_bytes, out, static_cast<uint32_t>(n),
                       units, chunks);
     } else {
         HIPLLM_LAUNCH(pack_x16_kernel<kQ6_K>, grid, dim3(256), 0, stream, wb, row_bytes, out, static_cast<uint32_t>(n),
@@ -1745,6 +1820,12 @@ int launch_gemv_x16(uint32_t type, const void* packed, const XGroup* xq, const f
     const uint32_t units = static_cast<uint32_t>(k / 256), nn = static_cast<uint32_t>(n);
     const int code = waves ? waves : x16_default_waves(nn, units, 0);
     const auto* wp = static_cast<const uint8_t*>(packed);
+    if (type == kQ8_0) {
+        // Q8_0 copies serve plain products (no norm data in or out).
+        if (kind != 0) return kInvalidArgument;
+        return launch_x16<kQ8_0, 0, 0>(code, wp, nullptr, xq, bias, residual, y, nullptr, nn, units, X16Norm{},
+                                       stream);
+    }
     return type == kQ4_K
                ? launch_x16_norm<kQ4_K, 0>(kind, code, wp, nullptr, xq, bias, residual, y, nullptr, nn, units, norm,
                                            stream)
@@ -1754,6 +1835,7 @@ int launch_gemv_x16(uint32_t type, const void* packed, const XGroup* xq, const f
 
 int launch_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, const XGroup* xq, float* y, XGroup* yq,
                            size_t n, size_t k, int waves, hipStream_t stream, const X16Norm* norm) {
+    if (type == kQ8_0) return kInvalidArgument;  // Q4_K / Q6_K pairs
     int rc = check_x16(type, gate, xq, y, n, k);
     if (rc == kOk) rc = check_x16(type, up, xq, y, n, k);
     if (rc != kOk) return rc;
@@ -1790,6 +1872,7 @@ int launch_x16_pair_types(int wpb, const X16Job& a, const X16Job& b, uint32_t bl
 int launch_gemv_x16_pair(uint32_t type_a, const void* packed_a, size_t n_a, float* y_a, uint32_t type_b,
                          const void* packed_b, size_t n_b, float* y_b, size_t k, const float* x, const float* gamma,
                          float eps, const float* conv_w, float* history, size_t ksize, hipStream_t stream) {
+    if (type_a == kQ8_0) return kInvalidArgument;  // job A: Q4_K or Q6_K
     int rc = check_x16(type_a, packed_a, reinterpret_cast<const XGroup*>(x), y_a, n_a, k);
     if (rc == kOk) rc = check_x16(type_b, packed_b, reinterpret_cast<const XGroup*>(x), y_b, n_b, k);
     if (rc != kOk) return rc;
@@ -1807,11 +1890,13 @@ int launch_gemv_x16_pair(uint32_t type_a, const void* packed_a, size_t n_a, floa
     const int wpb = units >= 8 ? 8 : 4;
     const uint32_t blocks = blocks_a + blocks_b;
     if (type_a == kQ4_K) {
-        return type_b == kQ4_K ? launch_x16_pair_types<kQ4_K, kQ4_K>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream)
-                               : launch_x16_pair_types<kQ4_K, kQ6_K>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream);
+        return type_b == kQ4_K   ? launch_x16_pair_types<kQ4_K, kQ4_K>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream)
+               : type_b == kQ6_K ? launch_x16_pair_types<kQ4_K, kQ6_K>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream)
+                                 : launch_x16_pair_types<kQ4_K, kQ8_0>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream);
     }
-    return type_b == kQ4_K ? launch_x16_pair_types<kQ6_K, kQ4_K>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream)
-                           : launch_x16_pair_types<kQ6_K, kQ6_K>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream);
+    return type_b == kQ4_K   ? launch_x16_pair_types<kQ6_K, kQ4_K>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream)
+           : type_b == kQ6_K ? launch_x16_pair_types<kQ6_K, kQ6_K>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream)
+                             : launch_x16_pair_types<kQ6_K, kQ8_0>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream);
 }
 
 namespace {
@@ -1856,6 +1941,7 @@ int launch_gemv_x16_routed(uint32_t type, const void* packed, const void* packed
                            int x_routed, float* y, XGroup* yq, size_t ldy, size_t n, size_t k, size_t experts,
                            size_t routes, const int32_t* ids, const float* logits, int32_t* ids_out,
                            float* weights_out, int waves, hipStream_t stream) {
+    if (type == kQ8_0) return kInvalidArgument;  // Q4_K / Q6_K expert blocks
     int rc = check_x16(type, packed, xq, y, n, k);
     if (rc == kOk && packed2) rc = check_x16(type, packed2, xq, y, n, k);
     if (rc != kOk) return rc;
@@ -1993,6 +2079,173 @@ int launch_gemv_moe_combine(uint32_t type, const void* w, size_t row_bytes, cons
     c.routes = static_cast<uint32_t>(routes);
     return launch_any_norm<2>(type, code, w, nullptr, row_bytes, x, nullptr, 0.0f, nullptr, residual, y, nullptr, nn,
                               units, static_cast<uint32_t>(k / 32), stream, c);
+}
+
+// One wave's products of a 16-row x16 tile (units tile-units from wt) with
+// an XGroup input row whose unit u is the 1 KiB at xg + 1024 u (global, or
+// LDS when x_lds): two units in flight, each unit's groups stored to the
+// wave's 1 KiB of LDS (global input) and read as the MFMA A slices; lanes r,
+// r + 16, r + 32, r + 48 then hold row r's four partial sums, returned
+// summed in lanes r < 16. lds: the wave's 2 KiB (input slot, zero region).
+// pro() runs once the first two units' loads are issued.
+template <uint32_t QT, typename Pro>
+__device__ __forceinline__ float x16_wave_tile(const uint8_t* __restrict__ wt, const uint8_t* xg, bool x_lds,
+                                               uint32_t units, uint8_t* lds, uint32_t lane, Pro pro) {
+    using F = X16<QT>;
+    constexpr uint32_t kTileUnit = 16 * F::kBlock;
+    const uint32_t r = lane & 15, s = lane >> 4;
+    if (lane < kMfmaZeroBytes / 16) *reinterpret_cast<uint4*>(lds + 1024 + 16 * lane) = make_uint4(0, 0, 0, 0);
+    const bool a_lane = (r >> 2) == s && (r & 3) < 3;
+    const uint32_t slot = F::group_base(s);
+    struct Slot {
+        uint4 x;
+        typename F::Unit w;
+    };
+    auto fill = [&](Slot& d, uint32_t u) {
+        if (!x_lds) d.x = reinterpret_cast<const uint4*>(xg + 1024 * u)[lane];
+        d.w = F::load(wt + static_cast<size_t>(u) * kTileUnit, r, s, lane);
+    };
+    auto consume = [&](const Slot& d, uint32_t u, float acc) {
+        const uint8_t* base = lds;
+        if (x_lds) {
+            base = xg + 1024 * u;
+        } else {
+            *reinterpret_cast<uint4*>(lds + 16 * lane) = d.x;
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        }
+        const uint8_t* a_src = a_lane ? base + slot + 16 * (r & 3) : lds + 1024;
+        acc = F::unit(d.w, a_src, base + slot + 48, r, s, acc);
+        if (!x_lds) {
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        }
+        return acc;
+    };
+    Slot s0, s1;
+    if (units > 0) fill(s0, 0);
+    if (units > 1) fill(s1, 1);
+    pro();
+    float acc = 0.0f;
+    for (uint32_t u = 0; u < units; u += 2) {
+        acc = consume(s0, u, acc);
+        if (u + 2 < units) fill(s0, u + 2);
+        if (u + 1 < units) {
+            acc = consume(s1, u + 1, acc);
+            if (u + 3 < units) fill(s1, u + 3);
+        }
+    }
+    acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 32);
+    return acc;
+}
+
+// The routed expert down projections of one token, the shared expert's down
+// projection and the MoE combine in one launch. Block = 16-row tile of the
+// output; wave j < routes multiplies the tile of expert ids[j] (clamped to
+// experts - 1) in the x16 copy of the whole down block by route j's SwiGLU
+// output (XGroup row j, ldx values apart), wave `routes` the shared expert's
+// tile by its SwiGLU output, which arrives as FP32 (sx, k_s values) and is
+// encoded into LDS by that wave. Epilogue (thread r < 16), the expression of
+// the vector combine: y = residual + (sum_j weights[j] down_j (route order)
+// + shared * sigmoid(sgate[0])).
+constexpr uint32_t kMoeDownMaxShared = 2048;  // shared-expert inner size held in LDS
+
+template <uint32_t QR, uint32_t QS>
+__global__ __launch_bounds__(64 * (kCombineRoutes + 1)) void x16_moe_down_kernel(
+    const uint8_t* __restrict__ down_x16, size_t expert_bytes, const int32_t* __restrict__ ids, uint32_t experts,
+    const XGroup* __restrict__ xq, uint32_t ldx, uint32_t units_r, const uint8_t* __restrict__ shared_x16,
+    const float* __restrict__ sx, uint32_t units_s, const float* __restrict__ weights,
+    const float* __restrict__ sgate, const float* __restrict__ residual, float* __restrict__ y, uint32_t n,
+    uint32_t routes) {
+    __shared__ __align__(16) uint8_t xs[kCombineRoutes + 1][2048];
+    __shared__ __align__(16) XGroup sxg[kMoeDownMaxShared / 16];
+    __shared__ float vals[kCombineRoutes + 1][16];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t tile = blockIdx.x, row = tile * 16 + threadIdx.x;
+    // Epilogue operands, loaded now.
+    float res = 0.0f, sg = 0.0f, wts[kCombineRoutes];
+    if (threadIdx.x < 16) {
+        if (row < n) res = residual[row];
+        sg = sgate[0];
+#pragma unroll
+        for (uint32_t q = 0; q < kCombineRoutes; ++q) wts[q] = q < routes ? weights[q] : 0.0f;
+    }
+    float v = 0.0f;
+    if (wave < routes) {
+        const uint32_t e = min(static_cast<uint32_t>(ids[wave]), experts - 1);
+        const uint8_t* wt = down_x16 + static_cast<size_t>(e) * expert_bytes +
+                            static_cast<size_t>(tile) * units_r * (16 * X16<QR>::kBlock);
+        v = x16_wave_tile<QR>(wt, reinterpret_cast<const uint8_t*>(xq + static_cast<size_t>(wave) * (ldx / 16)),
+                              false, units_r, xs[wave], lane, [] {});
+    } else if (wave == routes) {
+        const uint8_t* wt = shared_x16 + static_cast<size_t>(tile) * units_s * (16 * X16<QS>::kBlock);
+        // The input's XGroup form is made while the first weight loads fly.
+        v = x16_wave_tile<QS>(wt, reinterpret_cast<const uint8_t*>(sxg), true, units_s, xs[wave], lane, [&] {
+            for (uint32_t g = lane; g < 16 * units_s; g += 64) xgroup_encode_from(sx + 16 * g, sxg + g);
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        });
+    }
+    if (wave <= routes && lane < 16) vals[wave][lane] = v;
+    __syncthreads();
+    if (threadIdx.x < 16 && row < n) {
+        float acc = 0.0f;
+#pragma unroll
+        for (uint32_t q = 0; q < kCombineRoutes; ++q) {
+            if (q < routes) acc += wts[q] * vals[q][threadIdx.x];
+        }
+        float moe = acc;
+        moe += vals[routes][threadIdx.x] * sigmoid_ref(sg);
+        y[row] = res + moe;
+    }
+}
+
+int launch_x16_moe_down(uint32_t type_r, const void* down_x16, const int32_t* ids, size_t experts, const XGroup* xq,
+                        size_t ldx, size_t k_r, uint32_t type_s, const void* shared_x16, const float* sx, size_t k_s,
+                        const float* weights, const float* sgate, const float* residual, float* y, size_t n,
+                        size_t routes, hipStream_t stream) {
+    if (!down_x16 || !ids || !xq || !shared_x16 || !sx || !weights || !sgate || !residual || !y || experts == 0 ||
+        routes == 0 || routes > kCombineRoutes || n == 0 || n % 16 != 0) {
+        return kInvalidArgument;
+    }
+    if ((type_r != kQ4_K && type_r != kQ6_K) || !x16_type(type_s)) return kInvalidArgument;
+    if (k_r == 0 || k_r % 256 != 0 || k_s == 0 || k_s % 256 != 0 || k_s > kMoeDownMaxShared || ldx < k_r ||
+        ldx % 16 != 0) {
+        return kInvalidArgument;
+    }
+    for (const void* p : {static_cast<const void*>(down_x16), static_cast<const void*>(xq), shared_x16,
+                          static_cast<const void*>(sx)}) {
+        if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return kInvalidArgument;
+    }
+    if (n > 0x7fffffffull || experts > 0xffffffffull || ldx > 0xffffffffull) return kLengthError;
+    const size_t expert_bytes = x16_bytes(type_r, n, k_r);
+    const uint32_t ur = static_cast<uint32_t>(k_r / 256), us = static_cast<uint32_t>(k_s / 256);
+    const dim3 grid(static_cast<uint32_t>(n / 16)), block(static_cast<uint32_t>(64 * (routes + 1)));
+    const auto* dw = static_cast<const uint8_t*>(down_x16);
+    const auto* sw = static_cast<const uint8_t*>(shared_x16);
+    const uint32_t E = static_cast<uint32_t>(experts), nn = static_cast<uint32_t>(n), R = static_cast<uint32_t>(routes),
+                   lx = static_cast<uint32_t>(ldx);
+#define HIPLLM_MOE_DOWN(QR, QS)                                                                                         HIPLLM_LAUNCH((x16_moe_down_kernel<QR, QS>), grid, block, 0, stream, dw, expert_bytes, ids, E, xq, lx, ur, sw, sx,                   us, weights, sgate, residual, y, nn, R)
+    if (type_r == kQ4_K) {
+        if (type_s == kQ4_K) {
+            HIPLLM_MOE_DOWN(kQ4_K, kQ4_K);
+        } else if (type_s == kQ6_K) {
+            HIPLLM_MOE_DOWN(kQ4_K, kQ6_K);
+        } else {
+            HIPLLM_MOE_DOWN(kQ4_K, kQ8_0);
+        }
+    } else {
+        if (type_s == kQ4_K) {
+            HIPLLM_MOE_DOWN(kQ6_K, kQ4_K);
+        } else if (type_s == kQ6_K) {
+            HIPLLM_MOE_DOWN(kQ6_K, kQ6_K);
+        } else {
+            HIPLLM_MOE_DOWN(kQ6_K, kQ8_0);
+        }
+    }
+#undef HIPLLM_MOE_DOWN
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
 // Routed expert gate/up + SwiGLU with the routes chosen in every block's

@@ -127,6 +127,15 @@ int launch_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, cons
 int launch_gemv_x16_pair(uint32_t type_a, const void* packed_a, size_t n_a, float* y_a, uint32_t type_b,
                          const void* packed_b, size_t n_b, float* y_b, size_t k, const float* x, const float* gamma,
                          float eps, const float* conv_w, float* history, size_t ksize, hipStream_t stream);
+// One token's routed down projections (route j: expert ids[j]'s rows of the
+// x16 copy of the whole [experts * n, k_r] down block times XGroup row j of
+// xq), the shared expert's down projection (x16 copy, FP32 input sx of k_s
+// <= 2048 values) and the MoE combine in one launch: y = residual + (sum_j
+// weights[j] down_j + sigmoid(sgate[0]) shared); n % 16 == 0, routes <= 8.
+int launch_x16_moe_down(uint32_t type_r, const void* down_x16, const int32_t* ids, size_t experts, const XGroup* xq,
+                        size_t ldx, size_t k_r, uint32_t type_s, const void* shared_x16, const float* sx, size_t k_s,
+                        const float* weights, const float* sgate, const float* residual, float* y, size_t n,
+                        size_t routes, hipStream_t stream);
 // One token's routed expert vectors over the x16 copy of a whole expert block
 // ([experts * n, k], n rows per expert, n % 16 == 0): route j multiplies
 // expert ids[j] (or, with logits, the router's top-k picked in the kernel,

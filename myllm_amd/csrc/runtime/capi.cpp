@@ -246,6 +246,17 @@ int hipllm_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, cons
                   "launch failure");
 }
 
+int hipllm_gemv_x16_moe_down(uint32_t type_r, const void* down_packed, const int32_t* ids, size_t experts,
+                             const void* xq, size_t ldx, size_t k_r, uint32_t type_s, const void* shared_packed,
+                             const float* sx, size_t k_s, const float* weights, const float* sgate,
+                             const float* residual, float* y, size_t n, size_t routes, void* stream) {
+    return status(hipllm::launch_x16_moe_down(type_r, down_packed, ids, experts, xgc(xq), ldx, k_r, type_s,
+                                              shared_packed, sx, k_s, weights, sgate, residual, y, n, routes,
+                                              as_stream(stream)),
+                  "hipllm_gemv_x16_moe_down: invalid arguments (routed Q4_K / Q6_K, shared Q4_K / Q6_K / Q8_0, "
+                  "k % 256 == 0, k_s <= 2048, n % 16 == 0, 1..8 routes, 16-byte aligned buffers) or launch failure");
+}
+
 int hipllm_gemv_x16_pair(uint32_t type_a, const void* packed_a, size_t n_a, float* y_a, uint32_t type_b,
                          const void* packed_b, size_t n_b, float* y_b, size_t k, const float* x, const float* gamma,
                          float eps, const float* conv_w, float* history, size_t ksize, void* stream) {

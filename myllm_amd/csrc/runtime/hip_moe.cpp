@@ -309,6 +309,7 @@ void HipMoeLLM::Impl::pack_decode_weights() {
     struct Job {
         DevMatrix* m;
         std::size_t rows;  // rows packed: the matrix's, or every expert's
+        bool q8 = false;   // a Q8_0 copy (the shared down projection)
     };
     std::vector<Job> jobs = {{&output, output.rows}};
     auto expert_block = [&](DevMatrix& m) {
@@ -320,6 +321,11 @@ void HipMoeLLM::Impl::pack_decode_weights() {
             jobs.push_back({&L.qkv, L.qkv.rows});
             jobs.push_back({&L.z, L.z.rows});
         }
+        // The shared expert's down projection, for the launch that runs it
+        // with the routed down projections and the combine (Q8_0 too).
+        const DevMatrix& sd = L.sh_down;
+        const bool q8 = sd.type == hipllm::kQ8_0 && sd.cols % 256 == 0 && sd.row_bytes % 2 == 0;
+        if (sd.rows % 16 == 0 && sd.cols <= 2048 && (x16_packable(sd) || q8)) jobs.push_back({&L.sh_down, sd.rows, q8});
         if (expert_block(L.gate_exps) && expert_block(L.up_exps) && L.gate_exps.type == L.up_exps.type &&
             expert_block(L.down_exps)) {
             jobs.push_back({&L.gate_exps, E * L.gate_exps.rows});
@@ -331,7 +337,7 @@ void HipMoeLLM::Impl::pack_decode_weights() {
     std::size_t total = 0;
     for (const Job& j : jobs) {
         offs.push_back(total);
-        if (x16_packable(*j.m)) total = align_up(total + hipllm::x16_bytes(j.m->type, j.rows, j.m->cols), 256);
+        if (j.q8 || x16_packable(*j.m)) total = align_up(total + hipllm::x16_bytes(j.m->type, j.rows, j.m->cols), 256);
     }
     if (total == 0) return;
     hip_check(hipMalloc(&x16_arena, total), "hipMalloc(x16 decode weights)");
@@ -339,7 +345,7 @@ void HipMoeLLM::Impl::pack_decode_weights() {
     auto* base = static_cast<std::uint8_t*>(x16_arena);
     for (std::size_t i = 0; i < jobs.size(); ++i) {
         DevMatrix& m = *jobs[i].m;
-        if (!x16_packable(m)) continue;
+        if (!jobs[i].q8 && !x16_packable(m)) continue;
         launch_check(hipllm::launch_pack_x16(m.type, m.ptr, m.row_bytes, jobs[i].rows, m.cols, base + offs[i], stream),
                      "x16 packing");
         m.x16 = base + offs[i];
@@ -984,6 +990,17 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
                                                  act.act, act.actq, FF, H, rows * K, ids, E, K,
                                                  L.gate_exps.expert_stride, 0, H, FF, stream),
                      "expert gate/up");
+    }
+    // One token after the grouped launch: the routed and shared down
+    // projections and the combine as one launch on the x16 copies.
+    const bool x16_down = x16_experts && grp && !next_norm && L.sh_down.x16 && FF % 256 == 0 && FFs <= 2048 &&
+                          H % 16 == 0;
+    if (x16_down) {
+        launch_check(hipllm::launch_x16_moe_down(L.down_exps.type, L.down_exps.x16, ids, E, act.actq, FF, FF,
+                                                 L.sh_down.type, L.sh_down.x16, act.sh_act, FFs, act.rweight,
+                                                 act.rlog + E, hidden, next, H, K, stream),
+                     "expert down + shared down + MoE combine");
+        return;
     }
     if (x16_experts) {
         launch_check(hipllm::launch_gemv_x16_routed(L.down_exps.type, L.down_exps.x16, nullptr, act.actq, FF, 1,

@@ -31,7 +31,8 @@ pytestmark = pytest.mark.gpu
 
 SHAPES = [1104, 1108, 1116, 2104, 2108, 2116]
 TYPES = [synth.Q4_K, synth.Q6_K]
-BLOCK = {synth.Q4_K: 144, synth.Q6_K: 210}
+PLAIN_TYPES = TYPES + [synth.Q8_0]  # Q8_0 copies serve plain products only
+BLOCK = {synth.Q4_K: 144, synth.Q6_K: 210, synth.Q8_0: 272}
 
 
 def pack_ref(qtype: int, w: np.ndarray, n: int, k: int) -> np.ndarray:
@@ -50,7 +51,15 @@ def pack_ref(qtype: int, w: np.ndarray, n: int, k: int) -> np.ndarray:
             sl = np.stack([blk[:, :, offset_of_s(s): offset_of_s(s) + 16] for s in range(4)])  # [4, 16, units, 16]
             return sl.transpose(2, 0, 1, 3).reshape(units, 1024)
 
-        if qtype == synth.Q4_K:
+        if qtype == synth.Q8_0:
+            # MFMA i, lane 16 s + r: block 2 i + (s >> 1), quants 16 (s & 1) on; then
+            # per row its d values, half 4 p + i = block 2 i + p.
+            for i in range(4):
+                out[t, :, 1024 * i:1024 * (i + 1)] = lanes(lambda s, i=i: 34 * (2 * i + (s >> 1)) + 2 + 16 * (s & 1))
+            d = np.stack([blk[:, :, 34 * (2 * (h & 3) + (h >> 2)):34 * (2 * (h & 3) + (h >> 2)) + 2] for h in range(8)],
+                         axis=2)  # [16, units, 8, 2]
+            out[t, :, 4096:4352] = d.reshape(16, units, 16).transpose(1, 0, 2).reshape(units, 256)
+        elif qtype == synth.Q4_K:
             out[t, :, :256] = blk[:, :, :16].transpose(1, 0, 2).reshape(units, 256)
             out[t, :, 256:1280] = lanes(lambda s: 16 + 16 * s)
             out[t, :, 1280:2304] = lanes(lambda s: 80 + 16 * s)
@@ -88,7 +97,7 @@ def packed_case(cuda, qtype, n, k, seed, bias=False, residual=False, waves=0):
     return y.cpu().numpy(), yv.cpu().numpy(), ref, w, packed
 
 
-@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("qtype", PLAIN_TYPES)
 @pytest.mark.parametrize("n,k", [(1, 256), (16, 512), (37, 3584), (333, 2816), (1001, 1024)])
 def test_pack_layout(cuda, qtype, n, k):
     w = random_rows(qtype, n, k, n + k)
@@ -110,7 +119,7 @@ def test_pack_layout_q6k_odd_row_alignment(cuda):
     assert np.array_equal(packed.cpu().numpy(), pack_ref(synth.Q6_K, w, n, k))
 
 
-@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("qtype", PLAIN_TYPES)
 @pytest.mark.parametrize("n,k", [(1, 256), (16, 256), (37, 512), (333, 2816), (1001, 3584), (130, 18944)])
 def test_gemv_x16_matches_oracle_and_vector_path(cuda, qtype, n, k):
     y, yv, ref, _, _ = packed_case(cuda, qtype, n, k, seed=7 * n + k, bias=True, residual=True)
@@ -118,7 +127,7 @@ def test_gemv_x16_matches_oracle_and_vector_path(cuda, qtype, n, k):
     assert rel_err(y, yv) <= 1e-6
 
 
-@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("qtype", PLAIN_TYPES)
 @pytest.mark.parametrize("waves", SHAPES)
 def test_gemv_x16_launch_shapes(cuda, qtype, waves):
     # 7 units: fewer than some shapes' waves (idle waves), more than others'
@@ -129,7 +138,7 @@ def test_gemv_x16_launch_shapes(cuda, qtype, waves):
     assert rel_err(y, yv) <= 1e-6
 
 
-@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("qtype", PLAIN_TYPES)
 def test_gemv_x16_deterministic_and_long_rows(cuda, qtype):
     # 159 units (ten per wave at 16 waves per block): every shape reduces in a
     # fixed order, so repeated launches give the same bits.
@@ -140,7 +149,7 @@ def test_gemv_x16_deterministic_and_long_rows(cuda, qtype):
     assert np.array_equal(y.view(np.int32), y2.view(np.int32))
 
 
-@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("qtype", PLAIN_TYPES)
 def test_gemv_x16_nan_input_propagates(cuda, qtype):
     # A non-finite activation makes its XGroup's e NaN: the rows that read the
     # group are NaN, as FP32 arithmetic would make them.
@@ -163,11 +172,11 @@ def test_gemv_x16_rejects_bad_arguments(cuda):
     xq = xgroup.buffer(torch, k, cuda)
     y = torch.empty(n, dtype=torch.float32, device=cuda)
     assert kernels.x16_bytes(synth.Q4_K, n, 300) == 0
-    assert kernels.x16_bytes(synth.Q8_0, n, 256) == 0
+    assert kernels.x16_bytes(synth.Q5_0, n, 256) == 0
     with pytest.raises(ValueError):
         kernels.gemv_x16(synth.Q4_K, packed, xq, None, None, y, n, 300, 0)  # k % 256
     with pytest.raises(ValueError):
-        kernels.gemv_x16(synth.Q8_0, packed, xq, None, None, y, n, k, 0)  # not a packed type
+        kernels.gemv_x16(synth.Q5_0, packed, xq, None, None, y, n, k, 0)  # not a packed type
     with pytest.raises(ValueError):
         kernels.gemv_x16(synth.Q4_K, packed, xq, None, None, y, n, k, 1103)  # unknown launch shape
     with pytest.raises(ValueError):

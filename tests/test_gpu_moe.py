@@ -207,6 +207,67 @@ def test_gemv_x16_routed_matches_vector_routes(cuda, qtype, E, K, n, kdim, waves
     assert rel_err(d.cpu().numpy(), d_ref.cpu().numpy()) <= 1e-6
 
 
+@pytest.mark.parametrize("qr,qs,E,K,n,ff,ffs", [(synth.Q6_K, synth.Q8_0, 32, 8, 256, 512, 512),
+                                                 (synth.Q4_K, synth.Q6_K, 16, 3, 64, 256, 768),
+                                                 (synth.Q6_K, synth.Q4_K, 8, 1, 48, 1024, 256)])
+def test_gemv_x16_moe_down_matches_down_and_combine(cuda, qr, qs, E, K, n, ff, ffs):
+    """Routed down + shared down + combine in one launch against the routed
+    x16 down launch followed by the shared down with the combine in its
+    epilogue (vector GEMV on the GGUF rows), and against float64 over the
+    oracle's dequantization; repeated ids included."""
+    rng = np.random.default_rng(K + n)
+    wd = random_rows(qr, E * n, ff, 71)
+    ws = random_rows(qs, n, ffs, 72)
+
+    def pack(t, w, rows, cols):
+        p = torch.empty(kernels.x16_bytes(t, rows, cols), dtype=torch.uint8, device=cuda)
+        kernels.pack_x16(t, dev_bytes(w, cuda), w.shape[1], rows, cols, p)
+        return p
+
+    pd, ps = pack(qr, wd, E * n, ff), pack(qs, ws, n, ffs)
+    ids_np = rng.integers(0, E, size=K).astype(np.int32)
+    if K > 2:
+        ids_np[2] = ids_np[0]
+    ids = torch.from_numpy(ids_np).to(cuda)
+    act = rng.normal(size=(K, ff)).astype(np.float32)
+    actq = xgroup.buffer(torch, ff, cuda, K)
+    dact = t32(act, cuda)
+    for j in range(K):
+        kernels.prep_x(dact[j], actq[j * ff:(j + 1) * ff], ff)
+    sx = rng.normal(size=ffs).astype(np.float32)
+    wts = rng.random(K).astype(np.float32)
+    sg = np.array([0.7], dtype=np.float32)
+    res = rng.normal(size=n).astype(np.float32)
+    y = torch.empty(n, device=cuda)
+    kernels.gemv_x16_moe_down(qr, pd, ids, E, actq, ff, ff, qs, ps, t32(sx, cuda), ffs, t32(wts, cuda), t32(sg, cuda),
+                              t32(res, cuda), y, n, K)
+    down = torch.empty(K, n, device=cuda)
+    kernels.gemv_x16_routed(qr, pd, None, actq, ff, True, down, None, n, n, ff, E, K, ids=ids)
+    y_ref = torch.empty(n, device=cuda)
+    kernels.gemv_moe_combine(qs, dev_bytes(ws, cuda), ws.shape[1], t32(sx, cuda), t32(res, cuda), down,
+                             t32(wts, cuda), t32(sg, cuda), K, y_ref, n, ffs)
+    got = y.cpu().numpy()
+    assert rel_err(got, y_ref.cpu().numpy()) <= 1e-5
+    fd = oracle.dequant_rows(qr, wd, ff).astype(np.float64).reshape(E, n, ff)
+    fs = oracle.dequant_rows(qs, ws, ffs).astype(np.float64)
+    routed = sum(float(wts[j]) * (fd[ids_np[j]] @ act[j].astype(np.float64)) for j in range(K))
+    ref = res + routed + (fs @ sx.astype(np.float64)) / (1.0 + math.exp(-0.7))
+    assert rel_err(got, ref) <= 1e-4
+
+
+def test_gemv_x16_moe_down_rejects_bad_arguments(cuda):
+    z = torch.zeros(1 << 16, dtype=torch.uint8, device=cuda)
+    f = torch.zeros(4096, device=cuda)
+    ids = torch.zeros(8, dtype=torch.int32, device=cuda)
+    ok = [synth.Q6_K, z, ids, 4, f, 256, 256, synth.Q8_0, z, f, 256, f, f, f, f, 32, 2]
+    kernels.gemv_x16_moe_down(*ok)
+    for i, bad in ((0, synth.Q8_0), (7, synth.Q5_0), (6, 320), (10, 2304), (15, 40), (16, 9), (16, 0)):
+        args = list(ok)
+        args[i] = bad
+        with pytest.raises((ValueError, OverflowError)):
+            kernels.gemv_x16_moe_down(*args)
+
+
 def test_gemv_routed_swiglu_rejects_bad_arguments(cuda):
     w = torch.zeros(272 * 64, dtype=torch.uint8, device=cuda)
     x = torch.zeros(256, device=cuda)
