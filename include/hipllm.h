@@ -147,12 +147,16 @@ int hipllm_gemv_x16(uint32_t type, const void* packed, const void* xq, const flo
  * gamma (double sum of squares, every block normalising x itself; k <= 8192).
  * With conv_w, y_a is the input of a causal conv over its channels: y_a[c] =
  * silu(sum_j history[j][c] w[c][j] + (W_a n)[c] w[c][ksize - 1]) and the
- * (ksize - 1) x n_a history shifts by one row (ksize 2..4). Replaces the
+ * (ksize - 1) x n_a history shifts by one row (ksize 2..4). With xq and
+ * sumsq (both or neither) the norm comes from a producer's output norm data
+ * instead (the XGroup form of x * gamma and its per-16-value double sums of
+ * squares, as hipllm_gemv_x16 writes them); x and gamma are then unused. Replaces the
  * decode-step QKV / z GEVMs and the conv of encode_linear_attention
  * (moe_llm.mm:2436-2520; metal_llm.metal:708-781, 1320-1365). */
 int hipllm_gemv_x16_pair(uint32_t type_a, const void* packed_a, size_t n_a, float* y_a, uint32_t type_b,
                          const void* packed_b, size_t n_b, float* y_b, size_t k, const float* x, const float* gamma,
-                         float eps, const float* conv_w, float* history, size_t ksize, void* stream);
+                         float eps, const float* conv_w, float* history, size_t ksize, const void* xq,
+                         const double* sumsq, void* stream);
 
 /* The FFN gate/up pair over x16-packed weights of one type in one launch:
  * y = silu(Wg x) * (Wu x) (the sign-branched SiLU of cpu_llm.cpp:188-202),
@@ -187,13 +191,16 @@ int hipllm_gemv_x16_routed(uint32_t type, const void* packed, const void* packed
  * n, k_r] down block (Q4_K or Q6_K) by XGroup row j of xq (ldx values
  * apart), the shared expert's packed [n, k_s] down matrix (Q4_K, Q6_K or
  * Q8_0, k_s <= 2048) multiplies the FP32 row sx, and y = residual + (sum_j
- * weights[j] down_j + sigmoid(sgate[0]) shared) (n % 16 == 0). Replaces the
+ * weights[j] down_j + sigmoid(sgate[0]) shared) (n % 16 == 0). norm_out
+ * (nullable; gamma_out, yq_out and sumsq_out used) also writes the next
+ * RMSNorm's data as hipllm_gemv_x16 with an output norm does. Replaces the
  * expert down GEMMs, shared-expert down GEVM and the weighted sum of
  * encode_selected_moe (moe_llm.mm:2790-2843; metal_llm.metal:1424-1521). */
 int hipllm_gemv_x16_moe_down(uint32_t type_r, const void* down_packed, const int32_t* ids, size_t experts,
                              const void* xq, size_t ldx, size_t k_r, uint32_t type_s, const void* shared_packed,
                              const float* sx, size_t k_s, const float* weights, const float* sgate,
-                             const float* residual, float* y, size_t n, size_t routes, void* stream);
+                             const float* residual, float* y, size_t n, size_t routes,
+                             const HipllmX16Norm* norm_out, void* stream);
 
 /* hipllm_rmsnorm of the raw row x (gain gamma, k <= 8192, x and gamma
  * 16-byte aligned) followed by hipllm_gemv_prepped, in one launch: every
@@ -330,6 +337,19 @@ int hipllm_attn_decode_rope(const float* qkv, const float* cos_sin, size_t rot, 
 int hipllm_attn_decode_rope_gated(const float* qkv, const float* cos_sin, size_t rot, float* kcache, float* vcache,
                                   const float* gate, float* out, void* outq, float* scratch, size_t hq, size_t hkv,
                                   size_t d, size_t pos, float scale, void* stream);
+
+/* hipllm_split_qgate_norm and hipllm_attn_decode_rope_gated in one launch
+ * (the same operations; caches bit for bit, outputs to within a few ulps of
+ * the two launches'): mixed is the token's interleaved [Q_h | gate_h] row
+ * (2 d per head), kv its [K | V] row; the Q and K heads are RMS-normalised
+ * with q_gamma / k_gamma (eps), rotated, K / V written to the caches at pos,
+ * and out = attention * sigmoid(gate_h), outq its XGroup form. Offered for
+ * pos + 1 keys in 2 to 4 chunks of 64 (d 64 or 128; d 256 also) as one
+ * block per head. Replaces the decode step of encode_full_attention
+ * (moe_llm.mm:2238-2434; metal_llm.metal:1167-1197). */
+int hipllm_attn_decode_qgate(const float* mixed, const float* kv, const float* q_gamma, const float* k_gamma,
+                             float eps, const float* cos_sin, size_t rot, float* kcache, float* vcache, float* out,
+                             void* outq, size_t hq, size_t hkv, size_t d, size_t pos, float scale, void* stream);
 
 /* Scratch floats hipllm_attn_decode needs for up to max_len positions. */
 size_t hipllm_attn_decode_scratch_floats(size_t hq, size_t d, size_t max_len);

@@ -1333,7 +1333,7 @@ __device__ __forceinline__ void x16_body(const uint8_t* __restrict__ w, const ui
     static_assert(NORM != 2 || MODE == 0, "the output norm data comes from plain GEMVs");
     static_assert(RTE == 0 || NORM == 0, "routed vectors take no norm");
     static_assert(NORM != 3 || (MODE == 0 && RT == 1), "the in-block norm serves plain one-tile GEMVs");
-    static_assert(!CONV || NORM == 3, "the conv epilogue comes with the in-block norm");
+    static_assert(!CONV || NORM == 1 || NORM == 3, "the conv epilogue serves the paired launch");
     if constexpr (RTE != 0) {
         const uint32_t j = by;
         uint32_t e;
@@ -1570,15 +1570,19 @@ struct X16Job {
     uint32_t n;
 };
 
-template <uint32_t QA, uint32_t QB, int WPB>
+// NORM 3: each block normalises the raw row (nrm.x_in, nrm.gamma_in); NORM 1:
+// the producer left the XGroup form of x * gamma in xq and the per-16 sums
+// of squares in nrm.sumsq_in.
+template <uint32_t QA, uint32_t QB, int WPB, int NORM>
 __global__ __launch_bounds__(64 * WPB) void gemv_x16_pair_kernel(const X16Job a, const X16Job b, uint32_t blocks_a,
-                                                                 uint32_t units, X16Norm nrm, X16Conv cv) {
+                                                                 uint32_t units, const XGroup* __restrict__ xq,
+                                                                 X16Norm nrm, X16Conv cv) {
     if (blockIdx.x < blocks_a) {
-        x16_body<QA, WPB, 1, 0, 3, 0, true>(a.w, nullptr, nullptr, nullptr, nullptr, a.y, nullptr, a.n, units, nrm,
-                                            X16Route{}, cv, blockIdx.x, 0);
+        x16_body<QA, WPB, 1, 0, NORM, 0, true>(a.w, nullptr, xq, nullptr, nullptr, a.y, nullptr, a.n, units, nrm,
+                                               X16Route{}, cv, blockIdx.x, 0);
     } else {
-        x16_body<QB, WPB, 1, 0, 3, 0, false>(b.w, nullptr, nullptr, nullptr, nullptr, b.y, nullptr, b.n, units, nrm,
-                                             X16Route{}, X16Conv{}, blockIdx.x - blocks_a, 0);
+        x16_body<QB, WPB, 1, 0, NORM, 0, false>(b.w, nullptr, xq, nullptr, nullptr, b.y, nullptr, b.n, units, nrm,
+                                                X16Route{}, X16Conv{}, blockIdx.x - blocks_a, 0);
     }
 }
 
@@ -1854,14 +1858,25 @@ int launch_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, cons
 namespace {
 template <uint32_t QA, uint32_t QB>
 int launch_x16_pair_types(int wpb, const X16Job& a, const X16Job& b, uint32_t blocks, uint32_t blocks_a,
-                          uint32_t units, const X16Norm& nrm, const X16Conv& cv, hipStream_t stream) {
+                          uint32_t units, const XGroup* xq, const X16Norm& nrm, const X16Conv& cv,
+                          hipStream_t stream) {
+    if (xq) {
+        if (wpb == 4) {
+            HIPLLM_LAUNCH((gemv_x16_pair_kernel<QA, QB, 4, 1>), dim3(blocks), dim3(256), 0, stream, a, b, blocks_a,
+                          units, xq, nrm, cv);
+        } else {
+            HIPLLM_LAUNCH((gemv_x16_pair_kernel<QA, QB, 8, 1>), dim3(blocks), dim3(512), 0, stream, a, b, blocks_a,
+                          units, xq, nrm, cv);
+        }
+        return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+    }
     const size_t lds = static_cast<size_t>(units) * 1024;
     if (wpb == 4) {
-        HIPLLM_LAUNCH((gemv_x16_pair_kernel<QA, QB, 4>), dim3(blocks), dim3(256), lds, stream, a, b, blocks_a, units,
-                      nrm, cv);
+        HIPLLM_LAUNCH((gemv_x16_pair_kernel<QA, QB, 4, 3>), dim3(blocks), dim3(256), lds, stream, a, b, blocks_a, units,
+                      xq, nrm, cv);
     } else {
-        HIPLLM_LAUNCH((gemv_x16_pair_kernel<QA, QB, 8>), dim3(blocks), dim3(512), lds, stream, a, b, blocks_a, units,
-                      nrm, cv);
+        HIPLLM_LAUNCH((gemv_x16_pair_kernel<QA, QB, 8, 3>), dim3(blocks), dim3(512), lds, stream, a, b, blocks_a, units,
+                      xq, nrm, cv);
     }
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
@@ -1871,12 +1886,16 @@ int launch_x16_pair_types(int wpb, const X16Job& a, const X16Job& b, uint32_t bl
 // units per wave), 4 below.
 int launch_gemv_x16_pair(uint32_t type_a, const void* packed_a, size_t n_a, float* y_a, uint32_t type_b,
                          const void* packed_b, size_t n_b, float* y_b, size_t k, const float* x, const float* gamma,
-                         float eps, const float* conv_w, float* history, size_t ksize, hipStream_t stream) {
+                         float eps, const float* conv_w, float* history, size_t ksize, hipStream_t stream,
+                         const XGroup* xq, const double* sumsq) {
     if (type_a == kQ8_0) return kInvalidArgument;  // job A: Q4_K or Q6_K
-    int rc = check_x16(type_a, packed_a, reinterpret_cast<const XGroup*>(x), y_a, n_a, k);
-    if (rc == kOk) rc = check_x16(type_b, packed_b, reinterpret_cast<const XGroup*>(x), y_b, n_b, k);
+    if ((xq == nullptr) != (sumsq == nullptr)) return kInvalidArgument;
+    const XGroup* in = xq ? xq : reinterpret_cast<const XGroup*>(x);  // the input the shared checks see
+    int rc = check_x16(type_a, packed_a, in, y_a, n_a, k);
+    if (rc == kOk) rc = check_x16(type_b, packed_b, in, y_b, n_b, k);
     if (rc != kOk) return rc;
-    if (!gamma || reinterpret_cast<uintptr_t>(gamma) % 16 != 0 || !(eps > 0.0f) || k > 8192) return kInvalidArgument;
+    if (!xq && (!gamma || reinterpret_cast<uintptr_t>(gamma) % 16 != 0)) return kInvalidArgument;
+    if (!(eps > 0.0f) || k > 8192) return kInvalidArgument;
     if (conv_w && (!history || ksize < 2 || ksize > kX16ConvMax)) return kInvalidArgument;
     const uint32_t units = static_cast<uint32_t>(k / 256);
     const uint32_t blocks_a = static_cast<uint32_t>((n_a + 15) / 16), blocks_b = static_cast<uint32_t>((n_b + 15) / 16);
@@ -1886,17 +1905,18 @@ int launch_gemv_x16_pair(uint32_t type_a, const void* packed_a, size_t n_a, floa
     nrm.eps = eps;
     nrm.x_in = x;
     nrm.gamma_in = gamma;
+    nrm.sumsq_in = sumsq;
     const X16Conv cv{conv_w, history, static_cast<uint32_t>(n_a), static_cast<uint32_t>(ksize)};
     const int wpb = units >= 8 ? 8 : 4;
     const uint32_t blocks = blocks_a + blocks_b;
     if (type_a == kQ4_K) {
-        return type_b == kQ4_K   ? launch_x16_pair_types<kQ4_K, kQ4_K>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream)
-               : type_b == kQ6_K ? launch_x16_pair_types<kQ4_K, kQ6_K>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream)
-                                 : launch_x16_pair_types<kQ4_K, kQ8_0>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream);
+        return type_b == kQ4_K   ? launch_x16_pair_types<kQ4_K, kQ4_K>(wpb, a, b, blocks, blocks_a, units, xq, nrm, cv, stream)
+               : type_b == kQ6_K ? launch_x16_pair_types<kQ4_K, kQ6_K>(wpb, a, b, blocks, blocks_a, units, xq, nrm, cv, stream)
+                                 : launch_x16_pair_types<kQ4_K, kQ8_0>(wpb, a, b, blocks, blocks_a, units, xq, nrm, cv, stream);
     }
-    return type_b == kQ4_K   ? launch_x16_pair_types<kQ6_K, kQ4_K>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream)
-           : type_b == kQ6_K ? launch_x16_pair_types<kQ6_K, kQ6_K>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream)
-                             : launch_x16_pair_types<kQ6_K, kQ8_0>(wpb, a, b, blocks, blocks_a, units, nrm, cv, stream);
+    return type_b == kQ4_K   ? launch_x16_pair_types<kQ6_K, kQ4_K>(wpb, a, b, blocks, blocks_a, units, xq, nrm, cv, stream)
+           : type_b == kQ6_K ? launch_x16_pair_types<kQ6_K, kQ6_K>(wpb, a, b, blocks, blocks_a, units, xq, nrm, cv, stream)
+                             : launch_x16_pair_types<kQ6_K, kQ8_0>(wpb, a, b, blocks, blocks_a, units, xq, nrm, cv, stream);
 }
 
 namespace {
@@ -2151,22 +2171,27 @@ __device__ __forceinline__ float x16_wave_tile(const uint8_t* __restrict__ wt, c
 // + shared * sigmoid(sgate[0])).
 constexpr uint32_t kMoeDownMaxShared = 2048;  // shared-expert inner size held in LDS
 
+// nrm.gamma_out (nullable): each tile also writes the next RMSNorm's data as
+// an x16 NORM 2 launch does (the XGroup form of y * gamma_out into
+// nrm.yq_out, the double sum of squares of its 16 values in row order into
+// nrm.sumsq_out).
 template <uint32_t QR, uint32_t QS>
 __global__ __launch_bounds__(64 * (kCombineRoutes + 1)) void x16_moe_down_kernel(
     const uint8_t* __restrict__ down_x16, size_t expert_bytes, const int32_t* __restrict__ ids, uint32_t experts,
     const XGroup* __restrict__ xq, uint32_t ldx, uint32_t units_r, const uint8_t* __restrict__ shared_x16,
     const float* __restrict__ sx, uint32_t units_s, const float* __restrict__ weights,
     const float* __restrict__ sgate, const float* __restrict__ residual, float* __restrict__ y, uint32_t n,
-    uint32_t routes) {
+    uint32_t routes, const X16Norm nrm) {
     __shared__ __align__(16) uint8_t xs[kCombineRoutes + 1][2048];
     __shared__ __align__(16) XGroup sxg[kMoeDownMaxShared / 16];
     __shared__ float vals[kCombineRoutes + 1][16];
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const uint32_t tile = blockIdx.x, row = tile * 16 + threadIdx.x;
     // Epilogue operands, loaded now.
-    float res = 0.0f, sg = 0.0f, wts[kCombineRoutes];
+    float res = 0.0f, sg = 0.0f, gam = 0.0f, wts[kCombineRoutes];
     if (threadIdx.x < 16) {
         if (row < n) res = residual[row];
+        if (nrm.gamma_out && row < n) gam = nrm.gamma_out[row];
         sg = sgate[0];
 #pragma unroll
         for (uint32_t q = 0; q < kCombineRoutes; ++q) wts[q] = q < routes ? weights[q] : 0.0f;
@@ -2197,14 +2222,30 @@ __global__ __launch_bounds__(64 * (kCombineRoutes + 1)) void x16_moe_down_kernel
         }
         float moe = acc;
         moe += vals[routes][threadIdx.x] * sigmoid_ref(sg);
-        y[row] = res + moe;
+        const float out = res + moe;
+        y[row] = out;
+        vals[0][threadIdx.x] = out * gam;  // each thread rewrites its own slots after reading them
+        vals[1][threadIdx.x] = out;
+    }
+    if (nrm.gamma_out) {
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            xgroup_encode_from(vals[0], nrm.yq_out + tile);
+            double ss = 0.0;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const double t = vals[1][i];
+                ss += t * t;
+            }
+            nrm.sumsq_out[tile] = ss;
+        }
     }
 }
 
 int launch_x16_moe_down(uint32_t type_r, const void* down_x16, const int32_t* ids, size_t experts, const XGroup* xq,
                         size_t ldx, size_t k_r, uint32_t type_s, const void* shared_x16, const float* sx, size_t k_s,
                         const float* weights, const float* sgate, const float* residual, float* y, size_t n,
-                        size_t routes, hipStream_t stream) {
+                        size_t routes, hipStream_t stream, const X16Norm* norm_out) {
     if (!down_x16 || !ids || !xq || !shared_x16 || !sx || !weights || !sgate || !residual || !y || experts == 0 ||
         routes == 0 || routes > kCombineRoutes || n == 0 || n % 16 != 0) {
         return kInvalidArgument;
@@ -2218,6 +2259,15 @@ int launch_x16_moe_down(uint32_t type_r, const void* down_x16, const int32_t* id
                           static_cast<const void*>(sx)}) {
         if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return kInvalidArgument;
     }
+    X16Norm nrm{};
+    if (norm_out && norm_out->gamma_out) {
+        if (!norm_out->yq_out || !norm_out->sumsq_out || reinterpret_cast<uintptr_t>(norm_out->yq_out) % 16 != 0) {
+            return kInvalidArgument;
+        }
+        nrm.gamma_out = norm_out->gamma_out;
+        nrm.yq_out = norm_out->yq_out;
+        nrm.sumsq_out = norm_out->sumsq_out;
+    }
     if (n > 0x7fffffffull || experts > 0xffffffffull || ldx > 0xffffffffull) return kLengthError;
     const size_t expert_bytes = x16_bytes(type_r, n, k_r);
     const uint32_t ur = static_cast<uint32_t>(k_r / 256), us = static_cast<uint32_t>(k_s / 256);
@@ -2226,7 +2276,9 @@ int launch_x16_moe_down(uint32_t type_r, const void* down_x16, const int32_t* id
     const auto* sw = static_cast<const uint8_t*>(shared_x16);
     const uint32_t E = static_cast<uint32_t>(experts), nn = static_cast<uint32_t>(n), R = static_cast<uint32_t>(routes),
                    lx = static_cast<uint32_t>(ldx);
-#define HIPLLM_MOE_DOWN(QR, QS)                                                                                         HIPLLM_LAUNCH((x16_moe_down_kernel<QR, QS>), grid, block, 0, stream, dw, expert_bytes, ids, E, xq, lx, ur, sw, sx,                   us, weights, sgate, residual, y, nn, R)
+#define HIPLLM_MOE_DOWN(QR, QS)                                                                                    \
+    HIPLLM_LAUNCH((x16_moe_down_kernel<QR, QS>), grid, block, 0, stream, dw, expert_bytes, ids, E, xq, lx, ur, sw, sx, \
+                  us, weights, sgate, residual, y, nn, R, nrm)
     if (type_r == kQ4_K) {
         if (type_s == kQ4_K) {
             HIPLLM_MOE_DOWN(kQ4_K, kQ4_K);

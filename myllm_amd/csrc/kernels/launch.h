@@ -123,19 +123,24 @@ int launch_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, cons
 // y_a = conv(W_a rmsnorm(x) * gamma) (conv + SiLU over history when conv_w
 // is set, channel = row) and y_b = W_b rmsnorm(x) * gamma in one launch, each
 // block normalising the raw row x itself (k <= 8192, x and gamma 16-byte
-// aligned, ksize <= 4).
+// aligned, ksize <= 4); or, with xq and sumsq (the producer's NORM 2 data:
+// the XGroup form of x * gamma, per-16 sums of squares), from those (x and
+// gamma unused).
 int launch_gemv_x16_pair(uint32_t type_a, const void* packed_a, size_t n_a, float* y_a, uint32_t type_b,
                          const void* packed_b, size_t n_b, float* y_b, size_t k, const float* x, const float* gamma,
-                         float eps, const float* conv_w, float* history, size_t ksize, hipStream_t stream);
+                         float eps, const float* conv_w, float* history, size_t ksize, hipStream_t stream,
+                         const XGroup* xq = nullptr, const double* sumsq = nullptr);
 // One token's routed down projections (route j: expert ids[j]'s rows of the
 // x16 copy of the whole [experts * n, k_r] down block times XGroup row j of
 // xq), the shared expert's down projection (x16 copy, FP32 input sx of k_s
 // <= 2048 values) and the MoE combine in one launch: y = residual + (sum_j
 // weights[j] down_j + sigmoid(sgate[0]) shared); n % 16 == 0, routes <= 8.
+// norm_out (nullable; gamma_out, yq_out, sumsq_out used): also the next
+// RMSNorm's data, as a NORM 2 x16 launch writes it.
 int launch_x16_moe_down(uint32_t type_r, const void* down_x16, const int32_t* ids, size_t experts, const XGroup* xq,
                         size_t ldx, size_t k_r, uint32_t type_s, const void* shared_x16, const float* sx, size_t k_s,
                         const float* weights, const float* sgate, const float* residual, float* y, size_t n,
-                        size_t routes, hipStream_t stream);
+                        size_t routes, hipStream_t stream, const X16Norm* norm_out = nullptr);
 // One token's routed expert vectors over the x16 copy of a whole expert block
 // ([experts * n, k], n rows per expert, n % 16 == 0): route j multiplies
 // expert ids[j] (or, with logits, the router's top-k picked in the kernel,
@@ -186,6 +191,16 @@ int launch_attn_decode_rope(const float* qkv, const float* cos_sin, size_t rot, 
                             float* out, XGroup* outq, float* scratch, size_t hq, size_t hkv, size_t d, size_t pos,
                             float scale, hipStream_t stream, const uint32_t* dpos = nullptr, size_t capacity = 0,
                             const float* gate = nullptr);
+// Gated attention decode with its head norms in one launch (capacities of 2
+// to 4 chunks, d 64 / 128 / 256; attn_decode_qgate_fits): mixed is the
+// token's interleaved [Q_h | gate_h] row and kv its [K | V] row; Q and K
+// heads are RMS-normalised with q_gamma / k_gamma (launch_split_qgate_norm's
+// arithmetic) before the RoPE, then launch_attn_decode_rope with the gate.
+bool attn_decode_qgate_fits(size_t max_len, size_t d);
+int launch_attn_decode_qgate(const float* mixed, const float* kv, const float* q_gamma, const float* k_gamma,
+                             float eps, const float* cos_sin, size_t rot, float* kcache, float* vcache, float* out,
+                             XGroup* outq, size_t hq, size_t hkv, size_t d, size_t pos, float scale,
+                             hipStream_t stream, const uint32_t* dpos = nullptr, size_t capacity = 0);
 size_t argmax_scratch_bytes(size_t n);
 int launch_argmax(const float* x, size_t n, uint32_t* out, void* scratch, hipStream_t stream);
 int launch_swiglu(const float* g, const float* u, float* y, XGroup* yq, size_t n, hipStream_t stream);

@@ -360,14 +360,27 @@ __global__ __launch_bounds__(256) void attn_decode_partial(const float* __restri
 // taken from the block's own rotated values instead.
 // Same operations in the same order as the two launches: the output bits
 // are equal.
-template <uint32_t NG, uint32_t D>
+// QG (gated attention with head norms, rope set): q is the interleaved
+// [Q_h | gate_h] row (2 D per head) and qg.kv the [K | V] row; wave 0
+// RMS-normalises Q_h with qg.q_gamma and wave 1 K_g with qg.k_gamma into LDS
+// (split_qgate_norm_kernel's sums and products) before the RoPE, and the
+// output gate is gate_h.
+struct AttnQGate {
+    const float* kv;
+    const float* q_gamma;
+    const float* k_gamma;
+    float eps;
+};
+
+template <uint32_t NG, uint32_t D, bool QG = false>
 __global__ __launch_bounds__(256 * NG) void attn_decode_head(const float* __restrict__ q, float* __restrict__ kcache,
                                                              float* __restrict__ vcache, uint32_t hq, uint32_t hkv,
                                                              uint32_t len_arg, const uint32_t* __restrict__ dpos,
                                                              float scale, const float2* __restrict__ rope,
                                                              uint32_t half_rot, float* __restrict__ fout,
                                                              XGroup* __restrict__ foutq,
-                                                             const float* __restrict__ gate) {
+                                                             const float* __restrict__ gate,
+                                                             const AttnQGate qg = AttnQGate{}) {
     constexpr uint32_t D4 = D / 4;
     constexpr uint32_t PARTS = 256 / D4;           // p.V key subsets
     constexpr uint32_t KR = D4 / 4;                // float4 of a key per scoring lane
@@ -413,17 +426,35 @@ __global__ __launch_bounds__(256 * NG) void attn_decode_head(const float* __rest
             if (jj < cnt && t0 + jj != newrow) vr[r] = vrow[static_cast<size_t>(jj) * (kvd / 4)];
         }
     }
+    const float* qrow = q + h * D;
+    if constexpr (QG) qrow = q + static_cast<size_t>(h) * 2 * D;
+    const float* grow = QG ? qrow + D : (gate ? gate + h * D : nullptr);
+    __shared__ float qgn[QG ? 2 : 1][QG ? D : 1];
+    if constexpr (QG) {
+        if (tid < 128) {
+            const uint32_t wv = tid >> 6;
+            const float* src = wv == 0 ? qrow : qg.kv + g * D;
+            const float* gam = wv == 0 ? qg.q_gamma : qg.k_gamma;
+            float ss = 0.0f;
+            for (uint32_t i = lane; i < D; i += 64) ss += src[i] * src[i];
+            ss = wave_sum(ss);
+            const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + qg.eps);
+            for (uint32_t i = lane; i < D; i += 64) qgn[wv][i] = src[i] * inv * gam[i];
+        }
+        __syncthreads();
+    }
     if (rope) {
         const float2* tab = rope + static_cast<size_t>(len - 1) * half_rot;
-        const float* kn = q + hq * D + g * D;
-        const float* vn = kn + kvd;
+        const float* kn = QG ? qgn[QG ? 1 : 0] : q + hq * D + g * D;
+        const float* vn = QG ? qg.kv + kvd + g * D : kn + kvd;
+        const float* qn = QG ? qgn[0] : qrow;
         float* kc = kcache + static_cast<size_t>(len - 1) * kvd + g * D;
         float* vc = vcache + static_cast<size_t>(len - 1) * kvd + g * D;
         float* qs = reinterpret_cast<float*>(qs4);
         float* ks = reinterpret_cast<float*>(kn4);
         float* vs = reinterpret_cast<float*>(vn4);
         for (uint32_t i = tid; i < D; i += blockDim.x) {
-            qs[i] = rope_elem(q + h * D, tab, half_rot, i);
+            qs[i] = rope_elem(qn, tab, half_rot, i);
             const float kv = rope_elem(kn, tab, half_rot, i);
             ks[i] = kv;
             vs[i] = vn[i];
@@ -520,7 +551,7 @@ __global__ __launch_bounds__(256 * NG) void attn_decode_head(const float* __rest
             }
         }
         float v = a * (1.0f / L);
-        if (gate) v = v * sigmoid_ref(gate[h * D + tid]);
+        if (grow) v = v * sigmoid_ref(grow[tid]);
         fout[h * D + tid] = v;
         vals[tid] = v;
     }
@@ -900,6 +931,41 @@ int launch_attn_decode_rope(const float* qkv, const float* cos_sin, size_t rot, 
         HIPLLM_LAUNCH(attn_decode_merge, dim3(static_cast<uint32_t>(hq)), dim3(256), 0, stream, scratch, out,
                            outq, static_cast<uint32_t>(d), splits, gate);
     }
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
+bool attn_decode_qgate_fits(size_t max_len, size_t d) {
+    const uint32_t splits = attn_splits(max_len, d);
+    return splits >= 2 && splits <= kAttnHeadChunks && (d == 64 || d == 128 || d == 256);
+}
+
+int launch_attn_decode_qgate(const float* mixed, const float* kv, const float* q_gamma, const float* k_gamma,
+                             float eps, const float* cos_sin, size_t rot, float* kcache, float* vcache, float* out,
+                             XGroup* outq, size_t hq, size_t hkv, size_t d, size_t pos, float scale,
+                             hipStream_t stream, const uint32_t* dpos, size_t capacity) {
+    if (!mixed || !kv || !q_gamma || !k_gamma || !cos_sin || !kcache || !vcache || !out || hq == 0 || hkv == 0 ||
+        hq % hkv || !(eps > 0.0f)) {
+        return kInvalidArgument;
+    }
+    if (dpos && capacity == 0) return kInvalidArgument;
+    if (rot == 0 || rot % 2 != 0 || rot > d) return kInvalidArgument;
+    if (outq && reinterpret_cast<uintptr_t>(outq) % 16 != 0) return kInvalidArgument;
+    if (pos >= 0xffffffffull || capacity > 0xffffffffull || hq > 0xffffull) return kLengthError;
+    if (!attn_decode_qgate_fits(dpos ? capacity : pos + 1, d)) return kInvalidArgument;
+    const AttnQGate qg{kv, q_gamma, k_gamma, eps};
+#define HIPLLM_ATTN_QG(D)                                                                                          \
+    HIPLLM_LAUNCH((attn_decode_head<kAttnHeadChunks, D, true>), dim3(static_cast<uint32_t>(hq)),                   \
+                  dim3(256 * kAttnHeadChunks), 0, stream, mixed, kcache, vcache, static_cast<uint32_t>(hq),         \
+                  static_cast<uint32_t>(hkv), static_cast<uint32_t>(pos + 1), dpos, scale,                        \
+                  reinterpret_cast<const float2*>(cos_sin), static_cast<uint32_t>(rot / 2), out, outq, nullptr, qg)
+    if (d == 64) {
+        HIPLLM_ATTN_QG(64);
+    } else if (d == 128) {
+        HIPLLM_ATTN_QG(128);
+    } else {
+        HIPLLM_ATTN_QG(256);
+    }
+#undef HIPLLM_ATTN_QG
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 

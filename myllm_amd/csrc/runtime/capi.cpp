@@ -249,19 +249,22 @@ int hipllm_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, cons
 int hipllm_gemv_x16_moe_down(uint32_t type_r, const void* down_packed, const int32_t* ids, size_t experts,
                              const void* xq, size_t ldx, size_t k_r, uint32_t type_s, const void* shared_packed,
                              const float* sx, size_t k_s, const float* weights, const float* sgate,
-                             const float* residual, float* y, size_t n, size_t routes, void* stream) {
+                             const float* residual, float* y, size_t n, size_t routes,
+                             const HipllmX16Norm* norm_out, void* stream) {
+    const hipllm::X16Norm nrm = norm_out ? x16_norm(norm_out) : hipllm::X16Norm{};
     return status(hipllm::launch_x16_moe_down(type_r, down_packed, ids, experts, xgc(xq), ldx, k_r, type_s,
                                               shared_packed, sx, k_s, weights, sgate, residual, y, n, routes,
-                                              as_stream(stream)),
+                                              as_stream(stream), norm_out ? &nrm : nullptr),
                   "hipllm_gemv_x16_moe_down: invalid arguments (routed Q4_K / Q6_K, shared Q4_K / Q6_K / Q8_0, "
                   "k % 256 == 0, k_s <= 2048, n % 16 == 0, 1..8 routes, 16-byte aligned buffers) or launch failure");
 }
 
 int hipllm_gemv_x16_pair(uint32_t type_a, const void* packed_a, size_t n_a, float* y_a, uint32_t type_b,
                          const void* packed_b, size_t n_b, float* y_b, size_t k, const float* x, const float* gamma,
-                         float eps, const float* conv_w, float* history, size_t ksize, void* stream) {
+                         float eps, const float* conv_w, float* history, size_t ksize, const void* xq,
+                         const double* sumsq, void* stream) {
     return status(hipllm::launch_gemv_x16_pair(type_a, packed_a, n_a, y_a, type_b, packed_b, n_b, y_b, k, x, gamma,
-                                                eps, conv_w, history, ksize, as_stream(stream)),
+                                                eps, conv_w, history, ksize, as_stream(stream), xgc(xq), sumsq),
                   "hipllm_gemv_x16_pair: invalid arguments (Q4_K or Q6_K, k % 256 == 0, k <= 8192, 16-byte aligned "
                   "buffers, eps > 0, ksize 2..4 with a history) or launch failure");
 }
@@ -344,6 +347,15 @@ int hipllm_attn_decode_rope_gated(const float* qkv, const float* cos_sin, size_t
     return status(hipllm::launch_attn_decode_rope(qkv, cos_sin, rot, kcache, vcache, out, xg(outq), scratch, hq, hkv,
                                                   d, pos, scale, as_stream(stream), nullptr, 0, gate),
                   "hipllm_attn_decode_rope_gated: invalid arguments or launch failure");
+}
+
+int hipllm_attn_decode_qgate(const float* mixed, const float* kv, const float* q_gamma, const float* k_gamma,
+                             float eps, const float* cos_sin, size_t rot, float* kcache, float* vcache, float* out,
+                             void* outq, size_t hq, size_t hkv, size_t d, size_t pos, float scale, void* stream) {
+    return status(hipllm::launch_attn_decode_qgate(mixed, kv, q_gamma, k_gamma, eps, cos_sin, rot, kcache, vcache, out,
+                                                   xg(outq), hq, hkv, d, pos, scale, as_stream(stream)),
+                  "hipllm_attn_decode_qgate: invalid arguments (2 to 4 key chunks, d 64 / 128 / 256) or launch "
+                  "failure");
 }
 
 size_t hipllm_attn_decode_scratch_floats(size_t hq, size_t d, size_t max_len) {

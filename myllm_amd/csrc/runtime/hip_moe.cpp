@@ -54,6 +54,7 @@ struct MoeLayer {
     // gated full attention
     DevMatrix qgate, k, v, o;
     bool fused_kv = false;
+    DevMatrix kv;  // K and V rows as one matrix when fused_kv (for its x16 copy)
     const float* q_norm = nullptr;
     const float* k_norm = nullptr;
     float* kcache = nullptr;
@@ -96,6 +97,8 @@ struct MoeActivations {
     float* down = nullptr;                  // [T k, H]
     float* sh_act = nullptr;                // [T, FFs]
     hipllm::XGroup* sh_actq = nullptr;
+    hipllm::XGroup* inq = nullptr;          // [H / 16] next layer's input norm data (one token): x * gamma
+    double* in_sumsq = nullptr;             // [H / 16] and its per-16 sums of squares
     float* sh_gate = nullptr;               // [T, FFs] shared gate projection (prefill matmul form)
     void* xb = nullptr;                     // [T, max(H, inner, Hq D, FFs)] fp16 matmul input
     float* xscale = nullptr;                // [T] its row scales
@@ -206,6 +209,11 @@ struct HipMoeLLM::Impl {
                  bool store_norm, const char* what) const;
     bool grouped_mixer(const MoeLayer& L, std::size_t rows) const;
     bool x16_deltanet(const MoeLayer& L, std::size_t rows) const;
+    bool x16_attention_in(const MoeLayer& L, std::size_t rows) const;
+    // Set by a MoE launch that left the next layer's input norm data in
+    // act.inq / act.in_sumsq (one token), taken by that layer's x16 input
+    // projections.
+    bool in_norm = false;
     bool gathered_experts(const MoeLayer& L, std::size_t rows, const void* xb) const;
     bool grouped_moe(const MoeLayer& L, std::size_t rows) const;
     void attention_layer(std::size_t li, std::size_t rows, std::size_t pos0, float* hidden, float* next,
@@ -323,6 +331,17 @@ void HipMoeLLM::Impl::pack_decode_weights() {
         }
         // The shared expert's down projection, for the launch that runs it
         // with the routed down projections and the combine (Q8_0 too).
+        // The attention's Q / gate and K / V projections, for the paired
+        // launch that normalises the input in every block (K / V: Q8_0 too).
+        if (L.full && L.fused_kv && x16_packable(L.qgate)) {
+            L.kv = L.k;
+            L.kv.rows = L.k.rows + L.v.rows;
+            const bool kv8 = L.kv.type == hipllm::kQ8_0 && L.kv.cols % 256 == 0 && L.kv.row_bytes % 2 == 0;
+            if (x16_packable(L.kv) || kv8) {
+                jobs.push_back({&L.qgate, L.qgate.rows});
+                jobs.push_back({&L.kv, L.kv.rows, kv8});
+            }
+        }
         const DevMatrix& sd = L.sh_down;
         const bool q8 = sd.type == hipllm::kQ8_0 && sd.cols % 256 == 0 && sd.row_bytes % 2 == 0;
         if (sd.rows % 16 == 0 && sd.cols <= 2048 && (x16_packable(sd) || q8)) jobs.push_back({&L.sh_down, sd.rows, q8});
@@ -592,7 +611,8 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
                       o_grp = reserve(2 * hipllm::route_groups_max(n * K, E, hipllm::kGatherRows)),
                       o_ngr = reserve(1), o_gact = reserve(n * K * FF), o_actb = reserve((n * K * FF + 1) / 2),
                       o_xs = reserve(n), o_abs = reserve(n * K),
-                      o_mms = reserve(mm_floats), o_split = reserve(split_bytes / 4);
+                      o_mms = reserve(mm_floats), o_split = reserve(split_bytes / 4), o_inq = reserve(H),
+                      o_inss = reserve(H / 8);
     act_bytes = off;
     hip_check(hipMalloc(&act_arena, act_bytes), "hipMalloc(MoE activations)");
     auto* b = static_cast<std::uint8_t*>(act_arena);
@@ -602,6 +622,8 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
     act.hidden[1] = f(o_h1);
     act.norm = f(o_norm);
     act.normq = g(o_normq);
+    act.inq = g(o_inq);
+    act.in_sumsq = reinterpret_cast<double*>(b + o_inss);
     act.wide = f(o_wide);
     act.wide2 = f(o_wide2);
     act.kv = f(o_kv);
@@ -742,6 +764,12 @@ bool HipMoeLLM::Impl::x16_deltanet(const MoeLayer& L, std::size_t rows) const {
            config.ssm_conv_kernel >= 2 && config.ssm_conv_kernel <= 4;
 }
 
+// Whether attention layer L's decode step runs its Q / gate and K / V
+// projections on the x16 copies as one paired launch.
+bool HipMoeLLM::Impl::x16_attention_in(const MoeLayer& L, std::size_t rows) const {
+    return L.full && rows == 1 && grouped_mixer(L, rows) && L.qgate.x16 && L.kv.x16 && H <= 8192;
+}
+
 // Whether layer L's routed experts run as gathered fp16 matmuls: a prompt
 // whose dense projections already run as matmuls (xb holds its fp16 rows)
 // and routes at least four vectors per expert on average. Each group block
@@ -770,7 +798,17 @@ void HipMoeLLM::Impl::attention_layer(std::size_t li, std::size_t rows, std::siz
     const MoeLayer& L = layers[li];
     const float eps = config.norm_epsilon;
     const std::size_t ldqkv = q_w + 2 * kv_w;
-    if (grouped_mixer(L, rows)) {
+    if (x16_attention_in(L, rows)) {
+        // One token: Q / gate and K / V on their x16 copies in one launch,
+        // from the norm data the previous MoE launch left, or with every
+        // block normalising the input itself.
+        launch_check(hipllm::launch_gemv_x16_pair(L.qgate.type, L.qgate.x16, L.qgate.rows, act.wide, L.kv.type,
+                                                  L.kv.x16, L.kv.rows, act.kv, H, hidden, L.attn_norm, eps, nullptr,
+                                                  nullptr, 0, stream, in_norm ? act.inq : nullptr,
+                                                  in_norm ? act.in_sumsq : nullptr),
+                     "input norm + Q/gate + K/V");
+        in_norm = false;
+    } else if (grouped_mixer(L, rows)) {
         hipllm::GemvJob jobs[3];
         std::size_t nj = 0;
         jobs[nj++] = job(L.qgate, act.wide, L.qgate.rows);
@@ -790,6 +828,17 @@ void HipMoeLLM::Impl::attention_layer(std::size_t li, std::size_t rows, std::siz
             proj(L.k, act.norm, act.normq, H, rows, act.kv, 2 * kv_w, nullptr, 0, xb);
             proj(L.v, act.norm, act.normq, H, rows, act.kv + kv_w, 2 * kv_w, nullptr, 0, xb);  // after K in each row
         }
+    }
+    const float scale0 = 1.0f / std::sqrt(static_cast<float>(D));
+    if (rows == 1 && hipllm::attn_decode_qgate_fits(dpos ? capacity : pos0 + 1, D)) {
+        // One token: the Q / K head norms, RoPE, KV-cache write, attention
+        // and output gate in one launch.
+        launch_check(hipllm::launch_attn_decode_qgate(act.wide, act.kv, L.q_norm, L.k_norm, eps, rope_table,
+                                                      config.rotary_dimension, L.kcache, L.vcache, act.gated,
+                                                      act.gatedq, Hq, Hkv, D, pos0, scale0, stream, dpos, capacity),
+                     "Q/K head norms + RoPE/KV write + attention + output gate");
+        proj_out_norm(L.o, act.gated, act.gatedq, q_w, rows, next, hidden, L.post_norm, !grouped_moe(L, rows));
+        return;
     }
     launch_check(hipllm::launch_split_qgate_norm(act.wide, 2 * q_w, act.kv, 2 * kv_w, L.q_norm, L.k_norm, act.wide2,
                                                  ldqkv, act.feat, q_w, rows, Hq, Hkv, D, eps, stream),
@@ -824,8 +873,10 @@ void HipMoeLLM::Impl::deltanet_layer(std::size_t li, std::size_t rows, float* hi
     if (x16_deltanet(L, rows)) {
         launch_check(hipllm::launch_gemv_x16_pair(L.qkv.type, L.qkv.x16, qkv_w, act.wide, L.z.type, L.z.x16, inner,
                                                   act.feat, H, hidden, L.attn_norm, eps, L.conv, L.history,
-                                                  config.ssm_conv_kernel, stream),
+                                                  config.ssm_conv_kernel, stream, in_norm ? act.inq : nullptr,
+                                                  in_norm ? act.in_sumsq : nullptr),
                      "input norm + DeltaNet QKV (+ conv) / z");
+        in_norm = false;
         launch_check(hipllm::launch_gdn_decode(act.wide, hidden, L.attn_norm,
                                                reinterpret_cast<const float*>(L.alpha.ptr), H, L.dt_bias, L.a,
                                                L.state, act.feat, L.ssm_norm, act.gated, act.gatedq, Hv, G, S, eps,
@@ -996,10 +1047,21 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
     const bool x16_down = x16_experts && grp && !next_norm && L.sh_down.x16 && FF % 256 == 0 && FFs <= 2048 &&
                           H % 16 == 0;
     if (x16_down) {
+        // The next layer's x16 input projections take their norm from data
+        // this launch leaves (the XGroup form of next * gamma, per-16 sums of
+        // squares).
+        const bool last = li + 1 == layers.size();
+        const bool norm_out = !last && H % 16 == 0 &&
+                              (x16_deltanet(layers[li + 1], rows) || x16_attention_in(layers[li + 1], rows));
+        hipllm::X16Norm out{};
+        out.gamma_out = next_gamma;
+        out.yq_out = act.inq;
+        out.sumsq_out = act.in_sumsq;
         launch_check(hipllm::launch_x16_moe_down(L.down_exps.type, L.down_exps.x16, ids, E, act.actq, FF, FF,
                                                  L.sh_down.type, L.sh_down.x16, act.sh_act, FFs, act.rweight,
-                                                 act.rlog + E, hidden, next, H, K, stream),
+                                                 act.rlog + E, hidden, next, H, K, stream, norm_out ? &out : nullptr),
                      "expert down + shared down + MoE combine");
+        in_norm = norm_out;
         return;
     }
     if (x16_experts) {
@@ -1064,6 +1126,7 @@ void HipMoeLLM::Impl::forward(std::size_t rows, std::size_t pos0, const std::int
     const float eps = config.norm_epsilon;
     float* h = act.hidden[0];
     float* tmp = act.hidden[1];
+    in_norm = false;
     launch_check(hipllm::launch_embed(embedding.type, embedding.ptr, embedding.row_bytes, ids, rows,
                                       config.vocabulary_size, H, h, stream),
                  "embedding");

@@ -136,8 +136,10 @@ SIGNATURES = {
     "hipllm_gdn_scan_gated": (_I, [_P, _P, _S, _P, _S, _P, _P, _S, _P, _P, _P, _P, _S, _P, _P, _P, _S, _S, _S, _S,
                                    _S, _F, _P]),
     "hipllm_gdn_decode": (_I, [_P, _P, _P, _P, _S, _P, _P, _P, _P, _P, _P, _P, _S, _S, _S, _F, _P]),
-    "hipllm_gemv_x16_pair": (_I, [_U32, _P, _S, _P, _U32, _P, _S, _P, _S, _P, _P, _F, _P, _P, _S, _P]),
-    "hipllm_gemv_x16_moe_down": (_I, [_U32, _P, _P, _S, _P, _S, _S, _U32, _P, _P, _S, _P, _P, _P, _P, _S, _S, _P]),
+    "hipllm_attn_decode_qgate": (_I, [_P, _P, _P, _P, _F, _P, _S, _P, _P, _P, _P, _S, _S, _S, _S, _F, _P]),
+    "hipllm_gemv_x16_pair": (_I, [_U32, _P, _S, _P, _U32, _P, _S, _P, _S, _P, _P, _F, _P, _P, _S, _P, _P, _P]),
+    "hipllm_gemv_x16_moe_down": (_I, [_U32, _P, _P, _S, _P, _S, _S, _U32, _P, _P, _S, _P, _P, _P, _P, _S, _S, _P,
+                                      _P]),
     "hipllm_split_qgate_norm": (_I, [_P, _S, _P, _S, _P, _P, _P, _S, _P, _S, _S, _S, _S, _S, _F, _P]),
     "hipllm_gate_mul": (_I, [_P, _P, _P, _P, _S, _P]),
     "hipllm_destroy": (None, [_P]),
@@ -597,10 +599,10 @@ def _k_gemv_x16_routed(qtype, packed, packed2, xq, ldx, x_routed, y, yq, ldy, n,
 
 
 def _k_gemv_x16_moe_down(type_r, down_packed, ids, experts, xq, ldx, k_r, type_s, shared_packed, sx, k_s, weights,
-                         sgate, residual, y, n, routes, stream=None):
+                         sgate, residual, y, n, routes, norm_out=None, stream=None):
     check(lib().hipllm_gemv_x16_moe_down(type_r, _ptr(down_packed), _ptr(ids), experts, _ptr(xq), ldx, k_r, type_s,
                                          _ptr(shared_packed), _ptr(sx), k_s, _ptr(weights), _ptr(sgate),
-                                         _ptr(residual), _ptr(y), n, routes, _stream(stream)))
+                                         _ptr(residual), _ptr(y), n, routes, _x16_norm(norm_out), _stream(stream)))
 
 
 def _k_to_f16(x, ldx, xh, xscale, m, k, stream=None):
@@ -764,9 +766,10 @@ def _k_gdn_decode(qkv, x, x_gamma, ab_w, hidden, dt_bias, a, state, z, gamma, y,
 
 
 def _k_gemv_x16_pair(type_a, packed_a, n_a, y_a, type_b, packed_b, n_b, y_b, k, x, gamma, eps, conv_w=None,
-                     history=None, ksize=0, stream=None):
+                     history=None, ksize=0, xq=None, sumsq=None, stream=None):
     check(lib().hipllm_gemv_x16_pair(type_a, _ptr(packed_a), n_a, _ptr(y_a), type_b, _ptr(packed_b), n_b, _ptr(y_b), k,
-                                     _ptr(x), _ptr(gamma), eps, _ptr(conv_w), _ptr(history), ksize, _stream(stream)))
+                                     _ptr(x), _ptr(gamma), eps, _ptr(conv_w), _ptr(history), ksize, _ptr(xq),
+                                     _ptr(sumsq), _stream(stream)))
 
 
 def _k_split_qgate_norm(mixed, ldm, kv, ldkv, q_gamma, k_gamma, qkv, ldqkv, gate, ldg, tokens, hq, hkv, d, eps,
@@ -805,6 +808,13 @@ def _k_attn_decode_rope_gated(qkv, cos_sin, rot, kcache, vcache, gate, out, outq
                                               _stream(stream)))
 
 
+def _k_attn_decode_qgate(mixed, kv, q_gamma, k_gamma, eps, cos_sin, rot, kcache, vcache, out, outq, hq, hkv, d, pos,
+                         scale, stream=None):
+    check(lib().hipllm_attn_decode_qgate(_ptr(mixed), _ptr(kv), _ptr(q_gamma), _ptr(k_gamma), eps, _ptr(cos_sin), rot,
+                                         _ptr(kcache), _ptr(vcache), _ptr(out), _ptr(outq), hq, hkv, d, pos, scale,
+                                         _stream(stream)))
+
+
 def _k_attn_decode(q, kcache, vcache, out, outq, scratch, hq, hkv, d, length, scale, stream=None):
     check(lib().hipllm_attn_decode(_ptr(q), _ptr(kcache), _ptr(vcache), _ptr(out), _ptr(outq), _ptr(scratch),
                                    hq, hkv, d, length, scale, _stream(stream)))
@@ -837,7 +847,7 @@ kernels = types.SimpleNamespace(
     gdn_scan_chunked=_k_gdn_scan_chunked,
     gdn_chunk_scratch_floats=lambda t, h: lib().hipllm_gdn_chunk_scratch_floats(t, h),
     conv_l2norm=_k_conv_l2norm, gdn_scan_gated=_k_gdn_scan_gated, gdn_decode=_k_gdn_decode,
-    gemv_x16_pair=_k_gemv_x16_pair, gemv_x16_moe_down=_k_gemv_x16_moe_down,
+    gemv_x16_pair=_k_gemv_x16_pair, attn_decode_qgate=_k_attn_decode_qgate, gemv_x16_moe_down=_k_gemv_x16_moe_down,
     split_qgate_norm=_k_split_qgate_norm, gate_mul=_k_gate_mul,
     gemv_workspace_bytes=lambda k: lib().hipllm_gemv_workspace_bytes(k),
     attn_decode_scratch_floats=lambda hq, d, n: lib().hipllm_attn_decode_scratch_floats(hq, d, n),

@@ -359,14 +359,17 @@ def test_gemv_x16_norm_rejects_bad_combinations(cuda):
         kernels.gemv_x16(synth.Q4_K, pb, xb, None, None, y, 16, big, 0, norm={"sumsq_in": ssq})
 
 
+@pytest.mark.parametrize("src", ["raw row", "norm data"])
 @pytest.mark.parametrize("ta,tb,na,nb,k,ksize", [(synth.Q6_K, synth.Q4_K, 96, 64, 2048, 4),
                                                 (synth.Q4_K, synth.Q6_K, 40, 37, 512, 3),
-                                                (synth.Q4_K, synth.Q4_K, 64, 48, 768, 0)])
-def test_pair_norm_conv_matches_float64(cuda, ta, tb, na, nb, k, ksize):
+                                                (synth.Q4_K, synth.Q8_0, 64, 48, 768, 0)])
+def test_pair_norm_conv_matches_float64(cuda, ta, tb, na, nb, k, ksize, src):
     """Two GEMVs of one row in one launch, each block normalising the raw row
-    itself, job A with the causal conv + SiLU epilogue (history shifted by one
-    row), against float64 over the oracle's dequantization; two calls in a
-    row, so the second reads the history the first wrote."""
+    itself (or taking the norm from a producer's data: the XGroup form of
+    x * gamma and per-16 double sums of squares), job A with the causal
+    conv + SiLU epilogue (history shifted by one row), against float64 over
+    the oracle's dequantization; two calls in a row, so the second reads the
+    history the first wrote."""
     wa, wb = random_rows(ta, na, k, 61), random_rows(tb, nb, k, 62)
     pa = torch.empty(kernels.x16_bytes(ta, na, k), dtype=torch.uint8, device=cuda)
     pb = torch.empty(kernels.x16_bytes(tb, nb, k), dtype=torch.uint8, device=cuda)
@@ -384,8 +387,14 @@ def test_pair_norm_conv_matches_float64(cuda, ta, tb, na, nb, k, ksize):
         x = rng.normal(size=k).astype(np.float32)
         ya = torch.empty(na, device=cuda)
         yb = torch.empty(nb, device=cuda)
+        xq = ss = None
+        if src == "norm data":
+            xq = xgroup.buffer(torch, k, cuda)
+            kernels.prep_x(torch.from_numpy(x * gamma).to(cuda), xq, k)
+            xd = x.astype(np.float64).reshape(-1, 16)
+            ss = torch.from_numpy((xd * xd).sum(axis=1)).to(cuda)
         kernels.gemv_x16_pair(ta, pa, na, ya, tb, pb, nb, yb, k, torch.from_numpy(x).to(cuda),
-                              torch.from_numpy(gamma).to(cuda), 1e-6, dconv, dhist, ksize)
+                              torch.from_numpy(gamma).to(cuda), 1e-6, dconv, dhist, ksize, xq=xq, sumsq=ss)
         xs = x.astype(np.float64)
         n = xs / np.sqrt(np.mean(xs * xs) + 1e-6) * gamma
         pre = fa @ n

@@ -239,8 +239,12 @@ def test_gemv_x16_moe_down_matches_down_and_combine(cuda, qr, qs, E, K, n, ff, f
     sg = np.array([0.7], dtype=np.float32)
     res = rng.normal(size=n).astype(np.float32)
     y = torch.empty(n, device=cuda)
+    gam = rng.normal(size=n).astype(np.float32)
+    yq_out = xgroup.buffer(torch, n, cuda)
+    ss_out = torch.empty(n // 16, dtype=torch.float64, device=cuda)
     kernels.gemv_x16_moe_down(qr, pd, ids, E, actq, ff, ff, qs, ps, t32(sx, cuda), ffs, t32(wts, cuda), t32(sg, cuda),
-                              t32(res, cuda), y, n, K)
+                              t32(res, cuda), y, n, K,
+                              norm_out={"gamma_out": t32(gam, cuda), "yq_out": yq_out, "sumsq_out": ss_out})
     down = torch.empty(K, n, device=cuda)
     kernels.gemv_x16_routed(qr, pd, None, actq, ff, True, down, None, n, n, ff, E, K, ids=ids)
     y_ref = torch.empty(n, device=cuda)
@@ -248,6 +252,10 @@ def test_gemv_x16_moe_down_matches_down_and_combine(cuda, qr, qs, E, K, n, ff, f
                              t32(wts, cuda), t32(sg, cuda), K, y_ref, n, ffs)
     got = y.cpu().numpy()
     assert rel_err(got, y_ref.cpu().numpy()) <= 1e-5
+    # The next norm's data: XGroup form of y * gamma, per-16 double sums of squares.
+    xgroup.check(yq_out, got * gam)
+    gd = got.astype(np.float64).reshape(-1, 16)
+    np.testing.assert_allclose(ss_out.cpu().numpy(), (gd * gd).sum(axis=1), rtol=1e-13)
     fd = oracle.dequant_rows(qr, wd, ff).astype(np.float64).reshape(E, n, ff)
     fs = oracle.dequant_rows(qs, ws, ffs).astype(np.float64)
     routed = sum(float(wts[j]) * (fd[ids_np[j]] @ act[j].astype(np.float64)) for j in range(K))
@@ -695,6 +703,60 @@ def test_gdn_decode_rejects_bad_shapes(cuda):
 
 
 # ------------------------------------------------------------ attention pieces
+@pytest.mark.parametrize("hq,hkv,d,rot,pos", [(16, 2, 256, 64, 70), (16, 2, 256, 64, 128), (8, 2, 128, 128, 150),
+                                              (14, 2, 64, 64, 250)])
+def test_attn_decode_qgate_matches_split_and_gated_step(cuda, hq, hkv, d, rot, pos):
+    """Head norms + RoPE / KV write + attention + output gate in one launch
+    against split_qgate_norm followed by the gated decode step: both caches
+    bit for bit, the output within 1e-6 of the largest value (the two
+    kernels are compiled separately, and the compiler may fuse a multiply
+    and add in one and not the other: 14 heads of 64 at 251 keys differ by a
+    few ulps in one head) and its XGroup form."""
+    rng = np.random.default_rng(pos + d)
+    kvw = hkv * d
+    cap = pos + 3
+    mixed = rng.normal(size=hq * 2 * d).astype(np.float32)
+    kv = rng.normal(size=2 * kvw).astype(np.float32)
+    qg, kg = rng.normal(size=d).astype(np.float32), rng.normal(size=d).astype(np.float32)
+    ang = rng.uniform(-3.0, 3.0, size=(cap, rot // 2)).astype(np.float32)
+    table = torch.from_numpy(np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)).to(cuda)
+    kc0 = rng.normal(size=(cap, kvw)).astype(np.float32)
+    vc0 = rng.normal(size=(cap, kvw)).astype(np.float32)
+    scale = float(np.float32(1.0) / np.float32(math.sqrt(d)))
+    dm, dkv, dqg, dkg = t32(mixed, cuda), t32(kv, cuda), t32(qg, cuda), t32(kg, cuda)
+    outs = []
+    for fused in (False, True):
+        kc, vc = t32(kc0, cuda), t32(vc0, cuda)
+        out = torch.empty(hq * d, device=cuda)
+        outq = xgroup.buffer(torch, hq * d, cuda)
+        if fused:
+            kernels.attn_decode_qgate(dm, dkv, dqg, dkg, 1e-6, table, rot, kc, vc, out, outq, hq, hkv, d, pos, scale)
+        else:
+            ldqkv = (hq + 2 * hkv) * d
+            qkv = torch.zeros(1, ldqkv, device=cuda)
+            gate = torch.empty(1, hq * d, device=cuda)
+            kernels.split_qgate_norm(dm, hq * 2 * d, dkv, 2 * kvw, dqg, dkg, qkv, ldqkv, gate, hq * d, 1, hq, hkv, d,
+                                     1e-6)
+            scratch = torch.empty(kernels.attn_decode_scratch_floats(hq, d, pos + 1), device=cuda)
+            kernels.attn_decode_rope_gated(qkv, table, rot, kc, vc, gate, out, outq, scratch, hq, hkv, d, pos, scale)
+        outs.append([t.cpu().numpy() for t in (out, kc, vc)])
+        if fused:
+            xgroup.check(outq, outs[-1][0])
+    (o1, k1, v1), (o2, k2, v2) = outs
+    assert np.array_equal(k1.view(np.uint32), k2.view(np.uint32))
+    assert np.array_equal(v1.view(np.uint32), v2.view(np.uint32))
+    assert rel_err(o2, o1) <= 1e-6
+
+
+def test_attn_decode_qgate_rejects_other_lengths(cuda):
+    z = torch.zeros(1 << 16, device=cuda)
+    args = lambda d, pos: (z, z, z, z, 1e-6, z, 64, z, z, z, None, 16, 2, d, pos, 0.1)
+    kernels.attn_decode_qgate(*args(256, 100))
+    for d, pos in ((256, 10), (256, 300), (96, 100)):  # one chunk, five chunks, head size
+        with pytest.raises(ValueError):
+            kernels.attn_decode_qgate(*args(d, pos))
+
+
 def test_split_qgate_norm_and_gate_mul(cuda):
     rng = np.random.default_rng(8)
     T, Hq, Hkv, D = 2, 4, 2, 256
