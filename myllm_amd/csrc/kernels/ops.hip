@@ -51,21 +51,26 @@ __global__ void embed_kernel(uint32_t type, const uint8_t* __restrict__ table, s
 // Element i of a head rotated with the position's (cos, sin) pairs, the same
 // products and sum as rope_kv_kernel (contraction off): pairs (p, p + half)
 // for p < half, dims past 2 half unchanged.
-__device__ __forceinline__ float rope_elem(const float* __restrict__ x, const float2* __restrict__ tab, uint32_t half,
-                                          uint32_t i) {
+// Element i of the rotated row x, cs = the table pair of i (of i - half in
+// the second half; unused past 2 half).
+__device__ __forceinline__ float rope_apply(const float* __restrict__ x, float2 cs, uint32_t half, uint32_t i) {
     if (i < half) {
-        const float2 cs = tab[i];
         const float t1 = x[i] * cs.x;
         const float t2 = x[i + half] * cs.y;
         return t1 - t2;
     }
     if (i < 2 * half) {
-        const float2 cs = tab[i - half];
         const float t3 = x[i - half] * cs.y;
         const float t4 = x[i] * cs.x;
         return t3 + t4;
     }
     return x[i];
+}
+
+__device__ __forceinline__ float rope_elem(const float* __restrict__ x, const float2* __restrict__ tab, uint32_t half,
+                                          uint32_t i) {
+    const float2 cs = i < 2 * half ? tab[i < half ? i : i - half] : make_float2(0.0f, 0.0f);
+    return rope_apply(x, cs, half, i);
 }
 
 __global__ void rope_kv_kernel(float* __restrict__ qkv, const float2* __restrict__ table, uint32_t half_rot,
@@ -386,9 +391,10 @@ __global__ __launch_bounds__(256 * NG) void attn_decode_head(const float* __rest
     constexpr uint32_t KR = D4 / 4;                // float4 of a key per scoring lane
     constexpr uint32_t VR = kAttnChunk / PARTS;    // value rows per p.V lane
     // 256-dim heads load their rows where they are used: a lane's K (64
-    // floats) and V rows held from the start would exceed the registers of a
-    // 1024-thread block.
+    // floats) held from the start already exceeds the registers of a
+    // 1024-thread block (measured: 48 bytes of scratch per lane).
     constexpr bool kPre = D <= 128;
+    static_assert(256 * NG >= D, "one thread per head dimension");
     const uint32_t h = blockIdx.x;
     const uint32_t len = dpos ? *dpos + 1 : len_arg;
     const uint32_t nchunks = (len + kAttnChunk - 1) / kAttnChunk;  // <= NG
@@ -429,6 +435,19 @@ __global__ __launch_bounds__(256 * NG) void attn_decode_head(const float* __rest
     const float* qrow = q + h * D;
     if constexpr (QG) qrow = q + static_cast<size_t>(h) * 2 * D;
     const float* grow = QG ? qrow + D : (gate ? gate + h * D : nullptr);
+    // The new row's V value, table pair and output gate of this thread's
+    // dimension, loaded now.
+    const float* vn = QG ? qg.kv + kvd + g * D : q + hq * D + g * D + kvd;
+    float2 cs_pre = make_float2(0.0f, 0.0f);
+    float v_pre = 0.0f, g_pre = 0.0f;
+    if (tid < D) {
+        if (rope) {
+            const float2* tab = rope + static_cast<size_t>(len - 1) * half_rot;
+            if (tid < 2 * half_rot) cs_pre = tab[tid < half_rot ? tid : tid - half_rot];
+            v_pre = vn[tid];
+        }
+        if (grow) g_pre = grow[tid];
+    }
     __shared__ float qgn[QG ? 2 : 1][QG ? D : 1];
     if constexpr (QG) {
         if (tid < 128) {
@@ -444,22 +463,21 @@ __global__ __launch_bounds__(256 * NG) void attn_decode_head(const float* __rest
         __syncthreads();
     }
     if (rope) {
-        const float2* tab = rope + static_cast<size_t>(len - 1) * half_rot;
         const float* kn = QG ? qgn[QG ? 1 : 0] : q + hq * D + g * D;
-        const float* vn = QG ? qg.kv + kvd + g * D : kn + kvd;
         const float* qn = QG ? qgn[0] : qrow;
         float* kc = kcache + static_cast<size_t>(len - 1) * kvd + g * D;
         float* vc = vcache + static_cast<size_t>(len - 1) * kvd + g * D;
         float* qs = reinterpret_cast<float*>(qs4);
         float* ks = reinterpret_cast<float*>(kn4);
         float* vs = reinterpret_cast<float*>(vn4);
-        for (uint32_t i = tid; i < D; i += blockDim.x) {
-            qs[i] = rope_elem(qn, tab, half_rot, i);
-            const float kv = rope_elem(kn, tab, half_rot, i);
+        if (tid < D) {
+            const uint32_t i = tid;
+            qs[i] = rope_apply(qn, cs_pre, half_rot, i);
+            const float kv = rope_apply(kn, cs_pre, half_rot, i);
             ks[i] = kv;
-            vs[i] = vn[i];
+            vs[i] = v_pre;
             kc[i] = kv;
-            vc[i] = vn[i];
+            vc[i] = v_pre;
         }
     } else {
         for (uint32_t i = tid; i < D4; i += blockDim.x) qs4[i] = reinterpret_cast<const float4*>(q + h * D)[i];
@@ -551,7 +569,7 @@ __global__ __launch_bounds__(256 * NG) void attn_decode_head(const float* __rest
             }
         }
         float v = a * (1.0f / L);
-        if (grow) v = v * sigmoid_ref(grow[tid]);
+        if (grow) v = v * sigmoid_ref(g_pre);
         fout[h * D + tid] = v;
         vals[tid] = v;
     }
