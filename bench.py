@@ -31,7 +31,8 @@ The same JSON line carries:
   GPU/CPU decode ratio.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-e2e] [--no-cpu]
-                       [--no-14b] [--no-moe] [--profile-kernel gate] [--profile-reps N]
+                       [--no-14b] [--no-moe] [--profile-kernel gate|prefill64|prefill512|prefill2048]
+                       [--profile-reps N]
 """
 
 from __future__ import annotations
@@ -459,6 +460,35 @@ def profile_kernel(name, reps, torch, cuda):
                       "copy": copy}), flush=True)
 
 
+def profile_prefill(m, reps, torch, cuda):
+    """Runs the Q4_K prefill matmul (K = 3584, N = 18944, m rows, fp16
+    operands, the default tile and K split) `reps` times over 8 rotated
+    weight copies plus a plain copy of the weight bytes, for rocprofv3
+    counter collection."""
+    from myllm_amd import synth
+    from myllm_amd.hipllm import kernels, lib
+    K, N = 3584, 18944
+    src = synth.random_quantized(N, K, synth.Q4_K, seed=N * 7 + K)
+    ws = []
+    for _ in range(8):
+        w = torch.empty(src.nbytes + 256, dtype=torch.uint8, device=cuda)
+        w[: src.nbytes].copy_(torch.from_numpy(src.reshape(-1)))
+        ws.append(w)
+    x = torch.randn(m, K, device=cuda)
+    xh = torch.empty(m, K, device=cuda, dtype=torch.float16)
+    xs = torch.empty(m, device=cuda)
+    kernels.to_f16(x, K, xh, xs, m, K)
+    y = torch.empty(m, N, device=cuda)
+    split_ws = torch.empty(max(16, lib().hipllm_gemm_mfma_workspace_bytes(m, N, K, -1, 0)), dtype=torch.uint8,
+                           device=cuda)
+    for i in range(reps):
+        kernels.gemm_mfma(synth.Q4_K, ws[i % 8], src.shape[1], xh, xs, None, None, y, m, N, K, workspace=split_ws)
+    torch.cuda.synchronize()
+    copy = bench_copy(torch, cuda, src.nbytes // 256 * 256)
+    print(json.dumps({"profiled": f"prefill matmul M={m}", "launches": reps, "weight_bytes": int(src.nbytes),
+                      "flops": 2 * m * N * K, "copy": copy}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -468,7 +498,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-14b", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
-    ap.add_argument("--profile-kernel", choices=[s[0] for s in SHAPES])
+    ap.add_argument("--profile-kernel", choices=[s[0] for s in SHAPES] + ["prefill64", "prefill512", "prefill2048"])
     ap.add_argument("--e2e-only", choices=["qwen2.5-0.5b", "qwen2.5-7b", "qwen2.5-14b", "qwen3.5-35b-a3b"],
                     help="run one end-to-end model only (for profiling) and print its result")
     ap.add_argument("--profile-reps", type=int, default=200)
@@ -484,6 +514,9 @@ def main():
     cuda = torch.device("cuda:0")
     from myllm_amd import synth
 
+    if args.profile_kernel and args.profile_kernel.startswith("prefill"):
+        profile_prefill(int(args.profile_kernel[len("prefill"):]), min(args.profile_reps, 50), torch, cuda)
+        return
     if args.profile_kernel:
         profile_kernel(args.profile_kernel, args.profile_reps, torch, cuda)
         return
