@@ -274,7 +274,7 @@ int hipllm_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m,
  * accumulation; k % 128 == 0. `tile` < 0 picks the default, else
  * 0..3 = 128x32, 128x64, 256x64, 256x128 (weight rows x X rows per block),
  * 4, 5 = 128x128, 128x256 with each weight tile dequantized once into LDS
- * and shared by all four waves.
+ * and shared by all four waves, 6 = 128x128 dequantized in registers.
  * `splits` 0 picks the default K split, else 1..1024 blocks along k: with
  * more than one, every split writes its partial sums to `workspace` (16-byte
  * aligned, hipllm_gemm_mfma_workspace_bytes) and a second launch adds them in

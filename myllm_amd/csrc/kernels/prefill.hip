@@ -816,6 +816,7 @@ int launch_typed(int tile, const void* w, size_t row_bytes, const _Float16* xb, 
     case 1: launch_tile<T, 1, 2>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream); break;
     case 2: launch_tile<T, 2, 2>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream); break;
     case 3: launch_tile<T, 2, 4>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream); break;
+    case 6: launch_tile<T, 1, 4>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream); break;
     default: return kInvalidArgument;
     }
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
@@ -823,16 +824,20 @@ int launch_typed(int tile, const void* w, size_t row_bytes, const _Float16* xb, 
 
 }  // namespace
 
-// Tile choice: 0 = 128 x 32, 1 = 128 x 64, 2 = 256 x 64, 3 = 256 x 128
-// (weight rows x X rows per block, dequantized in registers), 4 = 128 x 128
-// and 5 = 128 x 256 (dequantized once into LDS). Measured on the 7B prefill
-// shapes (M 128 to 2048): 128 x 64 (three waves per SIMD) is fastest for the
-// short rows (k = 3584); for long rows (the down projection, k = 18944) the
+// Tile choice: 0 = 128 x 32, 1 = 128 x 64, 2 = 256 x 64, 3 = 256 x 128,
+// 6 = 128 x 128 (weight rows x X rows per block, dequantized in registers),
+// 4 = 128 x 128 and 5 = 128 x 256 (dequantized once into LDS). Measured on
+// the 7B prefill shapes (Q4_K, k = 3584, n = 18944): 128 x 64 (four waves per
+// SIMD) is fastest up to 512 rows (M 128: 55 us against 58 for 128 x 128);
+// from 1024 rows 128 x 128 in registers converts each weight half as often
+// and wins despite two waves per SIMD (M 1024: 212 against 233 us, M 2048:
+// 394 against 416); for long rows (the down projection, k = 18944) the
 // shared-dequant 128 x 128 tile with a K split is 10-15% faster. 128 x 32 for
 // a single X tile.
 int gemm_default_tile(uint32_t m, uint32_t, uint32_t k) {
     if (m <= 32) return 0;
-    return k >= 8192 ? 4 : 1;
+    if (k >= 8192) return 4;
+    return m >= 1024 ? 6 : 1;
 }
 
 int launch_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m, size_t k, hipStream_t stream) {
@@ -851,9 +856,9 @@ int launch_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m,
 // qwen35moe projections of short prompts: 1 to 64 tiles of 2048-long rows)
 // take up to eight splits where four 128-k steps per split allowed four.
 uint32_t gemm_default_splits(uint32_t m, uint32_t n, uint32_t k, int tile) {
-    const uint32_t bn[6] = {128, 128, 256, 256, 128, 128}, bm[6] = {32, 64, 64, 128, 128, 256};
+    const uint32_t bn[7] = {128, 128, 256, 256, 128, 128, 128}, bm[7] = {32, 64, 64, 128, 128, 256, 128};
     const uint64_t blocks = static_cast<uint64_t>((n + bn[tile] - 1) / bn[tile]) * ((m + bm[tile] - 1) / bm[tile]);
-    const uint64_t target = tile >= 4 ? 256 : 512;
+    const uint64_t target = tile == 4 || tile == 5 ? 256 : 512;
     const uint32_t steps = k / kStepK;
     if (blocks >= target * 3 / 4 || steps < 4) return 1;
     const uint32_t want = static_cast<uint32_t>((target + blocks - 1) / blocks);
@@ -875,7 +880,7 @@ uint32_t effective_splits(uint32_t m, uint32_t n, uint32_t k, int tile, int spli
 size_t gemm_split_bytes(size_t m, size_t n, size_t k, int tile, int splits) {
     if (m == 0 || n == 0 || k < kStepK || m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull) return 0;
     if (tile < 0) tile = gemm_default_tile(static_cast<uint32_t>(m), static_cast<uint32_t>(n), static_cast<uint32_t>(k));
-    if (tile > 5 || splits < 0 || splits > 1024) return 0;
+    if (tile > 6 || splits < 0 || splits > 1024) return 0;
     uint32_t per;
     const uint32_t s = effective_splits(static_cast<uint32_t>(m), static_cast<uint32_t>(n), static_cast<uint32_t>(k),
                                         tile, splits, &per);
@@ -901,7 +906,7 @@ int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void*
     }
     if (reinterpret_cast<uintptr_t>(xb) % 16 != 0) return kInvalidArgument;
     if (tile < 0) tile = gemm_default_tile(static_cast<uint32_t>(m), static_cast<uint32_t>(n), static_cast<uint32_t>(k));
-    if (tile > 5) return kInvalidArgument;
+    if (tile > 6) return kInvalidArgument;
     const uint32_t M = static_cast<uint32_t>(m), N = static_cast<uint32_t>(n), K = static_cast<uint32_t>(k);
     if (splits < 0 || splits > 1024) return kInvalidArgument;
     uint32_t per;

@@ -85,7 +85,7 @@ def gemm_case(cuda, qtype, m, n, k, seed, tile=-1, bias=False, residual=False, s
 
 
 @pytest.mark.parametrize("qtype", TYPES)
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6])
 def test_gemm_types_and_tiles_ragged(cuda, qtype, tile):
     # m = 77, n = 333: partial tiles on both axes; k = 512: four 128-steps
     # (both halves of a K-quant super-block).
@@ -221,7 +221,7 @@ def test_gemm_rejects_bad_arguments(cuda):
     with pytest.raises(ValueError):
         kernels.gemm_mfma(synth.Q4_K, w, 144, xh, xs, None, None, y, 2, 2, 192)  # k % 128 != 0
     with pytest.raises(ValueError):
-        kernels.gemm_mfma(synth.Q4_K, w, 144, xh, xs, None, None, y, 2, 2, 256, 7)  # unknown tile
+        kernels.gemm_mfma(synth.Q4_K, w, 144, xh, xs, None, None, y, 2, 2, 256, 8)  # unknown tile
     with pytest.raises(ValueError):
         kernels.gemm_mfma(99, w, 144, xh, xs, None, None, y, 2, 2, 256)  # unknown type
     with pytest.raises(ValueError):
