@@ -196,6 +196,21 @@ int hipllm_gemv_x16_routed(uint32_t type, const void* packed, const void* packed
  * RMSNorm's data as hipllm_gemv_x16 with an output norm does. Replaces the
  * expert down GEMMs, shared-expert down GEVM and the weighted sum of
  * encode_selected_moe (moe_llm.mm:2790-2843; metal_llm.metal:1424-1521). */
+/* Routed expert vectors of a prompt grouped by expert on x16 copies of the
+ * whole expert block ([experts * n, k], n % 16 == 0, Q4_K or Q6_K): the
+ * groups of hipllm_route_groups with vmax <= 4 (order, groups, ngroups;
+ * max_groups = hipllm_route_groups_max(vectors, experts, vmax)); each group
+ * reads its expert's tiles once for all its vectors. Vector v (an index
+ * into the routed vectors) reads XGroup row v (x_routed) or v / routes of xq
+ * (ldx values apart) and writes row v of y (ldy apart); packed2 != nullptr:
+ * the gate / up pair, y = silu(Wg x) * (Wu x), yq (nullable) its XGroup
+ * form. Replaces the expert GEMMs of encode_selected_moe for a prompt
+ * (moe_llm.mm:2642-2843; metal_llm.metal:1424-1521). */
+int hipllm_gemv_x16_grouped(uint32_t type, const void* packed, const void* packed2, const void* xq, size_t ldx,
+                            int x_routed, size_t routes, float* y, void* yq, size_t ldy, size_t n, size_t k,
+                            size_t experts, const int32_t* order, const int32_t* groups, const uint32_t* ngroups,
+                            size_t max_groups, void* stream);
+
 int hipllm_gemv_x16_moe_down(uint32_t type_r, const void* down_packed, const int32_t* ids, size_t experts,
                              const void* xq, size_t ldx, size_t k_r, uint32_t type_s, const void* shared_packed,
                              const float* sx, size_t k_s, const float* weights, const float* sgate,

@@ -2300,6 +2300,155 @@ int launch_x16_moe_down(uint32_t type_r, const void* down_x16, const int32_t* id
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
+// Routed expert vectors of a short prompt grouped by expert (route groups of
+// at most kX16GroupRows vectors, launch_route_groups): block (tile, group)
+// reads its expert's 16-row tile of the x16 copy of the whole expert block
+// once and multiplies it by every vector of the group. Vector j of the group
+// is routed vector order[first + j] (its input row: that index when
+// x_routed, else the index / routes; its output row: that index). 4 waves
+// split the units; per unit a wave loads the weights (both matrices for the
+// SwiGLU pair) and each vector's 1 KiB of input groups, then runs the
+// unit's MFMAs for each vector from its own LDS slot. MODE 0: y = W x;
+// MODE 1: y = silu(Wg x) * (Wu x) and yq its XGroup form (one group per
+// tile). Groups past *ngroups exit at once.
+template <uint32_t QT, int MODE>
+__global__ __launch_bounds__(256) void x16_grouped_kernel(
+    const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, size_t expert_bytes, uint32_t experts,
+    const XGroup* __restrict__ xq, uint32_t ldx, uint32_t x_routed, uint32_t routes, float* __restrict__ y,
+    XGroup* __restrict__ yq, uint32_t ldy, uint32_t n, uint32_t units, const int32_t* __restrict__ order,
+    const int32_t* __restrict__ groups, const uint32_t* __restrict__ ngroups) {
+    constexpr int WPB = 4, VB = kX16GroupRows, NM = MODE == 1 ? 2 : 1;
+    using F = X16<QT>;
+    constexpr uint32_t kTileUnit = 16 * F::kBlock;
+    if (blockIdx.y >= *ngroups) return;
+    const uint32_t first = static_cast<uint32_t>(groups[2 * blockIdx.y]);
+    const uint32_t packed = static_cast<uint32_t>(groups[2 * blockIdx.y + 1]);
+    const uint32_t e = min(packed & 0xffffu, experts - 1);
+    const uint32_t cnt = min(packed >> 16, static_cast<uint32_t>(VB));  // launch_route_groups with vmax <= VB
+    const uint32_t tile = blockIdx.x;
+    __shared__ __align__(16) uint8_t xs[WPB][VB + 1][1024];  // per wave: one slot per vector, then zeros
+    __shared__ float part[WPB][VB][NM][16];
+    __shared__ __align__(16) float outs[VB][16];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t r = lane & 15, s = lane >> 4;
+    const uint8_t* wt[NM];
+    wt[0] = w + static_cast<size_t>(e) * expert_bytes + static_cast<size_t>(tile) * units * kTileUnit;
+    if (MODE == 1) wt[NM - 1] = w2 + static_cast<size_t>(e) * expert_bytes + static_cast<size_t>(tile) * units * kTileUnit;
+    uint32_t vec[VB];
+    const uint4* xrow[VB];
+#pragma unroll
+    for (int j = 0; j < VB; ++j) {
+        vec[j] = j < static_cast<int>(cnt) ? static_cast<uint32_t>(order[first + j]) : 0u;
+        const uint32_t src = x_routed ? vec[j] : vec[j] / routes;
+        xrow[j] = reinterpret_cast<const uint4*>(xq + static_cast<size_t>(src) * (ldx / 16));
+    }
+    uint8_t* zero = xs[wave][VB];
+    for (uint32_t i = lane; i < kMfmaZeroBytes / 16; i += 64) reinterpret_cast<uint4*>(zero)[i] = make_uint4(0, 0, 0, 0);
+    const bool a_lane = (r >> 2) == s && (r & 3) < 3;
+    const uint32_t slot = F::group_base(s);
+    float acc[VB][NM];
+#pragma unroll
+    for (int j = 0; j < VB; ++j)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) acc[j][m] = 0.0f;
+    for (uint32_t u = wave; u < units; u += WPB) {
+        typename F::Unit wu[NM];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) wu[m] = F::load(wt[m] + static_cast<size_t>(u) * kTileUnit, r, s, lane);
+        uint4 xv[VB];
+#pragma unroll
+        for (int j = 0; j < VB; ++j) xv[j] = j < static_cast<int>(cnt) ? xrow[j][64 * u + lane] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < VB; ++j) *reinterpret_cast<uint4*>(xs[wave][j] + 16 * lane) = xv[j];
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int j = 0; j < VB; ++j) {
+            if (j < static_cast<int>(cnt)) {
+                const uint8_t* a_src = a_lane ? xs[wave][j] + slot + 16 * (r & 3) : zero;
+#pragma unroll
+                for (int m = 0; m < NM; ++m) acc[j][m] = F::unit(wu[m], a_src, xs[wave][j] + slot + 48, r, s, acc[j][m]);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int j = 0; j < VB; ++j) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            float v = acc[j][m];
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            if (lane < 16) part[wave][j][m][lane] = v;
+        }
+    }
+    __syncthreads();
+    if (tid < 16 * cnt) {
+        const uint32_t j = tid / 16, rr = tid % 16, row = tile * 16 + rr;
+        float v = part[0][j][0][rr];
+#pragma unroll
+        for (int i = 1; i < WPB; ++i) v += part[i][j][0][rr];
+        if (MODE == 1) {
+            float g2 = part[0][j][NM - 1][rr];
+#pragma unroll
+            for (int i = 1; i < WPB; ++i) g2 += part[i][j][NM - 1][rr];
+            v = row < n ? silu_mul(v, g2) : 0.0f;
+            outs[j][rr] = v;
+        }
+        if (row < n) y[static_cast<size_t>(order[first + j]) * ldy + row] = v;
+    }
+    if (MODE == 1 && yq) {
+        __syncthreads();
+        if (tid < cnt && tile * 16 < n) {
+            xgroup_encode_from(outs[tid], yq + static_cast<size_t>(order[first + tid]) * (ldy / 16) + tile);
+        }
+    }
+}
+
+int launch_x16_grouped(uint32_t type, const void* packed, const void* packed2, const XGroup* xq, size_t ldx,
+                       int x_routed, size_t routes, float* y, XGroup* yq, size_t ldy, size_t n, size_t k,
+                       size_t experts, const int32_t* order, const int32_t* groups, const uint32_t* ngroups,
+                       size_t max_groups, hipStream_t stream) {
+    if (type != kQ4_K && type != kQ6_K) return kInvalidArgument;
+    int rc = check_x16(type, packed, xq, y, n, k);
+    if (rc == kOk && packed2) rc = check_x16(type, packed2, xq, y, n, k);
+    if (rc != kOk) return rc;
+    if (n % 16 != 0 || experts == 0 || routes == 0 || !order || !groups || !ngroups || max_groups == 0 ||
+        ldx % 16 != 0 || ldx < k || ldy < n) {
+        return kInvalidArgument;
+    }
+    if (yq && (!packed2 || ldy % 16 != 0 || reinterpret_cast<uintptr_t>(yq) % 16 != 0)) return kInvalidArgument;
+    if (max_groups > 65535 || experts > 0xffffffffull || ldx > 0xffffffffull || ldy > 0xffffffffull) {
+        return kLengthError;
+    }
+    const size_t expert_bytes = x16_bytes(type, n, k);
+    const dim3 grid(static_cast<uint32_t>(n / 16), static_cast<uint32_t>(max_groups));
+    const auto* wp = static_cast<const uint8_t*>(packed);
+    const auto* wp2 = static_cast<const uint8_t*>(packed2);
+    const uint32_t E = static_cast<uint32_t>(experts), lx = static_cast<uint32_t>(ldx), xr = x_routed ? 1u : 0u,
+                   R = static_cast<uint32_t>(routes), ly = static_cast<uint32_t>(ldy), nn = static_cast<uint32_t>(n),
+                   units = static_cast<uint32_t>(k / 256);
+#define HIPLLM_X16G(QT, M)                                                                                          \
+    HIPLLM_LAUNCH((x16_grouped_kernel<QT, M>), grid, dim3(256), 0, stream, wp, wp2, expert_bytes, E, xq, lx, xr, R, y, \
+                  yq, ly, nn, units, order, groups, ngroups)
+    if (type == kQ4_K) {
+        if (packed2) {
+            HIPLLM_X16G(kQ4_K, 1);
+        } else {
+            HIPLLM_X16G(kQ4_K, 0);
+        }
+    } else {
+        if (packed2) {
+            HIPLLM_X16G(kQ6_K, 1);
+        } else {
+            HIPLLM_X16G(kQ6_K, 0);
+        }
+    }
+#undef HIPLLM_X16G
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+}
+
 // Routed expert gate/up + SwiGLU with the routes chosen in every block's
 // prologue (Batch, ROUTE): 16-row blocks, 2 rows x 4 octets, or 4 x 8 from
 // 8192 rows on.

@@ -130,6 +130,16 @@ int launch_gemv_x16_pair(uint32_t type_a, const void* packed_a, size_t n_a, floa
                          const void* packed_b, size_t n_b, float* y_b, size_t k, const float* x, const float* gamma,
                          float eps, const float* conv_w, float* history, size_t ksize, hipStream_t stream,
                          const XGroup* xq = nullptr, const double* sumsq = nullptr);
+// Routed expert vectors grouped by expert (launch_route_groups with vmax <=
+// kX16GroupRows): each expert tile of the x16 copy of the whole [experts *
+// n, k] block is read once per group and multiplied by every vector of it;
+// vector index v reads input row v (x_routed) or v / routes and writes row
+// v of y. packed2: the SwiGLU pair, yq (nullable) its XGroup form.
+constexpr uint32_t kX16GroupRows = 4;
+int launch_x16_grouped(uint32_t type, const void* packed, const void* packed2, const XGroup* xq, size_t ldx,
+                       int x_routed, size_t routes, float* y, XGroup* yq, size_t ldy, size_t n, size_t k,
+                       size_t experts, const int32_t* order, const int32_t* groups, const uint32_t* ngroups,
+                       size_t max_groups, hipStream_t stream);
 // One token's routed down projections (route j: expert ids[j]'s rows of the
 // x16 copy of the whole [experts * n, k_r] down block times XGroup row j of
 // xq), the shared expert's down projection (x16 copy, FP32 input sx of k_s

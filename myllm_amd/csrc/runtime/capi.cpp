@@ -246,6 +246,16 @@ int hipllm_gemv_x16_swiglu(uint32_t type, const void* gate, const void* up, cons
                   "launch failure");
 }
 
+int hipllm_gemv_x16_grouped(uint32_t type, const void* packed, const void* packed2, const void* xq, size_t ldx,
+                            int x_routed, size_t routes, float* y, void* yq, size_t ldy, size_t n, size_t k,
+                            size_t experts, const int32_t* order, const int32_t* groups, const uint32_t* ngroups,
+                            size_t max_groups, void* stream) {
+    return status(hipllm::launch_x16_grouped(type, packed, packed2, xgc(xq), ldx, x_routed, routes, y, xg(yq), ldy, n,
+                                             k, experts, order, groups, ngroups, max_groups, as_stream(stream)),
+                  "hipllm_gemv_x16_grouped: invalid arguments (Q4_K or Q6_K, k % 256 == 0, n % 16 == 0, 16-byte "
+                  "aligned buffers, max_groups <= 65535) or launch failure");
+}
+
 int hipllm_gemv_x16_moe_down(uint32_t type_r, const void* down_packed, const int32_t* ids, size_t experts,
                              const void* xq, size_t ldx, size_t k_r, uint32_t type_s, const void* shared_packed,
                              const float* sx, size_t k_s, const float* weights, const float* sgate,

@@ -608,7 +608,8 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
                       o_ids = reserve(n), o_tok = reserve(16), o_step = reserve(4),
                       o_shg = reserve(n * FFs), o_xb = reserve((n * std::max({H, inner, q_w, FFs}) + 1) / 2),
                       o_ord = reserve(n * K),
-                      o_grp = reserve(2 * hipllm::route_groups_max(n * K, E, hipllm::kGatherRows)),
+                      o_grp = reserve(2 * std::max(hipllm::route_groups_max(n * K, E, hipllm::kGatherRows),
+                                                   hipllm::route_groups_max(n * K, E, hipllm::kX16GroupRows))),
                       o_ngr = reserve(1), o_gact = reserve(n * K * FF), o_actb = reserve((n * K * FF + 1) / 2),
                       o_xs = reserve(n), o_abs = reserve(n * K),
                       o_mms = reserve(mm_floats), o_split = reserve(split_bytes / 4), o_inq = reserve(H),
@@ -998,6 +999,12 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
     // Routed experts: gate/up + SwiGLU (and its XGroup form) for every
     // (row, route), then down.
     const bool x16_experts = rows == 1 && E <= 256 && K <= 8 && L.gate_exps.x16 && L.up_exps.x16 && L.down_exps.x16;
+    // Prompts below the gathered-matmul threshold: the expert-grouped x16
+    // products (the vector form reads an expert's weights once per vector).
+    const bool x16_grouped = rows > 1 && !x16_experts && !route_in_gemv && !gathered_experts(L, rows, xb) &&
+                             L.gate_exps.x16 && L.up_exps.x16 && L.down_exps.x16 && L.gate_exps.type == L.up_exps.type &&
+                             FF % 16 == 0 && H % 16 == 0;
+    const std::size_t x16_groups = hipllm::route_groups_max(rows * K, E, hipllm::kX16GroupRows);
     if (x16_experts) {
         // One token: the expert gate / up pair on the x16 copies, with the
         // top-k in the kernel when the grouped launch left it to the experts
@@ -1035,6 +1042,17 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
         launch_check(hipllm::launch_to_f16(act.act, FF, act.act_b, act.act_bscale, nv, FF, stream),
                      "expert fp16 activations");
         gather(L.down_exps, act.act_b, act.act_bscale, act.down, H, FF, 1, "expert down (matmul)");
+    } else if (x16_grouped) {
+        // A short prompt: the routed vectors grouped by expert (at most four
+        // per group) and each expert tile of the x16 copies read once per
+        // group, gate / up with SwiGLU, then down.
+        launch_check(hipllm::launch_route_groups(ids, rows * K, E, hipllm::kX16GroupRows, act.route_order,
+                                                 act.route_groups, act.route_ngroups, stream),
+                     "route groups");
+        launch_check(hipllm::launch_x16_grouped(L.gate_exps.type, L.gate_exps.x16, L.up_exps.x16, act.normq, H, 0, K,
+                                                act.act, act.actq, FF, FF, H, E, act.route_order, act.route_groups,
+                                                act.route_ngroups, x16_groups, stream),
+                     "expert gate/up (x16, grouped)");
     } else {
         launch_check(hipllm::launch_gemv_batched(L.gate_exps.type, L.gate_exps.ptr, L.up_exps.ptr,
                                                  L.gate_exps.row_bytes, act.norm, act.normq, nullptr, nullptr,
@@ -1069,6 +1087,11 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
                                                     act.down, nullptr, H, H, FF, E, K, ids, nullptr, nullptr, nullptr,
                                                     0, stream),
                      "expert down");
+    } else if (x16_grouped) {
+        launch_check(hipllm::launch_x16_grouped(L.down_exps.type, L.down_exps.x16, nullptr, act.actq, FF, 1, K,
+                                                act.down, nullptr, H, H, FF, E, act.route_order, act.route_groups,
+                                                act.route_ngroups, x16_groups, stream),
+                     "expert down (x16, grouped)");
     } else if (!gathered_experts(L, rows, xb)) {
         launch_check(hipllm::launch_gemv_batched(L.down_exps.type, L.down_exps.ptr, nullptr, L.down_exps.row_bytes,
                                                  act.act, act.actq, nullptr, nullptr, act.down, nullptr, H, FF,

@@ -137,6 +137,7 @@ SIGNATURES = {
                                    _S, _F, _P]),
     "hipllm_gdn_decode": (_I, [_P, _P, _P, _P, _S, _P, _P, _P, _P, _P, _P, _P, _S, _S, _S, _F, _P]),
     "hipllm_attn_decode_qgate": (_I, [_P, _P, _P, _P, _F, _P, _S, _P, _P, _P, _P, _S, _S, _S, _S, _F, _P]),
+    "hipllm_gemv_x16_grouped": (_I, [_U32, _P, _P, _P, _S, _I, _S, _P, _P, _S, _S, _S, _S, _P, _P, _P, _S, _P]),
     "hipllm_gemv_x16_pair": (_I, [_U32, _P, _S, _P, _U32, _P, _S, _P, _S, _P, _P, _F, _P, _P, _S, _P, _P, _P]),
     "hipllm_gemv_x16_moe_down": (_I, [_U32, _P, _P, _S, _P, _S, _S, _U32, _P, _P, _S, _P, _P, _P, _P, _S, _S, _P,
                                       _P]),
@@ -598,6 +599,13 @@ def _k_gemv_x16_routed(qtype, packed, packed2, xq, ldx, x_routed, y, yq, ldy, n,
                                        _ptr(ids_out), _ptr(weights_out), waves, _stream(stream)))
 
 
+def _k_gemv_x16_grouped(qtype, packed, packed2, xq, ldx, x_routed, routes, y, yq, ldy, n, k, experts, order, groups,
+                        ngroups, max_groups, stream=None):
+    check(lib().hipllm_gemv_x16_grouped(qtype, _ptr(packed), _ptr(packed2), _ptr(xq), ldx, int(bool(x_routed)), routes,
+                                        _ptr(y), _ptr(yq), ldy, n, k, experts, _ptr(order), _ptr(groups), _ptr(ngroups),
+                                        max_groups, _stream(stream)))
+
+
 def _k_gemv_x16_moe_down(type_r, down_packed, ids, experts, xq, ldx, k_r, type_s, shared_packed, sx, k_s, weights,
                          sgate, residual, y, n, routes, norm_out=None, stream=None):
     check(lib().hipllm_gemv_x16_moe_down(type_r, _ptr(down_packed), _ptr(ids), experts, _ptr(xq), ldx, k_r, type_s,
@@ -847,7 +855,7 @@ kernels = types.SimpleNamespace(
     gdn_scan_chunked=_k_gdn_scan_chunked,
     gdn_chunk_scratch_floats=lambda t, h: lib().hipllm_gdn_chunk_scratch_floats(t, h),
     conv_l2norm=_k_conv_l2norm, gdn_scan_gated=_k_gdn_scan_gated, gdn_decode=_k_gdn_decode,
-    gemv_x16_pair=_k_gemv_x16_pair, attn_decode_qgate=_k_attn_decode_qgate, gemv_x16_moe_down=_k_gemv_x16_moe_down,
+    gemv_x16_pair=_k_gemv_x16_pair, gemv_x16_grouped=_k_gemv_x16_grouped, attn_decode_qgate=_k_attn_decode_qgate, gemv_x16_moe_down=_k_gemv_x16_moe_down,
     split_qgate_norm=_k_split_qgate_norm, gate_mul=_k_gate_mul,
     gemv_workspace_bytes=lambda k: lib().hipllm_gemv_workspace_bytes(k),
     attn_decode_scratch_floats=lambda hq, d, n: lib().hipllm_attn_decode_scratch_floats(hq, d, n),

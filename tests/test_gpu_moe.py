@@ -276,6 +276,61 @@ def test_gemv_x16_moe_down_rejects_bad_arguments(cuda):
             kernels.gemv_x16_moe_down(*args)
 
 
+@pytest.mark.parametrize("qtype,E,K,T,n,kdim", [(synth.Q4_K, 32, 8, 5, 64, 512), (synth.Q6_K, 8, 4, 9, 48, 768),
+                                                 (synth.Q4_K, 64, 8, 12, 512, 2048)])
+def test_gemv_x16_grouped_matches_batched(cuda, qtype, E, K, T, n, kdim):
+    """Expert-grouped x16 products of a prompt (groups of at most four
+    vectors) against the batched vector GEMV by the same ids on the GGUF rows:
+    gate / up with SwiGLU (outputs within 1e-6, XGroup form), then down from
+    the routed SwiGLU outputs (within 1e-6)."""
+    rng = np.random.default_rng(T + n)
+    wg, wu = random_rows(qtype, E * n, kdim, 81), random_rows(qtype, E * n, kdim, 82)
+    wd = random_rows(qtype, E * kdim, n, 83) if n % 256 == 0 else None
+
+    def pack(w, rows, cols):
+        p = torch.empty(kernels.x16_bytes(qtype, rows, cols), dtype=torch.uint8, device=cuda)
+        kernels.pack_x16(qtype, dev_bytes(w, cuda), w.shape[1], rows, cols, p)
+        return p
+
+    pg, pu = pack(wg, E * n, kdim), pack(wu, E * n, kdim)
+    x = rng.normal(size=(T, kdim)).astype(np.float32)
+    dx = t32(x, cuda)
+    xq = xgroup.buffer(torch, kdim, cuda, T)
+    for t in range(T):
+        kernels.prep_x(dx[t], xq[t * kdim:(t + 1) * kdim], kdim)
+    ids_np = rng.integers(0, E, size=(T, K)).astype(np.int32)
+    ids_np[1, :] = ids_np[0, :]  # experts shared by two tokens
+    ids = torch.from_numpy(ids_np.reshape(-1).copy()).to(cuda)
+    nv = T * K
+    mg = kernels.route_groups_max(nv, E, 4)
+    order = torch.empty(nv, dtype=torch.int32, device=cuda)
+    groups = torch.empty(2 * mg, dtype=torch.int32, device=cuda)
+    ngroups = torch.empty(1, dtype=torch.int32, device=cuda)
+    kernels.route_groups(ids, nv, E, 4, order, groups, ngroups)
+    y = torch.empty(nv, n, device=cuda)
+    yq = xgroup.buffer(torch, n, cuda, nv)
+    kernels.gemv_x16_grouped(qtype, pg, pu, xq, kdim, False, K, y, yq, n, n, kdim, E, order, groups, ngroups, mg)
+    y_ref = torch.empty(nv, n, device=cuda)
+    yq_ref = xgroup.buffer(torch, n, cuda, nv)
+    kernels.gemv_batched(qtype, dev_bytes(wg, cuda), dev_bytes(wu, cuda), wg.shape[1], dx, xq, None, None, y_ref,
+                         yq_ref, n, kdim, nv, ids=ids, experts=E, routes=K, expert_stride=n * wg.shape[1],
+                         x_routed=False, ldx=kdim, ldy=n)
+    got = y.cpu().numpy()
+    assert rel_err(got, y_ref.cpu().numpy()) <= 1e-6
+    for v in range(nv):
+        xgroup.check(yq[v * n:(v + 1) * n], got[v])
+    if wd is None:
+        return
+    pd = pack(wd, E * kdim, n)
+    d = torch.empty(nv, kdim, device=cuda)
+    kernels.gemv_x16_grouped(qtype, pd, None, yq, n, True, K, d, None, kdim, kdim, n, E, order, groups, ngroups, mg)
+    d_ref = torch.empty(nv, kdim, device=cuda)
+    kernels.gemv_batched(qtype, dev_bytes(wd, cuda), None, wd.shape[1], y, yq, None, None, d_ref, None, kdim, n, nv,
+                         ids=ids, experts=E, routes=K, expert_stride=kdim * wd.shape[1], x_routed=True, ldx=n,
+                         ldy=kdim)
+    assert rel_err(d.cpu().numpy(), d_ref.cpu().numpy()) <= 1e-6
+
+
 def test_gemv_routed_swiglu_rejects_bad_arguments(cuda):
     w = torch.zeros(272 * 64, dtype=torch.uint8, device=cuda)
     x = torch.zeros(256, device=cuda)
