@@ -2305,19 +2305,20 @@ int launch_x16_moe_down(uint32_t type_r, const void* down_x16, const int32_t* id
 // reads its expert's 16-row tile of the x16 copy of the whole expert block
 // once and multiplies it by every vector of the group. Vector j of the group
 // is routed vector order[first + j] (its input row: that index when
-// x_routed, else the index / routes; its output row: that index). 4 waves
-// split the units; per unit a wave loads the weights (both matrices for the
+// x_routed, else the index / routes; its output row: that index). WPB waves
+// (4, or 2 for rows of at most two units) split the units; per unit a wave
+// loads the weights (both matrices for the
 // SwiGLU pair) and each vector's 1 KiB of input groups, then runs the
 // unit's MFMAs for each vector from its own LDS slot. MODE 0: y = W x;
 // MODE 1: y = silu(Wg x) * (Wu x) and yq its XGroup form (one group per
 // tile). Groups past *ngroups exit at once.
-template <uint32_t QT, int MODE>
-__global__ __launch_bounds__(256) void x16_grouped_kernel(
+template <uint32_t QT, int MODE, int WPB>
+__global__ __launch_bounds__(64 * WPB) void x16_grouped_kernel(
     const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, size_t expert_bytes, uint32_t experts,
     const XGroup* __restrict__ xq, uint32_t ldx, uint32_t x_routed, uint32_t routes, float* __restrict__ y,
     XGroup* __restrict__ yq, uint32_t ldy, uint32_t n, uint32_t units, const int32_t* __restrict__ order,
     const int32_t* __restrict__ groups, const uint32_t* __restrict__ ngroups) {
-    constexpr int WPB = 4, VB = kX16GroupRows, NM = MODE == 1 ? 2 : 1;
+    constexpr int VB = kX16GroupRows, NM = MODE == 1 ? 2 : 1;
     using F = X16<QT>;
     constexpr uint32_t kTileUnit = 16 * F::kBlock;
     if (blockIdx.y >= *ngroups) return;
@@ -2430,8 +2431,13 @@ int launch_x16_grouped(uint32_t type, const void* packed, const void* packed2, c
                    R = static_cast<uint32_t>(routes), ly = static_cast<uint32_t>(ldy), nn = static_cast<uint32_t>(n),
                    units = static_cast<uint32_t>(k / 256);
 #define HIPLLM_X16G(QT, M)                                                                                          \
-    HIPLLM_LAUNCH((x16_grouped_kernel<QT, M>), grid, dim3(256), 0, stream, wp, wp2, expert_bytes, E, xq, lx, xr, R, y, \
-                  yq, ly, nn, units, order, groups, ngroups)
+    if (units <= 2) {                                                                                               \
+        HIPLLM_LAUNCH((x16_grouped_kernel<QT, M, 2>), grid, dim3(128), 0, stream, wp, wp2, expert_bytes, E, xq, lx, xr, \
+                      R, y, yq, ly, nn, units, order, groups, ngroups);                                              \
+    } else {                                                                                                        \
+        HIPLLM_LAUNCH((x16_grouped_kernel<QT, M, 4>), grid, dim3(256), 0, stream, wp, wp2, expert_bytes, E, xq, lx, xr, \
+                      R, y, yq, ly, nn, units, order, groups, ngroups);                                              \
+    }
     if (type == kQ4_K) {
         if (packed2) {
             HIPLLM_X16G(kQ4_K, 1);
