@@ -302,6 +302,20 @@ int hipllm_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m,
 int hipllm_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xh, const float* xscale,
                      const float* bias, const float* residual, float* y, size_t m, size_t n, size_t k, int tile,
                      int splits, void* workspace, size_t workspace_bytes, void* stream);
+/* The FFN gate / up matmuls of a prompt and their SwiGLU in three launches
+ * instead of six: y[m, n] = silu(X Wg^T) * (X Wu^T) (the sign-branched SwiGLU
+ * of cpu_llm.cpp:188-202) with X as for hipllm_gemm_mfma, Wg / Wu of one type
+ * (Q4_K, Q6_K, Q8_0 or Q5_0) and the default tile and K split; both products'
+ * partial planes go to `workspace` (16-byte aligned, at least
+ * hipllm_gemm_swiglu_workspace_bytes(m, n, k) bytes) and one launch adds each
+ * product's planes in split order and applies the SwiGLU: the same bits as
+ * two hipllm_gemm_mfma calls and hipllm_swiglu. Replaces the gate / up GEMMs
+ * and SwiGLU of cpu_prefill_layer (cpu_llm.cpp:774-841). */
+size_t hipllm_gemm_swiglu_workspace_bytes(size_t m, size_t n, size_t k);
+int hipllm_gemm_mfma_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const void* xh,
+                            const float* xscale, float* y, size_t m, size_t n, size_t k, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
 /* Workspace bytes hipllm_gemm_mfma's K split takes for this shape, tile and
  * splits request (0: it runs unsplit). */
 size_t hipllm_gemm_mfma_workspace_bytes(size_t m, size_t n, size_t k, int tile, int splits);

@@ -169,6 +169,15 @@ int launch_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m,
 // Bytes of the K-split partial planes launch_gemm_mfma uses for this shape
 // (0 when it runs unsplit).
 size_t gemm_split_bytes(size_t m, size_t n, size_t k, int tile, int splits);
+// The FFN gate / up matmuls of a prompt (weights of one type, Q4_K / Q6_K /
+// Q8_0 / Q5_0) and their SwiGLU: y = silu(X Wg^T) * (X Wu^T), the default
+// tile and K split, both products' partial planes in ws (at least
+// gemm_swiglu_bytes(m, n, k) bytes, 16-byte aligned) and one launch adding
+// them in split order and applying the SwiGLU.
+size_t gemm_swiglu_bytes(size_t m, size_t n, size_t k);
+int launch_gemm_mfma_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const void* xb,
+                            const float* xscale, float* y, size_t m, size_t n, size_t k, size_t ldy, void* ws,
+                            size_t ws_bytes, hipStream_t stream);
 // With a K split the partial sums go to split_ws (gemm_split_bytes, 16-byte
 // aligned) and are added in split order by a second launch; without enough
 // workspace the default split runs unsplit and an explicit one is rejected.

@@ -765,13 +765,13 @@ void launch_split_reduce(const float* part, uint32_t splits, const float* bias, 
 template <uint32_t T, int NSUB, int MSUB>
 void launch_tile(const void* w, size_t row_bytes, const _Float16* xb, const float* xscale, const float* bias,
                  const float* residual, float* y, uint32_t m, uint32_t n, uint32_t k, uint32_t ldy, uint32_t splits,
-                 uint32_t per, float* part, hipStream_t stream) {
+                 uint32_t per, float* part, hipStream_t stream, bool reduce = true) {
     constexpr uint32_t BN = 4 * 32 * NSUB, BM = 32 * MSUB;
     const dim3 grid(((n + BN - 1) / BN) * ((m + BM - 1) / BM), 1, splits);
     if (splits > 1) {
         HIPLLM_LAUNCH((gemm_mfma_kernel<T, NSUB, MSUB>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w),
                       row_bytes, xb, xscale, nullptr, nullptr, part, m, n, k, n, per);
-        launch_split_reduce(part, splits, bias, residual, y, m, n, ldy, stream);
+        if (reduce) launch_split_reduce(part, splits, bias, residual, y, m, n, ldy, stream);
     } else {
         HIPLLM_LAUNCH((gemm_mfma_kernel<T, NSUB, MSUB>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w),
                       row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, per);
@@ -792,13 +792,13 @@ void launch_gather(const void* w, size_t row_bytes, const _Float16* xb, const fl
 template <uint32_t T, int MT>
 void launch_lds(const void* w, size_t row_bytes, const _Float16* xb, const float* xscale, const float* bias,
                 const float* residual, float* y, uint32_t m, uint32_t n, uint32_t k, uint32_t ldy, uint32_t splits,
-                uint32_t per, float* part, hipStream_t stream) {
+                uint32_t per, float* part, hipStream_t stream, bool reduce = true) {
     constexpr uint32_t BN = 128, BM = 128 * MT;
     const dim3 grid(((n + BN - 1) / BN) * ((m + BM - 1) / BM), 1, splits);
     if (splits > 1) {
         HIPLLM_LAUNCH((gemm_lds_kernel<T, MT>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w), row_bytes,
                       xb, xscale, nullptr, nullptr, part, m, n, k, n, per);
-        launch_split_reduce(part, splits, bias, residual, y, m, n, ldy, stream);
+        if (reduce) launch_split_reduce(part, splits, bias, residual, y, m, n, ldy, stream);
     } else {
         HIPLLM_LAUNCH((gemm_lds_kernel<T, MT>), grid, dim3(256), 0, stream, static_cast<const uint8_t*>(w), row_bytes,
                       xb, xscale, bias, residual, y, m, n, k, ldy, per);
@@ -808,15 +808,15 @@ void launch_lds(const void* w, size_t row_bytes, const _Float16* xb, const float
 template <uint32_t T>
 int launch_typed(int tile, const void* w, size_t row_bytes, const _Float16* xb, const float* xscale,
                  const float* bias, const float* residual, float* y, uint32_t m, uint32_t n, uint32_t k, uint32_t ldy,
-                 uint32_t splits, uint32_t per, float* part, hipStream_t stream) {
+                 uint32_t splits, uint32_t per, float* part, hipStream_t stream, bool reduce = true) {
     switch (tile) {
-    case 4: launch_lds<T, 1>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream); break;
-    case 5: launch_lds<T, 2>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream); break;
-    case 0: launch_tile<T, 1, 1>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream); break;
-    case 1: launch_tile<T, 1, 2>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream); break;
-    case 2: launch_tile<T, 2, 2>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream); break;
-    case 3: launch_tile<T, 2, 4>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream); break;
-    case 6: launch_tile<T, 1, 4>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream); break;
+    case 4: launch_lds<T, 1>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream, reduce); break;
+    case 5: launch_lds<T, 2>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream, reduce); break;
+    case 0: launch_tile<T, 1, 1>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream, reduce); break;
+    case 1: launch_tile<T, 1, 2>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream, reduce); break;
+    case 2: launch_tile<T, 2, 2>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream, reduce); break;
+    case 3: launch_tile<T, 2, 4>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream, reduce); break;
+    case 6: launch_tile<T, 1, 4>(w, row_bytes, xb, xscale, bias, residual, y, m, n, k, ldy, splits, per, part, stream, reduce); break;
     default: return kInvalidArgument;
     }
     return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
@@ -932,6 +932,79 @@ int launch_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void*
     case kF16: return launch_typed<kF16>(tile, w, row_bytes, x, xscale, bias, residual, y, M, N, K, LD, S, per, part, stream);
     default: return kInvalidArgument;
     }
+}
+
+// The FFN gate and up matmuls of a prompt and their SwiGLU: both products
+// keep their K-split partial planes (or, unsplit, one plane each) in the
+// workspace, and one launch adds each product's planes in split order and
+// applies the sign-branched SwiGLU (swiglu_kernel's expression), saving the
+// two split reductions' and the SwiGLU launch's passes over the rows.
+__global__ __launch_bounds__(256) void gemm_split_swiglu_kernel(const float* __restrict__ pg,
+                                                                const float* __restrict__ pu, uint32_t splits,
+                                                                float* __restrict__ y, uint32_t m, uint32_t n,
+                                                                uint32_t ldy) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t plane = static_cast<size_t>(m) * n;
+    if (i >= plane) return;
+    float g = pg[i], u = pu[i];
+    for (uint32_t z = 1; z < splits; ++z) {
+        g += pg[z * plane + i];
+        u += pu[z * plane + i];
+    }
+    const float sig = g >= 0.0f ? 1.0f / (1.0f + expf(-g)) : expf(g) / (1.0f + expf(g));
+    y[(i / n) * ldy + i % n] = g * sig * u;
+}
+
+size_t gemm_swiglu_bytes(size_t m, size_t n, size_t k) {
+    if (m == 0 || n == 0 || k < kStepK || m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull) return 0;
+    uint32_t per;
+    const uint32_t M = static_cast<uint32_t>(m), N = static_cast<uint32_t>(n), K = static_cast<uint32_t>(k);
+    const uint32_t s = effective_splits(M, N, K, gemm_default_tile(M, N, K), 0, &per);
+    return 2 * static_cast<size_t>(s) * m * n * sizeof(float);
+}
+
+int launch_gemm_mfma_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const void* xb,
+                            const float* xscale, float* y, size_t m, size_t n, size_t k, size_t ldy, void* ws,
+                            size_t ws_bytes, hipStream_t stream) {
+    if (ldy == 0) ldy = n;
+    if (!wg || !wu || !xb || !xscale || !y || !ws || m == 0 || n == 0 || k == 0 || ldy < n || ldy > 0x7fffffffull ||
+        k % kStepK != 0) {
+        return kInvalidArgument;
+    }
+    if (m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull) return kLengthError;
+    if (type != kQ5_0 && type != kQ8_0 && type != kQ4_K && type != kQ6_K) return kInvalidArgument;
+    if (row_bytes < k / block_elems(type) * block_bytes(type) || row_bytes % 2 != 0) return kInvalidArgument;
+    for (const void* p : {wg, wu}) {
+        if (reinterpret_cast<uintptr_t>(p) % (type == kQ4_K ? 4 : 2) != 0) return kInvalidArgument;
+    }
+    if (type == kQ4_K && row_bytes % 4 != 0) return kInvalidArgument;
+    if (reinterpret_cast<uintptr_t>(xb) % 16 != 0 || reinterpret_cast<uintptr_t>(ws) % 16 != 0) return kInvalidArgument;
+    const size_t need = gemm_swiglu_bytes(m, n, k);
+    if (need == 0 || need > ws_bytes) return kInvalidArgument;
+    const uint32_t M = static_cast<uint32_t>(m), N = static_cast<uint32_t>(n), K = static_cast<uint32_t>(k);
+    const int tile = gemm_default_tile(M, N, K);
+    uint32_t per;
+    const uint32_t S = effective_splits(M, N, K, tile, 0, &per);
+    float* pg = static_cast<float*>(ws);
+    float* pu = pg + static_cast<size_t>(S) * m * n;
+    const auto* x = static_cast<const _Float16*>(xb);
+    // Unsplit, each product writes its one plane as y with ldy = n; split, its planes (no reduce).
+    int rc = kOk;
+    for (int j = 0; j < 2 && rc == kOk; ++j) {
+        const void* w = j == 0 ? wg : wu;
+        float* p = j == 0 ? pg : pu;
+        switch (type) {
+        case kQ4_K: rc = launch_typed<kQ4_K>(tile, w, row_bytes, x, xscale, nullptr, nullptr, p, M, N, K, N, S, per, p, stream, false); break;
+        case kQ6_K: rc = launch_typed<kQ6_K>(tile, w, row_bytes, x, xscale, nullptr, nullptr, p, M, N, K, N, S, per, p, stream, false); break;
+        case kQ8_0: rc = launch_typed<kQ8_0>(tile, w, row_bytes, x, xscale, nullptr, nullptr, p, M, N, K, N, S, per, p, stream, false); break;
+        default: rc = launch_typed<kQ5_0>(tile, w, row_bytes, x, xscale, nullptr, nullptr, p, M, N, K, N, S, per, p, stream, false); break;
+        }
+    }
+    if (rc != kOk) return rc;
+    const size_t total = static_cast<size_t>(m) * n;
+    HIPLLM_LAUNCH(gemm_split_swiglu_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, stream, pg,
+                  pu, S, y, M, N, static_cast<uint32_t>(ldy));
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
 int launch_gemm_gather(uint32_t type, const void* w, size_t row_bytes, const void* xb, const float* xscale, float* y,

@@ -305,6 +305,17 @@ int hipllm_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void*
                   "explicit split) or launch failure");
 }
 
+size_t hipllm_gemm_swiglu_workspace_bytes(size_t m, size_t n, size_t k) { return hipllm::gemm_swiglu_bytes(m, n, k); }
+
+int hipllm_gemm_mfma_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const void* xh,
+                            const float* xscale, float* y, size_t m, size_t n, size_t k, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+    return status(hipllm::launch_gemm_mfma_swiglu(type, wg, wu, row_bytes, xh, xscale, y, m, n, k, n, workspace,
+                                                  workspace_bytes, as_stream(stream)),
+                  "hipllm_gemm_mfma_swiglu: invalid arguments (Q4_K / Q6_K / Q8_0 / Q5_0 weights, k % 128 == 0, a "
+                  "workspace of hipllm_gemm_swiglu_workspace_bytes) or launch failure");
+}
+
 size_t hipllm_gemm_mfma_workspace_bytes(size_t m, size_t n, size_t k, int tile, int splits) {
     return hipllm::gemm_split_bytes(m, n, k, tile, splits);
 }

@@ -646,7 +646,7 @@ void HipLLM::Impl::ensure_prefill_rows(std::size_t n) {
     for (std::size_t m = 1; m <= n; ++m) {
         split_bytes = std::max({split_bytes, hipllm::gemm_split_bytes(m, H + 2 * kv_dim, H, -1, 0),
                                 hipllm::gemm_split_bytes(m, H, H, -1, 0), hipllm::gemm_split_bytes(m, F, H, -1, 0),
-                                hipllm::gemm_split_bytes(m, H, F, -1, 0)});
+                                hipllm::gemm_split_bytes(m, H, F, -1, 0), hipllm::gemm_swiglu_bytes(m, F, H)});
     }
     const std::size_t o_split = reserve(split_bytes);
     pre_bytes = off;
@@ -708,9 +708,20 @@ void HipLLM::Impl::prefill_layer(std::size_t li, std::size_t rows, float* hidden
     gemm(L.o, pre.xb, nullptr, hidden, next_hidden, rows, H);
     launch_check(hipllm::launch_rmsnorm(next_hidden, L.ffn_norm, pre.norm, nullptr, rows, H, eps, stream), "RMSNorm");
     launch_check(hipllm::launch_to_f16(pre.norm, H, pre.xb, pre.xscale, rows, H, stream), "fp16 activations");
-    gemm(L.gate, pre.xb, nullptr, nullptr, pre.gate, rows, F);
-    gemm(L.up, pre.xb, nullptr, nullptr, pre.up, rows, F);
-    launch_check(hipllm::launch_swiglu(pre.gate, pre.up, pre.gate, nullptr, rows * F, stream), "SwiGLU");
+    if (L.gate.type == L.up.type && L.gate.row_bytes == L.up.row_bytes &&
+        (L.gate.type == hipllm::kQ4_K || L.gate.type == hipllm::kQ6_K || L.gate.type == hipllm::kQ8_0 ||
+         L.gate.type == hipllm::kQ5_0)) {
+        // Gate and up keep their partial planes; one launch reduces both and
+        // applies the SwiGLU.
+        launch_check(hipllm::launch_gemm_mfma_swiglu(L.gate.type, L.gate.ptr, L.up.ptr, L.gate.row_bytes, pre.xb,
+                                                     pre.xscale, pre.gate, rows, F, L.gate.cols, F, pre.split,
+                                                     pre.split_bytes, stream),
+                     "prefill gate / up + SwiGLU");
+    } else {
+        gemm(L.gate, pre.xb, nullptr, nullptr, pre.gate, rows, F);
+        gemm(L.up, pre.xb, nullptr, nullptr, pre.up, rows, F);
+        launch_check(hipllm::launch_swiglu(pre.gate, pre.up, pre.gate, nullptr, rows * F, stream), "SwiGLU");
+    }
     launch_check(hipllm::launch_to_f16(pre.gate, F, pre.xb, pre.xscale, rows, F, stream), "fp16 activations");
     gemm(L.down, pre.xb, nullptr, next_hidden, hidden, rows, H);
 }

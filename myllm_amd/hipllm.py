@@ -137,6 +137,8 @@ SIGNATURES = {
                                    _S, _F, _P]),
     "hipllm_gdn_decode": (_I, [_P, _P, _P, _P, _S, _P, _P, _P, _P, _P, _P, _P, _S, _S, _S, _F, _P]),
     "hipllm_attn_decode_qgate": (_I, [_P, _P, _P, _P, _F, _P, _S, _P, _P, _P, _P, _S, _S, _S, _S, _F, _P]),
+    "hipllm_gemm_swiglu_workspace_bytes": (_S, [_S, _S, _S]),
+    "hipllm_gemm_mfma_swiglu": (_I, [_U32, _P, _P, _S, _P, _P, _P, _S, _S, _S, _P, _S, _P]),
     "hipllm_gemv_x16_grouped": (_I, [_U32, _P, _P, _P, _S, _I, _S, _P, _P, _S, _S, _S, _S, _P, _P, _P, _S, _P]),
     "hipllm_gemv_x16_pair": (_I, [_U32, _P, _S, _P, _U32, _P, _S, _P, _S, _P, _P, _F, _P, _P, _S, _P, _P, _P]),
     "hipllm_gemv_x16_moe_down": (_I, [_U32, _P, _P, _S, _P, _S, _S, _U32, _P, _P, _S, _P, _P, _P, _P, _S, _S, _P,
@@ -599,6 +601,16 @@ def _k_gemv_x16_routed(qtype, packed, packed2, xq, ldx, x_routed, y, yq, ldy, n,
                                        _ptr(ids_out), _ptr(weights_out), waves, _stream(stream)))
 
 
+def _k_gemm_mfma_swiglu(qtype, wg, wu, row_bytes, xh, xscale, y, m, n, k, workspace=None, stream=None):
+    if workspace is None:
+        import torch
+        workspace = torch.empty(max(16, lib().hipllm_gemm_swiglu_workspace_bytes(m, n, k)), dtype=torch.uint8,
+                                device=y.device)
+    nbytes = workspace.numel() * workspace.element_size()
+    check(lib().hipllm_gemm_mfma_swiglu(qtype, _ptr(wg), _ptr(wu), row_bytes, _ptr(xh), _ptr(xscale), _ptr(y), m, n, k,
+                                        _ptr(workspace), nbytes, _stream(stream)))
+
+
 def _k_gemv_x16_grouped(qtype, packed, packed2, xq, ldx, x_routed, routes, y, yq, ldy, n, k, experts, order, groups,
                         ngroups, max_groups, stream=None):
     check(lib().hipllm_gemv_x16_grouped(qtype, _ptr(packed), _ptr(packed2), _ptr(xq), ldx, int(bool(x_routed)), routes,
@@ -855,7 +867,7 @@ kernels = types.SimpleNamespace(
     gdn_scan_chunked=_k_gdn_scan_chunked,
     gdn_chunk_scratch_floats=lambda t, h: lib().hipllm_gdn_chunk_scratch_floats(t, h),
     conv_l2norm=_k_conv_l2norm, gdn_scan_gated=_k_gdn_scan_gated, gdn_decode=_k_gdn_decode,
-    gemv_x16_pair=_k_gemv_x16_pair, gemv_x16_grouped=_k_gemv_x16_grouped, attn_decode_qgate=_k_attn_decode_qgate, gemv_x16_moe_down=_k_gemv_x16_moe_down,
+    gemv_x16_pair=_k_gemv_x16_pair, gemv_x16_grouped=_k_gemv_x16_grouped, gemm_mfma_swiglu=_k_gemm_mfma_swiglu, attn_decode_qgate=_k_attn_decode_qgate, gemv_x16_moe_down=_k_gemv_x16_moe_down,
     split_qgate_norm=_k_split_qgate_norm, gate_mul=_k_gate_mul,
     gemv_workspace_bytes=lambda k: lib().hipllm_gemv_workspace_bytes(k),
     attn_decode_scratch_floats=lambda hq, d, n: lib().hipllm_attn_decode_scratch_floats(hq, d, n),

@@ -230,3 +230,40 @@ def test_gemm_rejects_bad_arguments(cuda):
         kernels.gemm_mfma(synth.Q4_K, w, 144, xh, xs, None, None, y, 2, 2, 256, 0, splits=1025)
     with pytest.raises(ValueError):
         kernels.gemm_mfma(synth.Q4_K, w, 144, xh, None, None, None, y, 2, 2, 256)  # no row scales
+
+
+@pytest.mark.parametrize("qtype,m,n,k", [(synth.Q4_K, 128, 4864, 1024), (synth.Q6_K, 45, 1280, 512),
+                                         (synth.Q8_0, 300, 512, 1024), (synth.Q4_K, 1100, 256, 512),
+                                         (synth.Q4_K, 512, 6144, 512), (synth.Q5_0, 64, 512, 256)])
+def test_gemm_swiglu_matches_two_matmuls_and_swiglu(cuda, qtype, m, n, k):
+    """Gate / up matmuls with their SwiGLU in one reduce launch against two
+    hipllm_gemm_mfma calls (default tile and K split) and hipllm_swiglu: the
+    same bits, split (few tiles) and unsplit (many rows)."""
+    wg, wu = random_rows(qtype, n, k, 91), random_rows(qtype, n, k, 92)
+    dg, du = dev_bytes(wg, cuda), dev_bytes(wu, cuda)
+    g = torch.Generator(device="cpu").manual_seed(93)
+    x = torch.randn(m, k, generator=g).to(cuda)
+    xh, xs = to_f16(x, cuda)
+    y = torch.empty(m, n, device=cuda)
+    kernels.gemm_mfma_swiglu(qtype, dg, du, wg.shape[1], xh, xs, y, m, n, k)
+    ga = torch.empty(m, n, device=cuda)
+    ua = torch.empty(m, n, device=cuda)
+    kernels.gemm_mfma(qtype, dg, wg.shape[1], xh, xs, None, None, ga, m, n, k)
+    kernels.gemm_mfma(qtype, du, wu.shape[1], xh, xs, None, None, ua, m, n, k)
+    ref = torch.empty(m, n, device=cuda)
+    kernels.swiglu(ga, ua, ref, None, m * n)
+    assert torch.equal(y.view(torch.int32), ref.view(torch.int32))
+
+
+def test_gemm_swiglu_rejects_bad_arguments(cuda):
+    w = torch.zeros(144 * 64, dtype=torch.uint8, device=cuda)
+    xh = torch.zeros(2, 256, dtype=torch.float16, device=cuda)
+    xs = torch.ones(2, device=cuda)
+    y = torch.zeros(2, 16, device=cuda)
+    small = torch.zeros(16, dtype=torch.uint8, device=cuda)
+    with pytest.raises(ValueError):
+        kernels.gemm_mfma_swiglu(synth.F32, w, w, 144, xh, xs, y, 2, 16, 256)  # quantized weights only
+    with pytest.raises(ValueError):
+        kernels.gemm_mfma_swiglu(synth.Q4_K, w, w, 144, xh, xs, y, 2, 16, 192)  # k % 128
+    with pytest.raises(ValueError):
+        kernels.gemm_mfma_swiglu(synth.Q4_K, w, w, 144, xh, xs, y, 2, 16, 256, workspace=small)  # workspace too small
