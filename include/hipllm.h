@@ -302,6 +302,14 @@ int hipllm_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m,
 int hipllm_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void* xh, const float* xscale,
                      const float* bias, const float* residual, float* y, size_t m, size_t n, size_t k, int tile,
                      int splits, void* workspace, size_t workspace_bytes, void* stream);
+/* hipllm_rmsnorm of `rows` rows (cols contiguous values, cols % 16 == 0,
+ * cols <= 8192; norm receives the normalised rows) and hipllm_to_f16 of its
+ * output (xh, xscale) in one launch, with the same bits as the two.
+ * Replaces the RMSNorm that precedes each prompt GEMM of cpu_prefill_layer
+ * (cpu_llm.cpp:774-841). */
+int hipllm_rmsnorm_f16(const float* x, const float* gamma, float* norm, void* xh, float* xscale, size_t rows,
+                       size_t cols, float eps, void* stream);
+
 /* The FFN gate / up matmuls of a prompt and their SwiGLU in three launches
  * instead of six: y[m, n] = silu(X Wg^T) * (X Wu^T) (the sign-branched SwiGLU
  * of cpu_llm.cpp:188-202) with X as for hipllm_gemm_mfma, Wg / Wu of one type

@@ -166,6 +166,10 @@ int gemm_default_tile(uint32_t m, uint32_t n, uint32_t k);
 uint32_t gemm_default_splits(uint32_t m, uint32_t n, uint32_t k, int tile);
 // X rows as fp16 MFMA operands with a power-of-two scale per row (xscale[m]).
 int launch_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m, size_t k, hipStream_t stream);
+// launch_rmsnorm (rows of k contiguous values, k % 16 == 0, k <= 8192) and
+// launch_to_f16 of its output in one launch, with the same bits.
+int launch_rmsnorm_f16(const float* x, const float* gamma, float* norm, void* xh, float* xscale, size_t m, size_t k,
+                       float eps, hipStream_t stream);
 // Bytes of the K-split partial planes launch_gemm_mfma uses for this shape
 // (0 when it runs unsplit).
 size_t gemm_split_bytes(size_t m, size_t n, size_t k, int tile, int splits);

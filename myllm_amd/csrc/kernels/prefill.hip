@@ -32,6 +32,7 @@
 //   must lie inside the fp16 range (|w| < 65504), as every GGUF block scale
 //   of a trained or synthetic model does by far.
 #include "common.h"
+#include "norm.h"
 
 namespace hipllm {
 
@@ -753,6 +754,59 @@ __global__ __launch_bounds__(256) void to_f16_kernel(const float* __restrict__ x
     }
 }
 
+// A row's RMSNorm and its fp16 operand form in one launch: the norm of
+// rmsnorm_row_groups (norm receives the FP32 row, as the norm kernel writes
+// it), then to_f16_kernel's conversion of that row, each thread converting
+// the 16-value groups it normalised (its own writes, read back), the row's
+// maximum reduced as there: the same bits as the two launches. One block
+// of 256 threads per row; k % 16 == 0 and k <= 8192.
+__global__ __launch_bounds__(256) void rmsnorm_f16_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
+                                                          float* __restrict__ norm, _Float16* __restrict__ xh,
+                                                          float* __restrict__ xscale, uint32_t k, float eps) {
+    const uint32_t r = blockIdx.x, tid = threadIdx.x, groups = k / 16;
+    float* yr = norm + static_cast<size_t>(r) * k;
+    rmsnorm_row_groups(x + static_cast<size_t>(r) * k, gamma, yr, nullptr, k, eps);
+    float v[2][16];
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t g = tid + 256 * j;
+        if (g < groups) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                v[j][i] = yr[16 * g + i];
+                mx = fmaxf(mx, fabsf(v[j][i]));
+            }
+        }
+    }
+    __shared__ float red[4];
+    mx = wave_max(mx);
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e = 0;
+    if (mx > 0.0f && mx <= 3.402823466e38f) {
+        frexpf(mx, &e);  // mx = f 2^e, f in [0.5, 1)
+        e = max(-126, min(127, e - 14));
+    }
+    const float down = ldexpf(1.0f, -e);
+    if (tid == 0) xscale[r] = ldexpf(1.0f, e);
+    _Float16* dst = xh + static_cast<size_t>(r) * k;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t g = tid + 256 * j;
+        if (g < groups) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float* a = v[j] + 8 * h;
+                const u32x4 u = {pack_h2(a[0] * down, a[1] * down), pack_h2(a[2] * down, a[3] * down),
+                                 pack_h2(a[4] * down, a[5] * down), pack_h2(a[6] * down, a[7] * down)};
+                *reinterpret_cast<u32x4*>(dst + 16 * g + 8 * h) = u;
+            }
+        }
+    }
+}
+
 // A K split of `splits` planes of `per` 128-k steps each writes its partial
 // sums to `part` (splits * m * n floats) and one reduce launch adds them.
 void launch_split_reduce(const float* part, uint32_t splits, const float* bias, const float* residual, float* y,
@@ -838,6 +892,21 @@ int gemm_default_tile(uint32_t m, uint32_t, uint32_t k) {
     if (m <= 32) return 0;
     if (k >= 8192) return 4;
     return m >= 1024 ? 6 : 1;
+}
+
+int launch_rmsnorm_f16(const float* x, const float* gamma, float* norm, void* xh, float* xscale, size_t m, size_t k,
+                       float eps, hipStream_t stream) {
+    if (!x || !gamma || !norm || !xh || !xscale || m == 0 || k == 0 || k % 16 != 0 || k > 8192 || !(eps > 0.0f)) {
+        return kInvalidArgument;
+    }
+    for (const void* p : {static_cast<const void*>(x), static_cast<const void*>(gamma), static_cast<const void*>(norm),
+                          static_cast<const void*>(xh)}) {
+        if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return kInvalidArgument;
+    }
+    if (m > 0x7fffffffull) return kLengthError;
+    HIPLLM_LAUNCH(rmsnorm_f16_kernel, dim3(static_cast<uint32_t>(m)), dim3(256), 0, stream, x, gamma, norm,
+                  static_cast<_Float16*>(xh), xscale, static_cast<uint32_t>(k), eps);
+    return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
 }
 
 int launch_to_f16(const float* x, size_t ldx, void* xh, float* xscale, size_t m, size_t k, hipStream_t stream) {

@@ -305,6 +305,13 @@ int hipllm_gemm_mfma(uint32_t type, const void* w, size_t row_bytes, const void*
                   "explicit split) or launch failure");
 }
 
+int hipllm_rmsnorm_f16(const float* x, const float* gamma, float* norm, void* xh, float* xscale, size_t rows,
+                       size_t cols, float eps, void* stream) {
+    return status(hipllm::launch_rmsnorm_f16(x, gamma, norm, xh, xscale, rows, cols, eps, as_stream(stream)),
+                  "hipllm_rmsnorm_f16: invalid arguments (cols % 16 == 0, cols <= 8192, 16-byte aligned buffers, "
+                  "eps > 0) or launch failure");
+}
+
 size_t hipllm_gemm_swiglu_workspace_bytes(size_t m, size_t n, size_t k) { return hipllm::gemm_swiglu_bytes(m, n, k); }
 
 int hipllm_gemm_mfma_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const void* xh,

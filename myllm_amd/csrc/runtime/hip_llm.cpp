@@ -179,6 +179,7 @@ struct HipLLM::Impl {
     void token_step(const std::int32_t* device_id, std::size_t pos, bool head, const std::uint32_t* dpos = nullptr);
     void capture_decode();
     void drop_decode_graph();
+    void norm_f16(const float* x, const float* gamma, std::size_t rows) const;
     void gemm(const DevMatrix& w, const void* xb, const float* bias, const float* residual, float* y,
               std::size_t rows, std::size_t ldy, std::size_t n_override = 0) const;
     void prefill_layer(std::size_t li, std::size_t rows, float* hidden, float* next_hidden);
@@ -671,6 +672,20 @@ bool HipLLM::Impl::batched_shapes() const {
     return config.embedding_size % 128 == 0 && config.feed_forward_size % 128 == 0;
 }
 
+// RMSNorm of `rows` hidden rows into pre.norm and its fp16 operand form
+// (pre.xb, pre.xscale): one launch where the row fits it.
+void HipLLM::Impl::norm_f16(const float* x, const float* gamma, std::size_t rows) const {
+    const std::size_t H = config.embedding_size;
+    const float eps = config.norm_epsilon;
+    if (H % 16 == 0 && H <= 8192) {
+        launch_check(hipllm::launch_rmsnorm_f16(x, gamma, pre.norm, pre.xb, pre.xscale, rows, H, eps, stream),
+                     "RMSNorm + fp16 activations");
+        return;
+    }
+    launch_check(hipllm::launch_rmsnorm(x, gamma, pre.norm, nullptr, rows, H, eps, stream), "RMSNorm");
+    launch_check(hipllm::launch_to_f16(pre.norm, H, pre.xb, pre.xscale, rows, H, stream), "fp16 activations");
+}
+
 void HipLLM::Impl::gemm(const DevMatrix& w, const void* xb, const float* bias, const float* residual, float* y,
                         std::size_t rows, std::size_t ldy, std::size_t n_override) const {
     const std::size_t n = n_override ? n_override : w.rows;
@@ -688,8 +703,7 @@ void HipLLM::Impl::prefill_layer(std::size_t li, std::size_t rows, float* hidden
     const std::size_t H = c.embedding_size, F = c.feed_forward_size;
     const std::size_t qkv_w = H + 2 * kv_dim;
     const float eps = c.norm_epsilon;
-    launch_check(hipllm::launch_rmsnorm(hidden, L.attn_norm, pre.norm, nullptr, rows, H, eps, stream), "RMSNorm");
-    launch_check(hipllm::launch_to_f16(pre.norm, H, pre.xb, pre.xscale, rows, H, stream), "fp16 activations");
+    norm_f16(hidden, L.attn_norm, rows);
     if (L.fused_qkv) {
         gemm(L.q, pre.xb, L.qkv_bias, nullptr, pre.qkv, rows, qkv_w, qkv_w);
     } else {
@@ -706,8 +720,7 @@ void HipLLM::Impl::prefill_layer(std::size_t li, std::size_t rows, float* hidden
                  "prefill attention");
     launch_check(hipllm::launch_to_f16(pre.attn, H, pre.xb, pre.xscale, rows, H, stream), "fp16 activations");
     gemm(L.o, pre.xb, nullptr, hidden, next_hidden, rows, H);
-    launch_check(hipllm::launch_rmsnorm(next_hidden, L.ffn_norm, pre.norm, nullptr, rows, H, eps, stream), "RMSNorm");
-    launch_check(hipllm::launch_to_f16(pre.norm, H, pre.xb, pre.xscale, rows, H, stream), "fp16 activations");
+    norm_f16(next_hidden, L.ffn_norm, rows);
     if (L.gate.type == L.up.type && L.gate.row_bytes == L.up.row_bytes &&
         (L.gate.type == hipllm::kQ4_K || L.gate.type == hipllm::kQ6_K || L.gate.type == hipllm::kQ8_0 ||
          L.gate.type == hipllm::kQ5_0)) {

@@ -137,6 +137,7 @@ SIGNATURES = {
                                    _S, _F, _P]),
     "hipllm_gdn_decode": (_I, [_P, _P, _P, _P, _S, _P, _P, _P, _P, _P, _P, _P, _S, _S, _S, _F, _P]),
     "hipllm_attn_decode_qgate": (_I, [_P, _P, _P, _P, _F, _P, _S, _P, _P, _P, _P, _S, _S, _S, _S, _F, _P]),
+    "hipllm_rmsnorm_f16": (_I, [_P, _P, _P, _P, _P, _S, _S, _F, _P]),
     "hipllm_gemm_swiglu_workspace_bytes": (_S, [_S, _S, _S]),
     "hipllm_gemm_mfma_swiglu": (_I, [_U32, _P, _P, _S, _P, _P, _P, _S, _S, _S, _P, _S, _P]),
     "hipllm_gemv_x16_grouped": (_I, [_U32, _P, _P, _P, _S, _I, _S, _P, _P, _S, _S, _S, _S, _P, _P, _P, _S, _P]),
@@ -601,6 +602,11 @@ def _k_gemv_x16_routed(qtype, packed, packed2, xq, ldx, x_routed, y, yq, ldy, n,
                                        _ptr(ids_out), _ptr(weights_out), waves, _stream(stream)))
 
 
+def _k_rmsnorm_f16(x, gamma, norm, xh, xscale, rows, cols, eps, stream=None):
+    check(lib().hipllm_rmsnorm_f16(_ptr(x), _ptr(gamma), _ptr(norm), _ptr(xh), _ptr(xscale), rows, cols, eps,
+                                   _stream(stream)))
+
+
 def _k_gemm_mfma_swiglu(qtype, wg, wu, row_bytes, xh, xscale, y, m, n, k, workspace=None, stream=None):
     if workspace is None:
         import torch
@@ -867,7 +873,8 @@ kernels = types.SimpleNamespace(
     gdn_scan_chunked=_k_gdn_scan_chunked,
     gdn_chunk_scratch_floats=lambda t, h: lib().hipllm_gdn_chunk_scratch_floats(t, h),
     conv_l2norm=_k_conv_l2norm, gdn_scan_gated=_k_gdn_scan_gated, gdn_decode=_k_gdn_decode,
-    gemv_x16_pair=_k_gemv_x16_pair, gemv_x16_grouped=_k_gemv_x16_grouped, gemm_mfma_swiglu=_k_gemm_mfma_swiglu, attn_decode_qgate=_k_attn_decode_qgate, gemv_x16_moe_down=_k_gemv_x16_moe_down,
+    gemv_x16_pair=_k_gemv_x16_pair, gemv_x16_grouped=_k_gemv_x16_grouped, gemm_mfma_swiglu=_k_gemm_mfma_swiglu,
+    rmsnorm_f16=_k_rmsnorm_f16, attn_decode_qgate=_k_attn_decode_qgate, gemv_x16_moe_down=_k_gemv_x16_moe_down,
     split_qgate_norm=_k_split_qgate_norm, gate_mul=_k_gate_mul,
     gemv_workspace_bytes=lambda k: lib().hipllm_gemv_workspace_bytes(k),
     attn_decode_scratch_floats=lambda hq, d, n: lib().hipllm_attn_decode_scratch_floats(hq, d, n),

@@ -267,3 +267,28 @@ def test_gemm_swiglu_rejects_bad_arguments(cuda):
         kernels.gemm_mfma_swiglu(synth.Q4_K, w, w, 144, xh, xs, y, 2, 16, 192)  # k % 128
     with pytest.raises(ValueError):
         kernels.gemm_mfma_swiglu(synth.Q4_K, w, w, 144, xh, xs, y, 2, 16, 256, workspace=small)  # workspace too small
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 896), (7, 3584), (130, 5120), (3, 8192)])
+def test_rmsnorm_f16_matches_norm_then_f16(cuda, rows, cols):
+    """RMSNorm and the fp16 operand form in one launch against hipllm_rmsnorm
+    followed by hipllm_to_f16: normalised rows, fp16 values and row scales
+    bit for bit (rows of very different magnitudes, one all zero)."""
+    g = torch.Generator(device="cpu").manual_seed(rows + cols)
+    x = torch.randn(rows, cols, generator=g) * torch.exp2(torch.randint(-20, 21, (rows, 1), generator=g).float())
+    if rows > 2:
+        x[1] = 0.0
+    x = x.to(cuda)
+    gamma = torch.randn(cols, generator=g).to(cuda)
+    norm = torch.empty(rows, cols, device=cuda)
+    xh = torch.empty(rows, cols, dtype=torch.float16, device=cuda)
+    xs = torch.empty(rows, device=cuda)
+    kernels.rmsnorm_f16(x, gamma, norm, xh, xs, rows, cols, 1e-6)
+    norm_r = torch.empty(rows, cols, device=cuda)
+    xh_r = torch.empty(rows, cols, dtype=torch.float16, device=cuda)
+    xs_r = torch.empty(rows, device=cuda)
+    kernels.rmsnorm(x, gamma, norm_r, None, rows, cols, 1e-6)
+    kernels.to_f16(norm_r, cols, xh_r, xs_r, rows, cols)
+    assert torch.equal(norm.view(torch.int32), norm_r.view(torch.int32))
+    assert torch.equal(xh.view(torch.int16), xh_r.view(torch.int16))
+    assert torch.equal(xs.view(torch.int32), xs_r.view(torch.int32))
