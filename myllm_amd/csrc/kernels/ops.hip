@@ -698,6 +698,128 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
     if (tid < d) out[static_cast<size_t>(r) * out_stride + h * d + tid] = acc / l_run;
 }
 
+// The same attention for head size D in {64, 128, 256}, tiled over queries:
+// block (tile of QT query rows, head h) keeps the tile's queries in LDS and
+// stages K and V KC keys at a time, so each cache row is read from L2 once per
+// (tile, head) instead of once per (query row, head). Score phase: thread
+// (key j = tid % KC, row group tid / KC) scores RQ rows; the online-softmax
+// max and sum run over the KC lanes of a row with xor shuffles. Output phase:
+// thread (column x = tid % D, row group tid / D) accumulates RP rows. Keys at
+// or past the tile's last position + 1 are staged as zeros, so cache rows
+// beyond the prompt are never read.
+template <uint32_t D, uint32_t QT>
+__global__ __launch_bounds__(256) void attn_prefill_tiled_kernel(const float* __restrict__ q, uint32_t q_stride,
+                                                                 const float* __restrict__ kcache,
+                                                                 const float* __restrict__ vcache,
+                                                                 float* __restrict__ out, uint32_t out_stride,
+                                                                 uint32_t rows, uint32_t hq, uint32_t hkv,
+                                                                 uint32_t pos0, float scale) {
+    constexpr uint32_t KC = 4096 / D > 256 / QT ? 4096 / D : 256 / QT;
+    constexpr uint32_t LDK = D + 4;
+    constexpr uint32_t RQ = QT * KC / 256;
+    constexpr uint32_t GQ = 256 / KC;
+    constexpr uint32_t RP = QT * D / 256;
+    static_assert(KC <= 64 && 64 % KC == 0 && RQ >= 1 && RP >= 1 && (QT * KC) % 256 == 0, "tile shape");
+    __shared__ __align__(16) float qs[QT * LDK];
+    __shared__ __align__(16) float ks[KC * LDK];
+    __shared__ __align__(16) float vs[KC * D];
+    __shared__ __align__(16) float ps[KC * QT];
+    __shared__ float corr[QT];
+    __shared__ float lsum[QT];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t r0 = blockIdx.x * QT, h = blockIdx.y;
+    const uint32_t g = h / (hq / hkv);
+    const uint32_t kvd = hkv * D;
+    const uint32_t nrow = min(QT, rows - r0);
+    const uint32_t kend = pos0 + r0 + nrow;  // keys [0, kend) cover every row of the tile
+    const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t e = tid; e < QT * D / 4; e += 256) {
+        const uint32_t i = e / (D / 4), c = e % (D / 4);
+        float4 v = zero4;
+        if (i < nrow) v = *reinterpret_cast<const float4*>(q + static_cast<size_t>(r0 + i) * q_stride + h * D + 4 * c);
+        *reinterpret_cast<float4*>(qs + i * LDK + 4 * c) = v;
+    }
+    const uint32_t j = tid % KC, ig = tid / KC;
+    const uint32_t x = tid % D, rg = tid / D;
+    float m_run[RQ], l_run[RQ], acc[RP];
+#pragma unroll
+    for (uint32_t m = 0; m < RQ; ++m) {
+        m_run[m] = -INFINITY;
+        l_run[m] = 0.0f;
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < RP; ++r) acc[r] = 0.0f;
+    for (uint32_t c0 = 0; c0 < kend; c0 += KC) {
+        __syncthreads();  // the previous chunk's ks / vs / ps / corr are consumed
+        for (uint32_t e = tid; e < KC * D / 4; e += 256) {
+            const uint32_t jj = e / (D / 4), c = e % (D / 4);
+            float4 kv = zero4, vv = zero4;
+            if (c0 + jj < kend) {
+                const size_t off = static_cast<size_t>(c0 + jj) * kvd + g * D + 4 * c;
+                kv = *reinterpret_cast<const float4*>(kcache + off);
+                vv = *reinterpret_cast<const float4*>(vcache + off);
+            }
+            *reinterpret_cast<float4*>(ks + jj * LDK + 4 * c) = kv;
+            *reinterpret_cast<float4*>(vs + jj * D + 4 * c) = vv;
+        }
+        __syncthreads();
+        float s[RQ];
+#pragma unroll
+        for (uint32_t m = 0; m < RQ; ++m) s[m] = 0.0f;
+#pragma unroll 8
+        for (uint32_t c = 0; c < D / 4; ++c) {
+            const float4 kv = *reinterpret_cast<const float4*>(ks + j * LDK + 4 * c);
+#pragma unroll
+            for (uint32_t m = 0; m < RQ; ++m) {
+                const float4 qv = *reinterpret_cast<const float4*>(qs + (ig + GQ * m) * LDK + 4 * c);
+                s[m] = fmaf(kv.x, qv.x, s[m]);
+                s[m] = fmaf(kv.y, qv.y, s[m]);
+                s[m] = fmaf(kv.z, qv.z, s[m]);
+                s[m] = fmaf(kv.w, qv.w, s[m]);
+            }
+        }
+        const uint32_t t = c0 + j;
+#pragma unroll
+        for (uint32_t m = 0; m < RQ; ++m) {
+            const uint32_t i = ig + GQ * m;
+            // key 0 is valid for every row, so m_new is finite from the first chunk on
+            const float sv = t <= pos0 + r0 + i && t < kend ? s[m] * scale : -INFINITY;
+            float cm = sv;
+#pragma unroll
+            for (uint32_t o = KC / 2; o > 0; o >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o));
+            const float m_new = fmaxf(m_run[m], cm);
+            const float p = expf(sv - m_new);
+            float cs = p;
+#pragma unroll
+            for (uint32_t o = KC / 2; o > 0; o >>= 1) cs += __shfl_xor(cs, o);
+            const float cr = expf(m_run[m] - m_new);
+            l_run[m] = l_run[m] * cr + cs;
+            m_run[m] = m_new;
+            ps[j * QT + i] = p;
+            if (j == 0) corr[i] = cr;
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t r = 0; r < RP; ++r) acc[r] *= corr[rg * RP + r];
+#pragma unroll 4
+        for (uint32_t jj = 0; jj < KC; ++jj) {
+            const float v = vs[jj * D + x];
+#pragma unroll
+            for (uint32_t r = 0; r < RP; ++r) acc[r] = fmaf(ps[jj * QT + rg * RP + r], v, acc[r]);
+        }
+    }
+    if (j == 0) {
+#pragma unroll
+        for (uint32_t m = 0; m < RQ; ++m) lsum[ig + GQ * m] = l_run[m];
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t r = 0; r < RP; ++r) {
+        const uint32_t i = rg * RP + r;
+        if (i < nrow) out[static_cast<size_t>(r0 + i) * out_stride + h * D + x] = acc[r] / lsum[i];
+    }
+}
+
 // ------------------------------------------------------------ argmax
 // Ties resolve to the lower index; NaN never wins (strict '>').
 __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
@@ -993,6 +1115,26 @@ int launch_attn_prefill(const float* q, size_t q_stride, const float* kcache, co
     if (!q || !kcache || !vcache || !out || rows == 0 || hq == 0 || hkv == 0 || hq % hkv) return kInvalidArgument;
     if (d == 0 || d > 256 || d % 4 != 0 || q_stride < hq * d || out_stride < hq * d) return kInvalidArgument;
     if (rows > 0x7fffffffull || hq > 0xffffull || pos0 + rows > 0xffffffffull) return kLengthError;
+    if (d == 64 || d == 128 || d == 256) {
+        // tiles of 16 rows once the grid holds two blocks per CU, else 8
+        const bool wide = d == 256 || (rows + 15) / 16 * hq >= 512;
+        const uint32_t qt = wide ? 16 : 8;
+        const dim3 grid(static_cast<uint32_t>((rows + qt - 1) / qt), static_cast<uint32_t>(hq));
+#define HIPLLM_ATTN_PF(D, QT)                                                                                     \
+    HIPLLM_LAUNCH((attn_prefill_tiled_kernel<D, QT>), grid, dim3(256), 0, stream, q,                            \
+                  static_cast<uint32_t>(q_stride), kcache, vcache, out, static_cast<uint32_t>(out_stride),       \
+                  static_cast<uint32_t>(rows), static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv),            \
+                  static_cast<uint32_t>(pos0), scale)
+        if (d == 64) {
+            if (wide) HIPLLM_ATTN_PF(64, 16); else HIPLLM_ATTN_PF(64, 8);
+        } else if (d == 128) {
+            if (wide) HIPLLM_ATTN_PF(128, 16); else HIPLLM_ATTN_PF(128, 8);
+        } else {
+            HIPLLM_ATTN_PF(256, 16);
+        }
+#undef HIPLLM_ATTN_PF
+        return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+    }
     HIPLLM_LAUNCH(attn_prefill_kernel, dim3(static_cast<uint32_t>(rows), static_cast<uint32_t>(hq)), dim3(256),
                        0, stream, q, static_cast<uint32_t>(q_stride), kcache, vcache, out,
                        static_cast<uint32_t>(out_stride), static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv),

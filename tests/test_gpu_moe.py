@@ -922,6 +922,37 @@ def test_attn_prefill_continues_a_cache(cuda):
     assert rel_err(out.cpu().numpy(), ref) <= 1e-4
 
 
+@pytest.mark.parametrize("hq,hkv,d,pos0,rows", [(28, 4, 128, 0, 37), (28, 4, 128, 3, 300), (14, 2, 64, 0, 21),
+                                                (16, 2, 64, 0, 520), (16, 2, 256, 7, 45), (8, 2, 96, 2, 9)])
+def test_attn_prefill_tiles_match_float64(cuda, hq, hkv, d, pos0, rows):
+    # Query tiles of 8 and 16 rows (the second and fourth cases fill the grid
+    # with 16-row tiles), ragged last tiles, a cache continued from pos0, and
+    # a head size (96) the tiled form does not take. Cache rows past the
+    # prompt hold NaN: the result must not read them.
+    rng = np.random.default_rng(rows + d)
+    cap = pos0 + rows + 20
+    K = rng.normal(size=(cap, hkv * d)).astype(np.float32)
+    V = rng.normal(size=(cap, hkv * d)).astype(np.float32)
+    K[pos0 + rows:] = np.nan
+    V[pos0 + rows:] = np.nan
+    q = rng.normal(size=(rows, hq * d)).astype(np.float32)
+    out = torch.empty(rows, hq * d, device=cuda)
+    scale = 1 / math.sqrt(d)
+    kernels.attn_prefill(t32(q, cuda), hq * d, t32(K, cuda), t32(V, cuda), out, hq * d, rows, hq, hkv, d, pos0, scale)
+    L = pos0 + rows
+    mask = np.arange(L)[None, :] > (pos0 + np.arange(rows))[:, None]
+    ref = np.empty((rows, hq * d))
+    for h in range(hq):
+        g = h // (hq // hkv)
+        kg = K[:L, g * d:(g + 1) * d].astype(np.float64)
+        s = q[:, h * d:(h + 1) * d].astype(np.float64) @ kg.T * scale
+        s[mask] = -np.inf
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        p /= p.sum(axis=1, keepdims=True)
+        ref[:, h * d:(h + 1) * d] = p @ V[:L, g * d:(g + 1) * d].astype(np.float64)
+    assert rel_err(out.cpu().numpy(), ref) <= 1e-4
+
+
 # ------------------------------------------------------------ whole models
 @pytest.fixture(scope="module")
 def moe_tiny(tmp_path_factory):
