@@ -704,9 +704,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
 // (tile, head) instead of once per (query row, head). Score phase: thread
 // (key j = tid % KC, row group tid / KC) scores RQ rows; the online-softmax
 // max and sum run over the KC lanes of a row with xor shuffles. Output phase:
-// thread (column x = tid % D, row group tid / D) accumulates RP rows. Keys at
-// or past the tile's last position + 1 are staged as zeros, so cache rows
-// beyond the prompt are never read.
+// thread (column x = tid % D, row group tid / D) accumulates RP rows (when the
+// tile has fewer scores than threads, row groups past QT idle in the score
+// phase). Keys at or past the tile's last position + 1 are staged as zeros,
+// so cache rows beyond the prompt are never read. Each chunk's K / V loads
+// are issued into registers while the previous chunk is scored.
 template <uint32_t D, uint32_t QT>
 __global__ __launch_bounds__(256) void attn_prefill_tiled_kernel(const float* __restrict__ q, uint32_t q_stride,
                                                                  const float* __restrict__ kcache,
@@ -714,12 +716,14 @@ __global__ __launch_bounds__(256) void attn_prefill_tiled_kernel(const float* __
                                                                  float* __restrict__ out, uint32_t out_stride,
                                                                  uint32_t rows, uint32_t hq, uint32_t hkv,
                                                                  uint32_t pos0, float scale) {
-    constexpr uint32_t KC = 4096 / D > 256 / QT ? 4096 / D : 256 / QT;
+    constexpr uint32_t KC = 4096 / D;  // keys per chunk
     constexpr uint32_t LDK = D + 4;
-    constexpr uint32_t RQ = QT * KC / 256;
-    constexpr uint32_t GQ = 256 / KC;
+    constexpr uint32_t GQ = 256 / KC;  // row groups of the score phase
+    constexpr uint32_t RQ = QT > GQ ? QT / GQ : 1;
     constexpr uint32_t RP = QT * D / 256;
-    static_assert(KC <= 64 && 64 % KC == 0 && RQ >= 1 && RP >= 1 && (QT * KC) % 256 == 0, "tile shape");
+    constexpr uint32_t NL = KC * D / 1024;  // float4 of K (and of V) per thread per chunk
+    static_assert(KC <= 64 && 64 % KC == 0 && RP >= 1 && QT % RQ == 0 && (QT > GQ ? QT % GQ == 0 : GQ % QT == 0),
+                  "tile shape");
     __shared__ __align__(16) float qs[QT * LDK];
     __shared__ __align__(16) float ks[KC * LDK];
     __shared__ __align__(16) float vs[KC * D];
@@ -740,7 +744,24 @@ __global__ __launch_bounds__(256) void attn_prefill_tiled_kernel(const float* __
         *reinterpret_cast<float4*>(qs + i * LDK + 4 * c) = v;
     }
     const uint32_t j = tid % KC, ig = tid / KC;
+    const bool scorer = ig < QT;  // false only for idle row groups (QT < GQ)
     const uint32_t x = tid % D, rg = tid / D;
+    float4 kpre[NL], vpre[NL];
+    auto fetch = [&](uint32_t c0) {
+#pragma unroll
+        for (uint32_t n = 0; n < NL; ++n) {
+            const uint32_t e = tid + 256 * n;
+            const uint32_t jj = e / (D / 4), c = e % (D / 4);
+            kpre[n] = zero4;
+            vpre[n] = zero4;
+            if (c0 + jj < kend) {
+                const size_t off = static_cast<size_t>(c0 + jj) * kvd + g * D + 4 * c;
+                kpre[n] = *reinterpret_cast<const float4*>(kcache + off);
+                vpre[n] = *reinterpret_cast<const float4*>(vcache + off);
+            }
+        }
+    };
+    fetch(0);
     float m_run[RQ], l_run[RQ], acc[RP];
 #pragma unroll
     for (uint32_t m = 0; m < RQ; ++m) {
@@ -751,18 +772,15 @@ __global__ __launch_bounds__(256) void attn_prefill_tiled_kernel(const float* __
     for (uint32_t r = 0; r < RP; ++r) acc[r] = 0.0f;
     for (uint32_t c0 = 0; c0 < kend; c0 += KC) {
         __syncthreads();  // the previous chunk's ks / vs / ps / corr are consumed
-        for (uint32_t e = tid; e < KC * D / 4; e += 256) {
+#pragma unroll
+        for (uint32_t n = 0; n < NL; ++n) {
+            const uint32_t e = tid + 256 * n;
             const uint32_t jj = e / (D / 4), c = e % (D / 4);
-            float4 kv = zero4, vv = zero4;
-            if (c0 + jj < kend) {
-                const size_t off = static_cast<size_t>(c0 + jj) * kvd + g * D + 4 * c;
-                kv = *reinterpret_cast<const float4*>(kcache + off);
-                vv = *reinterpret_cast<const float4*>(vcache + off);
-            }
-            *reinterpret_cast<float4*>(ks + jj * LDK + 4 * c) = kv;
-            *reinterpret_cast<float4*>(vs + jj * D + 4 * c) = vv;
+            *reinterpret_cast<float4*>(ks + jj * LDK + 4 * c) = kpre[n];
+            *reinterpret_cast<float4*>(vs + jj * D + 4 * c) = vpre[n];
         }
         __syncthreads();
+        if (c0 + KC < kend) fetch(c0 + KC);
         float s[RQ];
 #pragma unroll
         for (uint32_t m = 0; m < RQ; ++m) s[m] = 0.0f;
@@ -771,7 +789,7 @@ __global__ __launch_bounds__(256) void attn_prefill_tiled_kernel(const float* __
             const float4 kv = *reinterpret_cast<const float4*>(ks + j * LDK + 4 * c);
 #pragma unroll
             for (uint32_t m = 0; m < RQ; ++m) {
-                const float4 qv = *reinterpret_cast<const float4*>(qs + (ig + GQ * m) * LDK + 4 * c);
+                const float4 qv = *reinterpret_cast<const float4*>(qs + ((ig + GQ * m) % QT) * LDK + 4 * c);
                 s[m] = fmaf(kv.x, qv.x, s[m]);
                 s[m] = fmaf(kv.y, qv.y, s[m]);
                 s[m] = fmaf(kv.z, qv.z, s[m]);
@@ -795,8 +813,10 @@ __global__ __launch_bounds__(256) void attn_prefill_tiled_kernel(const float* __
             const float cr = expf(m_run[m] - m_new);
             l_run[m] = l_run[m] * cr + cs;
             m_run[m] = m_new;
-            ps[j * QT + i] = p;
-            if (j == 0) corr[i] = cr;
+            if (scorer) {
+                ps[j * QT + i] = p;
+                if (j == 0) corr[i] = cr;
+            }
         }
         __syncthreads();
 #pragma unroll
@@ -808,7 +828,7 @@ __global__ __launch_bounds__(256) void attn_prefill_tiled_kernel(const float* __
             for (uint32_t r = 0; r < RP; ++r) acc[r] = fmaf(ps[jj * QT + rg * RP + r], v, acc[r]);
         }
     }
-    if (j == 0) {
+    if (j == 0 && scorer) {
 #pragma unroll
         for (uint32_t m = 0; m < RQ; ++m) lsum[ig + GQ * m] = l_run[m];
     }
@@ -1117,7 +1137,7 @@ int launch_attn_prefill(const float* q, size_t q_stride, const float* kcache, co
     if (rows > 0x7fffffffull || hq > 0xffffull || pos0 + rows > 0xffffffffull) return kLengthError;
     if (d == 64 || d == 128 || d == 256) {
         // tiles of 16 rows once the grid holds two blocks per CU, else 8
-        const bool wide = d == 256 || (rows + 15) / 16 * hq >= 512;
+        const bool wide = (rows + 15) / 16 * hq >= 512;
         const uint32_t qt = wide ? 16 : 8;
         const dim3 grid(static_cast<uint32_t>((rows + qt - 1) / qt), static_cast<uint32_t>(hq));
 #define HIPLLM_ATTN_PF(D, QT)                                                                                     \
@@ -1130,7 +1150,7 @@ int launch_attn_prefill(const float* q, size_t q_stride, const float* kcache, co
         } else if (d == 128) {
             if (wide) HIPLLM_ATTN_PF(128, 16); else HIPLLM_ATTN_PF(128, 8);
         } else {
-            HIPLLM_ATTN_PF(256, 16);
+            if (wide) HIPLLM_ATTN_PF(256, 16); else HIPLLM_ATTN_PF(256, 8);
         }
 #undef HIPLLM_ATTN_PF
         return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;

@@ -923,9 +923,10 @@ def test_attn_prefill_continues_a_cache(cuda):
 
 
 @pytest.mark.parametrize("hq,hkv,d,pos0,rows", [(28, 4, 128, 0, 37), (28, 4, 128, 3, 300), (14, 2, 64, 0, 21),
-                                                (16, 2, 64, 0, 520), (16, 2, 256, 7, 45), (8, 2, 96, 2, 9)])
+                                                (16, 2, 64, 0, 520), (16, 2, 256, 7, 45), (16, 2, 256, 0, 520),
+                                                (8, 2, 96, 2, 9)])
 def test_attn_prefill_tiles_match_float64(cuda, hq, hkv, d, pos0, rows):
-    # Query tiles of 8 and 16 rows (the second and fourth cases fill the grid
+    # Query tiles of 8 and 16 rows (the 300- and 520-row cases fill the grid
     # with 16-row tiles), ragged last tiles, a cache continued from pos0, and
     # a head size (96) the tiled form does not take. Cache rows past the
     # prompt hold NaN: the result must not read them.
