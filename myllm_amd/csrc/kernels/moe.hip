@@ -157,40 +157,51 @@ __global__ __launch_bounds__(1024) void route_groups_kernel(const int32_t* __res
                                                             int32_t* __restrict__ order,
                                                             int32_t* __restrict__ groups,
                                                             uint32_t* __restrict__ ngroups) {
+    // One expert per thread (experts <= kMaxExperts == blockDim.x): the
+    // vector and group offsets are exclusive prefix sums over experts, a
+    // shuffle scan per wave and one over the wave totals.
     __shared__ uint32_t cnt[kMaxExperts];
-    __shared__ uint32_t off[kMaxExperts];
-    __shared__ uint32_t goff[kMaxExperts];
     __shared__ uint32_t cur[kMaxExperts];
-    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) cnt[e] = 0;
+    __shared__ uint32_t wtot[2][kMaxExperts / 64];
+    const uint32_t e = threadIdx.x, lane = e & 63, wave = e >> 6;
+    if (e < experts) cnt[e] = 0;
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
         atomicAdd(&cnt[min(static_cast<uint32_t>(ids[i]), experts - 1)], 1u);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t run = 0, grun = 0;
-        for (uint32_t e = 0; e < experts; ++e) {
-            const uint32_t c = cnt[e];
-            off[e] = run;
-            cur[e] = run;
-            goff[e] = grun;
-            run += c;
-            grun += (c + vmax - 1) / vmax;
+    const uint32_t c = e < experts ? cnt[e] : 0;
+    const uint32_t gc = (c + vmax - 1) / vmax;
+    uint32_t run = c, grun = gc;  // inclusive within the wave
+#pragma unroll
+    for (uint32_t o = 1; o < 64; o <<= 1) {
+        const uint32_t r = __shfl_up(run, o, 64), gr = __shfl_up(grun, o, 64);
+        if (lane >= o) {
+            run += r;
+            grun += gr;
         }
-        *ngroups = grun;
     }
+    if (lane == 63) {
+        wtot[0][wave] = run;
+        wtot[1][wave] = grun;
+    }
+    __syncthreads();
+    uint32_t base = 0, gbase = 0;
+    for (uint32_t w = 0; w < wave; ++w) {
+        base += wtot[0][w];
+        gbase += wtot[1][w];
+    }
+    const uint32_t start = base + run - c, gstart = gbase + grun - gc;
+    if (e < experts) cur[e] = start;
+    if (e == experts - 1) *ngroups = gstart + gc;
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
         const uint32_t slot = atomicAdd(&cur[min(static_cast<uint32_t>(ids[i]), experts - 1)], 1u);
         order[slot] = static_cast<int32_t>(i);
     }
-    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
-        const uint32_t start = off[e], c = cnt[e];
-        for (uint32_t q = 0; q * vmax < c; ++q) {
-            const uint32_t gq = goff[e] + q;
-            groups[2 * gq] = static_cast<int32_t>(start + q * vmax);
-            groups[2 * gq + 1] = static_cast<int32_t>(e | (min(vmax, c - q * vmax) << 16));
-        }
+    for (uint32_t q = 0; q < gc; ++q) {
+        groups[2 * (gstart + q)] = static_cast<int32_t>(start + q * vmax);
+        groups[2 * (gstart + q) + 1] = static_cast<int32_t>(e | (min(vmax, c - q * vmax) << 16));
     }
 }
 

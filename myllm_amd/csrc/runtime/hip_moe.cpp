@@ -587,6 +587,7 @@ void HipMoeLLM::Impl::ensure_rows(std::size_t n) {
         for (const auto& nk : mm_shapes) {
             if (nk[1] % 128 == 0) split_bytes = std::max(split_bytes, hipllm::gemm_split_bytes(r, nk[0], nk[1], -1, 0));
         }
+        if (H % 128 == 0) split_bytes = std::max(split_bytes, hipllm::gemm_swiglu_bytes(r, FFs, H));
     }
     const std::size_t feat = std::max(q_w, inner);
     std::size_t off = 0;
@@ -1099,7 +1100,18 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
                      "expert down");
     }
     // Shared expert (gate/up already in sh_act after a grouped launch).
-    if (!grp && xb) {
+    if (!grp && xb && FFs % 128 == 0 && L.sh_gate.type == L.sh_up.type &&
+        L.sh_gate.row_bytes == L.sh_up.row_bytes &&
+        (L.sh_gate.type == hipllm::kQ4_K || L.sh_gate.type == hipllm::kQ6_K || L.sh_gate.type == hipllm::kQ8_0 ||
+         L.sh_gate.type == hipllm::kQ5_0)) {
+        // Gate and up keep their partial planes; one launch reduces both and
+        // applies the SwiGLU (the down projection below reads fp16 rows of
+        // it, so no XGroup form is needed).
+        launch_check(hipllm::launch_gemm_mfma_swiglu(L.sh_gate.type, L.sh_gate.ptr, L.sh_up.ptr, L.sh_gate.row_bytes,
+                                                     xb, act.xscale, act.sh_act, rows, FFs, H, FFs, act.split,
+                                                     act.split_bytes, stream),
+                     "prefill shared gate / up + SwiGLU");
+    } else if (!grp && xb) {
         proj(L.sh_gate, act.norm, act.normq, H, rows, act.sh_gate, FFs, nullptr, 0, xb);
         proj(L.sh_up, act.norm, act.normq, H, rows, act.sh_act, FFs, nullptr, 0, xb);
         launch_check(hipllm::launch_swiglu(act.sh_gate, act.sh_act, act.sh_act, act.sh_actq, rows * FFs, stream),

@@ -399,7 +399,8 @@ def test_gemv_moe_combine_rejects_bad_arguments(cuda):
         kernels.gemv_moe_combine(synth.Q8_0, w, 34 * 16 * 20, x, x, x, x, x, 8, x, 1, 10240)
 
 
-@pytest.mark.parametrize("n,E,vmax", [(512, 256, 64), (37, 8, 4), (16384, 256, 64), (1, 1, 64), (600, 8, 64)])
+@pytest.mark.parametrize("n,E,vmax", [(512, 256, 64), (37, 8, 4), (16384, 256, 64), (1, 1, 64), (600, 8, 64),
+                                      (3000, 1024, 4), (70, 100, 3)])
 def test_route_groups(cuda, n, E, vmax):
     """The vectors sorted by expert (in any order inside one expert), cut
     into groups of at most vmax vectors of one expert, in expert order."""
