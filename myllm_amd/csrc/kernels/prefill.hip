@@ -890,7 +890,10 @@ int launch_typed(int tile, const void* w, size_t row_bytes, const _Float16* xb, 
 // a single X tile.
 int gemm_default_tile(uint32_t m, uint32_t, uint32_t k) {
     if (m <= 32) return 0;
-    if (k >= 8192) return 4;
+    // Long k (FFN down projections): the 128 x 128 register tile from 256
+    // rows; it measured faster than the shared-dequant tiles at every m
+    // (Q6_K 18944 -> 3584: m 256 136 -> 88 us, m 2048 546 -> 444 us).
+    if (k >= 8192) return m >= 256 ? 6 : 1;
     return m >= 1024 ? 6 : 1;
 }
 
@@ -930,6 +933,12 @@ uint32_t gemm_default_splits(uint32_t m, uint32_t n, uint32_t k, int tile) {
     const uint64_t target = tile == 4 || tile == 5 ? 256 : 512;
     const uint32_t steps = k / kStepK;
     if (blocks >= target * 3 / 4 || steps < 4) return 1;
+    // Long k on the register tiles: as many splits as keep the grid within
+    // 448 blocks (one round of resident blocks; each split plane also costs
+    // the reduce m * n * 8 bytes of traffic).
+    if (k >= 8192 && tile != 4 && tile != 5) {
+        return max(1u, min(static_cast<uint32_t>(448 / blocks), steps / 2));
+    }
     const uint32_t want = static_cast<uint32_t>((target + blocks - 1) / blocks);
     return max(1u, min(want, steps / 2));
 }
