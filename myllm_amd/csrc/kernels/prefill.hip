@@ -888,8 +888,11 @@ int launch_typed(int tile, const void* w, size_t row_bytes, const _Float16* xb, 
 // 394 against 416); for long rows (the down projection, k = 18944) the
 // shared-dequant 128 x 128 tile with a K split is 10-15% faster. 128 x 32 for
 // a single X tile.
-int gemm_default_tile(uint32_t m, uint32_t, uint32_t k) {
-    if (m <= 32) return 0;
+int gemm_default_tile(uint32_t m, uint32_t n, uint32_t k) {
+    // 128 x 32 up to 64 rows of up to 8192 outputs: twice the blocks of
+    // 128 x 64 (Q6_K 2048 -> 8192 at m 64: 25.1 -> 20.7 us); wider
+    // matrices fill the chip either way.
+    if (m <= 32 || (m <= 64 && n <= 8192)) return 0;
     // Long k (FFN down projections): the 128 x 128 register tile from 256
     // rows; it measured faster than the shared-dequant tiles at every m
     // (Q6_K 18944 -> 3584: m 256 136 -> 88 us, m 2048 546 -> 444 us).
