@@ -324,6 +324,14 @@ int hipllm_gemm_mfma_swiglu(uint32_t type, const void* wg, const void* wu, size_
                             const float* xscale, float* y, size_t m, size_t n, size_t k, void* workspace,
                             size_t workspace_bytes, void* stream);
 
+/* hipllm_gemm_mfma_swiglu with the SwiGLU rows written as the next matmul's
+ * operand rows instead of FP32: yh / yscale as hipllm_to_f16 would make them
+ * from y (the same bits; n % 8 == 0, n <= 32768, yh 16-byte aligned). The
+ * down projection's input of cpu_prefill_layer (cpu_llm.cpp:774-841). */
+int hipllm_gemm_mfma_swiglu_f16(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const void* xh,
+                                const float* xscale, void* yh, float* yscale, size_t m, size_t n, size_t k,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
 /* Workspace bytes hipllm_gemm_mfma's K split takes for this shape, tile and
  * splits request (0: it runs unsplit). */
 size_t hipllm_gemm_mfma_workspace_bytes(size_t m, size_t n, size_t k, int tile, int splits);

@@ -179,9 +179,11 @@ size_t gemm_split_bytes(size_t m, size_t n, size_t k, int tile, int splits);
 // gemm_swiglu_bytes(m, n, k) bytes, 16-byte aligned) and one launch adding
 // them in split order and applying the SwiGLU.
 size_t gemm_swiglu_bytes(size_t m, size_t n, size_t k);
+// With yh (and yscale) the SwiGLU rows go out as fp16 operand rows with their
+// scales (to_f16's form; n % 8 == 0, n <= 32768) instead of FP32 y.
 int launch_gemm_mfma_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const void* xb,
                             const float* xscale, float* y, size_t m, size_t n, size_t k, size_t ldy, void* ws,
-                            size_t ws_bytes, hipStream_t stream);
+                            size_t ws_bytes, hipStream_t stream, void* yh = nullptr, float* yscale = nullptr);
 // With a K split the partial sums go to split_ws (gemm_split_bytes, 16-byte
 // aligned) and are added in split order by a second launch; without enough
 // workspace the default split runs unsplit and an explicit one is rejected.

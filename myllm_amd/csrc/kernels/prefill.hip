@@ -1036,6 +1036,75 @@ __global__ __launch_bounds__(256) void gemm_split_swiglu_kernel(const float* __r
     y[(i / n) * ldy + i % n] = g * sig * u;
 }
 
+// gemm_split_swiglu_kernel's row followed by to_f16_kernel's conversion of
+// it, in one launch: block r (1024 threads) forms the n SwiGLU values of row
+// r from the planes as there (8 per thread and group, at most 32 per
+// thread, kept in registers), reduces the row's largest magnitude, and
+// writes the fp16 row and its scale as to_f16_kernel does: the same bits as
+// the two launches, without the FP32 row in memory. n % 8 == 0,
+// n <= kSwigluF16Max.
+constexpr uint32_t kSwigluF16Max = 32768;
+__global__ __launch_bounds__(1024) void gemm_split_swiglu_f16_kernel(const float* __restrict__ pg,
+                                                                     const float* __restrict__ pu, uint32_t splits,
+                                                                     _Float16* __restrict__ yh,
+                                                                     float* __restrict__ yscale, uint32_t m,
+                                                                     uint32_t n) {
+    constexpr uint32_t kGroups = kSwigluF16Max / 8 / 1024;
+    const uint32_t r = blockIdx.x, tid = threadIdx.x;
+    const size_t plane = static_cast<size_t>(m) * n;
+    const size_t row0 = static_cast<size_t>(r) * n;
+    float v[kGroups][8];
+    float mx = 0.0f;
+#pragma unroll
+    for (uint32_t j = 0; j < kGroups; ++j) {
+        const uint32_t c = 8 * (tid + 1024 * j);
+        if (c < n) {
+#pragma unroll
+            for (uint32_t h = 0; h < 2; ++h) {
+                const size_t i = row0 + c + 4 * h;
+                float4 g = *reinterpret_cast<const float4*>(pg + i), u = *reinterpret_cast<const float4*>(pu + i);
+                for (uint32_t z = 1; z < splits; ++z) {
+                    const float4 gz = *reinterpret_cast<const float4*>(pg + z * plane + i);
+                    const float4 uz = *reinterpret_cast<const float4*>(pu + z * plane + i);
+                    g.x += gz.x; g.y += gz.y; g.z += gz.z; g.w += gz.w;
+                    u.x += uz.x; u.y += uz.y; u.z += uz.z; u.w += uz.w;
+                }
+                const float gg[4] = {g.x, g.y, g.z, g.w}, uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (uint32_t q = 0; q < 4; ++q) {
+                    const float a = gg[q];
+                    const float sig = a >= 0.0f ? 1.0f / (1.0f + expf(-a)) : expf(a) / (1.0f + expf(a));
+                    const float y = a * sig * uu[q];
+                    v[j][4 * h + q] = y;
+                    mx = fmaxf(mx, fabsf(y));
+                }
+            }
+        }
+    }
+    __shared__ float red[16];
+    mx = wave_max(mx);
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = red[0];
+    for (uint32_t w = 1; w < 16; ++w) mx = fmaxf(mx, red[w]);
+    int e = 0;
+    if (mx > 0.0f && mx <= 3.402823466e38f) {
+        frexpf(mx, &e);
+        e = max(-126, min(127, e - 14));
+    }
+    const float down = ldexpf(1.0f, -e);
+    if (tid == 0) yscale[r] = ldexpf(1.0f, e);
+#pragma unroll
+    for (uint32_t j = 0; j < kGroups; ++j) {
+        const uint32_t c = 8 * (tid + 1024 * j);
+        if (c < n) {
+            const u32x4 o = {pack_h2(v[j][0] * down, v[j][1] * down), pack_h2(v[j][2] * down, v[j][3] * down),
+                             pack_h2(v[j][4] * down, v[j][5] * down), pack_h2(v[j][6] * down, v[j][7] * down)};
+            *reinterpret_cast<u32x4*>(yh + row0 + c) = o;
+        }
+    }
+}
+
 size_t gemm_swiglu_bytes(size_t m, size_t n, size_t k) {
     if (m == 0 || n == 0 || k < kStepK || m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull) return 0;
     uint32_t per;
@@ -1046,9 +1115,13 @@ size_t gemm_swiglu_bytes(size_t m, size_t n, size_t k) {
 
 int launch_gemm_mfma_swiglu(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const void* xb,
                             const float* xscale, float* y, size_t m, size_t n, size_t k, size_t ldy, void* ws,
-                            size_t ws_bytes, hipStream_t stream) {
+                            size_t ws_bytes, hipStream_t stream, void* yh, float* yscale) {
     if (ldy == 0) ldy = n;
-    if (!wg || !wu || !xb || !xscale || !y || !ws || m == 0 || n == 0 || k == 0 || ldy < n || ldy > 0x7fffffffull ||
+    const bool f16 = yh != nullptr;
+    if (f16 && (!yscale || n % 8 != 0 || n > kSwigluF16Max || reinterpret_cast<uintptr_t>(yh) % 16 != 0)) {
+        return kInvalidArgument;
+    }
+    if (!wg || !wu || !xb || !xscale || (!y && !f16) || !ws || m == 0 || n == 0 || k == 0 || ldy < n || ldy > 0x7fffffffull ||
         k % kStepK != 0) {
         return kInvalidArgument;
     }
@@ -1082,6 +1155,11 @@ int launch_gemm_mfma_swiglu(uint32_t type, const void* wg, const void* wu, size_
         }
     }
     if (rc != kOk) return rc;
+    if (f16) {
+        HIPLLM_LAUNCH(gemm_split_swiglu_f16_kernel, dim3(M), dim3(1024), 0, stream, pg, pu, S,
+                      static_cast<_Float16*>(yh), yscale, M, N);
+        return hipGetLastError() == hipSuccess ? kOk : kRuntimeError;
+    }
     const size_t total = static_cast<size_t>(m) * n;
     HIPLLM_LAUNCH(gemm_split_swiglu_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, stream, pg,
                   pu, S, y, M, N, static_cast<uint32_t>(ldy));

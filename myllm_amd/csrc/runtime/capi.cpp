@@ -323,6 +323,16 @@ int hipllm_gemm_mfma_swiglu(uint32_t type, const void* wg, const void* wu, size_
                   "workspace of hipllm_gemm_swiglu_workspace_bytes) or launch failure");
 }
 
+int hipllm_gemm_mfma_swiglu_f16(uint32_t type, const void* wg, const void* wu, size_t row_bytes, const void* xh,
+                                const float* xscale, void* yh, float* yscale, size_t m, size_t n, size_t k,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+    if (!yh) return status(hipllm::kInvalidArgument, "hipllm_gemm_mfma_swiglu_f16: yh is required");
+    return status(hipllm::launch_gemm_mfma_swiglu(type, wg, wu, row_bytes, xh, xscale, nullptr, m, n, k, n, workspace,
+                                                  workspace_bytes, as_stream(stream), yh, yscale),
+                  "hipllm_gemm_mfma_swiglu_f16: invalid arguments (as hipllm_gemm_mfma_swiglu, and n % 8 == 0, "
+                  "n <= 32768, yh 16-byte aligned, yscale given) or launch failure");
+}
+
 size_t hipllm_gemm_mfma_workspace_bytes(size_t m, size_t n, size_t k, int tile, int splits) {
     return hipllm::gemm_split_bytes(m, n, k, tile, splits);
 }

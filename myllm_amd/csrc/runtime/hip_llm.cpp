@@ -724,18 +724,24 @@ void HipLLM::Impl::prefill_layer(std::size_t li, std::size_t rows, float* hidden
     if (L.gate.type == L.up.type && L.gate.row_bytes == L.up.row_bytes &&
         (L.gate.type == hipllm::kQ4_K || L.gate.type == hipllm::kQ6_K || L.gate.type == hipllm::kQ8_0 ||
          L.gate.type == hipllm::kQ5_0)) {
-        // Gate and up keep their partial planes; one launch reduces both and
-        // applies the SwiGLU.
+        // Gate and up keep their partial planes; one launch reduces both,
+        // applies the SwiGLU and (F % 8 == 0, F <= 32768) writes the down
+        // projection's fp16 rows directly, after the matmuls have read xb.
+        const bool f16 = F % 8 == 0 && F <= 32768;
         launch_check(hipllm::launch_gemm_mfma_swiglu(L.gate.type, L.gate.ptr, L.up.ptr, L.gate.row_bytes, pre.xb,
                                                      pre.xscale, pre.gate, rows, F, L.gate.cols, F, pre.split,
-                                                     pre.split_bytes, stream),
+                                                     pre.split_bytes, stream, f16 ? pre.xb : nullptr,
+                                                     f16 ? pre.xscale : nullptr),
                      "prefill gate / up + SwiGLU");
+        if (!f16) {
+            launch_check(hipllm::launch_to_f16(pre.gate, F, pre.xb, pre.xscale, rows, F, stream), "fp16 activations");
+        }
     } else {
         gemm(L.gate, pre.xb, nullptr, nullptr, pre.gate, rows, F);
         gemm(L.up, pre.xb, nullptr, nullptr, pre.up, rows, F);
         launch_check(hipllm::launch_swiglu(pre.gate, pre.up, pre.gate, nullptr, rows * F, stream), "SwiGLU");
+        launch_check(hipllm::launch_to_f16(pre.gate, F, pre.xb, pre.xscale, rows, F, stream), "fp16 activations");
     }
-    launch_check(hipllm::launch_to_f16(pre.gate, F, pre.xb, pre.xscale, rows, F, stream), "fp16 activations");
     gemm(L.down, pre.xb, nullptr, next_hidden, hidden, rows, H);
 }
 

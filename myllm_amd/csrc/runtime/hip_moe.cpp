@@ -1100,17 +1100,19 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
                      "expert down");
     }
     // Shared expert (gate/up already in sh_act after a grouped launch).
-    if (!grp && xb && FFs % 128 == 0 && L.sh_gate.type == L.sh_up.type &&
+    bool sh_f16 = false;  // the shared activations are already act.xb's fp16 rows
+    if (!grp && xb && FFs % 128 == 0 && FFs <= 32768 && L.sh_gate.type == L.sh_up.type &&
         L.sh_gate.row_bytes == L.sh_up.row_bytes &&
         (L.sh_gate.type == hipllm::kQ4_K || L.sh_gate.type == hipllm::kQ6_K || L.sh_gate.type == hipllm::kQ8_0 ||
          L.sh_gate.type == hipllm::kQ5_0)) {
-        // Gate and up keep their partial planes; one launch reduces both and
-        // applies the SwiGLU (the down projection below reads fp16 rows of
-        // it, so no XGroup form is needed).
+        // Gate and up keep their partial planes; one launch reduces both,
+        // applies the SwiGLU and writes the down projection's fp16 rows into
+        // act.xb (after the matmuls have read it; no FP32 or XGroup form).
         launch_check(hipllm::launch_gemm_mfma_swiglu(L.sh_gate.type, L.sh_gate.ptr, L.sh_up.ptr, L.sh_gate.row_bytes,
-                                                     xb, act.xscale, act.sh_act, rows, FFs, H, FFs, act.split,
-                                                     act.split_bytes, stream),
+                                                     xb, act.xscale, nullptr, rows, FFs, H, FFs, act.split,
+                                                     act.split_bytes, stream, act.xb, act.xscale),
                      "prefill shared gate / up + SwiGLU");
+        sh_f16 = true;
     } else if (!grp && xb) {
         proj(L.sh_gate, act.norm, act.normq, H, rows, act.sh_gate, FFs, nullptr, 0, xb);
         proj(L.sh_up, act.norm, act.normq, H, rows, act.sh_act, FFs, nullptr, 0, xb);
@@ -1142,7 +1144,7 @@ void HipMoeLLM::Impl::moe_layer(std::size_t li, std::size_t rows, float* hidden,
                      "shared down");
     } else {
         proj(L.sh_down, act.sh_act, act.sh_actq, FFs, rows, act.sh_down, H, nullptr, 0,
-             f16_rows(act.sh_act, FFs, FFs, rows));
+             sh_f16 ? act.xb : f16_rows(act.sh_act, FFs, FFs, rows));
     }
     if (next_norm) {
         launch_check(hipllm::launch_moe_combine_norm(hidden, act.down, act.rweight, act.sh_down, act.rlog + E, ldr,

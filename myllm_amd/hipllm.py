@@ -140,6 +140,7 @@ SIGNATURES = {
     "hipllm_rmsnorm_f16": (_I, [_P, _P, _P, _P, _P, _S, _S, _F, _P]),
     "hipllm_gemm_swiglu_workspace_bytes": (_S, [_S, _S, _S]),
     "hipllm_gemm_mfma_swiglu": (_I, [_U32, _P, _P, _S, _P, _P, _P, _S, _S, _S, _P, _S, _P]),
+    "hipllm_gemm_mfma_swiglu_f16": (_I, [_U32, _P, _P, _S, _P, _P, _P, _P, _S, _S, _S, _P, _S, _P]),
     "hipllm_gemv_x16_grouped": (_I, [_U32, _P, _P, _P, _S, _I, _S, _P, _P, _S, _S, _S, _S, _P, _P, _P, _S, _P]),
     "hipllm_gemv_x16_pair": (_I, [_U32, _P, _S, _P, _U32, _P, _S, _P, _S, _P, _P, _F, _P, _P, _S, _P, _P, _P]),
     "hipllm_gemv_x16_moe_down": (_I, [_U32, _P, _P, _S, _P, _S, _S, _U32, _P, _P, _S, _P, _P, _P, _P, _S, _S, _P,
@@ -617,6 +618,16 @@ def _k_gemm_mfma_swiglu(qtype, wg, wu, row_bytes, xh, xscale, y, m, n, k, worksp
                                         _ptr(workspace), nbytes, _stream(stream)))
 
 
+def _k_gemm_mfma_swiglu_f16(qtype, wg, wu, row_bytes, xh, xscale, yh, yscale, m, n, k, workspace=None, stream=None):
+    if workspace is None:
+        import torch
+        workspace = torch.empty(max(16, lib().hipllm_gemm_swiglu_workspace_bytes(m, n, k)), dtype=torch.uint8,
+                                device=yh.device)
+    nbytes = workspace.numel() * workspace.element_size()
+    check(lib().hipllm_gemm_mfma_swiglu_f16(qtype, _ptr(wg), _ptr(wu), row_bytes, _ptr(xh), _ptr(xscale), _ptr(yh),
+                                            _ptr(yscale), m, n, k, _ptr(workspace), nbytes, _stream(stream)))
+
+
 def _k_gemv_x16_grouped(qtype, packed, packed2, xq, ldx, x_routed, routes, y, yq, ldy, n, k, experts, order, groups,
                         ngroups, max_groups, stream=None):
     check(lib().hipllm_gemv_x16_grouped(qtype, _ptr(packed), _ptr(packed2), _ptr(xq), ldx, int(bool(x_routed)), routes,
@@ -874,6 +885,7 @@ kernels = types.SimpleNamespace(
     gdn_chunk_scratch_floats=lambda t, h: lib().hipllm_gdn_chunk_scratch_floats(t, h),
     conv_l2norm=_k_conv_l2norm, gdn_scan_gated=_k_gdn_scan_gated, gdn_decode=_k_gdn_decode,
     gemv_x16_pair=_k_gemv_x16_pair, gemv_x16_grouped=_k_gemv_x16_grouped, gemm_mfma_swiglu=_k_gemm_mfma_swiglu,
+    gemm_mfma_swiglu_f16=_k_gemm_mfma_swiglu_f16,
     rmsnorm_f16=_k_rmsnorm_f16, attn_decode_qgate=_k_attn_decode_qgate, gemv_x16_moe_down=_k_gemv_x16_moe_down,
     split_qgate_norm=_k_split_qgate_norm, gate_mul=_k_gate_mul,
     gemv_workspace_bytes=lambda k: lib().hipllm_gemv_workspace_bytes(k),

@@ -255,6 +255,40 @@ def test_gemm_swiglu_matches_two_matmuls_and_swiglu(cuda, qtype, m, n, k):
     assert torch.equal(y.view(torch.int32), ref.view(torch.int32))
 
 
+@pytest.mark.parametrize("qtype,m,n,k", [(synth.Q4_K, 128, 18944, 512), (synth.Q6_K, 45, 1280, 512),
+                                         (synth.Q8_0, 64, 512, 1024), (synth.Q4_K, 300, 32768, 256),
+                                         (synth.Q4_K, 1100, 256, 512)])
+def test_gemm_swiglu_f16_matches_swiglu_then_f16(cuda, qtype, m, n, k):
+    """The SwiGLU rows written as fp16 operand rows in the reduce launch
+    against the FP32 form followed by hipllm_to_f16: the same fp16 bits and
+    row scales (n up to the 32768 limit, split and unsplit)."""
+    wg, wu = random_rows(qtype, n, k, 94), random_rows(qtype, n, k, 95)
+    dg, du = dev_bytes(wg, cuda), dev_bytes(wu, cuda)
+    g = torch.Generator(device="cpu").manual_seed(96)
+    x = torch.randn(m, k, generator=g).to(cuda)
+    xh, xs = to_f16(x, cuda)
+    yh = torch.empty(m, n, dtype=torch.float16, device=cuda)
+    ys = torch.empty(m, device=cuda)
+    kernels.gemm_mfma_swiglu_f16(qtype, dg, du, wg.shape[1], xh, xs, yh, ys, m, n, k)
+    y = torch.empty(m, n, device=cuda)
+    kernels.gemm_mfma_swiglu(qtype, dg, du, wg.shape[1], xh, xs, y, m, n, k)
+    rh, rs = to_f16(y, cuda)
+    assert torch.equal(yh.view(torch.int16), rh.view(torch.int16))
+    assert torch.equal(ys.view(torch.int32), rs.view(torch.int32))
+
+
+def test_gemm_swiglu_f16_rejects_bad_shapes(cuda):
+    w = torch.zeros(144 * 64, dtype=torch.uint8, device=cuda)
+    xh = torch.zeros(2, 256, dtype=torch.float16, device=cuda)
+    xs = torch.ones(2, device=cuda)
+    yh = torch.zeros(2, 32776, dtype=torch.float16, device=cuda)
+    ys = torch.zeros(2, device=cuda)
+    with pytest.raises(ValueError):  # n % 8
+        kernels.gemm_mfma_swiglu_f16(synth.Q4_K, w, w, 144, xh, xs, yh, ys, 2, 20, 256)
+    with pytest.raises(ValueError):  # n beyond 32768
+        kernels.gemm_mfma_swiglu_f16(synth.Q4_K, w, w, 144, xh, xs, yh, ys, 2, 32776, 256)
+
+
 def test_gemm_swiglu_rejects_bad_arguments(cuda):
     w = torch.zeros(144 * 64, dtype=torch.uint8, device=cuda)
     xh = torch.zeros(2, 256, dtype=torch.float16, device=cuda)
